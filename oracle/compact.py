@@ -1,0 +1,155 @@
+"""Compact-mode multi-tensor AdamW step (CPU oracle; test infrastructure only).
+
+Restates ``ApexW._multi_tensor_step`` (``apexw/optimizer.py:5297-5887``) for the
+standard AdamW update (no amsgrad / lion / AdEMAMix / nesterov / cautious,
+dynamic fp16 scaling inactive) with the same torch foreach ops, so every bf16
+rounding point of the reference is reproduced:
+
+1. decoupled weight decay ``p *= 1 - lr*wd`` (dim>=2 tensors when
+   decay_norm_only) -- optimizer.py:5585-5592
+2. ``m = m*b1``, ``m += (1-b1)*g``                 -- :5760-5761 / quad :5684-5685
+3. ``v`` EMA: SR path when beta2 >= 0.995 and SR on (fp32 math then SR to 16
+   bits, per tensor), else two foreach ops in v's dtype -- :5770-5776 / :5691-5697
+4. ``d = sqrt(v) + eps*sqrt(bc2)`` in v's dtype       -- :5799-5816 / :5704-5721
+5. parameter update: fp32 p ``addcdiv(p, m, d, -step_size)``; 16-bit p with SR
+   ``p = SR(p - (m/d)*step_size)``; quad: ``p -= (m/d_q)*step_size``   -- :5818-5828 / :5722-5745
+
+That is the *cold* step, taken whenever the optimizer (re)builds its cached
+execution plan.  Every later step replays the plan through
+``FastExecutionPlan.execute_foreach`` (optimizer.py:1069-1341), which rounds
+differently; ``replay_subgroup_step`` restates it:
+
+* no NaN/Inf sanitizing of the grads (only clip/centralization sanitize);
+* ``m = lerp(m, g, 1-b1)`` in one op when g and m share a dtype (:1231-1234);
+* the non-quad v EMA uses the grads in their own dtype (:1301-1302);
+* 16-bit params always take ``p = SR-or-RNE(p - (m/d)*step_size)`` (:1334-1338).
+"""
+
+import math
+
+import torch
+
+from .quant import store_16bit
+
+
+def sanitize_grads(grads):
+    """_sanitize_gradients_fast (optimizer.py:136-201): clone-and-clean only tensors with NaN/Inf."""
+    out = []
+    for g in grads:
+        if not bool(torch.isfinite(g).all()):
+            if g.dtype in (torch.float16, torch.bfloat16):
+                g = g.clone().clamp_(-65504.0, 65504.0).nan_to_num_(0.0)
+            else:
+                g = g.clone().nan_to_num_(0.0).clamp_(-65504.0, 65504.0)
+        out.append(g)
+    return out
+
+
+def bias_terms(lr, beta1, beta2, eps, step):
+    """Host scalars in double, as at optimizer.py:5577-5582."""
+    bc1 = 1.0 - beta1 ** step
+    bc2 = 1.0 - beta2 ** step
+    bc2_sqrt = math.sqrt(bc2)
+    return lr * bc2_sqrt / bc1, eps * bc2_sqrt
+
+
+def compact_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weight_decay,
+                          decay_norm_only, step, is_quad, stochastic):
+    """One step over a subgroup sharing (p dtype, m dtype, step count, quad flag).
+
+    ``step`` is the already-incremented step count.  Tensors are updated in place.
+    """
+    grads = sanitize_grads(grads)
+    step_size, eps_scaled = bias_terms(lr, beta1, beta2, eps, step)
+    if weight_decay != 0:
+        decay = [p for p in params if p.dim() >= 2] if decay_norm_only else list(params)
+        if decay:
+            torch._foreach_mul_(decay, 1.0 - lr * weight_decay)
+    gf = [g if g.dtype == torch.float32 else g.float() for g in grads]
+    mdt = ms[0].dtype
+    if mdt not in (torch.bfloat16, torch.float16):
+        raise NotImplementedError("oracle compact step expects 16-bit m")
+    torch._foreach_mul_(ms, beta1)
+    torch._foreach_add_(ms, gf, alpha=1.0 - beta1)
+    v16 = vs[0].dtype in (torch.bfloat16, torch.float16)
+    if is_quad:
+        gq = [g.reshape(-1, 4).square().mean(dim=1) for g in gf]
+        if beta2 >= 0.995 and stochastic and v16:
+            for v, q in zip(vs, gq):
+                store_16bit(v, v.float().mul_(beta2).add_(q, alpha=1.0 - beta2), True)
+        else:
+            torch._foreach_mul_(vs, beta2)
+            torch._foreach_add_(vs, gq, alpha=1.0 - beta2)
+        dens = torch._foreach_sqrt(vs)
+        torch._foreach_add_(dens, eps_scaled)
+        for p, m, d in zip(params, ms, dens):
+            delta = m.float().view(-1, 4).div_(d.float().unsqueeze(1)).mul_(step_size).view(p.shape)
+            if p.dtype == torch.float32:
+                p.sub_(delta)
+            else:
+                store_16bit(p, p.float().sub_(delta), stochastic)
+        return
+    if beta2 >= 0.995 and stochastic and v16:
+        for v, g in zip(vs, gf):
+            store_16bit(v, v.float().mul_(beta2).addcmul_(g, g, value=1.0 - beta2), True)
+    else:
+        torch._foreach_mul_(vs, beta2)
+        torch._foreach_addcmul_(vs, gf, gf, value=1.0 - beta2)
+    dens = torch._foreach_sqrt(vs)
+    torch._foreach_add_(dens, eps_scaled)
+    if params[0].dtype in (torch.bfloat16, torch.float16) and stochastic:
+        for p, m, d in zip(params, ms, dens):
+            delta = (m.float() / d.float()) * step_size
+            store_16bit(p, p.float().sub_(delta), True)
+    else:
+        torch._foreach_addcdiv_(params, ms, dens, value=-step_size)
+
+
+def replay_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weight_decay,
+                         apply_wd_mask, step, is_quad, stochastic):
+    """One replayed step over an (p dtype, compact, quad) subgroup (optimizer.py:1200-1338)."""
+    step_size, eps_scaled = bias_terms(lr, beta1, beta2, eps, step)
+    if weight_decay != 0.0:
+        decay = [p for p, w in zip(params, apply_wd_mask) if w]
+        if decay:
+            torch._foreach_mul_(decay, 1.0 - lr * weight_decay)
+    if grads[0].dtype == ms[0].dtype:
+        torch._foreach_lerp_(ms, grads, 1.0 - beta1)
+    else:
+        torch._foreach_mul_(ms, beta1)
+        torch._foreach_add_(ms, grads, alpha=1.0 - beta1)
+    v16 = vs[0].dtype in (torch.bfloat16, torch.float16)
+    sr_v = beta2 >= 0.995 and stochastic and v16
+    if is_quad:
+        gf = grads if grads[0].dtype == torch.float32 else [g.float() for g in grads]
+        gq = [g.reshape(-1, 4).square().mean(dim=1) for g in gf]
+        if sr_v:
+            for v, q in zip(vs, gq):
+                store_16bit(v, v.float().mul_(beta2).add_(q, alpha=1.0 - beta2), True)
+        else:
+            torch._foreach_mul_(vs, beta2)
+            torch._foreach_add_(vs, gq, alpha=1.0 - beta2)
+        dens = torch._foreach_sqrt(vs)
+        torch._foreach_add_(dens, eps_scaled)
+        for p, m, d in zip(params, ms, dens):
+            delta = m.float().view(-1, 4).div_(d.float().unsqueeze(1)).mul_(step_size).view(p.shape)
+            if p.dtype == torch.float32:
+                p.sub_(delta)
+            else:
+                store_16bit(p, p.float().sub_(delta), stochastic)
+        return
+    if sr_v:
+        for v, g in zip(vs, grads):
+            g32 = g.float()
+            store_16bit(v, v.float().mul_(beta2).addcmul_(g32, g32, value=1.0 - beta2), True)
+    else:
+        torch._foreach_mul_(vs, beta2)
+        torch._foreach_addcmul_(vs, grads, grads, value=1.0 - beta2)
+    dens = torch._foreach_sqrt(vs)
+    torch._foreach_add_(dens, eps_scaled)
+    if params[0].dtype in (torch.bfloat16, torch.float16):
+        for p, m, d in zip(params, ms, dens):
+            delta = (m.float() / d.float()) * step_size
+            store_16bit(p, p.float().sub_(delta), stochastic)
+    else:
+        torch._foreach_addcdiv_(params, ms, dens, value=-step_size)

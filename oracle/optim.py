@@ -1,0 +1,194 @@
+"""Oracle optimizer objects driving the CPU restatement (test infrastructure only).
+
+``OracleApexW`` mirrors the reference ``ApexW`` constructor defaults and the CPU
+dispatch of ``ApexW.step`` (``apexw/optimizer.py:3359-4094``) for the
+``compact`` and ``8bit`` precisions:
+
+* constructor: precision aliases (state.py:94-121), default betas (0.9, 0.999)
+  for 8bit and (0.9, 0.99) for compact, ``adamw_compat`` forcing
+  ``decay_norm_only=False`` and mapping betas (0.9, 0.95)/(0.9, 0.99) to
+  (0.9, 0.999) -- optimizer.py:1672-1714;
+* step: grad preparation (sanitize + global-norm clip, optimizer.py:204-258 and
+  :3469-3476), then for 8bit ``_step_ultra`` per parameter, and for compact
+  either ``torch._fused_adamw_`` when every state matches its parameter's dtype
+  and size (optimizer.py:3683-3766, ``_fused_step`` :4737-4835) or the foreach
+  path over (p dtype, m dtype, step, quad) subgroups (:5369-5381).
+
+Like the reference, the first step after the set of parameters-with-grad changes
+is a *cold* step; it caches a plan and the following steps *replay* it
+(``FastExecutionPlan``, optimizer.py:406-1341), which for the compact foreach
+path rounds differently (see ``oracle.compact``).  Plan validity follows
+``is_valid_for_step`` (optimizer.py:575-621).
+"""
+
+import torch
+
+from . import layout as L
+from .clip import clip_grads_
+from .compact import compact_subgroup_step, replay_subgroup_step, sanitize_grads
+from .q8 import q8_param_step
+
+_PREC = {
+    "compact": ("compact", "bf16", "bfloat16", "fp16", "float16", "half", "16", "16-bit"),
+    "8bit": ("8bit", "8-bit", "int8", "uint8", "q8", "adamw_8bit", "bnb_8bit"),
+}
+
+
+def normalize_precision(precision):
+    if isinstance(precision, torch.dtype):
+        if precision in (torch.bfloat16, torch.float16):
+            return "compact"
+        if precision in (torch.int8, torch.uint8):
+            return "8bit"
+        return "full"
+    key = precision.lower().strip()
+    for name, aliases in _PREC.items():
+        if key in aliases:
+            return name
+    if key in ("hybrid", "hybrid_apexw", "hybrid-apexw", "apex_hybrid", "hybrid_compact"):
+        return "compact"
+    raise NotImplementedError(f"oracle does not cover precision {precision!r}")
+
+
+class OracleApexW:
+    def __init__(self, params, lr=1e-3, betas=None, eps=1e-8, weight_decay=1e-2, decay_norm_only=True,
+                 adamw_compat=False, clip_grad_norm=None, precision="compact", stochastic_rounding=True,
+                 block_size=None, force_compact_v=False, int4_m=None):
+        precision = normalize_precision(precision)
+        if betas is None:
+            betas = (0.9, 0.999) if precision == "8bit" else (0.9, 0.99)
+        if adamw_compat:
+            decay_norm_only = False
+            if tuple(betas) in ((0.9, 0.95), (0.9, 0.99)):
+                betas = (0.9, 0.999)
+        self.params = list(params)
+        self.group = dict(lr=lr, betas=tuple(betas), eps=eps, weight_decay=weight_decay,
+                          decay_norm_only=decay_norm_only, clip_grad_norm=clip_grad_norm,
+                          precision=precision, stochastic_rounding=stochastic_rounding,
+                          block_size=block_size, force_compact_v=force_compact_v, int4_m=int4_m,
+                          params=self.params)
+        self.state = {}
+        self._plan = None
+
+    def _plan_valid(self):
+        plan = self._plan
+        if plan is None:
+            return False
+        active = set(plan["params"])
+        if any(p.grad is None for p in plan["params"]):
+            return False
+        return all(p.grad is None for p in self.params if p.requires_grad and p not in active)
+
+    def _prepare(self, grads, sanitize):
+        if sanitize:
+            grads = sanitize_grads(grads)
+        if self.group["clip_grad_norm"] is not None:
+            grads = [g.clone() for g in grads]
+            clip_grads_(grads, self.group["clip_grad_norm"])
+        return grads
+
+    def _kw(self):
+        grp = self.group
+        b1, b2 = grp["betas"]
+        return dict(lr=grp["lr"], beta1=b1, beta2=b2, eps=grp["eps"], weight_decay=grp["weight_decay"],
+                    decay_norm_only=grp["decay_norm_only"])
+
+    @torch.no_grad()
+    def step(self):
+        if self._plan_valid():
+            self._replay()
+            return
+        self._plan = None
+        grp = self.group
+        plist = [p for p in self.params if p.grad is not None]
+        if not plist:
+            return
+        peft = L.peft_context([grp])
+        for p in plist:
+            if p not in self.state:
+                self.state[p] = L.init_state(p, grp, len(self.params), peft)
+        prec = grp["precision"]
+        grads = self._prepare([p.grad for p in plist],
+                              sanitize=prec != "8bit" or grp["clip_grad_norm"] is not None)
+        kw = self._kw()
+        if prec == "8bit":
+            for p, g in zip(plist, grads):
+                st = self.state[p]
+                st["step"].add_(1)
+                q8_param_step(p, g, st, step=st["step"].item(), **kw)
+            self._plan = {"kind": "8bit", "params": plist}
+            return
+        sts = [self.state[p] for p in plist]
+        homogeneous = all(st["exp_avg"].dtype == st["exp_avg_sq"].dtype == p.dtype
+                          and st["exp_avg"].numel() == st["exp_avg_sq"].numel() for p, st in zip(plist, sts))
+        if homogeneous:
+            self._native_fused(plist, grads, sts, **kw)
+            self._plan = {"kind": "native", "params": plist}
+            return
+        sub = {}
+        for p, g, st in zip(plist, grads, sts):
+            key = (p.dtype, st["exp_avg"].dtype, int(st["step"].item()), self._is_quad(p))
+            sub.setdefault(key, []).append((p, g, st))
+        for (_, _, _, quad), items in sub.items():
+            for _, _, st in items:
+                st["step"].add_(1)
+            compact_subgroup_step([i[0] for i in items], [i[1] for i in items],
+                                  [i[2]["exp_avg"] for i in items], [i[2]["exp_avg_sq"] for i in items],
+                                  step=items[0][2]["step"].item(), is_quad=quad,
+                                  stochastic=grp["stochastic_rounding"], **kw)
+        self._plan = {"kind": "foreach", "params": plist}
+
+    def _is_quad(self, p):
+        v = self.state[p]["exp_avg_sq"]
+        return p.numel() >= 4 and p.numel() % 4 == 0 and v.numel() * 4 == p.numel()
+
+    def _replay(self):
+        grp = self.group
+        plan = self._plan
+        plist = plan["params"]
+        kw = self._kw()
+        grads = [p.grad for p in plist]
+        if plan["kind"] == "8bit":
+            grads = self._prepare(grads, sanitize=False)
+            for p, g in zip(plist, grads):
+                st = self.state[p]
+                st["step"].add_(1)
+                q8_param_step(p, g, st, step=st["step"].item(), **kw)
+            return
+        grads = self._prepare(grads, sanitize=grp["clip_grad_norm"] is not None)
+        sts = [self.state[p] for p in plist]
+        if plan["kind"] == "native":
+            self._native_fused(plist, grads, sts, sanitize=False, **kw)
+            return
+        steps = [st["step"] for st in sts]
+        torch._foreach_add_(steps, 1)
+        step = int(steps[0].item())
+        sub = {}
+        for p, g, st in zip(plist, grads, sts):
+            compact = st["exp_avg"].dtype in (torch.bfloat16, torch.float16)
+            sub.setdefault((p.dtype, compact, self._is_quad(p)), []).append((p, g, st))
+        dno = kw.pop("decay_norm_only")
+        for (_, _, quad), items in sub.items():
+            replay_subgroup_step([i[0] for i in items], [i[1] for i in items],
+                                 [i[2]["exp_avg"] for i in items], [i[2]["exp_avg_sq"] for i in items],
+                                 apply_wd_mask=[(i[0].dim() >= 2) if dno else True for i in items],
+                                 step=step, is_quad=quad, stochastic=grp["stochastic_rounding"], **kw)
+
+    @staticmethod
+    def _native_fused(params, grads, sts, *, lr, beta1, beta2, eps, weight_decay, decay_norm_only,
+                      sanitize=True):
+        if sanitize:
+            grads = sanitize_grads(grads)
+        steps = [st["step"] for st in sts]
+        torch._foreach_add_(steps, 1)
+        if decay_norm_only and weight_decay != 0.0:
+            parts = [([i for i, p in enumerate(params) if p.dim() >= 2], weight_decay),
+                     ([i for i, p in enumerate(params) if p.dim() < 2], 0.0)]
+        else:
+            parts = [(list(range(len(params))), weight_decay)]
+        for idx, wd in parts:
+            if idx:
+                torch._fused_adamw_([params[i] for i in idx], [grads[i] for i in idx],
+                                    [sts[i]["exp_avg"] for i in idx], [sts[i]["exp_avg_sq"] for i in idx],
+                                    [], [steps[i] for i in idx], amsgrad=False, lr=lr, beta1=beta1,
+                                    beta2=beta2, weight_decay=wd, eps=eps, maximize=False)

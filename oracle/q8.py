@@ -1,0 +1,162 @@
+"""8-bit AdamW step (CPU oracle; test infrastructure only).
+
+Restates ``ApexW._step_ultra`` (``apexw/optimizer.py:4313-4735``) for
+``precision="8bit"`` with the standard update (no amsgrad / lion / AdEMAMix /
+nesterov / cautious / factored-v), per parameter:
+
+* large contiguous quantized tensors (numel > 262144) use the chunked path,
+  optimizer.py:4402-4499 -- decay and update fused in fp32, one rounding of p;
+* other quantized tensors use the generic path, optimizer.py:4538-4639 -- decay
+  rounded into p first, then ``p -= bf16(update)`` (SR only for quad-v);
+* tensors with fewer than 64 elements keep 16-bit m/v, optimizer.py:4688-4735.
+
+The update is AdamW with the "Nesterov-SNR" lookahead gain: ``m_look =
+lerp(g, m, b1)``, gain ``1+0.2*b1`` where ``m*g >= 0`` else ``1-0.35*b1``.
+"""
+
+import math
+
+import torch
+
+from . import quant as Q
+
+CHUNK = 262144  # _FACTORED_CHUNK_ELEMS, state.py:44
+
+
+def _bias(lr, beta1, beta2, eps, step):
+    bc1 = 1.0 - beta1 ** step
+    bc2 = 1.0 - beta2 ** step
+    s = math.sqrt(bc2)
+    return lr * s / bc1, eps * s
+
+
+def _snr_num(m, g, beta1):
+    gain_hi = 1.0 + 0.20 * beta1
+    gain_lo = 1.0 - 0.35 * beta1
+    look = torch.lerp(g, m, beta1)
+    return look.mul_(torch.where(m * g >= 0.0, gain_hi, gain_lo))
+
+
+def q8_param_step(p, g, st, *, lr, beta1, beta2, eps, weight_decay, decay_norm_only, step):
+    """Update one parameter and its state in place.  ``step`` is already incremented."""
+    step_size, eps_scaled = _bias(lr, beta1, beta2, eps, step)
+    decay = max(1.0 - lr * weight_decay, 0.0) if weight_decay != 0 else 1.0
+    apply_wd = weight_decay != 0 and (not decay_norm_only or p.dim() >= 2)
+    sr = st.get("stochastic_rounding", True)
+    n = p.numel()
+    if st.get("is_8bit", False) and n > CHUNK and p.is_contiguous():
+        _chunked(p, g, st, beta1, beta2, eps, step_size, eps_scaled, decay if apply_wd else None, sr)
+        return
+    gf = torch.nan_to_num(g, nan=0.0, posinf=65504.0, neginf=-65504.0).float()
+    if apply_wd:
+        p.mul_(decay)
+    if st.get("is_8bit", False):
+        bs = st["block_size_8bit"]
+        int4 = st.get("is_4bit_m", False)
+        quad = bool(st.get("is_quad_v", False))
+        if int4:
+            m = Q.dequant_nf4(st["exp_avg"], st["exp_avg_scales"], n, bs).view(p.shape)
+        else:
+            m = Q.dequant_int8(st["exp_avg"], st["exp_avg_scales"], bs)
+        m.lerp_(gf, 1.0 - beta1)
+        if quad:
+            vbs = max(1, bs // 4)
+            v = Q.dequant_logu8(st["exp_avg_sq"], st["exp_avg_sq_scales"], vbs)
+            gq = gf.reshape(-1, 4).square().mean(dim=1)
+            v.mul_(beta2).add_(gq, alpha=1.0 - beta2)
+            v.nan_to_num_(nan=0.0, posinf=0.0, neginf=0.0)
+            den = v.sqrt().add_(eps_scaled).clamp_min_(eps).unsqueeze(1).expand(-1, 4).reshape(p.shape)
+        else:
+            vbs = bs
+            v = Q.dequant_logu8(st["exp_avg_sq"], st["exp_avg_sq_scales"], bs)
+            v.mul_(beta2).addcmul_(gf, gf, value=1.0 - beta2)
+            v.nan_to_num_(nan=0.0, posinf=0.0, neginf=0.0)
+            den = v.sqrt().add_(eps_scaled).clamp_min_(eps)
+        num = _snr_num(m, gf, beta1)
+        if p.dtype == torch.float32:
+            p.addcdiv_(num, den, value=-step_size)
+        else:
+            upd = (num / den).mul_(step_size)
+            if quad and sr:
+                Q.store_16bit(p, p.float().sub_(upd), True)
+            else:
+                p.sub_(upd.to(p.dtype))
+        if int4:
+            q, s = Q.quant_nf4(m, bs, st["exp_avg_scales"], sr)
+        else:
+            q, s = Q.quant_int8(m, bs, st["exp_avg_scales"], sr)
+        st["exp_avg"].copy_(q.view(st["exp_avg"].shape))
+        st["exp_avg_scales"].copy_(s)
+        qv, sv = Q.quant_logu8(v, vbs, st["exp_avg_sq_scales"], sr)
+        st["exp_avg_sq"].copy_(qv.view(st["exp_avg_sq"].shape))
+        st["exp_avg_sq_scales"].copy_(sv)
+        return
+    # tiny tensors: 16-bit (or fp32) m and v, fp32 math
+    m, v = st["exp_avg"], st["exp_avg_sq"]
+    mf = m.float().lerp_(gf, 1.0 - beta1)
+    m.copy_(mf.to(m.dtype))
+    vf = v.float().mul_(beta2).addcmul_(gf, gf, value=1.0 - beta2)
+    v.copy_(vf.to(v.dtype))
+    den = vf.sqrt().add_(eps_scaled)
+    upd = (mf / den).mul_(step_size)
+    p.sub_(upd.to(p.dtype))
+
+
+def _chunked(p, g, st, beta1, beta2, eps, step_size, eps_scaled, decay, sr):
+    n = p.numel()
+    bs = st["block_size_8bit"]
+    int4 = st.get("is_4bit_m", False)
+    mbuf, vbuf = st["exp_avg"].reshape(-1), st["exp_avg_sq"].reshape(-1)
+    msc, vsc = st["exp_avg_scales"], st["exp_avg_sq_scales"]
+    quad = bool(st.get("is_quad_v", False)) or (int4 and n % 4 == 0 and vbuf.numel() * 4 == n)
+    vbs = max(1, bs // 4) if quad else bs
+    step_elems = max(CHUNK // bs, 1) * bs
+    pf_all, gf_all = p.reshape(-1), g.reshape(-1)
+    for off in range(0, n, step_elems):
+        end = min(off + step_elems, n)
+        blk0, last = off // bs, end >= n
+        sl = slice(blk0, None) if last else slice(blk0, blk0 + (end - off) // bs)
+        sm, sv = msc[sl], vsc[sl]
+        gc = gf_all[off:end].float().nan_to_num_(nan=0.0, posinf=65504.0, neginf=-65504.0)
+        if int4:
+            msl = mbuf[off // 2:(end + 1) // 2]
+            m = Q.dequant_nf4(msl, sm, end - off, bs)
+        else:
+            msl = mbuf[off:end]
+            m = Q.dequant_int8(msl, sm, bs)
+        m.lerp_(gc, 1.0 - beta1)
+        num = _snr_num(m, gc, beta1)
+        if quad:
+            vsl = vbuf[off // 4:end // 4]
+            v = Q.dequant_logu8(vsl, sv, vbs)
+            v.mul_(beta2).add_(gc.view(-1, 4).square().mean(dim=1), alpha=1.0 - beta2)
+            v.nan_to_num_(nan=0.0, posinf=0.0, neginf=0.0)
+            den = v.sqrt().add_(eps_scaled).clamp_min_(eps)
+            num.view(-1, 4).div_(den.unsqueeze(1))
+            upd = num.mul_(step_size)
+        else:
+            vsl = vbuf[off:end]
+            v = Q.dequant_logu8(vsl, sv, bs)
+            v.mul_(beta2).addcmul_(gc, gc, value=1.0 - beta2)
+            v.nan_to_num_(nan=0.0, posinf=0.0, neginf=0.0)
+            den = v.sqrt().add_(eps_scaled).clamp_min_(eps)
+            upd = torch.div(num, den).mul_(step_size)
+        psl = pf_all[off:end]
+        if p.dtype == torch.float32:
+            if decay is not None:
+                psl.mul_(decay)
+            psl.sub_(upd)
+        else:
+            x = psl.float()
+            if decay is not None:
+                x.mul_(decay)
+            Q.store_16bit(psl, x.sub_(upd), sr)
+        if int4:
+            q, s = Q.quant_nf4(m, bs, sm, sr)
+        else:
+            q, s = Q.quant_int8(m, bs, sm, sr)
+        msl.copy_(q.view(msl.shape))
+        sm.copy_(s)
+        qv, s2 = Q.quant_logu8(v, vbs, sv, sr)
+        vsl.copy_(qv.view(vsl.shape))
+        sv.copy_(s2)

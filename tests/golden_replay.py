@@ -1,0 +1,80 @@
+"""Replay the golden trajectories (tests/golden/*.npz) against any optimizer factory.
+
+Inputs are regenerated with the same seeded generator and call order as
+``tests/golden/make_golden.py``; the stored fingerprints prove they match.
+"""
+
+import os
+
+import numpy as np
+import torch
+
+from golden.make_golden import _fingerprint, _grad, _param
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+# name -> (shapes, dtype, steps, seed, kwargs, grad_scales, zero_grad_idx); mirrors make_golden.py
+SHAPES_BF16 = [(128, 256), (64, 512), (16384,), (256, 96), (768,), (768,), (100,), (8, 4096), (3, 5), (36, 64)]
+RAGGED = [(300,), (64, 70), (16384,), (128, 128), (17,), (4, 1024), (1000,), (32, 33), (20000,)]
+RAGGED_SCALES = [10.0, 0.1, 1.0, 3.0, 0.5, 7.0, 0.2, 1.5, 0.05]
+Q8_SHAPES = [(512, 1024), (256, 256), (100, 300), (4096,), (1000,), (50,), (3000,), (16, 100), (64, 33)]
+CASES = {
+    "compact_c1_fp32_rne": ([(16384,)], torch.float32, 10, 0,
+                            dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, stochastic_rounding=False), None, ()),
+    "compact_bf16_quad_rne": (SHAPES_BF16, torch.bfloat16, 10, 1,
+                              dict(lr=1e-3, weight_decay=0.1, stochastic_rounding=False), None, ()),
+    "compact_bf16_fp32v_rne": (SHAPES_BF16, torch.bfloat16, 10, 2,
+                               dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, stochastic_rounding=False), None, ()),
+    "compact_fp32_quad_rne": (SHAPES_BF16, torch.float32, 10, 3,
+                              dict(lr=1e-3, weight_decay=0.1, stochastic_rounding=False), None, ()),
+    "compact_bf16_clip_rne": (RAGGED, torch.bfloat16, 6, 4,
+                              dict(lr=1e-3, weight_decay=0.1, stochastic_rounding=False, clip_grad_norm=1.0),
+                              RAGGED_SCALES, (4,)),
+    "q8_bf16_rne": (Q8_SHAPES, torch.bfloat16, 5, 5,
+                    dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, precision="8bit", stochastic_rounding=False),
+                    None, ()),
+    "q8_fp32_rne": ([(300, 1000), (128, 128), (2048,), (700,)], torch.float32, 4, 6,
+                    dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, precision="8bit", stochastic_rounding=False),
+                    None, ()),
+}
+
+
+def load(name):
+    with np.load(os.path.join(GOLDEN, f"{name}.npz"), allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def to_torch(arr, like_dtype):
+    if like_dtype == torch.bfloat16:
+        return torch.from_numpy(arr.astype(np.uint16).view(np.int16)).view(torch.bfloat16)
+    return torch.from_numpy(np.ascontiguousarray(arr))
+
+
+def replay(name, make_opt, device="cpu", get_state=None):
+    """Run case ``name`` with ``make_opt(params, **kwargs)``; return (params, opt, golden dict)."""
+    shapes, dtype, steps, seed, kwargs, scales, zidx = CASES[name]
+    gold = load(name)
+    gen = torch.Generator().manual_seed(seed)
+    host = [_param(s, dtype, gen) for s in shapes]
+    fp = [_fingerprint(p) for p in host]
+    params = [torch.nn.Parameter(h.to(device)) for h in host]
+    opt = make_opt(params, **kwargs)
+    for _ in range(steps):
+        for i, p in enumerate(params):
+            g = _grad(p.shape, dtype, gen, 1e-3 if scales is None else scales[i])
+            if i in zidx:
+                g.zero_()
+            fp.append(_fingerprint(g))
+            p.grad = g.to(device)
+        opt.step()
+    np.testing.assert_array_equal(np.array(fp, dtype=np.float64), gold["fingerprint"])
+    return params, opt, gold
+
+
+def bf16_ulp_diff(a, b):
+    """Distance in bf16 units-in-the-last-place between two bf16 tensors (sign-aware)."""
+    ia = a.view(torch.int16).to(torch.int32)
+    ib = b.view(torch.int16).to(torch.int32)
+    ia = torch.where(ia < 0, -(ia & 0x7FFF), ia)
+    ib = torch.where(ib < 0, -(ib & 0x7FFF), ib)
+    return (ia - ib).abs()

@@ -1,0 +1,110 @@
+"""ctypes binding of libapexw_hip.so (the C ABI declared in include/apexw_hip.h).
+
+The library is built in-tree by ``apexw_amd._build``.  There is no fallback: if
+the library is missing or was built for another ABI version, every entry point
+raises.  Struct layouts below mirror the header field for field; the numpy
+dtypes are the same layouts used to build device-resident tables in bulk.
+"""
+
+import ctypes
+import os
+
+import numpy as np
+
+from ._build import LIB_PATH
+
+ABI_VERSION = 1
+
+# dtype codes
+F32, BF16, F16, U8, I8 = 0, 1, 2, 3, 4
+
+# apexw_tensor.flags
+PDT_SHIFT, GDT_SHIFT, MDT_SHIFT, VDT_SHIFT = 0, 2, 4, 6
+FLAG_QUAD = 1 << 8
+FLAG_WD = 1 << 9
+FLAG_NF4 = 1 << 10
+FLAG_GENERIC = 1 << 11
+FLAG_DENSE16 = 1 << 12
+FLAG_SCALAR = 1 << 13
+
+COMPACT_UNIT = 2048
+
+MODE_COLD, MODE_REPLAY, MODE_NATIVE = 0, 1, 2
+
+HP_SR = 1 << 0
+HP_SR_V = 1 << 1
+HP_SANITIZE = 1 << 2
+HP_CLIP = 1 << 3
+HP_LERP_HI = 1 << 4
+HP_LOOK_HI = 1 << 5
+
+STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported dtype combination", 3: "launch failed",
+          4: "misaligned pointer"}
+
+TENSOR_DTYPE = np.dtype([
+    ("p", np.uint64), ("g", np.uint64), ("m", np.uint64), ("v", np.uint64),
+    ("m_scale", np.uint64), ("v_scale", np.uint64), ("n", np.int64),
+    ("flags", np.uint32), ("block", np.uint32),
+])
+UNIT_DTYPE = np.dtype([("tensor", np.uint32), ("unit", np.uint32)])
+assert TENSOR_DTYPE.itemsize == 64 and UNIT_DTYPE.itemsize == 8
+
+
+class Tensor(ctypes.Structure):
+    _fields_ = [("p", ctypes.c_void_p), ("g", ctypes.c_void_p), ("m", ctypes.c_void_p), ("v", ctypes.c_void_p),
+                ("m_scale", ctypes.c_void_p), ("v_scale", ctypes.c_void_p), ("n", ctypes.c_int64),
+                ("flags", ctypes.c_uint32), ("block", ctypes.c_uint32)]
+
+
+class HParams(ctypes.Structure):
+    _fields_ = [("beta1", ctypes.c_float), ("one_minus_beta1", ctypes.c_float),
+                ("beta2", ctypes.c_float), ("one_minus_beta2", ctypes.c_float),
+                ("wd_factor", ctypes.c_float), ("step_size", ctypes.c_float),
+                ("eps_scaled", ctypes.c_float), ("eps", ctypes.c_float),
+                ("lerp_coef", ctypes.c_float), ("look_coef", ctypes.c_float),
+                ("bc2_sqrt", ctypes.c_float), ("gain_hi", ctypes.c_float), ("gain_lo", ctypes.c_float),
+                ("clip_coef", ctypes.c_void_p), ("seed", ctypes.c_uint64), ("step", ctypes.c_uint32),
+                ("mode", ctypes.c_uint32), ("flags", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
+
+
+_vp, _i32, _i64, _f32, _u32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_uint32
+_HP = ctypes.POINTER(HParams)
+
+# name -> (restype, argtypes); every symbol the header declares
+SIGNATURES = {
+    "apexw_abi_version": (ctypes.c_int, []),
+    "apexw_check_tensor": (ctypes.c_int, [ctypes.POINTER(Tensor), _i32]),
+    "apexw_compact_step": (ctypes.c_int, [_vp, _i32, _vp, _i64, _HP, _vp]),
+    "apexw_q8_step": (ctypes.c_int, [_vp, _i32, _vp, _i64, _HP, _vp]),
+    "apexw_grad_clip_coef": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _vp, _vp, _vp, _f32, _u32, _vp, _vp]),
+}
+
+_LIB = None
+
+
+class ApexwError(RuntimeError):
+    pass
+
+
+def load(path=LIB_PATH):
+    """Load the library once; raise if it is missing or has another ABI version."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.exists(path):
+        raise ApexwError(f"{path} is not built; run `python -m apexw_amd._build` (hipcc, gfx950)")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    ver = lib.apexw_abi_version()
+    if ver != ABI_VERSION:
+        raise ApexwError(f"libapexw_hip ABI {ver}, expected {ABI_VERSION}; rebuild")
+    _LIB = lib
+    return lib
+
+
+def check(status, what):
+    if status != 0:
+        raise ApexwError(f"{what}: {STATUS.get(status, status)}")

@@ -1,0 +1,288 @@
+"""Cached execution plan of one parameter group: device tables + one launch per step.
+
+The reference caches per-group tensor lists in ``FastExecutionPlan``
+(apexw/optimizer.py:406-1341) and replays them from the second step on; the
+first step after a (re)build runs the uncached path.  Both paths round
+differently, and this plan keeps that distinction (``MODE_COLD`` for the first
+launch, ``MODE_REPLAY`` afterwards).
+
+What the plan owns, built once and reused every step:
+  * the tensor table (64-byte descriptors, device-resident) and the unit
+    (chunk) table that splits every tensor into 2048-element units (compact)
+    or quantization blocks (8-bit) -- one kernel launch covers the whole group;
+  * one shared CPU fp32 buffer holding every parameter's step counter; each
+    ``state["step"]`` is a 0-dim view into it, so advancing all counters is one
+    op instead of one per tensor;
+  * clip workspaces (per-unit partial sums, per-tensor norms, the coefficient).
+Only the grad pointers are re-read every step; if any changed, the tensor
+table is re-uploaded (one host-to-device copy).
+"""
+
+import math
+
+import numpy as np
+import torch
+
+from . import _lib as L
+
+_DT = {torch.float32: L.F32, torch.bfloat16: L.BF16, torch.float16: L.F16, torch.uint8: L.U8, torch.int8: L.I8}
+CHUNKED_MIN_NUMEL = 262144  # larger 8-bit tensors take the reference's chunked rounding order
+
+
+def _lerp_coef(w):
+    w32 = np.float32(w)
+    if abs(float(w32)) < 0.5:
+        return float(w32), False
+    return float(np.float32(w32 - np.float32(1.0))), True
+
+
+class StepPlan:
+    def __init__(self, opt, group, params, kind, native=False):
+        self.kind = kind                  # "compact" or "q8"
+        self.native = native              # compact group stepped with torch._fused_adamw_ rounding
+        self.params = list(params)
+        self.param_ids = tuple(id(p) for p in self.params)
+        active = set(self.params)
+        self.inactive = [p for p in group["params"] if getattr(p, "requires_grad", False) and p not in active]
+        self.precision = group["precision"]
+        self.decay_norm_only = group["decay_norm_only"]
+        self.device = self.params[0].device
+        self.states = [opt.state[p] for p in self.params]
+        self.cold_done = False
+        self._build_steps()
+        self._build_tables(group)
+
+    # ------------------------------------------------------------------ validity
+    def valid_for(self, group):
+        """The reference's FastExecutionPlan.is_valid_for_step (optimizer.py:575-621)."""
+        if not self.params:
+            return False
+        for p in self.params:
+            if p.grad is None:
+                return False
+        for p in self.inactive:
+            if p.grad is not None:
+                return False
+        if group.get("decay_norm_only", self.decay_norm_only) != self.decay_norm_only:
+            return False
+        if group.get("precision") != self.precision:
+            return False
+        return True
+
+    # ------------------------------------------------------------------ build
+    def _build_steps(self):
+        vals = [float(st["step"].item()) for st in self.states]
+        self.steps = torch.tensor(vals, dtype=torch.float32)
+        for i, st in enumerate(self.states):
+            st["step"] = self.steps[i]
+
+    def _tensor_flags(self, p, st, wd_on):
+        f = (_DT[p.dtype] << L.PDT_SHIFT) | (_DT[p.dtype] << L.GDT_SHIFT)
+        m, v = st["exp_avg"], st["exp_avg_sq"]
+        if wd_on and (not self.decay_norm_only or p.dim() >= 2):
+            f |= L.FLAG_WD
+        if self.kind == "compact":
+            f |= (_DT[m.dtype] << L.MDT_SHIFT) | (_DT[v.dtype] << L.VDT_SHIFT)
+            if v.numel() * 4 == p.numel() and p.numel() % 4 == 0:
+                f |= L.FLAG_QUAD
+            block = 0
+        elif st.get("is_8bit", False):
+            block = int(st["block_size_8bit"])
+            if st.get("is_4bit_m", False):
+                f |= L.FLAG_NF4
+            if st.get("is_quad_v", False):
+                f |= L.FLAG_QUAD
+            if not (p.numel() > CHUNKED_MIN_NUMEL and p.is_contiguous()):
+                f |= L.FLAG_GENERIC
+            if block % 8:
+                f |= L.FLAG_SCALAR
+        else:
+            f |= L.FLAG_DENSE16 | (_DT[m.dtype] << L.MDT_SHIFT) | (_DT[v.dtype] << L.VDT_SHIFT)
+            block = 0
+        return f, block
+
+    def _build_tables(self, group):
+        wd_on = group["weight_decay"] != 0
+        n = len(self.params)
+        self.grads = [None] * n
+        tab = np.zeros(n, dtype=L.TENSOR_DTYPE)
+        counts = np.zeros(n, dtype=np.int64)
+        lib = L.load()
+        for i, (p, st) in enumerate(zip(self.params, self.states)):
+            if not p.is_contiguous():
+                raise NotImplementedError("ApexW HIP step needs contiguous parameters")
+            f, block = self._tensor_flags(p, st, wd_on)
+            m, v = st["exp_avg"], st["exp_avg_sq"]
+            tab[i]["p"] = p.data_ptr()
+            tab[i]["m"] = m.data_ptr()
+            tab[i]["v"] = v.data_ptr()
+            if "exp_avg_scales" in st and st.get("is_8bit", False):
+                tab[i]["m_scale"] = st["exp_avg_scales"].data_ptr()
+                tab[i]["v_scale"] = st["exp_avg_sq_scales"].data_ptr()
+            tab[i]["n"] = p.numel()
+            tab[i]["flags"] = f
+            tab[i]["block"] = block
+            if self.kind == "compact":
+                counts[i] = (p.numel() + L.COMPACT_UNIT - 1) // L.COMPACT_UNIT
+            elif f & L.FLAG_DENSE16:
+                counts[i] = 1
+            else:
+                counts[i] = (p.numel() + block - 1) // block
+        self.host_table = tab
+        self.unit_counts = counts
+        self.unit_begin = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+        total = int(self.unit_begin[-1])
+        tidx = np.repeat(np.arange(n, dtype=np.uint32), counts)
+        uidx = (np.arange(total, dtype=np.int64) - np.repeat(self.unit_begin[:-1], counts)).astype(np.uint32)
+        units = np.zeros(total, dtype=L.UNIT_DTYPE)
+        units["tensor"] = tidx
+        units["unit"] = uidx
+        self.n_units = total
+        self.d_units = torch.from_numpy(units.view(np.uint8)).to(self.device)
+        self.d_unit_begin = torch.from_numpy(self.unit_begin).to(self.device)
+        self.d_table = None
+        self.kind_code = 0 if self.kind == "compact" else 1
+        self._lib = lib
+        self.clip_ws = None
+
+    def _refresh_grads(self):
+        """Point the table at this step's grad tensors; re-upload if any changed."""
+        changed = self.d_table is None
+        grads = []
+        for i, p in enumerate(self.params):
+            g = p.grad
+            if g.dtype != p.dtype:
+                raise NotImplementedError("grad dtype must match the parameter dtype")
+            if not g.is_contiguous():
+                g = g.contiguous()
+            grads.append(g)
+            if g is not self.grads[i]:
+                ptr = g.data_ptr()
+                if int(self.host_table[i]["g"]) != ptr:
+                    changed = True
+                    self.host_table[i]["g"] = ptr
+        self.grads = grads
+        if changed:
+            self._validate_and_align()
+            self.d_table = torch.from_numpy(self.host_table.view(np.uint8)).to(self.device)
+        return grads
+
+    def _validate_and_align(self):
+        lib = self._lib
+        for i in range(len(self.params)):
+            row = self.host_table[i]
+            ptrs = int(row["p"]) | int(row["g"]) | int(row["m"]) | int(row["v"])
+            if ptrs & 15:
+                row["flags"] = int(row["flags"]) | L.FLAG_SCALAR
+            t = L.Tensor(*(int(row[k]) for k in ("p", "g", "m", "v", "m_scale", "v_scale", "n", "flags", "block")))
+            L.check(lib.apexw_check_tensor(ctypes_ref(t), self.kind_code), f"tensor {i} ({tuple(self.params[i].shape)})")
+
+    # ------------------------------------------------------------------ launch
+    def _clip(self, clip, sanitize, stream):
+        if self.clip_ws is None:
+            self.clip_ws = (torch.empty(max(self.n_units, 1), dtype=torch.float32, device=self.device),
+                            torch.empty(len(self.params), dtype=torch.float32, device=self.device),
+                            torch.empty(1, dtype=torch.float32, device=self.device))
+        part, norms, coef = self.clip_ws
+        unit = L.COMPACT_UNIT if self.kind == "compact" else 0
+        st = self._lib.apexw_grad_clip_coef(
+            self.d_table.data_ptr(), len(self.params), self.d_units.data_ptr(), self.n_units, unit,
+            self.d_unit_begin.data_ptr(), part.data_ptr(), norms.data_ptr(), float(clip),
+            L.HP_SANITIZE if sanitize else 0, coef.data_ptr(), stream)
+        L.check(st, "apexw_grad_clip_coef")
+        return coef
+
+    def execute(self, group, seed):
+        """Run one optimizer step for the group (cold the first time, replay after)."""
+        mode_cold = not self.cold_done
+        self._refresh_grads()
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        lr, (b1, b2), eps, wd = group["lr"], group["betas"], group["eps"], group["weight_decay"]
+        sr = bool(group.get("stochastic_rounding", True))
+        clip = group.get("clip_grad_norm", None)
+        if self.kind == "compact":
+            sanitize = mode_cold or clip is not None
+        else:
+            sanitize = mode_cold and clip is not None
+        coef = self._clip(clip, sanitize, stream) if clip is not None else None
+        self.steps.add_(1.0)
+        # The reference's replayed compact step takes the bias correction of the
+        # first counter for the whole group (optimizer.py:1082-1090); every other
+        # path uses each parameter's own count.
+        if mode_cold or self.native or self.kind == "q8":
+            groups = self._split_by_step()
+        else:
+            groups = [(None, int(self.steps[0].item()))]
+        for units, step in groups:
+            hp = self._hparams(lr, b1, b2, eps, wd, step, sr, sanitize, coef, seed, mode_cold)
+            d_units, n_units = (self.d_units, self.n_units) if units is None else units
+            fn = self._lib.apexw_compact_step if self.kind == "compact" else self._lib.apexw_q8_step
+            L.check(fn(self.d_table.data_ptr(), len(self.params), d_units.data_ptr(), n_units,
+                       ctypes_ref(hp), stream), "apexw step")
+        self.cold_done = True
+
+    def _split_by_step(self):
+        vals = self.steps.tolist()
+        if all(v == vals[0] for v in vals):
+            return [(None, int(vals[0]))]
+        out = []
+        for val in sorted(set(vals), key=vals.index):
+            keep = np.array([v == val for v in vals])
+            mask = np.repeat(keep, self.unit_counts)
+            sel = self.d_units.view(-1, 8)[torch.from_numpy(mask).to(self.device)].reshape(-1)
+            out.append(((sel, int(mask.sum())), int(val)))
+        return out
+
+    def _hparams(self, lr, b1, b2, eps, wd, step, sr, sanitize, coef, seed, cold):
+        hp = L.HParams()
+        bc1 = 1.0 - b1 ** step
+        bc2 = 1.0 - b2 ** step
+        bc2s = math.sqrt(bc2)
+        hp.beta1, hp.one_minus_beta1 = b1, 1.0 - b1
+        hp.beta2, hp.one_minus_beta2 = b2, 1.0 - b2
+        flags = 0
+        if self.kind == "q8":
+            hp.wd_factor = max(1.0 - lr * wd, 0.0) if wd != 0 else 1.0
+            hp.step_size = lr * bc2s / bc1
+            hp.eps_scaled = eps * bc2s
+            hp.eps = eps
+            hp.gain_hi = 1.0 + 0.20 * b1
+            hp.gain_lo = 1.0 - 0.35 * b1
+            hp.mode = L.MODE_COLD if cold else L.MODE_REPLAY
+            if sr:
+                flags |= L.HP_SR
+        elif self.native:
+            hp.wd_factor = 1.0 - lr * wd
+            hp.step_size = lr / bc1
+            hp.bc2_sqrt = bc2s
+            hp.eps = eps
+            hp.mode = L.MODE_NATIVE
+        else:
+            hp.wd_factor = 1.0 - lr * wd
+            hp.step_size = lr * bc2s / bc1
+            hp.eps_scaled = eps * bc2s
+            hp.mode = L.MODE_COLD if cold else L.MODE_REPLAY
+            if sr:
+                flags |= L.HP_SR
+                if b2 >= 0.995:
+                    flags |= L.HP_SR_V
+        hp.lerp_coef, hi = _lerp_coef(1.0 - b1)
+        if hi:
+            flags |= L.HP_LERP_HI
+        hp.look_coef, hi = _lerp_coef(b1)
+        if hi:
+            flags |= L.HP_LOOK_HI
+        if sanitize:
+            flags |= L.HP_SANITIZE
+        if coef is not None:
+            flags |= L.HP_CLIP
+            hp.clip_coef = coef.data_ptr()
+        hp.seed = seed
+        hp.step = step & 0xFFFFFFFF
+        hp.flags = flags
+        return hp
+
+
+def ctypes_ref(obj):
+    import ctypes
+    return ctypes.byref(obj)

@@ -1,0 +1,103 @@
+// C-ABI entry points of libapexw_hip.so (declared in include/apexw_hip.h).
+//
+// Each entry point checks its scalar arguments before enqueueing anything and
+// returns an apexw_status.  Tensor and unit tables are device-resident arrays
+// built once per execution plan by the caller; apexw_check_tensor validates one
+// descriptor (host copy) when the plan is built, so the per-step calls do not
+// copy or inspect the tables.
+#include <mutex>
+
+#include "common.h"
+
+int apexw_launch_compact(const apexw_tensor*, int64_t, const apexw_unit*, const apexw_hparams*, int, hipStream_t);
+int apexw_launch_q8(const apexw_tensor*, int64_t, const apexw_unit*, const apexw_hparams*, int, hipStream_t);
+int apexw_launch_clip(const apexw_tensor*, int32_t, const apexw_unit*, int64_t, int64_t, const int64_t*, float*, float*,
+                      float, uint32_t, float*, int, int, hipStream_t);
+bool apexw_compact_flags_ok(uint32_t flags);
+bool apexw_q8_flags_ok(uint32_t flags, uint32_t block, int64_t n);
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+int g_cu_count[kMaxDevices];
+std::once_flag g_cu_once[kMaxDevices];
+
+int cu_count() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  std::call_once(g_cu_once[dev], [dev] {
+    int cu = 0;
+    if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cu <= 0) cu = 256;
+    g_cu_count[dev] = cu;
+  });
+  return g_cu_count[dev];
+}
+
+// Persistent grid: enough 4-wave workgroups to cover the units, capped at
+// `per_cu` resident workgroups per CU.
+int persistent_grid(int64_t n_units, int per_cu) {
+  const int64_t want = (n_units + 3) / 4;
+  const int64_t cap = (int64_t)cu_count() * per_cu;
+  const int64_t g = want < cap ? want : cap;
+  return (int)(g > 0 ? g : 1);
+}
+
+bool hp_ok(const apexw_hparams* hp) {
+  if (!hp) return false;
+  if (hp->mode > APEXW_MODE_NATIVE) return false;
+  if ((hp->flags & APEXW_HP_CLIP) && !hp->clip_coef) return false;
+  return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+int apexw_abi_version(void) { return APEXW_ABI_VERSION; }
+
+// Validate one tensor descriptor (host memory) for the given step kind
+// (0 = compact, 1 = 8-bit).  Returns APEXW_OK or the reason it is unsupported.
+int apexw_check_tensor(const apexw_tensor* t, int32_t kind) {
+  if (!t || !t->p || !t->g || !t->m || !t->v || t->n <= 0) return APEXW_ERR_ARG;
+  if (kind == 0) {
+    if (!apexw_compact_flags_ok(t->flags)) return APEXW_ERR_DTYPE;
+    if ((t->flags & APEXW_FLAG_QUAD) && (t->n % 4) != 0) return APEXW_ERR_ARG;
+  } else if (kind == 1) {
+    if (!apexw_q8_flags_ok(t->flags, t->block, t->n)) return APEXW_ERR_DTYPE;
+    if (!(t->flags & APEXW_FLAG_DENSE16) && (!t->m_scale || !t->v_scale)) return APEXW_ERR_ARG;
+  } else {
+    return APEXW_ERR_ARG;
+  }
+  if (!(t->flags & APEXW_FLAG_SCALAR)) {
+    const uintptr_t a = (uintptr_t)t->p | (uintptr_t)t->g | (uintptr_t)t->m | (uintptr_t)t->v;
+    if (a & 15u) return APEXW_ERR_ALIGN;
+  }
+  return APEXW_OK;
+}
+
+int apexw_compact_step(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,
+                       const apexw_hparams* hp, void* stream) {
+  if (!tensors || !units || n_tensors <= 0 || n_units < 0 || !hp_ok(hp)) return APEXW_ERR_ARG;
+  if (n_units == 0) return APEXW_OK;
+  return apexw_launch_compact(tensors, n_units, units, hp, persistent_grid(n_units, 8), (hipStream_t)stream);
+}
+
+int apexw_q8_step(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,
+                  const apexw_hparams* hp, void* stream) {
+  if (!tensors || !units || n_tensors <= 0 || n_units < 0 || !hp_ok(hp)) return APEXW_ERR_ARG;
+  if (hp->mode == APEXW_MODE_NATIVE) return APEXW_ERR_ARG;
+  if (n_units == 0) return APEXW_OK;
+  return apexw_launch_q8(tensors, n_units, units, hp, persistent_grid(n_units, 8), (hipStream_t)stream);
+}
+
+int apexw_grad_clip_coef(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,
+                         int64_t unit_size, const int64_t* unit_begin, float* unit_partial, float* tensor_norm,
+                         float clip, uint32_t flags, float* coef, void* stream) {
+  if (!tensors || !units || !unit_begin || !unit_partial || !tensor_norm || !coef) return APEXW_ERR_ARG;
+  if (n_tensors <= 0 || n_units < 0 || unit_size < 0 || !(clip > 0.0f)) return APEXW_ERR_ARG;
+  return apexw_launch_clip(tensors, n_tensors, units, n_units, unit_size, unit_begin, unit_partial, tensor_norm, clip,
+                           flags, coef, persistent_grid(n_units, 8), persistent_grid(n_tensors, 8),
+                           (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,271 @@
+// Compact-precision fused multi-tensor AdamW step (gfx950).
+//
+// One launch covers every tensor of a parameter group.  The chunk table splits
+// tensors into units of APEXW_COMPACT_UNIT (2048) elements; each wavefront takes
+// units in a grid-stride loop, so a launch of a few thousand workgroups keeps
+// all 256 CUs busy whatever the tensor sizes.  A lane owns 4 groups of 8
+// consecutive elements (16-byte loads for bf16, 2x16-byte for fp32) spaced one
+// wave-width apart, so every load/store instruction of a wave touches one
+// contiguous 1-2 KiB span.
+//
+// The arithmetic restates the reference's CPU op sequence (rounding to the
+// storage dtype after each torch op):
+//   cold   = ApexW._multi_tensor_step   (apexw/optimizer.py:5297-5887)
+//   replay = FastExecutionPlan.execute_foreach (apexw/optimizer.py:1069-1341)
+//   native = torch._fused_adamw_ as called by _fused_step (apexw/optimizer.py:4737-4835)
+#include "common.h"
+
+namespace {
+
+constexpr int kWaves = 4;        // wavefronts per workgroup
+constexpr int kGroups = 4;       // 8-element groups per lane per unit
+
+struct Ctx {
+  const apexw_hparams* hp;
+  float coef;
+  uint32_t key;
+  uint32_t tflags;
+};
+
+template <int GD> APEXW_DEV float prep_grad(float g, const Ctx& c) {
+  if (c.hp->flags & APEXW_HP_SANITIZE) g = sanitize<GD>(g);
+  if (c.hp->flags & APEXW_HP_CLIP) g = rnd<GD>(g * c.coef);
+  return g;
+}
+
+// p, g, m: 8 elements; v: 8 entries (non-quad) or 2 (quad).  cnt <= 8 valid.
+// e0 is the element index of slot 0 within the tensor (RNG counter).
+template <int PD, int GD, int MD, int VD, bool QUAD>
+APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8], int cnt,
+                       uint32_t e0, const Ctx& c) {
+  const apexw_hparams& hp = *c.hp;
+  const bool sr = hp.flags & APEXW_HP_SR;
+  const bool srv = hp.flags & APEXW_HP_SR_V;
+  const bool wd = c.tflags & APEXW_FLAG_WD;
+  uint32_t rnd_bits[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) rnd_bits[j] = (sr || srv) ? rng_at(c.key, e0 + (uint32_t)j) : 0u;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) g[j] = prep_grad<GD>(g[j], c);
+
+  if (hp.mode == APEXW_MODE_NATIVE) {
+    // torch._fused_adamw_: fp32 math on loaded values, one rounding per stored tensor.
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float pf = wd ? p[j] * hp.wd_factor : p[j];
+      float mf = (hp.flags & APEXW_HP_LERP_HI) ? fmaf(hp.lerp_coef, g[j] - m[j], g[j])
+                                                : fmaf(hp.lerp_coef, g[j] - m[j], m[j]);
+      float vf = v[j] * hp.beta2 + (hp.one_minus_beta2 * g[j]) * g[j];
+      float den = sqrtf(vf) / hp.bc2_sqrt + hp.eps;
+      pf = pf - (hp.step_size * mf) / den;
+      p[j] = rnd<PD>(pf);
+      m[j] = rnd<MD>(mf);
+      v[j] = rnd<VD>(vf);
+    }
+    return;
+  }
+
+  // Same-dtype foreach ops with a Python scalar (_foreach_mul_, _foreach_add_)
+  // round the scalar to the tensor dtype first on torch's CPU path, so the
+  // 16-bit tensors see bf16(beta1), bf16(beta2), bf16(1 - lr*wd), bf16(eps).
+  const float wd_p = rnd<PD>(hp.wd_factor), b1_m = rnd<MD>(hp.beta1), b2_v = rnd<VD>(hp.beta2);
+  const float eps_v = rnd<VD>(hp.eps_scaled);
+  if (wd) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) p[j] = rnd<PD>(p[j] * wd_p);
+  }
+  // first moment: cold = mul then add-with-alpha (two roundings); replay with
+  // matching grad/moment dtypes = one lerp.
+  if (hp.mode == APEXW_MODE_REPLAY && GD == MD) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float d = g[j] - m[j];
+      m[j] = rnd<MD>((hp.flags & APEXW_HP_LERP_HI) ? fmaf(hp.lerp_coef, d, g[j]) : fmaf(hp.lerp_coef, d, m[j]));
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float m1 = rnd<MD>(m[j] * b1_m);
+      m[j] = rnd<MD>(fmaf(hp.one_minus_beta1, g[j], m1));
+    }
+  }
+  const bool p16 = PD != APEXW_F32;
+  if constexpr (QUAD) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      if (4 * q >= cnt) break;
+      const int b = 4 * q;
+      float s = g[b] * g[b];
+      s = s + g[b + 1] * g[b + 1];
+      s = s + g[b + 2] * g[b + 2];
+      s = s + g[b + 3] * g[b + 3];
+      const float gq = s * 0.25f;
+      float vq;
+      if (srv) {
+        vq = sr_round<VD>(fmaf(hp.one_minus_beta2, gq, v[q] * hp.beta2), rnd_bits[b] >> 16);
+      } else {
+        float v1 = rnd<VD>(v[q] * b2_v);
+        vq = rnd<VD>(fmaf(hp.one_minus_beta2, gq, v1));
+      }
+      v[q] = vq;
+      float den = rnd<VD>(sqrtf(vq));
+      den = rnd<VD>(den + eps_v);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int j = b + i;
+        const float delta = (m[j] / den) * hp.step_size;
+        const float x = p[j] - delta;
+        p[j] = !p16 ? x : (sr ? sr_round<PD>(x, rnd_bits[j]) : rnd<PD>(x));
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float vf;
+      if (srv) {
+        vf = sr_round<VD>(fmaf(hp.one_minus_beta2 * g[j], g[j], v[j] * hp.beta2), rnd_bits[j] >> 16);
+      } else {
+        float v1 = rnd<VD>(v[j] * b2_v);
+        vf = rnd<VD>(fmaf(hp.one_minus_beta2 * g[j], g[j], v1));
+      }
+      v[j] = vf;
+      float den = rnd<VD>(sqrtf(vf));
+      den = rnd<VD>(den + eps_v);
+      if (!p16) {
+        p[j] = p[j] + (-hp.step_size * m[j]) / den;
+      } else if (sr) {
+        p[j] = sr_round<PD>(p[j] - (m[j] / den) * hp.step_size, rnd_bits[j]);
+      } else if (hp.mode == APEXW_MODE_REPLAY) {
+        p[j] = rnd<PD>(p[j] - (m[j] / den) * hp.step_size);
+      } else {
+        p[j] = rnd<PD>(p[j] + (-hp.step_size * m[j]) / den);
+      }
+    }
+  }
+}
+
+template <int PD, int MD, int VD, bool QUAD>
+APEXW_DEV void compact_unit(const apexw_tensor& t, int64_t start, const Ctx& c) {
+  constexpr int GD = PD;
+  const int64_t n = t.n;
+  const int lane = lane_id();
+  const bool vec = !(c.tflags & APEXW_FLAG_SCALAR);
+#pragma unroll
+  for (int k = 0; k < kGroups; ++k) {
+    const int64_t e0 = start + (int64_t)(k * 64 + lane) * 8;
+    if (e0 >= n) break;
+    const int cnt = (int)((n - e0) < 8 ? (n - e0) : 8);
+    float p[8], g[8], m[8], v[8];
+    const bool full = vec && cnt == 8;
+    if (full) {
+      load8<PD>(t.p, e0, p);
+      load8<GD>(t.g, e0, g);
+      load8<MD>(t.m, e0, m);
+      if constexpr (QUAD) {
+        if constexpr (VD == APEXW_F32) {
+          const u32x2 w = __builtin_nontemporal_load((const u32x2*)((const float*)t.v + (e0 >> 2)));
+          v[0] = __uint_as_float(w.x);
+          v[1] = __uint_as_float(w.y);
+        } else {
+          const uint32_t w = __builtin_nontemporal_load((const uint32_t*)((const uint16_t*)t.v + (e0 >> 2)));
+          v[0] = VD == APEXW_BF16 ? bf16_bits_to_f32(w & 0xFFFFu) : f16_bits_to_f32(w & 0xFFFFu);
+          v[1] = VD == APEXW_BF16 ? __uint_as_float(w & 0xFFFF0000u) : f16_bits_to_f32(w >> 16);
+        }
+      } else {
+        load8<VD>(t.v, e0, v);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const bool ok = j < cnt;
+        p[j] = ok ? load1<PD>(t.p, e0 + j) : 0.0f;
+        g[j] = ok ? load1<GD>(t.g, e0 + j) : 0.0f;
+        m[j] = ok ? load1<MD>(t.m, e0 + j) : 0.0f;
+        if constexpr (!QUAD) v[j] = ok ? load1<VD>(t.v, e0 + j) : 0.0f;
+      }
+      if constexpr (QUAD) {
+        v[0] = cnt >= 4 ? load1<VD>(t.v, e0 >> 2) : 0.0f;
+        v[1] = cnt >= 8 ? load1<VD>(t.v, (e0 >> 2) + 1) : 0.0f;
+      }
+    }
+    update8<PD, GD, MD, VD, QUAD>(p, g, m, v, cnt, (uint32_t)e0, c);
+    if (full) {
+      store8<PD>(t.p, e0, p);
+      store8<MD>(t.m, e0, m);
+      if constexpr (QUAD) {
+        if constexpr (VD == APEXW_F32) {
+          u32x2 w = {__float_as_uint(v[0]), __float_as_uint(v[1])};
+          __builtin_nontemporal_store(w, (u32x2*)((float*)t.v + (e0 >> 2)));
+        } else {
+          const uint32_t lo = VD == APEXW_BF16 ? (__float_as_uint(v[0]) >> 16) : f32_to_f16_bits(v[0]);
+          const uint32_t hi = VD == APEXW_BF16 ? (__float_as_uint(v[1]) >> 16) : f32_to_f16_bits(v[1]);
+          __builtin_nontemporal_store(lo | (hi << 16), (uint32_t*)((uint16_t*)t.v + (e0 >> 2)));
+        }
+      } else {
+        store8<VD>(t.v, e0, v);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (j < cnt) {
+          store1<PD>(t.p, e0 + j, p[j]);
+          store1<MD>(t.m, e0 + j, m[j]);
+          if constexpr (!QUAD) store1<VD>(t.v, e0 + j, v[j]);
+        }
+      }
+      if constexpr (QUAD) {
+        if (cnt >= 4) store1<VD>(t.v, e0 >> 2, v[0]);
+        if (cnt >= 8) store1<VD>(t.v, (e0 >> 2) + 1, v[1]);
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void compact_step_kernel(const apexw_tensor* __restrict__ tensors,
+                                                           const apexw_unit* __restrict__ units,
+                                                           int64_t n_units, apexw_hparams hp) {
+  const uint32_t wave = uniform(threadIdx.x >> 6);
+  Ctx c;
+  c.hp = &hp;
+  c.coef = (hp.flags & APEXW_HP_CLIP) ? *hp.clip_coef : 1.0f;
+  const int64_t stride = (int64_t)gridDim.x * kWaves;
+  for (int64_t u = (int64_t)blockIdx.x * kWaves + wave; u < n_units; u += stride) {
+    const apexw_unit un = units[u];
+    const apexw_tensor& t = tensors[un.tensor];
+    const int64_t start = (int64_t)un.unit * APEXW_COMPACT_UNIT;
+    c.tflags = t.flags;
+    c.key = rng_key(hp.seed, un.tensor, hp.step, 0u, (uint32_t)(start >> 32));
+    const uint32_t pd = (t.flags >> APEXW_FLAG_PDT_SHIFT) & 3u;
+    const uint32_t vd = (t.flags >> APEXW_FLAG_VDT_SHIFT) & 3u;
+    const bool quad = t.flags & APEXW_FLAG_QUAD;
+    if (pd == APEXW_F32) {
+      if (vd == APEXW_F32) compact_unit<APEXW_F32, APEXW_BF16, APEXW_F32, false>(t, start, c);
+      else if (quad) compact_unit<APEXW_F32, APEXW_BF16, APEXW_BF16, true>(t, start, c);
+      else compact_unit<APEXW_F32, APEXW_BF16, APEXW_BF16, false>(t, start, c);
+    } else {
+      if (vd == APEXW_F32) compact_unit<APEXW_BF16, APEXW_BF16, APEXW_F32, false>(t, start, c);
+      else if (quad) compact_unit<APEXW_BF16, APEXW_BF16, APEXW_BF16, true>(t, start, c);
+      else compact_unit<APEXW_BF16, APEXW_BF16, APEXW_BF16, false>(t, start, c);
+    }
+  }
+}
+
+}  // namespace
+
+// Host-side validation of the dtype combinations this kernel instantiates.
+static bool compact_combo_ok(uint32_t flags) {
+  const uint32_t pd = (flags >> APEXW_FLAG_PDT_SHIFT) & 3u, gd = (flags >> APEXW_FLAG_GDT_SHIFT) & 3u;
+  const uint32_t md = (flags >> APEXW_FLAG_MDT_SHIFT) & 3u, vd = (flags >> APEXW_FLAG_VDT_SHIFT) & 3u;
+  if (!(pd == APEXW_F32 || pd == APEXW_BF16) || gd != pd || md != APEXW_BF16) return false;
+  if (!(vd == APEXW_F32 || vd == APEXW_BF16)) return false;
+  if ((flags & APEXW_FLAG_QUAD) && vd != APEXW_BF16) return false;
+  return true;
+}
+
+int apexw_launch_compact(const apexw_tensor* tensors, int64_t n_units, const apexw_unit* units,
+                         const apexw_hparams* hp, int grid, hipStream_t stream) {
+  hipLaunchKernelGGL(compact_step_kernel, dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
+  return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
+}
+
+bool apexw_compact_flags_ok(uint32_t flags) { return compact_combo_ok(flags); }

@@ -1,0 +1,111 @@
+// Global-L2 gradient clip coefficient on the device (gfx950).
+//
+// Restates the clip of _prepare_grads (apexw/optimizer.py:242-256) without the
+// host synchronisation: per-tensor norms (torch._foreach_norm rounds each norm
+// to the grad dtype), the L2 norm of those norms, and
+// coef = min(clip / (total + 1e-6), 1).  The step kernels read the coefficient
+// from device memory and scale the grads in registers.
+//
+// Three short launches, deterministic (no atomics):
+//   1. one wavefront per work unit of the chunk table -> sum of squares
+//   2. one wavefront per tensor sums its (contiguous) units -> rounded norm
+//   3. one workgroup combines the tensor norms -> coefficient
+#include "common.h"
+
+namespace {
+
+template <int GD>
+APEXW_DEV float unit_sumsq(const apexw_tensor& t, int64_t start, int64_t cnt, bool san) {
+  const int lane = lane_id();
+  const bool vec = !(t.flags & APEXW_FLAG_SCALAR) && (start % 8) == 0;
+  float acc = 0.0f;
+  for (int64_t rel = (int64_t)lane * 8; rel < cnt; rel += 64 * 8) {
+    const int64_t e0 = start + rel;
+    const int c = (cnt - rel) < 8 ? (int)(cnt - rel) : 8;
+    float g[8];
+    if (vec && c == 8) {
+      load8<GD>(t.g, e0, g);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) g[j] = j < c ? load1<GD>(t.g, e0 + j) : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float x = san ? sanitize<GD>(g[j]) : g[j];
+      acc = fmaf(x, x, acc);
+    }
+  }
+  return wave_sum(acc);
+}
+
+__global__ __launch_bounds__(256) void sumsq_kernel(const apexw_tensor* __restrict__ tensors,
+                                                    const apexw_unit* __restrict__ units, int64_t n_units,
+                                                    int64_t unit_size, float* __restrict__ partial, uint32_t flags) {
+  const uint32_t wave = uniform(threadIdx.x >> 6);
+  const int64_t stride = (int64_t)gridDim.x * 4;
+  const bool san = flags & APEXW_HP_SANITIZE;
+  for (int64_t u = (int64_t)blockIdx.x * 4 + wave; u < n_units; u += stride) {
+    const apexw_unit un = units[u];
+    const apexw_tensor& t = tensors[un.tensor];
+    const int64_t us = unit_size > 0 ? unit_size : (t.block > 0 ? (int64_t)t.block : 64);
+    const int64_t start = (int64_t)un.unit * us;
+    const int64_t cnt = (t.n - start) < us ? (t.n - start) : us;
+    const uint32_t gd = (t.flags >> APEXW_FLAG_GDT_SHIFT) & 3u;
+    float s;
+    if (gd == APEXW_F32) s = unit_sumsq<APEXW_F32>(t, start, cnt, san);
+    else if (gd == APEXW_BF16) s = unit_sumsq<APEXW_BF16>(t, start, cnt, san);
+    else s = unit_sumsq<APEXW_F16>(t, start, cnt, san);
+    if (lane_id() == 0) partial[u] = s;
+  }
+}
+
+__global__ __launch_bounds__(256) void tensor_norm_kernel(const apexw_tensor* __restrict__ tensors, int32_t n_tensors,
+                                                          const int64_t* __restrict__ unit_begin,
+                                                          const float* __restrict__ partial, float* __restrict__ norm) {
+  const uint32_t wave = uniform(threadIdx.x >> 6);
+  const int64_t stride = (int64_t)gridDim.x * 4;
+  for (int64_t t = (int64_t)blockIdx.x * 4 + wave; t < n_tensors; t += stride) {
+    float acc = 0.0f;
+    for (int64_t u = unit_begin[t] + lane_id(); u < unit_begin[t + 1]; u += 64) acc += partial[u];
+    acc = wave_sum(acc);
+    const uint32_t gd = (tensors[t].flags >> APEXW_FLAG_GDT_SHIFT) & 3u;
+    float nrm = sqrtf(acc);
+    nrm = gd == APEXW_BF16 ? rnd<APEXW_BF16>(nrm) : (gd == APEXW_F16 ? rnd<APEXW_F16>(nrm) : nrm);
+    if (lane_id() == 0) norm[t] = nrm;
+  }
+}
+
+__global__ __launch_bounds__(1024) void clip_coef_kernel(const float* __restrict__ norm, int32_t n_tensors, float clip,
+                                                         float* __restrict__ coef) {
+  __shared__ float s_part[16];
+  float acc = 0.0f;
+  for (int32_t t = threadIdx.x; t < n_tensors; t += blockDim.x) acc = fmaf(norm[t], norm[t], acc);
+  acc = wave_sum(acc);
+  if (lane_id() == 0) s_part[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float tot = 0.0f;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) tot += s_part[w];
+    const float total = sqrtf(tot);
+    float c = clip / (total + 1e-6f);
+    // torch.clamp(c, max=1) then "multiply only if c < 1": NaN / >= 1 leave grads unscaled
+    coef[0] = (c < 1.0f) ? c : 1.0f;
+  }
+}
+
+}  // namespace
+
+int apexw_launch_clip(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,
+                      int64_t unit_size, const int64_t* unit_begin, float* unit_partial, float* tensor_norm,
+                      float clip, uint32_t flags, float* coef, int grid_units, int grid_tensors, hipStream_t stream) {
+  if (n_units > 0) {
+    hipLaunchKernelGGL(sumsq_kernel, dim3(grid_units), dim3(256), 0, stream, tensors, units, n_units, unit_size,
+                       unit_partial, flags);
+  }
+  if (n_tensors > 0) {
+    hipLaunchKernelGGL(tensor_norm_kernel, dim3(grid_tensors), dim3(256), 0, stream, tensors, n_tensors, unit_begin,
+                       unit_partial, tensor_norm);
+  }
+  hipLaunchKernelGGL(clip_coef_kernel, dim3(1), dim3(1024), 0, stream, tensor_norm, n_tensors, clip, coef);
+  return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
+}

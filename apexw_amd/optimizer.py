@@ -1,0 +1,260 @@
+"""ApexW: the optimizer front end (drop-in for the reference ``apexw.ApexW``).
+
+Same constructor (33 keyword arguments in the reference's positional order,
+apexw/optimizer.py:1632-1668), defaults, argument validation and precision
+aliases; same ``state`` keys and dtypes, ``state_dict()`` /
+``load_state_dict()`` schema, and ``use_muon=True`` / ``precision="hybrid"``
+routing to ``HybridApexW`` (apexw/optimizer.py:1593-1617).
+
+The step itself runs on the GPU through libapexw_hip.so: one fused
+multi-tensor kernel launch per parameter group and step (plus three tiny
+launches when global-norm clipping is on).  There is no CPU or torch-op
+fallback; options outside the hot path raise ``NotImplementedError`` at
+construction.
+"""
+
+import math
+import warnings
+
+import torch
+import torch.nn as nn
+from torch.optim.optimizer import Optimizer
+
+from . import state as S
+from ._plan import StepPlan
+
+_UNSUPPORTED_FLAGS = ("amsgrad", "nesterov", "cautious", "grad_centralization", "lion", "maximize",
+                      "capturable", "differentiable", "auto_pack", "factored_v", "six_bit")
+
+
+class ApexW(Optimizer):
+    """Memory-efficient AdamW with compact (bf16) or 8-bit (NF4 + log-uint8) state.
+
+    precision="compact": bf16 first moment, bf16 (or fp32) second moment,
+    quad-shared v for large tensors.  precision="8bit": NF4 momentum + quad
+    log-uint8 variance with per-block fp32 scales (INT8 + uint8 for small
+    tensors).  Weight decay is decoupled; ``adamw_compat=True`` decays every
+    tensor and maps betas (0.9, 0.95)/(0.9, 0.99) to (0.9, 0.999).
+    """
+
+    _step_supports_amp_scaling = True
+
+    def __new__(cls, *args, **kwargs):
+        first = args[0] if args else kwargs.get("params")
+        use_muon = kwargs.get("use_muon", args[26] if len(args) > 26 else False)
+        prec = kwargs.get("precision", args[16] if len(args) > 16 else None)
+        hybrid = bool(use_muon) or (isinstance(prec, str) and prec.lower().strip() in S.HYBRID_ALIASES)
+        if hybrid:
+            from .hybrid import HybridApexW
+            a = list(args)
+            kw = dict(kwargs)
+            kw.pop("use_muon", None)
+            if len(a) > 26:
+                a.pop(26)
+            if isinstance(kw.get("precision"), str) and kw["precision"].lower().strip() in S.HYBRID_ALIASES:
+                kw["precision"] = "compact"
+            if len(a) > 16 and isinstance(a[16], str) and a[16].lower().strip() in S.HYBRID_ALIASES:
+                a[16] = "compact"
+            return HybridApexW(*a, **kw)
+        if isinstance(first, nn.Module):
+            for name, p in first.named_parameters():
+                if not hasattr(p, "_param_name"):
+                    setattr(p, "_param_name", name)
+        return super().__new__(cls)
+
+    def __init__(self, params, lr=1e-3, betas=None, eps=1e-8, weight_decay=1e-2, amsgrad=False,
+                 nesterov=False, cautious=False, grad_centralization=False, decay_norm_only=True,
+                 adamw_compat=False, clip_grad_norm=None, beta3=None, alpha=5.0, lion=False, fused=None,
+                 precision="compact", threshold=65536, maximize=False, foreach=None, capturable=False,
+                 dynamic_scaling=True, differentiable=False, backend=None, auto_pack=False,
+                 pack_threshold=50000, use_muon=False, amp=None, stochastic_rounding=True, block_size=None,
+                 force_compact_v=False, factored_v=False, int4_m=None, six_bit=False):
+        precision = S.normalize_precision(precision)
+        if precision == "hybrid":
+            precision = "compact"
+        if betas is None:
+            betas = (0.9, 0.999) if precision in ("8bit", "full") else (0.9, 0.99)
+        if isinstance(params, nn.Module):
+            for name, p in params.named_parameters():
+                if not hasattr(p, "_param_name"):
+                    setattr(p, "_param_name", name)
+            trainable = [p for p in params.parameters() if p.requires_grad]
+            params = trainable if trainable else list(params.parameters())
+        if differentiable:
+            raise NotImplementedError("ApexW does not currently support differentiable=True.")
+        if not 0.0 <= lr:
+            raise ValueError(f"Invalid learning rate: {lr}")
+        if not 0.0 <= eps:
+            raise ValueError(f"Invalid epsilon value: {eps}")
+        if not 0.0 <= betas[0] < 1.0:
+            raise ValueError(f"Invalid beta1 parameter: {betas[0]}")
+        if not 0.0 <= betas[1] < 1.0:
+            raise ValueError(f"Invalid beta2 parameter: {betas[1]}")
+        if len(betas) > 2 and beta3 is None:
+            beta3 = betas[2]
+        if beta3 is not None and not 0.0 <= beta3 < 1.0:
+            raise ValueError(f"Invalid beta3 parameter: {beta3}")
+        if not 0.0 <= weight_decay:
+            raise ValueError(f"Invalid weight_decay value: {weight_decay}")
+        if clip_grad_norm is not None and clip_grad_norm <= 0.0:
+            raise ValueError(f"Invalid clip_grad_norm value: {clip_grad_norm}")
+        if block_size is not None and (isinstance(block_size, bool) or not isinstance(block_size, int) or block_size <= 0):
+            raise ValueError(f"Invalid block_size value: {block_size}. Must be a positive integer.")
+        if threshold <= 0:
+            raise ValueError(f"Invalid threshold value: {threshold}. Must be positive.")
+        if alpha < 0.0:
+            raise ValueError(f"Invalid alpha value: {alpha}")
+        if backend is not None and backend not in ("auto", "triton", "cuda", "mps", "foreach", "_multi_tensor", "xla"):
+            raise ValueError(f"Invalid backend '{backend}'. Must be 'auto', 'triton', 'cuda', 'mps', 'foreach', or 'xla'.")
+        if adamw_compat:
+            decay_norm_only = False
+            if tuple(betas[:2]) in ((0.9, 0.95), (0.9, 0.99)):
+                betas = (0.9, 0.999)
+        opts = dict(amsgrad=amsgrad, nesterov=nesterov, cautious=cautious, grad_centralization=grad_centralization,
+                    lion=lion, maximize=maximize, capturable=capturable, differentiable=differentiable,
+                    auto_pack=auto_pack, factored_v=factored_v, six_bit=six_bit)
+        bad = [k for k in _UNSUPPORTED_FLAGS if opts[k]]
+        if bad or beta3 is not None or precision not in ("compact", "8bit"):
+            what = ", ".join(bad + (["beta3"] if beta3 is not None else [])
+                             + ([f"precision={precision!r}"] if precision not in ("compact", "8bit") else []))
+            raise NotImplementedError(f"apexw_amd implements the compact and 8-bit AdamW step; not supported: {what}")
+        if precision == "compact" and betas[1] >= 0.99 and not stochastic_rounding and not adamw_compat:
+            warnings.warn(
+                f"ApexW: beta2={betas[1]} with precision='compact' and stochastic_rounding=False "
+                f"{'stores exp_avg_sq in float32' if betas[1] >= S.BETA2_V_FP32_THRESHOLD else 'may lose bf16 second-moment precision'}.",
+                UserWarning, stacklevel=2)
+        defaults = dict(lr=lr, betas=(betas[0], betas[1]), eps=eps, weight_decay=weight_decay, amsgrad=amsgrad,
+                        nesterov=nesterov, cautious=cautious, grad_centralization=grad_centralization,
+                        decay_norm_only=decay_norm_only, clip_grad_norm=clip_grad_norm, beta3=beta3, alpha=alpha,
+                        lion=lion, fused=fused, precision=precision, threshold=threshold, maximize=maximize,
+                        foreach=foreach, capturable=capturable, dynamic_scaling=dynamic_scaling,
+                        differentiable=differentiable, backend=backend, auto_pack=auto_pack,
+                        pack_threshold=pack_threshold, amp=amp, stochastic_rounding=stochastic_rounding,
+                        block_size=block_size, force_compact_v=force_compact_v, factored_v=factored_v,
+                        int4_m=int4_m, six_bit=six_bit)
+        super().__init__(params, defaults)
+        self._plans = {}
+        # seed of the counter-based rounding RNG (drawn from torch's generator, so
+        # torch.manual_seed makes runs reproducible)
+        self._seed = int(torch.randint(0, 2 ** 62, (1,)).item())
+
+    def __setstate__(self, state):
+        super().__setstate__(state)
+        for group in self.param_groups:
+            group.setdefault("decay_norm_only", True)
+            group.setdefault("clip_grad_norm", None)
+            group.setdefault("precision", "compact")
+            group.setdefault("stochastic_rounding", True)
+            group.setdefault("force_compact_v", False)
+            group.setdefault("int4_m", False)
+        self._plans = {}
+
+    # ------------------------------------------------------------------ step
+    @torch.no_grad()
+    def step(self, closure=None):
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+        found_inf = getattr(self, "found_inf", None)
+        if found_inf is not None and float(found_inf.item()) > 0:
+            return loss
+        if getattr(self, "grad_scale", None) is not None:
+            raise NotImplementedError("GradScaler unscaling inside step() is not supported; unscale first")
+        for group in self.param_groups:
+            gid = id(group)
+            plan = self._plans.get(gid)
+            if plan is not None and plan.valid_for(group):
+                plan.execute(group, self._seed)
+                continue
+            self._plans.pop(gid, None)
+            plan = self._build_plan(group)
+            if plan is None:
+                continue
+            plan.execute(group, self._seed)
+            self._plans[gid] = plan
+        return loss
+
+    def _build_plan(self, group):
+        group["precision"] = S.normalize_precision(group.get("precision", "compact"))
+        params = []
+        for p in group["params"]:
+            if p.grad is None:
+                continue
+            if p.grad.is_sparse:
+                raise RuntimeError("ApexW does not support sparse gradients")
+            if torch.is_complex(p) or p.dtype not in (torch.float32, torch.bfloat16):
+                raise NotImplementedError(f"apexw_amd steps fp32/bf16 parameters, got {p.dtype}")
+            if p.device.type != "cuda":
+                raise RuntimeError("apexw_amd runs the optimizer step on the GPU; parameters must be on cuda")
+            params.append(p)
+        if not params:
+            return None
+        peft = S.detect_peft_context(self.param_groups)
+        for p in params:
+            if len(self.state[p]) == 0:
+                self.state[p].update(S.init_state(p, group, peft))
+        if group["precision"] == "8bit":
+            return StepPlan(self, group, params, "q8")
+        sts = [self.state[p] for p in params]
+        homogeneous = all(st["exp_avg"].dtype == st["exp_avg_sq"].dtype == p.dtype
+                          and st["exp_avg"].numel() == st["exp_avg_sq"].numel() for p, st in zip(params, sts))
+        return StepPlan(self, group, params, "compact", native=homogeneous)
+
+    # ------------------------------------------------------------------ checkpoints
+    def state_dict(self):
+        sd = super().state_dict()
+        meta = {}
+        for p, s in self.state.items():
+            if "scale_v" in s:
+                meta[id(p)] = {"scale_v": s["scale_v"], "sqrt_scale_v": s.get("sqrt_scale_v", math.sqrt(s["scale_v"]))}
+        sd["_dynamic_scaling_meta"] = meta
+        return sd
+
+    def load_state_dict(self, state_dict):
+        """Load, then restore every state tensor in its saved dtype (the base loader
+        casts floating state to the parameter dtype)."""
+        sd = dict(state_dict)
+        sd.pop("_dynamic_scaling_meta", None)
+        saved = sd.get("state", {})
+        origin = {}
+        for sg, g in zip(sd.get("param_groups", []), self.param_groups):
+            for pid, p in zip(sg.get("params", ()), g["params"]):
+                if pid in saved:
+                    origin[p] = saved[pid]
+        super().load_state_dict(sd)
+        for p, s in self.state.items():
+            src = origin.get(p, {})
+            for k, v in src.items():
+                if torch.is_tensor(v) and k != "step":
+                    s[k] = v.detach().to(device=p.device).clone()
+        self._plans = {}
+
+    def zero_grad(self, set_to_none=True):
+        super().zero_grad(set_to_none=set_to_none)
+
+    # ------------------------------------------------------------------ reporting
+    def get_state_memory_mb(self):
+        total = 0
+        for st in self.state.values():
+            for k, v in st.items():
+                if torch.is_tensor(v) and k != "step":
+                    total += v.numel() * v.element_size()
+        return total / (1024 * 1024)
+
+    def get_memory_summary(self):
+        n = sum(p.numel() for g in self.param_groups for p in g["params"])
+        mb = self.get_state_memory_mb()
+        adamw_mb = n * 8 / (1024 * 1024)
+        return {"num_params": n, "state_mb": mb, "adamw_state_mb": adamw_mb,
+                "bytes_per_param": (mb * 1024 * 1024 / n) if n else 0.0,
+                "savings_pct": (100.0 * (1 - mb / adamw_mb)) if adamw_mb else 0.0}
+
+    def print_summary(self):
+        s = self.get_memory_summary()
+        print(f"ApexW: {s['num_params']:,} params, state {s['state_mb']:.2f} MB "
+              f"({s['bytes_per_param']:.3f} B/param) vs AdamW {s['adamw_state_mb']:.2f} MB "
+              f"({s['savings_pct']:.1f}% saved)")
+
+    def __repr__(self):
+        return f"ApexW(precision={self.defaults['precision']!r}, lr={self.defaults['lr']})"

@@ -1,0 +1,171 @@
+"""Optimizer-state layout rules and precision resolution for ApexW.
+
+Decides, per parameter, how its moments are stored -- the decisions of the
+reference's ``ApexW._init_group`` (apexw/optimizer.py:2574-2957) and resolvers
+(apexw/state.py:62-162):
+
+compact:
+  * m in bf16 (fp16 for fp16 params); v in the same dtype, or fp32 when
+    stochastic rounding is off and beta2 >= 0.995;
+  * quad-v (one v per 4 consecutive elements, numel/4 entries) when m and v are
+    16-bit, numel >= 16384, numel % 4 == 0, 1-D or min(shape) >= 8, and the
+    group has >= 8 parameters (or the model is a PEFT/LoRA model).
+8bit (numel >= 64):
+  * block size: user value, else 128/64 for narrow 2-D tensors (min dim <= 32,
+    numel < 2048), else 2048 halving down to 64;
+  * NF4 m (2 codes per byte) + quad log-uint8 v when numel >= 16384,
+    numel % 4 == 0, power-of-two block >= 64 and min(shape) >= 8; otherwise
+    INT8 m + full-size log-uint8 v; fp32 scales per block;
+  * tensors under 64 elements keep compact 16-bit m/v.
+Initial state: NF4 bytes 0x77 (both codes = 0.0), m scales 1e-12 (INT8: 1e-12/127),
+v codes 0 with scales 1e-12.
+"""
+
+import torch
+
+BETA2_V_FP32_THRESHOLD = 0.995
+
+_ALIASES = {
+    "full": ("full", "fp32", "float32", "float", "fp64", "float64", "double"),
+    "compact": ("compact", "bf16", "bfloat16", "fp16", "float16", "half", "16", "16-bit"),
+    "8bit": ("8bit", "8-bit", "int8", "uint8", "q8", "adamw_8bit", "bnb_8bit"),
+    "ultra": ("ultra", "ultra_stable", "3byte", "hybrid8"),
+    "hybrid": ("hybrid", "hybrid_apexw", "hybrid-apexw", "apex_hybrid", "hybrid_compact"),
+    "auto": ("auto", "smart", "adaptive"),
+}
+HYBRID_ALIASES = _ALIASES["hybrid"]
+
+
+def normalize_precision(precision):
+    """Precision aliases -> canonical name (apexw/state.py:94-121)."""
+    if isinstance(precision, torch.dtype):
+        if precision in (torch.float32, torch.float64):
+            return "full"
+        if precision in (torch.bfloat16, torch.float16):
+            return "compact"
+        if precision in (torch.int8, torch.uint8):
+            return "8bit"
+        return "full"
+    if isinstance(precision, str):
+        key = precision.lower().strip()
+        for name, aliases in _ALIASES.items():
+            if key in aliases:
+                return name
+    raise ValueError(
+        f"Invalid precision mode '{precision}'. Must be '8bit', 'compact', 'hybrid', 'ultra', 'auto', 'full', "
+        f"or a valid torch dtype (e.g. torch.float32, torch.bfloat16, torch.float16, torch.int8).")
+
+
+def is_peft_parameter(p):
+    """LoRA/adapter naming, or a thin 2-D matrix (min dim <= 64, max dim >= 256)."""
+    if getattr(p, "_is_lora", False):
+        return True
+    for attr in ("_param_name", "name"):
+        val = getattr(p, attr, None)
+        if isinstance(val, str):
+            low = val.lower()
+            if any(k in low for k in ("lora_a", "lora_b", "lora_embedding", "adapter", "lora_", "lora")):
+                return True
+    return p.dim() == 2 and min(p.shape) <= 64 and max(p.shape) >= 256
+
+
+def detect_peft_context(param_groups):
+    for g in param_groups:
+        for p in g.get("params", []):
+            if isinstance(p, torch.Tensor):
+                if is_peft_parameter(p):
+                    return True
+                if hasattr(p, "quant_state") or hasattr(p, "quant_type") or type(p).__name__ in ("Params4bit", "Linear4bit"):
+                    return True
+    return False
+
+
+def compact_dtype(p):
+    if p.dtype == torch.float16:
+        return torch.float16
+    return torch.bfloat16
+
+
+def v_dtype_for_beta2(cdt, beta2, force_compact_v=False, stochastic_rounding=True):
+    if force_compact_v:
+        return cdt
+    if not stochastic_rounding and cdt in (torch.bfloat16, torch.float16) and beta2 >= BETA2_V_FP32_THRESHOLD:
+        return torch.float32
+    return cdt
+
+
+def block_size_8bit(p, user_bs):
+    n = p.numel()
+    if user_bs is not None:
+        return int(user_bs)
+    if p.dim() >= 2 and min(p.shape) <= 32 and n < 2048:
+        return 128 if n >= 128 else 64
+    for bs in (2048, 1024, 512, 256, 128):
+        if n >= bs:
+            return bs
+    return 64
+
+
+def init_state(p, group, peft_ctx):
+    """Fresh state dict for ``p`` (keys and dtypes as the reference's _init_group)."""
+    prec = group["precision"]
+    beta2 = group["betas"][1]
+    sr = bool(group.get("stochastic_rounding", True))
+    dev = p.device
+    n = p.numel()
+    st = {"stochastic_rounding": sr, "step": torch.tensor(0.0, dtype=torch.float32)}
+    is_peft = is_peft_parameter(p) or peft_ctx
+    if prec == "8bit" and n >= 64:
+        bs = block_size_8bit(p, group.get("block_size"))
+        narrow = p.dim() >= 2 and min(p.shape) <= 32 and n < 2048
+        raw_int4 = group.get("int4_m", group.get("four_bit", None))
+        pow2 = bs >= 64 and (bs & (bs - 1)) == 0
+        auto_sub = (raw_int4 is not False and n >= 16384 and n % 4 == 0 and pow2
+                    and (p.dim() < 2 or min(p.shape) >= 8))
+        int4 = auto_sub or (bool(raw_int4) and n >= 512 and n >= bs and not narrow and not is_peft)
+        quad = bool(auto_sub and int4)
+        st.update(is_8bit=True, block_size_8bit=bs, is_factored_v=False, is_6bit_m=False,
+                  is_4bit_m=int4, is_quad_v=quad, m_numel=n)
+        st["state_dtype"] = torch.int8
+        st["state_dtype_v"] = torch.uint8
+        nblk = (n + bs - 1) // bs
+        if int4:
+            st["exp_avg"] = torch.full(((n + 1) // 2,), 0x77, dtype=torch.uint8, device=dev)
+            st["exp_avg_scales"] = torch.full((nblk, 1), 1e-12, dtype=torch.float32, device=dev)
+        else:
+            st["exp_avg"] = torch.zeros(p.shape, dtype=torch.int8, device=dev)
+            st["exp_avg_scales"] = torch.full((nblk, 1), 1e-12 / 127.0, dtype=torch.float32, device=dev)
+        if quad:
+            st["exp_avg_sq"] = torch.zeros((n // 4,), dtype=torch.uint8, device=dev)
+        else:
+            st["exp_avg_sq"] = torch.zeros(p.shape, dtype=torch.uint8, device=dev)
+        st["exp_avg_sq_scales"] = torch.full((nblk, 1), 1e-12, dtype=torch.float32, device=dev)
+        return st
+    if prec == "8bit":
+        st.update(is_8bit=False, is_factored_v=False, is_6bit_m=False, is_4bit_m=False, is_quad_v=False)
+    else:
+        st.update(is_6bit_m=False, is_4bit_m=False, is_factored_v=False)
+    mdt = compact_dtype(p)
+    vdt = v_dtype_for_beta2(mdt, beta2, group.get("force_compact_v", False), sr)
+    quad = (prec == "compact" and mdt in (torch.bfloat16, torch.float16) and vdt in (torch.bfloat16, torch.float16)
+            and group.get("int4_m", None) is not False and n >= 16384 and n % 4 == 0
+            and (p.dim() < 2 or min(p.shape) >= 8)
+            and (is_peft or len(group["params"]) >= 8))
+    if quad:
+        st["is_quad_v"] = True
+    st["state_dtype"] = mdt
+    st["state_dtype_v"] = vdt
+    st["exp_avg"] = torch.zeros(p.shape, dtype=mdt, device=dev)
+    if quad:
+        st["exp_avg_sq"] = torch.zeros((n // 4,), dtype=vdt, device=dev)
+    else:
+        st["exp_avg_sq"] = torch.zeros(p.shape, dtype=vdt, device=dev)
+    st["scale_v"] = 1.0
+    st["sqrt_scale_v"] = 1.0
+    return st
+
+
+def state_bytes_per_param(state, numel):
+    tot = sum(v.numel() * v.element_size() for k, v in state.items()
+              if isinstance(v, torch.Tensor) and k != "step")
+    return tot / max(numel, 1)

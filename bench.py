@@ -1,0 +1,200 @@
+"""Benchmark: the ApexW 8-bit optimizer step on a Llama-3-8B-shaped parameter set.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--config c3|c2|c4|c1] [--no-cpu]
+
+Prints ONE JSON line (rank 0).  A "step" is one ``ApexW.step()`` over the full
+parameter list with synthetic bf16 params ~N(0, 0.02) and grads ~N(0, 1e-3)
+already resident in HBM.  ``value`` is parameters updated per second.
+
+``roofline`` prices the fused step kernel against MI355X HBM bandwidth
+(8 TB/s): ``achieved`` = algorithmic bytes per launch (read + write of p, g,
+moment codes and block scales, computed from the actual state layout) divided
+by the average kernel time measured with HIP events on the launch stream.
+``cpu_baseline`` times the CPU oracle (the reference algorithm restated with
+torch CPU ops) on a bounded slice of the same workload on this host's cores.
+"""
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+METRIC = "optimizer params updated/sec + achieved HBM GB/s (% peak), 8B-param step"
+
+
+def llama3_8b_shapes():
+    s = [(128256, 4096)]
+    for _ in range(32):
+        s += [(4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (14336, 4096), (14336, 4096),
+              (4096, 14336), (4096,), (4096,)]
+    s += [(4096,), (128256, 4096)]
+    return s
+
+
+def gpt2_small_shapes():
+    s = [(50257, 768), (1024, 768)]
+    for _ in range(12):
+        s += [(768,), (768,), (768, 2304), (2304,), (768, 768), (768,), (768,), (768,),
+              (768, 3072), (3072,), (3072, 768), (768,)]
+    return s
+
+
+def ragged_shapes(n=20000, seed=2):
+    g = torch.Generator().manual_seed(seed)
+    lo, hi = math.log(64), math.log(2 ** 20)
+    sizes = torch.exp(torch.rand(n, generator=g, dtype=torch.float64) * (hi - lo) + lo).floor().long().tolist()
+    twod = (torch.rand(n, generator=g) < 0.5).tolist()
+    shapes = []
+    for sz, t in zip(sizes, twod):
+        if t and sz >= 64:
+            r = 8
+            while r * r < sz and sz % (r * 2) == 0:
+                r *= 2
+            shapes.append((r, sz // r) if sz % r == 0 else (sz,))
+        else:
+            shapes.append((sz,))
+    return shapes
+
+
+CONFIGS = {
+    "c1": dict(workload="C1 compact ApexW step, one fp32 tensor of 2^20", shapes=[(1 << 20,)], dtype=torch.float32,
+               kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True)),
+    "c2": dict(workload="C2 compact ApexW step, GPT-2-small (124M) bf16", shapes=gpt2_small_shapes(),
+               dtype=torch.bfloat16, kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True), per_tensor_scale=True),
+    "c3": dict(workload="C3 8-bit ApexW step, Llama-3-8B (8.03B params) bf16, SR on", shapes=llama3_8b_shapes(),
+               dtype=torch.bfloat16, kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, precision="8bit")),
+    "c4": dict(workload="C4 compact ApexW step, 20k ragged bf16 tensors, clip 1.0", shapes=ragged_shapes(),
+               dtype=torch.bfloat16, kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, clip_grad_norm=1.0),
+               zero_frac=0.05),
+}
+
+
+def make_params(cfg, device, seed=0):
+    g = torch.Generator(device=device).manual_seed(seed)
+    params, grads = [], []
+    for i, s in enumerate(cfg["shapes"]):
+        p = torch.empty(s, dtype=cfg["dtype"], device=device)
+        p.normal_(0.0, 0.02, generator=g)
+        gr = torch.empty(s, dtype=cfg["dtype"], device=device)
+        scale = 1e-3
+        if cfg.get("per_tensor_scale"):
+            scale *= math.exp((torch.rand((), generator=g, device=device).item() * 2 - 1) * math.log(10.0))
+        gr.normal_(0.0, scale, generator=g)
+        params.append(torch.nn.Parameter(p))
+        grads.append(gr)
+    zf = cfg.get("zero_frac", 0.0)
+    if zf:
+        k = int(len(grads) * zf)
+        for i in torch.randperm(len(grads), generator=torch.Generator().manual_seed(seed))[:k].tolist():
+            grads[i].zero_()
+    for p, gr in zip(params, grads):
+        p.grad = gr
+    return params
+
+
+def state_bytes(opt, params):
+    """Algorithmic HBM bytes of one step: p read+write, g read, every state tensor read+write."""
+    tot = 0
+    for p in params:
+        tot += 2 * p.numel() * p.element_size() + p.grad.numel() * p.grad.element_size()
+        for k, v in opt.state[p].items():
+            if torch.is_tensor(v) and k != "step" and v.device.type == "cuda":
+                tot += 2 * v.numel() * v.element_size()
+    return tot
+
+
+def cpu_baseline(cfg_name, budget_s=20.0):
+    """Time the CPU oracle on a bounded slice of the workload (whole steps)."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle.optim import OracleApexW
+    cfg = CONFIGS[cfg_name]
+    threads = os.cpu_count() or 1
+    threads = min(threads, 16)
+    torch.set_num_threads(threads)
+    if cfg_name == "c3":
+        shapes = llama3_8b_shapes()[1:10]          # one transformer layer (218M params)
+        sample = "one Llama-3-8B layer (q,k,v,o,gate,up,down + 2 RMSNorm, 218.1M params)"
+    elif cfg_name == "c4":
+        shapes = ragged_shapes()[:500]
+        sample = "first 500 of the 20k ragged tensors"
+    else:
+        shapes = cfg["shapes"]
+        sample = "full parameter list"
+    sub = dict(cfg, shapes=shapes)
+    params = make_params(sub, "cpu")
+    n = sum(p.numel() for p in params)
+    opt = OracleApexW(params, **cfg["kwargs"])
+    opt.step()  # cold step (state allocation)
+    steps, t0 = 0, time.perf_counter()
+    while True:
+        opt.step()
+        steps += 1
+        el = time.perf_counter() - t0
+        if el > budget_s or steps >= 50:
+            break
+    return {"value": n * steps / el, "unit": "params/s", "cores": threads, "kind": "port",
+            "sample": f"{sample}; {steps} steps after 1 cold step; CPU oracle (torch CPU ops)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
+    ap.add_argument("--cpu-budget", type=float, default=20.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the optimizer step is data-parallel per shard and this build "
+              "has no multi-GPU path; run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from apexw_amd import ApexW
+
+    cfg = CONFIGS[args.config]
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    params = make_params(cfg, dev)
+    n = sum(p.numel() for p in params)
+    opt = ApexW(params, **cfg["kwargs"])
+    for _ in range(args.warmup):
+        opt.step()
+    torch.cuda.synchronize()
+    nbytes = state_bytes(opt, params)
+    stream = torch.cuda.current_stream(dev)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        opt.step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = ev0.elapsed_time(ev1) / args.steps
+    ms = wall * 1e3 / args.steps
+    achieved = nbytes / (gpu_ms * 1e-3) / 1e9
+    out = {
+        "metric": METRIC, "value": n / (ms * 1e-3), "unit": "params/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": cfg["workload"], "params": n, "tensors": len(params),
+                   "param_dtype": str(cfg["dtype"]).replace("torch.", ""), **{k: v for k, v in cfg["kwargs"].items()}},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "kernel_ms": gpu_ms, "bytes_per_launch": nbytes, "bytes_per_param": nbytes / n},
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(args.config, args.cpu_budget)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,168 @@
+/*
+ * C ABI of libapexw_hip.so: the fused ApexW optimizer step and Muon
+ * Newton-Schulz kernels for AMD Instinct MI355X (gfx950).
+ *
+ * Everything is passed as plain pointers and sizes.  Device pointers point into
+ * memory owned by the caller (PyTorch tensors); the library never allocates
+ * caller-visible memory.  Every entry point validates its arguments before the
+ * first write and returns an apexw_status; APEXW_OK means the work was enqueued
+ * on `stream` (asynchronous, like a kernel launch).
+ *
+ * Reference interfaces replaced (paths relative to the reference checkout):
+ *   apexw_compact_step   <- pybind step_fused / fused_multi_tensor_adamw_cuda_step
+ *                           (apexw/csrc/apexw_cuda.cpp:109-234, :455-513;
+ *                           Python wrappers apexw/cuda_extension.py:123-158, :197-215)
+ *                           and the Triton bucket launch triton_multi_tensor_adamw_step
+ *                           (apexw/triton_kernel.py:2524-2874)
+ *   apexw_q8_step        <- pybind step_fused_8bit (apexw/csrc/apexw_cuda.cpp:310-453;
+ *                           wrapper apexw/cuda_extension.py:161-194) and
+ *                           _adamw_kernel_triton_8bit_batched (apexw/triton_kernel.py:1138-1531)
+ *   apexw_grad_clip_coef <- the global-norm clip of _prepare_grads
+ *                           (apexw/optimizer.py:242-256: _foreach_norm + vector_norm)
+ */
+#ifndef APEXW_HIP_H
+#define APEXW_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define APEXW_ABI_VERSION 1
+
+/* status codes */
+enum apexw_status {
+  APEXW_OK = 0,
+  APEXW_ERR_ARG = 1,      /* invalid argument (null pointer, bad size, bad flag) */
+  APEXW_ERR_DTYPE = 2,    /* unsupported dtype combination */
+  APEXW_ERR_LAUNCH = 3,   /* the HIP runtime rejected the launch */
+  APEXW_ERR_ALIGN = 4     /* pointer alignment the kernel requires is not met */
+};
+
+/* element dtype codes */
+enum apexw_dtype { APEXW_F32 = 0, APEXW_BF16 = 1, APEXW_F16 = 2, APEXW_U8 = 3, APEXW_I8 = 4 };
+
+/* apexw_tensor.flags: dtype fields (2 bits each) and per-tensor mode bits */
+#define APEXW_FLAG_PDT_SHIFT 0          /* param dtype */
+#define APEXW_FLAG_GDT_SHIFT 2          /* grad dtype */
+#define APEXW_FLAG_MDT_SHIFT 4          /* compact: first-moment dtype */
+#define APEXW_FLAG_VDT_SHIFT 6          /* compact: second-moment dtype */
+#define APEXW_FLAG_QUAD (1u << 8)       /* one v per 4 consecutive elements */
+#define APEXW_FLAG_WD (1u << 9)         /* apply decoupled weight decay */
+#define APEXW_FLAG_NF4 (1u << 10)       /* 8-bit: NF4 packed m (else INT8 m) */
+#define APEXW_FLAG_GENERIC (1u << 11)   /* 8-bit: per-parameter ("generic") rounding order */
+#define APEXW_FLAG_DENSE16 (1u << 12)   /* 8-bit mode tensor kept in 16-bit m/v (numel < 64) */
+#define APEXW_FLAG_SCALAR (1u << 13)    /* pointers not 16-byte aligned: element-wise path */
+
+/*
+ * One tensor of a multi-tensor launch (device-resident array, 64 bytes each).
+ * compact: m/v are the moment tensors (dtypes in flags), scales unused, block = 0.
+ * 8-bit:   m is the NF4 (uint8, 2 per byte, even element in the high nibble) or
+ *          INT8 code buffer, v the log-uint8 codes (n/4 entries when QUAD),
+ *          m_scale / v_scale the fp32 per-block scales, block the block size.
+ */
+typedef struct apexw_tensor {
+  void* p;
+  const void* g;
+  void* m;
+  void* v;
+  float* m_scale;
+  float* v_scale;
+  int64_t n;
+  uint32_t flags;
+  uint32_t block;
+} apexw_tensor;
+
+/*
+ * Work-unit (chunk) table entry: unit `unit` of tensor `tensor`.  A unit is
+ * APEXW_COMPACT_UNIT consecutive elements in compact mode and one quantization
+ * block in 8-bit mode.  Units of one tensor must be contiguous in the table.
+ */
+typedef struct apexw_unit {
+  uint32_t tensor;
+  uint32_t unit;
+} apexw_unit;
+
+#define APEXW_COMPACT_UNIT 2048
+
+/* apexw_hparams.mode */
+#define APEXW_MODE_COLD 0     /* first step of a plan: _multi_tensor_step rounding */
+#define APEXW_MODE_REPLAY 1   /* FastExecutionPlan.execute_foreach rounding */
+#define APEXW_MODE_NATIVE 2   /* torch._fused_adamw_ rounding (homogeneous 16-bit groups) */
+
+/* apexw_hparams.flags */
+#define APEXW_HP_SR (1u << 0)         /* stochastic rounding of 16-bit params / codes */
+#define APEXW_HP_SR_V (1u << 1)       /* compact: SR of the 16-bit v EMA (beta2 >= 0.995 and SR) */
+#define APEXW_HP_SANITIZE (1u << 2)   /* NaN -> 0, +-Inf -> +-65504 on the grads */
+#define APEXW_HP_CLIP (1u << 3)       /* multiply grads by *clip_coef (rounded to grad dtype) */
+#define APEXW_HP_LERP_HI (1u << 4)    /* m lerp weight (1 - beta1) >= 0.5: end-based form */
+#define APEXW_HP_LOOK_HI (1u << 5)    /* 8-bit lookahead lerp weight (beta1) >= 0.5 */
+
+/* Host-computed step scalars (the reference computes them in double). */
+typedef struct apexw_hparams {
+  float beta1, one_minus_beta1, beta2, one_minus_beta2;
+  float wd_factor;      /* compact: 1 - lr*wd; 8-bit: max(1 - lr*wd, 0) */
+  float step_size;      /* lr*sqrt(1-beta2^t)/(1-beta1^t); native mode: lr/(1-beta1^t) */
+  float eps_scaled;     /* eps*sqrt(1-beta2^t) */
+  float eps;            /* 8-bit: denominator floor; native mode: eps */
+  float lerp_coef;      /* m lerp toward g: w if w < 0.5 else w - 1 (w = fp32(1 - beta1)) */
+  float look_coef;      /* 8-bit lookahead lerp(g, m, beta1): same rule with w = fp32(beta1) */
+  float bc2_sqrt;       /* native mode: sqrt(1-beta2^t) */
+  float gain_hi, gain_lo;   /* 8-bit "Nesterov-SNR" gains 1+0.2*beta1, 1-0.35*beta1 */
+  const float* clip_coef;   /* device scalar written by apexw_grad_clip_coef, or NULL */
+  uint64_t seed;
+  uint32_t step;
+  uint32_t mode;
+  uint32_t flags;
+  uint32_t reserved;
+} apexw_hparams;
+
+/* ABI version of the loaded library (APEXW_ABI_VERSION). */
+int apexw_abi_version(void);
+
+/*
+ * Validate one tensor descriptor (HOST copy) before it is uploaded into a
+ * device table: kind 0 = compact step, 1 = 8-bit step.  Checks the dtype
+ * combination, block size and the 16-byte alignment the vector path needs
+ * (unless APEXW_FLAG_SCALAR is set).  Mirrors the per-call tensor checks of the
+ * reference's pybind glue (apexw/csrc/apexw_cuda.cpp:109-180, :310-380), done
+ * once per execution plan instead of per step.
+ */
+int apexw_check_tensor(const apexw_tensor* t, int32_t kind);
+
+/*
+ * Compact-precision fused AdamW step over every tensor of the table in one
+ * launch.  p, m, v are updated in place, g is read only.
+ */
+int apexw_compact_step(const apexw_tensor* tensors, int32_t n_tensors,
+                       const apexw_unit* units, int64_t n_units,
+                       const apexw_hparams* hp, void* stream);
+
+/*
+ * 8-bit fused step: dequantize m (NF4 or INT8) and v (log-uint8) with their
+ * block scales, AdamW with the SNR lookahead gain, write p, requantize m and v
+ * with block absmax / max scales (EMA-max 0.9 / 0.95).  One unit = one block.
+ */
+int apexw_q8_step(const apexw_tensor* tensors, int32_t n_tensors,
+                  const apexw_unit* units, int64_t n_units,
+                  const apexw_hparams* hp, void* stream);
+
+/*
+ * Global-L2 clip coefficient over the grads of the table:
+ *   norm_t = dtype_round(||g_t||_2), total = ||(norm_t)||_2,
+ *   *coef = min(clip / (total + 1e-6), 1)   (1 when total is not finite).
+ * unit_partial: n_units floats of workspace; tensor_norm: n_tensors floats;
+ * unit_begin: n_tensors + 1 int64 prefix offsets of each tensor's units.
+ * flags: APEXW_HP_SANITIZE to sanitize grads before squaring.
+ */
+int apexw_grad_clip_coef(const apexw_tensor* tensors, int32_t n_tensors,
+                         const apexw_unit* units, int64_t n_units, int64_t unit_size,
+                         const int64_t* unit_begin, float* unit_partial, float* tensor_norm,
+                         float clip, uint32_t flags, float* coef, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* APEXW_HIP_H */

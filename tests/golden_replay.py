@@ -67,7 +67,7 @@ def replay(name, make_opt, device="cpu", get_state=None):
             fp.append(_fingerprint(g))
             p.grad = g.to(device)
         opt.step()
-    np.testing.assert_array_equal(np.array(fp, dtype=np.float64), gold["fingerprint"])
+    np.testing.assert_array_equal(np.array(fp, dtype=np.int64), gold["fingerprint"])
     return params, opt, gold
 
 

@@ -1,0 +1,138 @@
+"""CPU-side checks: the C-ABI library, the host layout rules and the constructor contract."""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from golden_replay import load
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_symbols():
+    src = open(os.path.join(ROOT, "include", "apexw_hip.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"^\s*int\s+(apexw_\w+)\s*\(", src, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    from apexw_amd import _lib
+    lib = _lib.load()
+    syms = _declared_symbols()
+    assert syms, "no declarations parsed"
+    for s in syms:
+        assert hasattr(lib, s), s
+        assert s in _lib.SIGNATURES, f"{s} has no ctypes signature"
+    assert lib.apexw_abi_version() == _lib.ABI_VERSION
+
+
+def test_struct_layouts_match_header():
+    from apexw_amd import _lib
+    assert ctypes.sizeof(_lib.Tensor) == 64 == _lib.TENSOR_DTYPE.itemsize
+    assert ctypes.sizeof(_lib.HParams) == 88
+
+
+def test_check_tensor_rejects_bad_descriptors():
+    from apexw_amd import _lib
+    lib = _lib.load()
+    t = _lib.Tensor(16, 32, 48, 64, 0, 0, 100, (_lib.BF16 << 0) | (_lib.BF16 << 2) | (_lib.BF16 << 4) | (_lib.BF16 << 6), 0)
+    assert lib.apexw_check_tensor(ctypes.byref(t), 0) == 0
+    t.p = 0
+    assert lib.apexw_check_tensor(ctypes.byref(t), 0) == 1
+    t.p = 18  # misaligned without the scalar flag
+    assert lib.apexw_check_tensor(ctypes.byref(t), 0) == 4
+    t.flags |= _lib.FLAG_SCALAR
+    assert lib.apexw_check_tensor(ctypes.byref(t), 0) == 0
+    t.flags = (_lib.F16 << 0) | (_lib.F16 << 2)
+    assert lib.apexw_check_tensor(ctypes.byref(t), 0) == 2
+    q = _lib.Tensor(16, 32, 48, 64, 80, 96, 4096, (_lib.BF16 << 0) | (_lib.BF16 << 2) | _lib.FLAG_NF4 | _lib.FLAG_QUAD,
+                    2048)
+    assert lib.apexw_check_tensor(ctypes.byref(q), 1) == 0
+    q.block = 4096  # blocks above 2048 elements are not supported
+    assert lib.apexw_check_tensor(ctypes.byref(q), 1) == 2
+    # entry points reject null tables before touching the GPU
+    hp = _lib.HParams()
+    assert lib.apexw_compact_step(None, 1, None, 1, ctypes.byref(hp), None) == 1
+    assert lib.apexw_q8_step(None, 1, None, 1, ctypes.byref(hp), None) == 1
+
+
+_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2, torch.int8: 3, torch.uint8: 4}
+
+
+def _layout_rows(shapes, dtype, kwargs):
+    from apexw_amd import state as S
+    from apexw_amd.optimizer import ApexW
+    params = [torch.nn.Parameter(torch.empty(s, dtype=dtype, device="meta")) for s in shapes]
+    opt = ApexW(params, **kwargs)
+    g = opt.param_groups[0]
+    peft = S.detect_peft_context(opt.param_groups)
+    rows = []
+    for p in params:
+        st = S.init_state(p, g, peft)
+        m, v = st["exp_avg"], st["exp_avg_sq"]
+        rows.append([p.numel(), int(bool(st.get("is_quad_v", False))), int(bool(st.get("is_4bit_m", False))),
+                     int(bool(st.get("is_8bit", False))), int(st.get("block_size_8bit", 0) or 0),
+                     m.numel(), _CODES[m.dtype], v.numel(), _CODES[v.dtype],
+                     st["exp_avg_scales"].numel() if "exp_avg_scales" in st else 0])
+    return np.array(rows, dtype=np.int64)
+
+
+def test_state_layout_matches_reference():
+    import bench
+    from golden.make_golden import gpt2_small_shapes, llama3_8b_shapes
+    z = load("layout")
+    misc = [(5,), (63,), (64,), (65,), (127,), (128,), (500,), (1024,), (2047,), (2048,), (4096,),
+            (16, 100), (32, 64), (33, 40), (8, 2048), (7, 4096), (16384,), (16383,), (16388,), (128, 130)]
+    cases = {
+        "c2_compact_sr": (gpt2_small_shapes(), torch.bfloat16, dict(lr=1e-3, weight_decay=0.1, adamw_compat=True)),
+        "c2_compact_rne": (gpt2_small_shapes(), torch.bfloat16,
+                           dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, stochastic_rounding=False)),
+        "c2_compact_default": (gpt2_small_shapes(), torch.bfloat16, dict()),
+        "c3_8bit": (llama3_8b_shapes(), torch.bfloat16,
+                    dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, precision="8bit")),
+        "misc_8bit": (misc, torch.bfloat16, dict(precision="8bit")),
+        "misc_compact": (misc, torch.bfloat16, dict()),
+        "misc_compact_fp32": (misc, torch.float32, dict(adamw_compat=True, stochastic_rounding=False)),
+    }
+    assert bench.llama3_8b_shapes() == llama3_8b_shapes()
+    for name, (shapes, dt, kw) in cases.items():
+        np.testing.assert_array_equal(_layout_rows(shapes, dt, kw), z[name], err_msg=name)
+
+
+def test_constructor_contract():
+    from apexw_amd import ApexW
+    p = [torch.nn.Parameter(torch.zeros(4))]
+    o = ApexW(p)
+    assert o.defaults["betas"] == (0.9, 0.99) and o.defaults["precision"] == "compact"
+    assert o.defaults["decay_norm_only"] is True
+    o = ApexW(p, precision="int8")
+    assert o.defaults["betas"] == (0.9, 0.999) and o.defaults["precision"] == "8bit"
+    o = ApexW(p, adamw_compat=True, betas=(0.9, 0.95))
+    assert o.defaults["betas"] == (0.9, 0.999) and o.defaults["decay_norm_only"] is False
+    o = ApexW(p, adamw_compat=True, betas=(0.8, 0.9))
+    assert o.defaults["betas"] == (0.8, 0.9)
+    with pytest.raises(ValueError):
+        ApexW(p, lr=-1.0)
+    with pytest.raises(ValueError):
+        ApexW(p, betas=(1.0, 0.9))
+    with pytest.raises(ValueError):
+        ApexW(p, block_size=0)
+    with pytest.raises(ValueError):
+        ApexW(p, precision="nope")
+    with pytest.raises(NotImplementedError):
+        ApexW(p, amsgrad=True)
+    with pytest.raises(NotImplementedError):
+        ApexW(p, precision="full")
+    assert ApexW._step_supports_amp_scaling
+
+
+def test_step_requires_gpu_tensors():
+    from apexw_amd import ApexW
+    p = torch.nn.Parameter(torch.zeros(8))
+    p.grad = torch.zeros(8)
+    with pytest.raises(RuntimeError):
+        ApexW([p]).step()

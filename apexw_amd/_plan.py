@@ -107,7 +107,6 @@ class StepPlan:
         self.grads = [None] * n
         tab = np.zeros(n, dtype=L.TENSOR_DTYPE)
         counts = np.zeros(n, dtype=np.int64)
-        lib = L.load()
         for i, (p, st) in enumerate(zip(self.params, self.states)):
             if not p.is_contiguous():
                 raise NotImplementedError("ApexW HIP step needs contiguous parameters")
@@ -128,21 +127,31 @@ class StepPlan:
                 counts[i] = 1
             else:
                 counts[i] = (p.numel() + block - 1) // block
-        self.host_table = tab
-        self.unit_counts = counts
+        self.host_table = tab          # parameter order
+        self.counts = counts
+        self.kind_code = 0 if self.kind == "compact" else 1
+        self._lib = L.load()
+        self.clip_ws = None
+        self.d_table = None
+        self.perm = None
+
+    def _layout_units(self, fast):
+        """Device table in launch order (8-bit: full-block-kernel tensors first) and its unit table."""
+        n = len(self.params)
+        perm = np.arange(n) if fast is None else np.concatenate([np.nonzero(fast)[0], np.nonzero(~fast)[0]])
+        counts = self.counts[perm]
         self.unit_begin = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
         total = int(self.unit_begin[-1])
-        tidx = np.repeat(np.arange(n, dtype=np.uint32), counts)
-        uidx = (np.arange(total, dtype=np.int64) - np.repeat(self.unit_begin[:-1], counts)).astype(np.uint32)
         units = np.zeros(total, dtype=L.UNIT_DTYPE)
-        units["tensor"] = tidx
-        units["unit"] = uidx
+        units["tensor"] = np.repeat(np.arange(n, dtype=np.uint32), counts)
+        units["unit"] = (np.arange(total, dtype=np.int64) - np.repeat(self.unit_begin[:-1], counts)).astype(np.uint32)
         self.n_units = total
+        self.n_fast_units = int(counts[: int(fast.sum())].sum()) if fast is not None else 0
+        self.unit_counts = counts
+        self.perm = perm
+        self.fast = fast
         self.d_units = torch.from_numpy(units.view(np.uint8)).to(self.device)
         self.d_unit_begin = torch.from_numpy(self.unit_begin).to(self.device)
-        self.d_table = None
-        self.kind_code = 0 if self.kind == "compact" else 1
-        self._lib = lib
         self.clip_ws = None
 
     def _refresh_grads(self):
@@ -163,19 +172,29 @@ class StepPlan:
                     self.host_table[i]["g"] = ptr
         self.grads = grads
         if changed:
-            self._validate_and_align()
-            self.d_table = torch.from_numpy(self.host_table.view(np.uint8)).to(self.device)
+            fast = self._validate_and_align()
+            if self.perm is None or (fast is not None and not np.array_equal(fast, self.fast)):
+                self._layout_units(fast)
+            rows = np.ascontiguousarray(self.host_table[self.perm])
+            self.d_table = torch.from_numpy(rows.view(np.uint8)).to(self.device)
         return grads
 
     def _validate_and_align(self):
+        """Check every descriptor; mark unaligned ones element-wise; 8-bit: which take the full-block kernel."""
         lib = self._lib
+        fast = np.zeros(len(self.params), dtype=bool) if self.kind == "q8" else None
         for i in range(len(self.params)):
             row = self.host_table[i]
             ptrs = int(row["p"]) | int(row["g"]) | int(row["m"]) | int(row["v"])
-            if ptrs & 15:
-                row["flags"] = int(row["flags"]) | L.FLAG_SCALAR
+            flags = int(row["flags"]) & ~L.FLAG_SCALAR
+            if ptrs & 15 or (self.kind == "q8" and int(row["block"]) % 8):
+                flags |= L.FLAG_SCALAR
+            row["flags"] = flags
             t = L.Tensor(*(int(row[k]) for k in ("p", "g", "m", "v", "m_scale", "v_scale", "n", "flags", "block")))
             L.check(lib.apexw_check_tensor(ctypes_ref(t), self.kind_code), f"tensor {i} ({tuple(self.params[i].shape)})")
+            if fast is not None:
+                fast[i] = lib.apexw_check_tensor(ctypes_ref(t), 2) == 0
+        return fast
 
     # ------------------------------------------------------------------ launch
     def _clip(self, clip, sanitize, stream):
@@ -215,22 +234,27 @@ class StepPlan:
             groups = [(None, int(self.steps[0].item()))]
         for units, step in groups:
             hp = self._hparams(lr, b1, b2, eps, wd, step, sr, sanitize, coef, seed, mode_cold)
-            d_units, n_units = (self.d_units, self.n_units) if units is None else units
-            fn = self._lib.apexw_compact_step if self.kind == "compact" else self._lib.apexw_q8_step
-            L.check(fn(self.d_table.data_ptr(), len(self.params), d_units.data_ptr(), n_units,
-                       ctypes_ref(hp), stream), "apexw step")
+            d_units, n_units, n_fast = (self.d_units, self.n_units, self.n_fast_units) if units is None else units
+            if self.kind == "compact":
+                st = self._lib.apexw_compact_step(self.d_table.data_ptr(), len(self.params), d_units.data_ptr(),
+                                                  n_units, ctypes_ref(hp), stream)
+            else:
+                st = self._lib.apexw_q8_step(self.d_table.data_ptr(), len(self.params), d_units.data_ptr(),
+                                             n_units, n_fast, ctypes_ref(hp), stream)
+            L.check(st, "apexw step")
         self.cold_done = True
 
     def _split_by_step(self):
-        vals = self.steps.tolist()
-        if all(v == vals[0] for v in vals):
+        vals = self.steps.numpy()[self.perm]
+        if np.all(vals == vals[0]):
             return [(None, int(vals[0]))]
         out = []
-        for val in sorted(set(vals), key=vals.index):
-            keep = np.array([v == val for v in vals])
+        for val in sorted(set(vals.tolist()), key=vals.tolist().index):
+            keep = vals == val
             mask = np.repeat(keep, self.unit_counts)
             sel = self.d_units.view(-1, 8)[torch.from_numpy(mask).to(self.device)].reshape(-1)
-            out.append(((sel, int(mask.sum())), int(val)))
+            n_fast = int(mask[: self.n_fast_units].sum())
+            out.append(((sel, int(mask.sum()), n_fast), int(val)))
         return out
 
     def _hparams(self, lr, b1, b2, eps, wd, step, sr, sanitize, coef, seed, cold):

@@ -11,6 +11,8 @@
 
 int apexw_launch_compact(const apexw_tensor*, int64_t, const apexw_unit*, const apexw_hparams*, int, hipStream_t);
 int apexw_launch_q8(const apexw_tensor*, int64_t, const apexw_unit*, const apexw_hparams*, int, hipStream_t);
+int apexw_launch_q8_fast(const apexw_tensor*, int64_t, const apexw_unit*, const apexw_hparams*, int, hipStream_t);
+bool apexw_q8_fast_eligible(uint32_t flags, uint32_t block);
 int apexw_launch_clip(const apexw_tensor*, int32_t, const apexw_unit*, int64_t, int64_t, const int64_t*, float*, float*,
                       float, uint32_t, float*, int, int, hipStream_t);
 bool apexw_compact_flags_ok(uint32_t flags);
@@ -62,8 +64,9 @@ int apexw_check_tensor(const apexw_tensor* t, int32_t kind) {
   if (kind == 0) {
     if (!apexw_compact_flags_ok(t->flags)) return APEXW_ERR_DTYPE;
     if ((t->flags & APEXW_FLAG_QUAD) && (t->n % 4) != 0) return APEXW_ERR_ARG;
-  } else if (kind == 1) {
+  } else if (kind == 1 || kind == 2) {
     if (!apexw_q8_flags_ok(t->flags, t->block, t->n)) return APEXW_ERR_DTYPE;
+    if (kind == 2 && !apexw_q8_fast_eligible(t->flags, t->block)) return APEXW_ERR_DTYPE;
     if (!(t->flags & APEXW_FLAG_DENSE16) && (!t->m_scale || !t->v_scale)) return APEXW_ERR_ARG;
   } else {
     return APEXW_ERR_ARG;
@@ -83,11 +86,17 @@ int apexw_compact_step(const apexw_tensor* tensors, int32_t n_tensors, const ape
 }
 
 int apexw_q8_step(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,
-                  const apexw_hparams* hp, void* stream) {
+                  int64_t n_fast_units, const apexw_hparams* hp, void* stream) {
   if (!tensors || !units || n_tensors <= 0 || n_units < 0 || !hp_ok(hp)) return APEXW_ERR_ARG;
+  if (n_fast_units < 0 || n_fast_units > n_units) return APEXW_ERR_ARG;
   if (hp->mode == APEXW_MODE_NATIVE) return APEXW_ERR_ARG;
-  if (n_units == 0) return APEXW_OK;
-  return apexw_launch_q8(tensors, n_units, units, hp, persistent_grid(n_units, 8), (hipStream_t)stream);
+  int st = APEXW_OK;
+  if (n_fast_units > 0)
+    st = apexw_launch_q8_fast(tensors, n_fast_units, units, hp, persistent_grid(n_fast_units, 8), (hipStream_t)stream);
+  const int64_t rest = n_units - n_fast_units;
+  if (st == APEXW_OK && rest > 0)
+    st = apexw_launch_q8(tensors, rest, units + n_fast_units, hp, persistent_grid(rest, 8), (hipStream_t)stream);
+  return st;
 }
 
 int apexw_grad_clip_coef(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,

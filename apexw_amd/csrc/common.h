@@ -17,6 +17,10 @@
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
 typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
 
+// Pointers read out of the tensor table are generic; casting them to the global
+// address space lets the compiler emit global_load/global_store instead of flat.
+#define APEXW_GLOBAL(T, ptr) ((__attribute__((address_space(1))) T*)(ptr))
+
 // ---------------------------------------------------------------------------
 // dtype conversions
 // ---------------------------------------------------------------------------
@@ -67,12 +71,12 @@ template <> struct Elem<APEXW_F16> { static constexpr int bytes = 2; };
 // 16-bit types, 32-byte aligned for fp32) into fp32 registers.
 template <int DT> APEXW_DEV void load8(const void* base, int64_t i, float (&x)[8]) {
   if constexpr (DT == APEXW_F32) {
-    const u32x4* p = (const u32x4*)((const float*)base + i);
+    auto p = APEXW_GLOBAL(const u32x4, (const float*)base + i);
     u32x4 a = __builtin_nontemporal_load(p), b = __builtin_nontemporal_load(p + 1);
     x[0] = __uint_as_float(a.x); x[1] = __uint_as_float(a.y); x[2] = __uint_as_float(a.z); x[3] = __uint_as_float(a.w);
     x[4] = __uint_as_float(b.x); x[5] = __uint_as_float(b.y); x[6] = __uint_as_float(b.z); x[7] = __uint_as_float(b.w);
   } else {
-    const u32x4* p = (const u32x4*)((const uint16_t*)base + i);
+    auto p = APEXW_GLOBAL(const u32x4, (const uint16_t*)base + i);
     u32x4 a = __builtin_nontemporal_load(p);
     uint32_t w[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
@@ -91,7 +95,7 @@ template <int DT> APEXW_DEV void load8(const void* base, int64_t i, float (&x)[8
 // Store 8 fp32 values that are already representable in DT.
 template <int DT> APEXW_DEV void store8(void* base, int64_t i, const float (&x)[8]) {
   if constexpr (DT == APEXW_F32) {
-    u32x4* p = (u32x4*)((float*)base + i);
+    auto p = APEXW_GLOBAL(u32x4, (float*)base + i);
     u32x4 a = {__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]), __float_as_uint(x[3])};
     u32x4 b = {__float_as_uint(x[4]), __float_as_uint(x[5]), __float_as_uint(x[6]), __float_as_uint(x[7])};
     __builtin_nontemporal_store(a, p);
@@ -107,20 +111,20 @@ template <int DT> APEXW_DEV void store8(void* base, int64_t i, const float (&x)[
       }
     }
     u32x4 a = {w[0], w[1], w[2], w[3]};
-    __builtin_nontemporal_store(a, (u32x4*)((uint16_t*)base + i));
+    __builtin_nontemporal_store(a, APEXW_GLOBAL(u32x4, (uint16_t*)base + i));
   }
 }
 
 template <int DT> APEXW_DEV float load1(const void* base, int64_t i) {
-  if constexpr (DT == APEXW_F32) return ((const float*)base)[i];
-  else if constexpr (DT == APEXW_BF16) return bf16_bits_to_f32(((const uint16_t*)base)[i]);
-  else return f16_bits_to_f32(((const uint16_t*)base)[i]);
+  if constexpr (DT == APEXW_F32) return APEXW_GLOBAL(const float, base)[i];
+  else if constexpr (DT == APEXW_BF16) return bf16_bits_to_f32(APEXW_GLOBAL(const uint16_t, base)[i]);
+  else return f16_bits_to_f32(APEXW_GLOBAL(const uint16_t, base)[i]);
 }
 
 template <int DT> APEXW_DEV void store1(void* base, int64_t i, float x) {
-  if constexpr (DT == APEXW_F32) ((float*)base)[i] = x;
-  else if constexpr (DT == APEXW_BF16) ((uint16_t*)base)[i] = (uint16_t)(__float_as_uint(x) >> 16);
-  else ((uint16_t*)base)[i] = (uint16_t)f32_to_f16_bits(x);
+  if constexpr (DT == APEXW_F32) APEXW_GLOBAL(float, base)[i] = x;
+  else if constexpr (DT == APEXW_BF16) APEXW_GLOBAL(uint16_t, base)[i] = (uint16_t)(__float_as_uint(x) >> 16);
+  else APEXW_GLOBAL(uint16_t, base)[i] = (uint16_t)f32_to_f16_bits(x);
 }
 
 // ---------------------------------------------------------------------------
@@ -144,7 +148,9 @@ APEXW_DEV uint32_t rng_key(uint64_t seed, uint32_t tensor, uint32_t step, uint32
   return mix32(k ^ hi_index);
 }
 
-APEXW_DEV uint32_t rng_at(uint32_t key, uint32_t index) { return mix32(mix32(index ^ key) + key); }
+// one keyed hash per element: the key is already fully mixed, so a single
+// finaliser round over key + index decorrelates neighbouring elements.
+APEXW_DEV uint32_t rng_at(uint32_t key, uint32_t index) { return mix32(index + key); }
 
 // ---------------------------------------------------------------------------
 // Gradient sanitizing (NaN -> 0, +-Inf -> +-65504 after rounding to the grad dtype)

@@ -16,14 +16,24 @@
 #include "common.h"
 #include "luts.h"
 
+// A tensor takes the full-block kernel when it has bf16 params/grads, NF4 m,
+// quad log-uint8 v, 2048-element blocks and 16-byte aligned buffers.
+static __host__ __device__ inline bool apexw_q8_fast_ok(uint32_t flags, uint32_t block) {
+  const uint32_t pd = (flags >> APEXW_FLAG_PDT_SHIFT) & 3u, gd = (flags >> APEXW_FLAG_GDT_SHIFT) & 3u;
+  return pd == APEXW_BF16 && gd == APEXW_BF16 && (flags & APEXW_FLAG_NF4) && (flags & APEXW_FLAG_QUAD) &&
+         !(flags & (APEXW_FLAG_SCALAR | APEXW_FLAG_DENSE16)) && block == 2048;
+}
+
 namespace {
 
 constexpr int kWaves = 4;
 
 struct Q8Ctx {
   const apexw_hparams* hp;
-  const float* vlut;   // LDS
-  const float* code;   // LDS
+  const float* vlut;   // LDS: log-uint8 decode table
+  const float* code;   // LDS: NF4 codebook
+  const float2* pair;    // LDS: NF4 byte -> two values
+  const float4* frac16;  // LDS: signed fractional NF4 code buckets (x 65536, +7)
   float coef;
 };
 
@@ -102,7 +112,9 @@ APEXW_DEV float q8_param(float p, float upd, float decay, uint32_t tflags, bool 
   return sr ? sr_round<PD>(x, r) : rnd<PD>(x);
 }
 
-// One quantization block per wavefront.
+// One quantization block per wavefront, any layout (INT8 m, fp32 params, other
+// block sizes, unaligned tensors).  Runs in its own kernel so that its register
+// footprint does not lower the occupancy of the bf16 NF4 kernel below.
 template <int PD, bool NF4, bool QUAD>
 APEXW_DEV void q8_block(const apexw_tensor& t, uint32_t tix, uint32_t blk, const Q8Ctx& c) {
   constexpr int GD = PD;
@@ -378,6 +390,237 @@ APEXW_DEV void q8_block(const apexw_tensor& t, uint32_t tix, uint32_t blk, const
   }
 }
 
+
+// 2048-element block of a bf16 parameter with NF4 m and quad log-uint8 v
+// (every large matrix of an LLM); a short last block is masked.  Same
+// arithmetic as q8_block, organised for throughput:
+//  * all 16 loads of the wavefront are issued before any math;
+//  * SR off (the parity mode): exact IEEE divisions and midpoint comparisons,
+//    identical to q8_block;
+//  * SR on: random bits come from a per-lane xorshift32 stream seeded by a
+//    keyed hash of (tensor, block, lane) -- 32 bits per element: bits 0-15 round
+//    the bf16 parameter, bits 16-27 the NF4 code, bits 28-31 of the four
+//    elements of a quad its log-uint8 code; divisions use per-quad / per-block reciprocals; the
+//    parameter update is one fma (p*decay - update) before rounding; NF4 codes
+//    come from the signed fractional-index table: code = (G(x) + r12) >> 12.
+template <bool SR, bool FULL, bool GENERIC>
+APEXW_DEV void q8_block_fast(const apexw_tensor& t, uint32_t tix, uint32_t blk, const Q8Ctx& c) {
+  const apexw_hparams& hp = *c.hp;
+  const uint32_t hf = hp.flags, tf = t.flags;
+  const int lane = lane_id();
+  const int64_t start = (int64_t)blk * 2048;
+  const float ms_old = t.m_scale[blk];
+  const float vs_old = t.v_scale[blk];
+  const float decay = (tf & APEXW_FLAG_WD) ? hp.wd_factor : 1.0f;
+  const bool lerp_hi = hf & APEXW_HP_LERP_HI, look_hi = hf & APEXW_HP_LOOK_HI;
+
+  u32x4 pw[4], gw[4];
+  uint32_t mw[4], vw[4];
+  int cnt[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int64_t e = start + k * 512 + lane * 8;
+    if constexpr (FULL) {
+      cnt[k] = 8;
+      pw[k] = __builtin_nontemporal_load(APEXW_GLOBAL(const u32x4, (const uint16_t*)t.p + e));
+      gw[k] = __builtin_nontemporal_load(APEXW_GLOBAL(const u32x4, (const uint16_t*)t.g + e));
+      mw[k] = __builtin_nontemporal_load(APEXW_GLOBAL(const uint32_t, (const uint8_t*)t.m + (e >> 1)));
+      vw[k] = __builtin_nontemporal_load(APEXW_GLOBAL(const uint16_t, (const uint8_t*)t.v + (e >> 2)));
+    } else {
+      // numel % 4 == 0 for quad-v tensors, so a lane holds 0, 4 or 8 elements
+      cnt[k] = e >= t.n ? 0 : (t.n - e >= 8 ? 8 : 4);
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      pw[k] = z; gw[k] = z; mw[k] = 0x77777777u; vw[k] = 0u;
+      if (cnt[k] == 8) {
+        pw[k] = *APEXW_GLOBAL(const u32x4, (const uint16_t*)t.p + e);
+        gw[k] = *APEXW_GLOBAL(const u32x4, (const uint16_t*)t.g + e);
+        mw[k] = *APEXW_GLOBAL(const uint32_t, (const uint8_t*)t.m + (e >> 1));
+        vw[k] = *APEXW_GLOBAL(const uint16_t, (const uint8_t*)t.v + (e >> 2));
+      } else if (cnt[k] == 4) {
+        const u32x2 a = *APEXW_GLOBAL(const u32x2, (const uint16_t*)t.p + e);
+        const u32x2 b = *APEXW_GLOBAL(const u32x2, (const uint16_t*)t.g + e);
+        pw[k].x = a.x; pw[k].y = a.y; gw[k].x = b.x; gw[k].y = b.y;
+        mw[k] = 0x77770000u | *APEXW_GLOBAL(const uint16_t, (const uint8_t*)t.m + (e >> 1));
+        vw[k] = *APEXW_GLOBAL(const uint8_t, (const uint8_t*)t.v + (e >> 2));
+      }
+    }
+  }
+  uint32_t rs = 0;
+  if constexpr (SR) {
+    const uint32_t key = rng_key(hp.seed, tix, hp.step, 1u, (uint32_t)(start >> 32));
+    rs = mix32(key + (blk << 6) + (uint32_t)lane) | 1u;
+  }
+  const bool prep = hf & (APEXW_HP_SANITIZE | APEXW_HP_CLIP);
+
+  float mnew[4][8], vq[4][2];
+  uint32_t hbits[4][8];   // this pass's random words
+  uint32_t hm[4][4];      // bits 16-31 of two elements' words, kept for requantization
+  float amax = 0.0f, vmax = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float p[8], g[8], m[8];
+    const uint32_t pv[4] = {pw[k].x, pw[k].y, pw[k].z, pw[k].w};
+    const uint32_t gv[4] = {gw[k].x, gw[k].y, gw[k].z, gw[k].w};
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      p[2 * b] = __uint_as_float(pv[b] << 16);
+      p[2 * b + 1] = __uint_as_float(pv[b] & 0xFFFF0000u);
+      g[2 * b] = __uint_as_float(gv[b] << 16);
+      g[2 * b + 1] = __uint_as_float(gv[b] & 0xFFFF0000u);
+      const float2 pr = c.pair[(mw[k] >> (8 * b)) & 0xFFu];
+      m[2 * b] = pr.x * ms_old;
+      m[2 * b + 1] = pr.y * ms_old;
+    }
+    if (prep) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) g[j] = q8_grad<APEXW_BF16>(g[j], tf, c);
+    } else {
+      bool bad = false;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) bad |= !__builtin_isfinite(g[j]);
+      if (bad) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) g[j] = q8_grad<APEXW_BF16>(g[j], tf, c);
+      }
+    }
+    if constexpr (SR) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        rs ^= rs << 13;
+        rs ^= rs >> 17;
+        rs ^= rs << 5;
+        hbits[k][j] = rs;
+      }
+    }
+    float num[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      m[j] = lerp_to(m[j], g[j], hp.lerp_coef, lerp_hi);
+      const float look = lerp_to(g[j], m[j], hp.look_coef, look_hi);
+      num[j] = look * ((m[j] * g[j] >= 0.0f) ? hp.gain_hi : hp.gain_lo);
+    }
+    float upd[8];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int b = 4 * q;
+      float s2 = g[b] * g[b];
+      s2 = s2 + g[b + 1] * g[b + 1];
+      s2 = s2 + g[b + 2] * g[b + 2];
+      s2 = s2 + g[b + 3] * g[b + 3];
+      const float vold = c.vlut[(vw[k] >> (8 * q)) & 0xFFu] * vs_old;
+      float vv = fmaf(hp.one_minus_beta2, s2 * 0.25f, vold * hp.beta2);
+      if (!(fabsf(vv) <= 3.402823466e38f)) vv = 0.0f;
+      vq[k][q] = vv;
+      if (FULL || 4 * q < cnt[k]) vmax = fmaxf(vmax, vv);
+      if constexpr (SR) {
+        const float den = fmaxf(__builtin_amdgcn_sqrtf(vv) + hp.eps_scaled, hp.eps);
+        const float r = __builtin_amdgcn_rcpf(den) * hp.step_size;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) upd[b + i] = num[b + i] * r;
+      } else {
+        const float den = fmaxf(sqrtf(vv) + hp.eps_scaled, hp.eps);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) upd[b + i] = (num[b + i] / den) * hp.step_size;
+      }
+    }
+    uint32_t pout[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      float x[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int j = 2 * b + i;
+        if constexpr (SR) {
+          const float y = GENERIC ? rnd<APEXW_BF16>(p[j] * decay) - upd[j] : fmaf(p[j], decay, -upd[j]);
+          x[i] = __uint_as_float(__float_as_uint(y) + (hbits[k][j] & 0xFFFFu));
+        } else if constexpr (GENERIC) {
+          x[i] = rnd<APEXW_BF16>(rnd<APEXW_BF16>(p[j] * decay) - rnd<APEXW_BF16>(upd[j]));
+        } else {
+          x[i] = rnd<APEXW_BF16>(p[j] * decay - upd[j]);
+        }
+      }
+      pout[b] = (__float_as_uint(x[0]) >> 16) | (__float_as_uint(x[1]) & 0xFFFF0000u);
+      if constexpr (SR) hm[k][b] = (hbits[k][2 * b] >> 16) | (hbits[k][2 * b + 1] & 0xFFFF0000u);
+    }
+    const int64_t e = start + k * 512 + lane * 8;
+    u32x4 po = {pout[0], pout[1], pout[2], pout[3]};
+    if constexpr (FULL) {
+      __builtin_nontemporal_store(po, APEXW_GLOBAL(u32x4, (uint16_t*)t.p + e));
+    } else if (cnt[k] == 8) {
+      *APEXW_GLOBAL(u32x4, (uint16_t*)t.p + e) = po;
+    } else if (cnt[k] == 4) {
+      u32x2 p2 = {po.x, po.y};
+      *APEXW_GLOBAL(u32x2, (uint16_t*)t.p + e) = p2;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      mnew[k][j] = m[j];
+      if (FULL || j < cnt[k]) amax = fmaxf(amax, fabsf(m[j]));
+    }
+  }
+  amax = wave_max(amax);
+  vmax = wave_max(vmax);
+  const float ms = fmaxf(fmaxf(amax, 1e-12f), ms_old * 0.9f);
+  const float vs = fmaxf(fmaxf(vmax, 1e-12f), vs_old * 0.95f);
+  if (lane == 0) {
+    t.m_scale[blk] = ms;
+    t.v_scale[blk] = vs;
+  }
+  const float rms = 1.0f / ms, rvs = 1.0f / vs;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int64_t e = start + k * 512 + lane * 8;
+    uint32_t code[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if constexpr (SR) {
+        // x in [-1, 1 - 2^-22] keeps x + 3 inside [2, 4): its top 7 mantissa bits are the bucket
+        const float x = __builtin_amdgcn_fmed3f(mnew[k][j] * rms, -1.0f, 0x1.fffffcp-1f);
+        const uint32_t bkt = (__float_as_uint(x + 3.0f) >> 16) & 127u;
+        const float4 fr = c.frac16[bkt];
+        const float lim = __uint_as_float((__float_as_uint(x) & 0x80000000u) | 0x7F800000u);
+        const float gcode = __builtin_amdgcn_fmed3f(fmaf(fr.y, x, fr.x), fmaf(fr.w, x, fr.z), -lim);
+        const uint32_t r12 = (hm[k][j >> 1] >> ((j & 1) ? 16 : 0)) & 0xFFFu;
+        code[j] = ((uint32_t)gcode + r12) >> 12;
+      } else {
+        code[j] = nf4_rne(fminf(fmaxf(mnew[k][j] / ms, -1.0f), 1.0f));
+      }
+    }
+    uint32_t w = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) w |= ((code[2 * b] << 4) | code[2 * b + 1]) << (8 * b);
+    uint32_t vc[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const float vv = vq[k][q];
+      if (!(vv > 0.0f)) {
+        vc[q] = 0u;
+      } else if constexpr (SR) {
+        const float r = fmaxf(vv * rvs, 0x1p-24f);
+        // bits 28-31 of the quad's four words -> 16 bits -> u = (r + 1/2) / 2^16, then floor
+        const uint32_t a = hm[k][2 * q], b = hm[k][2 * q + 1];
+        const uint32_t r16 = ((a >> 12) & 0xFu) | ((a >> 24) & 0xF0u) | ((b >> 4) & 0xF00u) | ((b >> 16) & 0xF000u);
+        const float u = __uint_as_float(0x3F800040u | (r16 << 7)) - 1.0f;
+        const float qf = fmaf(__builtin_amdgcn_logf(r), 0x1.52aaaap+3f, 255.0f) + u;
+        vc[q] = (uint32_t)__builtin_amdgcn_fmed3f(qf, 1.0f, 255.0f);
+      } else {
+        vc[q] = logu8_code(vv, vs, false, 0u);
+      }
+    }
+    if constexpr (FULL) {
+      __builtin_nontemporal_store(w, APEXW_GLOBAL(uint32_t, (uint8_t*)t.m + (e >> 1)));
+      __builtin_nontemporal_store((uint16_t)(vc[0] | (vc[1] << 8)),
+                                  APEXW_GLOBAL(uint16_t, (uint8_t*)t.v + (e >> 2)));
+    } else if (cnt[k] == 8) {
+      *APEXW_GLOBAL(uint32_t, (uint8_t*)t.m + (e >> 1)) = w;
+      *APEXW_GLOBAL(uint16_t, (uint8_t*)t.v + (e >> 2)) = (uint16_t)(vc[0] | (vc[1] << 8));
+    } else if (cnt[k] == 4) {
+      *APEXW_GLOBAL(uint16_t, (uint8_t*)t.m + (e >> 1)) = (uint16_t)(w & 0xFFFFu);
+      *APEXW_GLOBAL(uint8_t, (uint8_t*)t.v + (e >> 2)) = (uint8_t)vc[0];
+    }
+  }
+}
+
 // Tensors under 64 elements in 8-bit mode keep 16-bit m/v (optimizer.py:4688-4735).
 template <int PD, int VD>
 APEXW_DEV void q8_dense16(const apexw_tensor& t, const Q8Ctx& c) {
@@ -400,6 +643,49 @@ APEXW_DEV void q8_dense16(const apexw_tensor& t, const Q8Ctx& c) {
   store1<PD>(t.p, i, p);
 }
 
+
+// Kernel for the units of fast-path tensors (see apexw_q8_fast_ok).
+__global__ __launch_bounds__(256) void q8_fast_kernel(const apexw_tensor* __restrict__ tensors,
+                                                      const apexw_unit* __restrict__ units,
+                                                      int64_t n_units, apexw_hparams hp) {
+  __shared__ float s_vlut[256];
+  __shared__ float2 s_pair[256];
+  __shared__ float4 s_frac16[128];
+  s_vlut[threadIdx.x] = kVLogLut[threadIdx.x];
+  s_pair[threadIdx.x] = make_float2(kNf4Pair[2 * threadIdx.x], kNf4Pair[2 * threadIdx.x + 1]);
+  if (threadIdx.x < 128)
+    s_frac16[threadIdx.x] = make_float4(kNf4Code16[4 * threadIdx.x], kNf4Code16[4 * threadIdx.x + 1],
+                                        kNf4Code16[4 * threadIdx.x + 2], kNf4Code16[4 * threadIdx.x + 3]);
+  __syncthreads();
+  Q8Ctx c;
+  c.hp = &hp;
+  c.vlut = s_vlut;
+  c.code = nullptr;
+  c.pair = s_pair;
+  c.frac16 = s_frac16;
+  c.coef = (hp.flags & APEXW_HP_CLIP) ? *hp.clip_coef : 1.0f;
+  const uint32_t wave = uniform(threadIdx.x >> 6);
+  const int64_t stride = (int64_t)gridDim.x * kWaves;
+  for (int64_t u = (int64_t)blockIdx.x * kWaves + wave; u < n_units; u += stride) {
+    const apexw_unit un = units[u];
+    const apexw_tensor& t = tensors[un.tensor];
+    if (!apexw_q8_fast_ok(t.flags, t.block)) continue;  // never reached for a valid plan
+    const bool full = (int64_t)(un.unit + 1) * 2048 <= t.n;
+    const bool gen = t.flags & APEXW_FLAG_GENERIC;
+    if (hp.flags & APEXW_HP_SR) {
+      if (full && !gen) q8_block_fast<true, true, false>(t, un.tensor, un.unit, c);
+      else if (full) q8_block_fast<true, true, true>(t, un.tensor, un.unit, c);
+      else if (!gen) q8_block_fast<true, false, false>(t, un.tensor, un.unit, c);
+      else q8_block_fast<true, false, true>(t, un.tensor, un.unit, c);
+    } else {
+      if (full && !gen) q8_block_fast<false, true, false>(t, un.tensor, un.unit, c);
+      else if (full) q8_block_fast<false, true, true>(t, un.tensor, un.unit, c);
+      else if (!gen) q8_block_fast<false, false, false>(t, un.tensor, un.unit, c);
+      else q8_block_fast<false, false, true>(t, un.tensor, un.unit, c);
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void q8_step_kernel(const apexw_tensor* __restrict__ tensors,
                                                       const apexw_unit* __restrict__ units,
                                                       int64_t n_units, apexw_hparams hp) {
@@ -412,6 +698,8 @@ __global__ __launch_bounds__(256) void q8_step_kernel(const apexw_tensor* __rest
   c.hp = &hp;
   c.vlut = s_vlut;
   c.code = s_code;
+  c.pair = nullptr;
+  c.frac16 = nullptr;
   c.coef = (hp.flags & APEXW_HP_CLIP) ? *hp.clip_coef : 1.0f;
   const uint32_t wave = uniform(threadIdx.x >> 6);
   const int64_t stride = (int64_t)gridDim.x * kWaves;
@@ -446,6 +734,8 @@ __global__ __launch_bounds__(256) void q8_step_kernel(const apexw_tensor* __rest
 
 }  // namespace
 
+bool apexw_q8_fast_eligible(uint32_t flags, uint32_t block) { return apexw_q8_fast_ok(flags, block); }
+
 bool apexw_q8_flags_ok(uint32_t flags, uint32_t block, int64_t n) {
   const uint32_t pd = (flags >> APEXW_FLAG_PDT_SHIFT) & 3u, gd = (flags >> APEXW_FLAG_GDT_SHIFT) & 3u;
   if (!(pd == APEXW_F32 || pd == APEXW_BF16) || gd != pd) return false;
@@ -463,5 +753,11 @@ bool apexw_q8_flags_ok(uint32_t flags, uint32_t block, int64_t n) {
 int apexw_launch_q8(const apexw_tensor* tensors, int64_t n_units, const apexw_unit* units,
                     const apexw_hparams* hp, int grid, hipStream_t stream) {
   hipLaunchKernelGGL(q8_step_kernel, dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
+  return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
+}
+
+int apexw_launch_q8_fast(const apexw_tensor* tensors, int64_t n_units, const apexw_unit* units,
+                         const apexw_hparams* hp, int grid, hipStream_t stream) {
+  hipLaunchKernelGGL(q8_fast_kernel, dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }

@@ -57,7 +57,12 @@ def test_check_tensor_rejects_bad_descriptors():
     # entry points reject null tables before touching the GPU
     hp = _lib.HParams()
     assert lib.apexw_compact_step(None, 1, None, 1, ctypes.byref(hp), None) == 1
-    assert lib.apexw_q8_step(None, 1, None, 1, ctypes.byref(hp), None) == 1
+    assert lib.apexw_q8_step(None, 1, None, 1, 0, ctypes.byref(hp), None) == 1
+    q.block = 2048
+    assert lib.apexw_check_tensor(ctypes.byref(q), 2) == 0
+    q.flags &= ~_lib.FLAG_NF4
+    q.flags &= ~_lib.FLAG_QUAD
+    assert lib.apexw_check_tensor(ctypes.byref(q), 2) == 2
 
 
 _CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2, torch.int8: 3, torch.uint8: 4}

@@ -1,0 +1,146 @@
+"""The execution-plan host logic, exercised on the CPU with the kernel launches recorded.
+
+The plan builds device tables from tensor pointers and launches through the
+C ABI; here the ABI step functions are replaced by recorders (no GPU), so table
+layout, unit splitting, fast/general partition, cold/replay mode and the
+host-computed scalars are checked without touching a device.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from apexw_amd import _lib as L
+from apexw_amd import _plan
+
+
+class _Recorder:
+    def __init__(self, real):
+        self.real = real
+        self.calls = []
+
+    def __getattr__(self, name):
+        return getattr(self.real, name)
+
+    def _rec(self, name, args):
+        hp = ctypes.cast(args[-2], ctypes.POINTER(L.HParams)).contents if name != "clip" else None
+        self.calls.append((name, args, None if hp is None else {f: getattr(hp, f) for f, _ in L.HParams._fields_}))
+        return 0
+
+    def apexw_compact_step(self, *a):
+        return self._rec("compact", a)
+
+    def apexw_q8_step(self, *a):
+        return self._rec("q8", a)
+
+    def apexw_grad_clip_coef(self, *a):
+        self.calls.append(("clip", a, None))
+        return 0
+
+
+@pytest.fixture
+def cpu_plans(monkeypatch):
+    """Let plans run on CPU tensors: current_stream -> dummy, library step calls recorded."""
+    rec = _Recorder(L.load())
+    monkeypatch.setattr(_plan.StepPlan, "_lib", property(lambda self: rec, lambda self, v: None), raising=False)
+
+    class _S:
+        cuda_stream = 0
+    monkeypatch.setattr(torch.cuda, "current_stream", lambda dev=None: _S())
+    return rec
+
+
+def _opt(params, **kw):
+    from apexw_amd.optimizer import ApexW
+    opt = ApexW(params, **kw)
+    opt._build_plan_orig = opt._build_plan
+    return opt
+
+
+def _build(opt):
+    group = opt.param_groups[0]
+    from apexw_amd import state as S
+    group["precision"] = S.normalize_precision(group["precision"])
+    params = [p for p in group["params"] if p.grad is not None]
+    peft = S.detect_peft_context(opt.param_groups)
+    for p in params:
+        if len(opt.state[p]) == 0:
+            opt.state[p].update(S.init_state(p, group, peft))
+    kind = "q8" if group["precision"] == "8bit" else "compact"
+    return _plan.StepPlan(opt, group, params, kind), group
+
+
+def _params(shapes, dtype):
+    ps = []
+    for s in shapes:
+        p = torch.nn.Parameter(torch.zeros(s, dtype=dtype))
+        p.grad = torch.zeros(s, dtype=dtype)
+        ps.append(p)
+    return ps
+
+
+def test_q8_plan_partitions_fast_tensors_first(cpu_plans):
+    shapes = [(4096,), (512, 1024), (100, 300), (50,), (64, 2048)]
+    ps = _params(shapes, torch.bfloat16)
+    opt = _opt(ps, precision="8bit", lr=1e-3, weight_decay=0.1, adamw_compat=True)
+    plan, group = _build(opt)
+    plan.execute(group, seed=7)
+    name, args, hp = cpu_plans.calls[-1]
+    assert name == "q8"
+    # fast: (512,1024), (100,300) (short last block) and (64,2048) -- bf16, NF4, quad, block 2048
+    fast_counts = [512 * 1024 // 2048, (30000 + 2047) // 2048, 64 * 2048 // 2048]
+    assert args[4] == sum(fast_counts)
+    assert plan.fast.tolist() == [False, True, True, False, True]
+    units = plan.d_units.cpu().numpy().view(L.UNIT_DTYPE)
+    assert units["tensor"][: sum(fast_counts)].max() == 2  # first three table rows are the fast tensors
+    assert hp["mode"] == L.MODE_COLD and hp["step"] == 1
+    assert hp["flags"] & L.HP_SR
+    table = plan.d_table.cpu().numpy().view(L.TENSOR_DTYPE)
+    assert [int(n) for n in table["n"]] == [512 * 1024, 30000, 64 * 2048, 4096, 50]
+    plan.execute(group, seed=7)
+    assert cpu_plans.calls[-1][2]["mode"] == L.MODE_REPLAY and cpu_plans.calls[-1][2]["step"] == 2
+
+
+def test_compact_plan_scalars_and_modes(cpu_plans):
+    ps = _params([(128, 256), (300,)], torch.float32)
+    opt = _opt(ps, lr=1e-3, weight_decay=0.1, adamw_compat=True, stochastic_rounding=False)
+    plan, group = _build(opt)
+    plan.execute(group, seed=1)
+    name, args, hp = cpu_plans.calls[-1]
+    assert name == "compact" and args[3] == 16 + 1
+    b1, b2 = 0.9, 0.999
+    bc1, bc2 = 1 - b1, 1 - b2
+    assert hp["step_size"] == pytest.approx(1e-3 * bc2 ** 0.5 / bc1, rel=1e-6)
+    assert hp["eps_scaled"] == pytest.approx(1e-8 * bc2 ** 0.5, rel=1e-6)
+    assert hp["wd_factor"] == pytest.approx(1 - 1e-4, rel=1e-7)
+    assert hp["flags"] & L.HP_SANITIZE and not hp["flags"] & L.HP_SR
+    assert hp["mode"] == L.MODE_COLD
+    table = plan.d_table.cpu().numpy().view(L.TENSOR_DTYPE)
+    assert all(table["flags"] & L.FLAG_WD)  # adamw_compat decays every tensor
+    plan.execute(group, seed=1)
+    hp2 = cpu_plans.calls[-1][2]
+    assert hp2["mode"] == L.MODE_REPLAY and not hp2["flags"] & L.HP_SANITIZE
+    assert [float(s) for s in (opt.state[p]["step"] for p in ps)] == [2.0, 2.0]
+
+
+def test_step_counters_share_one_buffer(cpu_plans):
+    ps = _params([(10,), (20,), (30,)], torch.bfloat16)
+    opt = _opt(ps)
+    plan, group = _build(opt)
+    for _ in range(3):
+        plan.execute(group, seed=0)
+    steps = [opt.state[p]["step"] for p in ps]
+    assert all(float(s) == 3.0 for s in steps)
+    assert all(s.untyped_storage().data_ptr() == plan.steps.untyped_storage().data_ptr() for s in steps)
+
+
+def test_cold_step_splits_by_step_count(cpu_plans):
+    ps = _params([(64,), (64,)], torch.bfloat16)
+    opt = _opt(ps, precision="8bit")
+    plan, group = _build(opt)
+    plan.steps[1] = 5.0
+    plan.execute(group, seed=0)
+    q8 = [c for c in cpu_plans.calls if c[0] == "q8"]
+    assert sorted(c[2]["step"] for c in q8[-2:]) == [1, 6]

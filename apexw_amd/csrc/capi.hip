@@ -9,12 +9,12 @@
 
 #include "common.h"
 
-int apexw_launch_compact(const apexw_tensor*, int64_t, const apexw_unit*, const apexw_hparams*, int, hipStream_t);
-int apexw_launch_q8(const apexw_tensor*, int64_t, const apexw_unit*, const apexw_hparams*, int, hipStream_t);
-int apexw_launch_q8_fast(const apexw_tensor*, int64_t, const apexw_unit*, const apexw_hparams*, int, hipStream_t);
+int apexw_launch_compact(const apexw_tensor*, int64_t, const apexw_unit*, const apexw_hparams*, hipStream_t);
+int apexw_launch_q8(const apexw_tensor*, int64_t, const apexw_unit*, const apexw_hparams*, hipStream_t);
+int apexw_launch_q8_fast(const apexw_tensor*, int64_t, const apexw_unit*, const apexw_hparams*, hipStream_t);
 bool apexw_q8_fast_eligible(uint32_t flags, uint32_t block);
 int apexw_launch_clip(const apexw_tensor*, int32_t, const apexw_unit*, int64_t, int64_t, const int64_t*, float*, float*,
-                      float, uint32_t, float*, int, int, hipStream_t);
+                      float, uint32_t, float*, hipStream_t);
 bool apexw_compact_flags_ok(uint32_t flags);
 bool apexw_q8_flags_ok(uint32_t flags, uint32_t block, int64_t n);
 
@@ -35,13 +35,27 @@ int cu_count() {
   return g_cu_count[dev];
 }
 
-// Persistent grid: enough 4-wave workgroups to cover the units, capped at
-// `per_cu` resident workgroups per CU.
-int persistent_grid(int64_t n_units, int per_cu) {
-  const int64_t want = (n_units + 3) / 4;
-  const int64_t cap = (int64_t)cu_count() * per_cu;
-  const int64_t g = want < cap ? want : cap;
-  return (int)(g > 0 ? g : 1);
+// Resident 256-thread workgroups per CU, cached per (device, kernel).
+struct OccEntry {
+  int dev;
+  const void* kernel;
+  int blocks;
+};
+constexpr int kMaxOcc = 64;
+OccEntry g_occ[kMaxOcc];
+int g_n_occ = 0;
+std::mutex g_occ_mu;
+
+int blocks_per_cu(const void* kernel) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+  std::lock_guard<std::mutex> lk(g_occ_mu);
+  for (int i = 0; i < g_n_occ; ++i)
+    if (g_occ[i].dev == dev && g_occ[i].kernel == kernel) return g_occ[i].blocks;
+  int b = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, kernel, 256, 0) != hipSuccess || b <= 0) b = 1;
+  if (g_n_occ < kMaxOcc) g_occ[g_n_occ++] = {dev, kernel, b};
+  return b;
 }
 
 bool hp_ok(const apexw_hparams* hp) {
@@ -52,6 +66,16 @@ bool hp_ok(const apexw_hparams* hp) {
 }
 
 }  // namespace
+
+int apexw_resident_grid(const void* kernel, int64_t n_units) {
+  const int64_t want = (n_units + 3) / 4;
+  // 16 workgroups per resident slot: workgroups queue behind the resident ones,
+  // so CUs that finish early pick up more of the grid (measured on the 8B 8-bit
+  // step: 16x is ~4% faster than a grid of exactly the resident workgroups)
+  const int64_t cap = (int64_t)cu_count() * blocks_per_cu(kernel) * 16;
+  const int64_t g = want < cap ? want : cap;
+  return (int)(g > 0 ? g : 1);
+}
 
 extern "C" {
 
@@ -82,7 +106,7 @@ int apexw_compact_step(const apexw_tensor* tensors, int32_t n_tensors, const ape
                        const apexw_hparams* hp, void* stream) {
   if (!tensors || !units || n_tensors <= 0 || n_units < 0 || !hp_ok(hp)) return APEXW_ERR_ARG;
   if (n_units == 0) return APEXW_OK;
-  return apexw_launch_compact(tensors, n_units, units, hp, persistent_grid(n_units, 8), (hipStream_t)stream);
+  return apexw_launch_compact(tensors, n_units, units, hp, (hipStream_t)stream);
 }
 
 int apexw_q8_step(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,
@@ -92,10 +116,10 @@ int apexw_q8_step(const apexw_tensor* tensors, int32_t n_tensors, const apexw_un
   if (hp->mode == APEXW_MODE_NATIVE) return APEXW_ERR_ARG;
   int st = APEXW_OK;
   if (n_fast_units > 0)
-    st = apexw_launch_q8_fast(tensors, n_fast_units, units, hp, persistent_grid(n_fast_units, 8), (hipStream_t)stream);
+    st = apexw_launch_q8_fast(tensors, n_fast_units, units, hp, (hipStream_t)stream);
   const int64_t rest = n_units - n_fast_units;
   if (st == APEXW_OK && rest > 0)
-    st = apexw_launch_q8(tensors, rest, units + n_fast_units, hp, persistent_grid(rest, 8), (hipStream_t)stream);
+    st = apexw_launch_q8(tensors, rest, units + n_fast_units, hp, (hipStream_t)stream);
   return st;
 }
 
@@ -105,8 +129,7 @@ int apexw_grad_clip_coef(const apexw_tensor* tensors, int32_t n_tensors, const a
   if (!tensors || !units || !unit_begin || !unit_partial || !tensor_norm || !coef) return APEXW_ERR_ARG;
   if (n_tensors <= 0 || n_units < 0 || unit_size < 0 || !(clip > 0.0f)) return APEXW_ERR_ARG;
   return apexw_launch_clip(tensors, n_tensors, units, n_units, unit_size, unit_begin, unit_partial, tensor_norm, clip,
-                           flags, coef, persistent_grid(n_units, 8), persistent_grid(n_tensors, 8),
-                           (hipStream_t)stream);
+                           flags, coef, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -16,6 +16,7 @@
 
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
 typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
 
 // Pointers read out of the tensor table are generic; casting them to the global
 // address space lets the compiler emit global_load/global_store instead of flat.
@@ -176,4 +177,9 @@ APEXW_DEV float wave_sum(float x) {
 }
 
 APEXW_DEV int lane_id() { return (int)(threadIdx.x & 63u); }
+
+// Grid for a 256-thread (4-wave) kernel that strides over `n_units` work units,
+// one unit per wave: at most 16 workgroups per resident slot (blocks per CU from
+// the kernel's occupancy on the current device).
+int apexw_resident_grid(const void* kernel, int64_t n_units);
 APEXW_DEV uint32_t uniform(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }

@@ -263,7 +263,8 @@ static bool compact_combo_ok(uint32_t flags) {
 }
 
 int apexw_launch_compact(const apexw_tensor* tensors, int64_t n_units, const apexw_unit* units,
-                         const apexw_hparams* hp, int grid, hipStream_t stream) {
+                         const apexw_hparams* hp, hipStream_t stream) {
+  const int grid = apexw_resident_grid((const void*)compact_step_kernel, n_units);
   hipLaunchKernelGGL(compact_step_kernel, dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }

@@ -97,12 +97,14 @@ __global__ __launch_bounds__(1024) void clip_coef_kernel(const float* __restrict
 
 int apexw_launch_clip(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,
                       int64_t unit_size, const int64_t* unit_begin, float* unit_partial, float* tensor_norm,
-                      float clip, uint32_t flags, float* coef, int grid_units, int grid_tensors, hipStream_t stream) {
+                      float clip, uint32_t flags, float* coef, hipStream_t stream) {
   if (n_units > 0) {
+    const int grid_units = apexw_resident_grid((const void*)sumsq_kernel, n_units);
     hipLaunchKernelGGL(sumsq_kernel, dim3(grid_units), dim3(256), 0, stream, tensors, units, n_units, unit_size,
                        unit_partial, flags);
   }
   if (n_tensors > 0) {
+    const int grid_tensors = apexw_resident_grid((const void*)tensor_norm_kernel, n_tensors);
     hipLaunchKernelGGL(tensor_norm_kernel, dim3(grid_tensors), dim3(256), 0, stream, tensors, n_tensors, unit_begin,
                        unit_partial, tensor_norm);
   }

@@ -398,11 +398,15 @@ APEXW_DEV void q8_block(const apexw_tensor& t, uint32_t tix, uint32_t blk, const
 //  * SR off (the parity mode): exact IEEE divisions and midpoint comparisons,
 //    identical to q8_block;
 //  * SR on: random bits come from a per-lane xorshift32 stream seeded by a
-//    keyed hash of (tensor, block, lane) -- 32 bits per element: bits 0-15 round
-//    the bf16 parameter, bits 16-27 the NF4 code, bits 28-31 of the four
-//    elements of a quad its log-uint8 code; divisions use per-quad / per-block reciprocals; the
-//    parameter update is one fma (p*decay - update) before rounding; NF4 codes
-//    come from the signed fractional-index table: code = (G(x) + r12) >> 12.
+//    keyed hash of (tensor, block, lane) -- 32 bits per element: bits 16-31 round
+//    the bf16 parameter (v_cvt_sr_bf16_f32), bits 0-11 the NF4 code, bits 12-15
+//    of the quad's first two elements its log-uint8 code; dequantisation is folded into the
+//    momentum update (m' = code*ms*b1 + (1-b1)*g), the SNR gain into the quad's
+//    reciprocal denominator, and a non-finite grad is detected from its quad's
+//    sum of squares; the parameter update is one fma (p*decay - update) before
+//    rounding; NF4 codes come from the signed fractional-index table:
+//    code = (G(x) + r12) >> 12, two codes per 32-bit integer add, gathered
+//    into bytes with v_perm_b32.
 template <bool SR, bool FULL, bool GENERIC>
 APEXW_DEV void q8_block_fast(const apexw_tensor& t, uint32_t tix, uint32_t blk, const Q8Ctx& c) {
   const apexw_hparams& hp = *c.hp;
@@ -451,6 +455,7 @@ APEXW_DEV void q8_block_fast(const apexw_tensor& t, uint32_t tix, uint32_t blk, 
     rs = mix32(key + (blk << 6) + (uint32_t)lane) | 1u;
   }
   const bool prep = hf & (APEXW_HP_SANITIZE | APEXW_HP_CLIP);
+  const float msb1 = ms_old * hp.beta1;  // dequantisation scale folded into the momentum decay
 
   float mnew[4][8], vq[4][2];
   uint32_t hbits[4][8];   // this pass's random words
@@ -461,20 +466,18 @@ APEXW_DEV void q8_block_fast(const apexw_tensor& t, uint32_t tix, uint32_t blk, 
     float p[8], g[8], m[8];
     const uint32_t pv[4] = {pw[k].x, pw[k].y, pw[k].z, pw[k].w};
     const uint32_t gv[4] = {gw[k].x, gw[k].y, gw[k].z, gw[k].w};
+    float look[8];
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
       p[2 * b] = __uint_as_float(pv[b] << 16);
       p[2 * b + 1] = __uint_as_float(pv[b] & 0xFFFF0000u);
       g[2 * b] = __uint_as_float(gv[b] << 16);
       g[2 * b + 1] = __uint_as_float(gv[b] & 0xFFFF0000u);
-      const float2 pr = c.pair[(mw[k] >> (8 * b)) & 0xFFu];
-      m[2 * b] = pr.x * ms_old;
-      m[2 * b + 1] = pr.y * ms_old;
     }
     if (prep) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) g[j] = q8_grad<APEXW_BF16>(g[j], tf, c);
-    } else {
+    } else if constexpr (!SR) {
       bool bad = false;
 #pragma unroll
       for (int j = 0; j < 8; ++j) bad |= !__builtin_isfinite(g[j]);
@@ -492,32 +495,80 @@ APEXW_DEV void q8_block_fast(const apexw_tensor& t, uint32_t tix, uint32_t blk, 
         hbits[k][j] = rs;
       }
     }
-    float num[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      m[j] = lerp_to(m[j], g[j], hp.lerp_coef, lerp_hi);
-      const float look = lerp_to(g[j], m[j], hp.look_coef, look_hi);
-      num[j] = look * ((m[j] * g[j] >= 0.0f) ? hp.gain_hi : hp.gain_lo);
-    }
     float upd[8];
+    if constexpr (SR) {
+      // quad sums of squares first: a non-finite grad makes its quad's sum
+      // non-finite, which sends the group through nan_to_num (rare path)
+      float s2[2];
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int b = 4 * q;
-      float s2 = g[b] * g[b];
-      s2 = s2 + g[b + 1] * g[b + 1];
-      s2 = s2 + g[b + 2] * g[b + 2];
-      s2 = s2 + g[b + 3] * g[b + 3];
-      const float vold = c.vlut[(vw[k] >> (8 * q)) & 0xFFu] * vs_old;
-      float vv = fmaf(hp.one_minus_beta2, s2 * 0.25f, vold * hp.beta2);
-      if (!(fabsf(vv) <= 3.402823466e38f)) vv = 0.0f;
-      vq[k][q] = vv;
-      if (FULL || 4 * q < cnt[k]) vmax = fmaxf(vmax, vv);
-      if constexpr (SR) {
-        const float den = fmaxf(__builtin_amdgcn_sqrtf(vv) + hp.eps_scaled, hp.eps);
-        const float r = __builtin_amdgcn_rcpf(den) * hp.step_size;
+      for (int q = 0; q < 2; ++q) {
+        const int b = 4 * q;
+        float t = g[b] * g[b];
+        t = fmaf(g[b + 1], g[b + 1], t);
+        t = fmaf(g[b + 2], g[b + 2], t);
+        s2[q] = fmaf(g[b + 3], g[b + 3], t);
+      }
+      if (!prep && !(__builtin_isfinite(s2[0]) && __builtin_isfinite(s2[1]))) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) upd[b + i] = num[b + i] * r;
-      } else {
+        for (int j = 0; j < 8; ++j) g[j] = q8_grad<APEXW_BF16>(g[j], tf, c);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const int b = 4 * q;
+          float t = g[b] * g[b];
+          t = fmaf(g[b + 1], g[b + 1], t);
+          t = fmaf(g[b + 2], g[b + 2], t);
+          s2[q] = fmaf(g[b + 3], g[b + 3], t);
+        }
+      }
+      // m' = lerp(dequant(m), g, 1-b1) = code*ms*b1 + (1-b1)*g, lookahead = b1*m' + (1-b1)*g
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const float2 pr = c.pair[(mw[k] >> (8 * b)) & 0xFFu];
+        const float wg0 = hp.one_minus_beta1 * g[2 * b], wg1 = hp.one_minus_beta1 * g[2 * b + 1];
+        m[2 * b] = fmaf(pr.x, msb1, wg0);
+        m[2 * b + 1] = fmaf(pr.y, msb1, wg1);
+        look[2 * b] = fmaf(hp.beta1, m[2 * b], wg0);
+        look[2 * b + 1] = fmaf(hp.beta1, m[2 * b + 1], wg1);
+      }
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int b = 4 * q;
+        const float vold = c.vlut[(vw[k] >> (8 * q)) & 0xFFu] * vs_old;
+        float vv = fmaf(hp.one_minus_beta2, s2[q] * 0.25f, vold * hp.beta2);
+        if (!(fabsf(vv) <= 3.402823466e38f)) vv = 0.0f;
+        vq[k][q] = vv;
+        if (FULL || 4 * q < cnt[k]) vmax = fmaxf(vmax, vv);
+        const float r = __builtin_amdgcn_rcpf(fmaxf(__builtin_amdgcn_sqrtf(vv) + hp.eps_scaled, hp.eps)) * hp.step_size;
+        const float r_hi = r * hp.gain_hi, r_lo = r * hp.gain_lo;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) upd[b + i] = look[b + i] * ((m[b + i] * g[b + i] >= 0.0f) ? r_hi : r_lo);
+      }
+    } else {
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const float2 pr = c.pair[(mw[k] >> (8 * b)) & 0xFFu];
+        m[2 * b] = pr.x * ms_old;
+        m[2 * b + 1] = pr.y * ms_old;
+      }
+      float num[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        m[j] = lerp_to(m[j], g[j], hp.lerp_coef, lerp_hi);
+        const float lk = lerp_to(g[j], m[j], hp.look_coef, look_hi);
+        num[j] = lk * ((m[j] * g[j] >= 0.0f) ? hp.gain_hi : hp.gain_lo);
+      }
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int b = 4 * q;
+        float s2 = g[b] * g[b];
+        s2 = s2 + g[b + 1] * g[b + 1];
+        s2 = s2 + g[b + 2] * g[b + 2];
+        s2 = s2 + g[b + 3] * g[b + 3];
+        const float vold = c.vlut[(vw[k] >> (8 * q)) & 0xFFu] * vs_old;
+        float vv = fmaf(hp.one_minus_beta2, s2 * 0.25f, vold * hp.beta2);
+        if (!(fabsf(vv) <= 3.402823466e38f)) vv = 0.0f;
+        vq[k][q] = vv;
+        if (FULL || 4 * q < cnt[k]) vmax = fmaxf(vmax, vv);
         const float den = fmaxf(sqrtf(vv) + hp.eps_scaled, hp.eps);
 #pragma unroll
         for (int i = 0; i < 4; ++i) upd[b + i] = (num[b + i] / den) * hp.step_size;
@@ -526,21 +577,34 @@ APEXW_DEV void q8_block_fast(const apexw_tensor& t, uint32_t tix, uint32_t blk, 
     uint32_t pout[4];
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-      float x[2];
+      if constexpr (SR) {
+        // v_cvt_sr_bf16_f32 adds bits 16-31 of the random word to the fp32 pattern
+        // and truncates (add-noise-then-truncate SR), writing one half of the pair
+        float y[2];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int j = 2 * b + i;
-        if constexpr (SR) {
-          const float y = GENERIC ? rnd<APEXW_BF16>(p[j] * decay) - upd[j] : fmaf(p[j], decay, -upd[j]);
-          x[i] = __uint_as_float(__float_as_uint(y) + (hbits[k][j] & 0xFFFFu));
-        } else if constexpr (GENERIC) {
-          x[i] = rnd<APEXW_BF16>(rnd<APEXW_BF16>(p[j] * decay) - rnd<APEXW_BF16>(upd[j]));
-        } else {
-          x[i] = rnd<APEXW_BF16>(p[j] * decay - upd[j]);
+        for (int i = 0; i < 2; ++i) {
+          const int j = 2 * b + i;
+          y[i] = GENERIC ? rnd<APEXW_BF16>(p[j] * decay) - upd[j] : fmaf(p[j], decay, -upd[j]);
         }
+        bf16x2 pr = __builtin_bit_cast(bf16x2, pv[b]);
+        pr = __builtin_amdgcn_cvt_sr_bf16_f32(pr, y[0], hbits[k][2 * b], false);
+        pr = __builtin_amdgcn_cvt_sr_bf16_f32(pr, y[1], hbits[k][2 * b + 1], true);
+        pout[b] = __builtin_bit_cast(uint32_t, pr);
+        // bits 0-15 of both words, kept for the NF4 (bits 0-11) and v (bits 12-15) codes
+        hm[k][b] = __builtin_amdgcn_perm(hbits[k][2 * b + 1], hbits[k][2 * b], 0x05040100u);
+      } else {
+        float x[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int j = 2 * b + i;
+          if constexpr (GENERIC) {
+            x[i] = rnd<APEXW_BF16>(rnd<APEXW_BF16>(p[j] * decay) - rnd<APEXW_BF16>(upd[j]));
+          } else {
+            x[i] = rnd<APEXW_BF16>(p[j] * decay - upd[j]);
+          }
+        }
+        pout[b] = (__float_as_uint(x[0]) >> 16) | (__float_as_uint(x[1]) & 0xFFFF0000u);
       }
-      pout[b] = (__float_as_uint(x[0]) >> 16) | (__float_as_uint(x[1]) & 0xFFFF0000u);
-      if constexpr (SR) hm[k][b] = (hbits[k][2 * b] >> 16) | (hbits[k][2 * b + 1] & 0xFFFF0000u);
     }
     const int64_t e = start + k * 512 + lane * 8;
     u32x4 po = {pout[0], pout[1], pout[2], pout[3]};
@@ -570,25 +634,38 @@ APEXW_DEV void q8_block_fast(const apexw_tensor& t, uint32_t tix, uint32_t blk, 
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int64_t e = start + k * 512 + lane * 8;
-    uint32_t code[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      if constexpr (SR) {
-        // x in [-1, 1 - 2^-22] keeps x + 3 inside [2, 4): its top 7 mantissa bits are the bucket
-        const float x = __builtin_amdgcn_fmed3f(mnew[k][j] * rms, -1.0f, 0x1.fffffcp-1f);
-        const uint32_t bkt = (__float_as_uint(x + 3.0f) >> 16) & 127u;
-        const float4 fr = c.frac16[bkt];
-        const float lim = __uint_as_float((__float_as_uint(x) & 0x80000000u) | 0x7F800000u);
-        const float gcode = __builtin_amdgcn_fmed3f(fmaf(fr.y, x, fr.x), fmaf(fr.w, x, fr.z), -lim);
-        const uint32_t r12 = (hm[k][j >> 1] >> ((j & 1) ? 16 : 0)) & 0xFFFu;
-        code[j] = ((uint32_t)gcode + r12) >> 12;
-      } else {
-        code[j] = nf4_rne(fminf(fmaxf(mnew[k][j] / ms, -1.0f), 1.0f));
-      }
-    }
     uint32_t w = 0;
+    if constexpr (SR) {
+      uint32_t sum[4];
 #pragma unroll
-    for (int b = 0; b < 4; ++b) w |= ((code[2 * b] << 4) | code[2 * b + 1]) << (8 * b);
+      for (int b = 0; b < 4; ++b) {
+        uint32_t gc[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          // y = x + 3 for x = m / scale in [-1, 1], clamped below 4: the top 7
+          // mantissa bits of y in [2, 4) are the bucket; the table is affine in y
+          const float y = __builtin_amdgcn_fmed3f(fmaf(mnew[k][2 * b + i], rms, 3.0f), 2.0f, 0x1.fffffep+1f);
+          const float4 fr = c.frac16[(__float_as_uint(y) >> 16) & 127u];
+          gc[i] = (uint32_t)fabsf(fminf(fmaf(fr.y, y, fr.x), fmaf(fr.w, y, fr.z)));
+        }
+        // two 16-bit lanes of G + r12 (r12 = bits 0-11 of the element's word):
+        // the stochastic code lands in bits 12-15 and 28-31
+        sum[b] = (gc[0] | (gc[1] << 16)) + (hm[k][b] & 0x0FFF0FFFu);
+      }
+      // gather bytes 1 and 3 (code << 4 | noise) of the four pair sums, then
+      // byte b = code[2b] << 4 | code[2b+1]
+      const uint32_t lo01 = __builtin_amdgcn_perm(sum[1], sum[0], 0x07030501u);  // s0.b1 s1.b1 s0.b3 s1.b3
+      const uint32_t lo23 = __builtin_amdgcn_perm(sum[3], sum[2], 0x07030501u);
+      const uint32_t even = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);      // code[2b] in high nibbles
+      const uint32_t odd = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);       // code[2b+1] in high nibbles
+      w = (even & 0xF0F0F0F0u) | ((odd >> 4) & 0x0F0F0F0Fu);
+    } else {
+      uint32_t code[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) code[j] = nf4_rne(fminf(fmaxf(mnew[k][j] / ms, -1.0f), 1.0f));
+#pragma unroll
+      for (int b = 0; b < 4; ++b) w |= ((code[2 * b] << 4) | code[2 * b + 1]) << (8 * b);
+    }
     uint32_t vc[2];
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
@@ -597,10 +674,10 @@ APEXW_DEV void q8_block_fast(const apexw_tensor& t, uint32_t tix, uint32_t blk, 
         vc[q] = 0u;
       } else if constexpr (SR) {
         const float r = fmaxf(vv * rvs, 0x1p-24f);
-        // bits 28-31 of the quad's four words -> 16 bits -> u = (r + 1/2) / 2^16, then floor
-        const uint32_t a = hm[k][2 * q], b = hm[k][2 * q + 1];
-        const uint32_t r16 = ((a >> 12) & 0xFu) | ((a >> 24) & 0xF0u) | ((b >> 4) & 0xF00u) | ((b >> 16) & 0xF000u);
-        const float u = __uint_as_float(0x3F800040u | (r16 << 7)) - 1.0f;
+        // bits 12-15 of the quad's first two words -> 8 bits -> u = (r + 1/2) / 2^8, then floor
+        const uint32_t a = hm[k][2 * q];
+        const uint32_t r8 = ((a >> 12) & 0xFu) | ((a >> 24) & 0xF0u);
+        const float u = __uint_as_float(0x3F804000u | (r8 << 15)) - 1.0f;
         const float qf = fmaf(__builtin_amdgcn_logf(r), 0x1.52aaaap+3f, 255.0f) + u;
         vc[q] = (uint32_t)__builtin_amdgcn_fmed3f(qf, 1.0f, 255.0f);
       } else {
@@ -751,13 +828,15 @@ bool apexw_q8_flags_ok(uint32_t flags, uint32_t block, int64_t n) {
 }
 
 int apexw_launch_q8(const apexw_tensor* tensors, int64_t n_units, const apexw_unit* units,
-                    const apexw_hparams* hp, int grid, hipStream_t stream) {
+                    const apexw_hparams* hp, hipStream_t stream) {
+  const int grid = apexw_resident_grid((const void*)q8_step_kernel, n_units);
   hipLaunchKernelGGL(q8_step_kernel, dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }
 
 int apexw_launch_q8_fast(const apexw_tensor* tensors, int64_t n_units, const apexw_unit* units,
-                         const apexw_hparams* hp, int grid, hipStream_t stream) {
+                         const apexw_hparams* hp, hipStream_t stream) {
+  const int grid = apexw_resident_grid((const void*)q8_fast_kernel, n_units);
   hipLaunchKernelGGL(q8_fast_kernel, dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }

@@ -1,6 +1,7 @@
 """Benchmark: the ApexW 8-bit optimizer step on a Llama-3-8B-shaped parameter set.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--config c3|c2|c4|c1] [--no-cpu]
+    python bench.py --copy-calibration     # 1 GiB device copy, for HBM counter scaling
 
 Prints ONE JSON line (rank 0).  A "step" is one ``ApexW.step()`` over the full
 parameter list with synthetic bf16 params ~N(0, 0.02) and grads ~N(0, 1e-3)
@@ -10,6 +11,9 @@ already resident in HBM.  ``value`` is parameters updated per second.
 (8 TB/s): ``achieved`` = algorithmic bytes per launch (read + write of p, g,
 moment codes and block scales, computed from the actual state layout) divided
 by the average kernel time measured with HIP events on the launch stream.
+``traffic`` is the HBM bytes per launch measured with rocprofv3 FETCH_SIZE and
+WRITE_SIZE passes (scaled by the same counters on a copy of known size), read
+from the committed profile summary of this workload when one exists.
 ``cpu_baseline`` times the CPU oracle (the reference algorithm restated with
 torch CPU ops) on a bounded slice of the same workload on this host's cores.
 """
@@ -98,6 +102,38 @@ def make_params(cfg, device, seed=0):
     return params
 
 
+PROFILE_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
+TRAFFIC_FILES = {"c3": "q8_fast_kernel_llama3_8b_traffic.md"}
+
+
+def measured_traffic(cfg_name):
+    """HBM bytes per launch from the profile summary ('traffic_bytes_per_launch: N'), or None."""
+    name = TRAFFIC_FILES.get(cfg_name)
+    if not name:
+        return None
+    try:
+        with open(os.path.join(PROFILE_DIR, name)) as f:
+            for line in f:
+                if line.strip().startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip().split()[0])
+    except OSError:
+        return None
+    return None
+
+
+def copy_calibration():
+    """One 1 GiB fp32 device-to-device copy, three times: FETCH_SIZE / WRITE_SIZE of
+    this kernel against its known 1 GiB read and 1 GiB write give the counter scale."""
+    n = (1 << 30) // 4
+    x = torch.ones(n, dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration": {"bytes_read": n * 4, "bytes_written": n * 4, "launches": 3}}), flush=True)
+
+
 def state_bytes(opt, params):
     """Algorithmic HBM bytes of one step: p read+write, g read, every state tensor read+write."""
     tot = 0
@@ -150,11 +186,15 @@ def main():
     ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--copy-calibration", action="store_true", help="run the counter-calibration copy and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the optimizer step is data-parallel per shard and this build "
               "has no multi-GPU path; run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration()
+        return
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from apexw_amd import ApexW
 
@@ -188,7 +228,7 @@ def main():
         "config": {"workload": cfg["workload"], "params": n, "tensors": len(params),
                    "param_dtype": str(cfg["dtype"]).replace("torch.", ""), **{k: v for k, v in cfg["kwargs"].items()}},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": measured_traffic(args.config),
                      "kernel_ms": gpu_ms, "bytes_per_launch": nbytes, "bytes_per_param": nbytes / n},
     }
     if not args.no_cpu:

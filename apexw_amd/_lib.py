@@ -77,7 +77,16 @@ SIGNATURES = {
     "apexw_compact_step": (ctypes.c_int, [_vp, _i32, _vp, _i64, _HP, _vp]),
     "apexw_q8_step": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _HP, _vp]),
     "apexw_grad_clip_coef": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _vp, _vp, _vp, _f32, _u32, _vp, _vp]),
+    "apexw_gemm_nt_bf16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+                                          _i32, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _vp]),
+    "apexw_muon_workspace_floats": (ctypes.c_int64, [_i64, _i64]),
+    "apexw_muon_prepare": (ctypes.c_int, [_vp, _vp, _i32, _i64, _i64, _f32, _f32, _i32, _f32, _vp, _vp, _i64, _i64,
+                                          _vp, _vp]),
+    "apexw_muon_apply": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _i64, _f32, _i32, _f32, _vp]),
 }
+
+GEMM_TILE = 256
+GEMM_KTILE = 64
 
 _LIB = None
 

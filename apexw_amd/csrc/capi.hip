@@ -16,6 +16,14 @@ bool apexw_q8_fast_eligible(uint32_t flags, uint32_t block);
 int apexw_launch_clip(const apexw_tensor*, int32_t, const apexw_unit*, int64_t, int64_t, const int64_t*, float*, float*,
                       float, uint32_t, float*, hipStream_t);
 bool apexw_compact_flags_ok(uint32_t flags);
+int apexw_launch_gemm_nt(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, uint16_t*, int32_t, int32_t,
+                         int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int64_t, int64_t, int64_t,
+                         int64_t, int64_t, float, float, hipStream_t);
+int apexw_muon_partials(int64_t n);
+int apexw_launch_muon_prepare(float*, const void*, int32_t, int64_t, int64_t, float, float, int32_t, float, uint16_t*,
+                              uint16_t*, int64_t, int64_t, float*, hipStream_t);
+int apexw_launch_muon_apply(void*, int32_t, const uint16_t*, int64_t, int64_t, int64_t, float, int32_t, float,
+                            hipStream_t);
 bool apexw_q8_flags_ok(uint32_t flags, uint32_t block, int64_t n);
 
 namespace {
@@ -121,6 +129,49 @@ int apexw_q8_step(const apexw_tensor* tensors, int32_t n_tensors, const apexw_un
   if (st == APEXW_OK && rest > 0)
     st = apexw_launch_q8(tensors, rest, units + n_fast_units, hp, (hipStream_t)stream);
   return st;
+}
+
+int apexw_gemm_nt_bf16(const void* a, const void* b, const void* et, void* c, void* ct, int32_t m, int32_t n,
+                       int32_t k, int32_t lda, int32_t ldb, int32_t lde, int32_t ldc, int32_t ldct, int32_t batch,
+                       int64_t stride_a, int64_t stride_b, int64_t stride_e, int64_t stride_c, int64_t stride_ct,
+                       float alpha, float beta, void* stream) {
+  if (!a || !b || (!c && !ct) || (beta != 0.0f && !et)) return APEXW_ERR_ARG;
+  if (m <= 0 || n <= 0 || k <= 0 || batch <= 0 || batch > 65535) return APEXW_ERR_ARG;
+  if (m % APEXW_GEMM_TILE || n % APEXW_GEMM_TILE || k % APEXW_GEMM_KTILE) return APEXW_ERR_ARG;
+  // operand rows must cover the tile extents they are read over
+  if (lda < k || ldb < k || (c && ldc < n) || (ct && ldct < m) || (et && lde < m)) return APEXW_ERR_ARG;
+  if ((lda | ldb | (et ? lde : 0) | (c ? ldc : 0) | (ct ? ldct : 0)) & 7) return APEXW_ERR_ALIGN;
+  const uintptr_t al = (uintptr_t)a | (uintptr_t)b | (uintptr_t)et | (uintptr_t)c | (uintptr_t)ct;
+  if (al & 15u) return APEXW_ERR_ALIGN;
+  if ((stride_a | stride_b | stride_e | stride_c | stride_ct) & 7) return APEXW_ERR_ALIGN;
+  return apexw_launch_gemm_nt((const uint16_t*)a, (const uint16_t*)b, (const uint16_t*)et, (uint16_t*)c,
+                              (uint16_t*)ct, m, n, k, lda, ldb, lde, ldc, ldct, batch, stride_a, stride_b, stride_e,
+                              stride_c, stride_ct, alpha, beta, (hipStream_t)stream);
+}
+
+int64_t apexw_muon_workspace_floats(int64_t rows, int64_t cols) {
+  return rows > 0 && cols > 0 ? apexw_muon_partials(rows * cols) : 0;
+}
+
+int apexw_muon_prepare(float* buf, const void* g, int32_t g_dtype, int64_t rows, int64_t cols, float mu,
+                       float one_minus_mu, int32_t nesterov, float eps, void* x, void* xt, int64_t ldx, int64_t ldxt,
+                       float* workspace, void* stream) {
+  if (!buf || !g || !x || !xt || !workspace || rows <= 0 || cols <= 0) return APEXW_ERR_ARG;
+  if (g_dtype != APEXW_F32 && g_dtype != APEXW_BF16 && g_dtype != APEXW_F16) return APEXW_ERR_DTYPE;
+  // work matrix X is [min x max], X^T is [max x min]
+  const int64_t lo = rows < cols ? rows : cols, hi = rows < cols ? cols : rows;
+  if (ldx < hi || ldxt < lo) return APEXW_ERR_ARG;
+  (void)lo;
+  return apexw_launch_muon_prepare(buf, g, g_dtype, rows, cols, mu, one_minus_mu, nesterov, eps, (uint16_t*)x,
+                                   (uint16_t*)xt, ldx, ldxt, workspace, (hipStream_t)stream);
+}
+
+int apexw_muon_apply(void* p, int32_t p_dtype, const void* u, int64_t rows, int64_t cols, int64_t ldu,
+                     float wd_factor, int32_t apply_wd, float neg_lr_eff, void* stream) {
+  if (!p || !u || rows <= 0 || cols <= 0 || ldu < cols) return APEXW_ERR_ARG;
+  if (p_dtype != APEXW_F32 && p_dtype != APEXW_BF16 && p_dtype != APEXW_F16) return APEXW_ERR_DTYPE;
+  return apexw_launch_muon_apply(p, p_dtype, (const uint16_t*)u, rows, cols, ldu, wd_factor, apply_wd, neg_lr_eff,
+                                 (hipStream_t)stream);
 }
 
 int apexw_grad_clip_coef(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,

@@ -1,0 +1,341 @@
+// Muon on gfx950: fp32 momentum, Newton-Schulz with bf16 MFMA GEMMs, decoupled
+// weight decay and the scaled orthogonalised update.
+//
+// Newton-Schulz (apexw/muon.py:102-108, :135-184), per iteration on the wide
+// work matrix X [m x n], m <= n:
+//   A  = X X^T                 (symmetric, K = n)
+//   B  = c A A + b A           (symmetric, K = m)
+//   X' = B X + a X             (K = m)
+// Every product is computed as an "NT" GEMM (both operands K-contiguous): X is
+// kept in both layouts, X [m x n] and X^T [n x m], so B X = B (X^T)^T reads X^T
+// rows.  The epilogue of the last product writes X' in both layouts; the
+// symmetric products are written through the transposed store (same matrix).
+// Work matrices are zero-padded to multiples of the 256 x 256 tile; zero rows
+// and columns stay zero through every product, so the kernel has no bounds
+// checks.
+#include "common.h"
+
+namespace {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(4))) uint16_t u16x4;
+
+constexpr int kBM = 256, kBN = 256, kBK = 64;
+constexpr int kLds = kBK + 8;  // LDS row pitch (elements): 144 B keeps 8 consecutive rows on distinct banks
+
+struct GemmArgs {
+  const uint16_t* a;   // [M x K] row-major, ld lda
+  const uint16_t* b;   // [N x K] row-major, ld ldb
+  const uint16_t* et;  // addend, transposed: et[j * lde + i] is E[i][j] (may be null when beta == 0)
+  uint16_t* c;         // [M x N] row-major output, ld ldc (may be null)
+  uint16_t* ct;        // [N x M] transposed output, ld ldct (may be null)
+  int64_t sa, sb, se, sc, sct;  // batch strides (elements)
+  int32_t m, n, k, lda, ldb, lde, ldc, ldct;
+  float alpha, beta;
+};
+
+APEXW_DEV float bf(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+APEXW_DEV uint16_t to_bf(float x) { return (uint16_t)f32_to_bf16_bits(x); }
+
+// C = alpha * A B^T + beta * E (bf16 in, fp32 accumulate, bf16 out, round to nearest even).
+// 256 threads = 4 waves in a 2 x 2 arrangement, each owning a 128 x 128 block of
+// the 256 x 256 tile as 4 x 4 MFMA 32x32x16 accumulators.
+// Template flags select the epilogue: write O row-major (kC), transposed (kCt),
+// add beta * E (kAdd).
+template <bool kC, bool kCt, bool kAdd>
+__global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmArgs g) {
+  __shared__ __attribute__((aligned(16))) uint16_t s_a[2][kBM * kLds];
+  __shared__ __attribute__((aligned(16))) uint16_t s_b[2][kBN * kLds];
+
+  const int tiles_m = g.m / kBM, tiles_n = g.n / kBN, tiles = tiles_m * tiles_n;
+  // Consecutive workgroups are dispatched round-robin over the 8 XCDs; give each
+  // XCD a contiguous range of tiles, ordered in groups of 4 tile rows, so the A
+  // and B panels a range touches stay in that XCD's L2.
+  const int per_xcd = (tiles + 7) / 8;
+  const int t = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+  if (t >= tiles) return;
+  constexpr int kGroup = 4;
+  const int group = t / (kGroup * tiles_n), first_m = group * kGroup;
+  const int gm = min(tiles_m - first_m, kGroup);
+  const int in_group = t % (kGroup * tiles_n);
+  const int tm = first_m + in_group % gm, tn = in_group / gm;
+
+  // tile base pointers are uniform (SGPRs); per-lane offsets stay 32-bit
+  const int64_t batch = blockIdx.y;
+  const uint16_t* __restrict__ A = g.a + batch * g.sa + (int64_t)tm * kBM * g.lda;
+  const uint16_t* __restrict__ B = g.b + batch * g.sb + (int64_t)tn * kBN * g.ldb;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // global -> register staging, half a K tile at a time (4 x 16 B of A and of B
+  // per thread): the next tile streams in while the current one is multiplied
+  u32x4 ra[4], rb[4];
+  auto load = [&](int k0, int half) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + 256 * (i + 4 * half), r = c >> 3, c16 = c & 7;
+      ra[i] = __builtin_nontemporal_load(APEXW_GLOBAL(const u32x4, (A + k0) + (uint32_t)(r * g.lda + c16 * 8)));
+      rb[i] = __builtin_nontemporal_load(APEXW_GLOBAL(const u32x4, (B + k0) + (uint32_t)(r * g.ldb + c16 * 8)));
+    }
+  };
+  auto store = [&](int buf, int half) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + 256 * (i + 4 * half), r = c >> 3, c16 = c & 7;
+      *(u32x4*)&s_a[buf][r * kLds + c16 * 8] = ra[i];
+      *(u32x4*)&s_b[buf][r * kLds + c16 * 8] = rb[i];
+    }
+  };
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) acc[a][b] = f32x16{};
+
+  // MFMA 32x32x16 operand layout: lane l supplies row (l % 32) and k = 8 (l / 32) .. +7
+  const int frag_row = lane & 31, frag_k = (lane >> 5) * 8;
+  auto mma = [&](int buf, int s) {
+    bf16x8 fa[4], fb[4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+      fa[a] = *(const bf16x8*)&s_a[buf][(wm * 128 + a * 32 + frag_row) * kLds + s * 16 + frag_k];
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      fb[b] = *(const bf16x8*)&s_b[buf][(wn * 128 + b * 32 + frag_row) * kLds + s * 16 + frag_k];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[a], fb[b], acc[a][b], 0, 0, 0);
+  };
+
+  const int k_tiles = g.k / kBK;
+  load(0, 0);
+  store(0, 0);
+  load(0, 1);
+  store(0, 1);
+  __syncthreads();
+  for (int kt = 0; kt < k_tiles; ++kt) {
+    // LDS buffer buf ^ 1 was last read before the previous barrier: free to refill
+    const int buf = kt & 1;
+    const bool next = kt + 1 < k_tiles;
+    if (next) load((kt + 1) * kBK, 0);
+    mma(buf, 0);
+    mma(buf, 1);
+    if (next) {
+      store(buf ^ 1, 0);
+      load((kt + 1) * kBK, 1);
+    }
+    mma(buf, 2);
+    mma(buf, 3);
+    if (next) store(buf ^ 1, 1);
+    __syncthreads();
+  }
+
+  // Epilogue.  Accumulator register r of lane l holds row 8 (r / 4) + 4 (l / 32) + r % 4,
+  // column l % 32 of its 32 x 32 block: four consecutive rows of one column per group.
+  const int row0 = tm * kBM, col0 = tn * kBN;
+  const uint16_t* __restrict__ Et = kAdd ? g.et + batch * g.se + (int64_t)col0 * g.lde + row0 : nullptr;
+  uint16_t* __restrict__ C = kC ? g.c + batch * g.sc + (int64_t)row0 * g.ldc + col0 : nullptr;
+  uint16_t* __restrict__ Ct = kCt ? g.ct + batch * g.sct + (int64_t)col0 * g.ldct + row0 : nullptr;
+  const int lr = wm * 128 + (lane >> 5) * 4, lc = wn * 128 + (lane & 31);
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int j = lc + b * 32;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int i0 = lr + a * 32 + q * 8;
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = g.alpha * acc[a][b][q * 4 + r];
+        if constexpr (kAdd) {
+          const u16x4 e = *APEXW_GLOBAL(const u16x4, Et + (uint32_t)(j * g.lde + i0));
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v[r] = fmaf(g.beta, bf(e[r]), v[r]);
+        }
+        u16x4 o;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = to_bf(v[r]);
+        if constexpr (kCt) *APEXW_GLOBAL(u16x4, Ct + (uint32_t)(j * g.ldct + i0)) = o;
+        if constexpr (kC) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) *APEXW_GLOBAL(uint16_t, C + (uint32_t)((i0 + r) * g.ldc + j)) = o[r];
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Momentum (apexw/muon.py:763-792, fp32 buffer): buf = buf * mu, then
+// buf += (1 - mu) * g with g sanitized (NaN -> 0, +-Inf -> +-65504) and widened
+// to fp32.  The NS input ("update source") is buf, or lerp(g, buf, mu) with
+// Nesterov.  Per-block partial sums of squares of bf16(update source) give the
+// Frobenius norm of the bf16 work matrix.
+// ---------------------------------------------------------------------------
+template <int GD> APEXW_DEV float muon_grad(const void* grad, int64_t i) {
+  float g = load1<GD>(grad, i);
+  if (__builtin_isnan(g)) return 0.0f;
+  if (__builtin_isinf(g)) return g > 0.0f ? 65504.0f : -65504.0f;
+  return g;
+}
+
+// torch.lerp(g, m, w): g + w (m - g) for w < 0.5, else m - (1 - w)(m - g), one fma each
+APEXW_DEV float nesterov_source(float g, float m, float mu) {
+  return mu < 0.5f ? fmaf(mu, m - g, g) : fmaf(mu - 1.0f, m - g, m);
+}
+
+template <int GD>
+__global__ __launch_bounds__(256) void muon_momentum_kernel(float* __restrict__ buf, const void* __restrict__ grad,
+                                                            int64_t n, float mu, float one_minus_mu, int nesterov,
+                                                            float* __restrict__ partial) {
+  float s = 0.0f;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const float g = muon_grad<GD>(grad, i);
+    const float m = fmaf(one_minus_mu, g, APEXW_GLOBAL(float, buf)[i] * mu);
+    APEXW_GLOBAL(float, buf)[i] = m;
+    const float x = rnd<APEXW_BF16>(nesterov ? nesterov_source(g, m, mu) : m);
+    s = fmaf(x, x, s);
+  }
+  s = wave_sum(s);
+  __shared__ float red[4];
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) partial[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// X = bf16(bf16(buf) / d) with d = bf16(bf16(||bf16(buf)||_F) + eps) (the bf16
+// torch ops of zeropower_via_newtonschulz5), written as the work matrix in both
+// layouts.  The work matrix is buf itself when rows <= cols, else buf^T.
+// 64 x 64 tiles through LDS so both layouts are written with coalesced rows.
+template <int GD>
+__global__ __launch_bounds__(256) void muon_normalize_kernel(const float* __restrict__ buf, const void* __restrict__ grad,
+                                                             int64_t rows, int64_t cols, float mu, int nesterov,
+                                                             const float* __restrict__ partial, int n_partial,
+                                                             float eps, int tall, uint16_t* __restrict__ x,
+                                                             uint16_t* __restrict__ xt, int64_t ldx, int64_t ldxt) {
+  __shared__ float red[4];
+  __shared__ uint16_t tile[64][66];
+  float s = 0.0f;
+  for (int i = threadIdx.x; i < n_partial; i += 256) s += partial[i];
+  s = wave_sum(s);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  const float total = (red[0] + red[1]) + (red[2] + red[3]);
+  const float d = rnd<APEXW_BF16>(rnd<APEXW_BF16>(sqrtf(total)) + eps);
+  // tile (tr, tc) of buf in its own [rows x cols] layout
+  const int64_t tr = (int64_t)blockIdx.y * 64, tc = (int64_t)blockIdx.x * 64;
+  for (int e = threadIdx.x; e < 64 * 64; e += 256) {
+    const int r = e >> 6, cidx = e & 63;
+    const int64_t gr = tr + r, gc = tc + cidx;
+    float v = 0.0f;
+    if (gr < rows && gc < cols) {
+      const int64_t i = gr * cols + gc;
+      float m = APEXW_GLOBAL(const float, buf)[i];
+      if (nesterov) m = nesterov_source(muon_grad<GD>(grad, i), m, mu);
+      v = rnd<APEXW_BF16>(m) / d;
+    }
+    tile[r][cidx] = to_bf(v);
+  }
+  __syncthreads();
+  // direct layout D[r][c] = buf-shaped; transposed layout T[c][r]
+  uint16_t* direct = tall ? xt : x;
+  uint16_t* trans = tall ? x : xt;
+  const int64_t ld_direct = tall ? ldxt : ldx, ld_trans = tall ? ldx : ldxt;
+  for (int e = threadIdx.x; e < 64 * 64; e += 256) {
+    const int r = e >> 6, cidx = e & 63;
+    // direct[tr + r][tc + cidx] = D(tr + r, tc + cidx); trans[tc + r][tr + cidx] = D(tr + cidx, tc + r)
+    if (tr + r < rows && tc + cidx < cols) APEXW_GLOBAL(uint16_t, direct)[(tr + r) * ld_direct + tc + cidx] = tile[r][cidx];
+    if (tc + r < cols && tr + cidx < rows) APEXW_GLOBAL(uint16_t, trans)[(tc + r) * ld_trans + tr + cidx] = tile[cidx][r];
+  }
+}
+
+// p = round(round(p * (1 - lr*wd)) + (-lr_eff) * U)   (p.mul_ then p.add_(U, alpha)),
+// U read from the NS output in p's [rows x cols] layout (bf16, leading dim ldu).
+template <int PD>
+__global__ __launch_bounds__(256) void muon_apply_kernel(void* __restrict__ p, const uint16_t* __restrict__ u,
+                                                         int64_t rows, int64_t cols, int64_t ldu, float wd_factor,
+                                                         int apply_wd, float neg_lr_eff) {
+  const int64_t n = rows * cols;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / cols, c = i - r * cols;
+    float x = load1<PD>(p, i);
+    if (apply_wd) x = rnd<PD>(x * wd_factor);
+    const float uu = bf(APEXW_GLOBAL(const uint16_t, u)[r * ldu + c]);
+    store1<PD>(p, i, rnd<PD>(fmaf(neg_lr_eff, uu, x)));
+  }
+}
+
+int grid_for(int64_t n) {
+  const int64_t b = (n + 255) / 256;
+  return (int)(b < 4096 ? (b > 0 ? b : 1) : 4096);
+}
+
+}  // namespace
+
+int apexw_launch_gemm_nt(const uint16_t* a, const uint16_t* b, const uint16_t* et, uint16_t* c, uint16_t* ct,
+                         int32_t m, int32_t n, int32_t k, int32_t lda, int32_t ldb, int32_t lde, int32_t ldc,
+                         int32_t ldct, int32_t batch, int64_t sa, int64_t sb, int64_t se, int64_t sc, int64_t sct,
+                         float alpha, float beta, hipStream_t stream) {
+  GemmArgs g{a, b, et, c, ct, sa, sb, se, sc, sct, m, n, k, lda, ldb, lde, ldc, ldct, alpha, beta};
+  const int tiles = (m / kBM) * (n / kBN);
+  const dim3 grid(((tiles + 7) / 8) * 8, batch);
+  const bool add = et && beta != 0.0f;
+  if (c && ct) {
+    if (add) hipLaunchKernelGGL((gemm_nt_kernel<true, true, true>), grid, dim3(256), 0, stream, g);
+    else hipLaunchKernelGGL((gemm_nt_kernel<true, true, false>), grid, dim3(256), 0, stream, g);
+  } else if (c) {
+    if (add) hipLaunchKernelGGL((gemm_nt_kernel<true, false, true>), grid, dim3(256), 0, stream, g);
+    else hipLaunchKernelGGL((gemm_nt_kernel<true, false, false>), grid, dim3(256), 0, stream, g);
+  } else {
+    if (add) hipLaunchKernelGGL((gemm_nt_kernel<false, true, true>), grid, dim3(256), 0, stream, g);
+    else hipLaunchKernelGGL((gemm_nt_kernel<false, true, false>), grid, dim3(256), 0, stream, g);
+  }
+  return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
+}
+
+int apexw_muon_partials(int64_t n) { return grid_for(n) < 1024 ? grid_for(n) : 1024; }
+
+template <int GD>
+void launch_prepare(float* buf, const void* g, int64_t rows, int64_t cols, float mu, float one_minus_mu, int nesterov,
+                    float eps, uint16_t* x, uint16_t* xt, int64_t ldx, int64_t ldxt, float* partial,
+                    hipStream_t stream) {
+  const int64_t n = rows * cols;
+  const int nb = apexw_muon_partials(n);
+  hipLaunchKernelGGL(muon_momentum_kernel<GD>, dim3(nb), dim3(256), 0, stream, buf, g, n, mu, one_minus_mu, nesterov,
+                     partial);
+  dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64));
+  hipLaunchKernelGGL(muon_normalize_kernel<GD>, grid, dim3(256), 0, stream, buf, g, rows, cols, mu, nesterov, partial,
+                     nb, eps, (int)(rows > cols), x, xt, ldx, ldxt);
+}
+
+int apexw_launch_muon_prepare(float* buf, const void* g, int32_t g_dtype, int64_t rows, int64_t cols, float mu,
+                              float one_minus_mu, int32_t nesterov, float eps, uint16_t* x, uint16_t* xt, int64_t ldx,
+                              int64_t ldxt, float* partial, hipStream_t stream) {
+  if (g_dtype == APEXW_F32)
+    launch_prepare<APEXW_F32>(buf, g, rows, cols, mu, one_minus_mu, nesterov, eps, x, xt, ldx, ldxt, partial, stream);
+  else if (g_dtype == APEXW_BF16)
+    launch_prepare<APEXW_BF16>(buf, g, rows, cols, mu, one_minus_mu, nesterov, eps, x, xt, ldx, ldxt, partial, stream);
+  else
+    launch_prepare<APEXW_F16>(buf, g, rows, cols, mu, one_minus_mu, nesterov, eps, x, xt, ldx, ldxt, partial, stream);
+  return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
+}
+
+int apexw_launch_muon_apply(void* p, int32_t p_dtype, const uint16_t* u, int64_t rows, int64_t cols, int64_t ldu,
+                            float wd_factor, int32_t apply_wd, float neg_lr_eff, hipStream_t stream) {
+  const int64_t n = rows * cols;
+  if (p_dtype == APEXW_F32)
+    hipLaunchKernelGGL(muon_apply_kernel<APEXW_F32>, dim3(grid_for(n)), dim3(256), 0, stream, p, u, rows, cols, ldu,
+                       wd_factor, apply_wd, neg_lr_eff);
+  else if (p_dtype == APEXW_BF16)
+    hipLaunchKernelGGL(muon_apply_kernel<APEXW_BF16>, dim3(grid_for(n)), dim3(256), 0, stream, p, u, rows, cols, ldu,
+                       wd_factor, apply_wd, neg_lr_eff);
+  else
+    hipLaunchKernelGGL(muon_apply_kernel<APEXW_F16>, dim3(grid_for(n)), dim3(256), 0, stream, p, u, rows, cols, ldu,
+                       wd_factor, apply_wd, neg_lr_eff);
+  return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
+}

@@ -19,6 +19,12 @@
  *                           _adamw_kernel_triton_8bit_batched (apexw/triton_kernel.py:1138-1531)
  *   apexw_grad_clip_coef <- the global-norm clip of _prepare_grads
  *                           (apexw/optimizer.py:242-256: _foreach_norm + vector_norm)
+ *   apexw_gemm_nt_bf16   <- the bf16 GEMMs of Newton-Schulz: X @ X.T and the two
+ *                           torch.addmm / baddbmm calls (apexw/muon.py:102-108, :187-211)
+ *   apexw_muon_prepare   <- ApexMuon momentum update and the work-matrix cast /
+ *                           normalisation / transpose (apexw/muon.py:763-792, :163-175, :190-200)
+ *   apexw_muon_apply     <- the decoupled decay and scaled update of ApexMuon
+ *                           (apexw/muon.py:852-858, :752-759)
  */
 #ifndef APEXW_HIP_H
 #define APEXW_HIP_H
@@ -165,6 +171,55 @@ int apexw_grad_clip_coef(const apexw_tensor* tensors, int32_t n_tensors,
                          const apexw_unit* units, int64_t n_units, int64_t unit_size,
                          const int64_t* unit_begin, float* unit_partial, float* tensor_norm,
                          float clip, uint32_t flags, float* coef, void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* Muon: Newton-Schulz on the matrix cores                                    */
+/* ------------------------------------------------------------------------- */
+
+#define APEXW_GEMM_TILE 256   /* M and N multiple of this */
+#define APEXW_GEMM_KTILE 64   /* K multiple of this */
+
+/*
+ * Batched bf16 "NT" GEMM on the matrix cores (fp32 accumulation, bf16 output
+ * rounded to nearest even):
+ *   O[b] = alpha * A[b] . B[b]^T + beta * E[b]
+ * A: [m x k] row-major (lda), B: [n x k] row-major (ldb).  E is given
+ * transposed: et[j * lde + i] = E[i][j] (needed when beta != 0).  O is written
+ * row-major to c ([m x n], ldc) and/or transposed to ct ([n x m], ldct); at
+ * least one of them.  m, n multiple of APEXW_GEMM_TILE, k of APEXW_GEMM_KTILE,
+ * pointers 16-byte aligned, leading dimensions and batch strides multiples of 8
+ * elements.  Outputs must not alias inputs.
+ */
+int apexw_gemm_nt_bf16(const void* a, const void* b, const void* et, void* c, void* ct,
+                       int32_t m, int32_t n, int32_t k, int32_t lda, int32_t ldb, int32_t lde,
+                       int32_t ldc, int32_t ldct, int32_t batch,
+                       int64_t stride_a, int64_t stride_b, int64_t stride_e, int64_t stride_c,
+                       int64_t stride_ct, float alpha, float beta, void* stream);
+
+/* fp32 workspace (floats) apexw_muon_prepare needs for a [rows x cols] matrix. */
+int64_t apexw_muon_workspace_floats(int64_t rows, int64_t cols);
+
+/*
+ * Muon momentum and Newton-Schulz input for one [rows x cols] parameter:
+ *   buf = buf * mu + (1 - mu) * g        (fp32 buffer; g sanitized NaN -> 0,
+ *                                         +-Inf -> +-65504; g dtype F32/BF16/F16)
+ *   s   = buf, or lerp(g, buf, mu) when nesterov
+ *   X   = bf16(bf16(s) / bf16(bf16(||bf16(s)||_F) + eps))
+ * X is written as the wide work matrix [min x max] to x (ldx) and as its
+ * transpose [max x min] to xt (ldxt): when rows > cols the work matrix is s^T.
+ * Elements of x / xt outside the matrix are not written (keep them zero).
+ */
+int apexw_muon_prepare(float* buf, const void* g, int32_t g_dtype, int64_t rows, int64_t cols,
+                       float mu, float one_minus_mu, int32_t nesterov, float eps,
+                       void* x, void* xt, int64_t ldx, int64_t ldxt, float* workspace, void* stream);
+
+/*
+ * p = round(round(p * wd_factor) + neg_lr_eff * U)   (the decay only if apply_wd)
+ * with U the bf16 Newton-Schulz result in p's [rows x cols] layout (leading
+ * dimension ldu); p dtype F32/BF16/F16, rounded to nearest even.
+ */
+int apexw_muon_apply(void* p, int32_t p_dtype, const void* u, int64_t rows, int64_t cols, int64_t ldu,
+                     float wd_factor, int32_t apply_wd, float neg_lr_eff, void* stream);
 
 #ifdef __cplusplus
 }

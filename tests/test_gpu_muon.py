@@ -1,0 +1,185 @@
+"""GPU: the bf16 MFMA GEMM, the Muon step and the hybrid optimizer.
+
+Tolerances:
+  * GEMM: |O - ref| <= 2^-8 |ref| + 1e-4 max|ref| against an fp32 product of the
+    same bf16 inputs (bf16 output rounding is <= 2^-9 relative);
+  * Newton-Schulz / Muon update: relative Frobenius error <= 3% against the fp32
+    CPU oracle.  The work dtype is bf16 (as the reference's on a bf16-capable
+    GPU); the reference's own bf16 path differs from its fp32 path by 0.9-1.5%
+    on these shapes (torch CPU bf16 matmuls), so 3% is twice that;
+  * fp32 momentum and the AdamW-routed parameters: the fp32 bounds of the
+    fused-step parity tests (1e-6 relative).
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from golden.make_golden import _fingerprint, _grad, _param
+from golden_replay import load
+from oracle.muon import newton_schulz5
+
+pytestmark = pytest.mark.gpu
+
+
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+
+
+def _rel_fro(got, ref):
+    got, ref = got.double().cpu(), ref.double().cpu()
+    return float((got - ref).norm() / ref.norm())
+
+
+@pytest.mark.parametrize("m,n,k,batch", [(256, 512, 320, 2), (512, 256, 1024, 1), (256, 256, 64, 3)])
+def test_gemm_nt_bf16_matches_fp32_product(m, n, k, batch):
+    _need_gpu()
+    from apexw_amd import _lib
+    lib = _lib.load()
+    print(f"gemm m={m} n={n} k={k} batch={batch}", flush=True)
+    g = torch.Generator().manual_seed(m + n + k)
+    A = torch.randn(batch, m, k, generator=g).bfloat16()
+    B = torch.randn(batch, n, k, generator=g).bfloat16()
+    E = torch.randn(batch, m, n, generator=g).bfloat16()
+    alpha, beta = 0.75, -1.25
+    ref = alpha * (A.float() @ B.float().transpose(1, 2)) + beta * E.float()   # fp32 on the CPU
+    dA, dB, dEt = A.cuda(), B.cuda(), E.transpose(1, 2).contiguous().cuda()
+    C = torch.full((batch, m, n), float("nan"), dtype=torch.bfloat16, device="cuda")
+    Ct = torch.full((batch, n, m), float("nan"), dtype=torch.bfloat16, device="cuda")
+    st = lib.apexw_gemm_nt_bf16(dA.data_ptr(), dB.data_ptr(), dEt.data_ptr(), C.data_ptr(), Ct.data_ptr(),
+                                m, n, k, k, k, m, n, m, batch, m * k, n * k, n * m, m * n, n * m, alpha, beta,
+                                torch.cuda.current_stream().cuda_stream)
+    assert st == 0
+    torch.cuda.synchronize()
+    got = C.float().cpu()
+    err = (got - ref).abs() - (2.0 ** -8 * ref.abs() + 1e-4 * ref.abs().max())
+    assert float(err.max()) <= 0, f"max excess {float(err.max()):.3e}"
+    assert torch.equal(Ct.cpu().transpose(1, 2), C.cpu())
+
+
+def test_gemm_rejects_bad_shapes_before_launch():
+    _need_gpu()
+    from apexw_amd import _lib
+    lib = _lib.load()
+    x = torch.zeros(256 * 256, dtype=torch.bfloat16, device="cuda")
+    p = x.data_ptr()
+    s = torch.cuda.current_stream().cuda_stream
+    assert lib.apexw_gemm_nt_bf16(p, p, None, None, p, 200, 256, 64, 64, 64, 0, 0, 256, 1, 0, 0, 0, 0, 0,
+                                  1.0, 0.0, s) == 1   # m not a tile multiple
+    assert lib.apexw_gemm_nt_bf16(p, p, None, None, None, 256, 256, 64, 64, 64, 0, 0, 256, 1, 0, 0, 0, 0, 0,
+                                  1.0, 0.0, s) == 1   # no output
+    assert lib.apexw_gemm_nt_bf16(p, p, None, None, p, 256, 256, 64, 64, 64, 0, 0, 256, 1, 0, 0, 0, 0, 0,
+                                  1.0, 2.0, s) == 1   # beta without addend
+    assert lib.apexw_gemm_nt_bf16(p + 2, p, None, None, p, 256, 256, 64, 64, 64, 0, 0, 256, 1, 0, 0, 0, 0, 0,
+                                  1.0, 0.0, s) == 4   # misaligned
+
+
+def _muon_updates(shapes, steps=1, seed=0, dtype=torch.float32, nesterov=False):
+    """Run ApexMuon on the GPU and the fp32 oracle recipe on the CPU; return per-param (gpu, cpu) pairs."""
+    from apexw_amd.muon import ApexMuon
+    g = torch.Generator().manual_seed(seed)
+    lr, wd, mu = 0.02, 0.1, 0.95
+    host = [(torch.randn(s, generator=g) * 0.02).to(dtype) for s in shapes]
+    ps = [torch.nn.Parameter(h.cuda()) for h in host]
+    opt = ApexMuon(ps, lr=lr, momentum=mu, weight_decay=wd, ns_steps=5, scale_mode="rms_matched",
+                   nesterov=nesterov)
+    ref = [h.float().clone() for h in host]
+    bufs = [torch.zeros(s) for s in shapes]
+    out = []
+    for _ in range(steps):
+        grads = [(torch.randn(s, generator=g) * 1e-3).to(dtype) for s in shapes]
+        before = [p.detach().float().cpu() for p in ps]
+        for p, gr in zip(ps, grads):
+            p.grad = gr.cuda()
+        opt.step()
+        torch.cuda.synchronize()
+        out = []
+        for i, s in enumerate(shapes):
+            bufs[i].mul_(mu).add_(grads[i].float(), alpha=1 - mu)
+            src = grads[i].float().lerp(bufs[i], mu) if nesterov else bufs[i]
+            U = newton_schulz5(src, 5, work_dtype=torch.float32)
+            scale = 0.2 * math.sqrt(max(s[0], int(np.prod(s)) // s[0]))
+            if dtype == torch.float32:
+                d_ref = -lr * scale * U
+                d_gpu = ps[i].detach().float().cpu() - before[i] * (1 - lr * wd)
+            else:
+                # same roundings as p.mul_(1 - lr*wd); p.add_(U, alpha=-lr*scale) on a 16-bit p
+                decayed = (before[i] * np.float32(1 - lr * wd)).to(dtype).float()
+                p_ref = (decayed + np.float32(-lr * scale) * U.to(dtype).float()).to(dtype).float()
+                d_ref = p_ref - before[i]
+                d_gpu = ps[i].detach().float().cpu() - before[i]
+            out.append((d_gpu, d_ref, opt.state[ps[i]], bufs[i].clone()))
+    return out
+
+
+@pytest.mark.parametrize("shapes", [[(256, 512)], [(512, 256)], [(300, 200)], [(64, 64)], [(256, 512), (256, 512)]])
+def test_muon_step_matches_fp32_oracle(shapes):
+    _need_gpu()
+    print(f"muon shapes={shapes}", flush=True)
+    for d_gpu, d_ref, st, buf in _muon_updates(shapes, steps=2, seed=len(shapes) + shapes[0][0]):
+        assert _rel_fro(d_gpu, d_ref) <= 0.03, _rel_fro(d_gpu, d_ref)
+        got = st["momentum"].cpu()
+        assert st["momentum"].dtype == torch.float32 and st["step"] == 2
+        assert torch.allclose(got, buf, rtol=1e-6, atol=1e-12)
+
+
+def test_muon_nesterov_and_bf16_params():
+    _need_gpu()
+    for d_gpu, d_ref, st, _ in _muon_updates([(256, 384), (384, 256)], steps=1, seed=7, nesterov=True):
+        assert _rel_fro(d_gpu, d_ref) <= 0.03
+    # bf16 params: both sides round the decayed and the updated parameter to bf16;
+    # a Newton-Schulz difference flips some of those roundings by one bf16 ulp
+    for d_gpu, d_ref, st, _ in _muon_updates([(256, 256)], steps=1, seed=8, dtype=torch.bfloat16):
+        assert _rel_fro(d_gpu, d_ref) <= 0.05, _rel_fro(d_gpu, d_ref)
+
+
+def test_muon_polar_invariant_on_gpu():
+    # reference known answer (tests/test_muon.py:26-51): singular values of the NS5 result in (0.5, 1.3)
+    _need_gpu()
+    from apexw_amd.muon import ApexMuon
+    torch.manual_seed(42)
+    for shape in [(64, 64), (128, 64), (64, 128)]:
+        G = torch.randn(shape)
+        p = torch.nn.Parameter(torch.zeros(shape, device="cuda"))
+        # one step from zero momentum with mu = 0: the NS input is G itself
+        opt = ApexMuon([p], lr=1.0, momentum=0.0, weight_decay=0.0, ns_steps=5, scale_mode="none")
+        p.grad = G.cuda()
+        opt.step()
+        U = -p.detach().double().cpu()
+        s = torch.linalg.svdvals(U)
+        assert float(s.min()) > 0.5 and float(s.max()) < 1.3, (shape, float(s.min()), float(s.max()))
+
+
+def test_hybrid_trajectory_matches_reference_vectors():
+    _need_gpu()
+    from apexw_amd import ApexW
+    z = load("muon")
+    shapes = [(64, 64), (64, 64), (48, 96), (64,), (4096, 32)]
+    gen = torch.Generator().manual_seed(12)
+    host = [_param(s, torch.float32, gen) for s in shapes]
+    init = [h.clone() for h in host]
+    fp = [_fingerprint(h) for h in host]
+    ps = [torch.nn.Parameter(h.cuda()) for h in host]
+    opt = ApexW(ps, lr=1e-3, weight_decay=0.1, use_muon=True, stochastic_rounding=False)
+    assert type(opt).__name__ == "HybridApexW"
+    for _ in range(3):
+        for p in ps:
+            gr = _grad(p.shape, torch.float32, gen, 1e-3)
+            fp.append(_fingerprint(gr))
+            p.grad = gr.cuda()
+        opt.step()
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(np.array(fp, dtype=np.int64), z["h_fingerprint"])
+    assert [1 if any(p is q for q in opt.muon_params) else 0 for p in ps] == z["h_route"].tolist()
+    for i, p in enumerate(ps):
+        got = p.detach().cpu().double()
+        gold = torch.from_numpy(z[f"hp_{i}"]).double()
+        if z["h_route"][i]:
+            # Muon: the accumulated update within the bf16 Newton-Schulz bound
+            assert _rel_fro(got - init[i].double(), gold - init[i].double()) <= 0.03, i
+        else:
+            err = (got - gold).abs() - (1e-6 * gold.abs() + 1e-9)
+            assert float(err.max()) <= 0, i

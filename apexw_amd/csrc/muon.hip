@@ -70,14 +70,23 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmArgs g) {
   const int wm = wave >> 1, wn = wave & 1;
 
   // global -> register staging, half a K tile at a time (4 x 16 B of A and of B
-  // per thread): the next tile streams in while the current one is multiplied
+  // per thread): the next tile streams in while the current one is multiplied.
+  // Addresses are a uniform base plus a 32-bit per-lane byte offset.
   u32x4 ra[4], rb[4];
+  uint32_t off_a[8], off_b[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int c = tid + 256 * i, r = c >> 3, c16 = c & 7;
+    off_a[i] = (uint32_t)(r * g.lda + c16 * 8) * 2u;
+    off_b[i] = (uint32_t)(r * g.ldb + c16 * 8) * 2u;
+  }
   auto load = [&](int k0, int half) {
+    const char* a0 = (const char*)(A + k0);
+    const char* b0 = (const char*)(B + k0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int c = tid + 256 * (i + 4 * half), r = c >> 3, c16 = c & 7;
-      ra[i] = __builtin_nontemporal_load(APEXW_GLOBAL(const u32x4, (A + k0) + (uint32_t)(r * g.lda + c16 * 8)));
-      rb[i] = __builtin_nontemporal_load(APEXW_GLOBAL(const u32x4, (B + k0) + (uint32_t)(r * g.ldb + c16 * 8)));
+      ra[i] = __builtin_nontemporal_load(APEXW_GLOBAL(const u32x4, a0 + off_a[i + 4 * half]));
+      rb[i] = __builtin_nontemporal_load(APEXW_GLOBAL(const u32x4, b0 + off_b[i + 4 * half]));
     }
   };
   auto store = [&](int buf, int half) {
@@ -95,21 +104,29 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmArgs g) {
 #pragma unroll
     for (int b = 0; b < 4; ++b) acc[a][b] = f32x16{};
 
-  // MFMA 32x32x16 operand layout: lane l supplies row (l % 32) and k = 8 (l / 32) .. +7
+  // MFMA 32x32x16 operand layout: lane l supplies row (l % 32) and k = 8 (l / 32) .. +7.
+  // Fragments are double-buffered in registers: the 8 LDS reads of k-step s + 1
+  // are issued before the 16 MFMAs of step s.  sched_barrier(0) pins that order
+  // (the scheduler would otherwise sink each read next to its first use and
+  // expose the full LDS latency before every few MFMAs).
   const int frag_row = lane & 31, frag_k = (lane >> 5) * 8;
-  auto mma = [&](int buf, int s) {
-    bf16x8 fa[4], fb[4];
+  bf16x8 fa[2][4], fb[2][4];
+  auto frags = [&](int buf, int s, int slot) {
 #pragma unroll
     for (int a = 0; a < 4; ++a)
-      fa[a] = *(const bf16x8*)&s_a[buf][(wm * 128 + a * 32 + frag_row) * kLds + s * 16 + frag_k];
+      fa[slot][a] = *(const bf16x8*)&s_a[buf][(wm * 128 + a * 32 + frag_row) * kLds + s * 16 + frag_k];
 #pragma unroll
     for (int b = 0; b < 4; ++b)
-      fb[b] = *(const bf16x8*)&s_b[buf][(wn * 128 + b * 32 + frag_row) * kLds + s * 16 + frag_k];
+      fb[slot][b] = *(const bf16x8*)&s_b[buf][(wn * 128 + b * 32 + frag_row) * kLds + s * 16 + frag_k];
+  };
+  auto mma = [&](int slot) {
 #pragma unroll
     for (int a = 0; a < 4; ++a)
 #pragma unroll
-      for (int b = 0; b < 4; ++b) acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[a], fb[b], acc[a][b], 0, 0, 0);
+      for (int b = 0; b < 4; ++b)
+        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[slot][a], fb[slot][b], acc[a][b], 0, 0, 0);
   };
+#define APEXW_SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
 
   const int k_tiles = g.k / kBK;
   load(0, 0);
@@ -122,17 +139,30 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmArgs g) {
     const int buf = kt & 1;
     const bool next = kt + 1 < k_tiles;
     if (next) load((kt + 1) * kBK, 0);
-    mma(buf, 0);
-    mma(buf, 1);
+    frags(buf, 0, 0);
+    APEXW_SCHED_FENCE();
+    frags(buf, 1, 1);
+    APEXW_SCHED_FENCE();
+    mma(0);
+    APEXW_SCHED_FENCE();
+    frags(buf, 2, 0);
+    APEXW_SCHED_FENCE();
+    mma(1);
+    APEXW_SCHED_FENCE();
     if (next) {
       store(buf ^ 1, 0);
       load((kt + 1) * kBK, 1);
     }
-    mma(buf, 2);
-    mma(buf, 3);
+    frags(buf, 3, 1);
+    APEXW_SCHED_FENCE();
+    mma(0);
+    APEXW_SCHED_FENCE();
+    mma(1);
+    APEXW_SCHED_FENCE();
     if (next) store(buf ^ 1, 1);
     __syncthreads();
   }
+#undef APEXW_SCHED_FENCE
 
   // Epilogue.  Accumulator register r of lane l holds row 8 (r / 4) + 4 (l / 32) + r % 4,
   // column l % 32 of its 32 x 32 block: four consecutive rows of one column per group.

@@ -76,6 +76,9 @@ CONFIGS = {
     "c4": dict(workload="C4 compact ApexW step, 20k ragged bf16 tensors, clip 1.0", shapes=ragged_shapes(),
                dtype=torch.bfloat16, kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, clip_grad_norm=1.0),
                zero_frac=0.05),
+    "c5": dict(workload="C5 hybrid Muon step (use_muon=True), one Llama-3-8B layer's matrices + 2 RMSNorm, bf16",
+               shapes=llama3_8b_shapes()[1:10], dtype=torch.bfloat16,
+               kwargs=dict(lr=1e-3, weight_decay=0.1, use_muon=True), mfma=True),
 }
 
 
@@ -145,6 +148,34 @@ def state_bytes(opt, params):
     return tot
 
 
+def ns_roofline(opt, stream, reps=3):
+    """MFMA utilisation of the Newton-Schulz GEMMs of one step: the step's NS
+    iterations are replayed on its own workspaces between HIP events on the
+    launch stream; FLOPs are the algorithmic 4 m^2 n + 2 m^3 per iteration per
+    matrix (m <= n), the count of the reference's three matmuls."""
+    from apexw_amd.muon import newton_schulz
+    mu = opt.muon_opt
+    steps = int(mu.param_groups[0]["ns_steps"])
+    flops = 0
+    for ws in mu._ws.values():
+        flops += ws.batch * steps * (4 * ws.m * ws.m * ws.n + 2 * ws.m ** 3)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    h = stream.cuda_stream
+    for ws in mu._ws.values():
+        newton_schulz(ws, steps, h)
+    ev0.record(stream)
+    for _ in range(reps):
+        for ws in mu._ws.values():
+            newton_schulz(ws, steps, h)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ns_ms = ev0.elapsed_time(ev1) / reps
+    achieved = flops / (ns_ms * 1e-3) / 1e12
+    return {"bound": "mfma", "achieved": achieved, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": achieved / MFMA_BF16_PEAK_TFLOPS, "traffic": None, "kernel_ms": ns_ms, "flops_per_step": flops,
+            "ns_steps": steps}
+
+
 def cpu_baseline(cfg_name, budget_s=20.0):
     """Time the CPU oracle on a bounded slice of the workload (whole steps)."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
@@ -153,6 +184,20 @@ def cpu_baseline(cfg_name, budget_s=20.0):
     threads = os.cpu_count() or 1
     threads = min(threads, 16)
     torch.set_num_threads(threads)
+    if cfg_name == "c5":
+        from oracle.muon import OracleHybrid
+        params = make_params(dict(cfg, shapes=[(4096, 4096)]), "cpu")
+        opt = OracleHybrid(params, **{k: v for k, v in cfg["kwargs"].items() if k != "use_muon"})
+        steps, t0 = 0, time.perf_counter()
+        while True:
+            opt.step()
+            steps += 1
+            el = time.perf_counter() - t0
+            if el > budget_s or steps >= 20:
+                break
+        return {"value": params[0].numel() * steps / el, "unit": "params/s", "cores": threads, "kind": "port",
+                "sample": f"the q matrix (4096x4096) of the layer; {steps} Muon steps, fp32 Newton-Schulz "
+                          f"(the reference's CPU work dtype); CPU oracle (torch CPU ops)"}
     if cfg_name == "c3":
         shapes = llama3_8b_shapes()[1:10]          # one transformer layer (218M params)
         sample = "one Llama-3-8B layer (q,k,v,o,gate,up,down + 2 RMSNorm, 218.1M params)"
@@ -207,7 +252,7 @@ def main():
     for _ in range(args.warmup):
         opt.step()
     torch.cuda.synchronize()
-    nbytes = state_bytes(opt, params)
+    nbytes = 0 if cfg.get("mfma") else state_bytes(opt, params)
     stream = torch.cuda.current_stream(dev)
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -221,15 +266,20 @@ def main():
     gpu_ms = ev0.elapsed_time(ev1) / args.steps
     ms = wall * 1e3 / args.steps
     achieved = nbytes / (gpu_ms * 1e-3) / 1e9
+    if cfg.get("mfma"):
+        roofline = ns_roofline(opt, stream)
+        roofline["step_ms"] = gpu_ms
+    else:
+        roofline = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": achieved / HBM_PEAK_GBS, "traffic": measured_traffic(args.config),
+                    "kernel_ms": gpu_ms, "bytes_per_launch": nbytes, "bytes_per_param": nbytes / n}
     out = {
         "metric": METRIC, "value": n / (ms * 1e-3), "unit": "params/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "vs_baseline": None, "dtype": "bf16" if cfg.get("mfma") else "f32", "data": "synthetic",
         "config": {"workload": cfg["workload"], "params": n, "tensors": len(params),
                    "param_dtype": str(cfg["dtype"]).replace("torch.", ""), **{k: v for k, v in cfg["kwargs"].items()}},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": measured_traffic(args.config),
-                     "kernel_ms": gpu_ms, "bytes_per_launch": nbytes, "bytes_per_param": nbytes / n},
+        "roofline": roofline,
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.config, args.cpu_budget)

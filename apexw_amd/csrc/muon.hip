@@ -22,7 +22,10 @@ typedef __attribute__((ext_vector_type(16))) float f32x16;
 typedef __attribute__((ext_vector_type(4))) uint16_t u16x4;
 
 constexpr int kBM = 256, kBN = 256, kBK = 64;
-constexpr int kLds = kBK + 8;  // LDS row pitch (elements): 144 B keeps 8 consecutive rows on distinct banks
+// LDS tiles are [rows x 64] bf16 with 128-byte rows; the eight 16-byte chunks of
+// row r are stored XOR-swizzled (chunk c at slot c ^ (r & 7)), so the MFMA
+// fragment reads of 8 consecutive rows hit 8 distinct bank groups.
+APEXW_DEV int lds_off(int row, int chunk) { return row * kBK + ((chunk ^ (row & 7)) << 3); }
 
 struct GemmArgs {
   const uint16_t* a;   // [M x K] row-major, ld lda
@@ -40,13 +43,14 @@ APEXW_DEV uint16_t to_bf(float x) { return (uint16_t)f32_to_bf16_bits(x); }
 
 // C = alpha * A B^T + beta * E (bf16 in, fp32 accumulate, bf16 out, round to nearest even).
 // 256 threads = 4 waves in a 2 x 2 arrangement, each owning a 128 x 128 block of
-// the 256 x 256 tile as 4 x 4 MFMA 32x32x16 accumulators.
+// the 256 x 256 tile as 4 x 4 MFMA 32x32x16 accumulators; K tiles of 64 are
+// double-buffered in LDS and loaded straight from global memory into LDS.
 // Template flags select the epilogue: write O row-major (kC), transposed (kCt),
 // add beta * E (kAdd).
 template <bool kC, bool kCt, bool kAdd>
 __global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(16))) uint16_t s_a[2][kBM * kLds];
-  __shared__ __attribute__((aligned(16))) uint16_t s_b[2][kBN * kLds];
+  __shared__ __attribute__((aligned(16))) uint16_t s_a[2][kBM * kBK];
+  __shared__ __attribute__((aligned(16))) uint16_t s_b[2][kBN * kBK];
 
   const int tiles_m = g.m / kBM, tiles_n = g.n / kBN, tiles = tiles_m * tiles_n;
   // Consecutive workgroups are dispatched round-robin over the 8 XCDs; give each
@@ -69,34 +73,33 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmArgs g) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  // global -> register staging, half a K tile at a time (4 x 16 B of A and of B
-  // per thread): the next tile streams in while the current one is multiplied.
-  // Addresses are a uniform base plus a 32-bit per-lane byte offset.
-  u32x4 ra[4], rb[4];
-  uint32_t off_a[8], off_b[8];
+  // global -> LDS without registers (global_load_lds_dwordx4): each wave
+  // instruction fills 1 KB of LDS = 8 tile rows, lane L landing at byte 16 L.
+  // Lane L of chunk q reads row 8 q + L / 8 at column chunk (L % 8) ^ (L / 8),
+  // which is the swizzled slot L % 8 of that row.  Per K tile each wave issues
+  // 8 instructions for A and 8 for B (chunks q = 8 wave + i).
+  uint32_t goff_a[8], goff_b[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int c = tid + 256 * i, r = c >> 3, c16 = c & 7;
-    off_a[i] = (uint32_t)(r * g.lda + c16 * 8) * 2u;
-    off_b[i] = (uint32_t)(r * g.ldb + c16 * 8) * 2u;
+    const int row = 8 * (8 * wave + i) + (lane >> 3), chunk = (lane & 7) ^ (lane >> 3);
+    goff_a[i] = (uint32_t)(row * g.lda + chunk * 8) * 2u;
+    goff_b[i] = (uint32_t)(row * g.ldb + chunk * 8) * 2u;
   }
-  auto load = [&](int k0, int half) {
+  auto issue_loads = [&](int buf, int k0) {
     const char* a0 = (const char*)(A + k0);
     const char* b0 = (const char*)(B + k0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      ra[i] = __builtin_nontemporal_load(APEXW_GLOBAL(const u32x4, a0 + off_a[i + 4 * half]));
-      rb[i] = __builtin_nontemporal_load(APEXW_GLOBAL(const u32x4, b0 + off_b[i + 4 * half]));
+    for (int i = 0; i < 8; ++i) {
+      const int q = 8 * wave + i;
+      __builtin_amdgcn_global_load_lds(APEXW_GLOBAL(const void, a0 + goff_a[i]),
+                                       (__attribute__((address_space(3))) void*)&s_a[buf][q * 512], 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(APEXW_GLOBAL(const void, b0 + goff_b[i]),
+                                       (__attribute__((address_space(3))) void*)&s_b[buf][q * 512], 16, 0, 0);
     }
   };
-  auto store = [&](int buf, int half) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid + 256 * (i + 4 * half), r = c >> 3, c16 = c & 7;
-      *(u32x4*)&s_a[buf][r * kLds + c16 * 8] = ra[i];
-      *(u32x4*)&s_b[buf][r * kLds + c16 * 8] = rb[i];
-    }
-  };
+  // the loads write LDS asynchronously: wait for this wave's, then the barrier
+  // makes every wave's visible
+  auto loads_done = [&]() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
 
   f32x16 acc[4][4];
 #pragma unroll
@@ -109,15 +112,15 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmArgs g) {
   // are issued before the 16 MFMAs of step s.  sched_barrier(0) pins that order
   // (the scheduler would otherwise sink each read next to its first use and
   // expose the full LDS latency before every few MFMAs).
-  const int frag_row = lane & 31, frag_k = (lane >> 5) * 8;
+  const int frag_row = lane & 31, frag_c = lane >> 5;
   bf16x8 fa[2][4], fb[2][4];
   auto frags = [&](int buf, int s, int slot) {
 #pragma unroll
     for (int a = 0; a < 4; ++a)
-      fa[slot][a] = *(const bf16x8*)&s_a[buf][(wm * 128 + a * 32 + frag_row) * kLds + s * 16 + frag_k];
+      fa[slot][a] = *(const bf16x8*)&s_a[buf][lds_off(wm * 128 + a * 32 + frag_row, s * 2 + frag_c)];
 #pragma unroll
     for (int b = 0; b < 4; ++b)
-      fb[slot][b] = *(const bf16x8*)&s_b[buf][(wn * 128 + b * 32 + frag_row) * kLds + s * 16 + frag_k];
+      fb[slot][b] = *(const bf16x8*)&s_b[buf][lds_off(wn * 128 + b * 32 + frag_row, s * 2 + frag_c)];
   };
   auto mma = [&](int slot) {
 #pragma unroll
@@ -129,16 +132,14 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmArgs g) {
 #define APEXW_SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
 
   const int k_tiles = g.k / kBK;
-  load(0, 0);
-  store(0, 0);
-  load(0, 1);
-  store(0, 1);
+  issue_loads(0, 0);
+  loads_done();
   __syncthreads();
   for (int kt = 0; kt < k_tiles; ++kt) {
-    // LDS buffer buf ^ 1 was last read before the previous barrier: free to refill
+    // stage buf ^ 1 was last read before the previous barrier: refill it with
+    // tile kt + 1 while tile kt is multiplied
     const int buf = kt & 1;
-    const bool next = kt + 1 < k_tiles;
-    if (next) load((kt + 1) * kBK, 0);
+    if (kt + 1 < k_tiles) issue_loads(buf ^ 1, (kt + 1) * kBK);
     frags(buf, 0, 0);
     APEXW_SCHED_FENCE();
     frags(buf, 1, 1);
@@ -149,17 +150,13 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmArgs g) {
     APEXW_SCHED_FENCE();
     mma(1);
     APEXW_SCHED_FENCE();
-    if (next) {
-      store(buf ^ 1, 0);
-      load((kt + 1) * kBK, 1);
-    }
     frags(buf, 3, 1);
     APEXW_SCHED_FENCE();
     mma(0);
     APEXW_SCHED_FENCE();
     mma(1);
     APEXW_SCHED_FENCE();
-    if (next) store(buf ^ 1, 1);
+    loads_done();
     __syncthreads();
   }
 #undef APEXW_SCHED_FENCE
@@ -171,6 +168,8 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmArgs g) {
   uint16_t* __restrict__ C = kC ? g.c + batch * g.sc + (int64_t)row0 * g.ldc + col0 : nullptr;
   uint16_t* __restrict__ Ct = kCt ? g.ct + batch * g.sct + (int64_t)col0 * g.ldct + row0 : nullptr;
   const int lr = wm * 128 + (lane >> 5) * 4, lc = wn * 128 + (lane & 31);
+  // after the last barrier the operand tiles are dead: 4 x 32 KB of LDS for the row-major staging
+  uint16_t* stage = (wave < 2 ? s_a[wave] : s_b[wave - 2]);
 #pragma unroll
   for (int a = 0; a < 4; ++a) {
 #pragma unroll
@@ -192,10 +191,21 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmArgs g) {
         for (int r = 0; r < 4; ++r) o[r] = to_bf(v[r]);
         if constexpr (kCt) *APEXW_GLOBAL(u16x4, Ct + (uint32_t)(j * g.ldct + i0)) = o;
         if constexpr (kC) {
+          // stage the wave's 128 x 128 block row-major in its own 32 KB of LDS
 #pragma unroll
-          for (int r = 0; r < 4; ++r) *APEXW_GLOBAL(uint16_t, C + (uint32_t)((i0 + r) * g.ldc + j)) = o[r];
+          for (int r = 0; r < 4; ++r) stage[(i0 - wm * 128 + r) * 128 + (j - wn * 128)] = o[r];
         }
       }
+    }
+  }
+  if constexpr (kC) {
+    // each wave reads back only what it wrote: LDS keeps one wave's accesses in order
+    uint16_t* __restrict__ Cw = C + (int64_t)(wm * 128) * g.ldc + wn * 128;
+#pragma unroll 4
+    for (int it = 0; it < 32; ++it) {
+      const int c = it * 64 + lane, r = c >> 4, c16 = c & 15;
+      const u32x4 v = *(const u32x4*)&stage[r * 128 + c16 * 8];
+      __builtin_nontemporal_store(v, APEXW_GLOBAL(u32x4, Cw + (uint32_t)(r * g.ldc + c16 * 8)));
     }
   }
 }
@@ -219,12 +229,32 @@ APEXW_DEV float nesterov_source(float g, float m, float mu) {
   return mu < 0.5f ? fmaf(mu, m - g, g) : fmaf(mu - 1.0f, m - g, m);
 }
 
-template <int GD>
+// VEC: 8 elements per thread with 16-byte accesses (buf and grad 16-byte
+// aligned); the n % 8 tail and unaligned tensors take the element-wise loop.
+template <int GD, bool VEC>
 __global__ __launch_bounds__(256) void muon_momentum_kernel(float* __restrict__ buf, const void* __restrict__ grad,
                                                             int64_t n, float mu, float one_minus_mu, int nesterov,
                                                             float* __restrict__ partial) {
   float s = 0.0f;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+  const int64_t tid = (int64_t)blockIdx.x * 256 + threadIdx.x, stride = (int64_t)gridDim.x * 256;
+  const int64_t n_vec = VEC ? n / 8 * 8 : 0;
+  if constexpr (VEC) {
+    for (int64_t i = tid * 8; i < n_vec; i += stride * 8) {
+      float g[8], m[8];
+      load8<GD>(grad, i, g);
+      load8<APEXW_F32>(buf, i, m);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (__builtin_isnan(g[j])) g[j] = 0.0f;
+        else if (__builtin_isinf(g[j])) g[j] = g[j] > 0.0f ? 65504.0f : -65504.0f;
+        m[j] = fmaf(one_minus_mu, g[j], m[j] * mu);
+        const float x = rnd<APEXW_BF16>(nesterov ? nesterov_source(g[j], m[j], mu) : m[j]);
+        s = fmaf(x, x, s);
+      }
+      store8<APEXW_F32>(buf, i, m);
+    }
+  }
+  for (int64_t i = n_vec + tid; i < n; i += stride) {
     const float g = muon_grad<GD>(grad, i);
     const float m = fmaf(one_minus_mu, g, APEXW_GLOBAL(float, buf)[i] * mu);
     APEXW_GLOBAL(float, buf)[i] = m;
@@ -286,11 +316,27 @@ __global__ __launch_bounds__(256) void muon_normalize_kernel(const float* __rest
 
 // p = round(round(p * (1 - lr*wd)) + (-lr_eff) * U)   (p.mul_ then p.add_(U, alpha)),
 // U read from the NS output in p's [rows x cols] layout (bf16, leading dim ldu).
-template <int PD>
+// VEC: cols % 8 == 0 and 16-byte aligned p / u rows: 8 elements of one row per thread.
+template <int PD, bool VEC>
 __global__ __launch_bounds__(256) void muon_apply_kernel(void* __restrict__ p, const uint16_t* __restrict__ u,
                                                          int64_t rows, int64_t cols, int64_t ldu, float wd_factor,
                                                          int apply_wd, float neg_lr_eff) {
   const int64_t n = rows * cols;
+  if constexpr (VEC) {
+    for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8; i < n; i += (int64_t)gridDim.x * 256 * 8) {
+      const int64_t r = i / cols, c = i - r * cols;
+      float x[8], uu[8];
+      load8<PD>(p, i, x);
+      load8<APEXW_BF16>(u, r * ldu + c, uu);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (apply_wd) x[j] = rnd<PD>(x[j] * wd_factor);
+        x[j] = rnd<PD>(fmaf(neg_lr_eff, uu[j], x[j]));
+      }
+      store8<PD>(p, i, x);
+    }
+    return;
+  }
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
     const int64_t r = i / cols, c = i - r * cols;
     float x = load1<PD>(p, i);
@@ -336,8 +382,12 @@ void launch_prepare(float* buf, const void* g, int64_t rows, int64_t cols, float
                     hipStream_t stream) {
   const int64_t n = rows * cols;
   const int nb = apexw_muon_partials(n);
-  hipLaunchKernelGGL(muon_momentum_kernel<GD>, dim3(nb), dim3(256), 0, stream, buf, g, n, mu, one_minus_mu, nesterov,
-                     partial);
+  if ((((uintptr_t)buf | (uintptr_t)g) & 15u) == 0)
+    hipLaunchKernelGGL((muon_momentum_kernel<GD, true>), dim3(nb), dim3(256), 0, stream, buf, g, n, mu, one_minus_mu,
+                       nesterov, partial);
+  else
+    hipLaunchKernelGGL((muon_momentum_kernel<GD, false>), dim3(nb), dim3(256), 0, stream, buf, g, n, mu, one_minus_mu,
+                       nesterov, partial);
   dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64));
   hipLaunchKernelGGL(muon_normalize_kernel<GD>, grid, dim3(256), 0, stream, buf, g, rows, cols, mu, nesterov, partial,
                      nb, eps, (int)(rows > cols), x, xt, ldx, ldxt);
@@ -358,14 +408,23 @@ int apexw_launch_muon_prepare(float* buf, const void* g, int32_t g_dtype, int64_
 int apexw_launch_muon_apply(void* p, int32_t p_dtype, const uint16_t* u, int64_t rows, int64_t cols, int64_t ldu,
                             float wd_factor, int32_t apply_wd, float neg_lr_eff, hipStream_t stream) {
   const int64_t n = rows * cols;
-  if (p_dtype == APEXW_F32)
-    hipLaunchKernelGGL(muon_apply_kernel<APEXW_F32>, dim3(grid_for(n)), dim3(256), 0, stream, p, u, rows, cols, ldu,
-                       wd_factor, apply_wd, neg_lr_eff);
-  else if (p_dtype == APEXW_BF16)
-    hipLaunchKernelGGL(muon_apply_kernel<APEXW_BF16>, dim3(grid_for(n)), dim3(256), 0, stream, p, u, rows, cols, ldu,
-                       wd_factor, apply_wd, neg_lr_eff);
-  else
-    hipLaunchKernelGGL(muon_apply_kernel<APEXW_F16>, dim3(grid_for(n)), dim3(256), 0, stream, p, u, rows, cols, ldu,
-                       wd_factor, apply_wd, neg_lr_eff);
+  const bool vec = cols % 8 == 0 && ldu % 8 == 0 && (((uintptr_t)p | (uintptr_t)u) & 15u) == 0;
+  const dim3 grid(grid_for(vec ? n / 8 : n));
+  if (p_dtype == APEXW_F32) {
+    if (vec) hipLaunchKernelGGL((muon_apply_kernel<APEXW_F32, true>), grid, dim3(256), 0, stream, p, u, rows, cols, ldu,
+                                wd_factor, apply_wd, neg_lr_eff);
+    else hipLaunchKernelGGL((muon_apply_kernel<APEXW_F32, false>), grid, dim3(256), 0, stream, p, u, rows, cols, ldu,
+                            wd_factor, apply_wd, neg_lr_eff);
+  } else if (p_dtype == APEXW_BF16) {
+    if (vec) hipLaunchKernelGGL((muon_apply_kernel<APEXW_BF16, true>), grid, dim3(256), 0, stream, p, u, rows, cols,
+                                ldu, wd_factor, apply_wd, neg_lr_eff);
+    else hipLaunchKernelGGL((muon_apply_kernel<APEXW_BF16, false>), grid, dim3(256), 0, stream, p, u, rows, cols, ldu,
+                            wd_factor, apply_wd, neg_lr_eff);
+  } else {
+    if (vec) hipLaunchKernelGGL((muon_apply_kernel<APEXW_F16, true>), grid, dim3(256), 0, stream, p, u, rows, cols, ldu,
+                                wd_factor, apply_wd, neg_lr_eff);
+    else hipLaunchKernelGGL((muon_apply_kernel<APEXW_F16, false>), grid, dim3(256), 0, stream, p, u, rows, cols, ldu,
+                            wd_factor, apply_wd, neg_lr_eff);
+  }
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }

@@ -115,7 +115,8 @@ def _muon_updates(shapes, steps=1, seed=0, dtype=torch.float32, nesterov=False):
     return out
 
 
-@pytest.mark.parametrize("shapes", [[(256, 512)], [(512, 256)], [(300, 200)], [(64, 64)], [(256, 512), (256, 512)]])
+@pytest.mark.parametrize("shapes", [[(256, 512)], [(512, 256)], [(300, 200)], [(64, 64)], [(256, 512), (256, 512)],
+                                    [(33, 50)], [(100, 36), (100, 36)]])
 def test_muon_step_matches_fp32_oracle(shapes):
     _need_gpu()
     print(f"muon shapes={shapes}", flush=True)

@@ -19,6 +19,8 @@ table is re-uploaded (one host-to-device copy).
 """
 
 import math
+import operator
+import weakref
 
 import numpy as np
 import torch
@@ -27,6 +29,9 @@ from . import _lib as L
 
 _DT = {torch.float32: L.F32, torch.bfloat16: L.BF16, torch.float16: L.F16, torch.uint8: L.U8, torch.int8: L.I8}
 CHUNKED_MIN_NUMEL = 262144  # larger 8-bit tensors take the reference's chunked rounding order
+_GRAD = operator.attrgetter("grad")
+_DATA_PTR = operator.methodcaller("data_ptr")
+_DEREF = weakref.ref.__call__
 
 
 def _lerp_coef(w):
@@ -54,11 +59,17 @@ class StepPlan:
 
     # ------------------------------------------------------------------ validity
     def valid_for(self, group):
-        """The reference's FastExecutionPlan.is_valid_for_step (optimizer.py:575-621)."""
+        """The reference's FastExecutionPlan.is_valid_for_step (optimizer.py:575-621).
+
+        The grads are gathered once per step; when every one is the tensor the
+        table already points at (the usual case: grads are accumulated in place),
+        nothing else is checked per parameter."""
         if not self.params:
             return False
-        for p in self.params:
-            if p.grad is None:
+        gs = list(map(_GRAD, self.params))
+        self._gathered = gs
+        if not self._same_grads(gs):
+            if any(g is None for g in gs):
                 return False
         for p in self.inactive:
             if p.grad is not None:
@@ -104,7 +115,7 @@ class StepPlan:
     def _build_tables(self, group):
         wd_on = group["weight_decay"] != 0
         n = len(self.params)
-        self.grads = [None] * n
+        self._grad_refs = None
         tab = np.zeros(n, dtype=L.TENSOR_DTYPE)
         counts = np.zeros(n, dtype=np.int64)
         for i, (p, st) in enumerate(zip(self.params, self.states)):
@@ -128,6 +139,8 @@ class StepPlan:
             else:
                 counts[i] = (p.numel() + block - 1) // block
         self.host_table = tab          # parameter order
+        self._gathered = None
+        self._fast_static = None
         self.counts = counts
         self.kind_code = 0 if self.kind == "compact" else 1
         self._lib = L.load()
@@ -154,47 +167,67 @@ class StepPlan:
         self.d_unit_begin = torch.from_numpy(self.unit_begin).to(self.device)
         self.clip_ws = None
 
+    def _same_grads(self, gs):
+        """Every grad is the tensor the table was built from (weak references:
+        the plan does not keep last step's grads alive)."""
+        return self._grad_refs is not None and all(map(operator.is_, gs, map(_DEREF, self._grad_refs)))
+
     def _refresh_grads(self):
-        """Point the table at this step's grad tensors; re-upload if any changed."""
-        changed = self.d_table is None
-        grads = []
-        for i, p in enumerate(self.params):
-            g = p.grad
+        """Point the table at this step's grad tensors; re-upload if any changed.
+
+        Grads that are the tensor seen last step need no check (one identity
+        test per parameter).  Otherwise dtype and layout are checked and the
+        grad-pointer column is rebuilt in one pass.  Returns the grads, which
+        the caller keeps alive until the launch is enqueued."""
+        gs = self._gathered if self._gathered is not None else list(map(_GRAD, self.params))
+        self._gathered = None
+        if self.d_table is not None and self._same_grads(gs):
+            return gs
+        for i, (p, g) in enumerate(zip(self.params, gs)):
+            if g is None:
+                raise RuntimeError("a parameter of the plan has no grad")
             if g.dtype != p.dtype:
                 raise NotImplementedError("grad dtype must match the parameter dtype")
             if not g.is_contiguous():
-                g = g.contiguous()
-            grads.append(g)
-            if g is not self.grads[i]:
-                ptr = g.data_ptr()
-                if int(self.host_table[i]["g"]) != ptr:
-                    changed = True
-                    self.host_table[i]["g"] = ptr
-        self.grads = grads
-        if changed:
+                gs[i] = g.contiguous()
+        self._grad_refs = [weakref.ref(g) for g in gs]
+        ptrs = np.fromiter(map(_DATA_PTR, gs), dtype=np.uint64, count=len(gs))
+        if self.d_table is None or not np.array_equal(ptrs, self.host_table["g"]):
+            self.host_table["g"] = ptrs
             fast = self._validate_and_align()
             if self.perm is None or (fast is not None and not np.array_equal(fast, self.fast)):
                 self._layout_units(fast)
             rows = np.ascontiguousarray(self.host_table[self.perm])
             self.d_table = torch.from_numpy(rows.view(np.uint8)).to(self.device)
-        return grads
+        return gs
 
     def _validate_and_align(self):
-        """Check every descriptor; mark unaligned ones element-wise; 8-bit: which take the full-block kernel."""
-        lib = self._lib
-        fast = np.zeros(len(self.params), dtype=bool) if self.kind == "q8" else None
-        for i in range(len(self.params)):
-            row = self.host_table[i]
-            ptrs = int(row["p"]) | int(row["g"]) | int(row["m"]) | int(row["v"])
-            flags = int(row["flags"]) & ~L.FLAG_SCALAR
-            if ptrs & 15 or (self.kind == "q8" and int(row["block"]) % 8):
-                flags |= L.FLAG_SCALAR
-            row["flags"] = flags
-            t = L.Tensor(*(int(row[k]) for k in ("p", "g", "m", "v", "m_scale", "v_scale", "n", "flags", "block")))
-            L.check(lib.apexw_check_tensor(ctypes_ref(t), self.kind_code), f"tensor {i} ({tuple(self.params[i].shape)})")
-            if fast is not None:
-                fast[i] = lib.apexw_check_tensor(ctypes_ref(t), 2) == 0
-        return fast
+        """Mark descriptors with an unaligned pointer element-wise; 8-bit: which take the full-block kernel.
+
+        The C ABI validates every descriptor once per plan (dtypes, flags, block,
+        pointers); later grad-pointer changes only move the alignment, which is
+        recomputed for all rows at once."""
+        tab = self.host_table
+        scalar = ((tab["p"] | tab["g"] | tab["m"] | tab["v"]) & np.uint64(15)) != 0
+        if self.kind == "q8":
+            scalar |= (tab["block"] % 8) != 0
+        bit = np.uint32(L.FLAG_SCALAR)
+        tab["flags"] = np.where(scalar, tab["flags"] | bit, tab["flags"] & ~bit)
+        if self._fast_static is None:
+            lib = self._lib
+            fast_static = np.zeros(len(self.params), dtype=bool)
+            for i in range(len(self.params)):
+                row = tab[i]
+                t = L.Tensor(*(int(row[k]) for k in ("p", "g", "m", "v", "m_scale", "v_scale", "n", "flags", "block")))
+                L.check(lib.apexw_check_tensor(ctypes_ref(t), self.kind_code),
+                        f"tensor {i} ({tuple(self.params[i].shape)})")
+                if self.kind == "q8":
+                    # full-block eligibility apart from alignment: same descriptor on aligned stand-in pointers
+                    t.p = t.g = t.m = t.v = 256
+                    t.flags = int(row["flags"]) & ~L.FLAG_SCALAR
+                    fast_static[i] = lib.apexw_check_tensor(ctypes_ref(t), 2) == 0
+            self._fast_static = fast_static
+        return (self._fast_static & ~scalar) if self.kind == "q8" else None
 
     # ------------------------------------------------------------------ launch
     def _clip(self, clip, sanitize, stream):
@@ -214,7 +247,7 @@ class StepPlan:
     def execute(self, group, seed):
         """Run one optimizer step for the group (cold the first time, replay after)."""
         mode_cold = not self.cold_done
-        self._refresh_grads()
+        grads = self._refresh_grads()  # noqa: F841 -- keeps contiguous copies alive until the launch
         stream = torch.cuda.current_stream(self.device).cuda_stream
         lr, (b1, b2), eps, wd = group["lr"], group["betas"], group["eps"], group["weight_decay"]
         sr = bool(group.get("stochastic_rounding", True))

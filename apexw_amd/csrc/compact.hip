@@ -144,16 +144,16 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
   }
 }
 
+// Group k (512 elements, 8 per lane) of the unit starting at element `start`.
 template <int PD, int MD, int VD, bool QUAD>
-APEXW_DEV void compact_unit(const apexw_tensor& t, int64_t start, const Ctx& c) {
+APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const Ctx& c) {
   constexpr int GD = PD;
   const int64_t n = t.n;
   const int lane = lane_id();
   const bool vec = !(c.tflags & APEXW_FLAG_SCALAR);
-#pragma unroll
-  for (int k = 0; k < kGroups; ++k) {
+  {
     const int64_t e0 = start + (int64_t)(k * 64 + lane) * 8;
-    if (e0 >= n) break;
+    if (e0 >= n) return;
     const int cnt = (int)((n - e0) < 8 ? (n - e0) : 8);
     float p[8], g[8], m[8], v[8];
     const bool full = vec && cnt == 8;
@@ -228,9 +228,13 @@ __global__ __launch_bounds__(256) void compact_step_kernel(const apexw_tensor* _
   Ctx c;
   c.hp = &hp;
   c.coef = (hp.flags & APEXW_HP_CLIP) ? *hp.clip_coef : 1.0f;
-  const int64_t stride = (int64_t)gridDim.x * kWaves;
-  for (int64_t u = (int64_t)blockIdx.x * kWaves + wave; u < n_units; u += stride) {
-    const apexw_unit un = units[u];
+  // one work item = one 512-element group of a unit, so a small launch still
+  // puts four waves per unit in flight (the per-element RNG is keyed by the
+  // element index, so the split does not change any result)
+  const int64_t stride = (int64_t)gridDim.x * kWaves, n_items = n_units * kGroups;
+  for (int64_t w = (int64_t)blockIdx.x * kWaves + wave; w < n_items; w += stride) {
+    const apexw_unit un = units[w / kGroups];
+    const int k = (int)(w % kGroups);
     const apexw_tensor& t = tensors[un.tensor];
     const int64_t start = (int64_t)un.unit * APEXW_COMPACT_UNIT;
     c.tflags = t.flags;
@@ -239,13 +243,13 @@ __global__ __launch_bounds__(256) void compact_step_kernel(const apexw_tensor* _
     const uint32_t vd = (t.flags >> APEXW_FLAG_VDT_SHIFT) & 3u;
     const bool quad = t.flags & APEXW_FLAG_QUAD;
     if (pd == APEXW_F32) {
-      if (vd == APEXW_F32) compact_unit<APEXW_F32, APEXW_BF16, APEXW_F32, false>(t, start, c);
-      else if (quad) compact_unit<APEXW_F32, APEXW_BF16, APEXW_BF16, true>(t, start, c);
-      else compact_unit<APEXW_F32, APEXW_BF16, APEXW_BF16, false>(t, start, c);
+      if (vd == APEXW_F32) compact_group<APEXW_F32, APEXW_BF16, APEXW_F32, false>(t, start, k, c);
+      else if (quad) compact_group<APEXW_F32, APEXW_BF16, APEXW_BF16, true>(t, start, k, c);
+      else compact_group<APEXW_F32, APEXW_BF16, APEXW_BF16, false>(t, start, k, c);
     } else {
-      if (vd == APEXW_F32) compact_unit<APEXW_BF16, APEXW_BF16, APEXW_F32, false>(t, start, c);
-      else if (quad) compact_unit<APEXW_BF16, APEXW_BF16, APEXW_BF16, true>(t, start, c);
-      else compact_unit<APEXW_BF16, APEXW_BF16, APEXW_BF16, false>(t, start, c);
+      if (vd == APEXW_F32) compact_group<APEXW_BF16, APEXW_BF16, APEXW_F32, false>(t, start, k, c);
+      else if (quad) compact_group<APEXW_BF16, APEXW_BF16, APEXW_BF16, true>(t, start, k, c);
+      else compact_group<APEXW_BF16, APEXW_BF16, APEXW_BF16, false>(t, start, k, c);
     }
   }
 }
@@ -264,7 +268,7 @@ static bool compact_combo_ok(uint32_t flags) {
 
 int apexw_launch_compact(const apexw_tensor* tensors, int64_t n_units, const apexw_unit* units,
                          const apexw_hparams* hp, hipStream_t stream) {
-  const int grid = apexw_resident_grid((const void*)compact_step_kernel, n_units);
+  const int grid = apexw_resident_grid((const void*)compact_step_kernel, n_units * kGroups);
   hipLaunchKernelGGL(compact_step_kernel, dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }

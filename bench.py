@@ -258,8 +258,11 @@ def main():
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     ev0.record(stream)
+    host = 0.0
     for _ in range(args.steps):
+        h0 = time.perf_counter()
         opt.step()
+        host += time.perf_counter() - h0
     ev1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -275,7 +278,8 @@ def main():
                     "kernel_ms": gpu_ms, "bytes_per_launch": nbytes, "bytes_per_param": nbytes / n}
     out = {
         "metric": METRIC, "value": n / (ms * 1e-3), "unit": "params/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "warmup": args.warmup, "ms_per_step": ms, "host_ms_per_step": host * 1e3 / args.steps,
+        "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16" if cfg.get("mfma") else "f32", "data": "synthetic",
         "config": {"workload": cfg["workload"], "params": n, "tensors": len(params),
                    "param_dtype": str(cfg["dtype"]).replace("torch.", ""), **{k: v for k, v in cfg["kwargs"].items()}},

@@ -149,9 +149,16 @@ class StepPlan:
         self.perm = None
 
     def _layout_units(self, fast):
-        """Device table in launch order (8-bit: full-block-kernel tensors first) and its unit table."""
+        """Device table in launch order and its unit table.  8-bit: full-block-kernel
+        tensors first (bf16, then fp32), then every other tensor."""
         n = len(self.params)
-        perm = np.arange(n) if fast is None else np.concatenate([np.nonzero(fast)[0], np.nonzero(~fast)[0]])
+        if fast is None:
+            perm, n_bf, n_f32 = np.arange(n), 0, 0
+        else:
+            is32 = np.array([p.dtype == torch.float32 for p in self.params], dtype=bool)
+            fb, ff = fast & ~is32, fast & is32
+            perm = np.concatenate([np.nonzero(fb)[0], np.nonzero(ff)[0], np.nonzero(~fast)[0]])
+            n_bf, n_f32 = int(fb.sum()), int(ff.sum())
         counts = self.counts[perm]
         self.unit_begin = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
         total = int(self.unit_begin[-1])
@@ -159,7 +166,8 @@ class StepPlan:
         units["tensor"] = np.repeat(np.arange(n, dtype=np.uint32), counts)
         units["unit"] = (np.arange(total, dtype=np.int64) - np.repeat(self.unit_begin[:-1], counts)).astype(np.uint32)
         self.n_units = total
-        self.n_fast_units = int(counts[: int(fast.sum())].sum()) if fast is not None else 0
+        self.n_fast_units = int(counts[:n_bf].sum())
+        self.n_fast_f32_units = int(counts[n_bf:n_bf + n_f32].sum())
         self.unit_counts = counts
         self.perm = perm
         self.fast = fast
@@ -267,13 +275,16 @@ class StepPlan:
             groups = [(None, int(self.steps[0].item()))]
         for units, step in groups:
             hp = self._hparams(lr, b1, b2, eps, wd, step, sr, sanitize, coef, seed, mode_cold)
-            d_units, n_units, n_fast = (self.d_units, self.n_units, self.n_fast_units) if units is None else units
+            if units is None:
+                d_units, n_units, n_fast, n_fast32 = self.d_units, self.n_units, self.n_fast_units, self.n_fast_f32_units
+            else:
+                d_units, n_units, n_fast, n_fast32 = units
             if self.kind == "compact":
                 st = self._lib.apexw_compact_step(self.d_table.data_ptr(), len(self.params), d_units.data_ptr(),
                                                   n_units, ctypes_ref(hp), stream)
             else:
                 st = self._lib.apexw_q8_step(self.d_table.data_ptr(), len(self.params), d_units.data_ptr(),
-                                             n_units, n_fast, ctypes_ref(hp), stream)
+                                             n_units, n_fast, n_fast32, ctypes_ref(hp), stream)
             L.check(st, "apexw step")
         self.cold_done = True
 
@@ -286,8 +297,8 @@ class StepPlan:
             keep = vals == val
             mask = np.repeat(keep, self.unit_counts)
             sel = self.d_units.view(-1, 8)[torch.from_numpy(mask).to(self.device)].reshape(-1)
-            n_fast = int(mask[: self.n_fast_units].sum())
-            out.append(((sel, int(mask.sum()), n_fast), int(val)))
+            nb, nf = self.n_fast_units, self.n_fast_f32_units
+            out.append(((sel, int(mask.sum()), int(mask[:nb].sum()), int(mask[nb:nb + nf].sum())), int(val)))
         return out
 
     def _hparams(self, lr, b1, b2, eps, wd, step, sr, sanitize, coef, seed, cold):

@@ -11,7 +11,7 @@
 
 int apexw_launch_compact(const apexw_tensor*, int64_t, const apexw_unit*, const apexw_hparams*, hipStream_t);
 int apexw_launch_q8(const apexw_tensor*, int64_t, const apexw_unit*, const apexw_hparams*, hipStream_t);
-int apexw_launch_q8_fast(const apexw_tensor*, int64_t, const apexw_unit*, const apexw_hparams*, hipStream_t);
+int apexw_launch_q8_fast(const apexw_tensor*, int64_t, const apexw_unit*, const apexw_hparams*, int32_t, hipStream_t);
 bool apexw_q8_fast_eligible(uint32_t flags, uint32_t block);
 int apexw_launch_clip(const apexw_tensor*, int32_t, const apexw_unit*, int64_t, int64_t, const int64_t*, float*, float*,
                       float, uint32_t, float*, hipStream_t);
@@ -118,16 +118,18 @@ int apexw_compact_step(const apexw_tensor* tensors, int32_t n_tensors, const ape
 }
 
 int apexw_q8_step(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,
-                  int64_t n_fast_units, const apexw_hparams* hp, void* stream) {
+                  int64_t n_fast_units, int64_t n_fast_f32_units, const apexw_hparams* hp, void* stream) {
   if (!tensors || !units || n_tensors <= 0 || n_units < 0 || !hp_ok(hp)) return APEXW_ERR_ARG;
-  if (n_fast_units < 0 || n_fast_units > n_units) return APEXW_ERR_ARG;
+  if (n_fast_units < 0 || n_fast_f32_units < 0 || n_fast_units + n_fast_f32_units > n_units) return APEXW_ERR_ARG;
   if (hp->mode == APEXW_MODE_NATIVE) return APEXW_ERR_ARG;
   int st = APEXW_OK;
   if (n_fast_units > 0)
-    st = apexw_launch_q8_fast(tensors, n_fast_units, units, hp, (hipStream_t)stream);
-  const int64_t rest = n_units - n_fast_units;
+    st = apexw_launch_q8_fast(tensors, n_fast_units, units, hp, APEXW_BF16, (hipStream_t)stream);
+  if (st == APEXW_OK && n_fast_f32_units > 0)
+    st = apexw_launch_q8_fast(tensors, n_fast_f32_units, units + n_fast_units, hp, APEXW_F32, (hipStream_t)stream);
+  const int64_t done = n_fast_units + n_fast_f32_units, rest = n_units - done;
   if (st == APEXW_OK && rest > 0)
-    st = apexw_launch_q8(tensors, rest, units + n_fast_units, hp, (hipStream_t)stream);
+    st = apexw_launch_q8(tensors, rest, units + done, hp, (hipStream_t)stream);
   return st;
 }
 

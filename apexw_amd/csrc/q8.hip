@@ -20,8 +20,8 @@
 // quad log-uint8 v, 2048-element blocks and 16-byte aligned buffers.
 static __host__ __device__ inline bool apexw_q8_fast_ok(uint32_t flags, uint32_t block) {
   const uint32_t pd = (flags >> APEXW_FLAG_PDT_SHIFT) & 3u, gd = (flags >> APEXW_FLAG_GDT_SHIFT) & 3u;
-  return pd == APEXW_BF16 && gd == APEXW_BF16 && (flags & APEXW_FLAG_NF4) && (flags & APEXW_FLAG_QUAD) &&
-         !(flags & (APEXW_FLAG_SCALAR | APEXW_FLAG_DENSE16)) && block == 2048;
+  return (pd == APEXW_BF16 || pd == APEXW_F32) && gd == pd && (flags & APEXW_FLAG_NF4) &&
+         (flags & APEXW_FLAG_QUAD) && !(flags & (APEXW_FLAG_SCALAR | APEXW_FLAG_DENSE16)) && block == 2048;
 }
 
 namespace {
@@ -33,27 +33,38 @@ struct Q8Ctx {
   const float* vlut;   // LDS: log-uint8 decode table
   const float* code;   // LDS: NF4 codebook
   const float2* pair;    // LDS: NF4 byte -> two values
-  const float4* frac16;  // LDS: signed fractional NF4 code buckets (x 65536, +7)
+  const float4* frac16;  // LDS: signed fractional NF4 code buckets (x 4096, +7, lines in y = x + 3)
+  const float2* midtab;  // LDS: NF4 round-to-nearest buckets (kNf4MidTab)
   float coef;
 };
+
+// Division by a denominator shared across a quad or a block, round-to-nearest:
+// r = RN-refined 1/y (one Newton step on v_rcp_f32), q0 = x r, then the exact
+// FMA residual e = x - q0 y corrects q0 (Markstein): the result equals the IEEE
+// quotient except within ~2^-46 of a rounding midpoint.  y is positive, finite
+// and normal at every call site (scales >= 1e-12, denominators >= eps).
+APEXW_DEV float rcp_refined(float y) {
+  const float r0 = __builtin_amdgcn_rcpf(y);
+  return fmaf(fmaf(-y, r0, 1.0f), r0, r0);
+}
+APEXW_DEV float div_shared(float x, float y, float r) {
+  const float q0 = x * r;
+  return fmaf(fmaf(-q0, y, x), r, q0);
+}
 
 APEXW_DEV float lerp_to(float a, float b, float coef, bool hi) {
   // torch lerp(a, b, w): |w| < 0.5 -> a + w*(b-a); else b + (w-1)*(b-a), one FMA each
   return hi ? fmaf(coef, b - a, b) : fmaf(coef, b - a, a);
 }
 
-// NF4 nearest code: searchsorted(mids, x) over the 14 decision points, using the
-// symmetry mids[13-k] = -mids[k].
-APEXW_DEV uint32_t nf4_rne(float x) {
-  const float mids[7] = {APEXW_NF4_MIDS};
+// NF4 nearest code, searchsorted(mids, x) over the 14 decision points (ties to the
+// lower code), through the 64-bucket midpoint table (LDS copy of kNf4MidTab):
+// one lookup and one comparison.
+APEXW_DEV uint32_t nf4_rne_tab(float x, const float2* tab) {
   const float a = fabsf(x);
-  uint32_t lt = 0, le = 0;
-#pragma unroll
-  for (int k = 0; k < 7; ++k) {
-    lt += (mids[k] < a) ? 1u : 0u;
-    le += (mids[k] <= a) ? 1u : 0u;
-  }
-  return x >= 0.0f ? 7u + lt : 7u - le;
+  const float2 e = tab[min((int)(a * 64.0f), 63)];
+  const uint32_t base = (uint32_t)e.x;
+  return x >= 0.0f ? 7u + base + (e.y < a ? 1u : 0u) : 7u - base - (e.y <= a ? 1u : 0u);
 }
 
 // NF4 stochastic code: hi = #(levels[0..14] < x), lo = hi - 1, P(hi) = (x - c_lo)/(c_hi - c_lo).
@@ -81,6 +92,14 @@ APEXW_DEV uint32_t logu8_code(float v, float vmax, bool sr, uint32_t r16) {
   q = rintf(q);
   q = fminf(fmaxf(q, 1.0f), 255.0f);
   return (uint32_t)q;
+}
+
+// logu8_code (round to nearest) with the block's shared reciprocal for v / vmax
+APEXW_DEV uint32_t logu8_code_shared(float v, float vmax, float rvmax) {
+  if (!(v > 0.0f)) return 0u;
+  const float r = fmaxf(div_shared(v, vmax, rvmax), 0x1p-24f);
+  const float q = rintf(log2f(r) * 0x1.52aaaap+3f + 255.0f);
+  return (uint32_t)fminf(fmaxf(q, 1.0f), 255.0f);
 }
 
 template <int GD> APEXW_DEV float q8_grad(float g, uint32_t tflags, const Q8Ctx& c) {
@@ -322,7 +341,7 @@ APEXW_DEV void q8_block(const apexw_tensor& t, uint32_t tix, uint32_t blk, const
       const uint32_t r = sr ? (rng_at(key, (uint32_t)(e0 + j)) >> 16) : 0u;
       if constexpr (NF4) {
         const float x = fminf(fmaxf(mnew[k][j] / ms, -1.0f), 1.0f);
-        mc[j] = sr ? nf4_sr(x, unit_uniform(r), c.code) : nf4_rne(x);
+        mc[j] = sr ? nf4_sr(x, unit_uniform(r), c.code) : nf4_rne_tab(x, c.midtab);
       } else {
         float y = mnew[k][j] / ms;
         if (sr) y = y + (unit_uniform(r) - 0.5f);
@@ -407,7 +426,7 @@ APEXW_DEV void q8_block(const apexw_tensor& t, uint32_t tix, uint32_t blk, const
 //    rounding; NF4 codes come from the signed fractional-index table:
 //    code = (G(x) + r12) >> 12, two codes per 32-bit integer add, gathered
 //    into bytes with v_perm_b32.
-template <bool SR, bool FULL, bool GENERIC>
+template <int PD, bool SR, bool FULL, bool GENERIC>
 APEXW_DEV void q8_block_fast(const apexw_tensor& t, uint32_t tix, uint32_t blk, const Q8Ctx& c) {
   const apexw_hparams& hp = *c.hp;
   const uint32_t hf = hp.flags, tf = t.flags;
@@ -418,32 +437,46 @@ APEXW_DEV void q8_block_fast(const apexw_tensor& t, uint32_t tix, uint32_t blk, 
   const float decay = (tf & APEXW_FLAG_WD) ? hp.wd_factor : 1.0f;
   const bool lerp_hi = hf & APEXW_HP_LERP_HI, look_hi = hf & APEXW_HP_LOOK_HI;
 
-  u32x4 pw[4], gw[4];
+  // p and g: 8 elements per lane per k; one 16-byte word for bf16, two for fp32
+  constexpr int PW = PD == APEXW_F32 ? 2 : 1;
+  u32x4 pw[4][PW], gw[4][PW];
   uint32_t mw[4], vw[4];
   int cnt[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int64_t e = start + k * 512 + lane * 8;
+    const auto pp = APEXW_GLOBAL(const u32x4, (const char*)t.p + e * Elem<PD>::bytes);
+    const auto gp = APEXW_GLOBAL(const u32x4, (const char*)t.g + e * Elem<PD>::bytes);
     if constexpr (FULL) {
       cnt[k] = 8;
-      pw[k] = __builtin_nontemporal_load(APEXW_GLOBAL(const u32x4, (const uint16_t*)t.p + e));
-      gw[k] = __builtin_nontemporal_load(APEXW_GLOBAL(const u32x4, (const uint16_t*)t.g + e));
+#pragma unroll
+      for (int h = 0; h < PW; ++h) {
+        pw[k][h] = __builtin_nontemporal_load(pp + h);
+        gw[k][h] = __builtin_nontemporal_load(gp + h);
+      }
       mw[k] = __builtin_nontemporal_load(APEXW_GLOBAL(const uint32_t, (const uint8_t*)t.m + (e >> 1)));
       vw[k] = __builtin_nontemporal_load(APEXW_GLOBAL(const uint16_t, (const uint8_t*)t.v + (e >> 2)));
     } else {
       // numel % 4 == 0 for quad-v tensors, so a lane holds 0, 4 or 8 elements
       cnt[k] = e >= t.n ? 0 : (t.n - e >= 8 ? 8 : 4);
       const u32x4 z = {0u, 0u, 0u, 0u};
-      pw[k] = z; gw[k] = z; mw[k] = 0x77777777u; vw[k] = 0u;
+#pragma unroll
+      for (int h = 0; h < PW; ++h) { pw[k][h] = z; gw[k][h] = z; }
+      mw[k] = 0x77777777u; vw[k] = 0u;
       if (cnt[k] == 8) {
-        pw[k] = *APEXW_GLOBAL(const u32x4, (const uint16_t*)t.p + e);
-        gw[k] = *APEXW_GLOBAL(const u32x4, (const uint16_t*)t.g + e);
+#pragma unroll
+        for (int h = 0; h < PW; ++h) { pw[k][h] = pp[h]; gw[k][h] = gp[h]; }
         mw[k] = *APEXW_GLOBAL(const uint32_t, (const uint8_t*)t.m + (e >> 1));
         vw[k] = *APEXW_GLOBAL(const uint16_t, (const uint8_t*)t.v + (e >> 2));
       } else if (cnt[k] == 4) {
-        const u32x2 a = *APEXW_GLOBAL(const u32x2, (const uint16_t*)t.p + e);
-        const u32x2 b = *APEXW_GLOBAL(const u32x2, (const uint16_t*)t.g + e);
-        pw[k].x = a.x; pw[k].y = a.y; gw[k].x = b.x; gw[k].y = b.y;
+        if constexpr (PD == APEXW_F32) {
+          pw[k][0] = pp[0];
+          gw[k][0] = gp[0];
+        } else {
+          const u32x2 a = *APEXW_GLOBAL(const u32x2, (const uint16_t*)t.p + e);
+          const u32x2 b = *APEXW_GLOBAL(const u32x2, (const uint16_t*)t.g + e);
+          pw[k][0].x = a.x; pw[k][0].y = a.y; gw[k][0].x = b.x; gw[k][0].y = b.y;
+        }
         mw[k] = 0x77770000u | *APEXW_GLOBAL(const uint16_t, (const uint8_t*)t.m + (e >> 1));
         vw[k] = *APEXW_GLOBAL(const uint8_t, (const uint8_t*)t.v + (e >> 2));
       }
@@ -464,26 +497,36 @@ APEXW_DEV void q8_block_fast(const apexw_tensor& t, uint32_t tix, uint32_t blk, 
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     float p[8], g[8], m[8];
-    const uint32_t pv[4] = {pw[k].x, pw[k].y, pw[k].z, pw[k].w};
-    const uint32_t gv[4] = {gw[k].x, gw[k].y, gw[k].z, gw[k].w};
+    const uint32_t pv[4] = {pw[k][0].x, pw[k][0].y, pw[k][0].z, pw[k][0].w};
     float look[8];
+    if constexpr (PD == APEXW_F32) {
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      p[2 * b] = __uint_as_float(pv[b] << 16);
-      p[2 * b + 1] = __uint_as_float(pv[b] & 0xFFFF0000u);
-      g[2 * b] = __uint_as_float(gv[b] << 16);
-      g[2 * b + 1] = __uint_as_float(gv[b] & 0xFFFF0000u);
+      for (int h = 0; h < 2; ++h) {
+        p[4 * h] = __uint_as_float(pw[k][h].x); p[4 * h + 1] = __uint_as_float(pw[k][h].y);
+        p[4 * h + 2] = __uint_as_float(pw[k][h].z); p[4 * h + 3] = __uint_as_float(pw[k][h].w);
+        g[4 * h] = __uint_as_float(gw[k][h].x); g[4 * h + 1] = __uint_as_float(gw[k][h].y);
+        g[4 * h + 2] = __uint_as_float(gw[k][h].z); g[4 * h + 3] = __uint_as_float(gw[k][h].w);
+      }
+    } else {
+      const uint32_t gv[4] = {gw[k][0].x, gw[k][0].y, gw[k][0].z, gw[k][0].w};
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        p[2 * b] = __uint_as_float(pv[b] << 16);
+        p[2 * b + 1] = __uint_as_float(pv[b] & 0xFFFF0000u);
+        g[2 * b] = __uint_as_float(gv[b] << 16);
+        g[2 * b + 1] = __uint_as_float(gv[b] & 0xFFFF0000u);
+      }
     }
     if (prep) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) g[j] = q8_grad<APEXW_BF16>(g[j], tf, c);
+      for (int j = 0; j < 8; ++j) g[j] = q8_grad<PD>(g[j], tf, c);
     } else if constexpr (!SR) {
       bool bad = false;
 #pragma unroll
       for (int j = 0; j < 8; ++j) bad |= !__builtin_isfinite(g[j]);
       if (bad) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) g[j] = q8_grad<APEXW_BF16>(g[j], tf, c);
+        for (int j = 0; j < 8; ++j) g[j] = q8_grad<PD>(g[j], tf, c);
       }
     }
     if constexpr (SR) {
@@ -510,7 +553,7 @@ APEXW_DEV void q8_block_fast(const apexw_tensor& t, uint32_t tix, uint32_t blk, 
       }
       if (!prep && !(__builtin_isfinite(s2[0]) && __builtin_isfinite(s2[1]))) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) g[j] = q8_grad<APEXW_BF16>(g[j], tf, c);
+        for (int j = 0; j < 8; ++j) g[j] = q8_grad<PD>(g[j], tf, c);
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
           const int b = 4 * q;
@@ -570,10 +613,34 @@ APEXW_DEV void q8_block_fast(const apexw_tensor& t, uint32_t tix, uint32_t blk, 
         vq[k][q] = vv;
         if (FULL || 4 * q < cnt[k]) vmax = fmaxf(vmax, vv);
         const float den = fmaxf(sqrtf(vv) + hp.eps_scaled, hp.eps);
+        const float rden = rcp_refined(den);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) upd[b + i] = (num[b + i] / den) * hp.step_size;
+        for (int i = 0; i < 4; ++i) upd[b + i] = div_shared(num[b + i], den, rden) * hp.step_size;
       }
     }
+    const int64_t e = start + k * 512 + lane * 8;
+    if constexpr (PD == APEXW_F32) {
+      // fp32 parameters: p * decay - update in fp32 (both rounding orders agree), no SR
+      float x[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[j] = p[j] * decay - upd[j];
+      if constexpr (SR) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) hm[k][b] = __builtin_amdgcn_perm(hbits[k][2 * b + 1], hbits[k][2 * b], 0x05040100u);
+      }
+      const u32x4 lo = {__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]), __float_as_uint(x[3])};
+      const u32x4 hi = {__float_as_uint(x[4]), __float_as_uint(x[5]), __float_as_uint(x[6]), __float_as_uint(x[7])};
+      const auto dst = APEXW_GLOBAL(u32x4, (float*)t.p + e);
+      if constexpr (FULL) {
+        __builtin_nontemporal_store(lo, dst);
+        __builtin_nontemporal_store(hi, dst + 1);
+      } else if (cnt[k] == 8) {
+        dst[0] = lo;
+        dst[1] = hi;
+      } else if (cnt[k] == 4) {
+        dst[0] = lo;
+      }
+    } else {
     uint32_t pout[4];
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
@@ -606,7 +673,6 @@ APEXW_DEV void q8_block_fast(const apexw_tensor& t, uint32_t tix, uint32_t blk, 
         pout[b] = (__float_as_uint(x[0]) >> 16) | (__float_as_uint(x[1]) & 0xFFFF0000u);
       }
     }
-    const int64_t e = start + k * 512 + lane * 8;
     u32x4 po = {pout[0], pout[1], pout[2], pout[3]};
     if constexpr (FULL) {
       __builtin_nontemporal_store(po, APEXW_GLOBAL(u32x4, (uint16_t*)t.p + e));
@@ -615,6 +681,7 @@ APEXW_DEV void q8_block_fast(const apexw_tensor& t, uint32_t tix, uint32_t blk, 
     } else if (cnt[k] == 4) {
       u32x2 p2 = {po.x, po.y};
       *APEXW_GLOBAL(u32x2, (uint16_t*)t.p + e) = p2;
+    }
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -631,6 +698,7 @@ APEXW_DEV void q8_block_fast(const apexw_tensor& t, uint32_t tix, uint32_t blk, 
     t.v_scale[blk] = vs;
   }
   const float rms = 1.0f / ms, rvs = 1.0f / vs;
+  const float rms_rn = rcp_refined(ms), rvs_rn = rcp_refined(vs);
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int64_t e = start + k * 512 + lane * 8;
@@ -662,7 +730,8 @@ APEXW_DEV void q8_block_fast(const apexw_tensor& t, uint32_t tix, uint32_t blk, 
     } else {
       uint32_t code[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) code[j] = nf4_rne(fminf(fmaxf(mnew[k][j] / ms, -1.0f), 1.0f));
+      for (int j = 0; j < 8; ++j)
+        code[j] = nf4_rne_tab(fminf(fmaxf(div_shared(mnew[k][j], ms, rms_rn), -1.0f), 1.0f), c.midtab);
 #pragma unroll
       for (int b = 0; b < 4; ++b) w |= ((code[2 * b] << 4) | code[2 * b + 1]) << (8 * b);
     }
@@ -681,7 +750,7 @@ APEXW_DEV void q8_block_fast(const apexw_tensor& t, uint32_t tix, uint32_t blk, 
         const float qf = fmaf(__builtin_amdgcn_logf(r), 0x1.52aaaap+3f, 255.0f) + u;
         vc[q] = (uint32_t)__builtin_amdgcn_fmed3f(qf, 1.0f, 255.0f);
       } else {
-        vc[q] = logu8_code(vv, vs, false, 0u);
+        vc[q] = logu8_code_shared(vv, vs, rvs_rn);
       }
     }
     if constexpr (FULL) {
@@ -721,14 +790,19 @@ APEXW_DEV void q8_dense16(const apexw_tensor& t, const Q8Ctx& c) {
 }
 
 
-// Kernel for the units of fast-path tensors (see apexw_q8_fast_ok).
+// Kernel for the units of fast-path tensors (see apexw_q8_fast_ok) with parameter
+// dtype PD; each dtype is its own kernel so the fp32 variant's larger register
+// footprint does not lower the bf16 kernel's occupancy.
+template <int PD>
 __global__ __launch_bounds__(256) void q8_fast_kernel(const apexw_tensor* __restrict__ tensors,
                                                       const apexw_unit* __restrict__ units,
                                                       int64_t n_units, apexw_hparams hp) {
   __shared__ float s_vlut[256];
   __shared__ float2 s_pair[256];
   __shared__ float4 s_frac16[128];
+  __shared__ float2 s_midtab[64];
   s_vlut[threadIdx.x] = kVLogLut[threadIdx.x];
+  if (threadIdx.x < 64) s_midtab[threadIdx.x] = make_float2(kNf4MidTab[2 * threadIdx.x], kNf4MidTab[2 * threadIdx.x + 1]);
   s_pair[threadIdx.x] = make_float2(kNf4Pair[2 * threadIdx.x], kNf4Pair[2 * threadIdx.x + 1]);
   if (threadIdx.x < 128)
     s_frac16[threadIdx.x] = make_float4(kNf4Code16[4 * threadIdx.x], kNf4Code16[4 * threadIdx.x + 1],
@@ -740,25 +814,27 @@ __global__ __launch_bounds__(256) void q8_fast_kernel(const apexw_tensor* __rest
   c.code = nullptr;
   c.pair = s_pair;
   c.frac16 = s_frac16;
+  c.midtab = s_midtab;
   c.coef = (hp.flags & APEXW_HP_CLIP) ? *hp.clip_coef : 1.0f;
   const uint32_t wave = uniform(threadIdx.x >> 6);
   const int64_t stride = (int64_t)gridDim.x * kWaves;
   for (int64_t u = (int64_t)blockIdx.x * kWaves + wave; u < n_units; u += stride) {
     const apexw_unit un = units[u];
     const apexw_tensor& t = tensors[un.tensor];
-    if (!apexw_q8_fast_ok(t.flags, t.block)) continue;  // never reached for a valid plan
+    // never taken for a valid plan: the unit ranges hold only this kernel's tensors
+    if (!apexw_q8_fast_ok(t.flags, t.block) || ((t.flags >> APEXW_FLAG_PDT_SHIFT) & 3u) != (uint32_t)PD) continue;
     const bool full = (int64_t)(un.unit + 1) * 2048 <= t.n;
     const bool gen = t.flags & APEXW_FLAG_GENERIC;
     if (hp.flags & APEXW_HP_SR) {
-      if (full && !gen) q8_block_fast<true, true, false>(t, un.tensor, un.unit, c);
-      else if (full) q8_block_fast<true, true, true>(t, un.tensor, un.unit, c);
-      else if (!gen) q8_block_fast<true, false, false>(t, un.tensor, un.unit, c);
-      else q8_block_fast<true, false, true>(t, un.tensor, un.unit, c);
+      if (full && !gen) q8_block_fast<PD, true, true, false>(t, un.tensor, un.unit, c);
+      else if (full) q8_block_fast<PD, true, true, true>(t, un.tensor, un.unit, c);
+      else if (!gen) q8_block_fast<PD, true, false, false>(t, un.tensor, un.unit, c);
+      else q8_block_fast<PD, true, false, true>(t, un.tensor, un.unit, c);
     } else {
-      if (full && !gen) q8_block_fast<false, true, false>(t, un.tensor, un.unit, c);
-      else if (full) q8_block_fast<false, true, true>(t, un.tensor, un.unit, c);
-      else if (!gen) q8_block_fast<false, false, false>(t, un.tensor, un.unit, c);
-      else q8_block_fast<false, false, true>(t, un.tensor, un.unit, c);
+      if (full && !gen) q8_block_fast<PD, false, true, false>(t, un.tensor, un.unit, c);
+      else if (full) q8_block_fast<PD, false, true, true>(t, un.tensor, un.unit, c);
+      else if (!gen) q8_block_fast<PD, false, false, false>(t, un.tensor, un.unit, c);
+      else q8_block_fast<PD, false, false, true>(t, un.tensor, un.unit, c);
     }
   }
 }
@@ -768,8 +844,10 @@ __global__ __launch_bounds__(256) void q8_step_kernel(const apexw_tensor* __rest
                                                       int64_t n_units, apexw_hparams hp) {
   __shared__ float s_vlut[256];
   __shared__ float s_code[16];
+  __shared__ float2 s_midtab[64];
   s_vlut[threadIdx.x] = kVLogLut[threadIdx.x];
   if (threadIdx.x < 16) s_code[threadIdx.x] = kNf4Code[threadIdx.x];
+  if (threadIdx.x < 64) s_midtab[threadIdx.x] = make_float2(kNf4MidTab[2 * threadIdx.x], kNf4MidTab[2 * threadIdx.x + 1]);
   __syncthreads();
   Q8Ctx c;
   c.hp = &hp;
@@ -777,6 +855,7 @@ __global__ __launch_bounds__(256) void q8_step_kernel(const apexw_tensor* __rest
   c.code = s_code;
   c.pair = nullptr;
   c.frac16 = nullptr;
+  c.midtab = s_midtab;
   c.coef = (hp.flags & APEXW_HP_CLIP) ? *hp.clip_coef : 1.0f;
   const uint32_t wave = uniform(threadIdx.x >> 6);
   const int64_t stride = (int64_t)gridDim.x * kWaves;
@@ -835,8 +914,13 @@ int apexw_launch_q8(const apexw_tensor* tensors, int64_t n_units, const apexw_un
 }
 
 int apexw_launch_q8_fast(const apexw_tensor* tensors, int64_t n_units, const apexw_unit* units,
-                         const apexw_hparams* hp, hipStream_t stream) {
-  const int grid = apexw_resident_grid((const void*)q8_fast_kernel, n_units);
-  hipLaunchKernelGGL(q8_fast_kernel, dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
+                         const apexw_hparams* hp, int32_t p_dtype, hipStream_t stream) {
+  if (p_dtype == APEXW_F32) {
+    const int grid = apexw_resident_grid((const void*)q8_fast_kernel<APEXW_F32>, n_units);
+    hipLaunchKernelGGL(q8_fast_kernel<APEXW_F32>, dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
+    return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
+  }
+  const int grid = apexw_resident_grid((const void*)q8_fast_kernel<APEXW_BF16>, n_units);
+  hipLaunchKernelGGL(q8_fast_kernel<APEXW_BF16>, dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define APEXW_ABI_VERSION 1
+#define APEXW_ABI_VERSION 2
 
 /* status codes */
 enum apexw_status {
@@ -130,7 +130,7 @@ int apexw_abi_version(void);
 /*
  * Validate one tensor descriptor (HOST copy) before it is uploaded into a
  * device table: kind 0 = compact step, 1 = 8-bit step, 2 = 8-bit step on the
- * full-block kernel (bf16 params, NF4 m, quad v, 2048-element blocks).  Checks the dtype
+ * full-block kernel (bf16 or fp32 params, NF4 m, quad v, 2048-element blocks).  Checks the dtype
  * combination, block size and the 16-byte alignment the vector path needs
  * (unless APEXW_FLAG_SCALAR is set).  Mirrors the per-call tensor checks of the
  * reference's pybind glue (apexw/csrc/apexw_cuda.cpp:109-180, :310-380), done
@@ -150,14 +150,16 @@ int apexw_compact_step(const apexw_tensor* tensors, int32_t n_tensors,
  * 8-bit fused step: dequantize m (NF4 or INT8) and v (log-uint8) with their
  * block scales, AdamW with the SNR lookahead gain, write p, requantize m and v
  * with block absmax / max scales (EMA-max 0.9 / 0.95).  One unit = one block.
- * units[0, n_fast_units) must belong to tensors accepted by
- * apexw_check_tensor(t, 2) (bf16 params, NF4 m, quad v, 2048-element blocks,
- * aligned): they run on the full-block kernel; the remaining units run on the
- * general kernel.
+ * Units are laid out in three ranges: units[0, n_fast_units) belong to bf16
+ * tensors accepted by apexw_check_tensor(t, 2) and run on the full-block
+ * kernel; the next n_fast_f32_units belong to fp32 tensors accepted by
+ * apexw_check_tensor(t, 2) and run on its fp32 variant; the remaining units
+ * (any layout) run on the general kernel.  Zero for both counts runs
+ * everything on the general kernel (same results with SR off).
  */
 int apexw_q8_step(const apexw_tensor* tensors, int32_t n_tensors,
                   const apexw_unit* units, int64_t n_units, int64_t n_fast_units,
-                  const apexw_hparams* hp, void* stream);
+                  int64_t n_fast_f32_units, const apexw_hparams* hp, void* stream);
 
 /*
  * Global-L2 clip coefficient over the grads of the table:

@@ -57,11 +57,16 @@ def test_check_tensor_rejects_bad_descriptors():
     # entry points reject null tables before touching the GPU
     hp = _lib.HParams()
     assert lib.apexw_compact_step(None, 1, None, 1, ctypes.byref(hp), None) == 1
-    assert lib.apexw_q8_step(None, 1, None, 1, 0, ctypes.byref(hp), None) == 1
+    assert lib.apexw_q8_step(None, 1, None, 1, 0, 0, ctypes.byref(hp), None) == 1
+    units = ctypes.c_uint64(0)
+    assert lib.apexw_q8_step(ctypes.byref(q), 1, ctypes.byref(units), 1, 1, 1, ctypes.byref(hp), None) == 1
     q.block = 2048
     assert lib.apexw_check_tensor(ctypes.byref(q), 2) == 0
-    q.flags &= ~_lib.FLAG_NF4
-    q.flags &= ~_lib.FLAG_QUAD
+    q.flags = (_lib.F32 << 0) | (_lib.F32 << 2) | _lib.FLAG_NF4 | _lib.FLAG_QUAD   # fp32 params: full-block kernel too
+    assert lib.apexw_check_tensor(ctypes.byref(q), 2) == 0
+    q.flags = (_lib.F32 << 0) | (_lib.BF16 << 2) | _lib.FLAG_NF4 | _lib.FLAG_QUAD  # mixed p / g dtypes: no
+    assert lib.apexw_check_tensor(ctypes.byref(q), 2) == 2
+    q.flags = (_lib.BF16 << 0) | (_lib.BF16 << 2)
     assert lib.apexw_check_tensor(ctypes.byref(q), 2) == 2
 
 

@@ -13,7 +13,7 @@ import numpy as np
 
 from ._build import LIB_PATH
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # dtype codes
 F32, BF16, F16, U8, I8 = 0, 1, 2, 3, 4
@@ -67,6 +67,19 @@ class HParams(ctypes.Structure):
                 ("mode", ctypes.c_uint32), ("flags", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
 
 
+# apexw_gemm_problem: one product of a grouped launch
+GEMM_PROBLEM_DTYPE = np.dtype([
+    ("a", np.uint64), ("b", np.uint64), ("et", np.uint64), ("c", np.uint64), ("ct", np.uint64),
+    ("m", np.int32), ("n", np.int32), ("k", np.int32), ("lda", np.int32), ("ldb", np.int32), ("lde", np.int32),
+    ("ldc", np.int32), ("ldct", np.int32), ("alpha", np.float32), ("beta", np.float32),
+    ("flags", np.uint32), ("reserved", np.uint32),
+])
+assert GEMM_PROBLEM_DTYPE.itemsize == 88
+GEMM_SYM = 1
+GEMM_OUT_C, GEMM_OUT_CT, GEMM_ADD = 1, 2, 4
+GEMM_MAX_PROBLEMS = 256
+GEMM_QUEUES = 8
+
 _vp, _i32, _i64, _f32, _u32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_uint32
 _HP = ctypes.POINTER(HParams)
 
@@ -79,6 +92,10 @@ SIGNATURES = {
     "apexw_grad_clip_coef": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _vp, _vp, _vp, _f32, _u32, _vp, _vp]),
     "apexw_gemm_nt_bf16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                           _i32, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _vp]),
+    "apexw_gemm_grouped_items": (ctypes.c_int64, [_vp, _i32]),
+    "apexw_gemm_grouped_schedule": (ctypes.c_int, [_vp, _i32, _vp, _i64, _vp, ctypes.POINTER(ctypes.c_int32),
+                                                   ctypes.POINTER(ctypes.c_int32)]),
+    "apexw_gemm_nt_grouped": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, _vp]),
     "apexw_muon_workspace_floats": (ctypes.c_int64, [_i64, _i64]),
     "apexw_muon_prepare": (ctypes.c_int, [_vp, _vp, _i32, _i64, _i64, _f32, _f32, _i32, _f32, _vp, _vp, _i64, _i64,
                                           _vp, _vp]),
@@ -117,3 +134,21 @@ def load(path=LIB_PATH):
 def check(status, what):
     if status != 0:
         raise ApexwError(f"{what}: {STATUS.get(status, status)}")
+
+
+def gemm_schedule(problems):
+    """Validate a host table of GEMM_PROBLEM_DTYPE rows and build its grouped-launch
+    tile queues: returns (items uint32[n_items], queue_offsets int32[GEMM_QUEUES + 1],
+    n_workgroups, kind)."""
+    lib = load()
+    problems = np.ascontiguousarray(problems, dtype=GEMM_PROBLEM_DTYPE)
+    n_items = int(lib.apexw_gemm_grouped_items(problems.ctypes.data, len(problems)))
+    if n_items < 0:
+        check(-n_items, "apexw_gemm_grouped_items")
+    items = np.empty(max(n_items, 1), dtype=np.uint32)
+    offsets = np.empty(GEMM_QUEUES + 1, dtype=np.int32)
+    n_wg, kind = ctypes.c_int32(0), ctypes.c_int32(0)
+    check(lib.apexw_gemm_grouped_schedule(problems.ctypes.data, len(problems), items.ctypes.data, n_items,
+                                          offsets.ctypes.data, ctypes.byref(n_wg), ctypes.byref(kind)),
+          "apexw_gemm_grouped_schedule")
+    return items[:n_items], offsets, n_wg.value, kind.value

@@ -5,7 +5,10 @@
 // built once per execution plan by the caller; apexw_check_tensor validates one
 // descriptor (host copy) when the plan is built, so the per-step calls do not
 // copy or inspect the tables.
+#include <algorithm>
 #include <mutex>
+#include <queue>
+#include <vector>
 
 #include "common.h"
 
@@ -20,6 +23,8 @@ int apexw_launch_gemm_nt(const uint16_t*, const uint16_t*, const uint16_t*, uint
                          int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int64_t, int64_t, int64_t,
                          int64_t, int64_t, float, float, hipStream_t);
 int apexw_muon_partials(int64_t n);
+int apexw_launch_gemm_grouped(const apexw_gemm_problem*, const uint32_t*, const int32_t*, int32_t, int32_t,
+                              hipStream_t);
 int apexw_launch_muon_prepare(float*, const void*, int32_t, int64_t, int64_t, float, float, int32_t, float, uint16_t*,
                               uint16_t*, int64_t, int64_t, float*, hipStream_t);
 int apexw_launch_muon_apply(void*, int32_t, const uint16_t*, int64_t, int64_t, int64_t, float, int32_t, float,
@@ -142,6 +147,9 @@ int apexw_gemm_nt_bf16(const void* a, const void* b, const void* et, void* c, vo
   if (m % APEXW_GEMM_TILE || n % APEXW_GEMM_TILE || k % APEXW_GEMM_KTILE) return APEXW_ERR_ARG;
   // operand rows must cover the tile extents they are read over
   if (lda < k || ldb < k || (c && ldc < n) || (ct && ldct < m) || (et && lde < m)) return APEXW_ERR_ARG;
+  if (lda > APEXW_GEMM_MAX_LD || ldb > APEXW_GEMM_MAX_LD || (et && lde > APEXW_GEMM_MAX_LD) ||
+      (c && ldc > APEXW_GEMM_MAX_LD) || (ct && ldct > APEXW_GEMM_MAX_LD))
+    return APEXW_ERR_ARG;
   if ((lda | ldb | (et ? lde : 0) | (c ? ldc : 0) | (ct ? ldct : 0)) & 7) return APEXW_ERR_ALIGN;
   const uintptr_t al = (uintptr_t)a | (uintptr_t)b | (uintptr_t)et | (uintptr_t)c | (uintptr_t)ct;
   if (al & 15u) return APEXW_ERR_ALIGN;
@@ -149,6 +157,123 @@ int apexw_gemm_nt_bf16(const void* a, const void* b, const void* et, void* c, vo
   return apexw_launch_gemm_nt((const uint16_t*)a, (const uint16_t*)b, (const uint16_t*)et, (uint16_t*)c,
                               (uint16_t*)ct, m, n, k, lda, ldb, lde, ldc, ldct, batch, stride_a, stride_b, stride_e,
                               stride_c, stride_ct, alpha, beta, (hipStream_t)stream);
+}
+
+namespace {
+
+constexpr int kTile = APEXW_GEMM_TILE;
+
+// Epilogue kind of one problem, or minus a status when it is invalid.
+int gemm_problem_kind(const apexw_gemm_problem& p) {
+  if (!p.a || !p.b || (!p.c && !p.ct) || (p.beta != 0.0f && !p.et)) return -APEXW_ERR_ARG;
+  if ((p.flags & ~APEXW_GEMM_SYM) || p.reserved) return -APEXW_ERR_ARG;
+  if (p.m <= 0 || p.n <= 0 || p.k <= 0) return -APEXW_ERR_ARG;
+  if (p.m % kTile || p.n % kTile || p.k % APEXW_GEMM_KTILE) return -APEXW_ERR_ARG;
+  if (p.m / kTile > 4096 || p.n / kTile > 4096) return -APEXW_ERR_ARG;
+  const bool add = p.beta != 0.0f;
+  if (p.lda < p.k || p.ldb < p.k || (p.c && p.ldc < p.n) || (p.ct && p.ldct < p.m) || (add && p.lde < p.m))
+    return -APEXW_ERR_ARG;
+  const int32_t lds[5] = {p.lda, p.ldb, add ? p.lde : 0, p.c ? p.ldc : 0, p.ct ? p.ldct : 0};
+  for (int32_t ld : lds) {
+    if (ld > APEXW_GEMM_MAX_LD) return -APEXW_ERR_ARG;
+    if (ld & 7) return -APEXW_ERR_ALIGN;
+  }
+  const uintptr_t al = (uintptr_t)p.a | (uintptr_t)p.b | (uintptr_t)(add ? p.et : nullptr) | (uintptr_t)p.c |
+                       (uintptr_t)p.ct;
+  if (al & 15u) return -APEXW_ERR_ALIGN;
+  if (p.flags & APEXW_GEMM_SYM) {
+    if (p.m != p.n || p.a != p.b || p.lda != p.ldb || !p.c || p.ct != p.c || p.ldct != p.ldc) return -APEXW_ERR_ARG;
+  }
+  return (p.c ? APEXW_GEMM_OUT_C : 0) | (p.ct ? APEXW_GEMM_OUT_CT : 0) | (add ? APEXW_GEMM_ADD : 0);
+}
+
+int64_t gemm_problem_tiles(const apexw_gemm_problem& p) {
+  const int64_t tm = p.m / kTile, tn = p.n / kTile;
+  return (p.flags & APEXW_GEMM_SYM) ? tm * (tm + 1) / 2 : tm * tn;
+}
+
+}  // namespace
+
+int64_t apexw_gemm_grouped_items(const apexw_gemm_problem* problems, int32_t n_problems) {
+  if (!problems || n_problems <= 0 || n_problems > 256) return -APEXW_ERR_ARG;
+  int64_t n = 0;
+  for (int32_t i = 0; i < n_problems; ++i) {
+    const int kind = gemm_problem_kind(problems[i]);
+    if (kind < 0) return kind;
+    n += gemm_problem_tiles(problems[i]);
+  }
+  return n;
+}
+
+int apexw_gemm_grouped_schedule(const apexw_gemm_problem* problems, int32_t n_problems, uint32_t* items,
+                                int64_t n_items, int32_t* queue_offsets, int32_t* n_workgroups, int32_t* kind) {
+  if (!items || !queue_offsets || !n_workgroups || !kind) return APEXW_ERR_ARG;
+  const int64_t want = apexw_gemm_grouped_items(problems, n_problems);
+  if (want < 0) return (int)-want;
+  if (want != n_items || n_items >= INT32_MAX) return APEXW_ERR_ARG;
+  const int kind0 = gemm_problem_kind(problems[0]);
+  for (int32_t i = 1; i < n_problems; ++i)
+    if (gemm_problem_kind(problems[i]) != kind0) return APEXW_ERR_ARG;
+
+  // Work list in locality order: per problem, bands of 4 tile rows, each band
+  // column by column, so a run of consecutive tiles shares A row panels and B
+  // column panels.  Cost = K tiles + a few for the epilogue's traffic.
+  struct Item {
+    uint32_t code;
+    int64_t cost;
+  };
+  std::vector<Item> list;
+  list.reserve((size_t)n_items);
+  const int64_t epi = 2 * (((kind0 & APEXW_GEMM_OUT_C) != 0) + ((kind0 & APEXW_GEMM_OUT_CT) != 0) +
+                           ((kind0 & APEXW_GEMM_ADD) != 0));
+  int64_t total = 0;
+  for (int32_t pi = 0; pi < n_problems; ++pi) {
+    const apexw_gemm_problem& p = problems[pi];
+    const int tiles_m = p.m / kTile, tiles_n = p.n / kTile;
+    const bool sym = (p.flags & APEXW_GEMM_SYM) != 0;
+    const int64_t cost = p.k / APEXW_GEMM_KTILE + epi;
+    for (int g0 = 0; g0 < tiles_m; g0 += 4)
+      for (int tn = 0; tn < tiles_n; ++tn)
+        for (int tm = g0; tm < std::min(g0 + 4, tiles_m); ++tm) {
+          if (sym && tm > tn) continue;
+          list.push_back({((uint32_t)pi << 24) | ((uint32_t)tm << 12) | (uint32_t)tn, cost});
+          total += cost;
+        }
+  }
+  // One contiguous band of the list per queue (per XCD), cut at equal cost;
+  // inside a band the longest tiles come first: the XCD starts them first and
+  // fills in with the short ones (longest-processing-time order).
+  constexpr int nq = APEXW_GEMM_QUEUES;
+  std::vector<std::vector<Item>> band(nq);
+  int64_t seen = 0;
+  for (const Item& it : list) {
+    const int64_t mid2 = 2 * seen + it.cost;  // twice the item's midpoint
+    const int x = (int)std::min<int64_t>((mid2 * nq) / (2 * total), nq - 1);
+    band[x].push_back(it);
+    seen += it.cost;
+  }
+  int64_t pos = 0;
+  for (int x = 0; x < nq; ++x) {
+    std::stable_sort(band[x].begin(), band[x].end(), [](const Item& l, const Item& r) { return l.cost > r.cost; });
+    queue_offsets[x] = (int32_t)pos;
+    for (const Item& it : band[x]) items[pos++] = it.code;
+  }
+  queue_offsets[nq] = (int32_t)pos;
+  size_t longest = 0;
+  for (int x = 0; x < nq; ++x) longest = std::max(longest, band[x].size());
+  if ((int64_t)longest * nq > INT32_MAX) return APEXW_ERR_ARG;
+  *n_workgroups = (int32_t)(longest * nq);
+  *kind = kind0;
+  return APEXW_OK;
+}
+
+int apexw_gemm_nt_grouped(const apexw_gemm_problem* problems, const uint32_t* items, const int32_t* queue_offsets,
+                          int32_t n_workgroups, int32_t kind, void* stream) {
+  if (!problems || !items || !queue_offsets) return APEXW_ERR_ARG;
+  if (n_workgroups <= 0 || n_workgroups % APEXW_GEMM_QUEUES) return APEXW_ERR_ARG;
+  if (kind <= 0 || kind > 7 || !(kind & (APEXW_GEMM_OUT_C | APEXW_GEMM_OUT_CT))) return APEXW_ERR_ARG;
+  if (((uintptr_t)problems | (uintptr_t)items | (uintptr_t)queue_offsets) & 3u) return APEXW_ERR_ALIGN;
+  return apexw_launch_gemm_grouped(problems, items, queue_offsets, n_workgroups, kind, (hipStream_t)stream);
 }
 
 int64_t apexw_muon_workspace_floats(int64_t rows, int64_t cols) {

@@ -41,35 +41,55 @@ struct GemmArgs {
 APEXW_DEV float bf(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 APEXW_DEV uint16_t to_bf(float x) { return (uint16_t)f32_to_bf16_bits(x); }
 
-// C = alpha * A B^T + beta * E (bf16 in, fp32 accumulate, bf16 out, round to nearest even).
-// 256 threads = 4 waves in a 2 x 2 arrangement, each owning a 128 x 128 block of
-// the 256 x 256 tile as 4 x 4 MFMA 32x32x16 accumulators; K tiles of 64 are
+typedef uint16_t LdsTile[kBM * kBK];
+
+// global -> LDS copy of 16 bytes per lane (global_load_lds_dwordx4): lane L's
+// 16 bytes at gbase + voff land at LDS byte lds_base + 16 L.  Issued as inline
+// assembly so that the compiler does not track it as an LDS write: it would
+// otherwise make every later LDS read wait for it (it cannot tell the two
+// stage buffers apart), serialising each K tile's prefetch with its math.  The
+// kernel orders these copies itself: s_waitcnt vmcnt(0) and a barrier before a
+// stage is read, and a stage is refilled only after the barrier that ends its
+// last reads.
+// M0 is written only here in these kernels (nothing else in them reads it); the
+// clobber records that, and clang's note that it cannot preserve a reserved
+// register across the statement does not apply.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+APEXW_DEV void lds_copy16(uint32_t lds_base, uint32_t voff, const void* gbase) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :
+               : "s"(lds_base), "v"(voff), "s"(gbase)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// A workgroup-uniform pointer held in SGPRs (the asm operand above needs one;
+// a pointer loaded from a table is not known to be uniform by the compiler).
+APEXW_DEV const uint16_t* uniform_ptr(const uint16_t* p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const uint16_t*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
+APEXW_DEV uint32_t lds_address(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// One 256 x 256 output tile: O = alpha * A B^T + beta * E (bf16 in, fp32
+// accumulate, bf16 out, round to nearest even).  A and B point at the tile's
+// first row of each operand; Et, C and Ct at the tile's origin in their own
+// layouts.  256 threads = 4 waves in a 2 x 2 arrangement, each owning a
+// 128 x 128 block as 4 x 4 MFMA 32x32x16 accumulators; K tiles of 64 are
 // double-buffered in LDS and loaded straight from global memory into LDS.
-// Template flags select the epilogue: write O row-major (kC), transposed (kCt),
-// add beta * E (kAdd).
+// Template flags select the epilogue: write O row-major (kC), transposed (kCt,
+// skipped at run time when write_ct is false), add beta * E (kAdd).
 template <bool kC, bool kCt, bool kAdd>
-__global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(16))) uint16_t s_a[2][kBM * kBK];
-  __shared__ __attribute__((aligned(16))) uint16_t s_b[2][kBN * kBK];
-
-  const int tiles_m = g.m / kBM, tiles_n = g.n / kBN, tiles = tiles_m * tiles_n;
-  // Consecutive workgroups are dispatched round-robin over the 8 XCDs; give each
-  // XCD a contiguous range of tiles, ordered in groups of 4 tile rows, so the A
-  // and B panels a range touches stay in that XCD's L2.
-  const int per_xcd = (tiles + 7) / 8;
-  const int t = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
-  if (t >= tiles) return;
-  constexpr int kGroup = 4;
-  const int group = t / (kGroup * tiles_n), first_m = group * kGroup;
-  const int gm = min(tiles_m - first_m, kGroup);
-  const int in_group = t % (kGroup * tiles_n);
-  const int tm = first_m + in_group % gm, tn = in_group / gm;
-
-  // tile base pointers are uniform (SGPRs); per-lane offsets stay 32-bit
-  const int64_t batch = blockIdx.y;
-  const uint16_t* __restrict__ A = g.a + batch * g.sa + (int64_t)tm * kBM * g.lda;
-  const uint16_t* __restrict__ B = g.b + batch * g.sb + (int64_t)tn * kBN * g.ldb;
-
+APEXW_DEV void gemm_tile(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, int32_t lda, int32_t ldb,
+                         int32_t k, const uint16_t* __restrict__ Et, int32_t lde, uint16_t* __restrict__ C,
+                         int32_t ldc, uint16_t* __restrict__ Ct, int32_t ldct, bool write_ct, float alpha,
+                         float beta, LdsTile* s_a, LdsTile* s_b) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
@@ -82,19 +102,22 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmArgs g) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int row = 8 * (8 * wave + i) + (lane >> 3), chunk = (lane & 7) ^ (lane >> 3);
-    goff_a[i] = (uint32_t)(row * g.lda + chunk * 8) * 2u;
-    goff_b[i] = (uint32_t)(row * g.ldb + chunk * 8) * 2u;
+    goff_a[i] = (uint32_t)(row * lda + chunk * 8) * 2u;
+    goff_b[i] = (uint32_t)(row * ldb + chunk * 8) * 2u;
   }
+  // LDS byte address of this wave's first chunk in each stage (wave-uniform)
+  const uint32_t lds_a0 = __builtin_amdgcn_readfirstlane(lds_address(&s_a[0][8 * wave * 512]));
+  const uint32_t lds_b0 = __builtin_amdgcn_readfirstlane(lds_address(&s_b[0][8 * wave * 512]));
+  constexpr uint32_t kStage = sizeof(LdsTile), kChunk = 512 * sizeof(uint16_t);
+  const uint16_t* A_s = uniform_ptr(A);
+  const uint16_t* B_s = uniform_ptr(B);
   auto issue_loads = [&](int buf, int k0) {
-    const char* a0 = (const char*)(A + k0);
-    const char* b0 = (const char*)(B + k0);
+    const uint16_t* a0 = A_s + k0;
+    const uint16_t* b0 = B_s + k0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int q = 8 * wave + i;
-      __builtin_amdgcn_global_load_lds(APEXW_GLOBAL(const void, a0 + goff_a[i]),
-                                       (__attribute__((address_space(3))) void*)&s_a[buf][q * 512], 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(APEXW_GLOBAL(const void, b0 + goff_b[i]),
-                                       (__attribute__((address_space(3))) void*)&s_b[buf][q * 512], 16, 0, 0);
+      lds_copy16(lds_a0 + buf * kStage + i * kChunk, goff_a[i], a0);
+      lds_copy16(lds_b0 + buf * kStage + i * kChunk, goff_b[i], b0);
     }
   };
   // the loads write LDS asynchronously: wait for this wave's, then the barrier
@@ -131,7 +154,7 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmArgs g) {
   };
 #define APEXW_SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
 
-  const int k_tiles = g.k / kBK;
+  const int k_tiles = k / kBK;
   issue_loads(0, 0);
   loads_done();
   __syncthreads();
@@ -163,51 +186,124 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmArgs g) {
 
   // Epilogue.  Accumulator register r of lane l holds row 8 (r / 4) + 4 (l / 32) + r % 4,
   // column l % 32 of its 32 x 32 block: four consecutive rows of one column per group.
-  const int row0 = tm * kBM, col0 = tn * kBN;
-  const uint16_t* __restrict__ Et = kAdd ? g.et + batch * g.se + (int64_t)col0 * g.lde + row0 : nullptr;
-  uint16_t* __restrict__ C = kC ? g.c + batch * g.sc + (int64_t)row0 * g.ldc + col0 : nullptr;
-  uint16_t* __restrict__ Ct = kCt ? g.ct + batch * g.sct + (int64_t)col0 * g.ldct + row0 : nullptr;
-  const int lr = wm * 128 + (lane >> 5) * 4, lc = wn * 128 + (lane & 31);
-  // after the last barrier the operand tiles are dead: 4 x 32 KB of LDS for the row-major staging
+  // After the last barrier the operand tiles are dead: each wave stages its
+  // 128 x 128 block of O in its own 32 KB of LDS, then writes it row by row to C
+  // and column by column to Ct, both as 16-byte stores along output rows.  The
+  // stage keeps 16-byte chunks XOR-swizzled by row / 8 so that the row reads
+  // (16 lanes per row) and the column reads (16 lanes down a column) each hit
+  // distinct banks.  A wave reads back only what it wrote itself, and LDS keeps
+  // one wave's accesses in order, so no barrier is needed.
   uint16_t* stage = (wave < 2 ? s_a[wave] : s_b[wave - 2]);
+  auto swz = [](int r, int c) { return r * 128 + ((((c >> 3) ^ (r >> 3)) & 15) << 3) + (c & 7); };
+  const int il0 = (lane >> 5) * 4, jl0 = lane & 31;           // within the wave's block
+  const int gi0 = wm * 128 + il0, gj0 = wn * 128 + jl0;       // within the tile
 #pragma unroll
   for (int a = 0; a < 4; ++a) {
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-      const int j = lc + b * 32;
+      const int jl = jl0 + b * 32;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int i0 = lr + a * 32 + q * 8;
+        const int il = il0 + a * 32 + q * 8;
         float v[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] = g.alpha * acc[a][b][q * 4 + r];
+        for (int r = 0; r < 4; ++r) v[r] = alpha * acc[a][b][q * 4 + r];
         if constexpr (kAdd) {
-          const u16x4 e = *APEXW_GLOBAL(const u16x4, Et + (uint32_t)(j * g.lde + i0));
+          const u16x4 e = *APEXW_GLOBAL(const u16x4, Et + (uint32_t)((gj0 + b * 32) * lde + gi0 + a * 32 + q * 8));
 #pragma unroll
-          for (int r = 0; r < 4; ++r) v[r] = fmaf(g.beta, bf(e[r]), v[r]);
+          for (int r = 0; r < 4; ++r) v[r] = fmaf(beta, bf(e[r]), v[r]);
         }
-        u16x4 o;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) o[r] = to_bf(v[r]);
-        if constexpr (kCt) *APEXW_GLOBAL(u16x4, Ct + (uint32_t)(j * g.ldct + i0)) = o;
-        if constexpr (kC) {
-          // stage the wave's 128 x 128 block row-major in its own 32 KB of LDS
-#pragma unroll
-          for (int r = 0; r < 4; ++r) stage[(i0 - wm * 128 + r) * 128 + (j - wn * 128)] = o[r];
-        }
+        for (int r = 0; r < 4; ++r) stage[swz(il + r, jl)] = to_bf(v[r]);
       }
     }
   }
   if constexpr (kC) {
-    // each wave reads back only what it wrote: LDS keeps one wave's accesses in order
-    uint16_t* __restrict__ Cw = C + (int64_t)(wm * 128) * g.ldc + wn * 128;
+    uint16_t* __restrict__ Cw = C + (int64_t)(wm * 128) * ldc + wn * 128;
 #pragma unroll 4
     for (int it = 0; it < 32; ++it) {
       const int c = it * 64 + lane, r = c >> 4, c16 = c & 15;
-      const u32x4 v = *(const u32x4*)&stage[r * 128 + c16 * 8];
-      __builtin_nontemporal_store(v, APEXW_GLOBAL(u32x4, Cw + (uint32_t)(r * g.ldc + c16 * 8)));
+      const u32x4 v = *(const u32x4*)&stage[swz(r, c16 * 8)];
+      __builtin_nontemporal_store(v, APEXW_GLOBAL(u32x4, Cw + (uint32_t)(r * ldc + c16 * 8)));
     }
   }
+  if constexpr (kCt) {
+    if (write_ct) {
+      uint16_t* __restrict__ Ctw = Ct + (int64_t)(wn * 128) * ldct + wm * 128;
+#pragma unroll 2
+      for (int it = 0; it < 32; ++it) {
+        // Ct row jl (= column jl of the block), elements il .. il + 7
+        const int c = it * 64 + lane, jl = c >> 4, il = (c & 15) * 8;
+        u32x4 v;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          v[t] = (uint32_t)stage[swz(il + 2 * t, jl)] | ((uint32_t)stage[swz(il + 2 * t + 1, jl)] << 16);
+        *APEXW_GLOBAL(u32x4, Ctw + (uint32_t)(jl * ldct + il)) = v;
+      }
+    }
+  }
+}
+
+// Batched GEMM over one shape: one workgroup per output tile, blockIdx.y = batch entry.
+template <bool kC, bool kCt, bool kAdd>
+__global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmArgs g) {
+  __shared__ __attribute__((aligned(16))) LdsTile s_a[2];
+  __shared__ __attribute__((aligned(16))) LdsTile s_b[2];
+
+  const int tiles_m = g.m / kBM, tiles_n = g.n / kBN, tiles = tiles_m * tiles_n;
+  // Consecutive workgroups are dispatched round-robin over the 8 XCDs; give each
+  // XCD a contiguous range of tiles, ordered in groups of 4 tile rows, so the A
+  // and B panels a range touches stay in that XCD's L2.
+  const int per_xcd = (tiles + 7) / 8;
+  const int t = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+  if (t >= tiles) return;
+  constexpr int kGroup = 4;
+  const int group = t / (kGroup * tiles_n), first_m = group * kGroup;
+  const int gm = min(tiles_m - first_m, kGroup);
+  const int in_group = t % (kGroup * tiles_n);
+  const int tm = first_m + in_group % gm, tn = in_group / gm;
+
+  const int64_t batch = blockIdx.y;
+  const int64_t row0 = (int64_t)tm * kBM, col0 = (int64_t)tn * kBN;
+  gemm_tile<kC, kCt, kAdd>(g.a + batch * g.sa + row0 * g.lda, g.b + batch * g.sb + col0 * g.ldb, g.lda, g.ldb, g.k,
+                           kAdd ? g.et + batch * g.se + col0 * g.lde + row0 : nullptr, g.lde,
+                           kC ? g.c + batch * g.sc + row0 * g.ldc + col0 : nullptr, g.ldc,
+                           kCt ? g.ct + batch * g.sct + col0 * g.ldct + row0 : nullptr, g.ldct, true, g.alpha, g.beta,
+                           s_a, s_b);
+}
+
+// Grouped GEMM: every problem of a launch (different shapes, K and operands)
+// in one grid, one workgroup per output tile.  The tiles are split into
+// kQueues queues, one per XCD: workgroups are dispatched round-robin over the
+// 8 XCDs, so workgroup b runs on XCD b % 8 and computes tile b / 8 of queue
+// b % 8.  Each XCD thus works through its own queue in order, a new workgroup
+// starting on whichever of its CUs frees first; a queue is one contiguous band
+// of tiles in locality order, longest first.  Workgroups past the end of their
+// queue exit at once.  An item packs (problem << 24) | (tile row << 12) | tile
+// column.  A symmetric problem (APEXW_GEMM_SYM) lists only tiles with
+// row <= column and mirrors each off-diagonal tile through the transposed
+// store (ct == c).
+constexpr int kQueues = APEXW_GEMM_QUEUES;
+
+template <bool kC, bool kCt, bool kAdd>
+__global__ __launch_bounds__(256, 1) void gemm_nt_grouped_kernel(const apexw_gemm_problem* __restrict__ probs,
+                                                                 const uint32_t* __restrict__ items,
+                                                                 const int32_t* __restrict__ queue_offsets) {
+  __shared__ __attribute__((aligned(16))) LdsTile s_a[2];
+  __shared__ __attribute__((aligned(16))) LdsTile s_b[2];
+  const int q = (int)(blockIdx.x % kQueues), i = (int)(blockIdx.x / kQueues);
+  const int begin = queue_offsets[q];
+  if (i >= queue_offsets[q + 1] - begin) return;
+  const uint32_t code = items[begin + i];
+  const apexw_gemm_problem& p = probs[code >> 24];
+  const int tm = (int)((code >> 12) & 0xfffu), tn = (int)(code & 0xfffu);
+  const int64_t row0 = (int64_t)tm * kBM, col0 = (int64_t)tn * kBN;
+  const bool mirror = !(p.flags & APEXW_GEMM_SYM) || tm != tn;
+  gemm_tile<kC, kCt, kAdd>((const uint16_t*)p.a + row0 * p.lda, (const uint16_t*)p.b + col0 * p.ldb, p.lda, p.ldb,
+                           p.k, kAdd ? (const uint16_t*)p.et + col0 * p.lde + row0 : nullptr, p.lde,
+                           kC ? (uint16_t*)p.c + row0 * p.ldc + col0 : nullptr, p.ldc,
+                           kCt ? (uint16_t*)p.ct + col0 * p.ldct + row0 : nullptr, p.ldct, mirror, p.alpha, p.beta,
+                           s_a, s_b);
 }
 
 // ---------------------------------------------------------------------------
@@ -370,6 +466,34 @@ int apexw_launch_gemm_nt(const uint16_t* a, const uint16_t* b, const uint16_t* e
   } else {
     if (add) hipLaunchKernelGGL((gemm_nt_kernel<false, true, true>), grid, dim3(256), 0, stream, g);
     else hipLaunchKernelGGL((gemm_nt_kernel<false, true, false>), grid, dim3(256), 0, stream, g);
+  }
+  return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
+}
+
+int apexw_launch_gemm_grouped(const apexw_gemm_problem* probs, const uint32_t* items, const int32_t* offsets,
+                              int32_t n_wg, int32_t kind, hipStream_t stream) {
+  const dim3 grid(n_wg), block(256);
+  switch (kind) {
+    case APEXW_GEMM_OUT_C:
+      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, false, false>), grid, block, 0, stream, probs, items, offsets);
+      break;
+    case APEXW_GEMM_OUT_C | APEXW_GEMM_ADD:
+      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, false, true>), grid, block, 0, stream, probs, items, offsets);
+      break;
+    case APEXW_GEMM_OUT_CT:
+      hipLaunchKernelGGL((gemm_nt_grouped_kernel<false, true, false>), grid, block, 0, stream, probs, items, offsets);
+      break;
+    case APEXW_GEMM_OUT_CT | APEXW_GEMM_ADD:
+      hipLaunchKernelGGL((gemm_nt_grouped_kernel<false, true, true>), grid, block, 0, stream, probs, items, offsets);
+      break;
+    case APEXW_GEMM_OUT_C | APEXW_GEMM_OUT_CT:
+      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, true, false>), grid, block, 0, stream, probs, items, offsets);
+      break;
+    case APEXW_GEMM_OUT_C | APEXW_GEMM_OUT_CT | APEXW_GEMM_ADD:
+      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, true, true>), grid, block, 0, stream, probs, items, offsets);
+      break;
+    default:
+      return APEXW_ERR_ARG;
   }
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }

@@ -7,9 +7,10 @@ handling.  The step runs through libapexw_hip.so:
 
 * ``apexw_muon_prepare``: fp32 momentum update, the bf16 work matrix normalised
   by its Frobenius norm, written in both orientations;
-* ``newton_schulz``: per iteration three bf16 MFMA GEMMs
-  (``A = X X^T``; ``B = c A A + b A``; ``X = B X + a X``) through
-  ``apexw_gemm_nt_bf16``, batched over same-shape matrices;
+* ``NSPlan``: per iteration three bf16 MFMA GEMMs
+  (``A = X X^T``; ``B = c A A + b A``; ``X = B X + a X``), each one grouped
+  launch (``apexw_gemm_nt_grouped``) over every Muon matrix of the step; the
+  two symmetric products compute only the tiles on and above the diagonal;
 * ``apexw_muon_apply``: decoupled weight decay and ``p -= lr * scale * U``.
 
 Like the reference on a bf16-capable GPU, the Newton-Schulz work dtype is
@@ -21,6 +22,7 @@ coefficients and scale_mode="rms" raise ``NotImplementedError``.
 import math
 from collections import defaultdict
 
+import numpy as np
 import torch
 from torch.optim.optimizer import Optimizer
 
@@ -59,7 +61,7 @@ class NSWorkspace:
     """
 
     def __init__(self, m, n, batch, device):
-        self.m, self.n, self.batch = m, n, batch
+        self.m, self.n, self.batch, self.device = m, n, batch, device
         t = _lib.GEMM_TILE
         self.mp, self.np_ = _pad(m, t), _pad(n, t)
         z = lambda *s: torch.zeros(*s, dtype=torch.bfloat16, device=device)  # noqa: E731
@@ -72,30 +74,73 @@ class NSWorkspace:
         self.partial = torch.empty(batch, max(per, 1), dtype=torch.float32, device=device)
 
 
-def _gemm(lib, stream, a, b, et, c, ct, m, n, k, lda, ldb, lde, ldc, ldct, batch, sa, sb, se, sc, sct, alpha, beta):
-    st = lib.apexw_gemm_nt_bf16(a, b, et, c, ct, m, n, k, lda, ldb, lde, ldc, ldct, batch, sa, sb, se, sc, sct,
-                                alpha, beta, stream)
-    _lib.check(st, "apexw_gemm_nt_bf16")
+def _ns_problems(ws, phase, cur, out):
+    """Append the GEMM problems of one Newton-Schulz product for every matrix of ws.
+
+    phase 0: A = X X^T (symmetric); phase 1: B = c A A + b A (symmetric);
+    phase 2: X' = B X + a X, read from X^T rows and written in both layouts.
+    cur is the ping-pong slot holding the current X.
+    """
+    mp, np_ = ws.mp, ws.np_
+    for e in range(ws.batch):
+        x, xt = ws.x[cur][e].data_ptr(), ws.xt[cur][e].data_ptr()
+        a, b = ws.a[e].data_ptr(), ws.b[e].data_ptr()
+        if phase == 0:
+            out.append((x, x, 0, a, a, mp, mp, np_, np_, np_, 0, mp, mp, 1.0, 0.0, _lib.GEMM_SYM, 0))
+        elif phase == 1:
+            out.append((a, a, a, b, b, mp, mp, mp, mp, mp, mp, mp, mp, NS_C, NS_B, _lib.GEMM_SYM, 0))
+        else:
+            nx, nxt = ws.x[cur ^ 1][e].data_ptr(), ws.xt[cur ^ 1][e].data_ptr()
+            out.append((b, xt, xt, nx, nxt, mp, np_, mp, mp, mp, mp, np_, mp, 1.0, NS_A, 0, 0))
 
 
-def newton_schulz(ws, steps, stream):
-    """Run `steps` quintic iterations on ws.x[0] / ws.xt[0]; returns the index of the result buffer."""
-    lib = _lib.load()
-    mp, np_, bt = ws.mp, ws.np_, ws.batch
-    sx, sa = mp * np_, mp * mp
-    cur = 0
-    for _ in range(steps):
-        x, xt = ws.x[cur].data_ptr(), ws.xt[cur].data_ptr()
-        nx, nxt = ws.x[cur ^ 1].data_ptr(), ws.xt[cur ^ 1].data_ptr()
-        a, b = ws.a.data_ptr(), ws.b.data_ptr()
-        # A = X X^T   (symmetric: stored through the transposed output)
-        _gemm(lib, stream, x, x, None, None, a, mp, mp, np_, np_, np_, 0, 0, mp, bt, sx, sx, 0, 0, sa, 1.0, 0.0)
-        # B = c A A + b A
-        _gemm(lib, stream, a, a, a, None, b, mp, mp, mp, mp, mp, mp, 0, mp, bt, sa, sa, sa, 0, sa, NS_C, NS_B)
-        # X' = B X + a X  with X read as X^T rows; written in both orientations
-        _gemm(lib, stream, b, xt, xt, nx, nxt, mp, np_, mp, mp, mp, mp, np_, mp, bt, sa, sx, sx, sx, sx, 1.0, NS_A)
-        cur ^= 1
-    return cur
+class NSPlan:
+    """Newton-Schulz for every Muon matrix of a step on one device, as grouped launches.
+
+    Iteration i runs three launches (A, B, X') over all workspaces that still
+    have iterations left; each launch covers every matrix of every shape, so the
+    GPU is filled by the whole step's work rather than one shape at a time.  The
+    problem tables and tile schedules are built once and kept on the device
+    (they hold the workspaces' addresses, which never change).
+    """
+
+    def __init__(self, wss, steps, device):
+        # algorithmic FLOPs (the reference's three matmuls, unpadded) and the
+        # FLOPs the kernels execute (padded; upper-triangle tiles of A and B)
+        self.flops = sum(ws.batch * s * (4 * ws.m * ws.m * ws.n + 2 * ws.m ** 3) for ws, s in zip(wss, steps))
+        self.exec_flops = 0
+        for ws, s in zip(wss, steps):
+            t = ws.mp // _lib.GEMM_TILE
+            tri = (t + 1) / (2 * t)
+            self.exec_flops += ws.batch * s * (tri * (2 * ws.mp ** 2 * ws.np_ + 2 * ws.mp ** 3) + 2 * ws.mp ** 2 * ws.np_)
+        built = {}
+        self.iters = []
+        for i in range(max(steps, default=0)):
+            active = tuple(j for j, s in enumerate(steps) if s > i)
+            key = (active, i % 2)
+            if key not in built:
+                built[key] = [self._launches([wss[j] for j in active], phase, i % 2, device) for phase in range(3)]
+            self.iters.append(built[key])
+
+    def _launches(self, wss, phase, cur, device):
+        rows = []
+        for ws in wss:
+            _ns_problems(ws, phase, cur, rows)
+        out = []
+        for c0 in range(0, len(rows), _lib.GEMM_MAX_PROBLEMS):
+            probs = np.array(rows[c0:c0 + _lib.GEMM_MAX_PROBLEMS], dtype=_lib.GEMM_PROBLEM_DTYPE)
+            items, offsets, n_wg, kind = _lib.gemm_schedule(probs)
+            to_dev = lambda a: torch.from_numpy(a.view(np.uint8).copy()).to(device)  # noqa: E731
+            out.append((to_dev(probs), to_dev(items), to_dev(offsets), n_wg, kind))
+        return out
+
+    def run(self, stream):
+        lib = _lib.load()
+        for phases in self.iters:
+            for launches in phases:
+                for probs, items, offsets, n_wg, kind in launches:
+                    _lib.check(lib.apexw_gemm_nt_grouped(probs.data_ptr(), items.data_ptr(), offsets.data_ptr(),
+                                                         n_wg, kind, stream), "apexw_gemm_nt_grouped")
 
 
 class ApexMuon(Optimizer):
@@ -135,6 +180,7 @@ class ApexMuon(Optimizer):
                         fused=fused, capturable=capturable, compiled=compiled)
         super().__init__(params, defaults)
         self._ws = {}
+        self._ns_plans = {}
 
     # ------------------------------------------------------------------ state
     def _init_param_state(self, p):
@@ -167,12 +213,20 @@ class ApexMuon(Optimizer):
             return math.sqrt(max(m_dim, n_dim)) * 0.2
         return 1.0
 
-    def _workspace(self, m, n, batch, device):
-        key = (m, n, batch, device)
+    def _workspace(self, key, m, n, batch, device):
+        # one workspace per (param group, shape): all of a step's work matrices
+        # are live together while the grouped Newton-Schulz runs
         ws = self._ws.get(key)
         if ws is None:
             ws = self._ws[key] = NSWorkspace(m, n, batch, device)
         return ws
+
+    def _ns_plan(self, jobs, device):
+        key = (device, tuple((id(j["ws"]), j["steps"]) for j in jobs))
+        plan = self._ns_plans.get(key)
+        if plan is None:
+            plan = self._ns_plans[key] = NSPlan([j["ws"] for j in jobs], [j["steps"] for j in jobs], device)
+        return plan
 
     @torch.no_grad()
     def step(self, closure=None):
@@ -187,7 +241,8 @@ class ApexMuon(Optimizer):
                 return loss
             if grad_scale is not None:
                 raise NotImplementedError("ApexMuon: GradScaler grad_scale hand-off is not supported; unscale first")
-            for group in self.param_groups:
+            jobs = []
+            for gi, group in enumerate(self.param_groups):
                 active = [p for p in group["params"] if p.grad is not None]
                 if not active:
                     continue
@@ -199,49 +254,68 @@ class ApexMuon(Optimizer):
                         raise NotImplementedError(
                             "ApexMuon: parameters with fewer than 16 rows or columns (the reference's coordinate-wise "
                             "fallback) are not supported; route them to ApexW (HybridApexW does)")
+                    if not p.is_contiguous():
+                        raise NotImplementedError("ApexMuon: parameters must be contiguous")
+                    if p.grad.dtype != p.dtype:
+                        raise NotImplementedError("ApexMuon: gradient dtype must match the parameter dtype")
                 shapes = defaultdict(list)
                 for p in active:
                     shapes[tuple(p.shape)].append(p)
                 for shape, plist in shapes.items():
                     # the reference batches same-shape matrices on the GPU (apexw/muon.py:593-615)
-                    self._step_matrices(plist, group, batched=len(plist) > 1)
+                    jobs.append(self._prepare(gi, shape, plist, group))
+            # Newton-Schulz of every matrix, grouped per device; matrices are
+            # independent, so running all momenta first and all updates last
+            # gives each parameter the result of the reference's per-shape loop
+            by_dev = defaultdict(list)
+            for j in jobs:
+                by_dev[j["ws"].device].append(j)
+            for dev, djobs in by_dev.items():
+                self._ns_plan(djobs, dev).run(torch.cuda.current_stream(dev).cuda_stream)
+            for j in jobs:
+                self._apply(j)
         finally:
             self.grad_scale = None
             self.found_inf = None
         return loss
 
-    def _step_matrices(self, plist, group, batched):
+    def _prepare(self, gi, shape, plist, group):
+        """Momentum update and normalised bf16 work matrix (both layouts) of one same-shape batch."""
         lib = _lib.load()
         p0 = plist[0]
         rows, cols = p0.shape[0], p0.numel() // p0.shape[0]
         m, n = min(rows, cols), max(rows, cols)
-        tall = rows > cols
         dev = p0.device
         stream = torch.cuda.current_stream(dev).cuda_stream
-        ws = self._workspace(m, n, len(plist), dev)
+        ws = self._workspace((gi, shape, len(plist), dev), m, n, len(plist), dev)
         mu = float(group["momentum"])
         for i, p in enumerate(plist):
             st = self._init_param_state(p)
             st["step"] += 1
             g = p.grad if p.grad.is_contiguous() else p.grad.contiguous()
-            if g.dtype != p.dtype:
-                raise NotImplementedError("ApexMuon: gradient dtype must match the parameter dtype")
             _lib.check(lib.apexw_muon_prepare(
                 st["momentum"].data_ptr(), g.data_ptr(), _dtype_code(g.dtype), rows, cols, mu, 1.0 - mu,
                 int(bool(group["nesterov"])), NS_EPS, ws.x[0][i].data_ptr(), ws.xt[0][i].data_ptr(), ws.np_, ws.mp,
                 ws.partial[i].data_ptr(), stream), "apexw_muon_prepare")
-        res = newton_schulz(ws, int(group["ns_steps"]), stream)
+        return {"plist": plist, "group": group, "ws": ws, "rows": rows, "cols": cols,
+                "steps": int(group["ns_steps"]), "batched": len(plist) > 1}
+
+    def _apply(self, job):
+        """Decoupled decay and the scaled orthogonalised update (apexw/muon.py:852-858)."""
+        lib = _lib.load()
+        plist, group, ws, rows, cols = job["plist"], job["group"], job["ws"], job["rows"], job["cols"]
+        p0 = plist[0]
+        stream = torch.cuda.current_stream(p0.device).cuda_stream
+        res = job["steps"] % 2                   # ping-pong slot of the Newton-Schulz result
         lr, wd = float(group["lr"]), float(group["weight_decay"])
         scale = self._scale(group["scale_mode"], rows, cols)
         wd_factor, neg_lr = 1.0 - lr * wd, -lr * scale
-        if batched:
+        if job["batched"]:
             # torch._foreach_mul_ / _foreach_add_ over same-dtype lists see the scalars in p's dtype
             wd_factor, neg_lr = _round_to(p0.dtype, wd_factor), _round_to(p0.dtype, neg_lr)
         # U in p's layout: the work matrix when wide, its transpose when tall
-        u_buf, ldu = (ws.xt[res], ws.mp) if tall else (ws.x[res], ws.np_)
+        u_buf, ldu = (ws.xt[res], ws.mp) if rows > cols else (ws.x[res], ws.np_)
         for i, p in enumerate(plist):
-            if not p.is_contiguous():
-                raise NotImplementedError("ApexMuon: parameters must be contiguous")
             _lib.check(lib.apexw_muon_apply(p.data_ptr(), _dtype_code(p.dtype), u_buf[i].data_ptr(), rows, cols, ldu,
                                             wd_factor, int(wd != 0.0), neg_lr, stream), "apexw_muon_apply")
 

@@ -21,6 +21,8 @@
  *                           (apexw/optimizer.py:242-256: _foreach_norm + vector_norm)
  *   apexw_gemm_nt_bf16   <- the bf16 GEMMs of Newton-Schulz: X @ X.T and the two
  *                           torch.addmm / baddbmm calls (apexw/muon.py:102-108, :187-211)
+ *   apexw_gemm_nt_grouped <- the same GEMMs for every Muon matrix of a step in one
+ *                           launch (per-shape loop of apexw/muon.py:593-615)
  *   apexw_muon_prepare   <- ApexMuon momentum update and the work-matrix cast /
  *                           normalisation / transpose (apexw/muon.py:763-792, :163-175, :190-200)
  *   apexw_muon_apply     <- the decoupled decay and scaled update of ApexMuon
@@ -35,7 +37,7 @@
 extern "C" {
 #endif
 
-#define APEXW_ABI_VERSION 2
+#define APEXW_ABI_VERSION 3
 
 /* status codes */
 enum apexw_status {
@@ -180,6 +182,7 @@ int apexw_grad_clip_coef(const apexw_tensor* tensors, int32_t n_tensors,
 
 #define APEXW_GEMM_TILE 256   /* M and N multiple of this */
 #define APEXW_GEMM_KTILE 64   /* K multiple of this */
+#define APEXW_GEMM_MAX_LD (1 << 22)   /* leading dimensions, elements */
 
 /*
  * Batched bf16 "NT" GEMM on the matrix cores (fp32 accumulation, bf16 output
@@ -190,13 +193,76 @@ int apexw_grad_clip_coef(const apexw_tensor* tensors, int32_t n_tensors,
  * row-major to c ([m x n], ldc) and/or transposed to ct ([n x m], ldct); at
  * least one of them.  m, n multiple of APEXW_GEMM_TILE, k of APEXW_GEMM_KTILE,
  * pointers 16-byte aligned, leading dimensions and batch strides multiples of 8
- * elements.  Outputs must not alias inputs.
+ * elements and at most APEXW_GEMM_MAX_LD.  Outputs must not alias inputs.
  */
 int apexw_gemm_nt_bf16(const void* a, const void* b, const void* et, void* c, void* ct,
                        int32_t m, int32_t n, int32_t k, int32_t lda, int32_t ldb, int32_t lde,
                        int32_t ldc, int32_t ldct, int32_t batch,
                        int64_t stride_a, int64_t stride_b, int64_t stride_e, int64_t stride_c,
                        int64_t stride_ct, float alpha, float beta, void* stream);
+
+/*
+ * Grouped launch: the same product for many matrices of different shapes in one
+ * persistent launch (one workgroup per CU), replacing the per-shape batched
+ * calls of ApexMuon._step_batched / _step_single (apexw/muon.py:593-615,
+ * :187-211).  Each problem is one "NT" product with the operand conventions of
+ * apexw_gemm_nt_bf16 (a single batch entry).  All problems of a launch write the
+ * same outputs (c and/or ct) and either all add beta * E or none does.
+ */
+typedef struct apexw_gemm_problem {
+  const void* a;       /* [m x k] bf16, lda */
+  const void* b;       /* [n x k] bf16, ldb */
+  const void* et;      /* E transposed, [n x m], lde; NULL when beta == 0 */
+  void* c;             /* [m x n] output, ldc; NULL = not written */
+  void* ct;            /* [n x m] transposed output, ldct; NULL = not written */
+  int32_t m, n, k;
+  int32_t lda, ldb, lde, ldc, ldct;
+  float alpha, beta;
+  uint32_t flags;      /* APEXW_GEMM_SYM */
+  uint32_t reserved;   /* 0 */
+} apexw_gemm_problem;  /* 88 bytes */
+
+/* The product is symmetric (A A^T, or c A A + b A with A symmetric): m == n,
+ * a == b, and ct == c with ldct == ldc.  Only tiles on and above the diagonal
+ * are computed; each off-diagonal tile is also stored mirrored, so c receives
+ * the whole matrix.  E, when added, must be symmetric. */
+#define APEXW_GEMM_SYM 1u
+
+/* epilogue kinds of a grouped launch (bit mask) */
+#define APEXW_GEMM_OUT_C 1   /* row-major output */
+#define APEXW_GEMM_OUT_CT 2  /* transposed output */
+#define APEXW_GEMM_ADD 4     /* beta * E added */
+
+/* Tile queues of a grouped launch: one per XCD of MI355X. */
+#define APEXW_GEMM_QUEUES 8
+
+/* Output tiles (work items) of a grouped launch, or minus an apexw_status when
+ * a problem is invalid. */
+int64_t apexw_gemm_grouped_items(const apexw_gemm_problem* problems, int32_t n_problems);
+
+/*
+ * Host-side: validate the problems (a host copy of the table that will be
+ * uploaded) and build the tile queues: items[n_items] (n_items from
+ * apexw_gemm_grouped_items) and queue_offsets[APEXW_GEMM_QUEUES + 1]; queue q
+ * is items[queue_offsets[q] .. queue_offsets[q + 1]).  The tiles, in locality
+ * order (bands of 4 tile rows), are cut into one contiguous band per queue of
+ * equal K-cost, longest tiles first within a band.  *n_workgroups receives the
+ * grid size of the launch (APEXW_GEMM_QUEUES x the longest queue) and *kind the
+ * epilogue kind.  At most 256 problems, 4096 tiles per side.
+ */
+int apexw_gemm_grouped_schedule(const apexw_gemm_problem* problems, int32_t n_problems, uint32_t* items,
+                                int64_t n_items, int32_t* queue_offsets, int32_t* n_workgroups, int32_t* kind);
+
+/*
+ * Run a grouped launch: one workgroup per tile; workgroup b computes tile
+ * b / APEXW_GEMM_QUEUES of queue b % APEXW_GEMM_QUEUES (workgroups are
+ * dispatched round-robin over the XCDs, so each XCD works through one queue).
+ * problems, items and queue_offsets are device copies of the arrays validated
+ * and built by apexw_gemm_grouped_schedule, n_workgroups and kind its outputs;
+ * like the tensor tables of the step, they are trusted as built.
+ */
+int apexw_gemm_nt_grouped(const apexw_gemm_problem* problems, const uint32_t* items, const int32_t* queue_offsets,
+                          int32_t n_workgroups, int32_t kind, void* stream);
 
 /* fp32 workspace (floats) apexw_muon_prepare needs for a [rows x cols] matrix. */
 int64_t apexw_muon_workspace_floats(int64_t rows, int64_t cols);

@@ -1,0 +1,145 @@
+"""CPU: validation and tile schedule of the grouped Newton-Schulz GEMM launch.
+
+apexw_gemm_grouped_items / apexw_gemm_grouped_schedule are host functions of
+the library (no GPU): they check every problem of a grouped launch and assign
+its output tiles to the persistent workgroups.  The pointers below are
+aligned stand-ins; nothing is dereferenced.
+"""
+
+import numpy as np
+import pytest
+
+from apexw_amd import _lib
+
+T = _lib.GEMM_TILE
+NS_A, NS_B, NS_C = 3.4445, -4.7750, 2.0315
+
+
+def _prob(a, b, et, c, ct, m, n, k, lda, ldb, lde, ldc, ldct, alpha=1.0, beta=0.0, flags=0):
+    return (a, b, et, c, ct, m, n, k, lda, ldb, lde, ldc, ldct, alpha, beta, flags, 0)
+
+
+def _ns_problems(m, n, batch, base):
+    """The three Newton-Schulz products of `batch` m x n work matrices (m <= n)."""
+    xx, aa, bx = [], [], []
+    for e in range(batch):
+        x, xt, a, b, nx, nxt = (base + (6 * e + i) * (1 << 32) for i in range(6))
+        xx.append(_prob(x, x, 0, a, a, m, m, n, n, n, 0, m, m, flags=_lib.GEMM_SYM))
+        aa.append(_prob(a, a, a, b, b, m, m, m, m, m, m, m, m, NS_C, NS_B, _lib.GEMM_SYM))
+        bx.append(_prob(b, xt, xt, nx, nxt, m, n, m, m, m, m, n, m, 1.0, NS_A))
+    return xx, aa, bx
+
+
+def _c5_phases():
+    """Llama-3-8B layer Muon matrices: q, o (4096^2, batched) and gate/up (+ down) at 4096 x 14336."""
+    q = _ns_problems(4096, 4096, 2, 1 << 40)
+    gu = _ns_problems(4096, 14336, 2, 2 << 40)
+    d = _ns_problems(4096, 14336, 1, 3 << 40)
+    return [q[i] + gu[i] + d[i] for i in range(3)]
+
+
+def _decode(items):
+    return items >> 24, (items >> 12) & 0xFFF, items & 0xFFF
+
+
+def _expected_tiles(probs):
+    out = set()
+    for pi, p in enumerate(probs):
+        m, n, sym = p[5], p[6], p[15] & _lib.GEMM_SYM
+        for tm in range(m // T):
+            for tn in range(n // T):
+                if not sym or tm <= tn:
+                    out.add((pi, tm, tn))
+    return out
+
+
+@pytest.mark.parametrize("phase,kind", [(0, _lib.GEMM_OUT_C | _lib.GEMM_OUT_CT),
+                                        (1, _lib.GEMM_OUT_C | _lib.GEMM_OUT_CT | _lib.GEMM_ADD),
+                                        (2, _lib.GEMM_OUT_C | _lib.GEMM_OUT_CT | _lib.GEMM_ADD)])
+def test_schedule_covers_every_tile_once_in_balanced_bands(phase, kind):
+    probs = _c5_phases()[phase]
+    items, offsets, n_wg, got_kind = _lib.gemm_schedule(np.array(probs, dtype=_lib.GEMM_PROBLEM_DTYPE))
+    nq = _lib.GEMM_QUEUES
+    assert got_kind == kind and len(offsets) == nq + 1
+    assert n_wg == nq * np.diff(offsets).max()          # one workgroup per slot of the longest queue
+    assert offsets[0] == 0 and offsets[-1] == len(items) and np.all(np.diff(offsets) >= 0)
+    p, tm, tn = _decode(items.astype(np.int64))
+    got = list(zip(p.tolist(), tm.tolist(), tn.tolist()))
+    assert len(got) == len(set(got)), "a tile is scheduled twice"
+    assert set(got) == _expected_tiles(probs)
+    # symmetric problems: only tiles on or above the diagonal
+    sym = np.array([probs[i][15] & _lib.GEMM_SYM for i in p.tolist()], dtype=bool)
+    assert np.all(tm[sym] <= tn[sym])
+    # every queue holds an equal share of the cost (K tiles + 2 per epilogue
+    # stream: C, Ct, E), within two of the longest tiles
+    epi = 2 * bin(kind).count("1")
+    ktiles = np.array([probs[i][7] // _lib.GEMM_KTILE for i in p.tolist()])
+    loads = np.array([(ktiles[offsets[q]:offsets[q + 1]] + epi).sum() for q in range(nq)])
+    assert loads.max() - loads.min() <= 2 * (ktiles.max() + epi), loads
+    # each queue is one contiguous band of the locality order, longest tiles first
+    order = {t: i for i, t in enumerate(sorted(_expected_tiles(probs), key=lambda t: (t[0], t[1] // 4, t[2], t[1])))}
+    prev_end = -1
+    for q in range(nq):
+        seg = got[offsets[q]:offsets[q + 1]]
+        pos = sorted(order[t] for t in seg)
+        assert pos == list(range(pos[0], pos[-1] + 1)) and pos[0] > prev_end, f"queue {q} band"
+        prev_end = pos[-1]
+        kt = ktiles[offsets[q]:offsets[q + 1]]
+        assert np.all(np.diff(kt) <= 0), f"queue {q} is not longest-first"
+
+
+def test_schedule_symmetric_tile_count():
+    probs = _ns_problems(1024, 1024, 1, 1 << 40)[0]
+    items, offsets, _, _ = _lib.gemm_schedule(np.array(probs, dtype=_lib.GEMM_PROBLEM_DTYPE))
+    assert len(items) == 4 * 5 // 2                    # 4 x 4 tiles -> 10 on or above the diagonal
+
+
+def test_schedule_rejects_invalid_problems():
+    lib = _lib.load()
+    good = _ns_problems(512, 768, 1, 1 << 40)
+
+    def status(rows):
+        arr = np.array([tuple(r) for r in rows], dtype=_lib.GEMM_PROBLEM_DTYPE)
+        n = lib.apexw_gemm_grouped_items(arr.ctypes.data, len(arr))
+        return int(-n) if n < 0 else 0
+
+    for rows in good:
+        assert status(rows) == 0
+    xx, aa, bx = (list(map(list, g)) for g in good)
+    bad = [list(bx[0]) for _ in range(1)]
+    bad[0][5] = 500                                       # m not a tile multiple
+    assert status(bad) == 1
+    bad = [list(bx[0])]
+    bad[0][7] = 100                                       # k not a K-tile multiple
+    assert status(bad) == 1
+    bad = [list(xx[0])]
+    bad[0][1] += 1 << 20                                  # symmetric product with a != b
+    assert status(bad) == 1
+    bad = [list(xx[0])]
+    bad[0][4] += 1 << 20                                  # symmetric product with ct != c
+    assert status(bad) == 1
+    bad = [list(bx[0])]
+    bad[0][0] += 2                                        # misaligned operand
+    assert status(bad) == 4
+    bad = [list(bx[0])]
+    bad[0][8] = 512 + 4                                   # leading dimension not a multiple of 8
+    assert status(bad) == 4
+    bad = [list(bx[0])]
+    bad[0][8] = 256                                       # lda < k
+    assert status(bad) == 1
+    bad = [list(bx[0])]
+    bad[0][16] = 1                                        # reserved field
+    assert status(bad) == 1
+    bad = [list(bx[0])]
+    bad[0][2] = 0                                         # beta != 0 without an addend
+    assert status(bad) == 1
+    assert status([bx[0]] * 257) == 1                     # more problems than the item code holds
+    # a launch mixes no epilogue kinds
+    arr = np.array([tuple(xx[0]), tuple(bx[0])], dtype=_lib.GEMM_PROBLEM_DTYPE)
+    with pytest.raises(_lib.ApexwError):
+        _lib.gemm_schedule(arr)
+    # the launch itself rejects bad kinds and null tables before enqueueing anything
+    assert lib.apexw_gemm_nt_grouped(None, None, None, 16, 3, None) == 1
+    assert lib.apexw_gemm_nt_grouped(16, 16, 16, 16, 4, None) == 1     # no output in the kind
+    assert lib.apexw_gemm_nt_grouped(16, 16, 16, 12, 3, None) == 1     # grid not a multiple of the queues
+    assert lib.apexw_gemm_nt_grouped(16, 18, 16, 16, 3, None) == 4     # misaligned table

@@ -16,7 +16,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 def _declared_symbols():
     src = open(os.path.join(ROOT, "include", "apexw_hip.h")).read()
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
-    return sorted(set(re.findall(r"^\s*int\s+(apexw_\w+)\s*\(", src, flags=re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int32_t|int64_t)\s+(apexw_\w+)\s*\(", src, flags=re.M)))
 
 
 def test_library_exports_every_declared_symbol():
@@ -34,6 +34,7 @@ def test_struct_layouts_match_header():
     from apexw_amd import _lib
     assert ctypes.sizeof(_lib.Tensor) == 64 == _lib.TENSOR_DTYPE.itemsize
     assert ctypes.sizeof(_lib.HParams) == 88
+    assert _lib.GEMM_PROBLEM_DTYPE.itemsize == 88
 
 
 def test_check_tensor_rejects_bad_descriptors():

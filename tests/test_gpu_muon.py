@@ -19,7 +19,7 @@ import torch
 
 from golden.make_golden import _fingerprint, _grad, _param
 from golden_replay import load
-from oracle.muon import newton_schulz5
+from oracle.muon import NS_A, NS_B, NS_C, newton_schulz5
 
 pytestmark = pytest.mark.gpu
 
@@ -184,3 +184,90 @@ def test_hybrid_trajectory_matches_reference_vectors():
         else:
             err = (got - gold).abs() - (1e-6 * gold.abs() + 1e-9)
             assert float(err.max()) <= 0, i
+
+
+def _grouped(lib, rows):
+    """Schedule and run one grouped launch of host-built problem rows."""
+    from apexw_amd import _lib
+    probs = np.array(rows, dtype=_lib.GEMM_PROBLEM_DTYPE)
+    items, offsets, n_wg, kind = _lib.gemm_schedule(probs)
+    dev = lambda a: torch.from_numpy(a.view(np.uint8).copy()).cuda()  # noqa: E731
+    dp, di, do = dev(probs), dev(items), dev(offsets)
+    st = lib.apexw_gemm_nt_grouped(dp.data_ptr(), di.data_ptr(), do.data_ptr(), n_wg, kind,
+                                   torch.cuda.current_stream().cuda_stream)
+    assert st == 0
+    torch.cuda.synchronize()
+
+
+def _assert_gemm_close(got, ref):
+    err = (got.float().cpu() - ref).abs() - (2.0 ** -8 * ref.abs() + 1e-4 * ref.abs().max())
+    assert float(err.max()) <= 0, f"max excess {float(err.max()):.3e}"
+
+
+def test_grouped_gemm_symmetric_and_plain_products():
+    """One grouped launch per Newton-Schulz product over matrices of two shapes:
+    the symmetric products fill both triangles (bitwise symmetric), the plain
+    product writes both layouts."""
+    _need_gpu()
+    from apexw_amd import _lib
+    lib = _lib.load()
+    print("grouped gemm", flush=True)
+    g = torch.Generator().manual_seed(11)
+    shapes = [(256, 512), (512, 768), (512, 768)]
+    X = [(torch.randn(m, n, generator=g) / math.sqrt(n)).bfloat16() for m, n in shapes]
+    dX = [x.cuda() for x in X]
+    dXt = [x.t().contiguous().cuda() for x in X]
+    nan = lambda *s: torch.full(s, float("nan"), dtype=torch.bfloat16, device="cuda")  # noqa: E731
+    dA = [nan(m, m) for m, _ in shapes]
+    dB = [nan(m, m) for m, _ in shapes]
+    dC = [nan(m, n) for m, n in shapes]
+    dCt = [nan(n, m) for m, n in shapes]
+    SYM = _lib.GEMM_SYM
+    # A = X X^T
+    _grouped(lib, [(x.data_ptr(), x.data_ptr(), 0, a.data_ptr(), a.data_ptr(), m, m, n, n, n, 0, m, m, 1.0, 0.0,
+                    SYM, 0) for x, a, (m, n) in zip(dX, dA, shapes)])
+    for x, a in zip(X, dA):
+        ref = x.float() @ x.float().t()
+        _assert_gemm_close(a, ref)
+        assert torch.equal(a.cpu(), a.cpu().t())
+    # B = c A A + b A
+    _grouped(lib, [(a.data_ptr(), a.data_ptr(), a.data_ptr(), b.data_ptr(), b.data_ptr(), m, m, m, m, m, m, m, m,
+                    NS_C, NS_B, SYM, 0) for a, b, (m, _) in zip(dA, dB, shapes)])
+    for a, b in zip(dA, dB):
+        af = a.float().cpu()
+        _assert_gemm_close(b, NS_C * (af @ af) + NS_B * af)
+        assert torch.equal(b.cpu(), b.cpu().t())
+    # X' = B X + a X, written row-major and transposed
+    _grouped(lib, [(b.data_ptr(), xt.data_ptr(), xt.data_ptr(), c.data_ptr(), ct.data_ptr(), m, n, m, m, m, m, n, m,
+                    1.0, NS_A, 0, 0) for b, xt, c, ct, (m, n) in zip(dB, dXt, dC, dCt, shapes)])
+    for b, x, c, ct in zip(dB, X, dC, dCt):
+        _assert_gemm_close(c, b.float().cpu() @ x.float() + NS_A * x.float())
+        assert torch.equal(ct.cpu().t(), c.cpu())
+
+
+def test_muon_groups_with_different_ns_steps_and_many_matrices():
+    """Param groups with different ns_steps share the grouped launches (a group
+    leaves them when its iterations are done), and more than 256 matrices split
+    into several launches; each parameter matches its own fp32 oracle update."""
+    _need_gpu()
+    from apexw_amd.muon import ApexMuon
+    g = torch.Generator().manual_seed(21)
+    big = [(torch.randn(256, 384, generator=g) * 0.02) for _ in range(2)]
+    small = [(torch.randn(32, 48, generator=g) * 0.02) for _ in range(260)]
+    pb = [torch.nn.Parameter(h.cuda()) for h in big]
+    ps = [torch.nn.Parameter(h.cuda()) for h in small]
+    lr, mu = 0.02, 0.95
+    opt = ApexMuon([{"params": pb, "ns_steps": 5}, {"params": ps, "ns_steps": 3}], lr=lr, momentum=mu,
+                   weight_decay=0.0, scale_mode="none")
+    grads = [(torch.randn(h.shape, generator=g) * 1e-3) for h in big + small]
+    for p, gr in zip(pb + ps, grads):
+        p.grad = gr.cuda()
+    opt.step()
+    torch.cuda.synchronize()
+    checks = [(pb[0], big[0], grads[0], 5), (pb[1], big[1], grads[1], 5)]
+    checks += [(ps[i], small[i], grads[2 + i], 3) for i in (0, 1, 255, 256, 259)]
+    for p, h, gr, steps in checks:
+        U = newton_schulz5((1 - mu) * gr, steps, work_dtype=torch.float32)
+        d_ref = -lr * U
+        d_gpu = p.detach().float().cpu() - h
+        assert _rel_fro(d_gpu, d_ref) <= 0.03, (tuple(p.shape), steps, _rel_fro(d_gpu, d_ref))

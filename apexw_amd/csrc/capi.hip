@@ -215,42 +215,44 @@ int apexw_gemm_grouped_schedule(const apexw_gemm_problem* problems, int32_t n_pr
   for (int32_t i = 1; i < n_problems; ++i)
     if (gemm_problem_kind(problems[i]) != kind0) return APEXW_ERR_ARG;
 
-  // Work list in locality order: per problem, bands of 4 tile rows, each band
+  // Per problem, the tiles in locality order (bands of 4 tile rows, each band
   // column by column, so a run of consecutive tiles shares A row panels and B
-  // column panels.  Cost = K tiles + a few for the epilogue's traffic.
+  // column panels) are cut into one contiguous band per queue: all XCDs work on
+  // the same matrix at once and share its panels in the Infinity Cache.  A
+  // problem's T tiles give every queue T / 8 of them, and the T % 8 left over go
+  // to the next queues in rotation across problems, so queues stay within about
+  // one tile of each other.  Inside a queue the longest tiles come first: the
+  // XCD starts them first and fills in with the short ones.
   struct Item {
     uint32_t code;
     int64_t cost;
   };
-  std::vector<Item> list;
-  list.reserve((size_t)n_items);
+  constexpr int nq = APEXW_GEMM_QUEUES;
   const int64_t epi = 2 * (((kind0 & APEXW_GEMM_OUT_C) != 0) + ((kind0 & APEXW_GEMM_OUT_CT) != 0) +
                            ((kind0 & APEXW_GEMM_ADD) != 0));
-  int64_t total = 0;
+  std::vector<std::vector<Item>> band(nq);
+  std::vector<Item> tiles;
+  int rotate = 0;
   for (int32_t pi = 0; pi < n_problems; ++pi) {
     const apexw_gemm_problem& p = problems[pi];
     const int tiles_m = p.m / kTile, tiles_n = p.n / kTile;
     const bool sym = (p.flags & APEXW_GEMM_SYM) != 0;
     const int64_t cost = p.k / APEXW_GEMM_KTILE + epi;
+    tiles.clear();
     for (int g0 = 0; g0 < tiles_m; g0 += 4)
       for (int tn = 0; tn < tiles_n; ++tn)
         for (int tm = g0; tm < std::min(g0 + 4, tiles_m); ++tm) {
           if (sym && tm > tn) continue;
-          list.push_back({((uint32_t)pi << 24) | ((uint32_t)tm << 12) | (uint32_t)tn, cost});
-          total += cost;
+          tiles.push_back({((uint32_t)pi << 24) | ((uint32_t)tm << 12) | (uint32_t)tn, cost});
         }
-  }
-  // One contiguous band of the list per queue (per XCD), cut at equal cost;
-  // inside a band the longest tiles come first: the XCD starts them first and
-  // fills in with the short ones (longest-processing-time order).
-  constexpr int nq = APEXW_GEMM_QUEUES;
-  std::vector<std::vector<Item>> band(nq);
-  int64_t seen = 0;
-  for (const Item& it : list) {
-    const int64_t mid2 = 2 * seen + it.cost;  // twice the item's midpoint
-    const int x = (int)std::min<int64_t>((mid2 * nq) / (2 * total), nq - 1);
-    band[x].push_back(it);
-    seen += it.cost;
+    const size_t t = tiles.size(), base = t / nq, rem = t % nq;
+    size_t off = 0;
+    for (int q = 0; q < nq; ++q) {
+      const size_t take = base + (((size_t)((q - rotate + nq) % nq)) < rem ? 1 : 0);
+      band[q].insert(band[q].end(), tiles.begin() + off, tiles.begin() + off + take);
+      off += take;
+    }
+    rotate = (int)((rotate + rem) % nq);
   }
   int64_t pos = 0;
   for (int x = 0; x < nq; ++x) {

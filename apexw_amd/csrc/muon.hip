@@ -13,6 +13,8 @@
 // Work matrices are zero-padded to multiples of the 256 x 256 tile; zero rows
 // and columns stay zero through every product, so the kernel has no bounds
 // checks.
+#include <type_traits>
+
 #include "common.h"
 
 namespace {
@@ -21,11 +23,14 @@ typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(16))) float f32x16;
 typedef __attribute__((ext_vector_type(4))) uint16_t u16x4;
 
-constexpr int kBM = 256, kBN = 256, kBK = 64;
-// LDS tiles are [rows x 64] bf16 with 128-byte rows; the eight 16-byte chunks of
-// row r are stored XOR-swizzled (chunk c at slot c ^ (r & 7)), so the MFMA
-// fragment reads of 8 consecutive rows hit 8 distinct bank groups.
-APEXW_DEV int lds_off(int row, int chunk) { return row * kBK + ((chunk ^ (row & 7)) << 3); }
+constexpr int kBM = 256, kBN = 256;
+// K is staged through LDS 32 at a time in kStages rotating buffers of 32 KB
+// (A then B, each [256 rows x 32] bf16 with 64-byte rows): 160 KB, all of a
+// CU's LDS.  The four 16-byte chunks of row r are stored XOR-swizzled (chunk c
+// at slot c ^ ((r / 4) % 4)), so the fragment reads of 16 consecutive rows
+// cover all 64 banks once.
+constexpr int kBK = 32, kStages = 5;
+APEXW_DEV int lds_off(int row, int chunk) { return row * kBK + ((chunk ^ ((row >> 2) & 3)) << 3); }
 
 struct GemmArgs {
   const uint16_t* a;   // [M x K] row-major, ld lda
@@ -41,7 +46,7 @@ struct GemmArgs {
 APEXW_DEV float bf(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 APEXW_DEV uint16_t to_bf(float x) { return (uint16_t)f32_to_bf16_bits(x); }
 
-typedef uint16_t LdsTile[kBM * kBK];
+typedef uint16_t LdsStage[2][kBM * kBK];   // [A | B][256 x 32]
 
 // global -> LDS copy of 16 bytes per lane (global_load_lds_dwordx4): lane L's
 // 16 bytes at gbase + voff land at LDS byte lds_base + 16 L.  Issued as inline
@@ -77,52 +82,75 @@ APEXW_DEV uint32_t lds_address(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
+// s_waitcnt vmcnt(n) for the n the K loop needs (an immediate operand).
+APEXW_DEV void wait_vm(int n) {
+  if (n >= 32) asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
+  else if (n >= 24) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+  else if (n >= 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+  else if (n >= 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
 // One 256 x 256 output tile: O = alpha * A B^T + beta * E (bf16 in, fp32
 // accumulate, bf16 out, round to nearest even).  A and B point at the tile's
 // first row of each operand; Et, C and Ct at the tile's origin in their own
 // layouts.  256 threads = 4 waves in a 2 x 2 arrangement, each owning a
-// 128 x 128 block as 4 x 4 MFMA 32x32x16 accumulators; K tiles of 64 are
-// double-buffered in LDS and loaded straight from global memory into LDS.
+// 128 x 128 block as 4 x 4 MFMA 32x32x16 accumulators.
 // Template flags select the epilogue: write O row-major (kC), transposed (kCt,
 // skipped at run time when write_ct is false), add beta * E (kAdd).
+//
+// K pipeline.  Stage h = K columns [32 h, 32 h + 32), buffer h % 5, two MFMA
+// k-steps (a, b) whose fragments sit in register slots 0 and 1.  Iteration h:
+//   1. the 16 MFMAs of step h.a, each followed by one LDS read of step h.b's
+//      fragments (slot 1, free since the MFMAs of step (h-1).b were issued);
+//   2. wait until stage h + 1's copies have landed and this wave's LDS reads
+//      have returned, then barrier;
+//   3. the 16 MFMAs of step h.b, the first 8 each followed by one LDS read of
+//      step (h+1).a (slot 0) and the last 8 by one global -> LDS copy of
+//      stage h + 5 into buffer h % 5.
+// Stage h + 1 is read only after the barrier in 2 that follows its wait, and
+// buffer h % 5 is refilled only after that barrier, which every wave reaches
+// after its last reads of stage h.  A stage's copies have about three and a
+// half iterations to land.
+//
+// Addend on the matrix cores (diag_k0 >= 0): when E is the B operand itself
+// read at K = diag_k0 + i (E[i][j] = B[j][diag_k0 + i], as in X' = B X + a X
+// with both X operands given as X^T rows) and alpha == 1, the B fragments of
+// K columns [diag_k0, diag_k0 + 256) are exactly the addend.  There each wave
+// adds beta E with extra MFMAs against a one-hot fragment holding beta on the
+// diagonal (beta split into two bf16 parts, hi + lo, within 2^-18 of beta), so
+// the epilogue reads no addend.
 template <bool kC, bool kCt, bool kAdd>
 APEXW_DEV void gemm_tile(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, int32_t lda, int32_t ldb,
                          int32_t k, const uint16_t* __restrict__ Et, int32_t lde, uint16_t* __restrict__ C,
                          int32_t ldc, uint16_t* __restrict__ Ct, int32_t ldct, bool write_ct, float alpha,
-                         float beta, LdsTile* s_a, LdsTile* s_b) {
+                         float beta, int32_t diag_k0, LdsStage* lds) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  // global -> LDS without registers (global_load_lds_dwordx4): each wave
-  // instruction fills 1 KB of LDS = 8 tile rows, lane L landing at byte 16 L.
-  // Lane L of chunk q reads row 8 q + L / 8 at column chunk (L % 8) ^ (L / 8),
-  // which is the swizzled slot L % 8 of that row.  Per K tile each wave issues
-  // 8 instructions for A and 8 for B (chunks q = 8 wave + i).
-  uint32_t goff_a[8], goff_b[8];
+  // Copies: each wave instruction fills 1 KB of LDS = 16 rows of 64 bytes,
+  // lane L landing at byte 16 L, i.e. row 16 q + L / 4, slot L % 4, which holds
+  // column chunk (L % 4) ^ ((L / 16) % 4).  A stage is 16 instructions for A and
+  // 16 for B; wave w issues q = 4 w .. 4 w + 3 of each.
+  uint32_t goff[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int row = 8 * (8 * wave + i) + (lane >> 3), chunk = (lane & 7) ^ (lane >> 3);
-    goff_a[i] = (uint32_t)(row * lda + chunk * 8) * 2u;
-    goff_b[i] = (uint32_t)(row * ldb + chunk * 8) * 2u;
+  for (int i = 0; i < 4; ++i) {
+    const int row = 16 * (4 * wave + i) + (lane >> 2), chunk = (lane & 3) ^ ((lane >> 4) & 3);
+    goff[i] = (uint32_t)(row * lda + chunk * 8) * 2u;
+    goff[4 + i] = (uint32_t)(row * ldb + chunk * 8) * 2u;
   }
-  // LDS byte address of this wave's first chunk in each stage (wave-uniform)
-  const uint32_t lds_a0 = __builtin_amdgcn_readfirstlane(lds_address(&s_a[0][8 * wave * 512]));
-  const uint32_t lds_b0 = __builtin_amdgcn_readfirstlane(lds_address(&s_b[0][8 * wave * 512]));
-  constexpr uint32_t kStage = sizeof(LdsTile), kChunk = 512 * sizeof(uint16_t);
+  // LDS byte address of this wave's first A chunk in stage 0 (wave-uniform)
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(&lds[0][0][4 * wave * 512]));
+  constexpr uint32_t kStageBytes = sizeof(LdsStage), kHalf = kStageBytes / 2, kChunk = 1024;
   const uint16_t* A_s = uniform_ptr(A);
   const uint16_t* B_s = uniform_ptr(B);
-  auto issue_loads = [&](int buf, int k0) {
-    const uint16_t* a0 = A_s + k0;
-    const uint16_t* b0 = B_s + k0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      lds_copy16(lds_a0 + buf * kStage + i * kChunk, goff_a[i], a0);
-      lds_copy16(lds_b0 + buf * kStage + i * kChunk, goff_b[i], b0);
-    }
+  // copy i (0..7) of stage h: A chunks 0..3, then B chunks 0..3
+  auto copy = [&](int h, int i) {
+    const uint32_t base = lds0 + (uint32_t)(h % kStages) * kStageBytes;
+    if (i < 4) lds_copy16(base + i * kChunk, goff[i], A_s + h * kBK);
+    else lds_copy16(base + kHalf + (i - 4) * kChunk, goff[i], B_s + h * kBK);
   };
-  // the loads write LDS asynchronously: wait for this wave's, then the barrier
-  // makes every wave's visible
-  auto loads_done = [&]() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
+  constexpr int kCopies = 8;   // per stage and wave
 
   f32x16 acc[4][4];
 #pragma unroll
@@ -131,58 +159,109 @@ APEXW_DEV void gemm_tile(const uint16_t* __restrict__ A, const uint16_t* __restr
     for (int b = 0; b < 4; ++b) acc[a][b] = f32x16{};
 
   // MFMA 32x32x16 operand layout: lane l supplies row (l % 32) and k = 8 (l / 32) .. +7.
-  // Fragments are double-buffered in registers: the 8 LDS reads of k-step s + 1
-  // are issued before the 16 MFMAs of step s.  sched_barrier(0) pins that order
-  // (the scheduler would otherwise sink each read next to its first use and
-  // expose the full LDS latency before every few MFMAs).
   const int frag_row = lane & 31, frag_c = lane >> 5;
   bf16x8 fa[2][4], fb[2][4];
-  auto frags = [&](int buf, int s, int slot) {
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-      fa[slot][a] = *(const bf16x8*)&s_a[buf][lds_off(wm * 128 + a * 32 + frag_row, s * 2 + frag_c)];
-#pragma unroll
-    for (int b = 0; b < 4; ++b)
-      fb[slot][b] = *(const bf16x8*)&s_b[buf][lds_off(wn * 128 + b * 32 + frag_row, s * 2 + frag_c)];
+  // fragment read i (0..7) of k-step s of stage h: A fragments 0..3, then B 0..3
+  auto frag = [&](int h, int s, int i) {
+    const uint16_t* st = lds[h % kStages][i < 4 ? 0 : 1];
+    const int row = (i < 4 ? wm * 128 + i * 32 : wn * 128 + (i - 4) * 32) + frag_row;
+    const bf16x8 v = *(const bf16x8*)&st[lds_off(row, s * 2 + frag_c)];
+    if (i < 4) fa[s][i] = v;
+    else fb[s][i - 4] = v;
   };
-  auto mma = [&](int slot) {
+  // the 16 MFMAs of slot s, side(j) issued after MFMA j; sched_barrier(0)
+  // fences keep that interleaving (the scheduler would otherwise cluster the
+  // reads next to their first use and expose the LDS latency)
+  auto mma = [&](int s, auto&& side) {
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-      for (int b = 0; b < 4; ++b)
-        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[slot][a], fb[slot][b], acc[a][b], 0, 0, 0);
+    for (int j = 0; j < 16; ++j) {
+      acc[j >> 2][j & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[s][j >> 2], fb[s][j & 3], acc[j >> 2][j & 3], 0,
+                                                                    0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      side(j);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   };
-#define APEXW_SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
+  // lgkmcnt(0) through the builtin (vmcnt and expcnt fields at their no-wait
+  // maxima), so the compiler knows this wave's LDS reads have returned and adds
+  // no later waits for them; the barrier itself is asm with a memory clobber so
+  // no LDS access moves across it
+  // beta E on the matrix cores (see above): stage h holds K columns
+  // [32 h, 32 h + 32), i.e. rows 32 h - diag_k0 .. + 31 of the addend, which
+  // fall in this wave's A block (32 h - diag_k0 - 128 wm) / 32 when in range
+  const bool diag = kAdd && diag_k0 >= 0;
+  const uint32_t beta_hi = f32_to_bf16_bits(beta);
+  const uint32_t beta_lo = f32_to_bf16_bits(beta - __uint_as_float(beta_hi << 16));
+  auto diag_mma = [&](int h, int s) {
+    const int rel = h * kBK - (diag_k0 + wm * 128);
+    if (rel < 0 || rel >= 128) return;
+    // lane l feeds row l % 32 of the block and k = 16 s + 8 (l / 32) + t: the
+    // diagonal element sits at t = l % 32 - 16 s - 8 (l / 32)
+    const int t = (lane & 31) - 16 * s - 8 * (lane >> 5);
+    u32x4 dh = {0u, 0u, 0u, 0u}, dl = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const bool hit = (t >> 1) == w && t >= 0 && t < 8;
+      const uint32_t sh = (uint32_t)(t & 1) * 16u;
+      dh[w] = hit ? beta_hi << sh : 0u;
+      dl[w] = hit ? beta_lo << sh : 0u;
+    }
+    const bf16x8 fh = __builtin_bit_cast(bf16x8, dh), fl = __builtin_bit_cast(bf16x8, dl);
+    auto add = [&](auto blk_c) {
+      constexpr int blk = decltype(blk_c)::value;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        acc[blk][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fh, fb[s][b], acc[blk][b], 0, 0, 0);
+        acc[blk][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fl, fb[s][b], acc[blk][b], 0, 0, 0);
+      }
+    };
+    switch (rel >> 5) {
+      case 0: add(std::integral_constant<int, 0>()); break;
+      case 1: add(std::integral_constant<int, 1>()); break;
+      case 2: add(std::integral_constant<int, 2>()); break;
+      default: add(std::integral_constant<int, 3>()); break;
+    }
+  };
+  auto barrier = [&]() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    asm volatile("s_barrier" ::: "memory");
+  };
 
-  const int k_tiles = k / kBK;
-  issue_loads(0, 0);
-  loads_done();
-  __syncthreads();
-  for (int kt = 0; kt < k_tiles; ++kt) {
-    // stage buf ^ 1 was last read before the previous barrier: refill it with
-    // tile kt + 1 while tile kt is multiplied
-    const int buf = kt & 1;
-    if (kt + 1 < k_tiles) issue_loads(buf ^ 1, (kt + 1) * kBK);
-    frags(buf, 0, 0);
-    APEXW_SCHED_FENCE();
-    frags(buf, 1, 1);
-    APEXW_SCHED_FENCE();
-    mma(0);
-    APEXW_SCHED_FENCE();
-    frags(buf, 2, 0);
-    APEXW_SCHED_FENCE();
-    mma(1);
-    APEXW_SCHED_FENCE();
-    frags(buf, 3, 1);
-    APEXW_SCHED_FENCE();
-    mma(0);
-    APEXW_SCHED_FENCE();
-    mma(1);
-    APEXW_SCHED_FENCE();
-    loads_done();
-    __syncthreads();
-  }
-#undef APEXW_SCHED_FENCE
+  const int n = k / kBK;
+  const int first = n < kStages ? n : kStages;
+  for (int h = 0; h < first; ++h)
+#pragma unroll
+    for (int i = 0; i < kCopies; ++i) copy(h, i);
+  wait_vm(kCopies * (first - 1));   // stage 0 landed
+  barrier();
+#pragma unroll
+  for (int i = 0; i < 8; ++i) frag(0, 0, i);
+  // one iteration; kNext: a stage h + 1 exists, kRefill: a stage h + 5 exists
+  auto iteration = [&](int h, auto next_c, auto refill_c) {
+    constexpr bool kNext = decltype(next_c)::value, kRefill = decltype(refill_c)::value;
+    mma(0, [&](int j) {
+      if (j < 8) frag(h, 1, j);
+    });
+    if (diag) diag_mma(h, 0);
+    // stage h + 1 landed; copies of the stages after it may still be in flight
+    const int last_issued = (h + kStages - 1 < n ? h + kStages - 1 : n - 1);
+    wait_vm(kNext ? kCopies * (last_issued - (h + 1)) : 0);
+    barrier();
+    mma(1, [&](int j) {
+      if (j < 8) {
+        if constexpr (kNext) frag(h + 1, 0, j);
+      } else {
+        if constexpr (kRefill) copy(h + kStages, j - 8);
+      }
+    });
+    if (diag) diag_mma(h, 1);
+  };
+  typedef std::integral_constant<bool, true> yes;
+  typedef std::integral_constant<bool, false> no;
+  int h = 0;
+  for (; h + kStages < n; ++h) iteration(h, yes(), yes());
+  for (; h + 1 < n; ++h) iteration(h, yes(), no());
+  iteration(h, no(), no());   // n >= 1: the last stage
 
   // Epilogue.  Accumulator register r of lane l holds row 8 (r / 4) + 4 (l / 32) + r % 4,
   // column l % 32 of its 32 x 32 block: four consecutive rows of one column per group.
@@ -193,7 +272,7 @@ APEXW_DEV void gemm_tile(const uint16_t* __restrict__ A, const uint16_t* __restr
   // (16 lanes per row) and the column reads (16 lanes down a column) each hit
   // distinct banks.  A wave reads back only what it wrote itself, and LDS keeps
   // one wave's accesses in order, so no barrier is needed.
-  uint16_t* stage = (wave < 2 ? s_a[wave] : s_b[wave - 2]);
+  uint16_t* stage = lds[wave][0];   // 32 KB per wave
   auto swz = [](int r, int c) { return r * 128 + ((((c >> 3) ^ (r >> 3)) & 15) << 3) + (c & 7); };
   const int il0 = (lane >> 5) * 4, jl0 = lane & 31;           // within the wave's block
   const int gi0 = wm * 128 + il0, gj0 = wn * 128 + jl0;       // within the tile
@@ -209,9 +288,11 @@ APEXW_DEV void gemm_tile(const uint16_t* __restrict__ A, const uint16_t* __restr
 #pragma unroll
         for (int r = 0; r < 4; ++r) v[r] = alpha * acc[a][b][q * 4 + r];
         if constexpr (kAdd) {
-          const u16x4 e = *APEXW_GLOBAL(const u16x4, Et + (uint32_t)((gj0 + b * 32) * lde + gi0 + a * 32 + q * 8));
+          if (!diag) {
+            const u16x4 e = *APEXW_GLOBAL(const u16x4, Et + (uint32_t)((gj0 + b * 32) * lde + gi0 + a * 32 + q * 8));
 #pragma unroll
-          for (int r = 0; r < 4; ++r) v[r] = fmaf(beta, bf(e[r]), v[r]);
+            for (int r = 0; r < 4; ++r) v[r] = fmaf(beta, bf(e[r]), v[r]);
+          }
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) stage[swz(il + r, jl)] = to_bf(v[r]);
@@ -247,8 +328,7 @@ APEXW_DEV void gemm_tile(const uint16_t* __restrict__ A, const uint16_t* __restr
 // Batched GEMM over one shape: one workgroup per output tile, blockIdx.y = batch entry.
 template <bool kC, bool kCt, bool kAdd>
 __global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(16))) LdsTile s_a[2];
-  __shared__ __attribute__((aligned(16))) LdsTile s_b[2];
+  __shared__ __attribute__((aligned(16))) LdsStage lds[kStages];
 
   const int tiles_m = g.m / kBM, tiles_n = g.n / kBN, tiles = tiles_m * tiles_n;
   // Consecutive workgroups are dispatched round-robin over the 8 XCDs; give each
@@ -269,7 +349,7 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmArgs g) {
                            kAdd ? g.et + batch * g.se + col0 * g.lde + row0 : nullptr, g.lde,
                            kC ? g.c + batch * g.sc + row0 * g.ldc + col0 : nullptr, g.ldc,
                            kCt ? g.ct + batch * g.sct + col0 * g.ldct + row0 : nullptr, g.ldct, true, g.alpha, g.beta,
-                           s_a, s_b);
+                           -1, lds);
 }
 
 // Grouped GEMM: every problem of a launch (different shapes, K and operands)
@@ -289,8 +369,7 @@ template <bool kC, bool kCt, bool kAdd>
 __global__ __launch_bounds__(256, 1) void gemm_nt_grouped_kernel(const apexw_gemm_problem* __restrict__ probs,
                                                                  const uint32_t* __restrict__ items,
                                                                  const int32_t* __restrict__ queue_offsets) {
-  __shared__ __attribute__((aligned(16))) LdsTile s_a[2];
-  __shared__ __attribute__((aligned(16))) LdsTile s_b[2];
+  __shared__ __attribute__((aligned(16))) LdsStage lds[kStages];
   const int q = (int)(blockIdx.x % kQueues), i = (int)(blockIdx.x / kQueues);
   const int begin = queue_offsets[q];
   if (i >= queue_offsets[q + 1] - begin) return;
@@ -299,11 +378,13 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_grouped_kernel(const apexw_gem
   const int tm = (int)((code >> 12) & 0xfffu), tn = (int)(code & 0xfffu);
   const int64_t row0 = (int64_t)tm * kBM, col0 = (int64_t)tn * kBN;
   const bool mirror = !(p.flags & APEXW_GEMM_SYM) || tm != tn;
+  // the addend is the B operand read at K = row0 + i: accumulate it on the matrix cores
+  const bool diag = kAdd && p.et == p.b && p.lde == p.ldb && p.alpha == 1.0f && row0 + kBM <= p.k;
   gemm_tile<kC, kCt, kAdd>((const uint16_t*)p.a + row0 * p.lda, (const uint16_t*)p.b + col0 * p.ldb, p.lda, p.ldb,
                            p.k, kAdd ? (const uint16_t*)p.et + col0 * p.lde + row0 : nullptr, p.lde,
                            kC ? (uint16_t*)p.c + row0 * p.ldc + col0 : nullptr, p.ldc,
                            kCt ? (uint16_t*)p.ct + col0 * p.ldct + row0 : nullptr, p.ldct, mirror, p.alpha, p.beta,
-                           s_a, s_b);
+                           diag ? (int32_t)row0 : -1, lds);
 }
 
 // ---------------------------------------------------------------------------

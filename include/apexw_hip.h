@@ -244,11 +244,13 @@ int64_t apexw_gemm_grouped_items(const apexw_gemm_problem* problems, int32_t n_p
  * Host-side: validate the problems (a host copy of the table that will be
  * uploaded) and build the tile queues: items[n_items] (n_items from
  * apexw_gemm_grouped_items) and queue_offsets[APEXW_GEMM_QUEUES + 1]; queue q
- * is items[queue_offsets[q] .. queue_offsets[q + 1]).  The tiles, in locality
- * order (bands of 4 tile rows), are cut into one contiguous band per queue of
- * equal K-cost, longest tiles first within a band.  *n_workgroups receives the
- * grid size of the launch (APEXW_GEMM_QUEUES x the longest queue) and *kind the
- * epilogue kind.  At most 256 problems, 4096 tiles per side.
+ * is items[queue_offsets[q] .. queue_offsets[q + 1]).  Each problem's tiles, in
+ * locality order (bands of 4 tile rows), are cut into one contiguous band per
+ * queue (so every XCD works on the same matrix at once), the remainders rotated
+ * across queues to balance them; longest tiles first within a queue.
+ * *n_workgroups receives the grid size of the launch (APEXW_GEMM_QUEUES x the
+ * longest queue) and *kind the epilogue kind.  At most 256 problems, 4096 tiles
+ * per side.
  */
 int apexw_gemm_grouped_schedule(const apexw_gemm_problem* problems, int32_t n_problems, uint32_t* items,
                                 int64_t n_items, int32_t* queue_offsets, int32_t* n_workgroups, int32_t* kind);

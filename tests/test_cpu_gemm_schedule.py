@@ -76,14 +76,19 @@ def test_schedule_covers_every_tile_once_in_balanced_bands(phase, kind):
     ktiles = np.array([probs[i][7] // _lib.GEMM_KTILE for i in p.tolist()])
     loads = np.array([(ktiles[offsets[q]:offsets[q + 1]] + epi).sum() for q in range(nq)])
     assert loads.max() - loads.min() <= 2 * (ktiles.max() + epi), loads
-    # each queue is one contiguous band of the locality order, longest tiles first
+    # per problem, queue q holds the q-th contiguous band of its locality order
+    # and every queue gets floor or ceil of the problem's tiles / 8
     order = {t: i for i, t in enumerate(sorted(_expected_tiles(probs), key=lambda t: (t[0], t[1] // 4, t[2], t[1])))}
-    prev_end = -1
+    for pi in range(len(probs)):
+        prev_end, sizes = -1, []
+        for q in range(nq):
+            pos = sorted(order[t] for t in got[offsets[q]:offsets[q + 1]] if t[0] == pi)
+            sizes.append(len(pos))
+            if pos:
+                assert pos == list(range(pos[0], pos[-1] + 1)) and pos[0] > prev_end, f"problem {pi} queue {q} band"
+                prev_end = pos[-1]
+        assert max(sizes) - min(sizes) <= 1, (pi, sizes)
     for q in range(nq):
-        seg = got[offsets[q]:offsets[q + 1]]
-        pos = sorted(order[t] for t in seg)
-        assert pos == list(range(pos[0], pos[-1] + 1)) and pos[0] > prev_end, f"queue {q} band"
-        prev_end = pos[-1]
         kt = ktiles[offsets[q]:offsets[q + 1]]
         assert np.all(np.diff(kt) <= 0), f"queue {q} is not longest-first"
 

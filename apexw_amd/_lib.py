@@ -13,7 +13,7 @@ import numpy as np
 
 from ._build import LIB_PATH
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # dtype codes
 F32, BF16, F16, U8, I8 = 0, 1, 2, 3, 4
@@ -75,8 +75,8 @@ GEMM_PROBLEM_DTYPE = np.dtype([
     ("flags", np.uint32), ("reserved", np.uint32),
 ])
 assert GEMM_PROBLEM_DTYPE.itemsize == 88
-GEMM_SYM = 1
-GEMM_OUT_C, GEMM_OUT_CT, GEMM_ADD = 1, 2, 4
+GEMM_SYM, GEMM_B_KN, GEMM_ADD_B = 1, 2, 4
+GEMM_OUT_C, GEMM_OUT_CT, GEMM_ADD, GEMM_KIND_NN = 1, 2, 4, 8
 GEMM_MAX_PROBLEMS = 256
 GEMM_QUEUES = 8
 
@@ -99,7 +99,7 @@ SIGNATURES = {
     "apexw_muon_workspace_floats": (ctypes.c_int64, [_i64, _i64]),
     "apexw_muon_prepare": (ctypes.c_int, [_vp, _vp, _i32, _i64, _i64, _f32, _f32, _i32, _f32, _vp, _vp, _i64, _i64,
                                           _vp, _vp]),
-    "apexw_muon_apply": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _i64, _f32, _i32, _f32, _vp]),
+    "apexw_muon_apply": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _i64, _i32, _f32, _i32, _f32, _vp]),
 }
 
 GEMM_TILE = 256

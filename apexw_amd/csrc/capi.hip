@@ -27,8 +27,8 @@ int apexw_launch_gemm_grouped(const apexw_gemm_problem*, const uint32_t*, const 
                               hipStream_t);
 int apexw_launch_muon_prepare(float*, const void*, int32_t, int64_t, int64_t, float, float, int32_t, float, uint16_t*,
                               uint16_t*, int64_t, int64_t, float*, hipStream_t);
-int apexw_launch_muon_apply(void*, int32_t, const uint16_t*, int64_t, int64_t, int64_t, float, int32_t, float,
-                            hipStream_t);
+int apexw_launch_muon_apply(void*, int32_t, const uint16_t*, int64_t, int64_t, int64_t, int32_t, float, int32_t,
+                            float, hipStream_t);
 bool apexw_q8_flags_ok(uint32_t flags, uint32_t block, int64_t n);
 
 namespace {
@@ -165,26 +165,32 @@ constexpr int kTile = APEXW_GEMM_TILE;
 
 // Epilogue kind of one problem, or minus a status when it is invalid.
 int gemm_problem_kind(const apexw_gemm_problem& p) {
-  if (!p.a || !p.b || (!p.c && !p.ct) || (p.beta != 0.0f && !p.et)) return -APEXW_ERR_ARG;
-  if ((p.flags & ~APEXW_GEMM_SYM) || p.reserved) return -APEXW_ERR_ARG;
+  const bool sym = p.flags & APEXW_GEMM_SYM, kn = p.flags & APEXW_GEMM_B_KN, add_b = p.flags & APEXW_GEMM_ADD_B;
+  const bool add = p.beta != 0.0f;
+  if (!p.a || !p.b || (!p.c && !p.ct)) return -APEXW_ERR_ARG;
+  if ((p.flags & ~(APEXW_GEMM_SYM | APEXW_GEMM_B_KN | APEXW_GEMM_ADD_B)) || p.reserved) return -APEXW_ERR_ARG;
+  if (add_b ? (p.et || !add || p.alpha != 1.0f || p.m > p.k) : (add && !p.et)) return -APEXW_ERR_ARG;
+  if (kn && (sym || p.ct)) return -APEXW_ERR_ARG;
   if (p.m <= 0 || p.n <= 0 || p.k <= 0) return -APEXW_ERR_ARG;
   if (p.m % kTile || p.n % kTile || p.k % APEXW_GEMM_KTILE) return -APEXW_ERR_ARG;
   if (p.m / kTile > 4096 || p.n / kTile > 4096) return -APEXW_ERR_ARG;
-  const bool add = p.beta != 0.0f;
-  if (p.lda < p.k || p.ldb < p.k || (p.c && p.ldc < p.n) || (p.ct && p.ldct < p.m) || (add && p.lde < p.m))
+  const bool read_e = add && !add_b;
+  if (p.lda < p.k || p.ldb < (kn ? p.n : p.k) || (p.c && p.ldc < p.n) || (p.ct && p.ldct < p.m) ||
+      (read_e && p.lde < p.m))
     return -APEXW_ERR_ARG;
-  const int32_t lds[5] = {p.lda, p.ldb, add ? p.lde : 0, p.c ? p.ldc : 0, p.ct ? p.ldct : 0};
+  const int32_t lds[5] = {p.lda, p.ldb, read_e ? p.lde : 0, p.c ? p.ldc : 0, p.ct ? p.ldct : 0};
   for (int32_t ld : lds) {
     if (ld > APEXW_GEMM_MAX_LD) return -APEXW_ERR_ARG;
     if (ld & 7) return -APEXW_ERR_ALIGN;
   }
-  const uintptr_t al = (uintptr_t)p.a | (uintptr_t)p.b | (uintptr_t)(add ? p.et : nullptr) | (uintptr_t)p.c |
+  const uintptr_t al = (uintptr_t)p.a | (uintptr_t)p.b | (uintptr_t)(read_e ? p.et : nullptr) | (uintptr_t)p.c |
                        (uintptr_t)p.ct;
   if (al & 15u) return -APEXW_ERR_ALIGN;
-  if (p.flags & APEXW_GEMM_SYM) {
+  if (sym) {
     if (p.m != p.n || p.a != p.b || p.lda != p.ldb || !p.c || p.ct != p.c || p.ldct != p.ldc) return -APEXW_ERR_ARG;
   }
-  return (p.c ? APEXW_GEMM_OUT_C : 0) | (p.ct ? APEXW_GEMM_OUT_CT : 0) | (add ? APEXW_GEMM_ADD : 0);
+  return (p.c ? APEXW_GEMM_OUT_C : 0) | (p.ct ? APEXW_GEMM_OUT_CT : 0) | (add ? APEXW_GEMM_ADD : 0) |
+         (kn ? APEXW_GEMM_KIND_NN : 0);
 }
 
 int64_t gemm_problem_tiles(const apexw_gemm_problem& p) {
@@ -273,7 +279,8 @@ int apexw_gemm_nt_grouped(const apexw_gemm_problem* problems, const uint32_t* it
                           int32_t n_workgroups, int32_t kind, void* stream) {
   if (!problems || !items || !queue_offsets) return APEXW_ERR_ARG;
   if (n_workgroups <= 0 || n_workgroups % APEXW_GEMM_QUEUES) return APEXW_ERR_ARG;
-  if (kind <= 0 || kind > 7 || !(kind & (APEXW_GEMM_OUT_C | APEXW_GEMM_OUT_CT))) return APEXW_ERR_ARG;
+  if (kind <= 0 || kind > 15 || !(kind & (APEXW_GEMM_OUT_C | APEXW_GEMM_OUT_CT))) return APEXW_ERR_ARG;
+  if ((kind & APEXW_GEMM_KIND_NN) && (kind & APEXW_GEMM_OUT_CT)) return APEXW_ERR_ARG;
   if (((uintptr_t)problems | (uintptr_t)items | (uintptr_t)queue_offsets) & 3u) return APEXW_ERR_ALIGN;
   return apexw_launch_gemm_grouped(problems, items, queue_offsets, n_workgroups, kind, (hipStream_t)stream);
 }
@@ -285,22 +292,22 @@ int64_t apexw_muon_workspace_floats(int64_t rows, int64_t cols) {
 int apexw_muon_prepare(float* buf, const void* g, int32_t g_dtype, int64_t rows, int64_t cols, float mu,
                        float one_minus_mu, int32_t nesterov, float eps, void* x, void* xt, int64_t ldx, int64_t ldxt,
                        float* workspace, void* stream) {
-  if (!buf || !g || !x || !xt || !workspace || rows <= 0 || cols <= 0) return APEXW_ERR_ARG;
+  if (!buf || !g || !x || !workspace || rows <= 0 || cols <= 0) return APEXW_ERR_ARG;
   if (g_dtype != APEXW_F32 && g_dtype != APEXW_BF16 && g_dtype != APEXW_F16) return APEXW_ERR_DTYPE;
-  // work matrix X is [min x max], X^T is [max x min]
+  // work matrix X is [min x max], X^T is [max x min] (optional)
   const int64_t lo = rows < cols ? rows : cols, hi = rows < cols ? cols : rows;
-  if (ldx < hi || ldxt < lo) return APEXW_ERR_ARG;
-  (void)lo;
+  if (ldx < hi || (xt && ldxt < lo)) return APEXW_ERR_ARG;
   return apexw_launch_muon_prepare(buf, g, g_dtype, rows, cols, mu, one_minus_mu, nesterov, eps, (uint16_t*)x,
                                    (uint16_t*)xt, ldx, ldxt, workspace, (hipStream_t)stream);
 }
 
 int apexw_muon_apply(void* p, int32_t p_dtype, const void* u, int64_t rows, int64_t cols, int64_t ldu,
-                     float wd_factor, int32_t apply_wd, float neg_lr_eff, void* stream) {
-  if (!p || !u || rows <= 0 || cols <= 0 || ldu < cols) return APEXW_ERR_ARG;
+                     int32_t u_transposed, float wd_factor, int32_t apply_wd, float neg_lr_eff, void* stream) {
+  if (!p || !u || rows <= 0 || cols <= 0 || ldu < (u_transposed ? rows : cols)) return APEXW_ERR_ARG;
+  if ((rows + 63) / 64 > 65535) return APEXW_ERR_ARG;   // grid y of the transposing kernel
   if (p_dtype != APEXW_F32 && p_dtype != APEXW_BF16 && p_dtype != APEXW_F16) return APEXW_ERR_DTYPE;
-  return apexw_launch_muon_apply(p, p_dtype, (const uint16_t*)u, rows, cols, ldu, wd_factor, apply_wd, neg_lr_eff,
-                                 (hipStream_t)stream);
+  return apexw_launch_muon_apply(p, p_dtype, (const uint16_t*)u, rows, cols, ldu, u_transposed != 0, wd_factor,
+                                 apply_wd, neg_lr_eff, (hipStream_t)stream);
 }
 
 int apexw_grad_clip_coef(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,

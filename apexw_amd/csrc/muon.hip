@@ -22,6 +22,8 @@ namespace {
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(16))) float f32x16;
 typedef __attribute__((ext_vector_type(4))) uint16_t u16x4;
+typedef __attribute__((ext_vector_type(4))) short v4i16;
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
 
 constexpr int kBM = 256, kBN = 256;
 // K is staged through LDS 32 at a time in kStages rotating buffers of 32 KB
@@ -113,14 +115,20 @@ APEXW_DEV void wait_vm(int n) {
 // after its last reads of stage h.  A stage's copies have about three and a
 // half iterations to land.
 //
+// kNN: B is given as [K x N] row-major (O = alpha A B + beta E) instead of
+// [N x K].  Its LDS stage is then 32 K rows x 256 columns, and each B fragment
+// (8 consecutive k of one column) is assembled by two transposing LDS reads
+// (ds_read_b64_tr_b16: in each group of 16 lanes, lane 4 r + c receives
+// element c of the 8-byte rows addressed by lanes r, r + 4, r + 8, r + 12).
+//
 // Addend on the matrix cores (diag_k0 >= 0): when E is the B operand itself
-// read at K = diag_k0 + i (E[i][j] = B[j][diag_k0 + i], as in X' = B X + a X
-// with both X operands given as X^T rows) and alpha == 1, the B fragments of
-// K columns [diag_k0, diag_k0 + 256) are exactly the addend.  There each wave
-// adds beta E with extra MFMAs against a one-hot fragment holding beta on the
+// read at K = diag_k0 + i (E[i][j] = B[j][diag_k0 + i], or B[diag_k0 + i][j]
+// for kNN, as in X' = B X + a X) and alpha == 1, the B fragments of K
+// [diag_k0, diag_k0 + 256) are exactly the addend.  There each wave adds
+// beta E with extra MFMAs against a one-hot fragment holding beta on the
 // diagonal (beta split into two bf16 parts, hi + lo, within 2^-18 of beta), so
 // the epilogue reads no addend.
-template <bool kC, bool kCt, bool kAdd>
+template <bool kC, bool kCt, bool kAdd, bool kNN>
 APEXW_DEV void gemm_tile(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, int32_t lda, int32_t ldb,
                          int32_t k, const uint16_t* __restrict__ Et, int32_t lde, uint16_t* __restrict__ C,
                          int32_t ldc, uint16_t* __restrict__ Ct, int32_t ldct, bool write_ct, float alpha,
@@ -128,16 +136,24 @@ APEXW_DEV void gemm_tile(const uint16_t* __restrict__ A, const uint16_t* __restr
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  // Copies: each wave instruction fills 1 KB of LDS = 16 rows of 64 bytes,
-  // lane L landing at byte 16 L, i.e. row 16 q + L / 4, slot L % 4, which holds
-  // column chunk (L % 4) ^ ((L / 16) % 4).  A stage is 16 instructions for A and
-  // 16 for B; wave w issues q = 4 w .. 4 w + 3 of each.
+  // Copies: each wave instruction fills 1 KB of LDS, lane L landing at byte
+  // 16 L.  [rows x K] operands: 16 rows of 64 bytes, lane L at row 16 q + L / 4,
+  // slot L % 4, which holds column chunk (L % 4) ^ ((L / 16) % 4).  kNN B: 2 K
+  // rows of 512 bytes, lane L at row 2 q + L / 32, slot L % 32, holding column
+  // chunk (L % 32) ^ (4 (row % 4)) (so the transposing reads of 4 consecutive
+  // rows hit distinct banks).  A stage is 16 instructions for A and 16 for B;
+  // wave w issues q = 4 w .. 4 w + 3 of each.
   uint32_t goff[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = 16 * (4 * wave + i) + (lane >> 2), chunk = (lane & 3) ^ ((lane >> 4) & 3);
     goff[i] = (uint32_t)(row * lda + chunk * 8) * 2u;
-    goff[4 + i] = (uint32_t)(row * ldb + chunk * 8) * 2u;
+    if constexpr (kNN) {
+      const int krow = 2 * (4 * wave + i) + (lane >> 5), nchunk = (lane & 31) ^ (4 * (krow & 3));
+      goff[4 + i] = (uint32_t)(krow * ldb + nchunk * 8) * 2u;
+    } else {
+      goff[4 + i] = (uint32_t)(row * ldb + chunk * 8) * 2u;
+    }
   }
   // LDS byte address of this wave's first A chunk in stage 0 (wave-uniform)
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(&lds[0][0][4 * wave * 512]));
@@ -148,7 +164,7 @@ APEXW_DEV void gemm_tile(const uint16_t* __restrict__ A, const uint16_t* __restr
   auto copy = [&](int h, int i) {
     const uint32_t base = lds0 + (uint32_t)(h % kStages) * kStageBytes;
     if (i < 4) lds_copy16(base + i * kChunk, goff[i], A_s + h * kBK);
-    else lds_copy16(base + kHalf + (i - 4) * kChunk, goff[i], B_s + h * kBK);
+    else lds_copy16(base + kHalf + (i - 4) * kChunk, goff[i], B_s + (kNN ? (int64_t)h * kBK * ldb : h * kBK));
   };
   constexpr int kCopies = 8;   // per stage and wave
 
@@ -164,6 +180,22 @@ APEXW_DEV void gemm_tile(const uint16_t* __restrict__ A, const uint16_t* __restr
   // fragment read i (0..7) of k-step s of stage h: A fragments 0..3, then B 0..3
   auto frag = [&](int h, int s, int i) {
     const uint16_t* st = lds[h % kStages][i < 4 ? 0 : 1];
+    if (kNN && i >= 4) {
+      // lane l = 16 g + 4 r + j' of group g addresses K row 16 s + 8 (g / 2) + j'
+      // (+ 4 for the upper half), columns n .. n + 3 with n = 16 (g % 2) + 4 r
+      // of the 32-column block; it receives column 16 (g % 2) + (l % 16) = l % 32
+      // at 4 consecutive K rows, i.e. the MFMA B layout
+      const int g = lane >> 4, r = lane & 3, jr = (lane >> 2) & 3;
+      const int n = wn * 128 + (i - 4) * 32 + 16 * (g & 1) + 4 * r;
+      const int k0 = 16 * s + 8 * (g >> 1) + jr;   // k0 % 4 == jr, as for k0 + 4
+      const int slot = (n >> 3) ^ (4 * jr);
+      const int e0 = k0 * 256 + slot * 8 + (n & 7), e1 = e0 + 4 * 256;
+      const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)&st[e0]);
+      const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)&st[e1]);
+      const u32x2 wl = __builtin_bit_cast(u32x2, lo), wh = __builtin_bit_cast(u32x2, hi);
+      fb[s][i - 4] = __builtin_bit_cast(bf16x8, u32x4{wl[0], wl[1], wh[0], wh[1]});
+      return;
+    }
     const int row = (i < 4 ? wm * 128 + i * 32 : wn * 128 + (i - 4) * 32) + frag_row;
     const bf16x8 v = *(const bf16x8*)&st[lds_off(row, s * 2 + frag_c)];
     if (i < 4) fa[s][i] = v;
@@ -182,10 +214,6 @@ APEXW_DEV void gemm_tile(const uint16_t* __restrict__ A, const uint16_t* __restr
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  // lgkmcnt(0) through the builtin (vmcnt and expcnt fields at their no-wait
-  // maxima), so the compiler knows this wave's LDS reads have returned and adds
-  // no later waits for them; the barrier itself is asm with a memory clobber so
-  // no LDS access moves across it
   // beta E on the matrix cores (see above): stage h holds K columns
   // [32 h, 32 h + 32), i.e. rows 32 h - diag_k0 .. + 31 of the addend, which
   // fall in this wave's A block (32 h - diag_k0 - 128 wm) / 32 when in range
@@ -222,6 +250,10 @@ APEXW_DEV void gemm_tile(const uint16_t* __restrict__ A, const uint16_t* __restr
       default: add(std::integral_constant<int, 3>()); break;
     }
   };
+  // lgkmcnt(0) through the builtin (vmcnt and expcnt fields at their no-wait
+  // maxima), so the compiler knows this wave's LDS reads have returned and adds
+  // no later waits for them; the barrier itself is asm with a memory clobber so
+  // no LDS access moves across it
   auto barrier = [&]() {
     __builtin_amdgcn_s_waitcnt(0xC07F);
     asm volatile("s_barrier" ::: "memory");
@@ -345,7 +377,7 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmArgs g) {
 
   const int64_t batch = blockIdx.y;
   const int64_t row0 = (int64_t)tm * kBM, col0 = (int64_t)tn * kBN;
-  gemm_tile<kC, kCt, kAdd>(g.a + batch * g.sa + row0 * g.lda, g.b + batch * g.sb + col0 * g.ldb, g.lda, g.ldb, g.k,
+  gemm_tile<kC, kCt, kAdd, false>(g.a + batch * g.sa + row0 * g.lda, g.b + batch * g.sb + col0 * g.ldb, g.lda, g.ldb, g.k,
                            kAdd ? g.et + batch * g.se + col0 * g.lde + row0 : nullptr, g.lde,
                            kC ? g.c + batch * g.sc + row0 * g.ldc + col0 : nullptr, g.ldc,
                            kCt ? g.ct + batch * g.sct + col0 * g.ldct + row0 : nullptr, g.ldct, true, g.alpha, g.beta,
@@ -365,7 +397,7 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmArgs g) {
 // store (ct == c).
 constexpr int kQueues = APEXW_GEMM_QUEUES;
 
-template <bool kC, bool kCt, bool kAdd>
+template <bool kC, bool kCt, bool kAdd, bool kNN>
 __global__ __launch_bounds__(256, 1) void gemm_nt_grouped_kernel(const apexw_gemm_problem* __restrict__ probs,
                                                                  const uint32_t* __restrict__ items,
                                                                  const int32_t* __restrict__ queue_offsets) {
@@ -378,10 +410,12 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_grouped_kernel(const apexw_gem
   const int tm = (int)((code >> 12) & 0xfffu), tn = (int)(code & 0xfffu);
   const int64_t row0 = (int64_t)tm * kBM, col0 = (int64_t)tn * kBN;
   const bool mirror = !(p.flags & APEXW_GEMM_SYM) || tm != tn;
-  // the addend is the B operand read at K = row0 + i: accumulate it on the matrix cores
-  const bool diag = kAdd && p.et == p.b && p.lde == p.ldb && p.alpha == 1.0f && row0 + kBM <= p.k;
-  gemm_tile<kC, kCt, kAdd>((const uint16_t*)p.a + row0 * p.lda, (const uint16_t*)p.b + col0 * p.ldb, p.lda, p.ldb,
-                           p.k, kAdd ? (const uint16_t*)p.et + col0 * p.lde + row0 : nullptr, p.lde,
+  // APEXW_GEMM_ADD_B: the addend is the B operand read at K = row0 + i,
+  // accumulated on the matrix cores (validated: alpha == 1, m <= k, no et)
+  const bool diag = kAdd && (p.flags & APEXW_GEMM_ADD_B);
+  const uint16_t* B = (const uint16_t*)p.b + (kNN ? col0 : col0 * p.ldb);
+  gemm_tile<kC, kCt, kAdd, kNN>((const uint16_t*)p.a + row0 * p.lda, B, p.lda, p.ldb, p.k,
+                                kAdd && !diag ? (const uint16_t*)p.et + col0 * p.lde + row0 : nullptr, p.lde,
                            kC ? (uint16_t*)p.c + row0 * p.ldc + col0 : nullptr, p.ldc,
                            kCt ? (uint16_t*)p.ct + col0 * p.ldct + row0 : nullptr, p.ldct, mirror, p.alpha, p.beta,
                            diag ? (int32_t)row0 : -1, lds);
@@ -479,15 +513,18 @@ __global__ __launch_bounds__(256) void muon_normalize_kernel(const float* __rest
     tile[r][cidx] = to_bf(v);
   }
   __syncthreads();
-  // direct layout D[r][c] = buf-shaped; transposed layout T[c][r]
+  // direct layout D[r][c] = buf-shaped; transposed layout T[c][r]; xt may be
+  // null (only the wide work matrix is wanted)
   uint16_t* direct = tall ? xt : x;
   uint16_t* trans = tall ? x : xt;
   const int64_t ld_direct = tall ? ldxt : ldx, ld_trans = tall ? ldx : ldxt;
   for (int e = threadIdx.x; e < 64 * 64; e += 256) {
     const int r = e >> 6, cidx = e & 63;
     // direct[tr + r][tc + cidx] = D(tr + r, tc + cidx); trans[tc + r][tr + cidx] = D(tr + cidx, tc + r)
-    if (tr + r < rows && tc + cidx < cols) APEXW_GLOBAL(uint16_t, direct)[(tr + r) * ld_direct + tc + cidx] = tile[r][cidx];
-    if (tc + r < cols && tr + cidx < rows) APEXW_GLOBAL(uint16_t, trans)[(tc + r) * ld_trans + tr + cidx] = tile[cidx][r];
+    if (direct && tr + r < rows && tc + cidx < cols)
+      APEXW_GLOBAL(uint16_t, direct)[(tr + r) * ld_direct + tc + cidx] = tile[r][cidx];
+    if (trans && tc + r < cols && tr + cidx < rows)
+      APEXW_GLOBAL(uint16_t, trans)[(tc + r) * ld_trans + tr + cidx] = tile[cidx][r];
   }
 }
 
@@ -520,6 +557,31 @@ __global__ __launch_bounds__(256) void muon_apply_kernel(void* __restrict__ p, c
     if (apply_wd) x = rnd<PD>(x * wd_factor);
     const float uu = bf(APEXW_GLOBAL(const uint16_t, u)[r * ldu + c]);
     store1<PD>(p, i, rnd<PD>(fmaf(neg_lr_eff, uu, x)));
+  }
+}
+
+// The same update with U given transposed, u[c * ldu + r] = U[r][c] (the wide
+// work matrix of a tall parameter): 64 x 64 tiles through LDS, so both U and p
+// are read and written along their rows.
+template <int PD>
+__global__ __launch_bounds__(256) void muon_apply_t_kernel(void* __restrict__ p, const uint16_t* __restrict__ u,
+                                                           int64_t rows, int64_t cols, int64_t ldu, float wd_factor,
+                                                           int apply_wd, float neg_lr_eff) {
+  __shared__ uint16_t tile[64][66];
+  const int64_t tr = (int64_t)blockIdx.y * 64, tc = (int64_t)blockIdx.x * 64;
+  for (int e = threadIdx.x; e < 64 * 64; e += 256) {
+    const int cc = e >> 6, rr = e & 63;
+    if (tc + cc < cols && tr + rr < rows) tile[cc][rr] = APEXW_GLOBAL(const uint16_t, u)[(tc + cc) * ldu + tr + rr];
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < 64 * 64; e += 256) {
+    const int rr = e >> 6, cc = e & 63;
+    if (tr + rr < rows && tc + cc < cols) {
+      const int64_t i = (tr + rr) * cols + tc + cc;
+      float x = load1<PD>(p, i);
+      if (apply_wd) x = rnd<PD>(x * wd_factor);
+      store1<PD>(p, i, rnd<PD>(fmaf(neg_lr_eff, bf(tile[cc][rr]), x)));
+    }
   }
 }
 
@@ -556,22 +618,28 @@ int apexw_launch_gemm_grouped(const apexw_gemm_problem* probs, const uint32_t* i
   const dim3 grid(n_wg), block(256);
   switch (kind) {
     case APEXW_GEMM_OUT_C:
-      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, false, false>), grid, block, 0, stream, probs, items, offsets);
+      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, false, false, false>), grid, block, 0, stream, probs, items, offsets);
       break;
     case APEXW_GEMM_OUT_C | APEXW_GEMM_ADD:
-      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, false, true>), grid, block, 0, stream, probs, items, offsets);
+      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, false, true, false>), grid, block, 0, stream, probs, items, offsets);
       break;
     case APEXW_GEMM_OUT_CT:
-      hipLaunchKernelGGL((gemm_nt_grouped_kernel<false, true, false>), grid, block, 0, stream, probs, items, offsets);
+      hipLaunchKernelGGL((gemm_nt_grouped_kernel<false, true, false, false>), grid, block, 0, stream, probs, items, offsets);
       break;
     case APEXW_GEMM_OUT_CT | APEXW_GEMM_ADD:
-      hipLaunchKernelGGL((gemm_nt_grouped_kernel<false, true, true>), grid, block, 0, stream, probs, items, offsets);
+      hipLaunchKernelGGL((gemm_nt_grouped_kernel<false, true, true, false>), grid, block, 0, stream, probs, items, offsets);
       break;
     case APEXW_GEMM_OUT_C | APEXW_GEMM_OUT_CT:
-      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, true, false>), grid, block, 0, stream, probs, items, offsets);
+      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, true, false, false>), grid, block, 0, stream, probs, items, offsets);
       break;
     case APEXW_GEMM_OUT_C | APEXW_GEMM_OUT_CT | APEXW_GEMM_ADD:
-      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, true, true>), grid, block, 0, stream, probs, items, offsets);
+      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, true, true, false>), grid, block, 0, stream, probs, items, offsets);
+      break;
+    case APEXW_GEMM_OUT_C | APEXW_GEMM_KIND_NN:
+      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, false, false, true>), grid, block, 0, stream, probs, items, offsets);
+      break;
+    case APEXW_GEMM_OUT_C | APEXW_GEMM_ADD | APEXW_GEMM_KIND_NN:
+      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, false, true, true>), grid, block, 0, stream, probs, items, offsets);
       break;
     default:
       return APEXW_ERR_ARG;
@@ -611,7 +679,21 @@ int apexw_launch_muon_prepare(float* buf, const void* g, int32_t g_dtype, int64_
 }
 
 int apexw_launch_muon_apply(void* p, int32_t p_dtype, const uint16_t* u, int64_t rows, int64_t cols, int64_t ldu,
-                            float wd_factor, int32_t apply_wd, float neg_lr_eff, hipStream_t stream) {
+                            int32_t u_transposed, float wd_factor, int32_t apply_wd, float neg_lr_eff,
+                            hipStream_t stream) {
+  if (u_transposed) {
+    const dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64));
+    if (p_dtype == APEXW_F32)
+      hipLaunchKernelGGL(muon_apply_t_kernel<APEXW_F32>, grid, dim3(256), 0, stream, p, u, rows, cols, ldu, wd_factor,
+                         apply_wd, neg_lr_eff);
+    else if (p_dtype == APEXW_BF16)
+      hipLaunchKernelGGL(muon_apply_t_kernel<APEXW_BF16>, grid, dim3(256), 0, stream, p, u, rows, cols, ldu, wd_factor,
+                         apply_wd, neg_lr_eff);
+    else
+      hipLaunchKernelGGL(muon_apply_t_kernel<APEXW_F16>, grid, dim3(256), 0, stream, p, u, rows, cols, ldu, wd_factor,
+                         apply_wd, neg_lr_eff);
+    return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
+  }
   const int64_t n = rows * cols;
   const bool vec = cols % 8 == 0 && ldu % 8 == 0 && (((uintptr_t)p | (uintptr_t)u) & 15u) == 0;
   const dim3 grid(grid_for(vec ? n / 8 : n));

@@ -5,8 +5,8 @@ the fp32-momentum configuration: same constructor, defaults, ``state`` keys
 (``step``, ``work_dtype``, ``momentum``) and ``load_state_dict`` dtype
 handling.  The step runs through libapexw_hip.so:
 
-* ``apexw_muon_prepare``: fp32 momentum update, the bf16 work matrix normalised
-  by its Frobenius norm, written in both orientations;
+* ``apexw_muon_prepare``: fp32 momentum update, the bf16 work matrix (the
+  wide orientation) normalised by its Frobenius norm;
 * ``NSPlan``: per iteration three bf16 MFMA GEMMs
   (``A = X X^T``; ``B = c A A + b A``; ``X = B X + a X``), each one grouped
   launch (``apexw_gemm_nt_grouped``) over every Muon matrix of the step; the
@@ -56,8 +56,8 @@ class NSWorkspace:
     """bf16 Newton-Schulz buffers for `batch` matrices whose wide work shape is m x n.
 
     Dimensions are padded to the GEMM tile; the padding is zero and stays zero
-    through every product.  X and its transpose are kept for two iterations
-    (ping-pong), plus the symmetric A and B.
+    through every product.  X is kept for two iterations (ping-pong), plus the
+    symmetric A and B.
     """
 
     def __init__(self, m, n, batch, device):
@@ -66,7 +66,6 @@ class NSWorkspace:
         self.mp, self.np_ = _pad(m, t), _pad(n, t)
         z = lambda *s: torch.zeros(*s, dtype=torch.bfloat16, device=device)  # noqa: E731
         self.x = [z(batch, self.mp, self.np_), z(batch, self.mp, self.np_)]
-        self.xt = [z(batch, self.np_, self.mp), z(batch, self.np_, self.mp)]
         self.a = z(batch, self.mp, self.mp)
         self.b = z(batch, self.mp, self.mp)
         lib = _lib.load()
@@ -78,20 +77,22 @@ def _ns_problems(ws, phase, cur, out):
     """Append the GEMM problems of one Newton-Schulz product for every matrix of ws.
 
     phase 0: A = X X^T (symmetric); phase 1: B = c A A + b A (symmetric);
-    phase 2: X' = B X + a X, read from X^T rows and written in both layouts.
-    cur is the ping-pong slot holding the current X.
+    phase 2: X' = B X + a X with X read as [K x N] rows and the addend a X
+    taken from that same operand on the matrix cores.  cur is the ping-pong
+    slot holding the current X.
     """
     mp, np_ = ws.mp, ws.np_
     for e in range(ws.batch):
-        x, xt = ws.x[cur][e].data_ptr(), ws.xt[cur][e].data_ptr()
+        x = ws.x[cur][e].data_ptr()
         a, b = ws.a[e].data_ptr(), ws.b[e].data_ptr()
         if phase == 0:
             out.append((x, x, 0, a, a, mp, mp, np_, np_, np_, 0, mp, mp, 1.0, 0.0, _lib.GEMM_SYM, 0))
         elif phase == 1:
             out.append((a, a, a, b, b, mp, mp, mp, mp, mp, mp, mp, mp, NS_C, NS_B, _lib.GEMM_SYM, 0))
         else:
-            nx, nxt = ws.x[cur ^ 1][e].data_ptr(), ws.xt[cur ^ 1][e].data_ptr()
-            out.append((b, xt, xt, nx, nxt, mp, np_, mp, mp, mp, mp, np_, mp, 1.0, NS_A, 0, 0))
+            nx = ws.x[cur ^ 1][e].data_ptr()
+            out.append((b, x, 0, nx, 0, mp, np_, mp, mp, np_, 0, np_, 0, 1.0, NS_A,
+                        _lib.GEMM_B_KN | _lib.GEMM_ADD_B, 0))
 
 
 class NSPlan:
@@ -295,7 +296,7 @@ class ApexMuon(Optimizer):
             g = p.grad if p.grad.is_contiguous() else p.grad.contiguous()
             _lib.check(lib.apexw_muon_prepare(
                 st["momentum"].data_ptr(), g.data_ptr(), _dtype_code(g.dtype), rows, cols, mu, 1.0 - mu,
-                int(bool(group["nesterov"])), NS_EPS, ws.x[0][i].data_ptr(), ws.xt[0][i].data_ptr(), ws.np_, ws.mp,
+                int(bool(group["nesterov"])), NS_EPS, ws.x[0][i].data_ptr(), None, ws.np_, 0,
                 ws.partial[i].data_ptr(), stream), "apexw_muon_prepare")
         return {"plist": plist, "group": group, "ws": ws, "rows": rows, "cols": cols,
                 "steps": int(group["ns_steps"]), "batched": len(plist) > 1}
@@ -313,11 +314,12 @@ class ApexMuon(Optimizer):
         if job["batched"]:
             # torch._foreach_mul_ / _foreach_add_ over same-dtype lists see the scalars in p's dtype
             wd_factor, neg_lr = _round_to(p0.dtype, wd_factor), _round_to(p0.dtype, neg_lr)
-        # U in p's layout: the work matrix when wide, its transpose when tall
-        u_buf, ldu = (ws.xt[res], ws.mp) if rows > cols else (ws.x[res], ws.np_)
+        # U is the wide work matrix: p's layout when wide, its transpose when tall
+        u_buf = ws.x[res]
         for i, p in enumerate(plist):
-            _lib.check(lib.apexw_muon_apply(p.data_ptr(), _dtype_code(p.dtype), u_buf[i].data_ptr(), rows, cols, ldu,
-                                            wd_factor, int(wd != 0.0), neg_lr, stream), "apexw_muon_apply")
+            _lib.check(lib.apexw_muon_apply(p.data_ptr(), _dtype_code(p.dtype), u_buf[i].data_ptr(), rows, cols,
+                                            ws.np_, int(rows > cols), wd_factor, int(wd != 0.0), neg_lr, stream),
+                       "apexw_muon_apply")
 
     def get_state_memory_mb(self):
         tot = 0

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define APEXW_ABI_VERSION 3
+#define APEXW_ABI_VERSION 4
 
 /* status codes */
 enum apexw_status {
@@ -211,8 +211,8 @@ int apexw_gemm_nt_bf16(const void* a, const void* b, const void* et, void* c, vo
  */
 typedef struct apexw_gemm_problem {
   const void* a;       /* [m x k] bf16, lda */
-  const void* b;       /* [n x k] bf16, ldb */
-  const void* et;      /* E transposed, [n x m], lde; NULL when beta == 0 */
+  const void* b;       /* [n x k] bf16, ldb ([k x n] with APEXW_GEMM_B_KN) */
+  const void* et;      /* E transposed, [n x m], lde; NULL when beta == 0 or APEXW_GEMM_ADD_B */
   void* c;             /* [m x n] output, ldc; NULL = not written */
   void* ct;            /* [n x m] transposed output, ldct; NULL = not written */
   int32_t m, n, k;
@@ -227,11 +227,20 @@ typedef struct apexw_gemm_problem {
  * are computed; each off-diagonal tile is also stored mirrored, so c receives
  * the whole matrix.  E, when added, must be symmetric. */
 #define APEXW_GEMM_SYM 1u
+/* B is given as [k x n] row-major (ldb >= n): O = alpha A B + beta E.  Not with
+ * APEXW_GEMM_SYM; only row-major output (ct NULL). */
+#define APEXW_GEMM_B_KN 2u
+/* The addend is the B operand read at K = row: E[i][j] = B[j][i] ([n x k] B) or
+ * B[i][j] (APEXW_GEMM_B_KN), as in X' = B X + a X.  Requires alpha == 1,
+ * m <= k, beta != 0 and et NULL; it is accumulated on the matrix cores (beta
+ * as two bf16 parts, within 2^-18 of beta) instead of read in the epilogue. */
+#define APEXW_GEMM_ADD_B 4u
 
 /* epilogue kinds of a grouped launch (bit mask) */
 #define APEXW_GEMM_OUT_C 1   /* row-major output */
 #define APEXW_GEMM_OUT_CT 2  /* transposed output */
 #define APEXW_GEMM_ADD 4     /* beta * E added */
+#define APEXW_GEMM_KIND_NN 8 /* B given as [k x n] (APEXW_GEMM_B_KN) */
 
 /* Tile queues of a grouped launch: one per XCD of MI355X. */
 #define APEXW_GEMM_QUEUES 8
@@ -275,9 +284,10 @@ int64_t apexw_muon_workspace_floats(int64_t rows, int64_t cols);
  *                                         +-Inf -> +-65504; g dtype F32/BF16/F16)
  *   s   = buf, or lerp(g, buf, mu) when nesterov
  *   X   = bf16(bf16(s) / bf16(bf16(||bf16(s)||_F) + eps))
- * X is written as the wide work matrix [min x max] to x (ldx) and as its
- * transpose [max x min] to xt (ldxt): when rows > cols the work matrix is s^T.
- * Elements of x / xt outside the matrix are not written (keep them zero).
+ * X is written as the wide work matrix [min x max] to x (ldx) and, when xt is
+ * not NULL, as its transpose [max x min] to xt (ldxt): when rows > cols the
+ * work matrix is s^T.  Elements of x / xt outside the matrix are not written
+ * (keep them zero).
  */
 int apexw_muon_prepare(float* buf, const void* g, int32_t g_dtype, int64_t rows, int64_t cols,
                        float mu, float one_minus_mu, int32_t nesterov, float eps,
@@ -286,10 +296,12 @@ int apexw_muon_prepare(float* buf, const void* g, int32_t g_dtype, int64_t rows,
 /*
  * p = round(round(p * wd_factor) + neg_lr_eff * U)   (the decay only if apply_wd)
  * with U the bf16 Newton-Schulz result in p's [rows x cols] layout (leading
- * dimension ldu); p dtype F32/BF16/F16, rounded to nearest even.
+ * dimension ldu), or, when u_transposed, given as U^T [cols x rows] (the wide
+ * work matrix of a tall parameter); p dtype F32/BF16/F16, rounded to nearest
+ * even.
  */
 int apexw_muon_apply(void* p, int32_t p_dtype, const void* u, int64_t rows, int64_t cols, int64_t ldu,
-                     float wd_factor, int32_t apply_wd, float neg_lr_eff, void* stream);
+                     int32_t u_transposed, float wd_factor, int32_t apply_wd, float neg_lr_eff, void* stream);
 
 #ifdef __cplusplus
 }

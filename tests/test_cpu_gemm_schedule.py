@@ -20,13 +20,15 @@ def _prob(a, b, et, c, ct, m, n, k, lda, ldb, lde, ldc, ldct, alpha=1.0, beta=0.
 
 
 def _ns_problems(m, n, batch, base):
-    """The three Newton-Schulz products of `batch` m x n work matrices (m <= n)."""
+    """The three Newton-Schulz products of `batch` m x n work matrices (m <= n),
+    as the optimizer issues them (X' = B X + a X with X as [K x N] rows and the
+    addend taken from that operand)."""
     xx, aa, bx = [], [], []
     for e in range(batch):
-        x, xt, a, b, nx, nxt = (base + (6 * e + i) * (1 << 32) for i in range(6))
+        x, a, b, nx = (base + (4 * e + i) * (1 << 32) for i in range(4))
         xx.append(_prob(x, x, 0, a, a, m, m, n, n, n, 0, m, m, flags=_lib.GEMM_SYM))
         aa.append(_prob(a, a, a, b, b, m, m, m, m, m, m, m, m, NS_C, NS_B, _lib.GEMM_SYM))
-        bx.append(_prob(b, xt, xt, nx, nxt, m, n, m, m, m, m, n, m, 1.0, NS_A))
+        bx.append(_prob(b, x, 0, nx, 0, m, n, m, m, n, 0, n, 0, 1.0, NS_A, _lib.GEMM_B_KN | _lib.GEMM_ADD_B))
     return xx, aa, bx
 
 
@@ -55,7 +57,7 @@ def _expected_tiles(probs):
 
 @pytest.mark.parametrize("phase,kind", [(0, _lib.GEMM_OUT_C | _lib.GEMM_OUT_CT),
                                         (1, _lib.GEMM_OUT_C | _lib.GEMM_OUT_CT | _lib.GEMM_ADD),
-                                        (2, _lib.GEMM_OUT_C | _lib.GEMM_OUT_CT | _lib.GEMM_ADD)])
+                                        (2, _lib.GEMM_OUT_C | _lib.GEMM_ADD | _lib.GEMM_KIND_NN)])
 def test_schedule_covers_every_tile_once_in_balanced_bands(phase, kind):
     probs = _c5_phases()[phase]
     items, offsets, n_wg, got_kind = _lib.gemm_schedule(np.array(probs, dtype=_lib.GEMM_PROBLEM_DTYPE))
@@ -133,10 +135,29 @@ def test_schedule_rejects_invalid_problems():
     bad[0][8] = 256                                       # lda < k
     assert status(bad) == 1
     bad = [list(bx[0])]
-    bad[0][16] = 1                                        # reserved field
+    bad[0][9] = 512                                       # [k x n] B with ldb < n
     assert status(bad) == 1
     bad = [list(bx[0])]
+    bad[0][16] = 1                                        # reserved field
+    assert status(bad) == 1
+    bad = [list(aa[0])]
     bad[0][2] = 0                                         # beta != 0 without an addend
+    assert status(bad) == 1
+    bad = [list(bx[0])]
+    bad[0][13] = 2.0                                      # addend from B needs alpha == 1
+    assert status(bad) == 1
+    bad = [list(bx[0])]
+    bad[0][2] = bad[0][0]                                 # addend from B takes no et
+    assert status(bad) == 1
+    bad = [list(bx[0])]
+    bad[0][4] = bad[0][3] + (1 << 20)                     # [k x n] B writes no transposed output
+    assert status(bad) == 1
+    bad = [list(xx[0])]
+    bad[0][15] |= _lib.GEMM_B_KN                          # symmetric product with [k x n] B
+    assert status(bad) == 1
+    bad = [list(bx[0])]
+    bad[0][5], bad[0][6], bad[0][7] = 768, 512, 512       # addend from B needs m <= k
+    bad[0][8], bad[0][9], bad[0][11] = 512, 512, 512
     assert status(bad) == 1
     assert status([bx[0]] * 257) == 1                     # more problems than the item code holds
     # a launch mixes no epilogue kinds
@@ -147,4 +168,5 @@ def test_schedule_rejects_invalid_problems():
     assert lib.apexw_gemm_nt_grouped(None, None, None, 16, 3, None) == 1
     assert lib.apexw_gemm_nt_grouped(16, 16, 16, 16, 4, None) == 1     # no output in the kind
     assert lib.apexw_gemm_nt_grouped(16, 16, 16, 12, 3, None) == 1     # grid not a multiple of the queues
+    assert lib.apexw_gemm_nt_grouped(16, 16, 16, 16, 2 | 8, None) == 1  # [k x n] B with a transposed output
     assert lib.apexw_gemm_nt_grouped(16, 18, 16, 16, 3, None) == 4     # misaligned table

@@ -243,6 +243,15 @@ def test_grouped_gemm_symmetric_and_plain_products():
     for b, x, c, ct in zip(dB, X, dC, dCt):
         _assert_gemm_close(c, b.float().cpu() @ x.float() + NS_A * x.float())
         assert torch.equal(ct.cpu().t(), c.cpu())
+    # the same product with X as [K x N] rows (transposing LDS reads) and the
+    # addend taken from that operand on the matrix cores (beta within 2^-18)
+    for c in dC:
+        c.fill_(float("nan"))
+    KN = _lib.GEMM_B_KN | _lib.GEMM_ADD_B
+    _grouped(lib, [(b.data_ptr(), x.data_ptr(), 0, c.data_ptr(), 0, m, n, m, m, n, 0, n, 0, 1.0, NS_A, KN, 0)
+                   for b, x, c, (m, n) in zip(dB, dX, dC, shapes)])
+    for b, x, c in zip(dB, X, dC):
+        _assert_gemm_close(c, b.float().cpu() @ x.float() + NS_A * x.float())
 
 
 def test_muon_groups_with_different_ns_steps_and_many_matrices():

@@ -13,7 +13,7 @@ import numpy as np
 
 from ._build import LIB_PATH
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # dtype codes
 F32, BF16, F16, U8, I8 = 0, 1, 2, 3, 4
@@ -37,6 +37,7 @@ HP_SANITIZE = 1 << 2
 HP_CLIP = 1 << 3
 HP_LERP_HI = 1 << 4
 HP_LOOK_HI = 1 << 5
+HP_UNSCALE = 1 << 6
 
 STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported dtype combination", 3: "launch failed",
           4: "misaligned pointer"}
@@ -64,7 +65,7 @@ class HParams(ctypes.Structure):
                 ("lerp_coef", ctypes.c_float), ("look_coef", ctypes.c_float),
                 ("bc2_sqrt", ctypes.c_float), ("gain_hi", ctypes.c_float), ("gain_lo", ctypes.c_float),
                 ("clip_coef", ctypes.c_void_p), ("seed", ctypes.c_uint64), ("step", ctypes.c_uint32),
-                ("mode", ctypes.c_uint32), ("flags", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
+                ("mode", ctypes.c_uint32), ("flags", ctypes.c_uint32), ("grad_inv_scale", ctypes.c_float)]
 
 
 # apexw_gemm_problem: one product of a grouped launch
@@ -89,7 +90,7 @@ SIGNATURES = {
     "apexw_check_tensor": (ctypes.c_int, [ctypes.POINTER(Tensor), _i32]),
     "apexw_compact_step": (ctypes.c_int, [_vp, _i32, _vp, _i64, _HP, _vp]),
     "apexw_q8_step": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _i64, _HP, _vp]),
-    "apexw_grad_clip_coef": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _vp, _vp, _vp, _f32, _u32, _vp, _vp]),
+    "apexw_grad_clip_coef": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _vp, _vp, _vp, _f32, _f32, _u32, _vp, _vp]),
     "apexw_gemm_nt_bf16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                           _i32, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _vp]),
     "apexw_gemm_grouped_items": (ctypes.c_int64, [_vp, _i32]),
@@ -97,8 +98,8 @@ SIGNATURES = {
                                                    ctypes.POINTER(ctypes.c_int32)]),
     "apexw_gemm_nt_grouped": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, _vp]),
     "apexw_muon_workspace_floats": (ctypes.c_int64, [_i64, _i64]),
-    "apexw_muon_prepare": (ctypes.c_int, [_vp, _vp, _i32, _i64, _i64, _f32, _f32, _i32, _f32, _vp, _vp, _i64, _i64,
-                                          _vp, _vp]),
+    "apexw_muon_prepare": (ctypes.c_int, [_vp, _vp, _i32, _i64, _i64, _f32, _f32, _i32, _f32, _f32, _vp, _vp, _i64,
+                                          _i64, _vp, _vp]),
     "apexw_muon_apply": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _i64, _i32, _f32, _i32, _f32, _vp]),
 }
 

@@ -238,7 +238,7 @@ class StepPlan:
         return (self._fast_static & ~scalar) if self.kind == "q8" else None
 
     # ------------------------------------------------------------------ launch
-    def _clip(self, clip, sanitize, stream):
+    def _clip(self, clip, sanitize, inv_scale, stream):
         if self.clip_ws is None:
             self.clip_ws = (torch.empty(max(self.n_units, 1), dtype=torch.float32, device=self.device),
                             torch.empty(len(self.params), dtype=torch.float32, device=self.device),
@@ -248,12 +248,15 @@ class StepPlan:
         st = self._lib.apexw_grad_clip_coef(
             self.d_table.data_ptr(), len(self.params), self.d_units.data_ptr(), self.n_units, unit,
             self.d_unit_begin.data_ptr(), part.data_ptr(), norms.data_ptr(), float(clip),
-            L.HP_SANITIZE if sanitize else 0, coef.data_ptr(), stream)
+            1.0 if inv_scale is None else inv_scale,
+            (L.HP_SANITIZE if sanitize else 0) | (L.HP_UNSCALE if inv_scale is not None else 0), coef.data_ptr(), stream)
         L.check(st, "apexw_grad_clip_coef")
         return coef
 
-    def execute(self, group, seed):
-        """Run one optimizer step for the group (cold the first time, replay after)."""
+    def execute(self, group, seed, inv_scale=None):
+        """Run one optimizer step for the group (cold the first time, replay after).
+
+        inv_scale: 1 / the AMP grad scale handed over by GradScaler, or None."""
         mode_cold = not self.cold_done
         grads = self._refresh_grads()  # noqa: F841 -- keeps contiguous copies alive until the launch
         stream = torch.cuda.current_stream(self.device).cuda_stream
@@ -264,7 +267,7 @@ class StepPlan:
             sanitize = mode_cold or clip is not None
         else:
             sanitize = mode_cold and clip is not None
-        coef = self._clip(clip, sanitize, stream) if clip is not None else None
+        coef = self._clip(clip, sanitize, inv_scale, stream) if clip is not None else None
         self.steps.add_(1.0)
         # The reference's replayed compact step takes the bias correction of the
         # first counter for the whole group (optimizer.py:1082-1090); every other
@@ -274,7 +277,7 @@ class StepPlan:
         else:
             groups = [(None, int(self.steps[0].item()))]
         for units, step in groups:
-            hp = self._hparams(lr, b1, b2, eps, wd, step, sr, sanitize, coef, seed, mode_cold)
+            hp = self._hparams(lr, b1, b2, eps, wd, step, sr, sanitize, coef, seed, mode_cold, inv_scale)
             if units is None:
                 d_units, n_units, n_fast, n_fast32 = self.d_units, self.n_units, self.n_fast_units, self.n_fast_f32_units
             else:
@@ -301,7 +304,7 @@ class StepPlan:
             out.append(((sel, int(mask.sum()), int(mask[:nb].sum()), int(mask[nb:nb + nf].sum())), int(val)))
         return out
 
-    def _hparams(self, lr, b1, b2, eps, wd, step, sr, sanitize, coef, seed, cold):
+    def _hparams(self, lr, b1, b2, eps, wd, step, sr, sanitize, coef, seed, cold, inv_scale=None):
         hp = L.HParams()
         bc1 = 1.0 - b1 ** step
         bc2 = 1.0 - b2 ** step
@@ -345,6 +348,9 @@ class StepPlan:
         if coef is not None:
             flags |= L.HP_CLIP
             hp.clip_coef = coef.data_ptr()
+        if inv_scale is not None:
+            flags |= L.HP_UNSCALE
+            hp.grad_inv_scale = inv_scale
         hp.seed = seed
         hp.step = step & 0xFFFFFFFF
         hp.flags = flags

@@ -17,7 +17,7 @@ int apexw_launch_q8(const apexw_tensor*, int64_t, const apexw_unit*, const apexw
 int apexw_launch_q8_fast(const apexw_tensor*, int64_t, const apexw_unit*, const apexw_hparams*, int32_t, hipStream_t);
 bool apexw_q8_fast_eligible(uint32_t flags, uint32_t block);
 int apexw_launch_clip(const apexw_tensor*, int32_t, const apexw_unit*, int64_t, int64_t, const int64_t*, float*, float*,
-                      float, uint32_t, float*, hipStream_t);
+                      float, float, uint32_t, float*, hipStream_t);
 bool apexw_compact_flags_ok(uint32_t flags);
 int apexw_launch_gemm_nt(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, uint16_t*, int32_t, int32_t,
                          int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int64_t, int64_t, int64_t,
@@ -25,8 +25,8 @@ int apexw_launch_gemm_nt(const uint16_t*, const uint16_t*, const uint16_t*, uint
 int apexw_muon_partials(int64_t n);
 int apexw_launch_gemm_grouped(const apexw_gemm_problem*, const uint32_t*, const int32_t*, int32_t, int32_t,
                               hipStream_t);
-int apexw_launch_muon_prepare(float*, const void*, int32_t, int64_t, int64_t, float, float, int32_t, float, uint16_t*,
-                              uint16_t*, int64_t, int64_t, float*, hipStream_t);
+int apexw_launch_muon_prepare(float*, const void*, int32_t, int64_t, int64_t, float, float, int32_t, float, float,
+                              uint16_t*, uint16_t*, int64_t, int64_t, float*, hipStream_t);
 int apexw_launch_muon_apply(void*, int32_t, const uint16_t*, int64_t, int64_t, int64_t, int32_t, float, int32_t,
                             float, hipStream_t);
 bool apexw_q8_flags_ok(uint32_t flags, uint32_t block, int64_t n);
@@ -75,6 +75,7 @@ bool hp_ok(const apexw_hparams* hp) {
   if (!hp) return false;
   if (hp->mode > APEXW_MODE_NATIVE) return false;
   if ((hp->flags & APEXW_HP_CLIP) && !hp->clip_coef) return false;
+  if ((hp->flags & APEXW_HP_UNSCALE) && !(hp->grad_inv_scale > 0.0f)) return false;
   return true;
 }
 
@@ -290,15 +291,16 @@ int64_t apexw_muon_workspace_floats(int64_t rows, int64_t cols) {
 }
 
 int apexw_muon_prepare(float* buf, const void* g, int32_t g_dtype, int64_t rows, int64_t cols, float mu,
-                       float one_minus_mu, int32_t nesterov, float eps, void* x, void* xt, int64_t ldx, int64_t ldxt,
-                       float* workspace, void* stream) {
+                       float one_minus_mu, int32_t nesterov, float eps, float grad_inv_scale, void* x, void* xt,
+                       int64_t ldx, int64_t ldxt, float* workspace, void* stream) {
   if (!buf || !g || !x || !workspace || rows <= 0 || cols <= 0) return APEXW_ERR_ARG;
   if (g_dtype != APEXW_F32 && g_dtype != APEXW_BF16 && g_dtype != APEXW_F16) return APEXW_ERR_DTYPE;
   // work matrix X is [min x max], X^T is [max x min] (optional)
   const int64_t lo = rows < cols ? rows : cols, hi = rows < cols ? cols : rows;
   if (ldx < hi || (xt && ldxt < lo)) return APEXW_ERR_ARG;
-  return apexw_launch_muon_prepare(buf, g, g_dtype, rows, cols, mu, one_minus_mu, nesterov, eps, (uint16_t*)x,
-                                   (uint16_t*)xt, ldx, ldxt, workspace, (hipStream_t)stream);
+  if (!(grad_inv_scale > 0.0f)) return APEXW_ERR_ARG;
+  return apexw_launch_muon_prepare(buf, g, g_dtype, rows, cols, mu, one_minus_mu, nesterov, eps, grad_inv_scale,
+                                   (uint16_t*)x, (uint16_t*)xt, ldx, ldxt, workspace, (hipStream_t)stream);
 }
 
 int apexw_muon_apply(void* p, int32_t p_dtype, const void* u, int64_t rows, int64_t cols, int64_t ldu,
@@ -312,11 +314,12 @@ int apexw_muon_apply(void* p, int32_t p_dtype, const void* u, int64_t rows, int6
 
 int apexw_grad_clip_coef(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,
                          int64_t unit_size, const int64_t* unit_begin, float* unit_partial, float* tensor_norm,
-                         float clip, uint32_t flags, float* coef, void* stream) {
+                         float clip, float grad_inv_scale, uint32_t flags, float* coef, void* stream) {
   if (!tensors || !units || !unit_begin || !unit_partial || !tensor_norm || !coef) return APEXW_ERR_ARG;
   if (n_tensors <= 0 || n_units < 0 || unit_size < 0 || !(clip > 0.0f)) return APEXW_ERR_ARG;
+  if ((flags & APEXW_HP_UNSCALE) && !(grad_inv_scale > 0.0f)) return APEXW_ERR_ARG;
   return apexw_launch_clip(tensors, n_tensors, units, n_units, unit_size, unit_begin, unit_partial, tensor_norm, clip,
-                           flags, coef, (hipStream_t)stream);
+                           grad_inv_scale, flags, coef, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -27,8 +27,11 @@ struct Ctx {
   uint32_t tflags;
 };
 
+// sanitize, AMP unscale (in place on the grads: _multi_tensor_step,
+// apexw/optimizer.py:5530-5537, or _prepare_grads before a clip), clip
 template <int GD> APEXW_DEV float prep_grad(float g, const Ctx& c) {
   if (c.hp->flags & APEXW_HP_SANITIZE) g = sanitize<GD>(g);
+  if (c.hp->flags & APEXW_HP_UNSCALE) g = rnd<GD>(g * c.hp->grad_inv_scale);
   if (c.hp->flags & APEXW_HP_CLIP) g = rnd<GD>(g * c.coef);
   return g;
 }

@@ -14,8 +14,10 @@
 
 namespace {
 
+// squares of sanitize(g) (when san), unscaled in the grad dtype when unscale
+// (AMP grads are unscaled before the clip, apexw/optimizer.py:227-237)
 template <int GD>
-APEXW_DEV float unit_sumsq(const apexw_tensor& t, int64_t start, int64_t cnt, bool san) {
+APEXW_DEV float unit_sumsq(const apexw_tensor& t, int64_t start, int64_t cnt, bool san, bool unscale, float inv) {
   const int lane = lane_id();
   const bool vec = !(t.flags & APEXW_FLAG_SCALAR) && (start % 8) == 0;
   float acc = 0.0f;
@@ -31,7 +33,8 @@ APEXW_DEV float unit_sumsq(const apexw_tensor& t, int64_t start, int64_t cnt, bo
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float x = san ? sanitize<GD>(g[j]) : g[j];
+      float x = san ? sanitize<GD>(g[j]) : g[j];
+      if (unscale) x = rnd<GD>(x * inv);
       acc = fmaf(x, x, acc);
     }
   }
@@ -40,10 +43,11 @@ APEXW_DEV float unit_sumsq(const apexw_tensor& t, int64_t start, int64_t cnt, bo
 
 __global__ __launch_bounds__(256) void sumsq_kernel(const apexw_tensor* __restrict__ tensors,
                                                     const apexw_unit* __restrict__ units, int64_t n_units,
-                                                    int64_t unit_size, float* __restrict__ partial, uint32_t flags) {
+                                                    int64_t unit_size, float* __restrict__ partial, uint32_t flags,
+                                                    float inv) {
   const uint32_t wave = uniform(threadIdx.x >> 6);
   const int64_t stride = (int64_t)gridDim.x * 4;
-  const bool san = flags & APEXW_HP_SANITIZE;
+  const bool san = flags & APEXW_HP_SANITIZE, unscale = flags & APEXW_HP_UNSCALE;
   for (int64_t u = (int64_t)blockIdx.x * 4 + wave; u < n_units; u += stride) {
     const apexw_unit un = units[u];
     const apexw_tensor& t = tensors[un.tensor];
@@ -52,9 +56,9 @@ __global__ __launch_bounds__(256) void sumsq_kernel(const apexw_tensor* __restri
     const int64_t cnt = (t.n - start) < us ? (t.n - start) : us;
     const uint32_t gd = (t.flags >> APEXW_FLAG_GDT_SHIFT) & 3u;
     float s;
-    if (gd == APEXW_F32) s = unit_sumsq<APEXW_F32>(t, start, cnt, san);
-    else if (gd == APEXW_BF16) s = unit_sumsq<APEXW_BF16>(t, start, cnt, san);
-    else s = unit_sumsq<APEXW_F16>(t, start, cnt, san);
+    if (gd == APEXW_F32) s = unit_sumsq<APEXW_F32>(t, start, cnt, san, unscale, inv);
+    else if (gd == APEXW_BF16) s = unit_sumsq<APEXW_BF16>(t, start, cnt, san, unscale, inv);
+    else s = unit_sumsq<APEXW_F16>(t, start, cnt, san, unscale, inv);
     if (lane_id() == 0) partial[u] = s;
   }
 }
@@ -97,11 +101,11 @@ __global__ __launch_bounds__(1024) void clip_coef_kernel(const float* __restrict
 
 int apexw_launch_clip(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,
                       int64_t unit_size, const int64_t* unit_begin, float* unit_partial, float* tensor_norm,
-                      float clip, uint32_t flags, float* coef, hipStream_t stream) {
+                      float clip, float inv, uint32_t flags, float* coef, hipStream_t stream) {
   if (n_units > 0) {
     const int grid_units = apexw_resident_grid((const void*)sumsq_kernel, n_units);
     hipLaunchKernelGGL(sumsq_kernel, dim3(grid_units), dim3(256), 0, stream, tensors, units, n_units, unit_size,
-                       unit_partial, flags);
+                       unit_partial, flags, inv);
   }
   if (n_tensors > 0) {
     const int grid_tensors = apexw_resident_grid((const void*)tensor_norm_kernel, n_tensors);

@@ -428,8 +428,11 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_grouped_kernel(const apexw_gem
 // Nesterov.  Per-block partial sums of squares of bf16(update source) give the
 // Frobenius norm of the bf16 work matrix.
 // ---------------------------------------------------------------------------
-template <int GD> APEXW_DEV float muon_grad(const void* grad, int64_t i) {
+// the reference unscales p.grad in place (grad dtype) before the step
+// (apexw/muon.py:566-590), then the momentum update sanitizes it
+template <int GD> APEXW_DEV float muon_grad(const void* grad, int64_t i, float inv) {
   float g = load1<GD>(grad, i);
+  if (inv != 1.0f) g = rnd<GD>(g * inv);
   if (__builtin_isnan(g)) return 0.0f;
   if (__builtin_isinf(g)) return g > 0.0f ? 65504.0f : -65504.0f;
   return g;
@@ -445,7 +448,7 @@ APEXW_DEV float nesterov_source(float g, float m, float mu) {
 template <int GD, bool VEC>
 __global__ __launch_bounds__(256) void muon_momentum_kernel(float* __restrict__ buf, const void* __restrict__ grad,
                                                             int64_t n, float mu, float one_minus_mu, int nesterov,
-                                                            float* __restrict__ partial) {
+                                                            float inv, float* __restrict__ partial) {
   float s = 0.0f;
   const int64_t tid = (int64_t)blockIdx.x * 256 + threadIdx.x, stride = (int64_t)gridDim.x * 256;
   const int64_t n_vec = VEC ? n / 8 * 8 : 0;
@@ -456,6 +459,7 @@ __global__ __launch_bounds__(256) void muon_momentum_kernel(float* __restrict__ 
       load8<APEXW_F32>(buf, i, m);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
+        if (inv != 1.0f) g[j] = rnd<GD>(g[j] * inv);
         if (__builtin_isnan(g[j])) g[j] = 0.0f;
         else if (__builtin_isinf(g[j])) g[j] = g[j] > 0.0f ? 65504.0f : -65504.0f;
         m[j] = fmaf(one_minus_mu, g[j], m[j] * mu);
@@ -466,7 +470,7 @@ __global__ __launch_bounds__(256) void muon_momentum_kernel(float* __restrict__ 
     }
   }
   for (int64_t i = n_vec + tid; i < n; i += stride) {
-    const float g = muon_grad<GD>(grad, i);
+    const float g = muon_grad<GD>(grad, i, inv);
     const float m = fmaf(one_minus_mu, g, APEXW_GLOBAL(float, buf)[i] * mu);
     APEXW_GLOBAL(float, buf)[i] = m;
     const float x = rnd<APEXW_BF16>(nesterov ? nesterov_source(g, m, mu) : m);
@@ -486,7 +490,7 @@ __global__ __launch_bounds__(256) void muon_momentum_kernel(float* __restrict__ 
 template <int GD>
 __global__ __launch_bounds__(256) void muon_normalize_kernel(const float* __restrict__ buf, const void* __restrict__ grad,
                                                              int64_t rows, int64_t cols, float mu, int nesterov,
-                                                             const float* __restrict__ partial, int n_partial,
+                                                             float inv, const float* __restrict__ partial, int n_partial,
                                                              float eps, int tall, uint16_t* __restrict__ x,
                                                              uint16_t* __restrict__ xt, int64_t ldx, int64_t ldxt) {
   __shared__ float red[4];
@@ -507,7 +511,7 @@ __global__ __launch_bounds__(256) void muon_normalize_kernel(const float* __rest
     if (gr < rows && gc < cols) {
       const int64_t i = gr * cols + gc;
       float m = APEXW_GLOBAL(const float, buf)[i];
-      if (nesterov) m = nesterov_source(muon_grad<GD>(grad, i), m, mu);
+      if (nesterov) m = nesterov_source(muon_grad<GD>(grad, i, inv), m, mu);
       v = rnd<APEXW_BF16>(m) / d;
     }
     tile[r][cidx] = to_bf(v);
@@ -651,30 +655,33 @@ int apexw_muon_partials(int64_t n) { return grid_for(n) < 1024 ? grid_for(n) : 1
 
 template <int GD>
 void launch_prepare(float* buf, const void* g, int64_t rows, int64_t cols, float mu, float one_minus_mu, int nesterov,
-                    float eps, uint16_t* x, uint16_t* xt, int64_t ldx, int64_t ldxt, float* partial,
+                    float eps, float inv, uint16_t* x, uint16_t* xt, int64_t ldx, int64_t ldxt, float* partial,
                     hipStream_t stream) {
   const int64_t n = rows * cols;
   const int nb = apexw_muon_partials(n);
   if ((((uintptr_t)buf | (uintptr_t)g) & 15u) == 0)
     hipLaunchKernelGGL((muon_momentum_kernel<GD, true>), dim3(nb), dim3(256), 0, stream, buf, g, n, mu, one_minus_mu,
-                       nesterov, partial);
+                       nesterov, inv, partial);
   else
     hipLaunchKernelGGL((muon_momentum_kernel<GD, false>), dim3(nb), dim3(256), 0, stream, buf, g, n, mu, one_minus_mu,
-                       nesterov, partial);
+                       nesterov, inv, partial);
   dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64));
-  hipLaunchKernelGGL(muon_normalize_kernel<GD>, grid, dim3(256), 0, stream, buf, g, rows, cols, mu, nesterov, partial,
-                     nb, eps, (int)(rows > cols), x, xt, ldx, ldxt);
+  hipLaunchKernelGGL(muon_normalize_kernel<GD>, grid, dim3(256), 0, stream, buf, g, rows, cols, mu, nesterov, inv,
+                     partial, nb, eps, (int)(rows > cols), x, xt, ldx, ldxt);
 }
 
 int apexw_launch_muon_prepare(float* buf, const void* g, int32_t g_dtype, int64_t rows, int64_t cols, float mu,
-                              float one_minus_mu, int32_t nesterov, float eps, uint16_t* x, uint16_t* xt, int64_t ldx,
-                              int64_t ldxt, float* partial, hipStream_t stream) {
+                              float one_minus_mu, int32_t nesterov, float eps, float inv, uint16_t* x, uint16_t* xt,
+                              int64_t ldx, int64_t ldxt, float* partial, hipStream_t stream) {
   if (g_dtype == APEXW_F32)
-    launch_prepare<APEXW_F32>(buf, g, rows, cols, mu, one_minus_mu, nesterov, eps, x, xt, ldx, ldxt, partial, stream);
+    launch_prepare<APEXW_F32>(buf, g, rows, cols, mu, one_minus_mu, nesterov, eps, inv, x, xt, ldx, ldxt, partial,
+                              stream);
   else if (g_dtype == APEXW_BF16)
-    launch_prepare<APEXW_BF16>(buf, g, rows, cols, mu, one_minus_mu, nesterov, eps, x, xt, ldx, ldxt, partial, stream);
+    launch_prepare<APEXW_BF16>(buf, g, rows, cols, mu, one_minus_mu, nesterov, eps, inv, x, xt, ldx, ldxt, partial,
+                               stream);
   else
-    launch_prepare<APEXW_F16>(buf, g, rows, cols, mu, one_minus_mu, nesterov, eps, x, xt, ldx, ldxt, partial, stream);
+    launch_prepare<APEXW_F16>(buf, g, rows, cols, mu, one_minus_mu, nesterov, eps, inv, x, xt, ldx, ldxt, partial,
+                              stream);
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }
 

@@ -104,14 +104,21 @@ APEXW_DEV uint32_t logu8_code_shared(float v, float vmax, float rvmax) {
 
 template <int GD> APEXW_DEV float q8_grad(float g, uint32_t tflags, const Q8Ctx& c) {
   const apexw_hparams& hp = *c.hp;
+  const bool unscale = hp.flags & APEXW_HP_UNSCALE, clip = hp.flags & APEXW_HP_CLIP;
   if (hp.flags & APEXW_HP_SANITIZE) g = sanitize<GD>(g);
-  if (hp.flags & APEXW_HP_CLIP) g = rnd<GD>(g * c.coef);
+  // AMP before a clip: _prepare_grads unscales in the grad dtype (apexw/optimizer.py:227-237)
+  if (unscale && clip) g = rnd<GD>(g * hp.grad_inv_scale);
+  if (clip) g = rnd<GD>(g * c.coef);
   // nan_to_num inside the step: on the fp32 copy (chunked) or on the grad dtype (generic)
-  if (__builtin_isnan(g)) return 0.0f;
-  if (__builtin_isinf(g)) {
+  if (__builtin_isnan(g)) {
+    g = 0.0f;
+  } else if (__builtin_isinf(g)) {
     const float big = (tflags & (APEXW_FLAG_GENERIC | APEXW_FLAG_DENSE16)) ? rnd<GD>(65504.0f) : 65504.0f;
-    return g > 0.0f ? big : -big;
+    g = g > 0.0f ? big : -big;
   }
+  // AMP without a clip: the step unscales its fp32 copy after nan_to_num
+  // (_prep_grad_chunk_fp32, apexw/state.py:326-347; apexw/optimizer.py:4500-4505)
+  if (unscale && !clip) g *= hp.grad_inv_scale;
   return g;
 }
 
@@ -487,7 +494,7 @@ APEXW_DEV void q8_block_fast(const apexw_tensor& t, uint32_t tix, uint32_t blk, 
     const uint32_t key = rng_key(hp.seed, tix, hp.step, 1u, (uint32_t)(start >> 32));
     rs = mix32(key + (blk << 6) + (uint32_t)lane) | 1u;
   }
-  const bool prep = hf & (APEXW_HP_SANITIZE | APEXW_HP_CLIP);
+  const bool prep = hf & (APEXW_HP_SANITIZE | APEXW_HP_CLIP | APEXW_HP_UNSCALE);
   const float msb1 = ms_old * hp.beta1;  // dequantisation scale folded into the momentum decay
 
   float mnew[4][8], vq[4][2];

@@ -240,8 +240,12 @@ class ApexMuon(Optimizer):
         try:
             if found_inf is not None and float(found_inf) != 0.0:
                 return loss
+            # AMP: the grads are unscaled inside the momentum kernel (the reference
+            # unscales p.grad in place first, apexw/muon.py:566-590)
+            inv_scale = 1.0
             if grad_scale is not None:
-                raise NotImplementedError("ApexMuon: GradScaler grad_scale hand-off is not supported; unscale first")
+                inv_scale = (float(grad_scale.reciprocal().item()) if torch.is_tensor(grad_scale)
+                             else 1.0 / float(grad_scale))
             jobs = []
             for gi, group in enumerate(self.param_groups):
                 active = [p for p in group["params"] if p.grad is not None]
@@ -264,7 +268,7 @@ class ApexMuon(Optimizer):
                     shapes[tuple(p.shape)].append(p)
                 for shape, plist in shapes.items():
                     # the reference batches same-shape matrices on the GPU (apexw/muon.py:593-615)
-                    jobs.append(self._prepare(gi, shape, plist, group))
+                    jobs.append(self._prepare(gi, shape, plist, group, inv_scale))
             # Newton-Schulz of every matrix, grouped per device; matrices are
             # independent, so running all momenta first and all updates last
             # gives each parameter the result of the reference's per-shape loop
@@ -280,7 +284,7 @@ class ApexMuon(Optimizer):
             self.found_inf = None
         return loss
 
-    def _prepare(self, gi, shape, plist, group):
+    def _prepare(self, gi, shape, plist, group, inv_scale=1.0):
         """Momentum update and normalised bf16 work matrix (both layouts) of one same-shape batch."""
         lib = _lib.load()
         p0 = plist[0]
@@ -296,7 +300,7 @@ class ApexMuon(Optimizer):
             g = p.grad if p.grad.is_contiguous() else p.grad.contiguous()
             _lib.check(lib.apexw_muon_prepare(
                 st["momentum"].data_ptr(), g.data_ptr(), _dtype_code(g.dtype), rows, cols, mu, 1.0 - mu,
-                int(bool(group["nesterov"])), NS_EPS, ws.x[0][i].data_ptr(), None, ws.np_, 0,
+                int(bool(group["nesterov"])), NS_EPS, inv_scale, ws.x[0][i].data_ptr(), None, ws.np_, 0,
                 ws.partial[i].data_ptr(), stream), "apexw_muon_prepare")
         return {"plist": plist, "group": group, "ws": ws, "rows": rows, "cols": cols,
                 "steps": int(group["ns_steps"]), "batched": len(plist) > 1}

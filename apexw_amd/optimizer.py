@@ -156,22 +156,29 @@ class ApexW(Optimizer):
         if closure is not None:
             with torch.enable_grad():
                 loss = closure()
+        # AMP: GradScaler hands over its scale and found_inf instead of unscaling
+        # (_step_supports_amp_scaling); an inf/NaN step is skipped, otherwise the
+        # grads are unscaled inside the step kernels (apexw/optimizer.py:3458-3480,
+        # :3627-3628)
         found_inf = getattr(self, "found_inf", None)
         if found_inf is not None and float(found_inf.item()) > 0:
             return loss
-        if getattr(self, "grad_scale", None) is not None:
-            raise NotImplementedError("GradScaler unscaling inside step() is not supported; unscale first")
+        grad_scale = getattr(self, "grad_scale", None)
+        inv_scale = None
+        if grad_scale is not None:
+            inv_scale = (float(grad_scale.reciprocal().item()) if torch.is_tensor(grad_scale)
+                         else 1.0 / float(grad_scale))
         for group in self.param_groups:
             gid = id(group)
             plan = self._plans.get(gid)
             if plan is not None and plan.valid_for(group):
-                plan.execute(group, self._seed)
+                plan.execute(group, self._seed, inv_scale)
                 continue
             self._plans.pop(gid, None)
             plan = self._build_plan(group)
             if plan is None:
                 continue
-            plan.execute(group, self._seed)
+            plan.execute(group, self._seed, inv_scale)
             self._plans[gid] = plan
         return loss
 

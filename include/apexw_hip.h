@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define APEXW_ABI_VERSION 4
+#define APEXW_ABI_VERSION 5
 
 /* status codes */
 enum apexw_status {
@@ -106,6 +106,9 @@ typedef struct apexw_unit {
 #define APEXW_HP_CLIP (1u << 3)       /* multiply grads by *clip_coef (rounded to grad dtype) */
 #define APEXW_HP_LERP_HI (1u << 4)    /* m lerp weight (1 - beta1) >= 0.5: end-based form */
 #define APEXW_HP_LOOK_HI (1u << 5)    /* 8-bit lookahead lerp weight (beta1) >= 0.5 */
+#define APEXW_HP_UNSCALE (1u << 6)    /* AMP: grads times grad_inv_scale (after sanitizing): in the
+                                         grad dtype for compact and before a clip, in fp32 after
+                                         the step's nan_to_num otherwise (8-bit) */
 
 /* Host-computed step scalars (the reference computes them in double). */
 typedef struct apexw_hparams {
@@ -123,7 +126,7 @@ typedef struct apexw_hparams {
   uint32_t step;
   uint32_t mode;
   uint32_t flags;
-  uint32_t reserved;
+  float grad_inv_scale; /* with APEXW_HP_UNSCALE: 1 / AMP grad scale (GradScaler) */
 } apexw_hparams;
 
 /* ABI version of the loaded library (APEXW_ABI_VERSION). */
@@ -169,12 +172,14 @@ int apexw_q8_step(const apexw_tensor* tensors, int32_t n_tensors,
  *   *coef = min(clip / (total + 1e-6), 1)   (1 when total is not finite).
  * unit_partial: n_units floats of workspace; tensor_norm: n_tensors floats;
  * unit_begin: n_tensors + 1 int64 prefix offsets of each tensor's units.
- * flags: APEXW_HP_SANITIZE to sanitize grads before squaring.
+ * flags: APEXW_HP_SANITIZE to sanitize grads before squaring; APEXW_HP_UNSCALE
+ * to take the norm of dtype_round(g * grad_inv_scale) (AMP grads are unscaled
+ * before the clip, apexw/optimizer.py:227-237).
  */
 int apexw_grad_clip_coef(const apexw_tensor* tensors, int32_t n_tensors,
                          const apexw_unit* units, int64_t n_units, int64_t unit_size,
                          const int64_t* unit_begin, float* unit_partial, float* tensor_norm,
-                         float clip, uint32_t flags, float* coef, void* stream);
+                         float clip, float grad_inv_scale, uint32_t flags, float* coef, void* stream);
 
 /* ------------------------------------------------------------------------- */
 /* Muon: Newton-Schulz on the matrix cores                                    */
@@ -280,8 +285,9 @@ int64_t apexw_muon_workspace_floats(int64_t rows, int64_t cols);
 
 /*
  * Muon momentum and Newton-Schulz input for one [rows x cols] parameter:
- *   buf = buf * mu + (1 - mu) * g        (fp32 buffer; g sanitized NaN -> 0,
- *                                         +-Inf -> +-65504; g dtype F32/BF16/F16)
+ *   buf = buf * mu + (1 - mu) * g        (fp32 buffer; g = dtype_round(g * grad_inv_scale)
+ *                                         when grad_inv_scale != 1 (AMP), then sanitized
+ *                                         NaN -> 0, +-Inf -> +-65504; g dtype F32/BF16/F16)
  *   s   = buf, or lerp(g, buf, mu) when nesterov
  *   X   = bf16(bf16(s) / bf16(bf16(||bf16(s)||_F) + eps))
  * X is written as the wide work matrix [min x max] to x (ldx) and, when xt is
@@ -290,7 +296,7 @@ int64_t apexw_muon_workspace_floats(int64_t rows, int64_t cols);
  * (keep them zero).
  */
 int apexw_muon_prepare(float* buf, const void* g, int32_t g_dtype, int64_t rows, int64_t cols,
-                       float mu, float one_minus_mu, int32_t nesterov, float eps,
+                       float mu, float one_minus_mu, int32_t nesterov, float eps, float grad_inv_scale,
                        void* x, void* xt, int64_t ldx, int64_t ldxt, float* workspace, void* stream);
 
 /*

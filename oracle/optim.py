@@ -9,7 +9,11 @@ dispatch of ``ApexW.step`` (``apexw/optimizer.py:3359-4094``) for the
   ``decay_norm_only=False`` and mapping betas (0.9, 0.95)/(0.9, 0.99) to
   (0.9, 0.999) -- optimizer.py:1672-1714;
 * step: grad preparation (sanitize + global-norm clip, optimizer.py:204-258 and
-  :3469-3476), then for 8bit ``_step_ultra`` per parameter, and for compact
+  :3469-3476; an AMP ``grad_scale`` attribute, as GradScaler sets it, is
+  unscaled before a clip in the grad dtype, else by the step: in place on the
+  grads after sanitizing for compact (:5530-5537), on the fp32 copy after
+  nan_to_num for 8bit (:4504-4505, state.py:326-347), inside
+  ``torch._fused_adamw_`` for the native path), then for 8bit ``_step_ultra`` per parameter, and for compact
   either ``torch._fused_adamw_`` when every state matches its parameter's dtype
   and size (optimizer.py:3683-3766, ``_fused_step`` :4737-4835) or the foreach
   path over (p dtype, m dtype, step, quad) subgroups (:5369-5381).
@@ -69,6 +73,8 @@ class OracleApexW:
                           params=self.params)
         self.state = {}
         self._plan = None
+        self.grad_scale = None
+        self.found_inf = None
 
     def _plan_valid(self):
         plan = self._plan
@@ -80,12 +86,30 @@ class OracleApexW:
         return all(p.grad is None for p in self.params if p.requires_grad and p not in active)
 
     def _prepare(self, grads, sanitize):
+        """_prepare_grads: returns (grads, grad scale still to apply or None)."""
         if sanitize:
             grads = sanitize_grads(grads)
+        scale = self.grad_scale
         if self.group["clip_grad_norm"] is not None:
             grads = [g.clone() for g in grads]
+            if scale is not None:                       # unscale before the clip (:227-237)
+                torch._foreach_mul_(grads, scale.reciprocal())
+                scale = None
             clip_grads_(grads, self.group["clip_grad_norm"])
+        return grads, scale
+
+    @staticmethod
+    def _unscale(grads, scale):
+        """In-place unscale of the (cloned) grads in their dtype (:5530-5537)."""
+        if scale is None:
+            return grads
+        grads = [g.clone() for g in grads]
+        torch._foreach_mul_(grads, scale.reciprocal())
         return grads
+
+    @staticmethod
+    def _inv(scale):
+        return None if scale is None else float(scale.reciprocal().item())
 
     def _kw(self):
         grp = self.group
@@ -95,6 +119,8 @@ class OracleApexW:
 
     @torch.no_grad()
     def step(self):
+        if self.found_inf is not None and float(self.found_inf) > 0:
+            return
         if self._plan_valid():
             self._replay()
             return
@@ -108,23 +134,24 @@ class OracleApexW:
             if p not in self.state:
                 self.state[p] = L.init_state(p, grp, len(self.params), peft)
         prec = grp["precision"]
-        grads = self._prepare([p.grad for p in plist],
-                              sanitize=prec != "8bit" or grp["clip_grad_norm"] is not None)
+        grads, scale = self._prepare([p.grad for p in plist],
+                                     sanitize=prec != "8bit" or grp["clip_grad_norm"] is not None)
         kw = self._kw()
         if prec == "8bit":
             for p, g in zip(plist, grads):
                 st = self.state[p]
                 st["step"].add_(1)
-                q8_param_step(p, g, st, step=st["step"].item(), **kw)
+                q8_param_step(p, g, st, step=st["step"].item(), inv_scale=self._inv(scale), **kw)
             self._plan = {"kind": "8bit", "params": plist}
             return
         sts = [self.state[p] for p in plist]
         homogeneous = all(st["exp_avg"].dtype == st["exp_avg_sq"].dtype == p.dtype
                           and st["exp_avg"].numel() == st["exp_avg_sq"].numel() for p, st in zip(plist, sts))
         if homogeneous:
-            self._native_fused(plist, grads, sts, **kw)
+            self._native_fused(plist, grads, sts, grad_scale=scale, **kw)
             self._plan = {"kind": "native", "params": plist}
             return
+        grads = self._unscale(grads, scale)
         sub = {}
         for p, g, st in zip(plist, grads, sts):
             key = (p.dtype, st["exp_avg"].dtype, int(st["step"].item()), self._is_quad(p))
@@ -149,17 +176,18 @@ class OracleApexW:
         kw = self._kw()
         grads = [p.grad for p in plist]
         if plan["kind"] == "8bit":
-            grads = self._prepare(grads, sanitize=False)
+            grads, scale = self._prepare(grads, sanitize=False)
             for p, g in zip(plist, grads):
                 st = self.state[p]
                 st["step"].add_(1)
-                q8_param_step(p, g, st, step=st["step"].item(), **kw)
+                q8_param_step(p, g, st, step=st["step"].item(), inv_scale=self._inv(scale), **kw)
             return
-        grads = self._prepare(grads, sanitize=grp["clip_grad_norm"] is not None)
+        grads, scale = self._prepare(grads, sanitize=grp["clip_grad_norm"] is not None)
         sts = [self.state[p] for p in plist]
         if plan["kind"] == "native":
-            self._native_fused(plist, grads, sts, sanitize=False, **kw)
+            self._native_fused(plist, grads, sts, sanitize=False, grad_scale=scale, **kw)
             return
+        grads = self._unscale(sanitize_grads(grads), scale)
         steps = [st["step"] for st in sts]
         torch._foreach_add_(steps, 1)
         step = int(steps[0].item())
@@ -176,7 +204,7 @@ class OracleApexW:
 
     @staticmethod
     def _native_fused(params, grads, sts, *, lr, beta1, beta2, eps, weight_decay, decay_norm_only,
-                      sanitize=True):
+                      sanitize=True, grad_scale=None):
         if sanitize:
             grads = sanitize_grads(grads)
         steps = [st["step"] for st in sts]
@@ -191,4 +219,5 @@ class OracleApexW:
                 torch._fused_adamw_([params[i] for i in idx], [grads[i] for i in idx],
                                     [sts[i]["exp_avg"] for i in idx], [sts[i]["exp_avg_sq"] for i in idx],
                                     [], [steps[i] for i in idx], amsgrad=False, lr=lr, beta1=beta1,
-                                    beta2=beta2, weight_decay=wd, eps=eps, maximize=False)
+                                    beta2=beta2, weight_decay=wd, eps=eps, maximize=False,
+                                    grad_scale=grad_scale)

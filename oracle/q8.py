@@ -37,7 +37,7 @@ def _snr_num(m, g, beta1):
     return look.mul_(torch.where(m * g >= 0.0, gain_hi, gain_lo))
 
 
-def q8_param_step(p, g, st, *, lr, beta1, beta2, eps, weight_decay, decay_norm_only, step):
+def q8_param_step(p, g, st, *, lr, beta1, beta2, eps, weight_decay, decay_norm_only, step, inv_scale=None):
     """Update one parameter and its state in place.  ``step`` is already incremented."""
     step_size, eps_scaled = _bias(lr, beta1, beta2, eps, step)
     decay = max(1.0 - lr * weight_decay, 0.0) if weight_decay != 0 else 1.0
@@ -45,9 +45,11 @@ def q8_param_step(p, g, st, *, lr, beta1, beta2, eps, weight_decay, decay_norm_o
     sr = st.get("stochastic_rounding", True)
     n = p.numel()
     if st.get("is_8bit", False) and n > CHUNK and p.is_contiguous():
-        _chunked(p, g, st, beta1, beta2, eps, step_size, eps_scaled, decay if apply_wd else None, sr)
+        _chunked(p, g, st, beta1, beta2, eps, step_size, eps_scaled, decay if apply_wd else None, sr, inv_scale)
         return
     gf = torch.nan_to_num(g, nan=0.0, posinf=65504.0, neginf=-65504.0).float()
+    if inv_scale is not None:                           # AMP: optimizer.py:4504-4505
+        gf.mul_(inv_scale)
     if apply_wd:
         p.mul_(decay)
     if st.get("is_8bit", False):
@@ -102,7 +104,7 @@ def q8_param_step(p, g, st, *, lr, beta1, beta2, eps, weight_decay, decay_norm_o
     p.sub_(upd.to(p.dtype))
 
 
-def _chunked(p, g, st, beta1, beta2, eps, step_size, eps_scaled, decay, sr):
+def _chunked(p, g, st, beta1, beta2, eps, step_size, eps_scaled, decay, sr, inv_scale=None):
     n = p.numel()
     bs = st["block_size_8bit"]
     int4 = st.get("is_4bit_m", False)
@@ -118,6 +120,8 @@ def _chunked(p, g, st, beta1, beta2, eps, step_size, eps_scaled, decay, sr):
         sl = slice(blk0, None) if last else slice(blk0, blk0 + (end - off) // bs)
         sm, sv = msc[sl], vsc[sl]
         gc = gf_all[off:end].float().nan_to_num_(nan=0.0, posinf=65504.0, neginf=-65504.0)
+        if inv_scale is not None:                       # AMP: _prep_grad_chunk_fp32, state.py:326-347
+            gc.mul_(inv_scale)
         if int4:
             msl = mbuf[off // 2:(end + 1) // 2]
             m = Q.dequant_nf4(msl, sm, end - off, bs)

@@ -1,0 +1,165 @@
+"""GPU: AMP grad-scale hand-off (torch.amp.GradScaler with
+``_step_supports_amp_scaling``): the step kernels unscale the grads.
+
+* kernels vs the CPU oracle with the same ``grad_scale`` on the same scaled
+  grads, every path (the parity bars of test_gpu_parity.py, SR off);
+* with the global-norm clip: the AMP step equals, bit for bit, the kernels'
+  own step on the unscaled grads.  (Against the oracle the clip coefficient, a
+  global sum of squares, differs from torch's CPU reduction order by a few
+  fp32 ulps; with fp32 grads and bf16 m that flips occasional m roundings, so
+  the oracle comparison of clipped fp32 steps is not bit-level);
+* a real GradScaler loop equals, bit for bit, the same loop without scaling
+  (power-of-two scales are exact in fp32);
+* ApexMuon: a power-of-two grad scale gives the step of the unscaled grads.
+"""
+
+import pytest
+import torch
+
+from test_gpu_edge import _compare
+
+pytestmark = pytest.mark.gpu
+
+SCALE = 1024.0
+
+
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+
+
+CASES = [
+    ("compact native bf16", [(64,), (32, 16)], torch.bfloat16, dict(precision="compact")),
+    ("compact foreach bf16 quad", [(256, 128), (64,)], torch.bfloat16, dict(precision="compact")),
+    ("compact foreach fp32", [(256, 128), (1000,)], torch.float32, dict(precision="compact", adamw_compat=True)),
+    ("8bit chunked + generic", [(1024, 512), (4096,)], torch.bfloat16, dict(precision="8bit")),
+    ("8bit fp32", [(2048, 256), (100,)], torch.float32, dict(precision="8bit")),
+]
+
+
+@pytest.mark.parametrize("name,shapes,dtype,kw", CASES, ids=[c[0] for c in CASES])
+def test_grad_scale_matches_oracle(name, shapes, dtype, kw):
+    _need_gpu()
+    from apexw_amd import ApexW
+    from oracle.optim import OracleApexW
+    print(f"amp {name}", flush=True)
+    kw = dict(kw, lr=1e-3, weight_decay=0.1, stochastic_rounding=False)
+    gen = torch.Generator().manual_seed(3)
+    host = [(torch.randn(s, generator=gen) * 0.02).to(dtype) for s in shapes]
+    gps = [torch.nn.Parameter(h.cuda()) for h in host]
+    cps = [torch.nn.Parameter(h.clone()) for h in host]
+    gopt, copt = ApexW(gps, **kw), OracleApexW(cps, **kw)
+    ggen = torch.Generator().manual_seed(4)
+    for _ in range(4):
+        for gp, cp in zip(gps, cps):
+            g = (torch.randn(gp.shape, generator=ggen) * 1e-3 * SCALE).to(dtype)
+            gp.grad, cp.grad = g.cuda(), g.clone()
+        gopt.grad_scale, gopt.found_inf = torch.tensor(SCALE, device="cuda"), torch.zeros((), device="cuda")
+        copt.grad_scale, copt.found_inf = torch.tensor(SCALE), torch.tensor(0.0)
+        gopt.step()
+        copt.step()
+    torch.cuda.synchronize()
+    _compare(gps, cps, gopt, copt, name)
+
+
+@pytest.mark.parametrize("name,shapes,dtype,kw", CASES, ids=[c[0] for c in CASES])
+def test_grad_scale_with_clip_equals_unscaled_step(name, shapes, dtype, kw):
+    """The clip must see the unscaled norm: a 2^10-scaled step with grad_scale
+    2^10 is bit-identical to the step on the unscaled grads."""
+    _need_gpu()
+    from apexw_amd import ApexW
+    print(f"amp clip {name}", flush=True)
+    kw = dict(kw, lr=1e-3, weight_decay=0.1, clip_grad_norm=1e-3, stochastic_rounding=False)
+    gen = torch.Generator().manual_seed(3)
+    host = [(torch.randn(s, generator=gen) * 0.02).to(dtype) for s in shapes]
+    pa = [torch.nn.Parameter(h.cuda()) for h in host]
+    pb = [torch.nn.Parameter(h.cuda()) for h in host]
+    oa, ob = ApexW(pa, **kw), ApexW(pb, **kw)
+    ggen = torch.Generator().manual_seed(4)
+    for _ in range(4):
+        for a, b in zip(pa, pb):
+            g = (torch.randn(a.shape, generator=ggen) * 1e-3).to(dtype)
+            a.grad, b.grad = (g * SCALE).cuda(), g.cuda()
+        oa.grad_scale, oa.found_inf = torch.tensor(SCALE, device="cuda"), torch.zeros((), device="cuda")
+        oa.step()
+        ob.step()
+    torch.cuda.synchronize()
+    for a, b in zip(pa, pb):
+        assert torch.equal(a, b), name
+        for k, v in oa.state[a].items():
+            if torch.is_tensor(v):
+                assert torch.equal(v, ob.state[b][k]), (name, k)
+
+
+def _model(seed):
+    torch.manual_seed(seed)
+    return torch.nn.Sequential(torch.nn.Linear(64, 128), torch.nn.GELU(), torch.nn.Linear(128, 32)).cuda()
+
+
+@pytest.mark.parametrize("precision", ["compact", "8bit"])
+def test_grad_scaler_loop_equals_unscaled_loop(precision):
+    _need_gpu()
+    from apexw_amd import ApexW
+    print(f"grad scaler loop {precision}", flush=True)
+    ma, mb = _model(0), _model(0)
+    kw = dict(lr=1e-3, weight_decay=0.1, precision=precision, stochastic_rounding=False)
+    oa, ob = ApexW(ma.parameters(), **kw), ApexW(mb.parameters(), **kw)
+    scaler = torch.amp.GradScaler("cuda", init_scale=2.0 ** 12)
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    for _ in range(5):
+        x = torch.randn(16, 64, device="cuda", generator=gen)
+        y = torch.randn(16, 32, device="cuda", generator=gen)
+        oa.zero_grad()
+        scaler.scale(torch.nn.functional.mse_loss(ma(x), y)).backward()
+        scaler.step(oa)
+        scaler.update()
+        ob.zero_grad()
+        torch.nn.functional.mse_loss(mb(x), y).backward()
+        ob.step()
+    torch.cuda.synchronize()
+    for pa, pb in zip(ma.parameters(), mb.parameters()):
+        assert torch.equal(pa, pb)
+
+
+def test_grad_scaler_skips_inf_step():
+    _need_gpu()
+    from apexw_amd import ApexW
+    m = _model(2)
+    opt = ApexW(m.parameters(), lr=1e-3)
+    scaler = torch.amp.GradScaler("cuda", init_scale=2.0 ** 12)
+    x = torch.randn(4, 64, device="cuda")
+    scaler.scale(m(x).sum()).backward()
+    scaler.step(opt)
+    scaler.update()
+    before = [p.detach().clone() for p in m.parameters()]
+    opt.zero_grad()
+    scaler.scale(m(x).sum()).backward()
+    next(m.parameters()).grad[0, 0] = float("inf")
+    scaler.step(opt)                     # found_inf -> skipped
+    scaler.update()
+    torch.cuda.synchronize()
+    for p, b in zip(m.parameters(), before):
+        assert torch.equal(p.detach(), b)
+    assert scaler.get_scale() == 2.0 ** 11
+
+
+def test_muon_grad_scale_equals_unscaled():
+    _need_gpu()
+    from apexw_amd.muon import ApexMuon
+    gen = torch.Generator().manual_seed(9)
+    host = [torch.randn(s, generator=gen) * 0.02 for s in [(256, 384), (384, 256)]]
+    pa = [torch.nn.Parameter(h.cuda()) for h in host]
+    pb = [torch.nn.Parameter(h.cuda()) for h in host]
+    oa = ApexMuon(pa, lr=0.02, weight_decay=0.1, scale_mode="rms_matched")
+    ob = ApexMuon(pb, lr=0.02, weight_decay=0.1, scale_mode="rms_matched")
+    for _ in range(2):
+        for a, b in zip(pa, pb):
+            g = torch.randn(a.shape, generator=gen) * 1e-3
+            a.grad, b.grad = (g * SCALE).cuda(), g.cuda()
+        oa.grad_scale, oa.found_inf = torch.tensor(SCALE, device="cuda"), torch.zeros((), device="cuda")
+        oa.step()
+        ob.step()
+    torch.cuda.synchronize()
+    for a, b in zip(pa, pb):
+        assert torch.equal(a, b)
+        assert torch.equal(oa.state[a]["momentum"], ob.state[b]["momentum"])

@@ -13,7 +13,7 @@ import numpy as np
 
 from ._build import LIB_PATH
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # dtype codes
 F32, BF16, F16, U8, I8 = 0, 1, 2, 3, 4
@@ -76,6 +76,12 @@ GEMM_PROBLEM_DTYPE = np.dtype([
     ("flags", np.uint32), ("reserved", np.uint32),
 ])
 assert GEMM_PROBLEM_DTYPE.itemsize == 88
+# apexw_grad_prep: one grad of a preparation launch (sanitize / unscale / centralize)
+GRAD_PREP_DTYPE = np.dtype([("g", np.uint64), ("out", np.uint64), ("n", np.int64), ("row_len", np.int64),
+                            ("dtype", np.uint32), ("reserved", np.uint32)])
+assert GRAD_PREP_DTYPE.itemsize == 40
+GRAD_PREP_CHUNK = 2048
+
 GEMM_SYM, GEMM_B_KN, GEMM_ADD_B = 1, 2, 4
 GEMM_OUT_C, GEMM_OUT_CT, GEMM_ADD, GEMM_KIND_NN = 1, 2, 4, 8
 GEMM_MAX_PROBLEMS = 256
@@ -93,6 +99,9 @@ SIGNATURES = {
     "apexw_grad_clip_coef": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _vp, _vp, _vp, _f32, _f32, _u32, _vp, _vp]),
     "apexw_gemm_nt_bf16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                           _i32, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _vp]),
+    "apexw_check_grad_prep": (ctypes.c_int, [_vp]),
+    "apexw_grad_prep_units": (ctypes.c_int64, [_vp]),
+    "apexw_grad_prepare": (ctypes.c_int, [_vp, _i32, _vp, _i64, _f32, _u32, _vp]),
     "apexw_gemm_grouped_items": (ctypes.c_int64, [_vp, _i32]),
     "apexw_gemm_grouped_schedule": (ctypes.c_int, [_vp, _i32, _vp, _i64, _vp, ctypes.POINTER(ctypes.c_int32),
                                                    ctypes.POINTER(ctypes.c_int32)]),

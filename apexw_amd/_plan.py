@@ -13,7 +13,10 @@ What the plan owns, built once and reused every step:
   * one shared CPU fp32 buffer holding every parameter's step counter; each
     ``state["step"]`` is a 0-dim view into it, so advancing all counters is one
     op instead of one per tensor;
-  * clip workspaces (per-unit partial sums, per-tensor norms, the coefficient).
+  * clip workspaces (per-unit partial sums, per-tensor norms, the coefficient);
+  * with grad_centralization, one prepared-grad buffer per parameter and the
+    preparation table: the reference's _prepare_grads works on a clone, and the
+    step and the clip read the prepared copy.
 Only the grad pointers are re-read every step; if any changed, the tensor
 table is re-uploaded (one host-to-device copy).
 """
@@ -53,6 +56,7 @@ class StepPlan:
         self.decay_norm_only = group["decay_norm_only"]
         self.device = self.params[0].device
         self.states = [opt.state[p] for p in self.params]
+        self.gc = bool(group.get("grad_centralization", False))
         self.cold_done = False
         self._build_steps()
         self._build_tables(group)
@@ -77,6 +81,8 @@ class StepPlan:
         if group.get("decay_norm_only", self.decay_norm_only) != self.decay_norm_only:
             return False
         if group.get("precision") != self.precision:
+            return False
+        if bool(group.get("grad_centralization", False)) != self.gc:
             return False
         return True
 
@@ -139,6 +145,8 @@ class StepPlan:
             else:
                 counts[i] = (p.numel() + block - 1) // block
         self.host_table = tab          # parameter order
+        if self.gc:
+            self._build_prep()
         self._gathered = None
         self._fast_static = None
         self.counts = counts
@@ -147,6 +155,41 @@ class StepPlan:
         self.clip_ws = None
         self.d_table = None
         self.perm = None
+
+    def _build_prep(self):
+        """Prepared-grad buffers and the preparation table (sources filled per step)."""
+        n = len(self.params)
+        self.gc_out = [torch.empty(p.numel(), dtype=p.dtype, device=self.device) for p in self.params]
+        prep = np.zeros(n, dtype=L.GRAD_PREP_DTYPE)
+        prep["out"] = [o.data_ptr() for o in self.gc_out]
+        prep["n"] = [p.numel() for p in self.params]
+        # the reference centralizes dim >= 2 grads over dims 1.. (optimizer.py:239-243)
+        prep["row_len"] = [p.numel() // p.shape[0] if p.dim() >= 2 else 0 for p in self.params]
+        prep["dtype"] = [_DT[p.dtype] for p in self.params]
+        self.host_prep = prep
+        self.d_prep = None
+        counts = []
+        for i in range(n):
+            row = prep[i:i + 1].copy()
+            row["g"] = 256                 # stand-in source, checked for real at upload
+            k = int(L.load().apexw_grad_prep_units(row.ctypes.data))
+            if k < 0:
+                L.check(-k, f"grad preparation of tensor {i}")
+            counts.append(k)
+        counts = np.array(counts, dtype=np.int64)
+        units = np.zeros(int(counts.sum()), dtype=L.UNIT_DTYPE)
+        begin = np.concatenate([[0], np.cumsum(counts)])
+        units["tensor"] = np.repeat(np.arange(n, dtype=np.uint32), counts)
+        units["unit"] = (np.arange(len(units), dtype=np.int64) - np.repeat(begin[:-1], counts)).astype(np.uint32)
+        self.n_prep_units = len(units)
+        self.d_prep_units = torch.from_numpy(units.view(np.uint8)).to(self.device)
+
+    def _prepare_grads(self, inv_scale, stream):
+        """Sanitize, unscale and centralize into the prepared-grad buffers."""
+        flags = L.HP_SANITIZE | (L.HP_UNSCALE if inv_scale is not None else 0)
+        st = self._lib.apexw_grad_prepare(self.d_prep.data_ptr(), len(self.params), self.d_prep_units.data_ptr(),
+                                          self.n_prep_units, 1.0 if inv_scale is None else inv_scale, flags, stream)
+        L.check(st, "apexw_grad_prepare")
 
     def _layout_units(self, fast):
         """Device table in launch order and its unit table.  8-bit: full-block-kernel
@@ -200,6 +243,15 @@ class StepPlan:
                 gs[i] = g.contiguous()
         self._grad_refs = [weakref.ref(g) for g in gs]
         ptrs = np.fromiter(map(_DATA_PTR, gs), dtype=np.uint64, count=len(gs))
+        if self.gc:
+            # the prepared copies feed the clip and the step; the sources feed the preparation
+            if self.d_prep is None or not np.array_equal(ptrs, self.host_prep["g"]):
+                self.host_prep["g"] = ptrs
+                for i in range(len(self.params)):
+                    L.check(self._lib.apexw_check_grad_prep(self.host_prep[i:i + 1].ctypes.data),
+                            f"grad preparation of tensor {i}")
+                self.d_prep = torch.from_numpy(self.host_prep.view(np.uint8).copy()).to(self.device)
+            ptrs = np.fromiter((o.data_ptr() for o in self.gc_out), dtype=np.uint64, count=len(gs))
         if self.d_table is None or not np.array_equal(ptrs, self.host_table["g"]):
             self.host_table["g"] = ptrs
             fast = self._validate_and_align()
@@ -267,6 +319,11 @@ class StepPlan:
             sanitize = mode_cold or clip is not None
         else:
             sanitize = mode_cold and clip is not None
+        if self.gc:
+            # _prepare_grads with centralization: sanitize, unscale, centralize;
+            # the clip and the step then see finite, unscaled grads
+            self._prepare_grads(inv_scale, stream)
+            sanitize, inv_scale = False, None
         coef = self._clip(clip, sanitize, inv_scale, stream) if clip is not None else None
         self.steps.add_(1.0)
         # The reference's replayed compact step takes the bias correction of the

@@ -23,6 +23,7 @@ int apexw_launch_gemm_nt(const uint16_t*, const uint16_t*, const uint16_t*, uint
                          int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int64_t, int64_t, int64_t,
                          int64_t, int64_t, float, float, hipStream_t);
 int apexw_muon_partials(int64_t n);
+int apexw_launch_grad_prep(const apexw_grad_prep*, const apexw_unit*, int64_t, float, uint32_t, hipStream_t);
 int apexw_launch_gemm_grouped(const apexw_gemm_problem*, const uint32_t*, const int32_t*, int32_t, int32_t,
                               hipStream_t);
 int apexw_launch_muon_prepare(float*, const void*, int32_t, int64_t, int64_t, float, float, int32_t, float, float,
@@ -320,6 +321,31 @@ int apexw_grad_clip_coef(const apexw_tensor* tensors, int32_t n_tensors, const a
   if ((flags & APEXW_HP_UNSCALE) && !(grad_inv_scale > 0.0f)) return APEXW_ERR_ARG;
   return apexw_launch_clip(tensors, n_tensors, units, n_units, unit_size, unit_begin, unit_partial, tensor_norm, clip,
                            grad_inv_scale, flags, coef, (hipStream_t)stream);
+}
+
+int apexw_check_grad_prep(const apexw_grad_prep* d) {
+  if (!d || !d->g || !d->out || d->n <= 0 || d->row_len < 0 || d->reserved) return APEXW_ERR_ARG;
+  if (d->dtype != APEXW_F32 && d->dtype != APEXW_BF16 && d->dtype != APEXW_F16) return APEXW_ERR_DTYPE;
+  if (d->row_len > 0 && d->n % d->row_len) return APEXW_ERR_ARG;
+  const int64_t size = d->dtype == APEXW_F32 ? 4 : 2;
+  const uintptr_t g = (uintptr_t)d->g, o = (uintptr_t)d->out;
+  if (g < o + (uintptr_t)(d->n * size) && o < g + (uintptr_t)(d->n * size)) return APEXW_ERR_ARG;   // aliasing
+  if ((g | o) & (uintptr_t)(size - 1)) return APEXW_ERR_ALIGN;
+  return APEXW_OK;
+}
+
+int64_t apexw_grad_prep_units(const apexw_grad_prep* d) {
+  const int st = apexw_check_grad_prep(d);
+  if (st != APEXW_OK) return -st;
+  return d->row_len > 0 ? d->n / d->row_len : (d->n + APEXW_GRAD_PREP_CHUNK - 1) / APEXW_GRAD_PREP_CHUNK;
+}
+
+int apexw_grad_prepare(const apexw_grad_prep* preps, int32_t n_preps, const apexw_unit* units, int64_t n_units,
+                       float grad_inv_scale, uint32_t flags, void* stream) {
+  if (!preps || !units || n_preps <= 0 || n_units < 0) return APEXW_ERR_ARG;
+  if (flags & ~(APEXW_HP_SANITIZE | APEXW_HP_UNSCALE)) return APEXW_ERR_ARG;
+  if ((flags & APEXW_HP_UNSCALE) && !(grad_inv_scale > 0.0f)) return APEXW_ERR_ARG;
+  return apexw_launch_grad_prep(preps, units, n_units, grad_inv_scale, flags, (hipStream_t)stream);
 }
 
 }  // extern "C"

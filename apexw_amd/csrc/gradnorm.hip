@@ -97,7 +97,65 @@ __global__ __launch_bounds__(1024) void clip_coef_kernel(const float* __restrict
   }
 }
 
+// ---------------------------------------------------------------------------
+// Gradient preparation (sanitize, AMP unscale, centralization), one 256-thread
+// workgroup per unit: a row of a centralized grad (sum pass, then subtract and
+// store; the row is re-read from L2) or a 2048-element chunk of any other grad.
+// ---------------------------------------------------------------------------
+template <int GD> APEXW_DEV float prep_value(const void* g, int64_t i, bool san, bool unscale, float inv) {
+  float x = load1<GD>(g, i);
+  if (san) x = sanitize<GD>(x);
+  if (unscale) x = rnd<GD>(x * inv);
+  return x;
+}
+
+template <int GD>
+APEXW_DEV void prep_unit(const apexw_grad_prep& d, int64_t unit, bool san, bool unscale, float inv, float* red) {
+  const int tid = threadIdx.x;
+  if (d.row_len > 0) {
+    const int64_t base = unit * d.row_len;
+    float s = 0.0f;
+    for (int64_t j = tid; j < d.row_len; j += 256) s += prep_value<GD>(d.g, base + j, san, unscale, inv);
+    s = wave_sum(s);
+    if ((tid & 63) == 0) red[tid >> 6] = s;
+    __syncthreads();
+    // torch's mean: sum in fp32, divided by the count, result in the grad dtype
+    const float mean = rnd<GD>(((red[0] + red[1]) + (red[2] + red[3])) / (float)d.row_len);
+    for (int64_t j = tid; j < d.row_len; j += 256) {
+      const float x = prep_value<GD>(d.g, base + j, san, unscale, inv);
+      store1<GD>(d.out, base + j, rnd<GD>(x - mean));
+    }
+  } else {
+    const int64_t base = unit * APEXW_GRAD_PREP_CHUNK;
+    const int64_t end = base + APEXW_GRAD_PREP_CHUNK < d.n ? base + APEXW_GRAD_PREP_CHUNK : d.n;
+    for (int64_t i = base + tid; i < end; i += 256) store1<GD>(d.out, i, prep_value<GD>(d.g, i, san, unscale, inv));
+  }
+}
+
+__global__ __launch_bounds__(256) void grad_prep_kernel(const apexw_grad_prep* __restrict__ preps,
+                                                        const apexw_unit* __restrict__ units, int64_t n_units,
+                                                        float inv, uint32_t flags) {
+  __shared__ float red[4];
+  const bool san = flags & APEXW_HP_SANITIZE, unscale = flags & APEXW_HP_UNSCALE;
+  for (int64_t u = blockIdx.x; u < n_units; u += gridDim.x) {
+    const apexw_unit un = units[u];
+    const apexw_grad_prep& d = preps[un.tensor];
+    if (d.dtype == APEXW_F32) prep_unit<APEXW_F32>(d, un.unit, san, unscale, inv, red);
+    else if (d.dtype == APEXW_BF16) prep_unit<APEXW_BF16>(d, un.unit, san, unscale, inv, red);
+    else prep_unit<APEXW_F16>(d, un.unit, san, unscale, inv, red);
+    __syncthreads();   // red is reused by the next unit
+  }
+}
+
 }  // namespace
+
+int apexw_launch_grad_prep(const apexw_grad_prep* preps, const apexw_unit* units, int64_t n_units, float inv,
+                           uint32_t flags, hipStream_t stream) {
+  if (n_units <= 0) return APEXW_OK;
+  const int64_t want = n_units < 65536 ? n_units : 65536;
+  hipLaunchKernelGGL(grad_prep_kernel, dim3((unsigned)want), dim3(256), 0, stream, preps, units, n_units, inv, flags);
+  return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
+}
 
 int apexw_launch_clip(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,
                       int64_t unit_size, const int64_t* unit_begin, float* unit_partial, float* tensor_norm,

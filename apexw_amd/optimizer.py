@@ -23,7 +23,7 @@ from torch.optim.optimizer import Optimizer
 from . import state as S
 from ._plan import StepPlan
 
-_UNSUPPORTED_FLAGS = ("amsgrad", "nesterov", "cautious", "grad_centralization", "lion", "maximize",
+_UNSUPPORTED_FLAGS = ("amsgrad", "nesterov", "cautious", "lion", "maximize",
                       "capturable", "differentiable", "auto_pack", "factored_v", "six_bit")
 
 

@@ -19,6 +19,8 @@
  *                           _adamw_kernel_triton_8bit_batched (apexw/triton_kernel.py:1138-1531)
  *   apexw_grad_clip_coef <- the global-norm clip of _prepare_grads
  *                           (apexw/optimizer.py:242-256: _foreach_norm + vector_norm)
+ *   apexw_grad_prepare   <- sanitize / AMP unscale / grad centralization of
+ *                           _prepare_grads (apexw/optimizer.py:204-240)
  *   apexw_gemm_nt_bf16   <- the bf16 GEMMs of Newton-Schulz: X @ X.T and the two
  *                           torch.addmm / baddbmm calls (apexw/muon.py:102-108, :187-211)
  *   apexw_gemm_nt_grouped <- the same GEMMs for every Muon matrix of a step in one
@@ -37,7 +39,7 @@
 extern "C" {
 #endif
 
-#define APEXW_ABI_VERSION 5
+#define APEXW_ABI_VERSION 6
 
 /* status codes */
 enum apexw_status {
@@ -180,6 +182,38 @@ int apexw_grad_clip_coef(const apexw_tensor* tensors, int32_t n_tensors,
                          const apexw_unit* units, int64_t n_units, int64_t unit_size,
                          const int64_t* unit_begin, float* unit_partial, float* tensor_norm,
                          float clip, float grad_inv_scale, uint32_t flags, float* coef, void* stream);
+
+/*
+ * Gradient preparation of _prepare_grads (apexw/optimizer.py:204-258) for a
+ * group with grad_centralization: writes, per grad, out = g sanitized (NaN -> 0,
+ * +-Inf -> +-65504, APEXW_HP_SANITIZE), unscaled (times grad_inv_scale in the
+ * grad dtype, APEXW_HP_UNSCALE) and, when row_len > 0, centralized:
+ *   out = dtype_round(x - dtype_round(mean over the row of x)),
+ * rows being the row_len consecutive elements of each index of dim 0 (the
+ * reference's g.sub_(g.mean(dim=(1, ...), keepdim=True)) for dim >= 2).  The
+ * step and the clip then read out (the reference also works on a clone).
+ */
+typedef struct apexw_grad_prep {
+  const void* g;        /* source grad, n elements */
+  void* out;            /* prepared grad, n elements, same dtype; not aliasing g */
+  int64_t n;
+  int64_t row_len;      /* centralize rows of this length (n % row_len == 0), or 0 */
+  uint32_t dtype;       /* APEXW_F32 / APEXW_BF16 / APEXW_F16 */
+  uint32_t reserved;    /* 0 */
+} apexw_grad_prep;      /* 40 bytes */
+
+/* Validate one descriptor (host copy) before it is uploaded. */
+int apexw_check_grad_prep(const apexw_grad_prep* d);
+
+/* Work units of apexw_grad_prepare for one descriptor: its rows when row_len > 0,
+ * else chunks of APEXW_GRAD_PREP_CHUNK elements (unit = index). */
+#define APEXW_GRAD_PREP_CHUNK 2048
+int64_t apexw_grad_prep_units(const apexw_grad_prep* d);
+
+/* Launch over a device table of descriptors and a unit table ({tensor, unit}
+ * entries as for the step), one workgroup per unit. */
+int apexw_grad_prepare(const apexw_grad_prep* preps, int32_t n_preps, const apexw_unit* units, int64_t n_units,
+                       float grad_inv_scale, uint32_t flags, void* stream);
 
 /* ------------------------------------------------------------------------- */
 /* Muon: Newton-Schulz on the matrix cores                                    */

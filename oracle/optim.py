@@ -57,7 +57,7 @@ def normalize_precision(precision):
 class OracleApexW:
     def __init__(self, params, lr=1e-3, betas=None, eps=1e-8, weight_decay=1e-2, decay_norm_only=True,
                  adamw_compat=False, clip_grad_norm=None, precision="compact", stochastic_rounding=True,
-                 block_size=None, force_compact_v=False, int4_m=None):
+                 block_size=None, force_compact_v=False, int4_m=None, grad_centralization=False):
         precision = normalize_precision(precision)
         if betas is None:
             betas = (0.9, 0.999) if precision == "8bit" else (0.9, 0.99)
@@ -70,7 +70,7 @@ class OracleApexW:
                           decay_norm_only=decay_norm_only, clip_grad_norm=clip_grad_norm,
                           precision=precision, stochastic_rounding=stochastic_rounding,
                           block_size=block_size, force_compact_v=force_compact_v, int4_m=int4_m,
-                          params=self.params)
+                          grad_centralization=grad_centralization, params=self.params)
         self.state = {}
         self._plan = None
         self.grad_scale = None
@@ -86,16 +86,25 @@ class OracleApexW:
         return all(p.grad is None for p in self.params if p.requires_grad and p not in active)
 
     def _prepare(self, grads, sanitize):
-        """_prepare_grads: returns (grads, grad scale still to apply or None)."""
-        if sanitize:
+        """_prepare_grads (optimizer.py:204-258): returns (grads, grad scale still
+        to apply or None).  Grad centralization forces sanitizing (:3469-3473) and
+        unscaling, then subtracts each dim >= 2 grad's mean over dims 1.. (:239-243)."""
+        gc = self.group.get("grad_centralization", False)
+        clip = self.group["clip_grad_norm"]
+        if sanitize or gc:
             grads = sanitize_grads(grads)
         scale = self.grad_scale
-        if self.group["clip_grad_norm"] is not None:
+        if clip is not None or gc:
             grads = [g.clone() for g in grads]
-            if scale is not None:                       # unscale before the clip (:227-237)
+            if scale is not None:                       # unscale first (:227-237)
                 torch._foreach_mul_(grads, scale.reciprocal())
                 scale = None
-            clip_grads_(grads, self.group["clip_grad_norm"])
+            if gc:
+                for g in grads:
+                    if g.dim() >= 2:
+                        g.sub_(g.mean(dim=tuple(range(1, g.dim())), keepdim=True))
+            if clip is not None:
+                clip_grads_(grads, clip)
         return grads, scale
 
     @staticmethod

@@ -44,10 +44,11 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("gc", [False, True])
 @pytest.mark.parametrize("clip", [None, 1e-3])
 @pytest.mark.parametrize("name,shapes,dtype,kw", CASES, ids=[c[0] for c in CASES])
-def test_pow2_grad_scale_equals_unscaled_step(name, shapes, dtype, kw, clip):
-    kw = dict(kw, lr=1e-3, weight_decay=0.1, clip_grad_norm=clip)
+def test_pow2_grad_scale_equals_unscaled_step(name, shapes, dtype, kw, clip, gc):
+    kw = dict(kw, lr=1e-3, weight_decay=0.1, clip_grad_norm=clip, grad_centralization=gc)
     kw.setdefault("stochastic_rounding", False)
     a, oa = _run(shapes, dtype, kw, amp=True)
     b, ob = _run(shapes, dtype, kw, amp=False)

@@ -1,9 +1,11 @@
-"""Build libapexw_hip.so in-tree with hipcc for gfx950.
+"""Build libapexw_hip.so (hipcc, gfx950) and the _host module (g++) in-tree.
 
     python -m apexw_amd._build            # or __graft_entry__.build()
 
 All HIP sources under apexw_amd/csrc are compiled into one shared library next
-to this file.  Flags:
+to this file.  csrc/host.cpp (the per-step scan of a plan's tensors, plain
+CPython C API over torch's tensor headers) becomes apexw_amd/_host*.so.
+HIP flags:
   -O3 --offload-arch=gfx950        CDNA4 code objects only
   -ffp-contract=off                no implicit FMA: kernels write fmaf() exactly
                                    where the reference's torch ops fuse
@@ -14,6 +16,7 @@ to this file.  Flags:
 import os
 import subprocess
 import sys
+import sysconfig
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
@@ -30,12 +33,42 @@ FLAGS = [
 ]
 
 
+HOST_SRC = os.path.join(CSRC, "host.cpp")
+HOST_PATH = os.path.join(HERE, "_host" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
 def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
 def build(verbose=False):
-    """Compile every HIP source into apexw_amd/libapexw_hip.so (always rebuilds)."""
+    """Compile the HIP library and the host module (always rebuilds both)."""
+    build_host(verbose)
+    return build_hip(verbose)
+
+
+def build_host(verbose=False):
+    """Compile csrc/host.cpp against the installed torch into apexw_amd/_host*.so."""
+    import torch
+    from torch.utils import cpp_extension as ce
+    tdir = os.path.dirname(torch.__file__)
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    tmp = HOST_PATH + ".tmp"
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           *(f"-I{p}" for p in ce.include_paths()), f"-I{sysconfig.get_paths()['include']}", HOST_SRC,
+           f"-L{os.path.join(tdir, 'lib')}", "-ltorch_python", "-ltorch", "-ltorch_cpu", "-lc10",
+           f"-Wl,-rpath,{os.path.join(tdir, 'lib')}", "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"g++ failed ({res.returncode}):\n{res.stderr}")
+    os.replace(tmp, HOST_PATH)
+    return HOST_PATH
+
+
+def build_hip(verbose=False):
+    """Compile every HIP source into apexw_amd/libapexw_hip.so."""
     tmp = LIB_PATH + ".tmp"
     cmd = [HIPCC, *FLAGS, "-I", os.path.join(ROOT, "include"), "-o", tmp, *sources()]
     if verbose:

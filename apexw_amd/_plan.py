@@ -17,24 +17,36 @@ What the plan owns, built once and reused every step:
   * with grad_centralization, one prepared-grad buffer per parameter and the
     preparation table: the reference's _prepare_grads works on a clone, and the
     step and the clip read the prepared copy.
-Only the grad pointers are re-read every step; if any changed, the tensor
-table is re-uploaded (one host-to-device copy).
+Every step the native scan (csrc/host.cpp) re-reads each parameter's data
+pointer and dtype and each grad's pointer: a grad that moved is re-pointed in
+the tensor table (one host-to-device copy); a parameter whose storage or dtype
+changed in place (``p.data = ...``, ``module.to(dtype)``) invalidates the plan.
 """
 
 import math
 import operator
-import weakref
 
 import numpy as np
 import torch
 
 from . import _lib as L
 
+
+
+def _host():
+    """The native scan module, imported on first use (the build imports this package)."""
+    try:
+        from . import _host as mod
+    except ImportError as exc:
+        raise ImportError("apexw_amd/_host*.so is not built; run `python -m apexw_amd._build`") from exc
+    return mod
+
 _DT = {torch.float32: L.F32, torch.bfloat16: L.BF16, torch.float16: L.F16, torch.uint8: L.U8, torch.int8: L.I8}
 CHUNKED_MIN_NUMEL = 262144  # larger 8-bit tensors take the reference's chunked rounding order
 _GRAD = operator.attrgetter("grad")
-_DATA_PTR = operator.methodcaller("data_ptr")
-_DEREF = weakref.ref.__call__
+
+# status of _host.scan (csrc/host.cpp)
+SCAN_SAME, SCAN_GRADS_MOVED, SCAN_MISSING, SCAN_REBUILT, SCAN_SLOW = range(5)
 
 
 def _lerp_coef(w):
@@ -63,28 +75,24 @@ class StepPlan:
 
     # ------------------------------------------------------------------ validity
     def valid_for(self, group):
-        """The reference's FastExecutionPlan.is_valid_for_step (optimizer.py:575-621).
-
-        The grads are gathered once per step; when every one is the tensor the
-        table already points at (the usual case: grads are accumulated in place),
-        nothing else is checked per parameter."""
+        """The reference's FastExecutionPlan.is_valid_for_step (optimizer.py:575-621):
+        every plan parameter has a grad and no other trainable parameter of the
+        group has one.  Also invalid when a parameter's storage or dtype changed
+        in place, since the table holds its address."""
         if not self.params:
             return False
-        gs = list(map(_GRAD, self.params))
-        self._gathered = gs
-        if not self._same_grads(gs):
-            if any(g is None for g in gs):
-                return False
-        for p in self.inactive:
-            if p.grad is not None:
-                return False
         if group.get("decay_norm_only", self.decay_norm_only) != self.decay_norm_only:
             return False
         if group.get("precision") != self.precision:
             return False
         if bool(group.get("grad_centralization", False)) != self.gc:
             return False
-        return True
+        self._scan_status = self._scan()
+        return self._scan_status in (SCAN_SAME, SCAN_GRADS_MOVED, SCAN_SLOW)
+
+    def _scan(self):
+        return self._H.scan(self.params, self.inactive, self.p_ptrs.ctypes.data, self.p_dtypes.ctypes.data,
+                      self.g_ptrs.ctypes.data, self.g_scan.ctypes.data)
 
     # ------------------------------------------------------------------ build
     def _build_steps(self):
@@ -121,7 +129,6 @@ class StepPlan:
     def _build_tables(self, group):
         wd_on = group["weight_decay"] != 0
         n = len(self.params)
-        self._grad_refs = None
         tab = np.zeros(n, dtype=L.TENSOR_DTYPE)
         counts = np.zeros(n, dtype=np.int64)
         for i, (p, st) in enumerate(zip(self.params, self.states)):
@@ -145,9 +152,15 @@ class StepPlan:
             else:
                 counts[i] = (p.numel() + block - 1) // block
         self.host_table = tab          # parameter order
+        self.p_ptrs = np.zeros(n, dtype=np.uint64)
+        self.p_dtypes = np.zeros(n, dtype=np.int8)
+        self._H = _host()
+        self._H.snapshot(self.params, self.p_ptrs.ctypes.data, self.p_dtypes.ctypes.data)
+        self.g_ptrs = np.zeros(n, dtype=np.uint64)     # grad pointers the table was built from
+        self.g_scan = np.zeros(n, dtype=np.uint64)     # the scan's current grad pointers
+        self._scan_status = None
         if self.gc:
             self._build_prep()
-        self._gathered = None
         self._fast_static = None
         self.counts = counts
         self.kind_code = 0 if self.kind == "compact" else 1
@@ -218,31 +231,31 @@ class StepPlan:
         self.d_unit_begin = torch.from_numpy(self.unit_begin).to(self.device)
         self.clip_ws = None
 
-    def _same_grads(self, gs):
-        """Every grad is the tensor the table was built from (weak references:
-        the plan does not keep last step's grads alive)."""
-        return self._grad_refs is not None and all(map(operator.is_, gs, map(_DEREF, self._grad_refs)))
-
     def _refresh_grads(self):
-        """Point the table at this step's grad tensors; re-upload if any changed.
+        """Point the table at this step's grads; re-upload it if any moved.
 
-        Grads that are the tensor seen last step need no check (one identity
-        test per parameter).  Otherwise dtype and layout are checked and the
-        grad-pointer column is rebuilt in one pass.  Returns the grads, which
-        the caller keeps alive until the launch is enqueued."""
-        gs = self._gathered if self._gathered is not None else list(map(_GRAD, self.params))
-        self._gathered = None
-        if self.d_table is not None and self._same_grads(gs):
-            return gs
-        for i, (p, g) in enumerate(zip(self.params, gs)):
-            if g is None:
-                raise RuntimeError("a parameter of the plan has no grad")
-            if g.dtype != p.dtype:
-                raise NotImplementedError("grad dtype must match the parameter dtype")
-            if not g.is_contiguous():
-                gs[i] = g.contiguous()
-        self._grad_refs = [weakref.ref(g) for g in gs]
-        ptrs = np.fromiter(map(_DATA_PTR, gs), dtype=np.uint64, count=len(gs))
+        Uses the scan done by ``valid_for`` (or scans now on a new plan).  Grads
+        that are non-contiguous are copied contiguous; the copies are returned
+        so the caller keeps them alive until the launch is enqueued."""
+        st = self._scan_status if self._scan_status is not None else self._scan()
+        self._scan_status = None
+        if st == SCAN_SAME and self.d_table is not None:
+            return None
+        if st in (SCAN_MISSING, SCAN_REBUILT):
+            raise RuntimeError("the step plan no longer matches its parameters or grads")
+        keep = None
+        if st == SCAN_SLOW:
+            keep = list(map(_GRAD, self.params))
+            for i, (p, g) in enumerate(zip(self.params, keep)):
+                if g.dtype != p.dtype:
+                    raise NotImplementedError("grad dtype must match the parameter dtype")
+                if g.numel() != p.numel():
+                    raise RuntimeError(f"grad of parameter {i} has {g.numel()} elements, the parameter {p.numel()}")
+                if not g.is_contiguous():
+                    keep[i] = g.contiguous()
+            self.g_scan[:] = [g.data_ptr() for g in keep]
+        ptrs = self.g_scan.copy()
+        self.g_ptrs[:] = ptrs
         if self.gc:
             # the prepared copies feed the clip and the step; the sources feed the preparation
             if self.d_prep is None or not np.array_equal(ptrs, self.host_prep["g"]):
@@ -251,7 +264,7 @@ class StepPlan:
                     L.check(self._lib.apexw_check_grad_prep(self.host_prep[i:i + 1].ctypes.data),
                             f"grad preparation of tensor {i}")
                 self.d_prep = torch.from_numpy(self.host_prep.view(np.uint8).copy()).to(self.device)
-            ptrs = np.fromiter((o.data_ptr() for o in self.gc_out), dtype=np.uint64, count=len(gs))
+            ptrs = np.fromiter((o.data_ptr() for o in self.gc_out), dtype=np.uint64, count=len(self.params))
         if self.d_table is None or not np.array_equal(ptrs, self.host_table["g"]):
             self.host_table["g"] = ptrs
             fast = self._validate_and_align()
@@ -259,7 +272,7 @@ class StepPlan:
                 self._layout_units(fast)
             rows = np.ascontiguousarray(self.host_table[self.perm])
             self.d_table = torch.from_numpy(rows.view(np.uint8)).to(self.device)
-        return gs
+        return keep
 
     def _validate_and_align(self):
         """Mark descriptors with an unaligned pointer element-wise; 8-bit: which take the full-block kernel.
@@ -310,7 +323,7 @@ class StepPlan:
 
         inv_scale: 1 / the AMP grad scale handed over by GradScaler, or None."""
         mode_cold = not self.cold_done
-        grads = self._refresh_grads()  # noqa: F841 -- keeps contiguous copies alive until the launch
+        keep = self._refresh_grads()  # noqa: F841 -- keeps contiguous copies alive until the launch
         stream = torch.cuda.current_stream(self.device).cuda_stream
         lr, (b1, b2), eps, wd = group["lr"], group["betas"], group["eps"], group["weight_decay"]
         sr = bool(group.get("stochastic_rounding", True))

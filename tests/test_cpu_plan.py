@@ -144,3 +144,80 @@ def test_cold_step_splits_by_step_count(cpu_plans):
     plan.execute(group, seed=0)
     q8 = [c for c in cpu_plans.calls if c[0] == "q8"]
     assert sorted(c[2]["step"] for c in q8[-2:]) == [1, 6]
+
+
+def _table(plan):
+    return plan.d_table.cpu().numpy().view(L.TENSOR_DTYPE)
+
+
+def test_scan_is_native():
+    from apexw_amd import _host  # noqa: F401 -- built by apexw_amd._build
+    ps = _params([(8,), (8,)], torch.float32)
+    pp, dt = np.zeros(2, np.uint64), np.zeros(2, np.int8)
+    _host.snapshot(ps, pp.ctypes.data, dt.ctypes.data)
+    assert pp.tolist() == [p.data_ptr() for p in ps]
+    with pytest.raises(TypeError):
+        _host.snapshot([1], pp.ctypes.data, dt.ctypes.data)
+
+
+def test_new_grads_are_repointed(cpu_plans):
+    ps = _params([(64, 64), (300,)], torch.bfloat16)
+    opt = _opt(ps)
+    plan, group = _build(opt)
+    plan.execute(group, seed=0)
+    assert [int(x) for x in _table(plan)["g"]] == [p.grad.data_ptr() for p in ps]
+    for p in ps:                       # zero_grad(set_to_none=True) + a new backward
+        p.grad = torch.ones_like(p)
+    assert plan.valid_for(group)
+    plan.execute(group, seed=0)
+    assert [int(x) for x in _table(plan)["g"]] == [p.grad.data_ptr() for p in ps]
+    # a grad whose storage is swapped in place keeps its Python object
+    ps[1].grad.data = torch.full((300,), 2.0, dtype=torch.bfloat16)
+    assert plan.valid_for(group)
+    plan.execute(group, seed=0)
+    assert int(_table(plan)["g"][1]) == ps[1].grad.data_ptr()
+
+
+def test_noncontiguous_grad_is_copied(cpu_plans):
+    ps = _params([(32, 64)], torch.bfloat16)
+    opt = _opt(ps)
+    plan, group = _build(opt)
+    ps[0].grad = torch.ones(64, 32, dtype=torch.bfloat16).t()
+    assert plan.valid_for(group)
+    keep = plan._refresh_grads()
+    assert keep[0].is_contiguous() and int(_table(plan)["g"][0]) == keep[0].data_ptr()
+    ps[0].grad_dtype = None                       # torch then accepts a grad of another dtype
+    ps[0].grad = torch.ones(64, 32, dtype=torch.float32).t()
+    assert plan.valid_for(group)
+    with pytest.raises(NotImplementedError):
+        plan._refresh_grads()
+
+
+def test_param_storage_or_dtype_change_invalidates(cpu_plans):
+    ps = _params([(64, 64), (300,)], torch.float32)
+    opt = _opt(ps)
+    plan, group = _build(opt)
+    plan.execute(group, seed=0)
+    assert plan.valid_for(group)
+    ps[0].data = ps[0].data.clone()               # same dtype, new address
+    assert not plan.valid_for(group)
+    plan, group = _build(opt)
+    assert plan.valid_for(group)
+    m = torch.nn.Module()
+    m.w = ps[1]
+    m.to(torch.bfloat16)                           # module cast: same objects, new storage and dtype
+    assert ps[1].dtype == torch.bfloat16 and not plan.valid_for(group)
+
+
+def test_missing_grad_or_inactive_grad_invalidates(cpu_plans):
+    ps = _params([(16,), (16,), (16,)], torch.bfloat16)
+    g2 = ps[2].grad
+    ps[2].grad = None
+    opt = _opt(ps)
+    plan, group = _build(opt)
+    assert plan.valid_for(group)
+    ps[2].grad = g2                               # a parameter outside the plan gains a grad
+    assert not plan.valid_for(group)
+    ps[2].grad = None
+    ps[0].grad = None                             # a plan parameter loses its grad
+    assert not plan.valid_for(group)

@@ -57,13 +57,17 @@ def _lerp_coef(w):
 
 
 class StepPlan:
-    def __init__(self, opt, group, params, kind, native=False):
+    def __init__(self, opt, group, params, kind, native=False, hooked=False):
         self.kind = kind                  # "compact" or "q8"
         self.native = native              # compact group stepped with torch._fused_adamw_ rounding
+        # hooked: a batch of in-backward steps; the caller passes the step counts,
+        # and the group's other parameters may hold grads meanwhile
+        self.hooked = hooked
         self.params = list(params)
         self.param_ids = tuple(id(p) for p in self.params)
         active = set(self.params)
-        self.inactive = [p for p in group["params"] if getattr(p, "requires_grad", False) and p not in active]
+        self.inactive = [] if hooked else [p for p in group["params"]
+                                           if getattr(p, "requires_grad", False) and p not in active]
         self.precision = group["precision"]
         self.decay_norm_only = group["decay_norm_only"]
         self.device = self.params[0].device
@@ -98,6 +102,8 @@ class StepPlan:
     def _build_steps(self):
         vals = [float(st["step"].item()) for st in self.states]
         self.steps = torch.tensor(vals, dtype=torch.float32)
+        if self.hooked:
+            return
         for i, st in enumerate(self.states):
             st["step"] = self.steps[i]
 
@@ -318,14 +324,18 @@ class StepPlan:
         L.check(st, "apexw_grad_clip_coef")
         return coef
 
-    def execute(self, group, seed, inv_scale=None):
+    def execute(self, group, seed, inv_scale=None, lr=None, wd=None, steps=None):
         """Run one optimizer step for the group (cold the first time, replay after).
 
-        inv_scale: 1 / the AMP grad scale handed over by GradScaler, or None."""
+        inv_scale: 1 / the AMP grad scale handed over by GradScaler, or None.
+        lr, wd: replace the group's values; steps: each parameter's step count
+        for this step (already advanced) instead of advancing the plan's own."""
         mode_cold = not self.cold_done
         keep = self._refresh_grads()  # noqa: F841 -- keeps contiguous copies alive until the launch
         stream = torch.cuda.current_stream(self.device).cuda_stream
-        lr, (b1, b2), eps, wd = group["lr"], group["betas"], group["eps"], group["weight_decay"]
+        (b1, b2), eps = group["betas"], group["eps"]
+        lr = group["lr"] if lr is None else lr
+        wd = group["weight_decay"] if wd is None else wd
         sr = bool(group.get("stochastic_rounding", True))
         clip = group.get("clip_grad_norm", None)
         if self.kind == "compact":
@@ -338,7 +348,10 @@ class StepPlan:
             self._prepare_grads(inv_scale, stream)
             sanitize, inv_scale = False, None
         coef = self._clip(clip, sanitize, inv_scale, stream) if clip is not None else None
-        self.steps.add_(1.0)
+        if steps is None:
+            self.steps.add_(1.0)
+        else:
+            self.steps.copy_(torch.tensor(steps, dtype=torch.float32))
         # The reference's replayed compact step takes the bias correction of the
         # first counter for the whole group (optimizer.py:1082-1090); every other
         # path uses each parameter's own count.

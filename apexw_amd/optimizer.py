@@ -11,17 +11,34 @@ multi-tensor kernel launch per parameter group and step (plus three tiny
 launches when global-norm clipping is on).  There is no CPU or torch-op
 fallback; options outside the hot path raise ``NotImplementedError`` at
 construction.
+
+precision="8bit" on a large model (>= 8 trainable tensors, >= 524,288
+elements, no clipping or centralization) turns on the reference's automatic
+runtime acceleration (optimizer.py:2059-2167): fp32 parameters of >= 1024
+elements are converted to bf16 in place, and parameters of >= 16384 elements
+(except the first) are stepped during backward, 14 at a time, by the same
+8-bit kernel (``_flush_auto_8bit_hook_queue``, optimizer.py:2226-2371).
 """
 
 import math
 import warnings
 
+import numpy as np
 import torch
 import torch.nn as nn
 from torch.optim.optimizer import Optimizer
 
+from . import runtime as R
 from . import state as S
 from ._plan import StepPlan
+
+R.install()
+
+AUTO_8BIT_MIN_TENSORS = 8          # optimizer.py:2087
+AUTO_8BIT_MIN_NUMEL = 524_288
+DOWNCAST_MIN_NUMEL = 1024          # optimizer.py:2100
+HOOK_MIN_NUMEL = 16384             # optimizer.py:2131
+HOOK_BATCH = 14                    # optimizer.py:2142
 
 _UNSUPPORTED_FLAGS = ("amsgrad", "nesterov", "cautious", "lion", "maximize",
                       "capturable", "differentiable", "auto_pack", "factored_v", "six_bit")
@@ -137,6 +154,20 @@ class ApexW(Optimizer):
         # seed of the counter-based rounding RNG (drawn from torch's generator, so
         # torch.manual_seed makes runs reproducible)
         self._seed = int(torch.randint(0, 2 ** 62, (1,)).item())
+        self._init_hook_state()
+        if precision == "8bit":
+            self._enable_8bit_runtime_acceleration()
+
+    def _init_hook_state(self):
+        self._has_stepped = False
+        self._auto_hook_handles = []
+        self._auto_hook_queue = []
+        self._auto_hook_stepped_count = 0
+        self._anchor_backward_count = 0
+        self._grad_accum_steps = 1
+        self._grad_accum_steps_known = False
+        self._hook_plans = {}
+        self._fused_backward_enabled = False
 
     def __setstate__(self, state):
         super().__setstate__(state)
@@ -148,6 +179,8 @@ class ApexW(Optimizer):
             group.setdefault("force_compact_v", False)
             group.setdefault("int4_m", False)
         self._plans = {}
+        if not hasattr(self, "_auto_hook_queue"):
+            self._init_hook_state()
 
     # ------------------------------------------------------------------ step
     @torch.no_grad()
@@ -156,6 +189,18 @@ class ApexW(Optimizer):
         if closure is not None:
             with torch.enable_grad():
                 loss = closure()
+        # in-backward 8-bit steps: step what is still queued, then learn the
+        # accumulation count from the backward passes seen (optimizer.py:3371-3381)
+        self._has_stepped = True
+        if self._auto_hook_queue:
+            self._flush_auto_8bit_hook_queue()
+        if self._auto_hook_stepped_count > 0:
+            if not self._grad_accum_steps_known and self._anchor_backward_count > 1:
+                self._grad_accum_steps = self._anchor_backward_count
+                self._grad_accum_steps_known = True
+            self._auto_hook_stepped_count = 0
+            self._anchor_backward_count = 0
+        R.amp_scaled_this_backward = False
         # AMP: GradScaler hands over its scale and found_inf instead of unscaling
         # (_step_supports_amp_scaling); an inf/NaN step is skipped, otherwise the
         # grads are unscaled inside the step kernels (apexw/optimizer.py:3458-3480,
@@ -239,6 +284,147 @@ class ApexW(Optimizer):
 
     def zero_grad(self, set_to_none=True):
         super().zero_grad(set_to_none=set_to_none)
+        self._auto_hook_queue.clear()
+
+    # ------------------------------------------------------------------ in-backward 8-bit steps
+    def _enable_8bit_runtime_acceleration(self, force=False):
+        """bf16 parameters and layer-batched in-backward steps for large 8-bit
+        models (optimizer.py:2059-2167)."""
+        d = self.defaults
+        if not force and (d.get("clip_grad_norm") is not None or d.get("grad_centralization", False)):
+            return
+        trainable = []
+        total = 0
+        for group in self.param_groups:
+            if S.normalize_precision(group.get("precision", "compact")) != "8bit":
+                continue
+            for p in group["params"]:
+                if (isinstance(p, torch.Tensor) and p.requires_grad and not torch.is_complex(p)
+                        and p.dtype != torch.float64):
+                    trainable.append((p, group))
+                    total += p.numel()
+        if not force and (len(trainable) < AUTO_8BIT_MIN_TENSORS or total < AUTO_8BIT_MIN_NUMEL):
+            return
+        if torch.cuda.is_available():
+            torch.backends.cuda.matmul.allow_tf32 = True
+            torch.backends.cudnn.allow_tf32 = True
+            torch.backends.cudnn.benchmark = True
+        converted = False
+        with torch.no_grad():
+            for p, _ in trainable:
+                if p.dtype == torch.float32 and p.numel() >= DOWNCAST_MIN_NUMEL:
+                    # fp16 only on devices without bf16 (compute capability < 8); MI355X has bf16
+                    target = torch.bfloat16
+                    if p.is_cuda and torch.cuda.get_device_capability(p.device)[0] < 8:
+                        target = torch.float16
+                    R.register_downcast(p, torch.float32)
+                    p.data = p.data.to(target)
+                    if p.grad is not None and p.grad.dtype != target:
+                        p.grad = p.grad.to(target)
+                    if target == torch.float16:
+                        R.fp16_active = True
+                    converted = True
+                elif p.dtype == torch.float16:
+                    R.fp16_active = True
+        if converted and torch.cuda.is_available():
+            torch.cuda.empty_cache()
+        self._disable_auto_8bit_hooks()
+        if len(trainable) >= 2:
+            anchor = trainable[0][0]
+            hooked = [(p, g) for p, g in trainable[1:] if p.numel() >= HOOK_MIN_NUMEL]
+            if hooked:
+                for p, g in hooked:
+                    self._auto_hook_handles.append(p.register_post_accumulate_grad_hook(self._layer_hook(p, g)))
+                self._auto_hook_handles.append(anchor.register_post_accumulate_grad_hook(self._anchor_hook))
+        R.register_optimizer(self)
+
+    def _layer_hook(self, param, group):
+        def hook(_):
+            if self._fused_backward_enabled or param.grad is None:
+                return
+            self._auto_hook_queue.append((param, group))
+            if len(self._auto_hook_queue) >= HOOK_BATCH:
+                self._flush_auto_8bit_hook_queue()
+        return hook
+
+    def _anchor_hook(self, _):
+        # the first parameter's grad comes last in backward: step what is queued
+        if self._fused_backward_enabled:
+            return
+        if self._auto_hook_queue:
+            self._flush_auto_8bit_hook_queue()
+        self._anchor_backward_count += 1
+
+    def _disable_auto_8bit_hooks(self):
+        for h in self._auto_hook_handles:
+            h.remove()
+        self._auto_hook_handles.clear()
+        self._auto_hook_queue.clear()
+        self._auto_hook_stepped_count = 0
+        self._anchor_backward_count = 0
+
+    @torch.no_grad()
+    def _flush_auto_8bit_hook_queue(self):
+        """Step the queued parameters with the 8-bit kernel and free their grads
+        (optimizer.py:2226-2371).  With K accumulated backward passes per step
+        (learned by step()), every pass steps with lr * K^-0.4, weight decay
+        wd / (K * K^-0.4) and the grads scaled by K; the stored step counter is
+        (passes - 1) // K + 1 and the bias correction uses the pass count."""
+        if not self._auto_hook_queue:
+            return
+        batch = list(self._auto_hook_queue)
+        self._auto_hook_queue.clear()
+        K = max(1, int(self._grad_accum_steps))
+        mult = 1.0 if K == 1 else K ** -0.40
+        amp = R.last_amp_scale
+        amp_inv = 1.0 / amp if (R.amp_scaled_this_backward and amp is not None and amp > 0.0) else 1.0
+        inv_scale = amp_inv * float(K)
+        by_group, seen = {}, set()
+        for p, group in batch:
+            if p.grad is None or id(p) in seen:
+                continue
+            seen.add(id(p))
+            by_group.setdefault(id(group), (group, []))[1].append(p)
+        for group, params in by_group.values():
+            msteps = []
+            for p in params:
+                st = S.ensure_8bit_state(self.state[p], p, group)
+                mstep = st.get("_hook_mstep", 0) + 1
+                st["_hook_mstep"] = mstep
+                # the reference's CPU path stores (mstep - 1) // K + 1 (optimizer.py:2366-2367);
+                # its CUDA path instead adds 1 every K passes, which differs once K changes
+                st["step"].fill_(float((mstep - 1) // K + 1))
+                msteps.append(mstep)
+                if p.grad.dtype != p.dtype:
+                    p.grad = p.grad.to(p.dtype)
+            lr_eff = float(group["lr"]) * mult
+            wd_raw = float(group["weight_decay"])
+            wd_eff = wd_raw / (float(K) * mult) if wd_raw != 0.0 else 0.0
+            # the step takes the grad scale as a float32 tensor and multiplies by its reciprocal
+            inv = None if inv_scale == 1.0 else float(np.float32(1.0) / np.float32(1.0 / inv_scale))
+            self._hook_plan(group, params).execute(group, self._hook_seed, inv, lr=lr_eff, wd=wd_eff, steps=msteps)
+            for p in params:
+                p.grad = None
+            self._auto_hook_stepped_count += len(params)
+
+    def _hook_plan(self, group, params):
+        key = (id(group), tuple(map(id, params)))
+        plan = self._hook_plans.get(key)
+        if plan is None or not plan.valid_for(group):
+            group["precision"] = S.normalize_precision(group.get("precision", "compact"))
+            for p in params:
+                if p.device.type != "cuda":
+                    raise RuntimeError("apexw_amd runs the optimizer step on the GPU; parameters must be on cuda")
+                if p.dtype not in (torch.float32, torch.bfloat16):
+                    raise NotImplementedError(f"apexw_amd steps fp32/bf16 parameters, got {p.dtype}")
+            plan = StepPlan(self, group, params, "q8", hooked=True)
+            self._hook_plans[key] = plan
+        return plan
+
+    @property
+    def _hook_seed(self):
+        # in-backward batches restart the tensor index at 0: give them their own RNG stream
+        return (self._seed ^ 0x5DEECE66D9E3779B) & (2 ** 64 - 1)
 
     # ------------------------------------------------------------------ reporting
     def get_state_memory_mb(self):

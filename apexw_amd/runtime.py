@@ -1,0 +1,175 @@
+"""Process-wide runtime state of the automatic 8-bit path.
+
+The reference keeps module-level registries and patches torch when its
+optimizer module is imported (apexw/optimizer.py:1346-1507); this module does
+the same for ``apexw_amd``:
+
+* ``DOWNCAST``: parameters an 8-bit ApexW converted from fp32 to bf16 at
+  construction.  They are converted back (and every optimizer's in-backward
+  hooks removed) when another optimizer is constructed -- unless it is another
+  8-bit ApexW and no 8-bit ApexW has stepped yet --, when a module owning one
+  of them loads a state dict, and when ``torch.cuda.reset_peak_memory_stats``
+  is called after a step.
+* AMP detection for the in-backward steps: ``GradScaler.scale`` records the
+  scale of the running backward (the in-backward steps unscale with it),
+  ``GradScaler.update`` forgets it; with fp16 parameters in play the scale is
+  clamped to 256.  ``GradScaler._unscale_grads_`` accepts fp16 grads for
+  optimizers that unscale inside their step.
+"""
+
+import weakref
+
+import torch
+import torch.nn as nn
+from torch.optim.optimizer import Optimizer
+
+DOWNCAST = {}      # id(p) -> (weakref to p, dtype before the downcast)
+OPTIMIZERS = []    # weakrefs to the ApexW instances holding in-backward hooks
+
+fp16_active = False
+amp_scaled_this_backward = False
+last_amp_scale = None
+_installed = False
+
+
+def _is_downcast(p):
+    entry = DOWNCAST.get(id(p))
+    return entry is not None and entry[0]() is p
+
+
+def register_downcast(p, orig_dtype):
+    if not _is_downcast(p):
+        DOWNCAST[id(p)] = (weakref.ref(p), orig_dtype)
+
+
+def register_optimizer(opt):
+    if not any(r() is opt for r in OPTIMIZERS):
+        OPTIMIZERS.append(weakref.ref(opt))
+
+
+def any_stepped():
+    return any(r() is not None and getattr(r(), "_has_stepped", False) for r in OPTIMIZERS)
+
+
+def restore_all_downcast_params():
+    """Convert every downcast parameter (and its grad) back to its original dtype
+    and remove every optimizer's in-backward hooks (optimizer.py:1352-1382)."""
+    global fp16_active, amp_scaled_this_backward
+    fp16_active = False
+    amp_scaled_this_backward = False
+    for ref in list(OPTIMIZERS):
+        opt = ref()
+        if opt is not None:
+            opt._disable_auto_8bit_hooks()
+    OPTIMIZERS.clear()
+    if not DOWNCAST:
+        return
+    with torch.no_grad():
+        for ref, dtype in list(DOWNCAST.values()):
+            p = ref()
+            if p is None or p.dtype == dtype:
+                continue
+            p.data = p.data.to(dtype)
+            if p.grad is not None and p.grad.dtype != dtype:
+                p.grad = p.grad.to(dtype)
+    DOWNCAST.clear()
+
+
+def install():
+    """Patch torch once per process (optimizer.py:1385-1507)."""
+    global _installed
+    if _installed:
+        return
+    _installed = True
+    _patch_grad_scaler()
+    _patch_optimizer_init()
+    _patch_module_load_state_dict()
+    _patch_reset_peak_memory_stats()
+
+
+def _patch_grad_scaler():
+    from torch.amp.grad_scaler import GradScaler
+    if getattr(GradScaler, "_apexw_amd_patched", False):
+        return
+    orig_unscale, orig_scale, orig_update = GradScaler._unscale_grads_, GradScaler.scale, GradScaler.update
+
+    def _unscale_grads_(self, optimizer, inv_scale, found_inf, allow_fp16=False):
+        if getattr(optimizer, "_step_supports_amp_scaling", False):
+            allow_fp16 = True
+        return orig_unscale(self, optimizer, inv_scale, found_inf, allow_fp16)
+
+    def scale(self, outputs):
+        global amp_scaled_this_backward, last_amp_scale
+        if getattr(self, "_enabled", False):
+            if isinstance(outputs, torch.Tensor) and self._scale is None:
+                self._lazy_init_scale_growth_tracker(outputs.device)
+            if self._scale is not None:
+                if fp16_active:
+                    with torch.no_grad():
+                        self._scale.clamp_(max=256.0)
+                if last_amp_scale is None:
+                    last_amp_scale = float(self._scale.item())
+                amp_scaled_this_backward = True
+        return orig_scale(self, outputs)
+
+    def update(self, new_scale=None):
+        global amp_scaled_this_backward, last_amp_scale
+        res = orig_update(self, new_scale=new_scale)
+        amp_scaled_this_backward = False
+        last_amp_scale = None
+        return res
+
+    GradScaler._unscale_grads_ = _unscale_grads_
+    GradScaler.scale = scale
+    GradScaler.update = update
+    GradScaler._apexw_amd_patched = True
+
+
+def _patch_optimizer_init():
+    if getattr(Optimizer, "_apexw_amd_init_patched", False):
+        return
+    orig_init = Optimizer.__init__
+
+    def __init__(self, params, defaults):
+        if DOWNCAST:
+            from .optimizer import ApexW
+            from .state import normalize_precision
+            is_8bit = (isinstance(self, ApexW) and isinstance(defaults, dict)
+                       and normalize_precision(defaults.get("precision", "compact")) == "8bit")
+            if not is_8bit or any_stepped():
+                restore_all_downcast_params()
+        return orig_init(self, params, defaults)
+
+    Optimizer.__init__ = __init__
+    Optimizer._apexw_amd_init_patched = True
+
+
+def _patch_module_load_state_dict():
+    if getattr(nn.Module, "_apexw_amd_load_sd_patched", False):
+        return
+    orig_load = nn.Module.load_state_dict
+
+    def load_state_dict(self, state_dict, *args, **kwargs):
+        if DOWNCAST and any(_is_downcast(p) for p in self.parameters()):
+            restore_all_downcast_params()
+        return orig_load(self, state_dict, *args, **kwargs)
+
+    nn.Module.load_state_dict = load_state_dict
+    nn.Module._apexw_amd_load_sd_patched = True
+
+
+def _patch_reset_peak_memory_stats():
+    if getattr(torch.cuda, "_apexw_amd_reset_peak_patched", False):
+        return
+    orig_reset = torch.cuda.reset_peak_memory_stats
+
+    def reset_peak_memory_stats(*args, **kwargs):
+        if DOWNCAST:
+            if any_stepped():
+                restore_all_downcast_params()
+            if torch.cuda.is_available():
+                torch.cuda.empty_cache()
+        return orig_reset(*args, **kwargs)
+
+    torch.cuda.reset_peak_memory_stats = reset_peak_memory_stats
+    torch.cuda._apexw_amd_reset_peak_patched = True

@@ -106,6 +106,55 @@ def block_size_8bit(p, user_bs):
     return 64
 
 
+def _auto_subbyte(p, group, bs):
+    """NF4 m + quad v eligibility (optimizer.py:2192-2201, the same rule in _init_group)."""
+    n = p.numel()
+    raw_int4 = group.get("int4_m", group.get("four_bit", None))
+    pow2 = bs >= 64 and (bs & (bs - 1)) == 0
+    return (raw_int4 is not False and n >= 16384 and n % 4 == 0 and pow2
+            and (p.dim() < 2 or min(p.shape) >= 8))
+
+
+def _q8_buffers(st, p, bs, int4, quad):
+    """8-bit state buffers: NF4 (packed, fill code 7) or INT8 m, quad or full log-u8 v,
+    per-block fp32 scales (optimizer.py:2210-2223)."""
+    n, dev = p.numel(), p.device
+    st.update(is_8bit=True, block_size_8bit=bs, is_factored_v=False, is_6bit_m=False,
+              is_4bit_m=bool(int4), is_quad_v=bool(quad), m_numel=n)
+    st["state_dtype"] = torch.int8
+    st["state_dtype_v"] = torch.uint8
+    nblk = (n + bs - 1) // bs
+    if int4:
+        st["exp_avg"] = torch.full(((n + 1) // 2,), 0x77, dtype=torch.uint8, device=dev)
+        st["exp_avg_scales"] = torch.full((nblk, 1), 1e-12, dtype=torch.float32, device=dev)
+    else:
+        st["exp_avg"] = torch.zeros(p.shape, dtype=torch.int8, device=dev)
+        st["exp_avg_scales"] = torch.full((nblk, 1), 1e-12 / 127.0, dtype=torch.float32, device=dev)
+    if quad:
+        st["exp_avg_sq"] = torch.zeros((n // 4,), dtype=torch.uint8, device=dev)
+    else:
+        st["exp_avg_sq"] = torch.zeros(p.shape, dtype=torch.uint8, device=dev)
+    st["exp_avg_sq_scales"] = torch.full((nblk, 1), 1e-12, dtype=torch.float32, device=dev)
+
+
+def ensure_8bit_state(st, p, group):
+    """The reference's _ensure_8bit_state_initialized (optimizer.py:2169-2224): the
+    state the in-backward steps create lazily.  Unlike _init_group it makes
+    8-bit buffers at any size and takes NF4 m exactly when quad v applies."""
+    if "exp_avg" in st and "exp_avg_sq" in st:
+        if st["exp_avg"].device != p.device:
+            st["exp_avg"] = st["exp_avg"].to(p.device)
+        if st["exp_avg_sq"].device != p.device:
+            st["exp_avg_sq"] = st["exp_avg_sq"].to(p.device)
+        return st
+    st["stochastic_rounding"] = bool(group.get("stochastic_rounding", True))
+    st["step"] = torch.tensor(0.0, dtype=torch.float32)
+    bs = block_size_8bit(p, group.get("block_size"))
+    sub = _auto_subbyte(p, group, bs)
+    _q8_buffers(st, p, bs, sub, sub)
+    return st
+
+
 def init_state(p, group, peft_ctx):
     """Fresh state dict for ``p`` (keys and dtypes as the reference's _init_group)."""
     prec = group["precision"]
@@ -118,28 +167,10 @@ def init_state(p, group, peft_ctx):
     if prec == "8bit" and n >= 64:
         bs = block_size_8bit(p, group.get("block_size"))
         narrow = p.dim() >= 2 and min(p.shape) <= 32 and n < 2048
+        auto_sub = _auto_subbyte(p, group, bs)
         raw_int4 = group.get("int4_m", group.get("four_bit", None))
-        pow2 = bs >= 64 and (bs & (bs - 1)) == 0
-        auto_sub = (raw_int4 is not False and n >= 16384 and n % 4 == 0 and pow2
-                    and (p.dim() < 2 or min(p.shape) >= 8))
         int4 = auto_sub or (bool(raw_int4) and n >= 512 and n >= bs and not narrow and not is_peft)
-        quad = bool(auto_sub and int4)
-        st.update(is_8bit=True, block_size_8bit=bs, is_factored_v=False, is_6bit_m=False,
-                  is_4bit_m=int4, is_quad_v=quad, m_numel=n)
-        st["state_dtype"] = torch.int8
-        st["state_dtype_v"] = torch.uint8
-        nblk = (n + bs - 1) // bs
-        if int4:
-            st["exp_avg"] = torch.full(((n + 1) // 2,), 0x77, dtype=torch.uint8, device=dev)
-            st["exp_avg_scales"] = torch.full((nblk, 1), 1e-12, dtype=torch.float32, device=dev)
-        else:
-            st["exp_avg"] = torch.zeros(p.shape, dtype=torch.int8, device=dev)
-            st["exp_avg_scales"] = torch.full((nblk, 1), 1e-12 / 127.0, dtype=torch.float32, device=dev)
-        if quad:
-            st["exp_avg_sq"] = torch.zeros((n // 4,), dtype=torch.uint8, device=dev)
-        else:
-            st["exp_avg_sq"] = torch.zeros(p.shape, dtype=torch.uint8, device=dev)
-        st["exp_avg_sq_scales"] = torch.full((nblk, 1), 1e-12, dtype=torch.float32, device=dev)
+        _q8_buffers(st, p, bs, int4, bool(auto_sub and int4))
         return st
     if prec == "8bit":
         st.update(is_8bit=False, is_factored_v=False, is_6bit_m=False, is_4bit_m=False, is_quad_v=False)

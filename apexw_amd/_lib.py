@@ -13,7 +13,7 @@ import numpy as np
 
 from ._build import LIB_PATH
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 # dtype codes
 F32, BF16, F16, U8, I8 = 0, 1, 2, 3, 4
@@ -29,7 +29,7 @@ FLAG_SCALAR = 1 << 13
 
 COMPACT_UNIT = 2048
 
-MODE_COLD, MODE_REPLAY, MODE_NATIVE = 0, 1, 2
+MODE_COLD, MODE_REPLAY, MODE_NATIVE, MODE_SINGLE = 0, 1, 2, 3
 
 HP_SR = 1 << 0
 HP_SR_V = 1 << 1

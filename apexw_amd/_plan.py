@@ -57,16 +57,18 @@ def _lerp_coef(w):
 
 
 class StepPlan:
-    def __init__(self, opt, group, params, kind, native=False, hooked=False):
+    def __init__(self, opt, group, params, kind, native=False, hooked=False, single=False):
         self.kind = kind                  # "compact" or "q8"
         self.native = native              # compact group stepped with torch._fused_adamw_ rounding
         # hooked: a batch of in-backward steps; the caller passes the step counts,
         # and the group's other parameters may hold grads meanwhile
-        self.hooked = hooked
+        # single: enable_fused_backward's per-parameter update (APEXW_MODE_SINGLE)
+        self.single = single
+        self.hooked = hooked or single
         self.params = list(params)
         self.param_ids = tuple(id(p) for p in self.params)
         active = set(self.params)
-        self.inactive = [] if hooked else [p for p in group["params"]
+        self.inactive = [] if self.hooked else [p for p in group["params"]
                                            if getattr(p, "requires_grad", False) and p not in active]
         self.precision = group["precision"]
         self.decay_norm_only = group["decay_norm_only"]
@@ -165,11 +167,11 @@ class StepPlan:
         self.g_ptrs = np.zeros(n, dtype=np.uint64)     # grad pointers the table was built from
         self.g_scan = np.zeros(n, dtype=np.uint64)     # the scan's current grad pointers
         self._scan_status = None
-        if self.gc:
+        if self.gc and not self.single:
             self._build_prep()
         self._fast_static = None
         self.counts = counts
-        self.kind_code = 0 if self.kind == "compact" else 1
+        self.kind_code = (3 if self.single else 0) if self.kind == "compact" else 1
         self._lib = L.load()
         self.clip_ws = None
         self.d_table = None
@@ -262,7 +264,7 @@ class StepPlan:
             self.g_scan[:] = [g.data_ptr() for g in keep]
         ptrs = self.g_scan.copy()
         self.g_ptrs[:] = ptrs
-        if self.gc:
+        if self.gc and not self.single:
             # the prepared copies feed the clip and the step; the sources feed the preparation
             if self.d_prep is None or not np.array_equal(ptrs, self.host_prep["g"]):
                 self.host_prep["g"] = ptrs
@@ -300,13 +302,13 @@ class StepPlan:
                 t = L.Tensor(*(int(row[k]) for k in ("p", "g", "m", "v", "m_scale", "v_scale", "n", "flags", "block")))
                 L.check(lib.apexw_check_tensor(ctypes_ref(t), self.kind_code),
                         f"tensor {i} ({tuple(self.params[i].shape)})")
-                if self.kind == "q8":
+                if self.kind == "q8" and not self.single:
                     # full-block eligibility apart from alignment: same descriptor on aligned stand-in pointers
                     t.p = t.g = t.m = t.v = 256
                     t.flags = int(row["flags"]) & ~L.FLAG_SCALAR
                     fast_static[i] = lib.apexw_check_tensor(ctypes_ref(t), 2) == 0
             self._fast_static = fast_static
-        return (self._fast_static & ~scalar) if self.kind == "q8" else None
+        return (self._fast_static & ~scalar) if self.kind == "q8" and not self.single else None
 
     # ------------------------------------------------------------------ launch
     def _clip(self, clip, sanitize, inv_scale, stream):
@@ -342,7 +344,10 @@ class StepPlan:
             sanitize = mode_cold or clip is not None
         else:
             sanitize = mode_cold and clip is not None
-        if self.gc:
+        if self.single:
+            # the per-parameter update takes the grads as they are (no sanitize, clip, AMP or centralization)
+            sanitize, clip, inv_scale = False, None, None
+        elif self.gc:
             # _prepare_grads with centralization: sanitize, unscale, centralize;
             # the clip and the step then see finite, unscaled grads
             self._prepare_grads(inv_scale, stream)
@@ -395,6 +400,19 @@ class StepPlan:
         hp.beta1, hp.one_minus_beta1 = b1, 1.0 - b1
         hp.beta2, hp.one_minus_beta2 = b2, 1.0 - b2
         flags = 0
+        if self.single:
+            # _step_single_param_fused's scalars (apexw/optimizer.py:2395-2407)
+            hp.wd_factor = max(1.0 - lr * wd, 0.0) if wd != 0 else 1.0
+            hp.step_size = lr * bc2s / bc1
+            hp.eps_scaled = eps * bc2s
+            hp.eps = eps
+            hp.gain_hi = 1.0 + 0.20 * b1
+            hp.gain_lo = 1.0 - 0.35 * b1
+            hp.mode = L.MODE_SINGLE
+            hp.seed = seed
+            hp.step = step & 0xFFFFFFFF
+            hp.flags = L.HP_SR if (sr and self.kind == "q8") else 0
+            return hp
         if self.kind == "q8":
             hp.wd_factor = max(1.0 - lr * wd, 0.0) if wd != 0 else 1.0
             hp.step_size = lr * bc2s / bc1

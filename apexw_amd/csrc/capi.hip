@@ -74,7 +74,10 @@ int blocks_per_cu(const void* kernel) {
 
 bool hp_ok(const apexw_hparams* hp) {
   if (!hp) return false;
-  if (hp->mode > APEXW_MODE_NATIVE) return false;
+  if (hp->mode > APEXW_MODE_SINGLE) return false;
+  // the per-parameter in-backward update uses the grads as given
+  if (hp->mode == APEXW_MODE_SINGLE && (hp->flags & (APEXW_HP_SANITIZE | APEXW_HP_CLIP | APEXW_HP_UNSCALE)))
+    return false;
   if ((hp->flags & APEXW_HP_CLIP) && !hp->clip_coef) return false;
   if ((hp->flags & APEXW_HP_UNSCALE) && !(hp->grad_inv_scale > 0.0f)) return false;
   return true;
@@ -100,9 +103,9 @@ int apexw_abi_version(void) { return APEXW_ABI_VERSION; }
 // (0 = compact, 1 = 8-bit).  Returns APEXW_OK or the reason it is unsupported.
 int apexw_check_tensor(const apexw_tensor* t, int32_t kind) {
   if (!t || !t->p || !t->g || !t->m || !t->v || t->n <= 0) return APEXW_ERR_ARG;
-  if (kind == 0) {
+  if (kind == 0 || kind == 3) {
     if (!apexw_compact_flags_ok(t->flags)) return APEXW_ERR_DTYPE;
-    if ((t->flags & APEXW_FLAG_QUAD) && (t->n % 4) != 0) return APEXW_ERR_ARG;
+    if ((t->flags & APEXW_FLAG_QUAD) && (kind == 3 || (t->n % 4) != 0)) return APEXW_ERR_ARG;
   } else if (kind == 1 || kind == 2) {
     if (!apexw_q8_flags_ok(t->flags, t->block, t->n)) return APEXW_ERR_DTYPE;
     if (kind == 2 && !apexw_q8_fast_eligible(t->flags, t->block)) return APEXW_ERR_DTYPE;
@@ -129,6 +132,7 @@ int apexw_q8_step(const apexw_tensor* tensors, int32_t n_tensors, const apexw_un
   if (!tensors || !units || n_tensors <= 0 || n_units < 0 || !hp_ok(hp)) return APEXW_ERR_ARG;
   if (n_fast_units < 0 || n_fast_f32_units < 0 || n_fast_units + n_fast_f32_units > n_units) return APEXW_ERR_ARG;
   if (hp->mode == APEXW_MODE_NATIVE) return APEXW_ERR_ARG;
+  if (hp->mode == APEXW_MODE_SINGLE && (n_fast_units || n_fast_f32_units)) return APEXW_ERR_ARG;
   int st = APEXW_OK;
   if (n_fast_units > 0)
     st = apexw_launch_q8_fast(tensors, n_fast_units, units, hp, APEXW_BF16, (hipStream_t)stream);

@@ -13,6 +13,7 @@
 //   cold   = ApexW._multi_tensor_step   (apexw/optimizer.py:5297-5887)
 //   replay = FastExecutionPlan.execute_foreach (apexw/optimizer.py:1069-1341)
 //   native = torch._fused_adamw_ as called by _fused_step (apexw/optimizer.py:4737-4835)
+//   single = ApexW._step_single_param_fused, compact branch (apexw/optimizer.py:2458-2471)
 #include "common.h"
 
 namespace {
@@ -50,6 +51,25 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
   for (int j = 0; j < 8; ++j) rnd_bits[j] = (sr || srv) ? rng_at(c.key, e0 + (uint32_t)j) : 0u;
 #pragma unroll
   for (int j = 0; j < 8; ++j) g[j] = prep_grad<GD>(g[j], c);
+
+  if constexpr (!QUAD) {
+    if (hp.mode == APEXW_MODE_SINGLE) {
+      // p.mul_(wd) in the parameter dtype (fp32 scalar), fp32 moments
+      // (mul_ then add_ with alpha: one FMA; addcmul_: one FMA), p.addcdiv_ in
+      // fp32 rounded once, m and v rounded once on store
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float pf = wd ? rnd<PD>(p[j] * hp.wd_factor) : p[j];
+        const float mf = fmaf(hp.one_minus_beta1, g[j], m[j] * hp.beta1);
+        const float vf = fmaf(hp.one_minus_beta2 * g[j], g[j], v[j] * hp.beta2);
+        const float den = sqrtf(vf) + hp.eps_scaled;
+        p[j] = rnd<PD>(pf + (-hp.step_size * mf) / den);
+        m[j] = rnd<MD>(mf);
+        v[j] = rnd<VD>(vf);
+      }
+      return;
+    }
+  }
 
   if (hp.mode == APEXW_MODE_NATIVE) {
     // torch._fused_adamw_: fp32 math on loaded values, one rounding per stored tensor.
@@ -245,6 +265,7 @@ __global__ __launch_bounds__(256) void compact_step_kernel(const apexw_tensor* _
     const uint32_t pd = (t.flags >> APEXW_FLAG_PDT_SHIFT) & 3u;
     const uint32_t vd = (t.flags >> APEXW_FLAG_VDT_SHIFT) & 3u;
     const bool quad = t.flags & APEXW_FLAG_QUAD;
+    if (quad && hp.mode == APEXW_MODE_SINGLE) continue;  // rejected on the host; never read v out of range
     if (pd == APEXW_F32) {
       if (vd == APEXW_F32) compact_group<APEXW_F32, APEXW_BF16, APEXW_F32, false>(t, start, k, c);
       else if (quad) compact_group<APEXW_F32, APEXW_BF16, APEXW_BF16, true>(t, start, k, c);

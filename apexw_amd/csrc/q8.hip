@@ -141,7 +141,12 @@ APEXW_DEV float q8_param(float p, float upd, float decay, uint32_t tflags, bool 
 // One quantization block per wavefront, any layout (INT8 m, fp32 params, other
 // block sizes, unaligned tensors).  Runs in its own kernel so that its register
 // footprint does not lower the occupancy of the bf16 NF4 kernel below.
-template <int PD, bool NF4, bool QUAD>
+// SINGLE: the per-parameter in-backward update (ApexW._step_single_param_fused,
+// apexw/optimizer.py:2411-2457): raw fp32 grads, m = b1 m + (1-b1) g,
+// lookahead b1 m' + (1-b1) g, denominator sqrt(v) + eps_scaled without the eps
+// floor, p decayed in fp32 then p + (-step_size * num) / den, INT8 m
+// requantised from its own absmax (no EMA, no SR).
+template <int PD, bool NF4, bool QUAD, bool SINGLE>
 APEXW_DEV void q8_block(const apexw_tensor& t, uint32_t tix, uint32_t blk, const Q8Ctx& c) {
   constexpr int GD = PD;
   const apexw_hparams& hp = *c.hp;
@@ -240,15 +245,21 @@ APEXW_DEV void q8_block(const apexw_tensor& t, uint32_t tix, uint32_t blk, const
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       h[j] = sr ? rng_at(key, (uint32_t)(e0 + j)) : 0u;
-      g[j] = q8_grad<GD>(g[j], tflags, c);
-      m[j] = lerp_to(m[j], g[j], hp.lerp_coef, hp.flags & APEXW_HP_LERP_HI);
+      if constexpr (SINGLE) {
+        m[j] = fmaf(hp.one_minus_beta1, g[j], m[j] * hp.beta1);
+      } else {
+        g[j] = q8_grad<GD>(g[j], tflags, c);
+        m[j] = lerp_to(m[j], g[j], hp.lerp_coef, hp.flags & APEXW_HP_LERP_HI);
+      }
     }
     float num[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float look = lerp_to(g[j], m[j], hp.look_coef, hp.flags & APEXW_HP_LOOK_HI);
+      const float look = SINGLE ? fmaf(hp.one_minus_beta1, g[j], m[j] * hp.beta1)
+                                : lerp_to(g[j], m[j], hp.look_coef, hp.flags & APEXW_HP_LOOK_HI);
       num[j] = look * ((m[j] * g[j] >= 0.0f) ? hp.gain_hi : hp.gain_lo);
     }
+    float dens[8] = {1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f};  // SINGLE: denominators
     float upd[8];
     if constexpr (QUAD) {
 #pragma unroll
@@ -260,6 +271,12 @@ APEXW_DEV void q8_block(const apexw_tensor& t, uint32_t tix, uint32_t blk, const
         s = s + g[b + 2] * g[b + 2];
         s = s + g[b + 3] * g[b + 3];
         float vq = fmaf(hp.one_minus_beta2, s * 0.25f, v[q] * hp.beta2);
+        if constexpr (SINGLE) {
+          // the update sees v as computed; the quantizer's nan_to_num only affects the stored codes
+          const float den = sqrtf(vq) + hp.eps_scaled;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) dens[b + i] = den;
+        }
         if (!(fabsf(vq) <= 3.402823466e38f)) vq = 0.0f;  // nan_to_num(0, 0, 0)
         v[q] = vq;
         const float den = fmaxf(sqrtf(vq) + hp.eps_scaled, hp.eps);
@@ -270,13 +287,24 @@ APEXW_DEV void q8_block(const apexw_tensor& t, uint32_t tix, uint32_t blk, const
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         float vf = fmaf(hp.one_minus_beta2 * g[j], g[j], v[j] * hp.beta2);
+        if constexpr (SINGLE) dens[j] = sqrtf(vf) + hp.eps_scaled;
         if (!(fabsf(vf) <= 3.402823466e38f)) vf = 0.0f;
         v[j] = vf;
         const float den = fmaxf(sqrtf(vf) + hp.eps_scaled, hp.eps);
         upd[j] = (num[j] / den) * hp.step_size;
       }
     }
-    if constexpr (PD == APEXW_F32) {
+    if constexpr (SINGLE) {
+      // p.mul_(wd) (fp32, on a float copy for 16-bit p), p.addcdiv_(num, den, -step_size),
+      // then SR or round-to-nearest into a 16-bit parameter
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float pp = (tflags & APEXW_FLAG_WD) ? p[j] * hp.wd_factor : p[j];
+        const float x = pp + (-hp.step_size * num[j]) / dens[j];
+        if constexpr (PD == APEXW_F32) p[j] = x;
+        else p[j] = sr ? sr_round<PD>(x, h[j]) : rnd<PD>(x);
+      }
+    } else if constexpr (PD == APEXW_F32) {
       if (generic) {
         // p.mul_(decay); p.addcdiv_(num, den, value=-step_size)
 #pragma unroll
@@ -327,7 +355,7 @@ APEXW_DEV void q8_block(const apexw_tensor& t, uint32_t tix, uint32_t blk, const
   vmax = wave_max(vmax);
   float ms = fmaxf(amax, 1e-12f);
   if (!NF4) ms = ms / 127.0f;
-  ms = fmaxf(ms, ms_old * 0.9f);
+  if (NF4 || !SINGLE) ms = fmaxf(ms, ms_old * 0.9f);
   float vs = fmaxf(vmax, 1e-12f);
   vs = fmaxf(vs, vs_old * 0.95f);
   if (lane == 0) {
@@ -351,7 +379,7 @@ APEXW_DEV void q8_block(const apexw_tensor& t, uint32_t tix, uint32_t blk, const
         mc[j] = sr ? nf4_sr(x, unit_uniform(r), c.code) : nf4_rne_tab(x, c.midtab);
       } else {
         float y = mnew[k][j] / ms;
-        if (sr) y = y + (unit_uniform(r) - 0.5f);
+        if (sr && !SINGLE) y = y + (unit_uniform(r) - 0.5f);
         y = fminf(fmaxf(rintf(y), -127.0f), 127.0f);
         mc[j] = (uint32_t)(int32_t)y & 0xFFu;
       }
@@ -775,13 +803,28 @@ APEXW_DEV void q8_block_fast(const apexw_tensor& t, uint32_t tix, uint32_t blk, 
 }
 
 // Tensors under 64 elements in 8-bit mode keep 16-bit m/v (optimizer.py:4688-4735).
-template <int PD, int VD>
+// SINGLE: the per-parameter in-backward update of such a tensor
+// (apexw/optimizer.py:2458-2471): p.mul_(wd) in the parameter dtype, fp32
+// moments, p.addcdiv_ rounded once, m and v rounded once on store.
+template <int PD, int VD, bool SINGLE>
 APEXW_DEV void q8_dense16(const apexw_tensor& t, const Q8Ctx& c) {
   constexpr int GD = PD;
   const apexw_hparams& hp = *c.hp;
   const int lane = lane_id();
   if (lane >= t.n) return;
   const int64_t i = lane;
+  if constexpr (SINGLE) {
+    float p = load1<PD>(t.p, i);
+    const float g = load1<GD>(t.g, i);
+    if (t.flags & APEXW_FLAG_WD) p = rnd<PD>(p * hp.wd_factor);
+    const float mf = fmaf(hp.one_minus_beta1, g, load1<APEXW_BF16>(t.m, i) * hp.beta1);
+    const float vf = fmaf(hp.one_minus_beta2 * g, g, load1<VD>(t.v, i) * hp.beta2);
+    const float den = sqrtf(vf) + hp.eps_scaled;
+    store1<APEXW_BF16>(t.m, i, rnd<APEXW_BF16>(mf));
+    store1<VD>(t.v, i, rnd<VD>(vf));
+    store1<PD>(t.p, i, rnd<PD>(p + (-hp.step_size * mf) / den));
+    return;
+  }
   float p = load1<PD>(t.p, i);
   float g = q8_grad<GD>(load1<GD>(t.g, i), t.flags, c);
   if (t.flags & APEXW_FLAG_WD) p = rnd<PD>(p * hp.wd_factor);
@@ -846,6 +889,7 @@ __global__ __launch_bounds__(256) void q8_fast_kernel(const apexw_tensor* __rest
   }
 }
 
+template <bool SINGLE>
 __global__ __launch_bounds__(256) void q8_step_kernel(const apexw_tensor* __restrict__ tensors,
                                                       const apexw_unit* __restrict__ units,
                                                       int64_t n_units, apexw_hparams hp) {
@@ -874,23 +918,23 @@ __global__ __launch_bounds__(256) void q8_step_kernel(const apexw_tensor* __rest
     if (f & APEXW_FLAG_DENSE16) {
       const uint32_t vd = (f >> APEXW_FLAG_VDT_SHIFT) & 3u;
       if (pd == APEXW_F32) {
-        if (vd == APEXW_F32) q8_dense16<APEXW_F32, APEXW_F32>(t, c);
-        else q8_dense16<APEXW_F32, APEXW_BF16>(t, c);
+        if (vd == APEXW_F32) q8_dense16<APEXW_F32, APEXW_F32, SINGLE>(t, c);
+        else q8_dense16<APEXW_F32, APEXW_BF16, SINGLE>(t, c);
       } else {
-        if (vd == APEXW_F32) q8_dense16<APEXW_BF16, APEXW_F32>(t, c);
-        else q8_dense16<APEXW_BF16, APEXW_BF16>(t, c);
+        if (vd == APEXW_F32) q8_dense16<APEXW_BF16, APEXW_F32, SINGLE>(t, c);
+        else q8_dense16<APEXW_BF16, APEXW_BF16, SINGLE>(t, c);
       }
       continue;
     }
     const bool nf4 = f & APEXW_FLAG_NF4, quad = f & APEXW_FLAG_QUAD;
     if (pd == APEXW_F32) {
-      if (nf4 && quad) q8_block<APEXW_F32, true, true>(t, un.tensor, un.unit, c);
-      else if (nf4) q8_block<APEXW_F32, true, false>(t, un.tensor, un.unit, c);
-      else q8_block<APEXW_F32, false, false>(t, un.tensor, un.unit, c);
+      if (nf4 && quad) q8_block<APEXW_F32, true, true, SINGLE>(t, un.tensor, un.unit, c);
+      else if (nf4) q8_block<APEXW_F32, true, false, SINGLE>(t, un.tensor, un.unit, c);
+      else q8_block<APEXW_F32, false, false, SINGLE>(t, un.tensor, un.unit, c);
     } else {
-      if (nf4 && quad) q8_block<APEXW_BF16, true, true>(t, un.tensor, un.unit, c);
-      else if (nf4) q8_block<APEXW_BF16, true, false>(t, un.tensor, un.unit, c);
-      else q8_block<APEXW_BF16, false, false>(t, un.tensor, un.unit, c);
+      if (nf4 && quad) q8_block<APEXW_BF16, true, true, SINGLE>(t, un.tensor, un.unit, c);
+      else if (nf4) q8_block<APEXW_BF16, true, false, SINGLE>(t, un.tensor, un.unit, c);
+      else q8_block<APEXW_BF16, false, false, SINGLE>(t, un.tensor, un.unit, c);
     }
   }
 }
@@ -915,8 +959,13 @@ bool apexw_q8_flags_ok(uint32_t flags, uint32_t block, int64_t n) {
 
 int apexw_launch_q8(const apexw_tensor* tensors, int64_t n_units, const apexw_unit* units,
                     const apexw_hparams* hp, hipStream_t stream) {
-  const int grid = apexw_resident_grid((const void*)q8_step_kernel, n_units);
-  hipLaunchKernelGGL(q8_step_kernel, dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
+  if (hp->mode == APEXW_MODE_SINGLE) {
+    const int grid = apexw_resident_grid((const void*)q8_step_kernel<true>, n_units);
+    hipLaunchKernelGGL(q8_step_kernel<true>, dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
+  } else {
+    const int grid = apexw_resident_grid((const void*)q8_step_kernel<false>, n_units);
+    hipLaunchKernelGGL(q8_step_kernel<false>, dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
+  }
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }
 

@@ -22,6 +22,7 @@ elements are converted to bf16 in place, and parameters of >= 16384 elements
 
 import math
 import warnings
+from collections import defaultdict
 
 import numpy as np
 import torch
@@ -167,6 +168,7 @@ class ApexW(Optimizer):
         self._grad_accum_steps = 1
         self._grad_accum_steps_known = False
         self._hook_plans = {}
+        self._single_plans = {}
         self._fused_backward_enabled = False
 
     def __setstate__(self, state):
@@ -420,6 +422,85 @@ class ApexW(Optimizer):
             plan = StepPlan(self, group, params, "q8", hooked=True)
             self._hook_plans[key] = plan
         return plan
+
+    # ------------------------------------------------------------------ fused backward
+    def enable_fused_backward(self, model=None, grad_accum_steps=1):
+        """Step every parameter inside backward, as soon as its grad is accumulated,
+        and free the grad (optimizer.py:1986-2034).  With grad_accum_steps = K a
+        parameter is stepped on every K-th grad it receives; ``step()`` then has
+        nothing left to do.  The update is the reference's per-parameter one
+        (``_step_single_param_fused``), not the fused multi-tensor step."""
+        self._fused_backward_enabled = True
+        self._grad_accum_steps = max(1, int(grad_accum_steps))
+        self._accum_counter = defaultdict(int)
+        self._fused_backward_handles = []
+        if model is not None and hasattr(model, "parameters"):
+            to_hook = [p for p in model.parameters() if p.requires_grad]
+        else:
+            to_hook = [p for g in self.param_groups for p in g["params"] if p.requires_grad]
+        owner = {id(p): g for g in self.param_groups for p in g["params"]}
+        for p in to_hook:
+            if id(p) in owner:
+                self._fused_backward_handles.append(p.register_post_accumulate_grad_hook(
+                    self._fused_hook(p, owner[id(p)])))
+
+    def disable_fused_backward(self):
+        """Remove the per-parameter hooks; ``step()`` steps again (optimizer.py:2036-2043)."""
+        self._fused_backward_enabled = False
+        for h in getattr(self, "_fused_backward_handles", ()):
+            h.remove()
+        if hasattr(self, "_fused_backward_handles"):
+            self._fused_backward_handles.clear()
+
+    def _fused_hook(self, param, group):
+        def hook(_):
+            if param.grad is None:
+                return
+            pid = id(param)
+            self._accum_counter[pid] += 1
+            if self._accum_counter[pid] < self._grad_accum_steps:
+                return
+            self._accum_counter[pid] = 0
+            self._step_single_param_fused(param, group)
+            param.grad = None
+        return hook
+
+    @torch.no_grad()
+    def _step_single_param_fused(self, p, group):
+        """One per-parameter update (optimizer.py:2373-2471) on the GPU: the same
+        state layouts, APEXW_MODE_SINGLE of the compact or 8-bit kernel."""
+        if p.grad is None:
+            return
+        prec = S.normalize_precision(group.get("precision", "compact"))
+        state = self.state[p]
+        if len(state) == 0:
+            if prec == "8bit":
+                S.ensure_8bit_state(state, p, group)
+            else:
+                state["stochastic_rounding"] = bool(group.get("stochastic_rounding", True))
+                state["step"] = torch.tensor(0.0, dtype=torch.float32)
+                cdt = S.compact_dtype(p) if prec == "compact" else torch.float32
+                state["exp_avg"] = torch.zeros_like(p, dtype=cdt)
+                state["exp_avg_sq"] = torch.zeros_like(p, dtype=cdt)
+        state["step"].add_(1)
+        step = int(state["step"].item())
+        if p.grad.dtype != p.dtype:
+            p.grad = p.grad.to(p.dtype)
+        plan = self._single_plans.get(id(p))
+        if plan is None or not plan.valid_for(group):
+            if p.device.type != "cuda":
+                raise RuntimeError("apexw_amd runs the optimizer step on the GPU; parameters must be on cuda")
+            if p.dtype not in (torch.float32, torch.bfloat16):
+                raise NotImplementedError(f"apexw_amd steps fp32/bf16 parameters, got {p.dtype}")
+            kind = "q8" if (state.get("is_8bit", False) or prec == "8bit") else "compact"
+            if kind == "compact" and state["exp_avg_sq"].numel() != p.numel():
+                # the reference's update broadcasts a full-size square against it and fails
+                raise RuntimeError("enable_fused_backward needs full-size exp_avg_sq; this parameter "
+                                   "has quad-v state from an earlier step()")
+            group["precision"] = prec
+            plan = StepPlan(self, group, [p], kind, single=True)
+            self._single_plans[id(p)] = plan
+        plan.execute(group, self._seed, None, steps=[step])
 
     @property
     def _hook_seed(self):

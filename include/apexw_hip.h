@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define APEXW_ABI_VERSION 6
+#define APEXW_ABI_VERSION 7
 
 /* status codes */
 enum apexw_status {
@@ -100,6 +100,13 @@ typedef struct apexw_unit {
 #define APEXW_MODE_COLD 0     /* first step of a plan: _multi_tensor_step rounding */
 #define APEXW_MODE_REPLAY 1   /* FastExecutionPlan.execute_foreach rounding */
 #define APEXW_MODE_NATIVE 2   /* torch._fused_adamw_ rounding (homogeneous 16-bit groups) */
+#define APEXW_MODE_SINGLE 3   /* the per-parameter in-backward update of enable_fused_backward
+                                 (ApexW._step_single_param_fused, apexw/optimizer.py:2373-2471):
+                                 fp32 m = b1 m + (1-b1) g, lookahead b1 m + (1-b1) g with the new m,
+                                 denominator sqrt(v) + eps_scaled (no floor), p decayed then
+                                 p + (-step_size * num) / den; INT8 m requantised without the
+                                 scale EMA and without SR; compact: full-size m and v only.
+                                 Grads are used as given (no sanitize, clip or AMP flags). */
 
 /* apexw_hparams.flags */
 #define APEXW_HP_SR (1u << 0)         /* stochastic rounding of 16-bit params / codes */
@@ -137,7 +144,8 @@ int apexw_abi_version(void);
 /*
  * Validate one tensor descriptor (HOST copy) before it is uploaded into a
  * device table: kind 0 = compact step, 1 = 8-bit step, 2 = 8-bit step on the
- * full-block kernel (bf16 or fp32 params, NF4 m, quad v, 2048-element blocks).  Checks the dtype
+ * full-block kernel (bf16 or fp32 params, NF4 m, quad v, 2048-element blocks),
+ * 3 = compact step in APEXW_MODE_SINGLE (full-size v only).  Checks the dtype
  * combination, block size and the 16-byte alignment the vector path needs
  * (unless APEXW_FLAG_SCALAR is set).  Mirrors the per-call tensor checks of the
  * reference's pybind glue (apexw/csrc/apexw_cuda.cpp:109-180, :310-380), done
@@ -163,6 +171,7 @@ int apexw_compact_step(const apexw_tensor* tensors, int32_t n_tensors,
  * apexw_check_tensor(t, 2) and run on its fp32 variant; the remaining units
  * (any layout) run on the general kernel.  Zero for both counts runs
  * everything on the general kernel (same results with SR off).
+ * APEXW_MODE_SINGLE runs every unit on the general kernel: both counts must be 0.
  */
 int apexw_q8_step(const apexw_tensor* tensors, int32_t n_tensors,
                   const apexw_unit* units, int64_t n_units, int64_t n_fast_units,

@@ -1,6 +1,7 @@
-"""In-backward 8-bit steps (CPU oracle; test infrastructure only).
+"""In-backward steps (CPU oracle; test infrastructure only).
 
-Restates the reference's automatic 8-bit runtime acceleration:
+Restates the reference's automatic 8-bit runtime acceleration and its
+``enable_fused_backward`` per-parameter update:
 
 * ``hook_partition`` -- which parameters are stepped during backward
   (``_enable_8bit_runtime_acceleration``, apexw/optimizer.py:2076-2133): the
@@ -14,20 +15,30 @@ Restates the reference's automatic 8-bit runtime acceleration:
   extension: ``_step_ultra`` with lr * K^-0.4, weight decay wd / (K * K^-0.4),
   the grad scale 1 / (amp_inv * K) as a float32 tensor, and the step counter set
   so that the bias correction uses the pass count (mstep) and the stored
-  counter ends at (mstep - 1) // K + 1.
+  counter ends at (mstep - 1) // K + 1;
+* ``fused_param_step`` -- ``_step_single_param_fused`` (optimizer.py:2373-2471),
+  the update ``enable_fused_backward`` runs per parameter: fp32 moments
+  (m = b1 m + (1-b1) g), lookahead b1 m' + (1-b1) g with the new m, no grad
+  sanitizing, a denominator sqrt(v) + eps_scaled without the eps floor, INT8 m
+  requantised from its own absmax (no EMA, round to nearest); the compact
+  branch keeps full-size fp32-math moments rounded once on store.
 
 Parity pins (tests/test_oracle_hooks.py): with K = 1 and no AMP a flush equals
 the ordinary 8-bit step of ``OracleApexW`` bit for bit; a first step from zero
 state with K = 2 and a large eps matches the closed form of the update (which
 depends on the grad scale K, on lr * K^-0.4 and on the decay lr * wd / K); an
 AMP scale that is a power of two cancels exactly; the state layout equals the
-golden-pinned ``layout.init_state`` wherever the two rules coincide.
+golden-pinned ``layout.init_state`` wherever the two rules coincide;
+``fused_param_step`` matches the closed form of a first step from zero state
+(8-bit and compact, where a large eps shows the missing floor) and, on a second
+step, the INT8 scale equals the new momentum's absmax / 127 (no EMA).
 """
 
 import numpy as np
 import torch
 
 from . import layout as L
+from . import quant as Q
 from .q8 import q8_param_step
 
 MIN_TENSORS = 8
@@ -128,3 +139,98 @@ def first_step_closed_form(p, g, *, lr, beta1, beta2, eps, weight_decay, K, amp_
     apply_wd = p.dim() >= 2
     base = p.double() * (decay if apply_wd else 1.0)
     return base - step_size * look * torch.from_numpy(gain) / den
+
+
+@torch.no_grad()
+def fused_param_step(p, g, st, group):
+    """One in-backward update of ``p`` with grad ``g``; ``st`` is its state dict."""
+    prec = group["precision"]
+    if len(st) == 0:
+        if prec == "8bit":
+            ensure_8bit_state(st, p, group)
+        else:
+            st["stochastic_rounding"] = bool(group.get("stochastic_rounding", True))
+            st["step"] = torch.tensor(0.0, dtype=torch.float32)
+            cdt = L.compact_dtype(p) if prec == "compact" else torch.float32
+            st["exp_avg"] = torch.zeros_like(p, dtype=cdt)
+            st["exp_avg_sq"] = torch.zeros_like(p, dtype=cdt)
+    st["step"].add_(1)
+    step = int(st["step"].item())
+    lr, (b1, b2), wd, eps = group["lr"], group["betas"], group["weight_decay"], group["eps"]
+    apply_wd = wd != 0 and (not group.get("decay_norm_only", True) or p.dim() >= 2)
+    wd_factor = max(1.0 - lr * wd, 0.0) if apply_wd else 1.0
+    bc1 = 1.0 - b1 ** step
+    bc2 = 1.0 - b2 ** step
+    step_size = lr * bc2 ** 0.5 / bc1
+    eps_scaled = eps * bc2 ** 0.5
+    if st.get("is_8bit", False):
+        m, v = st["exp_avg"], st["exp_avg_sq"]
+        ms, vs = st["exp_avg_scales"], st["exp_avg_sq_scales"]
+        bs = st["block_size_8bit"]
+        stoch = st.get("stochastic_rounding", True)
+        int4, quad = st.get("is_4bit_m", False), st.get("is_quad_v", False)
+        if int4:
+            mf = Q.dequant_nf4(m, ms, p.numel(), bs).view_as(p)
+        else:
+            mf = Q.dequant_int8(m, ms, bs)
+        vbs = max(bs // 4, 1) if quad else bs
+        vf = Q.dequant_logu8(v, vs, vbs)
+        gf = g.to(torch.float32)
+        mf.mul_(b1).add_(gf, alpha=1.0 - b1)
+        if quad:
+            gq = gf.reshape(-1, 4).square().mean(dim=1)
+            vf.mul_(b2).add_(gq, alpha=1.0 - b2)
+            den = vf.sqrt().add_(eps_scaled).unsqueeze(1).expand(-1, 4).reshape_as(p)
+        else:
+            vf.mul_(b2).addcmul_(gf, gf, value=1.0 - b2)
+            den = vf.sqrt().add_(eps_scaled)
+        look = mf.mul(b1).add_(gf, alpha=1.0 - b1)
+        look.mul_(torch.where(mf * gf >= 0, 1.0 + 0.20 * b1, 1.0 - 0.35 * b1))
+        if p.dtype == torch.float32:
+            if apply_wd:
+                p.mul_(wd_factor)
+            p.addcdiv_(look, den, value=-step_size)
+        else:
+            pf = p.float()
+            if apply_wd:
+                pf.mul_(wd_factor)
+            pf.addcdiv_(look, den, value=-step_size)
+            Q.store_16bit(p, pf, stoch)
+        if int4:
+            q, sc = Q.quant_nf4(mf, bs, ms, stoch)
+        else:
+            q, sc = Q.quant_int8(mf, bs)
+        m.copy_(q.view(m.shape))
+        ms.copy_(sc)
+        qv, sv = Q.quant_logu8(vf, vbs, vs, stoch)
+        v.copy_(qv.view(v.shape))
+        vs.copy_(sv)
+        return
+    m, v = st["exp_avg"], st["exp_avg_sq"]
+    if v.numel() != p.numel():
+        raise RuntimeError("the per-parameter update needs full-size exp_avg_sq (quad-v state)")
+    gf, mf, vf = g.to(torch.float32), m.to(torch.float32), v.to(torch.float32)
+    if apply_wd:
+        p.mul_(wd_factor)
+    mf.mul_(b1).add_(gf, alpha=1.0 - b1)
+    vf.mul_(b2).addcmul_(gf, gf, value=1.0 - b2)
+    den = vf.sqrt().add_(eps_scaled)
+    p.addcdiv_(mf, den, value=-step_size)
+    m.copy_(mf.to(m.dtype))
+    v.copy_(vf.to(v.dtype))
+
+
+def fused_first_step_closed_form(p, g, *, lr, beta1, beta2, eps, weight_decay):
+    """First per-parameter update from zero state in float64 (2-D p, decay on):
+    m = (1-b1) g, v = (1-b2) g^2, p' = p (1 - lr wd) - s num / (sqrt(v) + eps
+    sqrt(1-b2)) with num = (b1 m + (1-b1) g) times the lookahead gain (8-bit)
+    or num = m (compact)."""
+    G = g.double()
+    m = (1.0 - beta1) * G
+    v = (1.0 - beta2) * G * G
+    s = lr * (1.0 - beta2) ** 0.5 / (1.0 - beta1)
+    den = v.sqrt() + eps * (1.0 - beta2) ** 0.5
+    base = p.double() * max(1.0 - lr * weight_decay, 0.0)
+    look = beta1 * m + (1.0 - beta1) * G
+    gain = torch.where(m * G >= 0, 1.0 + 0.20 * beta1, 1.0 - 0.35 * beta1).double()
+    return base - s * look * gain / den, base - s * m / den

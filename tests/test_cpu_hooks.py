@@ -171,3 +171,26 @@ def test_restore_rules(rec):
     assert all(p.dtype == torch.bfloat16 for p in m.parameters())
     m.load_state_dict(sd)                              # loading weights restores fp32 first
     assert all(p.dtype == torch.float32 for p in m.parameters())
+
+
+def test_fused_backward_hooks_count_passes(monkeypatch):
+    """enable_fused_backward: one hook per trainable parameter, a step on every
+    K-th grad, the grad freed; the automatic 8-bit hooks stand aside."""
+    ps = _chain()
+    opt = ApexW(ps, lr=2e-4, precision="8bit")
+    calls = []
+
+    def fake(p, group):
+        calls.append(p)
+    monkeypatch.setattr(opt, "_step_single_param_fused", fake)
+    monkeypatch.setattr(opt, "_hook_plan", lambda group, params: pytest.fail("auto hooks must stand aside"))
+    opt.enable_fused_backward(grad_accum_steps=2)
+    assert len(opt._fused_backward_handles) == 16
+    x = torch.randn(16, 512, dtype=torch.bfloat16)
+    _loss(ps, x).backward()
+    assert not calls and all(p.grad is not None for p in ps)
+    _loss(ps, x).backward()
+    assert sorted(map(id, calls)) == sorted(map(id, ps)) and all(p.grad is None for p in ps)
+    opt.disable_fused_backward()
+    assert not opt._fused_backward_handles and not opt._fused_backward_enabled
+    R.restore_all_downcast_params()

@@ -227,3 +227,134 @@ def test_reference_convergence_vs_adamw(lr):
         losses8.append(loss.item())
     assert sum(losses8) / len(losses8) < sum(losses_adamw) / len(losses_adamw)
     assert losses8[-1] < losses_adamw[-1]
+
+
+class Small(nn.Module):
+    """Varied shapes: 2-D weights, 1-D norms and biases, a tensor under 64 elements."""
+
+    def __init__(self, seed):
+        super().__init__()
+        torch.manual_seed(seed)
+        self.a = nn.Linear(512, 256)
+        self.norm = nn.LayerNorm(256)
+        self.b = nn.Linear(256, 40)
+        self.c = nn.Linear(40, 8)
+
+    def forward(self, x):
+        return (self.c(torch.relu(self.b(self.norm(self.a(x))))).float() ** 2).mean()
+
+
+def _fused_setup(prec, dtype, seed, K=1, sr=False):
+    from apexw_amd import ApexW
+    model = Small(seed).cuda().to(dtype)
+    params = list(model.parameters())
+    kw = dict(lr=1e-2, weight_decay=0.1, precision=prec, stochastic_rounding=sr)
+    opt = ApexW(params, **kw)
+    cpu = {p: nn.Parameter(p.detach().cpu().clone()) for p in params}
+    seen = {}
+    for p in params:        # registered first: sees each accumulated grad before the fused step frees it
+        p.register_post_accumulate_grad_hook(lambda t, p=p: seen.setdefault(id(p), []).append(t.grad.detach().cpu().clone()))
+    opt.enable_fused_backward(model, grad_accum_steps=K)
+    group = dict(lr=1e-2, betas=(0.9, 0.999) if prec == "8bit" else (0.9, 0.99), eps=1e-8, weight_decay=0.1,
+                 decay_norm_only=True, precision=prec, stochastic_rounding=sr, block_size=None, int4_m=None)
+    return model, params, opt, cpu, seen, group
+
+
+def _compare_fused(params, opt, cpu, states, tag, prev):
+    """fp32 parameters: the bound is relative to the operands of the last add,
+    |p_prev| + |update|, not to the result.  torch's CPU sqrt (the oracle's) is
+    one ulp below the IEEE square root for about 0.7% of inputs on its AVX-512
+    build; at lr 1e-2 the first update is as large as p, and where it cancels p
+    that ulp is large relative to the result."""
+    torch.cuda.synchronize()
+    for i, p in enumerate(params):
+        if p.dtype == torch.float32:
+            got, ref, p0 = p.detach().cpu().double(), cpu[p].detach().double(), prev[p].double()
+            tol = 1e-6 * (ref.abs() + p0.abs() + (ref - p0).abs()) + 1e-9
+            assert ((got - ref).abs() <= tol).all(), f"{tag} p{i}: excess {float(((got - ref).abs() - tol).max()):.3e}"
+        else:
+            _assert_close(p, cpu[p], f"{tag} p{i}")
+        gs, cs = opt.state[p], states[cpu[p]]
+        assert set(gs) == set(cs), f"{tag} p{i} keys"
+        for k, v in cs.items():
+            if torch.is_tensor(v) and k != "step":
+                _assert_close(gs[k], v, f"{tag} p{i} {k}")
+                v.copy_(gs[k].cpu())
+        assert float(gs["step"]) == float(cs["step"])
+        with torch.no_grad():
+            cpu[p].copy_(p.detach().cpu())
+
+
+@pytest.mark.parametrize("prec,dtype", [("8bit", torch.float32), ("8bit", torch.bfloat16),
+                                        ("compact", torch.float32), ("compact", torch.bfloat16)])
+def test_fused_backward_matches_oracle(prec, dtype):
+    _need_gpu()
+    from oracle import hooks as H
+    print(f"fused backward {prec} {dtype}", flush=True)
+    model, params, opt, cpu, seen, group = _fused_setup(prec, dtype, 3)
+    states = {}
+    for it in range(3):
+        seen.clear()
+        g = torch.Generator().manual_seed(40 + it)
+        model(torch.randn(16, 512, generator=g).cuda().to(dtype)).backward()
+        assert all(p.grad is None for p in params)
+        opt.step()                                   # nothing left to step
+        prev = {p: cpu[p].detach().clone() for p in params}
+        for p in params:
+            H.fused_param_step(cpu[p], seen[id(p)][0], states.setdefault(cpu[p], {}), group)
+        _compare_fused(params, opt, cpu, states, f"iter {it}", prev)
+
+
+def test_fused_backward_accumulates_k_passes():
+    _need_gpu()
+    from oracle import hooks as H
+    print("fused backward K=2", flush=True)
+    model, params, opt, cpu, seen, group = _fused_setup("8bit", torch.bfloat16, 4, K=2)
+    states = {}
+    for it in range(2):
+        seen.clear()
+        for micro in range(2):
+            g = torch.Generator().manual_seed(60 + 2 * it + micro)
+            model(torch.randn(16, 512, generator=g).cuda().bfloat16()).backward()
+            assert all((p.grad is None) == (micro == 1) for p in params)
+        prev = {p: cpu[p].detach().clone() for p in params}
+        for p in params:
+            H.fused_param_step(cpu[p], seen[id(p)][1], states.setdefault(cpu[p], {}), group)
+        _compare_fused(params, opt, cpu, states, f"iter {it}", prev)
+
+
+@pytest.mark.parametrize("prec", ["compact", "8bit"])
+def test_reference_fused_backward_case(prec):
+    """The reference's test_quantization.py:794-816 on the GPU."""
+    _need_gpu()
+    from apexw_amd import ApexW
+    print(f"fused backward reference case {prec}", flush=True)
+    torch.manual_seed(42)
+    model = nn.Sequential(nn.Linear(32, 16), nn.ReLU(), nn.Linear(16, 8)).cuda()
+    opt = ApexW(model.parameters(), lr=1e-2, precision=prec)
+    opt.enable_fused_backward(model)
+    x = torch.randn(4, 32).cuda()
+    target = torch.randn(4, 8).cuda()
+    losses = []
+    for _ in range(10):
+        opt.zero_grad()
+        loss = ((model(x) - target) ** 2).mean()
+        loss.backward()
+        assert all(p.grad is None for p in model.parameters())
+        opt.step()
+        losses.append(loss.item())
+    assert losses[-1] < losses[0] * 0.5
+
+
+def test_reference_fused_backward_disable():
+    """The reference's test_quantization.py:818-830 on the GPU."""
+    _need_gpu()
+    from apexw_amd import ApexW
+    torch.manual_seed(42)
+    model = nn.Sequential(nn.Linear(32, 8)).cuda()
+    opt = ApexW(model.parameters(), lr=1e-2, precision="compact")
+    opt.enable_fused_backward(model)
+    opt.disable_fused_backward()
+    model(torch.randn(4, 32).cuda()).sum().backward()
+    assert all(p.grad is not None for p in model.parameters())
+    opt.step()

@@ -122,3 +122,48 @@ def test_lazy_state_matches_init_group_where_rules_coincide(shape):
     forced = H.ensure_8bit_state({}, torch.zeros(16386), _group(int4_m=True))
     assert not forced["is_4bit_m"] and not forced["is_quad_v"]
     assert L.init_state(torch.zeros(16386), _group(int4_m=True), 16, False)["is_4bit_m"]
+
+
+@pytest.mark.parametrize("prec", ["8bit", "compact"])
+def test_fused_first_step_matches_closed_form(prec):
+    """enable_fused_backward's update from zero state.  eps = 1 with
+    eps_scaled = sqrt(1 - b2) < 1: the 8-bit denominator has no eps floor here
+    (the ordinary 8-bit step would clamp it to 1)."""
+    group = _group(eps=1.0, lr=1e-2, precision=prec, stochastic_rounding=False)
+    ps, gs = _params([(40, 50)], torch.float32, 7)
+    gs = [g * 50.0 for g in gs]
+    p0 = ps[0].detach().clone()
+    st = {}
+    H.fused_param_step(ps[0], gs[0], st, group)
+    q8, compact = H.fused_first_step_closed_form(p0, gs[0], lr=1e-2, beta1=0.9, beta2=0.999, eps=1.0,
+                                                 weight_decay=0.1)
+    want = q8 if prec == "8bit" else compact
+    got = ps[0].detach().double()
+    upd = (want - p0.double() * (1 - 1e-3)).abs()
+    assert upd.max() > 1e-4
+    tol = 4 * 2.0 ** -24 * p0.double().abs() + 1e-5 * upd + 1e-12
+    assert ((got - want).abs() <= tol).all()
+    assert float(st["step"]) == 1.0
+    if prec == "compact":
+        assert set(st) == {"stochastic_rounding", "step", "exp_avg", "exp_avg_sq"}
+        assert st["exp_avg"].dtype == st["exp_avg_sq"].dtype == torch.bfloat16
+        assert torch.equal(st["exp_avg"], (0.1 * gs[0]).to(torch.bfloat16))
+
+
+def test_fused_int8_momentum_scale_has_no_ema():
+    """Second update with a grad that halves the momentum: the INT8 scale is the
+    new absmax / 127, below the 0.9 x old floor the ordinary step keeps."""
+    group = _group(precision="8bit", stochastic_rounding=False)
+    ps, gs = _params([(32, 128)], torch.float32, 8)
+    st = {}
+    H.fused_param_step(ps[0], gs[0], st, group)
+    bs = st["block_size_8bit"]
+    s1 = st["exp_avg_scales"].clone().double()
+    m1 = (st["exp_avg"].double().reshape(-1, bs) * s1).reshape(32, 128)
+    g2 = (-4.5 * m1).float()                   # m2 = 0.9 m1 + 0.1 g2 = 0.45 m1
+    H.fused_param_step(ps[0], g2, st, group)
+    m2 = 0.9 * m1 + 0.1 * g2.double()
+    want = m2.reshape(-1, bs).abs().amax(dim=1, keepdim=True) / 127.0
+    got = st["exp_avg_scales"].double()
+    assert torch.allclose(got, want, rtol=1e-6, atol=0)
+    assert (got < 0.9 * s1).all()

@@ -13,7 +13,7 @@ import numpy as np
 
 from ._build import LIB_PATH
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 # dtype codes
 F32, BF16, F16, U8, I8 = 0, 1, 2, 3, 4
@@ -26,6 +26,8 @@ FLAG_NF4 = 1 << 10
 FLAG_GENERIC = 1 << 11
 FLAG_DENSE16 = 1 << 12
 FLAG_SCALAR = 1 << 13
+FLAG_FACTORED = 1 << 14
+FLAG_M6 = 1 << 15
 
 COMPACT_UNIT = 2048
 
@@ -38,6 +40,7 @@ HP_CLIP = 1 << 3
 HP_LERP_HI = 1 << 4
 HP_LOOK_HI = 1 << 5
 HP_UNSCALE = 1 << 6
+HP_FV_SANITIZE = 1 << 7
 
 STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported dtype combination", 3: "launch failed",
           4: "misaligned pointer"}
@@ -81,6 +84,12 @@ GRAD_PREP_DTYPE = np.dtype([("g", np.uint64), ("out", np.uint64), ("n", np.int64
                             ("dtype", np.uint32), ("reserved", np.uint32)])
 assert GRAD_PREP_DTYPE.itemsize == 40
 GRAD_PREP_CHUNK = 2048
+# apexw_fv_tensor: one factored-v tensor of a group
+FV_TENSOR_DTYPE = np.dtype([("tensor", np.uint32), ("rows", np.int32), ("cols", np.int32), ("flags", np.uint32),
+                            ("ws", np.int64), ("band0", np.int32), ("cb0", np.int32)])
+assert FV_TENSOR_DTYPE.itemsize == 32
+FV_SUM_COLS = 1
+FV_BAND_ROWS = 32
 
 GEMM_SYM, GEMM_B_KN, GEMM_ADD_B = 1, 2, 4
 GEMM_OUT_C, GEMM_OUT_CT, GEMM_ADD, GEMM_KIND_NN = 1, 2, 4, 8
@@ -110,6 +119,9 @@ SIGNATURES = {
     "apexw_muon_prepare": (ctypes.c_int, [_vp, _vp, _i32, _i64, _i64, _f32, _f32, _i32, _f32, _f32, _vp, _vp, _i64,
                                           _i64, _vp, _vp]),
     "apexw_muon_apply": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _i64, _i32, _f32, _i32, _f32, _vp]),
+    "apexw_factored_layout": (ctypes.c_int64, [_vp, _i32, ctypes.POINTER(ctypes.c_int64),
+                                               ctypes.POINTER(ctypes.c_int64)]),
+    "apexw_factored_step": (ctypes.c_int, [_vp, _i32, _vp, _i32, _i64, _i64, _vp, _i64, _vp, _HP, _vp]),
 }
 
 GEMM_TILE = 256

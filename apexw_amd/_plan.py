@@ -111,9 +111,17 @@ class StepPlan:
 
     def _tensor_flags(self, p, st, wd_on):
         f = (_DT[p.dtype] << L.PDT_SHIFT) | (_DT[p.dtype] << L.GDT_SHIFT)
-        m, v = st["exp_avg"], st["exp_avg_sq"]
         if wd_on and (not self.decay_norm_only or p.dim() >= 2):
             f |= L.FLAG_WD
+        if st.get("is_factored_v", False):
+            # row / column v: stepped by apexw_factored_step, skipped by the step kernels
+            f |= L.FLAG_FACTORED
+            if st.get("is_8bit", False):
+                if st.get("is_6bit_m", False):
+                    f |= L.FLAG_M6
+                return f, int(st["block_size_8bit"])
+            return f | (_DT[st["exp_avg"].dtype] << L.MDT_SHIFT), 0
+        m, v = st["exp_avg"], st["exp_avg_sq"]
         if self.kind == "compact":
             f |= (_DT[m.dtype] << L.MDT_SHIFT) | (_DT[v.dtype] << L.VDT_SHIFT)
             if v.numel() * 4 == p.numel() and p.numel() % 4 == 0:
@@ -143,13 +151,18 @@ class StepPlan:
             if not p.is_contiguous():
                 raise NotImplementedError("ApexW HIP step needs contiguous parameters")
             f, block = self._tensor_flags(p, st, wd_on)
-            m, v = st["exp_avg"], st["exp_avg_sq"]
             tab[i]["p"] = p.data_ptr()
-            tab[i]["m"] = m.data_ptr()
-            tab[i]["v"] = v.data_ptr()
-            if "exp_avg_scales" in st and st.get("is_8bit", False):
-                tab[i]["m_scale"] = st["exp_avg_scales"].data_ptr()
-                tab[i]["v_scale"] = st["exp_avg_sq_scales"].data_ptr()
+            tab[i]["m"] = st["exp_avg"].data_ptr()
+            if f & L.FLAG_FACTORED:
+                tab[i]["v"] = st["exp_avg_sq_row"].data_ptr()
+                tab[i]["v_scale"] = st["exp_avg_sq_col"].data_ptr()
+                if block:
+                    tab[i]["m_scale"] = st["exp_avg_scales"].data_ptr()
+            else:
+                tab[i]["v"] = st["exp_avg_sq"].data_ptr()
+                if "exp_avg_scales" in st and st.get("is_8bit", False):
+                    tab[i]["m_scale"] = st["exp_avg_scales"].data_ptr()
+                    tab[i]["v_scale"] = st["exp_avg_sq_scales"].data_ptr()
             tab[i]["n"] = p.numel()
             tab[i]["flags"] = f
             tab[i]["block"] = block
@@ -160,6 +173,9 @@ class StepPlan:
             else:
                 counts[i] = (p.numel() + block - 1) // block
         self.host_table = tab          # parameter order
+        self.factored = (tab["flags"] & np.uint32(L.FLAG_FACTORED)) != 0
+        self.fv = None
+        self._fv_subsets = {}
         self.p_ptrs = np.zeros(n, dtype=np.uint64)
         self.p_dtypes = np.zeros(n, dtype=np.int8)
         self._H = _host()
@@ -230,6 +246,7 @@ class StepPlan:
         units["tensor"] = np.repeat(np.arange(n, dtype=np.uint32), counts)
         units["unit"] = (np.arange(total, dtype=np.int64) - np.repeat(self.unit_begin[:-1], counts)).astype(np.uint32)
         self.n_units = total
+        self._host_units = units
         self.n_fast_units = int(counts[:n_bf].sum())
         self.n_fast_f32_units = int(counts[n_bf:n_bf + n_f32].sum())
         self.unit_counts = counts
@@ -238,6 +255,29 @@ class StepPlan:
         self.d_units = torch.from_numpy(units.view(np.uint8)).to(self.device)
         self.d_unit_begin = torch.from_numpy(self.unit_begin).to(self.device)
         self.clip_ws = None
+        self._fv_subsets = {}
+        self.fv = self._fv_layout(tuple(int(i) for i in np.nonzero(self.factored[perm])[0])) \
+            if self.factored.any() else None
+
+    def _fv_layout(self, rows):
+        """Factored-v table, workspace and units for the device-table rows ``rows``."""
+        fv = np.zeros(len(rows), dtype=L.FV_TENSOR_DTYPE)
+        for k, d in enumerate(rows):
+            p = self.params[int(self.perm[d])]
+            fv[k]["tensor"] = d
+            fv[k]["rows"] = p.shape[0]
+            fv[k]["cols"] = p.numel() // p.shape[0]
+            fv[k]["flags"] = L.FV_SUM_COLS if p.numel() > 262144 else 0
+        nb, ncb = ctypes_int64(), ctypes_int64()
+        ws = int(self._lib.apexw_factored_layout(fv.ctypes.data, len(fv), ctypes_ref(nb), ctypes_ref(ncb)))
+        if ws < 0:
+            L.check(-ws, "apexw_factored_layout")
+        sel = np.isin(self._host_units["tensor"], np.array(rows, dtype=np.uint32))
+        units = np.ascontiguousarray(self._host_units[sel])
+        return dict(rows=rows, n=len(fv), d_fv=torch.from_numpy(fv.view(np.uint8)).to(self.device),
+                    ws=torch.empty(max(ws, 1), dtype=torch.float32, device=self.device),
+                    n_bands=nb.value, n_cb=ncb.value, n_units=len(units),
+                    d_units=torch.from_numpy(units.view(np.uint8)).to(self.device) if len(units) else None)
 
     def _refresh_grads(self):
         """Point the table at this step's grads; re-upload it if any moved.
@@ -300,9 +340,9 @@ class StepPlan:
             for i in range(len(self.params)):
                 row = tab[i]
                 t = L.Tensor(*(int(row[k]) for k in ("p", "g", "m", "v", "m_scale", "v_scale", "n", "flags", "block")))
-                L.check(lib.apexw_check_tensor(ctypes_ref(t), self.kind_code),
+                L.check(lib.apexw_check_tensor(ctypes_ref(t), 4 if self.factored[i] else self.kind_code),
                         f"tensor {i} ({tuple(self.params[i].shape)})")
-                if self.kind == "q8" and not self.single:
+                if self.kind == "q8" and not self.single and not self.factored[i]:
                     # full-block eligibility apart from alignment: same descriptor on aligned stand-in pointers
                     t.p = t.g = t.m = t.v = 256
                     t.flags = int(row["flags"]) & ~L.FLAG_SCALAR
@@ -377,7 +417,45 @@ class StepPlan:
                 st = self._lib.apexw_q8_step(self.d_table.data_ptr(), len(self.params), d_units.data_ptr(),
                                              n_units, n_fast, n_fast32, ctypes_ref(hp), stream)
             L.check(st, "apexw step")
+        if self.fv is not None:
+            replay_step = None if (mode_cold or self.native or self.kind == "q8") else groups[0][1]
+            self._factored_launch(lr, b1, b2, eps, wd, sr, sanitize, coef, seed, mode_cold, inv_scale, replay_step,
+                                  stream)
         self.cold_done = True
+
+    def _factored_launch(self, lr, b1, b2, eps, wd, sr, sanitize, coef, seed, cold, inv_scale, replay_step, stream):
+        """Step the factored-v rows: one apexw_factored_step per distinct step count
+        (the replayed compact plan uses its first counter for every tensor,
+        optimizer.py:1141-1163)."""
+        rows = self.fv["rows"]
+        if replay_step is not None:
+            buckets = {replay_step: list(rows)}
+        else:
+            vals = self.steps.numpy()[self.perm]
+            buckets = {}
+            for d in rows:
+                buckets.setdefault(int(vals[d]), []).append(d)
+        for step, members in buckets.items():
+            if len(members) == len(rows):
+                fv = self.fv
+            else:
+                key = tuple(members)
+                fv = self._fv_subsets.get(key)
+                if fv is None:
+                    fv = self._fv_subsets[key] = self._fv_layout(key)
+            hp = self._hparams(lr, b1, b2, eps, wd, step, sr, sanitize, coef, seed, cold, inv_scale)
+            hp.mode = L.MODE_COLD
+            hp.eps = eps
+            hp.wd_factor = max(1.0 - lr * wd, 0.0) if wd != 0 else 1.0
+            # nan_to_num on the fp32 grad: always in the 8-bit step, on the cold compact step
+            # (_apply_factored_v_int8_update's sanitize_g, optimizer.py:4380-4400, :5414-5432, :1147-1163)
+            if self.kind == "q8" or cold:
+                hp.flags |= L.HP_FV_SANITIZE
+            st = self._lib.apexw_factored_step(
+                self.d_table.data_ptr(), len(self.params), fv["d_fv"].data_ptr(), fv["n"], fv["n_bands"],
+                fv["n_cb"], fv["d_units"].data_ptr() if fv["d_units"] is not None else None, fv["n_units"],
+                fv["ws"].data_ptr(), ctypes_ref(hp), stream)
+            L.check(st, "apexw_factored_step")
 
     def _split_by_step(self):
         vals = self.steps.numpy()[self.perm]
@@ -461,3 +539,8 @@ class StepPlan:
 def ctypes_ref(obj):
     import ctypes
     return ctypes.byref(obj)
+
+
+def ctypes_int64():
+    import ctypes
+    return ctypes.c_int64(0)

@@ -31,6 +31,8 @@ int apexw_launch_muon_prepare(float*, const void*, int32_t, int64_t, int64_t, fl
 int apexw_launch_muon_apply(void*, int32_t, const uint16_t*, int64_t, int64_t, int64_t, int32_t, float, int32_t,
                             float, hipStream_t);
 bool apexw_q8_flags_ok(uint32_t flags, uint32_t block, int64_t n);
+int apexw_launch_factored(const apexw_tensor*, const apexw_fv_tensor*, int32_t, int64_t, int64_t, const apexw_unit*,
+                          int64_t, float*, const apexw_hparams*, hipStream_t);
 
 namespace {
 
@@ -106,6 +108,18 @@ int apexw_check_tensor(const apexw_tensor* t, int32_t kind) {
   if (kind == 0 || kind == 3) {
     if (!apexw_compact_flags_ok(t->flags)) return APEXW_ERR_DTYPE;
     if ((t->flags & APEXW_FLAG_QUAD) && (kind == 3 || (t->n % 4) != 0)) return APEXW_ERR_ARG;
+  } else if (kind == 4) {
+    // factored row: v / v_scale are the fp32 row / column EMAs
+    const uint32_t f = t->flags;
+    const uint32_t pd = (f >> APEXW_FLAG_PDT_SHIFT) & 3u, gd = (f >> APEXW_FLAG_GDT_SHIFT) & 3u;
+    if (!(f & APEXW_FLAG_FACTORED) || !(pd == APEXW_F32 || pd == APEXW_BF16) || gd != pd) return APEXW_ERR_DTYPE;
+    if (f & (APEXW_FLAG_QUAD | APEXW_FLAG_NF4 | APEXW_FLAG_DENSE16)) return APEXW_ERR_ARG;
+    if (t->block == 0) {
+      if ((f & APEXW_FLAG_M6) || ((f >> APEXW_FLAG_MDT_SHIFT) & 3u) != APEXW_BF16) return APEXW_ERR_DTYPE;
+    } else {
+      if (t->block > 2048 || !t->m_scale) return APEXW_ERR_ARG;
+      if ((f & APEXW_FLAG_M6) && (t->block % 4) != 0) return APEXW_ERR_ARG;
+    }
   } else if (kind == 1 || kind == 2) {
     if (!apexw_q8_flags_ok(t->flags, t->block, t->n)) return APEXW_ERR_DTYPE;
     if (kind == 2 && !apexw_q8_fast_eligible(t->flags, t->block)) return APEXW_ERR_DTYPE;
@@ -142,6 +156,39 @@ int apexw_q8_step(const apexw_tensor* tensors, int32_t n_tensors, const apexw_un
   if (st == APEXW_OK && rest > 0)
     st = apexw_launch_q8(tensors, rest, units + done, hp, (hipStream_t)stream);
   return st;
+}
+
+int64_t apexw_factored_layout(apexw_fv_tensor* fv, int32_t n_fv, int64_t* n_bands, int64_t* n_col_blocks) {
+  if (!fv || n_fv <= 0 || !n_bands || !n_col_blocks) return -APEXW_ERR_ARG;
+  int64_t ws = 0, bands = 0, cbs = 0;
+  for (int32_t i = 0; i < n_fv; ++i) {
+    apexw_fv_tensor& e = fv[i];
+    if (e.rows <= 0 || e.cols <= 0 || (e.flags & ~APEXW_FV_SUM_COLS)) return -APEXW_ERR_ARG;
+    if (i > 0 && e.tensor <= fv[i - 1].tensor) return -APEXW_ERR_ARG;
+    const int64_t nb = (e.rows + APEXW_FV_BAND_ROWS - 1) / APEXW_FV_BAND_ROWS;
+    e.ws = ws;
+    e.band0 = (int32_t)bands;
+    e.cb0 = (int32_t)cbs;
+    // row sums / norms, per-band column partials, column square roots; 16-byte aligned
+    ws += ((int64_t)e.rows + nb * e.cols + e.cols + 3) & ~(int64_t)3;
+    bands += nb;
+    cbs += ((int64_t)e.cols + 255) / 256;
+    if (bands > INT32_MAX || cbs > INT32_MAX) return -APEXW_ERR_ARG;
+  }
+  *n_bands = bands;
+  *n_col_blocks = cbs;
+  return ws;
+}
+
+int apexw_factored_step(const apexw_tensor* tensors, int32_t n_tensors, const apexw_fv_tensor* fv, int32_t n_fv,
+                        int64_t n_bands, int64_t n_col_blocks, const apexw_unit* units, int64_t n_units,
+                        float* workspace, const apexw_hparams* hp, void* stream) {
+  if (!tensors || !fv || !workspace || n_tensors <= 0 || n_fv <= 0 || n_fv > n_tensors || !hp_ok(hp)) return APEXW_ERR_ARG;
+  if (n_bands < n_fv || n_bands > INT32_MAX || n_col_blocks < n_fv || n_col_blocks + n_fv > INT32_MAX) return APEXW_ERR_ARG;
+  if (n_units < 0 || (n_units > 0 && !units)) return APEXW_ERR_ARG;
+  if (hp->mode == APEXW_MODE_SINGLE || hp->mode == APEXW_MODE_NATIVE) return APEXW_ERR_ARG;
+  return apexw_launch_factored(tensors, fv, n_fv, n_bands, n_col_blocks, units, n_units, workspace, hp,
+                               (hipStream_t)stream);
 }
 
 int apexw_gemm_nt_bf16(const void* a, const void* b, const void* et, void* c, void* ct, int32_t m, int32_t n,

@@ -266,6 +266,7 @@ __global__ __launch_bounds__(256) void compact_step_kernel(const apexw_tensor* _
     const uint32_t vd = (t.flags >> APEXW_FLAG_VDT_SHIFT) & 3u;
     const bool quad = t.flags & APEXW_FLAG_QUAD;
     if (quad && hp.mode == APEXW_MODE_SINGLE) continue;  // rejected on the host; never read v out of range
+    if (t.flags & APEXW_FLAG_FACTORED) continue;        // stepped by apexw_factored_step
     if (pd == APEXW_F32) {
       if (vd == APEXW_F32) compact_group<APEXW_F32, APEXW_BF16, APEXW_F32, false>(t, start, k, c);
       else if (quad) compact_group<APEXW_F32, APEXW_BF16, APEXW_BF16, true>(t, start, k, c);

@@ -21,7 +21,8 @@
 static __host__ __device__ inline bool apexw_q8_fast_ok(uint32_t flags, uint32_t block) {
   const uint32_t pd = (flags >> APEXW_FLAG_PDT_SHIFT) & 3u, gd = (flags >> APEXW_FLAG_GDT_SHIFT) & 3u;
   return (pd == APEXW_BF16 || pd == APEXW_F32) && gd == pd && (flags & APEXW_FLAG_NF4) &&
-         (flags & APEXW_FLAG_QUAD) && !(flags & (APEXW_FLAG_SCALAR | APEXW_FLAG_DENSE16)) && block == 2048;
+         (flags & APEXW_FLAG_QUAD) && !(flags & (APEXW_FLAG_SCALAR | APEXW_FLAG_DENSE16 | APEXW_FLAG_FACTORED)) &&
+         block == 2048;
 }
 
 namespace {
@@ -915,6 +916,7 @@ __global__ __launch_bounds__(256) void q8_step_kernel(const apexw_tensor* __rest
     const apexw_tensor& t = tensors[un.tensor];
     const uint32_t f = t.flags;
     const uint32_t pd = (f >> APEXW_FLAG_PDT_SHIFT) & 3u;
+    if (f & APEXW_FLAG_FACTORED) continue;  // stepped by apexw_factored_step
     if (f & APEXW_FLAG_DENSE16) {
       const uint32_t vd = (f >> APEXW_FLAG_VDT_SHIFT) & 3u;
       if (pd == APEXW_F32) {

@@ -42,7 +42,7 @@ HOOK_MIN_NUMEL = 16384             # optimizer.py:2131
 HOOK_BATCH = 14                    # optimizer.py:2142
 
 _UNSUPPORTED_FLAGS = ("amsgrad", "nesterov", "cautious", "lion", "maximize",
-                      "capturable", "differentiable", "auto_pack", "factored_v", "six_bit")
+                      "capturable", "differentiable", "auto_pack")
 
 
 class ApexW(Optimizer):
@@ -180,6 +180,8 @@ class ApexW(Optimizer):
             group.setdefault("stochastic_rounding", True)
             group.setdefault("force_compact_v", False)
             group.setdefault("int4_m", False)
+            group.setdefault("factored_v", False)
+            group.setdefault("six_bit", False)
         self._plans = {}
         if not hasattr(self, "_auto_hook_queue"):
             self._init_hook_state()
@@ -251,7 +253,7 @@ class ApexW(Optimizer):
         if group["precision"] == "8bit":
             return StepPlan(self, group, params, "q8")
         sts = [self.state[p] for p in params]
-        homogeneous = all(st["exp_avg"].dtype == st["exp_avg_sq"].dtype == p.dtype
+        homogeneous = all("exp_avg_sq" in st and st["exp_avg"].dtype == st["exp_avg_sq"].dtype == p.dtype
                           and st["exp_avg"].numel() == st["exp_avg_sq"].numel() for p, st in zip(params, sts))
         return StepPlan(self, group, params, "compact", native=homogeneous)
 

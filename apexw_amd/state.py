@@ -16,7 +16,11 @@ compact:
   * NF4 m (2 codes per byte) + quad log-uint8 v when numel >= 16384,
     numel % 4 == 0, power-of-two block >= 64 and min(shape) >= 8; otherwise
     INT8 m + full-size log-uint8 v; fp32 scales per block;
+  * factored_v=True: 2-D+ tensors of >= 65536 elements with rows, cols >= 128
+    keep fp32 row / column second moments and INT8 m (packed 6-bit m with
+    six_bit=True from 524,288 elements);
   * tensors under 64 elements keep compact 16-bit m/v.
+compact with factored_v=True: the same factored v from 524,288 elements, bf16 m.
 Initial state: NF4 bytes 0x77 (both codes = 0.0), m scales 1e-12 (INT8: 1e-12/127),
 v codes 0 with scales 1e-12.
 """
@@ -106,30 +110,64 @@ def block_size_8bit(p, user_bs):
     return 64
 
 
-def _auto_subbyte(p, group, bs):
-    """NF4 m + quad v eligibility (optimizer.py:2192-2201, the same rule in _init_group)."""
+def _auto_subbyte(p, group, bs, factored=False):
+    """NF4 m + quad v eligibility (optimizer.py:2192-2201, the same rule in _init_group,
+    where a factored tensor never takes it)."""
     n = p.numel()
     raw_int4 = group.get("int4_m", group.get("four_bit", None))
     pow2 = bs >= 64 and (bs & (bs - 1)) == 0
-    return (raw_int4 is not False and n >= 16384 and n % 4 == 0 and pow2
+    return (raw_int4 is not False and not factored and n >= 16384 and n % 4 == 0 and pow2
             and (p.dim() < 2 or min(p.shape) >= 8))
 
 
-def _q8_buffers(st, p, bs, int4, quad):
-    """8-bit state buffers: NF4 (packed, fill code 7) or INT8 m, quad or full log-u8 v,
-    per-block fp32 scales (optimizer.py:2210-2223)."""
+FACTORED_MIN_8BIT = 65536       # apexw/state.py:234-256
+FACTORED_MIN_COMPACT = 524288   # apexw/state.py:259-281
+SIX_BIT_MIN = 524288            # optimizer.py:2667-2673
+M6_ZERO = (0xDF, 0xF7, 0x7D)    # four codes of 31 (zero) in three bytes
+
+
+def _can_factor(p, is_peft, min_numel):
+    """Factored row/column v: 2-D+ real tensors, not PEFT, >= min_numel elements,
+    rows = shape[0] >= 128 and cols = numel / rows >= 128 (apexw/state.py:234-281)."""
+    if p.dim() < 2 or torch.is_complex(p) or p.dtype == torch.float64:
+        return False
+    rows = p.shape[0]
+    cols = p.numel() // rows
+    if is_peft or p.numel() < min_numel:
+        return False
+    return rows >= 128 and cols >= 128
+
+
+def _factored_v(st, p):
+    rows = p.shape[0]
+    st["exp_avg_sq_row"] = torch.zeros(rows, dtype=torch.float32, device=p.device)
+    st["exp_avg_sq_col"] = torch.zeros(p.numel() // rows, dtype=torch.float32, device=p.device)
+
+
+def _q8_buffers(st, p, bs, int4, quad, factored=False, six=False):
+    """8-bit state buffers: NF4 (packed, fill code 7), packed 6-bit (fill code 31) or
+    INT8 m; quad or full log-u8 v, or factored fp32 row/column v; per-block fp32
+    scales (optimizer.py:2798-2871)."""
     n, dev = p.numel(), p.device
-    st.update(is_8bit=True, block_size_8bit=bs, is_factored_v=False, is_6bit_m=False,
+    st.update(is_8bit=True, block_size_8bit=bs, is_factored_v=bool(factored), is_6bit_m=bool(six),
               is_4bit_m=bool(int4), is_quad_v=bool(quad), m_numel=n)
     st["state_dtype"] = torch.int8
     st["state_dtype_v"] = torch.uint8
     nblk = (n + bs - 1) // bs
-    if int4:
+    if six:
+        padded = nblk * bs
+        padded += (-padded) % 4
+        st["exp_avg"] = torch.tensor(M6_ZERO, dtype=torch.uint8, device=dev).repeat(padded // 4)
+        st["exp_avg_scales"] = torch.full((padded // bs, 1), 1e-12 / 31.0, dtype=torch.float32, device=dev)
+    elif int4:
         st["exp_avg"] = torch.full(((n + 1) // 2,), 0x77, dtype=torch.uint8, device=dev)
         st["exp_avg_scales"] = torch.full((nblk, 1), 1e-12, dtype=torch.float32, device=dev)
     else:
         st["exp_avg"] = torch.zeros(p.shape, dtype=torch.int8, device=dev)
         st["exp_avg_scales"] = torch.full((nblk, 1), 1e-12 / 127.0, dtype=torch.float32, device=dev)
+    if factored:
+        _factored_v(st, p)
+        return
     if quad:
         st["exp_avg_sq"] = torch.zeros((n // 4,), dtype=torch.uint8, device=dev)
     else:
@@ -167,15 +205,27 @@ def init_state(p, group, peft_ctx):
     if prec == "8bit" and n >= 64:
         bs = block_size_8bit(p, group.get("block_size"))
         narrow = p.dim() >= 2 and min(p.shape) <= 32 and n < 2048
-        auto_sub = _auto_subbyte(p, group, bs)
+        factored = bool(group.get("factored_v", False)) and _can_factor(p, is_peft, FACTORED_MIN_8BIT)
+        auto_sub = _auto_subbyte(p, group, bs, factored)
         raw_int4 = group.get("int4_m", group.get("four_bit", None))
-        int4 = auto_sub or (bool(raw_int4) and n >= 512 and n >= bs and not narrow and not is_peft)
-        _q8_buffers(st, p, bs, int4, bool(auto_sub and int4))
+        six = bool(group.get("six_bit", False)) and factored and n >= SIX_BIT_MIN and bs % 4 == 0
+        int4 = auto_sub or (bool(raw_int4) and not factored and n >= 512 and n >= bs and not narrow and not is_peft)
+        _q8_buffers(st, p, bs, int4, bool(auto_sub and int4), factored, six)
         return st
     if prec == "8bit":
         st.update(is_8bit=False, is_factored_v=False, is_6bit_m=False, is_4bit_m=False, is_quad_v=False)
     else:
-        st.update(is_6bit_m=False, is_4bit_m=False, is_factored_v=False)
+        factored = bool(group.get("factored_v", False)) and _can_factor(p, is_peft, FACTORED_MIN_COMPACT)
+        st.update(is_6bit_m=False, is_4bit_m=False, is_factored_v=factored)
+        if factored:
+            # 16-bit m, fp32 row/column v (optimizer.py:2749-2767, :2785-2787, :2859-2863)
+            st["state_dtype"] = compact_dtype(p)
+            st["state_dtype_v"] = torch.float32
+            st["exp_avg"] = torch.zeros(p.shape, dtype=compact_dtype(p), device=dev)
+            _factored_v(st, p)
+            st["scale_v"] = 1.0
+            st["sqrt_scale_v"] = 1.0
+            return st
     mdt = compact_dtype(p)
     vdt = v_dtype_for_beta2(mdt, beta2, group.get("force_compact_v", False), sr)
     quad = (prec == "compact" and mdt in (torch.bfloat16, torch.float16) and vdt in (torch.bfloat16, torch.float16)

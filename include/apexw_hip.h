@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define APEXW_ABI_VERSION 7
+#define APEXW_ABI_VERSION 8
 
 /* status codes */
 enum apexw_status {
@@ -64,6 +64,9 @@ enum apexw_dtype { APEXW_F32 = 0, APEXW_BF16 = 1, APEXW_F16 = 2, APEXW_U8 = 3, A
 #define APEXW_FLAG_GENERIC (1u << 11)   /* 8-bit: per-parameter ("generic") rounding order */
 #define APEXW_FLAG_DENSE16 (1u << 12)   /* 8-bit mode tensor kept in 16-bit m/v (numel < 64) */
 #define APEXW_FLAG_SCALAR (1u << 13)    /* pointers not 16-byte aligned: element-wise path */
+#define APEXW_FLAG_FACTORED (1u << 14)  /* factored second moment: stepped by apexw_factored_step;
+                                           the compact and 8-bit step kernels skip the row */
+#define APEXW_FLAG_M6 (1u << 15)        /* factored 8-bit: packed 6-bit m (4 codes in 3 bytes) */
 
 /*
  * One tensor of a multi-tensor launch (device-resident array, 64 bytes each).
@@ -71,6 +74,10 @@ enum apexw_dtype { APEXW_F32 = 0, APEXW_BF16 = 1, APEXW_F16 = 2, APEXW_U8 = 3, A
  * 8-bit:   m is the NF4 (uint8, 2 per byte, even element in the high nibble) or
  *          INT8 code buffer, v the log-uint8 codes (n/4 entries when QUAD),
  *          m_scale / v_scale the fp32 per-block scales, block the block size.
+ * factored (APEXW_FLAG_FACTORED): v is the fp32 row EMA (rows entries) and
+ *          v_scale the fp32 column EMA (cols entries); m is INT8 codes, packed
+ *          6-bit codes (APEXW_FLAG_M6) or, with block = 0, a 16-bit tensor of the
+ *          MDT dtype; m_scale the per-block scales of quantized m.
  */
 typedef struct apexw_tensor {
   void* p;
@@ -117,7 +124,8 @@ typedef struct apexw_unit {
 #define APEXW_HP_LOOK_HI (1u << 5)    /* 8-bit lookahead lerp weight (beta1) >= 0.5 */
 #define APEXW_HP_UNSCALE (1u << 6)    /* AMP: grads times grad_inv_scale (after sanitizing): in the
                                          grad dtype for compact and before a clip, in fp32 after
-                                         the step's nan_to_num otherwise (8-bit) */
+                                         the step's nan_to_num otherwise (8-bit, factored) */
+#define APEXW_HP_FV_SANITIZE (1u << 7) /* factored: nan_to_num(0, +-65504) on the fp32 grad */
 
 /* Host-computed step scalars (the reference computes them in double). */
 typedef struct apexw_hparams {
@@ -145,7 +153,8 @@ int apexw_abi_version(void);
  * Validate one tensor descriptor (HOST copy) before it is uploaded into a
  * device table: kind 0 = compact step, 1 = 8-bit step, 2 = 8-bit step on the
  * full-block kernel (bf16 or fp32 params, NF4 m, quad v, 2048-element blocks),
- * 3 = compact step in APEXW_MODE_SINGLE (full-size v only).  Checks the dtype
+ * 3 = compact step in APEXW_MODE_SINGLE (full-size v only), 4 = factored
+ * tensor (APEXW_FLAG_FACTORED row of either table).  Checks the dtype
  * combination, block size and the 16-byte alignment the vector path needs
  * (unless APEXW_FLAG_SCALAR is set).  Mirrors the per-call tensor checks of the
  * reference's pybind glue (apexw/csrc/apexw_cuda.cpp:109-180, :310-380), done
@@ -176,6 +185,52 @@ int apexw_compact_step(const apexw_tensor* tensors, int32_t n_tensors,
 int apexw_q8_step(const apexw_tensor* tensors, int32_t n_tensors,
                   const apexw_unit* units, int64_t n_units, int64_t n_fast_units,
                   int64_t n_fast_f32_units, const apexw_hparams* hp, void* stream);
+
+/*
+ * Factored second moment (Adafactor-style) for large matrices: the reference's
+ * _apply_factored_v_int8_update (apexw/state.py:442-608), used by precision
+ * "8bit" (INT8 or packed 6-bit m) and "compact" (16-bit m) with factored_v=True.
+ * Per step and tensor, with G = prepared fp32 grad viewed as [rows x cols]:
+ *   row  = b2 row + (1-b2) mean_c(G^2)          col = b2 col + (1-b2) mean_r(G^2)
+ *          (tensors above 262,144 elements: col = b2 col + ((1-b2)/rows) sum_r(G^2))
+ *   nan_to_num(row), nan_to_num(col)
+ *   den  = max(sqrt(row / mean(row)) sqrt(col) + eps_scaled, eps)
+ *   m    = lerp(m, G, 1-b1)  (dequantized; requantized with the EMA-max scale)
+ *   p    = p * wd_factor (where FLAG_WD) - (m / den) * step_size
+ * One entry per factored tensor (device array, 32 bytes each).
+ */
+typedef struct apexw_fv_tensor {
+  uint32_t tensor;   /* row of the tensor table */
+  int32_t rows;      /* shape[0] */
+  int32_t cols;      /* numel / rows */
+  uint32_t flags;    /* APEXW_FV_SUM_COLS: the column EMA of a tensor above 262,144 elements */
+  int64_t ws;        /* float offset of the tensor's workspace (set by apexw_factored_layout) */
+  int32_t band0;     /* first statistics band of the tensor (set by apexw_factored_layout) */
+  int32_t cb0;       /* first column block of the tensor (set by apexw_factored_layout) */
+} apexw_fv_tensor;
+
+#define APEXW_FV_SUM_COLS 1u
+#define APEXW_FV_BAND_ROWS 32   /* rows per statistics band */
+
+/*
+ * Host: lay out the workspace of n_fv factored tensors (HOST array, entries in
+ * ascending tensor order, rows * cols = the tensor's numel).  Writes ws, band0
+ * and cb0 of every entry and the totals; returns the workspace size in floats,
+ * or minus a status.
+ */
+int64_t apexw_factored_layout(apexw_fv_tensor* fv, int32_t n_fv, int64_t* n_bands, int64_t* n_col_blocks);
+
+/*
+ * One factored step of every tensor in fv (device array laid out by
+ * apexw_factored_layout): statistics, finalisation, then the block update over
+ * units (the factored tensors' units of the tensor table: one quantization
+ * block each for quantized m, APEXW_COMPACT_UNIT elements for 16-bit m).
+ * workspace: the floats apexw_factored_layout returned.  hp as for the step
+ * kernels (mode ignored); APEXW_HP_SR rounds the m codes stochastically.
+ */
+int apexw_factored_step(const apexw_tensor* tensors, int32_t n_tensors, const apexw_fv_tensor* fv, int32_t n_fv,
+                        int64_t n_bands, int64_t n_col_blocks, const apexw_unit* units, int64_t n_units,
+                        float* workspace, const apexw_hparams* hp, void* stream);
 
 /*
  * Global-L2 clip coefficient over the grads of the table:

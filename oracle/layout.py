@@ -62,6 +62,14 @@ def block_size_8bit(p, user_bs):
     return 64
 
 
+def can_factor(p, is_peft, min_numel):
+    """state.py:234-281: 2-D+, not PEFT, >= min_numel (65536 for 8bit, 524288 for
+    compact), rows = shape[0] >= 128, cols = numel / rows >= 128."""
+    if p.dim() < 2 or torch.is_complex(p) or p.dtype == torch.float64 or is_peft or p.numel() < min_numel:
+        return False
+    return p.shape[0] >= 128 and p.numel() // p.shape[0] >= 128
+
+
 def init_state(p, group, n_params_in_group, peft_ctx):
     """Allocate and return a fresh state dict for parameter ``p``."""
     prec = group["precision"]
@@ -75,20 +83,31 @@ def init_state(p, group, n_params_in_group, peft_ctx):
         narrow = p.dim() >= 2 and min(p.shape) <= 32 and n < 2048
         raw_int4 = group.get("int4_m")
         pow2 = bs >= 64 and (bs & (bs - 1)) == 0
-        auto_sub = (raw_int4 is not False and n >= 16384 and n % 4 == 0 and pow2
+        fv = bool(group.get("factored_v", False)) and can_factor(p, is_peft, 65536)
+        auto_sub = (raw_int4 is not False and not fv and n >= 16384 and n % 4 == 0 and pow2
                     and (p.dim() < 2 or min(p.shape) >= 8))
-        int4 = auto_sub or (bool(raw_int4) and n >= 512 and n >= bs and not narrow and not is_peft)
+        six = bool(group.get("six_bit", False)) and fv and n >= 524288 and bs % 4 == 0
+        int4 = auto_sub or (bool(raw_int4) and not fv and n >= 512 and n >= bs and not narrow and not is_peft)
         quad = bool(auto_sub and int4)
-        st.update(is_8bit=True, block_size_8bit=bs, is_factored_v=False, is_6bit_m=False,
+        st.update(is_8bit=True, block_size_8bit=bs, is_factored_v=fv, is_6bit_m=six,
                   is_4bit_m=int4, is_quad_v=quad, m_numel=n,
                   state_dtype=torch.int8, state_dtype_v=torch.uint8)
         nblk = (n + bs - 1) // bs
-        if int4:
+        if six:
+            padded = n + (bs - n % bs) % bs
+            padded += (4 - padded % 4) % 4
+            st["exp_avg"] = torch.tensor([0xDF, 0xF7, 0x7D], dtype=torch.uint8).repeat(padded // 4)
+            st["exp_avg_scales"] = torch.full((padded // bs, 1), 1e-12 / 31.0, dtype=torch.float32)
+        elif int4:
             st["exp_avg"] = torch.full(((n + 1) // 2,), 0x77, dtype=torch.uint8)
             st["exp_avg_scales"] = torch.full((nblk, 1), 1e-12, dtype=torch.float32)
         else:
             st["exp_avg"] = torch.zeros(p.shape, dtype=torch.int8)
             st["exp_avg_scales"] = torch.full((nblk, 1), 1e-12 / 127.0, dtype=torch.float32)
+        if fv:
+            st["exp_avg_sq_row"] = torch.zeros(p.shape[0], dtype=torch.float32)
+            st["exp_avg_sq_col"] = torch.zeros(n // p.shape[0], dtype=torch.float32)
+            return st
         st["exp_avg_sq"] = (torch.zeros((n // 4,), dtype=torch.uint8) if quad
                             else torch.zeros(p.shape, dtype=torch.uint8))
         st["exp_avg_sq_scales"] = torch.full((nblk, 1), 1e-12, dtype=torch.float32)
@@ -96,7 +115,17 @@ def init_state(p, group, n_params_in_group, peft_ctx):
     if prec == "8bit":
         st.update(is_8bit=False, is_factored_v=False, is_6bit_m=False, is_4bit_m=False, is_quad_v=False)
     elif prec == "compact":
-        st.update(is_6bit_m=False, is_4bit_m=False, is_factored_v=False)
+        fv = bool(group.get("factored_v", False)) and can_factor(p, is_peft, 524288)
+        st.update(is_6bit_m=False, is_4bit_m=False, is_factored_v=fv)
+        if fv:
+            st["state_dtype"] = compact_dtype(p)
+            st["state_dtype_v"] = torch.float32
+            st["exp_avg"] = torch.zeros(p.shape, dtype=compact_dtype(p))
+            st["exp_avg_sq_row"] = torch.zeros(p.shape[0], dtype=torch.float32)
+            st["exp_avg_sq_col"] = torch.zeros(n // p.shape[0], dtype=torch.float32)
+            st["scale_v"] = 1.0
+            st["sqrt_scale_v"] = 1.0
+            return st
     else:
         raise NotImplementedError(f"oracle covers compact and 8bit, not {prec!r}")
     mdt = compact_dtype(p)

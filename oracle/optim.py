@@ -25,11 +25,14 @@ path rounds differently (see ``oracle.compact``).  Plan validity follows
 ``is_valid_for_step`` (optimizer.py:575-621).
 """
 
+import math
+
 import torch
 
 from . import layout as L
 from .clip import clip_grads_
 from .compact import compact_subgroup_step, replay_subgroup_step, sanitize_grads
+from .factored import factored_update
 from .q8 import q8_param_step
 
 _PREC = {
@@ -57,7 +60,8 @@ def normalize_precision(precision):
 class OracleApexW:
     def __init__(self, params, lr=1e-3, betas=None, eps=1e-8, weight_decay=1e-2, decay_norm_only=True,
                  adamw_compat=False, clip_grad_norm=None, precision="compact", stochastic_rounding=True,
-                 block_size=None, force_compact_v=False, int4_m=None, grad_centralization=False):
+                 block_size=None, force_compact_v=False, int4_m=None, grad_centralization=False,
+                 factored_v=False, six_bit=False):
         precision = normalize_precision(precision)
         if betas is None:
             betas = (0.9, 0.999) if precision == "8bit" else (0.9, 0.99)
@@ -70,7 +74,8 @@ class OracleApexW:
                           decay_norm_only=decay_norm_only, clip_grad_norm=clip_grad_norm,
                           precision=precision, stochastic_rounding=stochastic_rounding,
                           block_size=block_size, force_compact_v=force_compact_v, int4_m=int4_m,
-                          grad_centralization=grad_centralization, params=self.params)
+                          grad_centralization=grad_centralization, factored_v=factored_v, six_bit=six_bit,
+                          params=self.params)
         self.state = {}
         self._plan = None
         self.grad_scale = None
@@ -154,12 +159,19 @@ class OracleApexW:
             self._plan = {"kind": "8bit", "params": plist}
             return
         sts = [self.state[p] for p in plist]
-        homogeneous = all(st["exp_avg"].dtype == st["exp_avg_sq"].dtype == p.dtype
+        homogeneous = all("exp_avg_sq" in st and st["exp_avg"].dtype == st["exp_avg_sq"].dtype == p.dtype
                           and st["exp_avg"].numel() == st["exp_avg_sq"].numel() for p, st in zip(plist, sts))
         if homogeneous:
             self._native_fused(plist, grads, sts, grad_scale=scale, **kw)
             self._plan = {"kind": "native", "params": plist}
             return
+        # factored-v tensors: their own update with their own step (optimizer.py:5382-5432)
+        for p, g, st in zip(plist, grads, sts):
+            if st.get("is_factored_v", False):
+                st["step"].add_(1)
+                self._factored(p, g, st, int(st["step"].item()), self._inv(scale), sanitize=True)
+        keep = [i for i, st in enumerate(sts) if not st.get("is_factored_v", False)]
+        plist, grads, sts = [plist[i] for i in keep], [grads[i] for i in keep], [sts[i] for i in keep]
         grads = self._unscale(grads, scale)
         sub = {}
         for p, g, st in zip(plist, grads, sts):
@@ -196,10 +208,16 @@ class OracleApexW:
         if plan["kind"] == "native":
             self._native_fused(plist, grads, sts, sanitize=False, grad_scale=scale, **kw)
             return
-        grads = self._unscale(sanitize_grads(grads), scale)
         steps = [st["step"] for st in sts]
         torch._foreach_add_(steps, 1)
         step = int(steps[0].item())
+        # factored-v entries of the replayed plan: the plan's step, no nan_to_num (optimizer.py:1141-1163)
+        for p, g, st in zip(plist, grads, sts):
+            if st.get("is_factored_v", False):
+                self._factored(p, g, st, step, self._inv(scale), sanitize=False)
+        keep = [i for i, st in enumerate(sts) if not st.get("is_factored_v", False)]
+        plist, grads, sts = [plist[i] for i in keep], [grads[i] for i in keep], [sts[i] for i in keep]
+        grads = self._unscale(sanitize_grads(grads), scale)
         sub = {}
         for p, g, st in zip(plist, grads, sts):
             compact = st["exp_avg"].dtype in (torch.bfloat16, torch.float16)
@@ -210,6 +228,17 @@ class OracleApexW:
                                  [i[2]["exp_avg"] for i in items], [i[2]["exp_avg_sq"] for i in items],
                                  apply_wd_mask=[(i[0].dim() >= 2) if dno else True for i in items],
                                  step=step, is_quad=quad, stochastic=grp["stochastic_rounding"], **kw)
+
+    def _factored(self, p, g, st, step, inv, sanitize):
+        grp = self.group
+        b1, b2 = grp["betas"]
+        lr, wd, eps = grp["lr"], grp["weight_decay"], grp["eps"]
+        bc1, bc2 = 1.0 - b1 ** step, 1.0 - b2 ** step
+        apply_wd = wd != 0 and (not grp["decay_norm_only"] or p.dim() >= 2)
+        factored_update(p, g, st, beta1=b1, beta2=b2, step_size=lr * math.sqrt(bc2) / bc1,
+                        eps_scaled=eps * math.sqrt(bc2), eps=eps, stochastic=st.get("stochastic_rounding", True),
+                        block_size=st.get("block_size_8bit", 256),
+                        wd_factor=max(1.0 - lr * wd, 0.0) if apply_wd else None, inv_scale=inv, sanitize=sanitize)
 
     @staticmethod
     def _native_fused(params, grads, sts, *, lr, beta1, beta2, eps, weight_decay, decay_norm_only,

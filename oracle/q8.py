@@ -19,6 +19,7 @@ import math
 import torch
 
 from . import quant as Q
+from .factored import factored_update
 
 CHUNK = 262144  # _FACTORED_CHUNK_ELEMS, state.py:44
 
@@ -44,6 +45,11 @@ def q8_param_step(p, g, st, *, lr, beta1, beta2, eps, weight_decay, decay_norm_o
     apply_wd = weight_decay != 0 and (not decay_norm_only or p.dim() >= 2)
     sr = st.get("stochastic_rounding", True)
     n = p.numel()
+    if st.get("is_factored_v", False):              # optimizer.py:4380-4400
+        factored_update(p, g, st, beta1=beta1, beta2=beta2, step_size=step_size, eps_scaled=eps_scaled, eps=eps,
+                        stochastic=sr, block_size=st.get("block_size_8bit", 256),
+                        wd_factor=decay if apply_wd else None, inv_scale=inv_scale, sanitize=True)
+        return
     if st.get("is_8bit", False) and n > CHUNK and p.is_contiguous():
         _chunked(p, g, st, beta1, beta2, eps, step_size, eps_scaled, decay if apply_wd else None, sr, inv_scale)
         return

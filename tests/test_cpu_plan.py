@@ -39,6 +39,11 @@ class _Recorder:
         self.calls.append(("clip", a, None))
         return 0
 
+    def apexw_factored_step(self, *a):
+        hp = ctypes.cast(a[-2], ctypes.POINTER(L.HParams)).contents
+        self.calls.append(("factored", a, {f: getattr(hp, f) for f, _ in L.HParams._fields_}))
+        return 0
+
 
 @pytest.fixture
 def cpu_plans(monkeypatch):
@@ -221,3 +226,38 @@ def test_missing_grad_or_inactive_grad_invalidates(cpu_plans):
     ps[2].grad = None
     ps[0].grad = None                             # a plan parameter loses its grad
     assert not plan.valid_for(group)
+
+
+@pytest.mark.parametrize("prec", ["8bit", "compact"])
+def test_factored_rows_and_launch(cpu_plans, prec):
+    """Factored tensors stay rows of the table (clip and centralization see them),
+    flagged so the step kernels skip them; apexw_factored_step gets their table
+    rows (ascending), shapes, workspace and units."""
+    shapes = [(1024, 512), (300,), (256, 512)] if prec == "compact" else [(256, 512), (300,), (1024, 512)]
+    ps = _params(shapes, torch.bfloat16)
+    opt = _opt(ps, precision=prec, factored_v=True, six_bit=True, lr=1e-3, weight_decay=0.1)
+    plan, group = _build(opt)
+    plan.execute(group, seed=0)
+    plan.execute(group, seed=0)
+    table = _table(plan)
+    fac = (table["flags"] & L.FLAG_FACTORED) != 0
+    big = [int(n) for n in table["n"][fac]]
+    if prec == "compact":
+        assert big == [1024 * 512]                  # 256 x 512 is under the compact threshold
+    else:
+        assert sorted(big) == [256 * 512, 1024 * 512]
+        m6 = (table["flags"] & L.FLAG_M6) != 0
+        assert [int(n) for n in table["n"][m6]] == [1024 * 512]
+    calls = [c for c in cpu_plans.calls if c[0] == "factored"]
+    assert len(calls) == 2
+    _, args, hp = calls[-1]
+    fv = plan.fv["d_fv"].cpu().numpy().view(L.FV_TENSOR_DTYPE)
+    assert list(fv["tensor"]) == sorted(fv["tensor"]) and args[3] == len(fv)
+    for row in fv:
+        d = int(row["tensor"])
+        assert fac[d] and int(row["rows"]) * int(row["cols"]) == int(table["n"][d])
+        assert int(row["flags"]) == (L.FV_SUM_COLS if int(table["n"][d]) > 262144 else 0)
+    units = plan.fv["d_units"].cpu().numpy().view(L.UNIT_DTYPE)
+    assert set(units["tensor"].tolist()) == set(fv["tensor"].tolist())
+    assert hp["step"] == 2 and hp["flags"] & L.HP_FV_SANITIZE == (L.HP_FV_SANITIZE if prec == "8bit" else 0)
+    assert hp["eps"] == pytest.approx(1e-8) and hp["mode"] == L.MODE_COLD

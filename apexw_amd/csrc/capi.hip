@@ -169,10 +169,11 @@ int64_t apexw_factored_layout(apexw_fv_tensor* fv, int32_t n_fv, int64_t* n_band
     e.ws = ws;
     e.band0 = (int32_t)bands;
     e.cb0 = (int32_t)cbs;
-    // row sums / norms, per-band column partials, column square roots; 16-byte aligned
-    ws += ((int64_t)e.rows + nb * e.cols + e.cols + 3) & ~(int64_t)3;
+    // band sums + inverse row mean, per-band column partials, column square roots; each 16-byte aligned
+    auto r4 = [](int64_t x) { return (x + 3) & ~(int64_t)3; };
+    ws += r4(nb + 1) + r4(nb * e.cols) + r4(e.cols);
     bands += nb;
-    cbs += ((int64_t)e.cols + 255) / 256;
+    cbs += ((int64_t)e.cols + 63) / 64;   // finalisation column blocks of 64
     if (bands > INT32_MAX || cbs > INT32_MAX) return -APEXW_ERR_ARG;
   }
   *n_bands = bands;

@@ -12,12 +12,14 @@
 //     band (column partials, written per band) and of its elements per row
 //     (row partials, reduced across the workgroup at the end of the band).  The
 //     grad is read once, in 4 KiB row segments per wave.
-//  2. finalisation: column blocks of 256 sum the band partials (fp64) and apply
-//     the column EMA; one workgroup per tensor applies the row EMA, reduces the
-//     row mean and writes sqrt(row / mean) in place of the row sums.
+//     At the end of the band it applies the row EMA to the band's rows and
+//     keeps their sum.
+//  2. finalisation: column blocks of 64 sum the band partials (fp64) and apply
+//     the column EMA; one workgroup per tensor sums the band sums into the row
+//     mean.
 //  3. update: one wave per unit (quantization block, or 2048 elements for 16-bit
-//     m): den = max(row_norm[r] col_sqrt[c] + eps_scaled, eps), m lerp, p update,
-//     block requantization with the EMA-max scale (0.9).
+//     m): den = max(sqrt(row[r] / mean) col_sqrt[c] + eps_scaled, eps), m lerp,
+//     p update, block requantization with the EMA-max scale (0.9).
 //
 // The reductions sum in a different order than torch's CPU kernels, so the row
 // and column EMAs agree with the reference to a few fp32 ulps, not bit for bit;
@@ -28,6 +30,7 @@ namespace {
 
 constexpr int kBand = APEXW_FV_BAND_ROWS;
 constexpr int kPass = 2048;  // columns per statistics pass (256 lanes x 8)
+constexpr int kColBlock = 64;  // columns per finalisation workgroup
 
 struct FvCtx {
   const apexw_hparams* hp;
@@ -35,6 +38,19 @@ struct FvCtx {
 };
 
 APEXW_DEV float unit_uniform(uint32_t r16) { return ((float)(r16 & 0xFFFFu) + 0.5f) * (1.0f / 65536.0f); }
+
+// Division with a refined reciprocal and one FMA residual correction (Markstein):
+// equal to the IEEE quotient except within ~2^-46 of a rounding midpoint.  The
+// divisors here are positive, finite and normal (scales >= 1e-12 / 127,
+// denominators >= eps).
+APEXW_DEV float rcp_refined(float y) {
+  const float r0 = __builtin_amdgcn_rcpf(y);
+  return fmaf(fmaf(-y, r0, 1.0f), r0, r0);
+}
+APEXW_DEV float div_refined(float x, float y, float r) {
+  const float q0 = x * r;
+  return fmaf(fmaf(-q0, y, x), r, q0);
+}
 
 APEXW_DEV float lerp_to(float a, float b, float coef, bool hi) {
   // torch lerp(a, b, w): |w| < 0.5 -> a + w*(b-a); else b + (w-1)*(b-a), one FMA each
@@ -85,28 +101,35 @@ APEXW_DEV int fv_find_tensor(const apexw_fv_tensor* fv, int n_fv, uint32_t tenso
   return lo;
 }
 
-// workspace of one tensor: [rows] row sums, then row norms in place;
-// [n_bands x cols] column partials; [cols] column square roots
+// workspace of one tensor: aux = [n_bands] band sums of the new row EMA, then
+// the inverse row mean at aux[n_bands]; [n_bands x cols] column partials;
+// [cols] column square roots
 struct FvWs {
-  float* row;
+  float* aux;
   float* part;
   float* col;
 };
+APEXW_DEV int64_t fv_round4(int64_t x) { return (x + 3) & ~(int64_t)3; }
 APEXW_DEV FvWs fv_ws(float* ws, const apexw_fv_tensor& e) {
+  // each part starts on a 16-byte boundary (apexw_factored_layout sizes them the same way)
   const int64_t nb = (e.rows + kBand - 1) / kBand;
   float* base = ws + e.ws;
-  return {base, base + e.rows, base + e.rows + nb * (int64_t)e.cols};
+  float* part = base + fv_round4(nb + 1);
+  return {base, part, part + fv_round4(nb * (int64_t)e.cols)};
 }
 
 // ---------------------------------------------------------------------------
 // 1. statistics
 // ---------------------------------------------------------------------------
-// band: the band's index within its tensor
+// band: the band's index within its tensor.  Writes the band's column partials,
+// applies the row EMA to its rows (exp_avg_sq_row) and leaves the band's sum of
+// the new row values in aux[band] for the row mean.
 template <int GD>
 APEXW_DEV void fv_stats_band(const apexw_tensor& t, const apexw_fv_tensor& e, int64_t band, float* ws,
                              const FvCtx& c) {
   __shared__ float s_row[4][kBand];
   const FvWs w = fv_ws(ws, e);
+  const apexw_hparams& hp = *c.hp;
   const int64_t cols = e.cols;
   const int r0 = (int)(band * kBand);
   const int nr = min(kBand, e.rows - r0);
@@ -146,7 +169,7 @@ APEXW_DEV void fv_stats_band(const apexw_tensor& t, const apexw_fv_tensor& e, in
     for (int j = 0; j < 8; ++j)
       if (j < cnt) w.part[band * cols + cb + j] = cacc[j];
   }
-  // rows: reduce each row partial across the workgroup
+  // rows: reduce each row partial across the workgroup, then the row EMA
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
   for (int i = 0; i < kBand; ++i) {
@@ -154,9 +177,18 @@ APEXW_DEV void fv_stats_band(const apexw_tensor& t, const apexw_fv_tensor& e, in
     if (lane == 0) s_row[wave][i] = s;
   }
   __syncthreads();
-  if ((int)threadIdx.x < nr) {
-    const int i = threadIdx.x;
-    w.row[r0 + i] = ((s_row[0][i] + s_row[1][i]) + s_row[2][i]) + s_row[3][i];
+  if (wave == 0) {
+    float rn = 0.0f;
+    if (lane < nr) {
+      const float sum = ((s_row[0][lane] + s_row[1][lane]) + s_row[2][lane]) + s_row[3][lane];
+      const float mean = (float)((double)sum / (double)cols);
+      float* rv = (float*)t.v;
+      rn = fmaf(mean, hp.one_minus_beta2, rv[r0 + lane] * hp.beta2);
+      if (!(fabsf(rn) <= 3.402823466e38f)) rn = 0.0f;  // nan_to_num(0, 0, 0)
+      rv[r0 + lane] = rn;
+    }
+    const float bs = wave_sum(rn);
+    if (lane == 0) w.aux[band] = bs;
   }
 }
 
@@ -183,18 +215,35 @@ __global__ __launch_bounds__(256) void fv_finalize_kernel(const apexw_tensor* __
                                                           int64_t n_col_blocks, float* __restrict__ ws,
                                                           apexw_hparams hp) {
   __shared__ double s_sum[4];
+  __shared__ double s_col[4][kColBlock];
   const int64_t b = blockIdx.x;
   if (b < n_col_blocks) {
-    // column EMA: the reference's mean over rows, or sum * (1-b2)/rows above 262,144 elements
+    // column EMA: the reference's mean over rows, or sum * (1-b2)/rows above 262,144 elements.
+    // 64 columns per workgroup, each summed by 4 waves over interleaved bands
+    // (4 fp64 accumulators per lane), then combined in a fixed order.
     const int k = fv_find_cb(fv, n_fv, b);
     const apexw_fv_tensor e = fv[k];
     const apexw_tensor& t = tensors[e.tensor];
     const FvWs w = fv_ws(ws, e);
-    const int64_t col = (b - e.cb0) * 256 + threadIdx.x;
-    if (col >= e.cols) return;
+    const int slice = threadIdx.x >> 6;
+    const int64_t col = (b - e.cb0) * kColBlock + (threadIdx.x & 63);
     const int64_t nb = (e.rows + kBand - 1) / kBand;
-    double s = 0.0;
-    for (int64_t i = 0; i < nb; ++i) s += (double)w.part[i * e.cols + col];
+    if (col < e.cols) {
+      double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
+      int64_t i = slice;
+      for (; i + 12 < nb; i += 16) {
+        a0 += (double)w.part[i * e.cols + col];
+        a1 += (double)w.part[(i + 4) * e.cols + col];
+        a2 += (double)w.part[(i + 8) * e.cols + col];
+        a3 += (double)w.part[(i + 12) * e.cols + col];
+      }
+      for (; i < nb; i += 4) a0 += (double)w.part[i * e.cols + col];
+      s_col[slice][threadIdx.x & 63] = (a0 + a1) + (a2 + a3);
+    }
+    __syncthreads();
+    if (slice != 0 || col >= e.cols) return;
+    const int l = threadIdx.x & 63;
+    const double s = ((s_col[0][l] + s_col[1][l]) + s_col[2][l]) + s_col[3][l];
     float* cv = t.v_scale;
     const float old = cv[col];
     float cn;
@@ -208,27 +257,20 @@ __global__ __launch_bounds__(256) void fv_finalize_kernel(const apexw_tensor* __
     w.col[col] = sqrtf(cn);
     return;
   }
-  // rows: EMA, nan_to_num, mean over rows, sqrt(row / mean)
+  // rows: mean of the new row EMA (band sums in fp64) -> 1 / max(mean, 1e-30)
   const apexw_fv_tensor e = fv[b - n_col_blocks];
-  const apexw_tensor& t = tensors[e.tensor];
   const FvWs w = fv_ws(ws, e);
-  float* rv = (float*)t.v;
+  const int64_t nb = (e.rows + kBand - 1) / kBand;
   double acc = 0.0;
-  for (int r = threadIdx.x; r < e.rows; r += 256) {
-    const float mean = (float)((double)w.row[r] / (double)e.cols);
-    float rn = fmaf(mean, hp.one_minus_beta2, rv[r] * hp.beta2);
-    if (!(fabsf(rn) <= 3.402823466e38f)) rn = 0.0f;
-    rv[r] = rn;
-    acc += (double)rn;
-  }
-  // workgroup sum in fp64
+  for (int64_t i = threadIdx.x; i < nb; i += 256) acc += (double)w.aux[i];
   for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
   if ((threadIdx.x & 63) == 0) s_sum[threadIdx.x >> 6] = acc;
   __syncthreads();
-  const double tot = ((s_sum[0] + s_sum[1]) + s_sum[2]) + s_sum[3];
-  const float mean = fmaxf((float)(tot / (double)e.rows), 1e-30f);
-  const float inv = 1.0f / mean;
-  for (int r = threadIdx.x; r < e.rows; r += 256) w.row[r] = sqrtf(rv[r] * inv);
+  if (threadIdx.x == 0) {
+    const double tot = ((s_sum[0] + s_sum[1]) + s_sum[2]) + s_sum[3];
+    const float mean = fmaxf((float)(tot / (double)e.rows), 1e-30f);
+    w.aux[nb] = 1.0f / mean;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -255,6 +297,9 @@ APEXW_DEV void fv_unit(const apexw_tensor& t, const apexw_fv_tensor& e, uint32_t
   const int64_t cols = e.cols;
   const float ms_old = MK == kM16 ? 0.0f : t.m_scale[unit];
   const uint32_t key = rng_key(hp.seed, tix, hp.step, 3u, (uint32_t)(start >> 32));
+  // row factor sqrt(row / mean(row)), as the reference forms it per row
+  const float* rvec = (const float*)t.v;
+  const float inv = w.aux[(e.rows + kBand - 1) / kBand];
 
   float mnew[4][8];
   float amax = 0.0f;
@@ -311,7 +356,7 @@ APEXW_DEV void fv_unit(const apexw_tensor& t, const apexw_fv_tensor& e, uint32_t
       if (j < cnt) {
         const float x = fv_grad<GD>(g[j], c);
         m[j] = lerp_to(m[j], x, hp.lerp_coef, hp.flags & APEXW_HP_LERP_HI);
-        const float den = fmaxf(w.row[row] * w.col[col] + hp.eps_scaled, hp.eps);
+        const float den = fmaxf(sqrtf(rvec[row] * inv) * w.col[col] + hp.eps_scaled, hp.eps);
         const float upd = (m[j] / den) * hp.step_size;
         if constexpr (PD == APEXW_F32) {
           p[j] = (wd ? p[j] * hp.wd_factor : p[j]) - upd;
@@ -390,6 +435,168 @@ APEXW_DEV void fv_unit(const apexw_tensor& t, const apexw_fv_tensor& e, uint32_t
   }
 }
 
+// A whole 2048-element unit with 16-byte aligned buffers: every load of the wave
+// is issued before any arithmetic, m moves as 8-byte (INT8) / 6-byte (6-bit) /
+// 16-byte (bf16) vectors, and the row / column of each lane's first element
+// comes from one 32-bit division per group.  Same arithmetic as fv_unit.
+template <int PD, int MK>
+APEXW_DEV void fv_unit_full(const apexw_tensor& t, const apexw_fv_tensor& e, uint32_t tix, uint32_t unit,
+                            float* ws, const FvCtx& c) {
+  constexpr int GD = PD;
+  constexpr int W = PD == APEXW_F32 ? 2 : 1;  // 16-byte words per 8 elements of p / g
+  const apexw_hparams& hp = *c.hp;
+  const bool sr = hp.flags & APEXW_HP_SR;
+  const bool wd = t.flags & APEXW_FLAG_WD;
+  const FvWs w = fv_ws(ws, e);
+  const int64_t start = (int64_t)unit * 2048;
+  const int lane = lane_id();
+  const uint32_t cols = (uint32_t)e.cols;
+  const int64_t row0 = start / (int64_t)cols;
+  const uint32_t col0 = (uint32_t)(start - row0 * (int64_t)cols);
+  const float ms_old = MK == kM16 ? 0.0f : t.m_scale[unit];
+  const uint32_t key = rng_key(hp.seed, tix, hp.step, 3u, (uint32_t)(start >> 32));
+  const float* rvec = (const float*)t.v;
+  const float inv = w.aux[(e.rows + kBand - 1) / kBand];
+  // ---- loads
+  u32x4 praw[4][W], graw[4][W];
+  u32x4 mw16[MK == kM16 ? 4 : 1];
+  u32x2 mw8[MK == kM16 ? 1 : 4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int64_t e0 = start + k * 512 + lane * 8;
+    const auto pp = APEXW_GLOBAL(const u32x4, (const uint8_t*)t.p + e0 * (PD == APEXW_F32 ? 4 : 2));
+    const auto gp = APEXW_GLOBAL(const u32x4, (const uint8_t*)t.g + e0 * (GD == APEXW_F32 ? 4 : 2));
+#pragma unroll
+    for (int i = 0; i < W; ++i) {
+      praw[k][i] = __builtin_nontemporal_load(pp + i);
+      graw[k][i] = __builtin_nontemporal_load(gp + i);
+    }
+    if constexpr (MK == kM16) {
+      mw16[k] = __builtin_nontemporal_load(APEXW_GLOBAL(const u32x4, (const uint16_t*)t.m + e0));
+    } else if constexpr (MK == kM8) {
+      mw8[k] = __builtin_nontemporal_load(APEXW_GLOBAL(const u32x2, (const int8_t*)t.m + e0));
+    } else {
+      // 6 bytes at (e0 / 4) * 3, 2-byte aligned: three 16-bit words
+      const auto mp = APEXW_GLOBAL(const uint16_t, (const uint8_t*)t.m + (e0 >> 2) * 3);
+      const uint32_t h0 = mp[0], h1 = mp[1], h2 = mp[2];
+      mw8[k] = u32x2{h0 | ((h1 & 0xFFu) << 16), (h1 >> 8) | (h2 << 8)};
+    }
+  }
+  // ---- update
+  float mnew[4][8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int64_t e0 = start + k * 512 + lane * 8;
+    float p[8], g[8], m[8];
+    const uint32_t* pw = (const uint32_t*)&praw[k][0];
+    const uint32_t* gw = (const uint32_t*)&graw[k][0];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      p[j] = PD == APEXW_F32 ? __uint_as_float(pw[j]) : (j & 1 ? __uint_as_float(pw[j >> 1] & 0xFFFF0000u)
+                                                              : bf16_bits_to_f32(pw[j >> 1] & 0xFFFFu));
+      g[j] = GD == APEXW_F32 ? __uint_as_float(gw[j]) : (j & 1 ? __uint_as_float(gw[j >> 1] & 0xFFFF0000u)
+                                                              : bf16_bits_to_f32(gw[j >> 1] & 0xFFFFu));
+    }
+    if constexpr (MK == kM16) {
+      const uint32_t* mw = (const uint32_t*)&mw16[k];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        m[j] = j & 1 ? __uint_as_float(mw[j >> 1] & 0xFFFF0000u) : bf16_bits_to_f32(mw[j >> 1] & 0xFFFFu);
+    } else if constexpr (MK == kM8) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        m[j] = (float)(int8_t)(((j < 4 ? mw8[k].x : mw8[k].y) >> (8 * (j & 3))) & 0xFFu) * ms_old;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        m[j] = ((float)(((j < 4 ? mw8[k].x : mw8[k].y) >> (6 * (j & 3))) & 63u) - 31.0f) * ms_old;
+    }
+    uint32_t x = col0 + (uint32_t)(k * 512 + lane * 8);
+    const uint32_t rq = x / cols;
+    int64_t row = row0 + rq;
+    uint32_t col = x - rq * cols;
+    float den[8];
+    if (col + 8 <= cols) {
+      // the 8 elements share a row: one row factor, the column roots as two 16-byte loads when aligned
+      const float rv = sqrtf(rvec[row] * inv);
+      float cs[8];
+      if ((col & 3u) == 0) {
+        const float4 a = *(const float4*)(w.col + col), b = *(const float4*)(w.col + col + 4);
+        cs[0] = a.x; cs[1] = a.y; cs[2] = a.z; cs[3] = a.w; cs[4] = b.x; cs[5] = b.y; cs[6] = b.z; cs[7] = b.w;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) cs[j] = w.col[col + j];
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) den[j] = fmaxf(rv * cs[j] + hp.eps_scaled, hp.eps);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        den[j] = fmaxf(sqrtf(rvec[row] * inv) * w.col[col] + hp.eps_scaled, hp.eps);
+        if (++col == cols) {
+          col = 0;
+          ++row;
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float gj = fv_grad<GD>(g[j], c);
+      m[j] = lerp_to(m[j], gj, hp.lerp_coef, hp.flags & APEXW_HP_LERP_HI);
+      const float upd = div_refined(m[j], den[j], rcp_refined(den[j])) * hp.step_size;
+      if constexpr (PD == APEXW_F32) {
+        p[j] = (wd ? p[j] * hp.wd_factor : p[j]) - upd;
+      } else {
+        const float pd = wd ? rnd<PD>(p[j] * hp.wd_factor) : p[j];
+        p[j] = rnd<PD>(pd - rnd<PD>(upd));
+      }
+      mnew[k][j] = m[j];
+      amax = fmaxf(amax, fabsf(m[j]));
+    }
+    store8<PD>(t.p, e0, p);
+    if constexpr (MK == kM16) store8<APEXW_BF16>(t.m, e0, m);
+  }
+  if constexpr (MK == kM16) return;
+  // ---- requantize m
+  amax = wave_max(amax);
+  float ms = fmaxf(amax, 1e-12f) / (MK == kM8 ? 127.0f : 31.0f);
+  ms = fmaxf(ms, ms_old * 0.9f);
+  if (lane == 0) t.m_scale[unit] = ms;
+  const float lim = MK == kM8 ? 127.0f : 31.0f;
+  const float rms = rcp_refined(ms);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int64_t e0 = start + k * 512 + lane * 8;
+    uint32_t q[8];
+    // SR noise: a per-lane xorshift32 stream seeded from the element index
+    uint32_t rs = rng_at(key, (uint32_t)e0) | 1u;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float y = div_refined(mnew[k][j], ms, rms);
+      if (sr) {
+        rs ^= rs << 13;
+        rs ^= rs >> 17;
+        rs ^= rs << 5;
+        y = y + (unit_uniform(rs >> 16) - 0.5f);
+      }
+      const int32_t qi = (int32_t)fminf(fmaxf(rintf(y), -lim), lim);
+      q[j] = MK == kM8 ? ((uint32_t)qi & 0xFFu) : (uint32_t)(qi + 31);
+    }
+    if constexpr (MK == kM8) {
+      const u32x2 v = {q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24), q[4] | (q[5] << 8) | (q[6] << 16) | (q[7] << 24)};
+      __builtin_nontemporal_store(v, APEXW_GLOBAL(u32x2, (int8_t*)t.m + e0));
+    } else {
+      const uint32_t w0 = q[0] | (q[1] << 6) | (q[2] << 12) | (q[3] << 18);
+      const uint32_t w1 = q[4] | (q[5] << 6) | (q[6] << 12) | (q[7] << 18);
+      const auto mp = APEXW_GLOBAL(uint16_t, (uint8_t*)t.m + (e0 >> 2) * 3);
+      mp[0] = (uint16_t)(w0 & 0xFFFFu);
+      mp[1] = (uint16_t)((w0 >> 16) | ((w1 & 0xFFu) << 8));
+      mp[2] = (uint16_t)(w1 >> 8);
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void fv_update_kernel(const apexw_tensor* __restrict__ tensors,
                                                         const apexw_fv_tensor* __restrict__ fv, int n_fv,
                                                         const apexw_unit* __restrict__ units, int64_t n_units,
@@ -405,6 +612,21 @@ __global__ __launch_bounds__(256) void fv_update_kernel(const apexw_tensor* __re
     const apexw_fv_tensor& e = fv[fv_find_tensor(fv, n_fv, un.tensor)];
     if (e.tensor != un.tensor || !(t.flags & APEXW_FLAG_FACTORED)) continue;  // never taken for a valid plan
     const bool p32 = ((t.flags >> APEXW_FLAG_PDT_SHIFT) & 3u) == APEXW_F32;
+    const bool full = !(t.flags & APEXW_FLAG_SCALAR) && (t.block == 0 || t.block == 2048) &&
+                      (int64_t)(un.unit + 1) * 2048 <= t.n;
+    if (full) {
+      if (t.block == 0) {
+        if (p32) fv_unit_full<APEXW_F32, kM16>(t, e, un.tensor, un.unit, ws, c);
+        else fv_unit_full<APEXW_BF16, kM16>(t, e, un.tensor, un.unit, ws, c);
+      } else if (t.flags & APEXW_FLAG_M6) {
+        if (p32) fv_unit_full<APEXW_F32, kM6>(t, e, un.tensor, un.unit, ws, c);
+        else fv_unit_full<APEXW_BF16, kM6>(t, e, un.tensor, un.unit, ws, c);
+      } else {
+        if (p32) fv_unit_full<APEXW_F32, kM8>(t, e, un.tensor, un.unit, ws, c);
+        else fv_unit_full<APEXW_BF16, kM8>(t, e, un.tensor, un.unit, ws, c);
+      }
+      continue;
+    }
     if (t.block == 0) {
       if (p32) fv_unit<APEXW_F32, kM16>(t, e, un.tensor, un.unit, ws, c);
       else fv_unit<APEXW_BF16, kM16>(t, e, un.tensor, un.unit, ws, c);

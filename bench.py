@@ -73,6 +73,13 @@ CONFIGS = {
                dtype=torch.bfloat16, kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True), per_tensor_scale=True),
     "c3": dict(workload="C3 8-bit ApexW step, Llama-3-8B (8.03B params) bf16, SR on", shapes=llama3_8b_shapes(),
                dtype=torch.bfloat16, kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, precision="8bit")),
+    "c3fv": dict(workload="C3 shapes, 8-bit ApexW with factored_v=True (INT8 m, fp32 row/column v), bf16, SR on",
+                 shapes=llama3_8b_shapes(), dtype=torch.bfloat16, grad_reads=2,
+                 kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, precision="8bit", factored_v=True)),
+    "c3fv6": dict(workload="C3 shapes, 8-bit ApexW with factored_v=True, six_bit=True (6-bit m), bf16, SR on",
+                  shapes=llama3_8b_shapes(), dtype=torch.bfloat16, grad_reads=2,
+                  kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, precision="8bit", factored_v=True,
+                              six_bit=True)),
     "c4": dict(workload="C4 compact ApexW step, 20k ragged bf16 tensors, clip 1.0", shapes=ragged_shapes(),
                dtype=torch.bfloat16, kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, clip_grad_norm=1.0),
                zero_frac=0.05),
@@ -137,11 +144,13 @@ def copy_calibration():
     print(json.dumps({"copy_calibration": {"bytes_read": n * 4, "bytes_written": n * 4, "launches": 3}}), flush=True)
 
 
-def state_bytes(opt, params):
-    """Algorithmic HBM bytes of one step: p read+write, g read, every state tensor read+write."""
+def state_bytes(opt, params, grad_reads=1):
+    """Algorithmic HBM bytes of one step: p read+write, g read (twice with a factored
+    second moment: its row / column statistics must be complete before any update),
+    every state tensor read+write."""
     tot = 0
     for p in params:
-        tot += 2 * p.numel() * p.element_size() + p.grad.numel() * p.grad.element_size()
+        tot += 2 * p.numel() * p.element_size() + grad_reads * p.grad.numel() * p.grad.element_size()
         for k, v in opt.state[p].items():
             if torch.is_tensor(v) and k != "step" and v.device.type == "cuda":
                 tot += 2 * v.numel() * v.element_size()
@@ -199,7 +208,7 @@ def cpu_baseline(cfg_name, budget_s=20.0):
         return {"value": params[0].numel() * steps / el, "unit": "params/s", "cores": threads, "kind": "port",
                 "sample": f"the q matrix (4096x4096) of the layer; {steps} Muon steps, fp32 Newton-Schulz "
                           f"(the reference's CPU work dtype); CPU oracle (torch CPU ops)"}
-    if cfg_name == "c3":
+    if cfg_name in ("c3", "c3fv", "c3fv6"):
         shapes = llama3_8b_shapes()[1:10]          # one transformer layer (218M params)
         sample = "one Llama-3-8B layer (q,k,v,o,gate,up,down + 2 RMSNorm, 218.1M params)"
     elif cfg_name == "c4":
@@ -253,7 +262,7 @@ def main():
     for _ in range(args.warmup):
         opt.step()
     torch.cuda.synchronize()
-    nbytes = 0 if cfg.get("mfma") else state_bytes(opt, params)
+    nbytes = 0 if cfg.get("mfma") else state_bytes(opt, params, cfg.get("grad_reads", 1))
     stream = torch.cuda.current_stream(dev)
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()

@@ -121,7 +121,7 @@ SIGNATURES = {
     "apexw_muon_apply": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _i64, _i32, _f32, _i32, _f32, _vp]),
     "apexw_factored_layout": (ctypes.c_int64, [_vp, _i32, ctypes.POINTER(ctypes.c_int64),
                                                ctypes.POINTER(ctypes.c_int64)]),
-    "apexw_factored_step": (ctypes.c_int, [_vp, _i32, _vp, _i32, _i64, _i64, _vp, _i64, _vp, _HP, _vp]),
+    "apexw_factored_step": (ctypes.c_int, [_vp, _i32, _vp, _i32, _i64, _i64, _vp, _i64, _i64, _vp, _HP, _vp]),
 }
 
 GEMM_TILE = 256

@@ -273,10 +273,14 @@ class StepPlan:
         if ws < 0:
             L.check(-ws, "apexw_factored_layout")
         sel = np.isin(self._host_units["tensor"], np.array(rows, dtype=np.uint32))
-        units = np.ascontiguousarray(self._host_units[sel])
+        units = self._host_units[sel]
+        # bf16-parameter tensors' units first: each parameter dtype runs on its own kernel
+        row32 = np.array([p.dtype == torch.float32 for p in self.params], dtype=bool)[self.perm]
+        p32 = row32[units["tensor"]]
+        units = np.ascontiguousarray(np.concatenate([units[~p32], units[p32]]))
         return dict(rows=rows, n=len(fv), d_fv=torch.from_numpy(fv.view(np.uint8)).to(self.device),
                     ws=torch.empty(max(ws, 1), dtype=torch.float32, device=self.device),
-                    n_bands=nb.value, n_cb=ncb.value, n_units=len(units),
+                    n_bands=nb.value, n_cb=ncb.value, n_units=len(units), n_bf16_units=int((~p32).sum()),
                     d_units=torch.from_numpy(units.view(np.uint8)).to(self.device) if len(units) else None)
 
     def _refresh_grads(self):
@@ -454,7 +458,7 @@ class StepPlan:
             st = self._lib.apexw_factored_step(
                 self.d_table.data_ptr(), len(self.params), fv["d_fv"].data_ptr(), fv["n"], fv["n_bands"],
                 fv["n_cb"], fv["d_units"].data_ptr() if fv["d_units"] is not None else None, fv["n_units"],
-                fv["ws"].data_ptr(), ctypes_ref(hp), stream)
+                fv["n_bf16_units"], fv["ws"].data_ptr(), ctypes_ref(hp), stream)
             L.check(st, "apexw_factored_step")
 
     def _split_by_step(self):

@@ -597,6 +597,9 @@ APEXW_DEV void fv_unit_full(const apexw_tensor& t, const apexw_fv_tensor& e, uin
   }
 }
 
+// One kernel per parameter dtype, each over its own range of units: the fp32
+// variant's larger register footprint does not lower the bf16 variant's occupancy.
+template <int PDK>
 __global__ __launch_bounds__(256) void fv_update_kernel(const apexw_tensor* __restrict__ tensors,
                                                         const apexw_fv_tensor* __restrict__ fv, int n_fv,
                                                         const apexw_unit* __restrict__ units, int64_t n_units,
@@ -612,46 +615,39 @@ __global__ __launch_bounds__(256) void fv_update_kernel(const apexw_tensor* __re
     const apexw_fv_tensor& e = fv[fv_find_tensor(fv, n_fv, un.tensor)];
     if (e.tensor != un.tensor || !(t.flags & APEXW_FLAG_FACTORED)) continue;  // never taken for a valid plan
     const bool p32 = ((t.flags >> APEXW_FLAG_PDT_SHIFT) & 3u) == APEXW_F32;
+    if (p32 != (PDK == APEXW_F32)) continue;
     const bool full = !(t.flags & APEXW_FLAG_SCALAR) && (t.block == 0 || t.block == 2048) &&
                       (int64_t)(un.unit + 1) * 2048 <= t.n;
     if (full) {
-      if (t.block == 0) {
-        if (p32) fv_unit_full<APEXW_F32, kM16>(t, e, un.tensor, un.unit, ws, c);
-        else fv_unit_full<APEXW_BF16, kM16>(t, e, un.tensor, un.unit, ws, c);
-      } else if (t.flags & APEXW_FLAG_M6) {
-        if (p32) fv_unit_full<APEXW_F32, kM6>(t, e, un.tensor, un.unit, ws, c);
-        else fv_unit_full<APEXW_BF16, kM6>(t, e, un.tensor, un.unit, ws, c);
-      } else {
-        if (p32) fv_unit_full<APEXW_F32, kM8>(t, e, un.tensor, un.unit, ws, c);
-        else fv_unit_full<APEXW_BF16, kM8>(t, e, un.tensor, un.unit, ws, c);
-      }
+      if (t.block == 0) fv_unit_full<PDK, kM16>(t, e, un.tensor, un.unit, ws, c);
+      else if (t.flags & APEXW_FLAG_M6) fv_unit_full<PDK, kM6>(t, e, un.tensor, un.unit, ws, c);
+      else fv_unit_full<PDK, kM8>(t, e, un.tensor, un.unit, ws, c);
       continue;
     }
-    if (t.block == 0) {
-      if (p32) fv_unit<APEXW_F32, kM16>(t, e, un.tensor, un.unit, ws, c);
-      else fv_unit<APEXW_BF16, kM16>(t, e, un.tensor, un.unit, ws, c);
-    } else if (t.flags & APEXW_FLAG_M6) {
-      if (p32) fv_unit<APEXW_F32, kM6>(t, e, un.tensor, un.unit, ws, c);
-      else fv_unit<APEXW_BF16, kM6>(t, e, un.tensor, un.unit, ws, c);
-    } else {
-      if (p32) fv_unit<APEXW_F32, kM8>(t, e, un.tensor, un.unit, ws, c);
-      else fv_unit<APEXW_BF16, kM8>(t, e, un.tensor, un.unit, ws, c);
-    }
+    if (t.block == 0) fv_unit<PDK, kM16>(t, e, un.tensor, un.unit, ws, c);
+    else if (t.flags & APEXW_FLAG_M6) fv_unit<PDK, kM6>(t, e, un.tensor, un.unit, ws, c);
+    else fv_unit<PDK, kM8>(t, e, un.tensor, un.unit, ws, c);
   }
 }
 
 }  // namespace
 
 int apexw_launch_factored(const apexw_tensor* tensors, const apexw_fv_tensor* fv, int32_t n_fv, int64_t n_bands,
-                          int64_t n_col_blocks, const apexw_unit* units, int64_t n_units, float* ws,
-                          const apexw_hparams* hp, hipStream_t stream) {
+                          int64_t n_col_blocks, const apexw_unit* units, int64_t n_units, int64_t n_bf16_units,
+                          float* ws, const apexw_hparams* hp, hipStream_t stream) {
   hipLaunchKernelGGL(fv_stats_kernel, dim3((unsigned)n_bands), dim3(256), 0, stream, tensors, fv, n_fv, ws, *hp);
   hipLaunchKernelGGL(fv_finalize_kernel, dim3((unsigned)(n_col_blocks + n_fv)), dim3(256), 0, stream, tensors, fv,
                      n_fv, n_col_blocks, ws, *hp);
-  if (n_units > 0) {
-    const int grid = apexw_resident_grid((const void*)fv_update_kernel, n_units);
-    hipLaunchKernelGGL(fv_update_kernel, dim3(grid), dim3(256), 0, stream, tensors, fv, n_fv, units, n_units, ws,
-                       *hp);
+  if (n_bf16_units > 0) {
+    const int g16 = apexw_resident_grid((const void*)fv_update_kernel<APEXW_BF16>, n_bf16_units);
+    hipLaunchKernelGGL(fv_update_kernel<APEXW_BF16>, dim3(g16), dim3(256), 0, stream, tensors, fv, n_fv, units,
+                       n_bf16_units, ws, *hp);
+  }
+  if (n_units > n_bf16_units) {
+    const int64_t n32 = n_units - n_bf16_units;
+    const int g32 = apexw_resident_grid((const void*)fv_update_kernel<APEXW_F32>, n32);
+    hipLaunchKernelGGL(fv_update_kernel<APEXW_F32>, dim3(g32), dim3(256), 0, stream, tensors, fv, n_fv,
+                       units + n_bf16_units, n32, ws, *hp);
   }
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }

@@ -224,13 +224,15 @@ int64_t apexw_factored_layout(apexw_fv_tensor* fv, int32_t n_fv, int64_t* n_band
  * One factored step of every tensor in fv (device array laid out by
  * apexw_factored_layout): statistics, finalisation, then the block update over
  * units (the factored tensors' units of the tensor table: one quantization
- * block each for quantized m, APEXW_COMPACT_UNIT elements for 16-bit m).
+ * block each for quantized m, APEXW_COMPACT_UNIT elements for 16-bit m).  The
+ * units of bf16-parameter tensors come first (n_bf16_units of them), then those
+ * of fp32-parameter tensors; each range runs on its own kernel.
  * workspace: the floats apexw_factored_layout returned.  hp as for the step
  * kernels (mode ignored); APEXW_HP_SR rounds the m codes stochastically.
  */
 int apexw_factored_step(const apexw_tensor* tensors, int32_t n_tensors, const apexw_fv_tensor* fv, int32_t n_fv,
                         int64_t n_bands, int64_t n_col_blocks, const apexw_unit* units, int64_t n_units,
-                        float* workspace, const apexw_hparams* hp, void* stream);
+                        int64_t n_bf16_units, float* workspace, const apexw_hparams* hp, void* stream);
 
 /*
  * Global-L2 clip coefficient over the grads of the table:

@@ -253,6 +253,7 @@ def test_factored_rows_and_launch(cpu_plans, prec):
     _, args, hp = calls[-1]
     fv = plan.fv["d_fv"].cpu().numpy().view(L.FV_TENSOR_DTYPE)
     assert list(fv["tensor"]) == sorted(fv["tensor"]) and args[3] == len(fv)
+    assert args[8] == plan.fv["n_units"]                     # every parameter here is bf16
     for row in fv:
         d = int(row["tensor"])
         assert fac[d] and int(row["rows"]) * int(row["cols"]) == int(table["n"][d])

@@ -270,3 +270,31 @@ def test_reference_compact_factored_threshold_and_convergence():
             assert opt.state[w]["is_factored_v"]
         return float(loss.item())
     assert run(True) < run(False) * 1.15 + 1e-4
+
+
+@pytest.mark.parametrize("prec", ["8bit", "compact"])
+def test_factored_with_centralization_and_clip_matches_oracle(prec):
+    """Grad centralization and the global-norm clip prepare the grads of factored
+    tensors as of any other (apexw/optimizer.py:204-258), beside an ordinary tensor."""
+    _need_gpu()
+    from apexw_amd import ApexW
+    from oracle.optim import OracleApexW
+    gen = torch.Generator().manual_seed(9)
+    shape = (1024, 512)
+    host = [(torch.randn(shape, generator=gen) * 0.02).bfloat16(), (torch.randn(4096, generator=gen) * 0.02).bfloat16()]
+    opts = dict(lr=1e-2, weight_decay=0.1, precision=prec, factored_v=True, stochastic_rounding=False,
+                grad_centralization=True, clip_grad_norm=0.5)
+    gps = [nn.Parameter(h.cuda()) for h in host]
+    cps = [nn.Parameter(h.clone()) for h in host]
+    gopt, copt = ApexW(gps, **opts), OracleApexW(cps, **opts)
+    for step in range(3):
+        gs = [(torch.randn(h.shape, generator=gen) * 1e-2).bfloat16() for h in host]
+        for gp, cp, g in zip(gps, cps, gs):
+            gp.grad, cp.grad = g.cuda(), g.clone()
+        prev = cps[0].detach().clone()
+        gopt.step()
+        copt.step()
+        torch.cuda.synchronize()
+        st_g, st_c = gopt.state[gps[0]], copt.state[cps[0]]
+        _check(gps[0], cps[0], prev, st_g, st_c, f"{prec} gc+clip step {step}")
+        _sync(gps[0], cps[0], st_g, st_c)

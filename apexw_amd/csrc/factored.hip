@@ -124,16 +124,40 @@ APEXW_DEV FvWs fv_ws(float* ws, const apexw_fv_tensor& e) {
 // band: the band's index within its tensor.  Writes the band's column partials,
 // applies the row EMA to its rows (exp_avg_sq_row) and leaves the band's sum of
 // the new row values in aux[band] for the row mean.
-template <int GD>
+// g^2 of one grad element.  PLAIN: no grad-dtype sanitize, clip or AMP unscale,
+// only the fp32 nan_to_num (NaN -> 0, +-inf -> +-65504), as selects.
+template <int GD, bool PLAIN> APEXW_DEV float fv_sq(float g, const FvCtx& c, bool fv_sanitize) {
+  if constexpr (PLAIN) {
+    const float sq = g * g;
+    if (!fv_sanitize) return sq;
+    return __builtin_isnan(g) ? 0.0f : (__builtin_isinf(g) ? 65504.0f * 65504.0f : sq);
+  } else {
+    const float x = fv_grad<GD>(g, c);
+    return x * x;
+  }
+}
+
+// band: the band's index within its tensor.  Writes the band's column partials,
+// applies the row EMA to its rows (exp_avg_sq_row) and leaves the band's sum of
+// the new row values in aux[band] for the row mean.
+//
+// A pass whose 32 x 2048 tile lies inside the tensor (and PLAIN) loads its rows
+// in batches (128 bytes per lane) and keeps the row partials in registers; other passes go row
+// by row and add each row's wave sum to the wave's LDS row slot.
+template <int GD, bool PLAIN>
 APEXW_DEV void fv_stats_band(const apexw_tensor& t, const apexw_fv_tensor& e, int64_t band, float* ws,
                              const FvCtx& c) {
   __shared__ float s_row[4][kBand];
   const FvWs w = fv_ws(ws, e);
   const apexw_hparams& hp = *c.hp;
+  const bool fs = hp.flags & APEXW_HP_FV_SANITIZE;
   const int64_t cols = e.cols;
   const int r0 = (int)(band * kBand);
   const int nr = min(kBand, e.rows - r0);
   const bool vec = !(t.flags & APEXW_FLAG_SCALAR) && (cols % 8) == 0;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if ((int)threadIdx.x < 4 * kBand) s_row[threadIdx.x / kBand][threadIdx.x % kBand] = 0.0f;
+  __syncthreads();
   float racc[kBand];
 #pragma unroll
   for (int i = 0; i < kBand; ++i) racc[i] = 0.0f;
@@ -143,38 +167,59 @@ APEXW_DEV void fv_stats_band(const apexw_tensor& t, const apexw_fv_tensor& e, in
     float cacc[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) cacc[j] = 0.0f;
+    if (PLAIN && vec && nr == kBand && c0 + kPass <= cols) {
+      constexpr int B = GD == APEXW_F32 ? 4 : 8;  // rows per batch: 128 bytes per lane
 #pragma unroll
-    for (int i = 0; i < kBand; ++i) {
-      if (i < nr && cnt > 0) {
-        const int64_t e0 = (int64_t)(r0 + i) * cols + cb;
-        float g[8];
-        if (vec && cnt == 8) {
-          load8<GD>(t.g, e0, g);
-        } else {
+      for (int i0 = 0; i0 < kBand; i0 += B) {
+        float g[B][8];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) g[j] = j < cnt ? load1<GD>(t.g, e0 + j) : 0.0f;
+        for (int i = 0; i < B; ++i) load8<GD>(t.g, (int64_t)(r0 + i0 + i) * cols + cb, g[i]);
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+          float rs = 0.0f;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float sq = fv_sq<GD, PLAIN>(g[i][j], c, fs);
+            cacc[j] = cacc[j] + sq;
+            rs = rs + sq;
+          }
+          racc[i0 + i] = racc[i0 + i] + rs;
         }
+      }
+    } else {
+#pragma unroll 1
+      for (int i = 0; i < nr; ++i) {
         float rs = 0.0f;
+        if (cnt > 0) {
+          const int64_t e0 = (int64_t)(r0 + i) * cols + cb;
+          float g[8];
+          if (vec && cnt == 8) {
+            load8<GD>(t.g, e0, g);
+          } else {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float x = j < cnt ? fv_grad<GD>(g[j], c) : 0.0f;
-          const float sq = x * x;
-          cacc[j] = cacc[j] + sq;
-          rs = rs + sq;
+            for (int j = 0; j < 8; ++j) g[j] = j < cnt ? load1<GD>(t.g, e0 + j) : 0.0f;
+          }
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float sq = j < cnt ? fv_sq<GD, PLAIN>(g[j], c, fs) : 0.0f;
+            cacc[j] = cacc[j] + sq;
+            rs = rs + sq;
+          }
         }
-        racc[i] = racc[i] + rs;
+        const float s = wave_sum(rs);
+        if (lane == 0) s_row[wave][i] += s;
       }
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j)
       if (j < cnt) w.part[band * cols + cb + j] = cacc[j];
   }
-  // rows: reduce each row partial across the workgroup, then the row EMA
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // rows: reduce the register row partials across each wave, then across the
+  // workgroup, then the row EMA
 #pragma unroll
   for (int i = 0; i < kBand; ++i) {
     const float s = wave_sum(racc[i]);
-    if (lane == 0) s_row[wave][i] = s;
+    if (lane == 0) s_row[wave][i] += s;
   }
   __syncthreads();
   if (wave == 0) {
@@ -203,8 +248,15 @@ __global__ __launch_bounds__(256) void fv_stats_kernel(const apexw_tensor* __res
   c.hp = &hp;
   c.coef = (hp.flags & APEXW_HP_CLIP) ? *hp.clip_coef : 1.0f;
   const int64_t lb = band - e.band0;
-  if (((t.flags >> APEXW_FLAG_GDT_SHIFT) & 3u) == APEXW_F32) fv_stats_band<APEXW_F32>(t, e, lb, ws, c);
-  else fv_stats_band<APEXW_BF16>(t, e, lb, ws, c);
+  const bool plain = !(hp.flags & (APEXW_HP_SANITIZE | APEXW_HP_CLIP | APEXW_HP_UNSCALE));
+  const bool f32 = ((t.flags >> APEXW_FLAG_GDT_SHIFT) & 3u) == APEXW_F32;
+  if (plain) {
+    if (f32) fv_stats_band<APEXW_F32, true>(t, e, lb, ws, c);
+    else fv_stats_band<APEXW_BF16, true>(t, e, lb, ws, c);
+  } else {
+    if (f32) fv_stats_band<APEXW_F32, false>(t, e, lb, ws, c);
+    else fv_stats_band<APEXW_BF16, false>(t, e, lb, ws, c);
+  }
 }
 
 // ---------------------------------------------------------------------------

@@ -13,7 +13,7 @@ import numpy as np
 
 from ._build import LIB_PATH
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 # dtype codes
 F32, BF16, F16, U8, I8 = 0, 1, 2, 3, 4

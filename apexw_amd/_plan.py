@@ -278,6 +278,8 @@ class StepPlan:
         row32 = np.array([p.dtype == torch.float32 for p in self.params], dtype=bool)[self.perm]
         p32 = row32[units["tensor"]]
         units = np.ascontiguousarray(np.concatenate([units[~p32], units[p32]]))
+        # the factored kernels address a unit's tensor through its fv entry (rows ascend)
+        units["tensor"] = np.searchsorted(fv["tensor"], units["tensor"]).astype(np.uint32)
         return dict(rows=rows, n=len(fv), d_fv=torch.from_numpy(fv.view(np.uint8)).to(self.device),
                     ws=torch.empty(max(ws, 1), dtype=torch.float32, device=self.device),
                     n_bands=nb.value, n_cb=ncb.value, n_units=len(units), n_bf16_units=int((~p32).sum()),

@@ -92,15 +92,6 @@ APEXW_DEV int fv_find_cb(const apexw_fv_tensor* fv, int n_fv, int64_t cb) {
   return lo;
 }
 
-APEXW_DEV int fv_find_tensor(const apexw_fv_tensor* fv, int n_fv, uint32_t tensor) {
-  int lo = 0, hi = n_fv - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (fv[mid].tensor <= tensor) lo = mid; else hi = mid - 1;
-  }
-  return lo;
-}
-
 // workspace of one tensor: aux = [n_bands] band sums of the new row EMA, then
 // the inverse row mean at aux[n_bands]; [n_bands x cols] column partials;
 // [cols] column square roots
@@ -487,6 +478,17 @@ APEXW_DEV void fv_unit(const apexw_tensor& t, const apexw_fv_tensor& e, uint32_t
   }
 }
 
+// SR noise for two elements from one xorshift32 step: the two 16-bit halves,
+// each as (h + 0.5) / 65536 - 0.5, uniform and symmetric on (-0.5, 0.5).
+APEXW_DEV void sr_pair(uint32_t& rs, float& n0, float& n1) {
+  rs ^= rs << 13;
+  rs ^= rs >> 17;
+  rs ^= rs << 5;
+  constexpr float k = 1.0f / 65536.0f, o = 0.5f / 65536.0f - 0.5f;
+  n0 = fmaf((float)(rs & 0xFFFFu), k, o);
+  n1 = fmaf((float)(rs >> 16), k, o);
+}
+
 // A whole 2048-element unit with 16-byte aligned buffers: every load of the wave
 // is issued before any arithmetic, m moves as 8-byte (INT8) / 6-byte (6-bit) /
 // 16-byte (bf16) vectors, and the row / column of each lane's first element
@@ -620,19 +622,24 @@ APEXW_DEV void fv_unit_full(const apexw_tensor& t, const apexw_fv_tensor& e, uin
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int64_t e0 = start + k * 512 + lane * 8;
+    float y[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) y[j] = div_refined(mnew[k][j], ms, rms);
+    if (sr) {
+      // SR noise: a per-lane xorshift32 stream seeded from the element index
+      uint32_t rs = rng_at(key, (uint32_t)e0) | 1u;
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) {
+        float n0, n1;
+        sr_pair(rs, n0, n1);
+        y[j] = y[j] + n0;
+        y[j + 1] = y[j + 1] + n1;
+      }
+    }
     uint32_t q[8];
-    // SR noise: a per-lane xorshift32 stream seeded from the element index
-    uint32_t rs = rng_at(key, (uint32_t)e0) | 1u;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      float y = div_refined(mnew[k][j], ms, rms);
-      if (sr) {
-        rs ^= rs << 13;
-        rs ^= rs >> 17;
-        rs ^= rs << 5;
-        y = y + (unit_uniform(rs >> 16) - 0.5f);
-      }
-      const int32_t qi = (int32_t)fminf(fmaxf(rintf(y), -lim), lim);
+      const int32_t qi = (int32_t)fminf(fmaxf(rintf(y[j]), -lim), lim);
       q[j] = MK == kM8 ? ((uint32_t)qi & 0xFFu) : (uint32_t)(qi + 31);
     }
     if constexpr (MK == kM8) {
@@ -649,6 +656,165 @@ APEXW_DEV void fv_unit_full(const apexw_tensor& t, const apexw_fv_tensor& e, uin
   }
 }
 
+// A whole unit inside one row of the matrix, for the common case: finite grads,
+// no grad-dtype sanitize / clip / AMP unscale, a lerp weight below 0.5 and
+// cols % 4 == 0.  The row factor is one value for the unit and the column roots
+// are 16-byte loads; the division is the refined one of fv_unit.  Returns false,
+// before any store, when the unit does not qualify (it crosses a row, or a grad
+// is not finite): the caller then runs fv_unit_full on it.
+template <int PD, int MK>
+APEXW_DEV bool fv_unit_row(const apexw_tensor& t, const apexw_fv_tensor& e, uint32_t tix, uint32_t unit,
+                           float* ws, const FvCtx& c) {
+  constexpr int W = PD == APEXW_F32 ? 2 : 1;  // 16-byte words per 8 elements of p / g
+  const apexw_hparams& hp = *c.hp;
+  const int64_t start = (int64_t)unit * 2048;
+  const int64_t cols = e.cols;
+  const int64_t row = start / cols;
+  const uint32_t col0 = (uint32_t)(start - row * cols);
+  if ((int64_t)col0 + 2048 > cols) return false;
+  const FvWs w = fv_ws(ws, e);
+  const int lane = lane_id();
+  const bool sr = hp.flags & APEXW_HP_SR;
+  const bool wd = t.flags & APEXW_FLAG_WD;
+  const float ms_old = MK == kM16 ? 0.0f : t.m_scale[unit];
+  // ---- loads
+  u32x4 praw[4][W], graw[4][W];
+  u32x4 mw16[MK == kM16 ? 4 : 1];
+  u32x2 mw8[MK == kM16 ? 1 : 4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int64_t e0 = start + k * 512 + lane * 8;
+    const auto pp = APEXW_GLOBAL(const u32x4, (const uint8_t*)t.p + e0 * (PD == APEXW_F32 ? 4 : 2));
+    const auto gp = APEXW_GLOBAL(const u32x4, (const uint8_t*)t.g + e0 * (PD == APEXW_F32 ? 4 : 2));
+#pragma unroll
+    for (int i = 0; i < W; ++i) {
+      praw[k][i] = __builtin_nontemporal_load(pp + i);
+      graw[k][i] = __builtin_nontemporal_load(gp + i);
+    }
+    if constexpr (MK == kM16) {
+      mw16[k] = __builtin_nontemporal_load(APEXW_GLOBAL(const u32x4, (const uint16_t*)t.m + e0));
+    } else if constexpr (MK == kM8) {
+      mw8[k] = __builtin_nontemporal_load(APEXW_GLOBAL(const u32x2, (const int8_t*)t.m + e0));
+    } else {
+      const auto mp = APEXW_GLOBAL(const uint16_t, (const uint8_t*)t.m + (e0 >> 2) * 3);
+      const uint32_t h0 = mp[0], h1 = mp[1], h2 = mp[2];
+      mw8[k] = u32x2{h0 | ((h1 & 0xFFu) << 16), (h1 >> 8) | (h2 << 8)};
+    }
+  }
+  const float rv = sqrtf(((const float*)t.v)[row] * w.aux[(e.rows + kBand - 1) / kBand]);
+  // ---- grads, and the finiteness check (g * 0 is NaN exactly for inf / NaN)
+  float g[4][8];
+  float chk = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t* gw = (const uint32_t*)&graw[k][0];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      g[k][j] = PD == APEXW_F32 ? __uint_as_float(gw[j])
+                                : (j & 1 ? __uint_as_float(gw[j >> 1] & 0xFFFF0000u) : __uint_as_float(gw[j >> 1] << 16));
+      chk = fmaf(g[k][j], 0.0f, chk);
+    }
+  }
+  if (__builtin_amdgcn_ballot_w64(!(chk == 0.0f)) != 0) return false;
+  // ---- update
+  float mnew[MK == kM16 ? 1 : 4][8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int64_t e0 = start + k * 512 + lane * 8;
+    const uint32_t* pw = (const uint32_t*)&praw[k][0];
+    float p[8], m[8], cs[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      p[j] = PD == APEXW_F32 ? __uint_as_float(pw[j])
+                             : (j & 1 ? __uint_as_float(pw[j >> 1] & 0xFFFF0000u) : __uint_as_float(pw[j >> 1] << 16));
+    if constexpr (MK == kM16) {
+      const uint32_t* mw = (const uint32_t*)&mw16[k];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        m[j] = j & 1 ? __uint_as_float(mw[j >> 1] & 0xFFFF0000u) : __uint_as_float(mw[j >> 1] << 16);
+    } else if constexpr (MK == kM8) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        m[j] = (float)(int8_t)(((j < 4 ? mw8[k].x : mw8[k].y) >> (8 * (j & 3))) & 0xFFu) * ms_old;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        m[j] = ((float)(((j < 4 ? mw8[k].x : mw8[k].y) >> (6 * (j & 3))) & 63u) - 31.0f) * ms_old;
+    }
+    {
+      const float* cp = w.col + col0 + k * 512 + lane * 8;
+      const float4 a = *(const float4*)cp, b = *(const float4*)(cp + 4);
+      cs[0] = a.x; cs[1] = a.y; cs[2] = a.z; cs[3] = a.w; cs[4] = b.x; cs[5] = b.y; cs[6] = b.z; cs[7] = b.w;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      m[j] = fmaf(hp.lerp_coef, g[k][j] - m[j], m[j]);
+      const float den = fmaxf(rv * cs[j] + hp.eps_scaled, hp.eps);
+      const float upd = div_refined(m[j], den, rcp_refined(den)) * hp.step_size;
+      if constexpr (PD == APEXW_F32) {
+        p[j] = (wd ? p[j] * hp.wd_factor : p[j]) - upd;
+      } else {
+        const float pd = wd ? rnd<PD>(p[j] * hp.wd_factor) : p[j];
+        p[j] = rnd<PD>(pd - rnd<PD>(upd));
+      }
+      if constexpr (MK != kM16) {
+        mnew[k][j] = m[j];
+        amax = fmaxf(amax, fabsf(m[j]));
+      }
+    }
+    store8<PD>(t.p, e0, p);
+    if constexpr (MK == kM16) store8<APEXW_BF16>(t.m, e0, m);
+  }
+  if constexpr (MK == kM16) {
+    return true;
+  } else {
+    // ---- requantize m
+    amax = wave_max(amax);
+    constexpr float lim = MK == kM8 ? 127.0f : 31.0f;
+    float ms = fmaxf(amax, 1e-12f) / lim;
+    ms = fmaxf(ms, ms_old * 0.9f);
+    if (lane == 0) t.m_scale[unit] = ms;
+    const float rms = rcp_refined(ms);
+    const uint32_t key = rng_key(hp.seed, tix, hp.step, 3u, (uint32_t)(start >> 32));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int64_t e0 = start + k * 512 + lane * 8;
+      float y[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) y[j] = div_refined(mnew[k][j], ms, rms);
+      if (sr) {
+        uint32_t rs = rng_at(key, (uint32_t)e0) | 1u;
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+          float n0, n1;
+          sr_pair(rs, n0, n1);
+          y[j] = y[j] + n0;
+          y[j + 1] = y[j + 1] + n1;
+        }
+      }
+      uint32_t q[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int32_t qi = (int32_t)fminf(fmaxf(rintf(y[j]), -lim), lim);
+        q[j] = MK == kM8 ? ((uint32_t)qi & 0xFFu) : (uint32_t)(qi + 31);
+      }
+      if constexpr (MK == kM8) {
+        const u32x2 v = {q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24), q[4] | (q[5] << 8) | (q[6] << 16) | (q[7] << 24)};
+        __builtin_nontemporal_store(v, APEXW_GLOBAL(u32x2, (int8_t*)t.m + e0));
+      } else {
+        const uint32_t w0 = q[0] | (q[1] << 6) | (q[2] << 12) | (q[3] << 18);
+        const uint32_t w1 = q[4] | (q[5] << 6) | (q[6] << 12) | (q[7] << 18);
+        const auto mp = APEXW_GLOBAL(uint16_t, (uint8_t*)t.m + (e0 >> 2) * 3);
+        mp[0] = (uint16_t)(w0 & 0xFFFFu);
+        mp[1] = (uint16_t)((w0 >> 16) | ((w1 & 0xFFu) << 8));
+        mp[2] = (uint16_t)(w1 >> 8);
+      }
+    }
+    return true;
+  }
+}
+
 // One kernel per parameter dtype, each over its own range of units: the fp32
 // variant's larger register footprint does not lower the bf16 variant's occupancy.
 template <int PDK>
@@ -661,24 +827,36 @@ __global__ __launch_bounds__(256) void fv_update_kernel(const apexw_tensor* __re
   c.coef = (hp.flags & APEXW_HP_CLIP) ? *hp.clip_coef : 1.0f;
   const uint32_t wave = uniform(threadIdx.x >> 6);
   const int64_t stride = (int64_t)gridDim.x * 4;
-  for (int64_t u = (int64_t)blockIdx.x * 4 + wave; u < n_units; u += stride) {
-    const apexw_unit un = units[u];
-    const apexw_tensor& t = tensors[un.tensor];
-    const apexw_fv_tensor& e = fv[fv_find_tensor(fv, n_fv, un.tensor)];
-    if (e.tensor != un.tensor || !(t.flags & APEXW_FLAG_FACTORED)) continue;  // never taken for a valid plan
+  const bool row_ok = !(hp.flags & (APEXW_HP_SANITIZE | APEXW_HP_CLIP | APEXW_HP_UNSCALE | APEXW_HP_LERP_HI));
+  int64_t u = (int64_t)blockIdx.x * 4 + wave;
+  // the next unit's descriptor is requested while this unit is processed
+  apexw_unit next = u < n_units ? units[u] : apexw_unit{0u, 0u};
+  for (; u < n_units; u += stride) {
+    const apexw_unit un = next;
+    if (u + stride < n_units) next = units[u + stride];
+    if (un.tensor >= (uint32_t)n_fv) continue;  // never taken for a valid plan
+    const apexw_fv_tensor& e = fv[un.tensor];
+    const apexw_tensor& t = tensors[e.tensor];
+    if (!(t.flags & APEXW_FLAG_FACTORED)) continue;  // never taken for a valid plan
     const bool p32 = ((t.flags >> APEXW_FLAG_PDT_SHIFT) & 3u) == APEXW_F32;
     if (p32 != (PDK == APEXW_F32)) continue;
     const bool full = !(t.flags & APEXW_FLAG_SCALAR) && (t.block == 0 || t.block == 2048) &&
                       (int64_t)(un.unit + 1) * 2048 <= t.n;
     if (full) {
-      if (t.block == 0) fv_unit_full<PDK, kM16>(t, e, un.tensor, un.unit, ws, c);
-      else if (t.flags & APEXW_FLAG_M6) fv_unit_full<PDK, kM6>(t, e, un.tensor, un.unit, ws, c);
-      else fv_unit_full<PDK, kM8>(t, e, un.tensor, un.unit, ws, c);
+      if (row_ok && (e.cols & 3) == 0) {
+        const bool done = t.block == 0 ? fv_unit_row<PDK, kM16>(t, e, e.tensor, un.unit, ws, c)
+                          : (t.flags & APEXW_FLAG_M6) ? fv_unit_row<PDK, kM6>(t, e, e.tensor, un.unit, ws, c)
+                                                      : fv_unit_row<PDK, kM8>(t, e, e.tensor, un.unit, ws, c);
+        if (done) continue;
+      }
+      if (t.block == 0) fv_unit_full<PDK, kM16>(t, e, e.tensor, un.unit, ws, c);
+      else if (t.flags & APEXW_FLAG_M6) fv_unit_full<PDK, kM6>(t, e, e.tensor, un.unit, ws, c);
+      else fv_unit_full<PDK, kM8>(t, e, e.tensor, un.unit, ws, c);
       continue;
     }
-    if (t.block == 0) fv_unit<PDK, kM16>(t, e, un.tensor, un.unit, ws, c);
-    else if (t.flags & APEXW_FLAG_M6) fv_unit<PDK, kM6>(t, e, un.tensor, un.unit, ws, c);
-    else fv_unit<PDK, kM8>(t, e, un.tensor, un.unit, ws, c);
+    if (t.block == 0) fv_unit<PDK, kM16>(t, e, e.tensor, un.unit, ws, c);
+    else if (t.flags & APEXW_FLAG_M6) fv_unit<PDK, kM6>(t, e, e.tensor, un.unit, ws, c);
+    else fv_unit<PDK, kM8>(t, e, e.tensor, un.unit, ws, c);
   }
 }
 

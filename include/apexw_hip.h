@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define APEXW_ABI_VERSION 8
+#define APEXW_ABI_VERSION 9
 
 /* status codes */
 enum apexw_status {
@@ -223,8 +223,9 @@ int64_t apexw_factored_layout(apexw_fv_tensor* fv, int32_t n_fv, int64_t* n_band
 /*
  * One factored step of every tensor in fv (device array laid out by
  * apexw_factored_layout): statistics, finalisation, then the block update over
- * units (the factored tensors' units of the tensor table: one quantization
- * block each for quantized m, APEXW_COMPACT_UNIT elements for 16-bit m).  The
+ * units (one quantization block each for quantized m, APEXW_COMPACT_UNIT
+ * elements for 16-bit m; a unit's `tensor` field is the index of its entry in
+ * fv, not a row of the tensor table, so no lookup precedes its loads).  The
  * units of bf16-parameter tensors come first (n_bf16_units of them), then those
  * of fp32-parameter tensors; each range runs on its own kernel.
  * workspace: the floats apexw_factored_layout returned.  hp as for the step

@@ -259,6 +259,8 @@ def test_factored_rows_and_launch(cpu_plans, prec):
         assert fac[d] and int(row["rows"]) * int(row["cols"]) == int(table["n"][d])
         assert int(row["flags"]) == (L.FV_SUM_COLS if int(table["n"][d]) > 262144 else 0)
     units = plan.fv["d_units"].cpu().numpy().view(L.UNIT_DTYPE)
-    assert set(units["tensor"].tolist()) == set(fv["tensor"].tolist())
+    assert set(units["tensor"].tolist()) == set(range(len(fv)))    # units name their fv entry
+    for k in range(len(fv)):
+        assert (units["tensor"] == k).sum() == plan.unit_counts[int(fv[k]["tensor"])]
     assert hp["step"] == 2 and hp["flags"] & L.HP_FV_SANITIZE == (L.HP_FV_SANITIZE if prec == "8bit" else 0)
     assert hp["eps"] == pytest.approx(1e-8) and hp["mode"] == L.MODE_COLD

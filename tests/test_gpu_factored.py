@@ -77,6 +77,11 @@ CASES = [
     ("8bit 6-bit m, partial last block", "8bit", (1030, 515), {"six_bit": True}),
     ("compact bf16 m", "compact", (1024, 512), {}),
     ("compact bf16 m, ragged", "compact", (1025, 515), {}),
+    # rows of 2048+ columns: units inside one row take the single-row update
+    ("8bit int8 m, wide rows", "8bit", (128, 4096), {}),
+    ("8bit 6-bit m, wide rows", "8bit", (128, 6144), {"six_bit": True}),
+    ("8bit int8 m, 3000-col rows", "8bit", (200, 3000), {}),      # units inside and across rows
+    ("compact bf16 m, 3000-col rows", "compact", (256, 3000), {}),
 ]
 
 
@@ -298,3 +303,32 @@ def test_factored_with_centralization_and_clip_matches_oracle(prec):
         st_g, st_c = gopt.state[gps[0]], copt.state[cps[0]]
         _check(gps[0], cps[0], prev, st_g, st_c, f"{prec} gc+clip step {step}")
         _sync(gps[0], cps[0], st_g, st_c)
+
+
+@pytest.mark.parametrize("six", [False, True])
+def test_factored_m_code_sr_unbiased(six):
+    """First step from zero state: m = (1 - b1) g exactly, so the codes must be
+    floor or ceil of m / scale, with a mean rounding error within 3 standard
+    errors of zero (10.5 M elements, one row per 2048-element unit)."""
+    _need_gpu()
+    from apexw_amd import ApexW
+    torch.manual_seed(2)
+    shape = (5120, 2048)
+    g = (torch.randn(shape) * 1e-3).bfloat16()
+    p = nn.Parameter(torch.zeros(shape, dtype=torch.bfloat16, device="cuda"))
+    p.grad = g.cuda()
+    opt = ApexW([p], lr=1e-3, weight_decay=0.0, precision="8bit", factored_v=True, six_bit=six,
+                stochastic_rounding=True)
+    opt.step()
+    st = opt.state[p]
+    assert st["is_factored_v"] and bool(st.get("is_6bit_m", False)) == six
+    m_exact = torch.tensor(np.float32(1 - 0.9)) * g.float().reshape(-1)   # lerp from zero: fma(w, g - 0, 0)
+    ms = st["exp_avg_scales"].cpu().reshape(-1)
+    codes = (_codes6(st["exp_avg"].cpu()) - 31).float() if six else st["exp_avg"].cpu().reshape(-1).float()
+    codes = codes[:m_exact.numel()]
+    x = (m_exact.view(ms.numel(), -1) / ms[:, None]).reshape(-1)
+    lo = torch.floor(x)
+    assert bool(((codes == lo) | (codes == lo + 1)).all()), "SR code is not floor or ceil of m / scale"
+    err = codes - x
+    mean, se = float(err.double().mean()), float(err.double().std()) / err.numel() ** 0.5
+    assert abs(mean) < 3 * se, f"factored m SR: mean {mean:.3e} vs 3*se {3 * se:.3e}"

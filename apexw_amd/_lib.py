@@ -13,7 +13,7 @@ import numpy as np
 
 from ._build import LIB_PATH
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 # dtype codes
 F32, BF16, F16, U8, I8 = 0, 1, 2, 3, 4
@@ -90,6 +90,7 @@ FV_TENSOR_DTYPE = np.dtype([("tensor", np.uint32), ("rows", np.int32), ("cols", 
 assert FV_TENSOR_DTYPE.itemsize == 32
 FV_SUM_COLS = 1
 FV_BAND_ROWS = 32
+FV_UNIT_RANGES = 6   # (bf16, fp32 parameters) x (INT8, 6-bit, bf16 m)
 
 GEMM_SYM, GEMM_B_KN, GEMM_ADD_B = 1, 2, 4
 GEMM_OUT_C, GEMM_OUT_CT, GEMM_ADD, GEMM_KIND_NN = 1, 2, 4, 8
@@ -121,7 +122,7 @@ SIGNATURES = {
     "apexw_muon_apply": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _i64, _i32, _f32, _i32, _f32, _vp]),
     "apexw_factored_layout": (ctypes.c_int64, [_vp, _i32, ctypes.POINTER(ctypes.c_int64),
                                                ctypes.POINTER(ctypes.c_int64)]),
-    "apexw_factored_step": (ctypes.c_int, [_vp, _i32, _vp, _i32, _i64, _i64, _vp, _i64, _i64, _vp, _HP, _vp]),
+    "apexw_factored_step": (ctypes.c_int, [_vp, _i32, _vp, _i32, _i64, _i64, _vp, _i64, _vp, _vp, _HP, _vp]),
 }
 
 GEMM_TILE = 256

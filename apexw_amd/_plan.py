@@ -274,15 +274,19 @@ class StepPlan:
             L.check(-ws, "apexw_factored_layout")
         sel = np.isin(self._host_units["tensor"], np.array(rows, dtype=np.uint32))
         units = self._host_units[sel]
-        # bf16-parameter tensors' units first: each parameter dtype runs on its own kernel
-        row32 = np.array([p.dtype == torch.float32 for p in self.params], dtype=bool)[self.perm]
-        p32 = row32[units["tensor"]]
-        units = np.ascontiguousarray(np.concatenate([units[~p32], units[p32]]))
+        # units grouped by (parameter dtype, m kind): each group runs on its own kernel
+        tab = self.host_table[self.perm]
+        p32 = ((tab["flags"] >> L.PDT_SHIFT) & 3) == L.F32
+        mk = np.where(tab["block"] == 0, 2, np.where(tab["flags"] & L.FLAG_M6, 1, 0))
+        group = (p32.astype(np.int64) * 3 + mk)[units["tensor"]]
+        order = np.argsort(group, kind="stable")
+        units = np.ascontiguousarray(units[order])
+        ends = np.cumsum(np.bincount(group, minlength=L.FV_UNIT_RANGES)).astype(np.int64)
         # the factored kernels address a unit's tensor through its fv entry (rows ascend)
         units["tensor"] = np.searchsorted(fv["tensor"], units["tensor"]).astype(np.uint32)
         return dict(rows=rows, n=len(fv), d_fv=torch.from_numpy(fv.view(np.uint8)).to(self.device),
                     ws=torch.empty(max(ws, 1), dtype=torch.float32, device=self.device),
-                    n_bands=nb.value, n_cb=ncb.value, n_units=len(units), n_bf16_units=int((~p32).sum()),
+                    n_bands=nb.value, n_cb=ncb.value, n_units=len(units), range_ends=ends,
                     d_units=torch.from_numpy(units.view(np.uint8)).to(self.device) if len(units) else None)
 
     def _refresh_grads(self):
@@ -460,7 +464,7 @@ class StepPlan:
             st = self._lib.apexw_factored_step(
                 self.d_table.data_ptr(), len(self.params), fv["d_fv"].data_ptr(), fv["n"], fv["n_bands"],
                 fv["n_cb"], fv["d_units"].data_ptr() if fv["d_units"] is not None else None, fv["n_units"],
-                fv["n_bf16_units"], fv["ws"].data_ptr(), ctypes_ref(hp), stream)
+                fv["range_ends"].ctypes.data, fv["ws"].data_ptr(), ctypes_ref(hp), stream)
             L.check(st, "apexw_factored_step")
 
     def _split_by_step(self):

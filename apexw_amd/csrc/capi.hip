@@ -32,7 +32,7 @@ int apexw_launch_muon_apply(void*, int32_t, const uint16_t*, int64_t, int64_t, i
                             float, hipStream_t);
 bool apexw_q8_flags_ok(uint32_t flags, uint32_t block, int64_t n);
 int apexw_launch_factored(const apexw_tensor*, const apexw_fv_tensor*, int32_t, int64_t, int64_t, const apexw_unit*,
-                          int64_t, int64_t, float*, const apexw_hparams*, hipStream_t);
+                          const int64_t*, float*, const apexw_hparams*, hipStream_t);
 
 namespace {
 
@@ -183,12 +183,18 @@ int64_t apexw_factored_layout(apexw_fv_tensor* fv, int32_t n_fv, int64_t* n_band
 
 int apexw_factored_step(const apexw_tensor* tensors, int32_t n_tensors, const apexw_fv_tensor* fv, int32_t n_fv,
                         int64_t n_bands, int64_t n_col_blocks, const apexw_unit* units, int64_t n_units,
-                        int64_t n_bf16_units, float* workspace, const apexw_hparams* hp, void* stream) {
+                        const int64_t* range_ends, float* workspace, const apexw_hparams* hp, void* stream) {
   if (!tensors || !fv || !workspace || n_tensors <= 0 || n_fv <= 0 || n_fv > n_tensors || !hp_ok(hp)) return APEXW_ERR_ARG;
   if (n_bands < n_fv || n_bands > INT32_MAX || n_col_blocks < n_fv || n_col_blocks + n_fv > INT32_MAX) return APEXW_ERR_ARG;
-  if (n_units < 0 || (n_units > 0 && !units) || n_bf16_units < 0 || n_bf16_units > n_units) return APEXW_ERR_ARG;
+  if (n_units < 0 || (n_units > 0 && !units) || !range_ends) return APEXW_ERR_ARG;
+  int64_t prev = 0;
+  for (int r = 0; r < APEXW_FV_UNIT_RANGES; ++r) {
+    if (range_ends[r] < prev || range_ends[r] > n_units) return APEXW_ERR_ARG;
+    prev = range_ends[r];
+  }
+  if (prev != n_units) return APEXW_ERR_ARG;
   if (hp->mode == APEXW_MODE_SINGLE || hp->mode == APEXW_MODE_NATIVE) return APEXW_ERR_ARG;
-  return apexw_launch_factored(tensors, fv, n_fv, n_bands, n_col_blocks, units, n_units, n_bf16_units, workspace, hp,
+  return apexw_launch_factored(tensors, fv, n_fv, n_bands, n_col_blocks, units, range_ends, workspace, hp,
                                (hipStream_t)stream);
 }
 

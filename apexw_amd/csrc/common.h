@@ -30,6 +30,11 @@ APEXW_DEV uint32_t f32_to_bf16_bits(float x) {
   __bf16 b = (__bf16)x;  // round to nearest even
   return (uint32_t)__builtin_bit_cast(uint16_t, b);
 }
+// Two fp32 values rounded to nearest-even bf16, packed (a in the low half).
+APEXW_DEV uint32_t pack_bf16x2(float a, float b) {
+  typedef __attribute__((ext_vector_type(2))) float f32x2;
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
+}
 APEXW_DEV float f16_bits_to_f32(uint32_t h) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }

@@ -409,6 +409,7 @@ APEXW_DEV void fv_unit(const apexw_tensor& t, const apexw_fv_tensor& e, uint32_t
         }
         mnew[k][j] = m[j];
         amax = fmaxf(amax, fabsf(m[j]));
+        if constexpr (MK == kM16) m[j] = rnd<APEXW_BF16>(m[j]);  // m.copy_(mf.to(bf16)): nearest-even
         if (++col == cols) {
           col = 0;
           ++row;
@@ -607,6 +608,7 @@ APEXW_DEV void fv_unit_full(const apexw_tensor& t, const apexw_fv_tensor& e, uin
       }
       mnew[k][j] = m[j];
       amax = fmaxf(amax, fabsf(m[j]));
+      if constexpr (MK == kM16) m[j] = rnd<APEXW_BF16>(m[j]);  // m.copy_(mf.to(bf16)): nearest-even
     }
     store8<PD>(t.p, e0, p);
     if constexpr (MK == kM16) store8<APEXW_BF16>(t.m, e0, m);
@@ -656,12 +658,12 @@ APEXW_DEV void fv_unit_full(const apexw_tensor& t, const apexw_fv_tensor& e, uin
   }
 }
 
-// A whole unit inside one row of the matrix, for the common case: finite grads,
-// no grad-dtype sanitize / clip / AMP unscale, a lerp weight below 0.5 and
+// A whole unit inside one row of the matrix, for the common case: no grad-dtype
+// sanitize / clip / AMP unscale, a lerp weight below 0.5 and
 // cols % 4 == 0.  The row factor is one value for the unit and the column roots
-// are 16-byte loads; the division is the refined one of fv_unit.  Returns false,
-// before any store, when the unit does not qualify (it crosses a row, or a grad
-// is not finite): the caller then runs fv_unit_full on it.
+// are 16-byte loads; the update's division is the refined one of fv_unit, and
+// bf16 roundings convert pairs.  Returns false, before any load, when the unit
+// crosses a row: the caller then runs fv_unit_full on it.
 template <int PD, int MK>
 APEXW_DEV bool fv_unit_row(const apexw_tensor& t, const apexw_fv_tensor& e, uint32_t tix, uint32_t unit,
                            float* ws, const FvCtx& c) {
@@ -701,8 +703,9 @@ APEXW_DEV bool fv_unit_row(const apexw_tensor& t, const apexw_fv_tensor& e, uint
       mw8[k] = u32x2{h0 | ((h1 & 0xFFu) << 16), (h1 >> 8) | (h2 << 8)};
     }
   }
-  const float rv = sqrtf(((const float*)t.v)[row] * w.aux[(e.rows + kBand - 1) / kBand]);
-  // ---- grads, and the finiteness check (g * 0 is NaN exactly for inf / NaN)
+  const float rv = sqrtf(APEXW_GLOBAL(const float, t.v)[row] * APEXW_GLOBAL(const float, w.aux)[(e.rows + kBand - 1) / kBand]);
+  // ---- grads; a non-finite grad (g * 0 is NaN exactly for inf / NaN) takes
+  // the nan_to_num of _prep_grad_chunk_fp32 in registers (rare, wave-uniform branch)
   float g[4][8];
   float chk = 0.0f;
 #pragma unroll
@@ -715,7 +718,15 @@ APEXW_DEV bool fv_unit_row(const apexw_tensor& t, const apexw_fv_tensor& e, uint
       chk = fmaf(g[k][j], 0.0f, chk);
     }
   }
-  if (__builtin_amdgcn_ballot_w64(!(chk == 0.0f)) != 0) return false;
+  if ((hp.flags & APEXW_HP_FV_SANITIZE) && __builtin_amdgcn_ballot_w64(!(chk == 0.0f)) != 0) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float x = g[k][j];
+        g[k][j] = __builtin_isnan(x) ? 0.0f : (__builtin_isinf(x) ? (x > 0.0f ? 65504.0f : -65504.0f) : x);
+      }
+  }
   // ---- update
   float mnew[MK == kM16 ? 1 : 4][8];
   float amax = 0.0f;
@@ -743,28 +754,49 @@ APEXW_DEV bool fv_unit_row(const apexw_tensor& t, const apexw_fv_tensor& e, uint
         m[j] = ((float)(((j < 4 ? mw8[k].x : mw8[k].y) >> (6 * (j & 3))) & 63u) - 31.0f) * ms_old;
     }
     {
-      const float* cp = w.col + col0 + k * 512 + lane * 8;
-      const float4 a = *(const float4*)cp, b = *(const float4*)(cp + 4);
-      cs[0] = a.x; cs[1] = a.y; cs[2] = a.z; cs[3] = a.w; cs[4] = b.x; cs[5] = b.y; cs[6] = b.z; cs[7] = b.w;
+      const auto cp = APEXW_GLOBAL(const u32x4, w.col + col0 + k * 512 + lane * 8);
+      const u32x4 a = cp[0], b = cp[1];
+      cs[0] = __uint_as_float(a.x); cs[1] = __uint_as_float(a.y); cs[2] = __uint_as_float(a.z);
+      cs[3] = __uint_as_float(a.w); cs[4] = __uint_as_float(b.x); cs[5] = __uint_as_float(b.y);
+      cs[6] = __uint_as_float(b.z); cs[7] = __uint_as_float(b.w);
     }
+    float upd[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       m[j] = fmaf(hp.lerp_coef, g[k][j] - m[j], m[j]);
       const float den = fmaxf(rv * cs[j] + hp.eps_scaled, hp.eps);
-      const float upd = div_refined(m[j], den, rcp_refined(den)) * hp.step_size;
-      if constexpr (PD == APEXW_F32) {
-        p[j] = (wd ? p[j] * hp.wd_factor : p[j]) - upd;
-      } else {
-        const float pd = wd ? rnd<PD>(p[j] * hp.wd_factor) : p[j];
-        p[j] = rnd<PD>(pd - rnd<PD>(upd));
-      }
+      upd[j] = div_refined(m[j], den, rcp_refined(den)) * hp.step_size;
       if constexpr (MK != kM16) {
         mnew[k][j] = m[j];
         amax = fmaxf(amax, fabsf(m[j]));
       }
     }
-    store8<PD>(t.p, e0, p);
-    if constexpr (MK == kM16) store8<APEXW_BF16>(t.m, e0, m);
+    const auto pp = APEXW_GLOBAL(u32x4, (uint8_t*)t.p + e0 * (PD == APEXW_F32 ? 4 : 2));
+    if constexpr (PD == APEXW_F32) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) p[j] = (wd ? p[j] * hp.wd_factor : p[j]) - upd[j];
+      __builtin_nontemporal_store(u32x4{__float_as_uint(p[0]), __float_as_uint(p[1]), __float_as_uint(p[2]),
+                                        __float_as_uint(p[3])}, pp);
+      __builtin_nontemporal_store(u32x4{__float_as_uint(p[4]), __float_as_uint(p[5]), __float_as_uint(p[6]),
+                                        __float_as_uint(p[7])}, pp + 1);
+    } else {
+      // pairs: rnd(rnd(p * wd) - rnd(upd)), each rounding one packed conversion
+      uint32_t out[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t pdw = wd ? pack_bf16x2(p[2 * i] * hp.wd_factor, p[2 * i + 1] * hp.wd_factor) : pw[i];
+        const uint32_t uw = pack_bf16x2(upd[2 * i], upd[2 * i + 1]);
+        out[i] = pack_bf16x2(__uint_as_float(pdw << 16) - __uint_as_float(uw << 16),
+                             __uint_as_float(pdw & 0xFFFF0000u) - __uint_as_float(uw & 0xFFFF0000u));
+      }
+      __builtin_nontemporal_store(u32x4{out[0], out[1], out[2], out[3]}, pp);
+    }
+    if constexpr (MK == kM16) {
+      // m.copy_(mf.to(bf16)): nearest-even
+      const u32x4 mv = {pack_bf16x2(m[0], m[1]), pack_bf16x2(m[2], m[3]), pack_bf16x2(m[4], m[5]),
+                        pack_bf16x2(m[6], m[7])};
+      __builtin_nontemporal_store(mv, APEXW_GLOBAL(u32x4, (uint16_t*)t.m + e0));
+    }
   }
   if constexpr (MK == kM16) {
     return true;
@@ -781,22 +813,27 @@ APEXW_DEV bool fv_unit_row(const apexw_tensor& t, const apexw_fv_tensor& e, uint
     for (int k = 0; k < 4; ++k) {
       const int64_t e0 = start + k * 512 + lane * 8;
       float y[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) y[j] = div_refined(mnew[k][j], ms, rms);
       if (sr) {
+        // floor(m / scale + u), u = (h + 0.5) / 65536 from 16 random bits h: the
+        // quotient as one product (the noise makes its last-ulp rounding immaterial)
         uint32_t rs = rng_at(key, (uint32_t)e0) | 1u;
 #pragma unroll
         for (int j = 0; j < 8; j += 2) {
-          float n0, n1;
-          sr_pair(rs, n0, n1);
-          y[j] = y[j] + n0;
-          y[j + 1] = y[j + 1] + n1;
+          rs ^= rs << 13;
+          rs ^= rs >> 17;
+          rs ^= rs << 5;
+          constexpr float k16 = 1.0f / 65536.0f, half = 0.5f / 65536.0f;
+          y[j] = floorf(fmaf((float)(rs & 0xFFFFu), k16, fmaf(mnew[k][j], rms, half)));
+          y[j + 1] = floorf(fmaf((float)(rs >> 16), k16, fmaf(mnew[k][j + 1], rms, half)));
         }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) y[j] = rintf(div_refined(mnew[k][j], ms, rms));
       }
       uint32_t q[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const int32_t qi = (int32_t)fminf(fmaxf(rintf(y[j]), -lim), lim);
+        const int32_t qi = (int32_t)fminf(fmaxf(y[j], -lim), lim);
         q[j] = MK == kM8 ? ((uint32_t)qi & 0xFFu) : (uint32_t)(qi + 31);
       }
       if constexpr (MK == kM8) {
@@ -815,9 +852,9 @@ APEXW_DEV bool fv_unit_row(const apexw_tensor& t, const apexw_fv_tensor& e, uint
   }
 }
 
-// One kernel per parameter dtype, each over its own range of units: the fp32
-// variant's larger register footprint does not lower the bf16 variant's occupancy.
-template <int PDK>
+// One kernel per (parameter dtype, m kind), each over its own range of units:
+// no variant's register footprint lowers another's occupancy.
+template <int PDK, int MK>
 __global__ __launch_bounds__(256) void fv_update_kernel(const apexw_tensor* __restrict__ tensors,
                                                         const apexw_fv_tensor* __restrict__ fv, int n_fv,
                                                         const apexw_unit* __restrict__ units, int64_t n_units,
@@ -834,50 +871,47 @@ __global__ __launch_bounds__(256) void fv_update_kernel(const apexw_tensor* __re
   for (; u < n_units; u += stride) {
     const apexw_unit un = next;
     if (u + stride < n_units) next = units[u + stride];
-    if (un.tensor >= (uint32_t)n_fv) continue;  // never taken for a valid plan
+    // the checks below are never taken for a valid plan
+    if (un.tensor >= (uint32_t)n_fv) continue;
     const apexw_fv_tensor& e = fv[un.tensor];
     const apexw_tensor& t = tensors[e.tensor];
-    if (!(t.flags & APEXW_FLAG_FACTORED)) continue;  // never taken for a valid plan
+    if (!(t.flags & APEXW_FLAG_FACTORED)) continue;
     const bool p32 = ((t.flags >> APEXW_FLAG_PDT_SHIFT) & 3u) == APEXW_F32;
-    if (p32 != (PDK == APEXW_F32)) continue;
+    const int mk = t.block == 0 ? kM16 : (t.flags & APEXW_FLAG_M6) ? kM6 : kM8;
+    if (p32 != (PDK == APEXW_F32) || mk != MK) continue;
     const bool full = !(t.flags & APEXW_FLAG_SCALAR) && (t.block == 0 || t.block == 2048) &&
                       (int64_t)(un.unit + 1) * 2048 <= t.n;
     if (full) {
-      if (row_ok && (e.cols & 3) == 0) {
-        const bool done = t.block == 0 ? fv_unit_row<PDK, kM16>(t, e, e.tensor, un.unit, ws, c)
-                          : (t.flags & APEXW_FLAG_M6) ? fv_unit_row<PDK, kM6>(t, e, e.tensor, un.unit, ws, c)
-                                                      : fv_unit_row<PDK, kM8>(t, e, e.tensor, un.unit, ws, c);
-        if (done) continue;
-      }
-      if (t.block == 0) fv_unit_full<PDK, kM16>(t, e, e.tensor, un.unit, ws, c);
-      else if (t.flags & APEXW_FLAG_M6) fv_unit_full<PDK, kM6>(t, e, e.tensor, un.unit, ws, c);
-      else fv_unit_full<PDK, kM8>(t, e, e.tensor, un.unit, ws, c);
-      continue;
+      if (row_ok && (e.cols & 3) == 0 && fv_unit_row<PDK, MK>(t, e, e.tensor, un.unit, ws, c)) continue;
+      fv_unit_full<PDK, MK>(t, e, e.tensor, un.unit, ws, c);
+    } else {
+      fv_unit<PDK, MK>(t, e, e.tensor, un.unit, ws, c);
     }
-    if (t.block == 0) fv_unit<PDK, kM16>(t, e, e.tensor, un.unit, ws, c);
-    else if (t.flags & APEXW_FLAG_M6) fv_unit<PDK, kM6>(t, e, e.tensor, un.unit, ws, c);
-    else fv_unit<PDK, kM8>(t, e, e.tensor, un.unit, ws, c);
   }
+}
+
+template <int PDK, int MK>
+void launch_update(const apexw_tensor* tensors, const apexw_fv_tensor* fv, int32_t n_fv, const apexw_unit* units,
+                   int64_t begin, int64_t end, float* ws, const apexw_hparams* hp, hipStream_t stream) {
+  if (end <= begin) return;
+  const int grid = apexw_resident_grid((const void*)fv_update_kernel<PDK, MK>, end - begin);
+  hipLaunchKernelGGL((fv_update_kernel<PDK, MK>), dim3(grid), dim3(256), 0, stream, tensors, fv, n_fv, units + begin,
+                     end - begin, ws, *hp);
 }
 
 }  // namespace
 
 int apexw_launch_factored(const apexw_tensor* tensors, const apexw_fv_tensor* fv, int32_t n_fv, int64_t n_bands,
-                          int64_t n_col_blocks, const apexw_unit* units, int64_t n_units, int64_t n_bf16_units,
-                          float* ws, const apexw_hparams* hp, hipStream_t stream) {
+                          int64_t n_col_blocks, const apexw_unit* units, const int64_t* ends, float* ws,
+                          const apexw_hparams* hp, hipStream_t stream) {
   hipLaunchKernelGGL(fv_stats_kernel, dim3((unsigned)n_bands), dim3(256), 0, stream, tensors, fv, n_fv, ws, *hp);
   hipLaunchKernelGGL(fv_finalize_kernel, dim3((unsigned)(n_col_blocks + n_fv)), dim3(256), 0, stream, tensors, fv,
                      n_fv, n_col_blocks, ws, *hp);
-  if (n_bf16_units > 0) {
-    const int g16 = apexw_resident_grid((const void*)fv_update_kernel<APEXW_BF16>, n_bf16_units);
-    hipLaunchKernelGGL(fv_update_kernel<APEXW_BF16>, dim3(g16), dim3(256), 0, stream, tensors, fv, n_fv, units,
-                       n_bf16_units, ws, *hp);
-  }
-  if (n_units > n_bf16_units) {
-    const int64_t n32 = n_units - n_bf16_units;
-    const int g32 = apexw_resident_grid((const void*)fv_update_kernel<APEXW_F32>, n32);
-    hipLaunchKernelGGL(fv_update_kernel<APEXW_F32>, dim3(g32), dim3(256), 0, stream, tensors, fv, n_fv,
-                       units + n_bf16_units, n32, ws, *hp);
-  }
+  launch_update<APEXW_BF16, kM8>(tensors, fv, n_fv, units, 0, ends[0], ws, hp, stream);
+  launch_update<APEXW_BF16, kM6>(tensors, fv, n_fv, units, ends[0], ends[1], ws, hp, stream);
+  launch_update<APEXW_BF16, kM16>(tensors, fv, n_fv, units, ends[1], ends[2], ws, hp, stream);
+  launch_update<APEXW_F32, kM8>(tensors, fv, n_fv, units, ends[2], ends[3], ws, hp, stream);
+  launch_update<APEXW_F32, kM6>(tensors, fv, n_fv, units, ends[3], ends[4], ws, hp, stream);
+  launch_update<APEXW_F32, kM16>(tensors, fv, n_fv, units, ends[4], ends[5], ws, hp, stream);
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define APEXW_ABI_VERSION 9
+#define APEXW_ABI_VERSION 10
 
 /* status codes */
 enum apexw_status {
@@ -226,14 +226,17 @@ int64_t apexw_factored_layout(apexw_fv_tensor* fv, int32_t n_fv, int64_t* n_band
  * units (one quantization block each for quantized m, APEXW_COMPACT_UNIT
  * elements for 16-bit m; a unit's `tensor` field is the index of its entry in
  * fv, not a row of the tensor table, so no lookup precedes its loads).  The
- * units of bf16-parameter tensors come first (n_bf16_units of them), then those
- * of fp32-parameter tensors; each range runs on its own kernel.
+ * units are grouped by (parameter dtype, m kind) in the order bf16 / INT8 m,
+ * bf16 / 6-bit m, bf16 / bf16 m, fp32 / INT8 m, fp32 / 6-bit m, fp32 / bf16 m;
+ * range_ends (HOST array of APEXW_FV_UNIT_RANGES) holds the end offset of each
+ * group (the last is n_units), and each non-empty group runs on its own kernel.
  * workspace: the floats apexw_factored_layout returned.  hp as for the step
  * kernels (mode ignored); APEXW_HP_SR rounds the m codes stochastically.
  */
+#define APEXW_FV_UNIT_RANGES 6
 int apexw_factored_step(const apexw_tensor* tensors, int32_t n_tensors, const apexw_fv_tensor* fv, int32_t n_fv,
                         int64_t n_bands, int64_t n_col_blocks, const apexw_unit* units, int64_t n_units,
-                        int64_t n_bf16_units, float* workspace, const apexw_hparams* hp, void* stream);
+                        const int64_t* range_ends, float* workspace, const apexw_hparams* hp, void* stream);
 
 /*
  * Global-L2 clip coefficient over the grads of the table:

@@ -253,7 +253,8 @@ def test_factored_rows_and_launch(cpu_plans, prec):
     _, args, hp = calls[-1]
     fv = plan.fv["d_fv"].cpu().numpy().view(L.FV_TENSOR_DTYPE)
     assert list(fv["tensor"]) == sorted(fv["tensor"]) and args[3] == len(fv)
-    assert args[8] == plan.fv["n_units"]                     # every parameter here is bf16
+    ends = plan.fv["range_ends"]
+    assert args[8] == ends.ctypes.data and len(ends) == L.FV_UNIT_RANGES and ends[-1] == plan.fv["n_units"]
     for row in fv:
         d = int(row["tensor"])
         assert fac[d] and int(row["rows"]) * int(row["cols"]) == int(table["n"][d])
@@ -262,5 +263,17 @@ def test_factored_rows_and_launch(cpu_plans, prec):
     assert set(units["tensor"].tolist()) == set(range(len(fv)))    # units name their fv entry
     for k in range(len(fv)):
         assert (units["tensor"] == k).sum() == plan.unit_counts[int(fv[k]["tensor"])]
+    # groups (bf16 params): INT8 m, then 6-bit m, then bf16 m; no fp32 groups
+    begins = np.concatenate([[0], ends[:-1]])
+    for r, (b, e) in enumerate(zip(begins, ends)):
+        for k in set(units["tensor"][b:e].tolist()):
+            row = table[int(fv[k]["tensor"])]
+            want = 2 if int(row["block"]) == 0 else (1 if int(row["flags"]) & L.FLAG_M6 else 0)
+            assert r == want
+    assert ends[2] == plan.fv["n_units"]
+    if prec == "compact":
+        assert ends[1] == 0
+    else:
+        assert 0 < ends[0] < ends[1] == ends[2]
     assert hp["step"] == 2 and hp["flags"] & L.HP_FV_SANITIZE == (L.HP_FV_SANITIZE if prec == "8bit" else 0)
     assert hp["eps"] == pytest.approx(1e-8) and hp["mode"] == L.MODE_COLD

@@ -74,6 +74,24 @@ template <int GD> APEXW_DEV float fv_grad(float g, const FvCtx& c) {
   return g;
 }
 
+// fv_grad as selects on the launch-uniform flags: no per-element branches in
+// the unrolled single-row update.  Same values as fv_grad.
+template <int GD> APEXW_DEV float fv_grad_sel(float g, const FvCtx& c) {
+  const uint32_t f = c.hp->flags;
+  const bool unscale = f & APEXW_HP_UNSCALE, clip = f & APEXW_HP_CLIP;
+  const float big = rnd<GD>(65504.0f);
+  float x = g;
+  const float xs = __builtin_isnan(x) ? 0.0f : (__builtin_isinf(x) ? __builtin_copysignf(big, x) : x);
+  x = (f & APEXW_HP_SANITIZE) ? xs : x;
+  const float xu = rnd<GD>(x * c.hp->grad_inv_scale);
+  x = (unscale && clip) ? xu : x;
+  const float xc = rnd<GD>(x * c.coef);
+  x = clip ? xc : x;
+  const float xf = __builtin_isnan(x) ? 0.0f : (__builtin_isinf(x) ? __builtin_copysignf(65504.0f, x) : x);
+  x = (f & APEXW_HP_FV_SANITIZE) ? xf : x;
+  return (unscale && !clip) ? x * c.hp->grad_inv_scale : x;
+}
+
 APEXW_DEV int fv_find_band(const apexw_fv_tensor* fv, int n_fv, int64_t band) {
   int lo = 0, hi = n_fv - 1;
   while (lo < hi) {
@@ -133,8 +151,9 @@ template <int GD, bool PLAIN> APEXW_DEV float fv_sq(float g, const FvCtx& c, boo
 // the new row values in aux[band] for the row mean.
 //
 // A pass whose 32 x 2048 tile lies inside the tensor (and PLAIN) loads its rows
-// in batches (128 bytes per lane) and keeps the row partials in registers; other passes go row
-// by row and add each row's wave sum to the wave's LDS row slot.
+// in batches (128 bytes per lane); other passes go row by row.  Both keep the
+// row partials in registers and sum in the same order, so the statistics do not
+// depend on which path a pass took.
 template <int GD, bool PLAIN>
 APEXW_DEV void fv_stats_band(const apexw_tensor& t, const apexw_fv_tensor& e, int64_t band, float* ws,
                              const FvCtx& c) {
@@ -147,8 +166,6 @@ APEXW_DEV void fv_stats_band(const apexw_tensor& t, const apexw_fv_tensor& e, in
   const int nr = min(kBand, e.rows - r0);
   const bool vec = !(t.flags & APEXW_FLAG_SCALAR) && (cols % 8) == 0;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  if ((int)threadIdx.x < 4 * kBand) s_row[threadIdx.x / kBand][threadIdx.x % kBand] = 0.0f;
-  __syncthreads();
   float racc[kBand];
 #pragma unroll
   for (int i = 0; i < kBand; ++i) racc[i] = 0.0f;
@@ -178,10 +195,11 @@ APEXW_DEV void fv_stats_band(const apexw_tensor& t, const apexw_fv_tensor& e, in
         }
       }
     } else {
-#pragma unroll 1
-      for (int i = 0; i < nr; ++i) {
-        float rs = 0.0f;
-        if (cnt > 0) {
+      // row by row; the same summation order as the whole-tile path (per lane:
+      // the row's 8 squares, then across passes; per column: down the rows)
+#pragma unroll
+      for (int i = 0; i < kBand; ++i) {
+        if (i < nr && cnt > 0) {
           const int64_t e0 = (int64_t)(r0 + i) * cols + cb;
           float g[8];
           if (vec && cnt == 8) {
@@ -190,15 +208,15 @@ APEXW_DEV void fv_stats_band(const apexw_tensor& t, const apexw_fv_tensor& e, in
 #pragma unroll
             for (int j = 0; j < 8; ++j) g[j] = j < cnt ? load1<GD>(t.g, e0 + j) : 0.0f;
           }
+          float rs = 0.0f;
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
             const float sq = j < cnt ? fv_sq<GD, PLAIN>(g[j], c, fs) : 0.0f;
             cacc[j] = cacc[j] + sq;
             rs = rs + sq;
           }
+          racc[i] = racc[i] + rs;
         }
-        const float s = wave_sum(rs);
-        if (lane == 0) s_row[wave][i] += s;
       }
     }
 #pragma unroll
@@ -210,7 +228,7 @@ APEXW_DEV void fv_stats_band(const apexw_tensor& t, const apexw_fv_tensor& e, in
 #pragma unroll
   for (int i = 0; i < kBand; ++i) {
     const float s = wave_sum(racc[i]);
-    if (lane == 0) s_row[wave][i] += s;
+    if (lane == 0) s_row[wave][i] = s;
   }
   __syncthreads();
   if (wave == 0) {
@@ -228,6 +246,9 @@ APEXW_DEV void fv_stats_band(const apexw_tensor& t, const apexw_fv_tensor& e, in
   }
 }
 
+// PLAIN (no grad-dtype sanitize, clip or AMP unscale) is a launch-wide property:
+// one instantiation each, so the plain kernel keeps its own register budget.
+template <bool PLAIN>
 __global__ __launch_bounds__(256) void fv_stats_kernel(const apexw_tensor* __restrict__ tensors,
                                                        const apexw_fv_tensor* __restrict__ fv, int n_fv,
                                                        float* __restrict__ ws, apexw_hparams hp) {
@@ -239,15 +260,8 @@ __global__ __launch_bounds__(256) void fv_stats_kernel(const apexw_tensor* __res
   c.hp = &hp;
   c.coef = (hp.flags & APEXW_HP_CLIP) ? *hp.clip_coef : 1.0f;
   const int64_t lb = band - e.band0;
-  const bool plain = !(hp.flags & (APEXW_HP_SANITIZE | APEXW_HP_CLIP | APEXW_HP_UNSCALE));
-  const bool f32 = ((t.flags >> APEXW_FLAG_GDT_SHIFT) & 3u) == APEXW_F32;
-  if (plain) {
-    if (f32) fv_stats_band<APEXW_F32, true>(t, e, lb, ws, c);
-    else fv_stats_band<APEXW_BF16, true>(t, e, lb, ws, c);
-  } else {
-    if (f32) fv_stats_band<APEXW_F32, false>(t, e, lb, ws, c);
-    else fv_stats_band<APEXW_BF16, false>(t, e, lb, ws, c);
-  }
+  if (((t.flags >> APEXW_FLAG_GDT_SHIFT) & 3u) == APEXW_F32) fv_stats_band<APEXW_F32, PLAIN>(t, e, lb, ws, c);
+  else fv_stats_band<APEXW_BF16, PLAIN>(t, e, lb, ws, c);
 }
 
 // ---------------------------------------------------------------------------
@@ -658,13 +672,13 @@ APEXW_DEV void fv_unit_full(const apexw_tensor& t, const apexw_fv_tensor& e, uin
   }
 }
 
-// A whole unit inside one row of the matrix, for the common case: no grad-dtype
-// sanitize / clip / AMP unscale, a lerp weight below 0.5 and
-// cols % 4 == 0.  The row factor is one value for the unit and the column roots
+// A whole unit inside one row of the matrix (cols % 4 == 0).  PLAIN: no grad-dtype
+// sanitize / clip / AMP unscale and a lerp weight below 0.5; otherwise the grad
+// goes through fv_grad_sel and the lerp picks its form per launch.  The row factor is one value for the unit and the column roots
 // are 16-byte loads; the update's division is the refined one of fv_unit, and
 // bf16 roundings convert pairs.  Returns false, before any load, when the unit
 // crosses a row: the caller then runs fv_unit_full on it.
-template <int PD, int MK>
+template <int PD, int MK, bool PLAIN>
 APEXW_DEV bool fv_unit_row(const apexw_tensor& t, const apexw_fv_tensor& e, uint32_t tix, uint32_t unit,
                            float* ws, const FvCtx& c) {
   constexpr int W = PD == APEXW_F32 ? 2 : 1;  // 16-byte words per 8 elements of p / g
@@ -715,10 +729,11 @@ APEXW_DEV bool fv_unit_row(const apexw_tensor& t, const apexw_fv_tensor& e, uint
     for (int j = 0; j < 8; ++j) {
       g[k][j] = PD == APEXW_F32 ? __uint_as_float(gw[j])
                                 : (j & 1 ? __uint_as_float(gw[j >> 1] & 0xFFFF0000u) : __uint_as_float(gw[j >> 1] << 16));
-      chk = fmaf(g[k][j], 0.0f, chk);
+      if constexpr (PLAIN) chk = fmaf(g[k][j], 0.0f, chk);
+      else g[k][j] = fv_grad_sel<PD>(g[k][j], c);
     }
   }
-  if ((hp.flags & APEXW_HP_FV_SANITIZE) && __builtin_amdgcn_ballot_w64(!(chk == 0.0f)) != 0) {
+  if (PLAIN && (hp.flags & APEXW_HP_FV_SANITIZE) && __builtin_amdgcn_ballot_w64(!(chk == 0.0f)) != 0) {
 #pragma unroll
     for (int k = 0; k < 4; ++k)
 #pragma unroll
@@ -763,7 +778,8 @@ APEXW_DEV bool fv_unit_row(const apexw_tensor& t, const apexw_fv_tensor& e, uint
     float upd[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      m[j] = fmaf(hp.lerp_coef, g[k][j] - m[j], m[j]);
+      m[j] = PLAIN ? fmaf(hp.lerp_coef, g[k][j] - m[j], m[j])
+                   : lerp_to(m[j], g[k][j], hp.lerp_coef, hp.flags & APEXW_HP_LERP_HI);
       const float den = fmaxf(rv * cs[j] + hp.eps_scaled, hp.eps);
       upd[j] = div_refined(m[j], den, rcp_refined(den)) * hp.step_size;
       if constexpr (MK != kM16) {
@@ -852,9 +868,9 @@ APEXW_DEV bool fv_unit_row(const apexw_tensor& t, const apexw_fv_tensor& e, uint
   }
 }
 
-// One kernel per (parameter dtype, m kind), each over its own range of units:
-// no variant's register footprint lowers another's occupancy.
-template <int PDK, int MK>
+// One kernel per (parameter dtype, m kind, PLAIN), each over its own range of
+// units: no variant's register footprint lowers another's occupancy.
+template <int PDK, int MK, bool PLAIN>
 __global__ __launch_bounds__(256) void fv_update_kernel(const apexw_tensor* __restrict__ tensors,
                                                         const apexw_fv_tensor* __restrict__ fv, int n_fv,
                                                         const apexw_unit* __restrict__ units, int64_t n_units,
@@ -864,7 +880,6 @@ __global__ __launch_bounds__(256) void fv_update_kernel(const apexw_tensor* __re
   c.coef = (hp.flags & APEXW_HP_CLIP) ? *hp.clip_coef : 1.0f;
   const uint32_t wave = uniform(threadIdx.x >> 6);
   const int64_t stride = (int64_t)gridDim.x * 4;
-  const bool row_ok = !(hp.flags & (APEXW_HP_SANITIZE | APEXW_HP_CLIP | APEXW_HP_UNSCALE | APEXW_HP_LERP_HI));
   int64_t u = (int64_t)blockIdx.x * 4 + wave;
   // the next unit's descriptor is requested while this unit is processed
   apexw_unit next = u < n_units ? units[u] : apexw_unit{0u, 0u};
@@ -882,7 +897,7 @@ __global__ __launch_bounds__(256) void fv_update_kernel(const apexw_tensor* __re
     const bool full = !(t.flags & APEXW_FLAG_SCALAR) && (t.block == 0 || t.block == 2048) &&
                       (int64_t)(un.unit + 1) * 2048 <= t.n;
     if (full) {
-      if (row_ok && (e.cols & 3) == 0 && fv_unit_row<PDK, MK>(t, e, e.tensor, un.unit, ws, c)) continue;
+      if ((e.cols & 3) == 0 && fv_unit_row<PDK, MK, PLAIN>(t, e, e.tensor, un.unit, ws, c)) continue;
       fv_unit_full<PDK, MK>(t, e, e.tensor, un.unit, ws, c);
     } else {
       fv_unit<PDK, MK>(t, e, e.tensor, un.unit, ws, c);
@@ -894,9 +909,15 @@ template <int PDK, int MK>
 void launch_update(const apexw_tensor* tensors, const apexw_fv_tensor* fv, int32_t n_fv, const apexw_unit* units,
                    int64_t begin, int64_t end, float* ws, const apexw_hparams* hp, hipStream_t stream) {
   if (end <= begin) return;
-  const int grid = apexw_resident_grid((const void*)fv_update_kernel<PDK, MK>, end - begin);
-  hipLaunchKernelGGL((fv_update_kernel<PDK, MK>), dim3(grid), dim3(256), 0, stream, tensors, fv, n_fv, units + begin,
-                     end - begin, ws, *hp);
+  const bool plain = !(hp->flags & (APEXW_HP_SANITIZE | APEXW_HP_CLIP | APEXW_HP_UNSCALE | APEXW_HP_LERP_HI));
+  const void* fn = plain ? (const void*)fv_update_kernel<PDK, MK, true> : (const void*)fv_update_kernel<PDK, MK, false>;
+  const int grid = apexw_resident_grid(fn, end - begin);
+  if (plain)
+    hipLaunchKernelGGL((fv_update_kernel<PDK, MK, true>), dim3(grid), dim3(256), 0, stream, tensors, fv, n_fv,
+                       units + begin, end - begin, ws, *hp);
+  else
+    hipLaunchKernelGGL((fv_update_kernel<PDK, MK, false>), dim3(grid), dim3(256), 0, stream, tensors, fv, n_fv,
+                       units + begin, end - begin, ws, *hp);
 }
 
 }  // namespace
@@ -904,7 +925,10 @@ void launch_update(const apexw_tensor* tensors, const apexw_fv_tensor* fv, int32
 int apexw_launch_factored(const apexw_tensor* tensors, const apexw_fv_tensor* fv, int32_t n_fv, int64_t n_bands,
                           int64_t n_col_blocks, const apexw_unit* units, const int64_t* ends, float* ws,
                           const apexw_hparams* hp, hipStream_t stream) {
-  hipLaunchKernelGGL(fv_stats_kernel, dim3((unsigned)n_bands), dim3(256), 0, stream, tensors, fv, n_fv, ws, *hp);
+  if (!(hp->flags & (APEXW_HP_SANITIZE | APEXW_HP_CLIP | APEXW_HP_UNSCALE)))
+    hipLaunchKernelGGL(fv_stats_kernel<true>, dim3((unsigned)n_bands), dim3(256), 0, stream, tensors, fv, n_fv, ws, *hp);
+  else
+    hipLaunchKernelGGL(fv_stats_kernel<false>, dim3((unsigned)n_bands), dim3(256), 0, stream, tensors, fv, n_fv, ws, *hp);
   hipLaunchKernelGGL(fv_finalize_kernel, dim3((unsigned)(n_col_blocks + n_fv)), dim3(256), 0, stream, tensors, fv,
                      n_fv, n_col_blocks, ws, *hp);
   launch_update<APEXW_BF16, kM8>(tensors, fv, n_fv, units, 0, ends[0], ws, hp, stream);

@@ -114,17 +114,19 @@ def test_factored_steps_match_oracle(name, prec, shape, kw, dtype):
 
 
 @pytest.mark.parametrize("prec", ["8bit", "compact"])
-def test_factored_with_clip_and_amp_equals_unscaled(prec):
+@pytest.mark.parametrize("clip", [0.5, None])
+@pytest.mark.parametrize("shape", [(1024, 512), (128, 4096)])      # 4096 columns: whole-tile statistics
+def test_factored_with_clip_and_amp_equals_unscaled(prec, shape, clip):
     """GradScaler's power-of-two scale cancels exactly, also through the clip."""
     _need_gpu()
     from apexw_amd import ApexW
     gen = torch.Generator().manual_seed(5)
-    host = (torch.randn(1024, 512, generator=gen) * 0.02).bfloat16()
+    host = (torch.randn(shape, generator=gen) * 0.02).bfloat16()
     pa, pb = nn.Parameter(host.cuda()), nn.Parameter(host.cuda())
-    kw = dict(lr=1e-2, precision=prec, factored_v=True, stochastic_rounding=False, clip_grad_norm=0.5)
+    kw = dict(lr=1e-2, precision=prec, factored_v=True, stochastic_rounding=False, clip_grad_norm=clip)
     oa, ob = ApexW([pa], **kw), ApexW([pb], **kw)
     for step in range(3):
-        g = (torch.randn(1024, 512, generator=gen) * 1e-2).bfloat16().cuda()
+        g = (torch.randn(shape, generator=gen) * 1e-2).bfloat16().cuda()
         pa.grad, pb.grad = g * 1024.0, g.clone()
         oa.grad_scale, oa.found_inf = torch.tensor(1024.0, device="cuda"), torch.tensor(0.0, device="cuda")
         oa.step()
@@ -278,14 +280,14 @@ def test_reference_compact_factored_threshold_and_convergence():
 
 
 @pytest.mark.parametrize("prec", ["8bit", "compact"])
-def test_factored_with_centralization_and_clip_matches_oracle(prec):
+@pytest.mark.parametrize("shape", [(1024, 512), (128, 4096)])      # 4096 columns: whole-tile statistics
+def test_factored_with_centralization_and_clip_matches_oracle(prec, shape):
     """Grad centralization and the global-norm clip prepare the grads of factored
     tensors as of any other (apexw/optimizer.py:204-258), beside an ordinary tensor."""
     _need_gpu()
     from apexw_amd import ApexW
     from oracle.optim import OracleApexW
     gen = torch.Generator().manual_seed(9)
-    shape = (1024, 512)
     host = [(torch.randn(shape, generator=gen) * 0.02).bfloat16(), (torch.randn(4096, generator=gen) * 0.02).bfloat16()]
     opts = dict(lr=1e-2, weight_decay=0.1, precision=prec, factored_v=True, stochastic_rounding=False,
                 grad_centralization=True, clip_grad_norm=0.5)

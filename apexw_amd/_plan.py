@@ -104,6 +104,7 @@ class StepPlan:
     def _build_steps(self):
         vals = [float(st["step"].item()) for st in self.states]
         self.steps = torch.tensor(vals, dtype=torch.float32)
+        self._steps_np = self.steps.numpy()   # the same memory: cheap host-side updates
         if self.hooked:
             return
         for i, st in enumerate(self.states):
@@ -404,16 +405,16 @@ class StepPlan:
             sanitize, inv_scale = False, None
         coef = self._clip(clip, sanitize, inv_scale, stream) if clip is not None else None
         if steps is None:
-            self.steps.add_(1.0)
+            self._steps_np += 1.0
         else:
-            self.steps.copy_(torch.tensor(steps, dtype=torch.float32))
+            self._steps_np[:] = np.asarray(steps, dtype=np.float32)
         # The reference's replayed compact step takes the bias correction of the
         # first counter for the whole group (optimizer.py:1082-1090); every other
         # path uses each parameter's own count.
         if mode_cold or self.native or self.kind == "q8":
             groups = self._split_by_step()
         else:
-            groups = [(None, int(self.steps[0].item()))]
+            groups = [(None, int(self._steps_np[0]))]
         for units, step in groups:
             hp = self._hparams(lr, b1, b2, eps, wd, step, sr, sanitize, coef, seed, mode_cold, inv_scale)
             if units is None:
@@ -468,9 +469,10 @@ class StepPlan:
             L.check(st, "apexw_factored_step")
 
     def _split_by_step(self):
-        vals = self.steps.numpy()[self.perm]
-        if np.all(vals == vals[0]):
-            return [(None, int(vals[0]))]
+        raw = self._steps_np
+        if raw.size == 1 or raw.min() == raw.max():
+            return [(None, int(raw[0]))]
+        vals = raw[self.perm]
         out = []
         for val in sorted(set(vals.tolist()), key=vals.tolist().index):
             keep = vals == val

@@ -19,6 +19,7 @@ from torch.optim.optimizer import Optimizer
 
 from . import state as S
 from .muon import ApexMuon
+from . import runtime as R
 from .optimizer import ApexW
 
 
@@ -251,6 +252,7 @@ class HybridApexW(Optimizer):
         self.apexw_opt = self.adamw_opt
         self._sync_groups()
 
+    @R.step_hooks
     @torch.no_grad()
     def step(self, closure=None):
         loss = None

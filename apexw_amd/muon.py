@@ -26,6 +26,7 @@ import numpy as np
 import torch
 from torch.optim.optimizer import Optimizer
 
+from . import runtime as R
 from . import _lib
 from . import state as S
 
@@ -229,6 +230,7 @@ class ApexMuon(Optimizer):
             plan = self._ns_plans[key] = NSPlan([j["ws"] for j in jobs], [j["steps"] for j in jobs], device)
         return plan
 
+    @R.step_hooks
     @torch.no_grad()
     def step(self, closure=None):
         loss = None

@@ -187,6 +187,7 @@ class ApexW(Optimizer):
             self._init_hook_state()
 
     # ------------------------------------------------------------------ step
+    @R.step_hooks
     @torch.no_grad()
     def step(self, closure=None):
         loss = None

@@ -173,3 +173,42 @@ def _patch_reset_peak_memory_stats():
 
     torch.cuda.reset_peak_memory_stats = reset_peak_memory_stats
     torch.cuda._apexw_amd_reset_peak_patched = True
+
+
+def step_hooks(func):
+    """torch.optim.Optimizer's step wrapper (``Optimizer.profile_hook_step``) with
+    the same hook semantics: global and per-optimizer pre hooks (which may
+    replace args / kwargs), ``_optimizer_step_code``, then post hooks.  The
+    ``Optimizer.step#<class>.step`` profiler range is opened only while a
+    profiler runs: outside one, entering and leaving it is a large share of a
+    small model's host time per step.  Marked ``hooked`` so that
+    ``Optimizer._patch_step_function`` does not wrap the method again."""
+    import functools
+    from itertools import chain
+
+    from torch.optim import optimizer as _opt
+
+    def run(self, args, kwargs):
+        for pre_hook in chain(_opt._global_optimizer_pre_hooks.values(), self._optimizer_step_pre_hooks.values()):
+            result = pre_hook(self, args, kwargs)
+            if result is not None:
+                if isinstance(result, tuple) and len(result) == 2:
+                    args, kwargs = result
+                else:
+                    raise RuntimeError(f"{func} must return None or a tuple of (new_args, new_kwargs), but got {result}.")
+        out = func(*args, **kwargs)
+        self._optimizer_step_code()
+        for post_hook in chain(self._optimizer_step_post_hooks.values(), _opt._global_optimizer_post_hooks.values()):
+            post_hook(self, args, kwargs)
+        return out
+
+    @functools.wraps(func)
+    def wrapper(*args, **kwargs):
+        self = args[0]
+        if torch.autograd._profiler_enabled():
+            with torch.autograd.profiler.record_function(f"Optimizer.step#{self.__class__.__name__}.step"):
+                return run(self, args, kwargs)
+        return run(self, args, kwargs)
+
+    wrapper.hooked = True
+    return wrapper

@@ -147,3 +147,31 @@ def test_step_requires_gpu_tensors():
     p.grad = torch.zeros(8)
     with pytest.raises(RuntimeError):
         ApexW([p]).step()
+
+
+def test_step_hooks_match_torch_semantics():
+    """The step wrapper keeps torch.optim's hook contract: global and
+    per-optimizer pre hooks (which may replace args), then post hooks, in
+    order; torch does not wrap the method a second time."""
+    from torch.optim.optimizer import register_optimizer_step_pre_hook
+    from apexw_amd import ApexW
+    from apexw_amd.hybrid import HybridApexW
+    from apexw_amd.muon import ApexMuon
+    for cls in (ApexW, ApexMuon, HybridApexW):
+        assert getattr(cls.step, "hooked", False)
+    p = torch.nn.Parameter(torch.zeros(4))
+    opt = ApexW([p], lr=1e-3)
+    assert getattr(type(opt).step, "hooked", False) and type(opt).step is ApexW.step
+    calls = []
+    g = register_optimizer_step_pre_hook(lambda o, a, k: calls.append(("global pre", len(a))))
+    h1 = opt.register_step_pre_hook(lambda o, a, k: calls.append(("pre", len(a))))
+    h2 = opt.register_step_post_hook(lambda o, a, k: calls.append(("post", len(a))))
+    try:
+        opt.step()                                   # no grads: nothing to step, hooks still run
+    finally:
+        g.remove(), h1.remove(), h2.remove()
+    assert calls == [("global pre", 1), ("pre", 1), ("post", 1)]
+    bad = opt.register_step_pre_hook(lambda o, a, k: 3)
+    with pytest.raises(RuntimeError):
+        opt.step()
+    bad.remove()

@@ -23,6 +23,7 @@ the tensor table (one host-to-device copy); a parameter whose storage or dtype
 changed in place (``p.data = ...``, ``module.to(dtype)``) invalidates the plan.
 """
 
+import functools
 import math
 import operator
 
@@ -49,6 +50,7 @@ _GRAD = operator.attrgetter("grad")
 SCAN_SAME, SCAN_GRADS_MOVED, SCAN_MISSING, SCAN_REBUILT, SCAN_SLOW = range(5)
 
 
+@functools.lru_cache(maxsize=64)
 def _lerp_coef(w):
     w32 = np.float32(w)
     if abs(float(w32)) < 0.5:
@@ -97,8 +99,7 @@ class StepPlan:
         return self._scan_status in (SCAN_SAME, SCAN_GRADS_MOVED, SCAN_SLOW)
 
     def _scan(self):
-        return self._H.scan(self.params, self.inactive, self.p_ptrs.ctypes.data, self.p_dtypes.ctypes.data,
-                      self.g_ptrs.ctypes.data, self.g_scan.ctypes.data)
+        return self._H.scan(self.params, self.inactive, *self._scan_addrs)
 
     # ------------------------------------------------------------------ build
     def _build_steps(self):
@@ -183,6 +184,9 @@ class StepPlan:
         self._H.snapshot(self.params, self.p_ptrs.ctypes.data, self.p_dtypes.ctypes.data)
         self.g_ptrs = np.zeros(n, dtype=np.uint64)     # grad pointers the table was built from
         self.g_scan = np.zeros(n, dtype=np.uint64)     # the scan's current grad pointers
+        # the arrays never move: their addresses are taken once
+        self._scan_addrs = (self.p_ptrs.ctypes.data, self.p_dtypes.ctypes.data, self.g_ptrs.ctypes.data,
+                            self.g_scan.ctypes.data)
         self._scan_status = None
         if self.gc and not self.single:
             self._build_prep()

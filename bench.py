@@ -1,6 +1,6 @@
 """Benchmark: the ApexW 8-bit optimizer step on a Llama-3-8B-shaped parameter set.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--config c3|c2|c4|c1] [--no-cpu]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--config c3|c2|c4|c1|...] [--no-cpu]
     python bench.py --copy-calibration     # 1 GiB device copy, for HBM counter scaling
 
 Prints ONE JSON line (rank 0).  A "step" is one ``ApexW.step()`` over the full
@@ -80,6 +80,15 @@ CONFIGS = {
                   shapes=llama3_8b_shapes(), dtype=torch.bfloat16, grad_reads=2,
                   kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, precision="8bit", factored_v=True,
                               six_bit=True)),
+    # in-backward stepping: a step is opt.zero_grad(), a backward whose graph hands every
+    # parameter its synthetic grad (p.view_as(p), no arithmetic), then opt.step(); with
+    # hooks the 8-bit kernel runs per batch of 14 layers inside the backward
+    "c3hooks": dict(workload="C3 shapes, 8-bit ApexW stepped inside backward (post-accumulate-grad hooks, "
+                             "batches of 14), bf16, SR on", shapes=llama3_8b_shapes(), dtype=torch.bfloat16,
+                    backward="hooks", kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, precision="8bit")),
+    "c3bwd": dict(workload="C3 shapes, 8-bit ApexW, the same backward with the in-backward hooks removed "
+                           "(one step after it), bf16, SR on", shapes=llama3_8b_shapes(), dtype=torch.bfloat16,
+                  backward="plain", kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, precision="8bit")),
     "c4": dict(workload="C4 compact ApexW step, 20k ragged bf16 tensors, clip 1.0", shapes=ragged_shapes(),
                dtype=torch.bfloat16, kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, clip_grad_norm=1.0),
                zero_frac=0.05),
@@ -144,13 +153,15 @@ def copy_calibration():
     print(json.dumps({"copy_calibration": {"bytes_read": n * 4, "bytes_written": n * 4, "launches": 3}}), flush=True)
 
 
-def state_bytes(opt, params, grad_reads=1):
+def state_bytes(opt, params, grad_reads=1, grads=None):
     """Algorithmic HBM bytes of one step: p read+write, g read (twice with a factored
     second moment: its row / column statistics must be complete before any update),
-    every state tensor read+write."""
+    every state tensor read+write.  grads: the step's grads when p.grad has been
+    released (the in-backward steps drop each grad once its batch is stepped)."""
     tot = 0
-    for p in params:
-        tot += 2 * p.numel() * p.element_size() + grad_reads * p.grad.numel() * p.grad.element_size()
+    for i, p in enumerate(params):
+        g = p.grad if grads is None else grads[i]
+        tot += 2 * p.numel() * p.element_size() + grad_reads * g.numel() * g.element_size()
         for k, v in opt.state[p].items():
             if torch.is_tensor(v) and k != "step" and v.device.type == "cuda":
                 tot += 2 * v.numel() * v.element_size()
@@ -259,10 +270,23 @@ def main():
     params = make_params(cfg, dev)
     n = sum(p.numel() for p in params)
     opt = ApexW(params, **cfg["kwargs"])
+    step = opt.step
+    if cfg.get("backward"):
+        grads = [p.grad for p in params]
+        for p in params:
+            p.grad = None
+        if cfg["backward"] == "plain":
+            opt._disable_auto_8bit_hooks()
+
+        def step():
+            opt.zero_grad(set_to_none=True)
+            torch.autograd.backward([p.view_as(p) for p in params], grad_tensors=grads)
+            opt.step()
     for _ in range(args.warmup):
-        opt.step()
+        step()
     torch.cuda.synchronize()
-    nbytes = 0 if cfg.get("mfma") else state_bytes(opt, params, cfg.get("grad_reads", 1))
+    nbytes = 0 if cfg.get("mfma") else state_bytes(opt, params, cfg.get("grad_reads", 1),
+                                                    grads if cfg.get("backward") else None)
     stream = torch.cuda.current_stream(dev)
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -271,7 +295,7 @@ def main():
     host = 0.0
     for _ in range(args.steps):
         h0 = time.perf_counter()
-        opt.step()
+        step()
         host += time.perf_counter() - h0
     ev1.record(stream)
     torch.cuda.synchronize()

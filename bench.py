@@ -92,6 +92,12 @@ CONFIGS = {
     "c4": dict(workload="C4 compact ApexW step, 20k ragged bf16 tensors, clip 1.0", shapes=ragged_shapes(),
                dtype=torch.bfloat16, kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, clip_grad_norm=1.0),
                zero_frac=0.05),
+    # grad centralization: the prepared copy is written once (g read twice: row sums, then
+    # subtract) and read by the clip and the step; counted as 4 grad passes
+    "c4gc": dict(workload="C4 compact ApexW step, 20k ragged bf16 tensors, clip 1.0, grad_centralization=True",
+                 shapes=ragged_shapes(), dtype=torch.bfloat16, grad_reads=4,
+                 kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, clip_grad_norm=1.0,
+                             grad_centralization=True), zero_frac=0.05),
     "c5": dict(workload="C5 hybrid Muon step (use_muon=True), one Llama-3-8B layer's matrices + 2 RMSNorm, bf16",
                shapes=llama3_8b_shapes()[1:10], dtype=torch.bfloat16,
                kwargs=dict(lr=1e-3, weight_decay=0.1, use_muon=True), mfma=True),

@@ -109,26 +109,71 @@ template <int GD> APEXW_DEV float prep_value(const void* g, int64_t i, bool san,
   return x;
 }
 
+template <int GD> APEXW_DEV void prep_vec8(const void* g, int64_t i, bool san, bool unscale, float inv,
+                                           float (&x)[8]) {
+  load8<GD>(g, i, x);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    if (san) x[j] = sanitize<GD>(x[j]);
+    if (unscale) x[j] = rnd<GD>(x[j] * inv);
+  }
+}
+
+// Elements [lo, hi) of a grad: the 8-aligned middle [a, b) in 8-element vectors
+// (16-byte bf16 / 32-byte fp32 accesses) when both buffers are aligned for
+// them, the ragged ends element by element.
+struct PrepSpan {
+  int64_t a, b;
+};
+template <int GD> APEXW_DEV PrepSpan prep_span(const apexw_grad_prep& d, int64_t lo, int64_t hi) {
+  constexpr uintptr_t align = GD == APEXW_F32 ? 31 : 15;
+  if ((((uintptr_t)d.g | (uintptr_t)d.out) & align) != 0) return {hi, hi};
+  const int64_t a = (lo + 7) & ~(int64_t)7, b = hi & ~(int64_t)7;
+  return a < b ? PrepSpan{a, b} : PrepSpan{hi, hi};
+}
+
 template <int GD>
 APEXW_DEV void prep_unit(const apexw_grad_prep& d, int64_t unit, bool san, bool unscale, float inv, float* red) {
   const int tid = threadIdx.x;
-  if (d.row_len > 0) {
-    const int64_t base = unit * d.row_len;
+  const bool row = d.row_len > 0;
+  const int64_t lo = row ? unit * d.row_len : unit * APEXW_GRAD_PREP_CHUNK;
+  const int64_t hi = row ? lo + d.row_len : (lo + APEXW_GRAD_PREP_CHUNK < d.n ? lo + APEXW_GRAD_PREP_CHUNK : d.n);
+  const PrepSpan sp = prep_span<GD>(d, lo, hi);
+  // ragged ends: [lo, a) and [b, hi) (the whole range when not vectorized)
+  const int64_t head = sp.a - lo, n_end = head + (hi - sp.b);
+  float mean = 0.0f;
+  if (row) {
     float s = 0.0f;
-    for (int64_t j = tid; j < d.row_len; j += 256) s += prep_value<GD>(d.g, base + j, san, unscale, inv);
+    for (int64_t i = sp.a + (int64_t)tid * 8; i < sp.b; i += 2048) {
+      float x[8];
+      prep_vec8<GD>(d.g, i, san, unscale, inv, x);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s += x[j];
+    }
+    for (int64_t k = tid; k < n_end; k += 256) {
+      const int64_t i = k < head ? lo + k : sp.b + (k - head);
+      s += prep_value<GD>(d.g, i, san, unscale, inv);
+    }
     s = wave_sum(s);
     if ((tid & 63) == 0) red[tid >> 6] = s;
     __syncthreads();
     // torch's mean: sum in fp32, divided by the count, result in the grad dtype
-    const float mean = rnd<GD>(((red[0] + red[1]) + (red[2] + red[3])) / (float)d.row_len);
-    for (int64_t j = tid; j < d.row_len; j += 256) {
-      const float x = prep_value<GD>(d.g, base + j, san, unscale, inv);
-      store1<GD>(d.out, base + j, rnd<GD>(x - mean));
+    mean = rnd<GD>(((red[0] + red[1]) + (red[2] + red[3])) / (float)d.row_len);
+  }
+  // second pass (the row is re-read from L2): subtract the mean and store
+  for (int64_t i = sp.a + (int64_t)tid * 8; i < sp.b; i += 2048) {
+    float x[8];
+    prep_vec8<GD>(d.g, i, san, unscale, inv, x);
+    if (row) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[j] = rnd<GD>(x[j] - mean);
     }
-  } else {
-    const int64_t base = unit * APEXW_GRAD_PREP_CHUNK;
-    const int64_t end = base + APEXW_GRAD_PREP_CHUNK < d.n ? base + APEXW_GRAD_PREP_CHUNK : d.n;
-    for (int64_t i = base + tid; i < end; i += 256) store1<GD>(d.out, i, prep_value<GD>(d.g, i, san, unscale, inv));
+    store8<GD>(d.out, i, x);
+  }
+  for (int64_t k = tid; k < n_end; k += 256) {
+    const int64_t i = k < head ? lo + k : sp.b + (k - head);
+    const float x = prep_value<GD>(d.g, i, san, unscale, inv);
+    store1<GD>(d.out, i, row ? rnd<GD>(x - mean) : x);
   }
 }
 

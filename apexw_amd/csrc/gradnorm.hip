@@ -21,6 +21,21 @@ APEXW_DEV float unit_sumsq(const apexw_tensor& t, int64_t start, int64_t cnt, bo
   const int lane = lane_id();
   const bool vec = !(t.flags & APEXW_FLAG_SCALAR) && (start % 8) == 0;
   float acc = 0.0f;
+  if (vec && cnt == 2048) {
+    // a whole 2048-element unit: the wave's four 8-element loads per lane are issued together
+    float g[4][8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) load8<GD>(t.g, start + k * 512 + lane * 8, g[k]);
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float x = san ? sanitize<GD>(g[k][j]) : g[k][j];
+        if (unscale) x = rnd<GD>(x * inv);
+        acc = fmaf(x, x, acc);
+      }
+    return wave_sum(acc);
+  }
   for (int64_t rel = (int64_t)lane * 8; rel < cnt; rel += 64 * 8) {
     const int64_t e0 = start + rel;
     const int c = (cnt - rel) < 8 ? (int)(cnt - rel) : 8;

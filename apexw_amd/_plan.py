@@ -259,6 +259,18 @@ class StepPlan:
         self.fast = fast
         self.d_units = torch.from_numpy(units.view(np.uint8)).to(self.device)
         self.d_unit_begin = torch.from_numpy(self.unit_begin).to(self.device)
+        # the step kernels' units: all but the factored rows' (apexw_factored_step steps
+        # those; the clip's norm pass still covers every unit).  Factored tensors are
+        # never full-block 8-bit tensors, so the fast prefix is unchanged.
+        fac_rows = self.factored[perm]
+        if fac_rows.any():
+            self._step_keep = ~fac_rows[units["tensor"]]
+            step_units = units[self._step_keep]
+            self.n_step_units = len(step_units)
+            self.d_step_units = torch.from_numpy(step_units.view(np.uint8)).to(self.device) \
+                if len(step_units) else self.d_units
+        else:
+            self._step_keep, self.n_step_units, self.d_step_units = None, total, self.d_units
         self.clip_ws = None
         self._fv_subsets = {}
         self.fv = self._fv_layout(tuple(int(i) for i in np.nonzero(self.factored[perm])[0])) \
@@ -422,9 +434,12 @@ class StepPlan:
         for units, step in groups:
             hp = self._hparams(lr, b1, b2, eps, wd, step, sr, sanitize, coef, seed, mode_cold, inv_scale)
             if units is None:
-                d_units, n_units, n_fast, n_fast32 = self.d_units, self.n_units, self.n_fast_units, self.n_fast_f32_units
+                d_units, n_units = self.d_step_units, self.n_step_units
+                n_fast, n_fast32 = self.n_fast_units, self.n_fast_f32_units
             else:
                 d_units, n_units, n_fast, n_fast32 = units
+            if n_units == 0:
+                continue
             if self.kind == "compact":
                 st = self._lib.apexw_compact_step(self.d_table.data_ptr(), len(self.params), d_units.data_ptr(),
                                                   n_units, ctypes_ref(hp), stream)
@@ -481,7 +496,9 @@ class StepPlan:
         for val in sorted(set(vals.tolist()), key=vals.tolist().index):
             keep = vals == val
             mask = np.repeat(keep, self.unit_counts)
-            sel = self.d_units.view(-1, 8)[torch.from_numpy(mask).to(self.device)].reshape(-1)
+            if self._step_keep is not None:
+                mask = mask[self._step_keep]
+            sel = self.d_step_units.view(-1, 8)[torch.from_numpy(mask).to(self.device)].reshape(-1)
             nb, nf = self.n_fast_units, self.n_fast_f32_units
             out.append(((sel, int(mask.sum()), int(mask[:nb].sum()), int(mask[nb:nb + nf].sum())), int(val)))
         return out

@@ -275,5 +275,12 @@ def test_factored_rows_and_launch(cpu_plans, prec):
         assert ends[1] == 0
     else:
         assert 0 < ends[0] < ends[1] == ends[2]
+    # the step kernels get only the other rows' units (the factored rows' are apexw_factored_step's)
+    steps = [c for c in cpu_plans.calls if c[0] in ("compact", "q8")]
+    assert len(steps) == 2
+    n_fac = sum(int(plan.unit_counts[int(r["tensor"])]) for r in fv)
+    assert steps[-1][1][3] == plan.n_units - n_fac == plan.n_step_units
+    step_units = plan.d_step_units.cpu().numpy().view(L.UNIT_DTYPE)[:plan.n_step_units]
+    assert not fac[step_units["tensor"]].any()
     assert hp["step"] == 2 and hp["flags"] & L.HP_FV_SANITIZE == (L.HP_FV_SANITIZE if prec == "8bit" else 0)
     assert hp["eps"] == pytest.approx(1e-8) and hp["mode"] == L.MODE_COLD

@@ -175,3 +175,21 @@ def test_step_hooks_match_torch_semantics():
     with pytest.raises(RuntimeError):
         opt.step()
     bad.remove()
+
+
+def test_bench_contract():
+    """bench.py: one GPU only (exit 2 with a message for --gpus N > 1, before any
+    device work); C3 is the default workload; every config names its workload and
+    the in-backward configs are 8-bit (the precision whose hooks they measure)."""
+    import subprocess
+    import sys
+    import bench
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2 and "one GPU" in r.stderr and r.stdout == ""
+    assert bench.CONFIGS["c3"]["workload"].startswith("C3 8-bit")
+    for name, cfg in bench.CONFIGS.items():
+        assert cfg["workload"] and cfg["shapes"], name
+        if cfg.get("backward"):
+            assert cfg["kwargs"]["precision"] == "8bit" and cfg["backward"] in ("hooks", "plain"), name

@@ -33,7 +33,7 @@ def _codes6(q):
     return torch.stack([(word >> (6 * i)) & 63 for i in range(4)], 1).reshape(-1)
 
 
-def _check(gpu_p, cpu_p, prev, gs, cs, tag):
+def _check(gpu_p, cpu_p, prev, gs, cs, tag, scale_rtol=1e-6, m_atol=None):
     got, ref = gpu_p.detach().cpu(), cpu_p.detach()
     if got.dtype == torch.bfloat16:
         # the update is rounded to bf16 before the subtraction, and a denominator a few
@@ -55,10 +55,14 @@ def _check(gpu_p, cpu_p, prev, gs, cs, tag):
     elif m_c.dtype == torch.int8:
         assert int((m_g.to(torch.int32) - m_c.to(torch.int32)).abs().max()) <= 1, f"{tag} int8 m"
     else:   # the lerp is elementwise and the fp32 result is rounded to nearest-even on both sides
-        assert int(bf16_ulp_diff(m_g.reshape(-1), m_c.reshape(-1)).max()) == 0, f"{tag} bf16 m"
+        if m_atol is None:
+            assert int(bf16_ulp_diff(m_g.reshape(-1), m_c.reshape(-1)).max()) == 0, f"{tag} bf16 m"
+        else:   # a reduction upstream of m: one bf16 ulp, plus its absolute error where it cancels
+            a, b = m_g.double(), m_c.double()
+            assert ((a - b).abs() <= 2.0 ** -7 * b.abs() + m_atol).all(), f"{tag} bf16 m"
     if "exp_avg_scales" in cs:
         a, b = gs["exp_avg_scales"].cpu().double(), cs["exp_avg_scales"].double()
-        assert ((a - b).abs() <= 1e-6 * b.abs()).all(), f"{tag} m scales"
+        assert ((a - b).abs() <= scale_rtol * b.abs()).all(), f"{tag} m scales"
 
 
 def _sync(gpu_p, cpu_p, gs, cs):
@@ -281,21 +285,22 @@ def test_reference_compact_factored_threshold_and_convergence():
 
 @pytest.mark.parametrize("prec", ["8bit", "compact"])
 @pytest.mark.parametrize("shape", [(1024, 512), (128, 4096)])      # 4096 columns: whole-tile statistics
-def test_factored_with_centralization_and_clip_matches_oracle(prec, shape):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_factored_with_centralization_and_clip_matches_oracle(prec, shape, dtype):
     """Grad centralization and the global-norm clip prepare the grads of factored
     tensors as of any other (apexw/optimizer.py:204-258), beside an ordinary tensor."""
     _need_gpu()
     from apexw_amd import ApexW
     from oracle.optim import OracleApexW
     gen = torch.Generator().manual_seed(9)
-    host = [(torch.randn(shape, generator=gen) * 0.02).bfloat16(), (torch.randn(4096, generator=gen) * 0.02).bfloat16()]
+    host = [(torch.randn(shape, generator=gen) * 0.02).to(dtype), (torch.randn(4096, generator=gen) * 0.02).to(dtype)]
     opts = dict(lr=1e-2, weight_decay=0.1, precision=prec, factored_v=True, stochastic_rounding=False,
                 grad_centralization=True, clip_grad_norm=0.5)
     gps = [nn.Parameter(h.cuda()) for h in host]
     cps = [nn.Parameter(h.clone()) for h in host]
     gopt, copt = ApexW(gps, **opts), OracleApexW(cps, **opts)
     for step in range(3):
-        gs = [(torch.randn(h.shape, generator=gen) * 1e-2).bfloat16() for h in host]
+        gs = [(torch.randn(h.shape, generator=gen) * 1e-2).to(dtype) for h in host]
         for gp, cp, g in zip(gps, cps, gs):
             gp.grad, cp.grad = g.cuda(), g.clone()
         prev = cps[0].detach().clone()
@@ -303,7 +308,14 @@ def test_factored_with_centralization_and_clip_matches_oracle(prec, shape):
         copt.step()
         torch.cuda.synchronize()
         st_g, st_c = gopt.state[gps[0]], copt.state[cps[0]]
-        _check(gps[0], cps[0], prev, st_g, st_c, f"{prec} gc+clip step {step}")
+        # fp32 grads: the clip coefficient (an fp32 norm over 0.5 M elements) and the
+        # centralization's row means are reductions in another order than the oracle's:
+        # a few fp32 ulps, which every m value and scale carries; where g is close to its
+        # row mean the subtraction cancels, so m is held to 1 bf16 ulp plus (1-b1) times
+        # the mean's absolute error (~2^-24 * 512 * 1e-2)
+        f32 = dtype == torch.float32
+        _check(gps[0], cps[0], prev, st_g, st_c, f"{prec} gc+clip step {step}",
+               scale_rtol=2e-6 if f32 else 1e-6, m_atol=1e-10 if f32 else None)
         _sync(gps[0], cps[0], st_g, st_c)
 
 

@@ -156,8 +156,7 @@ template <int GD, bool PLAIN> APEXW_DEV float fv_sq(float g, const FvCtx& c, boo
 // depend on which path a pass took.
 template <int GD, bool PLAIN>
 APEXW_DEV void fv_stats_band(const apexw_tensor& t, const apexw_fv_tensor& e, int64_t band, float* ws,
-                             const FvCtx& c) {
-  __shared__ float s_row[4][kBand];
+                             const FvCtx& c, float (*s_row)[kBand], float (*s_t)[kBand][65]) {
   const FvWs w = fv_ws(ws, e);
   const apexw_hparams& hp = *c.hp;
   const bool fs = hp.flags & APEXW_HP_FV_SANITIZE;
@@ -223,12 +222,18 @@ APEXW_DEV void fv_stats_band(const apexw_tensor& t, const apexw_fv_tensor& e, in
     for (int j = 0; j < 8; ++j)
       if (j < cnt) w.part[band * cols + cb + j] = cacc[j];
   }
-  // rows: reduce the register row partials across each wave, then across the
-  // workgroup, then the row EMA
+  // rows: the register row partials go through LDS transposed (row-major with a
+  // 65-float stride, conflict-free both ways); lane r < 32 of each wave sums its
+  // row over the wave's 64 lanes in lane order, then the waves' sums are combined
+  // and the row EMA applied
 #pragma unroll
-  for (int i = 0; i < kBand; ++i) {
-    const float s = wave_sum(racc[i]);
-    if (lane == 0) s_row[wave][i] = s;
+  for (int i = 0; i < kBand; ++i) s_t[wave][i][lane] = racc[i];
+  __syncthreads();
+  if (lane < kBand) {
+    float rsum = 0.0f;
+#pragma unroll 16
+    for (int l = 0; l < 64; ++l) rsum += s_t[wave][lane][l];
+    s_row[wave][lane] = rsum;
   }
   __syncthreads();
   if (wave == 0) {
@@ -260,8 +265,11 @@ __global__ __launch_bounds__(256) void fv_stats_kernel(const apexw_tensor* __res
   c.hp = &hp;
   c.coef = (hp.flags & APEXW_HP_CLIP) ? *hp.clip_coef : 1.0f;
   const int64_t lb = band - e.band0;
-  if (((t.flags >> APEXW_FLAG_GDT_SHIFT) & 3u) == APEXW_F32) fv_stats_band<APEXW_F32, PLAIN>(t, e, lb, ws, c);
-  else fv_stats_band<APEXW_BF16, PLAIN>(t, e, lb, ws, c);
+  // one copy of the LDS for both grad dtypes' instantiations
+  __shared__ float s_row[4][kBand];
+  __shared__ float s_t[4][kBand][65];
+  if (((t.flags >> APEXW_FLAG_GDT_SHIFT) & 3u) == APEXW_F32) fv_stats_band<APEXW_F32, PLAIN>(t, e, lb, ws, c, s_row, s_t);
+  else fv_stats_band<APEXW_BF16, PLAIN>(t, e, lb, ws, c, s_row, s_t);
 }
 
 // ---------------------------------------------------------------------------

@@ -489,7 +489,9 @@ class StepPlan:
 
     def _split_by_step(self):
         raw = self._steps_np
-        if raw.size == 1 or raw.min() == raw.max():
+        if raw.size == 1 or raw.min() == raw.max() or self.n_step_units == 0:
+            # one launch (or none: every tensor is factored and apexw_factored_step
+            # buckets those by their own step counts)
             return [(None, int(raw[0]))]
         vals = raw[self.perm]
         out = []

@@ -476,6 +476,11 @@ class ApexW(Optimizer):
             return
         prec = S.normalize_precision(group.get("precision", "compact"))
         state = self.state[p]
+        if state.get("is_factored_v", False):
+            # the reference's per-parameter update has no factored branch (it fails on the
+            # missing exp_avg_sq); refuse before touching the state or the step counter
+            raise RuntimeError("enable_fused_backward cannot step a parameter with factored_v state "
+                               "(exp_avg_sq_row / exp_avg_sq_col); use step()")
         if len(state) == 0:
             if prec == "8bit":
                 S.ensure_8bit_state(state, p, group)

@@ -170,6 +170,9 @@ class OracleApexW:
             if st.get("is_factored_v", False):
                 st["step"].add_(1)
                 self._factored(p, g, st, int(st["step"].item()), self._inv(scale), sanitize=True)
+        # the cached plan holds every parameter with a grad, factored ones included
+        # (FastExecutionPlan(params=params_with_grad, factored_mask=...), optimizer.py:4005-4020)
+        plan_params = list(plist)
         keep = [i for i, st in enumerate(sts) if not st.get("is_factored_v", False)]
         plist, grads, sts = [plist[i] for i in keep], [grads[i] for i in keep], [sts[i] for i in keep]
         grads = self._unscale(grads, scale)
@@ -184,7 +187,7 @@ class OracleApexW:
                                   [i[2]["exp_avg"] for i in items], [i[2]["exp_avg_sq"] for i in items],
                                   step=items[0][2]["step"].item(), is_quad=quad,
                                   stochastic=grp["stochastic_rounding"], **kw)
-        self._plan = {"kind": "foreach", "params": plist}
+        self._plan = {"kind": "foreach", "params": plan_params}
 
     def _is_quad(self, p):
         v = self.state[p]["exp_avg_sq"]

@@ -194,3 +194,20 @@ def test_fused_backward_hooks_count_passes(monkeypatch):
     opt.disable_fused_backward()
     assert not opt._fused_backward_handles and not opt._fused_backward_enabled
     R.restore_all_downcast_params()
+
+
+@pytest.mark.parametrize("prec", ["8bit", "compact"])
+def test_fused_backward_refuses_factored_state(prec):
+    """A parameter that step() gave factored-v state cannot take the per-parameter
+    in-backward update (the reference's has no factored branch): a clear error,
+    raised before the state or the step counter changes."""
+    p = nn.Parameter(torch.randn(256, 512))
+    opt = ApexW([p], precision=prec, factored_v=True)
+    st = opt.state[p]
+    st.update(step=torch.tensor(3.0), is_factored_v=True, exp_avg=torch.zeros(256, 512, dtype=torch.bfloat16),
+              exp_avg_sq_row=torch.zeros(256), exp_avg_sq_col=torch.zeros(512))
+    p.grad = torch.zeros_like(p)
+    with pytest.raises(RuntimeError, match="factored_v"):
+        opt._step_single_param_fused(p, opt.param_groups[0])
+    assert float(st["step"]) == 3.0
+    R.restore_all_downcast_params()

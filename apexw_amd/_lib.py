@@ -13,7 +13,7 @@ import numpy as np
 
 from ._build import LIB_PATH
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 # dtype codes
 F32, BF16, F16, U8, I8 = 0, 1, 2, 3, 4
@@ -43,7 +43,10 @@ HP_UNSCALE = 1 << 6
 HP_FV_SANITIZE = 1 << 7
 
 STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported dtype combination", 3: "launch failed",
-          4: "misaligned pointer"}
+          4: "misaligned pointer", 5: "exceeds the fixed workspace of the allocation-free entry point"}
+ERR_SIZE = 5
+NOALLOC_CLIP_MAX_UNITS = 1 << 21
+NOALLOC_CLIP_MAX_TENSORS = 1 << 17
 
 TENSOR_DTYPE = np.dtype([
     ("p", np.uint64), ("g", np.uint64), ("m", np.uint64), ("v", np.uint64),
@@ -107,6 +110,7 @@ SIGNATURES = {
     "apexw_compact_step": (ctypes.c_int, [_vp, _i32, _vp, _i64, _HP, _vp]),
     "apexw_q8_step": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _i64, _HP, _vp]),
     "apexw_grad_clip_coef": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _vp, _vp, _vp, _f32, _f32, _u32, _vp, _vp]),
+    "apexw_grad_clip_coef_noalloc": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _vp, _f32, _f32, _u32, _vp, _vp]),
     "apexw_gemm_nt_bf16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                           _i32, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _vp]),
     "apexw_check_grad_prep": (ctypes.c_int, [_vp]),

@@ -10,6 +10,8 @@
 //   1. one wavefront per work unit of the chunk table -> sum of squares
 //   2. one wavefront per tensor sums its (contiguous) units -> rounded norm
 //   3. one workgroup combines the tensor norms -> coefficient
+#include <mutex>
+
 #include "common.h"
 
 namespace {
@@ -215,6 +217,53 @@ int apexw_launch_grad_prep(const apexw_grad_prep* preps, const apexw_unit* units
   const int64_t want = n_units < 65536 ? n_units : 65536;
   hipLaunchKernelGGL(grad_prep_kernel, dim3((unsigned)want), dim3(256), 0, stream, preps, units, n_units, inv, flags);
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
+}
+
+int apexw_launch_clip(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,
+                      int64_t unit_size, const int64_t* unit_begin, float* unit_partial, float* tensor_norm,
+                      float clip, float inv, uint32_t flags, float* coef, hipStream_t stream);
+
+// ---------------------------------------------------------------------------
+// Allocation-free clip coefficient: the per-unit partials and per-tensor norms
+// live in this file-scope device array instead of caller workspace.  Each GPU
+// holds its own copy; its device address is looked up once per device with
+// hipGetSymbolAddress (the array's name is only a host-side stand-in).
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) float scratch[APEXW_NOALLOC_CLIP_MAX_UNITS + APEXW_NOALLOC_CLIP_MAX_TENSORS];
+
+namespace {
+
+constexpr int kScratchDevices = 64;
+std::once_flag g_scratch_once[kScratchDevices];
+float* g_scratch_ptr[kScratchDevices];
+
+// Device address of `scratch` on the current device, or nullptr if it cannot be had.
+float* scratch_on_current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchDevices) return nullptr;
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* ptr = nullptr;
+    // runs on the calling thread, whose current device is dev
+    g_scratch_ptr[dev] = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) == hipSuccess ? (float*)ptr : nullptr;
+  });
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+extern "C" int apexw_grad_clip_coef_noalloc(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units,
+                                            int64_t n_units, int64_t unit_size, const int64_t* unit_begin,
+                                            float clip, float grad_inv_scale, uint32_t flags, float* coef,
+                                            void* stream) {
+  if (!tensors || !units || !unit_begin || !coef) return APEXW_ERR_ARG;
+  if (n_tensors <= 0 || n_units < 0 || unit_size < 0 || !(clip > 0.0f)) return APEXW_ERR_ARG;
+  if ((flags & APEXW_HP_UNSCALE) && !(grad_inv_scale > 0.0f)) return APEXW_ERR_ARG;
+  if (n_units > APEXW_NOALLOC_CLIP_MAX_UNITS || n_tensors > APEXW_NOALLOC_CLIP_MAX_TENSORS) return APEXW_ERR_SIZE;
+  float* ptr = scratch_on_current_device();
+  if (!ptr) return APEXW_ERR_LAUNCH;
+  return apexw_launch_clip(tensors, n_tensors, units, n_units, unit_size, unit_begin, ptr,
+                           ptr + APEXW_NOALLOC_CLIP_MAX_UNITS, clip, grad_inv_scale, flags, coef,
+                           (hipStream_t)stream);
 }
 
 int apexw_launch_clip(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,

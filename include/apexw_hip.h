@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define APEXW_ABI_VERSION 10
+#define APEXW_ABI_VERSION 11
 
 /* status codes */
 enum apexw_status {
@@ -47,7 +47,8 @@ enum apexw_status {
   APEXW_ERR_ARG = 1,      /* invalid argument (null pointer, bad size, bad flag) */
   APEXW_ERR_DTYPE = 2,    /* unsupported dtype combination */
   APEXW_ERR_LAUNCH = 3,   /* the HIP runtime rejected the launch */
-  APEXW_ERR_ALIGN = 4     /* pointer alignment the kernel requires is not met */
+  APEXW_ERR_ALIGN = 4,    /* pointer alignment the kernel requires is not met */
+  APEXW_ERR_SIZE = 5      /* the work exceeds a fixed-size workspace (allocation-free entry points) */
 };
 
 /* element dtype codes */
@@ -252,6 +253,27 @@ int apexw_grad_clip_coef(const apexw_tensor* tensors, int32_t n_tensors,
                          const apexw_unit* units, int64_t n_units, int64_t unit_size,
                          const int64_t* unit_begin, float* unit_partial, float* tensor_norm,
                          float clip, float grad_inv_scale, uint32_t flags, float* coef, void* stream);
+
+/*
+ * apexw_grad_clip_coef without workspace arguments, allocating nothing: the
+ * per-unit partial sums and per-tensor norms live in a fixed device array of
+ * the library ((APEXW_NOALLOC_CLIP_MAX_UNITS + APEXW_NOALLOC_CLIP_MAX_TENSORS)
+ * floats, 8.5 MiB per GPU, held until the process ends).  Same kernels, same
+ * result as apexw_grad_clip_coef.  Returns APEXW_ERR_SIZE, before enqueueing
+ * anything, when n_units or n_tensors exceeds its limit.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (two streams, or two host threads) race.
+ * Nothing in the array needs to start at zero (every entry is written before
+ * it is read within one call).
+ */
+#define APEXW_NOALLOC_CLIP_MAX_UNITS (1 << 21)
+#define APEXW_NOALLOC_CLIP_MAX_TENSORS (1 << 17)
+int apexw_grad_clip_coef_noalloc(const apexw_tensor* tensors, int32_t n_tensors,
+                                 const apexw_unit* units, int64_t n_units, int64_t unit_size,
+                                 const int64_t* unit_begin, float clip, float grad_inv_scale,
+                                 uint32_t flags, float* coef, void* stream);
 
 /*
  * Gradient preparation of _prepare_grads (apexw/optimizer.py:204-258) for a

@@ -426,13 +426,17 @@ class StepPlan:
             self._steps_np[:] = np.asarray(steps, dtype=np.float32)
         # The reference's replayed compact step takes the bias correction of the
         # first counter for the whole group (optimizer.py:1082-1090); every other
-        # path uses each parameter's own count.
+        # path uses each parameter's own count.  SR: the 8-bit step and the
+        # per-parameter update read each parameter's state flag (optimizer.py:4377,
+        # :2419), the compact step and the in-backward batches the group's (:3789,
+        # :4004, :2286).
+        sr_t = self._state_sr() if self.kind == "q8" and (self.single or not self.hooked) else None
         if mode_cold or self.native or self.kind == "q8":
-            groups = self._split_by_step()
+            groups = self._split_launches(sr_t, sr)
         else:
-            groups = [(None, int(self._steps_np[0]))]
-        for units, step in groups:
-            hp = self._hparams(lr, b1, b2, eps, wd, step, sr, sanitize, coef, seed, mode_cold, inv_scale)
+            groups = [(None, int(self._steps_np[0]), sr)]
+        for units, step, sr_l in groups:
+            hp = self._hparams(lr, b1, b2, eps, wd, step, sr_l, sanitize, coef, seed, mode_cold, inv_scale)
             if units is None:
                 d_units, n_units = self.d_step_units, self.n_step_units
                 n_fast, n_fast32 = self.n_fast_units, self.n_fast_f32_units
@@ -449,23 +453,27 @@ class StepPlan:
             L.check(st, "apexw step")
         if self.fv is not None:
             replay_step = None if (mode_cold or self.native or self.kind == "q8") else groups[0][1]
-            self._factored_launch(lr, b1, b2, eps, wd, sr, sanitize, coef, seed, mode_cold, inv_scale, replay_step,
+            self._factored_launch(lr, b1, b2, eps, wd, sanitize, coef, seed, mode_cold, inv_scale, replay_step,
                                   stream)
         self.cold_done = True
 
-    def _factored_launch(self, lr, b1, b2, eps, wd, sr, sanitize, coef, seed, cold, inv_scale, replay_step, stream):
-        """Step the factored-v rows: one apexw_factored_step per distinct step count
-        (the replayed compact plan uses its first counter for every tensor,
-        optimizer.py:1141-1163)."""
+    def _state_sr(self):
+        return np.fromiter((bool(st.get("stochastic_rounding", True)) for st in self.states), dtype=bool,
+                           count=len(self.states))
+
+    def _factored_launch(self, lr, b1, b2, eps, wd, sanitize, coef, seed, cold, inv_scale, replay_step, stream):
+        """Step the factored-v rows: one apexw_factored_step per distinct (step count,
+        SR flag).  The replayed compact plan uses its first counter for every
+        tensor (optimizer.py:1141-1163); SR follows each parameter's state flag
+        (_apply_factored_v_int8_update's callers, optimizer.py:5426, :4377)."""
         rows = self.fv["rows"]
-        if replay_step is not None:
-            buckets = {replay_step: list(rows)}
-        else:
-            vals = self.steps.numpy()[self.perm]
-            buckets = {}
-            for d in rows:
-                buckets.setdefault(int(vals[d]), []).append(d)
-        for step, members in buckets.items():
+        vals = self.steps.numpy()[self.perm]
+        srs = self._state_sr()[self.perm]
+        buckets = {}
+        for d in rows:
+            key = (replay_step if replay_step is not None else int(vals[d]), bool(srs[d]))
+            buckets.setdefault(key, []).append(d)
+        for (step, sr), members in buckets.items():
             if len(members) == len(rows):
                 fv = self.fv
             else:
@@ -487,22 +495,32 @@ class StepPlan:
                 fv["range_ends"].ctypes.data, fv["ws"].data_ptr(), ctypes_ref(hp), stream)
             L.check(st, "apexw_factored_step")
 
-    def _split_by_step(self):
+    def _split_launches(self, sr_t, sr_default):
+        """Step-kernel launches as (units or None for all, step count, SR): one per
+        distinct (step count, SR flag) among the plan's tensors.  sr_t: each
+        parameter's SR flag, or None when the group's flag applies to all."""
         raw = self._steps_np
-        if raw.size == 1 or raw.min() == raw.max() or self.n_step_units == 0:
+        sr_uniform = sr_t is None or bool(sr_t.all()) or not bool(sr_t.any())
+        sr0 = sr_default if sr_t is None else bool(sr_t[0])
+        if ((raw.size == 1 or raw.min() == raw.max()) and sr_uniform) or self.n_step_units == 0:
             # one launch (or none: every tensor is factored and apexw_factored_step
-            # buckets those by their own step counts)
-            return [(None, int(raw[0]))]
+            # buckets those itself)
+            return [(None, int(raw[0]), sr0)]
         vals = raw[self.perm]
+        srp = np.full(len(vals), sr_default, dtype=bool) if sr_t is None else sr_t[self.perm]
+        keys = list(zip(vals.tolist(), srp.tolist()))
         out = []
-        for val in sorted(set(vals.tolist()), key=vals.tolist().index):
-            keep = vals == val
+        for val, srv in sorted(set(keys), key=keys.index):
+            keep = (vals == val) & (srp == srv)
             mask = np.repeat(keep, self.unit_counts)
             if self._step_keep is not None:
                 mask = mask[self._step_keep]
+            if not mask.any():
+                continue
             sel = self.d_step_units.view(-1, 8)[torch.from_numpy(mask).to(self.device)].reshape(-1)
             nb, nf = self.n_fast_units, self.n_fast_f32_units
-            out.append(((sel, int(mask.sum()), int(mask[:nb].sum()), int(mask[nb:nb + nf].sum())), int(val)))
+            out.append(((sel, int(mask.sum()), int(mask[:nb].sum()), int(mask[nb:nb + nf].sum())), int(val),
+                        bool(srv)))
         return out
 
     def _hparams(self, lr, b1, b2, eps, wd, step, sr, sanitize, coef, seed, cold, inv_scale=None):

@@ -524,7 +524,6 @@ APEXW_DEV void q8_block_fast(const apexw_tensor& t, uint32_t tix, uint32_t blk, 
     rs = mix32(key + (blk << 6) + (uint32_t)lane) | 1u;
   }
   const bool prep = hf & (APEXW_HP_SANITIZE | APEXW_HP_CLIP | APEXW_HP_UNSCALE);
-  const float msb1 = ms_old * hp.beta1;  // dequantisation scale folded into the momentum decay
 
   float mnew[4][8], vq[4][2];
   uint32_t hbits[4][8];   // this pass's random words
@@ -599,15 +598,16 @@ APEXW_DEV void q8_block_fast(const apexw_tensor& t, uint32_t tix, uint32_t blk, 
           s2[q] = fmaf(g[b + 3], g[b + 3], t);
         }
       }
-      // m' = lerp(dequant(m), g, 1-b1) = code*ms*b1 + (1-b1)*g, lookahead = b1*m' + (1-b1)*g
+      // m' = lerp(dequant(m), g, 1-b1) and the lookahead lerp(g, m', b1), rounded as torch's
+      // lerp: the SNR gain switches on the sign of m' g, so m' must be the reference's value
+      // to the last bit (an algebraically equal form can round a near-zero m' to the other sign)
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
         const float2 pr = c.pair[(mw[k] >> (8 * b)) & 0xFFu];
-        const float wg0 = hp.one_minus_beta1 * g[2 * b], wg1 = hp.one_minus_beta1 * g[2 * b + 1];
-        m[2 * b] = fmaf(pr.x, msb1, wg0);
-        m[2 * b + 1] = fmaf(pr.y, msb1, wg1);
-        look[2 * b] = fmaf(hp.beta1, m[2 * b], wg0);
-        look[2 * b + 1] = fmaf(hp.beta1, m[2 * b + 1], wg1);
+        m[2 * b] = lerp_to(pr.x * ms_old, g[2 * b], hp.lerp_coef, lerp_hi);
+        m[2 * b + 1] = lerp_to(pr.y * ms_old, g[2 * b + 1], hp.lerp_coef, lerp_hi);
+        look[2 * b] = lerp_to(g[2 * b], m[2 * b], hp.look_coef, look_hi);
+        look[2 * b + 1] = lerp_to(g[2 * b + 1], m[2 * b + 1], hp.look_coef, look_hi);
       }
 #pragma unroll
       for (int q = 0; q < 2; ++q) {

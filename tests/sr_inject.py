@@ -122,9 +122,11 @@ class SRCheck:
         self.stats = {k: Stat() for k in ("bf16", "nf4", "int8", "logu8")}
         self.captured = {"nf4": [], "int8": [], "logu8": []}
 
-    def target(self, oracle_tensor, gpu_result):
+    def target(self, oracle_tensor, gpu_result, label="bf16"):
+        """label: an extra statistic for this target's stores ("bf16/<label>"), beside
+        the pooled "bf16" one."""
         assert oracle_tensor.is_contiguous() and oracle_tensor.dtype == gpu_result.dtype
-        self.targets.append((oracle_tensor, gpu_result.detach().cpu().contiguous()))
+        self.targets.append((oracle_tensor, gpu_result.detach().cpu().contiguous(), label))
 
     def reset_captures(self):
         self.captured = {"nf4": [], "int8": [], "logu8": []}
@@ -142,18 +144,18 @@ class SRCheck:
 
     def _gpu_for(self, dst):
         esize = dst.element_size()
-        for t, gpu in self.targets:
+        for t, gpu, label in self.targets:
             lo = t.data_ptr()
             if t.dtype == dst.dtype and lo <= dst.data_ptr() < lo + t.numel() * esize:
                 off = (dst.data_ptr() - lo) // esize
-                return gpu.reshape(-1)[off:off + dst.numel()].view(dst.shape)
+                return gpu.reshape(-1)[off:off + dst.numel()].view(dst.shape), label
         raise AssertionError("an SR store into a tensor with no registered GPU result")
 
     def _store(self, dst, src_f32, stochastic):
         if not stochastic or dst.dtype == torch.float32:
             return self._orig[0](dst, src_f32, stochastic)
         assert dst.dtype == torch.bfloat16 and dst.is_contiguous()
-        gpu = self._gpu_for(dst)
+        gpu, label = self._gpu_for(dst)
         x = src_f32.float().reshape(-1)
         lo, hi = _bf16_bracket(x)
         # the GPU's pre-rounding value may differ by a few fp32 ulps of the operands
@@ -164,9 +166,10 @@ class SRCheck:
         lo_w, _ = _bf16_bracket(x - slack)
         _, hi_w = _bf16_bracket(x + slack)
         near = ((x - lo) <= slack) | ((hi - x) <= slack)
-        self.stats["bf16"].add(*offsets(gpu.reshape(-1).float(), x, lo, hi,
-                                        f"bf16 store (dst {tuple(dst.shape)}, before {dst.reshape(-1)[:1].tolist()})",
-                                        lo_w, hi_w, near))
+        res = offsets(gpu.reshape(-1).float(), x, lo, hi, f"bf16 store (dst {tuple(dst.shape)})", lo_w, hi_w, near)
+        self.stats["bf16"].add(*res)
+        if label != "bf16":
+            self.stats.setdefault(f"bf16/{label}", Stat()).add(*res)
         dst.copy_(gpu)
 
     def _nf4(self, x, block, old_scales=None, stochastic=False):

@@ -147,3 +147,42 @@ def test_compact_bf16_sr_unbiased():
     assert float(verr.abs().max()) <= 1.0 + 1e-6 and float(perr.abs().max()) <= 1.0 + 1e-3
     _unbiased(verr, "compact bf16 v SR")
     _unbiased(perr, "compact bf16 param SR")
+
+
+# ---------------------------------------------------------------------------
+# SR beyond the first step, per kernel branch: three round-to-nearest steps, then
+# two SR steps from the state they left, each against the oracle run from the
+# GPU's pre-step state (tests/sr_inject.py: every SR result in the bracket of the
+# exact pre-rounding value, |z| < 3 signed and by magnitude over >= 1e7 elements,
+# the deterministic parts at the round-to-nearest bars).
+# ---------------------------------------------------------------------------
+SR_BRANCHES = [
+    # name, precision, param dtype, shapes, extra kwargs, SR outputs with >= 1e7 elements
+    ("nf4 fast kernel, partial last blocks", "8bit", torch.bfloat16, [(4000, 1037)] * 10, {},
+     ("bf16", "nf4", "logu8")),
+    ("nf4 generic-order quad (<= 262144 elements)", "8bit", torch.bfloat16, [(256, 1024)] * 160, {},
+     ("bf16", "nf4", "logu8")),
+    ("int8 + log-u8, general kernel, generic order", "8bit", torch.bfloat16, [(10240,)] * 1024, {},
+     ("int8", "logu8")),
+    ("int8 + log-u8, general kernel, chunked order", "8bit", torch.bfloat16, [(1000002,)] * 11, {},
+     ("bf16", "int8", "logu8")),
+    ("fp32 parameters, nf4 codes", "8bit", torch.float32, [(4096, 10240)], {}, ("nf4", "logu8")),
+    # a homogeneous group (every state in the parameter dtype and size) takes the
+    # reference's torch._fused_adamw_ path, which has no SR; the quad tensor makes the
+    # group mixed, so the non-quad ones (numel % 4 != 0) take the foreach path with SR v
+    ("compact non-quad bf16 v with SR", "compact", torch.bfloat16, [(1000001,)] * 10 + [(2048, 1024)],
+     {"force_compact_v": True}, ("bf16",)),
+]
+
+
+@pytest.mark.parametrize("name,prec,dtype,shapes,extra,kinds", SR_BRANCHES, ids=[b[0] for b in SR_BRANCHES])
+def test_sr_branch_after_rne_steps(name, prec, dtype, shapes, extra, kinds):
+    _need_gpu()
+    from test_gpu_configs import KW, _drive
+    print(f"SR branch: {name}", flush=True)
+    kw = dict(KW, precision=prec, **extra)
+    stats = _drive(name, shapes, dtype, kw, [(i, None) for i in range(len(shapes))], 5, True,
+                   seed=sum(map(ord, name)) % 10007, sr_from=3)
+    for k in kinds:
+        st = stats[k]
+        assert st.n >= 10_000_000 and abs(st.z) < 3 and abs(st.z_mag) < 3, (k, st)

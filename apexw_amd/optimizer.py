@@ -33,8 +33,6 @@ from . import runtime as R
 from . import state as S
 from ._plan import StepPlan
 
-R.install()
-
 AUTO_8BIT_MIN_TENSORS = 8          # optimizer.py:2087
 AUTO_8BIT_MIN_NUMEL = 524_288
 DOWNCAST_MIN_NUMEL = 1024          # optimizer.py:2100
@@ -310,10 +308,10 @@ class ApexW(Optimizer):
                     total += p.numel()
         if not force and (len(trainable) < AUTO_8BIT_MIN_TENSORS or total < AUTO_8BIT_MIN_NUMEL):
             return
-        if torch.cuda.is_available():
-            torch.backends.cuda.matmul.allow_tf32 = True
-            torch.backends.cudnn.allow_tf32 = True
-            torch.backends.cudnn.benchmark = True
+        # the restore rules and the AMP scale detection the in-backward steps rely on
+        # (torch patches, installed once, only when this path turns on); the reference's
+        # process-wide TF32 / cuDNN benchmark settings are not taken over
+        R.install()
         converted = False
         with torch.no_grad():
             for p, _ in trainable:

@@ -13,8 +13,11 @@ the same for ``apexw_amd``:
 * AMP detection for the in-backward steps: ``GradScaler.scale`` records the
   scale of the running backward (the in-backward steps unscale with it),
   ``GradScaler.update`` forgets it; with fp16 parameters in play the scale is
-  clamped to 256.  ``GradScaler._unscale_grads_`` accepts fp16 grads for
-  optimizers that unscale inside their step.
+  clamped to 256.
+
+``install()`` applies these patches once per process, and only when an 8-bit
+ApexW turns its in-backward steps on (the reference patches at import); an
+application that never takes that path sees torch unchanged.
 """
 
 import weakref
@@ -76,7 +79,8 @@ def restore_all_downcast_params():
 
 
 def install():
-    """Patch torch once per process (optimizer.py:1385-1507)."""
+    """Patch torch once per process (the patches of optimizer.py:1385-1507 that the
+    in-backward steps need)."""
     global _installed
     if _installed:
         return
@@ -91,12 +95,7 @@ def _patch_grad_scaler():
     from torch.amp.grad_scaler import GradScaler
     if getattr(GradScaler, "_apexw_amd_patched", False):
         return
-    orig_unscale, orig_scale, orig_update = GradScaler._unscale_grads_, GradScaler.scale, GradScaler.update
-
-    def _unscale_grads_(self, optimizer, inv_scale, found_inf, allow_fp16=False):
-        if getattr(optimizer, "_step_supports_amp_scaling", False):
-            allow_fp16 = True
-        return orig_unscale(self, optimizer, inv_scale, found_inf, allow_fp16)
+    orig_scale, orig_update = GradScaler.scale, GradScaler.update
 
     def scale(self, outputs):
         global amp_scaled_this_backward, last_amp_scale
@@ -119,7 +118,6 @@ def _patch_grad_scaler():
         last_amp_scale = None
         return res
 
-    GradScaler._unscale_grads_ = _unscale_grads_
     GradScaler.scale = scale
     GradScaler.update = update
     GradScaler._apexw_amd_patched = True

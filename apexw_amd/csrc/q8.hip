@@ -28,6 +28,7 @@ static __host__ __device__ inline bool apexw_q8_fast_ok(uint32_t flags, uint32_t
 namespace {
 
 constexpr int kWaves = 4;
+constexpr int64_t kFastChunk = 64;   // units per workgroup pass of the full-block kernels
 
 struct Q8Ctx {
   const apexw_hparams* hp;
@@ -462,62 +463,82 @@ APEXW_DEV void q8_block(const apexw_tensor& t, uint32_t tix, uint32_t blk, const
 //    rounding; NF4 codes come from the signed fractional-index table:
 //    code = (G(x) + r12) >> 12, two codes per 32-bit integer add, gathered
 //    into bytes with v_perm_b32.
-template <int PD, bool SR, bool FULL, bool GENERIC>
-APEXW_DEV void q8_block_fast(const apexw_tensor& t, uint32_t tix, uint32_t blk, const Q8Ctx& c) {
-  const apexw_hparams& hp = *c.hp;
-  const uint32_t hf = hp.flags, tf = t.flags;
-  const int lane = lane_id();
-  const int64_t start = (int64_t)blk * 2048;
-  const float ms_old = t.m_scale[blk];
-  const float vs_old = t.v_scale[blk];
-  const float decay = (tf & APEXW_FLAG_WD) ? hp.wd_factor : 1.0f;
-  const bool lerp_hi = hf & APEXW_HP_LERP_HI, look_hi = hf & APEXW_HP_LOOK_HI;
-
-  // p and g: 8 elements per lane per k; one 16-byte word for bf16, two for fp32
-  constexpr int PW = PD == APEXW_F32 ? 2 : 1;
+// The loads of one fast-path block: p and g (8 elements per lane per k), the NF4
+// and log-uint8 code words and the block's two scales.
+template <int PD> struct FastRaw {
+  static constexpr int PW = PD == APEXW_F32 ? 2 : 1;   // 16-byte words of p / g per lane per k
   u32x4 pw[4][PW], gw[4][PW];
   uint32_t mw[4], vw[4];
   int cnt[4];
+  float ms_old, vs_old;
+};
+
+template <int PD, bool FULL>
+APEXW_DEV void q8_fast_load(const apexw_tensor& t, uint32_t blk, FastRaw<PD>& r) {
+  constexpr int PW = FastRaw<PD>::PW;
+  const int lane = lane_id();
+  const int64_t start = (int64_t)blk * 2048;
+  r.ms_old = t.m_scale[blk];
+  r.vs_old = t.v_scale[blk];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int64_t e = start + k * 512 + lane * 8;
     const auto pp = APEXW_GLOBAL(const u32x4, (const char*)t.p + e * Elem<PD>::bytes);
     const auto gp = APEXW_GLOBAL(const u32x4, (const char*)t.g + e * Elem<PD>::bytes);
     if constexpr (FULL) {
-      cnt[k] = 8;
+      r.cnt[k] = 8;
 #pragma unroll
       for (int h = 0; h < PW; ++h) {
-        pw[k][h] = __builtin_nontemporal_load(pp + h);
-        gw[k][h] = __builtin_nontemporal_load(gp + h);
+        r.pw[k][h] = __builtin_nontemporal_load(pp + h);
+        r.gw[k][h] = __builtin_nontemporal_load(gp + h);
       }
-      mw[k] = __builtin_nontemporal_load(APEXW_GLOBAL(const uint32_t, (const uint8_t*)t.m + (e >> 1)));
-      vw[k] = __builtin_nontemporal_load(APEXW_GLOBAL(const uint16_t, (const uint8_t*)t.v + (e >> 2)));
+      r.mw[k] = __builtin_nontemporal_load(APEXW_GLOBAL(const uint32_t, (const uint8_t*)t.m + (e >> 1)));
+      r.vw[k] = __builtin_nontemporal_load(APEXW_GLOBAL(const uint16_t, (const uint8_t*)t.v + (e >> 2)));
     } else {
       // numel % 4 == 0 for quad-v tensors, so a lane holds 0, 4 or 8 elements
-      cnt[k] = e >= t.n ? 0 : (t.n - e >= 8 ? 8 : 4);
+      r.cnt[k] = e >= t.n ? 0 : (t.n - e >= 8 ? 8 : 4);
       const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
-      for (int h = 0; h < PW; ++h) { pw[k][h] = z; gw[k][h] = z; }
-      mw[k] = 0x77777777u; vw[k] = 0u;
-      if (cnt[k] == 8) {
+      for (int h = 0; h < PW; ++h) { r.pw[k][h] = z; r.gw[k][h] = z; }
+      r.mw[k] = 0x77777777u; r.vw[k] = 0u;
+      if (r.cnt[k] == 8) {
 #pragma unroll
-        for (int h = 0; h < PW; ++h) { pw[k][h] = pp[h]; gw[k][h] = gp[h]; }
-        mw[k] = *APEXW_GLOBAL(const uint32_t, (const uint8_t*)t.m + (e >> 1));
-        vw[k] = *APEXW_GLOBAL(const uint16_t, (const uint8_t*)t.v + (e >> 2));
-      } else if (cnt[k] == 4) {
+        for (int h = 0; h < PW; ++h) { r.pw[k][h] = pp[h]; r.gw[k][h] = gp[h]; }
+        r.mw[k] = *APEXW_GLOBAL(const uint32_t, (const uint8_t*)t.m + (e >> 1));
+        r.vw[k] = *APEXW_GLOBAL(const uint16_t, (const uint8_t*)t.v + (e >> 2));
+      } else if (r.cnt[k] == 4) {
         if constexpr (PD == APEXW_F32) {
-          pw[k][0] = pp[0];
-          gw[k][0] = gp[0];
+          r.pw[k][0] = pp[0];
+          r.gw[k][0] = gp[0];
         } else {
           const u32x2 a = *APEXW_GLOBAL(const u32x2, (const uint16_t*)t.p + e);
           const u32x2 b = *APEXW_GLOBAL(const u32x2, (const uint16_t*)t.g + e);
-          pw[k][0].x = a.x; pw[k][0].y = a.y; gw[k][0].x = b.x; gw[k][0].y = b.y;
+          r.pw[k][0].x = a.x; r.pw[k][0].y = a.y; r.gw[k][0].x = b.x; r.gw[k][0].y = b.y;
         }
-        mw[k] = 0x77770000u | *APEXW_GLOBAL(const uint16_t, (const uint8_t*)t.m + (e >> 1));
-        vw[k] = *APEXW_GLOBAL(const uint8_t, (const uint8_t*)t.v + (e >> 2));
+        r.mw[k] = 0x77770000u | *APEXW_GLOBAL(const uint16_t, (const uint8_t*)t.m + (e >> 1));
+        r.vw[k] = *APEXW_GLOBAL(const uint8_t, (const uint8_t*)t.v + (e >> 2));
       }
     }
   }
+}
+
+// The arithmetic and stores of one fast-path block, from its loads.
+template <int PD, bool SR, bool FULL, bool GENERIC>
+APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk, const Q8Ctx& c,
+                               const FastRaw<PD>& r) {
+  const apexw_hparams& hp = *c.hp;
+  const uint32_t hf = hp.flags, tf = t.flags;
+  const int lane = lane_id();
+  const int64_t start = (int64_t)blk * 2048;
+  const float ms_old = r.ms_old;
+  const float vs_old = r.vs_old;
+  const float decay = (tf & APEXW_FLAG_WD) ? hp.wd_factor : 1.0f;
+  const bool lerp_hi = hf & APEXW_HP_LERP_HI, look_hi = hf & APEXW_HP_LOOK_HI;
+  const auto& pw = r.pw;
+  const auto& gw = r.gw;
+  const auto& mw = r.mw;
+  const auto& vw = r.vw;
+  const auto& cnt = r.cnt;
   uint32_t rs = 0;
   if constexpr (SR) {
     const uint32_t key = rng_key(hp.seed, tix, hp.step, 1u, (uint32_t)(start >> 32));
@@ -803,6 +824,13 @@ APEXW_DEV void q8_block_fast(const apexw_tensor& t, uint32_t tix, uint32_t blk, 
   }
 }
 
+template <int PD, bool SR, bool FULL, bool GENERIC>
+APEXW_DEV void q8_block_fast(const apexw_tensor& t, uint32_t tix, uint32_t blk, const Q8Ctx& c) {
+  FastRaw<PD> r;
+  q8_fast_load<PD, FULL>(t, blk, r);
+  q8_fast_compute<PD, SR, FULL, GENERIC>(t, tix, blk, c, r);
+}
+
 // Tensors under 64 elements in 8-bit mode keep 16-bit m/v (optimizer.py:4688-4735).
 // SINGLE: the per-parameter in-backward update of such a tensor
 // (apexw/optimizer.py:2458-2471): p.mul_(wd) in the parameter dtype, fp32
@@ -868,15 +896,19 @@ __global__ __launch_bounds__(256) void q8_fast_kernel(const apexw_tensor* __rest
   c.midtab = s_midtab;
   c.coef = (hp.flags & APEXW_HP_CLIP) ? *hp.clip_coef : 1.0f;
   const uint32_t wave = uniform(threadIdx.x >> 6);
-  const int64_t stride = (int64_t)gridDim.x * kWaves;
-  for (int64_t u = (int64_t)blockIdx.x * kWaves + wave; u < n_units; u += stride) {
+  const bool sr = hp.flags & APEXW_HP_SR;
+  // a workgroup walks a contiguous chunk of kFastChunk units, its waves interleaved
+  // (unit base + 4 i + wave): measured ~1% faster than workgroups striding by 4 units
+  for (int64_t base = (int64_t)blockIdx.x * kFastChunk; base < n_units; base += (int64_t)gridDim.x * kFastChunk)
+  for (int64_t u = base + wave, u_end = base + kFastChunk < n_units ? base + kFastChunk : n_units; u < u_end;
+       u += kWaves) {
     const apexw_unit un = units[u];
     const apexw_tensor& t = tensors[un.tensor];
     // never taken for a valid plan: the unit ranges hold only this kernel's tensors
     if (!apexw_q8_fast_ok(t.flags, t.block) || ((t.flags >> APEXW_FLAG_PDT_SHIFT) & 3u) != (uint32_t)PD) continue;
     const bool full = (int64_t)(un.unit + 1) * 2048 <= t.n;
     const bool gen = t.flags & APEXW_FLAG_GENERIC;
-    if (hp.flags & APEXW_HP_SR) {
+    if (sr) {
       if (full && !gen) q8_block_fast<PD, true, true, false>(t, un.tensor, un.unit, c);
       else if (full) q8_block_fast<PD, true, true, true>(t, un.tensor, un.unit, c);
       else if (!gen) q8_block_fast<PD, true, false, false>(t, un.tensor, un.unit, c);
@@ -973,12 +1005,14 @@ int apexw_launch_q8(const apexw_tensor* tensors, int64_t n_units, const apexw_un
 
 int apexw_launch_q8_fast(const apexw_tensor* tensors, int64_t n_units, const apexw_unit* units,
                          const apexw_hparams* hp, int32_t p_dtype, hipStream_t stream) {
+  // one workgroup per kFastChunk units: the hardware dispatcher balances the tail
+  // (measured ~1% faster than a persistent grid of 16 workgroups per resident slot)
+  const int64_t chunks = (n_units + kFastChunk - 1) / kFastChunk;
+  const int grid = (int)(chunks < INT32_MAX ? chunks : INT32_MAX);
   if (p_dtype == APEXW_F32) {
-    const int grid = apexw_resident_grid((const void*)q8_fast_kernel<APEXW_F32>, n_units);
     hipLaunchKernelGGL(q8_fast_kernel<APEXW_F32>, dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
     return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
   }
-  const int grid = apexw_resident_grid((const void*)q8_fast_kernel<APEXW_BF16>, n_units);
   hipLaunchKernelGGL(q8_fast_kernel<APEXW_BF16>, dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }

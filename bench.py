@@ -2,6 +2,7 @@
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--config c3|c2|c4|c1|...] [--no-cpu]
     python bench.py --copy-calibration     # 1 GiB device copy, for HBM counter scaling
+    python bench.py --ceiling              # HBM ceilings of the step's traffic (probe kernels)
 
 Prints ONE JSON line (rank 0).  A "step" is one ``ApexW.step()`` over the full
 parameter list with synthetic bf16 params ~N(0, 0.02) and grads ~N(0, 1e-3)
@@ -16,6 +17,9 @@ WRITE_SIZE passes (scaled by the same counters on a copy of known size), read
 from the committed profile summary of this workload when one exists.
 ``cpu_baseline`` times the CPU oracle (the reference algorithm restated with
 torch CPU ops) on a bounded slice of the same workload on this host's cores.
+The default (C3) line also carries ``mfma_roofline``: the C5 hybrid Muon step's
+Newton-Schulz GEMMs against the bf16 dense MFMA peak, measured after the C3
+tensors are freed.
 """
 
 import argparse
@@ -203,13 +207,25 @@ def ns_roofline(opt, stream, reps=3):
             "ns_steps": steps, "executed_tflops": sum(plan.exec_flops for plan in plans) / (ns_ms * 1e-3) / 1e12}
 
 
+def cpu_model():
+    """The host CPU's model name (first 'model name' line of /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(cfg_name, budget_s=20.0):
-    """Time the CPU oracle on a bounded slice of the workload (whole steps)."""
+    """Time the CPU oracle on a bounded slice of the workload (whole steps), on every
+    core this process may run on."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle.optim import OracleApexW
     cfg = CONFIGS[cfg_name]
-    threads = os.cpu_count() or 1
-    threads = min(threads, 16)
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
     torch.set_num_threads(threads)
     if cfg_name == "c5":
         from oracle.muon import OracleHybrid
@@ -223,6 +239,7 @@ def cpu_baseline(cfg_name, budget_s=20.0):
             if el > budget_s or steps >= 20:
                 break
         return {"value": params[0].numel() * steps / el, "unit": "params/s", "cores": threads, "kind": "port",
+                "cpu_model": cpu_model(),
                 "sample": f"the q matrix (4096x4096) of the layer; {steps} Muon steps, fp32 Newton-Schulz "
                           f"(the reference's CPU work dtype); CPU oracle (torch CPU ops)"}
     if cfg_name in ("c3", "c3fv", "c3fv6"):
@@ -246,8 +263,94 @@ def cpu_baseline(cfg_name, budget_s=20.0):
         el = time.perf_counter() - t0
         if el > budget_s or steps >= 50:
             break
-    return {"value": n * steps / el, "unit": "params/s", "cores": threads, "kind": "port",
+    return {"value": n * steps / el, "unit": "params/s", "cores": threads, "kind": "port", "cpu_model": cpu_model(),
             "sample": f"{sample}; {steps} steps after 1 cold step; CPU oracle (torch CPU ops)"}
+
+
+def ceiling(reps=5):
+    """HBM ceilings for the 8-bit step's traffic, HIP-event timed on the launch stream:
+    copy / read-only / write-only of 8 GiB (1, 4 and 16 KiB contiguous per wave), and
+    the step's exact access pattern with no arithmetic over the Llama-3-8B size
+    (1 and 4 consecutive blocks per wave).  Needs apexw_amd/libapexw_probe.so."""
+    import ctypes
+    from apexw_amd import _build
+    lib = ctypes.CDLL(_build.PROBE_PATH)
+    vp, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+    lib.apexw_probe_copy.argtypes = [vp, vp, i64, i32, i32, vp]
+    lib.apexw_probe_read.argtypes = [vp, i64, i32, i32, vp, vp]
+    lib.apexw_probe_write.argtypes = [vp, i64, i32, i32, vp]
+    lib.apexw_probe_q8_pattern.argtypes = [vp, vp, vp, vp, vp, vp, i64, i32, i32, vp]
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    nblk = sum(math.prod(s) for s in llama3_8b_shapes()) // 2048 // 4 * 4
+    p = torch.zeros(nblk * 2048, dtype=torch.bfloat16, device=dev)
+    g = torch.zeros_like(p)
+    m = torch.zeros(nblk * 1024, dtype=torch.uint8, device=dev)
+    v = torch.zeros(nblk * 512, dtype=torch.uint8, device=dev)
+    ms = torch.zeros(nblk, dtype=torch.float32, device=dev)
+    vs = torch.zeros_like(ms)
+    sink = torch.zeros(16, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    h = stream.cuda_stream
+
+    def timed(launch):
+        for _ in range(2):
+            assert launch() == 0
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            launch()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    cb = 8 << 30
+    grid = 32768
+    out = {}
+    for kib in (1, 4, 16):
+        ms_ = timed(lambda: lib.apexw_probe_copy(g.data_ptr(), p.data_ptr(), cb, kib, grid, h))
+        out[f"copy_{kib}k"] = 2 * cb / (ms_ * 1e-3) / 1e9
+    for kib in (4, 16):
+        ms_ = timed(lambda: lib.apexw_probe_read(g.data_ptr(), cb, kib, grid, sink.data_ptr(), h))
+        out[f"read_{kib}k"] = cb / (ms_ * 1e-3) / 1e9
+        ms_ = timed(lambda: lib.apexw_probe_write(p.data_ptr(), cb, kib, grid, h))
+        out[f"write_{kib}k"] = cb / (ms_ * 1e-3) / 1e9
+    pattern_bytes = nblk * (2048 * 7.5 + 16)   # p, g, m, v read and p, m, v written, two scales each way
+    for bpw in (1, 4):
+        for gr in (8192, 32768):
+            ms_ = timed(lambda: lib.apexw_probe_q8_pattern(p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(),
+                                                           ms.data_ptr(), vs.data_ptr(), nblk, bpw, gr, h))
+            out[f"q8_pattern_b{bpw}_grid{gr}"] = pattern_bytes / (ms_ * 1e-3) / 1e9
+    res = {"ceiling_gbs": {k: round(x, 1) for k, x in out.items()}, "peak_gbs": HBM_PEAK_GBS,
+           "copy_bytes": cb, "pattern_bytes": pattern_bytes, "grid": grid,
+           "device": torch.cuda.get_device_name(dev)}
+    print(json.dumps(res), flush=True)
+
+
+def mfma_extra(steps=10, warmup=3):
+    """The C5 Newton-Schulz roofline, for the default bench line: the hybrid Muon step on
+    one Llama-3-8B layer, then the step's grouped NS launches replayed between HIP events."""
+    from apexw_amd import ApexW
+    cfg = CONFIGS["c5"]
+    dev = torch.device("cuda", 0)
+    params = make_params(cfg, dev)
+    opt = ApexW(params, **cfg["kwargs"])
+    for _ in range(warmup):
+        opt.step()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(steps):
+        opt.step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    roof = ns_roofline(opt, stream)
+    roof["step_ms"] = e0.elapsed_time(e1) / steps
+    roof["workload"] = cfg["workload"]
+    del opt, params
+    torch.cuda.empty_cache()
+    return roof
 
 
 def main():
@@ -259,6 +362,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--copy-calibration", action="store_true", help="run the counter-calibration copy and exit")
+    ap.add_argument("--ceiling", action="store_true", help="measure the HBM ceilings of the step's traffic and exit")
+    ap.add_argument("--no-mfma", action="store_true", help="skip the C5 Newton-Schulz roofline of the default line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the optimizer step is data-parallel per shard and this build "
@@ -266,6 +371,9 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.ceiling:
+        ceiling()
         return
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from apexw_amd import ApexW
@@ -325,6 +433,11 @@ def main():
                    "param_dtype": str(cfg["dtype"]).replace("torch.", ""), **{k: v for k, v in cfg["kwargs"].items()}},
         "roofline": roofline,
     }
+    if args.config == "c3" and not args.no_mfma:
+        # the Muon half of the metric, measured after the C3 tensors are freed
+        del step, opt, params
+        torch.cuda.empty_cache()
+        out["mfma_roofline"] = mfma_extra()
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.config, args.cpu_budget)
     print(json.dumps(out), flush=True)

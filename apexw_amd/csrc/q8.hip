@@ -100,7 +100,9 @@ APEXW_DEV uint32_t logu8_code(float v, float vmax, bool sr, uint32_t r16) {
 APEXW_DEV uint32_t logu8_code_shared(float v, float vmax, float rvmax) {
   if (!(v > 0.0f)) return 0u;
   const float r = fmaxf(div_shared(v, vmax, rvmax), 0x1p-24f);
-  const float q = rintf(log2f(r) * 0x1.52aaaap+3f + 255.0f);
+  // r >= 2^-24 is a normal number, where log2f is v_log_f32 itself (its scaling of
+  // denormal inputs never applies)
+  const float q = rintf(__builtin_amdgcn_logf(r) * 0x1.52aaaap+3f + 255.0f);
   return (uint32_t)fminf(fmaxf(q, 1.0f), 255.0f);
 }
 
@@ -576,14 +578,6 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
     if (prep) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) g[j] = q8_grad<PD>(g[j], tf, c);
-    } else if constexpr (!SR) {
-      bool bad = false;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) bad |= !__builtin_isfinite(g[j]);
-      if (bad) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) g[j] = q8_grad<PD>(g[j], tf, c);
-      }
     }
     if constexpr (SR) {
 #pragma unroll
@@ -644,6 +638,30 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
         for (int i = 0; i < 4; ++i) upd[b + i] = look[b + i] * ((m[b + i] * g[b + i] >= 0.0f) ? r_hi : r_lo);
       }
     } else {
+      // quad sums of squares (torch's mean over 4: three plain adds) first: a non-finite
+      // grad makes its quad's sum non-finite, which sends the group through nan_to_num
+      // (rare path; a finite grad whose square overflows goes through it unchanged)
+      float s2[2];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int b = 4 * q;
+        float t = g[b] * g[b];
+        t = t + g[b + 1] * g[b + 1];
+        t = t + g[b + 2] * g[b + 2];
+        s2[q] = t + g[b + 3] * g[b + 3];
+      }
+      if (!prep && !(__builtin_isfinite(s2[0]) && __builtin_isfinite(s2[1]))) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) g[j] = q8_grad<PD>(g[j], tf, c);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const int b = 4 * q;
+          float t = g[b] * g[b];
+          t = t + g[b + 1] * g[b + 1];
+          t = t + g[b + 2] * g[b + 2];
+          s2[q] = t + g[b + 3] * g[b + 3];
+        }
+      }
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
         const float2 pr = c.pair[(mw[k] >> (8 * b)) & 0xFFu];
@@ -660,12 +678,8 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         const int b = 4 * q;
-        float s2 = g[b] * g[b];
-        s2 = s2 + g[b + 1] * g[b + 1];
-        s2 = s2 + g[b + 2] * g[b + 2];
-        s2 = s2 + g[b + 3] * g[b + 3];
         const float vold = c.vlut[(vw[k] >> (8 * q)) & 0xFFu] * vs_old;
-        float vv = fmaf(hp.one_minus_beta2, s2 * 0.25f, vold * hp.beta2);
+        float vv = fmaf(hp.one_minus_beta2, s2[q] * 0.25f, vold * hp.beta2);
         if (!(fabsf(vv) <= 3.402823466e38f)) vv = 0.0f;
         vq[k][q] = vv;
         if (FULL || 4 * q < cnt[k]) vmax = fmaxf(vmax, vv);
@@ -717,17 +731,18 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
         // bits 0-15 of both words, kept for the NF4 (bits 0-11) and v (bits 12-15) codes
         hm[k][b] = __builtin_amdgcn_perm(hbits[k][2 * b + 1], hbits[k][2 * b], 0x05040100u);
       } else {
+        // the final rounding to bf16 is the pack itself (v_cvt_pk_bf16_f32, nearest-even)
         float x[2];
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
           const int j = 2 * b + i;
           if constexpr (GENERIC) {
-            x[i] = rnd<APEXW_BF16>(rnd<APEXW_BF16>(p[j] * decay) - rnd<APEXW_BF16>(upd[j]));
+            x[i] = rnd<APEXW_BF16>(p[j] * decay) - rnd<APEXW_BF16>(upd[j]);
           } else {
-            x[i] = rnd<APEXW_BF16>(p[j] * decay - upd[j]);
+            x[i] = p[j] * decay - upd[j];
           }
         }
-        pout[b] = (__float_as_uint(x[0]) >> 16) | (__float_as_uint(x[1]) & 0xFFFF0000u);
+        pout[b] = pack_bf16x2(x[0], x[1]);
       }
     }
     u32x4 po = {pout[0], pout[1], pout[2], pout[3]};

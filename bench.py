@@ -77,6 +77,10 @@ CONFIGS = {
                dtype=torch.bfloat16, kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True), per_tensor_scale=True),
     "c3": dict(workload="C3 8-bit ApexW step, Llama-3-8B (8.03B params) bf16, SR on", shapes=llama3_8b_shapes(),
                dtype=torch.bfloat16, kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, precision="8bit")),
+    "c3rne": dict(workload="C3 shapes, 8-bit ApexW step with stochastic_rounding=False (the parity mode), bf16",
+                  shapes=llama3_8b_shapes(), dtype=torch.bfloat16,
+                  kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, precision="8bit",
+                              stochastic_rounding=False)),
     "c3fv": dict(workload="C3 shapes, 8-bit ApexW with factored_v=True (INT8 m, fp32 row/column v), bf16, SR on",
                  shapes=llama3_8b_shapes(), dtype=torch.bfloat16, grad_reads=2,
                  kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, precision="8bit", factored_v=True)),
@@ -242,7 +246,7 @@ def cpu_baseline(cfg_name, budget_s=20.0):
                 "cpu_model": cpu_model(),
                 "sample": f"the q matrix (4096x4096) of the layer; {steps} Muon steps, fp32 Newton-Schulz "
                           f"(the reference's CPU work dtype); CPU oracle (torch CPU ops)"}
-    if cfg_name in ("c3", "c3fv", "c3fv6"):
+    if cfg_name in ("c3", "c3rne", "c3fv", "c3fv6"):
         shapes = llama3_8b_shapes()[1:10]          # one transformer layer (218M params)
         sample = "one Llama-3-8B layer (q,k,v,o,gate,up,down + 2 RMSNorm, 218.1M params)"
     elif cfg_name == "c4":

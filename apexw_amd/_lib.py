@@ -13,7 +13,7 @@ import numpy as np
 
 from ._build import LIB_PATH
 
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 # dtype codes
 F32, BF16, F16, U8, I8 = 0, 1, 2, 3, 4
@@ -80,8 +80,18 @@ GEMM_PROBLEM_DTYPE = np.dtype([
     ("m", np.int32), ("n", np.int32), ("k", np.int32), ("lda", np.int32), ("ldb", np.int32), ("lde", np.int32),
     ("ldc", np.int32), ("ldct", np.int32), ("alpha", np.float32), ("beta", np.float32),
     ("flags", np.uint32), ("reserved", np.uint32),
+    ("p", np.uint64), ("p_dtype", np.int32), ("p_rows", np.int32), ("p_cols", np.int32),
+    ("wd_factor", np.float32), ("neg_lr", np.float32), ("reserved2", np.uint32),
 ])
-assert GEMM_PROBLEM_DTYPE.itemsize == 88
+assert GEMM_PROBLEM_DTYPE.itemsize == 120
+_GEMM_APPLY_ZERO = (0, 0, 0, 0, 0.0, 0.0, 0)
+
+
+def gemm_problems(rows):
+    """A host table of GEMM_PROBLEM_DTYPE from tuples: the 17 product fields (a .. reserved),
+    optionally followed by the 7 fields of a fused Muon update (p .. reserved2)."""
+    return np.array([tuple(r) if len(r) == 24 else tuple(r) + _GEMM_APPLY_ZERO for r in rows],
+                    dtype=GEMM_PROBLEM_DTYPE)
 # apexw_grad_prep: one grad of a preparation launch (sanitize / unscale / centralize)
 GRAD_PREP_DTYPE = np.dtype([("g", np.uint64), ("out", np.uint64), ("n", np.int64), ("row_len", np.int64),
                             ("dtype", np.uint32), ("reserved", np.uint32)])
@@ -95,7 +105,7 @@ FV_SUM_COLS = 1
 FV_BAND_ROWS = 32
 FV_UNIT_RANGES = 6   # (bf16, fp32 parameters) x (INT8, 6-bit, bf16 m)
 
-GEMM_SYM, GEMM_B_KN, GEMM_ADD_B = 1, 2, 4
+GEMM_SYM, GEMM_B_KN, GEMM_ADD_B, GEMM_APPLY, GEMM_APPLY_T, GEMM_APPLY_WD = 1, 2, 4, 8, 16, 32
 GEMM_OUT_C, GEMM_OUT_CT, GEMM_ADD, GEMM_KIND_NN = 1, 2, 4, 8
 GEMM_MAX_PROBLEMS = 256
 GEMM_QUEUES = 8
@@ -117,8 +127,8 @@ SIGNATURES = {
     "apexw_grad_prep_units": (ctypes.c_int64, [_vp]),
     "apexw_grad_prepare": (ctypes.c_int, [_vp, _i32, _vp, _i64, _f32, _u32, _vp]),
     "apexw_gemm_grouped_items": (ctypes.c_int64, [_vp, _i32]),
-    "apexw_gemm_grouped_schedule": (ctypes.c_int, [_vp, _i32, _vp, _i64, _vp, ctypes.POINTER(ctypes.c_int32),
-                                                   ctypes.POINTER(ctypes.c_int32)]),
+    "apexw_gemm_grouped_schedule": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i32, ctypes.POINTER(ctypes.c_int64), _vp,
+                                                   ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32)]),
     "apexw_gemm_nt_grouped": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, _vp]),
     "apexw_muon_workspace_floats": (ctypes.c_int64, [_i64, _i64]),
     "apexw_muon_prepare": (ctypes.c_int, [_vp, _vp, _i32, _i64, _i64, _f32, _f32, _i32, _f32, _f32, _vp, _vp, _i64,
@@ -163,19 +173,27 @@ def check(status, what):
         raise ApexwError(f"{what}: {STATUS.get(status, status)}")
 
 
-def gemm_schedule(problems):
+def gemm_schedule(problems, cus_per_queue=0):
     """Validate a host table of GEMM_PROBLEM_DTYPE rows and build its grouped-launch
     tile queues: returns (items uint32[n_items], queue_offsets int32[GEMM_QUEUES + 1],
-    n_workgroups, kind)."""
+    n_workgroups, kind).  cus_per_queue > 0 (the CUs of one XCD) lets the last
+    tiles of a queue split into 128-row halves (item bits 22-23)."""
     lib = load()
     problems = np.ascontiguousarray(problems, dtype=GEMM_PROBLEM_DTYPE)
-    n_items = int(lib.apexw_gemm_grouped_items(problems.ctypes.data, len(problems)))
-    if n_items < 0:
-        check(-n_items, "apexw_gemm_grouped_items")
-    items = np.empty(max(n_items, 1), dtype=np.uint32)
+    n_tiles = int(lib.apexw_gemm_grouped_items(problems.ctypes.data, len(problems)))
+    if n_tiles < 0:
+        check(-n_tiles, "apexw_gemm_grouped_items")
+    items = np.empty(max(2 * n_tiles, 1), dtype=np.uint32)
     offsets = np.empty(GEMM_QUEUES + 1, dtype=np.int32)
-    n_wg, kind = ctypes.c_int32(0), ctypes.c_int32(0)
-    check(lib.apexw_gemm_grouped_schedule(problems.ctypes.data, len(problems), items.ctypes.data, n_items,
-                                          offsets.ctypes.data, ctypes.byref(n_wg), ctypes.byref(kind)),
+    n_items, n_wg, kind = ctypes.c_int64(0), ctypes.c_int32(0), ctypes.c_int32(0)
+    check(lib.apexw_gemm_grouped_schedule(problems.ctypes.data, len(problems), items.ctypes.data, len(items),
+                                          int(cus_per_queue), ctypes.byref(n_items), offsets.ctypes.data,
+                                          ctypes.byref(n_wg), ctypes.byref(kind)),
           "apexw_gemm_grouped_schedule")
-    return items[:n_items], offsets, n_wg.value, kind.value
+    return items[:n_items.value].copy(), offsets, n_wg.value, kind.value
+
+
+def cus_per_queue(device):
+    """CUs of one XCD of `device` (its CU count over the grouped launch's queues)."""
+    import torch
+    return max(1, torch.cuda.get_device_properties(device).multi_processor_count // GEMM_QUEUES)

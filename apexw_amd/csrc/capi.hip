@@ -226,14 +226,29 @@ constexpr int kTile = APEXW_GEMM_TILE;
 // Epilogue kind of one problem, or minus a status when it is invalid.
 int gemm_problem_kind(const apexw_gemm_problem& p) {
   const bool sym = p.flags & APEXW_GEMM_SYM, kn = p.flags & APEXW_GEMM_B_KN, add_b = p.flags & APEXW_GEMM_ADD_B;
+  const bool apply = p.flags & APEXW_GEMM_APPLY;
   const bool add = p.beta != 0.0f;
-  if (!p.a || !p.b || (!p.c && !p.ct)) return -APEXW_ERR_ARG;
-  if ((p.flags & ~(APEXW_GEMM_SYM | APEXW_GEMM_B_KN | APEXW_GEMM_ADD_B)) || p.reserved) return -APEXW_ERR_ARG;
+  if (!p.a || !p.b || (!p.c && !p.ct && !apply)) return -APEXW_ERR_ARG;
+  constexpr uint32_t kKnown = APEXW_GEMM_SYM | APEXW_GEMM_B_KN | APEXW_GEMM_ADD_B | APEXW_GEMM_APPLY |
+                              APEXW_GEMM_APPLY_T | APEXW_GEMM_APPLY_WD;
+  if ((p.flags & ~kKnown) || p.reserved || p.reserved2) return -APEXW_ERR_ARG;
+  if (apply) {
+    // the X' product only; p covered by O
+    if (!kn || !add_b || p.ct || !p.p) return -APEXW_ERR_ARG;
+    if (p.p_dtype != APEXW_F32 && p.p_dtype != APEXW_BF16 && p.p_dtype != APEXW_F16) return -APEXW_ERR_DTYPE;
+    const bool t = p.flags & APEXW_GEMM_APPLY_T;
+    if (p.p_rows <= 0 || p.p_cols <= 0 || (t ? (p.p_cols > p.m || p.p_rows > p.n) : (p.p_rows > p.m || p.p_cols > p.n)))
+      return -APEXW_ERR_ARG;
+    if (((uintptr_t)p.p) & (p.p_dtype == APEXW_F32 ? 3u : 1u)) return -APEXW_ERR_ALIGN;
+  } else if (p.p || p.p_dtype || p.p_rows || p.p_cols || p.wd_factor != 0.0f || p.neg_lr != 0.0f ||
+             (p.flags & (APEXW_GEMM_APPLY_T | APEXW_GEMM_APPLY_WD))) {
+    return -APEXW_ERR_ARG;
+  }
   if (add_b ? (p.et || !add || p.alpha != 1.0f || p.m > p.k) : (add && !p.et)) return -APEXW_ERR_ARG;
   if (kn && (sym || p.ct)) return -APEXW_ERR_ARG;
   if (p.m <= 0 || p.n <= 0 || p.k <= 0) return -APEXW_ERR_ARG;
   if (p.m % kTile || p.n % kTile || p.k % APEXW_GEMM_KTILE) return -APEXW_ERR_ARG;
-  if (p.m / kTile > 4096 || p.n / kTile > 4096) return -APEXW_ERR_ARG;
+  if (p.m / kTile > 2048 || p.n / kTile > 2048) return -APEXW_ERR_ARG;
   const bool read_e = add && !add_b;
   if (p.lda < p.k || p.ldb < (kn ? p.n : p.k) || (p.c && p.ldc < p.n) || (p.ct && p.ldct < p.m) ||
       (read_e && p.lde < p.m))
@@ -249,7 +264,8 @@ int gemm_problem_kind(const apexw_gemm_problem& p) {
   if (sym) {
     if (p.m != p.n || p.a != p.b || p.lda != p.ldb || !p.c || p.ct != p.c || p.ldct != p.ldc) return -APEXW_ERR_ARG;
   }
-  return (p.c ? APEXW_GEMM_OUT_C : 0) | (p.ct ? APEXW_GEMM_OUT_CT : 0) | (add ? APEXW_GEMM_ADD : 0) |
+  // the applied update goes through the row-major epilogue (writing c too when given)
+  return (p.c || apply ? APEXW_GEMM_OUT_C : 0) | (p.ct ? APEXW_GEMM_OUT_CT : 0) | (add ? APEXW_GEMM_ADD : 0) |
          (kn ? APEXW_GEMM_KIND_NN : 0);
 }
 
@@ -271,12 +287,33 @@ int64_t apexw_gemm_grouped_items(const apexw_gemm_problem* problems, int32_t n_p
   return n;
 }
 
+namespace {
+
+// Makespan of one XCD's queue under the dispatcher's list scheduling: items
+// start in order, each on the CU that frees first.
+int64_t queue_makespan(const std::vector<int64_t>& costs, int cus) {
+  std::priority_queue<int64_t, std::vector<int64_t>, std::greater<int64_t>> free_at;
+  for (int c = 0; c < cus; ++c) free_at.push(0);
+  int64_t end = 0;
+  for (int64_t c : costs) {
+    const int64_t t = free_at.top() + c;
+    free_at.pop();
+    free_at.push(t);
+    end = std::max(end, t);
+  }
+  return end;
+}
+
+}  // namespace
+
 int apexw_gemm_grouped_schedule(const apexw_gemm_problem* problems, int32_t n_problems, uint32_t* items,
-                                int64_t n_items, int32_t* queue_offsets, int32_t* n_workgroups, int32_t* kind) {
-  if (!items || !queue_offsets || !n_workgroups || !kind) return APEXW_ERR_ARG;
+                                int64_t n_items, int32_t cus_per_queue, int64_t* n_items_out,
+                                int32_t* queue_offsets, int32_t* n_workgroups, int32_t* kind) {
+  if (!items || !queue_offsets || !n_workgroups || !kind || !n_items_out) return APEXW_ERR_ARG;
+  if (cus_per_queue < 0 || cus_per_queue > 1024) return APEXW_ERR_ARG;
   const int64_t want = apexw_gemm_grouped_items(problems, n_problems);
   if (want < 0) return (int)-want;
-  if (want != n_items || n_items >= INT32_MAX) return APEXW_ERR_ARG;
+  if (n_items < 2 * want || want >= INT32_MAX / 2) return APEXW_ERR_ARG;
   const int kind0 = gemm_problem_kind(problems[0]);
   for (int32_t i = 1; i < n_problems; ++i)
     if (gemm_problem_kind(problems[i]) != kind0) return APEXW_ERR_ARG;
@@ -289,9 +326,17 @@ int apexw_gemm_grouped_schedule(const apexw_gemm_problem* problems, int32_t n_pr
   // to the next queues in rotation across problems, so queues stay within about
   // one tile of each other.  Inside a queue the longest tiles come first: the
   // XCD starts them first and fills in with the short ones.
+  //
+  // Cost model, in twentieths of a K tile: a whole tile costs its K tiles plus
+  // 2 per epilogue stream (C, Ct, E); a 128-row half costs 0.55 of the K part
+  // (half the MFMAs, the same number of pipelined K steps) and half the
+  // epilogue.  With cus_per_queue > 0 (the CUs of one XCD), each queue's last
+  // s tiles are split into halves for the s that minimises the simulated
+  // makespan (ties keep fewer halves): 400 equal tiles on 32 CUs take 12.5
+  // rounds instead of 13 once the last 16 are halved.
   struct Item {
     uint32_t code;
-    int64_t cost;
+    int64_t cost, half_cost;
   };
   constexpr int nq = APEXW_GEMM_QUEUES;
   const int64_t epi = 2 * (((kind0 & APEXW_GEMM_OUT_C) != 0) + ((kind0 & APEXW_GEMM_OUT_CT) != 0) +
@@ -303,13 +348,14 @@ int apexw_gemm_grouped_schedule(const apexw_gemm_problem* problems, int32_t n_pr
     const apexw_gemm_problem& p = problems[pi];
     const int tiles_m = p.m / kTile, tiles_n = p.n / kTile;
     const bool sym = (p.flags & APEXW_GEMM_SYM) != 0;
-    const int64_t cost = p.k / APEXW_GEMM_KTILE + epi;
+    const int64_t kt = p.k / APEXW_GEMM_KTILE;
+    const int64_t cost = 20 * (kt + epi), half_cost = 11 * kt + 10 * epi;
     tiles.clear();
     for (int g0 = 0; g0 < tiles_m; g0 += 4)
       for (int tn = 0; tn < tiles_n; ++tn)
         for (int tm = g0; tm < std::min(g0 + 4, tiles_m); ++tm) {
           if (sym && tm > tn) continue;
-          tiles.push_back({((uint32_t)pi << 24) | ((uint32_t)tm << 12) | (uint32_t)tn, cost});
+          tiles.push_back({((uint32_t)pi << 24) | ((uint32_t)tm << 11) | (uint32_t)tn, cost, half_cost});
         }
     const size_t t = tiles.size(), base = t / nq, rem = t % nq;
     size_t off = 0;
@@ -321,15 +367,40 @@ int apexw_gemm_grouped_schedule(const apexw_gemm_problem* problems, int32_t n_pr
     rotate = (int)((rotate + rem) % nq);
   }
   int64_t pos = 0;
+  size_t longest = 0;
+  std::vector<int64_t> costs;
   for (int x = 0; x < nq; ++x) {
-    std::stable_sort(band[x].begin(), band[x].end(), [](const Item& l, const Item& r) { return l.cost > r.cost; });
+    std::vector<Item>& b = band[x];
+    std::stable_sort(b.begin(), b.end(), [](const Item& l, const Item& r) { return l.cost > r.cost; });
+    size_t split = 0;
+    if (cus_per_queue > 0) {
+      int64_t best = -1;
+      const size_t most = std::min(b.size(), (size_t)cus_per_queue);
+      for (size_t s = 0; s <= most; ++s) {
+        costs.clear();
+        for (size_t i = 0; i + s < b.size(); ++i) costs.push_back(b[i].cost);
+        for (size_t i = b.size() - s; i < b.size(); ++i) {
+          costs.push_back(b[i].half_cost);
+          costs.push_back(b[i].half_cost);
+        }
+        const int64_t span = queue_makespan(costs, cus_per_queue);
+        if (best < 0 || span < best) {
+          best = span;
+          split = s;
+        }
+      }
+    }
     queue_offsets[x] = (int32_t)pos;
-    for (const Item& it : band[x]) items[pos++] = it.code;
+    for (size_t i = 0; i + split < b.size(); ++i) items[pos++] = b[i].code;
+    for (size_t i = b.size() - split; i < b.size(); ++i) {
+      items[pos++] = b[i].code | (1u << 22);
+      items[pos++] = b[i].code | (2u << 22);
+    }
+    longest = std::max(longest, (size_t)(pos - queue_offsets[x]));
   }
   queue_offsets[nq] = (int32_t)pos;
-  size_t longest = 0;
-  for (int x = 0; x < nq; ++x) longest = std::max(longest, band[x].size());
   if ((int64_t)longest * nq > INT32_MAX) return APEXW_ERR_ARG;
+  *n_items_out = pos;
   *n_workgroups = (int32_t)(longest * nq);
   *kind = kind0;
   return APEXW_OK;

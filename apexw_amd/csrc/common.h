@@ -39,6 +39,11 @@ APEXW_DEV float f16_bits_to_f32(uint32_t h) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 APEXW_DEV uint32_t f32_to_f16_bits(float x) {
+  // x is a rounded fp32 value here: without this barrier the compiler folds a
+  // preceding multiply or fma into the conversion (v_fma_mixlo_f16, a single
+  // rounding of the exact result), which differs from torch's fp32 arithmetic
+  // followed by the fp16 store on values that fall on an fp16 tie
+  __asm__ volatile("" : "+v"(x));
   _Float16 h = (_Float16)x;
   return (uint32_t)__builtin_bit_cast(uint16_t, h);
 }

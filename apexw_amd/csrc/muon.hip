@@ -85,31 +85,74 @@ APEXW_DEV uint32_t lds_address(const void* p) {
 }
 
 // s_waitcnt vmcnt(n) for the n the K loop needs (an immediate operand).
+// Counts are multiples of the copies per stage (8, or 6 for half tiles); any
+// other n waits for the next lower listed count, which is also correct.
 APEXW_DEV void wait_vm(int n) {
   if (n >= 32) asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
   else if (n >= 24) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+  else if (n >= 18) asm volatile("s_waitcnt vmcnt(18)" ::: "memory");
   else if (n >= 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+  else if (n >= 12) asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
   else if (n >= 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else if (n >= 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
   else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-// One 256 x 256 output tile: O = alpha * A B^T + beta * E (bf16 in, fp32
-// accumulate, bf16 out, round to nearest even).  A and B point at the tile's
-// first row of each operand; Et, C and Ct at the tile's origin in their own
-// layouts.  256 threads = 4 waves in a 2 x 2 arrangement, each owning a
-// 128 x 128 block as 4 x 4 MFMA 32x32x16 accumulators.
+// The Muon update fused into the X' epilogue (APEXW_GEMM_APPLY): p [rows x
+// cols] row-major, O = p (or p^T when transposed) in the tile's coordinates;
+// row0 / col0 are the tile's origin in O.  p == nullptr: no update.
+struct ApplyArgs {
+  void* p;
+  int64_t rows, cols, row0, col0;
+  float wd_factor, neg_lr;
+  int dtype;
+  bool transposed, wd, vec;
+};
+
+// x = p; with decay x = rnd(x * wd_factor); p = rnd(x + neg_lr * u), for the
+// cnt (<= 8) consecutive elements of p from index i (the element order of
+// apexw/muon.py:852-858's p.mul_ then p.add_, as muon_apply_kernel does it)
+template <int PD>
+APEXW_DEV void apply_run(const ApplyArgs& ap, int64_t i, const float (&u)[8], int cnt) {
+  if (ap.vec && cnt == 8) {
+    float x[8];
+    load8<PD>(ap.p, i, x);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      if (ap.wd) x[t] = rnd<PD>(x[t] * ap.wd_factor);
+      x[t] = rnd<PD>(fmaf(ap.neg_lr, u[t], x[t]));
+    }
+    store8<PD>(ap.p, i, x);
+    return;
+  }
+  for (int t = 0; t < cnt; ++t) {
+    float x = load1<PD>(ap.p, i + t);
+    if (ap.wd) x = rnd<PD>(x * ap.wd_factor);
+    store1<PD>(ap.p, i + t, rnd<PD>(fmaf(ap.neg_lr, u[t], x)));
+  }
+}
+
+// One output tile: O = alpha * A B^T + beta * E (bf16 in, fp32 accumulate,
+// bf16 out, round to nearest even), 256 x 256, or 128 x 256 with kHalf (the
+// split tail tiles of a grouped launch).  A and B point at the tile's first row
+// of each operand; Et, C and Ct at the tile's origin in their own layouts.  256
+// threads = 4 waves in a 2 x 2 arrangement, each owning a kWM x 128 block
+// (kWM = 128, or 64 with kHalf) as (kWM / 32) x 4 MFMA 32x32x16 accumulators.
 // Template flags select the epilogue: write O row-major (kC), transposed (kCt,
 // skipped at run time when write_ct is false), add beta * E (kAdd).
 //
 // K pipeline.  Stage h = K columns [32 h, 32 h + 32), buffer h % 5, two MFMA
 // k-steps (a, b) whose fragments sit in register slots 0 and 1.  Iteration h:
-//   1. the 16 MFMAs of step h.a, each followed by one LDS read of step h.b's
-//      fragments (slot 1, free since the MFMAs of step (h-1).b were issued);
+//   1. the MFMAs of step h.a, each of the first kFrags followed by one LDS read
+//      of step h.b's fragments (slot 1, free since the MFMAs of step (h-1).b
+//      were issued);
 //   2. wait until stage h + 1's copies have landed and this wave's LDS reads
 //      have returned, then barrier;
-//   3. the 16 MFMAs of step h.b, the first 8 each followed by one LDS read of
-//      step (h+1).a (slot 0) and the last 8 by one global -> LDS copy of
-//      stage h + 5 into buffer h % 5.
+//   3. the MFMAs of step h.b, the first kFrags each followed by one LDS read of
+//      step (h+1).a (slot 0), and the kCopies global -> LDS copies of stage
+//      h + 5 into buffer h % 5 spread evenly over them (one after every other
+//      MFMA: issued in a burst, the copies stall the wave's in-order issue on a
+//      full memory pipeline, and with one wave per SIMD the matrix core idles).
 // Stage h + 1 is read only after the barrier in 2 that follows its wait, and
 // buffer h % 5 is refilled only after that barrier, which every wave reaches
 // after its last reads of stage h.  A stage's copies have about three and a
@@ -124,15 +167,21 @@ APEXW_DEV void wait_vm(int n) {
 // Addend on the matrix cores (diag_k0 >= 0): when E is the B operand itself
 // read at K = diag_k0 + i (E[i][j] = B[j][diag_k0 + i], or B[diag_k0 + i][j]
 // for kNN, as in X' = B X + a X) and alpha == 1, the B fragments of K
-// [diag_k0, diag_k0 + 256) are exactly the addend.  There each wave adds
+// [diag_k0, diag_k0 + rows) are exactly the addend.  There each wave adds
 // beta E with extra MFMAs against a one-hot fragment holding beta on the
 // diagonal (beta split into two bf16 parts, hi + lo, within 2^-18 of beta), so
 // the epilogue reads no addend.
-template <bool kC, bool kCt, bool kAdd, bool kNN>
+template <bool kC, bool kCt, bool kAdd, bool kNN, bool kHalf>
 APEXW_DEV void gemm_tile(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, int32_t lda, int32_t ldb,
                          int32_t k, const uint16_t* __restrict__ Et, int32_t lde, uint16_t* __restrict__ C,
                          int32_t ldc, uint16_t* __restrict__ Ct, int32_t ldct, bool write_ct, float alpha,
-                         float beta, int32_t diag_k0, LdsStage* lds) {
+                         float beta, int32_t diag_k0, const ApplyArgs& ap, LdsStage* lds) {
+  constexpr int kWM = kHalf ? 64 : 128;   // rows of a wave's block
+  constexpr int kFA = kWM / 32;           // A fragments (32-row blocks) per wave and k-step
+  constexpr int kACopies = kWM / 32;      // A copy instructions per wave and stage (16 rows each, 4 waves)
+  constexpr int kCopies = kACopies + 4;   // per stage and wave: A, then the 4 of B
+  constexpr int kFrags = kFA + 4;         // fragment reads per k-step
+  constexpr int kMM = kFA * 4;            // MFMAs per k-step
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
@@ -141,72 +190,76 @@ APEXW_DEV void gemm_tile(const uint16_t* __restrict__ A, const uint16_t* __restr
   // slot L % 4, which holds column chunk (L % 4) ^ ((L / 16) % 4).  kNN B: 2 K
   // rows of 512 bytes, lane L at row 2 q + L / 32, slot L % 32, holding column
   // chunk (L % 32) ^ (4 (row % 4)) (so the transposing reads of 4 consecutive
-  // rows hit distinct banks).  A stage is 16 instructions for A and 16 for B;
-  // wave w issues q = 4 w .. 4 w + 3 of each.
-  uint32_t goff[8];
+  // rows hit distinct banks).  A stage is 16 instructions for B and 16 (8 with
+  // kHalf) for A; wave w issues q = kACopies w .. of A and 4 w .. 4 w + 3 of B.
+  uint32_t goff[kCopies];
+#pragma unroll
+  for (int i = 0; i < kACopies; ++i) {
+    const int row = 16 * (kACopies * wave + i) + (lane >> 2), chunk = (lane & 3) ^ ((lane >> 4) & 3);
+    goff[i] = (uint32_t)(row * lda + chunk * 8) * 2u;
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int row = 16 * (4 * wave + i) + (lane >> 2), chunk = (lane & 3) ^ ((lane >> 4) & 3);
-    goff[i] = (uint32_t)(row * lda + chunk * 8) * 2u;
     if constexpr (kNN) {
       const int krow = 2 * (4 * wave + i) + (lane >> 5), nchunk = (lane & 31) ^ (4 * (krow & 3));
-      goff[4 + i] = (uint32_t)(krow * ldb + nchunk * 8) * 2u;
+      goff[kACopies + i] = (uint32_t)(krow * ldb + nchunk * 8) * 2u;
     } else {
-      goff[4 + i] = (uint32_t)(row * ldb + chunk * 8) * 2u;
+      const int row = 16 * (4 * wave + i) + (lane >> 2), chunk = (lane & 3) ^ ((lane >> 4) & 3);
+      goff[kACopies + i] = (uint32_t)(row * ldb + chunk * 8) * 2u;
     }
   }
-  // LDS byte address of this wave's first A chunk in stage 0 (wave-uniform)
-  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(&lds[0][0][4 * wave * 512]));
-  constexpr uint32_t kStageBytes = sizeof(LdsStage), kHalf = kStageBytes / 2, kChunk = 1024;
+  // LDS byte addresses of this wave's first A and B chunks in stage 0 (wave-uniform)
+  const uint32_t ldsA0 = __builtin_amdgcn_readfirstlane(lds_address(&lds[0][0][kACopies * wave * 512]));
+  const uint32_t ldsB0 = __builtin_amdgcn_readfirstlane(lds_address(&lds[0][1][4 * wave * 512]));
+  constexpr uint32_t kStageBytes = sizeof(LdsStage), kChunk = 1024;
   const uint16_t* A_s = uniform_ptr(A);
   const uint16_t* B_s = uniform_ptr(B);
-  // copy i (0..7) of stage h: A chunks 0..3, then B chunks 0..3
+  // copy i (0 .. kCopies - 1) of stage h: A chunks, then B chunks 0..3
   auto copy = [&](int h, int i) {
-    const uint32_t base = lds0 + (uint32_t)(h % kStages) * kStageBytes;
-    if (i < 4) lds_copy16(base + i * kChunk, goff[i], A_s + h * kBK);
-    else lds_copy16(base + kHalf + (i - 4) * kChunk, goff[i], B_s + (kNN ? (int64_t)h * kBK * ldb : h * kBK));
+    const uint32_t st = (uint32_t)(h % kStages) * kStageBytes;
+    if (i < kACopies) lds_copy16(ldsA0 + st + i * kChunk, goff[i], A_s + h * kBK);
+    else lds_copy16(ldsB0 + st + (i - kACopies) * kChunk, goff[i], B_s + (kNN ? (int64_t)h * kBK * ldb : h * kBK));
   };
-  constexpr int kCopies = 8;   // per stage and wave
 
-  f32x16 acc[4][4];
+  f32x16 acc[kFA][4];
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
+  for (int a = 0; a < kFA; ++a)
 #pragma unroll
     for (int b = 0; b < 4; ++b) acc[a][b] = f32x16{};
 
   // MFMA 32x32x16 operand layout: lane l supplies row (l % 32) and k = 8 (l / 32) .. +7.
   const int frag_row = lane & 31, frag_c = lane >> 5;
-  bf16x8 fa[2][4], fb[2][4];
-  // fragment read i (0..7) of k-step s of stage h: A fragments 0..3, then B 0..3
+  bf16x8 fa[2][kFA], fb[2][4];
+  // fragment read i (0 .. kFrags - 1) of k-step s of stage h: A fragments, then B 0..3
   auto frag = [&](int h, int s, int i) {
-    const uint16_t* st = lds[h % kStages][i < 4 ? 0 : 1];
-    if (kNN && i >= 4) {
+    const uint16_t* st = lds[h % kStages][i < kFA ? 0 : 1];
+    if (kNN && i >= kFA) {
       // lane l = 16 g + 4 r + j' of group g addresses K row 16 s + 8 (g / 2) + j'
       // (+ 4 for the upper half), columns n .. n + 3 with n = 16 (g % 2) + 4 r
       // of the 32-column block; it receives column 16 (g % 2) + (l % 16) = l % 32
       // at 4 consecutive K rows, i.e. the MFMA B layout
       const int g = lane >> 4, r = lane & 3, jr = (lane >> 2) & 3;
-      const int n = wn * 128 + (i - 4) * 32 + 16 * (g & 1) + 4 * r;
+      const int n = wn * 128 + (i - kFA) * 32 + 16 * (g & 1) + 4 * r;
       const int k0 = 16 * s + 8 * (g >> 1) + jr;   // k0 % 4 == jr, as for k0 + 4
       const int slot = (n >> 3) ^ (4 * jr);
       const int e0 = k0 * 256 + slot * 8 + (n & 7), e1 = e0 + 4 * 256;
       const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)&st[e0]);
       const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)&st[e1]);
       const u32x2 wl = __builtin_bit_cast(u32x2, lo), wh = __builtin_bit_cast(u32x2, hi);
-      fb[s][i - 4] = __builtin_bit_cast(bf16x8, u32x4{wl[0], wl[1], wh[0], wh[1]});
+      fb[s][i - kFA] = __builtin_bit_cast(bf16x8, u32x4{wl[0], wl[1], wh[0], wh[1]});
       return;
     }
-    const int row = (i < 4 ? wm * 128 + i * 32 : wn * 128 + (i - 4) * 32) + frag_row;
+    const int row = (i < kFA ? wm * kWM + i * 32 : wn * 128 + (i - kFA) * 32) + frag_row;
     const bf16x8 v = *(const bf16x8*)&st[lds_off(row, s * 2 + frag_c)];
-    if (i < 4) fa[s][i] = v;
-    else fb[s][i - 4] = v;
+    if (i < kFA) fa[s][i] = v;
+    else fb[s][i - kFA] = v;
   };
-  // the 16 MFMAs of slot s, side(j) issued after MFMA j; sched_barrier(0)
+  // the kMM MFMAs of slot s, side(j) issued after MFMA j; sched_barrier(0)
   // fences keep that interleaving (the scheduler would otherwise cluster the
   // reads next to their first use and expose the LDS latency)
   auto mma = [&](int s, auto&& side) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
+    for (int j = 0; j < kMM; ++j) {
       acc[j >> 2][j & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[s][j >> 2], fb[s][j & 3], acc[j >> 2][j & 3], 0,
                                                                     0, 0);
       __builtin_amdgcn_sched_barrier(0);
@@ -216,13 +269,13 @@ APEXW_DEV void gemm_tile(const uint16_t* __restrict__ A, const uint16_t* __restr
   };
   // beta E on the matrix cores (see above): stage h holds K columns
   // [32 h, 32 h + 32), i.e. rows 32 h - diag_k0 .. + 31 of the addend, which
-  // fall in this wave's A block (32 h - diag_k0 - 128 wm) / 32 when in range
+  // fall in this wave's A block (32 h - diag_k0 - kWM wm) / 32 when in range
   const bool diag = kAdd && diag_k0 >= 0;
   const uint32_t beta_hi = f32_to_bf16_bits(beta);
   const uint32_t beta_lo = f32_to_bf16_bits(beta - __uint_as_float(beta_hi << 16));
   auto diag_mma = [&](int h, int s) {
-    const int rel = h * kBK - (diag_k0 + wm * 128);
-    if (rel < 0 || rel >= 128) return;
+    const int rel = h * kBK - (diag_k0 + wm * kWM);
+    if (rel < 0 || rel >= kWM) return;
     // lane l feeds row l % 32 of the block and k = 16 s + 8 (l / 32) + t: the
     // diagonal element sits at t = l % 32 - 16 s - 8 (l / 32)
     const int t = (lane & 31) - 16 * s - 8 * (lane >> 5);
@@ -243,11 +296,16 @@ APEXW_DEV void gemm_tile(const uint16_t* __restrict__ A, const uint16_t* __restr
         acc[blk][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fl, fb[s][b], acc[blk][b], 0, 0, 0);
       }
     };
-    switch (rel >> 5) {
-      case 0: add(std::integral_constant<int, 0>()); break;
-      case 1: add(std::integral_constant<int, 1>()); break;
-      case 2: add(std::integral_constant<int, 2>()); break;
-      default: add(std::integral_constant<int, 3>()); break;
+    if constexpr (kFA == 4) {
+      switch (rel >> 5) {
+        case 0: add(std::integral_constant<int, 0>()); break;
+        case 1: add(std::integral_constant<int, 1>()); break;
+        case 2: add(std::integral_constant<int, 2>()); break;
+        default: add(std::integral_constant<int, 3>()); break;
+      }
+    } else {
+      if ((rel >> 5) == 0) add(std::integral_constant<int, 0>());
+      else add(std::integral_constant<int, 1>());
     }
   };
   // lgkmcnt(0) through the builtin (vmcnt and expcnt fields at their no-wait
@@ -267,12 +325,12 @@ APEXW_DEV void gemm_tile(const uint16_t* __restrict__ A, const uint16_t* __restr
   wait_vm(kCopies * (first - 1));   // stage 0 landed
   barrier();
 #pragma unroll
-  for (int i = 0; i < 8; ++i) frag(0, 0, i);
+  for (int i = 0; i < kFrags; ++i) frag(0, 0, i);
   // one iteration; kNext: a stage h + 1 exists, kRefill: a stage h + 5 exists
   auto iteration = [&](int h, auto next_c, auto refill_c) {
     constexpr bool kNext = decltype(next_c)::value, kRefill = decltype(refill_c)::value;
     mma(0, [&](int j) {
-      if (j < 8) frag(h, 1, j);
+      if (j < kFrags) frag(h, 1, j);
     });
     if (diag) diag_mma(h, 0);
     // stage h + 1 landed; copies of the stages after it may still be in flight
@@ -280,10 +338,11 @@ APEXW_DEV void gemm_tile(const uint16_t* __restrict__ A, const uint16_t* __restr
     wait_vm(kNext ? kCopies * (last_issued - (h + 1)) : 0);
     barrier();
     mma(1, [&](int j) {
-      if (j < 8) {
-        if constexpr (kNext) frag(h + 1, 0, j);
-      } else {
-        if constexpr (kRefill) copy(h + kStages, j - 8);
+      if constexpr (kNext) {
+        if (j < kFrags) frag(h + 1, 0, j);
+      }
+      if constexpr (kRefill) {
+        if ((j * kCopies) / kMM != ((j + 1) * kCopies) / kMM) copy(h + kStages, (j * kCopies) / kMM);
       }
     });
     if (diag) diag_mma(h, 1);
@@ -298,18 +357,18 @@ APEXW_DEV void gemm_tile(const uint16_t* __restrict__ A, const uint16_t* __restr
   // Epilogue.  Accumulator register r of lane l holds row 8 (r / 4) + 4 (l / 32) + r % 4,
   // column l % 32 of its 32 x 32 block: four consecutive rows of one column per group.
   // After the last barrier the operand tiles are dead: each wave stages its
-  // 128 x 128 block of O in its own 32 KB of LDS, then writes it row by row to C
+  // kWM x 128 block of O in its own 32 KB of LDS, then writes it row by row to C
   // and column by column to Ct, both as 16-byte stores along output rows.  The
   // stage keeps 16-byte chunks XOR-swizzled by row / 8 so that the row reads
-  // (16 lanes per row) and the column reads (16 lanes down a column) each hit
+  // (16 lanes per row) and the column reads (lanes down a column) each hit
   // distinct banks.  A wave reads back only what it wrote itself, and LDS keeps
   // one wave's accesses in order, so no barrier is needed.
   uint16_t* stage = lds[wave][0];   // 32 KB per wave
   auto swz = [](int r, int c) { return r * 128 + ((((c >> 3) ^ (r >> 3)) & 15) << 3) + (c & 7); };
   const int il0 = (lane >> 5) * 4, jl0 = lane & 31;           // within the wave's block
-  const int gi0 = wm * 128 + il0, gj0 = wn * 128 + jl0;       // within the tile
+  const int gi0 = wm * kWM + il0, gj0 = wn * 128 + jl0;       // within the tile
 #pragma unroll
-  for (int a = 0; a < 4; ++a) {
+  for (int a = 0; a < kFA; ++a) {
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
       const int jl = jl0 + b * 32;
@@ -332,21 +391,63 @@ APEXW_DEV void gemm_tile(const uint16_t* __restrict__ A, const uint16_t* __restr
     }
   }
   if constexpr (kC) {
-    uint16_t* __restrict__ Cw = C + (int64_t)(wm * 128) * ldc + wn * 128;
+    if (ap.p) {
+      // the wave's block of O in O coordinates; p elements outside p's shape
+      // (the zero padding of the work matrix) are skipped
+      const int64_t gr0 = ap.row0 + wm * kWM, gc0 = ap.col0 + wn * 128;
+      auto upd = [&](auto pd_c) {
+        constexpr int PD = decltype(pd_c)::value;
+        if (!ap.transposed) {
+          // row by row: lane chunk = 8 consecutive elements of one row of p
+          for (int it = 0; it < kWM / 4; ++it) {
+            const int c = it * 64 + lane, r = c >> 4, c16 = c & 15;
+            const int64_t gi = gr0 + r, gj = gc0 + c16 * 8;
+            if (gi >= ap.rows || gj >= ap.cols) continue;
+            const u32x4 v = *(const u32x4*)&stage[swz(r, c16 * 8)];
+            float u[8];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              u[2 * t] = bf((uint16_t)(v[t] & 0xFFFFu));
+              u[2 * t + 1] = bf((uint16_t)(v[t] >> 16));
+            }
+            apply_run<PD>(ap, gi * ap.cols + gj, u, (int)min<int64_t>(8, ap.cols - gj));
+          }
+        } else {
+          // column by column of the block = row by row of p: p[gc0 + jl][gr0 + il + t] = O[gr0 + il + t][gc0 + jl]
+          constexpr int kPerRow = kWM / 8;
+          for (int it = 0; it < kWM / 4; ++it) {
+            const int c = it * 64 + lane, jl = c / kPerRow, il = (c % kPerRow) * 8;
+            const int64_t prow = gc0 + jl, pcol = gr0 + il;
+            if (prow >= ap.rows || pcol >= ap.cols) continue;
+            float u[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) u[t] = bf(stage[swz(il + t, jl)]);
+            apply_run<PD>(ap, prow * ap.cols + pcol, u, (int)min<int64_t>(8, ap.cols - pcol));
+          }
+        }
+      };
+      if (ap.dtype == APEXW_F32) upd(std::integral_constant<int, APEXW_F32>());
+      else if (ap.dtype == APEXW_BF16) upd(std::integral_constant<int, APEXW_BF16>());
+      else upd(std::integral_constant<int, APEXW_F16>());
+    }
+    if (C) {
+      uint16_t* __restrict__ Cw = C + (int64_t)(wm * kWM) * ldc + wn * 128;
 #pragma unroll 4
-    for (int it = 0; it < 32; ++it) {
-      const int c = it * 64 + lane, r = c >> 4, c16 = c & 15;
-      const u32x4 v = *(const u32x4*)&stage[swz(r, c16 * 8)];
-      __builtin_nontemporal_store(v, APEXW_GLOBAL(u32x4, Cw + (uint32_t)(r * ldc + c16 * 8)));
+      for (int it = 0; it < kWM / 4; ++it) {
+        const int c = it * 64 + lane, r = c >> 4, c16 = c & 15;
+        const u32x4 v = *(const u32x4*)&stage[swz(r, c16 * 8)];
+        __builtin_nontemporal_store(v, APEXW_GLOBAL(u32x4, Cw + (uint32_t)(r * ldc + c16 * 8)));
+      }
     }
   }
   if constexpr (kCt) {
     if (write_ct) {
-      uint16_t* __restrict__ Ctw = Ct + (int64_t)(wn * 128) * ldct + wm * 128;
+      uint16_t* __restrict__ Ctw = Ct + (int64_t)(wn * 128) * ldct + wm * kWM;
+      constexpr int kPerRow = kWM / 8;   // 16-byte chunks per Ct row of the block
 #pragma unroll 2
-      for (int it = 0; it < 32; ++it) {
+      for (int it = 0; it < kWM / 4; ++it) {
         // Ct row jl (= column jl of the block), elements il .. il + 7
-        const int c = it * 64 + lane, jl = c >> 4, il = (c & 15) * 8;
+        const int c = it * 64 + lane, jl = c / kPerRow, il = (c % kPerRow) * 8;
         u32x4 v;
 #pragma unroll
         for (int t = 0; t < 4; ++t)
@@ -377,11 +478,11 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmArgs g) {
 
   const int64_t batch = blockIdx.y;
   const int64_t row0 = (int64_t)tm * kBM, col0 = (int64_t)tn * kBN;
-  gemm_tile<kC, kCt, kAdd, false>(g.a + batch * g.sa + row0 * g.lda, g.b + batch * g.sb + col0 * g.ldb, g.lda, g.ldb, g.k,
+  gemm_tile<kC, kCt, kAdd, false, false>(g.a + batch * g.sa + row0 * g.lda, g.b + batch * g.sb + col0 * g.ldb, g.lda, g.ldb, g.k,
                            kAdd ? g.et + batch * g.se + col0 * g.lde + row0 : nullptr, g.lde,
                            kC ? g.c + batch * g.sc + row0 * g.ldc + col0 : nullptr, g.ldc,
                            kCt ? g.ct + batch * g.sct + col0 * g.ldct + row0 : nullptr, g.ldct, true, g.alpha, g.beta,
-                           -1, lds);
+                           -1, ApplyArgs{}, lds);
 }
 
 // Grouped GEMM: every problem of a launch (different shapes, K and operands)
@@ -391,10 +492,12 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmArgs g) {
 // b % 8.  Each XCD thus works through its own queue in order, a new workgroup
 // starting on whichever of its CUs frees first; a queue is one contiguous band
 // of tiles in locality order, longest first.  Workgroups past the end of their
-// queue exit at once.  An item packs (problem << 24) | (tile row << 12) | tile
-// column.  A symmetric problem (APEXW_GEMM_SYM) lists only tiles with
-// row <= column and mirrors each off-diagonal tile through the transposed
-// store (ct == c).
+// queue exit at once.  An item packs (problem << 24) | (part << 22) |
+// (tile row << 11) | tile column, part 0 for a whole 256 x 256 tile and 1 / 2
+// for its upper / lower 128-row half (the tail of a queue may be split so that
+// its last round fills the XCD).  A symmetric problem (APEXW_GEMM_SYM) lists
+// only tiles with row <= column and mirrors each off-diagonal tile through the
+// transposed store (ct == c).
 constexpr int kQueues = APEXW_GEMM_QUEUES;
 
 template <bool kC, bool kCt, bool kAdd, bool kNN>
@@ -407,18 +510,39 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_grouped_kernel(const apexw_gem
   if (i >= queue_offsets[q + 1] - begin) return;
   const uint32_t code = items[begin + i];
   const apexw_gemm_problem& p = probs[code >> 24];
-  const int tm = (int)((code >> 12) & 0xfffu), tn = (int)(code & 0xfffu);
-  const int64_t row0 = (int64_t)tm * kBM, col0 = (int64_t)tn * kBN;
+  const int part = (int)((code >> 22) & 3u);
+  const int tm = (int)((code >> 11) & 0x7ffu), tn = (int)(code & 0x7ffu);
+  const int64_t row0 = (int64_t)tm * kBM + (part == 2 ? kBM / 2 : 0), col0 = (int64_t)tn * kBN;
   const bool mirror = !(p.flags & APEXW_GEMM_SYM) || tm != tn;
   // APEXW_GEMM_ADD_B: the addend is the B operand read at K = row0 + i,
   // accumulated on the matrix cores (validated: alpha == 1, m <= k, no et)
   const bool diag = kAdd && (p.flags & APEXW_GEMM_ADD_B);
+  const uint16_t* A = (const uint16_t*)p.a + row0 * p.lda;
   const uint16_t* B = (const uint16_t*)p.b + (kNN ? col0 : col0 * p.ldb);
-  gemm_tile<kC, kCt, kAdd, kNN>((const uint16_t*)p.a + row0 * p.lda, B, p.lda, p.ldb, p.k,
-                                kAdd && !diag ? (const uint16_t*)p.et + col0 * p.lde + row0 : nullptr, p.lde,
-                           kC ? (uint16_t*)p.c + row0 * p.ldc + col0 : nullptr, p.ldc,
-                           kCt ? (uint16_t*)p.ct + col0 * p.ldct + row0 : nullptr, p.ldct, mirror, p.alpha, p.beta,
-                           diag ? (int32_t)row0 : -1, lds);
+  const uint16_t* Et = kAdd && !diag ? (const uint16_t*)p.et + col0 * p.lde + row0 : nullptr;
+  uint16_t* C = kC && p.c ? (uint16_t*)p.c + row0 * p.ldc + col0 : nullptr;
+  uint16_t* Ct = kCt ? (uint16_t*)p.ct + col0 * p.ldct + row0 : nullptr;
+  const int32_t dk = diag ? (int32_t)row0 : -1;
+  ApplyArgs ap{};
+  if (kC && (p.flags & APEXW_GEMM_APPLY)) {
+    ap.p = p.p;
+    ap.rows = p.p_rows;
+    ap.cols = p.p_cols;
+    ap.row0 = row0;
+    ap.col0 = col0;
+    ap.wd_factor = p.wd_factor;
+    ap.neg_lr = p.neg_lr;
+    ap.dtype = p.p_dtype;
+    ap.transposed = (p.flags & APEXW_GEMM_APPLY_T) != 0;
+    ap.wd = (p.flags & APEXW_GEMM_APPLY_WD) != 0;
+    ap.vec = p.p_cols % 8 == 0 && ((uintptr_t)p.p & 15u) == 0;
+  }
+  if (part)
+    gemm_tile<kC, kCt, kAdd, kNN, true>(A, B, p.lda, p.ldb, p.k, Et, p.lde, C, p.ldc, Ct, p.ldct, mirror, p.alpha,
+                                        p.beta, dk, ap, lds);
+  else
+    gemm_tile<kC, kCt, kAdd, kNN, false>(A, B, p.lda, p.ldb, p.k, Et, p.lde, C, p.ldc, Ct, p.ldct, mirror, p.alpha,
+                                         p.beta, dk, ap, lds);
 }
 
 // ---------------------------------------------------------------------------

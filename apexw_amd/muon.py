@@ -11,7 +11,9 @@ handling.  The step runs through libapexw_hip.so:
   (``A = X X^T``; ``B = c A A + b A``; ``X = B X + a X``), each one grouped
   launch (``apexw_gemm_nt_grouped``) over every Muon matrix of the step; the
   two symmetric products compute only the tiles on and above the diagonal;
-* ``apexw_muon_apply``: decoupled weight decay and ``p -= lr * scale * U``.
+* the last ``X`` product of each matrix applies the decoupled weight decay and
+  ``p -= lr * scale * U`` in its epilogue (``APEXW_GEMM_APPLY``);
+  ``apexw_muon_apply`` does it as a separate pass when ``ns_steps == 0``.
 
 Like the reference on a bf16-capable GPU, the Newton-Schulz work dtype is
 bf16 (apexw/muon.py:76-89).  Quantised momentum (precision "8bit"/"ultra"),
@@ -74,16 +76,18 @@ class NSWorkspace:
         self.partial = torch.empty(batch, max(per, 1), dtype=torch.float32, device=device)
 
 
-def _ns_problems(ws, phase, cur, out):
+def _ns_problems(ws, phase, cur, out, tag=None, tags=None):
     """Append the GEMM problems of one Newton-Schulz product for every matrix of ws.
 
     phase 0: A = X X^T (symmetric); phase 1: B = c A A + b A (symmetric);
     phase 2: X' = B X + a X with X read as [K x N] rows and the addend a X
     taken from that same operand on the matrix cores.  cur is the ping-pong
-    slot holding the current X.
+    slot holding the current X.  With tags, (tag, entry) is appended per row.
     """
     mp, np_ = ws.mp, ws.np_
     for e in range(ws.batch):
+        if tags is not None:
+            tags.append((tag, e))
         x = ws.x[cur][e].data_ptr()
         a, b = ws.a[e].data_ptr(), ws.b[e].data_ptr()
         if phase == 0:
@@ -104,6 +108,12 @@ class NSPlan:
     GPU is filled by the whole step's work rather than one shape at a time.  The
     problem tables and tile schedules are built once and kept on the device
     (they hold the workspaces' addresses, which never change).
+
+    A workspace's last X' product carries the parameter update
+    (APEXW_GEMM_APPLY): its rows of the table are filled in at each run with
+    the parameters' addresses and the step's scalars, validated, and uploaded
+    ahead of the launch on the same stream.  Those rows write X' itself only
+    when keep_result is set.
     """
 
     def __init__(self, wss, steps, device):
@@ -115,34 +125,65 @@ class NSPlan:
             t = ws.mp // _lib.GEMM_TILE
             tri = (t + 1) / (2 * t)
             self.exec_flops += ws.batch * s * (tri * (2 * ws.mp ** 2 * ws.np_ + 2 * ws.mp ** 3) + 2 * ws.mp ** 2 * ws.np_)
+        self.device = device
         built = {}
         self.iters = []
         for i in range(max(steps, default=0)):
             active = tuple(j for j, s in enumerate(steps) if s > i)
-            key = (active, i % 2)
+            final = frozenset(j for j in active if steps[j] == i + 1)
+            key = (active, final, i % 2)
             if key not in built:
-                built[key] = [self._launches([wss[j] for j in active], phase, i % 2, device) for phase in range(3)]
+                built[key] = [self._launches(wss, active, final if phase == 2 else (), phase, i % 2, device)
+                              for phase in range(3)]
             self.iters.append(built[key])
 
-    def _launches(self, wss, phase, cur, device):
-        rows = []
-        for ws in wss:
-            _ns_problems(ws, phase, cur, rows)
+    def _launches(self, wss, active, final, phase, cur, device):
+        rows, tags = [], []
+        for j in active:
+            _ns_problems(wss[j], phase, cur, rows, j, tags)
         out = []
         for c0 in range(0, len(rows), _lib.GEMM_MAX_PROBLEMS):
-            probs = np.array(rows[c0:c0 + _lib.GEMM_MAX_PROBLEMS], dtype=_lib.GEMM_PROBLEM_DTYPE)
-            items, offsets, n_wg, kind = _lib.gemm_schedule(probs)
+            probs = _lib.gemm_problems(rows[c0:c0 + _lib.GEMM_MAX_PROBLEMS])
+            items, offsets, n_wg, kind = _lib.gemm_schedule(probs, _lib.cus_per_queue(device))
             to_dev = lambda a: torch.from_numpy(a.view(np.uint8).copy()).to(device)  # noqa: E731
-            out.append((to_dev(probs), to_dev(items), to_dev(offsets), n_wg, kind))
+            # rows (index in this launch, workspace, entry) whose X' is the final update
+            fin = [(r, j, e) for r, (j, e) in enumerate(tags[c0:c0 + _lib.GEMM_MAX_PROBLEMS]) if j in final]
+            out.append((to_dev(probs), to_dev(items), to_dev(offsets), n_wg, kind, probs if fin else None, fin))
         return out
 
-    def run(self, stream):
+    def run(self, stream, applies=None, keep_result=True):
+        """Run every launch on `stream`.  applies[j][e] = (p, dtype code, rows, cols,
+        transposed, apply_wd, wd_factor, neg_lr) for entry e of workspace j: that
+        matrix's final X' updates p in its epilogue.  Without applies the final X'
+        is only stored (keep_result is then implied)."""
         lib = _lib.load()
         for phases in self.iters:
             for launches in phases:
-                for probs, items, offsets, n_wg, kind in launches:
+                for probs, items, offsets, n_wg, kind, host, fin in launches:
+                    if fin and applies is not None:
+                        probs = self._upload_applies(lib, probs, host, fin, applies, keep_result)
                     _lib.check(lib.apexw_gemm_nt_grouped(probs.data_ptr(), items.data_ptr(), offsets.data_ptr(),
                                                          n_wg, kind, stream), "apexw_gemm_nt_grouped")
+
+    def _upload_applies(self, lib, dev_probs, host, fin, applies, keep_result):
+        tbl = host.copy()
+        for r, j, e in fin:
+            p, dt, rows, cols, transposed, apply_wd, wd_factor, neg_lr = applies[j][e]
+            tbl["flags"][r] |= (_lib.GEMM_APPLY | (_lib.GEMM_APPLY_T if transposed else 0)
+                                | (_lib.GEMM_APPLY_WD if apply_wd else 0))
+            tbl["p"][r], tbl["p_dtype"][r], tbl["p_rows"][r], tbl["p_cols"][r] = p, dt, rows, cols
+            tbl["wd_factor"][r], tbl["neg_lr"][r] = (wd_factor if apply_wd else 0.0), neg_lr
+            if not keep_result:
+                tbl["c"][r], tbl["ldc"][r] = 0, 0
+        n = int(lib.apexw_gemm_grouped_items(tbl.ctypes.data, len(tbl)))
+        if n < 0:
+            _lib.check(-n, "apexw_gemm_grouped_items (fused Muon update)")
+        # the table goes up through pinned memory on the launch stream; the
+        # caching host allocator keeps the block until that copy has run
+        staged = torch.from_numpy(tbl.view(np.uint8)).pin_memory()
+        out = torch.empty_like(dev_probs)
+        out.copy_(staged, non_blocking=True)
+        return out
 
 
 class ApexMuon(Optimizer):
@@ -176,6 +217,9 @@ class ApexMuon(Optimizer):
         if bad:
             raise NotImplementedError("apexw_amd ApexMuon implements fp32-momentum Newton-Schulz Muon; not supported: "
                                       + ", ".join(bad))
+        # True: also store each matrix's final Newton-Schulz result in its
+        # workspace (the update is applied to the parameter either way)
+        self.keep_ns_result = False
         defaults = dict(lr=lr, momentum=momentum, nesterov=nesterov, weight_decay=weight_decay, ns_steps=ns_steps,
                         beta3=beta3, alpha=alpha, cautious=cautious, grad_centralization=grad_centralization,
                         precision=precision, scale_mode=scale_mode, ns_method=ns_method, batch_bmm=batch_bmm,
@@ -274,13 +318,20 @@ class ApexMuon(Optimizer):
             # Newton-Schulz of every matrix, grouped per device; matrices are
             # independent, so running all momenta first and all updates last
             # gives each parameter the result of the reference's per-shape loop
+            # the last X' product of each matrix applies its update to the
+            # parameter (decoupled decay, then p += -lr * scale * U) in its
+            # epilogue; with ns_steps == 0 the update is the normalised
+            # momentum itself and goes through the separate apply pass
             by_dev = defaultdict(list)
             for j in jobs:
                 by_dev[j["ws"].device].append(j)
             for dev, djobs in by_dev.items():
-                self._ns_plan(djobs, dev).run(torch.cuda.current_stream(dev).cuda_stream)
+                plan = self._ns_plan(djobs, dev)
+                applies = [self._apply_args(j) for j in djobs]
+                plan.run(torch.cuda.current_stream(dev).cuda_stream, applies, self.keep_ns_result)
             for j in jobs:
-                self._apply(j)
+                if j["steps"] == 0:
+                    self._apply(j)
         finally:
             self.grad_scale = None
             self.found_inf = None
@@ -307,24 +358,36 @@ class ApexMuon(Optimizer):
         return {"plist": plist, "group": group, "ws": ws, "rows": rows, "cols": cols,
                 "steps": int(group["ns_steps"]), "batched": len(plist) > 1}
 
-    def _apply(self, job):
-        """Decoupled decay and the scaled orthogonalised update (apexw/muon.py:852-858)."""
-        lib = _lib.load()
-        plist, group, ws, rows, cols = job["plist"], job["group"], job["ws"], job["rows"], job["cols"]
-        p0 = plist[0]
-        stream = torch.cuda.current_stream(p0.device).cuda_stream
-        res = job["steps"] % 2                   # ping-pong slot of the Newton-Schulz result
+    def _update_scalars(self, job):
+        """(wd_factor, neg_lr, apply_wd) of the decoupled decay and the scaled
+        orthogonalised update (apexw/muon.py:852-858)."""
+        group, p0 = job["group"], job["plist"][0]
         lr, wd = float(group["lr"]), float(group["weight_decay"])
-        scale = self._scale(group["scale_mode"], rows, cols)
+        scale = self._scale(group["scale_mode"], job["rows"], job["cols"])
         wd_factor, neg_lr = 1.0 - lr * wd, -lr * scale
         if job["batched"]:
             # torch._foreach_mul_ / _foreach_add_ over same-dtype lists see the scalars in p's dtype
             wd_factor, neg_lr = _round_to(p0.dtype, wd_factor), _round_to(p0.dtype, neg_lr)
-        # U is the wide work matrix: p's layout when wide, its transpose when tall
-        u_buf = ws.x[res]
+        return wd_factor, neg_lr, wd != 0.0
+
+    def _apply_args(self, job):
+        """Per batch entry, the fused update of the final Newton-Schulz product (NSPlan.run).
+        U is the wide work matrix: p's layout when wide, its transpose when tall."""
+        wd_factor, neg_lr, apply_wd = self._update_scalars(job)
+        rows, cols = job["rows"], job["cols"]
+        return [(p.data_ptr(), _dtype_code(p.dtype), rows, cols, rows > cols, apply_wd, wd_factor, neg_lr)
+                for p in job["plist"]]
+
+    def _apply(self, job):
+        """The update as a separate pass over the work matrix (ns_steps == 0)."""
+        lib = _lib.load()
+        plist, ws, rows, cols = job["plist"], job["ws"], job["rows"], job["cols"]
+        stream = torch.cuda.current_stream(plist[0].device).cuda_stream
+        wd_factor, neg_lr, apply_wd = self._update_scalars(job)
+        u_buf = ws.x[job["steps"] % 2]           # ping-pong slot of the Newton-Schulz result
         for i, p in enumerate(plist):
             _lib.check(lib.apexw_muon_apply(p.data_ptr(), _dtype_code(p.dtype), u_buf[i].data_ptr(), rows, cols,
-                                            ws.np_, int(rows > cols), wd_factor, int(wd != 0.0), neg_lr, stream),
+                                            ws.np_, int(rows > cols), wd_factor, int(apply_wd), neg_lr, stream),
                        "apexw_muon_apply")
 
     def get_state_memory_mb(self):

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define APEXW_ABI_VERSION 11
+#define APEXW_ABI_VERSION 12
 
 /* status codes */
 enum apexw_status {
@@ -349,9 +349,18 @@ typedef struct apexw_gemm_problem {
   int32_t m, n, k;
   int32_t lda, ldb, lde, ldc, ldct;
   float alpha, beta;
-  uint32_t flags;      /* APEXW_GEMM_SYM */
+  uint32_t flags;      /* APEXW_GEMM_* bits below */
   uint32_t reserved;   /* 0 */
-} apexw_gemm_problem;  /* 88 bytes */
+  /* APEXW_GEMM_APPLY only (else 0): the Muon parameter update fused into the
+   * epilogue, p <- p * wd_factor (with APEXW_GEMM_APPLY_WD), then
+   * p <- p + neg_lr * O, each rounded to p's dtype, for every element of
+   * p [p_rows x p_cols] (row-major); O covers p (APEXW_GEMM_APPLY_T: O = p^T). */
+  void* p;
+  int32_t p_dtype;     /* APEXW_F32 / APEXW_BF16 / APEXW_F16 */
+  int32_t p_rows, p_cols;
+  float wd_factor, neg_lr;
+  uint32_t reserved2;  /* 0 */
+} apexw_gemm_problem;  /* 120 bytes */
 
 /* The product is symmetric (A A^T, or c A A + b A with A symmetric): m == n,
  * a == b, and ct == c with ldct == ldc.  Only tiles on and above the diagonal
@@ -366,6 +375,14 @@ typedef struct apexw_gemm_problem {
  * m <= k, beta != 0 and et NULL; it is accumulated on the matrix cores (beta
  * as two bf16 parts, within 2^-18 of beta) instead of read in the epilogue. */
 #define APEXW_GEMM_ADD_B 4u
+/* The epilogue applies the Muon update to p (fields above) instead of, or,
+ * when c is not NULL, besides writing O: ApexMuon's decoupled decay and
+ * scaled orthogonalised update (apexw/muon.py:852-858) on the last
+ * Newton-Schulz product, with no separate pass over O.  Only with
+ * APEXW_GEMM_B_KN and APEXW_GEMM_ADD_B (the X' = B X + a X product); ct NULL. */
+#define APEXW_GEMM_APPLY 8u
+#define APEXW_GEMM_APPLY_T 16u   /* O is p transposed (a tall parameter's wide work matrix) */
+#define APEXW_GEMM_APPLY_WD 32u  /* multiply p by wd_factor first */
 
 /* epilogue kinds of a grouped launch (bit mask) */
 #define APEXW_GEMM_OUT_C 1   /* row-major output */
@@ -382,18 +399,23 @@ int64_t apexw_gemm_grouped_items(const apexw_gemm_problem* problems, int32_t n_p
 
 /*
  * Host-side: validate the problems (a host copy of the table that will be
- * uploaded) and build the tile queues: items[n_items] (n_items from
- * apexw_gemm_grouped_items) and queue_offsets[APEXW_GEMM_QUEUES + 1]; queue q
- * is items[queue_offsets[q] .. queue_offsets[q + 1]).  Each problem's tiles, in
+ * uploaded) and build the tile queues: items[*n_items_out] (capacity n_items,
+ * at least twice apexw_gemm_grouped_items) and
+ * queue_offsets[APEXW_GEMM_QUEUES + 1]; queue q is
+ * items[queue_offsets[q] .. queue_offsets[q + 1]).  Each problem's tiles, in
  * locality order (bands of 4 tile rows), are cut into one contiguous band per
  * queue (so every XCD works on the same matrix at once), the remainders rotated
- * across queues to balance them; longest tiles first within a queue.
- * *n_workgroups receives the grid size of the launch (APEXW_GEMM_QUEUES x the
- * longest queue) and *kind the epilogue kind.  At most 256 problems, 4096 tiles
- * per side.
+ * across queues to balance them; longest tiles first within a queue.  With
+ * cus_per_queue > 0 (the CUs of one XCD: the device's CU count / 8), the last
+ * tiles of a queue may be split into two 128-row halves, as many as minimise
+ * the queue's simulated makespan, so that the last round fills the XCD; 0
+ * keeps whole tiles.  *n_workgroups receives the grid size of the launch
+ * (APEXW_GEMM_QUEUES x the longest queue) and *kind the epilogue kind.  At most
+ * 256 problems, 2048 tiles per side.
  */
 int apexw_gemm_grouped_schedule(const apexw_gemm_problem* problems, int32_t n_problems, uint32_t* items,
-                                int64_t n_items, int32_t* queue_offsets, int32_t* n_workgroups, int32_t* kind);
+                                int64_t n_items, int32_t cus_per_queue, int64_t* n_items_out,
+                                int32_t* queue_offsets, int32_t* n_workgroups, int32_t* kind);
 
 /*
  * Run a grouped launch: one workgroup per tile; workgroup b computes tile

@@ -41,7 +41,8 @@ def _c5_phases():
 
 
 def _decode(items):
-    return items >> 24, (items >> 12) & 0xFFF, items & 0xFFF
+    """(problem, tile row, tile column, part): part 0 = whole tile, 1 / 2 = upper / lower 128-row half."""
+    return items >> 24, (items >> 11) & 0x7FF, items & 0x7FF, (items >> 22) & 3
 
 
 def _expected_tiles(probs):
@@ -60,12 +61,13 @@ def _expected_tiles(probs):
                                         (2, _lib.GEMM_OUT_C | _lib.GEMM_ADD | _lib.GEMM_KIND_NN)])
 def test_schedule_covers_every_tile_once_in_balanced_bands(phase, kind):
     probs = _c5_phases()[phase]
-    items, offsets, n_wg, got_kind = _lib.gemm_schedule(np.array(probs, dtype=_lib.GEMM_PROBLEM_DTYPE))
+    items, offsets, n_wg, got_kind = _lib.gemm_schedule(_lib.gemm_problems(probs))
     nq = _lib.GEMM_QUEUES
     assert got_kind == kind and len(offsets) == nq + 1
     assert n_wg == nq * np.diff(offsets).max()          # one workgroup per slot of the longest queue
     assert offsets[0] == 0 and offsets[-1] == len(items) and np.all(np.diff(offsets) >= 0)
-    p, tm, tn = _decode(items.astype(np.int64))
+    p, tm, tn, part = _decode(items.astype(np.int64))
+    assert np.all(part == 0)                            # no CU count given: whole tiles only
     got = list(zip(p.tolist(), tm.tolist(), tn.tolist()))
     assert len(got) == len(set(got)), "a tile is scheduled twice"
     assert set(got) == _expected_tiles(probs)
@@ -95,9 +97,60 @@ def test_schedule_covers_every_tile_once_in_balanced_bands(phase, kind):
         assert np.all(np.diff(kt) <= 0), f"queue {q} is not longest-first"
 
 
+def _sim(costs, cus):
+    """List scheduling as the dispatcher does it: each item starts on the CU that frees first."""
+    free = [0] * cus
+    for c in costs:
+        i = min(range(cus), key=free.__getitem__)
+        free[i] += c
+    return max(free)
+
+
+def test_tail_tiles_split_into_halves_when_the_last_round_is_short():
+    """C5's B X launch: 3200 equal tiles, 400 per queue on 32 CUs per XCD = 12
+    rounds + 16 tiles.  With the CU count the last 16 tiles of every queue
+    become 32 halves (12.5 rounds of work instead of 13); each half pair covers
+    its tile exactly once and the halves come last in their queue."""
+    probs = _lib.gemm_problems(_c5_phases()[2])
+    items, offsets, n_wg, _ = _lib.gemm_schedule(probs, 32)
+    p, tm, tn, part = _decode(items.astype(np.int64))
+    nq = _lib.GEMM_QUEUES
+    whole = set(zip(p[part == 0].tolist(), tm[part == 0].tolist(), tn[part == 0].tolist()))
+    upper = list(zip(p[part == 1].tolist(), tm[part == 1].tolist(), tn[part == 1].tolist()))
+    lower = list(zip(p[part == 2].tolist(), tm[part == 2].tolist(), tn[part == 2].tolist()))
+    assert np.all(part < 3) and sorted(upper) == sorted(lower) and len(set(upper)) == len(upper)
+    assert whole.isdisjoint(upper) and whole | set(upper) == _expected_tiles(probs)
+    kt, epi = 4096 // _lib.GEMM_KTILE, 2 * 2
+    for q in range(nq):
+        qp = part[offsets[q]:offsets[q + 1]]
+        assert (qp > 0).sum() == 32, q                         # 16 tiles -> 32 halves
+        assert np.all(np.diff((qp > 0).astype(int)) >= 0), q   # halves last
+        costs = [20 * (kt + epi) if x == 0 else 11 * kt + 10 * epi for x in qp.tolist()]
+        assert _sim(costs, 32) < _sim([20 * (kt + epi)] * 400, 32)
+    assert n_wg == nq * np.diff(offsets).max() == nq * (384 + 32)
+    # a launch whose rounds are already full keeps whole tiles: 256 equal tiles per queue on 32 CUs
+    full = _lib.gemm_problems(_ns_problems(4096, 4096 * 8, 1, 1 << 40)[2])
+    items, _, _, _ = _lib.gemm_schedule(full, 32)
+    assert np.all(_decode(items.astype(np.int64))[3] == 0)
+
+
+def test_symmetric_tail_halves_keep_the_diagonal_unmirrored():
+    """A small symmetric launch on few CUs: halves of diagonal and
+    off-diagonal tiles both appear, and every tile on or above the diagonal is
+    covered once (the kernel mirrors only off-diagonal tiles)."""
+    probs = _lib.gemm_problems(_ns_problems(512, 512, 1, 1 << 40)[0])
+    items, offsets, n_wg, _ = _lib.gemm_schedule(probs, 4)
+    p, tm, tn, part = _decode(items.astype(np.int64))
+    assert sorted(zip(tm[part == 1].tolist(), tn[part == 1].tolist())) == \
+        sorted(zip(tm[part == 2].tolist(), tn[part == 2].tolist()))
+    cover = {(a, b) for a, b, x in zip(tm.tolist(), tn.tolist(), part.tolist())}
+    assert cover == {(0, 0), (0, 1), (1, 1)} and (part > 0).any()
+    assert np.all(tm <= tn)
+
+
 def test_schedule_symmetric_tile_count():
     probs = _ns_problems(1024, 1024, 1, 1 << 40)[0]
-    items, offsets, _, _ = _lib.gemm_schedule(np.array(probs, dtype=_lib.GEMM_PROBLEM_DTYPE))
+    items, offsets, _, _ = _lib.gemm_schedule(_lib.gemm_problems(probs))
     assert len(items) == 4 * 5 // 2                    # 4 x 4 tiles -> 10 on or above the diagonal
 
 
@@ -106,7 +159,7 @@ def test_schedule_rejects_invalid_problems():
     good = _ns_problems(512, 768, 1, 1 << 40)
 
     def status(rows):
-        arr = np.array([tuple(r) for r in rows], dtype=_lib.GEMM_PROBLEM_DTYPE)
+        arr = _lib.gemm_problems([tuple(r) for r in rows])
         n = lib.apexw_gemm_grouped_items(arr.ctypes.data, len(arr))
         return int(-n) if n < 0 else 0
 
@@ -160,8 +213,38 @@ def test_schedule_rejects_invalid_problems():
     bad[0][8], bad[0][9], bad[0][11] = 512, 512, 512
     assert status(bad) == 1
     assert status([bx[0]] * 257) == 1                     # more problems than the item code holds
+    # the fused Muon update (X' product only): p, dtype, shape within O, alignment
+    A = _lib.GEMM_APPLY
+    ok = list(bx[0]) + [1 << 41, 1, 512, 768, 0.99, -0.01, 0]
+    ok[15] |= A | _lib.GEMM_APPLY_WD
+    ok[3] = 0                                             # no X' store: the update is the only output
+    assert status([ok]) == 0
+    t = list(ok)
+    t[15] |= _lib.GEMM_APPLY_T
+    t[19], t[20] = 768, 512                               # p^T = O [512 x 768]
+    assert status([t]) == 0
+    t[19], t[20] = 512, 768                               # p^T would be 768 x 512: not covered by O
+    assert status([t]) == 1
+    bad = list(ok)
+    bad[17] = 0                                           # no parameter
+    assert status([bad]) == 1
+    bad = list(ok)
+    bad[18] = 7                                           # not a float dtype
+    assert status([bad]) == 2
+    bad = list(ok)
+    bad[19] = 513                                         # more rows than O
+    assert status([bad]) == 1
+    bad = list(ok)
+    bad[17] += 2                                          # fp32 parameter off its 4-byte alignment
+    bad[18] = 0
+    assert status([bad]) == 4
+    bad = list(xx[0]) + [1 << 41, 1, 512, 512, 1.0, -0.01, 0]
+    bad[15] |= A                                          # a symmetric product applies nothing
+    assert status([bad]) == 1
+    bad = list(bx[0]) + [1 << 41, 1, 512, 768, 0.0, -0.01, 0]
+    assert status([bad]) == 1                             # update fields without the flag
     # a launch mixes no epilogue kinds
-    arr = np.array([tuple(xx[0]), tuple(bx[0])], dtype=_lib.GEMM_PROBLEM_DTYPE)
+    arr = _lib.gemm_problems([tuple(xx[0]), tuple(bx[0])])
     with pytest.raises(_lib.ApexwError):
         _lib.gemm_schedule(arr)
     # the launch itself rejects bad kinds and null tables before enqueueing anything

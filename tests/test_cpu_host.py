@@ -34,7 +34,7 @@ def test_struct_layouts_match_header():
     from apexw_amd import _lib
     assert ctypes.sizeof(_lib.Tensor) == 64 == _lib.TENSOR_DTYPE.itemsize
     assert ctypes.sizeof(_lib.HParams) == 88
-    assert _lib.GEMM_PROBLEM_DTYPE.itemsize == 88
+    assert _lib.GEMM_PROBLEM_DTYPE.itemsize == 120
 
 
 def test_check_tensor_rejects_bad_descriptors():

@@ -462,7 +462,7 @@ def _torch_bf16_ns(G, steps=5, eps=1e-7):
 def _ns_launch(plan, phase, stream):
     from apexw_amd import _lib
     lib = _lib.load()
-    for probs, items, offsets, n_wg, kind in plan.iters[0][phase]:
+    for probs, items, offsets, n_wg, kind, *_ in plan.iters[0][phase]:
         _lib.check(lib.apexw_gemm_nt_grouped(probs.data_ptr(), items.data_ptr(), offsets.data_ptr(), n_wg, kind,
                                              stream), "apexw_gemm_nt_grouped")
 
@@ -520,6 +520,7 @@ def test_c5_hybrid_step_one_llama_layer():
     gen = torch.Generator(device="cuda").manual_seed(550)
     gps = _params(C5_SHAPES, torch.bfloat16, gen)
     opt = ApexW(gps, lr=1e-3, weight_decay=0.1, use_muon=True, stochastic_rounding=False)
+    opt.muon_opt.keep_ns_result = True   # the fused update's U, kept for the check below
     muon_idx = [0, 3, 4, 5, 6]
     assert [id(p) for p in opt.muon_params] == [id(gps[i]) for i in muon_idx]
     assert [id(p) for p in opt.adamw_params] == [id(gps[i]) for i in (1, 2, 7, 8)]

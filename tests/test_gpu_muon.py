@@ -186,11 +186,14 @@ def test_hybrid_trajectory_matches_reference_vectors():
             assert float(err.max()) <= 0, i
 
 
-def _grouped(lib, rows):
-    """Schedule and run one grouped launch of host-built problem rows."""
+def _grouped(lib, rows, cus=0):
+    """Schedule and run one grouped launch of host-built problem rows (cus > 0:
+    CUs per queue for the schedule, which then splits tail tiles into halves)."""
     from apexw_amd import _lib
-    probs = np.array(rows, dtype=_lib.GEMM_PROBLEM_DTYPE)
-    items, offsets, n_wg, kind = _lib.gemm_schedule(probs)
+    probs = _lib.gemm_problems(rows)
+    items, offsets, n_wg, kind = _lib.gemm_schedule(probs, cus)
+    if cus:
+        assert np.any((items >> 22) & 3), "no half tiles in the schedule"
     dev = lambda a: torch.from_numpy(a.view(np.uint8).copy()).cuda()  # noqa: E731
     dp, di, do = dev(probs), dev(items), dev(offsets)
     st = lib.apexw_gemm_nt_grouped(dp.data_ptr(), di.data_ptr(), do.data_ptr(), n_wg, kind,
@@ -204,14 +207,17 @@ def _assert_gemm_close(got, ref):
     assert float(err.max()) <= 0, f"max excess {float(err.max()):.3e}"
 
 
-def test_grouped_gemm_symmetric_and_plain_products():
+@pytest.mark.parametrize("cus", [0, 4])
+def test_grouped_gemm_symmetric_and_plain_products(cus):
     """One grouped launch per Newton-Schulz product over matrices of two shapes:
     the symmetric products fill both triangles (bitwise symmetric), the plain
-    product writes both layouts."""
+    product writes both layouts.  cus=4: a schedule for 4 CUs per queue, which
+    splits tiles into 128-row halves (every epilogue kind, the diagonal addend
+    and the [K x N] operand through the half-tile path)."""
     _need_gpu()
     from apexw_amd import _lib
     lib = _lib.load()
-    print("grouped gemm", flush=True)
+    print(f"grouped gemm cus={cus}", flush=True)
     g = torch.Generator().manual_seed(11)
     shapes = [(256, 512), (512, 768), (512, 768)]
     X = [(torch.randn(m, n, generator=g) / math.sqrt(n)).bfloat16() for m, n in shapes]
@@ -225,21 +231,21 @@ def test_grouped_gemm_symmetric_and_plain_products():
     SYM = _lib.GEMM_SYM
     # A = X X^T
     _grouped(lib, [(x.data_ptr(), x.data_ptr(), 0, a.data_ptr(), a.data_ptr(), m, m, n, n, n, 0, m, m, 1.0, 0.0,
-                    SYM, 0) for x, a, (m, n) in zip(dX, dA, shapes)])
+                    SYM, 0) for x, a, (m, n) in zip(dX, dA, shapes)], cus)
     for x, a in zip(X, dA):
         ref = x.float() @ x.float().t()
         _assert_gemm_close(a, ref)
         assert torch.equal(a.cpu(), a.cpu().t())
     # B = c A A + b A
     _grouped(lib, [(a.data_ptr(), a.data_ptr(), a.data_ptr(), b.data_ptr(), b.data_ptr(), m, m, m, m, m, m, m, m,
-                    NS_C, NS_B, SYM, 0) for a, b, (m, _) in zip(dA, dB, shapes)])
+                    NS_C, NS_B, SYM, 0) for a, b, (m, _) in zip(dA, dB, shapes)], cus)
     for a, b in zip(dA, dB):
         af = a.float().cpu()
         _assert_gemm_close(b, NS_C * (af @ af) + NS_B * af)
         assert torch.equal(b.cpu(), b.cpu().t())
     # X' = B X + a X, written row-major and transposed
     _grouped(lib, [(b.data_ptr(), xt.data_ptr(), xt.data_ptr(), c.data_ptr(), ct.data_ptr(), m, n, m, m, m, m, n, m,
-                    1.0, NS_A, 0, 0) for b, xt, c, ct, (m, n) in zip(dB, dXt, dC, dCt, shapes)])
+                    1.0, NS_A, 0, 0) for b, xt, c, ct, (m, n) in zip(dB, dXt, dC, dCt, shapes)], cus)
     for b, x, c, ct in zip(dB, X, dC, dCt):
         _assert_gemm_close(c, b.float().cpu() @ x.float() + NS_A * x.float())
         assert torch.equal(ct.cpu().t(), c.cpu())
@@ -249,7 +255,7 @@ def test_grouped_gemm_symmetric_and_plain_products():
         c.fill_(float("nan"))
     KN = _lib.GEMM_B_KN | _lib.GEMM_ADD_B
     _grouped(lib, [(b.data_ptr(), x.data_ptr(), 0, c.data_ptr(), 0, m, n, m, m, n, 0, n, 0, 1.0, NS_A, KN, 0)
-                   for b, x, c, (m, n) in zip(dB, dX, dC, shapes)])
+                   for b, x, c, (m, n) in zip(dB, dX, dC, shapes)], cus)
     for b, x, c in zip(dB, X, dC):
         _assert_gemm_close(c, b.float().cpu() @ x.float() + NS_A * x.float())
 
@@ -280,3 +286,51 @@ def test_muon_groups_with_different_ns_steps_and_many_matrices():
         d_ref = -lr * U
         d_gpu = p.detach().float().cpu() - h
         assert _rel_fro(d_gpu, d_ref) <= 0.03, (tuple(p.shape), steps, _rel_fro(d_gpu, d_ref))
+
+
+def test_fused_update_dtypes_layouts_and_zero_steps():
+    """The update applied in the last Newton-Schulz product's epilogue, for fp32,
+    bf16 and fp16 parameters, wide and tall (transposed work matrix), column
+    counts that are not multiples of 8 (per-element path) and padded tiles: p
+    equals round(round(p * (1 - lr wd)) - lr * U) from the kept U within one
+    ulp of p's dtype.  A group with ns_steps=0 takes the separate apply pass
+    (U = the normalised momentum)."""
+    _need_gpu()
+    from apexw_amd.muon import ApexMuon
+    g = torch.Generator().manual_seed(33)
+    specs = [((300, 20), torch.float32), ((40, 100), torch.bfloat16), ((520, 264), torch.float16),
+             ((64, 72), torch.float32)]
+    init = [(torch.randn(s, generator=g) * 0.02).to(dt) for s, dt in specs]
+    ps = [torch.nn.Parameter(h.cuda()) for h in init]
+    lr, wd, mu = 0.02, 0.1, 0.9
+    opt = ApexMuon([{"params": ps[:3], "ns_steps": 5}, {"params": ps[3:], "ns_steps": 0}], lr=lr, momentum=mu,
+                   weight_decay=wd, scale_mode="none")
+    opt.keep_ns_result = True
+    grads = [(torch.randn(s, generator=g) * 1e-3).to(dt) for s, dt in specs]
+    for p, gr in zip(ps, grads):
+        p.grad = gr.cuda()
+    opt.step()
+    torch.cuda.synchronize()
+    ws_by_shape = {k[1]: ws for k, ws in opt._ws.items()}
+    for p, h, gr, (shape, dt), steps in zip(ps, init, grads, specs, (5, 5, 5, 0)):
+        rows, cols = shape
+        ws = ws_by_shape[shape]
+        wide = ws.x[steps % 2][0][:min(rows, cols), :max(rows, cols)].float().cpu()
+        U = wide.T if rows > cols else wide
+        if steps:
+            U32 = newton_schulz5((1 - mu) * gr.float(), steps, work_dtype=torch.float32)
+            assert _rel_fro(U, U32) <= 0.03, (shape, _rel_fro(U, U32))
+        decayed = (h.float() * np.float32(1.0 - lr * wd)).to(dt).float()
+        step = np.float32(-lr) * U
+        p_ref = (decayed + step).to(dt).float()
+        got = p.detach().float().cpu()
+        # one ulp of the result, plus the fp32 rounding of the product and sum
+        # (the kernel fuses them into one fma): relative to the operands, which
+        # can exceed the result where they cancel
+        eps = 2.0 ** -7 if dt == torch.bfloat16 else 2.0 ** -10 if dt == torch.float16 else 2.0 ** -23
+        bar = eps * p_ref.abs() + 2.0 ** -23 * (decayed.abs() + step.abs()) + 1e-30
+        ex = (got - p_ref).abs() - bar
+        w = int(ex.argmax())
+        vals = {k: float(v.reshape(-1)[w]) for k, v in
+                (("p0", h.float()), ("got", got), ("ref", p_ref), ("decayed", decayed), ("step", step), ("U", U))}
+        assert float(ex.max()) <= 0, f"{shape} {dt} element {w}: {vals}"

@@ -9,7 +9,9 @@ import os
 import numpy as np
 import torch
 
-from golden.make_golden import _fingerprint, _grad, _param
+from golden.make_golden import (FV_KW, FV_Q8_SHAPES, HOOK_KW, HOOK_SHAPES, SD_CASES, _fingerprint, _grad,
+                                 _param)
+from golden.sd_codec import decode
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
@@ -37,6 +39,19 @@ CASES = {
                     dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, precision="8bit", stochastic_rounding=False),
                     None, ()),
 }
+
+
+# factored-v trajectories (every state tensor recorded as st_<i>_<key>)
+FV_CASES = {
+    "fv_q8_bf16_rne": (FV_Q8_SHAPES, torch.bfloat16, 4, 21, dict(FV_KW, precision="8bit"), None, ()),
+    "fv_q8_fp32_rne": ([(256, 256), (700,)], torch.float32, 3, 22, dict(FV_KW, precision="8bit"), None, ()),
+    "fv_6bit_bf16_rne": ([(512, 1024)], torch.bfloat16, 3, 23, dict(FV_KW, precision="8bit", six_bit=True),
+                         None, ()),
+    "fv_compact_bf16_rne": ([(512, 1024), (768,)], torch.bfloat16, 3, 24, FV_KW, None, ()),
+}
+CASES.update(FV_CASES)
+# in-backward trajectories: name -> (steps, backward passes per step, seed)
+HOOK_CASES = {"hooks_k1_rne": (3, 1, 31), "hooks_k2_rne": (3, 2, 32)}
 
 
 def load(name):
@@ -78,3 +93,58 @@ def bf16_ulp_diff(a, b):
     ia = torch.where(ia < 0, -(ia & 0x7FFF), ia)
     ib = torch.where(ib < 0, -(ib & 0x7FFF), ib)
     return (ia - ib).abs()
+
+
+def hook_inputs(name):
+    """Initial fp32 parameters and, per step, per pass, the grads of the in-backward
+    case ``name`` (grads in the dtype each parameter has after the downcast)."""
+    from oracle import hooks as H
+    steps, passes, seed = HOOK_CASES[name]
+    gold = load(name)
+    gen = torch.Generator().manual_seed(seed)
+    host = [_param(s, torch.float32, gen) for s in HOOK_SHAPES]
+    fp = [_fingerprint(p) for p in host]
+    dts = [H.downcast_dtype(p) for p in host]
+    grads = []
+    for _ in range(steps):
+        per_step = []
+        for _ in range(passes):
+            gs = [_grad(p.shape, dt, gen) for p, dt in zip(host, dts)]
+            fp.extend(_fingerprint(g) for g in gs)
+            per_step.append(gs)
+        grads.append(per_step)
+    np.testing.assert_array_equal(np.array(fp, dtype=np.int64), gold["fingerprint"])
+    return host, grads, gold
+
+
+def sd_inputs(name):
+    """(shapes, dtype, kwargs, the reference's state_dict after 3 steps, the parameters
+    then, the grads of the 2 steps after it, the golden dict) of checkpoint case ``name``."""
+    shapes, dtype, kwargs = SD_CASES[name]
+    gold = load(name)
+    gen = torch.Generator().manual_seed(41 + list(SD_CASES).index(name))
+    host = [_param(s, dtype, gen) for s in shapes]
+    fp = [_fingerprint(p) for p in host]
+    grads = []
+    for step in range(5):
+        gs = [_grad(p.shape, dtype, gen) for p in host]
+        fp.extend(_fingerprint(g) for g in gs)
+        if step >= 3:
+            grads.append(gs)
+    np.testing.assert_array_equal(np.array(fp, dtype=np.int64), gold["fingerprint"])
+    sd = decode(str(gold["sd_skeleton"]), {k: v for k, v in gold.items() if k.startswith("sd_")})
+    mid = [to_torch(gold[f"pmid_{i}"], dtype).reshape(s) for i, s in enumerate(shapes)]
+    return shapes, dtype, kwargs, sd, mid, grads, gold
+
+
+def state_keys(gold, i):
+    """The state tensor names recorded for parameter i."""
+    pre = f"st_{i}_"
+    return sorted(k[len(pre):] for k in gold if k.startswith(pre))
+
+
+def initial_params(name):
+    """The parameters case ``name`` starts from (the generator's first draws)."""
+    shapes, dtype, steps, seed, kwargs, scales, zidx = CASES[name]
+    gen = torch.Generator().manual_seed(seed)
+    return [_param(s, dtype, gen) for s in shapes]

@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from golden_replay import CASES, load, replay, to_torch
+from golden_replay import CASES, HOOK_CASES, SD_CASES, hook_inputs, load, replay, sd_inputs, state_keys, to_torch
 from oracle.clip import clip_grads_
 from oracle.optim import OracleApexW
 
@@ -34,6 +34,15 @@ def test_oracle_matches_reference_trajectory(name):
     params, opt, gold = replay(name, OracleApexW)
     for i, p in enumerate(params):
         np.testing.assert_array_equal(_as_np(p.data).reshape(-1), gold[f"p_{i}"].reshape(-1), err_msg=f"p_{i}")
+        if f"flags_{i}" not in gold:
+            # every state tensor was recorded (factored layouts)
+            keys = state_keys(gold, i)
+            assert keys == sorted(k for k, v in opt.state[p].items() if torch.is_tensor(v) and k != "step")
+            for k in keys:
+                np.testing.assert_array_equal(_as_np(opt.state[p][k]).reshape(-1), gold[f"st_{i}_{k}"].reshape(-1),
+                                              err_msg=f"{k}_{i}")
+            assert float(opt.state[p]["step"]) == float(gold[f"step_{i}"][0])
+            continue
         st = _state_arrays(opt, p)
         for key in ("m", "v", "ms", "vs"):
             if key in st:
@@ -54,3 +63,69 @@ def test_oracle_clip_matches_reference():
     clip_grads_(grads, 1.0)
     for i, g in enumerate(grads):
         np.testing.assert_array_equal(_as_np(g), z[f"gc_{i}"])
+
+
+@pytest.mark.parametrize("name", sorted(HOOK_CASES))
+def test_oracle_hooks_match_reference_trajectory(name):
+    """The in-backward path over several steps: the hooked tensors are stepped once per
+    backward pass by oracle.hooks.flush_8bit (K = 1 until the first step() has seen
+    the anchor's pass count), the anchor and the small tensors accumulate their
+    grads and take the ordinary 8-bit step in step()."""
+    from oracle import hooks as H
+    host, grads, gold = hook_inputs(name)
+    params = [torch.nn.Parameter(h.to(H.downcast_dtype(h))) for h in host]
+    on, anchor, hooked = H.hook_partition(params)
+    assert on and anchor is params[0]
+    hooked_ids = {id(p) for p in hooked}
+    rest = [p for p in params if id(p) not in hooked_ids]
+    kw = dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, precision="8bit", stochastic_rounding=False)
+    rest_opt = OracleApexW(rest, **kw)
+    group = dict(lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.1, decay_norm_only=False,
+                 precision="8bit", stochastic_rounding=False, block_size=None, int4_m=None)
+    states = {}
+    K = 1
+    for per_step in grads:
+        acc = {}
+        for gs in per_step:
+            H.flush_8bit(hooked, [gs[i] for i, p in enumerate(params) if id(p) in hooked_ids], states, group, K=K)
+            for i, p in enumerate(params):
+                if id(p) not in hooked_ids:
+                    acc[i] = gs[i].clone() if i not in acc else acc[i] + gs[i]
+        for i, p in enumerate(params):
+            if id(p) not in hooked_ids:
+                p.grad = acc[i]
+        rest_opt.step()
+        for p in rest:
+            p.grad = None
+        K = len(per_step)
+    np.testing.assert_array_equal(np.array([{torch.float32: 0, torch.bfloat16: 1}[p.dtype] for p in params]),
+                                  gold["dtypes"])
+    for i, p in enumerate(params):
+        np.testing.assert_array_equal(_as_np(p.data).reshape(-1), gold[f"p_{i}"].reshape(-1), err_msg=f"p_{i}")
+        st = states[p] if id(p) in hooked_ids else rest_opt.state[p]
+        for k in ("exp_avg", "exp_avg_scales", "exp_avg_sq", "exp_avg_sq_scales"):
+            np.testing.assert_array_equal(_as_np(st[k]).reshape(-1), gold[f"st_{i}_{k}"].reshape(-1),
+                                          err_msg=f"{k}_{i}")
+        assert float(st["step"]) == float(gold[f"step_{i}"][0]), f"step_{i}"
+
+
+@pytest.mark.parametrize("name", ["sd_compact", "sd_q8"])
+def test_oracle_resumes_reference_checkpoint(name):
+    """The reference's resume from its own checkpoint: a fresh optimizer loads the
+    state_dict written after 3 steps and takes 2 more -- a cold step from non-zero
+    state, then a replayed one.  The oracle, given the same state, lands on the
+    same bits."""
+    shapes, dtype, kwargs, sd, mid, grads, gold = sd_inputs(name)
+    params = [torch.nn.Parameter(m.clone()) for m in mid]
+    opt = OracleApexW(params, **kwargs)
+    for pid, p in zip(sd["param_groups"][0]["params"], params):
+        opt.state[p] = {k: (v.clone() if torch.is_tensor(v) else v) for k, v in sd["state"][pid].items()}
+    for gs in grads:
+        for p, g in zip(params, gs):
+            p.grad = g.clone()
+        opt.step()
+    for i, p in enumerate(params):
+        np.testing.assert_array_equal(_as_np(p.data).reshape(-1), gold[f"p_{i}"].reshape(-1), err_msg=f"p_{i}")
+        for k in state_keys(gold, i):
+            np.testing.assert_array_equal(_as_np(opt.state[p][k]).reshape(-1), gold[f"st_{i}_{k}"].reshape(-1),
+                                          err_msg=f"{k}_{i}")

@@ -13,7 +13,7 @@ import numpy as np
 
 from ._build import LIB_PATH
 
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 # dtype codes
 F32, BF16, F16, U8, I8 = 0, 1, 2, 3, 4
@@ -61,6 +61,17 @@ class Tensor(ctypes.Structure):
     _fields_ = [("p", ctypes.c_void_p), ("g", ctypes.c_void_p), ("m", ctypes.c_void_p), ("v", ctypes.c_void_p),
                 ("m_scale", ctypes.c_void_p), ("v_scale", ctypes.c_void_p), ("n", ctypes.c_int64),
                 ("flags", ctypes.c_uint32), ("block", ctypes.c_uint32)]
+
+
+class StateLayout(ctypes.Structure):
+    """apexw_state_layout: one parameter's moment buffers, for conversion between precision modes."""
+    _fields_ = [("m", ctypes.c_void_p), ("v", ctypes.c_void_p), ("m_scale", ctypes.c_void_p),
+                ("v_scale", ctypes.c_void_p), ("n", ctypes.c_int64), ("kind", ctypes.c_uint32),
+                ("flags", ctypes.c_uint32), ("block", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
+
+
+STATE_DENSE, STATE_Q8 = 0, 1
+assert ctypes.sizeof(StateLayout) == 56
 
 
 class HParams(ctypes.Structure):
@@ -137,6 +148,8 @@ SIGNATURES = {
     "apexw_factored_layout": (ctypes.c_int64, [_vp, _i32, ctypes.POINTER(ctypes.c_int64),
                                                ctypes.POINTER(ctypes.c_int64)]),
     "apexw_factored_step": (ctypes.c_int, [_vp, _i32, _vp, _i32, _i64, _i64, _vp, _i64, _vp, _vp, _HP, _vp]),
+    "apexw_state_decode": (ctypes.c_int, [ctypes.POINTER(StateLayout), _vp, _vp, _vp]),
+    "apexw_state_encode": (ctypes.c_int, [ctypes.POINTER(StateLayout), _vp, _vp, _vp]),
 }
 
 GEMM_TILE = 256

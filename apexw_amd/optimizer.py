@@ -285,6 +285,30 @@ class ApexW(Optimizer):
                     s[k] = v.detach().to(device=p.device).clone()
         self._plans = {}
 
+    def set_precision(self, precision):
+        """Move every group to ``precision`` ("compact" or "8bit", or an alias) and
+        convert each parameter's state whose layout belongs to the other mode on
+        the GPU (fp32 decode, then the new mode's quantizers; step counts kept).
+
+        For resuming a checkpoint in another precision: load_state_dict keeps the
+        saved groups and layouts, as the reference's does, then this converts them.
+        States already in a layout of the new mode are kept as they are."""
+        from . import convert as C
+        prec = S.normalize_precision(precision)
+        if prec not in ("compact", "8bit"):
+            raise NotImplementedError(f"apexw_amd implements the compact and 8-bit AdamW step; not supported: "
+                                      f"precision={prec!r}")
+        peft = S.detect_peft_context(self.param_groups)
+        for group in self.param_groups:
+            group["precision"] = prec
+            for p in group["params"]:
+                st = self.state.get(p)
+                if not st or "exp_avg" not in st:
+                    continue
+                if C.family(st) != C.target_family(p, group, peft):
+                    self.state[p] = C.convert(p, st, group, peft)
+        self._plans = {}
+
     def zero_grad(self, set_to_none=True):
         super().zero_grad(set_to_none=set_to_none)
         self._auto_hook_queue.clear()

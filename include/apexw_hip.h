@@ -29,6 +29,9 @@
  *                           normalisation / transpose (apexw/muon.py:763-792, :163-175, :190-200)
  *   apexw_muon_apply     <- the decoupled decay and scaled update of ApexMuon
  *                           (apexw/muon.py:852-858, :752-759)
+ *   apexw_state_decode / apexw_state_encode: no counterpart (the reference keeps
+ *                           a checkpoint's saved layout, apexw/optimizer.py:2487-2572);
+ *                           they convert a state between precision modes on load
  */
 #ifndef APEXW_HIP_H
 #define APEXW_HIP_H
@@ -39,7 +42,7 @@
 extern "C" {
 #endif
 
-#define APEXW_ABI_VERSION 12
+#define APEXW_ABI_VERSION 13
 
 /* status codes */
 enum apexw_status {
@@ -456,6 +459,55 @@ int apexw_muon_prepare(float* buf, const void* g, int32_t g_dtype, int64_t rows,
  */
 int apexw_muon_apply(void* p, int32_t p_dtype, const void* u, int64_t rows, int64_t cols, int64_t ldu,
                      int32_t u_transposed, float wd_factor, int32_t apply_wd, float neg_lr_eff, void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* Optimizer state across precision modes                                     */
+/* ------------------------------------------------------------------------- */
+
+/*
+ * One parameter's moment buffers (device pointers), for resuming a checkpoint
+ * in another precision mode.  Replaces nothing in the reference: its
+ * load_state_dict keeps the saved layout (apexw/optimizer.py:2487-2572), so a
+ * state saved by one mode cannot be stepped by another; ApexW.load_state_dict
+ * here converts it with these two calls.
+ *   APEXW_STATE_DENSE: m and v in the MDT / VDT dtypes of flags (F32 / BF16 /
+ *     F16), v with n/4 entries when APEXW_FLAG_QUAD; block = 0.
+ *   APEXW_STATE_Q8: m = NF4 codes (APEXW_FLAG_NF4: uint8, two per byte, even
+ *     element in the high nibble, (n+1)/2 bytes) or INT8 codes (n bytes), v =
+ *     log-uint8 codes (n/4 with APEXW_FLAG_QUAD, else n), m_scale / v_scale one
+ *     fp32 per block of `block` elements (<= 2048; a multiple of 8 with NF4 or
+ *     QUAD; the quad v block is block/4 codes under the same scale index).
+ */
+#define APEXW_STATE_DENSE 0u
+#define APEXW_STATE_Q8 1u
+typedef struct apexw_state_layout {
+  void* m;
+  void* v;
+  float* m_scale;
+  float* v_scale;
+  int64_t n;
+  uint32_t kind;
+  uint32_t flags;     /* APEXW_FLAG_MDT/VDT fields (dense), APEXW_FLAG_QUAD, APEXW_FLAG_NF4 (q8) */
+  uint32_t block;
+  uint32_t reserved;  /* 0 */
+} apexw_state_layout;   /* 56 bytes */
+
+/*
+ * Expand the state s (HOST descriptor of device buffers) to fp32 moments:
+ * m_out and v_out receive n floats each (a quad v value on each of its 4
+ * elements); 8-bit codes decode as codebook value (NF4), code (INT8) or
+ * 2^((q-1) 24/254 - 24) (log-uint8, 0 for q = 0) times the block scale.
+ */
+int apexw_state_decode(const apexw_state_layout* s, float* m_out, float* v_out, void* stream);
+
+/*
+ * Build the state s from fp32 moments m_in, v_in (n floats each): dense
+ * buffers rounded to nearest even (quad v: the mean of each 4, summed
+ * pairwise); 8-bit codes and block scales from the values alone, as the
+ * reference's quantizers with no previous scale (apexw/quantization.py:66-126,
+ * :277-357, :381-448), round to nearest.
+ */
+int apexw_state_encode(const apexw_state_layout* s, const float* m_in, const float* v_in, void* stream);
 
 #ifdef __cplusplus
 }

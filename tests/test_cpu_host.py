@@ -35,6 +35,32 @@ def test_struct_layouts_match_header():
     assert ctypes.sizeof(_lib.Tensor) == 64 == _lib.TENSOR_DTYPE.itemsize
     assert ctypes.sizeof(_lib.HParams) == 88
     assert _lib.GEMM_PROBLEM_DTYPE.itemsize == 120
+    assert ctypes.sizeof(_lib.StateLayout) == 56
+
+
+def test_state_conversion_rejects_bad_layouts():
+    """apexw_state_decode / _encode validate the layout before anything is enqueued
+    (stand-in pointers: a rejected call never dereferences them; skipped where a GPU
+    is present, so that a case the checks let through could not launch on them)."""
+    if torch.cuda.is_available():
+        pytest.skip("stand-in device pointers: run where no GPU is present")
+    from apexw_amd import _lib as L
+    lib = L.load()
+    A = 1 << 20
+    lay = L.StateLayout(A, A, A, A, 1002, L.STATE_Q8, L.FLAG_QUAD, 2048, 0)
+    assert lib.apexw_state_encode(ctypes.byref(lay), A, A, None) == 1  # quad, n % 4
+    lay.n, lay.flags, lay.block = 1000, 0, 4096
+    assert lib.apexw_state_encode(ctypes.byref(lay), A, A, None) == 1      # block > 2048
+    lay.block, lay.flags = 1004, L.FLAG_NF4
+    assert lib.apexw_state_encode(ctypes.byref(lay), A, A, None) == 1      # NF4 block not a multiple of 8
+    lay.block, lay.flags, lay.m_scale = 1024, 0, None
+    assert lib.apexw_state_decode(ctypes.byref(lay), A, A, None) == 1      # 8-bit without scales
+    lay = L.StateLayout(A, A, None, None, 1000, L.STATE_DENSE, 3 << L.MDT_SHIFT, 0, 0)
+    assert lib.apexw_state_decode(ctypes.byref(lay), A, A, None) == 2      # m dtype code 3 (u8) is not dense
+    lay.flags, lay.kind = 0, 7
+    assert lib.apexw_state_decode(ctypes.byref(lay), A, A, None) == 1      # unknown kind
+    lay.kind, lay.reserved = L.STATE_DENSE, 1
+    assert lib.apexw_state_decode(ctypes.byref(lay), A, A, None) == 1      # reserved must be 0
 
 
 def test_check_tensor_rejects_bad_descriptors():

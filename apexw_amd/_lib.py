@@ -148,6 +148,8 @@ SIGNATURES = {
     "apexw_factored_layout": (ctypes.c_int64, [_vp, _i32, ctypes.POINTER(ctypes.c_int64),
                                                ctypes.POINTER(ctypes.c_int64)]),
     "apexw_factored_step": (ctypes.c_int, [_vp, _i32, _vp, _i32, _i64, _i64, _vp, _i64, _vp, _vp, _HP, _vp]),
+    "apexw_muon_coordwise": (ctypes.c_int, [_vp, _vp, _i32, _vp, _i32, _i64, _f32, _f32, _i32, _f32, _f32, _i32,
+                                             _f32, _vp]),
     "apexw_state_decode": (ctypes.c_int, [ctypes.POINTER(StateLayout), _vp, _vp, _vp]),
     "apexw_state_encode": (ctypes.c_int, [ctypes.POINTER(StateLayout), _vp, _vp, _vp]),
 }

@@ -23,6 +23,8 @@ int apexw_launch_gemm_nt(const uint16_t*, const uint16_t*, const uint16_t*, uint
                          int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int64_t, int64_t, int64_t,
                          int64_t, int64_t, float, float, hipStream_t);
 int apexw_muon_partials(int64_t n);
+int apexw_launch_muon_coordwise(float*, const void*, int32_t, void*, int32_t, int64_t, float, float, int32_t, float,
+                                float, int32_t, float, hipStream_t);
 int apexw_launch_grad_prep(const apexw_grad_prep*, const apexw_unit*, int64_t, float, uint32_t, hipStream_t);
 int apexw_launch_gemm_grouped(const apexw_gemm_problem*, const uint32_t*, const int32_t*, int32_t, int32_t,
                               hipStream_t);
@@ -440,6 +442,17 @@ int apexw_muon_apply(void* p, int32_t p_dtype, const void* u, int64_t rows, int6
   if (p_dtype != APEXW_F32 && p_dtype != APEXW_BF16 && p_dtype != APEXW_F16) return APEXW_ERR_DTYPE;
   return apexw_launch_muon_apply(p, p_dtype, (const uint16_t*)u, rows, cols, ldu, u_transposed != 0, wd_factor,
                                  apply_wd, neg_lr_eff, (hipStream_t)stream);
+}
+
+int apexw_muon_coordwise(float* buf, const void* g, int32_t g_dtype, void* p, int32_t p_dtype, int64_t n, float mu,
+                         float one_minus_mu, int32_t nesterov, float grad_inv_scale, float wd_factor,
+                         int32_t apply_wd, float neg_lr, void* stream) {
+  if (!buf || !g || !p || n <= 0) return APEXW_ERR_ARG;
+  if (g_dtype != APEXW_F32 && g_dtype != APEXW_BF16 && g_dtype != APEXW_F16) return APEXW_ERR_DTYPE;
+  if (p_dtype != APEXW_F32 && p_dtype != APEXW_BF16 && p_dtype != APEXW_F16) return APEXW_ERR_DTYPE;
+  if (!(grad_inv_scale > 0.0f)) return APEXW_ERR_ARG;
+  return apexw_launch_muon_coordwise(buf, g, g_dtype, p, p_dtype, n, mu, one_minus_mu, nesterov, grad_inv_scale,
+                                     wd_factor, apply_wd, neg_lr, (hipStream_t)stream);
 }
 
 int apexw_grad_clip_coef(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,

@@ -720,6 +720,74 @@ int grid_for(int64_t n) {
 
 }  // namespace
 
+// Coordinate-wise update of a Muon parameter with a dimension under 16 (or a
+// vector): the reference's fallback in ApexMuon._step_single
+// (apexw/muon.py:775-799, :841-858).  One workgroup per tensor:
+//   g = nan_to_num(dtype_round(g * inv)); buf = buf * mu + (1 - mu) g;
+//   s = buf (or lerp(g, buf, mu) with nesterov);
+//   U = s / (std(s, unbiased=False) + 1e-7)   (numel 1: s / (|s| + 1e-7));
+//   p = dtype_round(p * wd_factor) (with decay); p = dtype_round(p + neg_lr * dtype_round(U)).
+// mean and variance are two passes over the tensor, each a workgroup reduction.
+constexpr int kCwThreads = 1024;
+
+APEXW_DEV float block_sum_cw(float x, float* red) {
+  x = wave_sum(x);
+  const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[w] = x;
+  __syncthreads();
+  float t = 0.0f;
+  for (int i = 0; i < nw; ++i) t += red[i];
+  __syncthreads();
+  return t;
+}
+
+template <int GD, int PD>
+__global__ __launch_bounds__(kCwThreads) void muon_coordwise_kernel(float* __restrict__ buf, const void* __restrict__ grad,
+                                                                    void* __restrict__ p, int64_t n, float mu,
+                                                                    float one_minus_mu, int nesterov, float inv,
+                                                                    float wd_factor, int apply_wd, float neg_lr) {
+  __shared__ float red[kCwThreads / 64];
+  const int64_t tid = threadIdx.x, stride = blockDim.x;
+  float sum = 0.0f;
+  for (int64_t i = tid; i < n; i += stride) {
+    const float g = muon_grad<GD>(grad, i, inv);
+    const float m = fmaf(one_minus_mu, g, buf[i] * mu);
+    buf[i] = m;
+    sum += nesterov ? nesterov_source(g, m, mu) : m;
+  }
+  const float mean = block_sum_cw(sum, red) / (float)n;
+  float sq = 0.0f;
+  for (int64_t i = tid; i < n; i += stride) {
+    const float m = buf[i];
+    const float s = nesterov ? nesterov_source(muon_grad<GD>(grad, i, inv), m, mu) : m;
+    const float d = s - mean;
+    sq = fmaf(d, d, sq);
+  }
+  const float std_all = sqrtf(block_sum_cw(sq, red) / (float)n) + 1e-7f;
+  for (int64_t i = tid; i < n; i += stride) {
+    const float m = buf[i];
+    const float s = nesterov ? nesterov_source(muon_grad<GD>(grad, i, inv), m, mu) : m;
+    const float u = s / (n <= 1 ? fabsf(s) + 1e-7f : std_all);
+    float x = load1<PD>(p, i);
+    if (apply_wd) x = rnd<PD>(x * wd_factor);
+    store1<PD>(p, i, rnd<PD>(fmaf(neg_lr, rnd<PD>(u), x)));
+  }
+}
+
+template <int GD>
+void launch_coordwise(float* buf, const void* g, void* p, int32_t p_dtype, int64_t n, float mu, float one_minus_mu,
+                      int nesterov, float inv, float wd_factor, int apply_wd, float neg_lr, hipStream_t stream) {
+  if (p_dtype == APEXW_F32)
+    hipLaunchKernelGGL((muon_coordwise_kernel<GD, APEXW_F32>), dim3(1), dim3(kCwThreads), 0, stream, buf, g, p, n, mu,
+                       one_minus_mu, nesterov, inv, wd_factor, apply_wd, neg_lr);
+  else if (p_dtype == APEXW_BF16)
+    hipLaunchKernelGGL((muon_coordwise_kernel<GD, APEXW_BF16>), dim3(1), dim3(kCwThreads), 0, stream, buf, g, p, n, mu,
+                       one_minus_mu, nesterov, inv, wd_factor, apply_wd, neg_lr);
+  else
+    hipLaunchKernelGGL((muon_coordwise_kernel<GD, APEXW_F16>), dim3(1), dim3(kCwThreads), 0, stream, buf, g, p, n, mu,
+                       one_minus_mu, nesterov, inv, wd_factor, apply_wd, neg_lr);
+}
+
 int apexw_launch_gemm_nt(const uint16_t* a, const uint16_t* b, const uint16_t* et, uint16_t* c, uint16_t* ct,
                          int32_t m, int32_t n, int32_t k, int32_t lda, int32_t ldb, int32_t lde, int32_t ldc,
                          int32_t ldct, int32_t batch, int64_t sa, int64_t sb, int64_t se, int64_t sc, int64_t sct,
@@ -844,5 +912,20 @@ int apexw_launch_muon_apply(void* p, int32_t p_dtype, const uint16_t* u, int64_t
     else hipLaunchKernelGGL((muon_apply_kernel<APEXW_F16, false>), grid, dim3(256), 0, stream, p, u, rows, cols, ldu,
                             wd_factor, apply_wd, neg_lr_eff);
   }
+  return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
+}
+
+int apexw_launch_muon_coordwise(float* buf, const void* g, int32_t g_dtype, void* p, int32_t p_dtype, int64_t n,
+                                float mu, float one_minus_mu, int32_t nesterov, float inv, float wd_factor,
+                                int32_t apply_wd, float neg_lr, hipStream_t stream) {
+  if (g_dtype == APEXW_F32)
+    launch_coordwise<APEXW_F32>(buf, g, p, p_dtype, n, mu, one_minus_mu, nesterov, inv, wd_factor, apply_wd, neg_lr,
+                                stream);
+  else if (g_dtype == APEXW_BF16)
+    launch_coordwise<APEXW_BF16>(buf, g, p, p_dtype, n, mu, one_minus_mu, nesterov, inv, wd_factor, apply_wd, neg_lr,
+                                 stream);
+  else
+    launch_coordwise<APEXW_F16>(buf, g, p, p_dtype, n, mu, one_minus_mu, nesterov, inv, wd_factor, apply_wd, neg_lr,
+                                stream);
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }

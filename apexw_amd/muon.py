@@ -16,7 +16,10 @@ handling.  The step runs through libapexw_hip.so:
   ``apexw_muon_apply`` does it as a separate pass when ``ns_steps == 0``.
 
 Like the reference on a bf16-capable GPU, the Newton-Schulz work dtype is
-bf16 (apexw/muon.py:76-89).  Quantised momentum (precision "8bit"/"ultra"),
+bf16 (apexw/muon.py:76-89).  Vectors and matrices with a dimension under 16
+take the reference's coordinate-wise update (``apexw_muon_coordwise``);
+non-contiguous parameters are stepped in a contiguous copy that is written
+back.  Quantised momentum (precision "8bit"/"ultra"),
 AdEMAMix (beta3), cautious masking, grad centralization, the Polar Express
 coefficients and scale_mode="rms" raise ``NotImplementedError``.
 """
@@ -227,6 +230,7 @@ class ApexMuon(Optimizer):
         super().__init__(params, defaults)
         self._ws = {}
         self._ns_plans = {}
+        self._copies = []
 
     # ------------------------------------------------------------------ state
     def _init_param_state(self, p):
@@ -293,24 +297,26 @@ class ApexMuon(Optimizer):
                 inv_scale = (float(grad_scale.reciprocal().item()) if torch.is_tensor(grad_scale)
                              else 1.0 / float(grad_scale))
             jobs = []
+            # a non-contiguous parameter is stepped in a contiguous copy, written back afterwards
+            self._copies = []
             for gi, group in enumerate(self.param_groups):
                 active = [p for p in group["params"] if p.grad is not None]
                 if not active:
                     continue
+                matrices = []
                 for p in active:
                     if not p.is_cuda:
                         raise RuntimeError("apexw_amd ApexMuon steps CUDA (ROCm) parameters only")
+                    if p.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+                        raise NotImplementedError(f"ApexMuon: unsupported dtype {p.dtype}")
                     rows = p.shape[0] if p.dim() >= 1 else 1
                     if p.dim() < 2 or min(rows, p.numel() // rows) < 16:
-                        raise NotImplementedError(
-                            "ApexMuon: parameters with fewer than 16 rows or columns (the reference's coordinate-wise "
-                            "fallback) are not supported; route them to ApexW (HybridApexW does)")
-                    if not p.is_contiguous():
-                        raise NotImplementedError("ApexMuon: parameters must be contiguous")
-                    if p.grad.dtype != p.dtype:
-                        raise NotImplementedError("ApexMuon: gradient dtype must match the parameter dtype")
+                        # vectors and dimensions under 16: coordinate-wise update (apexw/muon.py:841-847)
+                        self._coordwise(p, group, inv_scale)
+                    else:
+                        matrices.append(p)
                 shapes = defaultdict(list)
-                for p in active:
+                for p in matrices:
                     shapes[tuple(p.shape)].append(p)
                 for shape, plist in shapes.items():
                     # the reference batches same-shape matrices on the GPU (apexw/muon.py:593-615)
@@ -332,7 +338,10 @@ class ApexMuon(Optimizer):
             for j in jobs:
                 if j["steps"] == 0:
                     self._apply(j)
+            for p, work in self._copies:
+                p.copy_(work)
         finally:
+            self._copies = []
             self.grad_scale = None
             self.found_inf = None
         return loss
@@ -355,28 +364,54 @@ class ApexMuon(Optimizer):
                 st["momentum"].data_ptr(), g.data_ptr(), _dtype_code(g.dtype), rows, cols, mu, 1.0 - mu,
                 int(bool(group["nesterov"])), NS_EPS, inv_scale, ws.x[0][i].data_ptr(), None, ws.np_, 0,
                 ws.partial[i].data_ptr(), stream), "apexw_muon_prepare")
-        return {"plist": plist, "group": group, "ws": ws, "rows": rows, "cols": cols,
-                "steps": int(group["ns_steps"]), "batched": len(plist) > 1}
+        return {"plist": plist, "targets": [self._target(p) for p in plist], "group": group, "ws": ws,
+                "rows": rows, "cols": cols, "steps": int(group["ns_steps"]), "batched": len(plist) > 1}
 
     def _update_scalars(self, job):
         """(wd_factor, neg_lr, apply_wd) of the decoupled decay and the scaled
-        orthogonalised update (apexw/muon.py:852-858)."""
+        orthogonalised update (apexw/muon.py:852-858).  On a 16-bit p, torch's
+        add_ (and _foreach_add_) take alpha in p's dtype; mul_ keeps its scalar
+        in fp32 and only the same-dtype _foreach_mul_ of the batched path rounds it."""
         group, p0 = job["group"], job["plist"][0]
         lr, wd = float(group["lr"]), float(group["weight_decay"])
         scale = self._scale(group["scale_mode"], job["rows"], job["cols"])
-        wd_factor, neg_lr = 1.0 - lr * wd, -lr * scale
+        wd_factor, neg_lr = 1.0 - lr * wd, _round_to(p0.dtype, -lr * scale)
         if job["batched"]:
-            # torch._foreach_mul_ / _foreach_add_ over same-dtype lists see the scalars in p's dtype
-            wd_factor, neg_lr = _round_to(p0.dtype, wd_factor), _round_to(p0.dtype, neg_lr)
+            wd_factor = _round_to(p0.dtype, wd_factor)
         return wd_factor, neg_lr, wd != 0.0
+
+    def _target(self, p):
+        """The tensor the update is written into: p itself, or, when p is not
+        contiguous, a contiguous copy that step() writes back into p."""
+        if p.is_contiguous():
+            return p
+        work = p.detach().contiguous()
+        self._copies.append((p, work))
+        return work
+
+    def _coordwise(self, p, group, inv_scale):
+        """The reference's coordinate-wise fallback (apexw/muon.py:841-858): momentum,
+        U = s / (std(s) + 1e-7), p -= lr * 0.05 * U after the decoupled decay."""
+        lib = _lib.load()
+        st = self._init_param_state(p)
+        st["step"] += 1
+        mu = float(group["momentum"])
+        lr, wd = float(group["lr"]), float(group["weight_decay"])
+        g = p.grad if p.grad.is_contiguous() else p.grad.contiguous()
+        dst = self._target(p)
+        stream = torch.cuda.current_stream(p.device).cuda_stream
+        _lib.check(lib.apexw_muon_coordwise(
+            st["momentum"].data_ptr(), g.data_ptr(), _dtype_code(g.dtype), dst.data_ptr(), _dtype_code(p.dtype),
+            p.numel(), mu, 1.0 - mu, int(bool(group["nesterov"])), inv_scale, 1.0 - lr * wd, int(wd != 0.0),
+            _round_to(p.dtype, -lr * 0.05), stream), "apexw_muon_coordwise")
 
     def _apply_args(self, job):
         """Per batch entry, the fused update of the final Newton-Schulz product (NSPlan.run).
         U is the wide work matrix: p's layout when wide, its transpose when tall."""
         wd_factor, neg_lr, apply_wd = self._update_scalars(job)
         rows, cols = job["rows"], job["cols"]
-        return [(p.data_ptr(), _dtype_code(p.dtype), rows, cols, rows > cols, apply_wd, wd_factor, neg_lr)
-                for p in job["plist"]]
+        return [(t.data_ptr(), _dtype_code(t.dtype), rows, cols, rows > cols, apply_wd, wd_factor, neg_lr)
+                for t in job["targets"]]
 
     def _apply(self, job):
         """The update as a separate pass over the work matrix (ns_steps == 0)."""
@@ -385,7 +420,7 @@ class ApexMuon(Optimizer):
         stream = torch.cuda.current_stream(plist[0].device).cuda_stream
         wd_factor, neg_lr, apply_wd = self._update_scalars(job)
         u_buf = ws.x[job["steps"] % 2]           # ping-pong slot of the Newton-Schulz result
-        for i, p in enumerate(plist):
+        for i, p in enumerate(job["targets"]):
             _lib.check(lib.apexw_muon_apply(p.data_ptr(), _dtype_code(p.dtype), u_buf[i].data_ptr(), rows, cols,
                                             ws.np_, int(rows > cols), wd_factor, int(apply_wd), neg_lr, stream),
                        "apexw_muon_apply")

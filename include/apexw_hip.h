@@ -29,6 +29,8 @@
  *                           normalisation / transpose (apexw/muon.py:763-792, :163-175, :190-200)
  *   apexw_muon_apply     <- the decoupled decay and scaled update of ApexMuon
  *                           (apexw/muon.py:852-858, :752-759)
+ *   apexw_muon_coordwise <- ApexMuon._step_single's coordinate-wise fallback for
+ *                           vectors and dimensions under 16 (apexw/muon.py:775-799, :841-858)
  *   apexw_state_decode / apexw_state_encode: no counterpart (the reference keeps
  *                           a checkpoint's saved layout, apexw/optimizer.py:2487-2572);
  *                           they convert a state between precision modes on load
@@ -459,6 +461,21 @@ int apexw_muon_prepare(float* buf, const void* g, int32_t g_dtype, int64_t rows,
  */
 int apexw_muon_apply(void* p, int32_t p_dtype, const void* u, int64_t rows, int64_t cols, int64_t ldu,
                      int32_t u_transposed, float wd_factor, int32_t apply_wd, float neg_lr_eff, void* stream);
+
+/*
+ * Coordinate-wise Muon update of one parameter that Newton-Schulz does not take
+ * (a vector, or a matrix with a dimension under 16): ApexMuon._step_single's
+ * fallback (apexw/muon.py:775-799, :841-858).  n elements, contiguous:
+ *   g   = nan_to_num(dtype_round(g * grad_inv_scale), 0, +-65504)
+ *   buf = buf * mu + (1 - mu) * g                  (fp32)
+ *   s   = buf, or lerp(g, buf, mu) when nesterov
+ *   U   = s / (std(s, unbiased=False) + 1e-7)     (n == 1: s / (|s| + 1e-7))
+ *   p   = round(round(p * wd_factor) + neg_lr * round(U))   (the decay only if apply_wd)
+ * neg_lr = -lr * 0.05 for the reference's fallback scale.  One workgroup.
+ */
+int apexw_muon_coordwise(float* buf, const void* g, int32_t g_dtype, void* p, int32_t p_dtype, int64_t n, float mu,
+                         float one_minus_mu, int32_t nesterov, float grad_inv_scale, float wd_factor,
+                         int32_t apply_wd, float neg_lr, void* stream);
 
 /* ------------------------------------------------------------------------- */
 /* Optimizer state across precision modes                                     */

@@ -11,6 +11,14 @@
   (muon.py:539-861) with the ``HybridApexW`` defaults (hybrid.py:222-321:
   ns_steps 5, scale 0.2*sqrt(max(m, n)), muon lr = 5*lr) and hands the
   remaining parameters to ``OracleApexW``.
+* ``coordwise_step`` restates ``_step_single``'s coordinate-wise fallback for
+  vectors and dimensions under 16 (muon.py:775-799, :841-858): U = s /
+  (std(s, unbiased=False) + 1e-7), scale 0.05.  Pinned by
+  tests/test_oracle_muon_coordwise.py: two elements (the population std is
+  half their distance, where the unbiased one would be 1/sqrt(2) of it), one
+  element (U = s / (|s| + 1e-7)), invariance of U under a positive scaling
+  of the grad from zero momentum, and a first step from zero momentum whose
+  update is -lr * 0.05 * U after the decay.
 """
 
 import math
@@ -73,6 +81,29 @@ def partition_for_hybrid(params, exclude_embeddings=True, min_dim=32):
         elif p.requires_grad:
             aw.append(p)
     return mu, aw
+
+
+@torch.no_grad()
+def coordwise_step(p, grad, buf, *, lr, momentum, weight_decay, nesterov=False, inv_scale=None):
+    """ApexMuon._step_single for a parameter Newton-Schulz does not take (a vector,
+    or a dimension under 16): apexw/muon.py:775-799 then :841-858.  Updates p and
+    the fp32 momentum buf in place; returns U."""
+    g = grad
+    if inv_scale is not None:
+        g = g.mul(inv_scale)                       # p.grad.mul_(inv_scale) in the grad dtype (:566-590)
+    g = torch.nan_to_num(g, nan=0.0, posinf=65504.0, neginf=-65504.0)
+    g_fp = g if g.dtype == torch.float32 else g.float()
+    buf.mul_(momentum).add_(g_fp, alpha=1.0 - momentum)
+    src = g_fp.lerp(buf, momentum) if nesterov else buf
+    if src.numel() <= 1:
+        std = src.abs() + 1e-7
+    else:
+        std = src.std(unbiased=False) + 1e-7
+    U = src / std
+    if weight_decay != 0.0:
+        p.mul_(1.0 - lr * weight_decay)
+    p.add_(U.to(p.dtype), alpha=-lr * 0.05)
+    return U
 
 
 class OracleHybrid:

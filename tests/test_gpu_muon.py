@@ -292,8 +292,9 @@ def test_fused_update_dtypes_layouts_and_zero_steps():
     """The update applied in the last Newton-Schulz product's epilogue, for fp32,
     bf16 and fp16 parameters, wide and tall (transposed work matrix), column
     counts that are not multiples of 8 (per-element path) and padded tiles: p
-    equals round(round(p * (1 - lr wd)) - lr * U) from the kept U within one
-    ulp of p's dtype.  A group with ns_steps=0 takes the separate apply pass
+    equals round(round(p * (1 - lr wd)) + round(-lr) * U) from the kept U within
+    one ulp of p's dtype (alpha rounded to p's dtype, as torch's add_ on a
+    16-bit tensor does).  A group with ns_steps=0 takes the separate apply pass
     (U = the normalised momentum)."""
     _need_gpu()
     from apexw_amd.muon import ApexMuon
@@ -321,7 +322,8 @@ def test_fused_update_dtypes_layouts_and_zero_steps():
             U32 = newton_schulz5((1 - mu) * gr.float(), steps, work_dtype=torch.float32)
             assert _rel_fro(U, U32) <= 0.03, (shape, _rel_fro(U, U32))
         decayed = (h.float() * np.float32(1.0 - lr * wd)).to(dt).float()
-        step = np.float32(-lr) * U
+        # p.add_(U, alpha=-lr) on a 16-bit p takes alpha in p's dtype (torch CPU)
+        step = torch.tensor(-lr, dtype=torch.float32).to(dt).float() * U
         p_ref = (decayed + step).to(dt).float()
         got = p.detach().float().cpu()
         # one ulp of the result, plus the fp32 rounding of the product and sum
@@ -334,3 +336,81 @@ def test_fused_update_dtypes_layouts_and_zero_steps():
         vals = {k: float(v.reshape(-1)[w]) for k, v in
                 (("p0", h.float()), ("got", got), ("ref", p_ref), ("decayed", decayed), ("step", step), ("U", U))}
         assert float(ex.max()) <= 0, f"{shape} {dt} element {w}: {vals}"
+
+
+def _assert_p_close(got, ref, what, upd):
+    """p within one ulp of its dtype (fp32: 1e-6 relative + 1e-9) plus one ulp of
+    the update upd = |lr * 0.05 * U|, which U's rounding to p's dtype can move by
+    that much where the std differs in its last bits (it dominates where p ~ 0)."""
+    dt = got.dtype
+    got, ref, upd = got.detach().cpu().double(), ref.detach().double(), upd.detach().double().abs()
+    if dt == torch.float32:
+        tol = 1e-6 * ref.abs() + 1e-9 + 2.0 ** -23 * upd
+    else:
+        ulp = torch.finfo(dt).eps
+        tol = ulp * (torch.maximum(got.abs(), ref.abs()) + upd) + 1e-30
+    assert bool(((got - ref).abs() <= tol).all()), what
+
+
+COORDWISE = [((64,), torch.bfloat16, torch.bfloat16, False), ((1,), torch.float32, torch.float32, False),
+             ((2,), torch.float32, torch.float32, False), ((8, 4096), torch.bfloat16, torch.bfloat16, True),
+             ((3000,), torch.bfloat16, torch.float32, False), ((40, 12), torch.float32, torch.bfloat16, True),
+             ((15, 15), torch.float16, torch.float16, False)]
+
+
+@pytest.mark.parametrize("shape,pdt,gdt,nesterov", COORDWISE, ids=[f"{c[0]}-{c[1]}-{c[2]}-{c[3]}" for c in COORDWISE])
+def test_coordwise_fallback_matches_oracle(shape, pdt, gdt, nesterov):
+    """Vectors and dimensions under 16 take the reference's coordinate-wise update
+    (apexw/muon.py:841-858); grads may have another dtype than the parameter.
+    Bars: fp32 momentum within 1e-6 relative (the same fmas), p within one ulp of
+    its dtype (the std is a reduction in another order, ~1e-7 relative in U);
+    each step starts the oracle from the GPU's p."""
+    _need_gpu()
+    from apexw_amd.muon import ApexMuon
+    from oracle.muon import coordwise_step
+    print(f"coordwise {shape} {pdt} {gdt} nesterov={nesterov}", flush=True)
+    gen = torch.Generator().manual_seed(sum(shape))
+    host = (torch.randn(shape, generator=gen) * 0.02).to(pdt)
+    p = torch.nn.Parameter(host.cuda())
+    if gdt != pdt:
+        p.grad_dtype = None          # torch checks a grad's dtype against the parameter's unless told not to
+    cp = host.clone()
+    buf = torch.zeros(shape, dtype=torch.float32)
+    opt = ApexMuon([p], lr=1e-2, momentum=0.95, nesterov=nesterov, weight_decay=0.1, ns_steps=5)
+    for step in range(3):
+        g = (torch.randn(shape, generator=gen) * 1e-3 * (1 + step)).to(gdt)
+        p.grad = g.cuda()
+        opt.step()
+        U = coordwise_step(cp, g.clone(), buf, lr=1e-2, momentum=0.95, weight_decay=0.1, nesterov=nesterov)
+        torch.cuda.synchronize()
+        assert p.dtype == cp.dtype
+        _assert_p_close(p, cp, f"p step {step}", 1e-2 * 0.05 * U)
+        mom = opt.state[p]["momentum"].cpu().double()
+        assert float(((mom - buf.double()).abs() - (1e-6 * buf.double().abs() + 1e-12)).max()) <= 0, "momentum"
+        cp.copy_(p.detach().cpu())
+    assert opt.state[p]["step"] == 3
+
+
+def test_noncontiguous_matrix_and_grad_dtype():
+    """A transposed (non-contiguous) parameter is stepped like its contiguous copy,
+    with an fp32 grad on a bf16 parameter."""
+    _need_gpu()
+    from apexw_amd.muon import ApexMuon
+    gen = torch.Generator().manual_seed(5)
+    base = (torch.randn(96, 64, generator=gen) * 0.02).bfloat16().cuda()
+    p_nc = torch.nn.Parameter(base.t())                  # [64 x 96], strides (1, 64)
+    p_c = torch.nn.Parameter(base.t().contiguous())
+    assert not p_nc.is_contiguous()
+    p_nc.grad_dtype = None
+    p_c.grad_dtype = None
+    oa = ApexMuon([p_nc], lr=1e-2, weight_decay=0.1, ns_steps=5)
+    ob = ApexMuon([p_c], lr=1e-2, weight_decay=0.1, ns_steps=5)
+    for _ in range(2):
+        g = torch.randn(64, 96, generator=gen).cuda() * 1e-3
+        p_nc.grad = g.clone()
+        p_c.grad = g.clone()
+        oa.step()
+        ob.step()
+    torch.cuda.synchronize()
+    assert torch.equal(p_nc.detach().contiguous(), p_c.detach())
+    assert not p_nc.is_contiguous()

@@ -28,29 +28,67 @@ struct Ctx {
   uint32_t tflags;
 };
 
-// sanitize, AMP unscale (in place on the grads: _multi_tensor_step,
+// sanitize (san), AMP unscale (in place on the grads: _multi_tensor_step,
 // apexw/optimizer.py:5530-5537, or _prepare_grads before a clip), clip
-template <int GD> APEXW_DEV float prep_grad(float g, const Ctx& c) {
-  if (c.hp->flags & APEXW_HP_SANITIZE) g = sanitize<GD>(g);
+template <int GD> APEXW_DEV float prep_grad(float g, const Ctx& c, bool san) {
+  if (san) g = sanitize<GD>(g);
   if (c.hp->flags & APEXW_HP_UNSCALE) g = rnd<GD>(g * c.hp->grad_inv_scale);
   if (c.hp->flags & APEXW_HP_CLIP) g = rnd<GD>(g * c.coef);
   return g;
 }
 
+// True when any of the 8 grads is NaN or +-Inf (g * 0 is NaN exactly then): the
+// per-element sanitize runs only for such a lane (rare), one fma per element otherwise.
+APEXW_DEV bool any_nonfinite8(const float (&g)[8]) {
+  float t = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) t = fmaf(g[j], 0.0f, t);
+  return !(t == t);
+}
+
+// Quotient and square root: round to nearest (IEEE) without SR; with SR the
+// hardware reciprocal and square root (within 1 ulp), whose last-bit error is far
+// below the 2^-16-relative noise the stochastic rounding adds.
+template <bool SR> APEXW_DEV float q_div(float x, float y) {
+  if constexpr (SR) return x * __builtin_amdgcn_rcpf(y);
+  else return x / y;
+}
+template <bool SR> APEXW_DEV float q_sqrt(float x) {
+  if constexpr (SR) return __builtin_amdgcn_sqrtf(x);
+  else return sqrtf(x);
+}
+
 // p, g, m: 8 elements; v: 8 entries (non-quad) or 2 (quad).  cnt <= 8 valid.
 // e0 is the element index of slot 0 within the tensor (RNG counter).
-template <int PD, int GD, int MD, int VD, bool QUAD>
+// SR: the launch's APEXW_HP_SR flag (a template parameter so that each path
+// compiles to its own code); APEXW_HP_SR_V implies it.
+template <int PD, int GD, int MD, int VD, bool QUAD, bool SR>
 APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8], int cnt,
                        uint32_t e0, const Ctx& c) {
   const apexw_hparams& hp = *c.hp;
-  const bool sr = hp.flags & APEXW_HP_SR;
-  const bool srv = hp.flags & APEXW_HP_SR_V;
+  constexpr bool sr = SR;
+  const bool srv = SR && (hp.flags & APEXW_HP_SR_V);
   const bool wd = c.tflags & APEXW_FLAG_WD;
+  // 32 random bits per element (bits 0-15 round p, bits 16-31 round v): a xorshift32
+  // stream per lane and 8-element group, seeded by a keyed hash of the group's first
+  // element index
   uint32_t rnd_bits[8];
+  if constexpr (SR) {
+    uint32_t rs = mix32(c.key + e0) | 1u;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) rnd_bits[j] = (sr || srv) ? rng_at(c.key, e0 + (uint32_t)j) : 0u;
+    for (int j = 0; j < 8; ++j) {
+      rs ^= rs << 13;
+      rs ^= rs >> 17;
+      rs ^= rs << 5;
+      rnd_bits[j] = rs;
+    }
+  } else {
 #pragma unroll
-  for (int j = 0; j < 8; ++j) g[j] = prep_grad<GD>(g[j], c);
+    for (int j = 0; j < 8; ++j) rnd_bits[j] = 0u;
+  }
+  const bool san = (hp.flags & APEXW_HP_SANITIZE) && any_nonfinite8(g);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) g[j] = prep_grad<GD>(g[j], c, san);
 
   if constexpr (!QUAD) {
     if (hp.mode == APEXW_MODE_SINGLE) {
@@ -131,12 +169,12 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
         vq = rnd<VD>(fmaf(hp.one_minus_beta2, gq, v1));
       }
       v[q] = vq;
-      float den = rnd<VD>(sqrtf(vq));
+      float den = rnd<VD>(q_sqrt<SR>(vq));
       den = rnd<VD>(den + eps_v);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int j = b + i;
-        const float delta = (m[j] / den) * hp.step_size;
+        const float delta = q_div<SR>(m[j], den) * hp.step_size;
         const float x = p[j] - delta;
         p[j] = !p16 ? x : (sr ? sr_round<PD>(x, rnd_bits[j]) : rnd<PD>(x));
       }
@@ -152,12 +190,12 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
         vf = rnd<VD>(fmaf(hp.one_minus_beta2 * g[j], g[j], v1));
       }
       v[j] = vf;
-      float den = rnd<VD>(sqrtf(vf));
+      float den = rnd<VD>(q_sqrt<SR>(vf));
       den = rnd<VD>(den + eps_v);
       if (!p16) {
-        p[j] = p[j] + (-hp.step_size * m[j]) / den;
+        p[j] = p[j] + q_div<SR>(-hp.step_size * m[j], den);
       } else if (sr) {
-        p[j] = sr_round<PD>(p[j] - (m[j] / den) * hp.step_size, rnd_bits[j]);
+        p[j] = sr_round<PD>(p[j] - q_div<SR>(m[j], den) * hp.step_size, rnd_bits[j]);
       } else if (hp.mode == APEXW_MODE_REPLAY) {
         p[j] = rnd<PD>(p[j] - (m[j] / den) * hp.step_size);
       } else {
@@ -168,7 +206,7 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
 }
 
 // Group k (512 elements, 8 per lane) of the unit starting at element `start`.
-template <int PD, int MD, int VD, bool QUAD>
+template <int PD, int MD, int VD, bool QUAD, bool SR>
 APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const Ctx& c) {
   constexpr int GD = PD;
   const int64_t n = t.n;
@@ -211,7 +249,7 @@ APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const 
         v[1] = cnt >= 8 ? load1<VD>(t.v, (e0 >> 2) + 1) : 0.0f;
       }
     }
-    update8<PD, GD, MD, VD, QUAD>(p, g, m, v, cnt, (uint32_t)e0, c);
+    update8<PD, GD, MD, VD, QUAD, SR>(p, g, m, v, cnt, (uint32_t)e0, c);
     if (full) {
       store8<PD>(t.p, e0, p);
       store8<MD>(t.m, e0, m);
@@ -244,6 +282,20 @@ APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const 
   }
 }
 
+template <bool SR>
+APEXW_DEV void dispatch_group(const apexw_tensor& t, int64_t start, int k, const Ctx& c, uint32_t pd, uint32_t vd,
+                              bool quad) {
+  if (pd == APEXW_F32) {
+    if (vd == APEXW_F32) compact_group<APEXW_F32, APEXW_BF16, APEXW_F32, false, SR>(t, start, k, c);
+    else if (quad) compact_group<APEXW_F32, APEXW_BF16, APEXW_BF16, true, SR>(t, start, k, c);
+    else compact_group<APEXW_F32, APEXW_BF16, APEXW_BF16, false, SR>(t, start, k, c);
+  } else {
+    if (vd == APEXW_F32) compact_group<APEXW_BF16, APEXW_BF16, APEXW_F32, false, SR>(t, start, k, c);
+    else if (quad) compact_group<APEXW_BF16, APEXW_BF16, APEXW_BF16, true, SR>(t, start, k, c);
+    else compact_group<APEXW_BF16, APEXW_BF16, APEXW_BF16, false, SR>(t, start, k, c);
+  }
+}
+
 __global__ __launch_bounds__(256) void compact_step_kernel(const apexw_tensor* __restrict__ tensors,
                                                            const apexw_unit* __restrict__ units,
                                                            int64_t n_units, apexw_hparams hp) {
@@ -251,6 +303,9 @@ __global__ __launch_bounds__(256) void compact_step_kernel(const apexw_tensor* _
   Ctx c;
   c.hp = &hp;
   c.coef = (hp.flags & APEXW_HP_CLIP) ? *hp.clip_coef : 1.0f;
+  // SR applies to the 16-bit stores of the cold and replayed steps (the native and
+  // per-parameter modes never set it)
+  const bool sr = (hp.flags & APEXW_HP_SR) && (hp.mode == APEXW_MODE_COLD || hp.mode == APEXW_MODE_REPLAY);
   // one work item = one 512-element group of a unit, so a small launch still
   // puts four waves per unit in flight (the per-element RNG is keyed by the
   // element index, so the split does not change any result)
@@ -267,15 +322,8 @@ __global__ __launch_bounds__(256) void compact_step_kernel(const apexw_tensor* _
     const bool quad = t.flags & APEXW_FLAG_QUAD;
     if (quad && hp.mode == APEXW_MODE_SINGLE) continue;  // rejected on the host; never read v out of range
     if (t.flags & APEXW_FLAG_FACTORED) continue;        // stepped by apexw_factored_step
-    if (pd == APEXW_F32) {
-      if (vd == APEXW_F32) compact_group<APEXW_F32, APEXW_BF16, APEXW_F32, false>(t, start, k, c);
-      else if (quad) compact_group<APEXW_F32, APEXW_BF16, APEXW_BF16, true>(t, start, k, c);
-      else compact_group<APEXW_F32, APEXW_BF16, APEXW_BF16, false>(t, start, k, c);
-    } else {
-      if (vd == APEXW_F32) compact_group<APEXW_BF16, APEXW_BF16, APEXW_F32, false>(t, start, k, c);
-      else if (quad) compact_group<APEXW_BF16, APEXW_BF16, APEXW_BF16, true>(t, start, k, c);
-      else compact_group<APEXW_BF16, APEXW_BF16, APEXW_BF16, false>(t, start, k, c);
-    }
+    if (sr) dispatch_group<true>(t, start, k, c, pd, vd, quad);
+    else dispatch_group<false>(t, start, k, c, pd, vd, quad);
   }
 }
 

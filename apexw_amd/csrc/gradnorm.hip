@@ -17,7 +17,21 @@
 namespace {
 
 // squares of sanitize(g) (when san), unscaled in the grad dtype when unscale
-// (AMP grads are unscaled before the clip, apexw/optimizer.py:227-237)
+// (AMP grads are unscaled before the clip, apexw/optimizer.py:227-237).
+// Sanitizing changes only NaN / +-Inf grads, and one of those makes the lane's sum
+// non-finite: the sum is formed without it, and a lane whose sum is not finite
+// (rare) forms it again with it.
+template <int GD, int N>
+APEXW_DEV float sumsq_vals(const float (&g)[N], bool san, bool unscale, float inv, float acc) {
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    float x = san ? sanitize<GD>(g[j]) : g[j];
+    if (unscale) x = rnd<GD>(x * inv);
+    acc = fmaf(x, x, acc);
+  }
+  return acc;
+}
+
 template <int GD>
 APEXW_DEV float unit_sumsq(const apexw_tensor& t, int64_t start, int64_t cnt, bool san, bool unscale, float inv) {
   const int lane = lane_id();
@@ -29,31 +43,30 @@ APEXW_DEV float unit_sumsq(const apexw_tensor& t, int64_t start, int64_t cnt, bo
 #pragma unroll
     for (int k = 0; k < 4; ++k) load8<GD>(t.g, start + k * 512 + lane * 8, g[k]);
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
+    for (int k = 0; k < 4; ++k) acc = sumsq_vals<GD, 8>(g[k], false, unscale, inv, acc);
+    if (san && !(acc - acc == 0.0f)) {
+      acc = 0.0f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        float x = san ? sanitize<GD>(g[k][j]) : g[k][j];
-        if (unscale) x = rnd<GD>(x * inv);
-        acc = fmaf(x, x, acc);
-      }
+      for (int k = 0; k < 4; ++k) acc = sumsq_vals<GD, 8>(g[k], true, unscale, inv, acc);
+    }
     return wave_sum(acc);
   }
-  for (int64_t rel = (int64_t)lane * 8; rel < cnt; rel += 64 * 8) {
-    const int64_t e0 = start + rel;
-    const int c = (cnt - rel) < 8 ? (int)(cnt - rel) : 8;
-    float g[8];
-    if (vec && c == 8) {
-      load8<GD>(t.g, e0, g);
-    } else {
+  for (int pass = 0; pass < 2; ++pass) {
+    const bool s = pass == 1;
+    acc = 0.0f;
+    for (int64_t rel = (int64_t)lane * 8; rel < cnt; rel += 64 * 8) {
+      const int64_t e0 = start + rel;
+      const int c = (cnt - rel) < 8 ? (int)(cnt - rel) : 8;
+      float g[8];
+      if (vec && c == 8) {
+        load8<GD>(t.g, e0, g);
+      } else {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) g[j] = j < c ? load1<GD>(t.g, e0 + j) : 0.0f;
+        for (int j = 0; j < 8; ++j) g[j] = j < c ? load1<GD>(t.g, e0 + j) : 0.0f;
+      }
+      acc = sumsq_vals<GD, 8>(g, s, unscale, inv, acc);
     }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      float x = san ? sanitize<GD>(g[j]) : g[j];
-      if (unscale) x = rnd<GD>(x * inv);
-      acc = fmaf(x, x, acc);
-    }
+    if (!san || acc - acc == 0.0f) break;
   }
   return wave_sum(acc);
 }

@@ -570,9 +570,11 @@ def test_c5_hybrid_step_one_llama_layer():
                 # the update from the GPU's own U: p = round(round(p * wd_factor) - lr * scale * U)
                 scale = 0.2 * math.sqrt(max(rows, cols))
                 wdf, neg = 1.0 - lr_m * wd, -lr_m * scale
-                if batched:   # same-dtype foreach ops see their scalars in the parameter dtype
+                # torch's add_ (and _foreach_add_) on a bf16 p takes alpha in bf16; mul_ keeps
+                # its scalar in fp32, the same-dtype _foreach_mul_ of the batched path rounds it
+                neg = float(torch.tensor(neg).bfloat16().float())
+                if batched:
                     wdf = float(torch.tensor(wdf).bfloat16().float())
-                    neg = float(torch.tensor(neg).bfloat16().float())
                 decayed = (before[i].float() * np.float32(wdf)).bfloat16().float()
                 p_ref = (decayed + np.float32(neg) * U_gpu.float()).bfloat16()
                 _cmp(gps[i], p_ref.cpu(), f"C5 step {step} p {shape}[{k}]")

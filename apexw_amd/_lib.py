@@ -28,6 +28,7 @@ FLAG_DENSE16 = 1 << 12
 FLAG_SCALAR = 1 << 13
 FLAG_FACTORED = 1 << 14
 FLAG_M6 = 1 << 15
+FLAG_GC = 1 << 16
 
 COMPACT_UNIT = 2048
 
@@ -135,8 +136,10 @@ SIGNATURES = {
     "apexw_gemm_nt_bf16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                           _i32, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _vp]),
     "apexw_check_grad_prep": (ctypes.c_int, [_vp]),
+    "apexw_check_row_means": (ctypes.c_int, [_vp]),
     "apexw_grad_prep_units": (ctypes.c_int64, [_vp]),
     "apexw_grad_prepare": (ctypes.c_int, [_vp, _i32, _vp, _i64, _f32, _u32, _vp]),
+    "apexw_grad_row_means": (ctypes.c_int, [_vp, _i32, _vp, _i64, _f32, _u32, _vp]),
     "apexw_gemm_grouped_items": (ctypes.c_int64, [_vp, _i32]),
     "apexw_gemm_grouped_schedule": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i32, ctypes.POINTER(ctypes.c_int64), _vp,
                                                    ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32)]),

@@ -188,6 +188,9 @@ class StepPlan:
         self._scan_addrs = (self.p_ptrs.ctypes.data, self.p_dtypes.ctypes.data, self.g_ptrs.ctypes.data,
                             self.g_scan.ctypes.data)
         self._scan_status = None
+        # centralization: folded into the compact step and the clip (row means only) unless
+        # the plan holds 8-bit or factored tensors, which read a prepared copy of the grads
+        self.gc_fold = self.gc and not self.single and self.kind == "compact" and not self.factored.any()
         if self.gc and not self.single:
             self._build_prep()
         self._fast_static = None
@@ -199,21 +202,37 @@ class StepPlan:
         self.perm = None
 
     def _build_prep(self):
-        """Prepared-grad buffers and the preparation table (sources filled per step)."""
+        """The preparation table (sources filled per step) and its outputs: per
+        centralized tensor the fp32 row means (folded path), or per tensor a
+        prepared copy of the grad."""
         n = len(self.params)
-        self.gc_out = [torch.empty(p.numel(), dtype=p.dtype, device=self.device) for p in self.params]
         prep = np.zeros(n, dtype=L.GRAD_PREP_DTYPE)
-        prep["out"] = [o.data_ptr() for o in self.gc_out]
-        prep["n"] = [p.numel() for p in self.params]
         # the reference centralizes dim >= 2 grads over dims 1.. (optimizer.py:239-243)
-        prep["row_len"] = [p.numel() // p.shape[0] if p.dim() >= 2 else 0 for p in self.params]
+        prep["row_len"] = [p.numel() // p.shape[0] if p.dim() >= 2 and p.numel() > 0 else 0 for p in self.params]
+        prep["n"] = [p.numel() for p in self.params]
         prep["dtype"] = [_DT[p.dtype] for p in self.params]
+        if self.gc_fold:
+            self.gc_means = [torch.empty(max(p.numel() // int(prep["row_len"][i]), 1) if prep["row_len"][i] else 1,
+                                         dtype=torch.float32, device=self.device)
+                             for i, p in enumerate(self.params)]
+            prep["out"] = [m.data_ptr() for m in self.gc_means]
+            tab = self.host_table
+            rows = prep["row_len"] > 0
+            tab["flags"] = np.where(rows, tab["flags"] | np.uint32(L.FLAG_GC), tab["flags"])
+            tab["m_scale"] = np.where(rows, prep["out"], tab["m_scale"])
+            tab["block"] = np.where(rows, prep["row_len"].astype(np.uint32), tab["block"])
+        else:
+            self.gc_out = [torch.empty(p.numel(), dtype=p.dtype, device=self.device) for p in self.params]
+            prep["out"] = [o.data_ptr() for o in self.gc_out]
         self.host_prep = prep
         self.d_prep = None
         counts = []
         for i in range(n):
             row = prep[i:i + 1].copy()
             row["g"] = 256                 # stand-in source, checked for real at upload
+            if self.gc_fold and not row["row_len"][0]:
+                counts.append(0)          # no centralization: nothing to prepare
+                continue
             k = int(L.load().apexw_grad_prep_units(row.ctypes.data))
             if k < 0:
                 L.check(-k, f"grad preparation of tensor {i}")
@@ -227,11 +246,13 @@ class StepPlan:
         self.d_prep_units = torch.from_numpy(units.view(np.uint8)).to(self.device)
 
     def _prepare_grads(self, inv_scale, stream):
-        """Sanitize, unscale and centralize into the prepared-grad buffers."""
+        """Sanitize, unscale and centralize into the prepared-grad buffers, or (folded
+        path) only the row means of the sanitized, unscaled grads."""
         flags = L.HP_SANITIZE | (L.HP_UNSCALE if inv_scale is not None else 0)
-        st = self._lib.apexw_grad_prepare(self.d_prep.data_ptr(), len(self.params), self.d_prep_units.data_ptr(),
-                                          self.n_prep_units, 1.0 if inv_scale is None else inv_scale, flags, stream)
-        L.check(st, "apexw_grad_prepare")
+        fn = self._lib.apexw_grad_row_means if self.gc_fold else self._lib.apexw_grad_prepare
+        st = fn(self.d_prep.data_ptr(), len(self.params), self.d_prep_units.data_ptr(), self.n_prep_units,
+                1.0 if inv_scale is None else inv_scale, flags, stream)
+        L.check(st, "apexw_grad_row_means" if self.gc_fold else "apexw_grad_prepare")
 
     def _layout_units(self, fast):
         """Device table in launch order and its unit table.  8-bit: full-block-kernel
@@ -336,10 +357,16 @@ class StepPlan:
             if self.d_prep is None or not np.array_equal(ptrs, self.host_prep["g"]):
                 self.host_prep["g"] = ptrs
                 for i in range(len(self.params)):
+                    if self.gc_fold:
+                        if self.host_prep["row_len"][i]:
+                            L.check(self._lib.apexw_check_row_means(self.host_prep[i:i + 1].ctypes.data),
+                                    f"row means of tensor {i}")
+                        continue
                     L.check(self._lib.apexw_check_grad_prep(self.host_prep[i:i + 1].ctypes.data),
                             f"grad preparation of tensor {i}")
                 self.d_prep = torch.from_numpy(self.host_prep.view(np.uint8).copy()).to(self.device)
-            ptrs = np.fromiter((o.data_ptr() for o in self.gc_out), dtype=np.uint64, count=len(self.params))
+            if not self.gc_fold:
+                ptrs = np.fromiter((o.data_ptr() for o in self.gc_out), dtype=np.uint64, count=len(self.params))
         if self.d_table is None or not np.array_equal(ptrs, self.host_table["g"]):
             self.host_table["g"] = ptrs
             fast = self._validate_and_align()
@@ -414,6 +441,11 @@ class StepPlan:
         if self.single:
             # the per-parameter update takes the grads as they are (no sanitize, clip, AMP or centralization)
             sanitize, clip, inv_scale = False, None, None
+        elif self.gc_fold:
+            # _prepare_grads with centralization, folded: the row means first; the clip
+            # and the step read the raw grads and sanitize, unscale and subtract them
+            self._prepare_grads(inv_scale, stream)
+            sanitize = True
         elif self.gc:
             # _prepare_grads with centralization: sanitize, unscale, centralize;
             # the clip and the step then see finite, unscaled grads

@@ -26,6 +26,7 @@ int apexw_muon_partials(int64_t n);
 int apexw_launch_muon_coordwise(float*, const void*, int32_t, void*, int32_t, int64_t, float, float, int32_t, float,
                                 float, int32_t, float, hipStream_t);
 int apexw_launch_grad_prep(const apexw_grad_prep*, const apexw_unit*, int64_t, float, uint32_t, hipStream_t);
+int apexw_launch_row_means(const apexw_grad_prep*, const apexw_unit*, int64_t, float, uint32_t, hipStream_t);
 int apexw_launch_gemm_grouped(const apexw_gemm_problem*, const uint32_t*, const int32_t*, int32_t, int32_t,
                               hipStream_t);
 int apexw_launch_muon_prepare(float*, const void*, int32_t, int64_t, int64_t, float, float, int32_t, float, float,
@@ -107,9 +108,11 @@ int apexw_abi_version(void) { return APEXW_ABI_VERSION; }
 // (0 = compact, 1 = 8-bit).  Returns APEXW_OK or the reason it is unsupported.
 int apexw_check_tensor(const apexw_tensor* t, int32_t kind) {
   if (!t || !t->p || !t->g || !t->m || !t->v || t->n <= 0) return APEXW_ERR_ARG;
+  if ((t->flags & APEXW_FLAG_GC) && kind != 0) return APEXW_ERR_ARG;   // folded centralization: compact step only
   if (kind == 0 || kind == 3) {
     if (!apexw_compact_flags_ok(t->flags)) return APEXW_ERR_DTYPE;
     if ((t->flags & APEXW_FLAG_QUAD) && (kind == 3 || (t->n % 4) != 0)) return APEXW_ERR_ARG;
+    if ((t->flags & APEXW_FLAG_GC) && (!t->m_scale || t->block == 0 || (t->n % t->block) != 0)) return APEXW_ERR_ARG;
   } else if (kind == 4) {
     // factored row: v / v_scale are the fp32 row / column EMAs
     const uint32_t f = t->flags;
@@ -476,6 +479,18 @@ int apexw_check_grad_prep(const apexw_grad_prep* d) {
   return APEXW_OK;
 }
 
+int apexw_check_row_means(const apexw_grad_prep* d) {
+  if (!d || !d->g || !d->out || d->n <= 0 || d->row_len <= 0 || d->reserved) return APEXW_ERR_ARG;
+  if (d->dtype != APEXW_F32 && d->dtype != APEXW_BF16 && d->dtype != APEXW_F16) return APEXW_ERR_DTYPE;
+  if (d->n % d->row_len) return APEXW_ERR_ARG;
+  const int64_t size = d->dtype == APEXW_F32 ? 4 : 2;
+  const uintptr_t g = (uintptr_t)d->g, o = (uintptr_t)d->out;
+  const uintptr_t g_end = g + (uintptr_t)(d->n * size), o_end = o + (uintptr_t)(d->n / d->row_len * 4);
+  if (g < o_end && o < g_end) return APEXW_ERR_ARG;   // the means must not alias the grad
+  if ((g & (uintptr_t)(size - 1)) || (o & 3u)) return APEXW_ERR_ALIGN;
+  return APEXW_OK;
+}
+
 int64_t apexw_grad_prep_units(const apexw_grad_prep* d) {
   const int st = apexw_check_grad_prep(d);
   if (st != APEXW_OK) return -st;
@@ -488,6 +503,14 @@ int apexw_grad_prepare(const apexw_grad_prep* preps, int32_t n_preps, const apex
   if (flags & ~(APEXW_HP_SANITIZE | APEXW_HP_UNSCALE)) return APEXW_ERR_ARG;
   if ((flags & APEXW_HP_UNSCALE) && !(grad_inv_scale > 0.0f)) return APEXW_ERR_ARG;
   return apexw_launch_grad_prep(preps, units, n_units, grad_inv_scale, flags, (hipStream_t)stream);
+}
+
+int apexw_grad_row_means(const apexw_grad_prep* preps, int32_t n_preps, const apexw_unit* units, int64_t n_units,
+                         float grad_inv_scale, uint32_t flags, void* stream) {
+  if (!preps || !units || n_preps <= 0 || n_units < 0) return APEXW_ERR_ARG;
+  if (flags & ~(APEXW_HP_SANITIZE | APEXW_HP_UNSCALE)) return APEXW_ERR_ARG;
+  if ((flags & APEXW_HP_UNSCALE) && !(grad_inv_scale > 0.0f)) return APEXW_ERR_ARG;
+  return apexw_launch_row_means(preps, units, n_units, grad_inv_scale, flags, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -29,12 +29,37 @@ struct Ctx {
 };
 
 // sanitize (san), AMP unscale (in place on the grads: _multi_tensor_step,
-// apexw/optimizer.py:5530-5537, or _prepare_grads before a clip), clip
-template <int GD> APEXW_DEV float prep_grad(float g, const Ctx& c, bool san) {
+// apexw/optimizer.py:5530-5537, or _prepare_grads before a clip), grad
+// centralization (g - its row's mean, in the grad dtype, when gc), clip: the
+// order of _prepare_grads (apexw/optimizer.py:204-258)
+template <int GD> APEXW_DEV float prep_grad(float g, const Ctx& c, bool san, bool gc, float mean) {
   if (san) g = sanitize<GD>(g);
   if (c.hp->flags & APEXW_HP_UNSCALE) g = rnd<GD>(g * c.hp->grad_inv_scale);
+  if (gc) g = rnd<GD>(g - mean);
   if (c.hp->flags & APEXW_HP_CLIP) g = rnd<GD>(g * c.coef);
   return g;
+}
+
+// Row means of a centralized grad for the 8 elements from e0: the tensor's
+// row_len (t.block) elements form a row; t.m_scale holds each row's mean.
+APEXW_DEV void row_means8(const apexw_tensor& t, int64_t e0, float (&mean)[8]) {
+  const int64_t rl = (int64_t)t.block;
+  const float* means = t.m_scale;
+  const int64_t rows = t.n / rl;
+  if (rl >= 8) {
+    // at most one row boundary inside the 8 elements
+    const int64_t row = e0 / rl, col = e0 - row * rl;
+    const float m0 = means[row];
+    const float m1 = (col + 8 > rl && row + 1 < rows) ? means[row + 1] : m0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mean[j] = col + j < rl ? m0 : m1;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t r = (e0 + j) / rl;
+      mean[j] = means[r < rows ? r : rows - 1];
+    }
+  }
 }
 
 // True when any of the 8 grads is NaN or +-Inf (g * 0 is NaN exactly then): the
@@ -64,7 +89,7 @@ template <bool SR> APEXW_DEV float q_sqrt(float x) {
 // compiles to its own code); APEXW_HP_SR_V implies it.
 template <int PD, int GD, int MD, int VD, bool QUAD, bool SR>
 APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8], int cnt,
-                       uint32_t e0, const Ctx& c) {
+                       uint32_t e0, const Ctx& c, bool gc, const float (&mean)[8]) {
   const apexw_hparams& hp = *c.hp;
   constexpr bool sr = SR;
   const bool srv = SR && (hp.flags & APEXW_HP_SR_V);
@@ -88,7 +113,7 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
   }
   const bool san = (hp.flags & APEXW_HP_SANITIZE) && any_nonfinite8(g);
 #pragma unroll
-  for (int j = 0; j < 8; ++j) g[j] = prep_grad<GD>(g[j], c, san);
+  for (int j = 0; j < 8; ++j) g[j] = prep_grad<GD>(g[j], c, san, gc, mean[j]);
 
   if constexpr (!QUAD) {
     if (hp.mode == APEXW_MODE_SINGLE) {
@@ -249,7 +274,10 @@ APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const 
         v[1] = cnt >= 8 ? load1<VD>(t.v, (e0 >> 2) + 1) : 0.0f;
       }
     }
-    update8<PD, GD, MD, VD, QUAD, SR>(p, g, m, v, cnt, (uint32_t)e0, c);
+    const bool gc = c.tflags & APEXW_FLAG_GC;
+    float mean[8];
+    if (gc) row_means8(t, e0, mean);
+    update8<PD, GD, MD, VD, QUAD, SR>(p, g, m, v, cnt, (uint32_t)e0, c, gc, mean);
     if (full) {
       store8<PD>(t.p, e0, p);
       store8<MD>(t.m, e0, m);

@@ -22,14 +22,41 @@ namespace {
 // non-finite: the sum is formed without it, and a lane whose sum is not finite
 // (rare) forms it again with it.
 template <int GD, int N>
-APEXW_DEV float sumsq_vals(const float (&g)[N], bool san, bool unscale, float inv, float acc) {
+APEXW_DEV float sumsq_vals(const float (&g)[N], bool san, bool unscale, float inv, float acc, bool gc,
+                           const float (&mean)[N]) {
 #pragma unroll
   for (int j = 0; j < N; ++j) {
     float x = san ? sanitize<GD>(g[j]) : g[j];
     if (unscale) x = rnd<GD>(x * inv);
+    if (gc) x = rnd<GD>(x - mean[j]);
     acc = fmaf(x, x, acc);
   }
   return acc;
+}
+
+// Row means (APEXW_FLAG_GC: t.m_scale holds one per row of t.block elements) of
+// the 8 elements from e0; zeros for a tensor that is not centralized.
+APEXW_DEV void clip_means8(const apexw_tensor& t, int64_t e0, float (&mean)[8]) {
+  if (!(t.flags & APEXW_FLAG_GC)) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mean[j] = 0.0f;
+    return;
+  }
+  const int64_t rl = (int64_t)t.block, rows = t.n / rl;
+  if (rl >= 8) {
+    // at most one row boundary inside the 8 elements
+    const int64_t row = e0 / rl, col = e0 - row * rl;
+    const float m0 = t.m_scale[row < rows ? row : rows - 1];
+    const float m1 = (col + 8 > rl && row + 1 < rows) ? t.m_scale[row + 1] : m0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mean[j] = col + j < rl ? m0 : m1;
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int64_t r = (e0 + j) / rl;
+    mean[j] = t.m_scale[r < rows ? r : rows - 1];
+  }
 }
 
 template <int GD>
@@ -42,15 +69,20 @@ APEXW_DEV float unit_sumsq(const apexw_tensor& t, int64_t start, int64_t cnt, bo
     float g[4][8];
 #pragma unroll
     for (int k = 0; k < 4; ++k) load8<GD>(t.g, start + k * 512 + lane * 8, g[k]);
+    const bool gc = t.flags & APEXW_FLAG_GC;
+    float mean[4][8];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) acc = sumsq_vals<GD, 8>(g[k], false, unscale, inv, acc);
+    for (int k = 0; k < 4; ++k) clip_means8(t, start + k * 512 + lane * 8, mean[k]);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc = sumsq_vals<GD, 8>(g[k], false, unscale, inv, acc, gc, mean[k]);
     if (san && !(acc - acc == 0.0f)) {
       acc = 0.0f;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) acc = sumsq_vals<GD, 8>(g[k], true, unscale, inv, acc);
+      for (int k = 0; k < 4; ++k) acc = sumsq_vals<GD, 8>(g[k], true, unscale, inv, acc, gc, mean[k]);
     }
     return wave_sum(acc);
   }
+  const bool gc = t.flags & APEXW_FLAG_GC;
   for (int pass = 0; pass < 2; ++pass) {
     const bool s = pass == 1;
     acc = 0.0f;
@@ -64,7 +96,9 @@ APEXW_DEV float unit_sumsq(const apexw_tensor& t, int64_t start, int64_t cnt, bo
 #pragma unroll
         for (int j = 0; j < 8; ++j) g[j] = j < c ? load1<GD>(t.g, e0 + j) : 0.0f;
       }
-      acc = sumsq_vals<GD, 8>(g, s, unscale, inv, acc);
+      float mean[8];
+      clip_means8(t, e0, mean);
+      acc = sumsq_vals<GD, 8>(g, s, unscale, inv, acc, gc, mean);
     }
     if (!san || acc - acc == 0.0f) break;
   }
@@ -207,6 +241,48 @@ APEXW_DEV void prep_unit(const apexw_grad_prep& d, int64_t unit, bool san, bool 
   }
 }
 
+// Row means only (the fold of centralization into the step kernels): one workgroup
+// per row of a descriptor with row_len > 0; d.out is a float array of one mean
+// per row, each the grad dtype's rounding of the fp32 row sum over row_len of
+// the sanitized, unscaled grads -- the value prep_unit subtracts.
+template <int GD>
+APEXW_DEV void mean_unit(const apexw_grad_prep& d, int64_t row, bool san, bool unscale, float inv, float* red) {
+  const int tid = threadIdx.x;
+  const int64_t lo = row * d.row_len, hi = lo + d.row_len;
+  const PrepSpan sp = prep_span<GD>(d, lo, hi);
+  const int64_t head = sp.a - lo, n_end = head + (hi - sp.b);
+  float s = 0.0f;
+  for (int64_t i = sp.a + (int64_t)tid * 8; i < sp.b; i += 2048) {
+    float x[8];
+    prep_vec8<GD>(d.g, i, san, unscale, inv, x);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s += x[j];
+  }
+  for (int64_t k = tid; k < n_end; k += 256) {
+    const int64_t i = k < head ? lo + k : sp.b + (k - head);
+    s += prep_value<GD>(d.g, i, san, unscale, inv);
+  }
+  s = wave_sum(s);
+  if ((tid & 63) == 0) red[tid >> 6] = s;
+  __syncthreads();
+  if (tid == 0) ((float*)d.out)[row] = rnd<GD>(((red[0] + red[1]) + (red[2] + red[3])) / (float)d.row_len);
+}
+
+__global__ __launch_bounds__(256) void row_means_kernel(const apexw_grad_prep* __restrict__ preps,
+                                                        const apexw_unit* __restrict__ units, int64_t n_units,
+                                                        float inv, uint32_t flags) {
+  __shared__ float red[4];
+  const bool san = flags & APEXW_HP_SANITIZE, unscale = flags & APEXW_HP_UNSCALE;
+  for (int64_t u = blockIdx.x; u < n_units; u += gridDim.x) {
+    const apexw_unit un = units[u];
+    const apexw_grad_prep& d = preps[un.tensor];
+    if (d.dtype == APEXW_F32) mean_unit<APEXW_F32>(d, un.unit, san, unscale, inv, red);
+    else if (d.dtype == APEXW_BF16) mean_unit<APEXW_BF16>(d, un.unit, san, unscale, inv, red);
+    else mean_unit<APEXW_F16>(d, un.unit, san, unscale, inv, red);
+    __syncthreads();   // red is reused by the next unit
+  }
+}
+
 __global__ __launch_bounds__(256) void grad_prep_kernel(const apexw_grad_prep* __restrict__ preps,
                                                         const apexw_unit* __restrict__ units, int64_t n_units,
                                                         float inv, uint32_t flags) {
@@ -235,6 +311,14 @@ int apexw_launch_grad_prep(const apexw_grad_prep* preps, const apexw_unit* units
 int apexw_launch_clip(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,
                       int64_t unit_size, const int64_t* unit_begin, float* unit_partial, float* tensor_norm,
                       float clip, float inv, uint32_t flags, float* coef, hipStream_t stream);
+
+int apexw_launch_row_means(const apexw_grad_prep* preps, const apexw_unit* units, int64_t n_units, float inv,
+                           uint32_t flags, hipStream_t stream) {
+  if (n_units <= 0) return APEXW_OK;
+  const int64_t want = n_units < 65536 ? n_units : 65536;
+  hipLaunchKernelGGL(row_means_kernel, dim3((unsigned)want), dim3(256), 0, stream, preps, units, n_units, inv, flags);
+  return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
+}
 
 // ---------------------------------------------------------------------------
 // Allocation-free clip coefficient: the per-unit partials and per-tensor norms

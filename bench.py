@@ -97,13 +97,15 @@ CONFIGS = {
     "c3bwd": dict(workload="C3 shapes, 8-bit ApexW, the same backward with the in-backward hooks removed "
                            "(one step after it), bf16, SR on", shapes=llama3_8b_shapes(), dtype=torch.bfloat16,
                   backward="plain", kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, precision="8bit")),
+    # the clip's norm pass reads every grad once before the step reads it again (a global
+    # norm must be complete before any element is updated): 2 grad reads
     "c4": dict(workload="C4 compact ApexW step, 20k ragged bf16 tensors, clip 1.0", shapes=ragged_shapes(),
                dtype=torch.bfloat16, kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, clip_grad_norm=1.0),
-               zero_frac=0.05),
-    # grad centralization: the prepared copy is written once (g read twice: row sums, then
-    # subtract) and read by the clip and the step; counted as 4 grad passes
+               zero_frac=0.05, grad_reads=2),
+    # grad centralization folded into the clip and the step: the row means are one more
+    # grad read before them (3 grad reads; 1-D grads are read twice, counted as 3)
     "c4gc": dict(workload="C4 compact ApexW step, 20k ragged bf16 tensors, clip 1.0, grad_centralization=True",
-                 shapes=ragged_shapes(), dtype=torch.bfloat16, grad_reads=4,
+                 shapes=ragged_shapes(), dtype=torch.bfloat16, grad_reads=3,
                  kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, clip_grad_norm=1.0,
                              grad_centralization=True), zero_frac=0.05),
     "c5": dict(workload="C5 hybrid Muon step (use_muon=True), one Llama-3-8B layer's matrices + 2 RMSNorm, bf16",

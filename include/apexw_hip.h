@@ -73,6 +73,10 @@ enum apexw_dtype { APEXW_F32 = 0, APEXW_BF16 = 1, APEXW_F16 = 2, APEXW_U8 = 3, A
 #define APEXW_FLAG_FACTORED (1u << 14)  /* factored second moment: stepped by apexw_factored_step;
                                            the compact and 8-bit step kernels skip the row */
 #define APEXW_FLAG_M6 (1u << 15)        /* factored 8-bit: packed 6-bit m (4 codes in 3 bytes) */
+#define APEXW_FLAG_GC (1u << 16)        /* compact step and clip: grad centralization folded in; the grad
+                                           is read raw and g - mean(row) taken in its dtype (after
+                                           sanitize / unscale, before the clip), with m_scale = the fp32
+                                           row means (apexw_grad_row_means) and block = the row length */
 
 /*
  * One tensor of a multi-tensor launch (device-resident array, 64 bytes each).
@@ -311,6 +315,22 @@ int64_t apexw_grad_prep_units(const apexw_grad_prep* d);
  * entries as for the step), one workgroup per unit. */
 int apexw_grad_prepare(const apexw_grad_prep* preps, int32_t n_preps, const apexw_unit* units, int64_t n_units,
                        float grad_inv_scale, uint32_t flags, void* stream);
+
+/*
+ * Row means only, for centralization folded into the compact step and the clip
+ * (APEXW_FLAG_GC): per descriptor with row_len > 0, out is a float array of
+ * n / row_len entries and entry r receives dtype_round(sum of row r of
+ * sanitized, unscaled g / row_len) -- the mean apexw_grad_prepare subtracts.
+ * Units are the descriptors' rows (unit = row index), one workgroup each.
+ * Replaces the same _prepare_grads step as apexw_grad_prepare
+ * (apexw/optimizer.py:238-243) without writing a prepared copy of the grads.
+ */
+int apexw_grad_row_means(const apexw_grad_prep* preps, int32_t n_preps, const apexw_unit* units, int64_t n_units,
+                         float grad_inv_scale, uint32_t flags, void* stream);
+
+/* Validate one descriptor (host copy) of apexw_grad_row_means: row_len > 0 divides n, out holds
+ * n / row_len floats that do not overlap the grad. */
+int apexw_check_row_means(const apexw_grad_prep* d);
 
 /* ------------------------------------------------------------------------- */
 /* Muon: Newton-Schulz on the matrix cores                                    */

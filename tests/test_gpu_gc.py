@@ -1,10 +1,13 @@
-"""GPU: gradient centralization (grad_centralization=True) through
-apexw_grad_prepare, against the CPU oracle.
+"""GPU: gradient centralization (grad_centralization=True) against the CPU oracle.
 
-* the prepared grads (sanitized, centralized per row of every dim >= 2 grad)
-  vs the oracle's _prepare_grads: bf16 within 1 ulp (the row mean is a sum in
-  a different order, rounded to bf16), fp32 within 1e-6 of the row's largest
-  |g|;
+Compact groups fold it into the step and the clip (apexw_grad_row_means writes
+one mean per row, the kernels subtract it from the raw grad); 8-bit groups
+read a prepared copy (apexw_grad_prepare).
+* the prepared grads (8-bit plan: sanitized, centralized per row of every
+  dim >= 2 grad) vs the oracle's _prepare_grads, and the row means (compact
+  plan) vs torch's mean of the sanitized grads: bf16 within 1 ulp (the row
+  mean is a sum in a different order, rounded to bf16), fp32 within 1e-6 of
+  the row's largest |g|;
 * full steps with bf16 params (compact and 8-bit, SR off) at the parity bars of
   test_gpu_parity.py;
 * with AMP and the clip as well: the 2^10-scaled step equals the unscaled one
@@ -29,6 +32,39 @@ def _need_gpu():
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_row_means_match_oracle(dtype):
+    _need_gpu()
+    from apexw_amd import ApexW
+    from oracle.compact import sanitize_grads
+    print(f"gc row means {dtype}", flush=True)
+    gen = torch.Generator().manual_seed(11)
+    host = [(torch.randn(s, generator=gen) * 0.02).to(dtype) for s in SHAPES]
+    grads = [(torch.randn(s, generator=gen) * 1e-3 + 5e-4).to(dtype) for s in SHAPES]
+    grads[0][3, 7] = float("nan")
+    gps = [torch.nn.Parameter(h.cuda()) for h in host]
+    for p, g in zip(gps, grads):
+        p.grad = g.cuda()
+    opt = ApexW(gps, lr=1e-3, grad_centralization=True, stochastic_rounding=False)
+    opt.step()
+    torch.cuda.synchronize()
+    plan = next(iter(opt._plans.values()))
+    assert plan.gc_fold
+    for i, g in enumerate(sanitize_grads([g.clone() for g in grads])):
+        if g.dim() < 2:
+            continue
+        ref = g.mean(dim=tuple(range(1, g.dim()))).reshape(-1)       # torch's mean in the grad dtype
+        got = plan.gc_means[i].cpu()
+        assert got.numel() == ref.numel()
+        if dtype == torch.bfloat16:
+            assert torch.equal(got.bfloat16().float(), got), i          # the means are bf16 values
+            d = bf16_ulp_diff(got.bfloat16(), ref)
+            assert int(d.max()) <= 1, (i, int(d.max()))
+        else:
+            tol = 1e-6 * g.reshape(g.shape[0], -1).abs().amax(dim=1)
+            assert bool(((got.double() - ref.double()).abs() <= tol.double()).all()), i
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_prepared_grads_match_oracle(dtype):
     _need_gpu()
     from apexw_amd import ApexW
@@ -41,10 +77,12 @@ def test_prepared_grads_match_oracle(dtype):
     gps = [torch.nn.Parameter(h.cuda()) for h in host]
     for p, g in zip(gps, grads):
         p.grad = g.cuda()
-    opt = ApexW(gps, lr=1e-3, grad_centralization=True, stochastic_rounding=False)
+    # 8-bit groups step a prepared copy of the grads
+    opt = ApexW(gps, lr=1e-3, grad_centralization=True, stochastic_rounding=False, precision="8bit")
     opt.step()
     torch.cuda.synchronize()
     plan = next(iter(opt._plans.values()))
+    assert not plan.gc_fold
     cps = [torch.nn.Parameter(h.clone()) for h in host]
     ref, _ = OracleApexW(cps, grad_centralization=True)._prepare([g.clone() for g in grads], sanitize=True)
     for i, (out, r) in enumerate(zip(plan.gc_out, ref)):

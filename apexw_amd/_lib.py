@@ -13,7 +13,7 @@ import numpy as np
 
 from ._build import LIB_PATH
 
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 # dtype codes
 F32, BF16, F16, U8, I8 = 0, 1, 2, 3, 4
@@ -42,6 +42,7 @@ HP_LERP_HI = 1 << 4
 HP_LOOK_HI = 1 << 5
 HP_UNSCALE = 1 << 6
 HP_FV_SANITIZE = 1 << 7
+HP_AMP = 1 << 8
 
 STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported dtype combination", 3: "launch failed",
           4: "misaligned pointer", 5: "exceeds the fixed workspace of the allocation-free entry point"}
@@ -83,7 +84,16 @@ class HParams(ctypes.Structure):
                 ("lerp_coef", ctypes.c_float), ("look_coef", ctypes.c_float),
                 ("bc2_sqrt", ctypes.c_float), ("gain_hi", ctypes.c_float), ("gain_lo", ctypes.c_float),
                 ("clip_coef", ctypes.c_void_p), ("seed", ctypes.c_uint64), ("step", ctypes.c_uint32),
-                ("mode", ctypes.c_uint32), ("flags", ctypes.c_uint32), ("grad_inv_scale", ctypes.c_float)]
+                ("mode", ctypes.c_uint32), ("flags", ctypes.c_uint32), ("grad_inv_scale", ctypes.c_float),
+                ("amp", ctypes.c_void_p)]
+
+
+# apexw_amp_launch: one launch's host inputs to apexw_amp_prepare; apexw_amp_dyn: its device output
+AMP_LAUNCH_DTYPE = np.dtype([("lr", np.float64), ("beta1", np.float64), ("beta2", np.float64), ("eps", np.float64),
+                             ("step", np.float64), ("kind", np.uint32), ("reserved", np.uint32)])
+assert AMP_LAUNCH_DTYPE.itemsize == 48
+AMP_DYN_BYTES = 32
+AMP_MAX_LAUNCHES = 16
 
 
 # apexw_gemm_problem: one product of a grouped launch
@@ -131,15 +141,15 @@ SIGNATURES = {
     "apexw_check_tensor": (ctypes.c_int, [ctypes.POINTER(Tensor), _i32]),
     "apexw_compact_step": (ctypes.c_int, [_vp, _i32, _vp, _i64, _HP, _vp]),
     "apexw_q8_step": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _i64, _HP, _vp]),
-    "apexw_grad_clip_coef": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _vp, _vp, _vp, _f32, _f32, _u32, _vp, _vp]),
-    "apexw_grad_clip_coef_noalloc": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _vp, _f32, _f32, _u32, _vp, _vp]),
+    "apexw_grad_clip_coef": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _vp, _vp, _vp, _f32, _f32, _u32, _vp, _vp, _vp]),
+    "apexw_grad_clip_coef_noalloc": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _vp, _f32, _f32, _u32, _vp, _vp, _vp]),
     "apexw_gemm_nt_bf16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                           _i32, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _vp]),
     "apexw_check_grad_prep": (ctypes.c_int, [_vp]),
     "apexw_check_row_means": (ctypes.c_int, [_vp]),
     "apexw_grad_prep_units": (ctypes.c_int64, [_vp]),
-    "apexw_grad_prepare": (ctypes.c_int, [_vp, _i32, _vp, _i64, _f32, _u32, _vp]),
-    "apexw_grad_row_means": (ctypes.c_int, [_vp, _i32, _vp, _i64, _f32, _u32, _vp]),
+    "apexw_grad_prepare": (ctypes.c_int, [_vp, _i32, _vp, _i64, _f32, _u32, _vp, _vp]),
+    "apexw_grad_row_means": (ctypes.c_int, [_vp, _i32, _vp, _i64, _f32, _u32, _vp, _vp]),
     "apexw_gemm_grouped_items": (ctypes.c_int64, [_vp, _i32]),
     "apexw_gemm_grouped_schedule": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i32, ctypes.POINTER(ctypes.c_int64), _vp,
                                                    ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32)]),
@@ -153,6 +163,7 @@ SIGNATURES = {
     "apexw_factored_step": (ctypes.c_int, [_vp, _i32, _vp, _i32, _i64, _i64, _vp, _i64, _vp, _vp, _HP, _vp]),
     "apexw_muon_coordwise": (ctypes.c_int, [_vp, _vp, _i32, _vp, _i32, _i64, _f32, _f32, _i32, _f32, _f32, _i32,
                                              _f32, _vp]),
+    "apexw_amp_prepare": (ctypes.c_int, [_vp, _vp, _vp, _i32, _vp, _i32, _vp, _vp]),
     "apexw_state_decode": (ctypes.c_int, [ctypes.POINTER(StateLayout), _vp, _vp, _vp]),
     "apexw_state_encode": (ctypes.c_int, [ctypes.POINTER(StateLayout), _vp, _vp, _vp]),
 }

@@ -34,6 +34,18 @@ from . import _lib as L
 
 
 
+def _upload(a, device):
+    """Copy a host array to the device without a host synchronisation.
+
+    The bytes go through a pinned tensor from torch's caching host allocator,
+    which holds the block until the asynchronous copy has run, so a step that
+    re-uploads a table (grads that moved) does not wait for the device."""
+    t = torch.from_numpy(np.array(a, copy=True))
+    if torch.device(device).type == "cpu":     # host-only plans of the unit tests
+        return t
+    return t.pin_memory().to(device, non_blocking=True)
+
+
 def _host():
     """The native scan module, imported on first use (the build imports this package)."""
     try:
@@ -78,6 +90,7 @@ class StepPlan:
         self.states = [opt.state[p] for p in self.params]
         self.gc = bool(group.get("grad_centralization", False))
         self.cold_done = False
+        self.amp_dirty = False      # skips counted on the device that the host has not folded
         self._build_steps()
         self._build_tables(group)
 
@@ -243,15 +256,16 @@ class StepPlan:
         units["tensor"] = np.repeat(np.arange(n, dtype=np.uint32), counts)
         units["unit"] = (np.arange(len(units), dtype=np.int64) - np.repeat(begin[:-1], counts)).astype(np.uint32)
         self.n_prep_units = len(units)
-        self.d_prep_units = torch.from_numpy(units.view(np.uint8)).to(self.device)
+        self.d_prep_units = _upload(units.view(np.uint8), self.device)
 
-    def _prepare_grads(self, inv_scale, stream):
+    def _prepare_grads(self, inv_scale, stream, amp_dyn=None):
         """Sanitize, unscale and centralize into the prepared-grad buffers, or (folded
-        path) only the row means of the sanitized, unscaled grads."""
+        path) only the row means of the sanitized, unscaled grads.  amp_dyn: device
+        scalars of a GradScaler step (the unscale factor is read there)."""
         flags = L.HP_SANITIZE | (L.HP_UNSCALE if inv_scale is not None else 0)
         fn = self._lib.apexw_grad_row_means if self.gc_fold else self._lib.apexw_grad_prepare
         st = fn(self.d_prep.data_ptr(), len(self.params), self.d_prep_units.data_ptr(), self.n_prep_units,
-                1.0 if inv_scale is None else inv_scale, flags, stream)
+                1.0 if inv_scale is None else inv_scale, flags, amp_dyn, stream)
         L.check(st, "apexw_grad_row_means" if self.gc_fold else "apexw_grad_prepare")
 
     def _layout_units(self, fast):
@@ -278,8 +292,8 @@ class StepPlan:
         self.unit_counts = counts
         self.perm = perm
         self.fast = fast
-        self.d_units = torch.from_numpy(units.view(np.uint8)).to(self.device)
-        self.d_unit_begin = torch.from_numpy(self.unit_begin).to(self.device)
+        self.d_units = _upload(units.view(np.uint8), self.device)
+        self.d_unit_begin = _upload(self.unit_begin, self.device)
         # the step kernels' units: all but the factored rows' (apexw_factored_step steps
         # those; the clip's norm pass still covers every unit).  Factored tensors are
         # never full-block 8-bit tensors, so the fast prefix is unchanged.
@@ -288,7 +302,7 @@ class StepPlan:
             self._step_keep = ~fac_rows[units["tensor"]]
             step_units = units[self._step_keep]
             self.n_step_units = len(step_units)
-            self.d_step_units = torch.from_numpy(step_units.view(np.uint8)).to(self.device) \
+            self.d_step_units = _upload(step_units.view(np.uint8), self.device) \
                 if len(step_units) else self.d_units
         else:
             self._step_keep, self.n_step_units, self.d_step_units = None, total, self.d_units
@@ -322,10 +336,10 @@ class StepPlan:
         ends = np.cumsum(np.bincount(group, minlength=L.FV_UNIT_RANGES)).astype(np.int64)
         # the factored kernels address a unit's tensor through its fv entry (rows ascend)
         units["tensor"] = np.searchsorted(fv["tensor"], units["tensor"]).astype(np.uint32)
-        return dict(rows=rows, n=len(fv), d_fv=torch.from_numpy(fv.view(np.uint8)).to(self.device),
+        return dict(rows=rows, n=len(fv), d_fv=_upload(fv.view(np.uint8), self.device),
                     ws=torch.empty(max(ws, 1), dtype=torch.float32, device=self.device),
                     n_bands=nb.value, n_cb=ncb.value, n_units=len(units), range_ends=ends,
-                    d_units=torch.from_numpy(units.view(np.uint8)).to(self.device) if len(units) else None)
+                    d_units=_upload(units.view(np.uint8), self.device) if len(units) else None)
 
     def _refresh_grads(self):
         """Point the table at this step's grads; re-upload it if any moved.
@@ -364,7 +378,7 @@ class StepPlan:
                         continue
                     L.check(self._lib.apexw_check_grad_prep(self.host_prep[i:i + 1].ctypes.data),
                             f"grad preparation of tensor {i}")
-                self.d_prep = torch.from_numpy(self.host_prep.view(np.uint8).copy()).to(self.device)
+                self.d_prep = _upload(self.host_prep.view(np.uint8), self.device)
             if not self.gc_fold:
                 ptrs = np.fromiter((o.data_ptr() for o in self.gc_out), dtype=np.uint64, count=len(self.params))
         if self.d_table is None or not np.array_equal(ptrs, self.host_table["g"]):
@@ -373,7 +387,7 @@ class StepPlan:
             if self.perm is None or (fast is not None and not np.array_equal(fast, self.fast)):
                 self._layout_units(fast)
             rows = np.ascontiguousarray(self.host_table[self.perm])
-            self.d_table = torch.from_numpy(rows.view(np.uint8)).to(self.device)
+            self.d_table = _upload(rows.view(np.uint8), self.device)
         return keep
 
     def _validate_and_align(self):
@@ -405,7 +419,7 @@ class StepPlan:
         return (self._fast_static & ~scalar) if self.kind == "q8" and not self.single else None
 
     # ------------------------------------------------------------------ launch
-    def _clip(self, clip, sanitize, inv_scale, stream):
+    def _clip(self, clip, sanitize, inv_scale, stream, amp_dyn=None):
         if self.clip_ws is None:
             self.clip_ws = (torch.empty(max(self.n_units, 1), dtype=torch.float32, device=self.device),
                             torch.empty(len(self.params), dtype=torch.float32, device=self.device),
@@ -416,19 +430,72 @@ class StepPlan:
             self.d_table.data_ptr(), len(self.params), self.d_units.data_ptr(), self.n_units, unit,
             self.d_unit_begin.data_ptr(), part.data_ptr(), norms.data_ptr(), float(clip),
             1.0 if inv_scale is None else inv_scale,
-            (L.HP_SANITIZE if sanitize else 0) | (L.HP_UNSCALE if inv_scale is not None else 0), coef.data_ptr(), stream)
+            (L.HP_SANITIZE if sanitize else 0) | (L.HP_UNSCALE if inv_scale is not None else 0), coef.data_ptr(),
+            amp_dyn, stream)
         L.check(st, "apexw_grad_clip_coef")
         return coef
 
-    def execute(self, group, seed, inv_scale=None, lr=None, wd=None, steps=None):
+    # ------------------------------------------------------------------ AMP on the device
+    @property
+    def amp_device_ok(self):
+        """Whether GradScaler's scale and found_inf can be read on the device for this
+        plan (the compact and 8-bit step kernels; not the factored ones or the
+        in-backward batches)."""
+        return not (self.hooked or self.single or self.factored.any())
+
+    def amp_fold(self, sync=False):
+        """Subtract from the step counters the steps GradScaler skipped that the host
+        has seen (the device's skip count, copied back asynchronously after each
+        step).  sync: wait for the copies first, so every skip is folded."""
+        if getattr(self, "_amp_skips", None) is None:
+            return
+        if sync:
+            self._amp_event.synchronize()
+            self.amp_dirty = False
+        seen = int(self._amp_mirror.numpy()[0])
+        if seen > self._amp_folded:
+            self._steps_np -= float(seen - self._amp_folded)
+            self._amp_folded = seen
+
+    def _amp_prepare(self, amp, groups, lr, b1, b2, eps, stream):
+        """Device-side scalars of every launch of this step (apexw_amp_prepare)."""
+        if getattr(self, "_amp_skips", None) is None:
+            self._amp_skips = torch.zeros(1, dtype=torch.int32, device=self.device)
+            self._amp_mirror = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+            self._amp_dyn = torch.empty(L.AMP_MAX_LAUNCHES * L.AMP_DYN_BYTES // 4, dtype=torch.float32,
+                                        device=self.device)
+            self._amp_folded = 0
+            self._amp_event = torch.cuda.Event()
+        launches = np.zeros(len(groups), dtype=L.AMP_LAUNCH_DTYPE)
+        launches["lr"], launches["beta1"], launches["beta2"], launches["eps"] = lr, b1, b2, eps
+        launches["step"] = [g[1] for g in groups]
+        launches["kind"] = 1 if self.native else 0
+        scale, found_inf = amp
+        L.check(self._lib.apexw_amp_prepare(found_inf.data_ptr(), scale.data_ptr(), self._amp_skips.data_ptr(),
+                                            self._amp_folded, launches.ctypes.data, len(groups),
+                                            self._amp_dyn.data_ptr(), stream), "apexw_amp_prepare")
+        self._amp_mirror.copy_(self._amp_skips, non_blocking=True)
+        self._amp_event.record(torch.cuda.current_stream(self.device))
+        self.amp_dirty = True
+        return self._amp_dyn.data_ptr()
+
+    def execute(self, group, seed, inv_scale=None, lr=None, wd=None, steps=None, amp=None):
         """Run one optimizer step for the group (cold the first time, replay after).
 
         inv_scale: 1 / the AMP grad scale handed over by GradScaler, or None.
+        amp: instead, GradScaler's (scale, found_inf) device tensors, read on the
+        device (amp_device_ok plans): the kernels unscale with 1 / scale and skip
+        the step when found_inf is set; the step counters advance on the host and
+        the skips are subtracted once seen (amp_fold).
         lr, wd: replace the group's values; steps: each parameter's step count
         for this step (already advanced) instead of advancing the plan's own."""
         mode_cold = not self.cold_done
         keep = self._refresh_grads()  # noqa: F841 -- keeps contiguous copies alive until the launch
         stream = torch.cuda.current_stream(self.device).cuda_stream
+        amp_dyn = None
+        if amp is not None:
+            self.amp_fold()
+            inv_scale = 1.0          # a stand-in: the kernels read the factor from amp_dyn
         (b1, b2), eps = group["betas"], group["eps"]
         lr = group["lr"] if lr is None else lr
         wd = group["weight_decay"] if wd is None else wd
@@ -440,18 +507,7 @@ class StepPlan:
             sanitize = mode_cold and clip is not None
         if self.single:
             # the per-parameter update takes the grads as they are (no sanitize, clip, AMP or centralization)
-            sanitize, clip, inv_scale = False, None, None
-        elif self.gc_fold:
-            # _prepare_grads with centralization, folded: the row means first; the clip
-            # and the step read the raw grads and sanitize, unscale and subtract them
-            self._prepare_grads(inv_scale, stream)
-            sanitize = True
-        elif self.gc:
-            # _prepare_grads with centralization: sanitize, unscale, centralize;
-            # the clip and the step then see finite, unscaled grads
-            self._prepare_grads(inv_scale, stream)
-            sanitize, inv_scale = False, None
-        coef = self._clip(clip, sanitize, inv_scale, stream) if clip is not None else None
+            sanitize, clip, inv_scale, amp = False, None, None, None
         if steps is None:
             self._steps_np += 1.0
         else:
@@ -467,8 +523,26 @@ class StepPlan:
             groups = self._split_launches(sr_t, sr)
         else:
             groups = [(None, int(self._steps_np[0]), sr)]
-        for units, step, sr_l in groups:
+        if amp is not None:
+            amp_dyn = self._amp_prepare(amp, groups, lr, b1, b2, eps, stream)
+        if self.single:
+            pass
+        elif self.gc_fold:
+            # _prepare_grads with centralization, folded: the row means first; the clip
+            # and the step read the raw grads and sanitize, unscale and subtract them
+            self._prepare_grads(inv_scale, stream, amp_dyn)
+            sanitize = True
+        elif self.gc:
+            # _prepare_grads with centralization: sanitize, unscale, centralize;
+            # the clip and the step then see finite, unscaled grads
+            self._prepare_grads(inv_scale, stream, amp_dyn)
+            sanitize, inv_scale, amp_dyn = False, None, None
+        coef = self._clip(clip, sanitize, inv_scale, stream, amp_dyn) if clip is not None else None
+        for li, (units, step, sr_l) in enumerate(groups):
             hp = self._hparams(lr, b1, b2, eps, wd, step, sr_l, sanitize, coef, seed, mode_cold, inv_scale)
+            if amp_dyn is not None:
+                hp.flags |= L.HP_AMP
+                hp.amp = amp_dyn + li * L.AMP_DYN_BYTES
             if units is None:
                 d_units, n_units = self.d_step_units, self.n_step_units
                 n_fast, n_fast32 = self.n_fast_units, self.n_fast_f32_units
@@ -549,7 +623,8 @@ class StepPlan:
                 mask = mask[self._step_keep]
             if not mask.any():
                 continue
-            sel = self.d_step_units.view(-1, 8)[torch.from_numpy(mask).to(self.device)].reshape(-1)
+            idx = _upload(np.flatnonzero(mask), self.device)
+            sel = self.d_step_units.view(-1, 8).index_select(0, idx).reshape(-1)
             nb, nf = self.n_fast_units, self.n_fast_f32_units
             out.append(((sel, int(mask.sum()), int(mask[:nb].sum()), int(mask[nb:nb + nf].sum())), int(val),
                         bool(srv)))

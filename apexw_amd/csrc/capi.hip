@@ -17,7 +17,9 @@ int apexw_launch_q8(const apexw_tensor*, int64_t, const apexw_unit*, const apexw
 int apexw_launch_q8_fast(const apexw_tensor*, int64_t, const apexw_unit*, const apexw_hparams*, int32_t, hipStream_t);
 bool apexw_q8_fast_eligible(uint32_t flags, uint32_t block);
 int apexw_launch_clip(const apexw_tensor*, int32_t, const apexw_unit*, int64_t, int64_t, const int64_t*, float*, float*,
-                      float, float, uint32_t, float*, hipStream_t);
+                      float, float, uint32_t, float*, const apexw_amp_dyn*, hipStream_t);
+int apexw_launch_amp_prepare(const float*, const float*, int32_t*, int32_t, const apexw_amp_launch*, int32_t,
+                             apexw_amp_dyn*, hipStream_t);
 bool apexw_compact_flags_ok(uint32_t flags);
 int apexw_launch_gemm_nt(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, uint16_t*, int32_t, int32_t,
                          int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int64_t, int64_t, int64_t,
@@ -25,8 +27,10 @@ int apexw_launch_gemm_nt(const uint16_t*, const uint16_t*, const uint16_t*, uint
 int apexw_muon_partials(int64_t n);
 int apexw_launch_muon_coordwise(float*, const void*, int32_t, void*, int32_t, int64_t, float, float, int32_t, float,
                                 float, int32_t, float, hipStream_t);
-int apexw_launch_grad_prep(const apexw_grad_prep*, const apexw_unit*, int64_t, float, uint32_t, hipStream_t);
-int apexw_launch_row_means(const apexw_grad_prep*, const apexw_unit*, int64_t, float, uint32_t, hipStream_t);
+int apexw_launch_grad_prep(const apexw_grad_prep*, const apexw_unit*, int64_t, float, uint32_t, const apexw_amp_dyn*,
+                           hipStream_t);
+int apexw_launch_row_means(const apexw_grad_prep*, const apexw_unit*, int64_t, float, uint32_t, const apexw_amp_dyn*,
+                           hipStream_t);
 int apexw_launch_gemm_grouped(const apexw_gemm_problem*, const uint32_t*, const int32_t*, int32_t, int32_t,
                               hipStream_t);
 int apexw_launch_muon_prepare(float*, const void*, int32_t, int64_t, int64_t, float, float, int32_t, float, float,
@@ -84,7 +88,13 @@ bool hp_ok(const apexw_hparams* hp) {
   if (hp->mode == APEXW_MODE_SINGLE && (hp->flags & (APEXW_HP_SANITIZE | APEXW_HP_CLIP | APEXW_HP_UNSCALE)))
     return false;
   if ((hp->flags & APEXW_HP_CLIP) && !hp->clip_coef) return false;
-  if ((hp->flags & APEXW_HP_UNSCALE) && !(hp->grad_inv_scale > 0.0f)) return false;
+  if (hp->flags & APEXW_HP_AMP) {
+    // device-side AMP scalars: the compact and 8-bit step modes, with the unscale they carry
+    if (!hp->amp || ((uintptr_t)hp->amp & 15u) || hp->mode == APEXW_MODE_SINGLE) return false;
+    if (!(hp->flags & APEXW_HP_UNSCALE)) return false;
+  } else if ((hp->flags & APEXW_HP_UNSCALE) && !(hp->grad_inv_scale > 0.0f)) {
+    return false;
+  }
   return true;
 }
 
@@ -199,6 +209,7 @@ int apexw_factored_step(const apexw_tensor* tensors, int32_t n_tensors, const ap
   }
   if (prev != n_units) return APEXW_ERR_ARG;
   if (hp->mode == APEXW_MODE_SINGLE || hp->mode == APEXW_MODE_NATIVE) return APEXW_ERR_ARG;
+  if (hp->flags & APEXW_HP_AMP) return APEXW_ERR_ARG;   // factored steps take host-read AMP scalars
   return apexw_launch_factored(tensors, fv, n_fv, n_bands, n_col_blocks, units, range_ends, workspace, hp,
                                (hipStream_t)stream);
 }
@@ -460,12 +471,13 @@ int apexw_muon_coordwise(float* buf, const void* g, int32_t g_dtype, void* p, in
 
 int apexw_grad_clip_coef(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,
                          int64_t unit_size, const int64_t* unit_begin, float* unit_partial, float* tensor_norm,
-                         float clip, float grad_inv_scale, uint32_t flags, float* coef, void* stream) {
+                         float clip, float grad_inv_scale, uint32_t flags, float* coef, const apexw_amp_dyn* amp,
+                         void* stream) {
   if (!tensors || !units || !unit_begin || !unit_partial || !tensor_norm || !coef) return APEXW_ERR_ARG;
   if (n_tensors <= 0 || n_units < 0 || unit_size < 0 || !(clip > 0.0f)) return APEXW_ERR_ARG;
-  if ((flags & APEXW_HP_UNSCALE) && !(grad_inv_scale > 0.0f)) return APEXW_ERR_ARG;
+  if ((flags & APEXW_HP_UNSCALE) && !amp && !(grad_inv_scale > 0.0f)) return APEXW_ERR_ARG;
   return apexw_launch_clip(tensors, n_tensors, units, n_units, unit_size, unit_begin, unit_partial, tensor_norm, clip,
-                           grad_inv_scale, flags, coef, (hipStream_t)stream);
+                           grad_inv_scale, flags, coef, amp, (hipStream_t)stream);
 }
 
 int apexw_check_grad_prep(const apexw_grad_prep* d) {
@@ -498,19 +510,35 @@ int64_t apexw_grad_prep_units(const apexw_grad_prep* d) {
 }
 
 int apexw_grad_prepare(const apexw_grad_prep* preps, int32_t n_preps, const apexw_unit* units, int64_t n_units,
-                       float grad_inv_scale, uint32_t flags, void* stream) {
+                       float grad_inv_scale, uint32_t flags, const apexw_amp_dyn* amp, void* stream) {
   if (!preps || !units || n_preps <= 0 || n_units < 0) return APEXW_ERR_ARG;
   if (flags & ~(APEXW_HP_SANITIZE | APEXW_HP_UNSCALE)) return APEXW_ERR_ARG;
-  if ((flags & APEXW_HP_UNSCALE) && !(grad_inv_scale > 0.0f)) return APEXW_ERR_ARG;
-  return apexw_launch_grad_prep(preps, units, n_units, grad_inv_scale, flags, (hipStream_t)stream);
+  if ((flags & APEXW_HP_UNSCALE) && !amp && !(grad_inv_scale > 0.0f)) return APEXW_ERR_ARG;
+  return apexw_launch_grad_prep(preps, units, n_units, grad_inv_scale, flags, amp, (hipStream_t)stream);
 }
 
 int apexw_grad_row_means(const apexw_grad_prep* preps, int32_t n_preps, const apexw_unit* units, int64_t n_units,
-                         float grad_inv_scale, uint32_t flags, void* stream) {
+                         float grad_inv_scale, uint32_t flags, const apexw_amp_dyn* amp, void* stream) {
   if (!preps || !units || n_preps <= 0 || n_units < 0) return APEXW_ERR_ARG;
   if (flags & ~(APEXW_HP_SANITIZE | APEXW_HP_UNSCALE)) return APEXW_ERR_ARG;
-  if ((flags & APEXW_HP_UNSCALE) && !(grad_inv_scale > 0.0f)) return APEXW_ERR_ARG;
-  return apexw_launch_row_means(preps, units, n_units, grad_inv_scale, flags, (hipStream_t)stream);
+  if ((flags & APEXW_HP_UNSCALE) && !amp && !(grad_inv_scale > 0.0f)) return APEXW_ERR_ARG;
+  return apexw_launch_row_means(preps, units, n_units, grad_inv_scale, flags, amp, (hipStream_t)stream);
+}
+
+int apexw_amp_prepare(const float* found_inf, const float* grad_scale, int32_t* skips, int32_t skips_folded,
+                      const apexw_amp_launch* launches, int32_t n_launches, apexw_amp_dyn* dyn, void* stream) {
+  if (!found_inf || !grad_scale || !skips || !launches || !dyn) return APEXW_ERR_ARG;
+  if (n_launches <= 0 || n_launches > APEXW_AMP_MAX_LAUNCHES || skips_folded < 0) return APEXW_ERR_ARG;
+  for (int i = 0; i < n_launches; ++i) {
+    const apexw_amp_launch& l = launches[i];
+    if (l.kind > 1 || l.reserved || !(l.step >= 1.0) || !(l.beta1 >= 0.0 && l.beta1 < 1.0) ||
+        !(l.beta2 >= 0.0 && l.beta2 < 1.0))
+      return APEXW_ERR_ARG;
+  }
+  if (((uintptr_t)found_inf | (uintptr_t)grad_scale | (uintptr_t)skips) & 3u) return APEXW_ERR_ALIGN;
+  if ((uintptr_t)dyn & 15u) return APEXW_ERR_ALIGN;
+  return apexw_launch_amp_prepare(found_inf, grad_scale, skips, skips_folded, launches, n_launches, dyn,
+                                  (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -326,7 +326,17 @@ APEXW_DEV void dispatch_group(const apexw_tensor& t, int64_t start, int k, const
 
 __global__ __launch_bounds__(256) void compact_step_kernel(const apexw_tensor* __restrict__ tensors,
                                                            const apexw_unit* __restrict__ units,
-                                                           int64_t n_units, apexw_hparams hp) {
+                                                           int64_t n_units, apexw_hparams hp_in) {
+  apexw_hparams hp = hp_in;
+  if (hp.flags & APEXW_HP_AMP) {
+    // GradScaler's step read on the device: skip it (found_inf) or take its scalars
+    const apexw_amp_dyn d = *hp.amp;
+    if (d.skip) return;
+    hp.step_size = d.step_size;
+    hp.eps_scaled = d.eps_scaled;
+    hp.bc2_sqrt = d.bc2_sqrt;
+    hp.grad_inv_scale = d.grad_inv_scale;
+  }
   const uint32_t wave = uniform(threadIdx.x >> 6);
   Ctx c;
   c.hp = &hp;

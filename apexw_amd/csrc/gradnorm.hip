@@ -108,7 +108,8 @@ APEXW_DEV float unit_sumsq(const apexw_tensor& t, int64_t start, int64_t cnt, bo
 __global__ __launch_bounds__(256) void sumsq_kernel(const apexw_tensor* __restrict__ tensors,
                                                     const apexw_unit* __restrict__ units, int64_t n_units,
                                                     int64_t unit_size, float* __restrict__ partial, uint32_t flags,
-                                                    float inv) {
+                                                    float inv, const apexw_amp_dyn* __restrict__ amp) {
+  if (amp) inv = amp->grad_inv_scale;
   const uint32_t wave = uniform(threadIdx.x >> 6);
   const int64_t stride = (int64_t)gridDim.x * 4;
   const bool san = flags & APEXW_HP_SANITIZE, unscale = flags & APEXW_HP_UNSCALE;
@@ -270,8 +271,10 @@ APEXW_DEV void mean_unit(const apexw_grad_prep& d, int64_t row, bool san, bool u
 
 __global__ __launch_bounds__(256) void row_means_kernel(const apexw_grad_prep* __restrict__ preps,
                                                         const apexw_unit* __restrict__ units, int64_t n_units,
-                                                        float inv, uint32_t flags) {
+                                                        float inv, uint32_t flags,
+                                                        const apexw_amp_dyn* __restrict__ amp) {
   __shared__ float red[4];
+  if (amp) inv = amp->grad_inv_scale;
   const bool san = flags & APEXW_HP_SANITIZE, unscale = flags & APEXW_HP_UNSCALE;
   for (int64_t u = blockIdx.x; u < n_units; u += gridDim.x) {
     const apexw_unit un = units[u];
@@ -285,8 +288,10 @@ __global__ __launch_bounds__(256) void row_means_kernel(const apexw_grad_prep* _
 
 __global__ __launch_bounds__(256) void grad_prep_kernel(const apexw_grad_prep* __restrict__ preps,
                                                         const apexw_unit* __restrict__ units, int64_t n_units,
-                                                        float inv, uint32_t flags) {
+                                                        float inv, uint32_t flags,
+                                                        const apexw_amp_dyn* __restrict__ amp) {
   __shared__ float red[4];
+  if (amp) inv = amp->grad_inv_scale;
   const bool san = flags & APEXW_HP_SANITIZE, unscale = flags & APEXW_HP_UNSCALE;
   for (int64_t u = blockIdx.x; u < n_units; u += gridDim.x) {
     const apexw_unit un = units[u];
@@ -301,22 +306,25 @@ __global__ __launch_bounds__(256) void grad_prep_kernel(const apexw_grad_prep* _
 }  // namespace
 
 int apexw_launch_grad_prep(const apexw_grad_prep* preps, const apexw_unit* units, int64_t n_units, float inv,
-                           uint32_t flags, hipStream_t stream) {
+                           uint32_t flags, const apexw_amp_dyn* amp, hipStream_t stream) {
   if (n_units <= 0) return APEXW_OK;
   const int64_t want = n_units < 65536 ? n_units : 65536;
-  hipLaunchKernelGGL(grad_prep_kernel, dim3((unsigned)want), dim3(256), 0, stream, preps, units, n_units, inv, flags);
+  hipLaunchKernelGGL(grad_prep_kernel, dim3((unsigned)want), dim3(256), 0, stream, preps, units, n_units, inv, flags,
+                     amp);
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }
 
 int apexw_launch_clip(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,
                       int64_t unit_size, const int64_t* unit_begin, float* unit_partial, float* tensor_norm,
-                      float clip, float inv, uint32_t flags, float* coef, hipStream_t stream);
+                      float clip, float inv, uint32_t flags, float* coef, const apexw_amp_dyn* amp,
+                      hipStream_t stream);
 
 int apexw_launch_row_means(const apexw_grad_prep* preps, const apexw_unit* units, int64_t n_units, float inv,
-                           uint32_t flags, hipStream_t stream) {
+                           uint32_t flags, const apexw_amp_dyn* amp, hipStream_t stream) {
   if (n_units <= 0) return APEXW_OK;
   const int64_t want = n_units < 65536 ? n_units : 65536;
-  hipLaunchKernelGGL(row_means_kernel, dim3((unsigned)want), dim3(256), 0, stream, preps, units, n_units, inv, flags);
+  hipLaunchKernelGGL(row_means_kernel, dim3((unsigned)want), dim3(256), 0, stream, preps, units, n_units, inv, flags,
+                     amp);
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }
 
@@ -351,25 +359,26 @@ float* scratch_on_current_device() {
 extern "C" int apexw_grad_clip_coef_noalloc(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units,
                                             int64_t n_units, int64_t unit_size, const int64_t* unit_begin,
                                             float clip, float grad_inv_scale, uint32_t flags, float* coef,
-                                            void* stream) {
+                                            const apexw_amp_dyn* amp, void* stream) {
   if (!tensors || !units || !unit_begin || !coef) return APEXW_ERR_ARG;
   if (n_tensors <= 0 || n_units < 0 || unit_size < 0 || !(clip > 0.0f)) return APEXW_ERR_ARG;
-  if ((flags & APEXW_HP_UNSCALE) && !(grad_inv_scale > 0.0f)) return APEXW_ERR_ARG;
+  if ((flags & APEXW_HP_UNSCALE) && !amp && !(grad_inv_scale > 0.0f)) return APEXW_ERR_ARG;
   if (n_units > APEXW_NOALLOC_CLIP_MAX_UNITS || n_tensors > APEXW_NOALLOC_CLIP_MAX_TENSORS) return APEXW_ERR_SIZE;
   float* ptr = scratch_on_current_device();
   if (!ptr) return APEXW_ERR_LAUNCH;
   return apexw_launch_clip(tensors, n_tensors, units, n_units, unit_size, unit_begin, ptr,
-                           ptr + APEXW_NOALLOC_CLIP_MAX_UNITS, clip, grad_inv_scale, flags, coef,
+                           ptr + APEXW_NOALLOC_CLIP_MAX_UNITS, clip, grad_inv_scale, flags, coef, amp,
                            (hipStream_t)stream);
 }
 
 int apexw_launch_clip(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,
                       int64_t unit_size, const int64_t* unit_begin, float* unit_partial, float* tensor_norm,
-                      float clip, float inv, uint32_t flags, float* coef, hipStream_t stream) {
+                      float clip, float inv, uint32_t flags, float* coef, const apexw_amp_dyn* amp,
+                      hipStream_t stream) {
   if (n_units > 0) {
     const int grid_units = apexw_resident_grid((const void*)sumsq_kernel, n_units);
     hipLaunchKernelGGL(sumsq_kernel, dim3(grid_units), dim3(256), 0, stream, tensors, units, n_units, unit_size,
-                       unit_partial, flags, inv);
+                       unit_partial, flags, inv, amp);
   }
   if (n_tensors > 0) {
     const int grid_tensors = apexw_resident_grid((const void*)tensor_norm_kernel, n_tensors);
@@ -377,5 +386,57 @@ int apexw_launch_clip(const apexw_tensor* tensors, int32_t n_tensors, const apex
                        unit_partial, tensor_norm);
   }
   hipLaunchKernelGGL(clip_coef_kernel, dim3(1), dim3(1024), 0, stream, tensor_norm, n_tensors, clip, coef);
+  return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
+}
+
+// ---------------------------------------------------------------------------
+// GradScaler's scale and found_inf read on the device (apexw_amp_prepare): one
+// thread turns them and the host's step counts into each launch's scalars.
+// ---------------------------------------------------------------------------
+namespace {
+
+struct AmpLaunches {
+  apexw_amp_launch l[APEXW_AMP_MAX_LAUNCHES];
+};
+
+__global__ __launch_bounds__(64) void amp_prepare_kernel(const float* __restrict__ found_inf,
+                                                         const float* __restrict__ grad_scale,
+                                                         int32_t* __restrict__ skips, int32_t folded, AmpLaunches ls,
+                                                         int32_t n, apexw_amp_dyn* __restrict__ dyn) {
+  if (threadIdx.x != 0) return;
+  const uint32_t skip = *found_inf != 0.0f ? 1u : 0u;
+  const int32_t s = *skips;
+  if (skip) *skips = s + 1;
+  const float inv = 1.0f / *grad_scale;
+  for (int i = 0; i < n; ++i) {
+    const apexw_amp_launch& L = ls.l[i];
+    const double t = L.step - (double)(s - folded);
+    const double bc1 = 1.0 - pow(L.beta1, t), bc2 = 1.0 - pow(L.beta2, t);
+    const double bc2s = sqrt(bc2);
+    apexw_amp_dyn d;
+    if (L.kind == 1) {
+      d.step_size = (float)(L.lr / bc1);
+      d.eps_scaled = (float)L.eps;
+      d.bc2_sqrt = (float)bc2s;
+    } else {
+      d.step_size = (float)(L.lr * bc2s / bc1);
+      d.eps_scaled = (float)(L.eps * bc2s);
+      d.bc2_sqrt = (float)bc2s;
+    }
+    d.grad_inv_scale = inv;
+    d.skip = skip;
+    d.reserved[0] = d.reserved[1] = d.reserved[2] = 0u;
+    dyn[i] = d;
+  }
+}
+
+}  // namespace
+
+int apexw_launch_amp_prepare(const float* found_inf, const float* grad_scale, int32_t* skips, int32_t folded,
+                             const apexw_amp_launch* launches, int32_t n, apexw_amp_dyn* dyn, hipStream_t stream) {
+  AmpLaunches ls;
+  for (int i = 0; i < n; ++i) ls.l[i] = launches[i];
+  hipLaunchKernelGGL(amp_prepare_kernel, dim3(1), dim3(64), 0, stream, found_inf, grad_scale, skips, folded, ls, n,
+                     dyn);
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }

@@ -890,7 +890,17 @@ APEXW_DEV void q8_dense16(const apexw_tensor& t, const Q8Ctx& c) {
 template <int PD>
 __global__ __launch_bounds__(256) void q8_fast_kernel(const apexw_tensor* __restrict__ tensors,
                                                       const apexw_unit* __restrict__ units,
-                                                      int64_t n_units, apexw_hparams hp) {
+                                                      int64_t n_units, apexw_hparams hp_in) {
+  apexw_hparams hp = hp_in;
+  if (hp.flags & APEXW_HP_AMP) {
+    // GradScaler's step read on the device: skip it (found_inf) or take its scalars
+    const apexw_amp_dyn d = *hp.amp;
+    if (d.skip) return;
+    hp.step_size = d.step_size;
+    hp.eps_scaled = d.eps_scaled;
+    hp.bc2_sqrt = d.bc2_sqrt;
+    hp.grad_inv_scale = d.grad_inv_scale;
+  }
   __shared__ float s_vlut[256];
   __shared__ float2 s_pair[256];
   __shared__ float4 s_frac16[128];
@@ -940,7 +950,17 @@ __global__ __launch_bounds__(256) void q8_fast_kernel(const apexw_tensor* __rest
 template <bool SINGLE>
 __global__ __launch_bounds__(256) void q8_step_kernel(const apexw_tensor* __restrict__ tensors,
                                                       const apexw_unit* __restrict__ units,
-                                                      int64_t n_units, apexw_hparams hp) {
+                                                      int64_t n_units, apexw_hparams hp_in) {
+  apexw_hparams hp = hp_in;
+  if (hp.flags & APEXW_HP_AMP) {
+    // GradScaler's step read on the device: skip it (found_inf) or take its scalars
+    const apexw_amp_dyn d = *hp.amp;
+    if (d.skip) return;
+    hp.step_size = d.step_size;
+    hp.eps_scaled = d.eps_scaled;
+    hp.bc2_sqrt = d.bc2_sqrt;
+    hp.grad_inv_scale = d.grad_inv_scale;
+  }
   __shared__ float s_vlut[256];
   __shared__ float s_code[16];
   __shared__ float2 s_midtab[64];

@@ -43,6 +43,46 @@ _UNSUPPORTED_FLAGS = ("amsgrad", "nesterov", "cautious", "lion", "maximize",
                       "capturable", "differentiable", "auto_pack")
 
 
+class _StateMap(defaultdict):
+    """``optimizer.state`` with step counters that are exact when looked at.
+
+    A step whose GradScaler found_inf is read by the kernels advances the host's
+    counters optimistically; the device counts the skipped steps.  The first
+    lookup of a state after such a step subtracts them (one wait for the count),
+    so ``opt.state[p]["step"]`` reads as the reference's, whose skipped steps
+    leave it alone.  Inside ``step()`` the lookups do not wait (the owner's
+    ``_amp_unfolded`` is cleared meanwhile)."""
+
+    def __init__(self, owner, items=()):
+        super().__init__(dict, items)
+        self._owner = owner
+
+    def _fold(self):
+        o = self._owner
+        if o is not None and o._amp_unfolded:
+            o._fold_amp_skips()
+
+    def __getitem__(self, key):
+        self._fold()
+        return super().__getitem__(key)
+
+    def get(self, key, default=None):
+        self._fold()
+        return super().get(key, default)
+
+    def items(self):
+        self._fold()
+        return super().items()
+
+    def values(self):
+        self._fold()
+        return super().values()
+
+    def __reduce__(self):
+        # pickles and deep copies hold a plain defaultdict(dict), as torch's optimizers do
+        return defaultdict, (dict,), None, None, iter(dict.items(self))
+
+
 class ApexW(Optimizer):
     """Memory-efficient AdamW with compact (bf16) or 8-bit (NF4 + log-uint8) state.
 
@@ -149,6 +189,8 @@ class ApexW(Optimizer):
                         block_size=block_size, force_compact_v=force_compact_v, factored_v=factored_v,
                         int4_m=int4_m, six_bit=six_bit)
         super().__init__(params, defaults)
+        self._amp_unfolded = False
+        self.state = _StateMap(self, self.state)
         self._plans = {}
         # seed of the counter-based rounding RNG (drawn from torch's generator, so
         # torch.manual_seed makes runs reproducible)
@@ -171,6 +213,8 @@ class ApexW(Optimizer):
 
     def __setstate__(self, state):
         super().__setstate__(state)
+        self._amp_unfolded = False
+        self.state = _StateMap(self, dict.items(self.state))
         for group in self.param_groups:
             group.setdefault("decay_norm_only", True)
             group.setdefault("clip_grad_norm", None)
@@ -207,28 +251,73 @@ class ApexW(Optimizer):
         # AMP: GradScaler hands over its scale and found_inf instead of unscaling
         # (_step_supports_amp_scaling); an inf/NaN step is skipped, otherwise the
         # grads are unscaled inside the step kernels (apexw/optimizer.py:3458-3480,
-        # :3627-3628)
+        # :3627-3628).  The reference reads both on the host, which waits for the
+        # backward; here the step kernels read them on the device (plan.amp_device_ok)
+        # and the host reads them only for a plan whose kernels cannot.
         found_inf = getattr(self, "found_inf", None)
-        if found_inf is not None and float(found_inf.item()) > 0:
-            return loss
         grad_scale = getattr(self, "grad_scale", None)
-        inv_scale = None
-        if grad_scale is not None:
-            inv_scale = (float(grad_scale.reciprocal().item()) if torch.is_tensor(grad_scale)
-                         else 1.0 / float(grad_scale))
+        amp = None
+        if torch.is_tensor(found_inf) and found_inf.is_cuda and (
+                grad_scale is None or (torch.is_tensor(grad_scale) and grad_scale.is_cuda)):
+            amp = self._amp_tensors(grad_scale, found_inf)
+        self._amp_unfolded = False        # no waits in the lookups of the step itself
+        try:
+            self._step_groups(amp, grad_scale, found_inf)
+        finally:
+            self._amp_unfolded = any(pl.amp_dirty for pl in self._plans.values())
+        return loss
+
+    def _step_groups(self, amp, grad_scale, found_inf):
+        host_amp = None
         for group in self.param_groups:
             gid = id(group)
             plan = self._plans.get(gid)
-            if plan is not None and plan.valid_for(group):
-                plan.execute(group, self._seed, inv_scale)
+            if plan is None or not plan.valid_for(group):
+                old = self._plans.pop(gid, None)
+                if old is not None:
+                    old.amp_fold(sync=True)       # its counters are the states' until the new plan reads them
+                plan = self._build_plan(group)
+                if plan is None:
+                    continue
+                self._plans[gid] = plan
+            # a plan's first launch (the cold rounding order) stays on the host read, so that
+            # a skipped step cannot use it up: the next real step is the cold one, as in the reference
+            if amp is not None and plan.amp_device_ok and plan.cold_done:
+                plan.execute(group, self._seed, amp=amp)
                 continue
-            self._plans.pop(gid, None)
-            plan = self._build_plan(group)
-            if plan is None:
+            if host_amp is None:
+                host_amp = self._read_amp(grad_scale, found_inf)
+            skip, inv_scale = host_amp
+            if skip:
                 continue
             plan.execute(group, self._seed, inv_scale)
-            self._plans[gid] = plan
-        return loss
+
+    @staticmethod
+    def _read_amp(grad_scale, found_inf):
+        """(skip, inv_scale) read on the host, as the reference does."""
+        if found_inf is not None and float(found_inf.item()) > 0:
+            return True, None
+        if grad_scale is None:
+            return False, None
+        return False, (float(grad_scale.reciprocal().item()) if torch.is_tensor(grad_scale)
+                       else 1.0 / float(grad_scale))
+
+    def _amp_tensors(self, grad_scale, found_inf):
+        """(scale, found_inf) as fp32 device scalars for apexw_amp_prepare."""
+        dev = found_inf.device
+        if grad_scale is None:
+            one = getattr(self, "_amp_one", None)
+            if one is None or one.device != dev:
+                one = self._amp_one = torch.ones(1, dtype=torch.float32, device=dev)
+            grad_scale = one
+        return (grad_scale.detach().reshape(1).to(dev, torch.float32).contiguous(),
+                found_inf.detach().reshape(1).to(dev, torch.float32).contiguous())
+
+    def _fold_amp_skips(self):
+        """Make every step counter exact: subtract the steps GradScaler skipped on the device."""
+        self._amp_unfolded = False
+        for plan in self._plans.values():
+            plan.amp_fold(sync=True)
 
     def _build_plan(self, group):
         group["precision"] = S.normalize_precision(group.get("precision", "compact"))
@@ -258,6 +347,7 @@ class ApexW(Optimizer):
 
     # ------------------------------------------------------------------ checkpoints
     def state_dict(self):
+        self._fold_amp_skips()
         sd = super().state_dict()
         meta = {}
         for p, s in self.state.items():
@@ -269,6 +359,7 @@ class ApexW(Optimizer):
     def load_state_dict(self, state_dict):
         """Load, then restore every state tensor in its saved dtype (the base loader
         casts floating state to the parameter dtype)."""
+        self._fold_amp_skips()
         sd = dict(state_dict)
         sd.pop("_dynamic_scaling_meta", None)
         saved = sd.get("state", {})
@@ -294,6 +385,7 @@ class ApexW(Optimizer):
         saved groups and layouts, as the reference's does, then this converts them.
         States already in a layout of the new mode are kept as they are."""
         from . import convert as C
+        self._fold_amp_skips()
         prec = S.normalize_precision(precision)
         if prec not in ("compact", "8bit"):
             raise NotImplementedError(f"apexw_amd implements the compact and 8-bit AdamW step; not supported: "

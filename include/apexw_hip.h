@@ -44,7 +44,7 @@
 extern "C" {
 #endif
 
-#define APEXW_ABI_VERSION 13
+#define APEXW_ABI_VERSION 14
 
 /* status codes */
 enum apexw_status {
@@ -136,6 +136,17 @@ typedef struct apexw_unit {
                                          grad dtype for compact and before a clip, in fp32 after
                                          the step's nan_to_num otherwise (8-bit, factored) */
 #define APEXW_HP_FV_SANITIZE (1u << 7) /* factored: nan_to_num(0, +-65504) on the fp32 grad */
+#define APEXW_HP_AMP (1u << 8)         /* a GradScaler step read on the device: the kernels take
+                                          step_size, eps_scaled, bc2_sqrt and grad_inv_scale from
+                                          *amp (apexw_amp_prepare) and return before any write when
+                                          amp->skip (found_inf); APEXW_HP_UNSCALE is set with it */
+
+/* Step scalars of one launch, written on the device by apexw_amp_prepare (32 bytes). */
+typedef struct apexw_amp_dyn {
+  float step_size, eps_scaled, bc2_sqrt, grad_inv_scale;
+  uint32_t skip;         /* GradScaler found an inf / NaN: no update this step */
+  uint32_t reserved[3];
+} apexw_amp_dyn;
 
 /* Host-computed step scalars (the reference computes them in double). */
 typedef struct apexw_hparams {
@@ -154,7 +165,36 @@ typedef struct apexw_hparams {
   uint32_t mode;
   uint32_t flags;
   float grad_inv_scale; /* with APEXW_HP_UNSCALE: 1 / AMP grad scale (GradScaler) */
-} apexw_hparams;
+  const apexw_amp_dyn* amp;  /* with APEXW_HP_AMP: this launch's device-side step scalars */
+} apexw_hparams;          /* 96 bytes */
+
+/*
+ * GradScaler hands the optimizer its scale and found_inf as device tensors
+ * (torch's _step_supports_amp_scaling protocol); the reference reads both on
+ * the host (found_inf.item(), apexw/optimizer.py:3465-3467; grad_scale
+ * reciprocal, :5530-5537), which waits for the backward to finish.  This call
+ * reads them on the device instead, for up to APEXW_AMP_MAX_LAUNCHES launches
+ * of one step:
+ *   skip  = (*found_inf != 0)
+ *   s     = *skips  (steps skipped so far on the device); when skip, *skips = s + 1
+ *   t     = launch.step - (s - skips_folded)   (the host's step count, which counted
+ *           every step, less the skips it has not subtracted yet)
+ *   bc1   = 1 - beta1^t, bc2 = 1 - beta2^t (double)
+ *   kind 0: step_size = lr sqrt(bc2) / bc1, eps_scaled = eps sqrt(bc2)
+ *   kind 1 (torch._fused_adamw_ order): step_size = lr / bc1, bc2_sqrt = sqrt(bc2)
+ *   grad_inv_scale = 1 / *grad_scale (fp32)
+ * into dyn[i].  launches: HOST array (copied into the launch); skips: one device
+ * int32, zero at first use, owned by the caller's plan.
+ */
+#define APEXW_AMP_MAX_LAUNCHES 16
+typedef struct apexw_amp_launch {
+  double lr, beta1, beta2, eps;
+  double step;           /* the host's (already advanced) step count for this launch */
+  uint32_t kind;         /* 0 or 1, as above */
+  uint32_t reserved;
+} apexw_amp_launch;      /* 48 bytes */
+int apexw_amp_prepare(const float* found_inf, const float* grad_scale, int32_t* skips, int32_t skips_folded,
+                      const apexw_amp_launch* launches, int32_t n_launches, apexw_amp_dyn* dyn, void* stream);
 
 /* ABI version of the loaded library (APEXW_ABI_VERSION). */
 int apexw_abi_version(void);
@@ -256,12 +296,15 @@ int apexw_factored_step(const apexw_tensor* tensors, int32_t n_tensors, const ap
  * unit_begin: n_tensors + 1 int64 prefix offsets of each tensor's units.
  * flags: APEXW_HP_SANITIZE to sanitize grads before squaring; APEXW_HP_UNSCALE
  * to take the norm of dtype_round(g * grad_inv_scale) (AMP grads are unscaled
- * before the clip, apexw/optimizer.py:227-237).
+ * before the clip, apexw/optimizer.py:227-237).  amp: when not NULL, the
+ * unscale factor is amp->grad_inv_scale, read on the device (apexw_amp_prepare);
+ * the same holds for apexw_grad_prepare and apexw_grad_row_means below.
  */
 int apexw_grad_clip_coef(const apexw_tensor* tensors, int32_t n_tensors,
                          const apexw_unit* units, int64_t n_units, int64_t unit_size,
                          const int64_t* unit_begin, float* unit_partial, float* tensor_norm,
-                         float clip, float grad_inv_scale, uint32_t flags, float* coef, void* stream);
+                         float clip, float grad_inv_scale, uint32_t flags, float* coef,
+                         const apexw_amp_dyn* amp, void* stream);
 
 /*
  * apexw_grad_clip_coef without workspace arguments, allocating nothing: the
@@ -282,7 +325,7 @@ int apexw_grad_clip_coef(const apexw_tensor* tensors, int32_t n_tensors,
 int apexw_grad_clip_coef_noalloc(const apexw_tensor* tensors, int32_t n_tensors,
                                  const apexw_unit* units, int64_t n_units, int64_t unit_size,
                                  const int64_t* unit_begin, float clip, float grad_inv_scale,
-                                 uint32_t flags, float* coef, void* stream);
+                                 uint32_t flags, float* coef, const apexw_amp_dyn* amp, void* stream);
 
 /*
  * Gradient preparation of _prepare_grads (apexw/optimizer.py:204-258) for a
@@ -314,7 +357,7 @@ int64_t apexw_grad_prep_units(const apexw_grad_prep* d);
 /* Launch over a device table of descriptors and a unit table ({tensor, unit}
  * entries as for the step), one workgroup per unit. */
 int apexw_grad_prepare(const apexw_grad_prep* preps, int32_t n_preps, const apexw_unit* units, int64_t n_units,
-                       float grad_inv_scale, uint32_t flags, void* stream);
+                       float grad_inv_scale, uint32_t flags, const apexw_amp_dyn* amp, void* stream);
 
 /*
  * Row means only, for centralization folded into the compact step and the clip
@@ -326,7 +369,7 @@ int apexw_grad_prepare(const apexw_grad_prep* preps, int32_t n_preps, const apex
  * (apexw/optimizer.py:238-243) without writing a prepared copy of the grads.
  */
 int apexw_grad_row_means(const apexw_grad_prep* preps, int32_t n_preps, const apexw_unit* units, int64_t n_units,
-                         float grad_inv_scale, uint32_t flags, void* stream);
+                         float grad_inv_scale, uint32_t flags, const apexw_amp_dyn* amp, void* stream);
 
 /* Validate one descriptor (host copy) of apexw_grad_row_means: row_len > 0 divides n, out holds
  * n / row_len floats that do not overlap the grad. */

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 def test_struct_layouts_match_header():
     from apexw_amd import _lib
     assert ctypes.sizeof(_lib.Tensor) == 64 == _lib.TENSOR_DTYPE.itemsize
-    assert ctypes.sizeof(_lib.HParams) == 88
+    assert ctypes.sizeof(_lib.HParams) == 96
     assert _lib.GEMM_PROBLEM_DTYPE.itemsize == 120
     assert ctypes.sizeof(_lib.StateLayout) == 56
 
@@ -219,3 +219,22 @@ def test_bench_contract():
         assert cfg["workload"] and cfg["shapes"], name
         if cfg.get("backward"):
             assert cfg["kwargs"]["precision"] == "8bit" and cfg["backward"] in ("hooks", "plain"), name
+
+
+def test_state_map_pickles_as_plain_defaultdict():
+    """optimizer.state folds device-counted AMP skips on lookup; copies and
+    pickles of an optimizer hold torch's plain defaultdict(dict) and come back
+    as the folding map bound to the new optimizer."""
+    import copy
+    import pickle
+    from collections import defaultdict
+    from apexw_amd import ApexW
+    p = torch.nn.Parameter(torch.zeros(4))
+    opt = ApexW([p], lr=1e-3)
+    opt.state[p]["k"] = 1
+    assert type(pickle.loads(pickle.dumps(opt.state))) is defaultdict
+    twin = copy.deepcopy(opt)
+    assert twin.state._owner is twin and list(twin.state.values()) == [{"k": 1}]
+    other = ApexW([torch.nn.Parameter(torch.zeros(4))], lr=1e-3)
+    other.load_state_dict(opt.state_dict())
+    assert other.state._owner is other

@@ -163,3 +163,69 @@ def test_muon_grad_scale_equals_unscaled():
     for a, b in zip(pa, pb):
         assert torch.equal(a, b)
         assert torch.equal(oa.state[a]["momentum"], ob.state[b]["momentum"])
+
+
+def test_grad_scaler_step_reads_nothing_on_the_host():
+    """Once a plan has taken its first step, a GradScaler step launches without a
+    host synchronisation: found_inf and the scale are read by the kernels
+    (torch's sync debug mode raises on any synchronising torch call)."""
+    _need_gpu()
+    from apexw_amd import ApexW
+    for precision, clip, gc in (("compact", None, False), ("8bit", None, False), ("compact", 1.0, True)):
+        print(f"amp without host reads: {precision} clip={clip} gc={gc}", flush=True)
+        m = _model(3)
+        opt = ApexW(m.parameters(), lr=1e-3, precision=precision, clip_grad_norm=clip, grad_centralization=gc)
+        scaler = torch.amp.GradScaler("cuda", init_scale=2.0 ** 12)
+        x = torch.randn(8, 64, device="cuda")
+        for it in range(3):
+            opt.zero_grad()
+            scaler.scale(m(x).square().mean()).backward()
+            if it > 0:
+                torch.cuda.set_sync_debug_mode("error")
+            try:
+                scaler.step(opt)
+            finally:
+                torch.cuda.set_sync_debug_mode("default")
+            scaler.update()
+        torch.cuda.synchronize()
+        assert all(int(opt.state[p]["step"]) == 3 for p in m.parameters())
+
+
+@pytest.mark.parametrize("precision", ["compact", "8bit"])
+def test_device_amp_equals_host_amp_with_skipped_steps(precision):
+    """The same sequence of scaled steps, some with found_inf, through the device
+    path (GradScaler's CUDA tensors) and the host path (the same values as CPU
+    tensors, read on the host like the reference): identical parameters and
+    state, and step counters that count only the steps taken (exact after
+    state_dict(), which subtracts the skips the device saw)."""
+    _need_gpu()
+    from apexw_amd import ApexW
+    print(f"device vs host amp {precision}", flush=True)
+    gen = torch.Generator().manual_seed(21)
+    shapes = [(256, 128), (300,), (64, 33), (16384,)]
+    host = [(torch.randn(s, generator=gen) * 0.02).bfloat16() for s in shapes]
+    pa = [torch.nn.Parameter(h.cuda()) for h in host]
+    pb = [torch.nn.Parameter(h.cuda()) for h in host]
+    kw = dict(lr=1e-3, weight_decay=0.1, precision=precision, stochastic_rounding=False)
+    oa, ob = ApexW(pa, **kw), ApexW(pb, **kw)
+    scale = 1024.0
+    infs = [0, 0, 1, 0, 1, 1, 0]
+    for it, inf in enumerate(infs):
+        for a, b in zip(pa, pb):
+            g = (torch.randn(a.shape, generator=gen) * 1e-3 * scale).bfloat16()
+            a.grad, b.grad = g.cuda(), g.cuda()
+        oa.grad_scale, oa.found_inf = torch.tensor(scale, device="cuda"), torch.tensor(float(inf), device="cuda")
+        ob.grad_scale, ob.found_inf = torch.tensor(scale), torch.tensor(float(inf))
+        oa.step()
+        ob.step()
+    sd = oa.state_dict()
+    torch.cuda.synchronize()
+    taken = len(infs) - sum(infs)
+    for a, b in zip(pa, pb):
+        assert torch.equal(a, b)
+        sa, sb = oa.state[a], ob.state[b]
+        for k in ("exp_avg", "exp_avg_sq", "exp_avg_scales", "exp_avg_sq_scales"):
+            if k in sb:
+                assert torch.equal(sa[k], sb[k]), k
+        assert float(sa["step"]) == float(sb["step"]) == taken
+    assert all(float(st["step"]) == taken for st in sd["state"].values())

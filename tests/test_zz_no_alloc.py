@@ -54,9 +54,9 @@ def _coef_pair(shapes, seed, clip=1.0):
     coef_b = torch.full((1,), -2.0, device="cuda")
     L.check(lib.apexw_grad_clip_coef(tab.data_ptr(), len(grads), units.data_ptr(), n_units, L.COMPACT_UNIT,
                                      begin.data_ptr(), part.data_ptr(), norms.data_ptr(), clip, 1.0, L.HP_SANITIZE,
-                                     coef_a.data_ptr(), stream), "apexw_grad_clip_coef")
+                                     coef_a.data_ptr(), None, stream), "apexw_grad_clip_coef")
     L.check(lib.apexw_grad_clip_coef_noalloc(tab.data_ptr(), len(grads), units.data_ptr(), n_units, L.COMPACT_UNIT,
-                                             begin.data_ptr(), clip, 1.0, L.HP_SANITIZE, coef_b.data_ptr(), stream),
+                                             begin.data_ptr(), clip, 1.0, L.HP_SANITIZE, coef_b.data_ptr(), None, stream),
             "apexw_grad_clip_coef_noalloc")
     torch.cuda.synchronize()
     # each tensor norm is rounded to the grad dtype (torch._foreach_norm): within one
@@ -98,10 +98,10 @@ def test_noalloc_clip_refuses_oversized_work():
     coef = torch.zeros(1, device="cuda")
     stream = torch.cuda.current_stream().cuda_stream
     st = lib.apexw_grad_clip_coef_noalloc(tab.data_ptr(), 1, units.data_ptr(), L.NOALLOC_CLIP_MAX_UNITS + 1,
-                                          L.COMPACT_UNIT, begin.data_ptr(), 1.0, 1.0, 0, coef.data_ptr(), stream)
+                                          L.COMPACT_UNIT, begin.data_ptr(), 1.0, 1.0, 0, coef.data_ptr(), None, stream)
     assert st == L.ERR_SIZE
     st = lib.apexw_grad_clip_coef_noalloc(tab.data_ptr(), L.NOALLOC_CLIP_MAX_TENSORS + 1, units.data_ptr(), n_units,
-                                          L.COMPACT_UNIT, begin.data_ptr(), 1.0, 1.0, 0, coef.data_ptr(), stream)
+                                          L.COMPACT_UNIT, begin.data_ptr(), 1.0, 1.0, 0, coef.data_ptr(), None, stream)
     assert st == L.ERR_SIZE
     torch.cuda.synchronize()
     assert float(coef.item()) == 0.0     # nothing was enqueued

@@ -13,7 +13,7 @@ import numpy as np
 
 from ._build import LIB_PATH
 
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 # dtype codes
 F32, BF16, F16, U8, I8 = 0, 1, 2, 3, 4
@@ -24,11 +24,12 @@ FLAG_QUAD = 1 << 8
 FLAG_WD = 1 << 9
 FLAG_NF4 = 1 << 10
 FLAG_GENERIC = 1 << 11
-FLAG_DENSE16 = 1 << 12
+FLAG_DENSE = 1 << 12
 FLAG_SCALAR = 1 << 13
 FLAG_FACTORED = 1 << 14
 FLAG_M6 = 1 << 15
 FLAG_GC = 1 << 16
+FLAG_ULTRA = 1 << 17
 
 COMPACT_UNIT = 2048
 

@@ -142,6 +142,12 @@ class StepPlan:
             if v.numel() * 4 == p.numel() and p.numel() % 4 == 0:
                 f |= L.FLAG_QUAD
             block = 0
+        elif st.get("is_ultra", False):
+            # precision "ultra": INT8 m blocks, dense v, the per-parameter rounding order
+            block = int(st.get("block_size_8bit", st.get("ultra_block_size", 256)))
+            f |= L.FLAG_ULTRA | L.FLAG_GENERIC | (_DT[v.dtype] << L.VDT_SHIFT)
+            if block % 8:
+                f |= L.FLAG_SCALAR
         elif st.get("is_8bit", False):
             block = int(st["block_size_8bit"])
             if st.get("is_4bit_m", False):
@@ -153,8 +159,9 @@ class StepPlan:
             if block % 8:
                 f |= L.FLAG_SCALAR
         else:
-            f |= L.FLAG_DENSE16 | (_DT[m.dtype] << L.MDT_SHIFT) | (_DT[v.dtype] << L.VDT_SHIFT)
-            block = 0
+            # dense m / v, stepped in units of 2048 elements
+            f |= L.FLAG_DENSE | (_DT[m.dtype] << L.MDT_SHIFT) | (_DT[v.dtype] << L.VDT_SHIFT)
+            block = L.COMPACT_UNIT
         return f, block
 
     def _build_tables(self, group):
@@ -178,13 +185,13 @@ class StepPlan:
                 if "exp_avg_scales" in st and st.get("is_8bit", False):
                     tab[i]["m_scale"] = st["exp_avg_scales"].data_ptr()
                     tab[i]["v_scale"] = st["exp_avg_sq_scales"].data_ptr()
+                elif st.get("is_ultra", False):
+                    tab[i]["m_scale"] = st["exp_avg_scales"].data_ptr()
             tab[i]["n"] = p.numel()
             tab[i]["flags"] = f
             tab[i]["block"] = block
             if self.kind == "compact":
                 counts[i] = (p.numel() + L.COMPACT_UNIT - 1) // L.COMPACT_UNIT
-            elif f & L.FLAG_DENSE16:
-                counts[i] = 1
             else:
                 counts[i] = (p.numel() + block - 1) // block
         self.host_table = tab          # parameter order

@@ -128,7 +128,7 @@ int apexw_check_tensor(const apexw_tensor* t, int32_t kind) {
     const uint32_t f = t->flags;
     const uint32_t pd = (f >> APEXW_FLAG_PDT_SHIFT) & 3u, gd = (f >> APEXW_FLAG_GDT_SHIFT) & 3u;
     if (!(f & APEXW_FLAG_FACTORED) || !(pd == APEXW_F32 || pd == APEXW_BF16) || gd != pd) return APEXW_ERR_DTYPE;
-    if (f & (APEXW_FLAG_QUAD | APEXW_FLAG_NF4 | APEXW_FLAG_DENSE16)) return APEXW_ERR_ARG;
+    if (f & (APEXW_FLAG_QUAD | APEXW_FLAG_NF4 | APEXW_FLAG_DENSE)) return APEXW_ERR_ARG;
     if (t->block == 0) {
       if ((f & APEXW_FLAG_M6) || ((f >> APEXW_FLAG_MDT_SHIFT) & 3u) != APEXW_BF16) return APEXW_ERR_DTYPE;
     } else {
@@ -138,7 +138,8 @@ int apexw_check_tensor(const apexw_tensor* t, int32_t kind) {
   } else if (kind == 1 || kind == 2) {
     if (!apexw_q8_flags_ok(t->flags, t->block, t->n)) return APEXW_ERR_DTYPE;
     if (kind == 2 && !apexw_q8_fast_eligible(t->flags, t->block)) return APEXW_ERR_DTYPE;
-    if (!(t->flags & APEXW_FLAG_DENSE16) && (!t->m_scale || !t->v_scale)) return APEXW_ERR_ARG;
+    if (!(t->flags & APEXW_FLAG_DENSE) && !t->m_scale) return APEXW_ERR_ARG;
+    if (!(t->flags & (APEXW_FLAG_DENSE | APEXW_FLAG_ULTRA)) && !t->v_scale) return APEXW_ERR_ARG;
   } else {
     return APEXW_ERR_ARG;
   }

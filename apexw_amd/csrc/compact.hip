@@ -160,9 +160,12 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
 #pragma unroll
     for (int j = 0; j < 8; ++j) p[j] = rnd<PD>(p[j] * wd_p);
   }
-  // first moment: cold = mul then add-with-alpha (two roundings); replay with
-  // matching grad/moment dtypes = one lerp.
-  if (hp.mode == APEXW_MODE_REPLAY && GD == MD) {
+  // first moment: the cold step's 16-bit-moment branch = mul then add-with-alpha
+  // (two roundings), its fp32-moment branch = one lerp on the grads cast to fp32
+  // (apexw/optimizer.py:5778-5781); the replay = one lerp when grad and moment
+  // dtypes match, else mul then add (:1228-1238).
+  constexpr bool kLerpCold = MD == APEXW_F32, kLerpReplay = GD == MD;
+  if (hp.mode == APEXW_MODE_REPLAY ? kLerpReplay : kLerpCold) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       float d = g[j] - m[j];
@@ -311,8 +314,14 @@ APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const 
 }
 
 template <bool SR>
-APEXW_DEV void dispatch_group(const apexw_tensor& t, int64_t start, int k, const Ctx& c, uint32_t pd, uint32_t vd,
-                              bool quad) {
+APEXW_DEV void dispatch_group(const apexw_tensor& t, int64_t start, int k, const Ctx& c, uint32_t pd, uint32_t md,
+                              uint32_t vd, bool quad) {
+  if (md == APEXW_F32) {
+    // fp32 moments ("full" precision, small "auto" tensors): fp32 v, no quad (checked on the host)
+    if (pd == APEXW_F32) compact_group<APEXW_F32, APEXW_F32, APEXW_F32, false, SR>(t, start, k, c);
+    else compact_group<APEXW_BF16, APEXW_F32, APEXW_F32, false, SR>(t, start, k, c);
+    return;
+  }
   if (pd == APEXW_F32) {
     if (vd == APEXW_F32) compact_group<APEXW_F32, APEXW_BF16, APEXW_F32, false, SR>(t, start, k, c);
     else if (quad) compact_group<APEXW_F32, APEXW_BF16, APEXW_BF16, true, SR>(t, start, k, c);
@@ -356,12 +365,13 @@ __global__ __launch_bounds__(256) void compact_step_kernel(const apexw_tensor* _
     c.tflags = t.flags;
     c.key = rng_key(hp.seed, un.tensor, hp.step, 0u, (uint32_t)(start >> 32));
     const uint32_t pd = (t.flags >> APEXW_FLAG_PDT_SHIFT) & 3u;
+    const uint32_t md = (t.flags >> APEXW_FLAG_MDT_SHIFT) & 3u;
     const uint32_t vd = (t.flags >> APEXW_FLAG_VDT_SHIFT) & 3u;
     const bool quad = t.flags & APEXW_FLAG_QUAD;
     if (quad && hp.mode == APEXW_MODE_SINGLE) continue;  // rejected on the host; never read v out of range
     if (t.flags & APEXW_FLAG_FACTORED) continue;        // stepped by apexw_factored_step
-    if (sr) dispatch_group<true>(t, start, k, c, pd, vd, quad);
-    else dispatch_group<false>(t, start, k, c, pd, vd, quad);
+    if (sr) dispatch_group<true>(t, start, k, c, pd, md, vd, quad);
+    else dispatch_group<false>(t, start, k, c, pd, md, vd, quad);
   }
 }
 
@@ -371,8 +381,9 @@ __global__ __launch_bounds__(256) void compact_step_kernel(const apexw_tensor* _
 static bool compact_combo_ok(uint32_t flags) {
   const uint32_t pd = (flags >> APEXW_FLAG_PDT_SHIFT) & 3u, gd = (flags >> APEXW_FLAG_GDT_SHIFT) & 3u;
   const uint32_t md = (flags >> APEXW_FLAG_MDT_SHIFT) & 3u, vd = (flags >> APEXW_FLAG_VDT_SHIFT) & 3u;
-  if (!(pd == APEXW_F32 || pd == APEXW_BF16) || gd != pd || md != APEXW_BF16) return false;
-  if (!(vd == APEXW_F32 || vd == APEXW_BF16)) return false;
+  if (!(pd == APEXW_F32 || pd == APEXW_BF16) || gd != pd) return false;
+  if (md == APEXW_F32) return vd == APEXW_F32 && !(flags & APEXW_FLAG_QUAD);   // fp32 moments
+  if (md != APEXW_BF16 || !(vd == APEXW_F32 || vd == APEXW_BF16)) return false;
   if ((flags & APEXW_FLAG_QUAD) && vd != APEXW_BF16) return false;
   return true;
 }

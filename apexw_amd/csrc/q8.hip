@@ -21,7 +21,7 @@
 static __host__ __device__ inline bool apexw_q8_fast_ok(uint32_t flags, uint32_t block) {
   const uint32_t pd = (flags >> APEXW_FLAG_PDT_SHIFT) & 3u, gd = (flags >> APEXW_FLAG_GDT_SHIFT) & 3u;
   return (pd == APEXW_BF16 || pd == APEXW_F32) && gd == pd && (flags & APEXW_FLAG_NF4) &&
-         (flags & APEXW_FLAG_QUAD) && !(flags & (APEXW_FLAG_SCALAR | APEXW_FLAG_DENSE16 | APEXW_FLAG_FACTORED)) &&
+         (flags & APEXW_FLAG_QUAD) && !(flags & (APEXW_FLAG_SCALAR | APEXW_FLAG_DENSE | APEXW_FLAG_FACTORED)) &&
          block == 2048;
 }
 
@@ -117,7 +117,7 @@ template <int GD> APEXW_DEV float q8_grad(float g, uint32_t tflags, const Q8Ctx&
   if (__builtin_isnan(g)) {
     g = 0.0f;
   } else if (__builtin_isinf(g)) {
-    const float big = (tflags & (APEXW_FLAG_GENERIC | APEXW_FLAG_DENSE16)) ? rnd<GD>(65504.0f) : 65504.0f;
+    const float big = (tflags & (APEXW_FLAG_GENERIC | APEXW_FLAG_DENSE)) ? rnd<GD>(65504.0f) : 65504.0f;
     g = g > 0.0f ? big : -big;
   }
   // AMP without a clip: the step unscales its fp32 copy after nan_to_num
@@ -846,41 +846,155 @@ APEXW_DEV void q8_block_fast(const apexw_tensor& t, uint32_t tix, uint32_t blk, 
   q8_fast_compute<PD, SR, FULL, GENERIC>(t, tix, blk, c, r);
 }
 
-// Tensors under 64 elements in 8-bit mode keep 16-bit m/v (optimizer.py:4688-4735).
+// Dense m and v (bf16 or fp32): the fallback branch of _step_ultra
+// (optimizer.py:4688-4735) for 8-bit tensors under 64 elements and the small
+// tensors of precision "ultra" (fp32 m/v).  One 2048-element unit per wave,
+// one element per lane at a time (these tensors are small).
 // SINGLE: the per-parameter in-backward update of such a tensor
 // (apexw/optimizer.py:2458-2471): p.mul_(wd) in the parameter dtype, fp32
 // moments, p.addcdiv_ rounded once, m and v rounded once on store.
-template <int PD, int VD, bool SINGLE>
-APEXW_DEV void q8_dense16(const apexw_tensor& t, const Q8Ctx& c) {
+template <int PD, int MD, int VD, bool SINGLE>
+APEXW_DEV void q8_dense(const apexw_tensor& t, uint32_t unit, const Q8Ctx& c) {
   constexpr int GD = PD;
   const apexw_hparams& hp = *c.hp;
-  const int lane = lane_id();
-  if (lane >= t.n) return;
-  const int64_t i = lane;
-  if constexpr (SINGLE) {
+  const int64_t start = (int64_t)unit * 2048;
+  const int64_t end = (t.n - start) < 2048 ? t.n : start + 2048;
+  for (int64_t i = start + lane_id(); i < end; i += 64) {
     float p = load1<PD>(t.p, i);
-    const float g = load1<GD>(t.g, i);
+    if constexpr (SINGLE) {
+      const float g = load1<GD>(t.g, i);
+      if (t.flags & APEXW_FLAG_WD) p = rnd<PD>(p * hp.wd_factor);
+      const float mf = fmaf(hp.one_minus_beta1, g, load1<MD>(t.m, i) * hp.beta1);
+      const float vf = fmaf(hp.one_minus_beta2 * g, g, load1<VD>(t.v, i) * hp.beta2);
+      const float den = sqrtf(vf) + hp.eps_scaled;
+      store1<MD>(t.m, i, rnd<MD>(mf));
+      store1<VD>(t.v, i, rnd<VD>(vf));
+      store1<PD>(t.p, i, rnd<PD>(p + (-hp.step_size * mf) / den));
+      continue;
+    }
+    const float g = q8_grad<GD>(load1<GD>(t.g, i), t.flags, c);
     if (t.flags & APEXW_FLAG_WD) p = rnd<PD>(p * hp.wd_factor);
-    const float mf = fmaf(hp.one_minus_beta1, g, load1<APEXW_BF16>(t.m, i) * hp.beta1);
+    const float mf = lerp_to(load1<MD>(t.m, i), g, hp.lerp_coef, hp.flags & APEXW_HP_LERP_HI);
+    store1<MD>(t.m, i, rnd<MD>(mf));
     const float vf = fmaf(hp.one_minus_beta2 * g, g, load1<VD>(t.v, i) * hp.beta2);
-    const float den = sqrtf(vf) + hp.eps_scaled;
-    store1<APEXW_BF16>(t.m, i, rnd<APEXW_BF16>(mf));
     store1<VD>(t.v, i, rnd<VD>(vf));
-    store1<PD>(t.p, i, rnd<PD>(p + (-hp.step_size * mf) / den));
-    return;
+    const float den = sqrtf(vf) + hp.eps_scaled;
+    const float upd = (mf / den) * hp.step_size;
+    if constexpr (PD == APEXW_F32) p = p - upd;
+    else p = rnd<PD>(p - rnd<PD>(upd));
+    store1<PD>(t.p, i, p);
   }
-  float p = load1<PD>(t.p, i);
-  float g = q8_grad<GD>(load1<GD>(t.g, i), t.flags, c);
-  if (t.flags & APEXW_FLAG_WD) p = rnd<PD>(p * hp.wd_factor);
-  const float mf = lerp_to(load1<APEXW_BF16>(t.m, i), g, hp.lerp_coef, hp.flags & APEXW_HP_LERP_HI);
-  store1<APEXW_BF16>(t.m, i, rnd<APEXW_BF16>(mf));
-  const float vf = fmaf(hp.one_minus_beta2 * g, g, load1<VD>(t.v, i) * hp.beta2);
-  store1<VD>(t.v, i, rnd<VD>(vf));
-  const float den = sqrtf(vf) + hp.eps_scaled;
-  const float upd = (mf / den) * hp.step_size;
-  if constexpr (PD == APEXW_F32) p = p - upd;
-  else p = rnd<PD>(p - rnd<PD>(upd));
-  store1<PD>(t.p, i, p);
+}
+
+// Precision "ultra" (optimizer.py:4640-4686): one INT8 block of m per wave
+// (t.block = 2048 or 256 elements, scales EMA-max smoothed as for 8-bit) and a
+// dense v in VD.  m = lerp(dequant(m), g, 1 - beta1); v = beta2 v + (1 - beta2) g^2
+// in fp32, stored rounded to VD; the denominator sqrt(v) + eps_scaled comes from
+// the unrounded v, with no eps floor and no lookahead gain; p is decayed (rounded
+// to its dtype), then p - update rounded to p's dtype.
+template <int PD, int VD>
+APEXW_DEV void ultra_block(const apexw_tensor& t, uint32_t tix, uint32_t blk, const Q8Ctx& c) {
+  constexpr int GD = PD;
+  const apexw_hparams& hp = *c.hp;
+  const bool sr = hp.flags & APEXW_HP_SR;
+  const bool vec = !(t.flags & APEXW_FLAG_SCALAR);
+  const int64_t bs = t.block;
+  const int64_t start = (int64_t)blk * bs;
+  const int64_t cnt_blk = (t.n - start) < bs ? (t.n - start) : bs;
+  const int lane = lane_id();
+  const float ms_old = t.m_scale[blk];
+  const uint32_t key = rng_key(hp.seed, tix, hp.step, 1u, (uint32_t)(start >> 32));
+  float mnew[4][8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int64_t rel = (int64_t)(k * 64 + lane) * 8;
+    const int cnt = rel >= cnt_blk ? 0 : (int)((cnt_blk - rel) < 8 ? (cnt_blk - rel) : 8);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mnew[k][j] = 0.0f;
+    if (cnt == 0) continue;
+    const int64_t e0 = start + rel;
+    const bool full = vec && cnt == 8;
+    float p[8], g[8], m[8], v[8];
+    if (full) {
+      load8<PD>(t.p, e0, p);
+      load8<GD>(t.g, e0, g);
+      load8<VD>(t.v, e0, v);
+      const u32x2 w = __builtin_nontemporal_load((const u32x2*)((const int8_t*)t.m + e0));
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t word = j < 4 ? w.x : w.y;
+        m[j] = (float)(int8_t)((word >> (8 * (j & 3))) & 0xFFu) * ms_old;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const bool ok = j < cnt;
+        p[j] = ok ? load1<PD>(t.p, e0 + j) : 0.0f;
+        g[j] = ok ? load1<GD>(t.g, e0 + j) : 0.0f;
+        v[j] = ok ? load1<VD>(t.v, e0 + j) : 0.0f;
+        m[j] = ok ? (float)((const int8_t*)t.m)[e0 + j] * ms_old : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      g[j] = q8_grad<GD>(g[j], t.flags, c);
+      if (t.flags & APEXW_FLAG_WD) p[j] = rnd<PD>(p[j] * hp.wd_factor);
+      m[j] = lerp_to(m[j], g[j], hp.lerp_coef, hp.flags & APEXW_HP_LERP_HI);
+      const float vf = fmaf(hp.one_minus_beta2 * g[j], g[j], v[j] * hp.beta2);
+      v[j] = rnd<VD>(vf);
+      const float upd = (m[j] / (sqrtf(vf) + hp.eps_scaled)) * hp.step_size;
+      if constexpr (PD == APEXW_F32) p[j] = p[j] - upd;
+      else p[j] = rnd<PD>(p[j] - rnd<PD>(upd));
+    }
+    if (full) {
+      store8<PD>(t.p, e0, p);
+      store8<VD>(t.v, e0, v);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (j < cnt) {
+          store1<PD>(t.p, e0 + j, p[j]);
+          store1<VD>(t.v, e0 + j, v[j]);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (j < cnt) {
+        mnew[k][j] = m[j];
+        amax = fmaxf(amax, fabsf(m[j]));
+      }
+    }
+  }
+  // the block scale and the INT8 codes, as the 8-bit step's (quantize_blockwise_int8)
+  amax = wave_max(amax);
+  const float ms = fmaxf(fmaxf(amax, 1e-12f) / 127.0f, ms_old * 0.9f);
+  if (lane == 0) t.m_scale[blk] = ms;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int64_t rel = (int64_t)(k * 64 + lane) * 8;
+    const int cnt = rel >= cnt_blk ? 0 : (int)((cnt_blk - rel) < 8 ? (cnt_blk - rel) : 8);
+    if (cnt == 0) continue;
+    const int64_t e0 = start + rel;
+    uint32_t mc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float y = mnew[k][j] / ms;
+      if (sr) y = y + (unit_uniform(rng_at(key, (uint32_t)(e0 + j)) >> 16) - 0.5f);
+      y = fminf(fmaxf(rintf(y), -127.0f), 127.0f);
+      mc[j] = (uint32_t)(int32_t)y & 0xFFu;
+    }
+    if (vec && cnt == 8) {
+      u32x2 w = {mc[0] | (mc[1] << 8) | (mc[2] << 16) | (mc[3] << 24),
+                 mc[4] | (mc[5] << 8) | (mc[6] << 16) | (mc[7] << 24)};
+      __builtin_nontemporal_store(w, (u32x2*)((int8_t*)t.m + e0));
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (j < cnt) ((uint8_t*)t.m)[e0 + j] = (uint8_t)mc[j];
+    }
+  }
 }
 
 
@@ -984,14 +1098,32 @@ __global__ __launch_bounds__(256) void q8_step_kernel(const apexw_tensor* __rest
     const uint32_t f = t.flags;
     const uint32_t pd = (f >> APEXW_FLAG_PDT_SHIFT) & 3u;
     if (f & APEXW_FLAG_FACTORED) continue;  // stepped by apexw_factored_step
-    if (f & APEXW_FLAG_DENSE16) {
-      const uint32_t vd = (f >> APEXW_FLAG_VDT_SHIFT) & 3u;
-      if (pd == APEXW_F32) {
-        if (vd == APEXW_F32) q8_dense16<APEXW_F32, APEXW_F32, SINGLE>(t, c);
-        else q8_dense16<APEXW_F32, APEXW_BF16, SINGLE>(t, c);
+    const uint32_t vd = (f >> APEXW_FLAG_VDT_SHIFT) & 3u;
+    if (f & APEXW_FLAG_DENSE) {
+      const uint32_t md = (f >> APEXW_FLAG_MDT_SHIFT) & 3u;
+      if (md == APEXW_F32) {
+        // fp32 m implies fp32 v (checked on the host)
+        if (pd == APEXW_F32) q8_dense<APEXW_F32, APEXW_F32, APEXW_F32, SINGLE>(t, un.unit, c);
+        else q8_dense<APEXW_BF16, APEXW_F32, APEXW_F32, SINGLE>(t, un.unit, c);
+      } else if (pd == APEXW_F32) {
+        if (vd == APEXW_F32) q8_dense<APEXW_F32, APEXW_BF16, APEXW_F32, SINGLE>(t, un.unit, c);
+        else q8_dense<APEXW_F32, APEXW_BF16, APEXW_BF16, SINGLE>(t, un.unit, c);
       } else {
-        if (vd == APEXW_F32) q8_dense16<APEXW_BF16, APEXW_F32, SINGLE>(t, c);
-        else q8_dense16<APEXW_BF16, APEXW_BF16, SINGLE>(t, c);
+        if (vd == APEXW_F32) q8_dense<APEXW_BF16, APEXW_BF16, APEXW_F32, SINGLE>(t, un.unit, c);
+        else q8_dense<APEXW_BF16, APEXW_BF16, APEXW_BF16, SINGLE>(t, un.unit, c);
+      }
+      continue;
+    }
+    if (f & APEXW_FLAG_ULTRA) {
+      // the per-parameter update has no INT8-m form (refused on the host): never read v as codes
+      if constexpr (!SINGLE) {
+        if (pd == APEXW_F32) {
+          if (vd == APEXW_F32) ultra_block<APEXW_F32, APEXW_F32>(t, un.tensor, un.unit, c);
+          else ultra_block<APEXW_F32, APEXW_BF16>(t, un.tensor, un.unit, c);
+        } else {
+          if (vd == APEXW_F32) ultra_block<APEXW_BF16, APEXW_F32>(t, un.tensor, un.unit, c);
+          else ultra_block<APEXW_BF16, APEXW_BF16>(t, un.tensor, un.unit, c);
+        }
       }
       continue;
     }
@@ -1015,11 +1147,20 @@ bool apexw_q8_fast_eligible(uint32_t flags, uint32_t block) { return apexw_q8_fa
 bool apexw_q8_flags_ok(uint32_t flags, uint32_t block, int64_t n) {
   const uint32_t pd = (flags >> APEXW_FLAG_PDT_SHIFT) & 3u, gd = (flags >> APEXW_FLAG_GDT_SHIFT) & 3u;
   if (!(pd == APEXW_F32 || pd == APEXW_BF16) || gd != pd) return false;
-  if (flags & APEXW_FLAG_DENSE16) {
-    const uint32_t md = (flags >> APEXW_FLAG_MDT_SHIFT) & 3u, vd = (flags >> APEXW_FLAG_VDT_SHIFT) & 3u;
-    return n <= 64 && md == APEXW_BF16 && (vd == APEXW_BF16 || vd == APEXW_F32);
+  const uint32_t md = (flags >> APEXW_FLAG_MDT_SHIFT) & 3u, vd = (flags >> APEXW_FLAG_VDT_SHIFT) & 3u;
+  if (flags & APEXW_FLAG_DENSE) {
+    // units of 2048 elements; fp32 m comes with fp32 v
+    if (block != 2048 || (flags & (APEXW_FLAG_ULTRA | APEXW_FLAG_NF4 | APEXW_FLAG_QUAD))) return false;
+    if (md == APEXW_F32) return vd == APEXW_F32;
+    return md == APEXW_BF16 && (vd == APEXW_BF16 || vd == APEXW_F32);
   }
   if (block == 0 || block > 2048) return false;
+  if (flags & APEXW_FLAG_ULTRA) {
+    // INT8 m, dense v; a dense v needs no v scales
+    if (flags & (APEXW_FLAG_NF4 | APEXW_FLAG_QUAD)) return false;
+    if (!(vd == APEXW_BF16 || vd == APEXW_F32)) return false;
+    return (block % 8) == 0 || (flags & APEXW_FLAG_SCALAR);
+  }
   if ((flags & APEXW_FLAG_QUAD) && (!(flags & APEXW_FLAG_NF4) || (block % 8) != 0 || (n % 4) != 0)) return false;
   if ((flags & APEXW_FLAG_NF4) && (block % 8) != 0) return false;
   if ((block % 8) != 0 && !(flags & APEXW_FLAG_SCALAR)) return false;

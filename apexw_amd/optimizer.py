@@ -89,8 +89,12 @@ class ApexW(Optimizer):
     precision="compact": bf16 first moment, bf16 (or fp32) second moment,
     quad-shared v for large tensors.  precision="8bit": NF4 momentum + quad
     log-uint8 variance with per-block fp32 scales (INT8 + uint8 for small
-    tensors).  Weight decay is decoupled; ``adamw_compat=True`` decays every
-    tensor and maps betas (0.9, 0.95)/(0.9, 0.99) to (0.9, 0.999).
+    tensors).  precision="full": fp32 moments.  precision="auto": compact
+    moments for 2-D and large tensors, fp32 for small ones (fp32 for all in
+    pure-fp32 training).  precision="ultra": INT8 momentum blocks and a dense
+    16-bit (or fp32) variance for 2-D and large tensors, fp32 for small ones.
+    Weight decay is decoupled; ``adamw_compat=True`` decays every tensor and
+    maps betas (0.9, 0.95)/(0.9, 0.99) to (0.9, 0.999).
     """
 
     _step_supports_amp_scaling = True
@@ -170,10 +174,9 @@ class ApexW(Optimizer):
                     lion=lion, maximize=maximize, capturable=capturable, differentiable=differentiable,
                     auto_pack=auto_pack, factored_v=factored_v, six_bit=six_bit)
         bad = [k for k in _UNSUPPORTED_FLAGS if opts[k]]
-        if bad or beta3 is not None or precision not in ("compact", "8bit"):
-            what = ", ".join(bad + (["beta3"] if beta3 is not None else [])
-                             + ([f"precision={precision!r}"] if precision not in ("compact", "8bit") else []))
-            raise NotImplementedError(f"apexw_amd implements the compact and 8-bit AdamW step; not supported: {what}")
+        if bad or beta3 is not None:
+            what = ", ".join(bad + (["beta3"] if beta3 is not None else []))
+            raise NotImplementedError(f"apexw_amd implements the standard AdamW step; not supported: {what}")
         if precision == "compact" and betas[1] >= 0.99 and not stochastic_rounding and not adamw_compat:
             warnings.warn(
                 f"ApexW: beta2={betas[1]} with precision='compact' and stochastic_rounding=False "
@@ -335,15 +338,19 @@ class ApexW(Optimizer):
         if not params:
             return None
         peft = S.detect_peft_context(self.param_groups)
+        has16 = any(q.dtype in (torch.float16, torch.bfloat16) for g in self.param_groups for q in g["params"])
         for p in params:
             if len(self.state[p]) == 0:
-                self.state[p].update(S.init_state(p, group, peft))
-        if group["precision"] == "8bit":
+                self.state[p].update(S.init_state(p, group, peft, has16))
+        if group["precision"] in ("8bit", "ultra"):
+            # both run the reference's _step_ultra (optimizer.py:3583-3587)
             return StepPlan(self, group, params, "q8")
         sts = [self.state[p] for p in params]
+        # torch._fused_adamw_ when every state matches its parameter's dtype and size,
+        # unless fused=False asks for the foreach path (optimizer.py:3676-3720)
         homogeneous = all("exp_avg_sq" in st and st["exp_avg"].dtype == st["exp_avg_sq"].dtype == p.dtype
                           and st["exp_avg"].numel() == st["exp_avg_sq"].numel() for p, st in zip(params, sts))
-        return StepPlan(self, group, params, "compact", native=homogeneous)
+        return StepPlan(self, group, params, "compact", native=homogeneous and group.get("fused") is not False)
 
     # ------------------------------------------------------------------ checkpoints
     def state_dict(self):
@@ -595,6 +602,10 @@ class ApexW(Optimizer):
             # missing exp_avg_sq); refuse before touching the state or the step counter
             raise RuntimeError("enable_fused_backward cannot step a parameter with factored_v state "
                                "(exp_avg_sq_row / exp_avg_sq_col); use step()")
+        if state.get("is_ultra", False):
+            # the reference's per-parameter update would treat the INT8 m codes as a dense moment
+            raise RuntimeError("enable_fused_backward cannot step a parameter with ultra (INT8 m) state; "
+                               "use step()")
         if len(state) == 0:
             if prec == "8bit":
                 S.ensure_8bit_state(state, p, group)

@@ -21,6 +21,14 @@ compact:
     six_bit=True from 524,288 elements);
   * tensors under 64 elements keep compact 16-bit m/v.
 compact with factored_v=True: the same factored v from 524,288 elements, bf16 m.
+full (or fused=True): fp32 m and v for every parameter.
+auto: fp32 m/v for an fp32 parameter when nothing points at mixed precision (no
+  16-bit parameter in the optimizer, fp32 grad, amp not set, no PEFT); otherwise
+  compact m/v (quad v and factored v as for compact) for 2-D tensors and 1-D ones
+  of >= threshold elements, fp32 m/v for the other 1-D tensors.
+ultra: INT8 m with one fp32 scale per 2048 elements (256 below 2048 elements)
+  and a dense v in the compact v dtype, for 2-D tensors and 1-D ones of >=
+  threshold elements; fp32 m/v for the rest.
 Initial state: NF4 bytes 0x77 (both codes = 0.0), m scales 1e-12 (INT8: 1e-12/127),
 v codes 0 with scales 1e-12.
 """
@@ -193,8 +201,19 @@ def ensure_8bit_state(st, p, group):
     return st
 
 
-def init_state(p, group, peft_ctx):
-    """Fresh state dict for ``p`` (keys and dtypes as the reference's _init_group)."""
+def _mixed_precision_in_sight(p, group, has_16bit_params, is_peft):
+    """The "auto" precision's test for mixed-precision training
+    (apexw/optimizer.py:2699-2708)."""
+    return (bool(group.get("amp", False)) or has_16bit_params
+            or (p.grad is not None and p.grad.dtype in (torch.float16, torch.bfloat16))
+            or torch.is_autocast_enabled() or p.dtype in (torch.float16, torch.bfloat16) or is_peft)
+
+
+def init_state(p, group, peft_ctx, has_16bit_params=False):
+    """Fresh state dict for ``p`` (keys and dtypes as the reference's _init_group).
+
+    has_16bit_params: whether any parameter of the optimizer is 16-bit (the
+    "auto" precision keeps fp32 moments only when none is)."""
     prec = group["precision"]
     beta2 = group["betas"][1]
     sr = bool(group.get("stochastic_rounding", True))
@@ -202,6 +221,35 @@ def init_state(p, group, peft_ctx):
     n = p.numel()
     st = {"stochastic_rounding": sr, "step": torch.tensor(0.0, dtype=torch.float32)}
     is_peft = is_peft_parameter(p) or peft_ctx
+    large = p.dim() >= 2 or n >= group.get("threshold", 65536)
+    if group.get("fused") is True or prec == "full":
+        # optimizer.py:2625-2626, :2769-2772
+        st.update(is_factored_v=False, is_6bit_m=False)
+        return _moments(st, p, torch.float32, group, is_peft, prec)
+    if prec == "ultra":
+        # optimizer.py:2736-2748, :2779-2784, :2816-2834
+        st.update(is_factored_v=False, is_6bit_m=False)
+        if not large:
+            st["is_ultra"] = False
+            return _moments(st, p, torch.float32, group, is_peft, prec)
+        bs = 2048 if n >= 2048 else 256
+        vdt = v_dtype_for_beta2(compact_dtype(p), beta2, group.get("force_compact_v", False), sr)
+        st.update(is_ultra=True, ultra_block_size=bs, state_dtype=torch.int8, state_dtype_v=vdt)
+        st["exp_avg"] = torch.zeros(p.shape, dtype=torch.int8, device=dev)
+        st["exp_avg_scales"] = torch.full(((n + bs - 1) // bs, 1), 1e-12 / 127.0, dtype=torch.float32, device=dev)
+        st["exp_avg_sq"] = torch.zeros(p.shape, dtype=vdt, device=dev)
+        return st
+    if prec == "auto":
+        # optimizer.py:2694-2735 (the parameters here are on the GPU)
+        st.update(is_factored_v=False, is_6bit_m=False)
+        fp32_training = p.dtype == torch.float32 and not _mixed_precision_in_sight(p, group, has_16bit_params,
+                                                                                   is_peft)
+        if fp32_training or not large:
+            return _moments(st, p, torch.float32, group, is_peft, prec)
+        if bool(group.get("factored_v", False)) and _can_factor(p, is_peft, FACTORED_MIN_COMPACT):
+            st["is_factored_v"] = True
+            return _factored_compact(st, p)
+        return _moments(st, p, compact_dtype(p), group, is_peft, prec)
     if prec == "8bit" and n >= 64:
         bs = block_size_8bit(p, group.get("block_size"))
         narrow = p.dim() >= 2 and min(p.shape) <= 32 and n < 2048
@@ -218,17 +266,29 @@ def init_state(p, group, peft_ctx):
         factored = bool(group.get("factored_v", False)) and _can_factor(p, is_peft, FACTORED_MIN_COMPACT)
         st.update(is_6bit_m=False, is_4bit_m=False, is_factored_v=factored)
         if factored:
-            # 16-bit m, fp32 row/column v (optimizer.py:2749-2767, :2785-2787, :2859-2863)
-            st["state_dtype"] = compact_dtype(p)
-            st["state_dtype_v"] = torch.float32
-            st["exp_avg"] = torch.zeros(p.shape, dtype=compact_dtype(p), device=dev)
-            _factored_v(st, p)
-            st["scale_v"] = 1.0
-            st["sqrt_scale_v"] = 1.0
-            return st
-    mdt = compact_dtype(p)
-    vdt = v_dtype_for_beta2(mdt, beta2, group.get("force_compact_v", False), sr)
-    quad = (prec == "compact" and mdt in (torch.bfloat16, torch.float16) and vdt in (torch.bfloat16, torch.float16)
+            return _factored_compact(st, p)
+    return _moments(st, p, compact_dtype(p), group, is_peft, prec)
+
+
+def _factored_compact(st, p):
+    """16-bit m, fp32 row/column v (optimizer.py:2749-2767, :2785-2787, :2859-2863)."""
+    st["state_dtype"] = compact_dtype(p)
+    st["state_dtype_v"] = torch.float32
+    st["exp_avg"] = torch.zeros(p.shape, dtype=compact_dtype(p), device=p.device)
+    _factored_v(st, p)
+    st["scale_v"] = 1.0
+    st["sqrt_scale_v"] = 1.0
+    return st
+
+
+def _moments(st, p, mdt, group, is_peft, prec):
+    """Dense m in ``mdt``, v in the beta2 rule's dtype, quad v for large 16-bit
+    compact / auto tensors (optimizer.py:2788-2810, :2838-2872)."""
+    n, dev = p.numel(), p.device
+    vdt = v_dtype_for_beta2(mdt, group["betas"][1], group.get("force_compact_v", False),
+                            bool(group.get("stochastic_rounding", True)))
+    quad = (prec in ("compact", "auto") and mdt in (torch.bfloat16, torch.float16)
+            and vdt in (torch.bfloat16, torch.float16)
             and group.get("int4_m", None) is not False and n >= 16384 and n % 4 == 0
             and (p.dim() < 2 or min(p.shape) >= 8)
             and (is_peft or len(group["params"]) >= 8))

@@ -44,7 +44,7 @@
 extern "C" {
 #endif
 
-#define APEXW_ABI_VERSION 14
+#define APEXW_ABI_VERSION 15
 
 /* status codes */
 enum apexw_status {
@@ -68,7 +68,9 @@ enum apexw_dtype { APEXW_F32 = 0, APEXW_BF16 = 1, APEXW_F16 = 2, APEXW_U8 = 3, A
 #define APEXW_FLAG_WD (1u << 9)         /* apply decoupled weight decay */
 #define APEXW_FLAG_NF4 (1u << 10)       /* 8-bit: NF4 packed m (else INT8 m) */
 #define APEXW_FLAG_GENERIC (1u << 11)   /* 8-bit: per-parameter ("generic") rounding order */
-#define APEXW_FLAG_DENSE16 (1u << 12)   /* 8-bit mode tensor kept in 16-bit m/v (numel < 64) */
+#define APEXW_FLAG_DENSE (1u << 12)     /* 8-bit / ultra step: dense m and v (bf16 or fp32; MDT / VDT
+                                           fields), element-wise update in units of 2048 elements:
+                                           8-bit tensors under 64 elements, small ultra tensors */
 #define APEXW_FLAG_SCALAR (1u << 13)    /* pointers not 16-byte aligned: element-wise path */
 #define APEXW_FLAG_FACTORED (1u << 14)  /* factored second moment: stepped by apexw_factored_step;
                                            the compact and 8-bit step kernels skip the row */
@@ -77,6 +79,8 @@ enum apexw_dtype { APEXW_F32 = 0, APEXW_BF16 = 1, APEXW_F16 = 2, APEXW_U8 = 3, A
                                            is read raw and g - mean(row) taken in its dtype (after
                                            sanitize / unscale, before the clip), with m_scale = the fp32
                                            row means (apexw_grad_row_means) and block = the row length */
+#define APEXW_FLAG_ULTRA (1u << 17)     /* 8-bit step kernel, precision "ultra": INT8 m with one scale per
+                                           block (m_scale), dense v (VDT field), no v scales */
 
 /*
  * One tensor of a multi-tensor launch (device-resident array, 64 bytes each).

@@ -7,7 +7,8 @@ rounding point of the reference is reproduced:
 
 1. decoupled weight decay ``p *= 1 - lr*wd`` (dim>=2 tensors when
    decay_norm_only) -- optimizer.py:5585-5592
-2. ``m = m*b1``, ``m += (1-b1)*g``                 -- :5760-5761 / quad :5684-5685
+2. ``m = m*b1``, ``m += (1-b1)*g``                 -- :5760-5761 / quad :5684-5685;
+   fp32 m (``full`` / small ``auto`` tensors): ``m = lerp(m, g, 1-b1)`` -- :5780
 3. ``v`` EMA: SR path when beta2 >= 0.995 and SR on (fp32 math then SR to 16
    bits, per tensor), else two foreach ops in v's dtype -- :5770-5776 / :5691-5697
 4. ``d = sqrt(v) + eps*sqrt(bc2)`` in v's dtype       -- :5799-5816 / :5704-5721
@@ -66,11 +67,15 @@ def compact_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weigh
         if decay:
             torch._foreach_mul_(decay, 1.0 - lr * weight_decay)
     gf = [g if g.dtype == torch.float32 else g.float() for g in grads]
-    mdt = ms[0].dtype
-    if mdt not in (torch.bfloat16, torch.float16):
-        raise NotImplementedError("oracle compact step expects 16-bit m")
-    torch._foreach_mul_(ms, beta1)
-    torch._foreach_add_(ms, gf, alpha=1.0 - beta1)
+    if ms[0].dtype in (torch.bfloat16, torch.float16):
+        torch._foreach_mul_(ms, beta1)
+        torch._foreach_add_(ms, gf, alpha=1.0 - beta1)
+    elif ms[0].dtype == torch.float32:
+        # fp32 moments ("full", small "auto" tensors): the grads cast to m's dtype
+        # and one lerp (optimizer.py:5669-5674, :5778-5781)
+        torch._foreach_lerp_(ms, gf, 1.0 - beta1)
+    else:
+        raise NotImplementedError(f"oracle compact step: m dtype {ms[0].dtype}")
     v16 = vs[0].dtype in (torch.bfloat16, torch.float16)
     if is_quad:
         gq = [g.reshape(-1, 4).square().mean(dim=1) for g in gf]

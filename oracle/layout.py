@@ -2,7 +2,13 @@
 
 Restates the decisions of the reference's ``ApexW._init_group``
 (``apexw/optimizer.py:2574-2957``) and the dtype resolvers in
-``apexw/state.py:62-162`` for the ``compact`` and ``8bit`` precisions.
+``apexw/state.py:62-162`` for the ``compact``, ``8bit``, ``full``, ``auto`` and
+``ultra`` precisions.
+
+``auto`` keeps fp32 moments for an fp32 parameter on a CUDA device when no
+mixed precision is in sight (optimizer.py:2712-2715); ``cuda=True`` (the
+default) takes that branch for the GPU parameters the product steps, whose CPU
+copies the oracle updates.
 """
 
 import torch
@@ -70,14 +76,59 @@ def can_factor(p, is_peft, min_numel):
     return p.shape[0] >= 128 and p.numel() // p.shape[0] >= 128
 
 
-def init_state(p, group, n_params_in_group, peft_ctx):
-    """Allocate and return a fresh state dict for parameter ``p``."""
+def amp_active(p, group, has_16bit_params, is_peft):
+    """optimizer.py:2699-2708 (autocast outside step() aside)."""
+    return (bool(group.get("amp", False)) or has_16bit_params
+            or (p.grad is not None and p.grad.dtype in (torch.float16, torch.bfloat16))
+            or p.dtype in (torch.float16, torch.bfloat16) or is_peft)
+
+
+def init_state(p, group, n_params_in_group, peft_ctx, has_16bit_params=None, cuda=True):
+    """Allocate and return a fresh state dict for parameter ``p``.
+
+    has_16bit_params: whether any parameter of the optimizer is 16-bit (None:
+    this parameter's group decides); cuda: lay out as for a CUDA parameter."""
     prec = group["precision"]
     beta2 = group["betas"][1]
     sr = bool(group["stochastic_rounding"])
     st = {"stochastic_rounding": sr, "step": torch.tensor(0.0, dtype=torch.float32)}
     n = p.numel()
     is_peft = is_peft_param(p) or peft_ctx
+    if has_16bit_params is None:
+        has_16bit_params = any(q.dtype in (torch.float16, torch.bfloat16) for q in group.get("params", ()))
+    threshold = group.get("threshold", 65536)
+    massive = p.dim() >= 2 or n >= threshold
+    if group.get("fused") is True or prec == "full":
+        # fp32 moments whatever the parameter dtype (optimizer.py:2625-2626, :2769-2772)
+        st.update(is_factored_v=False, is_6bit_m=False)
+        return _dense(st, p, torch.float32, group, is_peft, n_params_in_group, prec)
+    if prec == "ultra":
+        # INT8 block-quantized m and a dense v for 2-D or large tensors, fp32 m/v
+        # for the rest (optimizer.py:2736-2748, :2779-2784, :2816-2834)
+        st.update(is_factored_v=False, is_6bit_m=False)
+        if not massive:
+            st["is_ultra"] = False
+            return _dense(st, p, torch.float32, group, is_peft, n_params_in_group, prec)
+        bs = 2048 if n >= 2048 else 256
+        vdt = v_dtype(compact_dtype(p), beta2, group.get("force_compact_v", False), sr)
+        st.update(is_ultra=True, ultra_block_size=bs, state_dtype=torch.int8, state_dtype_v=vdt)
+        st["exp_avg"] = torch.zeros(p.shape, dtype=torch.int8)
+        st["exp_avg_scales"] = torch.full(((n + bs - 1) // bs, 1), 1e-12 / 127.0, dtype=torch.float32)
+        st["exp_avg_sq"] = torch.zeros(p.shape, dtype=vdt)
+        return st
+    if prec == "auto":
+        # optimizer.py:2694-2735: fp32 moments for pure-fp32 CUDA training, else 16-bit
+        # for 2-D or large tensors and fp32 for small ones
+        st.update(is_factored_v=False, is_6bit_m=False)
+        if cuda and p.dtype == torch.float32 and not amp_active(p, group, has_16bit_params, is_peft):
+            return _dense(st, p, torch.float32, group, is_peft, n_params_in_group, prec)
+        if not massive:
+            return _dense(st, p, torch.float32, group, is_peft, n_params_in_group, prec)
+        cdt = compact_dtype(p)
+        if bool(group.get("factored_v", False)) and can_factor(p, is_peft, 524288):
+            st["is_factored_v"] = True
+            return _factored_compact(st, p, cdt)
+        return _dense(st, p, cdt, group, is_peft, n_params_in_group, prec)
     if prec == "8bit" and n >= 64:
         bs = block_size_8bit(p, group.get("block_size"))
         narrow = p.dim() >= 2 and min(p.shape) <= 32 and n < 2048
@@ -118,19 +169,32 @@ def init_state(p, group, n_params_in_group, peft_ctx):
         fv = bool(group.get("factored_v", False)) and can_factor(p, is_peft, 524288)
         st.update(is_6bit_m=False, is_4bit_m=False, is_factored_v=fv)
         if fv:
-            st["state_dtype"] = compact_dtype(p)
-            st["state_dtype_v"] = torch.float32
-            st["exp_avg"] = torch.zeros(p.shape, dtype=compact_dtype(p))
-            st["exp_avg_sq_row"] = torch.zeros(p.shape[0], dtype=torch.float32)
-            st["exp_avg_sq_col"] = torch.zeros(n // p.shape[0], dtype=torch.float32)
-            st["scale_v"] = 1.0
-            st["sqrt_scale_v"] = 1.0
-            return st
+            return _factored_compact(st, p, compact_dtype(p))
     else:
-        raise NotImplementedError(f"oracle covers compact and 8bit, not {prec!r}")
-    mdt = compact_dtype(p)
-    vdt = v_dtype(mdt, beta2, group.get("force_compact_v", False), sr)
-    quad = (prec == "compact" and mdt in (torch.bfloat16, torch.float16) and vdt in (torch.bfloat16, torch.float16)
+        raise NotImplementedError(f"oracle does not cover precision {prec!r}")
+    return _dense(st, p, compact_dtype(p), group, is_peft, n_params_in_group, prec)
+
+
+def _factored_compact(st, p, mdt):
+    """16-bit m, fp32 row / column v (optimizer.py:2785-2787, :2859-2863)."""
+    n = p.numel()
+    st["state_dtype"] = mdt
+    st["state_dtype_v"] = torch.float32
+    st["exp_avg"] = torch.zeros(p.shape, dtype=mdt)
+    st["exp_avg_sq_row"] = torch.zeros(p.shape[0], dtype=torch.float32)
+    st["exp_avg_sq_col"] = torch.zeros(n // p.shape[0], dtype=torch.float32)
+    st["scale_v"] = 1.0
+    st["sqrt_scale_v"] = 1.0
+    return st
+
+
+def _dense(st, p, mdt, group, is_peft, n_params_in_group, prec):
+    """m in ``mdt``, v in the dtype the beta2 rule gives, quad-shared v for large
+    16-bit compact/auto tensors (optimizer.py:2788-2810, :2838-2872)."""
+    n = p.numel()
+    vdt = v_dtype(mdt, group["betas"][1], group.get("force_compact_v", False), bool(group["stochastic_rounding"]))
+    quad = (prec in ("compact", "auto") and mdt in (torch.bfloat16, torch.float16)
+            and vdt in (torch.bfloat16, torch.float16)
             and group.get("int4_m") is not False and n >= 16384 and n % 4 == 0
             and (p.dim() < 2 or min(p.shape) >= 8) and (is_peft or n_params_in_group >= 8))
     if quad:

@@ -2,10 +2,12 @@
 
 ``OracleApexW`` mirrors the reference ``ApexW`` constructor defaults and the CPU
 dispatch of ``ApexW.step`` (``apexw/optimizer.py:3359-4094``) for the
-``compact`` and ``8bit`` precisions:
+``compact``, ``8bit``, ``full``, ``auto`` and ``ultra`` precisions (``ultra``
+steps like ``8bit`` through ``_step_ultra``; ``full`` and ``auto`` like
+``compact``, their state layouts aside):
 
 * constructor: precision aliases (state.py:94-121), default betas (0.9, 0.999)
-  for 8bit and (0.9, 0.99) for compact, ``adamw_compat`` forcing
+  for 8bit and full, (0.9, 0.99) otherwise, ``adamw_compat`` forcing
   ``decay_norm_only=False`` and mapping betas (0.9, 0.95)/(0.9, 0.99) to
   (0.9, 0.999) -- optimizer.py:1672-1714;
 * step: grad preparation (sanitize + global-norm clip, optimizer.py:204-258 and
@@ -36,8 +38,11 @@ from .factored import factored_update
 from .q8 import q8_param_step
 
 _PREC = {
+    "full": ("full", "fp32", "float32", "float", "fp64", "float64", "double"),
     "compact": ("compact", "bf16", "bfloat16", "fp16", "float16", "half", "16", "16-bit"),
     "8bit": ("8bit", "8-bit", "int8", "uint8", "q8", "adamw_8bit", "bnb_8bit"),
+    "ultra": ("ultra", "ultra_stable", "3byte", "hybrid8"),
+    "auto": ("auto", "smart", "adaptive"),
 }
 
 
@@ -61,10 +66,10 @@ class OracleApexW:
     def __init__(self, params, lr=1e-3, betas=None, eps=1e-8, weight_decay=1e-2, decay_norm_only=True,
                  adamw_compat=False, clip_grad_norm=None, precision="compact", stochastic_rounding=True,
                  block_size=None, force_compact_v=False, int4_m=None, grad_centralization=False,
-                 factored_v=False, six_bit=False):
+                 factored_v=False, six_bit=False, threshold=65536, amp=None):
         precision = normalize_precision(precision)
         if betas is None:
-            betas = (0.9, 0.999) if precision == "8bit" else (0.9, 0.99)
+            betas = (0.9, 0.999) if precision in ("8bit", "full") else (0.9, 0.99)
         if adamw_compat:
             decay_norm_only = False
             if tuple(betas) in ((0.9, 0.95), (0.9, 0.99)):
@@ -75,7 +80,7 @@ class OracleApexW:
                           precision=precision, stochastic_rounding=stochastic_rounding,
                           block_size=block_size, force_compact_v=force_compact_v, int4_m=int4_m,
                           grad_centralization=grad_centralization, factored_v=factored_v, six_bit=six_bit,
-                          params=self.params)
+                          threshold=threshold, amp=amp, params=self.params)
         self.state = {}
         self._plan = None
         self.grad_scale = None
@@ -148,10 +153,11 @@ class OracleApexW:
             if p not in self.state:
                 self.state[p] = L.init_state(p, grp, len(self.params), peft)
         prec = grp["precision"]
+        quantized = prec in ("8bit", "ultra")     # both run _step_ultra (optimizer.py:3583-3587)
         grads, scale = self._prepare([p.grad for p in plist],
-                                     sanitize=prec != "8bit" or grp["clip_grad_norm"] is not None)
+                                     sanitize=not quantized or grp["clip_grad_norm"] is not None)
         kw = self._kw()
-        if prec == "8bit":
+        if quantized:
             for p, g in zip(plist, grads):
                 st = self.state[p]
                 st["step"].add_(1)

@@ -10,6 +10,11 @@ nesterov / cautious / factored-v), per parameter:
   rounded into p first, then ``p -= bf16(update)`` (SR only for quad-v);
 * tensors with fewer than 64 elements keep 16-bit m/v, optimizer.py:4688-4735.
 
+``precision="ultra"`` runs the same function (optimizer.py:3583-3587): 2-D or
+large tensors hold INT8 m and a dense 16-bit (or fp32) v, updated without the
+lookahead gain and without the eps floor (:4640-4686); the others keep fp32
+m/v and take the dense branch above.
+
 The update is AdamW with the "Nesterov-SNR" lookahead gain: ``m_look =
 lerp(g, m, b1)``, gain ``1+0.2*b1`` where ``m*g >= 0`` else ``1-0.35*b1``.
 """
@@ -49,6 +54,9 @@ def q8_param_step(p, g, st, *, lr, beta1, beta2, eps, weight_decay, decay_norm_o
         factored_update(p, g, st, beta1=beta1, beta2=beta2, step_size=step_size, eps_scaled=eps_scaled, eps=eps,
                         stochastic=sr, block_size=st.get("block_size_8bit", 256),
                         wd_factor=decay if apply_wd else None, inv_scale=inv_scale, sanitize=True)
+        return
+    if st.get("is_ultra", False):
+        _ultra(p, g, st, beta1, beta2, step_size, eps_scaled, decay if apply_wd else None, sr, inv_scale)
         return
     if st.get("is_8bit", False) and n > CHUNK and p.is_contiguous():
         _chunked(p, g, st, beta1, beta2, eps, step_size, eps_scaled, decay if apply_wd else None, sr, inv_scale)
@@ -170,3 +178,26 @@ def _chunked(p, g, st, beta1, beta2, eps, step_size, eps_scaled, decay, sr, inv_
         qv, s2 = Q.quant_logu8(v, vbs, sv, sr)
         vsl.copy_(qv.view(vsl.shape))
         sv.copy_(s2)
+
+
+def _ultra(p, g, st, beta1, beta2, step_size, eps_scaled, decay, sr, inv_scale):
+    """optimizer.py:4500-4511, :4640-4686: INT8 m (block ``ultra_block_size``,
+    EMA-max scales), dense v rounded to its dtype once, the denominator from the
+    unrounded fp32 v, p decayed then ``p -= update.to(p.dtype)``."""
+    gf = torch.nan_to_num(g, nan=0.0, posinf=65504.0, neginf=-65504.0).float()
+    if inv_scale is not None:
+        gf.mul_(inv_scale)
+    if decay is not None:
+        p.mul_(decay)
+    bs = st.get("block_size_8bit", st.get("ultra_block_size", 256))
+    m = Q.dequant_int8(st["exp_avg"], st["exp_avg_scales"], bs)
+    m.lerp_(gf, 1.0 - beta1)
+    v = st["exp_avg_sq"]
+    vf = v.float().mul_(beta2).addcmul_(gf, gf, value=1.0 - beta2)
+    v.copy_(vf.to(v.dtype))
+    den = vf.sqrt().add_(eps_scaled)
+    upd = (m / den).mul_(step_size)
+    p.sub_(upd.to(p.dtype))
+    q, s = Q.quant_int8(m, bs, st["exp_avg_scales"], sr)
+    st["exp_avg"].copy_(q.view(st["exp_avg"].shape))
+    st["exp_avg_scales"].copy_(s)

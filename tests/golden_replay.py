@@ -9,8 +9,8 @@ import os
 import numpy as np
 import torch
 
-from golden.make_golden import (FV_KW, FV_Q8_SHAPES, HOOK_KW, HOOK_SHAPES, SD_CASES, _fingerprint, _grad,
-                                 _param)
+from golden.make_golden import (FV_KW, FV_Q8_SHAPES, HOOK_KW, HOOK_SHAPES, PREC_CASES, SD_CASES, _fingerprint,
+                                 _grad, _param)
 from golden.sd_codec import decode
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -50,6 +50,9 @@ FV_CASES = {
     "fv_compact_bf16_rne": ([(512, 1024), (768,)], torch.bfloat16, 3, 24, FV_KW, None, ()),
 }
 CASES.update(FV_CASES)
+# the full / auto / ultra precisions (every state tensor recorded)
+PREC_NAMES = sorted(PREC_CASES)
+CASES.update({k: (sh, dt, n, seed, kw, None, ()) for k, (sh, dt, n, seed, kw) in PREC_CASES.items()})
 # in-backward trajectories: name -> (steps, backward passes per step, seed)
 HOOK_CASES = {"hooks_k1_rne": (3, 1, 31), "hooks_k2_rne": (3, 2, 32)}
 

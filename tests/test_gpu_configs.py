@@ -157,7 +157,10 @@ class Mirror:
             with torch.no_grad():
                 cp.copy_(p0)
             if cp not in self.copt.state:
-                self.copt.state[cp] = OL.init_state(cp, self.copt.group, self.n_group, False)
+                # the PEFT context and the 16-bit test look at the whole GPU list, as the optimizer does
+                peft = OL.peft_context([{"params": self.gps}])
+                has16 = any(p.dtype in (torch.float16, torch.bfloat16) for p in self.gps)
+                self.copt.state[cp] = OL.init_state(cp, self.copt.group, self.n_group, peft, has_16bit_params=has16)
             if snap is None:
                 continue
             cst = self.copt.state[cp]
@@ -175,7 +178,7 @@ class Mirror:
             assert sorted(_tensor_keys(gs)) == sorted(_tensor_keys(cs)), f"{e}: state keys"
             for k in _tensor_keys(cs):
                 assert gs[k].dtype == cs[k].dtype and gs[k].numel() == cs[k].numel(), f"{e} {k} layout"
-            for k in ("is_8bit", "is_4bit_m", "is_quad_v", "block_size_8bit"):
+            for k in ("is_8bit", "is_4bit_m", "is_quad_v", "block_size_8bit", "is_ultra", "ultra_block_size"):
                 assert gs.get(k) == cs.get(k), f"{e} {k}"
 
     def step(self, grads, sr_check=None):
@@ -192,9 +195,12 @@ class Mirror:
             gs, cs = self._gpu_state(gopt, e), self.copt.state[cp]
             name = f"{tag} tensor {e}"
             # one bf16 ulp of the update where the reference rounds it (or its denominator) to
-            # bf16: compact with bf16 v, and 8-bit tensors in generic order (p -= bf16(update))
+            # bf16: compact with bf16 v, and the 8-bit / ultra step's tensors outside the chunked
+            # order (p -= bf16(update))
             bf16_den = not cs.get("is_8bit", False) and cs["exp_avg_sq"].dtype == torch.bfloat16
-            generic_8bit = cs.get("is_8bit", False) and cp.dtype == torch.bfloat16 and cp.numel() <= 262144
+            quantized_mode = self.copt.group["precision"] in ("8bit", "ultra")
+            chunked = cs.get("is_8bit", False) and cp.numel() > 262144
+            generic_8bit = quantized_mode and cp.dtype == torch.bfloat16 and not chunked
             _cmp_p(self._gpu_p(e), cp.detach(), self.pre[j][0], f"{name} p",
                    2.0 ** -7 if (bf16_den or generic_8bit) else 2.0 ** -22)
             for k in _tensor_keys(cs):
@@ -211,7 +217,7 @@ def _sr_targets(chk, mirror, gopt):
         if cp.dtype == torch.bfloat16:
             chk.target(cp.data, mirror._gpu_p(e), "p")
         cs = mirror.copt.state[cp]
-        if not cs.get("is_8bit", False) and cs["exp_avg_sq"].dtype == torch.bfloat16:
+        if not (cs.get("is_8bit", False) or cs.get("is_ultra", False)) and cs["exp_avg_sq"].dtype == torch.bfloat16:
             chk.target(cs["exp_avg_sq"], mirror._gpu_state(gopt, e)["exp_avg_sq"], "v")
 
 
@@ -219,6 +225,9 @@ def _check_codes(chk, mirror, gopt):
     """8-bit SR codes of each mirrored tensor against the captured pre-rounding values."""
     for e, cp in zip(mirror.entries, mirror.cps):
         cs = mirror.copt.state[cp]
+        if cs.get("is_ultra", False):
+            chk.check_int8(mirror._gpu_state(gopt, e)["exp_avg"], what=f"{e} ultra int8")
+            continue
         if not cs.get("is_8bit", False):
             continue
         gs = mirror._gpu_state(gopt, e)

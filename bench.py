@@ -102,10 +102,10 @@ CONFIGS = {
     "c4": dict(workload="C4 compact ApexW step, 20k ragged bf16 tensors, clip 1.0", shapes=ragged_shapes(),
                dtype=torch.bfloat16, kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, clip_grad_norm=1.0),
                zero_frac=0.05, grad_reads=2),
-    # grad centralization folded into the clip and the step: the row means are one more
-    # grad read before them (3 grad reads; 1-D grads are read twice, counted as 3)
+    # grad centralization folded into the clip and the step: the row means of the dim >= 2
+    # grads are one more read of those grads before the clip and the step
     "c4gc": dict(workload="C4 compact ApexW step, 20k ragged bf16 tensors, clip 1.0, grad_centralization=True",
-                 shapes=ragged_shapes(), dtype=torch.bfloat16, grad_reads=3,
+                 shapes=ragged_shapes(), dtype=torch.bfloat16, grad_reads=2, row_mean_reads=1,
                  kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, clip_grad_norm=1.0,
                              grad_centralization=True), zero_frac=0.05),
     "c5": dict(workload="C5 hybrid Muon step (use_muon=True), one Llama-3-8B layer's matrices + 2 RMSNorm, bf16",
@@ -169,15 +169,18 @@ def copy_calibration():
     print(json.dumps({"copy_calibration": {"bytes_read": n * 4, "bytes_written": n * 4, "launches": 3}}), flush=True)
 
 
-def state_bytes(opt, params, grad_reads=1, grads=None):
+def state_bytes(opt, params, grad_reads=1, grads=None, row_mean_reads=0):
     """Algorithmic HBM bytes of one step: p read+write, g read (twice with a factored
     second moment: its row / column statistics must be complete before any update),
     every state tensor read+write.  grads: the step's grads when p.grad has been
-    released (the in-backward steps drop each grad once its batch is stepped)."""
+    released (the in-backward steps drop each grad once its batch is stepped).
+    row_mean_reads: extra reads of the dim >= 2 grads only (grad centralization's
+    row means)."""
     tot = 0
     for i, p in enumerate(params):
         g = p.grad if grads is None else grads[i]
-        tot += 2 * p.numel() * p.element_size() + grad_reads * g.numel() * g.element_size()
+        reads = grad_reads + (row_mean_reads if p.dim() >= 2 else 0)
+        tot += 2 * p.numel() * p.element_size() + reads * g.numel() * g.element_size()
         for k, v in opt.state[p].items():
             if torch.is_tensor(v) and k != "step" and v.device.type == "cuda":
                 tot += 2 * v.numel() * v.element_size()
@@ -406,7 +409,8 @@ def main():
         step()
     torch.cuda.synchronize()
     nbytes = 0 if cfg.get("mfma") else state_bytes(opt, params, cfg.get("grad_reads", 1),
-                                                    grads if cfg.get("backward") else None)
+                                                    grads if cfg.get("backward") else None,
+                                                    cfg.get("row_mean_reads", 0))
     stream = torch.cuda.current_stream(dev)
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()

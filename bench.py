@@ -88,6 +88,16 @@ CONFIGS = {
                   shapes=llama3_8b_shapes(), dtype=torch.bfloat16, grad_reads=2,
                   kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, precision="8bit", factored_v=True,
                               six_bit=True)),
+    # the other precision modes on the same shapes
+    "c3ultra": dict(workload="C3 shapes, ApexW precision='ultra' (INT8 m blocks, dense bf16 v), bf16, SR on",
+                    shapes=llama3_8b_shapes(), dtype=torch.bfloat16,
+                    kwargs=dict(lr=1e-3, weight_decay=0.1, precision="ultra")),
+    "c2full": dict(workload="C2 shapes, ApexW precision='full' (fp32 m and v), bf16, SR on",
+                   shapes=gpt2_small_shapes(), dtype=torch.bfloat16,
+                   kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, precision="full"), per_tensor_scale=True),
+    "c2auto": dict(workload="C2 shapes, ApexW precision='auto' (bf16 m/v for matrices, fp32 for vectors), bf16, SR on",
+                   shapes=gpt2_small_shapes(), dtype=torch.bfloat16,
+                   kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, precision="auto"), per_tensor_scale=True),
     # in-backward stepping: a step is opt.zero_grad(), a backward whose graph hands every
     # parameter its synthetic grad (p.view_as(p), no arithmetic), then opt.step(); with
     # hooks the 8-bit kernel runs per batch of 14 layers inside the backward

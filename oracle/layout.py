@@ -94,8 +94,6 @@ def init_state(p, group, n_params_in_group, peft_ctx, has_16bit_params=None, cud
     st = {"stochastic_rounding": sr, "step": torch.tensor(0.0, dtype=torch.float32)}
     n = p.numel()
     is_peft = is_peft_param(p) or peft_ctx
-    if has_16bit_params is None:
-        has_16bit_params = any(q.dtype in (torch.float16, torch.bfloat16) for q in group.get("params", ()))
     threshold = group.get("threshold", 65536)
     massive = p.dim() >= 2 or n >= threshold
     if group.get("fused") is True or prec == "full":
@@ -120,6 +118,8 @@ def init_state(p, group, n_params_in_group, peft_ctx, has_16bit_params=None, cud
         # optimizer.py:2694-2735: fp32 moments for pure-fp32 CUDA training, else 16-bit
         # for 2-D or large tensors and fp32 for small ones
         st.update(is_factored_v=False, is_6bit_m=False)
+        if has_16bit_params is None:
+            has_16bit_params = any(q.dtype in (torch.float16, torch.bfloat16) for q in group.get("params", ()))
         if cuda and p.dtype == torch.float32 and not amp_active(p, group, has_16bit_params, is_peft):
             return _dense(st, p, torch.float32, group, is_peft, n_params_in_group, prec)
         if not massive:

@@ -269,3 +269,14 @@ def test_other_precision_layouts_match_oracle(prec, dtype, kw):
                 assert torch.equal(a[k], b[k]), (k, p.shape)
             else:
                 assert a[k] == b[k], (k, p.shape, a[k], b[k])
+
+
+def test_integration_binding_loads():
+    """The binding module of INTEGRATION.md compiles, loads the library, agrees
+    with its ABI version and binds both of the reference's entry points."""
+    from integration_binding import load_binding
+    rx = load_binding()
+    assert callable(rx.step_fused) and callable(rx.step_fused_8bit)
+    assert ctypes.sizeof(rx.HParams) == 96 and ctypes.sizeof(rx.Tensor) == 64 and ctypes.sizeof(rx.Unit) == 8
+    p = torch.zeros(4)          # CPU tensors: not handled, nothing written
+    assert rx.step_fused([p], [p], [p], [p], 1e-3, 0.9, 0.999, 1e-8, 0.0) is False

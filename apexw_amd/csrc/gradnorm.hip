@@ -64,25 +64,29 @@ APEXW_DEV float unit_sumsq(const apexw_tensor& t, int64_t start, int64_t cnt, bo
   const int lane = lane_id();
   const bool vec = !(t.flags & APEXW_FLAG_SCALAR) && (start % 8) == 0;
   float acc = 0.0f;
-  if (vec && cnt == 2048) {
-    // a whole 2048-element unit: the wave's four 8-element loads per lane are issued together
+  const bool gc = t.flags & APEXW_FLAG_GC;
+  if (vec && cnt == 2048 && !gc) {
+    // a whole 2048-element unit: the wave's four 8-element loads per lane are issued
+    // together (centralized tensors take the loop below, in the same summation order,
+    // so that their row means do not hold registers here)
     float g[4][8];
+    const float none[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int k = 0; k < 4; ++k) load8<GD>(t.g, start + k * 512 + lane * 8, g[k]);
-    const bool gc = t.flags & APEXW_FLAG_GC;
-    float mean[4][8];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) clip_means8(t, start + k * 512 + lane * 8, mean[k]);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) acc = sumsq_vals<GD, 8>(g[k], false, unscale, inv, acc, gc, mean[k]);
+    for (int k = 0; k < 4; ++k) acc = sumsq_vals<GD, 8>(g[k], false, unscale, inv, acc, false, none);
     if (san && !(acc - acc == 0.0f)) {
+      // rare: a NaN / Inf grad in this lane's elements; read them again (the values need
+      // not stay in registers past the first pass) and form the sum with them sanitized
       acc = 0.0f;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) acc = sumsq_vals<GD, 8>(g[k], true, unscale, inv, acc, gc, mean[k]);
+      for (int k = 0; k < 4; ++k) {
+        float h[8];
+        load8<GD>(t.g, start + k * 512 + lane * 8, h);
+        acc = sumsq_vals<GD, 8>(h, true, unscale, inv, acc, false, none);
+      }
     }
     return wave_sum(acc);
   }
-  const bool gc = t.flags & APEXW_FLAG_GC;
   for (int pass = 0; pass < 2; ++pass) {
     const bool s = pass == 1;
     acc = 0.0f;

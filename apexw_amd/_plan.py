@@ -215,7 +215,9 @@ class StepPlan:
             self._build_prep()
         self._fast_static = None
         self.counts = counts
-        self.kind_code = (3 if self.single else 0) if self.kind == "compact" else 1
+        # the ultra precision's rows run on their own kernel (apexw_ultra_step)
+        self.ultra = self.kind == "q8" and self.precision == "ultra"
+        self.kind_code = (3 if self.single else 0) if self.kind == "compact" else (5 if self.ultra else 1)
         self._lib = L.load()
         self.clip_ws = None
         self.d_table = None
@@ -417,7 +419,7 @@ class StepPlan:
                 t = L.Tensor(*(int(row[k]) for k in ("p", "g", "m", "v", "m_scale", "v_scale", "n", "flags", "block")))
                 L.check(lib.apexw_check_tensor(ctypes_ref(t), 4 if self.factored[i] else self.kind_code),
                         f"tensor {i} ({tuple(self.params[i].shape)})")
-                if self.kind == "q8" and not self.single and not self.factored[i]:
+                if self.kind == "q8" and not self.single and not self.ultra and not self.factored[i]:
                     # full-block eligibility apart from alignment: same descriptor on aligned stand-in pointers
                     t.p = t.g = t.m = t.v = 256
                     t.flags = int(row["flags"]) & ~L.FLAG_SCALAR
@@ -560,6 +562,9 @@ class StepPlan:
             if self.kind == "compact":
                 st = self._lib.apexw_compact_step(self.d_table.data_ptr(), len(self.params), d_units.data_ptr(),
                                                   n_units, ctypes_ref(hp), stream)
+            elif self.ultra:
+                st = self._lib.apexw_ultra_step(self.d_table.data_ptr(), len(self.params), d_units.data_ptr(),
+                                                n_units, ctypes_ref(hp), stream)
             else:
                 st = self._lib.apexw_q8_step(self.d_table.data_ptr(), len(self.params), d_units.data_ptr(),
                                              n_units, n_fast, n_fast32, ctypes_ref(hp), stream)

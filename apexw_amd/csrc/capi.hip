@@ -15,6 +15,7 @@
 int apexw_launch_compact(const apexw_tensor*, int64_t, const apexw_unit*, const apexw_hparams*, hipStream_t);
 int apexw_launch_q8(const apexw_tensor*, int64_t, const apexw_unit*, const apexw_hparams*, hipStream_t);
 int apexw_launch_q8_fast(const apexw_tensor*, int64_t, const apexw_unit*, const apexw_hparams*, int32_t, hipStream_t);
+int apexw_launch_ultra(const apexw_tensor*, int64_t, const apexw_unit*, const apexw_hparams*, hipStream_t);
 bool apexw_q8_fast_eligible(uint32_t flags, uint32_t block);
 int apexw_launch_clip(const apexw_tensor*, int32_t, const apexw_unit*, int64_t, int64_t, const int64_t*, float*, float*,
                       float, float, uint32_t, float*, const apexw_amp_dyn*, hipStream_t);
@@ -135,8 +136,11 @@ int apexw_check_tensor(const apexw_tensor* t, int32_t kind) {
       if (t->block > 2048 || !t->m_scale) return APEXW_ERR_ARG;
       if ((f & APEXW_FLAG_M6) && (t->block % 4) != 0) return APEXW_ERR_ARG;
     }
-  } else if (kind == 1 || kind == 2) {
+  } else if (kind == 1 || kind == 2 || kind == 5) {
     if (!apexw_q8_flags_ok(t->flags, t->block, t->n)) return APEXW_ERR_DTYPE;
+    // kind 5: the ultra step's rows (INT8-m blocks or dense m / v); kind 1: never ultra rows
+    if (kind == 5 && !(t->flags & (APEXW_FLAG_ULTRA | APEXW_FLAG_DENSE))) return APEXW_ERR_ARG;
+    if (kind == 1 && (t->flags & APEXW_FLAG_ULTRA)) return APEXW_ERR_ARG;
     if (kind == 2 && !apexw_q8_fast_eligible(t->flags, t->block)) return APEXW_ERR_DTYPE;
     if (!(t->flags & APEXW_FLAG_DENSE) && !t->m_scale) return APEXW_ERR_ARG;
     if (!(t->flags & (APEXW_FLAG_DENSE | APEXW_FLAG_ULTRA)) && !t->v_scale) return APEXW_ERR_ARG;
@@ -155,6 +159,14 @@ int apexw_compact_step(const apexw_tensor* tensors, int32_t n_tensors, const ape
   if (!tensors || !units || n_tensors <= 0 || n_units < 0 || !hp_ok(hp)) return APEXW_ERR_ARG;
   if (n_units == 0) return APEXW_OK;
   return apexw_launch_compact(tensors, n_units, units, hp, (hipStream_t)stream);
+}
+
+int apexw_ultra_step(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,
+                     const apexw_hparams* hp, void* stream) {
+  if (!tensors || !units || n_tensors <= 0 || n_units < 0 || !hp_ok(hp)) return APEXW_ERR_ARG;
+  if (hp->mode == APEXW_MODE_NATIVE || hp->mode == APEXW_MODE_SINGLE) return APEXW_ERR_ARG;
+  if (n_units == 0) return APEXW_OK;
+  return apexw_launch_ultra(tensors, n_units, units, hp, (hipStream_t)stream);
 }
 
 int apexw_q8_step(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,

@@ -998,6 +998,178 @@ APEXW_DEV void ultra_block(const apexw_tensor& t, uint32_t tix, uint32_t blk, co
 }
 
 
+// Raw 16-byte loads of 8 consecutive elements of dtype DT (two for fp32), and
+// their values.
+template <int DT> struct Raw8 {
+  u32x4 w[DT == APEXW_F32 ? 2 : 1];
+};
+template <int DT> APEXW_DEV void raw_load8(const void* base, int64_t i, Raw8<DT>& r) {
+  if constexpr (DT == APEXW_F32) {
+    auto p = APEXW_GLOBAL(const u32x4, (const float*)base + i);
+    r.w[0] = __builtin_nontemporal_load(p);
+    r.w[1] = __builtin_nontemporal_load(p + 1);
+  } else {
+    r.w[0] = __builtin_nontemporal_load(APEXW_GLOBAL(const u32x4, (const uint16_t*)base + i));
+  }
+}
+template <int DT> APEXW_DEV void unpack8(const Raw8<DT>& r, float (&x)[8]) {
+#pragma unroll
+  for (int q = 0; q < (DT == APEXW_F32 ? 2 : 1); ++q) {
+    const uint32_t w[4] = {r.w[q].x, r.w[q].y, r.w[q].z, r.w[q].w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if constexpr (DT == APEXW_F32) {
+        x[4 * q + k] = __uint_as_float(w[k]);
+      } else {
+        x[2 * k] = bf16_bits_to_f32(w[k] & 0xFFFFu);
+        x[2 * k + 1] = __uint_as_float(w[k] & 0xFFFF0000u);
+      }
+    }
+  }
+}
+
+// A whole 2048-element "ultra" block (the arithmetic of ultra_block): the loads of
+// KB of the wave's four 8-element groups per lane are issued before their
+// arithmetic (all four for bf16 p and v, two at a time when p or v is fp32), so the
+// block waits on memory once or twice instead of four times.
+template <int PD, int VD>
+APEXW_DEV void ultra_block_full(const apexw_tensor& t, uint32_t tix, uint32_t blk, const Q8Ctx& c) {
+  constexpr int GD = PD;
+  constexpr int KB = (PD == APEXW_F32 || VD == APEXW_F32) ? 2 : 4;
+  const apexw_hparams& hp = *c.hp;
+  const bool sr = hp.flags & APEXW_HP_SR;
+  const bool wd = t.flags & APEXW_FLAG_WD;
+  const int64_t start = (int64_t)blk * 2048;
+  const int lane = lane_id();
+  const float ms_old = t.m_scale[blk];
+  const uint32_t key = rng_key(hp.seed, tix, hp.step, 1u, (uint32_t)(start >> 32));
+  float mnew[4][8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int k0 = 0; k0 < 4; k0 += KB) {
+    Raw8<PD> rp[KB];
+    Raw8<GD> rg[KB];
+    Raw8<VD> rv[KB];
+    u32x2 rm[KB];
+#pragma unroll
+    for (int b = 0; b < KB; ++b) {
+      const int64_t e0 = start + (int64_t)((k0 + b) * 64 + lane) * 8;
+      raw_load8<PD>(t.p, e0, rp[b]);
+      raw_load8<GD>(t.g, e0, rg[b]);
+      raw_load8<VD>(t.v, e0, rv[b]);
+      rm[b] = __builtin_nontemporal_load(APEXW_GLOBAL(const u32x2, (const int8_t*)t.m + e0));
+    }
+#pragma unroll
+    for (int b = 0; b < KB; ++b) {
+      const int k = k0 + b;
+      const int64_t e0 = start + (int64_t)(k * 64 + lane) * 8;
+      float p[8], g[8], v[8];
+      unpack8<PD>(rp[b], p);
+      unpack8<GD>(rg[b], g);
+      unpack8<VD>(rv[b], v);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t word = j < 4 ? rm[b].x : rm[b].y;
+        const float m = (float)(int8_t)((word >> (8 * (j & 3))) & 0xFFu) * ms_old;
+        g[j] = q8_grad<GD>(g[j], t.flags, c);
+        if (wd) p[j] = rnd<PD>(p[j] * hp.wd_factor);
+        mnew[k][j] = lerp_to(m, g[j], hp.lerp_coef, hp.flags & APEXW_HP_LERP_HI);
+        amax = fmaxf(amax, fabsf(mnew[k][j]));
+        const float vf = fmaf(hp.one_minus_beta2 * g[j], g[j], v[j] * hp.beta2);
+        v[j] = rnd<VD>(vf);
+        const float upd = (mnew[k][j] / (sqrtf(vf) + hp.eps_scaled)) * hp.step_size;
+        if constexpr (PD == APEXW_F32) p[j] = p[j] - upd;
+        else p[j] = rnd<PD>(p[j] - rnd<PD>(upd));
+      }
+      store8<PD>(t.p, e0, p);
+      store8<VD>(t.v, e0, v);
+    }
+  }
+  amax = wave_max(amax);
+  const float ms = fmaxf(fmaxf(amax, 1e-12f) / 127.0f, ms_old * 0.9f);
+  if (lane == 0) t.m_scale[blk] = ms;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int64_t e0 = start + (int64_t)(k * 64 + lane) * 8;
+    uint32_t mc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float y = mnew[k][j] / ms;
+      if (sr) y = y + (unit_uniform(rng_at(key, (uint32_t)(e0 + j)) >> 16) - 0.5f);
+      y = fminf(fmaxf(rintf(y), -127.0f), 127.0f);
+      mc[j] = (uint32_t)(int32_t)y & 0xFFu;
+    }
+    u32x2 w = {mc[0] | (mc[1] << 8) | (mc[2] << 16) | (mc[3] << 24),
+               mc[4] | (mc[5] << 8) | (mc[6] << 16) | (mc[7] << 24)};
+    __builtin_nontemporal_store(w, (u32x2*)((int8_t*)t.m + e0));
+  }
+}
+
+template <int PD, int VD>
+APEXW_DEV void ultra_unit(const apexw_tensor& t, uint32_t tix, uint32_t blk, const Q8Ctx& c) {
+  const bool whole = t.block == 2048 && (int64_t)(blk + 1) * 2048 <= t.n && !(t.flags & APEXW_FLAG_SCALAR);
+  if (whole) ultra_block_full<PD, VD>(t, tix, blk, c);
+  else ultra_block<PD, VD>(t, tix, blk, c);
+}
+
+// The "ultra" precision's step: its INT8-m blocks (APEXW_FLAG_ULTRA) and its small
+// tensors' dense fp32 m / v (APEXW_FLAG_DENSE), in a kernel of their own so that the
+// general 8-bit kernel's NF4 / log-uint8 code does not set its register count.
+// Rows of any other kind are not this kernel's (the host never lists them).
+__global__ __launch_bounds__(256) void ultra_step_kernel(const apexw_tensor* __restrict__ tensors,
+                                                         const apexw_unit* __restrict__ units, int64_t n_units,
+                                                         apexw_hparams hp_in) {
+  apexw_hparams hp = hp_in;
+  if (hp.flags & APEXW_HP_AMP) {
+    // GradScaler's step read on the device: skip it (found_inf) or take its scalars
+    const apexw_amp_dyn d = *hp.amp;
+    if (d.skip) return;
+    hp.step_size = d.step_size;
+    hp.eps_scaled = d.eps_scaled;
+    hp.bc2_sqrt = d.bc2_sqrt;
+    hp.grad_inv_scale = d.grad_inv_scale;
+  }
+  Q8Ctx c;
+  c.hp = &hp;
+  c.vlut = nullptr;
+  c.code = nullptr;
+  c.pair = nullptr;
+  c.frac16 = nullptr;
+  c.midtab = nullptr;
+  c.coef = (hp.flags & APEXW_HP_CLIP) ? *hp.clip_coef : 1.0f;
+  const uint32_t wave = uniform(threadIdx.x >> 6);
+  const int64_t stride = (int64_t)gridDim.x * kWaves;
+  for (int64_t u = (int64_t)blockIdx.x * kWaves + wave; u < n_units; u += stride) {
+    const apexw_unit un = units[u];
+    const apexw_tensor& t = tensors[un.tensor];
+    const uint32_t f = t.flags;
+    const uint32_t pd = (f >> APEXW_FLAG_PDT_SHIFT) & 3u;
+    const uint32_t md = (f >> APEXW_FLAG_MDT_SHIFT) & 3u;
+    const uint32_t vd = (f >> APEXW_FLAG_VDT_SHIFT) & 3u;
+    if (f & APEXW_FLAG_DENSE) {
+      if (md == APEXW_F32) {
+        if (pd == APEXW_F32) q8_dense<APEXW_F32, APEXW_F32, APEXW_F32, false>(t, un.unit, c);
+        else q8_dense<APEXW_BF16, APEXW_F32, APEXW_F32, false>(t, un.unit, c);
+      } else if (pd == APEXW_F32) {
+        if (vd == APEXW_F32) q8_dense<APEXW_F32, APEXW_BF16, APEXW_F32, false>(t, un.unit, c);
+        else q8_dense<APEXW_F32, APEXW_BF16, APEXW_BF16, false>(t, un.unit, c);
+      } else {
+        if (vd == APEXW_F32) q8_dense<APEXW_BF16, APEXW_BF16, APEXW_F32, false>(t, un.unit, c);
+        else q8_dense<APEXW_BF16, APEXW_BF16, APEXW_BF16, false>(t, un.unit, c);
+      }
+    } else if (f & APEXW_FLAG_ULTRA) {
+      if (pd == APEXW_F32) {
+        if (vd == APEXW_F32) ultra_unit<APEXW_F32, APEXW_F32>(t, un.tensor, un.unit, c);
+        else ultra_unit<APEXW_F32, APEXW_BF16>(t, un.tensor, un.unit, c);
+      } else {
+        if (vd == APEXW_F32) ultra_unit<APEXW_BF16, APEXW_F32>(t, un.tensor, un.unit, c);
+        else ultra_unit<APEXW_BF16, APEXW_BF16>(t, un.tensor, un.unit, c);
+      }
+    }
+  }
+}
+
+
 // Kernel for the units of fast-path tensors (see apexw_q8_fast_ok) with parameter
 // dtype PD; each dtype is its own kernel so the fp32 variant's larger register
 // footprint does not lower the bf16 kernel's occupancy.
@@ -1114,19 +1286,8 @@ __global__ __launch_bounds__(256) void q8_step_kernel(const apexw_tensor* __rest
       }
       continue;
     }
-    if (f & APEXW_FLAG_ULTRA) {
-      // the per-parameter update has no INT8-m form (refused on the host): never read v as codes
-      if constexpr (!SINGLE) {
-        if (pd == APEXW_F32) {
-          if (vd == APEXW_F32) ultra_block<APEXW_F32, APEXW_F32>(t, un.tensor, un.unit, c);
-          else ultra_block<APEXW_F32, APEXW_BF16>(t, un.tensor, un.unit, c);
-        } else {
-          if (vd == APEXW_F32) ultra_block<APEXW_BF16, APEXW_F32>(t, un.tensor, un.unit, c);
-          else ultra_block<APEXW_BF16, APEXW_BF16>(t, un.tensor, un.unit, c);
-        }
-      }
-      continue;
-    }
+    // ultra rows belong to ultra_step_kernel (apexw_ultra_step): never read their dense v as codes
+    if (f & APEXW_FLAG_ULTRA) continue;
     const bool nf4 = f & APEXW_FLAG_NF4, quad = f & APEXW_FLAG_QUAD;
     if (pd == APEXW_F32) {
       if (nf4 && quad) q8_block<APEXW_F32, true, true, SINGLE>(t, un.tensor, un.unit, c);
@@ -1176,6 +1337,13 @@ int apexw_launch_q8(const apexw_tensor* tensors, int64_t n_units, const apexw_un
     const int grid = apexw_resident_grid((const void*)q8_step_kernel<false>, n_units);
     hipLaunchKernelGGL(q8_step_kernel<false>, dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
   }
+  return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
+}
+
+int apexw_launch_ultra(const apexw_tensor* tensors, int64_t n_units, const apexw_unit* units,
+                       const apexw_hparams* hp, hipStream_t stream) {
+  const int grid = apexw_resident_grid((const void*)ultra_step_kernel, n_units);
+  hipLaunchKernelGGL(ultra_step_kernel, dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }
 

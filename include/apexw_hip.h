@@ -44,7 +44,7 @@
 extern "C" {
 #endif
 
-#define APEXW_ABI_VERSION 15
+#define APEXW_ABI_VERSION 16
 
 /* status codes */
 enum apexw_status {
@@ -208,7 +208,8 @@ int apexw_abi_version(void);
  * device table: kind 0 = compact step, 1 = 8-bit step, 2 = 8-bit step on the
  * full-block kernel (bf16 or fp32 params, NF4 m, quad v, 2048-element blocks),
  * 3 = compact step in APEXW_MODE_SINGLE (full-size v only), 4 = factored
- * tensor (APEXW_FLAG_FACTORED row of either table).  Checks the dtype
+ * tensor (APEXW_FLAG_FACTORED row of either table), 5 = row of the ultra step
+ * (APEXW_FLAG_ULTRA or APEXW_FLAG_DENSE; kind 1 refuses ultra rows).  Checks the dtype
  * combination, block size and the 16-byte alignment the vector path needs
  * (unless APEXW_FLAG_SCALAR is set).  Mirrors the per-call tensor checks of the
  * reference's pybind glue (apexw/csrc/apexw_cuda.cpp:109-180, :310-380), done
@@ -223,6 +224,18 @@ int apexw_check_tensor(const apexw_tensor* t, int32_t kind);
 int apexw_compact_step(const apexw_tensor* tensors, int32_t n_tensors,
                        const apexw_unit* units, int64_t n_units,
                        const apexw_hparams* hp, void* stream);
+
+/*
+ * The "ultra" precision's step (ApexW._step_ultra, apexw/optimizer.py:4640-4686
+ * for its INT8-m tensors, :4688-4735 for its small fp32-moment tensors): units of
+ * rows flagged APEXW_FLAG_ULTRA (one INT8-m block each; dense v, no v scales)
+ * or APEXW_FLAG_DENSE (2048 elements each), validated with apexw_check_tensor
+ * kind 5.  Cold and replay modes round alike here (the reference's replay calls
+ * the same function).  Replaces the general 8-bit launch for these rows, whose
+ * kernel would hold them at a lower occupancy.
+ */
+int apexw_ultra_step(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,
+                     const apexw_hparams* hp, void* stream);
 
 /*
  * 8-bit fused step: dequantize m (NF4 or INT8) and v (log-uint8) with their

@@ -13,7 +13,7 @@ import numpy as np
 
 from ._build import LIB_PATH
 
-ABI_VERSION = 16
+ABI_VERSION = 17
 
 # dtype codes
 F32, BF16, F16, U8, I8 = 0, 1, 2, 3, 4
@@ -30,6 +30,7 @@ FLAG_FACTORED = 1 << 14
 FLAG_M6 = 1 << 15
 FLAG_GC = 1 << 16
 FLAG_ULTRA = 1 << 17
+FLAG_VSCALE = 1 << 18
 
 COMPACT_UNIT = 2048
 

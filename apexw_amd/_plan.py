@@ -141,6 +141,9 @@ class StepPlan:
             f |= (_DT[m.dtype] << L.MDT_SHIFT) | (_DT[v.dtype] << L.VDT_SHIFT)
             if v.numel() * 4 == p.numel() and p.numel() % 4 == 0:
                 f |= L.FLAG_QUAD
+            if torch.float16 in (m.dtype, v.dtype) and not self.native and not self.single:
+                # the dynamic v scale of fp16 subgroups (set per launch, see _update_vscales)
+                f |= L.FLAG_VSCALE
             block = 0
         elif st.get("is_ultra", False):
             # precision "ultra": INT8 m blocks, dense v, the per-parameter rounding order
@@ -196,6 +199,16 @@ class StepPlan:
                 counts[i] = (p.numel() + block - 1) // block
         self.host_table = tab          # parameter order
         self.factored = (tab["flags"] & np.uint32(L.FLAG_FACTORED)) != 0
+        # per tensor {scale_v, sqrt(scale_v)} of this launch, for rows flagged APEXW_FLAG_VSCALE
+        self.vscaled = (tab["flags"] & np.uint32(L.FLAG_VSCALE)) != 0
+        self.d_vscale = self.h_vscale = None
+        if self.vscaled.any():
+            self.d_vscale = torch.ones((n, 2), dtype=torch.float32, device=self.device)
+            self.h_vscale = np.ones((n, 2), dtype=np.float32)
+            base = self.d_vscale.data_ptr()
+            tab["v_scale"] = np.where(self.vscaled, np.arange(n, dtype=np.uint64) * np.uint64(8) + np.uint64(base),
+                                      tab["v_scale"])
+        self._sg_scale = {}
         self.fv = None
         self._fv_subsets = {}
         self.p_ptrs = np.zeros(n, dtype=np.uint64)
@@ -450,7 +463,7 @@ class StepPlan:
         """Whether GradScaler's scale and found_inf can be read on the device for this
         plan (the compact and 8-bit step kernels; not the factored ones or the
         in-backward batches)."""
-        return not (self.hooked or self.single or self.factored.any())
+        return not (self.hooked or self.single or self.factored.any() or self.vscaled.any())
 
     def amp_fold(self, sync=False):
         """Subtract from the step counters the steps GradScaler skipped that the host
@@ -488,6 +501,77 @@ class StepPlan:
         self.amp_dirty = True
         return self._amp_dyn.data_ptr()
 
+    # ------------------------------------------------------------------ fp16 v scales
+    def _subgroups(self, key_fn):
+        """The plan's non-factored tensors grouped by key_fn(i), in parameter order."""
+        out = {}
+        for i in range(len(self.params)):
+            if not self.factored[i]:
+                out.setdefault(key_fn(i), []).append(i)
+        return out
+
+    def _rescale_v(self, idx, cur_scale):
+        """Every-100-steps recalibration of a subgroup's v (optimizer.py:5622-5645,
+        :1165-1178): read max(v) on the host, as the reference does, and scale v
+        by 4 or 1/4 in place.  Returns the factor."""
+        vs = [self.states[i]["exp_avg_sq"] for i in idx]
+        v_max = float(torch.stack([v.max().float() for v in vs]).max().item())
+        factor = 1.0
+        if v_max < 0.25 and cur_scale < 65536.0:
+            factor = 4.0
+        elif v_max > 16384.0 and cur_scale > 1.0:
+            factor = 0.25
+        if factor != 1.0:
+            torch._foreach_mul_(vs, factor)
+        return factor
+
+    def _update_vscales(self, group, cold):
+        """Each tensor's v scale for this launch, as the reference picks it.
+
+        Cold step (_multi_tensor_step, optimizer.py:5600-5645): per subgroup of
+        (p dtype, m dtype, step count, quad), the first parameter's state scale when
+        m is fp16, recalibrated on every 100th step and written to every state of the
+        subgroup.  Replay (execute_foreach, :1165-1199): per subgroup of (p dtype,
+        16-bit m, quad), fp16 v is recalibrated every 100 steps with the subgroup's
+        remembered scale, and the step takes the first parameter's state scale,
+        which the replay itself never changes."""
+        dyn = bool(group.get("dynamic_scaling", True))
+        st, steps = self.states, self._steps_np
+        h = np.ones_like(self.h_vscale)
+        quad = (self.host_table["flags"] & np.uint32(L.FLAG_QUAD)) != 0
+        if cold:
+            subs = self._subgroups(lambda i: (self.params[i].dtype, st[i]["exp_avg"].dtype, int(steps[i]),
+                                              bool(quad[i])))
+            for (_, mdt, step, _), idx in subs.items():
+                if not (dyn and mdt == torch.float16):
+                    continue
+                scale = float(st[idx[0]]["scale_v"])
+                sqrt_scale = float(st[idx[0]].get("sqrt_scale_v", math.sqrt(scale)))
+                if step > 1 and step % 100 == 0:
+                    f = self._rescale_v(idx, scale)
+                    if f != 1.0:
+                        scale *= f
+                        sqrt_scale = math.sqrt(scale)
+                        for i in idx:
+                            st[i]["scale_v"], st[i]["sqrt_scale_v"] = scale, sqrt_scale
+                h[idx] = (scale, sqrt_scale)
+        else:
+            subs = self._subgroups(lambda i: (self.params[i].dtype, st[i]["exp_avg"].dtype != torch.float32,
+                                              bool(quad[i])))
+            step = int(steps[0])
+            if dyn and step > 1 and step % 100 == 0:
+                for key, idx in subs.items():
+                    if st[idx[0]]["exp_avg_sq"].dtype == torch.float16:
+                        self._rescale_v(idx, self._sg_scale.get(key, 1.0))
+            for key, idx in subs.items():
+                scale = float(st[idx[0]].get("scale_v", self._sg_scale.get(key, 1.0)))
+                sqrt_scale = float(st[idx[0]].get("sqrt_scale_v", math.sqrt(scale)))
+                self._sg_scale[key] = scale
+                h[idx] = (scale, sqrt_scale)
+        if not np.array_equal(h, self.h_vscale):
+            self.h_vscale = h
+            self.d_vscale.copy_(torch.from_numpy(h).pin_memory(), non_blocking=True)
+
     def execute(self, group, seed, inv_scale=None, lr=None, wd=None, steps=None, amp=None):
         """Run one optimizer step for the group (cold the first time, replay after).
 
@@ -521,6 +605,8 @@ class StepPlan:
             self._steps_np += 1.0
         else:
             self._steps_np[:] = np.asarray(steps, dtype=np.float32)
+        if self.h_vscale is not None:
+            self._update_vscales(group, mode_cold)
         # The reference's replayed compact step takes the bias correction of the
         # first counter for the whole group (optimizer.py:1082-1090); every other
         # path uses each parameter's own count.  SR: the 8-bit step and the
@@ -683,6 +769,7 @@ class StepPlan:
             hp.wd_factor = 1.0 - lr * wd
             hp.step_size = lr * bc2s / bc1
             hp.eps_scaled = eps * bc2s
+            hp.eps = eps                   # the replay's denominator floor with fp16 in the subgroup
             hp.mode = L.MODE_COLD if cold else L.MODE_REPLAY
             if sr:
                 flags |= L.HP_SR

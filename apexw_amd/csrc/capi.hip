@@ -124,6 +124,7 @@ int apexw_check_tensor(const apexw_tensor* t, int32_t kind) {
     if (!apexw_compact_flags_ok(t->flags)) return APEXW_ERR_DTYPE;
     if ((t->flags & APEXW_FLAG_QUAD) && (kind == 3 || (t->n % 4) != 0)) return APEXW_ERR_ARG;
     if ((t->flags & APEXW_FLAG_GC) && (!t->m_scale || t->block == 0 || (t->n % t->block) != 0)) return APEXW_ERR_ARG;
+    if ((t->flags & APEXW_FLAG_VSCALE) && (!t->v_scale || ((uintptr_t)t->v_scale & 7u))) return APEXW_ERR_ARG;
   } else if (kind == 4) {
     // factored row: v / v_scale are the fp32 row / column EMAs
     const uint32_t f = t->flags;

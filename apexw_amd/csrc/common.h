@@ -55,6 +55,9 @@ template <int DT> APEXW_DEV float rnd(float x) {
   else return x;
 }
 
+// torch's clamp to the fp16 range, which keeps NaN (fminf / fmaxf alone would not)
+APEXW_DEV float clamp_f16_range(float x) { return x == x ? fminf(fmaxf(x, -65504.0f), 65504.0f) : x; }
+
 // Stochastic rounding of fp32 to bf16 / fp16: add uniform random low bits to the
 // fp32 bit pattern and truncate (the published "add noise then truncate" SR).
 // r is 16 random bits for bf16 and 13 for fp16.  Returns the rounded value as fp32.
@@ -63,10 +66,10 @@ template <int DT> APEXW_DEV float sr_round(float x, uint32_t r) {
     uint32_t u = __float_as_uint(x) + (r & 0xFFFFu);
     return __uint_as_float(u & 0xFFFF0000u);
   } else if constexpr (DT == APEXW_F16) {
-    x = fminf(fmaxf(x, -65504.0f), 65504.0f);
+    x = clamp_f16_range(x);
     uint32_t u = __float_as_uint(x) + (r & 0x1FFFu);
     float y = __uint_as_float(u & 0xFFFFE000u);
-    y = fminf(fmaxf(y, -65504.0f), 65504.0f);
+    y = clamp_f16_range(y);
     return rnd<APEXW_F16>(y);
   } else {
     return x;

@@ -26,7 +26,15 @@ struct Ctx {
   float coef;
   uint32_t key;
   uint32_t tflags;
+  float vscale, vscale_sqrt;   // the tensor's dynamic fp16-v scale (APEXW_FLAG_VSCALE), else 1
 };
+
+// A 16-bit parameter stored through the reference's fp32 -> 16-bit copy
+// (_copy_fp32_to_16bit_sr_ without SR): fp16 is clamped to its range first.
+template <int PD> APEXW_DEV float store_p(float x) {
+  if constexpr (PD == APEXW_F16) return rnd<PD>(clamp_f16_range(x));
+  else return rnd<PD>(x);
+}
 
 // sanitize (san), AMP unscale (in place on the grads: _multi_tensor_step,
 // apexw/optimizer.py:5530-5537, or _prepare_grads before a clip), grad
@@ -155,7 +163,18 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
   // round the scalar to the tensor dtype first on torch's CPU path, so the
   // 16-bit tensors see bf16(beta1), bf16(beta2), bf16(1 - lr*wd), bf16(eps).
   const float wd_p = rnd<PD>(hp.wd_factor), b1_m = rnd<MD>(hp.beta1), b2_v = rnd<VD>(hp.beta2);
-  const float eps_v = rnd<VD>(hp.eps_scaled);
+  // a dynamically scaled v (fp16): the EMA adds (1 - beta2) * scale * g^2 (the scale is
+  // a power of two, so the product is exact) and the denominator is
+  // (sqrt(v) + eps_scaled * sqrt(scale)) / sqrt(scale) (apexw/optimizer.py:5691-5721,
+  // :5799-5816); the replay with fp16 in the subgroup clamps it below by eps (:1264-1265,
+  // :1310-1311)
+  const bool scaled = c.vscale != 1.0f;
+  const float omb2 = hp.one_minus_beta2 * c.vscale;
+  const float eps_v = rnd<VD>(scaled ? hp.eps_scaled * c.vscale_sqrt : hp.eps_scaled);
+  const float sqrt_scale_v = rnd<VD>(c.vscale_sqrt);
+  constexpr bool kFp16 = PD == APEXW_F16 || MD == APEXW_F16 || VD == APEXW_F16;
+  const bool clamp_den = kFp16 && hp.mode == APEXW_MODE_REPLAY;
+  const float eps_floor = rnd<VD>(hp.eps);
   if (wd) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) p[j] = rnd<PD>(p[j] * wd_p);
@@ -191,20 +210,22 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
       const float gq = s * 0.25f;
       float vq;
       if (srv) {
-        vq = sr_round<VD>(fmaf(hp.one_minus_beta2, gq, v[q] * hp.beta2), rnd_bits[b] >> 16);
+        vq = sr_round<VD>(fmaf(omb2, gq, v[q] * hp.beta2), rnd_bits[b] >> 16);
       } else {
         float v1 = rnd<VD>(v[q] * b2_v);
-        vq = rnd<VD>(fmaf(hp.one_minus_beta2, gq, v1));
+        vq = rnd<VD>(fmaf(omb2, gq, v1));
       }
       v[q] = vq;
       float den = rnd<VD>(q_sqrt<SR>(vq));
       den = rnd<VD>(den + eps_v);
+      if (scaled) den = rnd<VD>(den / sqrt_scale_v);
+      if (clamp_den) den = fmaxf(den, eps_floor);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int j = b + i;
         const float delta = q_div<SR>(m[j], den) * hp.step_size;
         const float x = p[j] - delta;
-        p[j] = !p16 ? x : (sr ? sr_round<PD>(x, rnd_bits[j]) : rnd<PD>(x));
+        p[j] = !p16 ? x : (sr ? sr_round<PD>(x, rnd_bits[j]) : store_p<PD>(x));
       }
     }
   } else {
@@ -212,20 +233,22 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
     for (int j = 0; j < 8; ++j) {
       float vf;
       if (srv) {
-        vf = sr_round<VD>(fmaf(hp.one_minus_beta2 * g[j], g[j], v[j] * hp.beta2), rnd_bits[j] >> 16);
+        vf = sr_round<VD>(fmaf(omb2 * g[j], g[j], v[j] * hp.beta2), rnd_bits[j] >> 16);
       } else {
         float v1 = rnd<VD>(v[j] * b2_v);
-        vf = rnd<VD>(fmaf(hp.one_minus_beta2 * g[j], g[j], v1));
+        vf = rnd<VD>(fmaf(omb2 * g[j], g[j], v1));
       }
       v[j] = vf;
       float den = rnd<VD>(q_sqrt<SR>(vf));
       den = rnd<VD>(den + eps_v);
+      if (scaled) den = rnd<VD>(den / sqrt_scale_v);
+      if (clamp_den) den = fmaxf(den, eps_floor);
       if (!p16) {
         p[j] = p[j] + q_div<SR>(-hp.step_size * m[j], den);
       } else if (sr) {
         p[j] = sr_round<PD>(p[j] - q_div<SR>(m[j], den) * hp.step_size, rnd_bits[j]);
       } else if (hp.mode == APEXW_MODE_REPLAY) {
-        p[j] = rnd<PD>(p[j] - (m[j] / den) * hp.step_size);
+        p[j] = store_p<PD>(p[j] - (m[j] / den) * hp.step_size);
       } else {
         p[j] = rnd<PD>(p[j] + (-hp.step_size * m[j]) / den);
       }
@@ -280,7 +303,12 @@ APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const 
     const bool gc = c.tflags & APEXW_FLAG_GC;
     float mean[8];
     if (gc) row_means8(t, e0, mean);
-    update8<PD, GD, MD, VD, QUAD, SR>(p, g, m, v, cnt, (uint32_t)e0, c, gc, mean);
+    Ctx cs = c;
+    if (c.tflags & APEXW_FLAG_VSCALE) {
+      cs.vscale = t.v_scale[0];
+      cs.vscale_sqrt = t.v_scale[1];
+    }
+    update8<PD, GD, MD, VD, QUAD, SR>(p, g, m, v, cnt, (uint32_t)e0, cs, gc, mean);
     if (full) {
       store8<PD>(t.p, e0, p);
       store8<MD>(t.m, e0, m);
@@ -319,7 +347,15 @@ APEXW_DEV void dispatch_group(const apexw_tensor& t, int64_t start, int k, const
   if (md == APEXW_F32) {
     // fp32 moments ("full" precision, small "auto" tensors): fp32 v, no quad (checked on the host)
     if (pd == APEXW_F32) compact_group<APEXW_F32, APEXW_F32, APEXW_F32, false, SR>(t, start, k, c);
-    else compact_group<APEXW_BF16, APEXW_F32, APEXW_F32, false, SR>(t, start, k, c);
+    else if (pd == APEXW_BF16) compact_group<APEXW_BF16, APEXW_F32, APEXW_F32, false, SR>(t, start, k, c);
+    else compact_group<APEXW_F16, APEXW_F32, APEXW_F32, false, SR>(t, start, k, c);
+    return;
+  }
+  if (pd == APEXW_F16) {
+    // fp16 parameters keep fp16 m (and fp16 or fp32 v)
+    if (vd == APEXW_F32) compact_group<APEXW_F16, APEXW_F16, APEXW_F32, false, SR>(t, start, k, c);
+    else if (quad) compact_group<APEXW_F16, APEXW_F16, APEXW_F16, true, SR>(t, start, k, c);
+    else compact_group<APEXW_F16, APEXW_F16, APEXW_F16, false, SR>(t, start, k, c);
     return;
   }
   if (pd == APEXW_F32) {
@@ -350,6 +386,8 @@ __global__ __launch_bounds__(256) void compact_step_kernel(const apexw_tensor* _
   Ctx c;
   c.hp = &hp;
   c.coef = (hp.flags & APEXW_HP_CLIP) ? *hp.clip_coef : 1.0f;
+  c.vscale = 1.0f;
+  c.vscale_sqrt = 1.0f;
   // SR applies to the 16-bit stores of the cold and replayed steps (the native and
   // per-parameter modes never set it)
   const bool sr = (hp.flags & APEXW_HP_SR) && (hp.mode == APEXW_MODE_COLD || hp.mode == APEXW_MODE_REPLAY);
@@ -381,10 +419,12 @@ __global__ __launch_bounds__(256) void compact_step_kernel(const apexw_tensor* _
 static bool compact_combo_ok(uint32_t flags) {
   const uint32_t pd = (flags >> APEXW_FLAG_PDT_SHIFT) & 3u, gd = (flags >> APEXW_FLAG_GDT_SHIFT) & 3u;
   const uint32_t md = (flags >> APEXW_FLAG_MDT_SHIFT) & 3u, vd = (flags >> APEXW_FLAG_VDT_SHIFT) & 3u;
-  if (!(pd == APEXW_F32 || pd == APEXW_BF16) || gd != pd) return false;
+  if (!(pd == APEXW_F32 || pd == APEXW_BF16 || pd == APEXW_F16) || gd != pd) return false;
   if (md == APEXW_F32) return vd == APEXW_F32 && !(flags & APEXW_FLAG_QUAD);   // fp32 moments
-  if (md != APEXW_BF16 || !(vd == APEXW_F32 || vd == APEXW_BF16)) return false;
-  if ((flags & APEXW_FLAG_QUAD) && vd != APEXW_BF16) return false;
+  // 16-bit moments are in the parameter's compact dtype: fp16 for fp16, else bf16
+  const uint32_t cd = pd == APEXW_F16 ? APEXW_F16 : APEXW_BF16;
+  if (md != cd || !(vd == APEXW_F32 || vd == cd)) return false;
+  if ((flags & APEXW_FLAG_QUAD) && vd != cd) return false;
   return true;
 }
 

@@ -139,7 +139,10 @@ APEXW_DEV float q8_param(float p, float upd, float decay, uint32_t tflags, bool 
   if (wd) p = p * decay;
   if constexpr (PD == APEXW_F32) return p - upd;
   const float x = p - upd;
-  return sr ? sr_round<PD>(x, r) : rnd<PD>(x);
+  if (sr) return sr_round<PD>(x, r);
+  // the fp32 -> 16-bit copy (_copy_fp32_to_16bit_sr_) clamps fp16 to its range
+  if constexpr (PD == APEXW_F16) return rnd<PD>(clamp_f16_range(x));
+  return rnd<PD>(x);
 }
 
 // One quantization block per wavefront, any layout (INT8 m, fp32 params, other
@@ -1020,9 +1023,12 @@ template <int DT> APEXW_DEV void unpack8(const Raw8<DT>& r, float (&x)[8]) {
     for (int k = 0; k < 4; ++k) {
       if constexpr (DT == APEXW_F32) {
         x[4 * q + k] = __uint_as_float(w[k]);
-      } else {
+      } else if constexpr (DT == APEXW_BF16) {
         x[2 * k] = bf16_bits_to_f32(w[k] & 0xFFFFu);
         x[2 * k + 1] = __uint_as_float(w[k] & 0xFFFF0000u);
+      } else {
+        x[2 * k] = f16_bits_to_f32(w[k] & 0xFFFFu);
+        x[2 * k + 1] = f16_bits_to_f32(w[k] >> 16);
       }
     }
   }
@@ -1112,6 +1118,28 @@ APEXW_DEV void ultra_unit(const apexw_tensor& t, uint32_t tix, uint32_t blk, con
   else ultra_block<PD, VD>(t, tix, blk, c);
 }
 
+// Dense m / v rows by dtype: m in the parameter's compact dtype (bf16; fp16 for fp16
+// parameters) with v in it or fp32, or fp32 m and v.
+template <bool SINGLE>
+APEXW_DEV void dense_dispatch(const apexw_tensor& t, uint32_t unit, const Q8Ctx& c, uint32_t pd, uint32_t md,
+                              uint32_t vd) {
+  if (md == APEXW_F32) {
+    // fp32 m implies fp32 v (checked on the host)
+    if (pd == APEXW_F32) q8_dense<APEXW_F32, APEXW_F32, APEXW_F32, SINGLE>(t, unit, c);
+    else if (pd == APEXW_BF16) q8_dense<APEXW_BF16, APEXW_F32, APEXW_F32, SINGLE>(t, unit, c);
+    else q8_dense<APEXW_F16, APEXW_F32, APEXW_F32, SINGLE>(t, unit, c);
+  } else if (pd == APEXW_F32) {
+    if (vd == APEXW_F32) q8_dense<APEXW_F32, APEXW_BF16, APEXW_F32, SINGLE>(t, unit, c);
+    else q8_dense<APEXW_F32, APEXW_BF16, APEXW_BF16, SINGLE>(t, unit, c);
+  } else if (pd == APEXW_BF16) {
+    if (vd == APEXW_F32) q8_dense<APEXW_BF16, APEXW_BF16, APEXW_F32, SINGLE>(t, unit, c);
+    else q8_dense<APEXW_BF16, APEXW_BF16, APEXW_BF16, SINGLE>(t, unit, c);
+  } else {
+    if (vd == APEXW_F32) q8_dense<APEXW_F16, APEXW_F16, APEXW_F32, SINGLE>(t, unit, c);
+    else q8_dense<APEXW_F16, APEXW_F16, APEXW_F16, SINGLE>(t, unit, c);
+  }
+}
+
 // The "ultra" precision's step: its INT8-m blocks (APEXW_FLAG_ULTRA) and its small
 // tensors' dense fp32 m / v (APEXW_FLAG_DENSE), in a kernel of their own so that the
 // general 8-bit kernel's NF4 / log-uint8 code does not set its register count.
@@ -1147,23 +1175,18 @@ __global__ __launch_bounds__(256) void ultra_step_kernel(const apexw_tensor* __r
     const uint32_t md = (f >> APEXW_FLAG_MDT_SHIFT) & 3u;
     const uint32_t vd = (f >> APEXW_FLAG_VDT_SHIFT) & 3u;
     if (f & APEXW_FLAG_DENSE) {
-      if (md == APEXW_F32) {
-        if (pd == APEXW_F32) q8_dense<APEXW_F32, APEXW_F32, APEXW_F32, false>(t, un.unit, c);
-        else q8_dense<APEXW_BF16, APEXW_F32, APEXW_F32, false>(t, un.unit, c);
-      } else if (pd == APEXW_F32) {
-        if (vd == APEXW_F32) q8_dense<APEXW_F32, APEXW_BF16, APEXW_F32, false>(t, un.unit, c);
-        else q8_dense<APEXW_F32, APEXW_BF16, APEXW_BF16, false>(t, un.unit, c);
-      } else {
-        if (vd == APEXW_F32) q8_dense<APEXW_BF16, APEXW_BF16, APEXW_F32, false>(t, un.unit, c);
-        else q8_dense<APEXW_BF16, APEXW_BF16, APEXW_BF16, false>(t, un.unit, c);
-      }
+      dense_dispatch<false>(t, un.unit, c, pd, md, vd);
     } else if (f & APEXW_FLAG_ULTRA) {
+      // v in the parameter's compact dtype (fp16 for fp16 parameters, else bf16) or fp32
       if (pd == APEXW_F32) {
         if (vd == APEXW_F32) ultra_unit<APEXW_F32, APEXW_F32>(t, un.tensor, un.unit, c);
         else ultra_unit<APEXW_F32, APEXW_BF16>(t, un.tensor, un.unit, c);
-      } else {
+      } else if (pd == APEXW_BF16) {
         if (vd == APEXW_F32) ultra_unit<APEXW_BF16, APEXW_F32>(t, un.tensor, un.unit, c);
         else ultra_unit<APEXW_BF16, APEXW_BF16>(t, un.tensor, un.unit, c);
+      } else {
+        if (vd == APEXW_F32) ultra_unit<APEXW_F16, APEXW_F32>(t, un.tensor, un.unit, c);
+        else ultra_unit<APEXW_F16, APEXW_F16>(t, un.tensor, un.unit, c);
       }
     }
   }
@@ -1272,18 +1295,7 @@ __global__ __launch_bounds__(256) void q8_step_kernel(const apexw_tensor* __rest
     if (f & APEXW_FLAG_FACTORED) continue;  // stepped by apexw_factored_step
     const uint32_t vd = (f >> APEXW_FLAG_VDT_SHIFT) & 3u;
     if (f & APEXW_FLAG_DENSE) {
-      const uint32_t md = (f >> APEXW_FLAG_MDT_SHIFT) & 3u;
-      if (md == APEXW_F32) {
-        // fp32 m implies fp32 v (checked on the host)
-        if (pd == APEXW_F32) q8_dense<APEXW_F32, APEXW_F32, APEXW_F32, SINGLE>(t, un.unit, c);
-        else q8_dense<APEXW_BF16, APEXW_F32, APEXW_F32, SINGLE>(t, un.unit, c);
-      } else if (pd == APEXW_F32) {
-        if (vd == APEXW_F32) q8_dense<APEXW_F32, APEXW_BF16, APEXW_F32, SINGLE>(t, un.unit, c);
-        else q8_dense<APEXW_F32, APEXW_BF16, APEXW_BF16, SINGLE>(t, un.unit, c);
-      } else {
-        if (vd == APEXW_F32) q8_dense<APEXW_BF16, APEXW_BF16, APEXW_F32, SINGLE>(t, un.unit, c);
-        else q8_dense<APEXW_BF16, APEXW_BF16, APEXW_BF16, SINGLE>(t, un.unit, c);
-      }
+      dense_dispatch<SINGLE>(t, un.unit, c, pd, (f >> APEXW_FLAG_MDT_SHIFT) & 3u, vd);
       continue;
     }
     // ultra rows belong to ultra_step_kernel (apexw_ultra_step): never read their dense v as codes
@@ -1293,10 +1305,14 @@ __global__ __launch_bounds__(256) void q8_step_kernel(const apexw_tensor* __rest
       if (nf4 && quad) q8_block<APEXW_F32, true, true, SINGLE>(t, un.tensor, un.unit, c);
       else if (nf4) q8_block<APEXW_F32, true, false, SINGLE>(t, un.tensor, un.unit, c);
       else q8_block<APEXW_F32, false, false, SINGLE>(t, un.tensor, un.unit, c);
-    } else {
+    } else if (pd == APEXW_BF16) {
       if (nf4 && quad) q8_block<APEXW_BF16, true, true, SINGLE>(t, un.tensor, un.unit, c);
       else if (nf4) q8_block<APEXW_BF16, true, false, SINGLE>(t, un.tensor, un.unit, c);
       else q8_block<APEXW_BF16, false, false, SINGLE>(t, un.tensor, un.unit, c);
+    } else {
+      if (nf4 && quad) q8_block<APEXW_F16, true, true, SINGLE>(t, un.tensor, un.unit, c);
+      else if (nf4) q8_block<APEXW_F16, true, false, SINGLE>(t, un.tensor, un.unit, c);
+      else q8_block<APEXW_F16, false, false, SINGLE>(t, un.tensor, un.unit, c);
     }
   }
 }
@@ -1307,19 +1323,20 @@ bool apexw_q8_fast_eligible(uint32_t flags, uint32_t block) { return apexw_q8_fa
 
 bool apexw_q8_flags_ok(uint32_t flags, uint32_t block, int64_t n) {
   const uint32_t pd = (flags >> APEXW_FLAG_PDT_SHIFT) & 3u, gd = (flags >> APEXW_FLAG_GDT_SHIFT) & 3u;
-  if (!(pd == APEXW_F32 || pd == APEXW_BF16) || gd != pd) return false;
+  if (!(pd == APEXW_F32 || pd == APEXW_BF16 || pd == APEXW_F16) || gd != pd) return false;
   const uint32_t md = (flags >> APEXW_FLAG_MDT_SHIFT) & 3u, vd = (flags >> APEXW_FLAG_VDT_SHIFT) & 3u;
+  const uint32_t cd = pd == APEXW_F16 ? APEXW_F16 : APEXW_BF16;   // the parameter's compact dtype
   if (flags & APEXW_FLAG_DENSE) {
     // units of 2048 elements; fp32 m comes with fp32 v
     if (block != 2048 || (flags & (APEXW_FLAG_ULTRA | APEXW_FLAG_NF4 | APEXW_FLAG_QUAD))) return false;
     if (md == APEXW_F32) return vd == APEXW_F32;
-    return md == APEXW_BF16 && (vd == APEXW_BF16 || vd == APEXW_F32);
+    return md == cd && (vd == cd || vd == APEXW_F32);
   }
   if (block == 0 || block > 2048) return false;
   if (flags & APEXW_FLAG_ULTRA) {
     // INT8 m, dense v; a dense v needs no v scales
     if (flags & (APEXW_FLAG_NF4 | APEXW_FLAG_QUAD)) return false;
-    if (!(vd == APEXW_BF16 || vd == APEXW_F32)) return false;
+    if (!(vd == cd || vd == APEXW_F32)) return false;
     return (block % 8) == 0 || (flags & APEXW_FLAG_SCALAR);
   }
   if ((flags & APEXW_FLAG_QUAD) && (!(flags & APEXW_FLAG_NF4) || (block % 8) != 0 || (n % 4) != 0)) return false;

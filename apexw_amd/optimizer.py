@@ -330,8 +330,8 @@ class ApexW(Optimizer):
                 continue
             if p.grad.is_sparse:
                 raise RuntimeError("ApexW does not support sparse gradients")
-            if torch.is_complex(p) or p.dtype not in (torch.float32, torch.bfloat16):
-                raise NotImplementedError(f"apexw_amd steps fp32/bf16 parameters, got {p.dtype}")
+            if torch.is_complex(p) or p.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+                raise NotImplementedError(f"apexw_amd steps fp32, bf16 and fp16 parameters, got {p.dtype}")
             if p.device.type != "cuda":
                 raise RuntimeError("apexw_amd runs the optimizer step on the GPU; parameters must be on cuda")
             params.append(p)
@@ -342,6 +342,8 @@ class ApexW(Optimizer):
         for p in params:
             if len(self.state[p]) == 0:
                 self.state[p].update(S.init_state(p, group, peft, has16))
+            if p.dtype == torch.float16 and self.state[p].get("is_factored_v", False):
+                raise NotImplementedError("apexw_amd: factored_v with fp16 parameters")
         if group["precision"] in ("8bit", "ultra"):
             # both run the reference's _step_ultra (optimizer.py:3583-3587)
             return StepPlan(self, group, params, "q8")

@@ -6,7 +6,8 @@ reference's ``ApexW._init_group`` (apexw/optimizer.py:2574-2957) and resolvers
 
 compact:
   * m in bf16 (fp16 for fp16 params); v in the same dtype, or fp32 when
-    stochastic rounding is off and beta2 >= 0.995;
+    stochastic rounding is off and beta2 >= 0.995; an fp16 v is stored times a
+    dynamic scale (scale_v, 1024 at first, recalibrated every 100 steps);
   * quad-v (one v per 4 consecutive elements, numel/4 entries) when m and v are
     16-bit, numel >= 16384, numel % 4 == 0, 1-D or min(shape) >= 8, and the
     group has >= 8 parameters (or the model is a PEFT/LoRA model).
@@ -301,8 +302,11 @@ def _moments(st, p, mdt, group, is_peft, prec):
         st["exp_avg_sq"] = torch.zeros((n // 4,), dtype=vdt, device=dev)
     else:
         st["exp_avg_sq"] = torch.zeros(p.shape, dtype=vdt, device=dev)
-    st["scale_v"] = 1.0
-    st["sqrt_scale_v"] = 1.0
+    # an fp16 v holds the second moment times a dynamic scale, 1024 at first
+    # (optimizer.py:2889-2898); every other v is unscaled
+    scaled = bool(group.get("dynamic_scaling", True)) and vdt == torch.float16
+    st["scale_v"] = 1024.0 if scaled else 1.0
+    st["sqrt_scale_v"] = 32.0 if scaled else 1.0
     return st
 
 

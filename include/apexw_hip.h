@@ -44,7 +44,7 @@
 extern "C" {
 #endif
 
-#define APEXW_ABI_VERSION 16
+#define APEXW_ABI_VERSION 17
 
 /* status codes */
 enum apexw_status {
@@ -79,6 +79,9 @@ enum apexw_dtype { APEXW_F32 = 0, APEXW_BF16 = 1, APEXW_F16 = 2, APEXW_U8 = 3, A
                                            is read raw and g - mean(row) taken in its dtype (after
                                            sanitize / unscale, before the clip), with m_scale = the fp32
                                            row means (apexw_grad_row_means) and block = the row length */
+#define APEXW_FLAG_VSCALE (1u << 18)    /* compact step: v holds the second moment times a dynamic scale
+                                           (fp16 v): v_scale points at {scale_v, sqrt(scale_v)} (fp32,
+                                           scale a power of two), read by the cold and replay modes */
 #define APEXW_FLAG_ULTRA (1u << 17)     /* 8-bit step kernel, precision "ultra": INT8 m with one scale per
                                            block (m_scale), dense v (VDT field), no v scales */
 

@@ -23,7 +23,13 @@ differently; ``replay_subgroup_step`` restates it:
 * no NaN/Inf sanitizing of the grads (only clip/centralization sanitize);
 * ``m = lerp(m, g, 1-b1)`` in one op when g and m share a dtype (:1231-1234);
 * the non-quad v EMA uses the grads in their own dtype (:1301-1302);
-* 16-bit params always take ``p = SR-or-RNE(p - (m/d)*step_size)`` (:1334-1338).
+* 16-bit params always take ``p = SR-or-RNE(p - (m/d)*step_size)`` (:1334-1338);
+* with fp16 in the subgroup the denominators are clamped below by eps.
+
+fp16 second moments carry a dynamic scale (``scale_v``, 1024 at first): v is
+stored times scale_v, the EMA adds (1-b2)*scale_v*g^2 and the denominator is
+(sqrt(v) + eps_scaled*sqrt(scale_v)) / sqrt(scale_v); every 100 steps the scale
+is recalibrated from max(v) (``rescale_v``).
 """
 
 import math
@@ -54,11 +60,25 @@ def bias_terms(lr, beta1, beta2, eps, step):
     return lr * bc2_sqrt / bc1, eps * bc2_sqrt
 
 
+def _denominators(vs, eps_scaled, scale_v, sqrt_scale_v):
+    """sqrt(v) + eps_scaled, in v's scaled units when fp16 v carries a dynamic
+    scale (optimizer.py:5799-5816, :1303-1308)."""
+    dens = torch._foreach_sqrt(vs)
+    if scale_v != 1.0:
+        torch._foreach_add_(dens, eps_scaled * sqrt_scale_v)
+        torch._foreach_div_(dens, sqrt_scale_v)
+    else:
+        torch._foreach_add_(dens, eps_scaled)
+    return dens
+
+
 def compact_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weight_decay,
-                          decay_norm_only, step, is_quad, stochastic):
+                          decay_norm_only, step, is_quad, stochastic, scale_v=1.0, sqrt_scale_v=1.0):
     """One step over a subgroup sharing (p dtype, m dtype, step count, quad flag).
 
     ``step`` is the already-incremented step count.  Tensors are updated in place.
+    scale_v / sqrt_scale_v: the dynamic scale of fp16 v (optimizer.py:5600-5645;
+    1.0 otherwise): v holds scale_v times the second moment.
     """
     grads = sanitize_grads(grads)
     step_size, eps_scaled = bias_terms(lr, beta1, beta2, eps, step)
@@ -81,12 +101,11 @@ def compact_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weigh
         gq = [g.reshape(-1, 4).square().mean(dim=1) for g in gf]
         if beta2 >= 0.995 and stochastic and v16:
             for v, q in zip(vs, gq):
-                store_16bit(v, v.float().mul_(beta2).add_(q, alpha=1.0 - beta2), True)
+                store_16bit(v, v.float().mul_(beta2).add_(q, alpha=(1.0 - beta2) * scale_v), True)
         else:
             torch._foreach_mul_(vs, beta2)
-            torch._foreach_add_(vs, gq, alpha=1.0 - beta2)
-        dens = torch._foreach_sqrt(vs)
-        torch._foreach_add_(dens, eps_scaled)
+            torch._foreach_add_(vs, gq, alpha=(1.0 - beta2) * scale_v)
+        dens = _denominators(vs, eps_scaled, scale_v, sqrt_scale_v)
         for p, m, d in zip(params, ms, dens):
             delta = m.float().view(-1, 4).div_(d.float().unsqueeze(1)).mul_(step_size).view(p.shape)
             if p.dtype == torch.float32:
@@ -96,12 +115,11 @@ def compact_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weigh
         return
     if beta2 >= 0.995 and stochastic and v16:
         for v, g in zip(vs, gf):
-            store_16bit(v, v.float().mul_(beta2).addcmul_(g, g, value=1.0 - beta2), True)
+            store_16bit(v, v.float().mul_(beta2).addcmul_(g, g, value=(1.0 - beta2) * scale_v), True)
     else:
         torch._foreach_mul_(vs, beta2)
-        torch._foreach_addcmul_(vs, gf, gf, value=1.0 - beta2)
-    dens = torch._foreach_sqrt(vs)
-    torch._foreach_add_(dens, eps_scaled)
+        torch._foreach_addcmul_(vs, gf, gf, value=(1.0 - beta2) * scale_v)
+    dens = _denominators(vs, eps_scaled, scale_v, sqrt_scale_v)
     if params[0].dtype in (torch.bfloat16, torch.float16) and stochastic:
         for p, m, d in zip(params, ms, dens):
             delta = (m.float() / d.float()) * step_size
@@ -111,8 +129,12 @@ def compact_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weigh
 
 
 def replay_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weight_decay,
-                         apply_wd_mask, step, is_quad, stochastic):
-    """One replayed step over an (p dtype, compact, quad) subgroup (optimizer.py:1200-1338)."""
+                         apply_wd_mask, step, is_quad, stochastic, scale_v=1.0, sqrt_scale_v=1.0):
+    """One replayed step over an (p dtype, compact, quad) subgroup (optimizer.py:1200-1338).
+
+    With an fp16 parameter, m or v the denominators are clamped below by eps
+    (:1202, :1264-1265, :1310-1311)."""
+    has_fp16 = torch.float16 in (params[0].dtype, ms[0].dtype, vs[0].dtype)
     step_size, eps_scaled = bias_terms(lr, beta1, beta2, eps, step)
     if weight_decay != 0.0:
         decay = [p for p, w in zip(params, apply_wd_mask) if w]
@@ -130,12 +152,13 @@ def replay_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weight
         gq = [g.reshape(-1, 4).square().mean(dim=1) for g in gf]
         if sr_v:
             for v, q in zip(vs, gq):
-                store_16bit(v, v.float().mul_(beta2).add_(q, alpha=1.0 - beta2), True)
+                store_16bit(v, v.float().mul_(beta2).add_(q, alpha=(1.0 - beta2) * scale_v), True)
         else:
             torch._foreach_mul_(vs, beta2)
-            torch._foreach_add_(vs, gq, alpha=1.0 - beta2)
-        dens = torch._foreach_sqrt(vs)
-        torch._foreach_add_(dens, eps_scaled)
+            torch._foreach_add_(vs, gq, alpha=(1.0 - beta2) * scale_v)
+        dens = _denominators(vs, eps_scaled, scale_v, sqrt_scale_v)
+        if has_fp16:
+            torch._foreach_clamp_min_(dens, eps)
         for p, m, d in zip(params, ms, dens):
             delta = m.float().view(-1, 4).div_(d.float().unsqueeze(1)).mul_(step_size).view(p.shape)
             if p.dtype == torch.float32:
@@ -146,15 +169,32 @@ def replay_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weight
     if sr_v:
         for v, g in zip(vs, grads):
             g32 = g.float()
-            store_16bit(v, v.float().mul_(beta2).addcmul_(g32, g32, value=1.0 - beta2), True)
+            store_16bit(v, v.float().mul_(beta2).addcmul_(g32, g32, value=(1.0 - beta2) * scale_v), True)
     else:
         torch._foreach_mul_(vs, beta2)
-        torch._foreach_addcmul_(vs, grads, grads, value=1.0 - beta2)
-    dens = torch._foreach_sqrt(vs)
-    torch._foreach_add_(dens, eps_scaled)
+        torch._foreach_addcmul_(vs, grads, grads, value=(1.0 - beta2) * scale_v)
+    dens = _denominators(vs, eps_scaled, scale_v, sqrt_scale_v)
+    if has_fp16:
+        torch._foreach_clamp_min_(dens, eps)
     if params[0].dtype in (torch.bfloat16, torch.float16):
         for p, m, d in zip(params, ms, dens):
             delta = (m.float() / d.float()) * step_size
             store_16bit(p, p.float().sub_(delta), stochastic)
     else:
         torch._foreach_addcdiv_(params, ms, dens, value=-step_size)
+
+
+def rescale_v(vs, cur_scale):
+    """The every-100-steps recalibration of fp16 v (optimizer.py:5622-5645,
+    :1165-1178): factor 4 when max(v) < 0.25 and the scale is below 65536, 0.25
+    when max(v) > 16384 and the scale is above 1, else 1; v is multiplied by it
+    (in its dtype).  Returns the factor."""
+    v_max = max(v.max().item() for v in vs) if vs else 1.0
+    factor = 1.0
+    if v_max < 0.25 and cur_scale < 65536.0:
+        factor = 4.0
+    elif v_max > 16384.0 and cur_scale > 1.0:
+        factor = 0.25
+    if factor != 1.0:
+        torch._foreach_mul_(vs, factor)
+    return factor

@@ -203,6 +203,8 @@ def _dense(st, p, mdt, group, is_peft, n_params_in_group, prec):
     st["state_dtype_v"] = vdt
     st["exp_avg"] = torch.zeros(p.shape, dtype=mdt)
     st["exp_avg_sq"] = torch.zeros((n // 4,), dtype=vdt) if quad else torch.zeros(p.shape, dtype=vdt)
-    st["scale_v"] = 1.0
-    st["sqrt_scale_v"] = 1.0
+    # fp16 v starts with a dynamic scale of 1024 (optimizer.py:2889-2898)
+    fp16_scaled = bool(group.get("dynamic_scaling", True)) and vdt == torch.float16
+    st["scale_v"] = 1024.0 if fp16_scaled else 1.0
+    st["sqrt_scale_v"] = 32.0 if fp16_scaled else 1.0
     return st

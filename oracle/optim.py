@@ -33,7 +33,7 @@ import torch
 
 from . import layout as L
 from .clip import clip_grads_
-from .compact import compact_subgroup_step, replay_subgroup_step, sanitize_grads
+from .compact import compact_subgroup_step, replay_subgroup_step, rescale_v, sanitize_grads
 from .factored import factored_update
 from .q8 import q8_param_step
 
@@ -66,7 +66,7 @@ class OracleApexW:
     def __init__(self, params, lr=1e-3, betas=None, eps=1e-8, weight_decay=1e-2, decay_norm_only=True,
                  adamw_compat=False, clip_grad_norm=None, precision="compact", stochastic_rounding=True,
                  block_size=None, force_compact_v=False, int4_m=None, grad_centralization=False,
-                 factored_v=False, six_bit=False, threshold=65536, amp=None):
+                 factored_v=False, six_bit=False, threshold=65536, amp=None, dynamic_scaling=True):
         precision = normalize_precision(precision)
         if betas is None:
             betas = (0.9, 0.999) if precision in ("8bit", "full") else (0.9, 0.99)
@@ -80,7 +80,7 @@ class OracleApexW:
                           precision=precision, stochastic_rounding=stochastic_rounding,
                           block_size=block_size, force_compact_v=force_compact_v, int4_m=int4_m,
                           grad_centralization=grad_centralization, factored_v=factored_v, six_bit=six_bit,
-                          threshold=threshold, amp=amp, params=self.params)
+                          threshold=threshold, amp=amp, dynamic_scaling=dynamic_scaling, params=self.params)
         self.state = {}
         self._plan = None
         self.grad_scale = None
@@ -186,14 +186,31 @@ class OracleApexW:
         for p, g, st in zip(plist, grads, sts):
             key = (p.dtype, st["exp_avg"].dtype, int(st["step"].item()), self._is_quad(p))
             sub.setdefault(key, []).append((p, g, st))
-        for (_, _, _, quad), items in sub.items():
+        for (_, mdt, _, quad), items in sub.items():
             for _, _, st in items:
                 st["step"].add_(1)
+            step = int(items[0][2]["step"].item())
+            vs = [i[2]["exp_avg_sq"] for i in items]
+            scale_v, sqrt_scale_v = 1.0, 1.0
+            if grp.get("dynamic_scaling", True) and mdt == torch.float16:
+                # the subgroup's v scale lives in its parameters' states; every 100 steps
+                # it is recalibrated from max(v) (optimizer.py:5600-5645; keyed on m's dtype)
+                st0 = items[0][2]
+                scale_v = st0["scale_v"]
+                sqrt_scale_v = st0.get("sqrt_scale_v", math.sqrt(scale_v))
+                if step > 1 and step % 100 == 0:
+                    f = rescale_v(vs, scale_v)
+                    if f != 1.0:
+                        scale_v *= f
+                        sqrt_scale_v = math.sqrt(scale_v)
+                        for _, _, st in items:
+                            st["scale_v"], st["sqrt_scale_v"] = scale_v, sqrt_scale_v
             compact_subgroup_step([i[0] for i in items], [i[1] for i in items],
-                                  [i[2]["exp_avg"] for i in items], [i[2]["exp_avg_sq"] for i in items],
-                                  step=items[0][2]["step"].item(), is_quad=quad,
-                                  stochastic=grp["stochastic_rounding"], **kw)
-        self._plan = {"kind": "foreach", "params": plan_params}
+                                  [i[2]["exp_avg"] for i in items], vs, step=step, is_quad=quad,
+                                  stochastic=grp["stochastic_rounding"], scale_v=scale_v,
+                                  sqrt_scale_v=sqrt_scale_v, **kw)
+        # the replayed plan's per-subgroup scales start at 1.0 (optimizer.py:546-560)
+        self._plan = {"kind": "foreach", "params": plan_params, "sg_scale": {}}
 
     def _is_quad(self, p):
         v = self.state[p]["exp_avg_sq"]
@@ -232,11 +249,26 @@ class OracleApexW:
             compact = st["exp_avg"].dtype in (torch.bfloat16, torch.float16)
             sub.setdefault((p.dtype, compact, self._is_quad(p)), []).append((p, g, st))
         dno = kw.pop("decay_norm_only")
-        for (_, _, quad), items in sub.items():
+        sg_scale = plan["sg_scale"]
+        if grp.get("dynamic_scaling", True) and step > 1 and step % 100 == 0:
+            # the replay's recalibration scales fp16 v by the factor, but the step below
+            # takes its scale from the first parameter's state, which the replay never
+            # updates (optimizer.py:1165-1178, :1193-1199)
+            for key, items in sub.items():
+                vs = [i[2]["exp_avg_sq"] for i in items]
+                if vs[0].dtype == torch.float16:
+                    rescale_v(vs, sg_scale.get(key, 1.0))
+        for key, items in sub.items():
+            quad = key[2]
+            st0 = items[0][2]
+            scale_v = st0.get("scale_v", sg_scale.get(key, 1.0))
+            sqrt_scale_v = st0.get("sqrt_scale_v", math.sqrt(scale_v))
+            sg_scale[key] = scale_v
             replay_subgroup_step([i[0] for i in items], [i[1] for i in items],
                                  [i[2]["exp_avg"] for i in items], [i[2]["exp_avg_sq"] for i in items],
                                  apply_wd_mask=[(i[0].dim() >= 2) if dno else True for i in items],
-                                 step=step, is_quad=quad, stochastic=grp["stochastic_rounding"], **kw)
+                                 step=step, is_quad=quad, stochastic=grp["stochastic_rounding"],
+                                 scale_v=scale_v, sqrt_scale_v=sqrt_scale_v, **kw)
 
     def _factored(self, p, g, st, step, inv, sanitize):
         grp = self.group

@@ -9,8 +9,8 @@ import os
 import numpy as np
 import torch
 
-from golden.make_golden import (FV_KW, FV_Q8_SHAPES, HOOK_KW, HOOK_SHAPES, PREC_CASES, SD_CASES, _fingerprint,
-                                 _grad, _param)
+from golden.make_golden import (FP16_CASES, FV_KW, FV_Q8_SHAPES, HOOK_KW, HOOK_SHAPES, PREC_CASES, SD_CASES,
+                                 _fingerprint, _grad, _param)
 from golden.sd_codec import decode
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -53,6 +53,10 @@ CASES.update(FV_CASES)
 # the full / auto / ultra precisions (every state tensor recorded)
 PREC_NAMES = sorted(PREC_CASES)
 CASES.update({k: (sh, dt, n, seed, kw, None, ()) for k, (sh, dt, n, seed, kw) in PREC_CASES.items()})
+# fp16 parameters (every state tensor and the v scales recorded); the eighth entry lists
+# (step, parameter) pairs without a grad
+FP16_NAMES = sorted(FP16_CASES)
+CASES.update({k: (sh, torch.float16, n, seed, kw, None, (), ng) for k, (sh, n, seed, kw, ng) in FP16_CASES.items()})
 # in-backward trajectories: name -> (steps, backward passes per step, seed)
 HOOK_CASES = {"hooks_k1_rne": (3, 1, 31), "hooks_k2_rne": (3, 2, 32)}
 
@@ -70,20 +74,21 @@ def to_torch(arr, like_dtype):
 
 def replay(name, make_opt, device="cpu", get_state=None):
     """Run case ``name`` with ``make_opt(params, **kwargs)``; return (params, opt, golden dict)."""
-    shapes, dtype, steps, seed, kwargs, scales, zidx = CASES[name]
+    shapes, dtype, steps, seed, kwargs, scales, zidx = CASES[name][:7]
+    none_grad = CASES[name][7] if len(CASES[name]) > 7 else ()
     gold = load(name)
     gen = torch.Generator().manual_seed(seed)
     host = [_param(s, dtype, gen) for s in shapes]
     fp = [_fingerprint(p) for p in host]
     params = [torch.nn.Parameter(h.to(device)) for h in host]
     opt = make_opt(params, **kwargs)
-    for _ in range(steps):
+    for step in range(steps):
         for i, p in enumerate(params):
             g = _grad(p.shape, dtype, gen, 1e-3 if scales is None else scales[i])
             if i in zidx:
                 g.zero_()
             fp.append(_fingerprint(g))
-            p.grad = g.to(device)
+            p.grad = None if (step, i) in none_grad else g.to(device)
         opt.step()
     np.testing.assert_array_equal(np.array(fp, dtype=np.int64), gold["fingerprint"])
     return params, opt, gold
@@ -148,6 +153,6 @@ def state_keys(gold, i):
 
 def initial_params(name):
     """The parameters case ``name`` starts from (the generator's first draws)."""
-    shapes, dtype, steps, seed, kwargs, scales, zidx = CASES[name]
+    shapes, dtype, steps, seed, kwargs, scales, zidx = CASES[name][:7]
     gen = torch.Generator().manual_seed(seed)
     return [_param(s, dtype, gen) for s in shapes]

@@ -74,7 +74,9 @@ def test_check_tensor_rejects_bad_descriptors():
     assert lib.apexw_check_tensor(ctypes.byref(t), 0) == 4
     t.flags |= _lib.FLAG_SCALAR
     assert lib.apexw_check_tensor(ctypes.byref(t), 0) == 0
-    t.flags = (_lib.F16 << 0) | (_lib.F16 << 2)
+    t.flags = (_lib.F16 << 0) | (_lib.F16 << 2) | (_lib.BF16 << 4) | (_lib.BF16 << 6)   # fp16 p keeps fp16 m
+    assert lib.apexw_check_tensor(ctypes.byref(t), 0) == 2
+    t.flags = (_lib.F16 << 0) | (_lib.BF16 << 2)                                      # p and g dtypes differ
     assert lib.apexw_check_tensor(ctypes.byref(t), 0) == 2
     q = _lib.Tensor(16, 32, 48, 64, 80, 96, 4096, (_lib.BF16 << 0) | (_lib.BF16 << 2) | _lib.FLAG_NF4 | _lib.FLAG_QUAD,
                     2048)
@@ -242,14 +244,14 @@ def test_state_map_pickles_as_plain_defaultdict():
     assert other.state._owner is other
 
 
-@pytest.mark.parametrize("prec", ["full", "auto", "ultra"])
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("prec", ["full", "auto", "ultra", "compact", "8bit"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
 @pytest.mark.parametrize("kw", [dict(), dict(adamw_compat=True, stochastic_rounding=False),
                                 dict(threshold=4096, force_compact_v=True), dict(fused=True)])
 def test_other_precision_layouts_match_oracle(prec, dtype, kw):
-    """The product's state layout for the full / auto / ultra precisions equals the
-    oracle's (pinned bit for bit by the reference-written full_*, auto_*, ultra_*
-    trajectories): the same keys, flags, dtypes, shapes and initial values."""
+    """The product's state layout for every precision and parameter dtype equals the
+    oracle's (pinned bit for bit by the reference-written trajectories, fp16_* for
+    fp16 parameters): the same keys, flags, dtypes, shapes, initial values and v scales."""
     from apexw_amd import state as S
     from apexw_amd.optimizer import ApexW
     from oracle import layout as OL

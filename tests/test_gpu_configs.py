@@ -59,6 +59,12 @@ def _bf16_ulp(x):
     return torch.exp2(e - 7)
 
 
+def _f16_ulp(x):
+    """Spacing of fp16 values at |x| (fp32 input; the subnormal spacing 2^-24 below 2^-14)."""
+    e = torch.floor(torch.log2(x.abs().clamp_min(2.0 ** -14)))
+    return torch.exp2(e - 10)
+
+
 def _cmp_p(got, ref, prev, what, den_rel):
     """A parameter: one bf16 ulp, or 1e-6 relative (fp32) -- plus den_rel of the
     update |ref - prev|.  The update's last fp32 bits differ between the GPU and
@@ -69,9 +75,12 @@ def _cmp_p(got, ref, prev, what, den_rel):
     got = got.detach().cpu().reshape(-1).double()
     ref64, prev64 = ref.detach().reshape(-1).double(), prev.detach().reshape(-1).double()
     upd = den_rel * (ref64 - prev64).abs()
-    if ref.dtype == torch.bfloat16:
-        ulp = torch.maximum(_bf16_ulp(ref64.float()), _bf16_ulp(got.float())).double()
+    if ref.dtype in (torch.bfloat16, torch.float16):
+        f = _bf16_ulp if ref.dtype == torch.bfloat16 else _f16_ulp
+        ulp = torch.maximum(f(ref64.float()), f(got.float())).double()
         err = (got - ref64).abs() - (ulp + upd)
+        both_nan = torch.isnan(got) & torch.isnan(ref64)
+        err = torch.where(both_nan, torch.full_like(err, -1.0), err)
     else:
         err = (got - ref64).abs() - (1e-6 * ref64.abs() + 1e-9 + upd)
     bad = err > 0
@@ -87,6 +96,9 @@ def _cmp(got, ref, what, floor=1e-9):
     if ref.dtype == torch.bfloat16:
         d = bf16_ulp_diff(got.contiguous(), ref.contiguous())
         assert int(d.max()) <= 1, f"{what}: {int(d.max())} bf16 ulps ({int((d > 1).sum())} elements)"
+    elif ref.dtype == torch.float16:
+        from test_gpu_parity import _cmp_f16
+        _cmp_f16(got, ref, what=what)
     elif ref.dtype == torch.float32:
         err = (got.double() - ref.double()).abs() - (1e-6 * ref.double().abs() + floor)
         assert float(err.max()) <= 0, f"{what}: max excess {float(err.max()):.3e}"
@@ -197,12 +209,15 @@ class Mirror:
             # one bf16 ulp of the update where the reference rounds it (or its denominator) to
             # bf16: compact with bf16 v, and the 8-bit / ultra step's tensors outside the chunked
             # order (p -= bf16(update))
-            bf16_den = not cs.get("is_8bit", False) and cs["exp_avg_sq"].dtype == torch.bfloat16
+            # (2^-10 for fp16: one ulp of an fp16 update or denominator)
+            half = (torch.bfloat16, torch.float16)
+            v16_den = not cs.get("is_8bit", False) and cs["exp_avg_sq"].dtype in half
             quantized_mode = self.copt.group["precision"] in ("8bit", "ultra")
             chunked = cs.get("is_8bit", False) and cp.numel() > 262144
-            generic_8bit = quantized_mode and cp.dtype == torch.bfloat16 and not chunked
-            _cmp_p(self._gpu_p(e), cp.detach(), self.pre[j][0], f"{name} p",
-                   2.0 ** -7 if (bf16_den or generic_8bit) else 2.0 ** -22)
+            generic_8bit = quantized_mode and cp.dtype in half and not chunked
+            fp16 = torch.float16 in (cp.dtype, cs["exp_avg_sq"].dtype)
+            den_rel = (2.0 ** -10 if fp16 else 2.0 ** -7) if (v16_den or generic_8bit) else 2.0 ** -22
+            _cmp_p(self._gpu_p(e), cp.detach(), self.pre[j][0], f"{name} p", den_rel)
             for k in _tensor_keys(cs):
                 if sr and cs[k].dtype in (torch.uint8, torch.int8) and not k.endswith("scales"):
                     continue            # SR codes: checked by the bracket / bias test

@@ -2,7 +2,7 @@
 
 Tolerances (round to nearest, SR off):
   * fp32 params:  |d| <= 1e-6*|ref| + 1e-9 (the absolute floor covers p ~ 0)
-  * bf16 tensors (params, m, v): <= 1 bf16 ulp
+  * bf16 tensors (params, m, v): <= 1 bf16 ulp; fp16 tensors <= 1 fp16 ulp
   * fp32 v (compact):             |d| <= 1e-6*|ref| + 1e-12
   * 8-bit codes: NF4/INT8/log-u8 differ by <= 1 code; block scales within 1e-6 relative
 Factored-v trajectories (S steps, no resynchronisation): the row / column EMAs
@@ -43,9 +43,27 @@ def _cmp_bf16(got, ref, ulps=1, what=""):
     assert int(d.max()) <= ulps, f"{what}: {int(d.max())} bf16 ulps ({int((d > ulps).sum())} elements)"
 
 
+def _cmp_f16(got, ref, ulps=1, what=""):
+    """fp16 tensors within ``ulps`` units in the last place (sign-aware bit distance);
+    NaN where the reference has NaN (an fp16 step can divide 0 by a denominator that
+    underflowed to 0, in the reference as here), whatever its sign bit."""
+    got = got.cpu().contiguous()
+    ref = ref.contiguous()
+    nan_a, nan_b = torch.isnan(got), torch.isnan(ref)
+    assert torch.equal(nan_a, nan_b), f"{what}: NaN at {int((nan_a != nan_b).sum())} elements not matched"
+    ia = got.view(torch.int16).to(torch.int32)
+    ib = ref.view(torch.int16).to(torch.int32)
+    ia = torch.where(ia < 0, -(ia & 0x7FFF), ia)
+    ib = torch.where(ib < 0, -(ib & 0x7FFF), ib)
+    d = torch.where(nan_b, torch.zeros_like(ia), (ia - ib).abs())
+    assert int(d.max()) <= ulps, f"{what}: {int(d.max())} fp16 ulps ({int((d > ulps).sum())} elements)"
+
+
 def _cmp_tensor(got, gold_arr, what):
     if got.dtype == torch.bfloat16:
         _cmp_bf16(got.reshape(-1), to_torch(gold_arr, torch.bfloat16).reshape(-1), what=what)
+    elif got.dtype == torch.float16:
+        _cmp_f16(got.reshape(-1), torch.from_numpy(gold_arr).reshape(-1), what=what)
     elif got.dtype == torch.float32:
         _cmp_f32(got.reshape(-1), torch.from_numpy(gold_arr).reshape(-1), floor=1e-12 if what.startswith("v") else 1e-9,
                  what=what)
@@ -92,6 +110,8 @@ def _cmp_factored(params, opt, gold, init, steps):
         keys = state_keys(gold, i)
         assert keys == sorted(k for k, v in st.items() if torch.is_tensor(v) and k != "step"), f"state keys {i}"
         assert float(st["step"]) == float(gold[f"step_{i}"][0])
+        if f"scale_{i}" in gold:
+            assert [float(st["scale_v"]), float(st["sqrt_scale_v"])] == gold[f"scale_{i}"].tolist(), f"scale_{i}"
         fac = bool(st.get("is_factored_v", False))
         if not fac:
             _cmp_tensor(p.data, gold[f"p_{i}"], f"p_{i}")

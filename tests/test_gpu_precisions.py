@@ -49,3 +49,22 @@ def test_precision_sr_is_unbiased(prec, dtype, stat):
                    seed=400 + CASES.index((prec, dtype)), sr_from=1)
     s = stats[stat]
     assert s.n >= 1_000_000 and abs(s.z) < 3 and abs(s.z_mag) < 3, stats
+
+
+FP16_CASES = [("compact", dict()), ("compact", dict(adamw_compat=True)), ("full", dict()), ("auto", dict()),
+              ("ultra", dict()), ("8bit", dict())]
+
+
+@pytest.mark.parametrize("prec,extra", FP16_CASES, ids=[f"{p}-{i}" for i, (p, _) in enumerate(FP16_CASES)])
+def test_fp16_parameters_match_oracle_rne(prec, extra):
+    """fp16 parameters in every precision, three steps, SR off: fp16 m / v with the
+    dynamic v scale (compact, auto), fp32 v (beta2 0.999), fp32 moments (full), INT8
+    blocks (ultra), NF4 / INT8 codes (8-bit, on the general kernel)."""
+    _need_gpu()
+    _say(f"fp16 {prec} {extra}")
+    kw = dict(KW, precision=prec, threshold=4096)
+    kw.update(extra)
+    if prec != "compact" or "adamw_compat" not in extra:
+        kw["adamw_compat"] = False
+    _drive(f"fp16-{prec}", SHAPES, torch.float16, kw, [(i, None) for i in range(len(SHAPES))], 3, False,
+           seed=500 + FP16_CASES.index((prec, extra)))

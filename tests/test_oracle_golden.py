@@ -42,6 +42,9 @@ def test_oracle_matches_reference_trajectory(name):
                 np.testing.assert_array_equal(_as_np(opt.state[p][k]).reshape(-1), gold[f"st_{i}_{k}"].reshape(-1),
                                               err_msg=f"{k}_{i}")
             assert float(opt.state[p]["step"]) == float(gold[f"step_{i}"][0])
+            if f"scale_{i}" in gold:
+                st = opt.state[p]
+                assert [float(st["scale_v"]), float(st["sqrt_scale_v"])] == gold[f"scale_{i}"].tolist()
             continue
         st = _state_arrays(opt, p)
         for key in ("m", "v", "ms", "vs"):

@@ -399,6 +399,9 @@ class ApexW(Optimizer):
         if prec not in ("compact", "8bit"):
             raise NotImplementedError(f"apexw_amd implements the compact and 8-bit AdamW step; not supported: "
                                       f"precision={prec!r}")
+        if any(p.dtype == torch.float16 for g in self.param_groups for p in g["params"]):
+            # an fp16 v holds the moment times its dynamic scale; no conversion of it here
+            raise NotImplementedError("apexw_amd: set_precision with fp16 parameters")
         peft = S.detect_peft_context(self.param_groups)
         for group in self.param_groups:
             group["precision"] = prec

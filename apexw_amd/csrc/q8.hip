@@ -1194,9 +1194,10 @@ __global__ __launch_bounds__(256) void ultra_step_kernel(const apexw_tensor* __r
 
 
 // Kernel for the units of fast-path tensors (see apexw_q8_fast_ok) with parameter
-// dtype PD; each dtype is its own kernel so the fp32 variant's larger register
-// footprint does not lower the bf16 kernel's occupancy.
-template <int PD>
+// dtype PD and stochastic rounding SR; each (dtype, SR) pair is its own kernel so
+// one variant's register footprint does not lower another's occupancy (bf16: 142
+// VGPRs with SR, occupancy 3; 93 without, occupancy 5).
+template <int PD, bool SR>
 __global__ __launch_bounds__(256) void q8_fast_kernel(const apexw_tensor* __restrict__ tensors,
                                                       const apexw_unit* __restrict__ units,
                                                       int64_t n_units, apexw_hparams hp_in) {
@@ -1230,7 +1231,6 @@ __global__ __launch_bounds__(256) void q8_fast_kernel(const apexw_tensor* __rest
   c.midtab = s_midtab;
   c.coef = (hp.flags & APEXW_HP_CLIP) ? *hp.clip_coef : 1.0f;
   const uint32_t wave = uniform(threadIdx.x >> 6);
-  const bool sr = hp.flags & APEXW_HP_SR;
   // a workgroup walks a contiguous chunk of kFastChunk units, its waves interleaved
   // (unit base + 4 i + wave): measured ~1% faster than workgroups striding by 4 units
   for (int64_t base = (int64_t)blockIdx.x * kFastChunk; base < n_units; base += (int64_t)gridDim.x * kFastChunk)
@@ -1242,17 +1242,10 @@ __global__ __launch_bounds__(256) void q8_fast_kernel(const apexw_tensor* __rest
     if (!apexw_q8_fast_ok(t.flags, t.block) || ((t.flags >> APEXW_FLAG_PDT_SHIFT) & 3u) != (uint32_t)PD) continue;
     const bool full = (int64_t)(un.unit + 1) * 2048 <= t.n;
     const bool gen = t.flags & APEXW_FLAG_GENERIC;
-    if (sr) {
-      if (full && !gen) q8_block_fast<PD, true, true, false>(t, un.tensor, un.unit, c);
-      else if (full) q8_block_fast<PD, true, true, true>(t, un.tensor, un.unit, c);
-      else if (!gen) q8_block_fast<PD, true, false, false>(t, un.tensor, un.unit, c);
-      else q8_block_fast<PD, true, false, true>(t, un.tensor, un.unit, c);
-    } else {
-      if (full && !gen) q8_block_fast<PD, false, true, false>(t, un.tensor, un.unit, c);
-      else if (full) q8_block_fast<PD, false, true, true>(t, un.tensor, un.unit, c);
-      else if (!gen) q8_block_fast<PD, false, false, false>(t, un.tensor, un.unit, c);
-      else q8_block_fast<PD, false, false, true>(t, un.tensor, un.unit, c);
-    }
+    if (full && !gen) q8_block_fast<PD, SR, true, false>(t, un.tensor, un.unit, c);
+    else if (full) q8_block_fast<PD, SR, true, true>(t, un.tensor, un.unit, c);
+    else if (!gen) q8_block_fast<PD, SR, false, false>(t, un.tensor, un.unit, c);
+    else q8_block_fast<PD, SR, false, true>(t, un.tensor, un.unit, c);
   }
 }
 
@@ -1370,10 +1363,13 @@ int apexw_launch_q8_fast(const apexw_tensor* tensors, int64_t n_units, const ape
   // (measured ~1% faster than a persistent grid of 16 workgroups per resident slot)
   const int64_t chunks = (n_units + kFastChunk - 1) / kFastChunk;
   const int grid = (int)(chunks < INT32_MAX ? chunks : INT32_MAX);
+  const bool sr = hp->flags & APEXW_HP_SR;
   if (p_dtype == APEXW_F32) {
-    hipLaunchKernelGGL(q8_fast_kernel<APEXW_F32>, dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
-    return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
+    if (sr) hipLaunchKernelGGL((q8_fast_kernel<APEXW_F32, true>), dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
+    else hipLaunchKernelGGL((q8_fast_kernel<APEXW_F32, false>), dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
+  } else {
+    if (sr) hipLaunchKernelGGL((q8_fast_kernel<APEXW_BF16, true>), dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
+    else hipLaunchKernelGGL((q8_fast_kernel<APEXW_BF16, false>), dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
   }
-  hipLaunchKernelGGL(q8_fast_kernel<APEXW_BF16>, dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }

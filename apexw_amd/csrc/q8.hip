@@ -551,9 +551,11 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
   }
   const bool prep = hf & (APEXW_HP_SANITIZE | APEXW_HP_CLIP | APEXW_HP_UNSCALE);
 
+  // SR noise: one xorshift32 word per element pair in this pass (its two halves
+  // round the pair's bf16 parameters) and one per pair in the requantization pass
+  // (two 12-bit NF4 noises and 8 bits of v noise), drawn from the same stream there
+  // rather than held in registers across the passes
   float mnew[4][8], vq[4][2];
-  uint32_t hbits[4][8];   // this pass's random words
-  uint32_t hm[4][4];      // bits 16-31 of two elements' words, kept for requantization
   float amax = 0.0f, vmax = 0.0f;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
@@ -581,15 +583,6 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
     if (prep) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) g[j] = q8_grad<PD>(g[j], tf, c);
-    }
-    if constexpr (SR) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        rs ^= rs << 13;
-        rs ^= rs >> 17;
-        rs ^= rs << 5;
-        hbits[k][j] = rs;
-      }
     }
     float upd[8];
     if constexpr (SR) {
@@ -698,10 +691,6 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
       float x[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) x[j] = p[j] * decay - upd[j];
-      if constexpr (SR) {
-#pragma unroll
-        for (int b = 0; b < 4; ++b) hm[k][b] = __builtin_amdgcn_perm(hbits[k][2 * b + 1], hbits[k][2 * b], 0x05040100u);
-      }
       const u32x4 lo = {__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]), __float_as_uint(x[3])};
       const u32x4 hi = {__float_as_uint(x[4]), __float_as_uint(x[5]), __float_as_uint(x[6]), __float_as_uint(x[7])};
       const auto dst = APEXW_GLOBAL(u32x4, (float*)t.p + e);
@@ -720,7 +709,11 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
     for (int b = 0; b < 4; ++b) {
       if constexpr (SR) {
         // v_cvt_sr_bf16_f32 adds bits 16-31 of the random word to the fp32 pattern
-        // and truncates (add-noise-then-truncate SR), writing one half of the pair
+        // and truncates (add-noise-then-truncate SR), writing one half of the pair:
+        // the pair's word rounds its first element, the word's low half its second
+        rs ^= rs << 13;
+        rs ^= rs >> 17;
+        rs ^= rs << 5;
         float y[2];
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -728,11 +721,9 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
           y[i] = GENERIC ? rnd<APEXW_BF16>(p[j] * decay) - upd[j] : fmaf(p[j], decay, -upd[j]);
         }
         bf16x2 pr = __builtin_bit_cast(bf16x2, pv[b]);
-        pr = __builtin_amdgcn_cvt_sr_bf16_f32(pr, y[0], hbits[k][2 * b], false);
-        pr = __builtin_amdgcn_cvt_sr_bf16_f32(pr, y[1], hbits[k][2 * b + 1], true);
+        pr = __builtin_amdgcn_cvt_sr_bf16_f32(pr, y[0], rs, false);
+        pr = __builtin_amdgcn_cvt_sr_bf16_f32(pr, y[1], rs << 16, true);
         pout[b] = __builtin_bit_cast(uint32_t, pr);
-        // bits 0-15 of both words, kept for the NF4 (bits 0-11) and v (bits 12-15) codes
-        hm[k][b] = __builtin_amdgcn_perm(hbits[k][2 * b + 1], hbits[k][2 * b], 0x05040100u);
       } else {
         // the final rounding to bf16 is the pack itself (v_cvt_pk_bf16_f32, nearest-even)
         float x[2];
@@ -778,7 +769,15 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
   for (int k = 0; k < 4; ++k) {
     const int64_t e = start + k * 512 + lane * 8;
     uint32_t w = 0;
+    uint32_t hw[4];   // pair b: bits 0-11 / 16-27 NF4 noise, bits 12-15 / 28-31 v noise
     if constexpr (SR) {
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        rs ^= rs << 13;
+        rs ^= rs >> 17;
+        rs ^= rs << 5;
+        hw[b] = rs;
+      }
       uint32_t sum[4];
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
@@ -793,7 +792,7 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
         }
         // two 16-bit lanes of G + r12 (r12 = bits 0-11 of the element's word):
         // the stochastic code lands in bits 12-15 and 28-31
-        sum[b] = (gc[0] | (gc[1] << 16)) + (hm[k][b] & 0x0FFF0FFFu);
+        sum[b] = (gc[0] | (gc[1] << 16)) + (hw[b] & 0x0FFF0FFFu);
       }
       // gather bytes 1 and 3 (code << 4 | noise) of the four pair sums, then
       // byte b = code[2b] << 4 | code[2b+1]
@@ -819,7 +818,7 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
       } else if constexpr (SR) {
         const float r = fmaxf(vv * rvs, 0x1p-24f);
         // bits 12-15 of the quad's first two words -> 8 bits -> u = (r + 1/2) / 2^8, then floor
-        const uint32_t a = hm[k][2 * q];
+        const uint32_t a = hw[2 * q];
         const uint32_t r8 = ((a >> 12) & 0xFu) | ((a >> 24) & 0xF0u);
         const float u = __uint_as_float(0x3F804000u | (r8 << 15)) - 1.0f;
         const float qf = fmaf(__builtin_amdgcn_logf(r), 0x1.52aaaap+3f, 255.0f) + u;

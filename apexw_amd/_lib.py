@@ -13,7 +13,7 @@ import numpy as np
 
 from ._build import LIB_PATH
 
-ABI_VERSION = 17
+ABI_VERSION = 18
 
 # dtype codes
 F32, BF16, F16, U8, I8 = 0, 1, 2, 3, 4
@@ -156,16 +156,16 @@ SIGNATURES = {
     "apexw_gemm_grouped_items": (ctypes.c_int64, [_vp, _i32]),
     "apexw_gemm_grouped_schedule": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i32, ctypes.POINTER(ctypes.c_int64), _vp,
                                                    ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32)]),
-    "apexw_gemm_nt_grouped": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, _vp]),
+    "apexw_gemm_nt_grouped": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, _vp, _vp]),
     "apexw_muon_workspace_floats": (ctypes.c_int64, [_i64, _i64]),
     "apexw_muon_prepare": (ctypes.c_int, [_vp, _vp, _i32, _i64, _i64, _f32, _f32, _i32, _f32, _f32, _vp, _vp, _i64,
-                                          _i64, _vp, _vp]),
-    "apexw_muon_apply": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _i64, _i32, _f32, _i32, _f32, _vp]),
+                                          _i64, _vp, _vp, _vp]),
+    "apexw_muon_apply": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _i64, _i32, _f32, _i32, _f32, _vp, _vp]),
     "apexw_factored_layout": (ctypes.c_int64, [_vp, _i32, ctypes.POINTER(ctypes.c_int64),
                                                ctypes.POINTER(ctypes.c_int64)]),
     "apexw_factored_step": (ctypes.c_int, [_vp, _i32, _vp, _i32, _i64, _i64, _vp, _i64, _vp, _vp, _HP, _vp]),
     "apexw_muon_coordwise": (ctypes.c_int, [_vp, _vp, _i32, _vp, _i32, _i64, _f32, _f32, _i32, _f32, _f32, _i32,
-                                             _f32, _vp]),
+                                             _f32, _vp, _vp]),
     "apexw_amp_prepare": (ctypes.c_int, [_vp, _vp, _vp, _i32, _vp, _i32, _vp, _vp]),
     "apexw_state_decode": (ctypes.c_int, [ctypes.POINTER(StateLayout), _vp, _vp, _vp]),
     "apexw_state_encode": (ctypes.c_int, [ctypes.POINTER(StateLayout), _vp, _vp, _vp]),

@@ -27,17 +27,17 @@ int apexw_launch_gemm_nt(const uint16_t*, const uint16_t*, const uint16_t*, uint
                          int64_t, int64_t, float, float, hipStream_t);
 int apexw_muon_partials(int64_t n);
 int apexw_launch_muon_coordwise(float*, const void*, int32_t, void*, int32_t, int64_t, float, float, int32_t, float,
-                                float, int32_t, float, hipStream_t);
+                                float, int32_t, float, const apexw_amp_dyn*, hipStream_t);
 int apexw_launch_grad_prep(const apexw_grad_prep*, const apexw_unit*, int64_t, float, uint32_t, const apexw_amp_dyn*,
                            hipStream_t);
 int apexw_launch_row_means(const apexw_grad_prep*, const apexw_unit*, int64_t, float, uint32_t, const apexw_amp_dyn*,
                            hipStream_t);
 int apexw_launch_gemm_grouped(const apexw_gemm_problem*, const uint32_t*, const int32_t*, int32_t, int32_t,
-                              hipStream_t);
+                              const apexw_amp_dyn*, hipStream_t);
 int apexw_launch_muon_prepare(float*, const void*, int32_t, int64_t, int64_t, float, float, int32_t, float, float,
-                              uint16_t*, uint16_t*, int64_t, int64_t, float*, hipStream_t);
+                              uint16_t*, uint16_t*, int64_t, int64_t, float*, const apexw_amp_dyn*, hipStream_t);
 int apexw_launch_muon_apply(void*, int32_t, const uint16_t*, int64_t, int64_t, int64_t, int32_t, float, int32_t,
-                            float, hipStream_t);
+                            float, const apexw_amp_dyn*, hipStream_t);
 bool apexw_q8_flags_ok(uint32_t flags, uint32_t block, int64_t n);
 int apexw_launch_factored(const apexw_tensor*, const apexw_fv_tensor*, int32_t, int64_t, int64_t, const apexw_unit*,
                           const int64_t*, float*, const apexw_hparams*, hipStream_t);
@@ -437,13 +437,14 @@ int apexw_gemm_grouped_schedule(const apexw_gemm_problem* problems, int32_t n_pr
 }
 
 int apexw_gemm_nt_grouped(const apexw_gemm_problem* problems, const uint32_t* items, const int32_t* queue_offsets,
-                          int32_t n_workgroups, int32_t kind, void* stream) {
+                          int32_t n_workgroups, int32_t kind, const apexw_amp_dyn* amp, void* stream) {
   if (!problems || !items || !queue_offsets) return APEXW_ERR_ARG;
+  if ((uintptr_t)amp & 15u) return APEXW_ERR_ALIGN;
   if (n_workgroups <= 0 || n_workgroups % APEXW_GEMM_QUEUES) return APEXW_ERR_ARG;
   if (kind <= 0 || kind > 15 || !(kind & (APEXW_GEMM_OUT_C | APEXW_GEMM_OUT_CT))) return APEXW_ERR_ARG;
   if ((kind & APEXW_GEMM_KIND_NN) && (kind & APEXW_GEMM_OUT_CT)) return APEXW_ERR_ARG;
   if (((uintptr_t)problems | (uintptr_t)items | (uintptr_t)queue_offsets) & 3u) return APEXW_ERR_ALIGN;
-  return apexw_launch_gemm_grouped(problems, items, queue_offsets, n_workgroups, kind, (hipStream_t)stream);
+  return apexw_launch_gemm_grouped(problems, items, queue_offsets, n_workgroups, kind, amp, (hipStream_t)stream);
 }
 
 int64_t apexw_muon_workspace_floats(int64_t rows, int64_t cols) {
@@ -452,35 +453,39 @@ int64_t apexw_muon_workspace_floats(int64_t rows, int64_t cols) {
 
 int apexw_muon_prepare(float* buf, const void* g, int32_t g_dtype, int64_t rows, int64_t cols, float mu,
                        float one_minus_mu, int32_t nesterov, float eps, float grad_inv_scale, void* x, void* xt,
-                       int64_t ldx, int64_t ldxt, float* workspace, void* stream) {
+                       int64_t ldx, int64_t ldxt, float* workspace, const apexw_amp_dyn* amp, void* stream) {
   if (!buf || !g || !x || !workspace || rows <= 0 || cols <= 0) return APEXW_ERR_ARG;
+  if ((uintptr_t)amp & 15u) return APEXW_ERR_ALIGN;
   if (g_dtype != APEXW_F32 && g_dtype != APEXW_BF16 && g_dtype != APEXW_F16) return APEXW_ERR_DTYPE;
   // work matrix X is [min x max], X^T is [max x min] (optional)
   const int64_t lo = rows < cols ? rows : cols, hi = rows < cols ? cols : rows;
   if (ldx < hi || (xt && ldxt < lo)) return APEXW_ERR_ARG;
-  if (!(grad_inv_scale > 0.0f)) return APEXW_ERR_ARG;
+  if (!amp && !(grad_inv_scale > 0.0f)) return APEXW_ERR_ARG;
   return apexw_launch_muon_prepare(buf, g, g_dtype, rows, cols, mu, one_minus_mu, nesterov, eps, grad_inv_scale,
-                                   (uint16_t*)x, (uint16_t*)xt, ldx, ldxt, workspace, (hipStream_t)stream);
+                                   (uint16_t*)x, (uint16_t*)xt, ldx, ldxt, workspace, amp, (hipStream_t)stream);
 }
 
 int apexw_muon_apply(void* p, int32_t p_dtype, const void* u, int64_t rows, int64_t cols, int64_t ldu,
-                     int32_t u_transposed, float wd_factor, int32_t apply_wd, float neg_lr_eff, void* stream) {
+                     int32_t u_transposed, float wd_factor, int32_t apply_wd, float neg_lr_eff,
+                     const apexw_amp_dyn* amp, void* stream) {
+  if ((uintptr_t)amp & 15u) return APEXW_ERR_ALIGN;
   if (!p || !u || rows <= 0 || cols <= 0 || ldu < (u_transposed ? rows : cols)) return APEXW_ERR_ARG;
   if ((rows + 63) / 64 > 65535) return APEXW_ERR_ARG;   // grid y of the transposing kernel
   if (p_dtype != APEXW_F32 && p_dtype != APEXW_BF16 && p_dtype != APEXW_F16) return APEXW_ERR_DTYPE;
   return apexw_launch_muon_apply(p, p_dtype, (const uint16_t*)u, rows, cols, ldu, u_transposed != 0, wd_factor,
-                                 apply_wd, neg_lr_eff, (hipStream_t)stream);
+                                 apply_wd, neg_lr_eff, amp, (hipStream_t)stream);
 }
 
 int apexw_muon_coordwise(float* buf, const void* g, int32_t g_dtype, void* p, int32_t p_dtype, int64_t n, float mu,
                          float one_minus_mu, int32_t nesterov, float grad_inv_scale, float wd_factor,
-                         int32_t apply_wd, float neg_lr, void* stream) {
+                         int32_t apply_wd, float neg_lr, const apexw_amp_dyn* amp, void* stream) {
   if (!buf || !g || !p || n <= 0) return APEXW_ERR_ARG;
+  if ((uintptr_t)amp & 15u) return APEXW_ERR_ALIGN;
   if (g_dtype != APEXW_F32 && g_dtype != APEXW_BF16 && g_dtype != APEXW_F16) return APEXW_ERR_DTYPE;
   if (p_dtype != APEXW_F32 && p_dtype != APEXW_BF16 && p_dtype != APEXW_F16) return APEXW_ERR_DTYPE;
-  if (!(grad_inv_scale > 0.0f)) return APEXW_ERR_ARG;
+  if (!amp && !(grad_inv_scale > 0.0f)) return APEXW_ERR_ARG;
   return apexw_launch_muon_coordwise(buf, g, g_dtype, p, p_dtype, n, mu, one_minus_mu, nesterov, grad_inv_scale,
-                                     wd_factor, apply_wd, neg_lr, (hipStream_t)stream);
+                                     wd_factor, apply_wd, neg_lr, amp, (hipStream_t)stream);
 }
 
 int apexw_grad_clip_coef(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,

@@ -503,8 +503,10 @@ constexpr int kQueues = APEXW_GEMM_QUEUES;
 template <bool kC, bool kCt, bool kAdd, bool kNN>
 __global__ __launch_bounds__(256, 1) void gemm_nt_grouped_kernel(const apexw_gemm_problem* __restrict__ probs,
                                                                  const uint32_t* __restrict__ items,
-                                                                 const int32_t* __restrict__ queue_offsets) {
+                                                                 const int32_t* __restrict__ queue_offsets,
+                                                                 const apexw_amp_dyn* __restrict__ amp) {
   __shared__ __attribute__((aligned(16))) LdsStage lds[kStages];
+  if (amp && amp->skip) return;   // GradScaler found an inf / NaN: no product, no update
   const int q = (int)(blockIdx.x % kQueues), i = (int)(blockIdx.x / kQueues);
   const int begin = queue_offsets[q];
   if (i >= queue_offsets[q + 1] - begin) return;
@@ -572,7 +574,12 @@ APEXW_DEV float nesterov_source(float g, float m, float mu) {
 template <int GD, bool VEC>
 __global__ __launch_bounds__(256) void muon_momentum_kernel(float* __restrict__ buf, const void* __restrict__ grad,
                                                             int64_t n, float mu, float one_minus_mu, int nesterov,
-                                                            float inv, float* __restrict__ partial) {
+                                                            float inv, float* __restrict__ partial,
+                                                            const apexw_amp_dyn* __restrict__ amp) {
+  if (amp) {
+    if (amp->skip) return;
+    inv = amp->grad_inv_scale;
+  }
   float s = 0.0f;
   const int64_t tid = (int64_t)blockIdx.x * 256 + threadIdx.x, stride = (int64_t)gridDim.x * 256;
   const int64_t n_vec = VEC ? n / 8 * 8 : 0;
@@ -616,9 +623,14 @@ __global__ __launch_bounds__(256) void muon_normalize_kernel(const float* __rest
                                                              int64_t rows, int64_t cols, float mu, int nesterov,
                                                              float inv, const float* __restrict__ partial, int n_partial,
                                                              float eps, int tall, uint16_t* __restrict__ x,
-                                                             uint16_t* __restrict__ xt, int64_t ldx, int64_t ldxt) {
+                                                             uint16_t* __restrict__ xt, int64_t ldx, int64_t ldxt,
+                                                             const apexw_amp_dyn* __restrict__ amp) {
   __shared__ float red[4];
   __shared__ uint16_t tile[64][66];
+  if (amp) {
+    if (amp->skip) return;
+    inv = amp->grad_inv_scale;
+  }
   float s = 0.0f;
   for (int i = threadIdx.x; i < n_partial; i += 256) s += partial[i];
   s = wave_sum(s);
@@ -662,7 +674,9 @@ __global__ __launch_bounds__(256) void muon_normalize_kernel(const float* __rest
 template <int PD, bool VEC>
 __global__ __launch_bounds__(256) void muon_apply_kernel(void* __restrict__ p, const uint16_t* __restrict__ u,
                                                          int64_t rows, int64_t cols, int64_t ldu, float wd_factor,
-                                                         int apply_wd, float neg_lr_eff) {
+                                                         int apply_wd, float neg_lr_eff,
+                                                         const apexw_amp_dyn* __restrict__ amp) {
+  if (amp && amp->skip) return;
   const int64_t n = rows * cols;
   if constexpr (VEC) {
     for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8; i < n; i += (int64_t)gridDim.x * 256 * 8) {
@@ -694,8 +708,10 @@ __global__ __launch_bounds__(256) void muon_apply_kernel(void* __restrict__ p, c
 template <int PD>
 __global__ __launch_bounds__(256) void muon_apply_t_kernel(void* __restrict__ p, const uint16_t* __restrict__ u,
                                                            int64_t rows, int64_t cols, int64_t ldu, float wd_factor,
-                                                           int apply_wd, float neg_lr_eff) {
+                                                           int apply_wd, float neg_lr_eff,
+                                                           const apexw_amp_dyn* __restrict__ amp) {
   __shared__ uint16_t tile[64][66];
+  if (amp && amp->skip) return;
   const int64_t tr = (int64_t)blockIdx.y * 64, tc = (int64_t)blockIdx.x * 64;
   for (int e = threadIdx.x; e < 64 * 64; e += 256) {
     const int cc = e >> 6, rr = e & 63;
@@ -745,8 +761,13 @@ template <int GD, int PD>
 __global__ __launch_bounds__(kCwThreads) void muon_coordwise_kernel(float* __restrict__ buf, const void* __restrict__ grad,
                                                                     void* __restrict__ p, int64_t n, float mu,
                                                                     float one_minus_mu, int nesterov, float inv,
-                                                                    float wd_factor, int apply_wd, float neg_lr) {
+                                                                    float wd_factor, int apply_wd, float neg_lr,
+                                                                    const apexw_amp_dyn* __restrict__ amp) {
   __shared__ float red[kCwThreads / 64];
+  if (amp) {
+    if (amp->skip) return;
+    inv = amp->grad_inv_scale;
+  }
   const int64_t tid = threadIdx.x, stride = blockDim.x;
   float sum = 0.0f;
   for (int64_t i = tid; i < n; i += stride) {
@@ -776,16 +797,17 @@ __global__ __launch_bounds__(kCwThreads) void muon_coordwise_kernel(float* __res
 
 template <int GD>
 void launch_coordwise(float* buf, const void* g, void* p, int32_t p_dtype, int64_t n, float mu, float one_minus_mu,
-                      int nesterov, float inv, float wd_factor, int apply_wd, float neg_lr, hipStream_t stream) {
+                      int nesterov, float inv, float wd_factor, int apply_wd, float neg_lr, const apexw_amp_dyn* amp,
+                      hipStream_t stream) {
   if (p_dtype == APEXW_F32)
     hipLaunchKernelGGL((muon_coordwise_kernel<GD, APEXW_F32>), dim3(1), dim3(kCwThreads), 0, stream, buf, g, p, n, mu,
-                       one_minus_mu, nesterov, inv, wd_factor, apply_wd, neg_lr);
+                       one_minus_mu, nesterov, inv, wd_factor, apply_wd, neg_lr, amp);
   else if (p_dtype == APEXW_BF16)
     hipLaunchKernelGGL((muon_coordwise_kernel<GD, APEXW_BF16>), dim3(1), dim3(kCwThreads), 0, stream, buf, g, p, n, mu,
-                       one_minus_mu, nesterov, inv, wd_factor, apply_wd, neg_lr);
+                       one_minus_mu, nesterov, inv, wd_factor, apply_wd, neg_lr, amp);
   else
     hipLaunchKernelGGL((muon_coordwise_kernel<GD, APEXW_F16>), dim3(1), dim3(kCwThreads), 0, stream, buf, g, p, n, mu,
-                       one_minus_mu, nesterov, inv, wd_factor, apply_wd, neg_lr);
+                       one_minus_mu, nesterov, inv, wd_factor, apply_wd, neg_lr, amp);
 }
 
 int apexw_launch_gemm_nt(const uint16_t* a, const uint16_t* b, const uint16_t* et, uint16_t* c, uint16_t* ct,
@@ -810,32 +832,40 @@ int apexw_launch_gemm_nt(const uint16_t* a, const uint16_t* b, const uint16_t* e
 }
 
 int apexw_launch_gemm_grouped(const apexw_gemm_problem* probs, const uint32_t* items, const int32_t* offsets,
-                              int32_t n_wg, int32_t kind, hipStream_t stream) {
+                              int32_t n_wg, int32_t kind, const apexw_amp_dyn* amp, hipStream_t stream) {
   const dim3 grid(n_wg), block(256);
   switch (kind) {
     case APEXW_GEMM_OUT_C:
-      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, false, false, false>), grid, block, 0, stream, probs, items, offsets);
+      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, false, false, false>), grid, block, 0, stream, probs, items, offsets,
+                         amp);
       break;
     case APEXW_GEMM_OUT_C | APEXW_GEMM_ADD:
-      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, false, true, false>), grid, block, 0, stream, probs, items, offsets);
+      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, false, true, false>), grid, block, 0, stream, probs, items, offsets,
+                         amp);
       break;
     case APEXW_GEMM_OUT_CT:
-      hipLaunchKernelGGL((gemm_nt_grouped_kernel<false, true, false, false>), grid, block, 0, stream, probs, items, offsets);
+      hipLaunchKernelGGL((gemm_nt_grouped_kernel<false, true, false, false>), grid, block, 0, stream, probs, items, offsets,
+                         amp);
       break;
     case APEXW_GEMM_OUT_CT | APEXW_GEMM_ADD:
-      hipLaunchKernelGGL((gemm_nt_grouped_kernel<false, true, true, false>), grid, block, 0, stream, probs, items, offsets);
+      hipLaunchKernelGGL((gemm_nt_grouped_kernel<false, true, true, false>), grid, block, 0, stream, probs, items, offsets,
+                         amp);
       break;
     case APEXW_GEMM_OUT_C | APEXW_GEMM_OUT_CT:
-      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, true, false, false>), grid, block, 0, stream, probs, items, offsets);
+      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, true, false, false>), grid, block, 0, stream, probs, items, offsets,
+                         amp);
       break;
     case APEXW_GEMM_OUT_C | APEXW_GEMM_OUT_CT | APEXW_GEMM_ADD:
-      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, true, true, false>), grid, block, 0, stream, probs, items, offsets);
+      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, true, true, false>), grid, block, 0, stream, probs, items, offsets,
+                         amp);
       break;
     case APEXW_GEMM_OUT_C | APEXW_GEMM_KIND_NN:
-      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, false, false, true>), grid, block, 0, stream, probs, items, offsets);
+      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, false, false, true>), grid, block, 0, stream, probs, items, offsets,
+                         amp);
       break;
     case APEXW_GEMM_OUT_C | APEXW_GEMM_ADD | APEXW_GEMM_KIND_NN:
-      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, false, true, true>), grid, block, 0, stream, probs, items, offsets);
+      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, false, true, true>), grid, block, 0, stream, probs, items, offsets,
+                         amp);
       break;
     default:
       return APEXW_ERR_ARG;
@@ -848,49 +878,50 @@ int apexw_muon_partials(int64_t n) { return grid_for(n) < 1024 ? grid_for(n) : 1
 template <int GD>
 void launch_prepare(float* buf, const void* g, int64_t rows, int64_t cols, float mu, float one_minus_mu, int nesterov,
                     float eps, float inv, uint16_t* x, uint16_t* xt, int64_t ldx, int64_t ldxt, float* partial,
-                    hipStream_t stream) {
+                    const apexw_amp_dyn* amp, hipStream_t stream) {
   const int64_t n = rows * cols;
   const int nb = apexw_muon_partials(n);
   if ((((uintptr_t)buf | (uintptr_t)g) & 15u) == 0)
     hipLaunchKernelGGL((muon_momentum_kernel<GD, true>), dim3(nb), dim3(256), 0, stream, buf, g, n, mu, one_minus_mu,
-                       nesterov, inv, partial);
+                       nesterov, inv, partial, amp);
   else
     hipLaunchKernelGGL((muon_momentum_kernel<GD, false>), dim3(nb), dim3(256), 0, stream, buf, g, n, mu, one_minus_mu,
-                       nesterov, inv, partial);
+                       nesterov, inv, partial, amp);
   dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64));
   hipLaunchKernelGGL(muon_normalize_kernel<GD>, grid, dim3(256), 0, stream, buf, g, rows, cols, mu, nesterov, inv,
-                     partial, nb, eps, (int)(rows > cols), x, xt, ldx, ldxt);
+                     partial, nb, eps, (int)(rows > cols), x, xt, ldx, ldxt, amp);
 }
 
 int apexw_launch_muon_prepare(float* buf, const void* g, int32_t g_dtype, int64_t rows, int64_t cols, float mu,
                               float one_minus_mu, int32_t nesterov, float eps, float inv, uint16_t* x, uint16_t* xt,
-                              int64_t ldx, int64_t ldxt, float* partial, hipStream_t stream) {
+                              int64_t ldx, int64_t ldxt, float* partial, const apexw_amp_dyn* amp,
+                              hipStream_t stream) {
   if (g_dtype == APEXW_F32)
     launch_prepare<APEXW_F32>(buf, g, rows, cols, mu, one_minus_mu, nesterov, eps, inv, x, xt, ldx, ldxt, partial,
-                              stream);
+                              amp, stream);
   else if (g_dtype == APEXW_BF16)
     launch_prepare<APEXW_BF16>(buf, g, rows, cols, mu, one_minus_mu, nesterov, eps, inv, x, xt, ldx, ldxt, partial,
-                               stream);
+                               amp, stream);
   else
     launch_prepare<APEXW_F16>(buf, g, rows, cols, mu, one_minus_mu, nesterov, eps, inv, x, xt, ldx, ldxt, partial,
-                              stream);
+                              amp, stream);
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }
 
 int apexw_launch_muon_apply(void* p, int32_t p_dtype, const uint16_t* u, int64_t rows, int64_t cols, int64_t ldu,
                             int32_t u_transposed, float wd_factor, int32_t apply_wd, float neg_lr_eff,
-                            hipStream_t stream) {
+                            const apexw_amp_dyn* amp, hipStream_t stream) {
   if (u_transposed) {
     const dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64));
     if (p_dtype == APEXW_F32)
       hipLaunchKernelGGL(muon_apply_t_kernel<APEXW_F32>, grid, dim3(256), 0, stream, p, u, rows, cols, ldu, wd_factor,
-                         apply_wd, neg_lr_eff);
+                         apply_wd, neg_lr_eff, amp);
     else if (p_dtype == APEXW_BF16)
       hipLaunchKernelGGL(muon_apply_t_kernel<APEXW_BF16>, grid, dim3(256), 0, stream, p, u, rows, cols, ldu, wd_factor,
-                         apply_wd, neg_lr_eff);
+                         apply_wd, neg_lr_eff, amp);
     else
       hipLaunchKernelGGL(muon_apply_t_kernel<APEXW_F16>, grid, dim3(256), 0, stream, p, u, rows, cols, ldu, wd_factor,
-                         apply_wd, neg_lr_eff);
+                         apply_wd, neg_lr_eff, amp);
     return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
   }
   const int64_t n = rows * cols;
@@ -898,34 +929,34 @@ int apexw_launch_muon_apply(void* p, int32_t p_dtype, const uint16_t* u, int64_t
   const dim3 grid(grid_for(vec ? n / 8 : n));
   if (p_dtype == APEXW_F32) {
     if (vec) hipLaunchKernelGGL((muon_apply_kernel<APEXW_F32, true>), grid, dim3(256), 0, stream, p, u, rows, cols, ldu,
-                                wd_factor, apply_wd, neg_lr_eff);
+                                wd_factor, apply_wd, neg_lr_eff, amp);
     else hipLaunchKernelGGL((muon_apply_kernel<APEXW_F32, false>), grid, dim3(256), 0, stream, p, u, rows, cols, ldu,
-                            wd_factor, apply_wd, neg_lr_eff);
+                            wd_factor, apply_wd, neg_lr_eff, amp);
   } else if (p_dtype == APEXW_BF16) {
     if (vec) hipLaunchKernelGGL((muon_apply_kernel<APEXW_BF16, true>), grid, dim3(256), 0, stream, p, u, rows, cols,
-                                ldu, wd_factor, apply_wd, neg_lr_eff);
+                                ldu, wd_factor, apply_wd, neg_lr_eff, amp);
     else hipLaunchKernelGGL((muon_apply_kernel<APEXW_BF16, false>), grid, dim3(256), 0, stream, p, u, rows, cols, ldu,
-                            wd_factor, apply_wd, neg_lr_eff);
+                            wd_factor, apply_wd, neg_lr_eff, amp);
   } else {
     if (vec) hipLaunchKernelGGL((muon_apply_kernel<APEXW_F16, true>), grid, dim3(256), 0, stream, p, u, rows, cols, ldu,
-                                wd_factor, apply_wd, neg_lr_eff);
+                                wd_factor, apply_wd, neg_lr_eff, amp);
     else hipLaunchKernelGGL((muon_apply_kernel<APEXW_F16, false>), grid, dim3(256), 0, stream, p, u, rows, cols, ldu,
-                            wd_factor, apply_wd, neg_lr_eff);
+                            wd_factor, apply_wd, neg_lr_eff, amp);
   }
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }
 
 int apexw_launch_muon_coordwise(float* buf, const void* g, int32_t g_dtype, void* p, int32_t p_dtype, int64_t n,
                                 float mu, float one_minus_mu, int32_t nesterov, float inv, float wd_factor,
-                                int32_t apply_wd, float neg_lr, hipStream_t stream) {
+                                int32_t apply_wd, float neg_lr, const apexw_amp_dyn* amp, hipStream_t stream) {
   if (g_dtype == APEXW_F32)
     launch_coordwise<APEXW_F32>(buf, g, p, p_dtype, n, mu, one_minus_mu, nesterov, inv, wd_factor, apply_wd, neg_lr,
-                                stream);
+                                amp, stream);
   else if (g_dtype == APEXW_BF16)
     launch_coordwise<APEXW_BF16>(buf, g, p, p_dtype, n, mu, one_minus_mu, nesterov, inv, wd_factor, apply_wd, neg_lr,
-                                 stream);
+                                 amp, stream);
   else
     launch_coordwise<APEXW_F16>(buf, g, p, p_dtype, n, mu, one_minus_mu, nesterov, inv, wd_factor, apply_wd, neg_lr,
-                                stream);
+                                amp, stream);
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }

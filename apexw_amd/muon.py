@@ -19,7 +19,10 @@ Like the reference on a bf16-capable GPU, the Newton-Schulz work dtype is
 bf16 (apexw/muon.py:76-89).  Vectors and matrices with a dimension under 16
 take the reference's coordinate-wise update (``apexw_muon_coordwise``);
 non-contiguous parameters are stepped in a contiguous copy that is written
-back.  Quantised momentum (precision "8bit"/"ultra"),
+back.  Under GradScaler, found_inf and the scale are read by the kernels
+(each takes the step's ``apexw_amp_dyn``): a skipped step writes nothing and
+the host's step counters are corrected when ``state`` is next looked at.
+Quantised momentum (precision "8bit"/"ultra"),
 AdEMAMix (beta3), cautious masking, grad centralization, the Polar Express
 coefficients and scale_mode="rms" raise ``NotImplementedError``.
 """
@@ -154,7 +157,7 @@ class NSPlan:
             out.append((to_dev(probs), to_dev(items), to_dev(offsets), n_wg, kind, probs if fin else None, fin))
         return out
 
-    def run(self, stream, applies=None, keep_result=True):
+    def run(self, stream, applies=None, keep_result=True, amp=None):
         """Run every launch on `stream`.  applies[j][e] = (p, dtype code, rows, cols,
         transposed, apply_wd, wd_factor, neg_lr) for entry e of workspace j: that
         matrix's final X' updates p in its epilogue.  Without applies the final X'
@@ -166,7 +169,7 @@ class NSPlan:
                     if fin and applies is not None:
                         probs = self._upload_applies(lib, probs, host, fin, applies, keep_result)
                     _lib.check(lib.apexw_gemm_nt_grouped(probs.data_ptr(), items.data_ptr(), offsets.data_ptr(),
-                                                         n_wg, kind, stream), "apexw_gemm_nt_grouped")
+                                                         n_wg, kind, amp, stream), "apexw_gemm_nt_grouped")
 
     def _upload_applies(self, lib, dev_probs, host, fin, applies, keep_result):
         tbl = host.copy()
@@ -231,6 +234,21 @@ class ApexMuon(Optimizer):
         self._ws = {}
         self._ns_plans = {}
         self._copies = []
+        self._amp_init()
+        self.state = R.StateMap(self, self.state)
+
+    def __setstate__(self, state):
+        super().__setstate__(state)
+        self._amp_init()
+        self.state = R.StateMap(self, dict.items(self.state))
+
+    def _amp_init(self):
+        # GradScaler steps read on the device: per step, the stepped states and a
+        # pinned copy of found_inf, until the host has seen the copy (_amp_drain)
+        self._amp_unfolded = False
+        self._amp_pending = []
+        self._amp_stepped = None
+        self._amp_dev = None
 
     # ------------------------------------------------------------------ state
     def _init_param_state(self, p):
@@ -287,15 +305,24 @@ class ApexMuon(Optimizer):
                 loss = closure()
         found_inf = getattr(self, "found_inf", None)
         grad_scale = getattr(self, "grad_scale", None)
+        self._amp_unfolded = False        # no waits in the lookups of the step itself
+        amp = None
         try:
-            if found_inf is not None and float(found_inf) != 0.0:
-                return loss
             # AMP: the grads are unscaled inside the momentum kernel (the reference
-            # unscales p.grad in place first, apexw/muon.py:566-590)
+            # unscales p.grad in place first, apexw/muon.py:566-590).  With found_inf
+            # and the scale on the parameters' device, the kernels read both there
+            # (the reference reads them on the host, :557-577)
             inv_scale = 1.0
-            if grad_scale is not None:
-                inv_scale = (float(grad_scale.reciprocal().item()) if torch.is_tensor(grad_scale)
-                             else 1.0 / float(grad_scale))
+            if self._amp_on_device(grad_scale, found_inf):
+                amp = self._amp_prepare(grad_scale, found_inf)
+            else:
+                if found_inf is not None and float(found_inf) != 0.0:
+                    return loss
+                if grad_scale is not None:
+                    inv_scale = (float(grad_scale.reciprocal().item()) if torch.is_tensor(grad_scale)
+                                 else 1.0 / float(grad_scale))
+            self._amp_stepped = [] if amp is not None else None
+            amp_ptr = amp.data_ptr() if amp is not None else None
             jobs = []
             # a non-contiguous parameter is stepped in a contiguous copy, written back afterwards
             self._copies = []
@@ -312,7 +339,7 @@ class ApexMuon(Optimizer):
                     rows = p.shape[0] if p.dim() >= 1 else 1
                     if p.dim() < 2 or min(rows, p.numel() // rows) < 16:
                         # vectors and dimensions under 16: coordinate-wise update (apexw/muon.py:841-847)
-                        self._coordwise(p, group, inv_scale)
+                        self._coordwise(p, group, inv_scale, amp_ptr)
                     else:
                         matrices.append(p)
                 shapes = defaultdict(list)
@@ -320,7 +347,7 @@ class ApexMuon(Optimizer):
                     shapes[tuple(p.shape)].append(p)
                 for shape, plist in shapes.items():
                     # the reference batches same-shape matrices on the GPU (apexw/muon.py:593-615)
-                    jobs.append(self._prepare(gi, shape, plist, group, inv_scale))
+                    jobs.append(self._prepare(gi, shape, plist, group, inv_scale, amp_ptr))
             # Newton-Schulz of every matrix, grouped per device; matrices are
             # independent, so running all momenta first and all updates last
             # gives each parameter the result of the reference's per-shape loop
@@ -334,19 +361,82 @@ class ApexMuon(Optimizer):
             for dev, djobs in by_dev.items():
                 plan = self._ns_plan(djobs, dev)
                 applies = [self._apply_args(j) for j in djobs]
-                plan.run(torch.cuda.current_stream(dev).cuda_stream, applies, self.keep_ns_result)
+                plan.run(torch.cuda.current_stream(dev).cuda_stream, applies, self.keep_ns_result, amp_ptr)
             for j in jobs:
                 if j["steps"] == 0:
-                    self._apply(j)
+                    self._apply(j, amp_ptr)
             for p, work in self._copies:
-                p.copy_(work)
+                p.copy_(work)   # after a skipped step, work still equals p
+            if amp is not None:
+                self._amp_record(found_inf)
         finally:
             self._copies = []
+            self._amp_stepped = None
             self.grad_scale = None
             self.found_inf = None
+            self._amp_unfolded = bool(self._amp_pending)
         return loss
 
-    def _prepare(self, gi, shape, plist, group, inv_scale=1.0):
+    # ------------------------------------------------------- AMP on the device
+    def _amp_on_device(self, grad_scale, found_inf):
+        """found_inf (and the scale, if any) are one-element tensors on the device
+        of every parameter stepped this time: the kernels read them there."""
+        if not (torch.is_tensor(found_inf) and found_inf.is_cuda and found_inf.numel() == 1):
+            return False
+        if grad_scale is not None and not (torch.is_tensor(grad_scale) and grad_scale.is_cuda
+                                           and grad_scale.numel() == 1):
+            return False
+        dev = found_inf.device
+        return all(p.device == dev for g in self.param_groups for p in g["params"] if p.grad is not None)
+
+    def _amp_prepare(self, grad_scale, found_inf):
+        """This step's skip flag and 1 / scale as a device apexw_amp_dyn
+        (apexw_amp_prepare; the Muon kernels read only skip and grad_inv_scale)."""
+        self._amp_drain(wait=False)
+        dev = found_inf.device
+        if self._amp_dev is None or self._amp_dev[0] != dev:
+            self._amp_dev = (dev, torch.zeros(1, dtype=torch.int32, device=dev),
+                             torch.empty(_lib.AMP_DYN_BYTES // 4, dtype=torch.float32, device=dev),
+                             torch.ones(1, dtype=torch.float32, device=dev))
+        _, skips, dyn, one = self._amp_dev
+        scale = one if grad_scale is None else grad_scale.detach().reshape(1).to(dev, torch.float32).contiguous()
+        fi = found_inf.detach().reshape(1).to(dev, torch.float32).contiguous()
+        launch = np.zeros(1, dtype=_lib.AMP_LAUNCH_DTYPE)
+        launch["beta1"], launch["beta2"], launch["step"] = 0.5, 0.5, 1.0
+        lib = _lib.load()
+        _lib.check(lib.apexw_amp_prepare(fi.data_ptr(), scale.data_ptr(), skips.data_ptr(), 0, launch.ctypes.data, 1,
+                                         dyn.data_ptr(), torch.cuda.current_stream(dev).cuda_stream),
+                   "apexw_amp_prepare")
+        return dyn
+
+    def _amp_record(self, found_inf):
+        """Keep this step's stepped states with an asynchronous copy of found_inf."""
+        flag = torch.empty(1, dtype=torch.float32, pin_memory=True)
+        flag.copy_(found_inf.detach().reshape(1), non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(found_inf.device))
+        self._amp_pending.append((ev, flag, self._amp_stepped))
+
+    def _amp_drain(self, wait):
+        """Take back the step counts of the skipped steps whose found_inf copy has
+        arrived (wait: of every pending step, after waiting for the copies)."""
+        while self._amp_pending:
+            ev, flag, stepped = self._amp_pending[0]
+            if wait:
+                ev.synchronize()
+            elif not ev.query():
+                break
+            self._amp_pending.pop(0)
+            if float(flag[0]) != 0.0:
+                for st in stepped:
+                    st["step"] -= 1
+
+    def _fold_amp_skips(self):
+        """Make every step counter exact (StateMap's first lookup after a step)."""
+        self._amp_unfolded = False
+        self._amp_drain(wait=True)
+
+    def _prepare(self, gi, shape, plist, group, inv_scale=1.0, amp=None):
         """Momentum update and normalised bf16 work matrix (both layouts) of one same-shape batch."""
         lib = _lib.load()
         p0 = plist[0]
@@ -358,12 +448,12 @@ class ApexMuon(Optimizer):
         mu = float(group["momentum"])
         for i, p in enumerate(plist):
             st = self._init_param_state(p)
-            st["step"] += 1
+            self._count_step(st)
             g = p.grad if p.grad.is_contiguous() else p.grad.contiguous()
             _lib.check(lib.apexw_muon_prepare(
                 st["momentum"].data_ptr(), g.data_ptr(), _dtype_code(g.dtype), rows, cols, mu, 1.0 - mu,
                 int(bool(group["nesterov"])), NS_EPS, inv_scale, ws.x[0][i].data_ptr(), None, ws.np_, 0,
-                ws.partial[i].data_ptr(), stream), "apexw_muon_prepare")
+                ws.partial[i].data_ptr(), amp, stream), "apexw_muon_prepare")
         return {"plist": plist, "targets": [self._target(p) for p in plist], "group": group, "ws": ws,
                 "rows": rows, "cols": cols, "steps": int(group["ns_steps"]), "batched": len(plist) > 1}
 
@@ -389,12 +479,17 @@ class ApexMuon(Optimizer):
         self._copies.append((p, work))
         return work
 
-    def _coordwise(self, p, group, inv_scale):
+    def _count_step(self, st):
+        st["step"] += 1
+        if self._amp_stepped is not None:
+            self._amp_stepped.append(st)
+
+    def _coordwise(self, p, group, inv_scale, amp=None):
         """The reference's coordinate-wise fallback (apexw/muon.py:841-858): momentum,
         U = s / (std(s) + 1e-7), p -= lr * 0.05 * U after the decoupled decay."""
         lib = _lib.load()
         st = self._init_param_state(p)
-        st["step"] += 1
+        self._count_step(st)
         mu = float(group["momentum"])
         lr, wd = float(group["lr"]), float(group["weight_decay"])
         g = p.grad if p.grad.is_contiguous() else p.grad.contiguous()
@@ -403,7 +498,7 @@ class ApexMuon(Optimizer):
         _lib.check(lib.apexw_muon_coordwise(
             st["momentum"].data_ptr(), g.data_ptr(), _dtype_code(g.dtype), dst.data_ptr(), _dtype_code(p.dtype),
             p.numel(), mu, 1.0 - mu, int(bool(group["nesterov"])), inv_scale, 1.0 - lr * wd, int(wd != 0.0),
-            _round_to(p.dtype, -lr * 0.05), stream), "apexw_muon_coordwise")
+            _round_to(p.dtype, -lr * 0.05), amp, stream), "apexw_muon_coordwise")
 
     def _apply_args(self, job):
         """Per batch entry, the fused update of the final Newton-Schulz product (NSPlan.run).
@@ -413,7 +508,7 @@ class ApexMuon(Optimizer):
         return [(t.data_ptr(), _dtype_code(t.dtype), rows, cols, rows > cols, apply_wd, wd_factor, neg_lr)
                 for t in job["targets"]]
 
-    def _apply(self, job):
+    def _apply(self, job, amp=None):
         """The update as a separate pass over the work matrix (ns_steps == 0)."""
         lib = _lib.load()
         plist, ws, rows, cols = job["plist"], job["ws"], job["rows"], job["cols"]
@@ -422,7 +517,8 @@ class ApexMuon(Optimizer):
         u_buf = ws.x[job["steps"] % 2]           # ping-pong slot of the Newton-Schulz result
         for i, p in enumerate(job["targets"]):
             _lib.check(lib.apexw_muon_apply(p.data_ptr(), _dtype_code(p.dtype), u_buf[i].data_ptr(), rows, cols,
-                                            ws.np_, int(rows > cols), wd_factor, int(apply_wd), neg_lr, stream),
+                                            ws.np_, int(rows > cols), wd_factor, int(apply_wd), neg_lr, amp,
+                                            stream),
                        "apexw_muon_apply")
 
     def get_state_memory_mb(self):

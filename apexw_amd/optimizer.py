@@ -43,46 +43,6 @@ _UNSUPPORTED_FLAGS = ("amsgrad", "nesterov", "cautious", "lion", "maximize",
                       "capturable", "differentiable", "auto_pack")
 
 
-class _StateMap(defaultdict):
-    """``optimizer.state`` with step counters that are exact when looked at.
-
-    A step whose GradScaler found_inf is read by the kernels advances the host's
-    counters optimistically; the device counts the skipped steps.  The first
-    lookup of a state after such a step subtracts them (one wait for the count),
-    so ``opt.state[p]["step"]`` reads as the reference's, whose skipped steps
-    leave it alone.  Inside ``step()`` the lookups do not wait (the owner's
-    ``_amp_unfolded`` is cleared meanwhile)."""
-
-    def __init__(self, owner, items=()):
-        super().__init__(dict, items)
-        self._owner = owner
-
-    def _fold(self):
-        o = self._owner
-        if o is not None and o._amp_unfolded:
-            o._fold_amp_skips()
-
-    def __getitem__(self, key):
-        self._fold()
-        return super().__getitem__(key)
-
-    def get(self, key, default=None):
-        self._fold()
-        return super().get(key, default)
-
-    def items(self):
-        self._fold()
-        return super().items()
-
-    def values(self):
-        self._fold()
-        return super().values()
-
-    def __reduce__(self):
-        # pickles and deep copies hold a plain defaultdict(dict), as torch's optimizers do
-        return defaultdict, (dict,), None, None, iter(dict.items(self))
-
-
 class ApexW(Optimizer):
     """Memory-efficient AdamW with compact (bf16) or 8-bit (NF4 + log-uint8) state.
 
@@ -193,7 +153,7 @@ class ApexW(Optimizer):
                         int4_m=int4_m, six_bit=six_bit)
         super().__init__(params, defaults)
         self._amp_unfolded = False
-        self.state = _StateMap(self, self.state)
+        self.state = R.StateMap(self, self.state)
         self._plans = {}
         # seed of the counter-based rounding RNG (drawn from torch's generator, so
         # torch.manual_seed makes runs reproducible)
@@ -217,7 +177,7 @@ class ApexW(Optimizer):
     def __setstate__(self, state):
         super().__setstate__(state)
         self._amp_unfolded = False
-        self.state = _StateMap(self, dict.items(self.state))
+        self.state = R.StateMap(self, dict.items(self.state))
         for group in self.param_groups:
             group.setdefault("decay_norm_only", True)
             group.setdefault("clip_grad_norm", None)

@@ -18,9 +18,13 @@ the same for ``apexw_amd``:
 ``install()`` applies these patches once per process, and only when an 8-bit
 ApexW turns its in-backward steps on (the reference patches at import); an
 application that never takes that path sees torch unchanged.
+
+``StateMap`` is the ``optimizer.state`` of ApexW and ApexMuon under GradScaler
+steps read on the device.
 """
 
 import weakref
+from collections import defaultdict
 
 import torch
 import torch.nn as nn
@@ -33,6 +37,47 @@ fp16_active = False
 amp_scaled_this_backward = False
 last_amp_scale = None
 _installed = False
+
+
+class StateMap(defaultdict):
+    """``optimizer.state`` with step counters that are exact when looked at
+    (ApexW, ApexMuon).
+
+    A step whose GradScaler found_inf is read by the kernels advances the host's
+    counters optimistically; the device knows which steps were skipped.  The
+    first lookup of a state after such a step has the owner subtract them (its
+    ``_fold_amp_skips``, one wait), so ``opt.state[p]["step"]`` reads as the
+    reference's, whose skipped steps leave it alone.  Inside ``step()`` the
+    lookups do not wait (the owner's ``_amp_unfolded`` is cleared meanwhile)."""
+
+    def __init__(self, owner, items=()):
+        super().__init__(dict, items)
+        self._owner = owner
+
+    def _fold(self):
+        o = self._owner
+        if o is not None and o._amp_unfolded:
+            o._fold_amp_skips()
+
+    def __getitem__(self, key):
+        self._fold()
+        return super().__getitem__(key)
+
+    def get(self, key, default=None):
+        self._fold()
+        return super().get(key, default)
+
+    def items(self):
+        self._fold()
+        return super().items()
+
+    def values(self):
+        self._fold()
+        return super().values()
+
+    def __reduce__(self):
+        # pickles and deep copies hold a plain defaultdict(dict), as torch's optimizers do
+        return defaultdict, (dict,), None, None, iter(dict.items(self))
 
 
 def _is_downcast(p):

@@ -44,7 +44,7 @@
 extern "C" {
 #endif
 
-#define APEXW_ABI_VERSION 17
+#define APEXW_ABI_VERSION 18
 
 /* status codes */
 enum apexw_status {
@@ -511,10 +511,12 @@ int apexw_gemm_grouped_schedule(const apexw_gemm_problem* problems, int32_t n_pr
  * dispatched round-robin over the XCDs, so each XCD works through one queue).
  * problems, items and queue_offsets are device copies of the arrays validated
  * and built by apexw_gemm_grouped_schedule, n_workgroups and kind its outputs;
- * like the tensor tables of the step, they are trusted as built.
+ * like the tensor tables of the step, they are trusted as built.  amp: NULL,
+ * or GradScaler's step read on the device (apexw_amp_prepare): every
+ * workgroup returns before any write when amp->skip.
  */
 int apexw_gemm_nt_grouped(const apexw_gemm_problem* problems, const uint32_t* items, const int32_t* queue_offsets,
-                          int32_t n_workgroups, int32_t kind, void* stream);
+                          int32_t n_workgroups, int32_t kind, const apexw_amp_dyn* amp, void* stream);
 
 /* fp32 workspace (floats) apexw_muon_prepare needs for a [rows x cols] matrix. */
 int64_t apexw_muon_workspace_floats(int64_t rows, int64_t cols);
@@ -529,11 +531,17 @@ int64_t apexw_muon_workspace_floats(int64_t rows, int64_t cols);
  * X is written as the wide work matrix [min x max] to x (ldx) and, when xt is
  * not NULL, as its transpose [max x min] to xt (ldxt): when rows > cols the
  * work matrix is s^T.  Elements of x / xt outside the matrix are not written
- * (keep them zero).
+ * (keep them zero).  amp (NULL or 16-byte aligned): GradScaler's step read on
+ * the device (apexw_amp_prepare), in place of the host's found_inf.item() /
+ * grad_scale.reciprocal().item() (apexw/muon.py:557-577): nothing is written
+ * when amp->skip, and amp->grad_inv_scale replaces grad_inv_scale.  The same
+ * argument of apexw_muon_apply, apexw_muon_coordwise and apexw_gemm_nt_grouped
+ * skips the rest of the step.
  */
 int apexw_muon_prepare(float* buf, const void* g, int32_t g_dtype, int64_t rows, int64_t cols,
                        float mu, float one_minus_mu, int32_t nesterov, float eps, float grad_inv_scale,
-                       void* x, void* xt, int64_t ldx, int64_t ldxt, float* workspace, void* stream);
+                       void* x, void* xt, int64_t ldx, int64_t ldxt, float* workspace, const apexw_amp_dyn* amp,
+                       void* stream);
 
 /*
  * p = round(round(p * wd_factor) + neg_lr_eff * U)   (the decay only if apply_wd)
@@ -543,7 +551,8 @@ int apexw_muon_prepare(float* buf, const void* g, int32_t g_dtype, int64_t rows,
  * even.
  */
 int apexw_muon_apply(void* p, int32_t p_dtype, const void* u, int64_t rows, int64_t cols, int64_t ldu,
-                     int32_t u_transposed, float wd_factor, int32_t apply_wd, float neg_lr_eff, void* stream);
+                     int32_t u_transposed, float wd_factor, int32_t apply_wd, float neg_lr_eff,
+                     const apexw_amp_dyn* amp, void* stream);
 
 /*
  * Coordinate-wise Muon update of one parameter that Newton-Schulz does not take
@@ -558,7 +567,7 @@ int apexw_muon_apply(void* p, int32_t p_dtype, const void* u, int64_t rows, int6
  */
 int apexw_muon_coordwise(float* buf, const void* g, int32_t g_dtype, void* p, int32_t p_dtype, int64_t n, float mu,
                          float one_minus_mu, int32_t nesterov, float grad_inv_scale, float wd_factor,
-                         int32_t apply_wd, float neg_lr, void* stream);
+                         int32_t apply_wd, float neg_lr, const apexw_amp_dyn* amp, void* stream);
 
 /* ------------------------------------------------------------------------- */
 /* Optimizer state across precision modes                                     */

@@ -248,8 +248,8 @@ def test_schedule_rejects_invalid_problems():
     with pytest.raises(_lib.ApexwError):
         _lib.gemm_schedule(arr)
     # the launch itself rejects bad kinds and null tables before enqueueing anything
-    assert lib.apexw_gemm_nt_grouped(None, None, None, 16, 3, None) == 1
-    assert lib.apexw_gemm_nt_grouped(16, 16, 16, 16, 4, None) == 1     # no output in the kind
-    assert lib.apexw_gemm_nt_grouped(16, 16, 16, 12, 3, None) == 1     # grid not a multiple of the queues
-    assert lib.apexw_gemm_nt_grouped(16, 16, 16, 16, 2 | 8, None) == 1  # [k x n] B with a transposed output
-    assert lib.apexw_gemm_nt_grouped(16, 18, 16, 16, 3, None) == 4     # misaligned table
+    assert lib.apexw_gemm_nt_grouped(None, None, None, 16, 3, None, None) == 1
+    assert lib.apexw_gemm_nt_grouped(16, 16, 16, 16, 4, None, None) == 1     # no output in the kind
+    assert lib.apexw_gemm_nt_grouped(16, 16, 16, 12, 3, None, None) == 1     # grid not a multiple of the queues
+    assert lib.apexw_gemm_nt_grouped(16, 16, 16, 16, 2 | 8, None, None) == 1  # [k x n] B with a transposed output
+    assert lib.apexw_gemm_nt_grouped(16, 18, 16, 16, 3, None, None) == 4     # misaligned table

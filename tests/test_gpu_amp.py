@@ -229,3 +229,77 @@ def test_device_amp_equals_host_amp_with_skipped_steps(precision):
                 assert torch.equal(sa[k], sb[k]), k
         assert float(sa["step"]) == float(sb["step"]) == taken
     assert all(float(st["step"]) == taken for st in sd["state"].values())
+
+
+def test_muon_device_amp_equals_host_amp_with_skipped_steps():
+    """ApexMuon under GradScaler: the device path (found_inf and the scale read by
+    the kernels) against the host path (the same values as CPU tensors, read on
+    the host like the reference, apexw/muon.py:557-577), over steps some of which
+    found an inf: identical parameters and momenta, and step counters that count
+    only the steps taken.  The parameters cover the grouped Newton-Schulz with its
+    fused update (wide, tall, non-contiguous), a group with ns_steps=0 (the
+    separate update pass) and the coordinate-wise fallback (a vector, a matrix
+    with a dimension under 16)."""
+    _need_gpu()
+    from apexw_amd.muon import ApexMuon
+    print("muon device vs host amp", flush=True)
+    gen = torch.Generator().manual_seed(31)
+    shapes = [(256, 384), (384, 256), (300,), (8, 40)]
+    host = [torch.randn(s, generator=gen) * 0.02 for s in shapes]
+    host_t = torch.randn(384, 128, generator=gen) * 0.02
+    host_z = torch.randn(128, 256, generator=gen) * 0.02
+
+    def params():
+        ps = [torch.nn.Parameter(h.cuda().bfloat16()) for h in host]
+        ps.append(torch.nn.Parameter(host_t.cuda().bfloat16().t()))     # non-contiguous [128 x 384]
+        return ps, torch.nn.Parameter(host_z.cuda())
+
+    (pa, za), (pb, zb) = params(), params()
+    kw = dict(lr=0.02, weight_decay=0.1, scale_mode="rms_matched")
+    oa = ApexMuon([{"params": pa}, {"params": [za], "ns_steps": 0}], **kw)
+    ob = ApexMuon([{"params": pb}, {"params": [zb], "ns_steps": 0}], **kw)
+    scale = 4096.0
+    infs = [0, 1, 0, 0, 1, 1, 0]
+    for inf in infs:
+        for a, b in zip(pa + [za], pb + [zb]):
+            g = torch.randn(a.shape, generator=gen) * 1e-3 * scale
+            if inf:
+                g.view(-1)[7] = float("inf")
+            a.grad, b.grad = g.to("cuda", a.dtype), g.to("cuda", b.dtype)
+        oa.grad_scale, oa.found_inf = torch.tensor(scale, device="cuda"), torch.tensor(float(inf), device="cuda")
+        ob.grad_scale, ob.found_inf = torch.tensor(scale), torch.tensor(float(inf))
+        oa.step()
+        ob.step()
+    sd = oa.state_dict()
+    torch.cuda.synchronize()
+    taken = len(infs) - sum(infs)
+    for a, b in zip(pa + [za], pb + [zb]):
+        assert torch.equal(a, b)
+        assert torch.equal(oa.state[a]["momentum"], ob.state[b]["momentum"])
+        assert oa.state[a]["step"] == ob.state[b]["step"] == taken
+    assert all(st["step"] == taken for st in sd["state"].values())
+
+
+def test_muon_grad_scaler_step_reads_nothing_on_the_host():
+    """After its first step, ApexMuon's GradScaler step (momentum, grouped
+    Newton-Schulz with the fused update, coordinate-wise vectors) launches without
+    a host synchronisation, and its step counters are exact when looked at."""
+    _need_gpu()
+    from apexw_amd.muon import ApexMuon
+    torch.manual_seed(5)
+    m = torch.nn.Sequential(torch.nn.Linear(64, 128), torch.nn.GELU(), torch.nn.Linear(128, 64)).cuda()
+    opt = ApexMuon(m.parameters(), lr=0.02, weight_decay=0.01)
+    scaler = torch.amp.GradScaler("cuda", init_scale=2.0 ** 12)
+    x = torch.randn(8, 64, device="cuda")
+    for it in range(3):
+        opt.zero_grad()
+        scaler.scale(m(x).square().mean()).backward()
+        if it > 0:
+            torch.cuda.set_sync_debug_mode("error")
+        try:
+            scaler.step(opt)
+        finally:
+            torch.cuda.set_sync_debug_mode("default")
+        scaler.update()
+    torch.cuda.synchronize()
+    assert all(opt.state[p]["step"] == 3 for p in m.parameters())

@@ -488,7 +488,7 @@ def _ns_launch(plan, phase, stream):
     lib = _lib.load()
     for probs, items, offsets, n_wg, kind, *_ in plan.iters[0][phase]:
         _lib.check(lib.apexw_gemm_nt_grouped(probs.data_ptr(), items.data_ptr(), offsets.data_ptr(), n_wg, kind,
-                                             stream), "apexw_gemm_nt_grouped")
+                                             None, stream), "apexw_gemm_nt_grouped")
 
 
 @pytest.mark.parametrize("rows,cols", [(4096, 4096), (4096, 14336)])

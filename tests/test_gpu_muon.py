@@ -196,7 +196,7 @@ def _grouped(lib, rows, cus=0):
         assert np.any((items >> 22) & 3), "no half tiles in the schedule"
     dev = lambda a: torch.from_numpy(a.view(np.uint8).copy()).cuda()  # noqa: E731
     dp, di, do = dev(probs), dev(items), dev(offsets)
-    st = lib.apexw_gemm_nt_grouped(dp.data_ptr(), di.data_ptr(), do.data_ptr(), n_wg, kind,
+    st = lib.apexw_gemm_nt_grouped(dp.data_ptr(), di.data_ptr(), do.data_ptr(), n_wg, kind, None,
                                    torch.cuda.current_stream().cuda_stream)
     assert st == 0
     torch.cuda.synchronize()

@@ -32,6 +32,9 @@ CASES = {
     "compact_bf16_clip_rne": (RAGGED, torch.bfloat16, 6, 4,
                               dict(lr=1e-3, weight_decay=0.1, stochastic_rounding=False, clip_grad_norm=1.0),
                               RAGGED_SCALES, (4,)),
+    "compact_fp32_clip_rne": (RAGGED, torch.float32, 6, 8,
+                              dict(lr=1e-3, weight_decay=0.1, stochastic_rounding=False, clip_grad_norm=1.0),
+                              RAGGED_SCALES, (4,)),
     "q8_bf16_rne": (Q8_SHAPES, torch.bfloat16, 5, 5,
                     dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, precision="8bit", stochastic_rounding=False),
                     None, ()),

@@ -1,7 +1,11 @@
 """GPU parity: the HIP step against the reference's own trajectories and the CPU oracle.
 
 Tolerances (round to nearest, SR off):
-  * fp32 params:  |d| <= 1e-6*|ref| + 1e-9 (the absolute floor covers p ~ 0)
+  * fp32 params:  |d| <= 1e-6*|ref| + 1e-9 (the absolute floor covers p ~ 0); under
+    the global-norm clip 1e-5*|ref| + 2^-8*S*lr + 1e-9 after S steps: the reference's
+    CPU fp32 norm reduction drifts from the exact norm (up to ~1e-5 relative), so the
+    coefficient differs by that much, which can flip the last bit of a bf16 m or v
+    (held to 1 ulp) and so move a step's update (|u| <= ~lr) by 2^-8 of itself
   * bf16 tensors (params, m, v): <= 1 bf16 ulp; fp16 tensors <= 1 fp16 ulp
   * fp32 v (compact):             |d| <= 1e-6*|ref| + 1e-12
   * 8-bit codes: NF4/INT8/log-u8 differ by <= 1 code; block scales within 1e-6 relative
@@ -25,6 +29,7 @@ from golden_replay import CASES, bf16_ulp_diff, initial_params, replay, state_ke
 pytestmark = pytest.mark.gpu
 
 dev = "cuda"
+FP32_CLIP_CASES = {"compact_fp32_clip_rne"}   # fp32 grads through the global-norm clip
 
 
 def _require_gpu():
@@ -59,14 +64,14 @@ def _cmp_f16(got, ref, ulps=1, what=""):
     assert int(d.max()) <= ulps, f"{what}: {int(d.max())} fp16 ulps ({int((d > ulps).sum())} elements)"
 
 
-def _cmp_tensor(got, gold_arr, what):
+def _cmp_tensor(got, gold_arr, what, rel=1e-6, floor=1e-9):
     if got.dtype == torch.bfloat16:
         _cmp_bf16(got.reshape(-1), to_torch(gold_arr, torch.bfloat16).reshape(-1), what=what)
     elif got.dtype == torch.float16:
         _cmp_f16(got.reshape(-1), torch.from_numpy(gold_arr).reshape(-1), what=what)
     elif got.dtype == torch.float32:
-        _cmp_f32(got.reshape(-1), torch.from_numpy(gold_arr).reshape(-1), floor=1e-12 if what.startswith("v") else 1e-9,
-                 what=what)
+        _cmp_f32(got.reshape(-1), torch.from_numpy(gold_arr).reshape(-1), rel=rel,
+                 floor=1e-12 if what.startswith("v") else floor, what=what)
     else:
         a = got.cpu().reshape(-1).to(torch.int32)
         b = torch.from_numpy(gold_arr.reshape(-1).astype(np.int32))
@@ -86,11 +91,15 @@ def test_hip_step_matches_reference_trajectory(name):
     if "flags_0" not in gold:
         _cmp_factored(params, opt, gold, initial_params(name), CASES[name][2])
         return
+    rel, floor = 1e-6, 1e-9
+    if name in FP32_CLIP_CASES:
+        steps, kw = CASES[name][2], CASES[name][4]
+        rel, floor = 1e-5, 2.0 ** -8 * steps * kw["lr"] + 1e-9
     for i, p in enumerate(params):
         st = opt.state[p]
-        _cmp_tensor(p.data, gold[f"p_{i}"], f"p_{i}")
-        _cmp_tensor(st["exp_avg"], gold[f"m_{i}"], f"m_{i}")
-        _cmp_tensor(st["exp_avg_sq"], gold[f"v_{i}"], f"v_{i}")
+        _cmp_tensor(p.data, gold[f"p_{i}"], f"p_{i}", rel, floor)
+        _cmp_tensor(st["exp_avg"], gold[f"m_{i}"], f"m_{i}", rel)
+        _cmp_tensor(st["exp_avg_sq"], gold[f"v_{i}"], f"v_{i}", rel)
         if f"ms_{i}" in gold:
             _cmp_f32(st["exp_avg_scales"].reshape(-1), torch.from_numpy(gold[f"ms_{i}"]).reshape(-1), floor=0,
                      rel=1e-6, what=f"ms_{i}")

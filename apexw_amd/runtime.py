@@ -76,7 +76,9 @@ class StateMap(defaultdict):
         return super().values()
 
     def __reduce__(self):
-        # pickles and deep copies hold a plain defaultdict(dict), as torch's optimizers do
+        # pickles and deep copies hold a plain defaultdict(dict), as torch's optimizers
+        # do, with the step counters made exact first
+        self._fold()
         return defaultdict, (dict,), None, None, iter(dict.items(self))
 
 

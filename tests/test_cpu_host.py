@@ -242,6 +242,17 @@ def test_state_map_pickles_as_plain_defaultdict():
     other = ApexW([torch.nn.Parameter(torch.zeros(4))], lr=1e-3)
     other.load_state_dict(opt.state_dict())
     assert other.state._owner is other
+    # ApexMuon keeps the same mapping; a copy folds the pending skips first
+    from apexw_amd.muon import ApexMuon
+    q = torch.nn.Parameter(torch.zeros(32, 32))
+    mu = ApexMuon([q], lr=0.02)
+    mu.state[q]["step"] = 3
+    folds = []
+    mu._fold_amp_skips = lambda: (folds.append(1), setattr(mu, "_amp_unfolded", False))
+    mu._amp_unfolded = True
+    twin = copy.deepcopy(mu)
+    assert folds == [1] and twin.state._owner is twin and [st["step"] for st in twin.state.values()] == [3]
+    assert type(pickle.loads(pickle.dumps(mu.state))) is defaultdict
 
 
 @pytest.mark.parametrize("prec", ["full", "auto", "ultra", "compact", "8bit"])

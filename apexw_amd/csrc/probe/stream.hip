@@ -6,7 +6,11 @@
 //   * the 8-bit step's exact access pattern (bf16 p and g, NF4 m, quad log-u8
 //     v, two fp32 scales per 2048-element block; p, m, v and the scales written
 //     back), blocks_per_wave consecutive blocks per wave per iteration, with
-//     the stored values changed (an xor) so that no store can be dropped.
+//     the stored values changed (an xor) so that no store can be dropped;
+//   * the compact step's pattern (bf16 p, g, m and a dense or quad bf16 v read,
+//     p, m and v written back): one 512-element group per wave and work item,
+//     8 consecutive elements per lane, the work items of a workgroup's waves
+//     consecutive, as the compact step kernel walks its units.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -116,6 +120,27 @@ __global__ __launch_bounds__(256) void q8_pattern_kernel(uint16_t* p, const uint
   }
 }
 
+template <bool QUAD>
+__global__ __launch_bounds__(256) void compact_pattern_kernel(uint16_t* p, const uint16_t* g, uint16_t* m, uint16_t* v,
+                                                              int64_t n_items) {
+  const int lane = threadIdx.x & 63;
+  for (int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); w < n_items; w += (int64_t)gridDim.x * 4) {
+    const int64_t e = w * 512 + lane * 8;
+    const u32x4 a = nt_load<u32x4>(p + e), b = nt_load<u32x4>(g + e), c = nt_load<u32x4>(m + e);
+    if constexpr (QUAD) {
+      const uint32_t d = nt_load<uint32_t>(v + (e >> 2));
+      nt_store(p + e, a ^ b ^ 1u);
+      nt_store(m + e, c ^ b ^ 2u);
+      nt_store(v + (e >> 2), d ^ b.x ^ 3u);
+    } else {
+      const u32x4 d = nt_load<u32x4>(v + e);
+      nt_store(p + e, a ^ b ^ 1u);
+      nt_store(m + e, c ^ b ^ 2u);
+      nt_store(v + e, d ^ b ^ 3u);
+    }
+  }
+}
+
 bool ok(int grid) { return grid > 0 && grid <= (1 << 20); }
 
 }  // namespace
@@ -167,5 +192,19 @@ PROBE_API int apexw_probe_q8_pattern(void* p, const void* g, void* m, void* v, f
                        (uint8_t*)m, (uint8_t*)v, ms, vs, n_blocks);
   else
     return 1;
+  return hipGetLastError() == hipSuccess ? 0 : 3;
+}
+
+// p, g, m: n_items * 512 bf16; v: the same (quad == 0) or n_items * 128 bf16 (quad == 1).
+PROBE_API int apexw_probe_compact_pattern(void* p, const void* g, void* m, void* v, int64_t n_items, int32_t quad,
+                                          int32_t grid, void* stream) {
+  if (!p || !g || !m || !v || n_items <= 0 || !ok(grid) || (quad != 0 && quad != 1)) return 1;
+  hipStream_t s = (hipStream_t)stream;
+  if (quad)
+    hipLaunchKernelGGL(compact_pattern_kernel<true>, dim3(grid), dim3(256), 0, s, (uint16_t*)p, (const uint16_t*)g,
+                       (uint16_t*)m, (uint16_t*)v, n_items);
+  else
+    hipLaunchKernelGGL(compact_pattern_kernel<false>, dim3(grid), dim3(256), 0, s, (uint16_t*)p, (const uint16_t*)g,
+                       (uint16_t*)m, (uint16_t*)v, n_items);
   return hipGetLastError() == hipSuccess ? 0 : 3;
 }

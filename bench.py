@@ -290,7 +290,8 @@ def ceiling(reps=5):
     """HBM ceilings for the 8-bit step's traffic, HIP-event timed on the launch stream:
     copy / read-only / write-only of 8 GiB (1, 4 and 16 KiB contiguous per wave), and
     the step's exact access pattern with no arithmetic over the Llama-3-8B size
-    (1 and 4 consecutive blocks per wave).  Needs apexw_amd/libapexw_probe.so."""
+    (1 and 4 consecutive blocks per wave), and the compact step's pattern (dense and
+    quad bf16 v) over 2^31 elements.  Needs apexw_amd/libapexw_probe.so."""
     import ctypes
     from apexw_amd import _build
     lib = ctypes.CDLL(_build.PROBE_PATH)
@@ -299,6 +300,7 @@ def ceiling(reps=5):
     lib.apexw_probe_read.argtypes = [vp, i64, i32, i32, vp, vp]
     lib.apexw_probe_write.argtypes = [vp, i64, i32, i32, vp]
     lib.apexw_probe_q8_pattern.argtypes = [vp, vp, vp, vp, vp, vp, i64, i32, i32, vp]
+    lib.apexw_probe_compact_pattern.argtypes = [vp, vp, vp, vp, i64, i32, i32, vp]
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     nblk = sum(math.prod(s) for s in llama3_8b_shapes()) // 2048 // 4 * 4
@@ -340,6 +342,15 @@ def ceiling(reps=5):
             ms_ = timed(lambda: lib.apexw_probe_q8_pattern(p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(),
                                                            ms.data_ptr(), vs.data_ptr(), nblk, bpw, gr, h))
             out[f"q8_pattern_b{bpw}_grid{gr}"] = pattern_bytes / (ms_ * 1e-3) / 1e9
+    # the compact step's pattern over 2^31 elements: p, m in p's buffer, g, v in g's
+    n_el = 1 << 31
+    pm, gv = p[:2 * n_el], g[:2 * n_el]
+    for quad, bpe in ((0, 14), (1, 11)):
+        for gr in (8192, 32768):
+            ms_ = timed(lambda: lib.apexw_probe_compact_pattern(pm[:n_el].data_ptr(), gv[:n_el].data_ptr(),
+                                                                pm[n_el:].data_ptr(), gv[n_el:].data_ptr(),
+                                                                n_el // 512, quad, gr, h))
+            out[f"compact_pattern_{'quad' if quad else 'dense'}_grid{gr}"] = bpe * n_el / (ms_ * 1e-3) / 1e9
     res = {"ceiling_gbs": {k: round(x, 1) for k, x in out.items()}, "peak_gbs": HBM_PEAK_GBS,
            "copy_bytes": cb, "pattern_bytes": pattern_bytes, "grid": grid,
            "device": torch.cuda.get_device_name(dev)}

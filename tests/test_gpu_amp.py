@@ -23,6 +23,15 @@ pytestmark = pytest.mark.gpu
 SCALE = 1024.0
 
 
+@pytest.fixture(autouse=True)
+def _fresh_fp16_flag(monkeypatch):
+    """An 8-bit ApexW over fp16 parameters sets a process-wide flag that clamps
+    GradScaler's scale to 256 (as the reference does); tests here start without it,
+    whichever tests ran before them in the process."""
+    from apexw_amd import runtime as R
+    monkeypatch.setattr(R, "fp16_active", False)
+
+
 def _need_gpu():
     if not torch.cuda.is_available():
         pytest.skip("needs a GPU")

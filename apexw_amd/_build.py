@@ -24,9 +24,6 @@ CSRC = os.path.join(HERE, "csrc")
 ROOT = os.path.dirname(HERE)
 LIB_NAME = "libapexw_hip.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
-# bandwidth probes for bench.py --ceiling: their own library, outside the optimizer's C ABI
-PROBE_SRC = os.path.join(CSRC, "probe", "stream.hip")
-PROBE_PATH = os.path.join(HERE, "libapexw_probe.so")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
@@ -47,24 +44,9 @@ def sources():
 
 
 def build(verbose=False):
-    """Compile the HIP library, the probe library and the host module (always rebuilds all)."""
+    """Compile the HIP library and the host module (always rebuilds both)."""
     build_host(verbose)
-    build_probe(verbose)
     return build_hip(verbose)
-
-
-def build_probe(verbose=False):
-    """Compile csrc/probe/stream.hip into apexw_amd/libapexw_probe.so."""
-    tmp = PROBE_PATH + ".tmp"
-    cmd = [HIPCC, *FLAGS, "-shared", "-o", tmp, PROBE_SRC]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        errs = "\n".join(l for l in res.stderr.splitlines() if "packed-fp32-ops" not in l)
-        raise RuntimeError(f"hipcc failed on the probe library ({res.returncode}):\n{errs}")
-    os.replace(tmp, PROBE_PATH)
-    return PROBE_PATH
 
 
 def build_host(verbose=False):

@@ -2,7 +2,6 @@
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--config c3|c2|c4|c1|...] [--no-cpu]
     python bench.py --copy-calibration     # 1 GiB device copy, for HBM counter scaling
-    python bench.py --ceiling              # HBM ceilings of the step's traffic (probe kernels)
 
 Prints ONE JSON line (rank 0).  A "step" is one ``ApexW.step()`` over the full
 parameter list with synthetic bf16 params ~N(0, 0.02) and grads ~N(0, 1e-3)
@@ -286,77 +285,6 @@ def cpu_baseline(cfg_name, budget_s=20.0):
             "sample": f"{sample}; {steps} steps after 1 cold step; CPU oracle (torch CPU ops)"}
 
 
-def ceiling(reps=5):
-    """HBM ceilings for the 8-bit step's traffic, HIP-event timed on the launch stream:
-    copy / read-only / write-only of 8 GiB (1, 4 and 16 KiB contiguous per wave), and
-    the step's exact access pattern with no arithmetic over the Llama-3-8B size
-    (1 and 4 consecutive blocks per wave), and the compact step's pattern (dense and
-    quad bf16 v) over 2^31 elements.  Needs apexw_amd/libapexw_probe.so."""
-    import ctypes
-    from apexw_amd import _build
-    lib = ctypes.CDLL(_build.PROBE_PATH)
-    vp, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
-    lib.apexw_probe_copy.argtypes = [vp, vp, i64, i32, i32, vp]
-    lib.apexw_probe_read.argtypes = [vp, i64, i32, i32, vp, vp]
-    lib.apexw_probe_write.argtypes = [vp, i64, i32, i32, vp]
-    lib.apexw_probe_q8_pattern.argtypes = [vp, vp, vp, vp, vp, vp, i64, i32, i32, vp]
-    lib.apexw_probe_compact_pattern.argtypes = [vp, vp, vp, vp, i64, i32, i32, vp]
-    dev = torch.device("cuda", 0)
-    torch.cuda.set_device(dev)
-    nblk = sum(math.prod(s) for s in llama3_8b_shapes()) // 2048 // 4 * 4
-    p = torch.zeros(nblk * 2048, dtype=torch.bfloat16, device=dev)
-    g = torch.zeros_like(p)
-    m = torch.zeros(nblk * 1024, dtype=torch.uint8, device=dev)
-    v = torch.zeros(nblk * 512, dtype=torch.uint8, device=dev)
-    ms = torch.zeros(nblk, dtype=torch.float32, device=dev)
-    vs = torch.zeros_like(ms)
-    sink = torch.zeros(16, dtype=torch.int32, device=dev)
-    stream = torch.cuda.current_stream(dev)
-    h = stream.cuda_stream
-
-    def timed(launch):
-        for _ in range(2):
-            assert launch() == 0
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(reps):
-            launch()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / reps
-
-    cb = 8 << 30
-    grid = 32768
-    out = {}
-    for kib in (1, 4, 16):
-        ms_ = timed(lambda: lib.apexw_probe_copy(g.data_ptr(), p.data_ptr(), cb, kib, grid, h))
-        out[f"copy_{kib}k"] = 2 * cb / (ms_ * 1e-3) / 1e9
-    for kib in (4, 16):
-        ms_ = timed(lambda: lib.apexw_probe_read(g.data_ptr(), cb, kib, grid, sink.data_ptr(), h))
-        out[f"read_{kib}k"] = cb / (ms_ * 1e-3) / 1e9
-        ms_ = timed(lambda: lib.apexw_probe_write(p.data_ptr(), cb, kib, grid, h))
-        out[f"write_{kib}k"] = cb / (ms_ * 1e-3) / 1e9
-    pattern_bytes = nblk * (2048 * 7.5 + 16)   # p, g, m, v read and p, m, v written, two scales each way
-    for bpw in (1, 4):
-        for gr in (8192, 32768):
-            ms_ = timed(lambda: lib.apexw_probe_q8_pattern(p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(),
-                                                           ms.data_ptr(), vs.data_ptr(), nblk, bpw, gr, h))
-            out[f"q8_pattern_b{bpw}_grid{gr}"] = pattern_bytes / (ms_ * 1e-3) / 1e9
-    # the compact step's pattern over 2^31 elements: p, m in p's buffer, g, v in g's
-    n_el = 1 << 31
-    pm, gv = p[:2 * n_el], g[:2 * n_el]
-    for quad, bpe in ((0, 14), (1, 11)):
-        for gr in (8192, 32768):
-            ms_ = timed(lambda: lib.apexw_probe_compact_pattern(pm[:n_el].data_ptr(), gv[:n_el].data_ptr(),
-                                                                pm[n_el:].data_ptr(), gv[n_el:].data_ptr(),
-                                                                n_el // 512, quad, gr, h))
-            out[f"compact_pattern_{'quad' if quad else 'dense'}_grid{gr}"] = bpe * n_el / (ms_ * 1e-3) / 1e9
-    res = {"ceiling_gbs": {k: round(x, 1) for k, x in out.items()}, "peak_gbs": HBM_PEAK_GBS,
-           "copy_bytes": cb, "pattern_bytes": pattern_bytes, "grid": grid,
-           "device": torch.cuda.get_device_name(dev)}
-    print(json.dumps(res), flush=True)
-
-
 def mfma_extra(steps=10, warmup=3):
     """The C5 Newton-Schulz roofline, for the default bench line: the hybrid Muon step on
     one Llama-3-8B layer, then the step's grouped NS launches replayed between HIP events."""
@@ -392,7 +320,6 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--copy-calibration", action="store_true", help="run the counter-calibration copy and exit")
-    ap.add_argument("--ceiling", action="store_true", help="measure the HBM ceilings of the step's traffic and exit")
     ap.add_argument("--no-mfma", action="store_true", help="skip the C5 Newton-Schulz roofline of the default line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -401,9 +328,6 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration()
-        return
-    if args.ceiling:
-        ceiling()
         return
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from apexw_amd import ApexW

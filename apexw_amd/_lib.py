@@ -13,7 +13,7 @@ import numpy as np
 
 from ._build import LIB_PATH
 
-ABI_VERSION = 18
+ABI_VERSION = 19
 
 # dtype codes
 F32, BF16, F16, U8, I8 = 0, 1, 2, 3, 4
@@ -49,7 +49,7 @@ HP_AMP = 1 << 8
 STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported dtype combination", 3: "launch failed",
           4: "misaligned pointer", 5: "exceeds the fixed workspace of the allocation-free entry point"}
 ERR_SIZE = 5
-NOALLOC_CLIP_MAX_UNITS = 1 << 21
+NOALLOC_CLIP_MAX_UNITS = 1 << 23
 NOALLOC_CLIP_MAX_TENSORS = 1 << 17
 
 TENSOR_DTYPE = np.dtype([
@@ -94,6 +94,9 @@ class HParams(ctypes.Structure):
 AMP_LAUNCH_DTYPE = np.dtype([("lr", np.float64), ("beta1", np.float64), ("beta2", np.float64), ("eps", np.float64),
                              ("step", np.float64), ("kind", np.uint32), ("reserved", np.uint32)])
 assert AMP_LAUNCH_DTYPE.itemsize == 48
+# apexw_check_launch kinds
+LAUNCH_COMPACT, LAUNCH_Q8, LAUNCH_FACTORED, LAUNCH_ULTRA = 0, 1, 4, 5
+
 AMP_DYN_BYTES = 32
 AMP_MAX_LAUNCHES = 16
 
@@ -141,6 +144,7 @@ _HP = ctypes.POINTER(HParams)
 SIGNATURES = {
     "apexw_abi_version": (ctypes.c_int, []),
     "apexw_check_tensor": (ctypes.c_int, [ctypes.POINTER(Tensor), _i32]),
+    "apexw_check_launch": (ctypes.c_int, [_i32, _i32, _i64, _i64, _i64, _HP]),
     "apexw_compact_step": (ctypes.c_int, [_vp, _i32, _vp, _i64, _HP, _vp]),
     "apexw_ultra_step": (ctypes.c_int, [_vp, _i32, _vp, _i64, _HP, _vp]),
     "apexw_q8_step": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _i64, _HP, _vp]),

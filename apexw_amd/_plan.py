@@ -441,12 +441,15 @@ class StepPlan:
         return (self._fast_static & ~scalar) if self.kind == "q8" and not self.single else None
 
     # ------------------------------------------------------------------ launch
-    def _clip(self, clip, sanitize, inv_scale, stream, amp_dyn=None):
+    def _clip_buffers(self):
         if self.clip_ws is None:
             self.clip_ws = (torch.empty(max(self.n_units, 1), dtype=torch.float32, device=self.device),
                             torch.empty(len(self.params), dtype=torch.float32, device=self.device),
                             torch.empty(1, dtype=torch.float32, device=self.device))
-        part, norms, coef = self.clip_ws
+        return self.clip_ws
+
+    def _clip(self, clip, sanitize, inv_scale, stream, amp_dyn=None):
+        part, norms, coef = self._clip_buffers()
         unit = L.COMPACT_UNIT if self.kind == "compact" else 0
         st = self._lib.apexw_grad_clip_coef(
             self.d_table.data_ptr(), len(self.params), self.d_units.data_ptr(), self.n_units, unit,
@@ -463,7 +466,11 @@ class StepPlan:
         """Whether GradScaler's scale and found_inf can be read on the device for this
         plan (the compact and 8-bit step kernels; not the factored ones or the
         in-backward batches)."""
-        return not (self.hooked or self.single or self.factored.any() or self.vscaled.any())
+        # a prepared copy of the grads (8-bit / factored groups that centralize) is unscaled
+        # by apexw_grad_prepare and the step launches then carry no AMP scalars, so they
+        # could not skip an inf / NaN step: such plans read found_inf on the host
+        return not (self.hooked or self.single or self.factored.any() or self.vscaled.any()
+                    or (self.gc and not self.gc_fold))
 
     def amp_fold(self, sync=False):
         """Subtract from the step counters the steps GradScaler skipped that the host
@@ -479,8 +486,8 @@ class StepPlan:
             self._steps_np -= float(seen - self._amp_folded)
             self._amp_folded = seen
 
-    def _amp_prepare(self, amp, groups, lr, b1, b2, eps, stream):
-        """Device-side scalars of every launch of this step (apexw_amp_prepare)."""
+    def _amp_buffers(self):
+        """The device-side AMP scalars' buffers (allocated once); returns their address."""
         if getattr(self, "_amp_skips", None) is None:
             self._amp_skips = torch.zeros(1, dtype=torch.int32, device=self.device)
             self._amp_mirror = torch.zeros(1, dtype=torch.int32, pin_memory=True)
@@ -488,6 +495,11 @@ class StepPlan:
                                         device=self.device)
             self._amp_folded = 0
             self._amp_event = torch.cuda.Event()
+        return self._amp_dyn.data_ptr()
+
+    def _amp_prepare(self, amp, groups, lr, b1, b2, eps, stream):
+        """Device-side scalars of every launch of this step (apexw_amp_prepare)."""
+        self._amp_buffers()
         launches = np.zeros(len(groups), dtype=L.AMP_LAUNCH_DTYPE)
         launches["lr"], launches["beta1"], launches["beta2"], launches["eps"] = lr, b1, b2, eps
         launches["step"] = [g[1] for g in groups]
@@ -573,22 +585,54 @@ class StepPlan:
             self.d_vscale.copy_(torch.from_numpy(h).pin_memory(), non_blocking=True)
 
     def execute(self, group, seed, inv_scale=None, lr=None, wd=None, steps=None, amp=None):
-        """Run one optimizer step for the group (cold the first time, replay after).
+        """Run one optimizer step for the group (cold the first time, replay after):
+        prepare() then run().  Arguments as prepare()."""
+        prog = self.prepare(group, seed, inv_scale, lr, wd, steps, amp)
+        if prog is None:
+            raise L.ApexwError("device-side AMP is unavailable for this step; pass the host-read scale")
+        prog.run()
+
+    def prepare(self, group, seed, inv_scale=None, lr=None, wd=None, steps=None, amp=None):
+        """Everything of one step up to its first device launch: the grads are
+        re-pointed, the step counters advanced, each launch's scalars built and
+        checked by the library (apexw_check_launch, the checks every step entry
+        point runs before it enqueues).  Nothing the caller can see changes on the
+        device here, and a refusal restores the counters, so a caller that prepares
+        every group before running any refuses a whole step before any parameter
+        moves -- the reference's validate-before-mutate order and step-counter
+        rollback around its fused launches (apexw/optimizer.py:3184-3356, :3806).
 
         inv_scale: 1 / the AMP grad scale handed over by GradScaler, or None.
         amp: instead, GradScaler's (scale, found_inf) device tensors, read on the
         device (amp_device_ok plans): the kernels unscale with 1 / scale and skip
         the step when found_inf is set; the step counters advance on the host and
-        the skips are subtracted once seen (amp_fold).
+        the skips are subtracted once seen (amp_fold).  Returns None, with the
+        counters untouched, when this step needs more launches than the device-side
+        AMP table holds (APEXW_AMP_MAX_LAUNCHES); the caller then reads the scale on
+        the host.
         lr, wd: replace the group's values; steps: each parameter's step count
-        for this step (already advanced) instead of advancing the plan's own."""
-        mode_cold = not self.cold_done
-        keep = self._refresh_grads()  # noqa: F841 -- keeps contiguous copies alive until the launch
-        stream = torch.cuda.current_stream(self.device).cuda_stream
-        amp_dyn = None
+        for this step (already advanced) instead of advancing the plan's own.
+        Returns a _Program whose run() enqueues the step and rollback() undoes the
+        counters."""
         if amp is not None:
             self.amp_fold()
-            inv_scale = 1.0          # a stand-in: the kernels read the factor from amp_dyn
+        saved = self._steps_np.copy()
+        try:
+            prog = self._prepare(group, seed, inv_scale, lr, wd, steps, amp)
+        except BaseException:
+            self._steps_np[:] = saved
+            raise
+        if prog is None:
+            self._steps_np[:] = saved
+            return None
+        prog.saved = saved
+        return prog
+
+    def _prepare(self, group, seed, inv_scale, lr, wd, steps, amp):
+        mode_cold = not self.cold_done
+        keep = self._refresh_grads()      # contiguous copies of non-contiguous grads, alive until the launch
+        if amp is not None:
+            inv_scale = 1.0          # a stand-in: the kernels read the factor from the device scalars
         (b1, b2), eps = group["betas"], group["eps"]
         lr = group["lr"] if lr is None else lr
         wd = group["weight_decay"] if wd is None else wd
@@ -605,8 +649,6 @@ class StepPlan:
             self._steps_np += 1.0
         else:
             self._steps_np[:] = np.asarray(steps, dtype=np.float32)
-        if self.h_vscale is not None:
-            self._update_vscales(group, mode_cold)
         # The reference's replayed compact step takes the bias correction of the
         # first counter for the whole group (optimizer.py:1082-1090); every other
         # path uses each parameter's own count.  SR: the 8-bit step and the
@@ -618,21 +660,27 @@ class StepPlan:
             groups = self._split_launches(sr_t, sr)
         else:
             groups = [(None, int(self._steps_np[0]), sr)]
-        if amp is not None:
-            amp_dyn = self._amp_prepare(amp, groups, lr, b1, b2, eps, stream)
+        if amp is not None and len(groups) > L.AMP_MAX_LAUNCHES:
+            return None
+        amp_dyn = self._amp_buffers() if amp is not None else None
+        prep = None
         if self.single:
             pass
         elif self.gc_fold:
             # _prepare_grads with centralization, folded: the row means first; the clip
             # and the step read the raw grads and sanitize, unscale and subtract them
-            self._prepare_grads(inv_scale, stream, amp_dyn)
+            prep = (inv_scale, amp_dyn)
             sanitize = True
         elif self.gc:
             # _prepare_grads with centralization: sanitize, unscale, centralize;
             # the clip and the step then see finite, unscaled grads
-            self._prepare_grads(inv_scale, stream, amp_dyn)
+            prep = (inv_scale, amp_dyn)
             sanitize, inv_scale, amp_dyn = False, None, None
-        coef = self._clip(clip, sanitize, inv_scale, stream, amp_dyn) if clip is not None else None
+        coef = None
+        if clip is not None:
+            coef = self._clip_buffers()[2]
+        launch_kind = L.LAUNCH_COMPACT if self.kind == "compact" else (L.LAUNCH_ULTRA if self.ultra else L.LAUNCH_Q8)
+        launches = []
         for li, (units, step, sr_l) in enumerate(groups):
             hp = self._hparams(lr, b1, b2, eps, wd, step, sr_l, sanitize, coef, seed, mode_cold, inv_scale)
             if amp_dyn is not None:
@@ -645,31 +693,62 @@ class StepPlan:
                 d_units, n_units, n_fast, n_fast32 = units
             if n_units == 0:
                 continue
-            if self.kind == "compact":
-                st = self._lib.apexw_compact_step(self.d_table.data_ptr(), len(self.params), d_units.data_ptr(),
-                                                  n_units, ctypes_ref(hp), stream)
-            elif self.ultra:
-                st = self._lib.apexw_ultra_step(self.d_table.data_ptr(), len(self.params), d_units.data_ptr(),
-                                                n_units, ctypes_ref(hp), stream)
-            else:
-                st = self._lib.apexw_q8_step(self.d_table.data_ptr(), len(self.params), d_units.data_ptr(),
-                                             n_units, n_fast, n_fast32, ctypes_ref(hp), stream)
-            L.check(st, "apexw step")
+            if self.kind == "compact" or self.ultra:
+                n_fast = n_fast32 = 0
+            L.check(self._lib.apexw_check_launch(launch_kind, len(self.params), n_units, n_fast, n_fast32,
+                                                 ctypes_ref(hp)), "apexw step")
+            launches.append((d_units, n_units, n_fast, n_fast32, hp))
+        fv_launches = []
         if self.fv is not None:
             replay_step = None if (mode_cold or self.native or self.kind == "q8") else groups[0][1]
-            self._factored_launch(lr, b1, b2, eps, wd, sanitize, coef, seed, mode_cold, inv_scale, replay_step,
-                                  stream)
+            fv_launches = self._factored_launches(lr, b1, b2, eps, wd, sanitize, coef, seed, mode_cold, inv_scale,
+                                                  replay_step)
+        return _Program(self, group=group, mode_cold=mode_cold, keep=keep, amp=amp, amp_groups=groups,
+                        amp_scalars=(lr, b1, b2, eps), prep=prep, clip=clip, sanitize=sanitize,
+                        inv_scale=inv_scale, amp_dyn=amp_dyn, launches=launches, fv_launches=fv_launches)
+
+    def _run(self, prog):
+        """Enqueue one prepared step (prepare())."""
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        if self.h_vscale is not None:
+            self._update_vscales(prog.group, prog.mode_cold)
+        if prog.amp is not None:
+            lr, b1, b2, eps = prog.amp_scalars
+            self._amp_prepare(prog.amp, prog.amp_groups, lr, b1, b2, eps, stream)
+        if prog.prep is not None:
+            self._prepare_grads(prog.prep[0], stream, prog.prep[1])
+        if prog.clip is not None:
+            self._clip(prog.clip, prog.sanitize, prog.inv_scale, stream, prog.amp_dyn)
+        table = self.d_table.data_ptr()
+        for d_units, n_units, n_fast, n_fast32, hp in prog.launches:
+            if self.kind == "compact":
+                st = self._lib.apexw_compact_step(table, len(self.params), d_units.data_ptr(), n_units,
+                                                  ctypes_ref(hp), stream)
+            elif self.ultra:
+                st = self._lib.apexw_ultra_step(table, len(self.params), d_units.data_ptr(), n_units,
+                                                ctypes_ref(hp), stream)
+            else:
+                st = self._lib.apexw_q8_step(table, len(self.params), d_units.data_ptr(), n_units, n_fast, n_fast32,
+                                             ctypes_ref(hp), stream)
+            L.check(st, "apexw step")
+        for fv, hp in prog.fv_launches:
+            st = self._lib.apexw_factored_step(
+                table, len(self.params), fv["d_fv"].data_ptr(), fv["n"], fv["n_bands"],
+                fv["n_cb"], fv["d_units"].data_ptr() if fv["d_units"] is not None else None, fv["n_units"],
+                fv["range_ends"].ctypes.data, fv["ws"].data_ptr(), ctypes_ref(hp), stream)
+            L.check(st, "apexw_factored_step")
         self.cold_done = True
 
     def _state_sr(self):
         return np.fromiter((bool(st.get("stochastic_rounding", True)) for st in self.states), dtype=bool,
                            count=len(self.states))
 
-    def _factored_launch(self, lr, b1, b2, eps, wd, sanitize, coef, seed, cold, inv_scale, replay_step, stream):
-        """Step the factored-v rows: one apexw_factored_step per distinct (step count,
-        SR flag).  The replayed compact plan uses its first counter for every
-        tensor (optimizer.py:1141-1163); SR follows each parameter's state flag
-        (_apply_factored_v_int8_update's callers, optimizer.py:5426, :4377)."""
+    def _factored_launches(self, lr, b1, b2, eps, wd, sanitize, coef, seed, cold, inv_scale, replay_step):
+        """The factored-v rows' launches, checked: one apexw_factored_step per distinct
+        (step count, SR flag).  The replayed compact plan uses its first counter for
+        every tensor (optimizer.py:1141-1163); SR follows each parameter's state flag
+        (_apply_factored_v_int8_update's callers, optimizer.py:5426, :4377).
+        Returns [(layout, hparams)]."""
         rows = self.fv["rows"]
         vals = self.steps.numpy()[self.perm]
         srs = self._state_sr()[self.perm]
@@ -677,6 +756,7 @@ class StepPlan:
         for d in rows:
             key = (replay_step if replay_step is not None else int(vals[d]), bool(srs[d]))
             buckets.setdefault(key, []).append(d)
+        out = []
         for (step, sr), members in buckets.items():
             if len(members) == len(rows):
                 fv = self.fv
@@ -693,11 +773,10 @@ class StepPlan:
             # (_apply_factored_v_int8_update's sanitize_g, optimizer.py:4380-4400, :5414-5432, :1147-1163)
             if self.kind == "q8" or cold:
                 hp.flags |= L.HP_FV_SANITIZE
-            st = self._lib.apexw_factored_step(
-                self.d_table.data_ptr(), len(self.params), fv["d_fv"].data_ptr(), fv["n"], fv["n_bands"],
-                fv["n_cb"], fv["d_units"].data_ptr() if fv["d_units"] is not None else None, fv["n_units"],
-                fv["range_ends"].ctypes.data, fv["ws"].data_ptr(), ctypes_ref(hp), stream)
-            L.check(st, "apexw_factored_step")
+            L.check(self._lib.apexw_check_launch(L.LAUNCH_FACTORED, len(self.params), fv["n_units"], 0, 0,
+                                                 ctypes_ref(hp)), "apexw_factored_step")
+            out.append((fv, hp))
+        return out
 
     def _split_launches(self, sr_t, sr_default):
         """Step-kernel launches as (units or None for all, step count, SR): one per
@@ -793,6 +872,27 @@ class StepPlan:
         hp.step = step & 0xFFFFFFFF
         hp.flags = flags
         return hp
+
+
+class _Program:
+    """One prepared step of a StepPlan: run() enqueues it, rollback() restores the
+    step counters it advanced (when a later group of the same step is refused)."""
+
+    def __init__(self, plan, **kw):
+        self.plan = plan
+        self.saved = None
+        self.__dict__.update(kw)
+
+    def run(self):
+        try:
+            self.plan._run(self)
+        except BaseException:
+            self.rollback()
+            raise
+
+    def rollback(self):
+        if self.saved is not None:
+            self.plan._steps_np[:] = self.saved
 
 
 def ctypes_ref(obj):

@@ -155,28 +155,57 @@ int apexw_check_tensor(const apexw_tensor* t, int32_t kind) {
   return APEXW_OK;
 }
 
+// The scalar checks of one step launch (kind: APEXW_LAUNCH_COMPACT / _Q8 / _ULTRA /
+// _FACTORED), shared by the step entry points and apexw_check_launch.
+static int launch_args_status(int32_t kind, int32_t n_tensors, int64_t n_units, int64_t n_fast_units,
+                              int64_t n_fast_f32_units, const apexw_hparams* hp) {
+  if (n_tensors <= 0 || n_units < 0 || !hp_ok(hp)) return APEXW_ERR_ARG;
+  switch (kind) {
+    case APEXW_LAUNCH_COMPACT:
+      return (n_fast_units || n_fast_f32_units) ? APEXW_ERR_ARG : APEXW_OK;
+    case APEXW_LAUNCH_ULTRA:
+      if (n_fast_units || n_fast_f32_units) return APEXW_ERR_ARG;
+      return (hp->mode == APEXW_MODE_NATIVE || hp->mode == APEXW_MODE_SINGLE) ? APEXW_ERR_ARG : APEXW_OK;
+    case APEXW_LAUNCH_Q8:
+      if (n_fast_units < 0 || n_fast_f32_units < 0 || n_fast_units + n_fast_f32_units > n_units) return APEXW_ERR_ARG;
+      if (hp->mode == APEXW_MODE_NATIVE) return APEXW_ERR_ARG;
+      if (hp->mode == APEXW_MODE_SINGLE && (n_fast_units || n_fast_f32_units)) return APEXW_ERR_ARG;
+      return APEXW_OK;
+    case APEXW_LAUNCH_FACTORED:
+      if (n_fast_units || n_fast_f32_units) return APEXW_ERR_ARG;
+      if (hp->mode == APEXW_MODE_SINGLE || hp->mode == APEXW_MODE_NATIVE) return APEXW_ERR_ARG;
+      return (hp->flags & APEXW_HP_AMP) ? APEXW_ERR_ARG : APEXW_OK;   // factored steps take host-read AMP scalars
+    default:
+      return APEXW_ERR_ARG;
+  }
+}
+
+int apexw_check_launch(int32_t kind, int32_t n_tensors, int64_t n_units, int64_t n_fast_units,
+                       int64_t n_fast_f32_units, const apexw_hparams* hp) {
+  return launch_args_status(kind, n_tensors, n_units, n_fast_units, n_fast_f32_units, hp);
+}
+
 int apexw_compact_step(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,
                        const apexw_hparams* hp, void* stream) {
-  if (!tensors || !units || n_tensors <= 0 || n_units < 0 || !hp_ok(hp)) return APEXW_ERR_ARG;
-  if (n_units == 0) return APEXW_OK;
+  if (!tensors || !units) return APEXW_ERR_ARG;
+  const int st = launch_args_status(APEXW_LAUNCH_COMPACT, n_tensors, n_units, 0, 0, hp);
+  if (st != APEXW_OK || n_units == 0) return st;
   return apexw_launch_compact(tensors, n_units, units, hp, (hipStream_t)stream);
 }
 
 int apexw_ultra_step(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,
                      const apexw_hparams* hp, void* stream) {
-  if (!tensors || !units || n_tensors <= 0 || n_units < 0 || !hp_ok(hp)) return APEXW_ERR_ARG;
-  if (hp->mode == APEXW_MODE_NATIVE || hp->mode == APEXW_MODE_SINGLE) return APEXW_ERR_ARG;
-  if (n_units == 0) return APEXW_OK;
+  if (!tensors || !units) return APEXW_ERR_ARG;
+  const int st = launch_args_status(APEXW_LAUNCH_ULTRA, n_tensors, n_units, 0, 0, hp);
+  if (st != APEXW_OK || n_units == 0) return st;
   return apexw_launch_ultra(tensors, n_units, units, hp, (hipStream_t)stream);
 }
 
 int apexw_q8_step(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,
                   int64_t n_fast_units, int64_t n_fast_f32_units, const apexw_hparams* hp, void* stream) {
-  if (!tensors || !units || n_tensors <= 0 || n_units < 0 || !hp_ok(hp)) return APEXW_ERR_ARG;
-  if (n_fast_units < 0 || n_fast_f32_units < 0 || n_fast_units + n_fast_f32_units > n_units) return APEXW_ERR_ARG;
-  if (hp->mode == APEXW_MODE_NATIVE) return APEXW_ERR_ARG;
-  if (hp->mode == APEXW_MODE_SINGLE && (n_fast_units || n_fast_f32_units)) return APEXW_ERR_ARG;
-  int st = APEXW_OK;
+  if (!tensors || !units) return APEXW_ERR_ARG;
+  int st = launch_args_status(APEXW_LAUNCH_Q8, n_tensors, n_units, n_fast_units, n_fast_f32_units, hp);
+  if (st != APEXW_OK) return st;
   if (n_fast_units > 0)
     st = apexw_launch_q8_fast(tensors, n_fast_units, units, hp, APEXW_BF16, (hipStream_t)stream);
   if (st == APEXW_OK && n_fast_f32_units > 0)
@@ -213,7 +242,8 @@ int64_t apexw_factored_layout(apexw_fv_tensor* fv, int32_t n_fv, int64_t* n_band
 int apexw_factored_step(const apexw_tensor* tensors, int32_t n_tensors, const apexw_fv_tensor* fv, int32_t n_fv,
                         int64_t n_bands, int64_t n_col_blocks, const apexw_unit* units, int64_t n_units,
                         const int64_t* range_ends, float* workspace, const apexw_hparams* hp, void* stream) {
-  if (!tensors || !fv || !workspace || n_tensors <= 0 || n_fv <= 0 || n_fv > n_tensors || !hp_ok(hp)) return APEXW_ERR_ARG;
+  if (!tensors || !fv || !workspace || n_fv <= 0 || n_fv > n_tensors) return APEXW_ERR_ARG;
+  if (launch_args_status(APEXW_LAUNCH_FACTORED, n_tensors, n_units, 0, 0, hp) != APEXW_OK) return APEXW_ERR_ARG;
   if (n_bands < n_fv || n_bands > INT32_MAX || n_col_blocks < n_fv || n_col_blocks + n_fv > INT32_MAX) return APEXW_ERR_ARG;
   if (n_units < 0 || (n_units > 0 && !units) || !range_ends) return APEXW_ERR_ARG;
   int64_t prev = 0;
@@ -222,8 +252,6 @@ int apexw_factored_step(const apexw_tensor* tensors, int32_t n_tensors, const ap
     prev = range_ends[r];
   }
   if (prev != n_units) return APEXW_ERR_ARG;
-  if (hp->mode == APEXW_MODE_SINGLE || hp->mode == APEXW_MODE_NATIVE) return APEXW_ERR_ARG;
-  if (hp->flags & APEXW_HP_AMP) return APEXW_ERR_ARG;   // factored steps take host-read AMP scalars
   return apexw_launch_factored(tensors, fv, n_fv, n_bands, n_col_blocks, units, range_ends, workspace, hp,
                                (hipStream_t)stream);
 }

@@ -346,19 +346,24 @@ static __device__ __align__(256) float scratch[APEXW_NOALLOC_CLIP_MAX_UNITS + AP
 namespace {
 
 constexpr int kScratchDevices = 64;
-std::once_flag g_scratch_once[kScratchDevices];
+std::mutex g_scratch_mu;
 float* g_scratch_ptr[kScratchDevices];
 
-// Device address of `scratch` on the current device, or nullptr if it cannot be had.
-float* scratch_on_current_device() {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchDevices) return nullptr;
-  std::call_once(g_scratch_once[dev], [dev] {
-    void* ptr = nullptr;
-    // runs on the calling thread, whose current device is dev
-    g_scratch_ptr[dev] = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) == hipSuccess ? (float*)ptr : nullptr;
-  });
-  return g_scratch_ptr[dev];
+// Device address of `scratch` on device dev, or nullptr if it cannot be had.  A
+// lookup that fails is not cached: the next call tries again.
+float* scratch_on_device(int dev) {
+  if (dev < 0 || dev >= kScratchDevices) return nullptr;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr[dev]) return g_scratch_ptr[dev];
+  int cur = -1;
+  if (hipGetDevice(&cur) != hipSuccess) return nullptr;
+  // hipGetSymbolAddress answers for the calling thread's current device
+  if (cur != dev && hipSetDevice(dev) != hipSuccess) return nullptr;
+  void* ptr = nullptr;
+  const bool ok = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) == hipSuccess && ptr;
+  if (cur != dev) (void)hipSetDevice(cur);
+  if (ok) g_scratch_ptr[dev] = (float*)ptr;
+  return ok ? (float*)ptr : nullptr;
 }
 
 }  // namespace
@@ -371,7 +376,15 @@ extern "C" int apexw_grad_clip_coef_noalloc(const apexw_tensor* tensors, int32_t
   if (n_tensors <= 0 || n_units < 0 || unit_size < 0 || !(clip > 0.0f)) return APEXW_ERR_ARG;
   if ((flags & APEXW_HP_UNSCALE) && !amp && !(grad_inv_scale > 0.0f)) return APEXW_ERR_ARG;
   if (n_units > APEXW_NOALLOC_CLIP_MAX_UNITS || n_tensors > APEXW_NOALLOC_CLIP_MAX_TENSORS) return APEXW_ERR_SIZE;
-  float* ptr = scratch_on_current_device();
+  // the array of the GPU the kernels run on: the stream's device (the null stream is
+  // the current device's)
+  int dev = -1;
+  if (stream) {
+    if (hipStreamGetDevice((hipStream_t)stream, &dev) != hipSuccess) return APEXW_ERR_ARG;
+  } else if (hipGetDevice(&dev) != hipSuccess) {
+    return APEXW_ERR_LAUNCH;
+  }
+  float* ptr = scratch_on_device(dev);
   if (!ptr) return APEXW_ERR_LAUNCH;
   return apexw_launch_clip(tensors, n_tensors, units, n_units, unit_size, unit_begin, ptr,
                            ptr + APEXW_NOALLOC_CLIP_MAX_UNITS, clip, grad_inv_scale, flags, coef, amp,

@@ -231,29 +231,51 @@ class ApexW(Optimizer):
         return loss
 
     def _step_groups(self, amp, grad_scale, found_inf):
+        """Two phases, as the reference's fused dispatch orders validation before any
+        mutation and rolls its step counters back when a launch is refused
+        (apexw/optimizer.py:3184-3356, :3806): every group's plan is built and its
+        step prepared (counters advanced, every launch checked by the library), then
+        the groups run.  A refusal while preparing restores every counter and leaves
+        every parameter and state untouched; a launch that fails while running
+        restores the counters of that group and of the groups after it."""
         host_amp = None
-        for group in self.param_groups:
-            gid = id(group)
-            plan = self._plans.get(gid)
-            if plan is None or not plan.valid_for(group):
-                old = self._plans.pop(gid, None)
-                if old is not None:
-                    old.amp_fold(sync=True)       # its counters are the states' until the new plan reads them
-                plan = self._build_plan(group)
-                if plan is None:
+        progs = []
+        try:
+            for group in self.param_groups:
+                gid = id(group)
+                plan = self._plans.get(gid)
+                if plan is None or not plan.valid_for(group):
+                    old = self._plans.pop(gid, None)
+                    if old is not None:
+                        old.amp_fold(sync=True)       # its counters are the states' until the new plan reads them
+                    plan = self._build_plan(group)
+                    if plan is None:
+                        continue
+                    self._plans[gid] = plan
+                # a plan's first launch (the cold rounding order) stays on the host read, so that
+                # a skipped step cannot use it up: the next real step is the cold one, as in the reference
+                if amp is not None and plan.amp_device_ok and plan.cold_done:
+                    prog = plan.prepare(group, self._seed, amp=amp)
+                    if prog is not None:
+                        progs.append(prog)
+                        continue
+                if host_amp is None:
+                    host_amp = self._read_amp(grad_scale, found_inf)
+                skip, inv_scale = host_amp
+                if skip:
                     continue
-                self._plans[gid] = plan
-            # a plan's first launch (the cold rounding order) stays on the host read, so that
-            # a skipped step cannot use it up: the next real step is the cold one, as in the reference
-            if amp is not None and plan.amp_device_ok and plan.cold_done:
-                plan.execute(group, self._seed, amp=amp)
-                continue
-            if host_amp is None:
-                host_amp = self._read_amp(grad_scale, found_inf)
-            skip, inv_scale = host_amp
-            if skip:
-                continue
-            plan.execute(group, self._seed, inv_scale)
+                progs.append(plan.prepare(group, self._seed, inv_scale))
+        except BaseException:
+            for prog in progs:
+                prog.rollback()
+            raise
+        for i, prog in enumerate(progs):
+            try:
+                prog.run()
+            except BaseException:
+                for later in progs[i + 1:]:
+                    later.rollback()
+                raise
 
     @staticmethod
     def _read_amp(grad_scale, found_inf):
@@ -476,24 +498,39 @@ class ApexW(Optimizer):
                 continue
             seen.add(id(p))
             by_group.setdefault(id(group), (group, []))[1].append(p)
-        for group, params in by_group.values():
-            msteps = []
-            for p in params:
-                st = S.ensure_8bit_state(self.state[p], p, group)
-                mstep = st.get("_hook_mstep", 0) + 1
+        # every batch is prepared (counters advanced, launches checked) before any runs;
+        # a refusal restores each parameter's counters, as step() does
+        progs, undo = [], []
+        try:
+            for group, params in by_group.values():
+                msteps = []
+                for p in params:
+                    st = S.ensure_8bit_state(self.state[p], p, group)
+                    undo.append((st, st.get("_hook_mstep", 0), float(st["step"])))
+                    mstep = st.get("_hook_mstep", 0) + 1
+                    st["_hook_mstep"] = mstep
+                    # the reference's CPU path stores (mstep - 1) // K + 1 (optimizer.py:2366-2367);
+                    # its CUDA path instead adds 1 every K passes, which differs once K changes
+                    st["step"].fill_(float((mstep - 1) // K + 1))
+                    msteps.append(mstep)
+                lr_eff = float(group["lr"]) * mult
+                wd_raw = float(group["weight_decay"])
+                wd_eff = wd_raw / (float(K) * mult) if wd_raw != 0.0 else 0.0
+                # the step takes the grad scale as a float32 tensor and multiplies by its reciprocal
+                inv = None if inv_scale == 1.0 else float(np.float32(1.0) / np.float32(1.0 / inv_scale))
+                for p in params:
+                    if p.grad.dtype != p.dtype:
+                        p.grad = p.grad.to(p.dtype)
+                plan = self._hook_plan(group, params)
+                progs.append((plan.prepare(group, self._hook_seed, inv, lr=lr_eff, wd=wd_eff, steps=msteps),
+                              params))
+        except BaseException:
+            for st, mstep, step in undo:
                 st["_hook_mstep"] = mstep
-                # the reference's CPU path stores (mstep - 1) // K + 1 (optimizer.py:2366-2367);
-                # its CUDA path instead adds 1 every K passes, which differs once K changes
-                st["step"].fill_(float((mstep - 1) // K + 1))
-                msteps.append(mstep)
-                if p.grad.dtype != p.dtype:
-                    p.grad = p.grad.to(p.dtype)
-            lr_eff = float(group["lr"]) * mult
-            wd_raw = float(group["weight_decay"])
-            wd_eff = wd_raw / (float(K) * mult) if wd_raw != 0.0 else 0.0
-            # the step takes the grad scale as a float32 tensor and multiplies by its reciprocal
-            inv = None if inv_scale == 1.0 else float(np.float32(1.0) / np.float32(1.0 / inv_scale))
-            self._hook_plan(group, params).execute(group, self._hook_seed, inv, lr=lr_eff, wd=wd_eff, steps=msteps)
+                st["step"].fill_(step)
+            raise
+        for prog, params in progs:
+            prog.run()
             for p in params:
                 p.grad = None
             self._auto_hook_stepped_count += len(params)

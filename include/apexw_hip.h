@@ -44,7 +44,7 @@
 extern "C" {
 #endif
 
-#define APEXW_ABI_VERSION 18
+#define APEXW_ABI_VERSION 19
 
 /* status codes */
 enum apexw_status {
@@ -221,6 +221,24 @@ int apexw_abi_version(void);
 int apexw_check_tensor(const apexw_tensor* t, int32_t kind);
 
 /*
+ * The scalar argument checks that a step entry point applies before it enqueues
+ * anything, without enqueueing: kind APEXW_LAUNCH_COMPACT (apexw_compact_step),
+ * APEXW_LAUNCH_Q8 (apexw_q8_step), APEXW_LAUNCH_ULTRA (apexw_ultra_step) or
+ * APEXW_LAUNCH_FACTORED (apexw_factored_step; n_fast counts 0).  The entry points
+ * run exactly these checks, so a caller that checks every launch of a step first
+ * can refuse the whole step before any parameter changes.  Replaces the
+ * reference's validate-before-mutate order around step_fused_8bit
+ * (_execute_cuda_8bit_partition, apexw/optimizer.py:3184-3356) and its step
+ * counter rollback on a refused launch (:3806, :3888, :3969).
+ */
+#define APEXW_LAUNCH_COMPACT 0
+#define APEXW_LAUNCH_Q8 1
+#define APEXW_LAUNCH_FACTORED 4
+#define APEXW_LAUNCH_ULTRA 5
+int apexw_check_launch(int32_t kind, int32_t n_tensors, int64_t n_units, int64_t n_fast_units,
+                       int64_t n_fast_f32_units, const apexw_hparams* hp);
+
+/*
  * Compact-precision fused AdamW step over every tensor of the table in one
  * launch.  p, m, v are updated in place, g is read only.
  */
@@ -330,9 +348,11 @@ int apexw_grad_clip_coef(const apexw_tensor* tensors, int32_t n_tensors,
  * apexw_grad_clip_coef without workspace arguments, allocating nothing: the
  * per-unit partial sums and per-tensor norms live in a fixed device array of
  * the library ((APEXW_NOALLOC_CLIP_MAX_UNITS + APEXW_NOALLOC_CLIP_MAX_TENSORS)
- * floats, 8.5 MiB per GPU, held until the process ends).  Same kernels, same
- * result as apexw_grad_clip_coef.  Returns APEXW_ERR_SIZE, before enqueueing
- * anything, when n_units or n_tensors exceeds its limit.
+ * floats, 32.5 MiB per GPU, held until the process ends: 2^23 units cover an
+ * 8B-parameter list in 2048-element units).  The array used is that of the
+ * stream's device (hipStreamGetDevice; the current device for the null stream).
+ * Same kernels, same result as apexw_grad_clip_coef.  Returns APEXW_ERR_SIZE,
+ * before enqueueing anything, when n_units or n_tensors exceeds its limit.
  * No counterpart in the reference: it is for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc).  Every call on one GPU shares that GPU's array:
@@ -340,7 +360,7 @@ int apexw_grad_clip_coef(const apexw_tensor* tensors, int32_t n_tensors,
  * Nothing in the array needs to start at zero (every entry is written before
  * it is read within one call).
  */
-#define APEXW_NOALLOC_CLIP_MAX_UNITS (1 << 21)
+#define APEXW_NOALLOC_CLIP_MAX_UNITS (1 << 23)
 #define APEXW_NOALLOC_CLIP_MAX_TENSORS (1 << 17)
 int apexw_grad_clip_coef_noalloc(const apexw_tensor* tensors, int32_t n_tensors,
                                  const apexw_unit* units, int64_t n_units, int64_t unit_size,

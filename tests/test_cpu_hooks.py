@@ -25,8 +25,16 @@ class _Rec:
             def __init__(self, group, params):
                 self.group, self.params = group, params
 
-            def execute(self, group, seed, inv, lr=None, wd=None, steps=None):
-                rec.calls.append(dict(params=list(self.params), inv=inv, lr=lr, wd=wd, steps=list(steps)))
+            def prepare(self, group, seed, inv, lr=None, wd=None, steps=None):
+                call = dict(params=list(self.params), inv=inv, lr=lr, wd=wd, steps=list(steps))
+
+                class _Prog:
+                    def run(self):
+                        rec.calls.append(call)
+
+                    def rollback(self):
+                        pass
+                return _Prog()
         return lambda group, params: _Plan(group, params)
 
 

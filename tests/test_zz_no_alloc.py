@@ -22,14 +22,15 @@ def _need_gpu():
         pytest.skip("needs a GPU")
 
 
-def _tables(shapes, seed, dtype=torch.bfloat16):
-    """Device tensor and unit tables (2048-element units) of one grad per shape."""
+def _tables(shapes, seed, dtype=torch.bfloat16, unit=None):
+    """Device tensor and unit tables (2048-element units unless `unit`) of one grad per shape."""
     from apexw_amd import _lib as L
     gen = torch.Generator().manual_seed(seed)
     grads = [(torch.randn(s, generator=gen) * (1e-3 * (1 + i % 7))).to(dtype).cuda() for i, s in enumerate(shapes)]
     code = L.BF16 if dtype == torch.bfloat16 else L.F32
+    unit = unit or L.COMPACT_UNIT
     tab = np.zeros(len(grads), dtype=L.TENSOR_DTYPE)
-    counts = np.array([(g.numel() + L.COMPACT_UNIT - 1) // L.COMPACT_UNIT for g in grads], dtype=np.int64)
+    counts = np.array([(g.numel() + unit - 1) // unit for g in grads], dtype=np.int64)
     for i, g in enumerate(grads):
         # the clip reads only g; p/m/v point at the grad so the descriptor is well formed
         tab[i]["p"] = tab[i]["g"] = tab[i]["m"] = tab[i]["v"] = g.data_ptr()
@@ -43,19 +44,20 @@ def _tables(shapes, seed, dtype=torch.bfloat16):
     return grads, dev(tab), dev(units), torch.from_numpy(begin).cuda(), len(units)
 
 
-def _coef_pair(shapes, seed, clip=1.0):
+def _coef_pair(shapes, seed, clip=1.0, unit=None):
     from apexw_amd import _lib as L
     lib = L.load()
-    grads, tab, units, begin, n_units = _tables(shapes, seed)
+    unit = unit or L.COMPACT_UNIT
+    grads, tab, units, begin, n_units = _tables(shapes, seed, unit=unit)
     stream = torch.cuda.current_stream().cuda_stream
     part = torch.empty(max(n_units, 1), dtype=torch.float32, device="cuda")
     norms = torch.empty(len(grads), dtype=torch.float32, device="cuda")
     coef_a = torch.full((1,), -1.0, device="cuda")
     coef_b = torch.full((1,), -2.0, device="cuda")
-    L.check(lib.apexw_grad_clip_coef(tab.data_ptr(), len(grads), units.data_ptr(), n_units, L.COMPACT_UNIT,
+    L.check(lib.apexw_grad_clip_coef(tab.data_ptr(), len(grads), units.data_ptr(), n_units, unit,
                                      begin.data_ptr(), part.data_ptr(), norms.data_ptr(), clip, 1.0, L.HP_SANITIZE,
                                      coef_a.data_ptr(), None, stream), "apexw_grad_clip_coef")
-    L.check(lib.apexw_grad_clip_coef_noalloc(tab.data_ptr(), len(grads), units.data_ptr(), n_units, L.COMPACT_UNIT,
+    L.check(lib.apexw_grad_clip_coef_noalloc(tab.data_ptr(), len(grads), units.data_ptr(), n_units, unit,
                                              begin.data_ptr(), clip, 1.0, L.HP_SANITIZE, coef_b.data_ptr(), None, stream),
             "apexw_grad_clip_coef_noalloc")
     torch.cuda.synchronize()
@@ -81,6 +83,31 @@ def test_noalloc_clip_matches_workspace_entry_point_twice():
         assert a == b, f"noalloc {b!r} != workspace {a!r}"
         assert 0.0 < b < 1.0
         assert abs(b - ref) <= 1e-6 * ref, (b, ref)
+
+
+def test_noalloc_clip_covers_an_8b_unit_count():
+    """More units than an 8B-parameter list has in 2048-element units (3.92 M at
+    Llama-3-8B), well above 2^21: here as 64-element units of a 256 M-element list,
+    then a smaller list in the same array."""
+    _need_gpu()
+    print("noalloc clip: 4,000,000 units of 64 elements, then 2^21 + 5", flush=True)
+    cases = (([((4_000_000 - 1000) * 64,), (1000 * 64,)], 11), ([(((1 << 21) + 5) * 64,)], 12))
+    for shapes, seed in cases:
+        a, b, ref = _coef_pair(shapes, seed, clip=1.0, unit=64)
+        assert a == b, f"noalloc {b!r} != workspace {a!r}"
+        assert 0.0 < b < 1.0
+        assert abs(b - ref) <= 1e-6 * ref, (b, ref)
+
+
+def test_noalloc_clip_uses_the_streams_device_array():
+    """A non-default stream of the current device: the stream's device array is used and
+    the result equals the workspace entry point's."""
+    _need_gpu()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        a, b, ref = _coef_pair([(5000,), (64, 300)], 13, clip=0.01)
+    torch.cuda.synchronize()
+    assert a == b and abs(b - ref) <= 1e-6 * ref
 
 
 def test_noalloc_clip_unclipped_is_one():

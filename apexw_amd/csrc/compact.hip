@@ -394,8 +394,11 @@ __global__ __launch_bounds__(256) void compact_step_kernel(const apexw_tensor* _
   // one work item = one 512-element group of a unit, so a small launch still
   // puts four waves per unit in flight (the per-element RNG is keyed by the
   // element index, so the split does not change any result)
-  const int64_t stride = (int64_t)gridDim.x * kWaves, n_items = n_units * kGroups;
-  for (int64_t w = (int64_t)blockIdx.x * kWaves + wave; w < n_items; w += stride) {
+  // workgroup b takes items [chunk b, chunk (b + 1)), then strides by the grid (a
+  // grid of one workgroup per unit makes that one pass, see apexw_launch_compact)
+  const int64_t n_items = n_units * kGroups;
+  for (int64_t base = (int64_t)blockIdx.x * kWaves; base < n_items; base += (int64_t)gridDim.x * kWaves)
+  for (int64_t w = base + wave; w < base + kWaves && w < n_items; w += kWaves) {
     const apexw_unit un = units[w / kGroups];
     const int k = (int)(w % kGroups);
     const apexw_tensor& t = tensors[un.tensor];
@@ -430,7 +433,14 @@ static bool compact_combo_ok(uint32_t flags) {
 
 int apexw_launch_compact(const apexw_tensor* tensors, int64_t n_units, const apexw_unit* units,
                          const apexw_hparams* hp, hipStream_t stream) {
-  const int grid = apexw_resident_grid((const void*)compact_step_kernel, n_units * kGroups);
+  // Large launches: one workgroup per unit (its four 512-element groups, one per
+  // wave), so the resident workgroups sweep a narrow, advancing window of the
+  // tensors (C4, 2.16 B elements: 5.45-5.51 ms per step against 5.75-5.95 with a
+  // resident grid striding over the whole launch).  Launches that a resident grid
+  // covers in a few passes keep it (C2, 124 M elements: 0.234-0.257 ms against
+  // 0.252-0.288 with a workgroup per unit).
+  const int resident = apexw_resident_grid((const void*)compact_step_kernel, n_units * kGroups);
+  const int grid = n_units > (int64_t)resident * 8 ? (int)(n_units < INT32_MAX ? n_units : INT32_MAX) : resident;
   hipLaunchKernelGGL(compact_step_kernel, dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }

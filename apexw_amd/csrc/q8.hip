@@ -28,7 +28,10 @@ static __host__ __device__ inline bool apexw_q8_fast_ok(uint32_t flags, uint32_t
 namespace {
 
 constexpr int kWaves = 4;
-constexpr int64_t kFastChunk = 64;   // units per workgroup pass of the full-block kernels
+// units per workgroup of the full-block kernels: a small chunk keeps the resident
+// workgroups on a narrow, advancing window of the tensors (C3, 8.03 B parameters:
+// 11.27 ms per step with 8 units, 11.35 with 16, 11.55 with 32, 11.67 with 64)
+constexpr int64_t kFastChunk = 8;
 
 struct Q8Ctx {
   const apexw_hparams* hp;
@@ -528,7 +531,10 @@ APEXW_DEV void q8_fast_load(const apexw_tensor& t, uint32_t blk, FastRaw<PD>& r)
 }
 
 // The arithmetic and stores of one fast-path block, from its loads.
-template <int PD, bool SR, bool FULL, bool GENERIC>
+// B1HI: the usual orientation of the two lerps, fixed at compile time (beta1 > 1/2:
+// m' = lerp(m, g, 1-b1) takes the a + w (b - a) form and the lookahead lerp(g, m', b1)
+// the b + (w - 1)(b - a) form); otherwise both come from the launch's flags.
+template <int PD, bool SR, bool FULL, bool GENERIC, bool B1HI>
 APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk, const Q8Ctx& c,
                                const FastRaw<PD>& r) {
   const apexw_hparams& hp = *c.hp;
@@ -538,7 +544,8 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
   const float ms_old = r.ms_old;
   const float vs_old = r.vs_old;
   const float decay = (tf & APEXW_FLAG_WD) ? hp.wd_factor : 1.0f;
-  const bool lerp_hi = hf & APEXW_HP_LERP_HI, look_hi = hf & APEXW_HP_LOOK_HI;
+  const bool lerp_hi = B1HI ? false : (bool)(hf & APEXW_HP_LERP_HI);
+  const bool look_hi = B1HI ? true : (bool)(hf & APEXW_HP_LOOK_HI);
   const auto& pw = r.pw;
   const auto& gw = r.gw;
   const auto& mw = r.mw;
@@ -629,7 +636,10 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
         vq[k][q] = vv;
         if (FULL || 4 * q < cnt[k]) vmax = fmaxf(vmax, vv);
         const float r = __builtin_amdgcn_rcpf(fmaxf(__builtin_amdgcn_sqrtf(vv) + hp.eps_scaled, hp.eps)) * hp.step_size;
-        const float r_hi = r * hp.gain_hi, r_lo = r * hp.gain_lo;
+        float r_hi = r * hp.gain_hi, r_lo = r * hp.gain_lo;
+        // keep the two products per quad: otherwise the compiler sinks them below the
+        // per-element select, one multiply per element instead of two per quad
+        asm volatile("" : "+v"(r_hi), "+v"(r_lo));
 #pragma unroll
         for (int i = 0; i < 4; ++i) upd[b + i] = look[b + i] * ((m[b + i] * g[b + i] >= 0.0f) ? r_hi : r_lo);
       }
@@ -763,7 +773,11 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
     t.m_scale[blk] = ms;
     t.v_scale[blk] = vs;
   }
-  const float rms = 1.0f / ms, rvs = 1.0f / vs;
+  const float rvs = __builtin_amdgcn_rcpf(vs);
+  // SR: x = m / ms through the hardware reciprocal (within 1 ulp) shrunk by 2^-20, so
+  // |x| <= (1 + 2^-23)(1 - 2^-20) < 1 - 2^-21 and y = x + 3 rounds inside [2, 4): the
+  // code's bucket needs no clamp (the 2^-20 relative shrink is far below the code noise)
+  const float rms_sr = __builtin_amdgcn_rcpf(ms) * 0x1.ffffep-1f;
   const float rms_rn = rcp_refined(ms), rvs_rn = rcp_refined(vs);
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
@@ -784,9 +798,9 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
         uint32_t gc[2];
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-          // y = x + 3 for x = m / scale in [-1, 1], clamped below 4: the top 7
-          // mantissa bits of y in [2, 4) are the bucket; the table is affine in y
-          const float y = __builtin_amdgcn_fmed3f(fmaf(mnew[k][2 * b + i], rms, 3.0f), 2.0f, 0x1.fffffep+1f);
+          // y = x + 3 for x = m / scale in (-1, 1): the top 7 mantissa bits of y in
+          // [2, 4) are the bucket; the table is affine in y
+          const float y = fmaf(mnew[k][2 * b + i], rms_sr, 3.0f);
           const float4 fr = c.frac16[(__float_as_uint(y) >> 16) & 127u];
           gc[i] = (uint32_t)fabsf(fminf(fmaf(fr.y, y, fr.x), fmaf(fr.w, y, fr.z)));
         }
@@ -841,11 +855,11 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
   }
 }
 
-template <int PD, bool SR, bool FULL, bool GENERIC>
+template <int PD, bool SR, bool FULL, bool GENERIC, bool B1HI>
 APEXW_DEV void q8_block_fast(const apexw_tensor& t, uint32_t tix, uint32_t blk, const Q8Ctx& c) {
   FastRaw<PD> r;
   q8_fast_load<PD, FULL>(t, blk, r);
-  q8_fast_compute<PD, SR, FULL, GENERIC>(t, tix, blk, c, r);
+  q8_fast_compute<PD, SR, FULL, GENERIC, B1HI>(t, tix, blk, c, r);
 }
 
 // Dense m and v (bf16 or fp32): the fallback branch of _step_ultra
@@ -1196,7 +1210,7 @@ __global__ __launch_bounds__(256) void ultra_step_kernel(const apexw_tensor* __r
 // dtype PD and stochastic rounding SR; each (dtype, SR) pair is its own kernel so
 // one variant's register footprint does not lower another's occupancy (bf16: 142
 // VGPRs with SR, occupancy 3; 93 without, occupancy 5).
-template <int PD, bool SR>
+template <int PD, bool SR, bool B1HI>
 __global__ __launch_bounds__(256) void q8_fast_kernel(const apexw_tensor* __restrict__ tensors,
                                                       const apexw_unit* __restrict__ units,
                                                       int64_t n_units, apexw_hparams hp_in) {
@@ -1241,10 +1255,10 @@ __global__ __launch_bounds__(256) void q8_fast_kernel(const apexw_tensor* __rest
     if (!apexw_q8_fast_ok(t.flags, t.block) || ((t.flags >> APEXW_FLAG_PDT_SHIFT) & 3u) != (uint32_t)PD) continue;
     const bool full = (int64_t)(un.unit + 1) * 2048 <= t.n;
     const bool gen = t.flags & APEXW_FLAG_GENERIC;
-    if (full && !gen) q8_block_fast<PD, SR, true, false>(t, un.tensor, un.unit, c);
-    else if (full) q8_block_fast<PD, SR, true, true>(t, un.tensor, un.unit, c);
-    else if (!gen) q8_block_fast<PD, SR, false, false>(t, un.tensor, un.unit, c);
-    else q8_block_fast<PD, SR, false, true>(t, un.tensor, un.unit, c);
+    if (full && !gen) q8_block_fast<PD, SR, true, false, B1HI>(t, un.tensor, un.unit, c);
+    else if (full) q8_block_fast<PD, SR, true, true, B1HI>(t, un.tensor, un.unit, c);
+    else if (!gen) q8_block_fast<PD, SR, false, false, B1HI>(t, un.tensor, un.unit, c);
+    else q8_block_fast<PD, SR, false, true, B1HI>(t, un.tensor, un.unit, c);
   }
 }
 
@@ -1363,12 +1377,16 @@ int apexw_launch_q8_fast(const apexw_tensor* tensors, int64_t n_units, const ape
   const int64_t chunks = (n_units + kFastChunk - 1) / kFastChunk;
   const int grid = (int)(chunks < INT32_MAX ? chunks : INT32_MAX);
   const bool sr = hp->flags & APEXW_HP_SR;
+  const bool b1hi = !(hp->flags & APEXW_HP_LERP_HI) && (hp->flags & APEXW_HP_LOOK_HI);
+#define APEXW_FAST(PD, SR, HI) \
+  hipLaunchKernelGGL((q8_fast_kernel<PD, SR, HI>), dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp)
   if (p_dtype == APEXW_F32) {
-    if (sr) hipLaunchKernelGGL((q8_fast_kernel<APEXW_F32, true>), dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
-    else hipLaunchKernelGGL((q8_fast_kernel<APEXW_F32, false>), dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
+    if (sr) { if (b1hi) APEXW_FAST(APEXW_F32, true, true); else APEXW_FAST(APEXW_F32, true, false); }
+    else { if (b1hi) APEXW_FAST(APEXW_F32, false, true); else APEXW_FAST(APEXW_F32, false, false); }
   } else {
-    if (sr) hipLaunchKernelGGL((q8_fast_kernel<APEXW_BF16, true>), dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
-    else hipLaunchKernelGGL((q8_fast_kernel<APEXW_BF16, false>), dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
+    if (sr) { if (b1hi) APEXW_FAST(APEXW_BF16, true, true); else APEXW_FAST(APEXW_BF16, true, false); }
+    else { if (b1hi) APEXW_FAST(APEXW_BF16, false, true); else APEXW_FAST(APEXW_BF16, false, false); }
   }
+#undef APEXW_FAST
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }

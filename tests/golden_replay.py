@@ -9,8 +9,8 @@ import os
 import numpy as np
 import torch
 
-from golden.make_golden import (FP16_CASES, FV_KW, FV_Q8_SHAPES, HOOK_KW, HOOK_SHAPES, PREC_CASES, SD_CASES,
-                                 _fingerprint, _grad, _param)
+from golden.make_golden import (FP16_CASES, FUSED_CASES, FUSED_SHAPES, FV_KW, FV_Q8_SHAPES, HOOK_KW, HOOK_SHAPES,
+                                 PREC_CASES, SD_CASES, _fingerprint, _grad, _param)
 from golden.sd_codec import decode
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -126,6 +126,26 @@ def hook_inputs(name):
         grads.append(per_step)
     np.testing.assert_array_equal(np.array(fp, dtype=np.int64), gold["fingerprint"])
     return host, grads, gold
+
+
+def fused_inputs(name):
+    """enable_fused_backward case ``name``: (dtype, kwargs, initial parameters, per
+    step the list of per-pass grads, golden dict)."""
+    dtype, steps, passes, seed, kwargs = FUSED_CASES[name]
+    gold = load(name)
+    gen = torch.Generator().manual_seed(seed)
+    host = [_param(s, dtype, gen) for s in FUSED_SHAPES]
+    fp = [_fingerprint(p) for p in host]
+    grads = []
+    for _ in range(steps):
+        per_step = []
+        for _ in range(passes):
+            gs = [_grad(p.shape, dtype, gen) for p in host]
+            fp.extend(_fingerprint(g) for g in gs)
+            per_step.append(gs)
+        grads.append(per_step)
+    np.testing.assert_array_equal(np.array(fp, dtype=np.int64), gold["fingerprint"])
+    return dtype, kwargs, host, grads, gold
 
 
 def sd_inputs(name):

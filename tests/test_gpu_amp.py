@@ -200,28 +200,64 @@ def test_grad_scaler_step_reads_nothing_on_the_host():
         assert all(int(opt.state[p]["step"]) == 3 for p in m.parameters())
 
 
-@pytest.mark.parametrize("precision", ["compact", "8bit"])
-def test_device_amp_equals_host_amp_with_skipped_steps(precision):
+AMP_PAIR_CASES = [
+    ("compact", {}, 0),
+    ("8bit", {}, 0),
+    # a centralized 8-bit group unscales a prepared copy of its grads: it must read
+    # found_inf on the host, or an inf step would be applied to the sanitized grads
+    ("8bit", dict(grad_centralization=True), 0),
+    ("ultra", dict(threshold=4096), 0),
+    # step counts near 5e4: the device's bias corrections (double pow) against the host's
+    ("8bit", {}, 49_990),
+    ("compact", {}, 49_990),
+]
+
+
+def _restep(opt, start):
+    """Set every parameter's step counter to ``start`` through the state mapping,
+    as a resumed checkpoint would."""
+    sd = opt.state_dict()
+    for st in sd["state"].values():
+        st["step"] = torch.tensor(float(start))
+    opt.load_state_dict(sd)
+
+
+@pytest.mark.parametrize("precision,extra,start", AMP_PAIR_CASES,
+                         ids=[f"{c[0]}{'-gc' if c[1].get('grad_centralization') else ''}-from{c[2]}"
+                              for c in AMP_PAIR_CASES])
+def test_device_amp_equals_host_amp_with_skipped_steps(precision, extra, start):
     """The same sequence of scaled steps, some with found_inf, through the device
     path (GradScaler's CUDA tensors) and the host path (the same values as CPU
     tensors, read on the host like the reference): identical parameters and
     state, and step counters that count only the steps taken (exact after
-    state_dict(), which subtracts the skips the device saw)."""
+    state_dict(), which subtracts the skips the device saw).  ``start``: the
+    step counters are first set to it (one unscaled step, then a state_dict
+    round trip), so the bias corrections come from large step counts."""
     _need_gpu()
     from apexw_amd import ApexW
-    print(f"device vs host amp {precision}", flush=True)
+    print(f"device vs host amp {precision} {extra} from step {start}", flush=True)
     gen = torch.Generator().manual_seed(21)
-    shapes = [(256, 128), (300,), (64, 33), (16384,)]
+    shapes = [(256, 128), (300,), (64, 33), (16384,), (512, 64)]
     host = [(torch.randn(s, generator=gen) * 0.02).bfloat16() for s in shapes]
     pa = [torch.nn.Parameter(h.cuda()) for h in host]
     pb = [torch.nn.Parameter(h.cuda()) for h in host]
-    kw = dict(lr=1e-3, weight_decay=0.1, precision=precision, stochastic_rounding=False)
+    kw = dict(lr=1e-3, weight_decay=0.1, precision=precision, stochastic_rounding=False, **extra)
     oa, ob = ApexW(pa, **kw), ApexW(pb, **kw)
+    if start:
+        for a, b in zip(pa, pb):
+            g = (torch.randn(a.shape, generator=gen) * 1e-3).bfloat16()
+            a.grad, b.grad = g.cuda(), g.cuda()
+        oa.step()
+        ob.step()
+        _restep(oa, start)
+        _restep(ob, start)
     scale = 1024.0
     infs = [0, 0, 1, 0, 1, 1, 0]
     for it, inf in enumerate(infs):
         for a, b in zip(pa, pb):
             g = (torch.randn(a.shape, generator=gen) * 1e-3 * scale).bfloat16()
+            if inf and a.dim() == 2:
+                g[0, 0] = float("inf")            # the step GradScaler found an inf in
             a.grad, b.grad = g.cuda(), g.cuda()
         oa.grad_scale, oa.found_inf = torch.tensor(scale, device="cuda"), torch.tensor(float(inf), device="cuda")
         ob.grad_scale, ob.found_inf = torch.tensor(scale), torch.tensor(float(inf))
@@ -229,15 +265,55 @@ def test_device_amp_equals_host_amp_with_skipped_steps(precision):
         ob.step()
     sd = oa.state_dict()
     torch.cuda.synchronize()
-    taken = len(infs) - sum(infs)
+    taken = start + len(infs) - sum(infs)
     for a, b in zip(pa, pb):
         assert torch.equal(a, b)
+        assert bool(torch.isfinite(a).all())
         sa, sb = oa.state[a], ob.state[b]
         for k in ("exp_avg", "exp_avg_sq", "exp_avg_scales", "exp_avg_sq_scales"):
             if k in sb:
                 assert torch.equal(sa[k], sb[k]), k
         assert float(sa["step"]) == float(sb["step"]) == taken
     assert all(float(st["step"]) == taken for st in sd["state"].values())
+
+
+def test_device_amp_with_more_step_counts_than_its_table():
+    """An 8-bit group whose parameters hold 20 distinct step counts (more launches
+    than the device-side AMP table's 16): GradScaler's scale is then read on the
+    host for that step, and the results equal the host path's."""
+    _need_gpu()
+    from apexw_amd import ApexW
+    from apexw_amd import _lib as L
+    print("device amp, 20 distinct step counts", flush=True)
+    gen = torch.Generator().manual_seed(23)
+    n = 20
+    assert n > L.AMP_MAX_LAUNCHES
+    host = [(torch.randn(64, 64, generator=gen) * 0.02).bfloat16() for _ in range(n)]
+    pa = [torch.nn.Parameter(h.cuda()) for h in host]
+    pb = [torch.nn.Parameter(h.cuda()) for h in host]
+    kw = dict(lr=1e-3, weight_decay=0.1, precision="8bit", stochastic_rounding=False)
+    oa, ob = ApexW(pa, **kw), ApexW(pb, **kw)
+    scale = 256.0
+    for it in range(n + 3):
+        for i, (a, b) in enumerate(zip(pa, pb)):
+            if it < n and i < it:
+                a.grad = b.grad = None          # parameter i misses the first i steps
+                continue
+            g = (torch.randn(a.shape, generator=gen) * 1e-3 * scale).bfloat16()
+            a.grad, b.grad = g.cuda(), g.cuda()
+        inf = float(it == n + 1)
+        oa.grad_scale, oa.found_inf = torch.tensor(scale, device="cuda"), torch.tensor(inf, device="cuda")
+        ob.grad_scale, ob.found_inf = torch.tensor(scale), torch.tensor(inf)
+        oa.step()
+        ob.step()
+    torch.cuda.synchronize()
+    counts = sorted({int(oa.state[a]["step"]) for a in pa})
+    assert len(counts) == n, counts
+    for i, (a, b) in enumerate(zip(pa, pb)):
+        assert torch.equal(a, b), i
+        for k in ("exp_avg", "exp_avg_sq", "exp_avg_scales", "exp_avg_sq_scales"):
+            assert torch.equal(oa.state[a][k], ob.state[b][k]), (i, k)
+        assert float(oa.state[a]["step"]) == float(ob.state[b]["step"]) == i + 3   # i + 1, then 2 of 3
 
 
 def test_muon_device_amp_equals_host_amp_with_skipped_steps():

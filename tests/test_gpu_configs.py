@@ -117,40 +117,60 @@ def _tensor_keys(st):
 
 # ---------------------------------------------------------------------- the mirror
 class Mirror:
-    """CPU oracle copies of selected GPU parameters (whole tensors, or their last
-    ``rows`` rows with the matching state slices), re-synced from the GPU
-    before every step."""
+    """CPU oracle copies of selected GPU parameters, re-synced from the GPU before
+    every step.  An entry is (i, None): the whole tensor i; (i, rows): its last
+    ``rows`` rows; or (i, rows, row0): rows row0 .. row0 + rows - 1 -- each with
+    the matching slices of its state (the slice must start on a quantization
+    block).  ``retarget`` moves the slices between steps (same row counts)."""
 
     def __init__(self, gps, entries, kw, n_group):
-        self.gps, self.entries, self.n_group = gps, entries, n_group
-        self.cps = [nn.Parameter(self._gpu_p(e).cpu().clone()) for e in entries]
+        self.gps, self.entries, self.n_group = gps, list(entries), n_group
+        self.cps = [nn.Parameter(self._gpu_p(e).cpu().clone()) for e in self.entries]
         self.copt = OracleApexW(self.cps, **kw)
         self.pre = None
 
+    def retarget(self, entries):
+        entries = list(entries)
+        assert [(e[0], e[1]) for e in entries] == [(e[0], e[1]) for e in self.entries], "retarget: same tensors and rows"
+        self.entries = entries
+
+    def _row0(self, e):
+        i, rows = e[0], e[1]
+        return self.gps[i].shape[0] - rows if len(e) < 3 else e[2]
+
     def _gpu_p(self, e):
-        i, rows = e
+        i, rows = e[0], e[1]
         p = self.gps[i].detach()
-        return p if rows is None else p[-rows:]
+        if rows is None:
+            return p
+        r0 = self._row0(e)
+        assert 0 <= r0 and r0 + rows <= p.shape[0], f"rows {r0}..{r0 + rows} of {tuple(p.shape)}"
+        return p[r0:r0 + rows]
 
     def _gpu_state(self, gopt, e):
-        i, rows = e
+        i, rows = e[0], e[1]
         st = gopt.state[self.gps[i]]
         if rows is None:
             return st
         p = self.gps[i]
-        n0 = p.numel() - rows * (p.numel() // p.shape[0])
+        n0 = self._row0(e) * (p.numel() // p.shape[0])
+        n1 = n0 + rows * (p.numel() // p.shape[0])
         out = {}
         for k, v in st.items():
             if torch.is_tensor(v) and k != "step":
                 ratio = v.numel() / p.numel()
-                assert float(n0 * ratio).is_integer(), f"slice of {k} not aligned"
-                out[k] = v.reshape(-1)[int(n0 * ratio):]
+                assert float(n0 * ratio).is_integer() and float(n1 * ratio).is_integer(), f"slice of {k} not aligned"
+                out[k] = v.reshape(-1)[int(n0 * ratio):int(n1 * ratio)]
             else:
                 out[k] = v
         return out
 
     def grads(self, gpu_grads):
-        return [(gpu_grads[i] if rows is None else gpu_grads[i][-rows:]).cpu().clone() for i, rows in self.entries]
+        out = []
+        for e in self.entries:
+            g = gpu_grads[e[0]]
+            out.append((g if e[1] is None else g[self._row0(e):self._row0(e) + e[1]]).cpu().clone())
+        return out
 
     def snapshot(self, gopt):
         """Before the GPU step: the subset's parameters and (existing) state."""
@@ -282,7 +302,9 @@ def _set_sr(gopt, mirror, on):
 
 
 def _drive(tag, shapes, dtype, kw, entries, steps, sr, seed, scales=None, zero=(), per_step=None, sr_from=0):
-    """Step the full list on the GPU ``steps`` times; mirror ``entries`` on the CPU.
+    """Step the full list on the GPU ``steps`` times; mirror ``entries`` on the CPU
+    (a list, or a function of the step number returning the step's entries: the
+    same tensors and row counts every step, the slices free to move).
 
     sr: stochastic rounding from step ``sr_from`` on (off before it).
     per_step(step, gopt, gps, grads, cpu_grads) may replace the oracle's grads
@@ -295,9 +317,12 @@ def _drive(tag, shapes, dtype, kw, entries, steps, sr, seed, scales=None, zero=(
     torch.manual_seed(seed)      # ApexW draws its rounding-noise seed from torch's generator
     gopt = ApexW(gps, **kw)
     okw = {k: v for k, v in kw.items() if k != "clip_grad_norm"}
-    mirror = Mirror(gps, entries, okw, len(shapes))
+    entries_at = entries if callable(entries) else (lambda step: entries)
+    mirror = Mirror(gps, entries_at(0), okw, len(shapes))
     stats = None
     for step in range(steps):
+        if step:
+            mirror.retarget(entries_at(step))
         sr_step = sr and step >= sr_from
         if sr and step == sr_from and step > 0:
             _set_sr(gopt, mirror, True)
@@ -371,36 +396,148 @@ def test_c2_gpt2_small_sr_3_steps():
     assert stats["bf16"].n >= 10_000_000
 
 
+def _c2_drift_entries(shapes):
+    """Every C2 tensor: vectors whole, matrices as 64-row slices (the first rows of
+    the even-numbered tensors, the last rows of the odd ones)."""
+    out = []
+    for i, s in enumerate(shapes):
+        if len(s) == 1 or s[0] <= 64:
+            out.append((i, None))
+        else:
+            out.append((i, 64, 0) if i % 2 == 0 else (i, 64))
+    return out
+
+
+def _ulps(got, ref):
+    """bf16 distance in ulps (int64) between a GPU tensor and a CPU oracle tensor."""
+    return bf16_ulp_diff(got.detach().cpu().reshape(-1).contiguous(), ref.detach().reshape(-1).contiguous()).long()
+
+
+def test_c2_gpt2_small_drift_100_steps():
+    """C2 for BASELINE's 100 steps, SR off, with NO re-sync: the GPU steps the whole
+    list, the oracle steps its own copy of every tensor (vectors whole, 64-row
+    slices of the matrices, 5.6 M elements) from the same start with the same
+    grads, and the two trajectories are compared every 10 steps.
+
+    m and v never read p and both sides see the same grads, so their differences
+    come from rounding alone and stay at the per-step bars (bf16 m <= 1 ulp, a
+    difference decays by beta1 each step; fp32 v 1e-6 relative).  p carries
+    every rounding flip forward: a flip is one bf16 ulp of p where it happened,
+    and |p| never exceeded |p_0| + 2 lr t by step t (AdamW's update is about lr
+    per step), so a difference is measured in ulps of that magnitude, e = dp /
+    ulp(|p_0| + 2 lr t).  A flip needs the GPU's and torch's fp32 update to
+    straddle a bf16 rounding boundary, which the per-step tests see on a few
+    elements per million; bars: |e| <= 1 anywhere, e != 0 on fewer than 1e-4 of
+    the elements, mean signed e under 1e-5 -- a systematic error (a bias
+    correction or a decay off after some step count) moves every element the
+    same way and fails the last two bars at once."""
+    _need_gpu()
+    from apexw_amd import ApexW
+    _say("C2 drift, 100 steps")
+    shapes, scales = _gpt2()
+    gen = torch.Generator(device="cuda").manual_seed(202)
+    gps = _params(shapes, torch.bfloat16, gen)
+    kw = dict(KW, stochastic_rounding=False)
+    torch.manual_seed(202)
+    gopt = ApexW(gps, **kw)
+    entries = _c2_drift_entries(shapes)
+    mirror = Mirror(gps, entries, kw, len(shapes))
+    p0 = [cp.detach().float().abs().reshape(-1).clone() for cp in mirror.cps]
+    n_el = sum(cp.numel() for cp in mirror.cps)
+    assert n_el > 5_000_000
+    lr = kw["lr"]
+    for step in range(100):
+        grads = _grads(shapes, torch.bfloat16, gen, scales)
+        for p, g in zip(gps, grads):
+            p.grad = g
+        if step == 0:
+            mirror.snapshot(gopt)
+        gopt.step()
+        cgrads = mirror.grads(grads)
+        if step == 0:
+            mirror.load()
+            torch.cuda.synchronize()
+            mirror.check_layout(gopt)
+        mirror.step(cgrads)
+        if (step + 1) % 10:
+            continue
+        torch.cuda.synchronize()
+        t = step + 1
+        diff, signed, worst, worst_at, worst_m, worst_v = 0, 0.0, 0.0, None, 0, 0.0
+        for j, (e, cp) in enumerate(zip(mirror.entries, mirror.cps)):
+            gp = mirror._gpu_p(e).detach().cpu().float().reshape(-1)
+            rp = cp.detach().float().reshape(-1)
+            unit = _bf16_ulp(p0[j] + 2.0 * lr * t)
+            err = (gp.double() - rp.double()) / unit.double()
+            diff += int((err != 0).sum())
+            signed += float(err.sum())
+            if float(err.abs().max()) > worst:
+                worst, worst_at = float(err.abs().max()), e
+            gs, cs = mirror._gpu_state(gopt, e), mirror.copt.state[cp]
+            worst_m = max(worst_m, int(_ulps(gs["exp_avg"], cs["exp_avg"]).max()))
+            v, vr = gs["exp_avg_sq"].detach().cpu().reshape(-1).double(), cs["exp_avg_sq"].reshape(-1).double()
+            worst_v = max(worst_v, float(((v - vr).abs() / (vr.abs() + 1e-30)).max()))
+            assert float(gs["step"]) == float(cs["step"]) == t
+        frac, mean = diff / n_el, signed / n_el
+        _say(f"C2 drift step {t}: p differs at {diff} of {n_el} elements ({frac:.2e}), worst {worst:.2f} "
+             f"(tensor {worst_at}), mean signed {mean:+.2e}; m worst {worst_m} ulp; v worst {worst_v:.2e} relative")
+        assert worst <= 1 and worst_m <= 1 and worst_v <= 1e-6, (t, worst, worst_m, worst_v)
+        assert frac < 1e-4 and abs(mean) < 1e-5, (t, frac, mean)
+
+
 # ---------------------------------------------------------------------- C3
-def _c3_entries(shapes):
-    layer = [(i, None) for i in range(1, 10)]                                  # q k v o gate up down + 2 norms
-    norms = [(i, None) for i, s in enumerate(shapes) if len(s) == 1 and i > 9]  # the other 63 RMSNorms
-    tails = [(0, 256), (len(shapes) - 1, 256)]                                 # last 2^20 of embed / lm_head
-    return layer + norms + tails
+def _c3_slice_rows(shape):
+    """Rows of a mirrored C3 matrix slice: more than 262,144 elements (the oracle's
+    chunked path, as for the whole tensor) in whole 2048-element blocks."""
+    cols = shape[1]
+    rows = -(-262145 // cols)
+    while (rows * cols) % 2048:
+        rows += 1
+    return rows
+
+
+def _c3_entries(shapes, seed):
+    """Per step, for every one of the 291 tensors: the 65 RMSNorms whole, and for
+    each of the 226 matrices two row slices of more than 2^18 elements (130 or
+    133 2048-element blocks) -- one at a random offset, drawn afresh each step,
+    and the last rows (the tensor's last block)."""
+    norms = [(i, None) for i, s in enumerate(shapes) if len(s) == 1]
+    mats = [i for i, s in enumerate(shapes) if len(s) == 2]
+
+    def at(step):
+        rng = np.random.default_rng(seed + 7919 * step)
+        out = list(norms)
+        for i in mats:
+            rows = _c3_slice_rows(shapes[i])
+            r0 = int(rng.integers(0, shapes[i][0] - 2 * rows + 1))
+            out += [(i, rows, r0), (i, rows)]
+        return out
+    return at
 
 
 def test_c3_llama3_8b_8bit_rne_2_steps():
-    """C3 shapes (8.03B params, 291 tensors), 8-bit, SR off, 2 steps; checked: one
-    whole layer, all 65 RMSNorms and the last 2^20 elements of embed and lm_head."""
+    """C3 shapes (8.03B params, 291 tensors), 8-bit, SR off, 2 steps; checked every
+    step: all 65 RMSNorms, and for each of the 226 matrices a random slice and
+    its last rows (more than 2^18 elements each, 121 M elements per step)."""
     _need_gpu()
     _say("C3 rne")
     shapes = llama3_8b_shapes()
     assert len(shapes) == 291 and sum(math.prod(s) for s in shapes) == 8_030_261_248
     try:
-        _drive("C3", shapes, torch.bfloat16, dict(KW, precision="8bit"), _c3_entries(shapes), 2, False, seed=300)
+        _drive("C3", shapes, torch.bfloat16, dict(KW, precision="8bit"), _c3_entries(shapes, 300), 2, False, seed=300)
     finally:
         torch.cuda.empty_cache()
 
 
 def test_c3_llama3_8b_8bit_sr_3_steps():
-    """C3 as benchmarked (SR on), 3 steps: the fast full-block NF4 kernel on the layer's
-    matrices and the embed / lm_head tails, the INT8 + log-u8 general kernel on the
-    RMSNorms; steps 2 and 3 start from non-zero state."""
+    """C3 as benchmarked (SR on), 3 steps, the slices of the RNE test: the fast
+    full-block NF4 kernel on every matrix, the INT8 + log-u8 general kernel on
+    the RMSNorms; steps 2 and 3 start from non-zero state."""
     _need_gpu()
     _say("C3 sr")
     shapes = llama3_8b_shapes()
     try:
-        stats = _drive("C3", shapes, torch.bfloat16, dict(KW, precision="8bit"), _c3_entries(shapes), 3, True,
+        stats = _drive("C3", shapes, torch.bfloat16, dict(KW, precision="8bit"), _c3_entries(shapes, 301), 3, True,
                        seed=301)
     finally:
         torch.cuda.empty_cache()

@@ -12,6 +12,12 @@
   8-bit ApexW that converts them to bf16 and steps the large ones inside
   backward, 3 optimizer steps of one or two backward passes each, with no
   resynchronisation between steps; same bars.
+* enable_fused_backward trajectories (tests/golden/fused_*.npz): 8-bit and
+  compact, bf16 and fp32 parameters, 6 optimizer steps of one or two backward
+  passes each (grad_accum_steps), every parameter stepped inside its own
+  post-accumulate hook; no resynchronisation; same bars, except fp32
+  parameters: 1e-6 relative plus 2^-20 lr per step taken (a few fp32 ulps of
+  each step's update, which at lr 1e-2 is as large as p and can cancel it).
 """
 
 import numpy as np
@@ -19,7 +25,7 @@ import pytest
 import torch
 import torch.nn as nn
 
-from golden_replay import HOOK_CASES, SD_CASES, hook_inputs, sd_inputs, state_keys
+from golden_replay import FUSED_CASES, HOOK_CASES, SD_CASES, fused_inputs, hook_inputs, sd_inputs, state_keys
 from test_gpu_parity import _cmp_f32, _cmp_tensor
 
 pytestmark = pytest.mark.gpu
@@ -64,6 +70,33 @@ def test_in_backward_matches_reference_trajectory(name):
         _cmp_state(st, gold, i, ("exp_avg", "exp_avg_scales", "exp_avg_sq", "exp_avg_sq_scales"))
         assert float(st["step"]) == float(gold[f"step_{i}"][0]), f"step_{i}"
     opt._disable_auto_8bit_hooks()
+
+
+@pytest.mark.parametrize("name", sorted(FUSED_CASES))
+def test_fused_backward_matches_reference_trajectory(name):
+    _need_gpu()
+    from apexw_amd import ApexW
+    print(f"reference enable_fused_backward trajectory {name}", flush=True)
+    dtype, kwargs, host, grads, gold = fused_inputs(name)
+    params = [nn.Parameter(h.cuda()) for h in host]
+    opt = ApexW(params, **kwargs)
+    opt.enable_fused_backward(grad_accum_steps=len(grads[0]))
+    for per_step in grads:
+        for gs in per_step:
+            torch.autograd.backward([p.view_as(p) for p in params], grad_tensors=[g.cuda() for g in gs])
+        assert all(p.grad is None for p in params)
+        opt.step()
+        opt.zero_grad(set_to_none=True)
+    torch.cuda.synchronize()
+    steps = len(grads)
+    for i, p in enumerate(params):
+        _cmp_tensor(p.data, gold[f"p_{i}"], f"p_{i}", floor=2.0 ** -20 * kwargs["lr"] * steps + 1e-9)
+        st = opt.state[p]
+        keys = state_keys(gold, i)
+        assert keys == sorted(k for k, v in st.items() if torch.is_tensor(v) and k != "step"), f"state keys {i}"
+        _cmp_state(st, gold, i, keys)
+        assert float(st["step"]) == float(gold[f"step_{i}"][0]) == 6.0, f"step_{i}"
+    opt.disable_fused_backward()
 
 
 def _rel_fro(a, b):

@@ -15,7 +15,8 @@ import numpy as np
 import pytest
 import torch
 
-from golden_replay import CASES, HOOK_CASES, SD_CASES, hook_inputs, load, replay, sd_inputs, state_keys, to_torch
+from golden_replay import (CASES, FUSED_CASES, HOOK_CASES, SD_CASES, fused_inputs, hook_inputs, load, replay,
+                           sd_inputs, state_keys, to_torch)
 from oracle.clip import clip_grads_
 from oracle.optim import OracleApexW
 
@@ -183,6 +184,42 @@ def test_oracle_hooks_match_reference_trajectory(name):
             np.testing.assert_array_equal(_as_np(st[k]).reshape(-1), gold[f"st_{i}_{k}"].reshape(-1),
                                           err_msg=f"{k}_{i}")
         assert float(st["step"]) == float(gold[f"step_{i}"][0]), f"step_{i}"
+
+
+def fused_group(kwargs):
+    """The group dict oracle.hooks.fused_param_step reads, from ApexW's constructor
+    defaults (8-bit betas (0.9, 0.999), compact (0.9, 0.99), eps 1e-8,
+    decay_norm_only on)."""
+    prec = kwargs.get("precision", "compact")
+    return dict(lr=kwargs["lr"], betas=(0.9, 0.999) if prec == "8bit" else (0.9, 0.99), eps=1e-8,
+                weight_decay=kwargs["weight_decay"], decay_norm_only=True, precision=prec,
+                stochastic_rounding=kwargs["stochastic_rounding"], block_size=None, int4_m=None)
+
+
+@pytest.mark.parametrize("name", sorted(FUSED_CASES))
+def test_oracle_fused_backward_matches_reference_trajectory(name):
+    """enable_fused_backward over 6 steps (bias corrections of steps 1..6, the
+    momentum's INT8 scale without the EMA floor from step 2 on), one or two
+    backward passes per step: each parameter's grads summed in its own dtype, as
+    autograd accumulates them, then oracle.hooks.fused_param_step.  Bit-exact."""
+    from oracle import hooks as H
+    dtype, kwargs, host, grads, gold = fused_inputs(name)
+    group = fused_group(kwargs)
+    params = [torch.nn.Parameter(h.clone()) for h in host]
+    states = {}
+    for per_step in grads:
+        for i, p in enumerate(params):
+            acc = per_step[0][i].clone()
+            for gs in per_step[1:]:
+                acc += gs[i]
+            H.fused_param_step(p, acc, states.setdefault(p, {}), group)
+    for i, p in enumerate(params):
+        np.testing.assert_array_equal(_as_np(p.data).reshape(-1), gold[f"p_{i}"].reshape(-1), err_msg=f"p_{i}")
+        st = states[p]
+        for k in state_keys(gold, i):
+            np.testing.assert_array_equal(_as_np(st[k]).reshape(-1), gold[f"st_{i}_{k}"].reshape(-1),
+                                          err_msg=f"{k}_{i}")
+        assert float(st["step"]) == float(gold[f"step_{i}"][0]) == 6.0
 
 
 @pytest.mark.parametrize("name", ["sd_compact", "sd_q8"])

@@ -13,7 +13,7 @@ import numpy as np
 
 from ._build import LIB_PATH
 
-ABI_VERSION = 19
+ABI_VERSION = 20
 
 # dtype codes
 F32, BF16, F16, U8, I8 = 0, 1, 2, 3, 4
@@ -87,7 +87,12 @@ class HParams(ctypes.Structure):
                 ("bc2_sqrt", ctypes.c_float), ("gain_hi", ctypes.c_float), ("gain_lo", ctypes.c_float),
                 ("clip_coef", ctypes.c_void_p), ("seed", ctypes.c_uint64), ("step", ctypes.c_uint32),
                 ("mode", ctypes.c_uint32), ("flags", ctypes.c_uint32), ("grad_inv_scale", ctypes.c_float),
-                ("amp", ctypes.c_void_p)]
+                ("amp", ctypes.c_void_p), ("rows", ctypes.c_void_p)]
+
+
+assert ctypes.sizeof(HParams) == 104
+# apexw_row_means: grad centralization's row means of one 8-bit / ultra descriptor
+ROW_MEANS_DTYPE = np.dtype([("means", np.uint64), ("row_len", np.int64)])
 
 
 # apexw_amp_launch: one launch's host inputs to apexw_amp_prepare; apexw_amp_dyn: its device output
@@ -148,7 +153,8 @@ SIGNATURES = {
     "apexw_compact_step": (ctypes.c_int, [_vp, _i32, _vp, _i64, _HP, _vp]),
     "apexw_ultra_step": (ctypes.c_int, [_vp, _i32, _vp, _i64, _HP, _vp]),
     "apexw_q8_step": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _i64, _HP, _vp]),
-    "apexw_grad_clip_coef": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _vp, _vp, _vp, _f32, _f32, _u32, _vp, _vp, _vp]),
+    "apexw_grad_clip_coef": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _vp, _vp, _vp, _f32, _f32, _u32, _vp, _vp, _vp,
+                                            _vp]),
     "apexw_grad_clip_coef_noalloc": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _vp, _f32, _f32, _u32, _vp, _vp, _vp]),
     "apexw_gemm_nt_bf16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                           _i32, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _vp]),

@@ -221,9 +221,11 @@ class StepPlan:
         self._scan_addrs = (self.p_ptrs.ctypes.data, self.p_dtypes.ctypes.data, self.g_ptrs.ctypes.data,
                             self.g_scan.ctypes.data)
         self._scan_status = None
-        # centralization: folded into the compact step and the clip (row means only) unless
-        # the plan holds 8-bit or factored tensors, which read a prepared copy of the grads
-        self.gc_fold = self.gc and not self.single and self.kind == "compact" and not self.factored.any()
+        # centralization: folded into the step kernels and the clip (row means only: compact
+        # descriptors hold them in m_scale / block, 8-bit and ultra ones in a side table)
+        # unless the plan holds factored tensors, which read a prepared copy of the grads
+        self.gc_fold = self.gc and not self.single and not self.factored.any()
+        self.host_rows = self.d_rows = None
         if self.gc and not self.single:
             self._build_prep()
         self._fast_static = None
@@ -254,8 +256,15 @@ class StepPlan:
             tab = self.host_table
             rows = prep["row_len"] > 0
             tab["flags"] = np.where(rows, tab["flags"] | np.uint32(L.FLAG_GC), tab["flags"])
-            tab["m_scale"] = np.where(rows, prep["out"], tab["m_scale"])
-            tab["block"] = np.where(rows, prep["row_len"].astype(np.uint32), tab["block"])
+            if self.kind == "compact":
+                tab["m_scale"] = np.where(rows, prep["out"], tab["m_scale"])
+                tab["block"] = np.where(rows, prep["row_len"].astype(np.uint32), tab["block"])
+            else:
+                # 8-bit / ultra descriptors keep their quantization scales and block: the row
+                # means go to the launch's side table (hparams.rows, in device-table order)
+                self.host_rows = np.zeros(n, dtype=L.ROW_MEANS_DTYPE)
+                self.host_rows["means"] = np.where(rows, prep["out"], 0)
+                self.host_rows["row_len"] = prep["row_len"]
         else:
             self.gc_out = [torch.empty(p.numel(), dtype=p.dtype, device=self.device) for p in self.params]
             prep["out"] = [o.data_ptr() for o in self.gc_out]
@@ -410,6 +419,8 @@ class StepPlan:
                 self._layout_units(fast)
             rows = np.ascontiguousarray(self.host_table[self.perm])
             self.d_table = _upload(rows.view(np.uint8), self.device)
+            if self.host_rows is not None:
+                self.d_rows = _upload(np.ascontiguousarray(self.host_rows[self.perm]).view(np.uint8), self.device)
         return keep
 
     def _validate_and_align(self):
@@ -456,7 +467,7 @@ class StepPlan:
             self.d_unit_begin.data_ptr(), part.data_ptr(), norms.data_ptr(), float(clip),
             1.0 if inv_scale is None else inv_scale,
             (L.HP_SANITIZE if sanitize else 0) | (L.HP_UNSCALE if inv_scale is not None else 0), coef.data_ptr(),
-            amp_dyn, stream)
+            amp_dyn, self.d_rows.data_ptr() if self.d_rows is not None else None, stream)
         L.check(st, "apexw_grad_clip_coef")
         return coef
 
@@ -868,6 +879,8 @@ class StepPlan:
         if inv_scale is not None:
             flags |= L.HP_UNSCALE
             hp.grad_inv_scale = inv_scale
+        if self.d_rows is not None:
+            hp.rows = self.d_rows.data_ptr()
         hp.seed = seed
         hp.step = step & 0xFFFFFFFF
         hp.flags = flags

@@ -18,7 +18,7 @@ int apexw_launch_q8_fast(const apexw_tensor*, int64_t, const apexw_unit*, const 
 int apexw_launch_ultra(const apexw_tensor*, int64_t, const apexw_unit*, const apexw_hparams*, hipStream_t);
 bool apexw_q8_fast_eligible(uint32_t flags, uint32_t block);
 int apexw_launch_clip(const apexw_tensor*, int32_t, const apexw_unit*, int64_t, int64_t, const int64_t*, float*, float*,
-                      float, float, uint32_t, float*, const apexw_amp_dyn*, hipStream_t);
+                      float, float, uint32_t, float*, const apexw_amp_dyn*, const apexw_row_means*, hipStream_t);
 int apexw_launch_amp_prepare(const float*, const float*, int32_t*, int32_t, const apexw_amp_launch*, int32_t,
                              apexw_amp_dyn*, hipStream_t);
 bool apexw_compact_flags_ok(uint32_t flags);
@@ -119,7 +119,9 @@ int apexw_abi_version(void) { return APEXW_ABI_VERSION; }
 // (0 = compact, 1 = 8-bit).  Returns APEXW_OK or the reason it is unsupported.
 int apexw_check_tensor(const apexw_tensor* t, int32_t kind) {
   if (!t || !t->p || !t->g || !t->m || !t->v || t->n <= 0) return APEXW_ERR_ARG;
-  if ((t->flags & APEXW_FLAG_GC) && kind != 0) return APEXW_ERR_ARG;   // folded centralization: compact step only
+  // folded centralization: compact (row means in m_scale / block) and 8-bit / ultra
+  // (row means in the launch's side table) steps; not the per-parameter or factored ones
+  if ((t->flags & APEXW_FLAG_GC) && (kind == 3 || kind == 4)) return APEXW_ERR_ARG;
   if (kind == 0 || kind == 3) {
     if (!apexw_compact_flags_ok(t->flags)) return APEXW_ERR_DTYPE;
     if ((t->flags & APEXW_FLAG_QUAD) && (kind == 3 || (t->n % 4) != 0)) return APEXW_ERR_ARG;
@@ -519,12 +521,12 @@ int apexw_muon_coordwise(float* buf, const void* g, int32_t g_dtype, void* p, in
 int apexw_grad_clip_coef(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,
                          int64_t unit_size, const int64_t* unit_begin, float* unit_partial, float* tensor_norm,
                          float clip, float grad_inv_scale, uint32_t flags, float* coef, const apexw_amp_dyn* amp,
-                         void* stream) {
+                         const apexw_row_means* rows, void* stream) {
   if (!tensors || !units || !unit_begin || !unit_partial || !tensor_norm || !coef) return APEXW_ERR_ARG;
   if (n_tensors <= 0 || n_units < 0 || unit_size < 0 || !(clip > 0.0f)) return APEXW_ERR_ARG;
   if ((flags & APEXW_HP_UNSCALE) && !amp && !(grad_inv_scale > 0.0f)) return APEXW_ERR_ARG;
   return apexw_launch_clip(tensors, n_tensors, units, n_units, unit_size, unit_begin, unit_partial, tensor_norm, clip,
-                           grad_inv_scale, flags, coef, amp, (hipStream_t)stream);
+                           grad_inv_scale, flags, coef, amp, rows, (hipStream_t)stream);
 }
 
 int apexw_check_grad_prep(const apexw_grad_prep* d) {

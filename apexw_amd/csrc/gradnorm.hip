@@ -34,20 +34,20 @@ APEXW_DEV float sumsq_vals(const float (&g)[N], bool san, bool unscale, float in
   return acc;
 }
 
-// Row means (APEXW_FLAG_GC: t.m_scale holds one per row of t.block elements) of
-// the 8 elements from e0; zeros for a tensor that is not centralized.
-APEXW_DEV void clip_means8(const apexw_tensor& t, int64_t e0, float (&mean)[8]) {
-  if (!(t.flags & APEXW_FLAG_GC)) {
+// Row means (APEXW_FLAG_GC: `means` holds one per row of rl elements) of the 8
+// elements from e0; zeros for a tensor that is not centralized (means == nullptr).
+APEXW_DEV void clip_means8(const apexw_tensor& t, const float* means, int64_t rl, int64_t e0, float (&mean)[8]) {
+  if (!means) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) mean[j] = 0.0f;
     return;
   }
-  const int64_t rl = (int64_t)t.block, rows = t.n / rl;
+  const int64_t rows = t.n / rl;
   if (rl >= 8) {
     // at most one row boundary inside the 8 elements
     const int64_t row = e0 / rl, col = e0 - row * rl;
-    const float m0 = t.m_scale[row < rows ? row : rows - 1];
-    const float m1 = (col + 8 > rl && row + 1 < rows) ? t.m_scale[row + 1] : m0;
+    const float m0 = means[row < rows ? row : rows - 1];
+    const float m1 = (col + 8 > rl && row + 1 < rows) ? means[row + 1] : m0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) mean[j] = col + j < rl ? m0 : m1;
     return;
@@ -55,16 +55,19 @@ APEXW_DEV void clip_means8(const apexw_tensor& t, int64_t e0, float (&mean)[8]) 
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int64_t r = (e0 + j) / rl;
-    mean[j] = t.m_scale[r < rows ? r : rows - 1];
+    mean[j] = means[r < rows ? r : rows - 1];
   }
 }
 
+// means / rl: the tensor's row means and row length when it is centralized, else
+// nullptr / 0
 template <int GD>
-APEXW_DEV float unit_sumsq(const apexw_tensor& t, int64_t start, int64_t cnt, bool san, bool unscale, float inv) {
+APEXW_DEV float unit_sumsq(const apexw_tensor& t, int64_t start, int64_t cnt, bool san, bool unscale, float inv,
+                           const float* means, int64_t rl) {
   const int lane = lane_id();
   const bool vec = !(t.flags & APEXW_FLAG_SCALAR) && (start % 8) == 0;
   float acc = 0.0f;
-  const bool gc = t.flags & APEXW_FLAG_GC;
+  const bool gc = means != nullptr;
   if (vec && cnt == 2048 && !gc) {
     // a whole 2048-element unit: the wave's four 8-element loads per lane are issued
     // together (centralized tensors take the loop below, in the same summation order,
@@ -101,7 +104,7 @@ APEXW_DEV float unit_sumsq(const apexw_tensor& t, int64_t start, int64_t cnt, bo
         for (int j = 0; j < 8; ++j) g[j] = j < c ? load1<GD>(t.g, e0 + j) : 0.0f;
       }
       float mean[8];
-      clip_means8(t, e0, mean);
+      clip_means8(t, means, rl, e0, mean);
       acc = sumsq_vals<GD, 8>(g, s, unscale, inv, acc, gc, mean);
     }
     if (!san || acc - acc == 0.0f) break;
@@ -112,7 +115,8 @@ APEXW_DEV float unit_sumsq(const apexw_tensor& t, int64_t start, int64_t cnt, bo
 __global__ __launch_bounds__(256) void sumsq_kernel(const apexw_tensor* __restrict__ tensors,
                                                     const apexw_unit* __restrict__ units, int64_t n_units,
                                                     int64_t unit_size, float* __restrict__ partial, uint32_t flags,
-                                                    float inv, const apexw_amp_dyn* __restrict__ amp) {
+                                                    float inv, const apexw_amp_dyn* __restrict__ amp,
+                                                    const apexw_row_means* __restrict__ rows) {
   if (amp) inv = amp->grad_inv_scale;
   const uint32_t wave = uniform(threadIdx.x >> 6);
   const bool san = flags & APEXW_HP_SANITIZE, unscale = flags & APEXW_HP_UNSCALE;
@@ -127,10 +131,18 @@ __global__ __launch_bounds__(256) void sumsq_kernel(const apexw_tensor* __restri
     const int64_t start = (int64_t)un.unit * us;
     const int64_t cnt = (t.n - start) < us ? (t.n - start) : us;
     const uint32_t gd = (t.flags >> APEXW_FLAG_GDT_SHIFT) & 3u;
+    // a centralized tensor's row means: its descriptor's own fields (compact tables) or
+    // its entry of the side table (8-bit / ultra tables)
+    const float* means = nullptr;
+    int64_t rl = 0;
+    if (t.flags & APEXW_FLAG_GC) {
+      means = rows ? rows[un.tensor].means : t.m_scale;
+      rl = rows ? rows[un.tensor].row_len : (int64_t)t.block;
+    }
     float s;
-    if (gd == APEXW_F32) s = unit_sumsq<APEXW_F32>(t, start, cnt, san, unscale, inv);
-    else if (gd == APEXW_BF16) s = unit_sumsq<APEXW_BF16>(t, start, cnt, san, unscale, inv);
-    else s = unit_sumsq<APEXW_F16>(t, start, cnt, san, unscale, inv);
+    if (gd == APEXW_F32) s = unit_sumsq<APEXW_F32>(t, start, cnt, san, unscale, inv, means, rl);
+    else if (gd == APEXW_BF16) s = unit_sumsq<APEXW_BF16>(t, start, cnt, san, unscale, inv, means, rl);
+    else s = unit_sumsq<APEXW_F16>(t, start, cnt, san, unscale, inv, means, rl);
     if (lane_id() == 0) partial[u] = s;
   }
 }
@@ -249,47 +261,58 @@ APEXW_DEV void prep_unit(const apexw_grad_prep& d, int64_t unit, bool san, bool 
   }
 }
 
-// Row means only (the fold of centralization into the step kernels): one workgroup
-// per row of a descriptor with row_len > 0; d.out is a float array of one mean
-// per row, each the grad dtype's rounding of the fp32 row sum over row_len of
-// the sanitized, unscaled grads -- the value prep_unit subtracts.
+// Row means only (the fold of centralization into the step kernels): one wave per
+// row of a descriptor with row_len > 0; d.out is a float array of one mean per
+// row, each the grad dtype's rounding of the fp32 row sum over row_len of the
+// sanitized, unscaled grads.  A lane sums its 8-element vectors (four loads issued
+// before they are added; eight measured slower at C3), then the wave's lanes are
+// summed.
 template <int GD>
-APEXW_DEV void mean_unit(const apexw_grad_prep& d, int64_t row, bool san, bool unscale, float inv, float* red) {
-  const int tid = threadIdx.x;
+APEXW_DEV void mean_row(const apexw_grad_prep& d, int64_t row, bool san, bool unscale, float inv) {
+  const int lane = lane_id();
   const int64_t lo = row * d.row_len, hi = lo + d.row_len;
   const PrepSpan sp = prep_span<GD>(d, lo, hi);
   const int64_t head = sp.a - lo, n_end = head + (hi - sp.b);
   float s = 0.0f;
-  for (int64_t i = sp.a + (int64_t)tid * 8; i < sp.b; i += 2048) {
+  int64_t i = sp.a + (int64_t)lane * 8;
+  for (; i + 3 * 512 < sp.b; i += 4 * 512) {
+    float x[4][8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) prep_vec8<GD>(d.g, i + q * 512, san, unscale, inv, x[q]);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s += x[q][j];
+  }
+  for (; i < sp.b; i += 512) {
     float x[8];
     prep_vec8<GD>(d.g, i, san, unscale, inv, x);
 #pragma unroll
     for (int j = 0; j < 8; ++j) s += x[j];
   }
-  for (int64_t k = tid; k < n_end; k += 256) {
+  for (int64_t k = lane; k < n_end; k += 64) {
     const int64_t i = k < head ? lo + k : sp.b + (k - head);
     s += prep_value<GD>(d.g, i, san, unscale, inv);
   }
   s = wave_sum(s);
-  if ((tid & 63) == 0) red[tid >> 6] = s;
-  __syncthreads();
-  if (tid == 0) ((float*)d.out)[row] = rnd<GD>(((red[0] + red[1]) + (red[2] + red[3])) / (float)d.row_len);
+  if (lane == 0) ((float*)d.out)[row] = rnd<GD>(s / (float)d.row_len);
 }
 
 __global__ __launch_bounds__(256) void row_means_kernel(const apexw_grad_prep* __restrict__ preps,
                                                         const apexw_unit* __restrict__ units, int64_t n_units,
                                                         float inv, uint32_t flags,
                                                         const apexw_amp_dyn* __restrict__ amp) {
-  __shared__ float red[4];
   if (amp) inv = amp->grad_inv_scale;
   const bool san = flags & APEXW_HP_SANITIZE, unscale = flags & APEXW_HP_UNSCALE;
-  for (int64_t u = blockIdx.x; u < n_units; u += gridDim.x) {
+  const uint32_t wave = uniform(threadIdx.x >> 6);
+  // workgroup b takes a contiguous chunk of 64 rows, its waves interleaved
+  for (int64_t base = (int64_t)blockIdx.x * 64; base < n_units; base += (int64_t)gridDim.x * 64)
+  for (int64_t u = base + wave, u_end = base + 64 < n_units ? base + 64 : n_units; u < u_end; u += 4) {
     const apexw_unit un = units[u];
     const apexw_grad_prep& d = preps[un.tensor];
-    if (d.dtype == APEXW_F32) mean_unit<APEXW_F32>(d, un.unit, san, unscale, inv, red);
-    else if (d.dtype == APEXW_BF16) mean_unit<APEXW_BF16>(d, un.unit, san, unscale, inv, red);
-    else mean_unit<APEXW_F16>(d, un.unit, san, unscale, inv, red);
-    __syncthreads();   // red is reused by the next unit
+    if (d.dtype == APEXW_F32) mean_row<APEXW_F32>(d, un.unit, san, unscale, inv);
+    else if (d.dtype == APEXW_BF16) mean_row<APEXW_BF16>(d, un.unit, san, unscale, inv);
+    else mean_row<APEXW_F16>(d, un.unit, san, unscale, inv);
   }
 }
 
@@ -324,14 +347,14 @@ int apexw_launch_grad_prep(const apexw_grad_prep* preps, const apexw_unit* units
 int apexw_launch_clip(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,
                       int64_t unit_size, const int64_t* unit_begin, float* unit_partial, float* tensor_norm,
                       float clip, float inv, uint32_t flags, float* coef, const apexw_amp_dyn* amp,
-                      hipStream_t stream);
+                      const apexw_row_means* rows, hipStream_t stream);
 
 int apexw_launch_row_means(const apexw_grad_prep* preps, const apexw_unit* units, int64_t n_units, float inv,
                            uint32_t flags, const apexw_amp_dyn* amp, hipStream_t stream) {
   if (n_units <= 0) return APEXW_OK;
-  const int64_t want = n_units < 65536 ? n_units : 65536;
-  hipLaunchKernelGGL(row_means_kernel, dim3((unsigned)want), dim3(256), 0, stream, preps, units, n_units, inv, flags,
-                     amp);
+  const int64_t chunks = (n_units + 63) / 64;
+  const unsigned grid = (unsigned)(chunks < INT32_MAX ? chunks : INT32_MAX);
+  hipLaunchKernelGGL(row_means_kernel, dim3(grid), dim3(256), 0, stream, preps, units, n_units, inv, flags, amp);
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }
 
@@ -387,19 +410,19 @@ extern "C" int apexw_grad_clip_coef_noalloc(const apexw_tensor* tensors, int32_t
   float* ptr = scratch_on_device(dev);
   if (!ptr) return APEXW_ERR_LAUNCH;
   return apexw_launch_clip(tensors, n_tensors, units, n_units, unit_size, unit_begin, ptr,
-                           ptr + APEXW_NOALLOC_CLIP_MAX_UNITS, clip, grad_inv_scale, flags, coef, amp,
+                           ptr + APEXW_NOALLOC_CLIP_MAX_UNITS, clip, grad_inv_scale, flags, coef, amp, nullptr,
                            (hipStream_t)stream);
 }
 
 int apexw_launch_clip(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,
                       int64_t unit_size, const int64_t* unit_begin, float* unit_partial, float* tensor_norm,
                       float clip, float inv, uint32_t flags, float* coef, const apexw_amp_dyn* amp,
-                      hipStream_t stream) {
+                      const apexw_row_means* rows, hipStream_t stream) {
   if (n_units > 0) {
     const int64_t chunks = (n_units + 63) / 64;
     const int grid_units = (int)(chunks < INT32_MAX ? chunks : INT32_MAX);
     hipLaunchKernelGGL(sumsq_kernel, dim3(grid_units), dim3(256), 0, stream, tensors, units, n_units, unit_size,
-                       unit_partial, flags, inv, amp);
+                       unit_partial, flags, inv, amp, rows);
   }
   if (n_tensors > 0) {
     const int grid_tensors = apexw_resident_grid((const void*)tensor_norm_kernel, n_tensors);

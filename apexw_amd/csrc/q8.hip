@@ -41,7 +41,82 @@ struct Q8Ctx {
   const float4* frac16;  // LDS: signed fractional NF4 code buckets (x 4096, +7, lines in y = x + 3)
   const float2* midtab;  // LDS: NF4 round-to-nearest buckets (kNf4MidTab)
   float coef;
+  // grad centralization of the current unit's tensor (APEXW_FLAG_GC): its fp32 row
+  // means and row length from the launch's side table (hparams.rows), else nullptr
+  const float* gc_means;
+  int64_t gc_rl;
 };
+
+// Point the context at the row means of tensor tix (or at none).
+APEXW_DEV void q8_set_rows(Q8Ctx& c, const apexw_tensor& t, uint32_t tix) {
+  c.gc_means = nullptr;
+  c.gc_rl = 0;
+  if ((t.flags & APEXW_FLAG_GC) && c.hp->rows) {
+    const apexw_row_means r = c.hp->rows[tix];
+    c.gc_means = r.means;
+    c.gc_rl = r.row_len;
+  }
+}
+
+// a / b for 0 <= a, 0 < b, in 32 bits when both fit (a 64-bit division is a long
+// software sequence)
+APEXW_DEV int64_t q8_udiv(int64_t a, int64_t b) {
+  if (((uint64_t)a | (uint64_t)b) >> 32) return a / b;
+  return (int64_t)((uint32_t)a / (uint32_t)b);
+}
+
+// Row means of the 8 elements from e0 of a centralized tensor; zeros otherwise.
+APEXW_DEV void q8_means8(const Q8Ctx& c, const apexw_tensor& t, int64_t e0, float (&mean)[8]) {
+  if (!c.gc_means) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mean[j] = 0.0f;
+    return;
+  }
+  const int64_t rl = c.gc_rl, rows = q8_udiv(t.n, rl);
+  if (rl >= 8) {
+    // at most one row boundary inside the 8 elements
+    const int64_t row = q8_udiv(e0, rl), col = e0 - row * rl;
+    const float m0 = c.gc_means[row < rows ? row : rows - 1];
+    const float m1 = (col + 8 > rl && row + 1 < rows) ? c.gc_means[row + 1] : m0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mean[j] = col + j < rl ? m0 : m1;
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int64_t r = q8_udiv(e0 + j, rl);
+    mean[j] = c.gc_means[r < rows ? r : rows - 1];
+  }
+}
+
+APEXW_DEV float q8_mean1(const Q8Ctx& c, const apexw_tensor& t, int64_t i) {
+  if (!c.gc_means) return 0.0f;
+  const int64_t r = q8_udiv(i, c.gc_rl), rows = q8_udiv(t.n, c.gc_rl);
+  return c.gc_means[r < rows ? r : rows - 1];
+}
+
+// The row means of one 2048-element block of a centralized tensor whose rows hold
+// at least 2048 elements: the block meets at most one row boundary, so elements
+// below `split` take m0 and the others m1 (one division per block, not per element).
+struct BlockMeans {
+  int64_t split;
+  float m0, m1;
+  bool one;    // rows of >= 2048 elements: split / m0 / m1 hold
+  bool by8;    // and of a multiple of 8 elements: no 8-element group straddles two rows
+};
+
+APEXW_DEV BlockMeans q8_block_means(const Q8Ctx& c, const apexw_tensor& t, int64_t start) {
+  BlockMeans b{0, 0.0f, 0.0f, false, false};
+  if (!c.gc_means || c.gc_rl < 2048) return b;
+  const int64_t rl = c.gc_rl, rows = q8_udiv(t.n, rl);
+  const int64_t row = q8_udiv(start, rl);
+  b.one = true;
+  b.by8 = (rl & 7) == 0;
+  b.split = (row + 1) * rl;
+  b.m0 = c.gc_means[row < rows ? row : rows - 1];
+  b.m1 = row + 1 < rows ? c.gc_means[row + 1] : b.m0;
+  return b;
+}
 
 // Division by a denominator shared across a quad or a block, round-to-nearest:
 // r = RN-refined 1/y (one Newton step on v_rcp_f32), q0 = x r, then the exact
@@ -109,23 +184,39 @@ APEXW_DEV uint32_t logu8_code_shared(float v, float vmax, float rvmax) {
   return (uint32_t)fminf(fmaxf(q, 1.0f), 255.0f);
 }
 
-template <int GD> APEXW_DEV float q8_grad(float g, uint32_t tflags, const Q8Ctx& c) {
+// nan_to_num inside the step: on the fp32 copy (chunked) or on the grad dtype (generic)
+template <int GD> APEXW_DEV float q8_nan_to_num(float g, uint32_t tflags) {
+  if (__builtin_isnan(g)) return 0.0f;
+  if (__builtin_isinf(g)) {
+    const float big = (tflags & (APEXW_FLAG_GENERIC | APEXW_FLAG_DENSE)) ? rnd<GD>(65504.0f) : 65504.0f;
+    return g > 0.0f ? big : -big;
+  }
+  return g;
+}
+
+// True when any of the 8 values is NaN or +-Inf (x * 0 is NaN exactly then).
+APEXW_DEV bool q8_any_nonfinite8(const float (&x)[8]) {
+  float t = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) t = fmaf(x[j], 0.0f, t);
+  return !(t == t);
+}
+
+// mean: the element's row mean when its tensor is centralized (c.gc_means).
+template <int GD> APEXW_DEV float q8_grad(float g, uint32_t tflags, const Q8Ctx& c, float mean = 0.0f) {
   const apexw_hparams& hp = *c.hp;
   const bool unscale = hp.flags & APEXW_HP_UNSCALE, clip = hp.flags & APEXW_HP_CLIP;
+  const bool gc = c.gc_means != nullptr;
   if (hp.flags & APEXW_HP_SANITIZE) g = sanitize<GD>(g);
-  // AMP before a clip: _prepare_grads unscales in the grad dtype (apexw/optimizer.py:227-237)
-  if (unscale && clip) g = rnd<GD>(g * hp.grad_inv_scale);
+  // AMP before a clip or a centralization: _prepare_grads unscales in the grad dtype
+  // (apexw/optimizer.py:227-237), then subtracts each row's mean (:239-243), then clips
+  if (unscale && (clip || gc)) g = rnd<GD>(g * hp.grad_inv_scale);
+  if (gc) g = rnd<GD>(g - mean);
   if (clip) g = rnd<GD>(g * c.coef);
-  // nan_to_num inside the step: on the fp32 copy (chunked) or on the grad dtype (generic)
-  if (__builtin_isnan(g)) {
-    g = 0.0f;
-  } else if (__builtin_isinf(g)) {
-    const float big = (tflags & (APEXW_FLAG_GENERIC | APEXW_FLAG_DENSE)) ? rnd<GD>(65504.0f) : 65504.0f;
-    g = g > 0.0f ? big : -big;
-  }
+  g = q8_nan_to_num<GD>(g, tflags);
   // AMP without a clip: the step unscales its fp32 copy after nan_to_num
   // (_prep_grad_chunk_fp32, apexw/state.py:326-347; apexw/optimizer.py:4500-4505)
-  if (unscale && !clip) g *= hp.grad_inv_scale;
+  if (unscale && !clip && !gc) g *= hp.grad_inv_scale;
   return g;
 }
 
@@ -252,13 +343,15 @@ APEXW_DEV void q8_block(const apexw_tensor& t, uint32_t tix, uint32_t blk, const
     }
     // ---- update
     uint32_t h[8];
+    float mean[8];
+    q8_means8(c, t, e0, mean);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       h[j] = sr ? rng_at(key, (uint32_t)(e0 + j)) : 0u;
       if constexpr (SINGLE) {
         m[j] = fmaf(hp.one_minus_beta1, g[j], m[j] * hp.beta1);
       } else {
-        g[j] = q8_grad<GD>(g[j], tflags, c);
+        g[j] = q8_grad<GD>(g[j], tflags, c, mean[j]);
         m[j] = lerp_to(m[j], g[j], hp.lerp_coef, hp.flags & APEXW_HP_LERP_HI);
       }
     }
@@ -534,7 +627,7 @@ APEXW_DEV void q8_fast_load(const apexw_tensor& t, uint32_t blk, FastRaw<PD>& r)
 // B1HI: the usual orientation of the two lerps, fixed at compile time (beta1 > 1/2:
 // m' = lerp(m, g, 1-b1) takes the a + w (b - a) form and the lookahead lerp(g, m', b1)
 // the b + (w - 1)(b - a) form); otherwise both come from the launch's flags.
-template <int PD, bool SR, bool FULL, bool GENERIC, bool B1HI>
+template <int PD, bool SR, bool FULL, bool GENERIC, bool B1HI, bool GC>
 APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk, const Q8Ctx& c,
                                const FastRaw<PD>& r) {
   const apexw_hparams& hp = *c.hp;
@@ -557,6 +650,8 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
     rs = mix32(key + (blk << 6) + (uint32_t)lane) | 1u;
   }
   const bool prep = hf & (APEXW_HP_SANITIZE | APEXW_HP_CLIP | APEXW_HP_UNSCALE);
+  BlockMeans bm{0, 0.0f, 0.0f, false, false};
+  if constexpr (GC) bm = q8_block_means(c, t, start);
 
   // SR noise: one xorshift32 word per element pair in this pass (its two halves
   // round the pair's bf16 parameters) and one per pair in the requantization pass
@@ -588,8 +683,36 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
       }
     }
     if (prep) {
+      if constexpr (GC) {
+        const int64_t e = start + k * 512 + lane * 8;
+        float mean[8];
+        if (bm.by8) {
+          const float mg = e < bm.split ? bm.m0 : bm.m1;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) g[j] = q8_grad<PD>(g[j], tf, c);
+          for (int j = 0; j < 8; ++j) mean[j] = mg;
+        } else if (bm.one) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) mean[j] = e + j < bm.split ? bm.m0 : bm.m1;
+        } else {
+          q8_means8(c, t, e, mean);
+        }
+        // the common case, centralization alone on finite grads (sanitizing changes
+        // nothing): g - mean in the grad dtype; a non-finite difference (a non-finite
+        // grad, or an overflow) sends the group through the general preparation
+        float d[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) d[j] = rnd<PD>(g[j] - mean[j]);
+        if (!(hf & (APEXW_HP_CLIP | APEXW_HP_UNSCALE)) && !q8_any_nonfinite8(d)) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) g[j] = d[j];
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) g[j] = q8_grad<PD>(g[j], tf, c, mean[j]);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) g[j] = q8_grad<PD>(g[j], tf, c);
+      }
     }
     float upd[8];
     if constexpr (SR) {
@@ -855,11 +978,11 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
   }
 }
 
-template <int PD, bool SR, bool FULL, bool GENERIC, bool B1HI>
+template <int PD, bool SR, bool FULL, bool GENERIC, bool B1HI, bool GC>
 APEXW_DEV void q8_block_fast(const apexw_tensor& t, uint32_t tix, uint32_t blk, const Q8Ctx& c) {
   FastRaw<PD> r;
   q8_fast_load<PD, FULL>(t, blk, r);
-  q8_fast_compute<PD, SR, FULL, GENERIC, B1HI>(t, tix, blk, c, r);
+  q8_fast_compute<PD, SR, FULL, GENERIC, B1HI, GC>(t, tix, blk, c, r);
 }
 
 // Dense m and v (bf16 or fp32): the fallback branch of _step_ultra
@@ -888,7 +1011,7 @@ APEXW_DEV void q8_dense(const apexw_tensor& t, uint32_t unit, const Q8Ctx& c) {
       store1<PD>(t.p, i, rnd<PD>(p + (-hp.step_size * mf) / den));
       continue;
     }
-    const float g = q8_grad<GD>(load1<GD>(t.g, i), t.flags, c);
+    const float g = q8_grad<GD>(load1<GD>(t.g, i), t.flags, c, q8_mean1(c, t, i));
     if (t.flags & APEXW_FLAG_WD) p = rnd<PD>(p * hp.wd_factor);
     const float mf = lerp_to(load1<MD>(t.m, i), g, hp.lerp_coef, hp.flags & APEXW_HP_LERP_HI);
     store1<MD>(t.m, i, rnd<MD>(mf));
@@ -952,9 +1075,11 @@ APEXW_DEV void ultra_block(const apexw_tensor& t, uint32_t tix, uint32_t blk, co
         m[j] = ok ? (float)((const int8_t*)t.m)[e0 + j] * ms_old : 0.0f;
       }
     }
+    float mean[8];
+    q8_means8(c, t, e0, mean);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      g[j] = q8_grad<GD>(g[j], t.flags, c);
+      g[j] = q8_grad<GD>(g[j], t.flags, c, mean[j]);
       if (t.flags & APEXW_FLAG_WD) p[j] = rnd<PD>(p[j] * hp.wd_factor);
       m[j] = lerp_to(m[j], g[j], hp.lerp_coef, hp.flags & APEXW_HP_LERP_HI);
       const float vf = fmaf(hp.one_minus_beta2 * g[j], g[j], v[j] * hp.beta2);
@@ -1086,11 +1211,13 @@ APEXW_DEV void ultra_block_full(const apexw_tensor& t, uint32_t tix, uint32_t bl
       unpack8<PD>(rp[b], p);
       unpack8<GD>(rg[b], g);
       unpack8<VD>(rv[b], v);
+      float mean[8];
+      q8_means8(c, t, e0, mean);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const uint32_t word = j < 4 ? rm[b].x : rm[b].y;
         const float m = (float)(int8_t)((word >> (8 * (j & 3))) & 0xFFu) * ms_old;
-        g[j] = q8_grad<GD>(g[j], t.flags, c);
+        g[j] = q8_grad<GD>(g[j], t.flags, c, mean[j]);
         if (wd) p[j] = rnd<PD>(p[j] * hp.wd_factor);
         mnew[k][j] = lerp_to(m, g[j], hp.lerp_coef, hp.flags & APEXW_HP_LERP_HI);
         amax = fmaxf(amax, fabsf(mnew[k][j]));
@@ -1178,11 +1305,14 @@ __global__ __launch_bounds__(256) void ultra_step_kernel(const apexw_tensor* __r
   c.frac16 = nullptr;
   c.midtab = nullptr;
   c.coef = (hp.flags & APEXW_HP_CLIP) ? *hp.clip_coef : 1.0f;
+  c.gc_means = nullptr;
+  c.gc_rl = 0;
   const uint32_t wave = uniform(threadIdx.x >> 6);
   const int64_t stride = (int64_t)gridDim.x * kWaves;
   for (int64_t u = (int64_t)blockIdx.x * kWaves + wave; u < n_units; u += stride) {
     const apexw_unit un = units[u];
     const apexw_tensor& t = tensors[un.tensor];
+    q8_set_rows(c, t, un.tensor);
     const uint32_t f = t.flags;
     const uint32_t pd = (f >> APEXW_FLAG_PDT_SHIFT) & 3u;
     const uint32_t md = (f >> APEXW_FLAG_MDT_SHIFT) & 3u;
@@ -1209,8 +1339,10 @@ __global__ __launch_bounds__(256) void ultra_step_kernel(const apexw_tensor* __r
 // Kernel for the units of fast-path tensors (see apexw_q8_fast_ok) with parameter
 // dtype PD and stochastic rounding SR; each (dtype, SR) pair is its own kernel so
 // one variant's register footprint does not lower another's occupancy (bf16: 142
-// VGPRs with SR, occupancy 3; 93 without, occupancy 5).
-template <int PD, bool SR, bool B1HI>
+// VGPRs with SR, occupancy 3; 93 without, occupancy 5).  GC: the launch holds
+// centralized tensors (hparams.rows), an instantiation of its own so that the
+// others keep their register counts.
+template <int PD, bool SR, bool B1HI, bool GC>
 __global__ __launch_bounds__(256) void q8_fast_kernel(const apexw_tensor* __restrict__ tensors,
                                                       const apexw_unit* __restrict__ units,
                                                       int64_t n_units, apexw_hparams hp_in) {
@@ -1243,6 +1375,8 @@ __global__ __launch_bounds__(256) void q8_fast_kernel(const apexw_tensor* __rest
   c.frac16 = s_frac16;
   c.midtab = s_midtab;
   c.coef = (hp.flags & APEXW_HP_CLIP) ? *hp.clip_coef : 1.0f;
+  c.gc_means = nullptr;
+  c.gc_rl = 0;
   const uint32_t wave = uniform(threadIdx.x >> 6);
   // a workgroup walks a contiguous chunk of kFastChunk units, its waves interleaved
   // (unit base + 4 i + wave): measured ~1% faster than workgroups striding by 4 units
@@ -1253,12 +1387,13 @@ __global__ __launch_bounds__(256) void q8_fast_kernel(const apexw_tensor* __rest
     const apexw_tensor& t = tensors[un.tensor];
     // never taken for a valid plan: the unit ranges hold only this kernel's tensors
     if (!apexw_q8_fast_ok(t.flags, t.block) || ((t.flags >> APEXW_FLAG_PDT_SHIFT) & 3u) != (uint32_t)PD) continue;
+    if constexpr (GC) q8_set_rows(c, t, un.tensor);
     const bool full = (int64_t)(un.unit + 1) * 2048 <= t.n;
     const bool gen = t.flags & APEXW_FLAG_GENERIC;
-    if (full && !gen) q8_block_fast<PD, SR, true, false, B1HI>(t, un.tensor, un.unit, c);
-    else if (full) q8_block_fast<PD, SR, true, true, B1HI>(t, un.tensor, un.unit, c);
-    else if (!gen) q8_block_fast<PD, SR, false, false, B1HI>(t, un.tensor, un.unit, c);
-    else q8_block_fast<PD, SR, false, true, B1HI>(t, un.tensor, un.unit, c);
+    if (full && !gen) q8_block_fast<PD, SR, true, false, B1HI, GC>(t, un.tensor, un.unit, c);
+    else if (full) q8_block_fast<PD, SR, true, true, B1HI, GC>(t, un.tensor, un.unit, c);
+    else if (!gen) q8_block_fast<PD, SR, false, false, B1HI, GC>(t, un.tensor, un.unit, c);
+    else q8_block_fast<PD, SR, false, true, B1HI, GC>(t, un.tensor, un.unit, c);
   }
 }
 
@@ -1291,11 +1426,14 @@ __global__ __launch_bounds__(256) void q8_step_kernel(const apexw_tensor* __rest
   c.frac16 = nullptr;
   c.midtab = s_midtab;
   c.coef = (hp.flags & APEXW_HP_CLIP) ? *hp.clip_coef : 1.0f;
+  c.gc_means = nullptr;
+  c.gc_rl = 0;
   const uint32_t wave = uniform(threadIdx.x >> 6);
   const int64_t stride = (int64_t)gridDim.x * kWaves;
   for (int64_t u = (int64_t)blockIdx.x * kWaves + wave; u < n_units; u += stride) {
     const apexw_unit un = units[u];
     const apexw_tensor& t = tensors[un.tensor];
+    q8_set_rows(c, t, un.tensor);
     const uint32_t f = t.flags;
     const uint32_t pd = (f >> APEXW_FLAG_PDT_SHIFT) & 3u;
     if (f & APEXW_FLAG_FACTORED) continue;  // stepped by apexw_factored_step
@@ -1378,14 +1516,23 @@ int apexw_launch_q8_fast(const apexw_tensor* tensors, int64_t n_units, const ape
   const int grid = (int)(chunks < INT32_MAX ? chunks : INT32_MAX);
   const bool sr = hp->flags & APEXW_HP_SR;
   const bool b1hi = !(hp->flags & APEXW_HP_LERP_HI) && (hp->flags & APEXW_HP_LOOK_HI);
-#define APEXW_FAST(PD, SR, HI) \
-  hipLaunchKernelGGL((q8_fast_kernel<PD, SR, HI>), dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp)
-  if (p_dtype == APEXW_F32) {
-    if (sr) { if (b1hi) APEXW_FAST(APEXW_F32, true, true); else APEXW_FAST(APEXW_F32, true, false); }
-    else { if (b1hi) APEXW_FAST(APEXW_F32, false, true); else APEXW_FAST(APEXW_F32, false, false); }
+#define APEXW_FAST(PD, SR, HI, GC) \
+  hipLaunchKernelGGL((q8_fast_kernel<PD, SR, HI, GC>), dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp)
+  if (hp->rows) {
+    // centralized tensors in the launch
+    if (p_dtype == APEXW_F32) {
+      if (sr) { if (b1hi) APEXW_FAST(APEXW_F32, true, true, true); else APEXW_FAST(APEXW_F32, true, false, true); }
+      else { if (b1hi) APEXW_FAST(APEXW_F32, false, true, true); else APEXW_FAST(APEXW_F32, false, false, true); }
+    } else {
+      if (sr) { if (b1hi) APEXW_FAST(APEXW_BF16, true, true, true); else APEXW_FAST(APEXW_BF16, true, false, true); }
+      else { if (b1hi) APEXW_FAST(APEXW_BF16, false, true, true); else APEXW_FAST(APEXW_BF16, false, false, true); }
+    }
+  } else if (p_dtype == APEXW_F32) {
+    if (sr) { if (b1hi) APEXW_FAST(APEXW_F32, true, true, false); else APEXW_FAST(APEXW_F32, true, false, false); }
+    else { if (b1hi) APEXW_FAST(APEXW_F32, false, true, false); else APEXW_FAST(APEXW_F32, false, false, false); }
   } else {
-    if (sr) { if (b1hi) APEXW_FAST(APEXW_BF16, true, true); else APEXW_FAST(APEXW_BF16, true, false); }
-    else { if (b1hi) APEXW_FAST(APEXW_BF16, false, true); else APEXW_FAST(APEXW_BF16, false, false); }
+    if (sr) { if (b1hi) APEXW_FAST(APEXW_BF16, true, true, false); else APEXW_FAST(APEXW_BF16, true, false, false); }
+    else { if (b1hi) APEXW_FAST(APEXW_BF16, false, true, false); else APEXW_FAST(APEXW_BF16, false, false, false); }
   }
 #undef APEXW_FAST
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;

@@ -17,8 +17,9 @@ from the committed profile summary of this workload when one exists.
 ``cpu_baseline`` times the CPU oracle (the reference algorithm restated with
 torch CPU ops) on a bounded slice of the same workload on this host's cores.
 The default (C3) line also carries ``mfma_roofline``: the C5 hybrid Muon step's
-Newton-Schulz GEMMs against the bf16 dense MFMA peak, measured after the C3
-tensors are freed.
+Newton-Schulz GEMMs against the bf16 dense MFMA peak, and ``c4_roofline``: the
+C4 compact step over 20,000 ragged tensors with the clip (the whole step, and
+its fused step kernel alone), each measured after the earlier tensors are freed.
 """
 
 import argparse
@@ -106,6 +107,12 @@ CONFIGS = {
     "c3bwd": dict(workload="C3 shapes, 8-bit ApexW, the same backward with the in-backward hooks removed "
                            "(one step after it), bf16, SR on", shapes=llama3_8b_shapes(), dtype=torch.bfloat16,
                   backward="plain", kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, precision="8bit")),
+    # grad centralization folded into the 8-bit step: the row means of the dim >= 2 grads are
+    # one more read of those grads before the step
+    "c3gc": dict(workload="C3 8-bit ApexW step, Llama-3-8B (8.03B params) bf16, SR on, grad_centralization=True",
+                 shapes=llama3_8b_shapes(), dtype=torch.bfloat16, row_mean_reads=1,
+                 kwargs=dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, precision="8bit",
+                             grad_centralization=True)),
     # the clip's norm pass reads every grad once before the step reads it again (a global
     # norm must be complete before any element is updated): 2 grad reads
     "c4": dict(workload="C4 compact ApexW step, 20k ragged bf16 tensors, clip 1.0", shapes=ragged_shapes(),
@@ -223,6 +230,75 @@ def ns_roofline(opt, stream, reps=3):
     return {"bound": "mfma", "achieved": achieved, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": achieved / MFMA_BF16_PEAK_TFLOPS, "traffic": None, "kernel_ms": ns_ms, "flops_per_step": flops,
             "ns_steps": steps, "executed_tflops": sum(plan.exec_flops for plan in plans) / (ns_ms * 1e-3) / 1e12}
+
+
+def step_kernel_roofline(opt, stream, reps=5):
+    """The fused step kernel alone: each group's prepared step launches (the step
+    kernel only; the clip's coefficient from the last step stays on the device)
+    replayed between HIP events on the launch stream, the step counters restored
+    afterwards.  Bytes: p read+write, g read once, the state read+write."""
+    import ctypes
+    from apexw_amd import _lib as L
+    groups = {id(g): g for g in opt.param_groups}
+    progs = [(plan, plan.prepare(groups[gid], opt._seed)) for gid, plan in opt._plans.items()]
+    h = stream.cuda_stream
+
+    def launch():
+        for plan, prog in progs:
+            for d_units, n_units, n_fast, n_fast32, hp in prog.launches:
+                if plan.kind == "compact":
+                    st = plan._lib.apexw_compact_step(plan.d_table.data_ptr(), len(plan.params), d_units.data_ptr(),
+                                                      n_units, ctypes.byref(hp), h)
+                else:
+                    st = plan._lib.apexw_q8_step(plan.d_table.data_ptr(), len(plan.params), d_units.data_ptr(),
+                                                 n_units, n_fast, n_fast32, ctypes.byref(hp), h)
+                L.check(st, "step kernel replay")
+    try:
+        launch()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record(stream)
+        for _ in range(reps):
+            launch()
+        ev1.record(stream)
+        torch.cuda.synchronize()
+    finally:
+        for _, prog in progs:
+            prog.rollback()
+    return ev0.elapsed_time(ev1) / reps
+
+
+def hbm_extra(cfg_name, steps=10, warmup=3):
+    """Another HBM-bound configuration's roofline for the default bench line (C4: the
+    compact step over 20,000 ragged tensors with the global-norm clip): the whole
+    step (the clip's norm pass reads every grad before the step reads it again),
+    then the fused step kernel alone."""
+    from apexw_amd import ApexW
+    cfg = CONFIGS[cfg_name]
+    dev = torch.device("cuda", 0)
+    params = make_params(cfg, dev)
+    opt = ApexW(params, **cfg["kwargs"])
+    for _ in range(warmup):
+        opt.step()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(steps):
+        opt.step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    step_ms = e0.elapsed_time(e1) / steps
+    step_bytes = state_bytes(opt, params, cfg.get("grad_reads", 1), None, cfg.get("row_mean_reads", 0))
+    kern_ms = step_kernel_roofline(opt, stream)
+    kern_bytes = state_bytes(opt, params, 1)
+    achieved = kern_bytes / (kern_ms * 1e-3) / 1e9
+    out = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+           "traffic": None, "kernel": "compact_step_kernel", "kernel_ms": kern_ms, "bytes_per_launch": kern_bytes,
+           "step_ms": step_ms, "step_bytes": step_bytes, "step_gbs": step_bytes / (step_ms * 1e-3) / 1e9,
+           "params": sum(p.numel() for p in params), "tensors": len(params), "workload": cfg["workload"]}
+    del opt, params
+    torch.cuda.empty_cache()
+    return out
 
 
 def cpu_model():
@@ -393,6 +469,7 @@ def main():
         del step, opt, params
         torch.cuda.empty_cache()
         out["mfma_roofline"] = mfma_extra()
+        out["c4_roofline"] = hbm_extra("c4")
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.config, args.cpu_budget)
     print(json.dumps(out), flush=True)

@@ -44,7 +44,7 @@
 extern "C" {
 #endif
 
-#define APEXW_ABI_VERSION 19
+#define APEXW_ABI_VERSION 20
 
 /* status codes */
 enum apexw_status {
@@ -75,10 +75,14 @@ enum apexw_dtype { APEXW_F32 = 0, APEXW_BF16 = 1, APEXW_F16 = 2, APEXW_U8 = 3, A
 #define APEXW_FLAG_FACTORED (1u << 14)  /* factored second moment: stepped by apexw_factored_step;
                                            the compact and 8-bit step kernels skip the row */
 #define APEXW_FLAG_M6 (1u << 15)        /* factored 8-bit: packed 6-bit m (4 codes in 3 bytes) */
-#define APEXW_FLAG_GC (1u << 16)        /* compact step and clip: grad centralization folded in; the grad
+#define APEXW_FLAG_GC (1u << 16)        /* step kernels and clip: grad centralization folded in; the grad
                                            is read raw and g - mean(row) taken in its dtype (after
-                                           sanitize / unscale, before the clip), with m_scale = the fp32
-                                           row means (apexw_grad_row_means) and block = the row length */
+                                           sanitize / unscale, before the clip).  The fp32 row means
+                                           (apexw_grad_row_means) and the row length: in compact
+                                           tables m_scale and block; in 8-bit / ultra tables (whose
+                                           m_scale and block hold the quantization scales and block)
+                                           the descriptor's apexw_row_means entry (hparams.rows, and
+                                           the clip's rows argument) */
 #define APEXW_FLAG_VSCALE (1u << 18)    /* compact step: v holds the second moment times a dynamic scale
                                            (fp16 v): v_scale points at {scale_v, sqrt(scale_v)} (fp32,
                                            scale a power of two), read by the cold and replay modes */
@@ -155,6 +159,14 @@ typedef struct apexw_amp_dyn {
   uint32_t reserved[3];
 } apexw_amp_dyn;
 
+/* Grad centralization's row means of descriptor i of an 8-bit / ultra table
+ * (APEXW_FLAG_GC): means[r] is the fp32 mean of row r, rows of row_len
+ * elements (written by apexw_grad_row_means; 16 bytes). */
+typedef struct apexw_row_means {
+  const float* means;
+  int64_t row_len;
+} apexw_row_means;
+
 /* Host-computed step scalars (the reference computes them in double). */
 typedef struct apexw_hparams {
   float beta1, one_minus_beta1, beta2, one_minus_beta2;
@@ -173,7 +185,9 @@ typedef struct apexw_hparams {
   uint32_t flags;
   float grad_inv_scale; /* with APEXW_HP_UNSCALE: 1 / AMP grad scale (GradScaler) */
   const apexw_amp_dyn* amp;  /* with APEXW_HP_AMP: this launch's device-side step scalars */
-} apexw_hparams;          /* 96 bytes */
+  const apexw_row_means* rows;  /* 8-bit / ultra tables with APEXW_FLAG_GC rows: one entry per
+                                   descriptor of the table, else NULL */
+} apexw_hparams;          /* 104 bytes */
 
 /*
  * GradScaler hands the optimizer its scale and found_inf as device tensors
@@ -337,12 +351,15 @@ int apexw_factored_step(const apexw_tensor* tensors, int32_t n_tensors, const ap
  * before the clip, apexw/optimizer.py:227-237).  amp: when not NULL, the
  * unscale factor is amp->grad_inv_scale, read on the device (apexw_amp_prepare);
  * the same holds for apexw_grad_prepare and apexw_grad_row_means below.
+ * APEXW_FLAG_GC descriptors: the norm is that of the centralized grad (its row
+ * means from m_scale / block, or from rows[i] when rows is not NULL: 8-bit /
+ * ultra tables, one entry per descriptor).
  */
 int apexw_grad_clip_coef(const apexw_tensor* tensors, int32_t n_tensors,
                          const apexw_unit* units, int64_t n_units, int64_t unit_size,
                          const int64_t* unit_begin, float* unit_partial, float* tensor_norm,
                          float clip, float grad_inv_scale, uint32_t flags, float* coef,
-                         const apexw_amp_dyn* amp, void* stream);
+                         const apexw_amp_dyn* amp, const apexw_row_means* rows, void* stream);
 
 /*
  * apexw_grad_clip_coef without workspace arguments, allocating nothing: the
@@ -351,7 +368,7 @@ int apexw_grad_clip_coef(const apexw_tensor* tensors, int32_t n_tensors,
  * floats, 32.5 MiB per GPU, held until the process ends: 2^23 units cover an
  * 8B-parameter list in 2048-element units).  The array used is that of the
  * stream's device (hipStreamGetDevice; the current device for the null stream).
- * Same kernels, same result as apexw_grad_clip_coef.  Returns APEXW_ERR_SIZE,
+ * Same kernels, same result as apexw_grad_clip_coef with rows = NULL.  Returns APEXW_ERR_SIZE,
  * before enqueueing anything, when n_units or n_tensors exceeds its limit.
  * No counterpart in the reference: it is for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops, harnesses

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 def test_struct_layouts_match_header():
     from apexw_amd import _lib
     assert ctypes.sizeof(_lib.Tensor) == 64 == _lib.TENSOR_DTYPE.itemsize
-    assert ctypes.sizeof(_lib.HParams) == 96
+    assert ctypes.sizeof(_lib.HParams) == 104
     assert _lib.GEMM_PROBLEM_DTYPE.itemsize == 120
     assert ctypes.sizeof(_lib.StateLayout) == 56
 
@@ -290,6 +290,6 @@ def test_integration_binding_loads():
     from integration_binding import load_binding
     rx = load_binding()
     assert callable(rx.step_fused) and callable(rx.step_fused_8bit)
-    assert ctypes.sizeof(rx.HParams) == 96 and ctypes.sizeof(rx.Tensor) == 64 and ctypes.sizeof(rx.Unit) == 8
+    assert ctypes.sizeof(rx.HParams) == 104 and ctypes.sizeof(rx.Tensor) == 64 and ctypes.sizeof(rx.Unit) == 8
     p = torch.zeros(4)          # CPU tensors: not handled, nothing written
     assert rx.step_fused([p], [p], [p], [p], 1e-3, 0.9, 0.999, 1e-8, 0.0) is False

@@ -1,15 +1,16 @@
 """GPU: gradient centralization (grad_centralization=True) against the CPU oracle.
 
-Compact groups fold it into the step and the clip (apexw_grad_row_means writes
-one mean per row, the kernels subtract it from the raw grad); 8-bit groups
-read a prepared copy (apexw_grad_prepare).
-* the prepared grads (8-bit plan: sanitized, centralized per row of every
-  dim >= 2 grad) vs the oracle's _prepare_grads, and the row means (compact
-  plan) vs torch's mean of the sanitized grads: bf16 within 1 ulp (the row
-  mean is a sum in a different order, rounded to bf16), fp32 within 1e-6 of
-  the row's largest |g|;
-* full steps with bf16 params (compact and 8-bit, SR off) at the parity bars of
-  test_gpu_parity.py;
+Compact, 8-bit and ultra groups fold it into the step and the clip
+(apexw_grad_row_means writes one mean per row, the kernels subtract it from the
+raw grad: compact descriptors carry the means, 8-bit / ultra ones a side table);
+groups with factored tensors read a prepared copy (apexw_grad_prepare).
+* the prepared grads (8-bit plan with a factored tensor: sanitized, centralized
+  per row of every dim >= 2 grad) vs the oracle's _prepare_grads, and the row
+  means (compact plan) vs torch's mean of the sanitized grads: bf16 within 1
+  ulp (the row mean is a sum in a different order, rounded to bf16), fp32
+  within 1e-6 of the row's largest |g|;
+* full steps with bf16 params (compact, 8-bit with and without a full-block
+  NF4 tensor, ultra; SR off) at the parity bars of test_gpu_parity.py;
 * with AMP and the clip as well: the 2^10-scaled step equals the unscaled one
   bit for bit (unscale before centralizing, clip on centralized grads).
 """
@@ -71,18 +72,22 @@ def test_prepared_grads_match_oracle(dtype):
     from oracle.optim import OracleApexW
     print(f"gc prepared {dtype}", flush=True)
     gen = torch.Generator().manual_seed(11)
-    host = [(torch.randn(s, generator=gen) * 0.02).to(dtype) for s in SHAPES]
-    grads = [(torch.randn(s, generator=gen) * 1e-3 + 5e-4).to(dtype) for s in SHAPES]
+    # (256, 512) is factored with factored_v=True (>= 65536 elements, >= 128 rows and columns); no
+    # thin matrix such as (64, 2048), which would make the group look like an adapter (no factoring)
+    shapes = [s for s in SHAPES if s != (64, 2048)] + [(256, 512)]
+    host = [(torch.randn(s, generator=gen) * 0.02).to(dtype) for s in shapes]
+    grads = [(torch.randn(s, generator=gen) * 1e-3 + 5e-4).to(dtype) for s in shapes]
     grads[0][3, 7] = float("nan")
     gps = [torch.nn.Parameter(h.cuda()) for h in host]
     for p, g in zip(gps, grads):
         p.grad = g.cuda()
-    # 8-bit groups step a prepared copy of the grads
-    opt = ApexW(gps, lr=1e-3, grad_centralization=True, stochastic_rounding=False, precision="8bit")
+    # a group with a factored tensor steps a prepared copy of the grads
+    opt = ApexW(gps, lr=1e-3, grad_centralization=True, stochastic_rounding=False, precision="8bit",
+                factored_v=True)
     opt.step()
     torch.cuda.synchronize()
     plan = next(iter(opt._plans.values()))
-    assert not plan.gc_fold
+    assert plan.factored.any() and not plan.gc_fold
     cps = [torch.nn.Parameter(h.clone()) for h in host]
     ref, _ = OracleApexW(cps, grad_centralization=True)._prepare([g.clone() for g in grads], sanitize=True)
     for i, (out, r) in enumerate(zip(plan.gc_out, ref)):
@@ -97,15 +102,21 @@ def test_prepared_grads_match_oracle(dtype):
             assert float(err.max()) <= 0, (i, float(err.max()))
 
 
-@pytest.mark.parametrize("precision", ["compact", "8bit"])
-def test_gc_steps_match_oracle_bf16(precision):
+@pytest.mark.parametrize("precision,extra", [("compact", ()), ("8bit", ()), ("8bit", ((512, 1024), (300, 2048))),
+                                             ("ultra", ())], ids=["compact", "8bit", "8bit-fullblock", "ultra"])
+def test_gc_steps_match_oracle_bf16(precision, extra):
+    """4 steps; "8bit-fullblock" adds tensors of more than 2^18 elements (the
+    full-block NF4 kernel, its centralized instantiation) with rows of 1024 and
+    2048 elements."""
     _need_gpu()
     from apexw_amd import ApexW
     from oracle.optim import OracleApexW
-    print(f"gc steps {precision}", flush=True)
+    print(f"gc steps {precision} {extra}", flush=True)
     kw = dict(lr=1e-3, weight_decay=0.1, precision=precision, stochastic_rounding=False, grad_centralization=True)
+    if precision == "ultra":
+        kw["threshold"] = 4096
     gen = torch.Generator().manual_seed(12)
-    host = [(torch.randn(s, generator=gen) * 0.02).bfloat16() for s in SHAPES]
+    host = [(torch.randn(s, generator=gen) * 0.02).bfloat16() for s in SHAPES + list(extra)]
     gps = [torch.nn.Parameter(h.cuda()) for h in host]
     cps = [torch.nn.Parameter(h.clone()) for h in host]
     gopt, copt = ApexW(gps, **kw), OracleApexW(cps, **kw)
@@ -116,11 +127,16 @@ def test_gc_steps_match_oracle_bf16(precision):
         gopt.step()
         copt.step()
     torch.cuda.synchronize()
+    plan = next(iter(gopt._plans.values()))
+    assert plan.gc_fold
+    if extra:
+        assert plan.fast is not None and plan.fast.any(), "no tensor took the full-block kernel"
     _compare(gps, cps, gopt, copt, f"gc {precision}")
 
 
 @pytest.mark.parametrize("precision,dtype", [("compact", torch.bfloat16), ("compact", torch.float32),
-                                             ("8bit", torch.bfloat16)])
+                                             ("8bit", torch.bfloat16), ("8bit", torch.float32),
+                                             ("ultra", torch.bfloat16)])
 def test_gc_with_amp_and_clip_equals_unscaled(precision, dtype):
     _need_gpu()
     from apexw_amd import ApexW

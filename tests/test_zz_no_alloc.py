@@ -56,7 +56,7 @@ def _coef_pair(shapes, seed, clip=1.0, unit=None):
     coef_b = torch.full((1,), -2.0, device="cuda")
     L.check(lib.apexw_grad_clip_coef(tab.data_ptr(), len(grads), units.data_ptr(), n_units, unit,
                                      begin.data_ptr(), part.data_ptr(), norms.data_ptr(), clip, 1.0, L.HP_SANITIZE,
-                                     coef_a.data_ptr(), None, stream), "apexw_grad_clip_coef")
+                                     coef_a.data_ptr(), None, None, stream), "apexw_grad_clip_coef")
     L.check(lib.apexw_grad_clip_coef_noalloc(tab.data_ptr(), len(grads), units.data_ptr(), n_units, unit,
                                              begin.data_ptr(), clip, 1.0, L.HP_SANITIZE, coef_b.data_ptr(), None, stream),
             "apexw_grad_clip_coef_noalloc")

@@ -27,6 +27,7 @@ AdEMAMix (beta3), cautious masking, grad centralization, the Polar Express
 coefficients and scale_mode="rms" raise ``NotImplementedError``.
 """
 
+import functools
 import math
 from collections import defaultdict
 
@@ -56,8 +57,10 @@ def _pad(x, to):
     return (x + to - 1) // to * to
 
 
+@functools.lru_cache(maxsize=1024)
 def _round_to(dtype, x):
-    """A Python scalar as torch's same-dtype foreach ops see it (rounded to dtype)."""
+    """A Python scalar as torch's same-dtype foreach ops see it (rounded to dtype);
+    cached, since a step asks for the same few values every time."""
     return float(torch.tensor(x, dtype=torch.float32).to(dtype).float()) if dtype != torch.float32 else x
 
 
@@ -132,6 +135,7 @@ class NSPlan:
             tri = (t + 1) / (2 * t)
             self.exec_flops += ws.batch * s * (tri * (2 * ws.mp ** 2 * ws.np_ + 2 * ws.mp ** 3) + 2 * ws.mp ** 2 * ws.np_)
         self.device = device
+        self._applied = {}      # id(host table) -> (applies key, device table with the fused update)
         built = {}
         self.iters = []
         for i in range(max(steps, default=0)):
@@ -163,11 +167,21 @@ class NSPlan:
         matrix's final X' updates p in its epilogue.  Without applies the final X'
         is only stored (keep_result is then implied)."""
         lib = _lib.load()
+        key = None
+        if applies is not None:
+            key = (tuple(tuple(a) for a in applies), bool(keep_result))
         for phases in self.iters:
             for launches in phases:
                 for probs, items, offsets, n_wg, kind, host, fin in launches:
                     if fin and applies is not None:
-                        probs = self._upload_applies(lib, probs, host, fin, applies, keep_result)
+                        # the fused update's table changes only with the parameters' addresses
+                        # or the step's scalars: reuse the last upload while they hold
+                        hit = self._applied.get(id(host))
+                        if hit is not None and hit[0] == key:
+                            probs = hit[1]
+                        else:
+                            probs = self._upload_applies(lib, probs, host, fin, applies, keep_result)
+                            self._applied[id(host)] = (key, probs)
                     _lib.check(lib.apexw_gemm_nt_grouped(probs.data_ptr(), items.data_ptr(), offsets.data_ptr(),
                                                          n_wg, kind, amp, stream), "apexw_gemm_nt_grouped")
 

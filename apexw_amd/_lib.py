@@ -45,6 +45,7 @@ HP_LOOK_HI = 1 << 5
 HP_UNSCALE = 1 << 6
 HP_FV_SANITIZE = 1 << 7
 HP_AMP = 1 << 8
+HP_NESTEROV = 1 << 9
 
 STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported dtype combination", 3: "launch failed",
           4: "misaligned pointer", 5: "exceeds the fixed workspace of the allocation-free entry point"}

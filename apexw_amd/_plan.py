@@ -90,6 +90,7 @@ class StepPlan:
         self.states = [opt.state[p] for p in self.params]
         self.gc = bool(group.get("grad_centralization", False))
         self.cold_done = False
+        self._nesterov = False
         self.amp_dirty = False      # skips counted on the device that the host has not folded
         self._build_steps()
         self._build_tables(group)
@@ -641,6 +642,8 @@ class StepPlan:
 
     def _prepare(self, group, seed, inv_scale, lr, wd, steps, amp):
         mode_cold = not self.cold_done
+        # the in-backward flush steps without nesterov whatever the group says (optimizer.py:2358)
+        self._nesterov = bool(group.get("nesterov", False)) and not (self.single or self.hooked)
         keep = self._refresh_grads()      # contiguous copies of non-contiguous grads, alive until the launch
         if amp is not None:
             inv_scale = 1.0          # a stand-in: the kernels read the factor from the device scalars
@@ -844,8 +847,15 @@ class StepPlan:
             hp.step_size = lr * bc2s / bc1
             hp.eps_scaled = eps * bc2s
             hp.eps = eps
-            hp.gain_hi = 1.0 + 0.20 * b1
-            hp.gain_lo = 1.0 - 0.35 * b1
+            if self._nesterov:
+                # nesterov: num = lerp(g, m, beta1) with no SNR gain (optimizer.py:4581-4583,
+                # :4444-4445): the blocks multiply by a gain of exactly 1, the dense and
+                # ultra rows take the lookahead instead of m
+                hp.gain_hi = hp.gain_lo = 1.0
+                flags |= L.HP_NESTEROV
+            else:
+                hp.gain_hi = 1.0 + 0.20 * b1
+                hp.gain_lo = 1.0 - 0.35 * b1
             hp.mode = L.MODE_COLD if cold else L.MODE_REPLAY
             if sr:
                 flags |= L.HP_SR

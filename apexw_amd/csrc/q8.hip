@@ -1018,7 +1018,9 @@ APEXW_DEV void q8_dense(const apexw_tensor& t, uint32_t unit, const Q8Ctx& c) {
     const float vf = fmaf(hp.one_minus_beta2 * g, g, load1<VD>(t.v, i) * hp.beta2);
     store1<VD>(t.v, i, rnd<VD>(vf));
     const float den = sqrtf(vf) + hp.eps_scaled;
-    const float upd = (mf / den) * hp.step_size;
+    // Nesterov: torch.lerp(g, m, beta1) on the fp32 m (optimizer.py:4719-4724)
+    const float num = (hp.flags & APEXW_HP_NESTEROV) ? lerp_to(g, mf, hp.look_coef, hp.flags & APEXW_HP_LOOK_HI) : mf;
+    const float upd = (num / den) * hp.step_size;
     if constexpr (PD == APEXW_F32) p = p - upd;
     else p = rnd<PD>(p - rnd<PD>(upd));
     store1<PD>(t.p, i, p);
@@ -1084,7 +1086,10 @@ APEXW_DEV void ultra_block(const apexw_tensor& t, uint32_t tix, uint32_t blk, co
       m[j] = lerp_to(m[j], g[j], hp.lerp_coef, hp.flags & APEXW_HP_LERP_HI);
       const float vf = fmaf(hp.one_minus_beta2 * g[j], g[j], v[j] * hp.beta2);
       v[j] = rnd<VD>(vf);
-      const float upd = (m[j] / (sqrtf(vf) + hp.eps_scaled)) * hp.step_size;
+      // Nesterov: torch.lerp(g, m, beta1) on the fp32 m (optimizer.py:4667-4670)
+      const float num = (hp.flags & APEXW_HP_NESTEROV)
+                            ? lerp_to(g[j], m[j], hp.look_coef, hp.flags & APEXW_HP_LOOK_HI) : m[j];
+      const float upd = (num / (sqrtf(vf) + hp.eps_scaled)) * hp.step_size;
       if constexpr (PD == APEXW_F32) p[j] = p[j] - upd;
       else p[j] = rnd<PD>(p[j] - rnd<PD>(upd));
     }
@@ -1223,7 +1228,9 @@ APEXW_DEV void ultra_block_full(const apexw_tensor& t, uint32_t tix, uint32_t bl
         amax = fmaxf(amax, fabsf(mnew[k][j]));
         const float vf = fmaf(hp.one_minus_beta2 * g[j], g[j], v[j] * hp.beta2);
         v[j] = rnd<VD>(vf);
-        const float upd = (mnew[k][j] / (sqrtf(vf) + hp.eps_scaled)) * hp.step_size;
+        const float num = (hp.flags & APEXW_HP_NESTEROV)
+                              ? lerp_to(g[j], mnew[k][j], hp.look_coef, hp.flags & APEXW_HP_LOOK_HI) : mnew[k][j];
+        const float upd = (num / (sqrtf(vf) + hp.eps_scaled)) * hp.step_size;
         if constexpr (PD == APEXW_F32) p[j] = p[j] - upd;
         else p[j] = rnd<PD>(p[j] - rnd<PD>(upd));
       }

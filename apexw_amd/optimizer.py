@@ -39,8 +39,21 @@ DOWNCAST_MIN_NUMEL = 1024          # optimizer.py:2100
 HOOK_MIN_NUMEL = 16384             # optimizer.py:2131
 HOOK_BATCH = 14                    # optimizer.py:2142
 
-_UNSUPPORTED_FLAGS = ("amsgrad", "nesterov", "cautious", "lion", "maximize",
+_UNSUPPORTED_FLAGS = ("amsgrad", "cautious", "lion", "maximize",
                       "capturable", "differentiable", "auto_pack")
+# nesterov=True runs in the precisions whose step is _step_ultra (optimizer.py:4313-4735)
+_NESTEROV_PRECISIONS = ("8bit", "ultra")
+
+
+def _check_nesterov(precision, factored):
+    """nesterov=True: the 8-bit and ultra steps take it (the lookahead numerator
+    lerp(g, m, beta1) without the SNR gain); the compact-kernel precisions and
+    factored second moments do not."""
+    if precision not in _NESTEROV_PRECISIONS:
+        raise NotImplementedError(f"apexw_amd: nesterov=True with precision {precision!r} "
+                                  f"(supported: {', '.join(_NESTEROV_PRECISIONS)})")
+    if factored:
+        raise NotImplementedError("apexw_amd: nesterov=True with factored_v")
 
 
 class ApexW(Optimizer):
@@ -137,6 +150,8 @@ class ApexW(Optimizer):
         if bad or beta3 is not None:
             what = ", ".join(bad + (["beta3"] if beta3 is not None else []))
             raise NotImplementedError(f"apexw_amd implements the standard AdamW step; not supported: {what}")
+        if nesterov:
+            _check_nesterov(S.normalize_precision(precision), factored_v)
         if precision == "compact" and betas[1] >= 0.99 and not stochastic_rounding and not adamw_compat:
             warnings.warn(
                 f"ApexW: beta2={betas[1]} with precision='compact' and stochastic_rounding=False "
@@ -326,6 +341,8 @@ class ApexW(Optimizer):
                 self.state[p].update(S.init_state(p, group, peft, has16))
             if p.dtype == torch.float16 and self.state[p].get("is_factored_v", False):
                 raise NotImplementedError("apexw_amd: factored_v with fp16 parameters")
+        if group.get("nesterov", False):
+            _check_nesterov(group["precision"], any(self.state[p].get("is_factored_v", False) for p in params))
         if group["precision"] in ("8bit", "ultra"):
             # both run the reference's _step_ultra (optimizer.py:3583-3587)
             return StepPlan(self, group, params, "q8")
@@ -404,7 +421,8 @@ class ApexW(Optimizer):
         """bf16 parameters and layer-batched in-backward steps for large 8-bit
         models (optimizer.py:2059-2167)."""
         d = self.defaults
-        if not force and (d.get("clip_grad_norm") is not None or d.get("grad_centralization", False)):
+        if not force and (d.get("clip_grad_norm") is not None or d.get("grad_centralization", False)
+                          or d.get("nesterov", False)):
             return
         trainable = []
         total = 0

@@ -151,6 +151,9 @@ typedef struct apexw_unit {
                                           step_size, eps_scaled, bc2_sqrt and grad_inv_scale from
                                           *amp (apexw_amp_prepare) and return before any write when
                                           amp->skip (found_inf); APEXW_HP_UNSCALE is set with it */
+#define APEXW_HP_NESTEROV (1u << 9)    /* 8-bit / ultra steps with nesterov=True: the dense and ultra
+                                          rows' numerator is lerp(g, m, beta1) instead of m (the NF4 /
+                                          INT8 blocks take Nesterov through gain_hi = gain_lo = 1) */
 
 /* Step scalars of one launch, written on the device by apexw_amp_prepare (32 bytes). */
 typedef struct apexw_amp_dyn {

@@ -1,8 +1,8 @@
 """8-bit AdamW step (CPU oracle; test infrastructure only).
 
 Restates ``ApexW._step_ultra`` (``apexw/optimizer.py:4313-4735``) for
-``precision="8bit"`` with the standard update (no amsgrad / lion / AdEMAMix /
-nesterov / cautious / factored-v), per parameter:
+``precision="8bit"`` with the standard update or ``nesterov=True`` (no amsgrad /
+lion / AdEMAMix / cautious), per parameter:
 
 * large contiguous quantized tensors (numel > 262144) use the chunked path,
   optimizer.py:4402-4499 -- decay and update fused in fp32, one rounding of p;
@@ -17,6 +17,9 @@ m/v and take the dense branch above.
 
 The update is AdamW with the "Nesterov-SNR" lookahead gain: ``m_look =
 lerp(g, m, b1)``, gain ``1+0.2*b1`` where ``m*g >= 0`` else ``1-0.35*b1``.
+With ``nesterov=True`` the numerator is ``lerp(g, m, b1)`` without the gain in the
+quantized branches (optimizer.py:4444-4445, :4581-4582), and replaces ``m`` in the
+dense and ultra ones (:4667-4670, :4719-4724).
 """
 
 import math
@@ -36,14 +39,17 @@ def _bias(lr, beta1, beta2, eps, step):
     return lr * s / bc1, eps * s
 
 
-def _snr_num(m, g, beta1):
+def _snr_num(m, g, beta1, nesterov=False):
+    if nesterov:
+        return torch.lerp(g, m, beta1)
     gain_hi = 1.0 + 0.20 * beta1
     gain_lo = 1.0 - 0.35 * beta1
     look = torch.lerp(g, m, beta1)
     return look.mul_(torch.where(m * g >= 0.0, gain_hi, gain_lo))
 
 
-def q8_param_step(p, g, st, *, lr, beta1, beta2, eps, weight_decay, decay_norm_only, step, inv_scale=None):
+def q8_param_step(p, g, st, *, lr, beta1, beta2, eps, weight_decay, decay_norm_only, step, inv_scale=None,
+                  nesterov=False):
     """Update one parameter and its state in place.  ``step`` is already incremented."""
     step_size, eps_scaled = _bias(lr, beta1, beta2, eps, step)
     decay = max(1.0 - lr * weight_decay, 0.0) if weight_decay != 0 else 1.0
@@ -56,10 +62,11 @@ def q8_param_step(p, g, st, *, lr, beta1, beta2, eps, weight_decay, decay_norm_o
                         wd_factor=decay if apply_wd else None, inv_scale=inv_scale, sanitize=True)
         return
     if st.get("is_ultra", False):
-        _ultra(p, g, st, beta1, beta2, step_size, eps_scaled, decay if apply_wd else None, sr, inv_scale)
+        _ultra(p, g, st, beta1, beta2, step_size, eps_scaled, decay if apply_wd else None, sr, inv_scale, nesterov)
         return
     if st.get("is_8bit", False) and n > CHUNK and p.is_contiguous():
-        _chunked(p, g, st, beta1, beta2, eps, step_size, eps_scaled, decay if apply_wd else None, sr, inv_scale)
+        _chunked(p, g, st, beta1, beta2, eps, step_size, eps_scaled, decay if apply_wd else None, sr, inv_scale,
+                 nesterov)
         return
     gf = torch.nan_to_num(g, nan=0.0, posinf=65504.0, neginf=-65504.0).float()
     if inv_scale is not None:                           # AMP: optimizer.py:4504-4505
@@ -88,7 +95,7 @@ def q8_param_step(p, g, st, *, lr, beta1, beta2, eps, weight_decay, decay_norm_o
             v.mul_(beta2).addcmul_(gf, gf, value=1.0 - beta2)
             v.nan_to_num_(nan=0.0, posinf=0.0, neginf=0.0)
             den = v.sqrt().add_(eps_scaled).clamp_min_(eps)
-        num = _snr_num(m, gf, beta1)
+        num = _snr_num(m, gf, beta1, nesterov)
         if p.dtype == torch.float32:
             p.addcdiv_(num, den, value=-step_size)
         else:
@@ -114,11 +121,12 @@ def q8_param_step(p, g, st, *, lr, beta1, beta2, eps, weight_decay, decay_norm_o
     vf = v.float().mul_(beta2).addcmul_(gf, gf, value=1.0 - beta2)
     v.copy_(vf.to(v.dtype))
     den = vf.sqrt().add_(eps_scaled)
-    upd = (mf / den).mul_(step_size)
+    num = torch.lerp(gf, mf, beta1) if nesterov else mf
+    upd = (num / den).mul_(step_size)
     p.sub_(upd.to(p.dtype))
 
 
-def _chunked(p, g, st, beta1, beta2, eps, step_size, eps_scaled, decay, sr, inv_scale=None):
+def _chunked(p, g, st, beta1, beta2, eps, step_size, eps_scaled, decay, sr, inv_scale=None, nesterov=False):
     n = p.numel()
     bs = st["block_size_8bit"]
     int4 = st.get("is_4bit_m", False)
@@ -143,7 +151,7 @@ def _chunked(p, g, st, beta1, beta2, eps, step_size, eps_scaled, decay, sr, inv_
             msl = mbuf[off:end]
             m = Q.dequant_int8(msl, sm, bs)
         m.lerp_(gc, 1.0 - beta1)
-        num = _snr_num(m, gc, beta1)
+        num = _snr_num(m, gc, beta1, nesterov)
         if quad:
             vsl = vbuf[off // 4:end // 4]
             v = Q.dequant_logu8(vsl, sv, vbs)
@@ -180,7 +188,7 @@ def _chunked(p, g, st, beta1, beta2, eps, step_size, eps_scaled, decay, sr, inv_
         sv.copy_(s2)
 
 
-def _ultra(p, g, st, beta1, beta2, step_size, eps_scaled, decay, sr, inv_scale):
+def _ultra(p, g, st, beta1, beta2, step_size, eps_scaled, decay, sr, inv_scale, nesterov=False):
     """optimizer.py:4500-4511, :4640-4686: INT8 m (block ``ultra_block_size``,
     EMA-max scales), dense v rounded to its dtype once, the denominator from the
     unrounded fp32 v, p decayed then ``p -= update.to(p.dtype)``."""
@@ -196,7 +204,8 @@ def _ultra(p, g, st, beta1, beta2, step_size, eps_scaled, decay, sr, inv_scale):
     vf = v.float().mul_(beta2).addcmul_(gf, gf, value=1.0 - beta2)
     v.copy_(vf.to(v.dtype))
     den = vf.sqrt().add_(eps_scaled)
-    upd = (m / den).mul_(step_size)
+    num = torch.lerp(gf, m, beta1) if nesterov else m
+    upd = (num / den).mul_(step_size)
     p.sub_(upd.to(p.dtype))
     q, s = Q.quant_int8(m, bs, st["exp_avg_scales"], sr)
     st["exp_avg"].copy_(q.view(st["exp_avg"].shape))

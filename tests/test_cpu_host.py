@@ -164,6 +164,14 @@ def test_constructor_contract():
         ApexW(p, precision="nope")
     with pytest.raises(NotImplementedError):
         ApexW(p, amsgrad=True)
+    # nesterov: the _step_ultra precisions only, without factored second moments
+    for prec in ("8bit", "ultra", "3byte"):
+        assert ApexW(p, precision=prec, nesterov=True).defaults["nesterov"]
+    for prec in ("compact", "full", "auto"):
+        with pytest.raises(NotImplementedError):
+            ApexW(p, precision=prec, nesterov=True)
+    with pytest.raises(NotImplementedError):
+        ApexW(p, precision="8bit", nesterov=True, factored_v=True)
     for prec, betas in (("full", (0.9, 0.999)), ("fp32", (0.9, 0.999)), ("auto", (0.9, 0.99)),
                         ("smart", (0.9, 0.99)), ("ultra", (0.9, 0.99)), ("3byte", (0.9, 0.99))):
         o = ApexW(p, precision=prec)

@@ -174,8 +174,8 @@ def test_reference_factored_8bit_routing():
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_reference_factored_8bit_convergence(dtype):
-    """test_quantization.py:594-623 on the GPU (the plain update; cautious and
-    nesterov are outside this build)."""
+    """test_quantization.py:594-623 on the GPU (the plain update; cautious, and
+    nesterov with factored second moments, are outside this build)."""
     _need_gpu()
     from apexw_amd import ApexW
     torch.manual_seed(7)

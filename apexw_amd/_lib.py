@@ -46,6 +46,7 @@ HP_UNSCALE = 1 << 6
 HP_FV_SANITIZE = 1 << 7
 HP_AMP = 1 << 8
 HP_NESTEROV = 1 << 9
+HP_CAUTIOUS = 1 << 10
 
 STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported dtype combination", 3: "launch failed",
           4: "misaligned pointer", 5: "exceeds the fixed workspace of the allocation-free entry point"}
@@ -88,10 +89,10 @@ class HParams(ctypes.Structure):
                 ("bc2_sqrt", ctypes.c_float), ("gain_hi", ctypes.c_float), ("gain_lo", ctypes.c_float),
                 ("clip_coef", ctypes.c_void_p), ("seed", ctypes.c_uint64), ("step", ctypes.c_uint32),
                 ("mode", ctypes.c_uint32), ("flags", ctypes.c_uint32), ("grad_inv_scale", ctypes.c_float),
-                ("amp", ctypes.c_void_p), ("rows", ctypes.c_void_p)]
+                ("amp", ctypes.c_void_p), ("rows", ctypes.c_void_p), ("counts", ctypes.c_void_p)]
 
 
-assert ctypes.sizeof(HParams) == 104
+assert ctypes.sizeof(HParams) == 112
 # apexw_row_means: grad centralization's row means of one 8-bit / ultra descriptor
 ROW_MEANS_DTYPE = np.dtype([("means", np.uint64), ("row_len", np.int64)])
 
@@ -101,7 +102,7 @@ AMP_LAUNCH_DTYPE = np.dtype([("lr", np.float64), ("beta1", np.float64), ("beta2"
                              ("step", np.float64), ("kind", np.uint32), ("reserved", np.uint32)])
 assert AMP_LAUNCH_DTYPE.itemsize == 48
 # apexw_check_launch kinds
-LAUNCH_COMPACT, LAUNCH_Q8, LAUNCH_FACTORED, LAUNCH_ULTRA = 0, 1, 4, 5
+LAUNCH_COMPACT, LAUNCH_Q8, LAUNCH_FACTORED, LAUNCH_ULTRA, LAUNCH_CAUTIOUS = 0, 1, 4, 5, 6
 
 AMP_DYN_BYTES = 32
 AMP_MAX_LAUNCHES = 16
@@ -154,6 +155,7 @@ SIGNATURES = {
     "apexw_compact_step": (ctypes.c_int, [_vp, _i32, _vp, _i64, _HP, _vp]),
     "apexw_ultra_step": (ctypes.c_int, [_vp, _i32, _vp, _i64, _HP, _vp]),
     "apexw_q8_step": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _i64, _HP, _vp]),
+    "apexw_q8_cautious_count": (ctypes.c_int, [_vp, _i32, _vp, _i64, _HP, _vp]),
     "apexw_grad_clip_coef": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _vp, _vp, _vp, _f32, _f32, _u32, _vp, _vp, _vp,
                                             _vp]),
     "apexw_grad_clip_coef_noalloc": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _vp, _f32, _f32, _u32, _vp, _vp, _vp]),

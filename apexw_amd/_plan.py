@@ -89,11 +89,20 @@ class StepPlan:
         self.device = self.params[0].device
         self.states = [opt.state[p] for p in self.params]
         self.gc = bool(group.get("grad_centralization", False))
+        # cautious=True (8-bit / ultra): a count pass forms the mask's mean before the step
+        self.cautious = self._cautious_of(group)
+        self.d_counts = None
         self.cold_done = False
         self._nesterov = False
         self.amp_dirty = False      # skips counted on the device that the host has not folded
         self._build_steps()
         self._build_tables(group)
+
+    def _cautious_of(self, group):
+        """The group's cautious flag as this plan's kernels take it: the 8-bit / ultra
+        steps, not enable_fused_backward's per-parameter update (which has no
+        cautious branch, optimizer.py:2373-2471)."""
+        return bool(group.get("cautious", False)) and self.kind == "q8" and not self.single
 
     # ------------------------------------------------------------------ validity
     def valid_for(self, group):
@@ -108,6 +117,8 @@ class StepPlan:
         if group.get("precision") != self.precision:
             return False
         if bool(group.get("grad_centralization", False)) != self.gc:
+            return False
+        if self._cautious_of(group) != self.cautious:
             return False
         self._scan_status = self._scan()
         return self._scan_status in (SCAN_SAME, SCAN_GRADS_MOVED, SCAN_SLOW)
@@ -158,7 +169,8 @@ class StepPlan:
                 f |= L.FLAG_NF4
             if st.get("is_quad_v", False):
                 f |= L.FLAG_QUAD
-            if not (p.numel() > CHUNKED_MIN_NUMEL and p.is_contiguous()):
+            # cautious=True keeps every tensor off the chunked order (optimizer.py:4402-4414)
+            if self.cautious or not (p.numel() > CHUNKED_MIN_NUMEL and p.is_contiguous()):
                 f |= L.FLAG_GENERIC
             if block % 8:
                 f |= L.FLAG_SCALAR
@@ -642,6 +654,8 @@ class StepPlan:
 
     def _prepare(self, group, seed, inv_scale, lr, wd, steps, amp):
         mode_cold = not self.cold_done
+        if self.cautious and self.d_counts is None:
+            self.d_counts = torch.zeros(len(self.params), dtype=torch.int64, device=self.device)
         # the in-backward flush steps without nesterov whatever the group says (optimizer.py:2358)
         self._nesterov = bool(group.get("nesterov", False)) and not (self.single or self.hooked)
         keep = self._refresh_grads()      # contiguous copies of non-contiguous grads, alive until the launch
@@ -712,6 +726,9 @@ class StepPlan:
             L.check(self._lib.apexw_check_launch(launch_kind, len(self.params), n_units, n_fast, n_fast32,
                                                  ctypes_ref(hp)), "apexw step")
             launches.append((d_units, n_units, n_fast, n_fast32, hp))
+        if self.cautious and launches:
+            L.check(self._lib.apexw_check_launch(L.LAUNCH_CAUTIOUS, len(self.params), self.n_units, 0, 0,
+                                                 ctypes_ref(launches[0][4])), "apexw_q8_cautious_count")
         fv_launches = []
         if self.fv is not None:
             replay_step = None if (mode_cold or self.native or self.kind == "q8") else groups[0][1]
@@ -734,6 +751,12 @@ class StepPlan:
         if prog.clip is not None:
             self._clip(prog.clip, prog.sanitize, prog.inv_scale, stream, prog.amp_dyn)
         table = self.d_table.data_ptr()
+        if self.cautious and prog.launches:
+            # the mask counts of every tensor, from the grads as prepared above (clip,
+            # centralization, AMP), before any launch updates a moment
+            L.check(self._lib.apexw_q8_cautious_count(table, len(self.params), self.d_units.data_ptr(), self.n_units,
+                                                      ctypes_ref(prog.launches[0][4]), stream),
+                    "apexw_q8_cautious_count")
         for d_units, n_units, n_fast, n_fast32, hp in prog.launches:
             if self.kind == "compact":
                 st = self._lib.apexw_compact_step(table, len(self.params), d_units.data_ptr(), n_units,
@@ -853,6 +876,12 @@ class StepPlan:
                 # ultra rows take the lookahead instead of m
                 hp.gain_hi = hp.gain_lo = 1.0
                 flags |= L.HP_NESTEROV
+            elif self.cautious:
+                # cautious: num = m' (no lookahead) times the mask over its mean
+                # (optimizer.py:4583-4588); the kernels take each tensor's gains from its count
+                hp.gain_hi, hp.gain_lo = 1.0, 0.0
+                flags |= L.HP_CAUTIOUS
+                hp.counts = self.d_counts.data_ptr()
             else:
                 hp.gain_hi = 1.0 + 0.20 * b1
                 hp.gain_lo = 1.0 - 0.35 * b1
@@ -880,6 +909,10 @@ class StepPlan:
             flags |= L.HP_LERP_HI
         hp.look_coef, hi = _lerp_coef(b1)
         if hi:
+            flags |= L.HP_LOOK_HI
+        if flags & L.HP_CAUTIOUS:
+            # lerp(g, m', b1) with coefficient 0 in the end-based form is m' itself
+            hp.look_coef = 0.0
             flags |= L.HP_LOOK_HI
         if sanitize:
             flags |= L.HP_SANITIZE

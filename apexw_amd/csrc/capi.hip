@@ -16,6 +16,8 @@ int apexw_launch_compact(const apexw_tensor*, int64_t, const apexw_unit*, const 
 int apexw_launch_q8(const apexw_tensor*, int64_t, const apexw_unit*, const apexw_hparams*, hipStream_t);
 int apexw_launch_q8_fast(const apexw_tensor*, int64_t, const apexw_unit*, const apexw_hparams*, int32_t, hipStream_t);
 int apexw_launch_ultra(const apexw_tensor*, int64_t, const apexw_unit*, const apexw_hparams*, hipStream_t);
+int apexw_launch_q8_cautious_count(const apexw_tensor*, int32_t, const apexw_unit*, int64_t, const apexw_hparams*,
+                                   hipStream_t);
 bool apexw_q8_fast_eligible(uint32_t flags, uint32_t block);
 int apexw_launch_clip(const apexw_tensor*, int32_t, const apexw_unit*, int64_t, int64_t, const int64_t*, float*, float*,
                       float, float, uint32_t, float*, const apexw_amp_dyn*, const apexw_row_means*, hipStream_t);
@@ -89,6 +91,7 @@ bool hp_ok(const apexw_hparams* hp) {
   if (hp->mode == APEXW_MODE_SINGLE && (hp->flags & (APEXW_HP_SANITIZE | APEXW_HP_CLIP | APEXW_HP_UNSCALE)))
     return false;
   if ((hp->flags & APEXW_HP_CLIP) && !hp->clip_coef) return false;
+  if ((hp->flags & APEXW_HP_CAUTIOUS) && (!hp->counts || hp->mode == APEXW_MODE_SINGLE)) return false;
   if (hp->flags & APEXW_HP_AMP) {
     // device-side AMP scalars: the compact and 8-bit step modes, with the unscale they carry
     if (!hp->amp || ((uintptr_t)hp->amp & 15u) || hp->mode == APEXW_MODE_SINGLE) return false;
@@ -173,6 +176,11 @@ static int launch_args_status(int32_t kind, int32_t n_tensors, int64_t n_units, 
       if (hp->mode == APEXW_MODE_NATIVE) return APEXW_ERR_ARG;
       if (hp->mode == APEXW_MODE_SINGLE && (n_fast_units || n_fast_f32_units)) return APEXW_ERR_ARG;
       return APEXW_OK;
+    case APEXW_LAUNCH_CAUTIOUS:
+      if (n_fast_units || n_fast_f32_units) return APEXW_ERR_ARG;
+      if (!(hp->flags & APEXW_HP_CAUTIOUS) || !hp->counts) return APEXW_ERR_ARG;
+      if (hp->mode == APEXW_MODE_NATIVE || hp->mode == APEXW_MODE_SINGLE) return APEXW_ERR_ARG;
+      return ((uintptr_t)hp->counts & 7u) ? APEXW_ERR_ALIGN : APEXW_OK;
     case APEXW_LAUNCH_FACTORED:
       if (n_fast_units || n_fast_f32_units) return APEXW_ERR_ARG;
       if (hp->mode == APEXW_MODE_SINGLE || hp->mode == APEXW_MODE_NATIVE) return APEXW_ERR_ARG;
@@ -193,6 +201,14 @@ int apexw_compact_step(const apexw_tensor* tensors, int32_t n_tensors, const ape
   const int st = launch_args_status(APEXW_LAUNCH_COMPACT, n_tensors, n_units, 0, 0, hp);
   if (st != APEXW_OK || n_units == 0) return st;
   return apexw_launch_compact(tensors, n_units, units, hp, (hipStream_t)stream);
+}
+
+int apexw_q8_cautious_count(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,
+                            const apexw_hparams* hp, void* stream) {
+  if (!tensors || !units) return APEXW_ERR_ARG;
+  const int st = launch_args_status(APEXW_LAUNCH_CAUTIOUS, n_tensors, n_units, 0, 0, hp);
+  if (st != APEXW_OK) return st;
+  return apexw_launch_q8_cautious_count(tensors, n_tensors, units, n_units, hp, (hipStream_t)stream);
 }
 
 int apexw_ultra_step(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,

@@ -45,7 +45,25 @@ struct Q8Ctx {
   // means and row length from the launch's side table (hparams.rows), else nullptr
   const float* gc_means;
   int64_t gc_rl;
+  // the SNR gains of the current unit's tensor: the launch's, or with cautious=True
+  // (q_t, 0), q_t = 1 / max(c_t / n_t, 1e-3) from the tensor's mask count
+  float gain_hi, gain_lo;
 };
+
+// The gains of tensor tix (APEXW_HP_CAUTIOUS: the cautious mask's 1 / mean and 0;
+// torch's float32 mean of the 0 / 1 mask is the count over n, exactly rounded,
+// for tensors of up to 2^24 elements, apexw/optimizer.py:4585-4588).
+APEXW_DEV void q8_set_gains(Q8Ctx& c, const apexw_tensor& t, uint32_t tix) {
+  const apexw_hparams& hp = *c.hp;
+  if (hp.flags & APEXW_HP_CAUTIOUS) {
+    const float mean = fmaxf((float)hp.counts[tix] / (float)t.n, 1e-3f);
+    c.gain_hi = 1.0f / mean;
+    c.gain_lo = 0.0f;
+  } else {
+    c.gain_hi = hp.gain_hi;
+    c.gain_lo = hp.gain_lo;
+  }
+}
 
 // Point the context at the row means of tensor tix (or at none).
 APEXW_DEV void q8_set_rows(Q8Ctx& c, const apexw_tensor& t, uint32_t tix) {
@@ -360,7 +378,7 @@ APEXW_DEV void q8_block(const apexw_tensor& t, uint32_t tix, uint32_t blk, const
     for (int j = 0; j < 8; ++j) {
       const float look = SINGLE ? fmaf(hp.one_minus_beta1, g[j], m[j] * hp.beta1)
                                 : lerp_to(g[j], m[j], hp.look_coef, hp.flags & APEXW_HP_LOOK_HI);
-      num[j] = look * ((m[j] * g[j] >= 0.0f) ? hp.gain_hi : hp.gain_lo);
+      num[j] = look * ((m[j] * g[j] >= 0.0f) ? c.gain_hi : c.gain_lo);
     }
     float dens[8] = {1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f};  // SINGLE: denominators
     float upd[8];
@@ -759,7 +777,7 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
         vq[k][q] = vv;
         if (FULL || 4 * q < cnt[k]) vmax = fmaxf(vmax, vv);
         const float r = __builtin_amdgcn_rcpf(fmaxf(__builtin_amdgcn_sqrtf(vv) + hp.eps_scaled, hp.eps)) * hp.step_size;
-        float r_hi = r * hp.gain_hi, r_lo = r * hp.gain_lo;
+        float r_hi = r * c.gain_hi, r_lo = r * c.gain_lo;
         // keep the two products per quad: otherwise the compiler sinks them below the
         // per-element select, one multiply per element instead of two per quad
         asm volatile("" : "+v"(r_hi), "+v"(r_lo));
@@ -802,7 +820,7 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
       for (int j = 0; j < 8; ++j) {
         m[j] = lerp_to(m[j], g[j], hp.lerp_coef, lerp_hi);
         const float lk = lerp_to(g[j], m[j], hp.look_coef, look_hi);
-        num[j] = lk * ((m[j] * g[j] >= 0.0f) ? hp.gain_hi : hp.gain_lo);
+        num[j] = lk * ((m[j] * g[j] >= 0.0f) ? c.gain_hi : c.gain_lo);
       }
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
@@ -1019,7 +1037,9 @@ APEXW_DEV void q8_dense(const apexw_tensor& t, uint32_t unit, const Q8Ctx& c) {
     store1<VD>(t.v, i, rnd<VD>(vf));
     const float den = sqrtf(vf) + hp.eps_scaled;
     // Nesterov: torch.lerp(g, m, beta1) on the fp32 m (optimizer.py:4719-4724)
-    const float num = (hp.flags & APEXW_HP_NESTEROV) ? lerp_to(g, mf, hp.look_coef, hp.flags & APEXW_HP_LOOK_HI) : mf;
+    float num = (hp.flags & APEXW_HP_NESTEROV) ? lerp_to(g, mf, hp.look_coef, hp.flags & APEXW_HP_LOOK_HI) : mf;
+    // cautious: num * (mask / mean(mask)), mask = num g >= 0 (optimizer.py:4726-4729)
+    if (hp.flags & APEXW_HP_CAUTIOUS) num = num * ((num * g >= 0.0f) ? c.gain_hi : 0.0f);
     const float upd = (num / den) * hp.step_size;
     if constexpr (PD == APEXW_F32) p = p - upd;
     else p = rnd<PD>(p - rnd<PD>(upd));
@@ -1087,8 +1107,10 @@ APEXW_DEV void ultra_block(const apexw_tensor& t, uint32_t tix, uint32_t blk, co
       const float vf = fmaf(hp.one_minus_beta2 * g[j], g[j], v[j] * hp.beta2);
       v[j] = rnd<VD>(vf);
       // Nesterov: torch.lerp(g, m, beta1) on the fp32 m (optimizer.py:4667-4670)
-      const float num = (hp.flags & APEXW_HP_NESTEROV)
-                            ? lerp_to(g[j], m[j], hp.look_coef, hp.flags & APEXW_HP_LOOK_HI) : m[j];
+      float num = (hp.flags & APEXW_HP_NESTEROV)
+                      ? lerp_to(g[j], m[j], hp.look_coef, hp.flags & APEXW_HP_LOOK_HI) : m[j];
+      // cautious: num * (mask / mean(mask)), mask = num g >= 0 (optimizer.py:4672-4675)
+      if (hp.flags & APEXW_HP_CAUTIOUS) num = num * ((num * g[j] >= 0.0f) ? c.gain_hi : 0.0f);
       const float upd = (num / (sqrtf(vf) + hp.eps_scaled)) * hp.step_size;
       if constexpr (PD == APEXW_F32) p[j] = p[j] - upd;
       else p[j] = rnd<PD>(p[j] - rnd<PD>(upd));
@@ -1228,8 +1250,9 @@ APEXW_DEV void ultra_block_full(const apexw_tensor& t, uint32_t tix, uint32_t bl
         amax = fmaxf(amax, fabsf(mnew[k][j]));
         const float vf = fmaf(hp.one_minus_beta2 * g[j], g[j], v[j] * hp.beta2);
         v[j] = rnd<VD>(vf);
-        const float num = (hp.flags & APEXW_HP_NESTEROV)
-                              ? lerp_to(g[j], mnew[k][j], hp.look_coef, hp.flags & APEXW_HP_LOOK_HI) : mnew[k][j];
+        float num = (hp.flags & APEXW_HP_NESTEROV)
+                        ? lerp_to(g[j], mnew[k][j], hp.look_coef, hp.flags & APEXW_HP_LOOK_HI) : mnew[k][j];
+        if (hp.flags & APEXW_HP_CAUTIOUS) num = num * ((num * g[j] >= 0.0f) ? c.gain_hi : 0.0f);
         const float upd = (num / (sqrtf(vf) + hp.eps_scaled)) * hp.step_size;
         if constexpr (PD == APEXW_F32) p[j] = p[j] - upd;
         else p[j] = rnd<PD>(p[j] - rnd<PD>(upd));
@@ -1320,6 +1343,7 @@ __global__ __launch_bounds__(256) void ultra_step_kernel(const apexw_tensor* __r
     const apexw_unit un = units[u];
     const apexw_tensor& t = tensors[un.tensor];
     q8_set_rows(c, t, un.tensor);
+    q8_set_gains(c, t, un.tensor);
     const uint32_t f = t.flags;
     const uint32_t pd = (f >> APEXW_FLAG_PDT_SHIFT) & 3u;
     const uint32_t md = (f >> APEXW_FLAG_MDT_SHIFT) & 3u;
@@ -1395,6 +1419,7 @@ __global__ __launch_bounds__(256) void q8_fast_kernel(const apexw_tensor* __rest
     // never taken for a valid plan: the unit ranges hold only this kernel's tensors
     if (!apexw_q8_fast_ok(t.flags, t.block) || ((t.flags >> APEXW_FLAG_PDT_SHIFT) & 3u) != (uint32_t)PD) continue;
     if constexpr (GC) q8_set_rows(c, t, un.tensor);
+    q8_set_gains(c, t, un.tensor);
     const bool full = (int64_t)(un.unit + 1) * 2048 <= t.n;
     const bool gen = t.flags & APEXW_FLAG_GENERIC;
     if (full && !gen) q8_block_fast<PD, SR, true, false, B1HI, GC>(t, un.tensor, un.unit, c);
@@ -1441,6 +1466,7 @@ __global__ __launch_bounds__(256) void q8_step_kernel(const apexw_tensor* __rest
     const apexw_unit un = units[u];
     const apexw_tensor& t = tensors[un.tensor];
     q8_set_rows(c, t, un.tensor);
+    q8_set_gains(c, t, un.tensor);
     const uint32_t f = t.flags;
     const uint32_t pd = (f >> APEXW_FLAG_PDT_SHIFT) & 3u;
     if (f & APEXW_FLAG_FACTORED) continue;  // stepped by apexw_factored_step
@@ -1466,6 +1492,81 @@ __global__ __launch_bounds__(256) void q8_step_kernel(const apexw_tensor* __rest
       else q8_block<APEXW_F16, false, false, SINGLE>(t, un.tensor, un.unit, c);
     }
   }
+}
+
+// cautious=True: per descriptor, the number of elements whose updated first
+// moment m' = lerp(m, g', 1 - beta1) has m' g' >= 0 (the reference's mask, whose
+// mean scales the numerator: apexw/optimizer.py:4585-4588, :4672-4675, :4726-4729),
+// g' the grad as the step prepares it.  One unit per wave (a quantization block, or
+// 2048 elements of a dense row), one element per lane at a time; one atomic add of
+// the wave's count per unit.
+__global__ __launch_bounds__(256) void q8_cautious_count_kernel(const apexw_tensor* __restrict__ tensors,
+                                                                const apexw_unit* __restrict__ units,
+                                                                int64_t n_units, apexw_hparams hp_in) {
+  apexw_hparams hp = hp_in;
+  if (hp.flags & APEXW_HP_AMP) {
+    const apexw_amp_dyn d = *hp.amp;
+    if (d.skip) return;
+    hp.grad_inv_scale = d.grad_inv_scale;
+  }
+  __shared__ float s_code[16];
+  if (threadIdx.x < 16) s_code[threadIdx.x] = kNf4Code[threadIdx.x];
+  __syncthreads();
+  Q8Ctx c;
+  c.hp = &hp;
+  c.vlut = nullptr;
+  c.code = s_code;
+  c.pair = nullptr;
+  c.frac16 = nullptr;
+  c.midtab = nullptr;
+  c.coef = (hp.flags & APEXW_HP_CLIP) ? *hp.clip_coef : 1.0f;
+  c.gc_means = nullptr;
+  c.gc_rl = 0;
+  c.gain_hi = c.gain_lo = 0.0f;
+  const bool lerp_hi = hp.flags & APEXW_HP_LERP_HI;
+  const uint32_t wave = uniform(threadIdx.x >> 6);
+  const int lane = lane_id();
+  const int64_t stride = (int64_t)gridDim.x * kWaves;
+  for (int64_t u = (int64_t)blockIdx.x * kWaves + wave; u < n_units; u += stride) {
+    const apexw_unit un = units[u];
+    const apexw_tensor& t = tensors[un.tensor];
+    const uint32_t f = t.flags;
+    if (f & APEXW_FLAG_FACTORED) continue;
+    q8_set_rows(c, t, un.tensor);
+    const uint32_t pd = (f >> APEXW_FLAG_PDT_SHIFT) & 3u, md = (f >> APEXW_FLAG_MDT_SHIFT) & 3u;
+    const bool dense = f & APEXW_FLAG_DENSE, nf4 = f & APEXW_FLAG_NF4;
+    const int64_t bs = dense ? 2048 : (int64_t)t.block;
+    const int64_t start = (int64_t)un.unit * bs, end = (t.n - start) < bs ? t.n : start + bs;
+    const float ms = dense ? 0.0f : t.m_scale[un.unit];
+    uint32_t cnt = 0;
+    for (int64_t i = start + lane; i < end; i += 64) {
+      const float mean = q8_mean1(c, t, i);
+      float g;
+      if (pd == APEXW_F32) g = q8_grad<APEXW_F32>(load1<APEXW_F32>(t.g, i), f, c, mean);
+      else if (pd == APEXW_BF16) g = q8_grad<APEXW_BF16>(load1<APEXW_BF16>(t.g, i), f, c, mean);
+      else g = q8_grad<APEXW_F16>(load1<APEXW_F16>(t.g, i), f, c, mean);
+      float m;
+      if (dense) {
+        m = md == APEXW_F32 ? load1<APEXW_F32>(t.m, i)
+                            : (md == APEXW_BF16 ? load1<APEXW_BF16>(t.m, i) : load1<APEXW_F16>(t.m, i));
+      } else if (nf4) {
+        const uint32_t byte = ((const uint8_t*)t.m)[i >> 1];
+        m = c.code[(i & 1) ? (byte & 15u) : (byte >> 4)] * ms;
+      } else {
+        m = (float)((const int8_t*)t.m)[i] * ms;
+      }
+      const float mn = lerp_to(m, g, hp.lerp_coef, lerp_hi);
+      cnt += (mn * g >= 0.0f) ? 1u : 0u;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
+    if (lane == 0 && cnt) atomicAdd(&hp.counts[un.tensor], (unsigned long long)cnt);
+  }
+}
+
+__global__ __launch_bounds__(256) void counts_zero_kernel(unsigned long long* __restrict__ counts, int32_t n) {
+  const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (i < n) counts[i] = 0ull;
 }
 
 }  // namespace
@@ -1504,6 +1605,18 @@ int apexw_launch_q8(const apexw_tensor* tensors, int64_t n_units, const apexw_un
   } else {
     const int grid = apexw_resident_grid((const void*)q8_step_kernel<false>, n_units);
     hipLaunchKernelGGL(q8_step_kernel<false>, dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
+  }
+  return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
+}
+
+int apexw_launch_q8_cautious_count(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units,
+                                   int64_t n_units, const apexw_hparams* hp, hipStream_t stream) {
+  // the counters are cleared by a kernel (not hipMemsetAsync), which a captured graph replays reliably
+  hipLaunchKernelGGL(counts_zero_kernel, dim3((unsigned)((n_tensors + 255) / 256)), dim3(256), 0, stream, hp->counts,
+                     n_tensors);
+  if (n_units > 0) {
+    const int grid = apexw_resident_grid((const void*)q8_cautious_count_kernel, n_units);
+    hipLaunchKernelGGL(q8_cautious_count_kernel, dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
   }
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }

@@ -39,21 +39,27 @@ DOWNCAST_MIN_NUMEL = 1024          # optimizer.py:2100
 HOOK_MIN_NUMEL = 16384             # optimizer.py:2131
 HOOK_BATCH = 14                    # optimizer.py:2142
 
-_UNSUPPORTED_FLAGS = ("amsgrad", "cautious", "lion", "maximize",
-                      "capturable", "differentiable", "auto_pack")
-# nesterov=True runs in the precisions whose step is _step_ultra (optimizer.py:4313-4735)
+_UNSUPPORTED_FLAGS = ("amsgrad", "lion", "maximize", "capturable", "differentiable", "auto_pack")
+# nesterov=True and cautious=True run in the precisions whose step is _step_ultra
+# (optimizer.py:4313-4735)
 _NESTEROV_PRECISIONS = ("8bit", "ultra")
 
 
-def _check_nesterov(precision, factored):
-    """nesterov=True: the 8-bit and ultra steps take it (the lookahead numerator
-    lerp(g, m, beta1) without the SNR gain); the compact-kernel precisions and
-    factored second moments do not."""
-    if precision not in _NESTEROV_PRECISIONS:
-        raise NotImplementedError(f"apexw_amd: nesterov=True with precision {precision!r} "
-                                  f"(supported: {', '.join(_NESTEROV_PRECISIONS)})")
-    if factored:
-        raise NotImplementedError("apexw_amd: nesterov=True with factored_v")
+def _check_variants(precision, factored, nesterov, cautious):
+    """nesterov=True and cautious=True: the 8-bit and ultra steps take them (the
+    lookahead numerator lerp(g, m, beta1) without the SNR gain; the numerator m
+    times the sign-agreement mask over its mean); the compact-kernel precisions,
+    factored second moments and the two together do not."""
+    for name, on in (("nesterov", nesterov), ("cautious", cautious)):
+        if not on:
+            continue
+        if precision not in _NESTEROV_PRECISIONS:
+            raise NotImplementedError(f"apexw_amd: {name}=True with precision {precision!r} "
+                                      f"(supported: {', '.join(_NESTEROV_PRECISIONS)})")
+        if factored:
+            raise NotImplementedError(f"apexw_amd: {name}=True with factored_v")
+    if nesterov and cautious:
+        raise NotImplementedError("apexw_amd: nesterov=True together with cautious=True")
 
 
 class ApexW(Optimizer):
@@ -150,8 +156,8 @@ class ApexW(Optimizer):
         if bad or beta3 is not None:
             what = ", ".join(bad + (["beta3"] if beta3 is not None else []))
             raise NotImplementedError(f"apexw_amd implements the standard AdamW step; not supported: {what}")
-        if nesterov:
-            _check_nesterov(S.normalize_precision(precision), factored_v)
+        if nesterov or cautious:
+            _check_variants(S.normalize_precision(precision), factored_v, nesterov, cautious)
         if precision == "compact" and betas[1] >= 0.99 and not stochastic_rounding and not adamw_compat:
             warnings.warn(
                 f"ApexW: beta2={betas[1]} with precision='compact' and stochastic_rounding=False "
@@ -341,8 +347,9 @@ class ApexW(Optimizer):
                 self.state[p].update(S.init_state(p, group, peft, has16))
             if p.dtype == torch.float16 and self.state[p].get("is_factored_v", False):
                 raise NotImplementedError("apexw_amd: factored_v with fp16 parameters")
-        if group.get("nesterov", False):
-            _check_nesterov(group["precision"], any(self.state[p].get("is_factored_v", False) for p in params))
+        if group.get("nesterov", False) or group.get("cautious", False):
+            _check_variants(group["precision"], any(self.state[p].get("is_factored_v", False) for p in params),
+                            bool(group.get("nesterov", False)), bool(group.get("cautious", False)))
         if group["precision"] in ("8bit", "ultra"):
             # both run the reference's _step_ultra (optimizer.py:3583-3587)
             return StepPlan(self, group, params, "q8")

@@ -154,6 +154,12 @@ typedef struct apexw_unit {
 #define APEXW_HP_NESTEROV (1u << 9)    /* 8-bit / ultra steps with nesterov=True: the dense and ultra
                                           rows' numerator is lerp(g, m, beta1) instead of m (the NF4 /
                                           INT8 blocks take Nesterov through gain_hi = gain_lo = 1) */
+#define APEXW_HP_CAUTIOUS (1u << 10)   /* 8-bit / ultra steps with cautious=True: the numerator is
+                                          m' x q_t where m' g >= 0, else 0 (q_t = 1 / max(c_t / n_t,
+                                          1e-3), c_t = hparams.counts[t] written by
+                                          apexw_q8_cautious_count); the blocks take it with
+                                          look_coef = 0 under APEXW_HP_LOOK_HI (numerator m', no
+                                          lookahead) and gain_lo = 0 */
 
 /* Step scalars of one launch, written on the device by apexw_amp_prepare (32 bytes). */
 typedef struct apexw_amp_dyn {
@@ -190,7 +196,8 @@ typedef struct apexw_hparams {
   const apexw_amp_dyn* amp;  /* with APEXW_HP_AMP: this launch's device-side step scalars */
   const apexw_row_means* rows;  /* 8-bit / ultra tables with APEXW_FLAG_GC rows: one entry per
                                    descriptor of the table, else NULL */
-} apexw_hparams;          /* 104 bytes */
+  unsigned long long* counts;   /* APEXW_HP_CAUTIOUS: one counter per descriptor of the table */
+} apexw_hparams;          /* 112 bytes */
 
 /*
  * GradScaler hands the optimizer its scale and found_inf as device tensors
@@ -241,7 +248,8 @@ int apexw_check_tensor(const apexw_tensor* t, int32_t kind);
  * The scalar argument checks that a step entry point applies before it enqueues
  * anything, without enqueueing: kind APEXW_LAUNCH_COMPACT (apexw_compact_step),
  * APEXW_LAUNCH_Q8 (apexw_q8_step), APEXW_LAUNCH_ULTRA (apexw_ultra_step) or
- * APEXW_LAUNCH_FACTORED (apexw_factored_step; n_fast counts 0).  The entry points
+ * APEXW_LAUNCH_FACTORED (apexw_factored_step; n_fast counts 0) or APEXW_LAUNCH_CAUTIOUS
+ * (apexw_q8_cautious_count; n_fast counts 0).  The entry points
  * run exactly these checks, so a caller that checks every launch of a step first
  * can refuse the whole step before any parameter changes.  Replaces the
  * reference's validate-before-mutate order around step_fused_8bit
@@ -252,8 +260,22 @@ int apexw_check_tensor(const apexw_tensor* t, int32_t kind);
 #define APEXW_LAUNCH_Q8 1
 #define APEXW_LAUNCH_FACTORED 4
 #define APEXW_LAUNCH_ULTRA 5
+#define APEXW_LAUNCH_CAUTIOUS 6   /* apexw_q8_cautious_count */
 int apexw_check_launch(int32_t kind, int32_t n_tensors, int64_t n_units, int64_t n_fast_units,
                        int64_t n_fast_f32_units, const apexw_hparams* hp);
+
+/*
+ * The cautious mask's counts of one 8-bit / ultra step (cautious=True,
+ * apexw/optimizer.py:4585-4588, :4672-4675, :4726-4729): sets hp->counts[t] to
+ * the number of elements of descriptor t whose updated first moment
+ * m' = lerp(m, g', 1 - beta1) (g' the grad as the step prepares it) has
+ * m' g' >= 0, over the units given (all of the step's units).  hp as for the
+ * step that follows (its mode, flags and scalars; APEXW_HP_CAUTIOUS and counts
+ * set).  The step reads the counts in the same stream order.  No counterpart
+ * kernel in the reference, which forms the mask on the host.
+ */
+int apexw_q8_cautious_count(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,
+                            const apexw_hparams* hp, void* stream);
 
 /*
  * Compact-precision fused AdamW step over every tensor of the table in one

@@ -116,7 +116,7 @@ def flush_8bit(params, grads, states, group, K=1, amp_scale=None):
         st["_hook_mstep"] = mstep
         q8_param_step(p, g.to(p.dtype), st, lr=lr_eff, beta1=b1, beta2=b2, eps=float(group["eps"]),
                       weight_decay=wd_eff, decay_norm_only=bool(group.get("decay_norm_only", True)),
-                      step=mstep, inv_scale=inv)
+                      step=mstep, inv_scale=inv, cautious=bool(group.get("cautious", False)))
         st["step"].fill_(float((mstep - 1) // K + 1))
 
 

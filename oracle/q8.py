@@ -1,8 +1,8 @@
 """8-bit AdamW step (CPU oracle; test infrastructure only).
 
 Restates ``ApexW._step_ultra`` (``apexw/optimizer.py:4313-4735``) for
-``precision="8bit"`` with the standard update or ``nesterov=True`` (no amsgrad /
-lion / AdEMAMix / cautious), per parameter:
+``precision="8bit"`` with the standard update, ``nesterov=True`` or
+``cautious=True`` (no amsgrad / lion / AdEMAMix), per parameter:
 
 * large contiguous quantized tensors (numel > 262144) use the chunked path,
   optimizer.py:4402-4499 -- decay and update fused in fp32, one rounding of p;
@@ -19,7 +19,10 @@ The update is AdamW with the "Nesterov-SNR" lookahead gain: ``m_look =
 lerp(g, m, b1)``, gain ``1+0.2*b1`` where ``m*g >= 0`` else ``1-0.35*b1``.
 With ``nesterov=True`` the numerator is ``lerp(g, m, b1)`` without the gain in the
 quantized branches (optimizer.py:4444-4445, :4581-4582), and replaces ``m`` in the
-dense and ultra ones (:4667-4670, :4719-4724).
+dense and ultra ones (:4667-4670, :4719-4724).  With ``cautious=True`` no tensor
+takes the chunked path (:4402-4414), the numerator is ``m`` and it is multiplied
+by ``mask / mask.mean().clamp(min=1e-3)``, ``mask = num * g >= 0`` over the whole
+tensor (:4585-4588, :4672-4675, :4726-4729).
 """
 
 import math
@@ -39,7 +42,15 @@ def _bias(lr, beta1, beta2, eps, step):
     return lr * s / bc1, eps * s
 
 
-def _snr_num(m, g, beta1, nesterov=False):
+def _cautious(num, g):
+    """num * (mask / mean(mask)), mask = num * g >= 0 as float32 (optimizer.py:4585-4588)."""
+    mask = (num * g >= 0).to(torch.float32)
+    return num * (mask / mask.mean().clamp(min=1e-3))
+
+
+def _snr_num(m, g, beta1, nesterov=False, cautious=False):
+    if cautious:
+        return _cautious(m, g)
     if nesterov:
         return torch.lerp(g, m, beta1)
     gain_hi = 1.0 + 0.20 * beta1
@@ -49,7 +60,7 @@ def _snr_num(m, g, beta1, nesterov=False):
 
 
 def q8_param_step(p, g, st, *, lr, beta1, beta2, eps, weight_decay, decay_norm_only, step, inv_scale=None,
-                  nesterov=False):
+                  nesterov=False, cautious=False):
     """Update one parameter and its state in place.  ``step`` is already incremented."""
     step_size, eps_scaled = _bias(lr, beta1, beta2, eps, step)
     decay = max(1.0 - lr * weight_decay, 0.0) if weight_decay != 0 else 1.0
@@ -62,9 +73,10 @@ def q8_param_step(p, g, st, *, lr, beta1, beta2, eps, weight_decay, decay_norm_o
                         wd_factor=decay if apply_wd else None, inv_scale=inv_scale, sanitize=True)
         return
     if st.get("is_ultra", False):
-        _ultra(p, g, st, beta1, beta2, step_size, eps_scaled, decay if apply_wd else None, sr, inv_scale, nesterov)
+        _ultra(p, g, st, beta1, beta2, step_size, eps_scaled, decay if apply_wd else None, sr, inv_scale, nesterov,
+               cautious)
         return
-    if st.get("is_8bit", False) and n > CHUNK and p.is_contiguous():
+    if st.get("is_8bit", False) and n > CHUNK and p.is_contiguous() and not cautious:
         _chunked(p, g, st, beta1, beta2, eps, step_size, eps_scaled, decay if apply_wd else None, sr, inv_scale,
                  nesterov)
         return
@@ -95,7 +107,7 @@ def q8_param_step(p, g, st, *, lr, beta1, beta2, eps, weight_decay, decay_norm_o
             v.mul_(beta2).addcmul_(gf, gf, value=1.0 - beta2)
             v.nan_to_num_(nan=0.0, posinf=0.0, neginf=0.0)
             den = v.sqrt().add_(eps_scaled).clamp_min_(eps)
-        num = _snr_num(m, gf, beta1, nesterov)
+        num = _snr_num(m, gf, beta1, nesterov, cautious)
         if p.dtype == torch.float32:
             p.addcdiv_(num, den, value=-step_size)
         else:
@@ -122,6 +134,8 @@ def q8_param_step(p, g, st, *, lr, beta1, beta2, eps, weight_decay, decay_norm_o
     v.copy_(vf.to(v.dtype))
     den = vf.sqrt().add_(eps_scaled)
     num = torch.lerp(gf, mf, beta1) if nesterov else mf
+    if cautious:
+        num = _cautious(num, gf)
     upd = (num / den).mul_(step_size)
     p.sub_(upd.to(p.dtype))
 
@@ -188,7 +202,7 @@ def _chunked(p, g, st, beta1, beta2, eps, step_size, eps_scaled, decay, sr, inv_
         sv.copy_(s2)
 
 
-def _ultra(p, g, st, beta1, beta2, step_size, eps_scaled, decay, sr, inv_scale, nesterov=False):
+def _ultra(p, g, st, beta1, beta2, step_size, eps_scaled, decay, sr, inv_scale, nesterov=False, cautious=False):
     """optimizer.py:4500-4511, :4640-4686: INT8 m (block ``ultra_block_size``,
     EMA-max scales), dense v rounded to its dtype once, the denominator from the
     unrounded fp32 v, p decayed then ``p -= update.to(p.dtype)``."""
@@ -205,6 +219,8 @@ def _ultra(p, g, st, beta1, beta2, step_size, eps_scaled, decay, sr, inv_scale, 
     v.copy_(vf.to(v.dtype))
     den = vf.sqrt().add_(eps_scaled)
     num = torch.lerp(gf, m, beta1) if nesterov else m
+    if cautious:
+        num = _cautious(num, gf)
     upd = (num / den).mul_(step_size)
     p.sub_(upd.to(p.dtype))
     q, s = Q.quant_int8(m, bs, st["exp_avg_scales"], sr)

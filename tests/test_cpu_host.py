@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 def test_struct_layouts_match_header():
     from apexw_amd import _lib
     assert ctypes.sizeof(_lib.Tensor) == 64 == _lib.TENSOR_DTYPE.itemsize
-    assert ctypes.sizeof(_lib.HParams) == 104
+    assert ctypes.sizeof(_lib.HParams) == 112
     assert _lib.GEMM_PROBLEM_DTYPE.itemsize == 120
     assert ctypes.sizeof(_lib.StateLayout) == 56
 
@@ -172,6 +172,12 @@ def test_constructor_contract():
             ApexW(p, precision=prec, nesterov=True)
     with pytest.raises(NotImplementedError):
         ApexW(p, precision="8bit", nesterov=True, factored_v=True)
+    # cautious: the same precisions, not with factored second moments nor with nesterov
+    assert ApexW(p, precision="8bit", cautious=True).defaults["cautious"]
+    assert ApexW(p, precision="ultra", cautious=True).defaults["cautious"]
+    for kw in (dict(precision="compact"), dict(precision="8bit", factored_v=True), dict(precision="8bit", nesterov=True)):
+        with pytest.raises(NotImplementedError):
+            ApexW(p, cautious=True, **kw)
     for prec, betas in (("full", (0.9, 0.999)), ("fp32", (0.9, 0.999)), ("auto", (0.9, 0.99)),
                         ("smart", (0.9, 0.99)), ("ultra", (0.9, 0.99)), ("3byte", (0.9, 0.99))):
         o = ApexW(p, precision=prec)
@@ -298,6 +304,6 @@ def test_integration_binding_loads():
     from integration_binding import load_binding
     rx = load_binding()
     assert callable(rx.step_fused) and callable(rx.step_fused_8bit)
-    assert ctypes.sizeof(rx.HParams) == 104 and ctypes.sizeof(rx.Tensor) == 64 and ctypes.sizeof(rx.Unit) == 8
+    assert ctypes.sizeof(rx.HParams) == 112 and ctypes.sizeof(rx.Tensor) == 64 and ctypes.sizeof(rx.Unit) == 8
     p = torch.zeros(4)          # CPU tensors: not handled, nothing written
     assert rx.step_fused([p], [p], [p], [p], 1e-3, 0.9, 0.999, 1e-8, 0.0) is False

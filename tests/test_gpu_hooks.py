@@ -96,11 +96,16 @@ def _compare(params, opt, cpu, hooked_states, oracle_rest, hooked, tag, only=Non
             cpu[p].copy_(p.detach().cpu())
 
 
-def test_backward_steps_match_oracle():
+@pytest.mark.parametrize("cautious", [False, True], ids=["plain", "cautious"])
+def test_backward_steps_match_oracle(cautious):
+    """cautious=True: the in-backward batches take the mask too (the reference's flush
+    passes it to _step_ultra, apexw/optimizer.py:2359)."""
     _need_gpu()
     from oracle import hooks as H
-    print("hooks: K=1, 3 iterations", flush=True)
-    model, params, opt, cpu, hooked, rest, oracle_rest, group, captured = _setup(0)
+    print(f"hooks: K=1, 3 iterations, cautious={cautious}", flush=True)
+    kw = dict(cautious=True) if cautious else {}
+    model, params, opt, cpu, hooked, rest, oracle_rest, group, captured = _setup(0, **kw)
+    group = dict(group, **kw)
     states = {}
     for it in range(3):
         captured.clear()

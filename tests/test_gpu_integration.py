@@ -6,7 +6,8 @@ reference's ``apexw.cuda_extension`` signatures) then step state laid out as
 the reference lays it out, and the results are held to the CPU oracle at the
 parity bars of test_gpu_configs.py: the compact call against the cold foreach
 step (``_multi_tensor_step``), the 8-bit call against ``_step_ultra`` per
-tensor (chunked order above 262,144 elements, generic below), SR off.
+tensor (chunked order above 262,144 elements, generic below; every tensor
+generic with cautious=True), SR off.
 """
 
 import pytest
@@ -79,10 +80,11 @@ def test_binding_step_fused_matches_oracle(dtype):
         gs = [g * 0.7 for g in gs]
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_binding_step_fused_8bit_matches_oracle(dtype):
+@pytest.mark.parametrize("dtype,cautious", [(torch.bfloat16, False), (torch.float32, False), (torch.bfloat16, True),
+                                            (torch.float32, True)])
+def test_binding_step_fused_8bit_matches_oracle(dtype, cautious):
     _need_gpu()
-    print(f"binding step_fused_8bit {dtype}", flush=True)
+    print(f"binding step_fused_8bit {dtype} cautious={cautious}", flush=True)
     rx = load_binding()
     shapes = [(512, 1024), (256, 256), (4096,), (3000,), (100, 300), (70,)]
     ps, gs, sts = _setup(shapes, dtype, "8bit", 6)
@@ -92,16 +94,16 @@ def test_binding_step_fused_8bit_matches_oracle(dtype):
     ok = rx.step_fused_8bit(dp, [g.cuda() for g in gs], [d["exp_avg"] for d in dst],
                             [d["exp_avg_scales"] for d in dst], [d["exp_avg_sq"] for d in dst],
                             [d["exp_avg_sq_scales"] for d in dst], [st["block_size_8bit"] for st in sts],
-                            step=1, decay_norm_only=True, stochastic=False, **KW)
+                            step=1, decay_norm_only=True, stochastic=False, cautious=cautious, **KW)
     assert ok
     prev = [p.clone() for p in ps]
     for p, g, st in zip(ps, gs, sts):
         OQ.q8_param_step(p, g, st, lr=KW["lr"], beta1=KW["beta1"], beta2=KW["beta2"], eps=KW["eps"],
-                         weight_decay=KW["weight_decay"], decay_norm_only=True, step=1)
+                         weight_decay=KW["weight_decay"], decay_norm_only=True, step=1, cautious=cautious)
     torch.cuda.synchronize()
     for i in range(len(shapes)):
         what = f"tensor {i} {shapes[i]}"
-        generic = dtype == torch.bfloat16 and ps[i].numel() <= OQ.CHUNK
+        generic = dtype == torch.bfloat16 and (ps[i].numel() <= OQ.CHUNK or cautious)
         _cmp_p(dp[i], ps[i], prev[i], f"{what} p", 2.0 ** -7 if generic else 2.0 ** -22)
         for k in keys:
             kind = "#nf4" if (k == "exp_avg" and sts[i].get("is_4bit_m")) else ""

@@ -91,6 +91,9 @@ class StepPlan:
         self.gc = bool(group.get("grad_centralization", False))
         # cautious=True (8-bit / ultra): a count pass forms the mask's mean before the step
         self.cautious = self._cautious_of(group)
+        # maximize=True (8-bit / ultra; not the in-backward flush nor the per-parameter update,
+        # which step without it): the grads are negated through a negative unscale factor
+        self.maximize = self._maximize_of(group)
         self.d_counts = None
         self.cold_done = False
         self._nesterov = False
@@ -103,6 +106,9 @@ class StepPlan:
         steps, not enable_fused_backward's per-parameter update (which has no
         cautious branch, optimizer.py:2373-2471)."""
         return bool(group.get("cautious", False)) and self.kind == "q8" and not self.single
+
+    def _maximize_of(self, group):
+        return bool(group.get("maximize", False)) and self.kind == "q8" and not self.hooked
 
     # ------------------------------------------------------------------ validity
     def valid_for(self, group):
@@ -118,7 +124,7 @@ class StepPlan:
             return False
         if bool(group.get("grad_centralization", False)) != self.gc:
             return False
-        if self._cautious_of(group) != self.cautious:
+        if self._cautious_of(group) != self.cautious or self._maximize_of(group) != self.maximize:
             return False
         self._scan_status = self._scan()
         return self._scan_status in (SCAN_SAME, SCAN_GRADS_MOVED, SCAN_SLOW)
@@ -494,7 +500,7 @@ class StepPlan:
         # by apexw_grad_prepare and the step launches then carry no AMP scalars, so they
         # could not skip an inf / NaN step: such plans read found_inf on the host
         return not (self.hooked or self.single or self.factored.any() or self.vscaled.any()
-                    or (self.gc and not self.gc_fold))
+                    or (self.gc and not self.gc_fold) or self.maximize)
 
     def amp_fold(self, sync=False):
         """Subtract from the step counters the steps GradScaler skipped that the host
@@ -661,6 +667,10 @@ class StepPlan:
         keep = self._refresh_grads()      # contiguous copies of non-contiguous grads, alive until the launch
         if amp is not None:
             inv_scale = 1.0          # a stand-in: the kernels read the factor from the device scalars
+        elif self.maximize:
+            # maximize: g -> -g, through the unscale factor (exact, and it commutes with
+            # nan_to_num, the clip, centralization and AMP's unscale: optimizer.py:4502-4503)
+            inv_scale = -(1.0 if inv_scale is None else inv_scale)
         (b1, b2), eps = group["betas"], group["eps"]
         lr = group["lr"] if lr is None else lr
         wd = group["weight_decay"] if wd is None else wd

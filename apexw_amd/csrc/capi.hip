@@ -96,7 +96,7 @@ bool hp_ok(const apexw_hparams* hp) {
     // device-side AMP scalars: the compact and 8-bit step modes, with the unscale they carry
     if (!hp->amp || ((uintptr_t)hp->amp & 15u) || hp->mode == APEXW_MODE_SINGLE) return false;
     if (!(hp->flags & APEXW_HP_UNSCALE)) return false;
-  } else if ((hp->flags & APEXW_HP_UNSCALE) && !(hp->grad_inv_scale > 0.0f)) {
+  } else if ((hp->flags & APEXW_HP_UNSCALE) && !apexw_inv_scale_ok(hp->grad_inv_scale)) {
     return false;
   }
   return true;
@@ -540,7 +540,7 @@ int apexw_grad_clip_coef(const apexw_tensor* tensors, int32_t n_tensors, const a
                          const apexw_row_means* rows, void* stream) {
   if (!tensors || !units || !unit_begin || !unit_partial || !tensor_norm || !coef) return APEXW_ERR_ARG;
   if (n_tensors <= 0 || n_units < 0 || unit_size < 0 || !(clip > 0.0f)) return APEXW_ERR_ARG;
-  if ((flags & APEXW_HP_UNSCALE) && !amp && !(grad_inv_scale > 0.0f)) return APEXW_ERR_ARG;
+  if ((flags & APEXW_HP_UNSCALE) && !amp && !apexw_inv_scale_ok(grad_inv_scale)) return APEXW_ERR_ARG;
   return apexw_launch_clip(tensors, n_tensors, units, n_units, unit_size, unit_begin, unit_partial, tensor_norm, clip,
                            grad_inv_scale, flags, coef, amp, rows, (hipStream_t)stream);
 }
@@ -578,7 +578,7 @@ int apexw_grad_prepare(const apexw_grad_prep* preps, int32_t n_preps, const apex
                        float grad_inv_scale, uint32_t flags, const apexw_amp_dyn* amp, void* stream) {
   if (!preps || !units || n_preps <= 0 || n_units < 0) return APEXW_ERR_ARG;
   if (flags & ~(APEXW_HP_SANITIZE | APEXW_HP_UNSCALE)) return APEXW_ERR_ARG;
-  if ((flags & APEXW_HP_UNSCALE) && !amp && !(grad_inv_scale > 0.0f)) return APEXW_ERR_ARG;
+  if ((flags & APEXW_HP_UNSCALE) && !amp && !apexw_inv_scale_ok(grad_inv_scale)) return APEXW_ERR_ARG;
   return apexw_launch_grad_prep(preps, units, n_units, grad_inv_scale, flags, amp, (hipStream_t)stream);
 }
 
@@ -586,7 +586,7 @@ int apexw_grad_row_means(const apexw_grad_prep* preps, int32_t n_preps, const ap
                          float grad_inv_scale, uint32_t flags, const apexw_amp_dyn* amp, void* stream) {
   if (!preps || !units || n_preps <= 0 || n_units < 0) return APEXW_ERR_ARG;
   if (flags & ~(APEXW_HP_SANITIZE | APEXW_HP_UNSCALE)) return APEXW_ERR_ARG;
-  if ((flags & APEXW_HP_UNSCALE) && !amp && !(grad_inv_scale > 0.0f)) return APEXW_ERR_ARG;
+  if ((flags & APEXW_HP_UNSCALE) && !amp && !apexw_inv_scale_ok(grad_inv_scale)) return APEXW_ERR_ARG;
   return apexw_launch_row_means(preps, units, n_units, grad_inv_scale, flags, amp, (hipStream_t)stream);
 }
 

@@ -194,5 +194,9 @@ APEXW_DEV int lane_id() { return (int)(threadIdx.x & 63u); }
 // Grid for a 256-thread (4-wave) kernel that strides over `n_units` work units,
 // one unit per wave: at most 16 workgroups per resident slot (blocks per CU from
 // the kernel's occupancy on the current device).
+// An AMP unscale factor the kernels take: finite and non-zero (negative with
+// maximize=True, which negates the grads: exact, and commutes with every other
+// grad preparation step).
+inline bool apexw_inv_scale_ok(float x) { return x == x && x != 0.0f && x - x == 0.0f; }
 int apexw_resident_grid(const void* kernel, int64_t n_units);
 APEXW_DEV uint32_t uniform(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }

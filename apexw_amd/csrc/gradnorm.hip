@@ -397,7 +397,7 @@ extern "C" int apexw_grad_clip_coef_noalloc(const apexw_tensor* tensors, int32_t
                                             const apexw_amp_dyn* amp, void* stream) {
   if (!tensors || !units || !unit_begin || !coef) return APEXW_ERR_ARG;
   if (n_tensors <= 0 || n_units < 0 || unit_size < 0 || !(clip > 0.0f)) return APEXW_ERR_ARG;
-  if ((flags & APEXW_HP_UNSCALE) && !amp && !(grad_inv_scale > 0.0f)) return APEXW_ERR_ARG;
+  if ((flags & APEXW_HP_UNSCALE) && !amp && !apexw_inv_scale_ok(grad_inv_scale)) return APEXW_ERR_ARG;
   if (n_units > APEXW_NOALLOC_CLIP_MAX_UNITS || n_tensors > APEXW_NOALLOC_CLIP_MAX_TENSORS) return APEXW_ERR_SIZE;
   // the array of the GPU the kernels run on: the stream's device (the null stream is
   // the current device's)

@@ -39,18 +39,19 @@ DOWNCAST_MIN_NUMEL = 1024          # optimizer.py:2100
 HOOK_MIN_NUMEL = 16384             # optimizer.py:2131
 HOOK_BATCH = 14                    # optimizer.py:2142
 
-_UNSUPPORTED_FLAGS = ("amsgrad", "lion", "maximize", "capturable", "differentiable", "auto_pack")
-# nesterov=True and cautious=True run in the precisions whose step is _step_ultra
-# (optimizer.py:4313-4735)
+_UNSUPPORTED_FLAGS = ("amsgrad", "lion", "capturable", "differentiable", "auto_pack")
+# nesterov=True, cautious=True and maximize=True run in the precisions whose step is
+# _step_ultra (optimizer.py:4313-4735)
 _NESTEROV_PRECISIONS = ("8bit", "ultra")
 
 
-def _check_variants(precision, factored, nesterov, cautious):
-    """nesterov=True and cautious=True: the 8-bit and ultra steps take them (the
-    lookahead numerator lerp(g, m, beta1) without the SNR gain; the numerator m
-    times the sign-agreement mask over its mean); the compact-kernel precisions,
-    factored second moments and the two together do not."""
-    for name, on in (("nesterov", nesterov), ("cautious", cautious)):
+def _check_variants(precision, factored, nesterov, cautious, maximize=False):
+    """nesterov=True, cautious=True and maximize=True: the 8-bit and ultra steps take
+    them (the lookahead numerator lerp(g, m, beta1) without the SNR gain; the
+    numerator m times the sign-agreement mask over its mean; the negated grads);
+    the compact-kernel precisions, factored second moments, and nesterov together
+    with cautious do not."""
+    for name, on in (("nesterov", nesterov), ("cautious", cautious), ("maximize", maximize)):
         if not on:
             continue
         if precision not in _NESTEROV_PRECISIONS:
@@ -156,8 +157,8 @@ class ApexW(Optimizer):
         if bad or beta3 is not None:
             what = ", ".join(bad + (["beta3"] if beta3 is not None else []))
             raise NotImplementedError(f"apexw_amd implements the standard AdamW step; not supported: {what}")
-        if nesterov or cautious:
-            _check_variants(S.normalize_precision(precision), factored_v, nesterov, cautious)
+        if nesterov or cautious or maximize:
+            _check_variants(S.normalize_precision(precision), factored_v, nesterov, cautious, maximize)
         if precision == "compact" and betas[1] >= 0.99 and not stochastic_rounding and not adamw_compat:
             warnings.warn(
                 f"ApexW: beta2={betas[1]} with precision='compact' and stochastic_rounding=False "
@@ -347,9 +348,10 @@ class ApexW(Optimizer):
                 self.state[p].update(S.init_state(p, group, peft, has16))
             if p.dtype == torch.float16 and self.state[p].get("is_factored_v", False):
                 raise NotImplementedError("apexw_amd: factored_v with fp16 parameters")
-        if group.get("nesterov", False) or group.get("cautious", False):
+        if group.get("nesterov", False) or group.get("cautious", False) or group.get("maximize", False):
             _check_variants(group["precision"], any(self.state[p].get("is_factored_v", False) for p in params),
-                            bool(group.get("nesterov", False)), bool(group.get("cautious", False)))
+                            bool(group.get("nesterov", False)), bool(group.get("cautious", False)),
+                            bool(group.get("maximize", False)))
         if group["precision"] in ("8bit", "ultra"):
             # both run the reference's _step_ultra (optimizer.py:3583-3587)
             return StepPlan(self, group, params, "q8")
@@ -429,7 +431,7 @@ class ApexW(Optimizer):
         models (optimizer.py:2059-2167)."""
         d = self.defaults
         if not force and (d.get("clip_grad_norm") is not None or d.get("grad_centralization", False)
-                          or d.get("nesterov", False)):
+                          or d.get("nesterov", False) or d.get("maximize", False)):
             return
         trainable = []
         total = 0

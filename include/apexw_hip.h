@@ -192,7 +192,8 @@ typedef struct apexw_hparams {
   uint32_t step;
   uint32_t mode;
   uint32_t flags;
-  float grad_inv_scale; /* with APEXW_HP_UNSCALE: 1 / AMP grad scale (GradScaler) */
+  float grad_inv_scale; /* with APEXW_HP_UNSCALE: 1 / AMP grad scale (GradScaler); negated for
+                           maximize=True (the grads are negated too; finite, non-zero) */
   const apexw_amp_dyn* amp;  /* with APEXW_HP_AMP: this launch's device-side step scalars */
   const apexw_row_means* rows;  /* 8-bit / ultra tables with APEXW_FLAG_GC rows: one entry per
                                    descriptor of the table, else NULL */

@@ -67,7 +67,7 @@ class OracleApexW:
                  adamw_compat=False, clip_grad_norm=None, precision="compact", stochastic_rounding=True,
                  block_size=None, force_compact_v=False, int4_m=None, grad_centralization=False,
                  factored_v=False, six_bit=False, threshold=65536, amp=None, dynamic_scaling=True, nesterov=False,
-                 cautious=False):
+                 cautious=False, maximize=False):
         precision = normalize_precision(precision)
         if betas is None:
             betas = (0.9, 0.999) if precision in ("8bit", "full") else (0.9, 0.99)
@@ -82,9 +82,9 @@ class OracleApexW:
                           block_size=block_size, force_compact_v=force_compact_v, int4_m=int4_m,
                           grad_centralization=grad_centralization, factored_v=factored_v, six_bit=six_bit,
                           threshold=threshold, amp=amp, dynamic_scaling=dynamic_scaling, nesterov=bool(nesterov),
-                          cautious=bool(cautious), params=self.params)
-        if (nesterov or cautious) and precision not in ("8bit", "ultra"):
-            raise NotImplementedError("oracle: nesterov / cautious restate the _step_ultra precisions only")
+                          cautious=bool(cautious), maximize=bool(maximize), params=self.params)
+        if (nesterov or cautious or maximize) and precision not in ("8bit", "ultra"):
+            raise NotImplementedError("oracle: nesterov / cautious / maximize restate the _step_ultra precisions only")
         self.state = {}
         self._plan = None
         self.grad_scale = None
@@ -166,7 +166,7 @@ class OracleApexW:
                 st = self.state[p]
                 st["step"].add_(1)
                 q8_param_step(p, g, st, step=st["step"].item(), inv_scale=self._inv(scale), nesterov=grp["nesterov"],
-                              cautious=grp["cautious"], **kw)
+                              cautious=grp["cautious"], maximize=grp["maximize"], **kw)
             self._plan = {"kind": "8bit", "params": plist}
             return
         sts = [self.state[p] for p in plist]
@@ -233,7 +233,7 @@ class OracleApexW:
                 st = self.state[p]
                 st["step"].add_(1)
                 q8_param_step(p, g, st, step=st["step"].item(), inv_scale=self._inv(scale), nesterov=grp["nesterov"],
-                              cautious=grp["cautious"], **kw)
+                              cautious=grp["cautious"], maximize=grp["maximize"], **kw)
             return
         grads, scale = self._prepare(grads, sanitize=grp["clip_grad_norm"] is not None)
         sts = [self.state[p] for p in plist]

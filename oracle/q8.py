@@ -1,8 +1,8 @@
 """8-bit AdamW step (CPU oracle; test infrastructure only).
 
 Restates ``ApexW._step_ultra`` (``apexw/optimizer.py:4313-4735``) for
-``precision="8bit"`` with the standard update, ``nesterov=True`` or
-``cautious=True`` (no amsgrad / lion / AdEMAMix), per parameter:
+``precision="8bit"`` with the standard update, ``nesterov=True``,
+``cautious=True`` or ``maximize=True`` (no amsgrad / lion / AdEMAMix), per parameter:
 
 * large contiguous quantized tensors (numel > 262144) use the chunked path,
   optimizer.py:4402-4499 -- decay and update fused in fp32, one rounding of p;
@@ -60,8 +60,14 @@ def _snr_num(m, g, beta1, nesterov=False, cautious=False):
 
 
 def q8_param_step(p, g, st, *, lr, beta1, beta2, eps, weight_decay, decay_norm_only, step, inv_scale=None,
-                  nesterov=False, cautious=False):
-    """Update one parameter and its state in place.  ``step`` is already incremented."""
+                  nesterov=False, cautious=False, maximize=False):
+    """Update one parameter and its state in place.  ``step`` is already incremented.
+    maximize: the grad is negated after nan_to_num, before the unscale
+    (optimizer.py:4500-4505; state.py:341-346 in the chunked order)."""
+    if maximize:
+        # negation is exact and commutes with nan_to_num's +-65504 and the unscale, so the
+        # grads can be negated once here for every branch below
+        g = -g
     step_size, eps_scaled = _bias(lr, beta1, beta2, eps, step)
     decay = max(1.0 - lr * weight_decay, 0.0) if weight_decay != 0 else 1.0
     apply_wd = weight_decay != 0 and (not decay_norm_only or p.dim() >= 2)

@@ -43,6 +43,9 @@ CASES = [
     ("compact foreach fp32", [(256, 128), (1000,)], torch.float32, dict(precision="compact", adamw_compat=True)),
     ("8bit chunked + generic", [(1024, 512), (4096,)], torch.bfloat16, dict(precision="8bit")),
     ("8bit fp32", [(2048, 256), (100,)], torch.float32, dict(precision="8bit")),
+    # maximize: the negative unscale factor carries both (GradScaler read on the host)
+    ("8bit maximize", [(1024, 512), (4096,), (40,)], torch.bfloat16, dict(precision="8bit", maximize=True)),
+    ("8bit cautious", [(1024, 512), (4096,), (40,)], torch.bfloat16, dict(precision="8bit", cautious=True)),
 ]
 
 
@@ -98,6 +101,40 @@ def test_grad_scale_with_clip_equals_unscaled_step(name, shapes, dtype, kw):
         for k, v in oa.state[a].items():
             if torch.is_tensor(v):
                 assert torch.equal(v, ob.state[b][k]), (name, k)
+
+
+@pytest.mark.parametrize("precision,extra", [("8bit", {}), ("8bit", dict(clip_grad_norm=1e-3)),
+                                             ("8bit", dict(grad_centralization=True, clip_grad_norm=1e-3)),
+                                             ("ultra", dict(threshold=4096, clip_grad_norm=1e-3))],
+                         ids=["8bit", "8bit-clip", "8bit-gc-clip", "ultra-clip"])
+def test_maximize_equals_negated_grads(precision, extra):
+    """maximize=True on grads g steps exactly as maximize=False on -g (the
+    reference negates the grads after nan_to_num, and negation commutes with the
+    clip, centralization and AMP's unscale): bit-identical parameters and states,
+    with a GradScaler scale of 2^10 on every step."""
+    _need_gpu()
+    from apexw_amd import ApexW
+    print(f"maximize {precision} {extra}", flush=True)
+    kw = dict(lr=1e-3, weight_decay=0.1, precision=precision, stochastic_rounding=False, **extra)
+    gen = torch.Generator().manual_seed(5)
+    shapes = [(1024, 512), (256, 128), (4096,), (40,)]
+    host = [(torch.randn(s, generator=gen) * 0.02).bfloat16() for s in shapes]
+    pa = [torch.nn.Parameter(h.cuda()) for h in host]
+    pb = [torch.nn.Parameter(h.cuda()) for h in host]
+    oa, ob = ApexW(pa, maximize=True, **kw), ApexW(pb, **kw)
+    for _ in range(3):
+        for a, b in zip(pa, pb):
+            g = (torch.randn(a.shape, generator=gen) * 1e-3 * SCALE).bfloat16()
+            a.grad, b.grad = g.cuda(), (-g).cuda()
+        for o in (oa, ob):
+            o.grad_scale, o.found_inf = torch.tensor(SCALE, device="cuda"), torch.zeros((), device="cuda")
+            o.step()
+    torch.cuda.synchronize()
+    for a, b in zip(pa, pb):
+        assert torch.equal(a, b)
+        for k, v in oa.state[a].items():
+            if torch.is_tensor(v):
+                assert torch.equal(v, ob.state[b][k]), k
 
 
 def _model(seed):

@@ -154,7 +154,9 @@ def make_params(cfg, device, seed=0):
 
 
 PROFILE_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
-TRAFFIC_FILES = {"c3": "q8_fast_kernel_llama3_8b_traffic.md"}
+# measured HBM bytes per launch: the default line's step kernel (c3) and the C4 step
+# kernel of hbm_extra ("c4_step"; the clip's norm pass is not in that figure)
+TRAFFIC_FILES = {"c3": "q8_fast_kernel_llama3_8b_traffic.md", "c4_step": "compact_step_kernel_c4_ragged_clip.md"}
 
 
 def measured_traffic(cfg_name):
@@ -293,7 +295,7 @@ def hbm_extra(cfg_name, steps=10, warmup=3):
     kern_bytes = state_bytes(opt, params, 1)
     achieved = kern_bytes / (kern_ms * 1e-3) / 1e9
     out = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-           "traffic": None, "kernel": "compact_step_kernel", "kernel_ms": kern_ms, "bytes_per_launch": kern_bytes,
+           "traffic": measured_traffic(cfg_name + "_step"), "kernel": "compact_step_kernel", "kernel_ms": kern_ms, "bytes_per_launch": kern_bytes,
            "step_ms": step_ms, "step_bytes": step_bytes, "step_gbs": step_bytes / (step_ms * 1e-3) / 1e9,
            "params": sum(p.numel() for p in params), "tensors": len(params), "workload": cfg["workload"]}
     del opt, params

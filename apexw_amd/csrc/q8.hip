@@ -592,18 +592,41 @@ template <int PD> struct FastRaw {
   float ms_old, vs_old;
 };
 
+// Block-uniform byte pointers of one 2048-element block (scalar registers: the
+// tensor descriptor is read with scalar loads).  Element e = start + o of the
+// block is addressed as base + 32-bit lane offset, so each access is one
+// SGPR-base + VGPR-offset (+ immediate) instruction with no 64-bit VALU address
+// arithmetic.
+// The lane's offset passes through an empty asm statement in each block so the
+// compiler does not hoist its 64-bit extension out of the unit loop (the
+// SGPR-base form needs the 32-bit offset in the block that uses it).
+template <int PD> struct FastBase {
+  char* p;
+  const char* g;
+  uint8_t* m;
+  uint8_t* v;
+  uint32_t lane8;   // 8 * lane: the lane's first element in each 512-element group
+  __device__ __forceinline__ FastBase(const apexw_tensor& t, int64_t start)
+      : p((char*)t.p + start * Elem<PD>::bytes), g((const char*)t.g + start * Elem<PD>::bytes),
+        m((uint8_t*)t.m + (start >> 1)), v((uint8_t*)t.v + (start >> 2)), lane8((uint32_t)lane_id() * 8u) {
+    asm volatile("" : "+v"(lane8));
+  }
+};
+
 template <int PD, bool FULL>
 APEXW_DEV void q8_fast_load(const apexw_tensor& t, uint32_t blk, FastRaw<PD>& r) {
   constexpr int PW = FastRaw<PD>::PW;
   const int lane = lane_id();
   const int64_t start = (int64_t)blk * 2048;
+  const FastBase<PD> fb(t, start);
   r.ms_old = t.m_scale[blk];
   r.vs_old = t.v_scale[blk];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int64_t e = start + k * 512 + lane * 8;
-    const auto pp = APEXW_GLOBAL(const u32x4, (const char*)t.p + e * Elem<PD>::bytes);
-    const auto gp = APEXW_GLOBAL(const u32x4, (const char*)t.g + e * Elem<PD>::bytes);
+    const uint32_t o = (uint32_t)(k * 512) + fb.lane8;   // element offset within the block
+    const auto pp = APEXW_GLOBAL(const u32x4, fb.p + o * Elem<PD>::bytes);
+    const auto gp = APEXW_GLOBAL(const u32x4, fb.g + o * Elem<PD>::bytes);
     if constexpr (FULL) {
       r.cnt[k] = 8;
 #pragma unroll
@@ -611,8 +634,8 @@ APEXW_DEV void q8_fast_load(const apexw_tensor& t, uint32_t blk, FastRaw<PD>& r)
         r.pw[k][h] = __builtin_nontemporal_load(pp + h);
         r.gw[k][h] = __builtin_nontemporal_load(gp + h);
       }
-      r.mw[k] = __builtin_nontemporal_load(APEXW_GLOBAL(const uint32_t, (const uint8_t*)t.m + (e >> 1)));
-      r.vw[k] = __builtin_nontemporal_load(APEXW_GLOBAL(const uint16_t, (const uint8_t*)t.v + (e >> 2)));
+      r.mw[k] = __builtin_nontemporal_load(APEXW_GLOBAL(const uint32_t, fb.m + (o >> 1)));
+      r.vw[k] = __builtin_nontemporal_load(APEXW_GLOBAL(const uint16_t, fb.v + (o >> 2)));
     } else {
       // numel % 4 == 0 for quad-v tensors, so a lane holds 0, 4 or 8 elements
       r.cnt[k] = e >= t.n ? 0 : (t.n - e >= 8 ? 8 : 4);
@@ -623,19 +646,19 @@ APEXW_DEV void q8_fast_load(const apexw_tensor& t, uint32_t blk, FastRaw<PD>& r)
       if (r.cnt[k] == 8) {
 #pragma unroll
         for (int h = 0; h < PW; ++h) { r.pw[k][h] = pp[h]; r.gw[k][h] = gp[h]; }
-        r.mw[k] = *APEXW_GLOBAL(const uint32_t, (const uint8_t*)t.m + (e >> 1));
-        r.vw[k] = *APEXW_GLOBAL(const uint16_t, (const uint8_t*)t.v + (e >> 2));
+        r.mw[k] = *APEXW_GLOBAL(const uint32_t, fb.m + (o >> 1));
+        r.vw[k] = *APEXW_GLOBAL(const uint16_t, fb.v + (o >> 2));
       } else if (r.cnt[k] == 4) {
         if constexpr (PD == APEXW_F32) {
           r.pw[k][0] = pp[0];
           r.gw[k][0] = gp[0];
         } else {
-          const u32x2 a = *APEXW_GLOBAL(const u32x2, (const uint16_t*)t.p + e);
-          const u32x2 b = *APEXW_GLOBAL(const u32x2, (const uint16_t*)t.g + e);
+          const u32x2 a = *APEXW_GLOBAL(const u32x2, fb.p + o * 2u);
+          const u32x2 b = *APEXW_GLOBAL(const u32x2, fb.g + o * 2u);
           r.pw[k][0].x = a.x; r.pw[k][0].y = a.y; r.gw[k][0].x = b.x; r.gw[k][0].y = b.y;
         }
-        r.mw[k] = 0x77770000u | *APEXW_GLOBAL(const uint16_t, (const uint8_t*)t.m + (e >> 1));
-        r.vw[k] = *APEXW_GLOBAL(const uint8_t, (const uint8_t*)t.v + (e >> 2));
+        r.mw[k] = 0x77770000u | *APEXW_GLOBAL(const uint16_t, fb.m + (o >> 1));
+        r.vw[k] = *APEXW_GLOBAL(const uint8_t, fb.v + (o >> 2));
       }
     }
   }
@@ -652,6 +675,7 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
   const uint32_t hf = hp.flags, tf = t.flags;
   const int lane = lane_id();
   const int64_t start = (int64_t)blk * 2048;
+  const FastBase<PD> fb(t, start);
   const float ms_old = r.ms_old;
   const float vs_old = r.vs_old;
   const float decay = (tf & APEXW_FLAG_WD) ? hp.wd_factor : 1.0f;
@@ -677,6 +701,10 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
   // rather than held in registers across the passes
   float mnew[4][8], vq[4][2];
   float amax = 0.0f, vmax = 0.0f;
+  // SR path constants: (1 - b2) / 4 (exact), b2 * vs_old, and the step size times
+  // each SNR gain
+  const float omb2_q = hp.one_minus_beta2 * 0.25f, vsb2 = vs_old * hp.beta2;
+  const float sg_hi = hp.step_size * c.gain_hi, sg_lo = hp.step_size * c.gain_lo;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     float p[8], g[8], m[8];
@@ -771,13 +799,14 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         const int b = 4 * q;
-        const float vold = c.vlut[(vw[k] >> (8 * q)) & 0xFFu] * vs_old;
-        float vv = fmaf(hp.one_minus_beta2, s2[q] * 0.25f, vold * hp.beta2);
+        // v' = b2 v + (1 - b2) mean4(g^2) with the block's b2 * vs_old and (1 - b2) / 4
+        // folded into constants (within an fp32 ulp of the two-product form; SR only)
+        float vv = fmaf(omb2_q, s2[q], c.vlut[(vw[k] >> (8 * q)) & 0xFFu] * vsb2);
         if (!(fabsf(vv) <= 3.402823466e38f)) vv = 0.0f;
         vq[k][q] = vv;
         if (FULL || 4 * q < cnt[k]) vmax = fmaxf(vmax, vv);
-        const float r = __builtin_amdgcn_rcpf(fmaxf(__builtin_amdgcn_sqrtf(vv) + hp.eps_scaled, hp.eps)) * hp.step_size;
-        float r_hi = r * c.gain_hi, r_lo = r * c.gain_lo;
+        const float r = __builtin_amdgcn_rcpf(fmaxf(__builtin_amdgcn_sqrtf(vv) + hp.eps_scaled, hp.eps));
+        float r_hi = r * sg_hi, r_lo = r * sg_lo;
         // keep the two products per quad: otherwise the compiler sinks them below the
         // per-element select, one multiply per element instead of two per quad
         asm volatile("" : "+v"(r_hi), "+v"(r_lo));
@@ -836,7 +865,7 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
         for (int i = 0; i < 4; ++i) upd[b + i] = div_shared(num[b + i], den, rden) * hp.step_size;
       }
     }
-    const int64_t e = start + k * 512 + lane * 8;
+    const uint32_t o = (uint32_t)(k * 512) + fb.lane8;   // element offset within the block
     if constexpr (PD == APEXW_F32) {
       // fp32 parameters: p * decay - update in fp32 (both rounding orders agree), no SR
       float x[8];
@@ -844,7 +873,7 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
       for (int j = 0; j < 8; ++j) x[j] = p[j] * decay - upd[j];
       const u32x4 lo = {__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]), __float_as_uint(x[3])};
       const u32x4 hi = {__float_as_uint(x[4]), __float_as_uint(x[5]), __float_as_uint(x[6]), __float_as_uint(x[7])};
-      const auto dst = APEXW_GLOBAL(u32x4, (float*)t.p + e);
+      const auto dst = APEXW_GLOBAL(u32x4, fb.p + o * 4u);
       if constexpr (FULL) {
         __builtin_nontemporal_store(lo, dst);
         __builtin_nontemporal_store(hi, dst + 1);
@@ -892,12 +921,12 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
     }
     u32x4 po = {pout[0], pout[1], pout[2], pout[3]};
     if constexpr (FULL) {
-      __builtin_nontemporal_store(po, APEXW_GLOBAL(u32x4, (uint16_t*)t.p + e));
+      __builtin_nontemporal_store(po, APEXW_GLOBAL(u32x4, fb.p + o * 2u));
     } else if (cnt[k] == 8) {
-      *APEXW_GLOBAL(u32x4, (uint16_t*)t.p + e) = po;
+      *APEXW_GLOBAL(u32x4, fb.p + o * 2u) = po;
     } else if (cnt[k] == 4) {
       u32x2 p2 = {po.x, po.y};
-      *APEXW_GLOBAL(u32x2, (uint16_t*)t.p + e) = p2;
+      *APEXW_GLOBAL(u32x2, fb.p + o * 2u) = p2;
     }
     }
 #pragma unroll
@@ -922,7 +951,7 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
   const float rms_rn = rcp_refined(ms), rvs_rn = rcp_refined(vs);
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const int64_t e = start + k * 512 + lane * 8;
+    const uint32_t o = (uint32_t)(k * 512) + fb.lane8;   // element offset within the block
     uint32_t w = 0;
     uint32_t hw[4];   // pair b: bits 0-11 / 16-27 NF4 noise, bits 12-15 / 28-31 v noise
     if constexpr (SR) {
@@ -942,7 +971,10 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
           // y = x + 3 for x = m / scale in (-1, 1): the top 7 mantissa bits of y in
           // [2, 4) are the bucket; the table is affine in y
           const float y = fmaf(mnew[k][2 * b + i], rms_sr, 3.0f);
-          const float4 fr = c.frac16[(__float_as_uint(y) >> 16) & 127u];
+          // byte 2 of y: its exponent bit (bit 23) is 0 in [2, 4), so this is the
+          // 7-bit bucket, read with one byte-select shift (the table has 256 entries,
+          // the upper half a copy, so any byte stays inside it)
+          const float4 fr = c.frac16[(__float_as_uint(y) >> 16) & 255u];
           gc[i] = (uint32_t)fabsf(fminf(fmaf(fr.y, y, fr.x), fmaf(fr.w, y, fr.z)));
         }
         // two 16-bit lanes of G + r12 (r12 = bits 0-11 of the element's word):
@@ -983,15 +1015,14 @@ APEXW_DEV void q8_fast_compute(const apexw_tensor& t, uint32_t tix, uint32_t blk
       }
     }
     if constexpr (FULL) {
-      __builtin_nontemporal_store(w, APEXW_GLOBAL(uint32_t, (uint8_t*)t.m + (e >> 1)));
-      __builtin_nontemporal_store((uint16_t)(vc[0] | (vc[1] << 8)),
-                                  APEXW_GLOBAL(uint16_t, (uint8_t*)t.v + (e >> 2)));
+      __builtin_nontemporal_store(w, APEXW_GLOBAL(uint32_t, fb.m + (o >> 1)));
+      __builtin_nontemporal_store((uint16_t)(vc[0] | (vc[1] << 8)), APEXW_GLOBAL(uint16_t, fb.v + (o >> 2)));
     } else if (cnt[k] == 8) {
-      *APEXW_GLOBAL(uint32_t, (uint8_t*)t.m + (e >> 1)) = w;
-      *APEXW_GLOBAL(uint16_t, (uint8_t*)t.v + (e >> 2)) = (uint16_t)(vc[0] | (vc[1] << 8));
+      *APEXW_GLOBAL(uint32_t, fb.m + (o >> 1)) = w;
+      *APEXW_GLOBAL(uint16_t, fb.v + (o >> 2)) = (uint16_t)(vc[0] | (vc[1] << 8));
     } else if (cnt[k] == 4) {
-      *APEXW_GLOBAL(uint16_t, (uint8_t*)t.m + (e >> 1)) = (uint16_t)(w & 0xFFFFu);
-      *APEXW_GLOBAL(uint8_t, (uint8_t*)t.v + (e >> 2)) = (uint8_t)vc[0];
+      *APEXW_GLOBAL(uint16_t, fb.m + (o >> 1)) = (uint16_t)(w & 0xFFFFu);
+      *APEXW_GLOBAL(uint8_t, fb.v + (o >> 2)) = (uint8_t)vc[0];
     }
   }
 }
@@ -1389,14 +1420,16 @@ __global__ __launch_bounds__(256) void q8_fast_kernel(const apexw_tensor* __rest
   }
   __shared__ float s_vlut[256];
   __shared__ float2 s_pair[256];
-  __shared__ float4 s_frac16[128];
+  __shared__ float4 s_frac16[256];   // 128 buckets, then a copy of them
   __shared__ float2 s_midtab[64];
   s_vlut[threadIdx.x] = kVLogLut[threadIdx.x];
   if (threadIdx.x < 64) s_midtab[threadIdx.x] = make_float2(kNf4MidTab[2 * threadIdx.x], kNf4MidTab[2 * threadIdx.x + 1]);
   s_pair[threadIdx.x] = make_float2(kNf4Pair[2 * threadIdx.x], kNf4Pair[2 * threadIdx.x + 1]);
-  if (threadIdx.x < 128)
-    s_frac16[threadIdx.x] = make_float4(kNf4Code16[4 * threadIdx.x], kNf4Code16[4 * threadIdx.x + 1],
-                                        kNf4Code16[4 * threadIdx.x + 2], kNf4Code16[4 * threadIdx.x + 3]);
+  {
+    const int f = threadIdx.x & 127;
+    s_frac16[threadIdx.x] = make_float4(kNf4Code16[4 * f], kNf4Code16[4 * f + 1], kNf4Code16[4 * f + 2],
+                                        kNf4Code16[4 * f + 3]);
+  }
   __syncthreads();
   Q8Ctx c;
   c.hp = &hp;

@@ -13,7 +13,7 @@ import numpy as np
 
 from ._build import LIB_PATH
 
-ABI_VERSION = 20
+ABI_VERSION = 21
 
 # dtype codes
 F32, BF16, F16, U8, I8 = 0, 1, 2, 3, 4
@@ -139,8 +139,9 @@ FV_SUM_COLS = 1
 FV_BAND_ROWS = 32
 FV_UNIT_RANGES = 6   # (bf16, fp32 parameters) x (INT8, 6-bit, bf16 m)
 
-GEMM_SYM, GEMM_B_KN, GEMM_ADD_B, GEMM_APPLY, GEMM_APPLY_T, GEMM_APPLY_WD = 1, 2, 4, 8, 16, 32
-GEMM_OUT_C, GEMM_OUT_CT, GEMM_ADD, GEMM_KIND_NN = 1, 2, 4, 8
+GEMM_SYM, GEMM_B_KN, GEMM_ADD_B, GEMM_APPLY, GEMM_APPLY_T, GEMM_APPLY_WD, GEMM_PANEL = 1, 2, 4, 8, 16, 32, 64
+GEMM_OUT_C, GEMM_OUT_CT, GEMM_ADD, GEMM_KIND_NN, GEMM_KIND_PANEL = 1, 2, 4, 8, 16
+LAYOUT_ROWS, LAYOUT_PANEL = 0, 1   # Newton-Schulz work matrices: row-major or 32 x 32 panels
 GEMM_MAX_PROBLEMS = 256
 GEMM_QUEUES = 8
 
@@ -172,8 +173,8 @@ SIGNATURES = {
     "apexw_gemm_nt_grouped": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, _vp, _vp]),
     "apexw_muon_workspace_floats": (ctypes.c_int64, [_i64, _i64]),
     "apexw_muon_prepare": (ctypes.c_int, [_vp, _vp, _i32, _i64, _i64, _f32, _f32, _i32, _f32, _f32, _vp, _vp, _i64,
-                                          _i64, _vp, _vp, _vp]),
-    "apexw_muon_apply": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _i64, _i32, _f32, _i32, _f32, _vp, _vp]),
+                                          _i64, _i32, _vp, _vp, _vp]),
+    "apexw_muon_apply": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _i64, _i32, _i32, _f32, _i32, _f32, _vp, _vp]),
     "apexw_factored_layout": (ctypes.c_int64, [_vp, _i32, ctypes.POINTER(ctypes.c_int64),
                                                ctypes.POINTER(ctypes.c_int64)]),
     "apexw_factored_step": (ctypes.c_int, [_vp, _i32, _vp, _i32, _i64, _i64, _vp, _i64, _vp, _vp, _HP, _vp]),

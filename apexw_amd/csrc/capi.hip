@@ -37,8 +37,8 @@ int apexw_launch_row_means(const apexw_grad_prep*, const apexw_unit*, int64_t, f
 int apexw_launch_gemm_grouped(const apexw_gemm_problem*, const uint32_t*, const int32_t*, int32_t, int32_t,
                               const apexw_amp_dyn*, hipStream_t);
 int apexw_launch_muon_prepare(float*, const void*, int32_t, int64_t, int64_t, float, float, int32_t, float, float,
-                              uint16_t*, uint16_t*, int64_t, int64_t, float*, const apexw_amp_dyn*, hipStream_t);
-int apexw_launch_muon_apply(void*, int32_t, const uint16_t*, int64_t, int64_t, int64_t, int32_t, float, int32_t,
+                              uint16_t*, uint16_t*, int64_t, int64_t, bool, float*, const apexw_amp_dyn*, hipStream_t);
+int apexw_launch_muon_apply(void*, int32_t, const uint16_t*, int64_t, int64_t, int64_t, bool, int32_t, float, int32_t,
                             float, const apexw_amp_dyn*, hipStream_t);
 bool apexw_q8_flags_ok(uint32_t flags, uint32_t block, int64_t n);
 int apexw_launch_factored(const apexw_tensor*, const apexw_fv_tensor*, int32_t, int64_t, int64_t, const apexw_unit*,
@@ -306,7 +306,7 @@ int gemm_problem_kind(const apexw_gemm_problem& p) {
   const bool add = p.beta != 0.0f;
   if (!p.a || !p.b || (!p.c && !p.ct && !apply)) return -APEXW_ERR_ARG;
   constexpr uint32_t kKnown = APEXW_GEMM_SYM | APEXW_GEMM_B_KN | APEXW_GEMM_ADD_B | APEXW_GEMM_APPLY |
-                              APEXW_GEMM_APPLY_T | APEXW_GEMM_APPLY_WD;
+                              APEXW_GEMM_APPLY_T | APEXW_GEMM_APPLY_WD | APEXW_GEMM_PANEL;
   if ((p.flags & ~kKnown) || p.reserved || p.reserved2) return -APEXW_ERR_ARG;
   if (apply) {
     // the X' product only; p covered by O
@@ -330,9 +330,10 @@ int gemm_problem_kind(const apexw_gemm_problem& p) {
       (read_e && p.lde < p.m))
     return -APEXW_ERR_ARG;
   const int32_t lds[5] = {p.lda, p.ldb, read_e ? p.lde : 0, p.c ? p.ldc : 0, p.ct ? p.ldct : 0};
+  const int32_t ld_align = (p.flags & APEXW_GEMM_PANEL) ? 31 : 7;
   for (int32_t ld : lds) {
     if (ld > APEXW_GEMM_MAX_LD) return -APEXW_ERR_ARG;
-    if (ld & 7) return -APEXW_ERR_ALIGN;
+    if (ld & ld_align) return -APEXW_ERR_ALIGN;
   }
   const uintptr_t al = (uintptr_t)p.a | (uintptr_t)p.b | (uintptr_t)(read_e ? p.et : nullptr) | (uintptr_t)p.c |
                        (uintptr_t)p.ct;
@@ -342,7 +343,7 @@ int gemm_problem_kind(const apexw_gemm_problem& p) {
   }
   // the applied update goes through the row-major epilogue (writing c too when given)
   return (p.c || apply ? APEXW_GEMM_OUT_C : 0) | (p.ct ? APEXW_GEMM_OUT_CT : 0) | (add ? APEXW_GEMM_ADD : 0) |
-         (kn ? APEXW_GEMM_KIND_NN : 0);
+         (kn ? APEXW_GEMM_KIND_NN : 0) | ((p.flags & APEXW_GEMM_PANEL) ? APEXW_GEMM_KIND_PANEL : 0);
 }
 
 int64_t gemm_problem_tiles(const apexw_gemm_problem& p) {
@@ -487,7 +488,7 @@ int apexw_gemm_nt_grouped(const apexw_gemm_problem* problems, const uint32_t* it
   if (!problems || !items || !queue_offsets) return APEXW_ERR_ARG;
   if ((uintptr_t)amp & 15u) return APEXW_ERR_ALIGN;
   if (n_workgroups <= 0 || n_workgroups % APEXW_GEMM_QUEUES) return APEXW_ERR_ARG;
-  if (kind <= 0 || kind > 15 || !(kind & (APEXW_GEMM_OUT_C | APEXW_GEMM_OUT_CT))) return APEXW_ERR_ARG;
+  if (kind <= 0 || kind > 31 || !(kind & (APEXW_GEMM_OUT_C | APEXW_GEMM_OUT_CT))) return APEXW_ERR_ARG;
   if ((kind & APEXW_GEMM_KIND_NN) && (kind & APEXW_GEMM_OUT_CT)) return APEXW_ERR_ARG;
   if (((uintptr_t)problems | (uintptr_t)items | (uintptr_t)queue_offsets) & 3u) return APEXW_ERR_ALIGN;
   return apexw_launch_gemm_grouped(problems, items, queue_offsets, n_workgroups, kind, amp, (hipStream_t)stream);
@@ -499,27 +500,33 @@ int64_t apexw_muon_workspace_floats(int64_t rows, int64_t cols) {
 
 int apexw_muon_prepare(float* buf, const void* g, int32_t g_dtype, int64_t rows, int64_t cols, float mu,
                        float one_minus_mu, int32_t nesterov, float eps, float grad_inv_scale, void* x, void* xt,
-                       int64_t ldx, int64_t ldxt, float* workspace, const apexw_amp_dyn* amp, void* stream) {
+                       int64_t ldx, int64_t ldxt, int32_t layout, float* workspace, const apexw_amp_dyn* amp,
+                       void* stream) {
   if (!buf || !g || !x || !workspace || rows <= 0 || cols <= 0) return APEXW_ERR_ARG;
   if ((uintptr_t)amp & 15u) return APEXW_ERR_ALIGN;
   if (g_dtype != APEXW_F32 && g_dtype != APEXW_BF16 && g_dtype != APEXW_F16) return APEXW_ERR_DTYPE;
+  if (layout != APEXW_LAYOUT_ROWS && layout != APEXW_LAYOUT_PANEL) return APEXW_ERR_ARG;
   // work matrix X is [min x max], X^T is [max x min] (optional)
   const int64_t lo = rows < cols ? rows : cols, hi = rows < cols ? cols : rows;
   if (ldx < hi || (xt && ldxt < lo)) return APEXW_ERR_ARG;
+  if (layout == APEXW_LAYOUT_PANEL && ((ldx & 31) || (xt && (ldxt & 31)))) return APEXW_ERR_ALIGN;
   if (!amp && !(grad_inv_scale > 0.0f)) return APEXW_ERR_ARG;
   return apexw_launch_muon_prepare(buf, g, g_dtype, rows, cols, mu, one_minus_mu, nesterov, eps, grad_inv_scale,
-                                   (uint16_t*)x, (uint16_t*)xt, ldx, ldxt, workspace, amp, (hipStream_t)stream);
+                                   (uint16_t*)x, (uint16_t*)xt, ldx, ldxt, layout == APEXW_LAYOUT_PANEL, workspace,
+                                   amp, (hipStream_t)stream);
 }
 
 int apexw_muon_apply(void* p, int32_t p_dtype, const void* u, int64_t rows, int64_t cols, int64_t ldu,
-                     int32_t u_transposed, float wd_factor, int32_t apply_wd, float neg_lr_eff,
+                     int32_t layout, int32_t u_transposed, float wd_factor, int32_t apply_wd, float neg_lr_eff,
                      const apexw_amp_dyn* amp, void* stream) {
   if ((uintptr_t)amp & 15u) return APEXW_ERR_ALIGN;
   if (!p || !u || rows <= 0 || cols <= 0 || ldu < (u_transposed ? rows : cols)) return APEXW_ERR_ARG;
+  if (layout != APEXW_LAYOUT_ROWS && layout != APEXW_LAYOUT_PANEL) return APEXW_ERR_ARG;
+  if (layout == APEXW_LAYOUT_PANEL && (ldu & 31)) return APEXW_ERR_ALIGN;
   if ((rows + 63) / 64 > 65535) return APEXW_ERR_ARG;   // grid y of the transposing kernel
   if (p_dtype != APEXW_F32 && p_dtype != APEXW_BF16 && p_dtype != APEXW_F16) return APEXW_ERR_DTYPE;
-  return apexw_launch_muon_apply(p, p_dtype, (const uint16_t*)u, rows, cols, ldu, u_transposed != 0, wd_factor,
-                                 apply_wd, neg_lr_eff, amp, (hipStream_t)stream);
+  return apexw_launch_muon_apply(p, p_dtype, (const uint16_t*)u, rows, cols, ldu, layout == APEXW_LAYOUT_PANEL,
+                                 u_transposed != 0, wd_factor, apply_wd, neg_lr_eff, amp, (hipStream_t)stream);
 }
 
 int apexw_muon_coordwise(float* buf, const void* g, int32_t g_dtype, void* p, int32_t p_dtype, int64_t n, float mu,

@@ -34,6 +34,20 @@ constexpr int kBM = 256, kBN = 256;
 constexpr int kBK = 32, kStages = 5;
 APEXW_DEV int lds_off(int row, int chunk) { return row * kBK + ((chunk ^ ((row >> 2) & 3)) << 3); }
 
+// Element offset of (r, c) in a matrix with ld columns, row-major or in 32 x 32
+// panels (APEXW_GEMM_PANEL: panel (r / 32, c / 32) is 1024 contiguous elements,
+// row-major inside, panels in row-major order).  For r and c multiples of 32 the
+// offsets of the two layouts differ only in the column term, and offsets add:
+// poff(r0 + r, c0 + c) = poff(r0, c0) + poff(r, c).
+APEXW_DEV uint32_t poff(int r, int c, int ld, bool panel) {
+  return panel ? (uint32_t)((r >> 5) * 32 * ld + ((c >> 5) << 10) + ((r & 31) << 5) + (c & 31))
+               : (uint32_t)(r * ld + c);
+}
+// the same for whole matrices (64-bit offsets)
+APEXW_DEV int64_t poff64(int64_t r, int64_t c, int64_t ld, bool panel) {
+  return panel ? (r >> 5) * 32 * ld + ((c >> 5) << 10) + ((r & 31) << 5) + (c & 31) : r * ld + c;
+}
+
 struct GemmArgs {
   const uint16_t* a;   // [M x K] row-major, ld lda
   const uint16_t* b;   // [N x K] row-major, ld ldb
@@ -171,11 +185,12 @@ APEXW_DEV void apply_run(const ApplyArgs& ap, int64_t i, const float (&u)[8], in
 // beta E with extra MFMAs against a one-hot fragment holding beta on the
 // diagonal (beta split into two bf16 parts, hi + lo, within 2^-18 of beta), so
 // the epilogue reads no addend.
-template <bool kC, bool kCt, bool kAdd, bool kNN, bool kHalf>
+template <bool kC, bool kCt, bool kAdd, bool kNN, bool kHalf, bool kPanel>
 APEXW_DEV void gemm_tile(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, int32_t lda, int32_t ldb,
                          int32_t k, const uint16_t* __restrict__ Et, int32_t lde, uint16_t* __restrict__ C,
                          int32_t ldc, uint16_t* __restrict__ Ct, int32_t ldct, bool write_ct, float alpha,
                          float beta, int32_t diag_k0, const ApplyArgs& ap, LdsStage* lds) {
+  constexpr bool panel = kPanel;   // operands and outputs in 32 x 32 panels (APEXW_GEMM_PANEL)
   constexpr int kWM = kHalf ? 64 : 128;   // rows of a wave's block
   constexpr int kFA = kWM / 32;           // A fragments (32-row blocks) per wave and k-step
   constexpr int kACopies = kWM / 32;      // A copy instructions per wave and stage (16 rows each, 4 waves)
@@ -192,20 +207,22 @@ APEXW_DEV void gemm_tile(const uint16_t* __restrict__ A, const uint16_t* __restr
   // chunk (L % 32) ^ (4 (row % 4)) (so the transposing reads of 4 consecutive
   // rows hit distinct banks).  A stage is 16 instructions for B and 16 (8 with
   // kHalf) for A; wave w issues q = kACopies w .. of A and 4 w .. 4 w + 3 of B.
+  // With panels a [rows x K] stage of 16 rows is 1 KB of one panel, contiguous,
+  // and a [K x N] stage row band is 8 consecutive panels: full 128-byte lines.
   uint32_t goff[kCopies];
 #pragma unroll
   for (int i = 0; i < kACopies; ++i) {
     const int row = 16 * (kACopies * wave + i) + (lane >> 2), chunk = (lane & 3) ^ ((lane >> 4) & 3);
-    goff[i] = (uint32_t)(row * lda + chunk * 8) * 2u;
+    goff[i] = poff(row, chunk * 8, lda, panel) * 2u;
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     if constexpr (kNN) {
       const int krow = 2 * (4 * wave + i) + (lane >> 5), nchunk = (lane & 31) ^ (4 * (krow & 3));
-      goff[kACopies + i] = (uint32_t)(krow * ldb + nchunk * 8) * 2u;
+      goff[kACopies + i] = poff(krow, nchunk * 8, ldb, panel) * 2u;
     } else {
       const int row = 16 * (4 * wave + i) + (lane >> 2), chunk = (lane & 3) ^ ((lane >> 4) & 3);
-      goff[kACopies + i] = (uint32_t)(row * ldb + chunk * 8) * 2u;
+      goff[kACopies + i] = poff(row, chunk * 8, ldb, panel) * 2u;
     }
   }
   // LDS byte addresses of this wave's first A and B chunks in stage 0 (wave-uniform)
@@ -214,11 +231,15 @@ APEXW_DEV void gemm_tile(const uint16_t* __restrict__ A, const uint16_t* __restr
   constexpr uint32_t kStageBytes = sizeof(LdsStage), kChunk = 1024;
   const uint16_t* A_s = uniform_ptr(A);
   const uint16_t* B_s = uniform_ptr(B);
+  // elements from one K stage to the next along a [rows x K] operand: the next
+  // 32 columns, or the next panel; a [K x N] operand moves 32 rows in both layouts
+  const int kstep = panel ? 1024 : kBK;
   // copy i (0 .. kCopies - 1) of stage h: A chunks, then B chunks 0..3
   auto copy = [&](int h, int i) {
     const uint32_t st = (uint32_t)(h % kStages) * kStageBytes;
-    if (i < kACopies) lds_copy16(ldsA0 + st + i * kChunk, goff[i], A_s + h * kBK);
-    else lds_copy16(ldsB0 + st + (i - kACopies) * kChunk, goff[i], B_s + (kNN ? (int64_t)h * kBK * ldb : h * kBK));
+    if (i < kACopies) lds_copy16(ldsA0 + st + i * kChunk, goff[i], A_s + (int64_t)h * kstep);
+    else lds_copy16(ldsB0 + st + (i - kACopies) * kChunk, goff[i],
+                    B_s + (kNN ? (int64_t)h * kBK * ldb : (int64_t)h * kstep));
   };
 
   f32x16 acc[kFA][4];
@@ -380,7 +401,7 @@ APEXW_DEV void gemm_tile(const uint16_t* __restrict__ A, const uint16_t* __restr
         for (int r = 0; r < 4; ++r) v[r] = alpha * acc[a][b][q * 4 + r];
         if constexpr (kAdd) {
           if (!diag) {
-            const u16x4 e = *APEXW_GLOBAL(const u16x4, Et + (uint32_t)((gj0 + b * 32) * lde + gi0 + a * 32 + q * 8));
+            const u16x4 e = *APEXW_GLOBAL(const u16x4, Et + poff(gj0 + b * 32, gi0 + a * 32 + q * 8, lde, panel));
 #pragma unroll
             for (int r = 0; r < 4; ++r) v[r] = fmaf(beta, bf(e[r]), v[r]);
           }
@@ -431,18 +452,16 @@ APEXW_DEV void gemm_tile(const uint16_t* __restrict__ A, const uint16_t* __restr
       else upd(std::integral_constant<int, APEXW_F16>());
     }
     if (C) {
-      uint16_t* __restrict__ Cw = C + (int64_t)(wm * kWM) * ldc + wn * 128;
 #pragma unroll 4
       for (int it = 0; it < kWM / 4; ++it) {
         const int c = it * 64 + lane, r = c >> 4, c16 = c & 15;
         const u32x4 v = *(const u32x4*)&stage[swz(r, c16 * 8)];
-        __builtin_nontemporal_store(v, APEXW_GLOBAL(u32x4, Cw + (uint32_t)(r * ldc + c16 * 8)));
+        __builtin_nontemporal_store(v, APEXW_GLOBAL(u32x4, C + poff(wm * kWM + r, wn * 128 + c16 * 8, ldc, panel)));
       }
     }
   }
   if constexpr (kCt) {
     if (write_ct) {
-      uint16_t* __restrict__ Ctw = Ct + (int64_t)(wn * 128) * ldct + wm * kWM;
       constexpr int kPerRow = kWM / 8;   // 16-byte chunks per Ct row of the block
 #pragma unroll 2
       for (int it = 0; it < kWM / 4; ++it) {
@@ -452,7 +471,7 @@ APEXW_DEV void gemm_tile(const uint16_t* __restrict__ A, const uint16_t* __restr
 #pragma unroll
         for (int t = 0; t < 4; ++t)
           v[t] = (uint32_t)stage[swz(il + 2 * t, jl)] | ((uint32_t)stage[swz(il + 2 * t + 1, jl)] << 16);
-        *APEXW_GLOBAL(u32x4, Ctw + (uint32_t)(jl * ldct + il)) = v;
+        *APEXW_GLOBAL(u32x4, Ct + poff(wn * 128 + jl, wm * kWM + il, ldct, panel)) = v;
       }
     }
   }
@@ -478,11 +497,11 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmArgs g) {
 
   const int64_t batch = blockIdx.y;
   const int64_t row0 = (int64_t)tm * kBM, col0 = (int64_t)tn * kBN;
-  gemm_tile<kC, kCt, kAdd, false, false>(g.a + batch * g.sa + row0 * g.lda, g.b + batch * g.sb + col0 * g.ldb, g.lda, g.ldb, g.k,
-                           kAdd ? g.et + batch * g.se + col0 * g.lde + row0 : nullptr, g.lde,
-                           kC ? g.c + batch * g.sc + row0 * g.ldc + col0 : nullptr, g.ldc,
-                           kCt ? g.ct + batch * g.sct + col0 * g.ldct + row0 : nullptr, g.ldct, true, g.alpha, g.beta,
-                           -1, ApplyArgs{}, lds);
+  gemm_tile<kC, kCt, kAdd, false, false, false>(
+      g.a + batch * g.sa + row0 * g.lda, g.b + batch * g.sb + col0 * g.ldb, g.lda, g.ldb, g.k,
+      kAdd ? g.et + batch * g.se + col0 * g.lde + row0 : nullptr, g.lde,
+      kC ? g.c + batch * g.sc + row0 * g.ldc + col0 : nullptr, g.ldc,
+      kCt ? g.ct + batch * g.sct + col0 * g.ldct + row0 : nullptr, g.ldct, true, g.alpha, g.beta, -1, ApplyArgs{}, lds);
 }
 
 // Grouped GEMM: every problem of a launch (different shapes, K and operands)
@@ -500,7 +519,7 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmArgs g) {
 // transposed store (ct == c).
 constexpr int kQueues = APEXW_GEMM_QUEUES;
 
-template <bool kC, bool kCt, bool kAdd, bool kNN>
+template <bool kC, bool kCt, bool kAdd, bool kNN, bool kPanel>
 __global__ __launch_bounds__(256, 1) void gemm_nt_grouped_kernel(const apexw_gemm_problem* __restrict__ probs,
                                                                  const uint32_t* __restrict__ items,
                                                                  const int32_t* __restrict__ queue_offsets,
@@ -519,11 +538,14 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_grouped_kernel(const apexw_gem
   // APEXW_GEMM_ADD_B: the addend is the B operand read at K = row0 + i,
   // accumulated on the matrix cores (validated: alpha == 1, m <= k, no et)
   const bool diag = kAdd && (p.flags & APEXW_GEMM_ADD_B);
+  // tile origins are multiples of 32: with panels only the column term of a
+  // base offset changes (column c0 starts panel column c0 / 32, c0 * 32 elements in)
+  const int64_t cs = kPanel ? 32 : 1;
   const uint16_t* A = (const uint16_t*)p.a + row0 * p.lda;
-  const uint16_t* B = (const uint16_t*)p.b + (kNN ? col0 : col0 * p.ldb);
-  const uint16_t* Et = kAdd && !diag ? (const uint16_t*)p.et + col0 * p.lde + row0 : nullptr;
-  uint16_t* C = kC && p.c ? (uint16_t*)p.c + row0 * p.ldc + col0 : nullptr;
-  uint16_t* Ct = kCt ? (uint16_t*)p.ct + col0 * p.ldct + row0 : nullptr;
+  const uint16_t* B = (const uint16_t*)p.b + (kNN ? col0 * cs : col0 * p.ldb);
+  const uint16_t* Et = kAdd && !diag ? (const uint16_t*)p.et + col0 * p.lde + row0 * cs : nullptr;
+  uint16_t* C = kC && p.c ? (uint16_t*)p.c + row0 * p.ldc + col0 * cs : nullptr;
+  uint16_t* Ct = kCt ? (uint16_t*)p.ct + col0 * p.ldct + row0 * cs : nullptr;
   const int32_t dk = diag ? (int32_t)row0 : -1;
   ApplyArgs ap{};
   if (kC && (p.flags & APEXW_GEMM_APPLY)) {
@@ -540,11 +562,11 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_grouped_kernel(const apexw_gem
     ap.vec = p.p_cols % 8 == 0 && ((uintptr_t)p.p & 15u) == 0;
   }
   if (part)
-    gemm_tile<kC, kCt, kAdd, kNN, true>(A, B, p.lda, p.ldb, p.k, Et, p.lde, C, p.ldc, Ct, p.ldct, mirror, p.alpha,
-                                        p.beta, dk, ap, lds);
+    gemm_tile<kC, kCt, kAdd, kNN, true, kPanel>(A, B, p.lda, p.ldb, p.k, Et, p.lde, C, p.ldc, Ct, p.ldct, mirror,
+                                                p.alpha, p.beta, dk, ap, lds);
   else
-    gemm_tile<kC, kCt, kAdd, kNN, false>(A, B, p.lda, p.ldb, p.k, Et, p.lde, C, p.ldc, Ct, p.ldct, mirror, p.alpha,
-                                         p.beta, dk, ap, lds);
+    gemm_tile<kC, kCt, kAdd, kNN, false, kPanel>(A, B, p.lda, p.ldb, p.k, Et, p.lde, C, p.ldc, Ct, p.ldct, mirror,
+                                                 p.alpha, p.beta, dk, ap, lds);
 }
 
 // ---------------------------------------------------------------------------
@@ -616,15 +638,16 @@ __global__ __launch_bounds__(256) void muon_momentum_kernel(float* __restrict__ 
 
 // X = bf16(bf16(buf) / d) with d = bf16(bf16(||bf16(buf)||_F) + eps) (the bf16
 // torch ops of zeropower_via_newtonschulz5), written as the work matrix in both
-// layouts.  The work matrix is buf itself when rows <= cols, else buf^T.
-// 64 x 64 tiles through LDS so both layouts are written with coalesced rows.
+// orientations.  The work matrix is buf itself when rows <= cols, else buf^T.
+// 64 x 64 tiles through LDS so both are written along their rows; panel: the
+// outputs are stored in 32 x 32 panels (the grouped GEMM's APEXW_GEMM_PANEL).
 template <int GD>
 __global__ __launch_bounds__(256) void muon_normalize_kernel(const float* __restrict__ buf, const void* __restrict__ grad,
                                                              int64_t rows, int64_t cols, float mu, int nesterov,
                                                              float inv, const float* __restrict__ partial, int n_partial,
                                                              float eps, int tall, uint16_t* __restrict__ x,
                                                              uint16_t* __restrict__ xt, int64_t ldx, int64_t ldxt,
-                                                             const apexw_amp_dyn* __restrict__ amp) {
+                                                             bool panel, const apexw_amp_dyn* __restrict__ amp) {
   __shared__ float red[4];
   __shared__ uint16_t tile[64][66];
   if (amp) {
@@ -662,19 +685,21 @@ __global__ __launch_bounds__(256) void muon_normalize_kernel(const float* __rest
     const int r = e >> 6, cidx = e & 63;
     // direct[tr + r][tc + cidx] = D(tr + r, tc + cidx); trans[tc + r][tr + cidx] = D(tr + cidx, tc + r)
     if (direct && tr + r < rows && tc + cidx < cols)
-      APEXW_GLOBAL(uint16_t, direct)[(tr + r) * ld_direct + tc + cidx] = tile[r][cidx];
+      APEXW_GLOBAL(uint16_t, direct)[poff64(tr + r, tc + cidx, ld_direct, panel)] = tile[r][cidx];
     if (trans && tc + r < cols && tr + cidx < rows)
-      APEXW_GLOBAL(uint16_t, trans)[(tc + r) * ld_trans + tr + cidx] = tile[cidx][r];
+      APEXW_GLOBAL(uint16_t, trans)[poff64(tc + r, tr + cidx, ld_trans, panel)] = tile[cidx][r];
   }
 }
 
 // p = round(round(p * (1 - lr*wd)) + (-lr_eff) * U)   (p.mul_ then p.add_(U, alpha)),
 // U read from the NS output in p's [rows x cols] layout (bf16, leading dim ldu).
 // VEC: cols % 8 == 0 and 16-byte aligned p / u rows: 8 elements of one row per thread.
+// panel: U stored in 32 x 32 panels (APEXW_GEMM_PANEL); 8 consecutive elements of
+// a row starting at a multiple of 8 stay inside one panel row.
 template <int PD, bool VEC>
 __global__ __launch_bounds__(256) void muon_apply_kernel(void* __restrict__ p, const uint16_t* __restrict__ u,
-                                                         int64_t rows, int64_t cols, int64_t ldu, float wd_factor,
-                                                         int apply_wd, float neg_lr_eff,
+                                                         int64_t rows, int64_t cols, int64_t ldu, bool panel,
+                                                         float wd_factor, int apply_wd, float neg_lr_eff,
                                                          const apexw_amp_dyn* __restrict__ amp) {
   if (amp && amp->skip) return;
   const int64_t n = rows * cols;
@@ -683,7 +708,7 @@ __global__ __launch_bounds__(256) void muon_apply_kernel(void* __restrict__ p, c
       const int64_t r = i / cols, c = i - r * cols;
       float x[8], uu[8];
       load8<PD>(p, i, x);
-      load8<APEXW_BF16>(u, r * ldu + c, uu);
+      load8<APEXW_BF16>(u, poff64(r, c, ldu, panel), uu);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         if (apply_wd) x[j] = rnd<PD>(x[j] * wd_factor);
@@ -697,7 +722,7 @@ __global__ __launch_bounds__(256) void muon_apply_kernel(void* __restrict__ p, c
     const int64_t r = i / cols, c = i - r * cols;
     float x = load1<PD>(p, i);
     if (apply_wd) x = rnd<PD>(x * wd_factor);
-    const float uu = bf(APEXW_GLOBAL(const uint16_t, u)[r * ldu + c]);
+    const float uu = bf(APEXW_GLOBAL(const uint16_t, u)[poff64(r, c, ldu, panel)]);
     store1<PD>(p, i, rnd<PD>(fmaf(neg_lr_eff, uu, x)));
   }
 }
@@ -707,15 +732,16 @@ __global__ __launch_bounds__(256) void muon_apply_kernel(void* __restrict__ p, c
 // are read and written along their rows.
 template <int PD>
 __global__ __launch_bounds__(256) void muon_apply_t_kernel(void* __restrict__ p, const uint16_t* __restrict__ u,
-                                                           int64_t rows, int64_t cols, int64_t ldu, float wd_factor,
-                                                           int apply_wd, float neg_lr_eff,
+                                                           int64_t rows, int64_t cols, int64_t ldu, bool panel,
+                                                           float wd_factor, int apply_wd, float neg_lr_eff,
                                                            const apexw_amp_dyn* __restrict__ amp) {
   __shared__ uint16_t tile[64][66];
   if (amp && amp->skip) return;
   const int64_t tr = (int64_t)blockIdx.y * 64, tc = (int64_t)blockIdx.x * 64;
   for (int e = threadIdx.x; e < 64 * 64; e += 256) {
     const int cc = e >> 6, rr = e & 63;
-    if (tc + cc < cols && tr + rr < rows) tile[cc][rr] = APEXW_GLOBAL(const uint16_t, u)[(tc + cc) * ldu + tr + rr];
+    if (tc + cc < cols && tr + rr < rows)
+      tile[cc][rr] = APEXW_GLOBAL(const uint16_t, u)[poff64(tc + cc, tr + rr, ldu, panel)];
   }
   __syncthreads();
   for (int e = threadIdx.x; e < 64 * 64; e += 256) {
@@ -831,54 +857,47 @@ int apexw_launch_gemm_nt(const uint16_t* a, const uint16_t* b, const uint16_t* e
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }
 
+namespace {
+
+// one grouped launch of the epilogue kind's instantiation (kind without the
+// panel bit, which selects kPanel)
+template <bool kPanel>
+int launch_grouped(const apexw_gemm_problem* probs, const uint32_t* items, const int32_t* offsets, int32_t n_wg,
+                   int32_t kind, const apexw_amp_dyn* amp, hipStream_t stream) {
+  const dim3 grid(n_wg), block(256);
+#define APEXW_GROUPED(C, CT, ADD, NN)                                                                              \
+  hipLaunchKernelGGL((gemm_nt_grouped_kernel<C, CT, ADD, NN, kPanel>), grid, block, 0, stream, probs, items, offsets, \
+                     amp)
+  switch (kind) {
+    case APEXW_GEMM_OUT_C: APEXW_GROUPED(true, false, false, false); break;
+    case APEXW_GEMM_OUT_C | APEXW_GEMM_ADD: APEXW_GROUPED(true, false, true, false); break;
+    case APEXW_GEMM_OUT_CT: APEXW_GROUPED(false, true, false, false); break;
+    case APEXW_GEMM_OUT_CT | APEXW_GEMM_ADD: APEXW_GROUPED(false, true, true, false); break;
+    case APEXW_GEMM_OUT_C | APEXW_GEMM_OUT_CT: APEXW_GROUPED(true, true, false, false); break;
+    case APEXW_GEMM_OUT_C | APEXW_GEMM_OUT_CT | APEXW_GEMM_ADD: APEXW_GROUPED(true, true, true, false); break;
+    case APEXW_GEMM_OUT_C | APEXW_GEMM_KIND_NN: APEXW_GROUPED(true, false, false, true); break;
+    case APEXW_GEMM_OUT_C | APEXW_GEMM_ADD | APEXW_GEMM_KIND_NN: APEXW_GROUPED(true, false, true, true); break;
+    default: return APEXW_ERR_ARG;
+  }
+#undef APEXW_GROUPED
+  return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
+}
+
+}  // namespace
+
 int apexw_launch_gemm_grouped(const apexw_gemm_problem* probs, const uint32_t* items, const int32_t* offsets,
                               int32_t n_wg, int32_t kind, const apexw_amp_dyn* amp, hipStream_t stream) {
-  const dim3 grid(n_wg), block(256);
-  switch (kind) {
-    case APEXW_GEMM_OUT_C:
-      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, false, false, false>), grid, block, 0, stream, probs, items, offsets,
-                         amp);
-      break;
-    case APEXW_GEMM_OUT_C | APEXW_GEMM_ADD:
-      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, false, true, false>), grid, block, 0, stream, probs, items, offsets,
-                         amp);
-      break;
-    case APEXW_GEMM_OUT_CT:
-      hipLaunchKernelGGL((gemm_nt_grouped_kernel<false, true, false, false>), grid, block, 0, stream, probs, items, offsets,
-                         amp);
-      break;
-    case APEXW_GEMM_OUT_CT | APEXW_GEMM_ADD:
-      hipLaunchKernelGGL((gemm_nt_grouped_kernel<false, true, true, false>), grid, block, 0, stream, probs, items, offsets,
-                         amp);
-      break;
-    case APEXW_GEMM_OUT_C | APEXW_GEMM_OUT_CT:
-      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, true, false, false>), grid, block, 0, stream, probs, items, offsets,
-                         amp);
-      break;
-    case APEXW_GEMM_OUT_C | APEXW_GEMM_OUT_CT | APEXW_GEMM_ADD:
-      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, true, true, false>), grid, block, 0, stream, probs, items, offsets,
-                         amp);
-      break;
-    case APEXW_GEMM_OUT_C | APEXW_GEMM_KIND_NN:
-      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, false, false, true>), grid, block, 0, stream, probs, items, offsets,
-                         amp);
-      break;
-    case APEXW_GEMM_OUT_C | APEXW_GEMM_ADD | APEXW_GEMM_KIND_NN:
-      hipLaunchKernelGGL((gemm_nt_grouped_kernel<true, false, true, true>), grid, block, 0, stream, probs, items, offsets,
-                         amp);
-      break;
-    default:
-      return APEXW_ERR_ARG;
-  }
-  return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
+  const int32_t base = kind & ~APEXW_GEMM_KIND_PANEL;
+  return (kind & APEXW_GEMM_KIND_PANEL) ? launch_grouped<true>(probs, items, offsets, n_wg, base, amp, stream)
+                                        : launch_grouped<false>(probs, items, offsets, n_wg, base, amp, stream);
 }
 
 int apexw_muon_partials(int64_t n) { return grid_for(n) < 1024 ? grid_for(n) : 1024; }
 
 template <int GD>
 void launch_prepare(float* buf, const void* g, int64_t rows, int64_t cols, float mu, float one_minus_mu, int nesterov,
-                    float eps, float inv, uint16_t* x, uint16_t* xt, int64_t ldx, int64_t ldxt, float* partial,
-                    const apexw_amp_dyn* amp, hipStream_t stream) {
+                    float eps, float inv, uint16_t* x, uint16_t* xt, int64_t ldx, int64_t ldxt, bool panel,
+                    float* partial, const apexw_amp_dyn* amp, hipStream_t stream) {
   const int64_t n = rows * cols;
   const int nb = apexw_muon_partials(n);
   if ((((uintptr_t)buf | (uintptr_t)g) & 15u) == 0)
@@ -889,60 +908,52 @@ void launch_prepare(float* buf, const void* g, int64_t rows, int64_t cols, float
                        nesterov, inv, partial, amp);
   dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64));
   hipLaunchKernelGGL(muon_normalize_kernel<GD>, grid, dim3(256), 0, stream, buf, g, rows, cols, mu, nesterov, inv,
-                     partial, nb, eps, (int)(rows > cols), x, xt, ldx, ldxt, amp);
+                     partial, nb, eps, (int)(rows > cols), x, xt, ldx, ldxt, panel, amp);
 }
 
 int apexw_launch_muon_prepare(float* buf, const void* g, int32_t g_dtype, int64_t rows, int64_t cols, float mu,
                               float one_minus_mu, int32_t nesterov, float eps, float inv, uint16_t* x, uint16_t* xt,
-                              int64_t ldx, int64_t ldxt, float* partial, const apexw_amp_dyn* amp,
+                              int64_t ldx, int64_t ldxt, bool panel, float* partial, const apexw_amp_dyn* amp,
                               hipStream_t stream) {
   if (g_dtype == APEXW_F32)
-    launch_prepare<APEXW_F32>(buf, g, rows, cols, mu, one_minus_mu, nesterov, eps, inv, x, xt, ldx, ldxt, partial,
-                              amp, stream);
+    launch_prepare<APEXW_F32>(buf, g, rows, cols, mu, one_minus_mu, nesterov, eps, inv, x, xt, ldx, ldxt, panel,
+                              partial, amp, stream);
   else if (g_dtype == APEXW_BF16)
-    launch_prepare<APEXW_BF16>(buf, g, rows, cols, mu, one_minus_mu, nesterov, eps, inv, x, xt, ldx, ldxt, partial,
-                               amp, stream);
+    launch_prepare<APEXW_BF16>(buf, g, rows, cols, mu, one_minus_mu, nesterov, eps, inv, x, xt, ldx, ldxt, panel,
+                               partial, amp, stream);
   else
-    launch_prepare<APEXW_F16>(buf, g, rows, cols, mu, one_minus_mu, nesterov, eps, inv, x, xt, ldx, ldxt, partial,
-                              amp, stream);
+    launch_prepare<APEXW_F16>(buf, g, rows, cols, mu, one_minus_mu, nesterov, eps, inv, x, xt, ldx, ldxt, panel,
+                              partial, amp, stream);
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }
 
 int apexw_launch_muon_apply(void* p, int32_t p_dtype, const uint16_t* u, int64_t rows, int64_t cols, int64_t ldu,
-                            int32_t u_transposed, float wd_factor, int32_t apply_wd, float neg_lr_eff,
+                            bool panel, int32_t u_transposed, float wd_factor, int32_t apply_wd, float neg_lr_eff,
                             const apexw_amp_dyn* amp, hipStream_t stream) {
+#define APEXW_APPLY(KERNEL, GRID)                                                                                  \
+  hipLaunchKernelGGL(KERNEL, GRID, dim3(256), 0, stream, p, u, rows, cols, ldu, panel, wd_factor, apply_wd,          \
+                     neg_lr_eff, amp)
   if (u_transposed) {
     const dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64));
-    if (p_dtype == APEXW_F32)
-      hipLaunchKernelGGL(muon_apply_t_kernel<APEXW_F32>, grid, dim3(256), 0, stream, p, u, rows, cols, ldu, wd_factor,
-                         apply_wd, neg_lr_eff, amp);
-    else if (p_dtype == APEXW_BF16)
-      hipLaunchKernelGGL(muon_apply_t_kernel<APEXW_BF16>, grid, dim3(256), 0, stream, p, u, rows, cols, ldu, wd_factor,
-                         apply_wd, neg_lr_eff, amp);
-    else
-      hipLaunchKernelGGL(muon_apply_t_kernel<APEXW_F16>, grid, dim3(256), 0, stream, p, u, rows, cols, ldu, wd_factor,
-                         apply_wd, neg_lr_eff, amp);
+    if (p_dtype == APEXW_F32) APEXW_APPLY(muon_apply_t_kernel<APEXW_F32>, grid);
+    else if (p_dtype == APEXW_BF16) APEXW_APPLY(muon_apply_t_kernel<APEXW_BF16>, grid);
+    else APEXW_APPLY(muon_apply_t_kernel<APEXW_F16>, grid);
     return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
   }
   const int64_t n = rows * cols;
   const bool vec = cols % 8 == 0 && ldu % 8 == 0 && (((uintptr_t)p | (uintptr_t)u) & 15u) == 0;
   const dim3 grid(grid_for(vec ? n / 8 : n));
   if (p_dtype == APEXW_F32) {
-    if (vec) hipLaunchKernelGGL((muon_apply_kernel<APEXW_F32, true>), grid, dim3(256), 0, stream, p, u, rows, cols, ldu,
-                                wd_factor, apply_wd, neg_lr_eff, amp);
-    else hipLaunchKernelGGL((muon_apply_kernel<APEXW_F32, false>), grid, dim3(256), 0, stream, p, u, rows, cols, ldu,
-                            wd_factor, apply_wd, neg_lr_eff, amp);
+    if (vec) APEXW_APPLY((muon_apply_kernel<APEXW_F32, true>), grid);
+    else APEXW_APPLY((muon_apply_kernel<APEXW_F32, false>), grid);
   } else if (p_dtype == APEXW_BF16) {
-    if (vec) hipLaunchKernelGGL((muon_apply_kernel<APEXW_BF16, true>), grid, dim3(256), 0, stream, p, u, rows, cols,
-                                ldu, wd_factor, apply_wd, neg_lr_eff, amp);
-    else hipLaunchKernelGGL((muon_apply_kernel<APEXW_BF16, false>), grid, dim3(256), 0, stream, p, u, rows, cols, ldu,
-                            wd_factor, apply_wd, neg_lr_eff, amp);
+    if (vec) APEXW_APPLY((muon_apply_kernel<APEXW_BF16, true>), grid);
+    else APEXW_APPLY((muon_apply_kernel<APEXW_BF16, false>), grid);
   } else {
-    if (vec) hipLaunchKernelGGL((muon_apply_kernel<APEXW_F16, true>), grid, dim3(256), 0, stream, p, u, rows, cols, ldu,
-                                wd_factor, apply_wd, neg_lr_eff, amp);
-    else hipLaunchKernelGGL((muon_apply_kernel<APEXW_F16, false>), grid, dim3(256), 0, stream, p, u, rows, cols, ldu,
-                            wd_factor, apply_wd, neg_lr_eff, amp);
+    if (vec) APEXW_APPLY((muon_apply_kernel<APEXW_F16, true>), grid);
+    else APEXW_APPLY((muon_apply_kernel<APEXW_F16, false>), grid);
   }
+#undef APEXW_APPLY
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }
 

@@ -64,16 +64,33 @@ def _round_to(dtype, x):
     return float(torch.tensor(x, dtype=torch.float32).to(dtype).float()) if dtype != torch.float32 else x
 
 
+def _to_panels(t):
+    """A row-major [R x C] bf16 matrix (R, C multiples of 32) in 32 x 32 panels."""
+    r, c = t.shape
+    return t.view(r // 32, 32, c // 32, 32).transpose(1, 2).contiguous().view(r, c)
+
+
+def _from_panels(t):
+    """The row-major matrix of a [R x C] buffer stored in 32 x 32 panels."""
+    r, c = t.shape
+    return t.view(r // 32, c // 32, 32, 32).transpose(1, 2).contiguous().view(r, c)
+
+
 class NSWorkspace:
     """bf16 Newton-Schulz buffers for `batch` matrices whose wide work shape is m x n.
 
     Dimensions are padded to the GEMM tile; the padding is zero and stays zero
     through every product.  X is kept for two iterations (ping-pong), plus the
-    symmetric A and B.
+    symmetric A and B.  The buffers hold their matrices in 32 x 32 panels
+    (APEXW_GEMM_PANEL): each K stage of a product's operand is then whole
+    128-byte lines, which the grouped GEMM reads with fewer L2 requests than
+    the 64-byte row pieces of a row-major operand (panel=False keeps row-major).
     """
 
-    def __init__(self, m, n, batch, device):
+    def __init__(self, m, n, batch, device, panel=True):
         self.m, self.n, self.batch, self.device = m, n, batch, device
+        self.panel = bool(panel)
+        self.layout = _lib.LAYOUT_PANEL if self.panel else _lib.LAYOUT_ROWS
         t = _lib.GEMM_TILE
         self.mp, self.np_ = _pad(m, t), _pad(n, t)
         z = lambda *s: torch.zeros(*s, dtype=torch.bfloat16, device=device)  # noqa: E731
@@ -83,6 +100,14 @@ class NSWorkspace:
         lib = _lib.load()
         per = int(lib.apexw_muon_workspace_floats(m, n))
         self.partial = torch.empty(batch, max(per, 1), dtype=torch.float32, device=device)
+
+    def rows_of(self, buf):
+        """One matrix of x, a or b as a row-major tensor (a copy when in panels)."""
+        return _from_panels(buf) if self.panel else buf
+
+    def in_layout(self, mat):
+        """A row-major matrix of a buffer's padded shape in this workspace's layout."""
+        return _to_panels(mat) if self.panel else mat
 
 
 def _ns_problems(ws, phase, cur, out, tag=None, tags=None):
@@ -94,19 +119,20 @@ def _ns_problems(ws, phase, cur, out, tag=None, tags=None):
     slot holding the current X.  With tags, (tag, entry) is appended per row.
     """
     mp, np_ = ws.mp, ws.np_
+    pf = _lib.GEMM_PANEL if ws.panel else 0
     for e in range(ws.batch):
         if tags is not None:
             tags.append((tag, e))
         x = ws.x[cur][e].data_ptr()
         a, b = ws.a[e].data_ptr(), ws.b[e].data_ptr()
         if phase == 0:
-            out.append((x, x, 0, a, a, mp, mp, np_, np_, np_, 0, mp, mp, 1.0, 0.0, _lib.GEMM_SYM, 0))
+            out.append((x, x, 0, a, a, mp, mp, np_, np_, np_, 0, mp, mp, 1.0, 0.0, _lib.GEMM_SYM | pf, 0))
         elif phase == 1:
-            out.append((a, a, a, b, b, mp, mp, mp, mp, mp, mp, mp, mp, NS_C, NS_B, _lib.GEMM_SYM, 0))
+            out.append((a, a, a, b, b, mp, mp, mp, mp, mp, mp, mp, mp, NS_C, NS_B, _lib.GEMM_SYM | pf, 0))
         else:
             nx = ws.x[cur ^ 1][e].data_ptr()
             out.append((b, x, 0, nx, 0, mp, np_, mp, mp, np_, 0, np_, 0, 1.0, NS_A,
-                        _lib.GEMM_B_KN | _lib.GEMM_ADD_B, 0))
+                        _lib.GEMM_B_KN | _lib.GEMM_ADD_B | pf, 0))
 
 
 class NSPlan:
@@ -240,6 +266,9 @@ class ApexMuon(Optimizer):
         # True: also store each matrix's final Newton-Schulz result in its
         # workspace (the update is applied to the parameter either way)
         self.keep_ns_result = False
+        # work matrices in 32 x 32 panels (False: row-major; same results, read
+        # by the products with more L2 requests); read when a workspace is made
+        self.ns_panels = True
         defaults = dict(lr=lr, momentum=momentum, nesterov=nesterov, weight_decay=weight_decay, ns_steps=ns_steps,
                         beta3=beta3, alpha=alpha, cautious=cautious, grad_centralization=grad_centralization,
                         precision=precision, scale_mode=scale_mode, ns_method=ns_method, batch_bmm=batch_bmm,
@@ -300,7 +329,7 @@ class ApexMuon(Optimizer):
         # are live together while the grouped Newton-Schulz runs
         ws = self._ws.get(key)
         if ws is None:
-            ws = self._ws[key] = NSWorkspace(m, n, batch, device)
+            ws = self._ws[key] = NSWorkspace(m, n, batch, device, panel=getattr(self, "ns_panels", True))
         return ws
 
     def _ns_plan(self, jobs, device):
@@ -466,7 +495,7 @@ class ApexMuon(Optimizer):
             g = p.grad if p.grad.is_contiguous() else p.grad.contiguous()
             _lib.check(lib.apexw_muon_prepare(
                 st["momentum"].data_ptr(), g.data_ptr(), _dtype_code(g.dtype), rows, cols, mu, 1.0 - mu,
-                int(bool(group["nesterov"])), NS_EPS, inv_scale, ws.x[0][i].data_ptr(), None, ws.np_, 0,
+                int(bool(group["nesterov"])), NS_EPS, inv_scale, ws.x[0][i].data_ptr(), None, ws.np_, 0, ws.layout,
                 ws.partial[i].data_ptr(), amp, stream), "apexw_muon_prepare")
         return {"plist": plist, "targets": [self._target(p) for p in plist], "group": group, "ws": ws,
                 "rows": rows, "cols": cols, "steps": int(group["ns_steps"]), "batched": len(plist) > 1}
@@ -531,7 +560,7 @@ class ApexMuon(Optimizer):
         u_buf = ws.x[job["steps"] % 2]           # ping-pong slot of the Newton-Schulz result
         for i, p in enumerate(job["targets"]):
             _lib.check(lib.apexw_muon_apply(p.data_ptr(), _dtype_code(p.dtype), u_buf[i].data_ptr(), rows, cols,
-                                            ws.np_, int(rows > cols), wd_factor, int(apply_wd), neg_lr, amp,
+                                            ws.np_, ws.layout, int(rows > cols), wd_factor, int(apply_wd), neg_lr, amp,
                                             stream),
                        "apexw_muon_apply")
 

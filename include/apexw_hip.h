@@ -44,7 +44,7 @@
 extern "C" {
 #endif
 
-#define APEXW_ABI_VERSION 20
+#define APEXW_ABI_VERSION 21
 
 /* status codes */
 enum apexw_status {
@@ -534,12 +534,20 @@ typedef struct apexw_gemm_problem {
 #define APEXW_GEMM_APPLY 8u
 #define APEXW_GEMM_APPLY_T 16u   /* O is p transposed (a tall parameter's wide work matrix) */
 #define APEXW_GEMM_APPLY_WD 32u  /* multiply p by wd_factor first */
+/* Every matrix of the problem (a, b, et, c, ct) is stored in 32 x 32 panels:
+ * element (r, c) of a matrix whose leading dimension is ld sits at
+ * (r / 32) * 32 * ld + (c / 32) * 1024 + (r % 32) * 32 + c % 32 (panels of 1024
+ * contiguous elements, row-major inside and in row-major order).  Every K stage
+ * of an operand is then a run of whole 128-byte lines.  Leading dimensions must
+ * be multiples of 32.  p (APEXW_GEMM_APPLY) stays row-major. */
+#define APEXW_GEMM_PANEL 64u
 
 /* epilogue kinds of a grouped launch (bit mask) */
 #define APEXW_GEMM_OUT_C 1   /* row-major output */
 #define APEXW_GEMM_OUT_CT 2  /* transposed output */
 #define APEXW_GEMM_ADD 4     /* beta * E added */
 #define APEXW_GEMM_KIND_NN 8 /* B given as [k x n] (APEXW_GEMM_B_KN) */
+#define APEXW_GEMM_KIND_PANEL 16 /* matrices in 32 x 32 panels (APEXW_GEMM_PANEL) */
 
 /* Tile queues of a grouped launch: one per XCD of MI355X. */
 #define APEXW_GEMM_QUEUES 8
@@ -582,6 +590,11 @@ int apexw_gemm_nt_grouped(const apexw_gemm_problem* problems, const uint32_t* it
                           int32_t n_workgroups, int32_t kind, const apexw_amp_dyn* amp, void* stream);
 
 /* fp32 workspace (floats) apexw_muon_prepare needs for a [rows x cols] matrix. */
+/* Layout of a Newton-Schulz work matrix in apexw_muon_prepare / apexw_muon_apply:
+ * row-major with leading dimension ld, or 32 x 32 panels as APEXW_GEMM_PANEL
+ * describes (ld a multiple of 32; the rows the panels cover rounded up to 32). */
+#define APEXW_LAYOUT_ROWS 0
+#define APEXW_LAYOUT_PANEL 1
 int64_t apexw_muon_workspace_floats(int64_t rows, int64_t cols);
 
 /*
@@ -593,8 +606,9 @@ int64_t apexw_muon_workspace_floats(int64_t rows, int64_t cols);
  *   X   = bf16(bf16(s) / bf16(bf16(||bf16(s)||_F) + eps))
  * X is written as the wide work matrix [min x max] to x (ldx) and, when xt is
  * not NULL, as its transpose [max x min] to xt (ldxt): when rows > cols the
- * work matrix is s^T.  Elements of x / xt outside the matrix are not written
- * (keep them zero).  amp (NULL or 16-byte aligned): GradScaler's step read on
+ * work matrix is s^T.  Both in `layout` (APEXW_LAYOUT_ROWS or _PANEL, the latter
+ * for grouped products with APEXW_GEMM_PANEL).  Elements of x / xt outside the
+ * matrix are not written (keep them zero).  amp (NULL or 16-byte aligned): GradScaler's step read on
  * the device (apexw_amp_prepare), in place of the host's found_inf.item() /
  * grad_scale.reciprocal().item() (apexw/muon.py:557-577): nothing is written
  * when amp->skip, and amp->grad_inv_scale replaces grad_inv_scale.  The same
@@ -603,18 +617,18 @@ int64_t apexw_muon_workspace_floats(int64_t rows, int64_t cols);
  */
 int apexw_muon_prepare(float* buf, const void* g, int32_t g_dtype, int64_t rows, int64_t cols,
                        float mu, float one_minus_mu, int32_t nesterov, float eps, float grad_inv_scale,
-                       void* x, void* xt, int64_t ldx, int64_t ldxt, float* workspace, const apexw_amp_dyn* amp,
-                       void* stream);
+                       void* x, void* xt, int64_t ldx, int64_t ldxt, int32_t layout, float* workspace,
+                       const apexw_amp_dyn* amp, void* stream);
 
 /*
  * p = round(round(p * wd_factor) + neg_lr_eff * U)   (the decay only if apply_wd)
- * with U the bf16 Newton-Schulz result in p's [rows x cols] layout (leading
- * dimension ldu), or, when u_transposed, given as U^T [cols x rows] (the wide
- * work matrix of a tall parameter); p dtype F32/BF16/F16, rounded to nearest
- * even.
+ * with U the bf16 Newton-Schulz result in p's [rows x cols] shape (leading
+ * dimension ldu, stored in `layout`: APEXW_LAYOUT_ROWS or _PANEL), or, when
+ * u_transposed, given as U^T [cols x rows] (the wide work matrix of a tall
+ * parameter); p dtype F32/BF16/F16, rounded to nearest even.
  */
 int apexw_muon_apply(void* p, int32_t p_dtype, const void* u, int64_t rows, int64_t cols, int64_t ldu,
-                     int32_t u_transposed, float wd_factor, int32_t apply_wd, float neg_lr_eff,
+                     int32_t layout, int32_t u_transposed, float wd_factor, int32_t apply_wd, float neg_lr_eff,
                      const apexw_amp_dyn* amp, void* stream);
 
 /*

@@ -253,3 +253,59 @@ def test_schedule_rejects_invalid_problems():
     assert lib.apexw_gemm_nt_grouped(16, 16, 16, 12, 3, None, None) == 1     # grid not a multiple of the queues
     assert lib.apexw_gemm_nt_grouped(16, 16, 16, 16, 2 | 8, None, None) == 1  # [k x n] B with a transposed output
     assert lib.apexw_gemm_nt_grouped(16, 18, 16, 16, 3, None, None) == 4     # misaligned table
+
+
+def test_panel_layout_flag():
+    """APEXW_GEMM_PANEL: the launch's epilogue kind carries it (the kernel takes the
+    layout at compile time), leading dimensions must be multiples of 32, a launch
+    holds one layout, and the layout arguments of prepare / apply are checked."""
+    lib = _lib.load()
+    P = _lib.GEMM_PANEL
+    for phase, rows in enumerate(_ns_problems(512, 1024, 2, 1 << 40)):
+        panel = [tuple(r[:15]) + (r[15] | P, 0) for r in rows]
+        *_, kind_rows = _lib.gemm_schedule(_lib.gemm_problems(rows))
+        *_, kind_panel = _lib.gemm_schedule(_lib.gemm_problems(panel))
+        assert kind_panel == kind_rows | _lib.GEMM_KIND_PANEL, phase
+        # one layout per launch
+        with pytest.raises(_lib.ApexwError):
+            _lib.gemm_schedule(_lib.gemm_problems([panel[0], rows[1]]))
+    # leading dimensions: multiples of 8 row-major, of 32 in panels
+    x, a, nx = 1 << 40, 2 << 40, 3 << 40
+    ok = _prob(a, x, 0, nx, 0, 512, 1024 + 256, 512, 520, 1288, 0, 1288, 0, 1.0, NS_A,
+               _lib.GEMM_B_KN | _lib.GEMM_ADD_B)
+    assert lib.apexw_gemm_grouped_items(_lib.gemm_problems([ok]).ctypes.data, 1) > 0
+    bad = ok[:15] + (ok[15] | P, 0)
+    assert lib.apexw_gemm_grouped_items(_lib.gemm_problems([bad]).ctypes.data, 1) == -4   # ld 520 / 1288
+    # the launch accepts the panel bit in its kind, nothing above it
+    assert lib.apexw_gemm_nt_grouped(16, 16, 16, 16, 32 | 1, None, None) == 1
+    # prepare / apply: unknown layouts, and panels need ld % 32 == 0 (all pointers are
+    # stand-ins: each call fails validation before anything is launched)
+    st = lib.apexw_muon_prepare(16, 16, _lib.BF16, 300, 700, 0.9, 0.1, 0, 1e-7, 1.0, 16, None, 768, 0, 2, 16,
+                                None, None)
+    assert st == 1
+    st = lib.apexw_muon_prepare(16, 16, _lib.BF16, 300, 700, 0.9, 0.1, 0, 1e-7, 1.0, 16, None, 712, 0,
+                                _lib.LAYOUT_PANEL, 16, None, None)
+    assert st == 4
+    st = lib.apexw_muon_apply(16, _lib.BF16, 16, 300, 700, 712, _lib.LAYOUT_PANEL, 0, 0.99, 1, -0.01, None, None)
+    assert st == 4
+    st = lib.apexw_muon_apply(16, _lib.BF16, 16, 300, 700, 768, 5, 0, 0.99, 1, -0.01, None, None)
+    assert st == 1
+
+
+def test_panel_helpers_follow_the_documented_offsets():
+    """NSWorkspace's row-major <-> panel conversions place element (r, c) of a
+    matrix with ld columns at (r // 32) * 32 * ld + (c // 32) * 1024 + (r % 32) * 32
+    + c % 32, the offset include/apexw_hip.h documents for APEXW_GEMM_PANEL, and
+    invert each other."""
+    import torch
+    from apexw_amd.muon import _from_panels, _to_panels
+    R, C = 96, 160
+    t = torch.arange(R * C, dtype=torch.float32).view(R, C)
+    p = _to_panels(t).reshape(-1)
+    r = torch.arange(R).view(-1, 1).expand(R, C)
+    c = torch.arange(C).view(1, -1).expand(R, C)
+    off = (r // 32) * 32 * C + (c // 32) * 1024 + (r % 32) * 32 + c % 32
+    assert torch.equal(p[off.reshape(-1)].view(R, C), t)
+    assert torch.equal(_from_panels(_to_panels(t)), t)
+    # a whole 32 x 32 panel is 1024 contiguous elements: rows 32..63, columns 64..95
+    assert torch.equal(p[(1 * 5 + 2) * 1024:(1 * 5 + 3) * 1024].view(32, 32), t[32:64, 64:96])

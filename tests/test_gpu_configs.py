@@ -640,7 +640,9 @@ def test_c5_ns_products_full_size(rows, cols):
     gen = torch.Generator(device="cuda").manual_seed(500 + cols)
     ws = NSWorkspace(rows, cols, 1, torch.device("cuda"))
     G = torch.randn(rows, cols, generator=gen, device="cuda")
-    ws.x[0][0][:rows, :cols] = (G / G.norm()).bfloat16()
+    X0 = torch.zeros(ws.mp, ws.np_, dtype=torch.bfloat16, device="cuda")
+    X0[:rows, :cols] = (G / G.norm()).bfloat16()
+    ws.x[0][0].copy_(ws.in_layout(X0))   # the work buffers hold 32 x 32 panels
     plan = NSPlan([ws], [1], torch.device("cuda"))
     stream = torch.cuda.current_stream().cuda_stream
 
@@ -648,20 +650,21 @@ def test_c5_ns_products_full_size(rows, cols):
         err = (got.float() - ref).abs() - (2.0 ** -8 * ref.abs() + 1e-4 * ref.abs().max())
         assert float(err.max()) <= 0, f"{what}: max excess {float(err.max()):.3e}"
 
-    X = ws.x[0][0].float()
+    X = ws.rows_of(ws.x[0][0]).float()
     _ns_launch(plan, 0, stream)
     torch.cuda.synchronize()
-    bar(ws.a[0], X @ X.T, "A = X X^T")
-    A = ws.a[0].float()
+    bar(ws.rows_of(ws.a[0]), X @ X.T, "A = X X^T")
+    A = ws.rows_of(ws.a[0]).float()
     _ns_launch(plan, 1, stream)
     torch.cuda.synchronize()
-    bar(ws.b[0], NS_C * (A @ A) + NS_B * A, "B = c A A + b A")
-    B = ws.b[0].float()
+    bar(ws.rows_of(ws.b[0]), NS_C * (A @ A) + NS_B * A, "B = c A A + b A")
+    B = ws.rows_of(ws.b[0]).float()
     _ns_launch(plan, 2, stream)
     torch.cuda.synchronize()
-    bar(ws.x[1][0], B @ X + NS_A * X, "X' = B X + a X")
+    Xn = ws.rows_of(ws.x[1][0])
+    bar(Xn, B @ X + NS_A * X, "X' = B X + a X")
     # the zero padding stays zero through the products
-    assert float(ws.x[1][0][rows:].abs().max() if ws.mp > rows else 0.0) == 0.0
+    assert float(Xn[rows:].abs().max() if ws.mp > rows else 0.0) == 0.0
 
 
 def test_c5_hybrid_step_one_llama_layer():
@@ -716,7 +719,7 @@ def test_c5_hybrid_step_one_llama_layer():
                 bufs[i].mul_(mu).add_(grads[i].float(), alpha=1.0 - mu)
                 st = opt.muon_opt.state[gps[i]]
                 _cmp(st["momentum"], bufs[i].cpu(), f"C5 step {step} momentum {shape}")
-                wide = ws.x[5 % 2][k][:min(rows, cols), :max(rows, cols)]
+                wide = ws.rows_of(ws.x[5 % 2][k])[:min(rows, cols), :max(rows, cols)]
                 U_gpu = wide.T if rows > cols else wide
                 U32 = newton_schulz5(bufs[i], 5, work_dtype=torch.float32)
                 U16 = _torch_bf16_ns(bufs[i])

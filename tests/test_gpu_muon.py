@@ -260,6 +260,80 @@ def test_grouped_gemm_symmetric_and_plain_products(cus):
         _assert_gemm_close(c, b.float().cpu() @ x.float() + NS_A * x.float())
 
 
+@pytest.mark.parametrize("cus", [0, 4])
+def test_grouped_gemm_panels_equal_row_major(cus):
+    """APEXW_GEMM_PANEL: the same products with every matrix in 32 x 32 panels give
+    the row-major results bit for bit (only the operand and output addresses
+    differ), for each epilogue kind Newton-Schulz uses and the plain product with
+    both outputs and a read addend; cus=4 runs the half tiles too."""
+    _need_gpu()
+    from apexw_amd import _lib
+    from apexw_amd.muon import _from_panels, _to_panels
+    lib = _lib.load()
+    print(f"grouped gemm panels cus={cus}", flush=True)
+    g = torch.Generator().manual_seed(12)
+    shapes = [(256, 512), (512, 768), (512, 768)]
+    X = [(torch.randn(m, n, generator=g) / math.sqrt(n)).bfloat16().cuda() for m, n in shapes]
+
+    def run(panel):
+        lay = _to_panels if panel else (lambda t: t.clone())
+        back = _from_panels if panel else (lambda t: t)
+        pf = _lib.GEMM_PANEL if panel else 0
+        dX = [lay(x) for x in X]
+        dXt = [lay(x.t().contiguous()) for x in X]
+        nan = lambda *s: torch.full(s, float("nan"), dtype=torch.bfloat16, device="cuda")  # noqa: E731
+        dA, dB = [nan(m, m) for m, _ in shapes], [nan(m, m) for m, _ in shapes]
+        dC, dCt, dK = [nan(m, n) for m, n in shapes], [nan(n, m) for m, n in shapes], [nan(m, n) for m, n in shapes]
+        SYM = _lib.GEMM_SYM | pf
+        _grouped(lib, [(x.data_ptr(), x.data_ptr(), 0, a.data_ptr(), a.data_ptr(), m, m, n, n, n, 0, m, m, 1.0, 0.0,
+                        SYM, 0) for x, a, (m, n) in zip(dX, dA, shapes)], cus)
+        _grouped(lib, [(a.data_ptr(), a.data_ptr(), a.data_ptr(), b.data_ptr(), b.data_ptr(), m, m, m, m, m, m, m, m,
+                        NS_C, NS_B, SYM, 0) for a, b, (m, _) in zip(dA, dB, shapes)], cus)
+        _grouped(lib, [(b.data_ptr(), xt.data_ptr(), xt.data_ptr(), c.data_ptr(), ct.data_ptr(), m, n, m, m, m, m, n,
+                        m, 1.0, NS_A, pf, 0) for b, xt, c, ct, (m, n) in zip(dB, dXt, dC, dCt, shapes)], cus)
+        KN = _lib.GEMM_B_KN | _lib.GEMM_ADD_B | pf
+        _grouped(lib, [(b.data_ptr(), x.data_ptr(), 0, k.data_ptr(), 0, m, n, m, m, n, 0, n, 0, 1.0, NS_A, KN, 0)
+                       for b, x, k, (m, n) in zip(dB, dX, dK, shapes)], cus)
+        return [[back(t).cpu() for t in ts] for ts in (dA, dB, dC, dCt, dK)]
+
+    rows, panels = run(False), run(True)
+    for what, r, p in zip(("X X^T", "c A A + b A", "B X^T + a E (C)", "B X^T + a E (C^T)", "B X + a X"), rows,
+                          panels):
+        for i, (x, y) in enumerate(zip(r, p)):
+            assert not torch.isnan(x).any(), (what, i)
+            assert torch.equal(x, y), (what, i)
+
+
+def test_muon_panels_match_row_major():
+    """ApexMuon with its Newton-Schulz work matrices in 32 x 32 panels (the default)
+    and row-major (ns_panels = False) gives the same parameters bit for bit over
+    two steps: wide, tall and padded shapes, a batched shape, and an ns_steps == 0
+    group, whose separate update pass reads the work matrix in its layout."""
+    _need_gpu()
+    from apexw_amd import ApexMuon
+    print("muon panels vs row-major", flush=True)
+    shapes = [(300, 700), (700, 300), (256, 512), (256, 512), (96, 160), (160, 96)]
+    g = torch.Generator().manual_seed(13)
+    init = [(torch.randn(s, generator=g) * 0.02).bfloat16() for s in shapes]
+    grads = [[(torch.randn(s, generator=g) * 1e-3).bfloat16() for s in shapes] for _ in range(2)]
+
+    def run(panels):
+        ps = [torch.nn.Parameter(h.cuda()) for h in init]
+        opt = ApexMuon([{"params": ps[:4], "ns_steps": 5}, {"params": ps[4:], "ns_steps": 0}], lr=0.02,
+                       momentum=0.9, weight_decay=0.1, scale_mode="none")
+        opt.ns_panels = panels
+        for gs in grads:
+            for p, gr in zip(ps, gs):
+                p.grad = gr.cuda()
+            opt.step()
+        torch.cuda.synchronize()
+        assert opt._ws and all(ws.panel == panels for ws in opt._ws.values())
+        return [p.detach().cpu() for p in ps]
+
+    for s, x, y in zip(shapes, run(True), run(False)):
+        assert torch.equal(x, y), s
+
+
 def test_muon_groups_with_different_ns_steps_and_many_matrices():
     """Param groups with different ns_steps share the grouped launches (a group
     leaves them when its iterations are done), and more than 256 matrices split
@@ -316,7 +390,7 @@ def test_fused_update_dtypes_layouts_and_zero_steps():
     for p, h, gr, (shape, dt), steps in zip(ps, init, grads, specs, (5, 5, 5, 0)):
         rows, cols = shape
         ws = ws_by_shape[shape]
-        wide = ws.x[steps % 2][0][:min(rows, cols), :max(rows, cols)].float().cpu()
+        wide = ws.rows_of(ws.x[steps % 2][0])[:min(rows, cols), :max(rows, cols)].float().cpu()
         U = wide.T if rows > cols else wide
         if steps:
             U32 = newton_schulz5((1 - mu) * gr.float(), steps, work_dtype=torch.float32)

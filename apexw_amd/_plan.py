@@ -91,8 +91,8 @@ class StepPlan:
         self.gc = bool(group.get("grad_centralization", False))
         # cautious=True (8-bit / ultra): a count pass forms the mask's mean before the step
         self.cautious = self._cautious_of(group)
-        # maximize=True (8-bit / ultra; not the in-backward flush nor the per-parameter update,
-        # which step without it): the grads are negated through a negative unscale factor
+        # maximize=True (not the in-backward flush nor the per-parameter update, which step
+        # without it): the grads are negated through a negative unscale factor
         self.maximize = self._maximize_of(group)
         self.d_counts = None
         self.cold_done = False
@@ -108,7 +108,7 @@ class StepPlan:
         return bool(group.get("cautious", False)) and self.kind == "q8" and not self.single
 
     def _maximize_of(self, group):
-        return bool(group.get("maximize", False)) and self.kind == "q8" and not self.hooked
+        return bool(group.get("maximize", False)) and not self.hooked
 
     # ------------------------------------------------------------------ validity
     def valid_for(self, group):
@@ -669,7 +669,8 @@ class StepPlan:
             inv_scale = 1.0          # a stand-in: the kernels read the factor from the device scalars
         elif self.maximize:
             # maximize: g -> -g, through the unscale factor (exact, and it commutes with
-            # nan_to_num, the clip, centralization and AMP's unscale: optimizer.py:4502-4503)
+            # nan_to_num, the clip, centralization and AMP's unscale: optimizer.py:4502-4503,
+            # :1104-1105, :5515-5517)
             inv_scale = -(1.0 if inv_scale is None else inv_scale)
         (b1, b2), eps = group["betas"], group["eps"]
         lr = group["lr"] if lr is None else lr

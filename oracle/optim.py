@@ -83,8 +83,8 @@ class OracleApexW:
                           grad_centralization=grad_centralization, factored_v=factored_v, six_bit=six_bit,
                           threshold=threshold, amp=amp, dynamic_scaling=dynamic_scaling, nesterov=bool(nesterov),
                           cautious=bool(cautious), maximize=bool(maximize), params=self.params)
-        if (nesterov or cautious or maximize) and precision not in ("8bit", "ultra"):
-            raise NotImplementedError("oracle: nesterov / cautious / maximize restate the _step_ultra precisions only")
+        if (nesterov or cautious) and precision not in ("8bit", "ultra"):
+            raise NotImplementedError("oracle: nesterov / cautious restate the _step_ultra precisions only")
         self.state = {}
         self._plan = None
         self.grad_scale = None
@@ -130,6 +130,15 @@ class OracleApexW:
         torch._foreach_mul_(grads, scale.reciprocal())
         return grads
 
+    def _signed(self, grads, quantized):
+        """maximize in the compact-kernel precisions: the grads negated before anything
+        else (the replayed plan, optimizer.py:1104-1105; the cold step negates inside
+        _multi_tensor_step after clip and centralization, :5515-5517, which commute with
+        the negation).  The quantized step negates inside q8_param_step."""
+        if self.group["maximize"] and not quantized:
+            return [-g for g in grads]
+        return grads
+
     @staticmethod
     def _inv(scale):
         return None if scale is None else float(scale.reciprocal().item())
@@ -158,7 +167,7 @@ class OracleApexW:
                 self.state[p] = L.init_state(p, grp, len(self.params), peft)
         prec = grp["precision"]
         quantized = prec in ("8bit", "ultra")     # both run _step_ultra (optimizer.py:3583-3587)
-        grads, scale = self._prepare([p.grad for p in plist],
+        grads, scale = self._prepare(self._signed([p.grad for p in plist], quantized),
                                      sanitize=not quantized or grp["clip_grad_norm"] is not None)
         kw = self._kw()
         if quantized:
@@ -172,7 +181,8 @@ class OracleApexW:
         sts = [self.state[p] for p in plist]
         homogeneous = all("exp_avg_sq" in st and st["exp_avg"].dtype == st["exp_avg_sq"].dtype == p.dtype
                           and st["exp_avg"].numel() == st["exp_avg_sq"].numel() for p, st in zip(plist, sts))
-        if homogeneous:
+        if homogeneous and not grp["maximize"]:
+            # maximize leaves the native fused step (optimizer.py:3733, :593-600)
             self._native_fused(plist, grads, sts, grad_scale=scale, **kw)
             self._plan = {"kind": "native", "params": plist}
             return
@@ -235,7 +245,7 @@ class OracleApexW:
                 q8_param_step(p, g, st, step=st["step"].item(), inv_scale=self._inv(scale), nesterov=grp["nesterov"],
                               cautious=grp["cautious"], maximize=grp["maximize"], **kw)
             return
-        grads, scale = self._prepare(grads, sanitize=grp["clip_grad_norm"] is not None)
+        grads, scale = self._prepare(self._signed(grads, False), sanitize=grp["clip_grad_norm"] is not None)
         sts = [self.state[p] for p in plist]
         if plan["kind"] == "native":
             self._native_fused(plist, grads, sts, sanitize=False, grad_scale=scale, **kw)

@@ -178,9 +178,10 @@ def test_constructor_contract():
     for kw in (dict(precision="compact"), dict(precision="8bit", factored_v=True), dict(precision="8bit", nesterov=True)):
         with pytest.raises(NotImplementedError):
             ApexW(p, cautious=True, **kw)
-    # maximize: the same precisions, not with factored second moments
-    assert ApexW(p, precision="8bit", maximize=True).defaults["maximize"]
-    for kw in (dict(precision="compact"), dict(precision="full"), dict(precision="8bit", factored_v=True)):
+    # maximize: every precision, not with factored second moments
+    for prec in ("8bit", "ultra", "compact", "full", "auto"):
+        assert ApexW(p, precision=prec, maximize=True).defaults["maximize"]
+    for kw in (dict(precision="8bit", factored_v=True), dict(precision="compact", factored_v=True)):
         with pytest.raises(NotImplementedError):
             ApexW(p, maximize=True, **kw)
     for prec, betas in (("full", (0.9, 0.999)), ("fp32", (0.9, 0.999)), ("auto", (0.9, 0.99)),

@@ -46,6 +46,7 @@ CASES = [
     # maximize: the negative unscale factor carries both (GradScaler read on the host)
     ("8bit maximize", [(1024, 512), (4096,), (40,)], torch.bfloat16, dict(precision="8bit", maximize=True)),
     ("8bit cautious", [(1024, 512), (4096,), (40,)], torch.bfloat16, dict(precision="8bit", cautious=True)),
+    ("compact maximize", [(256, 128), (1000,), (64,)], torch.bfloat16, dict(precision="compact", maximize=True)),
 ]
 
 
@@ -105,13 +106,20 @@ def test_grad_scale_with_clip_equals_unscaled_step(name, shapes, dtype, kw):
 
 @pytest.mark.parametrize("precision,extra", [("8bit", {}), ("8bit", dict(clip_grad_norm=1e-3)),
                                              ("8bit", dict(grad_centralization=True, clip_grad_norm=1e-3)),
-                                             ("ultra", dict(threshold=4096, clip_grad_norm=1e-3))],
-                         ids=["8bit", "8bit-clip", "8bit-gc-clip", "ultra-clip"])
+                                             ("ultra", dict(threshold=4096, clip_grad_norm=1e-3)),
+                                             ("compact", {}), ("compact", dict(clip_grad_norm=1e-3)),
+                                             ("compact", dict(grad_centralization=True, clip_grad_norm=1e-3)),
+                                             ("full", dict(clip_grad_norm=1e-3)), ("auto", dict(threshold=4096))],
+                         ids=["8bit", "8bit-clip", "8bit-gc-clip", "ultra-clip", "compact", "compact-clip",
+                              "compact-gc-clip", "full-clip", "auto"])
 def test_maximize_equals_negated_grads(precision, extra):
     """maximize=True on grads g steps exactly as maximize=False on -g (the
     reference negates the grads after nan_to_num, and negation commutes with the
     clip, centralization and AMP's unscale): bit-identical parameters and states,
-    with a GradScaler scale of 2^10 on every step."""
+    with a GradScaler scale of 2^10 on every step.  maximize leaves the native fused
+    order of a compact group whose states all match their parameters (as the
+    reference's plan does), so the plain run there takes the foreach order too
+    (fused=False)."""
     _need_gpu()
     from apexw_amd import ApexW
     print(f"maximize {precision} {extra}", flush=True)
@@ -121,7 +129,8 @@ def test_maximize_equals_negated_grads(precision, extra):
     host = [(torch.randn(s, generator=gen) * 0.02).bfloat16() for s in shapes]
     pa = [torch.nn.Parameter(h.cuda()) for h in host]
     pb = [torch.nn.Parameter(h.cuda()) for h in host]
-    oa, ob = ApexW(pa, maximize=True, **kw), ApexW(pb, **kw)
+    plain = dict(kw, fused=False) if precision in ("compact", "full", "auto") else kw
+    oa, ob = ApexW(pa, maximize=True, **kw), ApexW(pb, **plain)
     for _ in range(3):
         for a, b in zip(pa, pb):
             g = (torch.randn(a.shape, generator=gen) * 1e-3 * SCALE).bfloat16()

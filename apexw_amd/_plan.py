@@ -94,6 +94,9 @@ class StepPlan:
         # maximize=True (not the in-backward flush nor the per-parameter update, which step
         # without it): the grads are negated through a negative unscale factor
         self.maximize = self._maximize_of(group)
+        # nesterov=True: a compact group's step scalars come from the host (no device AMP);
+        # refreshed from the group each step (valid_for)
+        self.nesterov = bool(group.get("nesterov", False))
         self.d_counts = None
         self.cold_done = False
         self._nesterov = False
@@ -125,6 +128,11 @@ class StepPlan:
         if bool(group.get("grad_centralization", False)) != self.gc:
             return False
         if self._cautious_of(group) != self.cautious or self._maximize_of(group) != self.maximize:
+            return False
+        # nesterov: the replayed plan takes a change in place (the reference's
+        # replayed plan stays valid, optimizer.py:575-621); the native fused plan does not
+        self.nesterov = bool(group.get("nesterov", False))
+        if self.native and self.nesterov:
             return False
         self._scan_status = self._scan()
         return self._scan_status in (SCAN_SAME, SCAN_GRADS_MOVED, SCAN_SLOW)
@@ -500,7 +508,8 @@ class StepPlan:
         # by apexw_grad_prepare and the step launches then carry no AMP scalars, so they
         # could not skip an inf / NaN step: such plans read found_inf on the host
         return not (self.hooked or self.single or self.factored.any() or self.vscaled.any()
-                    or (self.gc and not self.gc_fold) or self.maximize)
+                    or (self.gc and not self.gc_fold) or self.maximize
+                    or (self.kind == "compact" and self.nesterov))
 
     def amp_fold(self, sync=False):
         """Subtract from the step counters the steps GradScaler skipped that the host
@@ -915,6 +924,13 @@ class StepPlan:
                 flags |= L.HP_SR
                 if b2 >= 0.995:
                     flags |= L.HP_SR_V
+            if self._nesterov:
+                # nesterov (optimizer.py:5865-5877, :1329-1331): p += (-step_size*b1) m / d, then
+                # p += (-step_size*(1-b1)) g / d, the Python products taken to fp32 by torch;
+                # quad tensors take lerp(g, m, b1) as the numerator (look_coef below)
+                hp.gain_hi = -(lr * bc2s / bc1) * b1
+                hp.gain_lo = -(lr * bc2s / bc1) * (1.0 - b1)
+                flags |= L.HP_NESTEROV
         hp.lerp_coef, hi = _lerp_coef(1.0 - b1)
         if hi:
             flags |= L.HP_LERP_HI

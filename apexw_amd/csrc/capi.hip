@@ -167,7 +167,13 @@ static int launch_args_status(int32_t kind, int32_t n_tensors, int64_t n_units, 
   if (n_tensors <= 0 || n_units < 0 || !hp_ok(hp)) return APEXW_ERR_ARG;
   switch (kind) {
     case APEXW_LAUNCH_COMPACT:
-      return (n_fast_units || n_fast_f32_units) ? APEXW_ERR_ARG : APEXW_OK;
+      if (n_fast_units || n_fast_f32_units) return APEXW_ERR_ARG;
+      if (hp->flags & APEXW_HP_CAUTIOUS) return APEXW_ERR_ARG;   // an 8-bit / ultra option
+      // nesterov: the cold and replayed orders, with the host's step scalars in gain_hi / gain_lo
+      if ((hp->flags & APEXW_HP_NESTEROV) &&
+          (hp->mode == APEXW_MODE_NATIVE || hp->mode == APEXW_MODE_SINGLE || (hp->flags & APEXW_HP_AMP)))
+        return APEXW_ERR_ARG;
+      return APEXW_OK;
     case APEXW_LAUNCH_ULTRA:
       if (n_fast_units || n_fast_f32_units) return APEXW_ERR_ARG;
       return (hp->mode == APEXW_MODE_NATIVE || hp->mode == APEXW_MODE_SINGLE) ? APEXW_ERR_ARG : APEXW_OK;

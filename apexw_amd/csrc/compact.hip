@@ -198,6 +198,13 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
     }
   }
   const bool p16 = PD != APEXW_F32;
+  // nesterov (the cold and the replayed foreach orders): quad tensors take
+  // lerp(g, m, beta1) as the numerator (apexw/optimizer.py:5732-5733, :1276-1277,
+  // look_coef / APEXW_HP_LOOK_HI as the 8-bit lookahead); the others two addcdiv
+  // passes, p += (gain_hi * m) / d then p += (gain_lo * g) / d with gain_hi =
+  // -step_size * beta1 and gain_lo = -step_size * (1 - beta1), each rounded to p's
+  // dtype and never stochastic (:5865-5877, :1329-1331)
+  const bool nest = hp.flags & APEXW_HP_NESTEROV;
   if constexpr (QUAD) {
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
@@ -223,7 +230,12 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int j = b + i;
-        const float delta = q_div<SR>(m[j], den) * hp.step_size;
+        float num = m[j];
+        if (nest) {
+          const float d = m[j] - g[j];
+          num = (hp.flags & APEXW_HP_LOOK_HI) ? fmaf(hp.look_coef, d, m[j]) : fmaf(hp.look_coef, d, g[j]);
+        }
+        const float delta = q_div<SR>(num, den) * hp.step_size;
         const float x = p[j] - delta;
         p[j] = !p16 ? x : (sr ? sr_round<PD>(x, rnd_bits[j]) : store_p<PD>(x));
       }
@@ -243,7 +255,10 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
       den = rnd<VD>(den + eps_v);
       if (scaled) den = rnd<VD>(den / sqrt_scale_v);
       if (clamp_den) den = fmaxf(den, eps_floor);
-      if (!p16) {
+      if (nest) {
+        const float p1 = rnd<PD>(p[j] + (hp.gain_hi * m[j]) / den);
+        p[j] = rnd<PD>(p1 + (hp.gain_lo * g[j]) / den);
+      } else if (!p16) {
         p[j] = p[j] + q_div<SR>(-hp.step_size * m[j], den);
       } else if (sr) {
         p[j] = sr_round<PD>(p[j] - q_div<SR>(m[j], den) * hp.step_size, rnd_bits[j]);

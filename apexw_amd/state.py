@@ -284,13 +284,14 @@ def _factored_compact(st, p):
 
 def _moments(st, p, mdt, group, is_peft, prec):
     """Dense m in ``mdt``, v in the beta2 rule's dtype, quad v for large 16-bit
-    compact / auto tensors (optimizer.py:2788-2810, :2838-2872)."""
+    compact / auto tensors, not under nesterov (optimizer.py:2788-2810, :2838-2872)."""
     n, dev = p.numel(), p.device
     vdt = v_dtype_for_beta2(mdt, group["betas"][1], group.get("force_compact_v", False),
                             bool(group.get("stochastic_rounding", True)))
     quad = (prec in ("compact", "auto") and mdt in (torch.bfloat16, torch.float16)
             and vdt in (torch.bfloat16, torch.float16)
-            and group.get("int4_m", None) is not False and n >= 16384 and n % 4 == 0
+            and group.get("int4_m", None) is not False and not group.get("nesterov", False)
+            and n >= 16384 and n % 4 == 0
             and (p.dim() < 2 or min(p.shape) >= 8)
             and (is_peft or len(group["params"]) >= 8))
     if quad:

@@ -151,9 +151,14 @@ typedef struct apexw_unit {
                                           step_size, eps_scaled, bc2_sqrt and grad_inv_scale from
                                           *amp (apexw_amp_prepare) and return before any write when
                                           amp->skip (found_inf); APEXW_HP_UNSCALE is set with it */
-#define APEXW_HP_NESTEROV (1u << 9)    /* 8-bit / ultra steps with nesterov=True: the dense and ultra
+#define APEXW_HP_NESTEROV (1u << 9)    /* nesterov=True.  8-bit / ultra steps: the dense and ultra
                                           rows' numerator is lerp(g, m, beta1) instead of m (the NF4 /
-                                          INT8 blocks take Nesterov through gain_hi = gain_lo = 1) */
+                                          INT8 blocks take Nesterov through gain_hi = gain_lo = 1).
+                                          Compact step (cold and replay modes, no APEXW_HP_AMP): quad
+                                          tensors take lerp(g, m, beta1) (look_coef, APEXW_HP_LOOK_HI),
+                                          the others p += gain_hi * m / d, then p += gain_lo * g / d,
+                                          each rounded to p's dtype, never stochastic (gain_hi =
+                                          -step_size * beta1, gain_lo = -step_size * (1 - beta1)) */
 #define APEXW_HP_CAUTIOUS (1u << 10)   /* 8-bit / ultra steps with cautious=True: the numerator is
                                           m' x q_t where m' g >= 0, else 0 (q_t = 1 / max(c_t / n_t,
                                           1e-3), c_t = hparams.counts[t] written by
@@ -186,7 +191,8 @@ typedef struct apexw_hparams {
   float lerp_coef;      /* m lerp toward g: w if w < 0.5 else w - 1 (w = fp32(1 - beta1)) */
   float look_coef;      /* 8-bit lookahead lerp(g, m, beta1): same rule with w = fp32(beta1) */
   float bc2_sqrt;       /* native mode: sqrt(1-beta2^t) */
-  float gain_hi, gain_lo;   /* 8-bit "Nesterov-SNR" gains 1+0.2*beta1, 1-0.35*beta1 */
+  float gain_hi, gain_lo;   /* 8-bit "Nesterov-SNR" gains 1+0.2*beta1, 1-0.35*beta1; compact
+                               with APEXW_HP_NESTEROV: the two addcdiv scalars (see the flag) */
   const float* clip_coef;   /* device scalar written by apexw_grad_clip_coef, or NULL */
   uint64_t seed;
   uint32_t step;

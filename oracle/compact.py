@@ -1,9 +1,9 @@
 """Compact-mode multi-tensor AdamW step (CPU oracle; test infrastructure only).
 
 Restates ``ApexW._multi_tensor_step`` (``apexw/optimizer.py:5297-5887``) for the
-standard AdamW update (no amsgrad / lion / AdEMAMix / nesterov / cautious,
-dynamic fp16 scaling inactive) with the same torch foreach ops, so every bf16
-rounding point of the reference is reproduced:
+AdamW update and its nesterov variant (no amsgrad / lion / AdEMAMix / cautious)
+with the same torch foreach ops, so every bf16 rounding point of the reference is
+reproduced:
 
 1. decoupled weight decay ``p *= 1 - lr*wd`` (dim>=2 tensors when
    decay_norm_only) -- optimizer.py:5585-5592
@@ -13,7 +13,9 @@ rounding point of the reference is reproduced:
    bits, per tensor), else two foreach ops in v's dtype -- :5770-5776 / :5691-5697
 4. ``d = sqrt(v) + eps*sqrt(bc2)`` in v's dtype       -- :5799-5816 / :5704-5721
 5. parameter update: fp32 p ``addcdiv(p, m, d, -step_size)``; 16-bit p with SR
-   ``p = SR(p - (m/d)*step_size)``; quad: ``p -= (m/d_q)*step_size``   -- :5818-5828 / :5722-5745
+   ``p = SR(p - (m/d)*step_size)``; quad: ``p -= (m/d_q)*step_size``   -- :5818-5828 / :5722-5745;
+   nesterov: two ``addcdiv`` (m with -step_size*b1, g with -step_size*(1-b1)), each rounded
+   to p's dtype and never stochastic (:5865-5877); quad: ``lerp(g, m, b1)`` in place of m (:5732-5733)
 
 That is the *cold* step, taken whenever the optimizer (re)builds its cached
 execution plan.  Every later step replays the plan through
@@ -73,7 +75,8 @@ def _denominators(vs, eps_scaled, scale_v, sqrt_scale_v):
 
 
 def compact_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weight_decay,
-                          decay_norm_only, step, is_quad, stochastic, scale_v=1.0, sqrt_scale_v=1.0):
+                          decay_norm_only, step, is_quad, stochastic, scale_v=1.0, sqrt_scale_v=1.0,
+                          nesterov=False):
     """One step over a subgroup sharing (p dtype, m dtype, step count, quad flag).
 
     ``step`` is the already-incremented step count.  Tensors are updated in place.
@@ -106,8 +109,9 @@ def compact_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weigh
             torch._foreach_mul_(vs, beta2)
             torch._foreach_add_(vs, gq, alpha=(1.0 - beta2) * scale_v)
         dens = _denominators(vs, eps_scaled, scale_v, sqrt_scale_v)
-        for p, m, d in zip(params, ms, dens):
-            delta = m.float().view(-1, 4).div_(d.float().unsqueeze(1)).mul_(step_size).view(p.shape)
+        for p, g, m, d in zip(params, gf, ms, dens):
+            num = torch.lerp(g, m.float(), beta1) if nesterov else m.float()
+            delta = num.view(-1, 4).div_(d.float().unsqueeze(1)).mul_(step_size).view(p.shape)
             if p.dtype == torch.float32:
                 p.sub_(delta)
             else:
@@ -120,7 +124,12 @@ def compact_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weigh
         torch._foreach_mul_(vs, beta2)
         torch._foreach_addcmul_(vs, gf, gf, value=(1.0 - beta2) * scale_v)
     dens = _denominators(vs, eps_scaled, scale_v, sqrt_scale_v)
-    if params[0].dtype in (torch.bfloat16, torch.float16) and stochastic:
+    if nesterov:
+        # fp32 p with 16-bit m takes m upcast (optimizer.py:5834-5838)
+        mf = [m.float() for m in ms] if params[0].dtype == torch.float32 and ms[0].dtype != torch.float32 else ms
+        torch._foreach_addcdiv_(params, mf, dens, value=-step_size * beta1)
+        torch._foreach_addcdiv_(params, gf, dens, value=-step_size * (1.0 - beta1))
+    elif params[0].dtype in (torch.bfloat16, torch.float16) and stochastic:
         for p, m, d in zip(params, ms, dens):
             delta = (m.float() / d.float()) * step_size
             store_16bit(p, p.float().sub_(delta), True)
@@ -129,7 +138,8 @@ def compact_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weigh
 
 
 def replay_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weight_decay,
-                         apply_wd_mask, step, is_quad, stochastic, scale_v=1.0, sqrt_scale_v=1.0):
+                         apply_wd_mask, step, is_quad, stochastic, scale_v=1.0, sqrt_scale_v=1.0,
+                         nesterov=False):
     """One replayed step over an (p dtype, compact, quad) subgroup (optimizer.py:1200-1338).
 
     With an fp16 parameter, m or v the denominators are clamped below by eps
@@ -159,8 +169,9 @@ def replay_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weight
         dens = _denominators(vs, eps_scaled, scale_v, sqrt_scale_v)
         if has_fp16:
             torch._foreach_clamp_min_(dens, eps)
-        for p, m, d in zip(params, ms, dens):
-            delta = m.float().view(-1, 4).div_(d.float().unsqueeze(1)).mul_(step_size).view(p.shape)
+        for p, g, m, d in zip(params, gf, ms, dens):
+            num = torch.lerp(g, m.float(), beta1) if nesterov else m.float()    # :1276-1277
+            delta = num.view(-1, 4).div_(d.float().unsqueeze(1)).mul_(step_size).view(p.shape)
             if p.dtype == torch.float32:
                 p.sub_(delta)
             else:
@@ -176,7 +187,11 @@ def replay_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weight
     dens = _denominators(vs, eps_scaled, scale_v, sqrt_scale_v)
     if has_fp16:
         torch._foreach_clamp_min_(dens, eps)
-    if params[0].dtype in (torch.bfloat16, torch.float16):
+    if nesterov:
+        # the grads in their own dtype (optimizer.py:1329-1331)
+        torch._foreach_addcdiv_(params, ms, dens, value=-step_size * beta1)
+        torch._foreach_addcdiv_(params, grads, dens, value=-step_size * (1.0 - beta1))
+    elif params[0].dtype in (torch.bfloat16, torch.float16):
         for p, m, d in zip(params, ms, dens):
             delta = (m.float() / d.float()) * step_size
             store_16bit(p, p.float().sub_(delta), stochastic)

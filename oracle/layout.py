@@ -190,12 +190,13 @@ def _factored_compact(st, p, mdt):
 
 def _dense(st, p, mdt, group, is_peft, n_params_in_group, prec):
     """m in ``mdt``, v in the dtype the beta2 rule gives, quad-shared v for large
-    16-bit compact/auto tensors (optimizer.py:2788-2810, :2838-2872)."""
+    16-bit compact/auto tensors, not under nesterov (optimizer.py:2788-2810, :2838-2872)."""
     n = p.numel()
     vdt = v_dtype(mdt, group["betas"][1], group.get("force_compact_v", False), bool(group["stochastic_rounding"]))
     quad = (prec in ("compact", "auto") and mdt in (torch.bfloat16, torch.float16)
             and vdt in (torch.bfloat16, torch.float16)
-            and group.get("int4_m") is not False and n >= 16384 and n % 4 == 0
+            and group.get("int4_m") is not False and not group.get("nesterov", False)
+            and n >= 16384 and n % 4 == 0
             and (p.dim() < 2 or min(p.shape) >= 8) and (is_peft or n_params_in_group >= 8))
     if quad:
         st["is_quad_v"] = True

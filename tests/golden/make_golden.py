@@ -25,8 +25,10 @@ Functions covered, with the reference entry points they exercise:
   * checkpoints                    -> ApexW / HybridApexW state_dict (optimizer.py:2473-2485,
                                       hybrid.py:436-472), plus the steps after them
   * full / auto / ultra precisions -> _init_group, _fused_step, _multi_tensor_step, _step_ultra
-  * nesterov=True (8-bit, ultra)   -> _step_ultra's Nesterov numerators (optimizer.py:4444-4445,
-                                      :4581-4582, :4667-4670, :4719-4724)
+  * nesterov=True                  -> _step_ultra's Nesterov numerators (optimizer.py:4444-4445,
+                                      :4581-4582, :4667-4670, :4719-4724); the compact, full
+                                      and auto steps' (:5732-5733, :5865-5877, :1276-1277,
+                                      :1329-1331)
   * cautious=True (8-bit, ultra)   -> _step_ultra's cautious mask (optimizer.py:4583-4588, :4672-4675,
                                       :4726-4729)
   * maximize=True                  -> _step_ultra's negated grads (optimizer.py:4502-4503,
@@ -497,6 +499,14 @@ PREC_CASES = {
     "full_fp32_maximize_rne": (PREC_SHAPES, torch.float32, 4, 72, dict(PREC_KW, precision="full", maximize=True)),
     "auto_bf16_maximize_rne": (PREC_SHAPES, torch.bfloat16, 4, 73,
                                dict(PREC_KW, precision="auto", adamw_compat=True, maximize=True)),
+    # nesterov=True in the compact-kernel precisions: two addcdiv passes (m, then g) rounded to
+    # the parameter dtype, lerp(g, m, beta1) for quad v, in the cold and the replayed order
+    "compact_bf16_nesterov_rne": (PREC_SHAPES, torch.bfloat16, 5, 74, dict(PREC_KW, nesterov=True)),
+    "compact_fp32_nesterov_rne": (PREC_SHAPES, torch.float32, 4, 75, dict(PREC_KW, nesterov=True)),
+    "full_bf16_nesterov_rne": (PREC_SHAPES, torch.bfloat16, 4, 76, dict(PREC_KW, precision="full", nesterov=True)),
+    "full_fp32_nesterov_rne": (PREC_SHAPES, torch.float32, 4, 77, dict(PREC_KW, precision="full", nesterov=True)),
+    "auto_bf16_nesterov_rne": (PREC_SHAPES, torch.bfloat16, 4, 78,
+                               dict(PREC_KW, precision="auto", adamw_compat=True, nesterov=True)),
 }
 
 

@@ -164,18 +164,17 @@ def test_constructor_contract():
         ApexW(p, precision="nope")
     with pytest.raises(NotImplementedError):
         ApexW(p, amsgrad=True)
-    # nesterov: the _step_ultra precisions only, without factored second moments
-    for prec in ("8bit", "ultra", "3byte"):
+    # nesterov: every precision, without factored second moments
+    for prec in ("8bit", "ultra", "3byte", "compact", "full", "auto"):
         assert ApexW(p, precision=prec, nesterov=True).defaults["nesterov"]
-    for prec in ("compact", "full", "auto"):
+    for prec in ("8bit", "compact"):
         with pytest.raises(NotImplementedError):
-            ApexW(p, precision=prec, nesterov=True)
-    with pytest.raises(NotImplementedError):
-        ApexW(p, precision="8bit", nesterov=True, factored_v=True)
+            ApexW(p, precision=prec, nesterov=True, factored_v=True)
     # cautious: the same precisions, not with factored second moments nor with nesterov
     assert ApexW(p, precision="8bit", cautious=True).defaults["cautious"]
     assert ApexW(p, precision="ultra", cautious=True).defaults["cautious"]
-    for kw in (dict(precision="compact"), dict(precision="8bit", factored_v=True), dict(precision="8bit", nesterov=True)):
+    for kw in (dict(precision="compact"), dict(precision="full"), dict(precision="8bit", factored_v=True),
+               dict(precision="8bit", nesterov=True)):
         with pytest.raises(NotImplementedError):
             ApexW(p, cautious=True, **kw)
     # maximize: every precision, not with factored second moments

@@ -79,13 +79,15 @@ def test_oracle_matches_reference_trajectory(name, monkeypatch):
         assert int(s.get("block_size_8bit", 0) or 0) == fl[3]
 
 
-@pytest.mark.parametrize("name", sorted(n for n in CASES if "maximize" in n))
-def test_maximize_goldens_pin_the_negation(name):
-    """Each maximize trajectory tells the negated grads from the plain ones: the same
-    run with maximize=False ends on other parameters (so the golden pins the sign
-    the oracle gives the grads, not only the rest of the step)."""
+@pytest.mark.parametrize("name", sorted(n for n in CASES if "maximize" in n or "nesterov" in n))
+def test_variant_goldens_pin_the_variant(name):
+    """Each maximize / nesterov trajectory tells the variant from the plain step: the
+    same run with the option off ends on other parameters (so the golden pins the
+    negated grads or the Nesterov numerator, not only the rest of the step)."""
+    option = "maximize" if "maximize" in name else "nesterov"
+
     def plain(params, **kw):
-        return OracleApexW(params, **dict(kw, maximize=False))
+        return OracleApexW(params, **dict(kw, **{option: False}))
     params, _, gold = replay(name, plain)
     assert any(not np.array_equal(_as_np(p.data).reshape(-1), gold[f"p_{i}"].reshape(-1))
                for i, p in enumerate(params))

@@ -157,6 +157,7 @@ SIGNATURES = {
     "apexw_ultra_step": (ctypes.c_int, [_vp, _i32, _vp, _i64, _HP, _vp]),
     "apexw_q8_step": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _i64, _HP, _vp]),
     "apexw_q8_cautious_count": (ctypes.c_int, [_vp, _i32, _vp, _i64, _HP, _vp]),
+    "apexw_compact_cautious_count": (ctypes.c_int, [_vp, _i32, _vp, _i64, _HP, _vp]),
     "apexw_grad_clip_coef": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _vp, _vp, _vp, _f32, _f32, _u32, _vp, _vp, _vp,
                                             _vp]),
     "apexw_grad_clip_coef_noalloc": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _vp, _f32, _f32, _u32, _vp, _vp, _vp]),

@@ -89,7 +89,7 @@ class StepPlan:
         self.device = self.params[0].device
         self.states = [opt.state[p] for p in self.params]
         self.gc = bool(group.get("grad_centralization", False))
-        # cautious=True (8-bit / ultra): a count pass forms the mask's mean before the step
+        # cautious=True: a count pass forms the mask's mean before the step
         self.cautious = self._cautious_of(group)
         # maximize=True (not the in-backward flush nor the per-parameter update, which step
         # without it): the grads are negated through a negative unscale factor
@@ -106,9 +106,9 @@ class StepPlan:
 
     def _cautious_of(self, group):
         """The group's cautious flag as this plan's kernels take it: the 8-bit / ultra
-        steps, not enable_fused_backward's per-parameter update (which has no
-        cautious branch, optimizer.py:2373-2471)."""
-        return bool(group.get("cautious", False)) and self.kind == "q8" and not self.single
+        and compact steps, not enable_fused_backward's per-parameter update (which has
+        no cautious branch, optimizer.py:2373-2471)."""
+        return bool(group.get("cautious", False)) and not self.single
 
     def _maximize_of(self, group):
         return bool(group.get("maximize", False)) and not self.hooked
@@ -127,8 +127,18 @@ class StepPlan:
             return False
         if bool(group.get("grad_centralization", False)) != self.gc:
             return False
-        if self._cautious_of(group) != self.cautious or self._maximize_of(group) != self.maximize:
+        if self._maximize_of(group) != self.maximize:
             return False
+        if self.kind == "q8":
+            # cautious keeps every 8-bit tensor in the generic order: another table
+            if self._cautious_of(group) != self.cautious:
+                return False
+        else:
+            # compact: the replayed plan takes cautious in place, as the reference's does;
+            # the native fused plan does not
+            self.cautious = self._cautious_of(group)
+            if self.native and self.cautious:
+                return False
         # nesterov: the replayed plan takes a change in place (the reference's
         # replayed plan stays valid, optimizer.py:575-621); the native fused plan does not
         self.nesterov = bool(group.get("nesterov", False))
@@ -748,7 +758,7 @@ class StepPlan:
             launches.append((d_units, n_units, n_fast, n_fast32, hp))
         if self.cautious and launches:
             L.check(self._lib.apexw_check_launch(L.LAUNCH_CAUTIOUS, len(self.params), self.n_units, 0, 0,
-                                                 ctypes_ref(launches[0][4])), "apexw_q8_cautious_count")
+                                                 ctypes_ref(launches[0][4])), "cautious count")
         fv_launches = []
         if self.fv is not None:
             replay_step = None if (mode_cold or self.native or self.kind == "q8") else groups[0][1]
@@ -774,9 +784,10 @@ class StepPlan:
         if self.cautious and prog.launches:
             # the mask counts of every tensor, from the grads as prepared above (clip,
             # centralization, AMP), before any launch updates a moment
-            L.check(self._lib.apexw_q8_cautious_count(table, len(self.params), self.d_units.data_ptr(), self.n_units,
-                                                      ctypes_ref(prog.launches[0][4]), stream),
-                    "apexw_q8_cautious_count")
+            count = (self._lib.apexw_compact_cautious_count if self.kind == "compact"
+                     else self._lib.apexw_q8_cautious_count)
+            L.check(count(table, len(self.params), self.d_units.data_ptr(), self.n_units,
+                          ctypes_ref(prog.launches[0][4]), stream), "cautious count")
         for d_units, n_units, n_fast, n_fast32, hp in prog.launches:
             if self.kind == "compact":
                 st = self._lib.apexw_compact_step(table, len(self.params), d_units.data_ptr(), n_units,
@@ -924,7 +935,12 @@ class StepPlan:
                 flags |= L.HP_SR
                 if b2 >= 0.995:
                     flags |= L.HP_SR_V
-            if self._nesterov:
+            if self.cautious:
+                # cautious (optimizer.py:5847-5864, :1321-1328): m times the mask over its mean,
+                # the counts from apexw_compact_cautious_count
+                flags |= L.HP_CAUTIOUS
+                hp.counts = self.d_counts.data_ptr()
+            elif self._nesterov:
                 # nesterov (optimizer.py:5865-5877, :1329-1331): p += (-step_size*b1) m / d, then
                 # p += (-step_size*(1-b1)) g / d, the Python products taken to fp32 by torch;
                 # quad tensors take lerp(g, m, b1) as the numerator (look_coef below)

@@ -18,6 +18,8 @@ int apexw_launch_q8_fast(const apexw_tensor*, int64_t, const apexw_unit*, const 
 int apexw_launch_ultra(const apexw_tensor*, int64_t, const apexw_unit*, const apexw_hparams*, hipStream_t);
 int apexw_launch_q8_cautious_count(const apexw_tensor*, int32_t, const apexw_unit*, int64_t, const apexw_hparams*,
                                    hipStream_t);
+int apexw_launch_compact_cautious_count(const apexw_tensor*, int32_t, const apexw_unit*, int64_t,
+                                        const apexw_hparams*, hipStream_t);
 bool apexw_q8_fast_eligible(uint32_t flags, uint32_t block);
 int apexw_launch_clip(const apexw_tensor*, int32_t, const apexw_unit*, int64_t, int64_t, const int64_t*, float*, float*,
                       float, float, uint32_t, float*, const apexw_amp_dyn*, const apexw_row_means*, hipStream_t);
@@ -168,7 +170,9 @@ static int launch_args_status(int32_t kind, int32_t n_tensors, int64_t n_units, 
   switch (kind) {
     case APEXW_LAUNCH_COMPACT:
       if (n_fast_units || n_fast_f32_units) return APEXW_ERR_ARG;
-      if (hp->flags & APEXW_HP_CAUTIOUS) return APEXW_ERR_ARG;   // an 8-bit / ultra option
+      // cautious: the counts of apexw_compact_cautious_count, in the cold and replayed orders
+      if ((hp->flags & APEXW_HP_CAUTIOUS) && (hp->mode == APEXW_MODE_NATIVE || ((uintptr_t)hp->counts & 7u)))
+        return APEXW_ERR_ARG;
       // nesterov: the cold and replayed orders, with the host's step scalars in gain_hi / gain_lo
       if ((hp->flags & APEXW_HP_NESTEROV) &&
           (hp->mode == APEXW_MODE_NATIVE || hp->mode == APEXW_MODE_SINGLE || (hp->flags & APEXW_HP_AMP)))
@@ -215,6 +219,14 @@ int apexw_q8_cautious_count(const apexw_tensor* tensors, int32_t n_tensors, cons
   const int st = launch_args_status(APEXW_LAUNCH_CAUTIOUS, n_tensors, n_units, 0, 0, hp);
   if (st != APEXW_OK) return st;
   return apexw_launch_q8_cautious_count(tensors, n_tensors, units, n_units, hp, (hipStream_t)stream);
+}
+
+int apexw_compact_cautious_count(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units,
+                                 int64_t n_units, const apexw_hparams* hp, void* stream) {
+  if (!tensors || !units) return APEXW_ERR_ARG;
+  const int st = launch_args_status(APEXW_LAUNCH_CAUTIOUS, n_tensors, n_units, 0, 0, hp);
+  if (st != APEXW_OK) return st;
+  return apexw_launch_compact_cautious_count(tensors, n_tensors, units, n_units, hp, (hipStream_t)stream);
 }
 
 int apexw_ultra_step(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,

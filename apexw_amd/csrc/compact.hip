@@ -27,6 +27,7 @@ struct Ctx {
   uint32_t key;
   uint32_t tflags;
   float vscale, vscale_sqrt;   // the tensor's dynamic fp16-v scale (APEXW_FLAG_VSCALE), else 1
+  float cq;                    // cautious: the tensor's 1 / mean(mask) (caut_q), else unused
 };
 
 // A 16-bit parameter stored through the reference's fp32 -> 16-bit copy
@@ -91,11 +92,63 @@ template <bool SR> APEXW_DEV float q_sqrt(float x) {
   else return sqrtf(x);
 }
 
+// First moment of the cold and replayed orders: the cold step's 16-bit-moment
+// branch = mul then add-with-alpha (two roundings), its fp32-moment branch = one
+// lerp on the grads cast to fp32 (apexw/optimizer.py:5778-5781); the replay = one
+// lerp when grad and moment dtypes match, else mul then add (:1228-1238).
+template <int GD, int MD> APEXW_DEV void m_update8(float (&m)[8], const float (&g)[8], const apexw_hparams& hp) {
+  constexpr bool kLerpCold = MD == APEXW_F32, kLerpReplay = GD == MD;
+  if (hp.mode == APEXW_MODE_REPLAY ? kLerpReplay : kLerpCold) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float d = g[j] - m[j];
+      m[j] = rnd<MD>((hp.flags & APEXW_HP_LERP_HI) ? fmaf(hp.lerp_coef, d, g[j]) : fmaf(hp.lerp_coef, d, m[j]));
+    }
+  } else {
+    const float b1_m = rnd<MD>(hp.beta1);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float m1 = rnd<MD>(m[j] * b1_m);
+      m[j] = rnd<MD>(fmaf(hp.one_minus_beta1, g[j], m1));
+    }
+  }
+}
+
+// cautious (APEXW_HP_CAUTIOUS): the mask g m >= 0 of one element (g prepared, m
+// updated), its product formed where the reference forms it: in fp32 for quad v
+// (apexw/optimizer.py:5728, :1272) and the cold order (:5851-5853), in the grads'
+// dtype after m is cast to it for the replayed order (:1322-1325)
+template <int GD, bool QUAD> APEXW_DEV bool caut_mask(float g, float m, int mode) {
+  if (!QUAD && mode == APEXW_MODE_REPLAY) return rnd<GD>(g * rnd<GD>(m)) >= 0.0f;
+  return g * m >= 0.0f;
+}
+
+// 1 / mean(mask) of a tensor with cnt of its n mask bits set, as the reference forms
+// it: the mean clamped below by 1e-3, then the quotient, in fp32 for quad v and in
+// the parameter's dtype otherwise (the mask is cast to it), each rounded to it
+// (torch's CPU mean of a 0/1 mask is fl32(cnt) / fl32(n) rounded to the mask dtype)
+APEXW_DEV float caut_q(unsigned long long cnt, int64_t n, bool quad, uint32_t pd) {
+  const float mean = (float)cnt / (float)n;
+  if (quad || pd == APEXW_F32) return 1.0f / fmaxf(mean, 1e-3f);
+  if (pd == APEXW_BF16) return rnd<APEXW_BF16>(1.0f / fmaxf(rnd<APEXW_BF16>(mean), rnd<APEXW_BF16>(1e-3f)));
+  return rnd<APEXW_F16>(1.0f / fmaxf(rnd<APEXW_F16>(mean), rnd<APEXW_F16>(1e-3f)));
+}
+
+// The dtype torch gives the cold order's cautious numerator m * mask: m (upcast to
+// fp32 for an fp32 parameter, optimizer.py:5834-5838) times the mask in the
+// parameter's dtype, by type promotion
+template <int PD, int MD> constexpr int caut_cold_dtype() {
+  constexpr int nd = (PD == APEXW_F32 && MD != APEXW_F32) ? APEXW_F32 : MD;
+  return nd == PD ? PD : APEXW_F32;
+}
+
 // p, g, m: 8 elements; v: 8 entries (non-quad) or 2 (quad).  cnt <= 8 valid.
 // e0 is the element index of slot 0 within the tensor (RNG counter).
 // SR: the launch's APEXW_HP_SR flag (a template parameter so that each path
 // compiles to its own code); APEXW_HP_SR_V implies it.
-template <int PD, int GD, int MD, int VD, bool QUAD, bool SR>
+// VAR: the launch may carry nesterov or cautious (APEXW_HP_NESTEROV / _CAUTIOUS); the
+// plain instantiation compiles without them and keeps its registers for the rest.
+template <int PD, int GD, int MD, int VD, bool QUAD, bool SR, bool VAR>
 APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8], int cnt,
                        uint32_t e0, const Ctx& c, bool gc, const float (&mean)[8]) {
   const apexw_hparams& hp = *c.hp;
@@ -162,7 +215,7 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
   // Same-dtype foreach ops with a Python scalar (_foreach_mul_, _foreach_add_)
   // round the scalar to the tensor dtype first on torch's CPU path, so the
   // 16-bit tensors see bf16(beta1), bf16(beta2), bf16(1 - lr*wd), bf16(eps).
-  const float wd_p = rnd<PD>(hp.wd_factor), b1_m = rnd<MD>(hp.beta1), b2_v = rnd<VD>(hp.beta2);
+  const float wd_p = rnd<PD>(hp.wd_factor), b2_v = rnd<VD>(hp.beta2);
   // a dynamically scaled v (fp16): the EMA adds (1 - beta2) * scale * g^2 (the scale is
   // a power of two, so the product is exact) and the denominator is
   // (sqrt(v) + eps_scaled * sqrt(scale)) / sqrt(scale) (apexw/optimizer.py:5691-5721,
@@ -179,24 +232,7 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
 #pragma unroll
     for (int j = 0; j < 8; ++j) p[j] = rnd<PD>(p[j] * wd_p);
   }
-  // first moment: the cold step's 16-bit-moment branch = mul then add-with-alpha
-  // (two roundings), its fp32-moment branch = one lerp on the grads cast to fp32
-  // (apexw/optimizer.py:5778-5781); the replay = one lerp when grad and moment
-  // dtypes match, else mul then add (:1228-1238).
-  constexpr bool kLerpCold = MD == APEXW_F32, kLerpReplay = GD == MD;
-  if (hp.mode == APEXW_MODE_REPLAY ? kLerpReplay : kLerpCold) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      float d = g[j] - m[j];
-      m[j] = rnd<MD>((hp.flags & APEXW_HP_LERP_HI) ? fmaf(hp.lerp_coef, d, g[j]) : fmaf(hp.lerp_coef, d, m[j]));
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      float m1 = rnd<MD>(m[j] * b1_m);
-      m[j] = rnd<MD>(fmaf(hp.one_minus_beta1, g[j], m1));
-    }
-  }
+  m_update8<GD, MD>(m, g, hp);
   const bool p16 = PD != APEXW_F32;
   // nesterov (the cold and the replayed foreach orders): quad tensors take
   // lerp(g, m, beta1) as the numerator (apexw/optimizer.py:5732-5733, :1276-1277,
@@ -204,7 +240,12 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
   // passes, p += (gain_hi * m) / d then p += (gain_lo * g) / d with gain_hi =
   // -step_size * beta1 and gain_lo = -step_size * (1 - beta1), each rounded to p's
   // dtype and never stochastic (:5865-5877, :1329-1331)
-  const bool nest = hp.flags & APEXW_HP_NESTEROV;
+  const bool nest = VAR && (hp.flags & APEXW_HP_NESTEROV);
+  // cautious: m times the mask over its mean (c.cq), in fp32 for quad v (then the usual
+  // quad update); otherwise in the dtypes caut_mask / caut_cold_dtype give, then one
+  // addcdiv rounded to p's dtype, never stochastic (apexw/optimizer.py:5847-5864,
+  // :1321-1328)
+  const bool caut = VAR && (hp.flags & APEXW_HP_CAUTIOUS);
   if constexpr (QUAD) {
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
@@ -231,7 +272,9 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
       for (int i = 0; i < 4; ++i) {
         const int j = b + i;
         float num = m[j];
-        if (nest) {
+        if (caut) {
+          num = m[j] * (caut_mask<GD, true>(g[j], m[j], hp.mode) ? c.cq : 0.0f);
+        } else if (nest) {
           const float d = m[j] - g[j];
           num = (hp.flags & APEXW_HP_LOOK_HI) ? fmaf(hp.look_coef, d, m[j]) : fmaf(hp.look_coef, d, g[j]);
         }
@@ -255,7 +298,13 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
       den = rnd<VD>(den + eps_v);
       if (scaled) den = rnd<VD>(den / sqrt_scale_v);
       if (clamp_den) den = fmaxf(den, eps_floor);
-      if (nest) {
+      if (caut) {
+        const bool replay = hp.mode == APEXW_MODE_REPLAY;
+        const float num = replay ? rnd<GD>(m[j]) : m[j];
+        float nf = num * (caut_mask<GD, false>(g[j], m[j], hp.mode) ? c.cq : 0.0f);
+        nf = replay ? rnd<PD>(nf) : rnd<caut_cold_dtype<PD, MD>()>(nf);
+        p[j] = rnd<PD>(p[j] + (-hp.step_size * nf) / den);
+      } else if (nest) {
         const float p1 = rnd<PD>(p[j] + (hp.gain_hi * m[j]) / den);
         p[j] = rnd<PD>(p1 + (hp.gain_lo * g[j]) / den);
       } else if (!p16) {
@@ -272,7 +321,7 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
 }
 
 // Group k (512 elements, 8 per lane) of the unit starting at element `start`.
-template <int PD, int MD, int VD, bool QUAD, bool SR>
+template <int PD, int MD, int VD, bool QUAD, bool SR, bool VAR>
 APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const Ctx& c) {
   constexpr int GD = PD;
   const int64_t n = t.n;
@@ -323,7 +372,7 @@ APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const 
       cs.vscale = t.v_scale[0];
       cs.vscale_sqrt = t.v_scale[1];
     }
-    update8<PD, GD, MD, VD, QUAD, SR>(p, g, m, v, cnt, (uint32_t)e0, cs, gc, mean);
+    update8<PD, GD, MD, VD, QUAD, SR, VAR>(p, g, m, v, cnt, (uint32_t)e0, cs, gc, mean);
     if (full) {
       store8<PD>(t.p, e0, p);
       store8<MD>(t.m, e0, m);
@@ -356,34 +405,123 @@ APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const 
   }
 }
 
-template <bool SR>
+template <bool SR, bool VAR>
 APEXW_DEV void dispatch_group(const apexw_tensor& t, int64_t start, int k, const Ctx& c, uint32_t pd, uint32_t md,
                               uint32_t vd, bool quad) {
   if (md == APEXW_F32) {
     // fp32 moments ("full" precision, small "auto" tensors): fp32 v, no quad (checked on the host)
-    if (pd == APEXW_F32) compact_group<APEXW_F32, APEXW_F32, APEXW_F32, false, SR>(t, start, k, c);
-    else if (pd == APEXW_BF16) compact_group<APEXW_BF16, APEXW_F32, APEXW_F32, false, SR>(t, start, k, c);
-    else compact_group<APEXW_F16, APEXW_F32, APEXW_F32, false, SR>(t, start, k, c);
+    if (pd == APEXW_F32) compact_group<APEXW_F32, APEXW_F32, APEXW_F32, false, SR, VAR>(t, start, k, c);
+    else if (pd == APEXW_BF16) compact_group<APEXW_BF16, APEXW_F32, APEXW_F32, false, SR, VAR>(t, start, k, c);
+    else compact_group<APEXW_F16, APEXW_F32, APEXW_F32, false, SR, VAR>(t, start, k, c);
     return;
   }
   if (pd == APEXW_F16) {
     // fp16 parameters keep fp16 m (and fp16 or fp32 v)
-    if (vd == APEXW_F32) compact_group<APEXW_F16, APEXW_F16, APEXW_F32, false, SR>(t, start, k, c);
-    else if (quad) compact_group<APEXW_F16, APEXW_F16, APEXW_F16, true, SR>(t, start, k, c);
-    else compact_group<APEXW_F16, APEXW_F16, APEXW_F16, false, SR>(t, start, k, c);
+    if (vd == APEXW_F32) compact_group<APEXW_F16, APEXW_F16, APEXW_F32, false, SR, VAR>(t, start, k, c);
+    else if (quad) compact_group<APEXW_F16, APEXW_F16, APEXW_F16, true, SR, VAR>(t, start, k, c);
+    else compact_group<APEXW_F16, APEXW_F16, APEXW_F16, false, SR, VAR>(t, start, k, c);
     return;
   }
   if (pd == APEXW_F32) {
-    if (vd == APEXW_F32) compact_group<APEXW_F32, APEXW_BF16, APEXW_F32, false, SR>(t, start, k, c);
-    else if (quad) compact_group<APEXW_F32, APEXW_BF16, APEXW_BF16, true, SR>(t, start, k, c);
-    else compact_group<APEXW_F32, APEXW_BF16, APEXW_BF16, false, SR>(t, start, k, c);
+    if (vd == APEXW_F32) compact_group<APEXW_F32, APEXW_BF16, APEXW_F32, false, SR, VAR>(t, start, k, c);
+    else if (quad) compact_group<APEXW_F32, APEXW_BF16, APEXW_BF16, true, SR, VAR>(t, start, k, c);
+    else compact_group<APEXW_F32, APEXW_BF16, APEXW_BF16, false, SR, VAR>(t, start, k, c);
   } else {
-    if (vd == APEXW_F32) compact_group<APEXW_BF16, APEXW_BF16, APEXW_F32, false, SR>(t, start, k, c);
-    else if (quad) compact_group<APEXW_BF16, APEXW_BF16, APEXW_BF16, true, SR>(t, start, k, c);
-    else compact_group<APEXW_BF16, APEXW_BF16, APEXW_BF16, false, SR>(t, start, k, c);
+    if (vd == APEXW_F32) compact_group<APEXW_BF16, APEXW_BF16, APEXW_F32, false, SR, VAR>(t, start, k, c);
+    else if (quad) compact_group<APEXW_BF16, APEXW_BF16, APEXW_BF16, true, SR, VAR>(t, start, k, c);
+    else compact_group<APEXW_BF16, APEXW_BF16, APEXW_BF16, false, SR, VAR>(t, start, k, c);
   }
 }
 
+// cautious count pass: of group k (8 elements per lane) of the unit at `start`, the
+// elements whose mask is set, from the grads as the step prepares them and the first
+// moment as it updates it (nothing is written)
+template <int PD, int MD, bool QUAD>
+APEXW_DEV uint32_t count_group(const apexw_tensor& t, int64_t start, int k, const Ctx& c) {
+  constexpr int GD = PD;
+  const int64_t e0 = start + (int64_t)(k * 64 + lane_id()) * 8;
+  if (e0 >= t.n) return 0u;
+  const int cnt = (int)((t.n - e0) < 8 ? (t.n - e0) : 8);
+  float g[8], m[8];
+  if (!(c.tflags & APEXW_FLAG_SCALAR) && cnt == 8) {
+    load8<GD>(t.g, e0, g);
+    load8<MD>(t.m, e0, m);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      g[j] = j < cnt ? load1<GD>(t.g, e0 + j) : 0.0f;
+      m[j] = j < cnt ? load1<MD>(t.m, e0 + j) : 0.0f;
+    }
+  }
+  const bool gc = c.tflags & APEXW_FLAG_GC;
+  float mean[8];
+  if (gc) row_means8(t, e0, mean);
+  const bool san = (c.hp->flags & APEXW_HP_SANITIZE) && any_nonfinite8(g);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) g[j] = prep_grad<GD>(g[j], c, san, gc, mean[j]);
+  m_update8<GD, MD>(m, g, *c.hp);
+  uint32_t n_set = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) n_set += (j < cnt && caut_mask<GD, QUAD>(g[j], m[j], c.hp->mode)) ? 1u : 0u;
+  return n_set;
+}
+
+APEXW_DEV uint32_t dispatch_count(const apexw_tensor& t, int64_t start, int k, const Ctx& c, uint32_t pd, uint32_t md,
+                                  bool quad) {
+  if (md == APEXW_F32) {
+    if (pd == APEXW_F32) return count_group<APEXW_F32, APEXW_F32, false>(t, start, k, c);
+    if (pd == APEXW_BF16) return count_group<APEXW_BF16, APEXW_F32, false>(t, start, k, c);
+    return count_group<APEXW_F16, APEXW_F32, false>(t, start, k, c);
+  }
+  if (pd == APEXW_F16)
+    return quad ? count_group<APEXW_F16, APEXW_F16, true>(t, start, k, c)
+                : count_group<APEXW_F16, APEXW_F16, false>(t, start, k, c);
+  if (pd == APEXW_F32)
+    return quad ? count_group<APEXW_F32, APEXW_BF16, true>(t, start, k, c)
+                : count_group<APEXW_F32, APEXW_BF16, false>(t, start, k, c);
+  return quad ? count_group<APEXW_BF16, APEXW_BF16, true>(t, start, k, c)
+              : count_group<APEXW_BF16, APEXW_BF16, false>(t, start, k, c);
+}
+
+// Per tensor, the count of set mask bits into hp.counts (cleared before the pass);
+// the work items are the step kernel's.
+__global__ __launch_bounds__(256) void compact_count_kernel(const apexw_tensor* __restrict__ tensors,
+                                                            const apexw_unit* __restrict__ units,
+                                                            int64_t n_units, apexw_hparams hp_in) {
+  apexw_hparams hp = hp_in;
+  if (hp.flags & APEXW_HP_AMP) {
+    const apexw_amp_dyn d = *hp.amp;
+    if (d.skip) return;
+    hp.grad_inv_scale = d.grad_inv_scale;
+  }
+  const uint32_t wave = uniform(threadIdx.x >> 6);
+  Ctx c;
+  c.hp = &hp;
+  c.coef = (hp.flags & APEXW_HP_CLIP) ? *hp.clip_coef : 1.0f;
+  c.vscale = c.vscale_sqrt = 1.0f;
+  c.cq = 0.0f;
+  const int64_t n_items = n_units * kGroups;
+  for (int64_t w = (int64_t)blockIdx.x * kWaves + wave; w < n_items; w += (int64_t)gridDim.x * kWaves) {
+    const apexw_unit un = units[w / kGroups];
+    const apexw_tensor& t = tensors[un.tensor];
+    if (t.flags & APEXW_FLAG_FACTORED) continue;
+    c.tflags = t.flags;
+    const uint32_t pd = (t.flags >> APEXW_FLAG_PDT_SHIFT) & 3u, md = (t.flags >> APEXW_FLAG_MDT_SHIFT) & 3u;
+    uint32_t n_set = dispatch_count(t, (int64_t)un.unit * APEXW_COMPACT_UNIT, (int)(w % kGroups), c, pd, md,
+                                    t.flags & APEXW_FLAG_QUAD);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) n_set += __shfl_xor(n_set, off, 64);
+    if (lane_id() == 0 && n_set) atomicAdd(&hp.counts[un.tensor], (unsigned long long)n_set);
+  }
+}
+
+__global__ __launch_bounds__(256) void compact_counts_zero_kernel(unsigned long long* __restrict__ counts,
+                                                                  int32_t n) {
+  const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (i < n) counts[i] = 0ull;
+}
+
+template <bool VAR>
 __global__ __launch_bounds__(256) void compact_step_kernel(const apexw_tensor* __restrict__ tensors,
                                                            const apexw_unit* __restrict__ units,
                                                            int64_t n_units, apexw_hparams hp_in) {
@@ -403,6 +541,7 @@ __global__ __launch_bounds__(256) void compact_step_kernel(const apexw_tensor* _
   c.coef = (hp.flags & APEXW_HP_CLIP) ? *hp.clip_coef : 1.0f;
   c.vscale = 1.0f;
   c.vscale_sqrt = 1.0f;
+  c.cq = 0.0f;
   // SR applies to the 16-bit stores of the cold and replayed steps (the native and
   // per-parameter modes never set it)
   const bool sr = (hp.flags & APEXW_HP_SR) && (hp.mode == APEXW_MODE_COLD || hp.mode == APEXW_MODE_REPLAY);
@@ -426,8 +565,9 @@ __global__ __launch_bounds__(256) void compact_step_kernel(const apexw_tensor* _
     const bool quad = t.flags & APEXW_FLAG_QUAD;
     if (quad && hp.mode == APEXW_MODE_SINGLE) continue;  // rejected on the host; never read v out of range
     if (t.flags & APEXW_FLAG_FACTORED) continue;        // stepped by apexw_factored_step
-    if (sr) dispatch_group<true>(t, start, k, c, pd, md, vd, quad);
-    else dispatch_group<false>(t, start, k, c, pd, md, vd, quad);
+    if (VAR && (hp.flags & APEXW_HP_CAUTIOUS)) c.cq = caut_q(hp.counts[un.tensor], t.n, quad, pd);
+    if (sr) dispatch_group<true, VAR>(t, start, k, c, pd, md, vd, quad);
+    else dispatch_group<false, VAR>(t, start, k, c, pd, md, vd, quad);
   }
 }
 
@@ -454,9 +594,27 @@ int apexw_launch_compact(const apexw_tensor* tensors, int64_t n_units, const ape
   // resident grid striding over the whole launch).  Launches that a resident grid
   // covers in a few passes keep it (C2, 124 M elements: 0.234-0.257 ms against
   // 0.252-0.288 with a workgroup per unit).
-  const int resident = apexw_resident_grid((const void*)compact_step_kernel, n_units * kGroups);
+  // nesterov / cautious launches take the instantiation that holds them
+  const bool var = hp->flags & (APEXW_HP_NESTEROV | APEXW_HP_CAUTIOUS);
+  const void* kernel = var ? (const void*)compact_step_kernel<true> : (const void*)compact_step_kernel<false>;
+  const int resident = apexw_resident_grid(kernel, n_units * kGroups);
   const int grid = n_units > (int64_t)resident * 8 ? (int)(n_units < INT32_MAX ? n_units : INT32_MAX) : resident;
-  hipLaunchKernelGGL(compact_step_kernel, dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
+  if (var)
+    hipLaunchKernelGGL(compact_step_kernel<true>, dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
+  else
+    hipLaunchKernelGGL(compact_step_kernel<false>, dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
+  return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
+}
+
+int apexw_launch_compact_cautious_count(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units,
+                                        int64_t n_units, const apexw_hparams* hp, hipStream_t stream) {
+  // the counters are cleared by a kernel (not hipMemsetAsync), which a captured graph replays reliably
+  hipLaunchKernelGGL(compact_counts_zero_kernel, dim3((unsigned)((n_tensors + 255) / 256)), dim3(256), 0, stream,
+                     hp->counts, n_tensors);
+  if (n_units > 0) {
+    const int grid = apexw_resident_grid((const void*)compact_count_kernel, n_units * kGroups);
+    hipLaunchKernelGGL(compact_count_kernel, dim3(grid), dim3(256), 0, stream, tensors, units, n_units, *hp);
+  }
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }
 

@@ -40,25 +40,15 @@ HOOK_MIN_NUMEL = 16384             # optimizer.py:2131
 HOOK_BATCH = 14                    # optimizer.py:2142
 
 _UNSUPPORTED_FLAGS = ("amsgrad", "lion", "capturable", "differentiable", "auto_pack")
-# cautious=True runs in the precisions whose step is _step_ultra (optimizer.py:4313-4735);
-# nesterov=True and maximize=True in every precision
-_CAUTIOUS_PRECISIONS = ("8bit", "ultra")
-
-
 def _check_variants(precision, factored, nesterov, cautious, maximize=False):
-    """nesterov=True, cautious=True and maximize=True: every precision takes nesterov
-    (the 8-bit and ultra steps' lookahead numerator lerp(g, m, beta1) without the SNR
-    gain; the compact, full and auto steps' two addcdiv passes, or lerp(g, m, beta1)
-    for quad v) and the negated grads of maximize; the 8-bit and ultra steps take
-    cautious (the numerator m times the sign-agreement mask over its mean).  The
-    compact-kernel precisions with cautious, factored second moments, and nesterov
-    together with cautious do not."""
+    """nesterov=True, cautious=True and maximize=True run in every precision: the
+    8-bit and ultra steps' lookahead numerator lerp(g, m, beta1) without the SNR gain
+    and the compact, full and auto steps' two addcdiv passes (lerp(g, m, beta1) for
+    quad v); the numerator m times the sign-agreement mask over its mean; the negated
+    grads.  Factored second moments, and nesterov together with cautious, do not."""
     for name, on in (("nesterov", nesterov), ("cautious", cautious), ("maximize", maximize)):
         if not on:
             continue
-        if name == "cautious" and precision not in _CAUTIOUS_PRECISIONS:
-            raise NotImplementedError(f"apexw_amd: {name}=True with precision {precision!r} "
-                                      f"(supported: {', '.join(_CAUTIOUS_PRECISIONS)})")
         if factored:
             raise NotImplementedError(f"apexw_amd: {name}=True with factored_v")
     if nesterov and cautious:
@@ -362,10 +352,10 @@ class ApexW(Optimizer):
         # unless fused=False asks for the foreach path (optimizer.py:3676-3720)
         homogeneous = all("exp_avg_sq" in st and st["exp_avg"].dtype == st["exp_avg_sq"].dtype == p.dtype
                           and st["exp_avg"].numel() == st["exp_avg_sq"].numel() for p, st in zip(params, sts))
-        # maximize=True and nesterov=True leave the native fused plan (FastExecutionPlan.
+        # maximize, nesterov and cautious leave the native fused plan (FastExecutionPlan.
         # is_valid_for_step, optimizer.py:593-600): the foreach order instead
         native = (homogeneous and group.get("fused") is not False and not group.get("maximize", False)
-                  and not group.get("nesterov", False))
+                  and not group.get("nesterov", False) and not group.get("cautious", False))
         return StepPlan(self, group, params, "compact", native=native)
 
     # ------------------------------------------------------------------ checkpoints

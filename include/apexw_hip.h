@@ -159,7 +159,8 @@ typedef struct apexw_unit {
                                           the others p += gain_hi * m / d, then p += gain_lo * g / d,
                                           each rounded to p's dtype, never stochastic (gain_hi =
                                           -step_size * beta1, gain_lo = -step_size * (1 - beta1)) */
-#define APEXW_HP_CAUTIOUS (1u << 10)   /* 8-bit / ultra steps with cautious=True: the numerator is
+#define APEXW_HP_CAUTIOUS (1u << 10)   /* cautious=True.  Compact step: see
+                                          apexw_compact_cautious_count.  8-bit / ultra steps: the numerator is
                                           m' x q_t where m' g >= 0, else 0 (q_t = 1 / max(c_t / n_t,
                                           1e-3), c_t = hparams.counts[t] written by
                                           apexw_q8_cautious_count); the blocks take it with
@@ -256,7 +257,7 @@ int apexw_check_tensor(const apexw_tensor* t, int32_t kind);
  * anything, without enqueueing: kind APEXW_LAUNCH_COMPACT (apexw_compact_step),
  * APEXW_LAUNCH_Q8 (apexw_q8_step), APEXW_LAUNCH_ULTRA (apexw_ultra_step) or
  * APEXW_LAUNCH_FACTORED (apexw_factored_step; n_fast counts 0) or APEXW_LAUNCH_CAUTIOUS
- * (apexw_q8_cautious_count; n_fast counts 0).  The entry points
+ * (apexw_q8_cautious_count / apexw_compact_cautious_count; n_fast counts 0).  The entry points
  * run exactly these checks, so a caller that checks every launch of a step first
  * can refuse the whole step before any parameter changes.  Replaces the
  * reference's validate-before-mutate order around step_fused_8bit
@@ -267,7 +268,7 @@ int apexw_check_tensor(const apexw_tensor* t, int32_t kind);
 #define APEXW_LAUNCH_Q8 1
 #define APEXW_LAUNCH_FACTORED 4
 #define APEXW_LAUNCH_ULTRA 5
-#define APEXW_LAUNCH_CAUTIOUS 6   /* apexw_q8_cautious_count */
+#define APEXW_LAUNCH_CAUTIOUS 6   /* apexw_q8_cautious_count, apexw_compact_cautious_count */
 int apexw_check_launch(int32_t kind, int32_t n_tensors, int64_t n_units, int64_t n_fast_units,
                        int64_t n_fast_f32_units, const apexw_hparams* hp);
 
@@ -283,6 +284,17 @@ int apexw_check_launch(int32_t kind, int32_t n_tensors, int64_t n_units, int64_t
  */
 int apexw_q8_cautious_count(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units, int64_t n_units,
                             const apexw_hparams* hp, void* stream);
+
+/*
+ * The same counts for a compact-precision step (compact, full and auto; cautious=True,
+ * apexw/optimizer.py:5728-5731, :5847-5864, :1272-1275, :1321-1328): elements whose
+ * updated first moment m' and prepared grad g' have m' g' >= 0, the product formed
+ * in fp32 (quad v and the cold mode) or, in the replay mode, in the grad dtype after
+ * m' is cast to it.  The step (APEXW_HP_CAUTIOUS) turns each count into
+ * 1 / max(mean, 1e-3), in fp32 for quad v and in the parameter's dtype otherwise.
+ */
+int apexw_compact_cautious_count(const apexw_tensor* tensors, int32_t n_tensors, const apexw_unit* units,
+                                 int64_t n_units, const apexw_hparams* hp, void* stream);
 
 /*
  * Compact-precision fused AdamW step over every tensor of the table in one

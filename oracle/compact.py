@@ -1,8 +1,8 @@
 """Compact-mode multi-tensor AdamW step (CPU oracle; test infrastructure only).
 
 Restates ``ApexW._multi_tensor_step`` (``apexw/optimizer.py:5297-5887``) for the
-AdamW update and its nesterov variant (no amsgrad / lion / AdEMAMix / cautious)
-with the same torch foreach ops, so every bf16 rounding point of the reference is
+AdamW update and its nesterov and cautious variants (no amsgrad / lion / AdEMAMix)
+with the same torch ops, so every bf16 rounding point of the reference is
 reproduced:
 
 1. decoupled weight decay ``p *= 1 - lr*wd`` (dim>=2 tensors when
@@ -15,7 +15,10 @@ reproduced:
 5. parameter update: fp32 p ``addcdiv(p, m, d, -step_size)``; 16-bit p with SR
    ``p = SR(p - (m/d)*step_size)``; quad: ``p -= (m/d_q)*step_size``   -- :5818-5828 / :5722-5745;
    nesterov: two ``addcdiv`` (m with -step_size*b1, g with -step_size*(1-b1)), each rounded
-   to p's dtype and never stochastic (:5865-5877); quad: ``lerp(g, m, b1)`` in place of m (:5732-5733)
+   to p's dtype and never stochastic (:5865-5877); quad: ``lerp(g, m, b1)`` in place of m (:5732-5733);
+   cautious: m times the mask ``g m >= 0`` over its mean (clamped at 1e-3), the mask, its mean
+   and the product in the parameter's / m's dtype, then one ``addcdiv`` (:5847-5864); quad:
+   the same in fp32 (:5728-5731)
 
 That is the *cold* step, taken whenever the optimizer (re)builds its cached
 execution plan.  Every later step replays the plan through
@@ -74,9 +77,30 @@ def _denominators(vs, eps_scaled, scale_v, sqrt_scale_v):
     return dens
 
 
+def _quad_cautious(g, m):
+    """fp32 numerator m * mask / mean(mask) of a quad-v tensor (optimizer.py:5728-5731, :1272-1275)."""
+    mask = (g * m >= 0).to(torch.float32)
+    mask_mean = mask.mean().clamp(min=1e-3)
+    return m.mul(mask.div_(mask_mean))
+
+
+def _masked(nums, lhs, rhs, params):
+    """cautious numerators of the non-quad tensors: nums[i] * mask / mean(mask), the
+    mask (lhs[i] * rhs[i] >= 0, the product in their dtype) and its mean and quotient
+    in the parameter's dtype, the product with the numerator by torch's promotion
+    (optimizer.py:5850-5861, :1321-1327)."""
+    out = []
+    for num, a, b, p in zip(nums, lhs, rhs, params):
+        mask = (a * b >= 0).to(p.dtype)
+        mask_mean = mask.mean().clamp(min=1e-3)
+        mask.div_(mask_mean)
+        out.append(num * mask)
+    return out
+
+
 def compact_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weight_decay,
                           decay_norm_only, step, is_quad, stochastic, scale_v=1.0, sqrt_scale_v=1.0,
-                          nesterov=False):
+                          nesterov=False, cautious=False):
     """One step over a subgroup sharing (p dtype, m dtype, step count, quad flag).
 
     ``step`` is the already-incremented step count.  Tensors are updated in place.
@@ -110,7 +134,10 @@ def compact_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weigh
             torch._foreach_add_(vs, gq, alpha=(1.0 - beta2) * scale_v)
         dens = _denominators(vs, eps_scaled, scale_v, sqrt_scale_v)
         for p, g, m, d in zip(params, gf, ms, dens):
-            num = torch.lerp(g, m.float(), beta1) if nesterov else m.float()
+            if cautious:
+                num = _quad_cautious(g, m.float())
+            else:
+                num = torch.lerp(g, m.float(), beta1) if nesterov else m.float()
             delta = num.view(-1, 4).div_(d.float().unsqueeze(1)).mul_(step_size).view(p.shape)
             if p.dtype == torch.float32:
                 p.sub_(delta)
@@ -124,7 +151,13 @@ def compact_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weigh
         torch._foreach_mul_(vs, beta2)
         torch._foreach_addcmul_(vs, gf, gf, value=(1.0 - beta2) * scale_v)
     dens = _denominators(vs, eps_scaled, scale_v, sqrt_scale_v)
-    if nesterov:
+    if cautious:
+        # fp32 p with 16-bit m takes m upcast (optimizer.py:5834-5838); the mask from
+        # g.float() * num.float() (:5851-5853)
+        mf = [m.float() for m in ms] if params[0].dtype == torch.float32 and ms[0].dtype != torch.float32 else ms
+        nums = _masked(mf, gf, [n.float() for n in mf], params)
+        torch._foreach_addcdiv_(params, nums, dens, value=-step_size)
+    elif nesterov:
         # fp32 p with 16-bit m takes m upcast (optimizer.py:5834-5838)
         mf = [m.float() for m in ms] if params[0].dtype == torch.float32 and ms[0].dtype != torch.float32 else ms
         torch._foreach_addcdiv_(params, mf, dens, value=-step_size * beta1)
@@ -139,7 +172,7 @@ def compact_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weigh
 
 def replay_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weight_decay,
                          apply_wd_mask, step, is_quad, stochastic, scale_v=1.0, sqrt_scale_v=1.0,
-                         nesterov=False):
+                         nesterov=False, cautious=False):
     """One replayed step over an (p dtype, compact, quad) subgroup (optimizer.py:1200-1338).
 
     With an fp16 parameter, m or v the denominators are clamped below by eps
@@ -170,7 +203,10 @@ def replay_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weight
         if has_fp16:
             torch._foreach_clamp_min_(dens, eps)
         for p, g, m, d in zip(params, gf, ms, dens):
-            num = torch.lerp(g, m.float(), beta1) if nesterov else m.float()    # :1276-1277
+            if cautious:
+                num = _quad_cautious(g, m.float())                             # :1272-1275
+            else:
+                num = torch.lerp(g, m.float(), beta1) if nesterov else m.float()    # :1276-1277
             delta = num.view(-1, 4).div_(d.float().unsqueeze(1)).mul_(step_size).view(p.shape)
             if p.dtype == torch.float32:
                 p.sub_(delta)
@@ -187,7 +223,11 @@ def replay_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weight
     dens = _denominators(vs, eps_scaled, scale_v, sqrt_scale_v)
     if has_fp16:
         torch._foreach_clamp_min_(dens, eps)
-    if nesterov:
+    if cautious:
+        # m cast to the grads' dtype, the mask from their product in it (optimizer.py:1321-1328)
+        nums = [m.to(g.dtype) if m.dtype != g.dtype else m for g, m in zip(grads, ms)]
+        torch._foreach_addcdiv_(params, _masked(nums, grads, nums, params), dens, value=-step_size)
+    elif nesterov:
         # the grads in their own dtype (optimizer.py:1329-1331)
         torch._foreach_addcdiv_(params, ms, dens, value=-step_size * beta1)
         torch._foreach_addcdiv_(params, grads, dens, value=-step_size * (1.0 - beta1))

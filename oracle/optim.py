@@ -83,8 +83,6 @@ class OracleApexW:
                           grad_centralization=grad_centralization, factored_v=factored_v, six_bit=six_bit,
                           threshold=threshold, amp=amp, dynamic_scaling=dynamic_scaling, nesterov=bool(nesterov),
                           cautious=bool(cautious), maximize=bool(maximize), params=self.params)
-        if cautious and precision not in ("8bit", "ultra"):
-            raise NotImplementedError("oracle: cautious restates the _step_ultra precisions only")
         self.state = {}
         self._plan = None
         self.grad_scale = None
@@ -181,8 +179,8 @@ class OracleApexW:
         sts = [self.state[p] for p in plist]
         homogeneous = all("exp_avg_sq" in st and st["exp_avg"].dtype == st["exp_avg_sq"].dtype == p.dtype
                           and st["exp_avg"].numel() == st["exp_avg_sq"].numel() for p, st in zip(plist, sts))
-        if homogeneous and not (grp["maximize"] or grp["nesterov"]):
-            # maximize and nesterov leave the native fused step (optimizer.py:3733, :593-600)
+        if homogeneous and not (grp["maximize"] or grp["nesterov"] or grp["cautious"]):
+            # maximize, nesterov and cautious leave the native fused step (optimizer.py:3733, :593-600)
             self._native_fused(plist, grads, sts, grad_scale=scale, **kw)
             self._plan = {"kind": "native", "params": plist}
             return
@@ -223,7 +221,8 @@ class OracleApexW:
             compact_subgroup_step([i[0] for i in items], [i[1] for i in items],
                                   [i[2]["exp_avg"] for i in items], vs, step=step, is_quad=quad,
                                   stochastic=grp["stochastic_rounding"], scale_v=scale_v,
-                                  sqrt_scale_v=sqrt_scale_v, nesterov=grp["nesterov"], **kw)
+                                  sqrt_scale_v=sqrt_scale_v, nesterov=grp["nesterov"],
+                                  cautious=grp["cautious"], **kw)
         # the replayed plan's per-subgroup scales start at 1.0 (optimizer.py:546-560)
         self._plan = {"kind": "foreach", "params": plan_params, "sg_scale": {}}
 
@@ -284,7 +283,8 @@ class OracleApexW:
                                  [i[2]["exp_avg"] for i in items], [i[2]["exp_avg_sq"] for i in items],
                                  apply_wd_mask=[(i[0].dim() >= 2) if dno else True for i in items],
                                  step=step, is_quad=quad, stochastic=grp["stochastic_rounding"],
-                                 scale_v=scale_v, sqrt_scale_v=sqrt_scale_v, nesterov=grp["nesterov"], **kw)
+                                 scale_v=scale_v, sqrt_scale_v=sqrt_scale_v, nesterov=grp["nesterov"],
+                                 cautious=grp["cautious"], **kw)
 
     def _factored(self, p, g, st, step, inv, sanitize):
         grp = self.group

@@ -29,8 +29,9 @@ Functions covered, with the reference entry points they exercise:
                                       :4581-4582, :4667-4670, :4719-4724); the compact, full
                                       and auto steps' (:5732-5733, :5865-5877, :1276-1277,
                                       :1329-1331)
-  * cautious=True (8-bit, ultra)   -> _step_ultra's cautious mask (optimizer.py:4583-4588, :4672-4675,
-                                      :4726-4729)
+  * cautious=True                  -> _step_ultra's cautious mask (optimizer.py:4583-4588, :4672-4675,
+                                      :4726-4729); the compact, full and auto steps'
+                                      (:5728-5731, :5847-5864, :1272-1275, :1321-1328)
   * maximize=True                  -> _step_ultra's negated grads (optimizer.py:4502-4503,
                                       state.py:341-342); the compact, full and auto steps'
                                       (:1104-1105, :5515-5517)
@@ -507,6 +508,14 @@ PREC_CASES = {
     "full_fp32_nesterov_rne": (PREC_SHAPES, torch.float32, 4, 77, dict(PREC_KW, precision="full", nesterov=True)),
     "auto_bf16_nesterov_rne": (PREC_SHAPES, torch.bfloat16, 4, 78,
                                dict(PREC_KW, precision="auto", adamw_compat=True, nesterov=True)),
+    # cautious=True in the compact-kernel precisions: the mask over its mean in the parameter's
+    # dtype (non-quad, cold and replayed orders) or in fp32 (quad v)
+    "compact_bf16_cautious_rne": (PREC_SHAPES, torch.bfloat16, 5, 79, dict(PREC_KW, cautious=True)),
+    "compact_fp32_cautious_rne": (PREC_SHAPES, torch.float32, 4, 80, dict(PREC_KW, cautious=True)),
+    "full_bf16_cautious_rne": (PREC_SHAPES, torch.bfloat16, 4, 81, dict(PREC_KW, precision="full", cautious=True)),
+    "full_fp32_cautious_rne": (PREC_SHAPES, torch.float32, 4, 82, dict(PREC_KW, precision="full", cautious=True)),
+    "auto_bf16_cautious_rne": (PREC_SHAPES, torch.bfloat16, 4, 83,
+                               dict(PREC_KW, precision="auto", adamw_compat=True, cautious=True)),
 }
 
 

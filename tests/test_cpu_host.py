@@ -170,11 +170,11 @@ def test_constructor_contract():
     for prec in ("8bit", "compact"):
         with pytest.raises(NotImplementedError):
             ApexW(p, precision=prec, nesterov=True, factored_v=True)
-    # cautious: the same precisions, not with factored second moments nor with nesterov
-    assert ApexW(p, precision="8bit", cautious=True).defaults["cautious"]
-    assert ApexW(p, precision="ultra", cautious=True).defaults["cautious"]
-    for kw in (dict(precision="compact"), dict(precision="full"), dict(precision="8bit", factored_v=True),
-               dict(precision="8bit", nesterov=True)):
+    # cautious: every precision, not with factored second moments nor with nesterov
+    for prec in ("8bit", "ultra", "compact", "full", "auto"):
+        assert ApexW(p, precision=prec, cautious=True).defaults["cautious"]
+    for kw in (dict(precision="8bit", factored_v=True), dict(precision="compact", factored_v=True),
+               dict(precision="8bit", nesterov=True), dict(precision="compact", nesterov=True)):
         with pytest.raises(NotImplementedError):
             ApexW(p, cautious=True, **kw)
     # maximize: every precision, not with factored second moments

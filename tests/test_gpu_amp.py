@@ -47,6 +47,9 @@ CASES = [
     ("8bit maximize", [(1024, 512), (4096,), (40,)], torch.bfloat16, dict(precision="8bit", maximize=True)),
     ("8bit cautious", [(1024, 512), (4096,), (40,)], torch.bfloat16, dict(precision="8bit", cautious=True)),
     ("compact maximize", [(256, 128), (1000,), (64,)], torch.bfloat16, dict(precision="compact", maximize=True)),
+    # cautious: the count pass reads the device scalars too (8 tensors: quad v for the large ones)
+    ("compact cautious", [(256, 128), (20000,)] + [(64,)] * 6, torch.bfloat16,
+     dict(precision="compact", cautious=True)),
 ]
 
 

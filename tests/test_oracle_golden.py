@@ -79,12 +79,16 @@ def test_oracle_matches_reference_trajectory(name, monkeypatch):
         assert int(s.get("block_size_8bit", 0) or 0) == fl[3]
 
 
-@pytest.mark.parametrize("name", sorted(n for n in CASES if "maximize" in n or "nesterov" in n))
+VARIANT_OPTIONS = ("maximize", "nesterov", "cautious")
+
+
+@pytest.mark.parametrize("name", sorted(n for n in CASES if any(o in n for o in VARIANT_OPTIONS)))
 def test_variant_goldens_pin_the_variant(name):
-    """Each maximize / nesterov trajectory tells the variant from the plain step: the
-    same run with the option off ends on other parameters (so the golden pins the
-    negated grads or the Nesterov numerator, not only the rest of the step)."""
-    option = "maximize" if "maximize" in name else "nesterov"
+    """Each maximize / nesterov / cautious trajectory tells the variant from the plain
+    step: the same run with the option off ends on other parameters (so the golden
+    pins the negated grads, the Nesterov numerator or the mask, not only the rest of
+    the step)."""
+    option = next(o for o in VARIANT_OPTIONS if o in name)
 
     def plain(params, **kw):
         return OracleApexW(params, **dict(kw, **{option: False}))

@@ -29,9 +29,10 @@ namespace {
 
 constexpr int kWaves = 4;
 // units per workgroup of the full-block kernels: a small chunk keeps the resident
-// workgroups on a narrow, advancing window of the tensors (C3, 8.03 B parameters:
-// 11.27 ms per step with 8 units, 11.35 with 16, 11.55 with 32, 11.67 with 64)
-constexpr int64_t kFastChunk = 8;
+// workgroups on a narrow, advancing window of the tensors; 4 is one unit per wave
+// (C3, 8.03 B parameters, one box: 10.76 ms per step with 4 units, 10.91 with 8,
+// 11.39 with 16; on an earlier build 8 -> 64 units went 11.27 -> 11.67 ms)
+constexpr int64_t kFastChunk = 4;
 
 struct Q8Ctx {
   const apexw_hparams* hp;

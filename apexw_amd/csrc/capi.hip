@@ -327,8 +327,9 @@ int gemm_problem_kind(const apexw_gemm_problem& p) {
                               APEXW_GEMM_APPLY_T | APEXW_GEMM_APPLY_WD | APEXW_GEMM_PANEL;
   if ((p.flags & ~kKnown) || p.reserved || p.reserved2) return -APEXW_ERR_ARG;
   if (apply) {
-    // the X' product only; p covered by O
-    if (!kn || !add_b || p.ct || !p.p) return -APEXW_ERR_ARG;
+    // the X' product only (X as [K x N] rows, or X^T as the [N x K] operand, which may
+    // also write O^T); p covered by O
+    if (!add_b || (kn && p.ct) || !p.p) return -APEXW_ERR_ARG;
     if (p.p_dtype != APEXW_F32 && p.p_dtype != APEXW_BF16 && p.p_dtype != APEXW_F16) return -APEXW_ERR_DTYPE;
     const bool t = p.flags & APEXW_GEMM_APPLY_T;
     if (p.p_rows <= 0 || p.p_cols <= 0 || (t ? (p.p_cols > p.m || p.p_rows > p.n) : (p.p_rows > p.m || p.p_cols > p.n)))

@@ -548,7 +548,8 @@ typedef struct apexw_gemm_problem {
  * when c is not NULL, besides writing O: ApexMuon's decoupled decay and
  * scaled orthogonalised update (apexw/muon.py:852-858) on the last
  * Newton-Schulz product, with no separate pass over O.  Only with
- * APEXW_GEMM_B_KN and APEXW_GEMM_ADD_B (the X' = B X + a X product); ct NULL. */
+ * APEXW_GEMM_ADD_B (the X' = B X + a X product): with APEXW_GEMM_B_KN ct is NULL;
+ * with X^T as the [n x k] operand ct may receive O^T as well. */
 #define APEXW_GEMM_APPLY 8u
 #define APEXW_GEMM_APPLY_T 16u   /* O is p transposed (a tall parameter's wide work matrix) */
 #define APEXW_GEMM_APPLY_WD 32u  /* multiply p by wd_factor first */

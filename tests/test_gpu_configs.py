@@ -643,7 +643,11 @@ def test_c5_ns_products_full_size(rows, cols):
     X0 = torch.zeros(ws.mp, ws.np_, dtype=torch.bfloat16, device="cuda")
     X0[:rows, :cols] = (G / G.norm()).bfloat16()
     ws.x[0][0].copy_(ws.in_layout(X0))   # the work buffers hold 32 x 32 panels
-    plan = NSPlan([ws], [1], torch.device("cuda"))
+    ws.xt[0][0].copy_(ws.in_layout(X0.t().contiguous()))   # X' = B X + a X reads X^T
+    # two iterations: the first (run below) is not the last, so its X' product also
+    # writes X'^T for the next one (a last product's X'^T is dropped when no other
+    # matrix of the launch needs it)
+    plan = NSPlan([ws], [2], torch.device("cuda"))
     stream = torch.cuda.current_stream().cuda_stream
 
     def bar(got, ref, what):
@@ -663,6 +667,8 @@ def test_c5_ns_products_full_size(rows, cols):
     torch.cuda.synchronize()
     Xn = ws.rows_of(ws.x[1][0])
     bar(Xn, B @ X + NS_A * X, "X' = B X + a X")
+    # and its transpose, for the next iteration's X' product
+    assert torch.equal(ws.rows_of(ws.xt[1][0]), Xn.t().contiguous())
     # the zero padding stays zero through the products
     assert float(Xn[rows:].abs().max() if ws.mp > rows else 0.0) == 0.0
 

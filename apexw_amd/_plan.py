@@ -97,6 +97,8 @@ class StepPlan:
         # nesterov=True: a compact group's step scalars come from the host (no device AMP);
         # refreshed from the group each step (valid_for)
         self.nesterov = bool(group.get("nesterov", False))
+        # amsgrad=True: the compact step keeps a running max of v (hparams.max_v)
+        self.amsgrad = self._amsgrad_of(group)
         self.d_counts = None
         self.cold_done = False
         self._nesterov = False
@@ -113,6 +115,12 @@ class StepPlan:
     def _maximize_of(self, group):
         return bool(group.get("maximize", False)) and not self.hooked
 
+    def _amsgrad_of(self, group):
+        """The group's amsgrad flag as this plan's kernels take it: the compact step, not
+        the in-backward batches nor the per-parameter update (which step without it,
+        optimizer.py:2360, :2373-2471)."""
+        return bool(group.get("amsgrad", False)) and self.kind == "compact" and not self.hooked
+
     # ------------------------------------------------------------------ validity
     def valid_for(self, group):
         """The reference's FastExecutionPlan.is_valid_for_step (optimizer.py:575-621):
@@ -128,6 +136,10 @@ class StepPlan:
         if bool(group.get("grad_centralization", False)) != self.gc:
             return False
         if self._maximize_of(group) != self.maximize:
+            return False
+        # amsgrad switched on or off: a new plan (FastExecutionPlan.is_valid_for_step,
+        # optimizer.py:585-586)
+        if self._amsgrad_of(group) != self.amsgrad:
             return False
         if self.kind == "q8":
             # cautious keeps every 8-bit tensor in the generic order: another table
@@ -236,6 +248,17 @@ class StepPlan:
                 counts[i] = (p.numel() + block - 1) // block
         self.host_table = tab          # parameter order
         self.factored = (tab["flags"] & np.uint32(L.FLAG_FACTORED)) != 0
+        self.max_v_ptrs = self.d_max_v = None
+        if self.amsgrad:
+            self.max_v_ptrs = np.zeros(n, dtype=np.uint64)
+            for i, (p, st) in enumerate(zip(self.params, self.states)):
+                mx, v = st.get("max_exp_avg_sq"), st.get("exp_avg_sq")
+                if (mx is None or v is None or tab[i]["flags"] & (L.FLAG_QUAD | L.FLAG_FACTORED)
+                        or mx.numel() != p.numel() or mx.dtype != v.dtype or not mx.is_contiguous()
+                        or mx.device != p.device):
+                    raise NotImplementedError(f"apexw_amd: amsgrad state of tensor {i} ({tuple(p.shape)}): "
+                                              "max_exp_avg_sq must be a contiguous full-size tensor in v's dtype")
+                self.max_v_ptrs[i] = mx.data_ptr()
         # per tensor {scale_v, sqrt(scale_v)} of this launch, for rows flagged APEXW_FLAG_VSCALE
         self.vscaled = (tab["flags"] & np.uint32(L.FLAG_VSCALE)) != 0
         self.d_vscale = self.h_vscale = None
@@ -361,6 +384,9 @@ class StepPlan:
         self.perm = perm
         self.fast = fast
         self.d_units = _upload(units.view(np.uint8), self.device)
+        if self.max_v_ptrs is not None:
+            # hparams.max_v: one pointer per descriptor, in device-table order
+            self.d_max_v = _upload(np.ascontiguousarray(self.max_v_ptrs[perm]), self.device)
         self.d_unit_begin = _upload(self.unit_begin, self.device)
         # the step kernels' units: all but the factored rows' (apexw_factored_step steps
         # those; the clip's norm pass still covers every unit).  Factored tensors are
@@ -468,6 +494,8 @@ class StepPlan:
         recomputed for all rows at once."""
         tab = self.host_table
         scalar = ((tab["p"] | tab["g"] | tab["m"] | tab["v"]) & np.uint64(15)) != 0
+        if self.max_v_ptrs is not None:
+            scalar |= (self.max_v_ptrs & np.uint64(15)) != 0
         if self.kind == "q8":
             scalar |= (tab["block"] % 8) != 0
         bit = np.uint32(L.FLAG_SCALAR)
@@ -967,6 +995,11 @@ class StepPlan:
             hp.grad_inv_scale = inv_scale
         if self.d_rows is not None:
             hp.rows = self.d_rows.data_ptr()
+        if self.amsgrad:
+            # amsgrad: the denominators take max(max_v, v) (optimizer.py:5788-5790, :1253-1255;
+            # torch._fused_adamw_ for the native plan)
+            flags |= L.HP_AMSGRAD
+            hp.max_v = self.d_max_v.data_ptr()
         hp.seed = seed
         hp.step = step & 0xFFFFFFFF
         hp.flags = flags

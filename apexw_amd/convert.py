@@ -79,6 +79,9 @@ def convert(p, st, group, peft):
                 "apexw_state_decode")
         L.check(lib.apexw_state_encode(ctypes.byref(_layout(target, n)), m32.data_ptr(), v32.data_ptr(), stream),
                 "apexw_state_encode")
+    if "max_exp_avg_sq" in target and "max_exp_avg_sq" in st:
+        # amsgrad's running max carries over, rounded to the new layout's dtype
+        target["max_exp_avg_sq"].copy_(src["max_exp_avg_sq"].reshape(target["max_exp_avg_sq"].shape))
     step = st.get("step")
     target["step"] = (step.detach().to("cpu", torch.float32).clone() if torch.is_tensor(step)
                       else torch.tensor(float(step or 0.0), dtype=torch.float32))

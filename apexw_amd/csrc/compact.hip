@@ -30,6 +30,9 @@ struct Ctx {
   float cq;                    // cautious: the tensor's 1 / mean(mask) (caut_q), else unused
 };
 
+// torch.maximum of two second moments: NaN when either is NaN
+APEXW_DEV float max_nan(float a, float b) { return (b > a || b != b) ? b : a; }
+
 // A 16-bit parameter stored through the reference's fp32 -> 16-bit copy
 // (_copy_fp32_to_16bit_sr_ without SR): fp16 is clamped to its range first.
 template <int PD> APEXW_DEV float store_p(float x) {
@@ -146,11 +149,12 @@ template <int PD, int MD> constexpr int caut_cold_dtype() {
 // e0 is the element index of slot 0 within the tensor (RNG counter).
 // SR: the launch's APEXW_HP_SR flag (a template parameter so that each path
 // compiles to its own code); APEXW_HP_SR_V implies it.
-// VAR: the launch may carry nesterov or cautious (APEXW_HP_NESTEROV / _CAUTIOUS); the
-// plain instantiation compiles without them and keeps its registers for the rest.
+// VAR: the launch may carry nesterov, cautious or amsgrad (APEXW_HP_NESTEROV /
+// _CAUTIOUS / _AMSGRAD); the plain instantiation compiles without them and keeps its
+// registers for the rest.  x: amsgrad's running max of v (8 entries, non-quad only).
 template <int PD, int GD, int MD, int VD, bool QUAD, bool SR, bool VAR>
-APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8], int cnt,
-                       uint32_t e0, const Ctx& c, bool gc, const float (&mean)[8]) {
+APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8], float (&x)[8], int cnt,
+                       uint32_t e0, const Ctx& c, bool gc, const float (&mean)[8], bool ams) {
   const apexw_hparams& hp = *c.hp;
   constexpr bool sr = SR;
   const bool srv = SR && (hp.flags & APEXW_HP_SR_V);
@@ -175,6 +179,9 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
   const bool san = (hp.flags & APEXW_HP_SANITIZE) && any_nonfinite8(g);
 #pragma unroll
   for (int j = 0; j < 8; ++j) g[j] = prep_grad<GD>(g[j], c, san, gc, mean[j]);
+  // ams (amsgrad): the denominator's v is max(max_v, v') (torch._foreach_maximum_ after
+  // the v update, apexw/optimizer.py:5788-5790, :1253-1255; inside torch._fused_adamw_ for
+  // the native mode)
 
   if constexpr (!QUAD) {
     if (hp.mode == APEXW_MODE_SINGLE) {
@@ -203,7 +210,13 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
       float mf = (hp.flags & APEXW_HP_LERP_HI) ? fmaf(hp.lerp_coef, g[j] - m[j], g[j])
                                                 : fmaf(hp.lerp_coef, g[j] - m[j], m[j]);
       float vf = v[j] * hp.beta2 + (hp.one_minus_beta2 * g[j]) * g[j];
-      float den = sqrtf(vf) / hp.bc2_sqrt + hp.eps;
+      float vs = vf;
+      if (ams) {
+        // the fp32 max feeds the denominator; the stored max is rounded
+        vs = max_nan(x[j], vf);
+        x[j] = rnd<VD>(vs);
+      }
+      float den = sqrtf(vs) / hp.bc2_sqrt + hp.eps;
       pf = pf - (hp.step_size * mf) / den;
       p[j] = rnd<PD>(pf);
       m[j] = rnd<MD>(mf);
@@ -294,6 +307,11 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
         vf = rnd<VD>(fmaf(omb2 * g[j], g[j], v1));
       }
       v[j] = vf;
+      if (ams) {
+        // both sides hold VD values: the max is exact
+        vf = max_nan(x[j], vf);
+        x[j] = vf;
+      }
       float den = rnd<VD>(q_sqrt<SR>(vf));
       den = rnd<VD>(den + eps_v);
       if (scaled) den = rnd<VD>(den / sqrt_scale_v);
@@ -321,8 +339,9 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
 }
 
 // Group k (512 elements, 8 per lane) of the unit starting at element `start`.
+// vmax: amsgrad's running max of v for this tensor (hparams.max_v), else NULL.
 template <int PD, int MD, int VD, bool QUAD, bool SR, bool VAR>
-APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const Ctx& c) {
+APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const Ctx& c, void* vmax) {
   constexpr int GD = PD;
   const int64_t n = t.n;
   const int lane = lane_id();
@@ -331,8 +350,9 @@ APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const 
     const int64_t e0 = start + (int64_t)(k * 64 + lane) * 8;
     if (e0 >= n) return;
     const int cnt = (int)((n - e0) < 8 ? (n - e0) : 8);
-    float p[8], g[8], m[8], v[8];
+    float p[8], g[8], m[8], v[8], x[8];
     const bool full = vec && cnt == 8;
+    const bool ams = VAR && !QUAD && vmax != nullptr;
     if (full) {
       load8<PD>(t.p, e0, p);
       load8<GD>(t.g, e0, g);
@@ -349,6 +369,7 @@ APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const 
         }
       } else {
         load8<VD>(t.v, e0, v);
+        if (ams) load8<VD>(vmax, e0, x);
       }
     } else {
 #pragma unroll
@@ -358,6 +379,7 @@ APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const 
         g[j] = ok ? load1<GD>(t.g, e0 + j) : 0.0f;
         m[j] = ok ? load1<MD>(t.m, e0 + j) : 0.0f;
         if constexpr (!QUAD) v[j] = ok ? load1<VD>(t.v, e0 + j) : 0.0f;
+        x[j] = (ams && ok) ? load1<VD>(vmax, e0 + j) : 0.0f;
       }
       if constexpr (QUAD) {
         v[0] = cnt >= 4 ? load1<VD>(t.v, e0 >> 2) : 0.0f;
@@ -372,7 +394,7 @@ APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const 
       cs.vscale = t.v_scale[0];
       cs.vscale_sqrt = t.v_scale[1];
     }
-    update8<PD, GD, MD, VD, QUAD, SR, VAR>(p, g, m, v, cnt, (uint32_t)e0, cs, gc, mean);
+    update8<PD, GD, MD, VD, QUAD, SR, VAR>(p, g, m, v, x, cnt, (uint32_t)e0, cs, gc, mean, ams);
     if (full) {
       store8<PD>(t.p, e0, p);
       store8<MD>(t.m, e0, m);
@@ -387,6 +409,7 @@ APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const 
         }
       } else {
         store8<VD>(t.v, e0, v);
+        if (ams) store8<VD>(vmax, e0, x);
       }
     } else {
 #pragma unroll
@@ -395,6 +418,7 @@ APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const 
           store1<PD>(t.p, e0 + j, p[j]);
           store1<MD>(t.m, e0 + j, m[j]);
           if constexpr (!QUAD) store1<VD>(t.v, e0 + j, v[j]);
+          if (ams) store1<VD>(vmax, e0 + j, x[j]);
         }
       }
       if constexpr (QUAD) {
@@ -407,29 +431,29 @@ APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const 
 
 template <bool SR, bool VAR>
 APEXW_DEV void dispatch_group(const apexw_tensor& t, int64_t start, int k, const Ctx& c, uint32_t pd, uint32_t md,
-                              uint32_t vd, bool quad) {
+                              uint32_t vd, bool quad, void* vmax) {
   if (md == APEXW_F32) {
     // fp32 moments ("full" precision, small "auto" tensors): fp32 v, no quad (checked on the host)
-    if (pd == APEXW_F32) compact_group<APEXW_F32, APEXW_F32, APEXW_F32, false, SR, VAR>(t, start, k, c);
-    else if (pd == APEXW_BF16) compact_group<APEXW_BF16, APEXW_F32, APEXW_F32, false, SR, VAR>(t, start, k, c);
-    else compact_group<APEXW_F16, APEXW_F32, APEXW_F32, false, SR, VAR>(t, start, k, c);
+    if (pd == APEXW_F32) compact_group<APEXW_F32, APEXW_F32, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax);
+    else if (pd == APEXW_BF16) compact_group<APEXW_BF16, APEXW_F32, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax);
+    else compact_group<APEXW_F16, APEXW_F32, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax);
     return;
   }
   if (pd == APEXW_F16) {
     // fp16 parameters keep fp16 m (and fp16 or fp32 v)
-    if (vd == APEXW_F32) compact_group<APEXW_F16, APEXW_F16, APEXW_F32, false, SR, VAR>(t, start, k, c);
-    else if (quad) compact_group<APEXW_F16, APEXW_F16, APEXW_F16, true, SR, VAR>(t, start, k, c);
-    else compact_group<APEXW_F16, APEXW_F16, APEXW_F16, false, SR, VAR>(t, start, k, c);
+    if (vd == APEXW_F32) compact_group<APEXW_F16, APEXW_F16, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax);
+    else if (quad) compact_group<APEXW_F16, APEXW_F16, APEXW_F16, true, SR, VAR>(t, start, k, c, vmax);
+    else compact_group<APEXW_F16, APEXW_F16, APEXW_F16, false, SR, VAR>(t, start, k, c, vmax);
     return;
   }
   if (pd == APEXW_F32) {
-    if (vd == APEXW_F32) compact_group<APEXW_F32, APEXW_BF16, APEXW_F32, false, SR, VAR>(t, start, k, c);
-    else if (quad) compact_group<APEXW_F32, APEXW_BF16, APEXW_BF16, true, SR, VAR>(t, start, k, c);
-    else compact_group<APEXW_F32, APEXW_BF16, APEXW_BF16, false, SR, VAR>(t, start, k, c);
+    if (vd == APEXW_F32) compact_group<APEXW_F32, APEXW_BF16, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax);
+    else if (quad) compact_group<APEXW_F32, APEXW_BF16, APEXW_BF16, true, SR, VAR>(t, start, k, c, vmax);
+    else compact_group<APEXW_F32, APEXW_BF16, APEXW_BF16, false, SR, VAR>(t, start, k, c, vmax);
   } else {
-    if (vd == APEXW_F32) compact_group<APEXW_BF16, APEXW_BF16, APEXW_F32, false, SR, VAR>(t, start, k, c);
-    else if (quad) compact_group<APEXW_BF16, APEXW_BF16, APEXW_BF16, true, SR, VAR>(t, start, k, c);
-    else compact_group<APEXW_BF16, APEXW_BF16, APEXW_BF16, false, SR, VAR>(t, start, k, c);
+    if (vd == APEXW_F32) compact_group<APEXW_BF16, APEXW_BF16, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax);
+    else if (quad) compact_group<APEXW_BF16, APEXW_BF16, APEXW_BF16, true, SR, VAR>(t, start, k, c, vmax);
+    else compact_group<APEXW_BF16, APEXW_BF16, APEXW_BF16, false, SR, VAR>(t, start, k, c, vmax);
   }
 }
 
@@ -566,8 +590,9 @@ __global__ __launch_bounds__(256) void compact_step_kernel(const apexw_tensor* _
     if (quad && hp.mode == APEXW_MODE_SINGLE) continue;  // rejected on the host; never read v out of range
     if (t.flags & APEXW_FLAG_FACTORED) continue;        // stepped by apexw_factored_step
     if (VAR && (hp.flags & APEXW_HP_CAUTIOUS)) c.cq = caut_q(hp.counts[un.tensor], t.n, quad, pd);
-    if (sr) dispatch_group<true, VAR>(t, start, k, c, pd, md, vd, quad);
-    else dispatch_group<false, VAR>(t, start, k, c, pd, md, vd, quad);
+    void* vmax = (VAR && (hp.flags & APEXW_HP_AMSGRAD) && !quad) ? hp.max_v[un.tensor] : nullptr;
+    if (sr) dispatch_group<true, VAR>(t, start, k, c, pd, md, vd, quad, vmax);
+    else dispatch_group<false, VAR>(t, start, k, c, pd, md, vd, quad, vmax);
   }
 }
 
@@ -594,8 +619,8 @@ int apexw_launch_compact(const apexw_tensor* tensors, int64_t n_units, const ape
   // resident grid striding over the whole launch).  Launches that a resident grid
   // covers in a few passes keep it (C2, 124 M elements: 0.234-0.257 ms against
   // 0.252-0.288 with a workgroup per unit).
-  // nesterov / cautious launches take the instantiation that holds them
-  const bool var = hp->flags & (APEXW_HP_NESTEROV | APEXW_HP_CAUTIOUS);
+  // nesterov / cautious / amsgrad launches take the instantiation that holds them
+  const bool var = hp->flags & (APEXW_HP_NESTEROV | APEXW_HP_CAUTIOUS | APEXW_HP_AMSGRAD);
   const void* kernel = var ? (const void*)compact_step_kernel<true> : (const void*)compact_step_kernel<false>;
   const int resident = apexw_resident_grid(kernel, n_units * kGroups);
   const int grid = n_units > (int64_t)resident * 8 ? (int)(n_units < INT32_MAX ? n_units : INT32_MAX) : resident;

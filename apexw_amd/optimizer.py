@@ -39,20 +39,25 @@ DOWNCAST_MIN_NUMEL = 1024          # optimizer.py:2100
 HOOK_MIN_NUMEL = 16384             # optimizer.py:2131
 HOOK_BATCH = 14                    # optimizer.py:2142
 
-_UNSUPPORTED_FLAGS = ("amsgrad", "lion", "capturable", "differentiable", "auto_pack")
-def _check_variants(precision, factored, nesterov, cautious, maximize=False):
+_UNSUPPORTED_FLAGS = ("lion", "capturable", "differentiable", "auto_pack")
+def _check_variants(precision, factored, nesterov, cautious, maximize=False, amsgrad=False):
     """nesterov=True, cautious=True and maximize=True run in every precision: the
     8-bit and ultra steps' lookahead numerator lerp(g, m, beta1) without the SNR gain
     and the compact, full and auto steps' two addcdiv passes (lerp(g, m, beta1) for
     quad v); the numerator m times the sign-agreement mask over its mean; the negated
-    grads.  Factored second moments, and nesterov together with cautious, do not."""
-    for name, on in (("nesterov", nesterov), ("cautious", cautious), ("maximize", maximize)):
+    grads.  amsgrad=True runs in the compact, full and auto precisions (a running max
+    of v beside it, no quad v).  Factored second moments, nesterov together with
+    cautious, and amsgrad in the 8bit and ultra precisions do not."""
+    for name, on in (("nesterov", nesterov), ("cautious", cautious), ("maximize", maximize),
+                     ("amsgrad", amsgrad)):
         if not on:
             continue
         if factored:
             raise NotImplementedError(f"apexw_amd: {name}=True with factored_v")
     if nesterov and cautious:
         raise NotImplementedError("apexw_amd: nesterov=True together with cautious=True")
+    if amsgrad and precision in ("8bit", "ultra"):
+        raise NotImplementedError(f"apexw_amd: amsgrad=True with precision={precision!r}")
 
 
 class ApexW(Optimizer):
@@ -149,8 +154,8 @@ class ApexW(Optimizer):
         if bad or beta3 is not None:
             what = ", ".join(bad + (["beta3"] if beta3 is not None else []))
             raise NotImplementedError(f"apexw_amd implements the standard AdamW step; not supported: {what}")
-        if nesterov or cautious or maximize:
-            _check_variants(S.normalize_precision(precision), factored_v, nesterov, cautious, maximize)
+        if nesterov or cautious or maximize or amsgrad:
+            _check_variants(S.normalize_precision(precision), factored_v, nesterov, cautious, maximize, amsgrad)
         if precision == "compact" and betas[1] >= 0.99 and not stochastic_rounding and not adamw_compat:
             warnings.warn(
                 f"ApexW: beta2={betas[1]} with precision='compact' and stochastic_rounding=False "
@@ -340,10 +345,19 @@ class ApexW(Optimizer):
                 self.state[p].update(S.init_state(p, group, peft, has16))
             if p.dtype == torch.float16 and self.state[p].get("is_factored_v", False):
                 raise NotImplementedError("apexw_amd: factored_v with fp16 parameters")
-        if group.get("nesterov", False) or group.get("cautious", False) or group.get("maximize", False):
+        ams = bool(group.get("amsgrad", False))
+        if group.get("nesterov", False) or group.get("cautious", False) or group.get("maximize", False) or ams:
             _check_variants(group["precision"], any(self.state[p].get("is_factored_v", False) for p in params),
                             bool(group.get("nesterov", False)), bool(group.get("cautious", False)),
-                            bool(group.get("maximize", False)))
+                            bool(group.get("maximize", False)), ams)
+        if ams:
+            for p in params:
+                st = self.state[p]
+                if st["exp_avg_sq"].numel() != p.numel():
+                    # quad v laid out before amsgrad was switched on: the reference's
+                    # torch._foreach_maximum_ over max_v (numel) and v (numel / 4) fails too
+                    raise NotImplementedError("apexw_amd: amsgrad=True on a tensor whose state holds quad v")
+                S.ensure_max_v(st, p)         # amsgrad switched on after the first step (optimizer.py:2917-2922)
         if group["precision"] in ("8bit", "ultra"):
             # both run the reference's _step_ultra (optimizer.py:3583-3587)
             return StepPlan(self, group, params, "q8")
@@ -406,6 +420,8 @@ class ApexW(Optimizer):
         if any(p.dtype == torch.float16 for g in self.param_groups for p in g["params"]):
             # an fp16 v holds the moment times its dynamic scale; no conversion of it here
             raise NotImplementedError("apexw_amd: set_precision with fp16 parameters")
+        if prec == "8bit" and any(g.get("amsgrad", False) for g in self.param_groups):
+            raise NotImplementedError("apexw_amd: amsgrad=True with precision='8bit'")
         peft = S.detect_peft_context(self.param_groups)
         for group in self.param_groups:
             group["precision"] = prec
@@ -427,7 +443,7 @@ class ApexW(Optimizer):
         models (optimizer.py:2059-2167)."""
         d = self.defaults
         if not force and (d.get("clip_grad_norm") is not None or d.get("grad_centralization", False)
-                          or d.get("nesterov", False) or d.get("maximize", False)):
+                          or d.get("nesterov", False) or d.get("maximize", False) or d.get("amsgrad", False)):
             return
         trainable = []
         total = 0

@@ -121,11 +121,11 @@ def block_size_8bit(p, user_bs):
 
 def _auto_subbyte(p, group, bs, factored=False):
     """NF4 m + quad v eligibility (optimizer.py:2192-2201, the same rule in _init_group,
-    where a factored tensor never takes it)."""
+    where a factored tensor never takes it; never under amsgrad)."""
     n = p.numel()
     raw_int4 = group.get("int4_m", group.get("four_bit", None))
     pow2 = bs >= 64 and (bs & (bs - 1)) == 0
-    return (raw_int4 is not False and not factored and n >= 16384 and n % 4 == 0 and pow2
+    return (raw_int4 is not False and not factored and not group.get("amsgrad", False) and n >= 16384 and n % 4 == 0 and pow2
             and (p.dim() < 2 or min(p.shape) >= 8))
 
 
@@ -135,10 +135,10 @@ SIX_BIT_MIN = 524288            # optimizer.py:2667-2673
 M6_ZERO = (0xDF, 0xF7, 0x7D)    # four codes of 31 (zero) in three bytes
 
 
-def _can_factor(p, is_peft, min_numel):
-    """Factored row/column v: 2-D+ real tensors, not PEFT, >= min_numel elements,
-    rows = shape[0] >= 128 and cols = numel / rows >= 128 (apexw/state.py:234-281)."""
-    if p.dim() < 2 or torch.is_complex(p) or p.dtype == torch.float64:
+def _can_factor(p, is_peft, min_numel, amsgrad=False):
+    """Factored row/column v: 2-D+ real tensors, not under amsgrad, not PEFT, >= min_numel
+    elements, rows = shape[0] >= 128 and cols = numel / rows >= 128 (apexw/state.py:234-281)."""
+    if amsgrad or p.dim() < 2 or torch.is_complex(p) or p.dtype == torch.float64:
         return False
     rows = p.shape[0]
     cols = p.numel() // rows
@@ -214,7 +214,26 @@ def init_state(p, group, peft_ctx, has_16bit_params=False):
     """Fresh state dict for ``p`` (keys and dtypes as the reference's _init_group).
 
     has_16bit_params: whether any parameter of the optimizer is 16-bit (the
-    "auto" precision keeps fp32 moments only when none is)."""
+    "auto" precision keeps fp32 moments only when none is).  amsgrad adds
+    ``max_exp_avg_sq`` (ensure_max_v)."""
+    st = _init_state(p, group, peft_ctx, has_16bit_params)
+    if group.get("amsgrad", False):
+        ensure_max_v(st, p)
+    return st
+
+
+def ensure_max_v(st, p):
+    """amsgrad's running max of v: numel zeros in p's shape, fp32 for quantized v, else
+    v's dtype (optimizer.py:2878-2886), created when missing (at init, or on the first
+    step after amsgrad is switched on: :2917-2922)."""
+    if "max_exp_avg_sq" in st:
+        return
+    quantized = st.get("is_8bit", False) or st.get("is_ultra", False)
+    dt = torch.float32 if quantized else st.get("state_dtype_v", st.get("state_dtype", p.dtype))
+    st["max_exp_avg_sq"] = torch.zeros(p.numel(), dtype=dt, device=p.device).reshape(p.shape)
+
+
+def _init_state(p, group, peft_ctx, has_16bit_params):
     prec = group["precision"]
     beta2 = group["betas"][1]
     sr = bool(group.get("stochastic_rounding", True))
@@ -222,6 +241,7 @@ def init_state(p, group, peft_ctx, has_16bit_params=False):
     n = p.numel()
     st = {"stochastic_rounding": sr, "step": torch.tensor(0.0, dtype=torch.float32)}
     is_peft = is_peft_parameter(p) or peft_ctx
+    ams = bool(group.get("amsgrad", False))
     large = p.dim() >= 2 or n >= group.get("threshold", 65536)
     if group.get("fused") is True or prec == "full":
         # optimizer.py:2625-2626, :2769-2772
@@ -247,14 +267,14 @@ def init_state(p, group, peft_ctx, has_16bit_params=False):
                                                                                    is_peft)
         if fp32_training or not large:
             return _moments(st, p, torch.float32, group, is_peft, prec)
-        if bool(group.get("factored_v", False)) and _can_factor(p, is_peft, FACTORED_MIN_COMPACT):
+        if bool(group.get("factored_v", False)) and _can_factor(p, is_peft, FACTORED_MIN_COMPACT, ams):
             st["is_factored_v"] = True
             return _factored_compact(st, p)
         return _moments(st, p, compact_dtype(p), group, is_peft, prec)
     if prec == "8bit" and n >= 64:
         bs = block_size_8bit(p, group.get("block_size"))
         narrow = p.dim() >= 2 and min(p.shape) <= 32 and n < 2048
-        factored = bool(group.get("factored_v", False)) and _can_factor(p, is_peft, FACTORED_MIN_8BIT)
+        factored = bool(group.get("factored_v", False)) and _can_factor(p, is_peft, FACTORED_MIN_8BIT, ams)
         auto_sub = _auto_subbyte(p, group, bs, factored)
         raw_int4 = group.get("int4_m", group.get("four_bit", None))
         six = bool(group.get("six_bit", False)) and factored and n >= SIX_BIT_MIN and bs % 4 == 0
@@ -264,7 +284,7 @@ def init_state(p, group, peft_ctx, has_16bit_params=False):
     if prec == "8bit":
         st.update(is_8bit=False, is_factored_v=False, is_6bit_m=False, is_4bit_m=False, is_quad_v=False)
     else:
-        factored = bool(group.get("factored_v", False)) and _can_factor(p, is_peft, FACTORED_MIN_COMPACT)
+        factored = bool(group.get("factored_v", False)) and _can_factor(p, is_peft, FACTORED_MIN_COMPACT, ams)
         st.update(is_6bit_m=False, is_4bit_m=False, is_factored_v=factored)
         if factored:
             return _factored_compact(st, p)
@@ -284,13 +304,15 @@ def _factored_compact(st, p):
 
 def _moments(st, p, mdt, group, is_peft, prec):
     """Dense m in ``mdt``, v in the beta2 rule's dtype, quad v for large 16-bit
-    compact / auto tensors, not under nesterov (optimizer.py:2788-2810, :2838-2872)."""
+    compact / auto tensors, not under nesterov or amsgrad (optimizer.py:2788-2810,
+    :2838-2872)."""
     n, dev = p.numel(), p.device
     vdt = v_dtype_for_beta2(mdt, group["betas"][1], group.get("force_compact_v", False),
                             bool(group.get("stochastic_rounding", True)))
     quad = (prec in ("compact", "auto") and mdt in (torch.bfloat16, torch.float16)
             and vdt in (torch.bfloat16, torch.float16)
             and group.get("int4_m", None) is not False and not group.get("nesterov", False)
+            and not group.get("amsgrad", False)
             and n >= 16384 and n % 4 == 0
             and (p.dim() < 2 or min(p.shape) >= 8)
             and (is_peft or len(group["params"]) >= 8))

@@ -44,7 +44,7 @@
 extern "C" {
 #endif
 
-#define APEXW_ABI_VERSION 21
+#define APEXW_ABI_VERSION 22
 
 /* status codes */
 enum apexw_status {
@@ -166,6 +166,13 @@ typedef struct apexw_unit {
                                           apexw_q8_cautious_count); the blocks take it with
                                           look_coef = 0 under APEXW_HP_LOOK_HI (numerator m', no
                                           lookahead) and gain_lo = 0 */
+#define APEXW_HP_AMSGRAD (1u << 11)    /* amsgrad=True.  Compact step (cold, replay and native modes;
+                                          full-size v only, quad descriptors ignore it): the
+                                          denominator takes vmax = max(max_v[t], v') instead of v'
+                                          and vmax is stored back to max_v[t] (VDT dtype, n elements,
+                                          16-byte aligned unless APEXW_FLAG_SCALAR).  Cold and replay:
+                                          v' as stored; native: the fp32 v' (torch._fused_adamw_),
+                                          vmax stored rounded.  A NaN on either side gives NaN. */
 
 /* Step scalars of one launch, written on the device by apexw_amp_prepare (32 bytes). */
 typedef struct apexw_amp_dyn {
@@ -205,7 +212,9 @@ typedef struct apexw_hparams {
   const apexw_row_means* rows;  /* 8-bit / ultra tables with APEXW_FLAG_GC rows: one entry per
                                    descriptor of the table, else NULL */
   unsigned long long* counts;   /* APEXW_HP_CAUTIOUS: one counter per descriptor of the table */
-} apexw_hparams;          /* 112 bytes */
+  void* const* max_v;           /* APEXW_HP_AMSGRAD: one device pointer per descriptor of the table
+                                   (the running max of v), in device memory, else NULL */
+} apexw_hparams;          /* 120 bytes */
 
 /*
  * GradScaler hands the optimizer its scale and found_inf as device tensors

@@ -1,7 +1,7 @@
 """Compact-mode multi-tensor AdamW step (CPU oracle; test infrastructure only).
 
 Restates ``ApexW._multi_tensor_step`` (``apexw/optimizer.py:5297-5887``) for the
-AdamW update and its nesterov and cautious variants (no amsgrad / lion / AdEMAMix)
+AdamW update and its nesterov, cautious and amsgrad variants (no lion / AdEMAMix)
 with the same torch ops, so every bf16 rounding point of the reference is
 reproduced:
 
@@ -18,7 +18,9 @@ reproduced:
    to p's dtype and never stochastic (:5865-5877); quad: ``lerp(g, m, b1)`` in place of m (:5732-5733);
    cautious: m times the mask ``g m >= 0`` over its mean (clamped at 1e-3), the mask, its mean
    and the product in the parameter's / m's dtype, then one ``addcdiv`` (:5847-5864); quad:
-   the same in fp32 (:5728-5731)
+   the same in fp32 (:5728-5731);
+   amsgrad: ``max_v = maximum(max_v, v)`` after the v EMA and ``d`` from max_v instead of v
+   (:5788-5790; the quad branch :5700-5702 is never reached, quad v being off under amsgrad)
 
 That is the *cold* step, taken whenever the optimizer (re)builds its cached
 execution plan.  Every later step replays the plan through
@@ -77,6 +79,15 @@ def _denominators(vs, eps_scaled, scale_v, sqrt_scale_v):
     return dens
 
 
+def _amsgrad_max(max_vs, vs):
+    """amsgrad: max_v = maximum(max_v, v) in place and the denominators' source
+    (optimizer.py:5788-5790, :1253-1255); plain v otherwise."""
+    if max_vs is None:
+        return vs
+    torch._foreach_maximum_(max_vs, vs)
+    return max_vs
+
+
 def _quad_cautious(g, m):
     """fp32 numerator m * mask / mean(mask) of a quad-v tensor (optimizer.py:5728-5731, :1272-1275)."""
     mask = (g * m >= 0).to(torch.float32)
@@ -100,7 +111,7 @@ def _masked(nums, lhs, rhs, params):
 
 def compact_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weight_decay,
                           decay_norm_only, step, is_quad, stochastic, scale_v=1.0, sqrt_scale_v=1.0,
-                          nesterov=False, cautious=False):
+                          nesterov=False, cautious=False, max_vs=None):
     """One step over a subgroup sharing (p dtype, m dtype, step count, quad flag).
 
     ``step`` is the already-incremented step count.  Tensors are updated in place.
@@ -125,6 +136,8 @@ def compact_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weigh
         raise NotImplementedError(f"oracle compact step: m dtype {ms[0].dtype}")
     v16 = vs[0].dtype in (torch.bfloat16, torch.float16)
     if is_quad:
+        if max_vs is not None:
+            raise NotImplementedError("oracle compact step: amsgrad with quad v")
         gq = [g.reshape(-1, 4).square().mean(dim=1) for g in gf]
         if beta2 >= 0.995 and stochastic and v16:
             for v, q in zip(vs, gq):
@@ -150,7 +163,7 @@ def compact_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weigh
     else:
         torch._foreach_mul_(vs, beta2)
         torch._foreach_addcmul_(vs, gf, gf, value=(1.0 - beta2) * scale_v)
-    dens = _denominators(vs, eps_scaled, scale_v, sqrt_scale_v)
+    dens = _denominators(_amsgrad_max(max_vs, vs), eps_scaled, scale_v, sqrt_scale_v)
     if cautious:
         # fp32 p with 16-bit m takes m upcast (optimizer.py:5834-5838); the mask from
         # g.float() * num.float() (:5851-5853)
@@ -172,7 +185,7 @@ def compact_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weigh
 
 def replay_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weight_decay,
                          apply_wd_mask, step, is_quad, stochastic, scale_v=1.0, sqrt_scale_v=1.0,
-                         nesterov=False, cautious=False):
+                         nesterov=False, cautious=False, max_vs=None):
     """One replayed step over an (p dtype, compact, quad) subgroup (optimizer.py:1200-1338).
 
     With an fp16 parameter, m or v the denominators are clamped below by eps
@@ -191,6 +204,8 @@ def replay_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weight
     v16 = vs[0].dtype in (torch.bfloat16, torch.float16)
     sr_v = beta2 >= 0.995 and stochastic and v16
     if is_quad:
+        if max_vs is not None:
+            raise NotImplementedError("oracle compact replay: amsgrad with quad v")
         gf = grads if grads[0].dtype == torch.float32 else [g.float() for g in grads]
         gq = [g.reshape(-1, 4).square().mean(dim=1) for g in gf]
         if sr_v:
@@ -220,7 +235,7 @@ def replay_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weight
     else:
         torch._foreach_mul_(vs, beta2)
         torch._foreach_addcmul_(vs, grads, grads, value=(1.0 - beta2) * scale_v)
-    dens = _denominators(vs, eps_scaled, scale_v, sqrt_scale_v)
+    dens = _denominators(_amsgrad_max(max_vs, vs), eps_scaled, scale_v, sqrt_scale_v)
     if has_fp16:
         torch._foreach_clamp_min_(dens, eps)
     if cautious:

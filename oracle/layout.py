@@ -68,10 +68,10 @@ def block_size_8bit(p, user_bs):
     return 64
 
 
-def can_factor(p, is_peft, min_numel):
-    """state.py:234-281: 2-D+, not PEFT, >= min_numel (65536 for 8bit, 524288 for
-    compact), rows = shape[0] >= 128, cols = numel / rows >= 128."""
-    if p.dim() < 2 or torch.is_complex(p) or p.dtype == torch.float64 or is_peft or p.numel() < min_numel:
+def can_factor(p, is_peft, min_numel, amsgrad=False):
+    """state.py:234-281: 2-D+, not amsgrad, not PEFT, >= min_numel (65536 for 8bit,
+    524288 for compact), rows = shape[0] >= 128, cols = numel / rows >= 128."""
+    if amsgrad or p.dim() < 2 or torch.is_complex(p) or p.dtype == torch.float64 or is_peft or p.numel() < min_numel:
         return False
     return p.shape[0] >= 128 and p.numel() // p.shape[0] >= 128
 
@@ -87,13 +87,33 @@ def init_state(p, group, n_params_in_group, peft_ctx, has_16bit_params=None, cud
     """Allocate and return a fresh state dict for parameter ``p``.
 
     has_16bit_params: whether any parameter of the optimizer is 16-bit (None:
-    this parameter's group decides); cuda: lay out as for a CUDA parameter."""
+    this parameter's group decides); cuda: lay out as for a CUDA parameter.
+    amsgrad adds ``max_exp_avg_sq``: numel zeros in p's shape, fp32 for quantized v,
+    else v's dtype (optimizer.py:2878-2886)."""
+    st = _init_state(p, group, n_params_in_group, peft_ctx, has_16bit_params, cuda)
+    if group.get("amsgrad", False):
+        ensure_max_v(st, p)
+    return st
+
+
+def ensure_max_v(st, p):
+    """amsgrad's running max of v, created when missing (at init, or on the first step
+    after amsgrad is switched on: optimizer.py:2917-2922)."""
+    if "max_exp_avg_sq" in st:
+        return
+    quantized = st.get("is_8bit", False) or st.get("is_ultra", False)
+    dt = torch.float32 if quantized else st.get("state_dtype_v", st.get("state_dtype", p.dtype))
+    st["max_exp_avg_sq"] = torch.zeros(p.numel(), dtype=dt, device=p.device).reshape(p.shape)
+
+
+def _init_state(p, group, n_params_in_group, peft_ctx, has_16bit_params, cuda):
     prec = group["precision"]
     beta2 = group["betas"][1]
     sr = bool(group["stochastic_rounding"])
     st = {"stochastic_rounding": sr, "step": torch.tensor(0.0, dtype=torch.float32)}
     n = p.numel()
     is_peft = is_peft_param(p) or peft_ctx
+    ams = bool(group.get("amsgrad", False))
     threshold = group.get("threshold", 65536)
     massive = p.dim() >= 2 or n >= threshold
     if group.get("fused") is True or prec == "full":
@@ -125,7 +145,7 @@ def init_state(p, group, n_params_in_group, peft_ctx, has_16bit_params=None, cud
         if not massive:
             return _dense(st, p, torch.float32, group, is_peft, n_params_in_group, prec)
         cdt = compact_dtype(p)
-        if bool(group.get("factored_v", False)) and can_factor(p, is_peft, 524288):
+        if bool(group.get("factored_v", False)) and can_factor(p, is_peft, 524288, ams):
             st["is_factored_v"] = True
             return _factored_compact(st, p, cdt)
         return _dense(st, p, cdt, group, is_peft, n_params_in_group, prec)
@@ -134,8 +154,8 @@ def init_state(p, group, n_params_in_group, peft_ctx, has_16bit_params=None, cud
         narrow = p.dim() >= 2 and min(p.shape) <= 32 and n < 2048
         raw_int4 = group.get("int4_m")
         pow2 = bs >= 64 and (bs & (bs - 1)) == 0
-        fv = bool(group.get("factored_v", False)) and can_factor(p, is_peft, 65536)
-        auto_sub = (raw_int4 is not False and not fv and n >= 16384 and n % 4 == 0 and pow2
+        fv = bool(group.get("factored_v", False)) and can_factor(p, is_peft, 65536, ams)
+        auto_sub = (raw_int4 is not False and not fv and not ams and n >= 16384 and n % 4 == 0 and pow2
                     and (p.dim() < 2 or min(p.shape) >= 8))
         six = bool(group.get("six_bit", False)) and fv and n >= 524288 and bs % 4 == 0
         int4 = auto_sub or (bool(raw_int4) and not fv and n >= 512 and n >= bs and not narrow and not is_peft)
@@ -166,7 +186,7 @@ def init_state(p, group, n_params_in_group, peft_ctx, has_16bit_params=None, cud
     if prec == "8bit":
         st.update(is_8bit=False, is_factored_v=False, is_6bit_m=False, is_4bit_m=False, is_quad_v=False)
     elif prec == "compact":
-        fv = bool(group.get("factored_v", False)) and can_factor(p, is_peft, 524288)
+        fv = bool(group.get("factored_v", False)) and can_factor(p, is_peft, 524288, ams)
         st.update(is_6bit_m=False, is_4bit_m=False, is_factored_v=fv)
         if fv:
             return _factored_compact(st, p, compact_dtype(p))
@@ -190,13 +210,14 @@ def _factored_compact(st, p, mdt):
 
 def _dense(st, p, mdt, group, is_peft, n_params_in_group, prec):
     """m in ``mdt``, v in the dtype the beta2 rule gives, quad-shared v for large
-    16-bit compact/auto tensors, not under nesterov (optimizer.py:2788-2810, :2838-2872)."""
+    16-bit compact/auto tensors, not under nesterov or amsgrad (optimizer.py:2788-2810,
+    :2838-2872)."""
     n = p.numel()
     vdt = v_dtype(mdt, group["betas"][1], group.get("force_compact_v", False), bool(group["stochastic_rounding"]))
     quad = (prec in ("compact", "auto") and mdt in (torch.bfloat16, torch.float16)
             and vdt in (torch.bfloat16, torch.float16)
             and group.get("int4_m") is not False and not group.get("nesterov", False)
-            and n >= 16384 and n % 4 == 0
+            and not group.get("amsgrad", False) and n >= 16384 and n % 4 == 0
             and (p.dim() < 2 or min(p.shape) >= 8) and (is_peft or n_params_in_group >= 8))
     if quad:
         st["is_quad_v"] = True

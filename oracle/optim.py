@@ -18,7 +18,8 @@ steps like ``8bit`` through ``_step_ultra``; ``full`` and ``auto`` like
   ``torch._fused_adamw_`` for the native path), then for 8bit ``_step_ultra`` per parameter, and for compact
   either ``torch._fused_adamw_`` when every state matches its parameter's dtype
   and size (optimizer.py:3683-3766, ``_fused_step`` :4737-4835) or the foreach
-  path over (p dtype, m dtype, step, quad) subgroups (:5369-5381).
+  path over (p dtype, m dtype, step, quad) subgroups (:5369-5381); amsgrad keeps a
+  running max of v beside each of them (the 8bit and ultra precisions excepted).
 
 Like the reference, the first step after the set of parameters-with-grad changes
 is a *cold* step; it caches a plan and the following steps *replay* it
@@ -67,7 +68,7 @@ class OracleApexW:
                  adamw_compat=False, clip_grad_norm=None, precision="compact", stochastic_rounding=True,
                  block_size=None, force_compact_v=False, int4_m=None, grad_centralization=False,
                  factored_v=False, six_bit=False, threshold=65536, amp=None, dynamic_scaling=True, nesterov=False,
-                 cautious=False, maximize=False):
+                 cautious=False, maximize=False, amsgrad=False, fused=None):
         precision = normalize_precision(precision)
         if betas is None:
             betas = (0.9, 0.999) if precision in ("8bit", "full") else (0.9, 0.99)
@@ -82,7 +83,8 @@ class OracleApexW:
                           block_size=block_size, force_compact_v=force_compact_v, int4_m=int4_m,
                           grad_centralization=grad_centralization, factored_v=factored_v, six_bit=six_bit,
                           threshold=threshold, amp=amp, dynamic_scaling=dynamic_scaling, nesterov=bool(nesterov),
-                          cautious=bool(cautious), maximize=bool(maximize), params=self.params)
+                          cautious=bool(cautious), maximize=bool(maximize), amsgrad=bool(amsgrad),
+                          fused=fused, params=self.params)
         self.state = {}
         self._plan = None
         self.grad_scale = None
@@ -94,6 +96,9 @@ class OracleApexW:
             return False
         active = set(plan["params"])
         if any(p.grad is None for p in plan["params"]):
+            return False
+        # amsgrad switched on or off since the plan was made (optimizer.py:585-586)
+        if plan["amsgrad"] != self.group["amsgrad"]:
             return False
         return all(p.grad is None for p in self.params if p.requires_grad and p not in active)
 
@@ -163,7 +168,12 @@ class OracleApexW:
         for p in plist:
             if p not in self.state:
                 self.state[p] = L.init_state(p, grp, len(self.params), peft)
+            elif grp["amsgrad"] and not grp["precision"] in ("8bit", "ultra"):
+                L.ensure_max_v(self.state[p], p)      # amsgrad switched on later (optimizer.py:2917-2922)
         prec = grp["precision"]
+        ams = grp["amsgrad"]
+        if ams and prec in ("8bit", "ultra"):
+            raise NotImplementedError("oracle: amsgrad in the 8bit / ultra precisions")
         quantized = prec in ("8bit", "ultra")     # both run _step_ultra (optimizer.py:3583-3587)
         grads, scale = self._prepare(self._signed([p.grad for p in plist], quantized),
                                      sanitize=not quantized or grp["clip_grad_norm"] is not None)
@@ -174,15 +184,16 @@ class OracleApexW:
                 st["step"].add_(1)
                 q8_param_step(p, g, st, step=st["step"].item(), inv_scale=self._inv(scale), nesterov=grp["nesterov"],
                               cautious=grp["cautious"], maximize=grp["maximize"], **kw)
-            self._plan = {"kind": "8bit", "params": plist}
+            self._plan = {"kind": "8bit", "params": plist, "amsgrad": ams}
             return
         sts = [self.state[p] for p in plist]
         homogeneous = all("exp_avg_sq" in st and st["exp_avg"].dtype == st["exp_avg_sq"].dtype == p.dtype
                           and st["exp_avg"].numel() == st["exp_avg_sq"].numel() for p, st in zip(plist, sts))
-        if homogeneous and not (grp["maximize"] or grp["nesterov"] or grp["cautious"]):
-            # maximize, nesterov and cautious leave the native fused step (optimizer.py:3733, :593-600)
-            self._native_fused(plist, grads, sts, grad_scale=scale, **kw)
-            self._plan = {"kind": "native", "params": plist}
+        if homogeneous and grp["fused"] is not False and not (grp["maximize"] or grp["nesterov"] or grp["cautious"]):
+            # maximize, nesterov and cautious leave the native fused step (optimizer.py:3733, :593-600),
+            # and so does fused=False (:3723)
+            self._native_fused(plist, grads, sts, grad_scale=scale, amsgrad=ams, **kw)
+            self._plan = {"kind": "native", "params": plist, "amsgrad": ams}
             return
         # factored-v tensors: their own update with their own step (optimizer.py:5382-5432)
         for p, g, st in zip(plist, grads, sts):
@@ -222,9 +233,10 @@ class OracleApexW:
                                   [i[2]["exp_avg"] for i in items], vs, step=step, is_quad=quad,
                                   stochastic=grp["stochastic_rounding"], scale_v=scale_v,
                                   sqrt_scale_v=sqrt_scale_v, nesterov=grp["nesterov"],
-                                  cautious=grp["cautious"], **kw)
+                                  cautious=grp["cautious"],
+                                  max_vs=[i[2]["max_exp_avg_sq"] for i in items] if ams else None, **kw)
         # the replayed plan's per-subgroup scales start at 1.0 (optimizer.py:546-560)
-        self._plan = {"kind": "foreach", "params": plan_params, "sg_scale": {}}
+        self._plan = {"kind": "foreach", "params": plan_params, "sg_scale": {}, "amsgrad": ams}
 
     def _is_quad(self, p):
         v = self.state[p]["exp_avg_sq"]
@@ -246,8 +258,9 @@ class OracleApexW:
             return
         grads, scale = self._prepare(self._signed(grads, False), sanitize=grp["clip_grad_norm"] is not None)
         sts = [self.state[p] for p in plist]
+        ams = plan["amsgrad"]
         if plan["kind"] == "native":
-            self._native_fused(plist, grads, sts, sanitize=False, grad_scale=scale, **kw)
+            self._native_fused(plist, grads, sts, sanitize=False, grad_scale=scale, amsgrad=ams, **kw)
             return
         steps = [st["step"] for st in sts]
         torch._foreach_add_(steps, 1)
@@ -284,7 +297,8 @@ class OracleApexW:
                                  apply_wd_mask=[(i[0].dim() >= 2) if dno else True for i in items],
                                  step=step, is_quad=quad, stochastic=grp["stochastic_rounding"],
                                  scale_v=scale_v, sqrt_scale_v=sqrt_scale_v, nesterov=grp["nesterov"],
-                                 cautious=grp["cautious"], **kw)
+                                 cautious=grp["cautious"],
+                                 max_vs=[i[2]["max_exp_avg_sq"] for i in items] if ams else None, **kw)
 
     def _factored(self, p, g, st, step, inv, sanitize):
         grp = self.group
@@ -299,7 +313,7 @@ class OracleApexW:
 
     @staticmethod
     def _native_fused(params, grads, sts, *, lr, beta1, beta2, eps, weight_decay, decay_norm_only,
-                      sanitize=True, grad_scale=None):
+                      sanitize=True, grad_scale=None, amsgrad=False):
         if sanitize:
             grads = sanitize_grads(grads)
         steps = [st["step"] for st in sts]
@@ -313,6 +327,7 @@ class OracleApexW:
             if idx:
                 torch._fused_adamw_([params[i] for i in idx], [grads[i] for i in idx],
                                     [sts[i]["exp_avg"] for i in idx], [sts[i]["exp_avg_sq"] for i in idx],
-                                    [], [steps[i] for i in idx], amsgrad=False, lr=lr, beta1=beta1,
+                                    [sts[i]["max_exp_avg_sq"] for i in idx] if amsgrad else [],
+                                    [steps[i] for i in idx], amsgrad=amsgrad, lr=lr, beta1=beta1,
                                     beta2=beta2, weight_decay=wd, eps=eps, maximize=False,
                                     grad_scale=grad_scale)

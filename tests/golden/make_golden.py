@@ -516,6 +516,20 @@ PREC_CASES = {
     "full_fp32_cautious_rne": (PREC_SHAPES, torch.float32, 4, 82, dict(PREC_KW, precision="full", cautious=True)),
     "auto_bf16_cautious_rne": (PREC_SHAPES, torch.bfloat16, 4, 83,
                                dict(PREC_KW, precision="auto", adamw_compat=True, cautious=True)),
+    # amsgrad=True in the compact-kernel precisions: max_exp_avg_sq beside v, no quad v.
+    # bf16 compact and fp32 full groups are homogeneous (torch._fused_adamw_ with its max);
+    # fused=False, fp32 parameters with bf16 moments and bf16 parameters with fp32 moments
+    # take the foreach order, cold then replayed
+    "compact_bf16_amsgrad_rne": (PREC_SHAPES, torch.bfloat16, 5, 84, dict(PREC_KW, amsgrad=True)),
+    "compact_bf16_amsgrad_foreach_rne": (PREC_SHAPES, torch.bfloat16, 5, 85,
+                                         dict(PREC_KW, amsgrad=True, fused=False)),
+    "compact_fp32_amsgrad_rne": (PREC_SHAPES, torch.float32, 4, 86, dict(PREC_KW, amsgrad=True)),
+    "full_bf16_amsgrad_rne": (PREC_SHAPES, torch.bfloat16, 4, 87, dict(PREC_KW, precision="full", amsgrad=True)),
+    "full_fp32_amsgrad_rne": (PREC_SHAPES, torch.float32, 4, 88, dict(PREC_KW, precision="full", amsgrad=True)),
+    "auto_bf16_amsgrad_rne": (PREC_SHAPES, torch.bfloat16, 4, 89,
+                              dict(PREC_KW, precision="auto", adamw_compat=True, amsgrad=True)),
+    "compact_bf16_amsgrad_cautious_rne": (PREC_SHAPES, torch.bfloat16, 4, 90,
+                                          dict(PREC_KW, amsgrad=True, cautious=True)),
 }
 
 
@@ -538,6 +552,11 @@ FP16_CASES = {
                       dict(FP16_KW, adamw_compat=True, precision="8bit"), ()),
     "fp16_full_rne": (FP16_SHAPES, 4, 56, dict(FP16_KW, precision="full"), ()),
     "fp16_ultra_rne": (FP16_SHAPES, 4, 57, dict(FP16_KW, precision="ultra", threshold=4096), ()),
+    # amsgrad: fp16 m / v and their max, natively fused (homogeneous; beta2 0.5 keeps the
+    # unscaled fp16 v of 1e-3 grads off zero) or in the foreach order with the dynamic v
+    # scale (fused=False)
+    "fp16_amsgrad_native_rne": (FP16_SHAPES, 4, 58, dict(FP16_KW, amsgrad=True, betas=(0.9, 0.5)), ()),
+    "fp16_amsgrad_foreach_rne": (FP16_SHAPES, 5, 59, dict(FP16_KW, amsgrad=True, fused=False), ()),
 }
 
 

@@ -50,6 +50,10 @@ CASES = [
     # cautious: the count pass reads the device scalars too (8 tensors: quad v for the large ones)
     ("compact cautious", [(256, 128), (20000,)] + [(64,)] * 6, torch.bfloat16,
      dict(precision="compact", cautious=True)),
+    # amsgrad: the running max in the native fused order and in the foreach one
+    ("compact amsgrad native", [(256, 128), (1000,), (64,)], torch.bfloat16, dict(precision="compact", amsgrad=True)),
+    ("compact amsgrad foreach fp32", [(256, 128), (1000,)], torch.float32,
+     dict(precision="compact", amsgrad=True)),
 ]
 
 

@@ -56,7 +56,7 @@ def _compare(gps, cps, gopt, copt, tag):
         _assert_close(gp, cp, f"{tag} p{i}")
         gs, cs = gopt.state[gp], copt.state[cp]
         assert set(gs) == set(cs), f"{tag} p{i} state keys"
-        for k in ("exp_avg", "exp_avg_sq", "exp_avg_scales", "exp_avg_sq_scales"):
+        for k in ("exp_avg", "exp_avg_sq", "exp_avg_scales", "exp_avg_sq_scales", "max_exp_avg_sq"):
             if k in cs and torch.is_tensor(cs[k]):
                 assert gs[k].dtype == cs[k].dtype and gs[k].shape == cs[k].shape
                 _assert_close(gs[k], cs[k], f"{tag} p{i} {k}")

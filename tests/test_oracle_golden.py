@@ -79,20 +79,53 @@ def test_oracle_matches_reference_trajectory(name, monkeypatch):
         assert int(s.get("block_size_8bit", 0) or 0) == fl[3]
 
 
-VARIANT_OPTIONS = ("maximize", "nesterov", "cautious")
+VARIANT_OPTIONS = ("amsgrad", "maximize", "nesterov", "cautious")
 
 
 @pytest.mark.parametrize("name", sorted(n for n in CASES if any(o in n for o in VARIANT_OPTIONS)))
 def test_variant_goldens_pin_the_variant(name):
-    """Each maximize / nesterov / cautious trajectory tells the variant from the plain
-    step: the same run with the option off ends on other parameters (so the golden
-    pins the negated grads, the Nesterov numerator or the mask, not only the rest of
-    the step)."""
+    """Each amsgrad / maximize / nesterov / cautious trajectory tells the variant from
+    the plain step: the same run with the option off ends on other parameters (so the
+    golden pins the running max, the negated grads, the Nesterov numerator or the
+    mask, not only the rest of the step)."""
     option = next(o for o in VARIANT_OPTIONS if o in name)
 
     def plain(params, **kw):
         return OracleApexW(params, **dict(kw, **{option: False}))
     params, _, gold = replay(name, plain)
+    assert any(not np.array_equal(_as_np(p.data).reshape(-1), gold[f"p_{i}"].reshape(-1))
+               for i, p in enumerate(params))
+
+
+AMSGRAD_CASES = sorted(n for n in CASES if "amsgrad" in n)
+# homogeneous groups: torch._fused_adamw_ takes the max itself
+AMSGRAD_NATIVE = {"compact_bf16_amsgrad_rne", "full_fp32_amsgrad_rne", "fp16_amsgrad_native_rne"}
+
+
+@pytest.mark.parametrize("name", AMSGRAD_CASES)
+def test_amsgrad_goldens_hold_an_active_max(name):
+    """The reference's running max ends above v somewhere in every amsgrad trajectory,
+    so the max (not v) fed some denominator of the recorded steps."""
+    gold = load(name)
+    n = len(CASES[name][0])
+    assert any((gold[f"st_{i}_max_exp_avg_sq"] != gold[f"st_{i}_exp_avg_sq"]).any() for i in range(n))
+
+
+@pytest.mark.parametrize("name", AMSGRAD_CASES)
+def test_amsgrad_goldens_pin_the_max_in_the_denominator(name, monkeypatch):
+    """The foreach-order trajectories tell a step that keeps the max but divides by v
+    from the reference's (the native ones take torch._fused_adamw_'s own max)."""
+    import oracle.compact as C
+
+    def v_denominator(max_vs, vs):
+        if max_vs is not None:
+            torch._foreach_maximum_(max_vs, vs)
+        return vs
+    monkeypatch.setattr(C, "_amsgrad_max", v_denominator)
+    params, opt, gold = replay(name, OracleApexW)
+    assert (opt._plan["kind"] == "native") == (name in AMSGRAD_NATIVE)
+    if name in AMSGRAD_NATIVE:
+        return
     assert any(not np.array_equal(_as_np(p.data).reshape(-1), gold[f"p_{i}"].reshape(-1))
                for i, p in enumerate(params))
 

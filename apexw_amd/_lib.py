@@ -48,6 +48,7 @@ HP_AMP = 1 << 8
 HP_NESTEROV = 1 << 9
 HP_CAUTIOUS = 1 << 10
 HP_AMSGRAD = 1 << 11
+HP_LION = 1 << 12
 
 STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported dtype combination", 3: "launch failed",
           4: "misaligned pointer", 5: "exceeds the fixed workspace of the allocation-free entry point"}

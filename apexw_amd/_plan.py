@@ -97,6 +97,8 @@ class StepPlan:
         # nesterov=True: a compact group's step scalars come from the host (no device AMP);
         # refreshed from the group each step (valid_for)
         self.nesterov = bool(group.get("nesterov", False))
+        # lion=True: the compact step's sign update in place of AdamW's (no v read)
+        self.lion = self._lion_of(group)
         # amsgrad=True: the compact step keeps a running max of v (hparams.max_v)
         self.amsgrad = self._amsgrad_of(group)
         self.d_counts = None
@@ -109,8 +111,10 @@ class StepPlan:
     def _cautious_of(self, group):
         """The group's cautious flag as this plan's kernels take it: the 8-bit / ultra
         and compact steps, not enable_fused_backward's per-parameter update (which has
-        no cautious branch, optimizer.py:2373-2471)."""
-        return bool(group.get("cautious", False)) and not self.single
+        no cautious branch, optimizer.py:2373-2471); lion takes the place of the AdamW
+        update, cautious with it (optimizer.py:5677-5683)."""
+        return bool(group.get("cautious", False)) and not self.single and not (
+            self.kind == "compact" and self._lion_of(group))
 
     def _maximize_of(self, group):
         return bool(group.get("maximize", False)) and not self.hooked
@@ -119,7 +123,13 @@ class StepPlan:
         """The group's amsgrad flag as this plan's kernels take it: the compact step, not
         the in-backward batches nor the per-parameter update (which step without it,
         optimizer.py:2360, :2373-2471)."""
-        return bool(group.get("amsgrad", False)) and self.kind == "compact" and not self.hooked
+        return (bool(group.get("amsgrad", False)) and self.kind == "compact" and not self.hooked
+                and not self._lion_of(group))
+
+    def _lion_of(self, group):
+        """The group's lion flag as this plan's kernels take it: the compact step, not the
+        per-parameter update, which steps AdamW whatever the group says (optimizer.py:2373-2471)."""
+        return bool(group.get("lion", False)) and self.kind == "compact" and not self.hooked
 
     # ------------------------------------------------------------------ validity
     def valid_for(self, group):
@@ -138,8 +148,9 @@ class StepPlan:
         if self._maximize_of(group) != self.maximize:
             return False
         # amsgrad switched on or off: a new plan (FastExecutionPlan.is_valid_for_step,
-        # optimizer.py:585-586)
-        if self._amsgrad_of(group) != self.amsgrad:
+        # optimizer.py:585-586: the plan holds max_exp_avg_sq lists only when it was made
+        # with amsgrad and without lion, so lion with amsgrad makes every step a cold one)
+        if self.kind == "compact" and not self.hooked and bool(group.get("amsgrad", False)) != self.amsgrad:
             return False
         if self.kind == "q8":
             # cautious keeps every 8-bit tensor in the generic order: another table
@@ -157,7 +168,15 @@ class StepPlan:
         if self.native and self.nesterov:
             return False
         self._scan_status = self._scan()
-        return self._scan_status in (SCAN_SAME, SCAN_GRADS_MOVED, SCAN_SLOW)
+        ok = self._scan_status in (SCAN_SAME, SCAN_GRADS_MOVED, SCAN_SLOW)
+        if ok and self._lion_of(group) != self.lion:
+            # lion switched on or off: the descriptors change (no v under lion), so a new
+            # plan; the reference's replayed foreach plan stays valid across the switch
+            # (optimizer.py:575-621) and its native fused one does not, so the new plan keeps
+            # this one's replay order when there is one (keep_replay)
+            self.keep_replay = self.cold_done and not self.native
+            return False
+        return ok
 
     def _scan(self):
         return self._H.scan(self.params, self.inactive, *self._scan_addrs)
@@ -184,12 +203,14 @@ class StepPlan:
                     f |= L.FLAG_M6
                 return f, int(st["block_size_8bit"])
             return f | (_DT[st["exp_avg"].dtype] << L.MDT_SHIFT), 0
-        m, v = st["exp_avg"], st["exp_avg_sq"]
+        m = st["exp_avg"]
+        # lion reads no v: its descriptors describe m in v's place (never quad, never scaled)
+        v = m if self.lion else st["exp_avg_sq"]
         if self.kind == "compact":
             f |= (_DT[m.dtype] << L.MDT_SHIFT) | (_DT[v.dtype] << L.VDT_SHIFT)
             if v.numel() * 4 == p.numel() and p.numel() % 4 == 0:
                 f |= L.FLAG_QUAD
-            if torch.float16 in (m.dtype, v.dtype) and not self.native and not self.single:
+            if torch.float16 in (m.dtype, v.dtype) and not self.native and not self.single and not self.lion:
                 # the dynamic v scale of fp16 subgroups (set per launch, see _update_vscales)
                 f |= L.FLAG_VSCALE
             block = 0
@@ -232,6 +253,8 @@ class StepPlan:
                 tab[i]["v_scale"] = st["exp_avg_sq_col"].data_ptr()
                 if block:
                     tab[i]["m_scale"] = st["exp_avg_scales"].data_ptr()
+            elif self.lion:
+                tab[i]["v"] = st["exp_avg"].data_ptr()     # never read under APEXW_HP_LION
             else:
                 tab[i]["v"] = st["exp_avg_sq"].data_ptr()
                 if "exp_avg_scales" in st and st.get("is_8bit", False):
@@ -959,11 +982,16 @@ class StepPlan:
             hp.eps_scaled = eps * bc2s
             hp.eps = eps                   # the replay's denominator floor with fp16 in the subgroup
             hp.mode = L.MODE_COLD if cold else L.MODE_REPLAY
-            if sr:
+            if sr and not self.lion:
                 flags |= L.HP_SR
                 if b2 >= 0.995:
                     flags |= L.HP_SR_V
-            if self.cautious:
+            if self.lion:
+                # lion (optimizer.py:5677-5683, :1214-1225): the sign update with -lr, m
+                # toward g with weight 1 - beta2 (lerp_coef below); no SR
+                flags |= L.HP_LION
+                hp.gain_hi = lr
+            elif self.cautious:
                 # cautious (optimizer.py:5847-5864, :1321-1328): m times the mask over its mean,
                 # the counts from apexw_compact_cautious_count
                 flags |= L.HP_CAUTIOUS
@@ -975,7 +1003,7 @@ class StepPlan:
                 hp.gain_hi = -(lr * bc2s / bc1) * b1
                 hp.gain_lo = -(lr * bc2s / bc1) * (1.0 - b1)
                 flags |= L.HP_NESTEROV
-        hp.lerp_coef, hi = _lerp_coef(1.0 - b1)
+        hp.lerp_coef, hi = _lerp_coef(1.0 - (b2 if flags & L.HP_LION else b1))
         if hi:
             flags |= L.HP_LERP_HI
         hp.look_coef, hi = _lerp_coef(b1)

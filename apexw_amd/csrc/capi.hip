@@ -179,13 +179,18 @@ static int launch_args_status(int32_t kind, int32_t n_tensors, int64_t n_units, 
       if ((hp->flags & APEXW_HP_NESTEROV) &&
           (hp->mode == APEXW_MODE_NATIVE || hp->mode == APEXW_MODE_SINGLE || (hp->flags & APEXW_HP_AMP)))
         return APEXW_ERR_ARG;
+      // lion: the cold and replayed orders, alone (it takes the place of the AdamW update)
+      if ((hp->flags & APEXW_HP_LION) &&
+          (hp->mode == APEXW_MODE_NATIVE || hp->mode == APEXW_MODE_SINGLE ||
+           (hp->flags & (APEXW_HP_NESTEROV | APEXW_HP_CAUTIOUS | APEXW_HP_AMSGRAD))))
+        return APEXW_ERR_ARG;
       return APEXW_OK;
     case APEXW_LAUNCH_ULTRA:
-      if (n_fast_units || n_fast_f32_units || (hp->flags & APEXW_HP_AMSGRAD)) return APEXW_ERR_ARG;
+      if (n_fast_units || n_fast_f32_units || (hp->flags & (APEXW_HP_AMSGRAD | APEXW_HP_LION))) return APEXW_ERR_ARG;
       return (hp->mode == APEXW_MODE_NATIVE || hp->mode == APEXW_MODE_SINGLE) ? APEXW_ERR_ARG : APEXW_OK;
     case APEXW_LAUNCH_Q8:
       if (n_fast_units < 0 || n_fast_f32_units < 0 || n_fast_units + n_fast_f32_units > n_units) return APEXW_ERR_ARG;
-      if (hp->mode == APEXW_MODE_NATIVE || (hp->flags & APEXW_HP_AMSGRAD)) return APEXW_ERR_ARG;
+      if (hp->mode == APEXW_MODE_NATIVE || (hp->flags & (APEXW_HP_AMSGRAD | APEXW_HP_LION))) return APEXW_ERR_ARG;
       if (hp->mode == APEXW_MODE_SINGLE && (n_fast_units || n_fast_f32_units)) return APEXW_ERR_ARG;
       return APEXW_OK;
     case APEXW_LAUNCH_CAUTIOUS:
@@ -194,7 +199,7 @@ static int launch_args_status(int32_t kind, int32_t n_tensors, int64_t n_units, 
       if (hp->mode == APEXW_MODE_NATIVE || hp->mode == APEXW_MODE_SINGLE) return APEXW_ERR_ARG;
       return ((uintptr_t)hp->counts & 7u) ? APEXW_ERR_ALIGN : APEXW_OK;
     case APEXW_LAUNCH_FACTORED:
-      if (n_fast_units || n_fast_f32_units || (hp->flags & APEXW_HP_AMSGRAD)) return APEXW_ERR_ARG;
+      if (n_fast_units || n_fast_f32_units || (hp->flags & (APEXW_HP_AMSGRAD | APEXW_HP_LION))) return APEXW_ERR_ARG;
       if (hp->mode == APEXW_MODE_SINGLE || hp->mode == APEXW_MODE_NATIVE) return APEXW_ERR_ARG;
       return (hp->flags & APEXW_HP_AMP) ? APEXW_ERR_ARG : APEXW_OK;   // factored steps take host-read AMP scalars
     default:

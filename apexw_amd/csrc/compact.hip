@@ -183,6 +183,30 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
   // the v update, apexw/optimizer.py:5788-5790, :1253-1255; inside torch._fused_adamw_ for
   // the native mode)
 
+  if constexpr (VAR && !QUAD) {
+    if (hp.flags & APEXW_HP_LION) {
+      // lion (the cold and the replayed order alike, apexw/optimizer.py:5677-5683,
+      // :1214-1225): the grads cast to m's dtype; u = lerp(g', m, beta1) rounded to it;
+      // p += -lr * sign(u), the scalar rounded to p's dtype when p and u share a 16-bit
+      // dtype (torch's same-dtype add with alpha); m = lerp(m, g', 1 - beta2)
+      constexpr bool kAlpha16 = PD == MD && PD != APEXW_F32;
+      const float alpha = kAlpha16 ? rnd<PD>(-hp.gain_hi) : -hp.gain_hi;
+      const float wd_l = rnd<PD>(hp.wd_factor);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float pw = wd ? rnd<PD>(p[j] * wd_l) : p[j];
+        const float gm = rnd<MD>(g[j]);
+        const float d = m[j] - gm;
+        const float u = rnd<MD>((hp.flags & APEXW_HP_LOOK_HI) ? fmaf(hp.look_coef, d, m[j])
+                                                               : fmaf(hp.look_coef, d, gm));
+        const float sg = u > 0.0f ? 1.0f : (u < 0.0f ? -1.0f : 0.0f);
+        p[j] = rnd<PD>(pw + alpha * sg);
+        m[j] = rnd<MD>((hp.flags & APEXW_HP_LERP_HI) ? fmaf(hp.lerp_coef, -d, gm) : fmaf(hp.lerp_coef, -d, m[j]));
+      }
+      return;
+    }
+  }
+
   if constexpr (!QUAD) {
     if (hp.mode == APEXW_MODE_SINGLE) {
       // p.mul_(wd) in the parameter dtype (fp32 scalar), fp32 moments
@@ -353,6 +377,8 @@ APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const 
     float p[8], g[8], m[8], v[8], x[8];
     const bool full = vec && cnt == 8;
     const bool ams = VAR && !QUAD && vmax != nullptr;
+    // lion keeps no second moment: v is neither read nor written
+    const bool lion = VAR && !QUAD && (c.hp->flags & APEXW_HP_LION);
     if (full) {
       load8<PD>(t.p, e0, p);
       load8<GD>(t.g, e0, g);
@@ -367,7 +393,7 @@ APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const 
           v[0] = VD == APEXW_BF16 ? bf16_bits_to_f32(w & 0xFFFFu) : f16_bits_to_f32(w & 0xFFFFu);
           v[1] = VD == APEXW_BF16 ? __uint_as_float(w & 0xFFFF0000u) : f16_bits_to_f32(w >> 16);
         }
-      } else {
+      } else if (!lion) {
         load8<VD>(t.v, e0, v);
         if (ams) load8<VD>(vmax, e0, x);
       }
@@ -378,7 +404,7 @@ APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const 
         p[j] = ok ? load1<PD>(t.p, e0 + j) : 0.0f;
         g[j] = ok ? load1<GD>(t.g, e0 + j) : 0.0f;
         m[j] = ok ? load1<MD>(t.m, e0 + j) : 0.0f;
-        if constexpr (!QUAD) v[j] = ok ? load1<VD>(t.v, e0 + j) : 0.0f;
+        if constexpr (!QUAD) v[j] = (ok && !lion) ? load1<VD>(t.v, e0 + j) : 0.0f;
         x[j] = (ams && ok) ? load1<VD>(vmax, e0 + j) : 0.0f;
       }
       if constexpr (QUAD) {
@@ -407,7 +433,7 @@ APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const 
           const uint32_t hi = VD == APEXW_BF16 ? (__float_as_uint(v[1]) >> 16) : f32_to_f16_bits(v[1]);
           __builtin_nontemporal_store(lo | (hi << 16), (uint32_t*)((uint16_t*)t.v + (e0 >> 2)));
         }
-      } else {
+      } else if (!lion) {
         store8<VD>(t.v, e0, v);
         if (ams) store8<VD>(vmax, e0, x);
       }
@@ -417,7 +443,9 @@ APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const 
         if (j < cnt) {
           store1<PD>(t.p, e0 + j, p[j]);
           store1<MD>(t.m, e0 + j, m[j]);
-          if constexpr (!QUAD) store1<VD>(t.v, e0 + j, v[j]);
+          if constexpr (!QUAD) {
+            if (!lion) store1<VD>(t.v, e0 + j, v[j]);
+          }
           if (ams) store1<VD>(vmax, e0 + j, x[j]);
         }
       }
@@ -619,8 +647,8 @@ int apexw_launch_compact(const apexw_tensor* tensors, int64_t n_units, const ape
   // resident grid striding over the whole launch).  Launches that a resident grid
   // covers in a few passes keep it (C2, 124 M elements: 0.234-0.257 ms against
   // 0.252-0.288 with a workgroup per unit).
-  // nesterov / cautious / amsgrad launches take the instantiation that holds them
-  const bool var = hp->flags & (APEXW_HP_NESTEROV | APEXW_HP_CAUTIOUS | APEXW_HP_AMSGRAD);
+  // nesterov / cautious / amsgrad / lion launches take the instantiation that holds them
+  const bool var = hp->flags & (APEXW_HP_NESTEROV | APEXW_HP_CAUTIOUS | APEXW_HP_AMSGRAD | APEXW_HP_LION);
   const void* kernel = var ? (const void*)compact_step_kernel<true> : (const void*)compact_step_kernel<false>;
   const int resident = apexw_resident_grid(kernel, n_units * kGroups);
   const int grid = n_units > (int64_t)resident * 8 ? (int)(n_units < INT32_MAX ? n_units : INT32_MAX) : resident;

@@ -39,15 +39,17 @@ DOWNCAST_MIN_NUMEL = 1024          # optimizer.py:2100
 HOOK_MIN_NUMEL = 16384             # optimizer.py:2131
 HOOK_BATCH = 14                    # optimizer.py:2142
 
-_UNSUPPORTED_FLAGS = ("lion", "capturable", "differentiable", "auto_pack")
-def _check_variants(precision, factored, nesterov, cautious, maximize=False, amsgrad=False):
+_UNSUPPORTED_FLAGS = ("capturable", "differentiable", "auto_pack")
+def _check_variants(precision, factored, nesterov, cautious, maximize=False, amsgrad=False, lion=False):
     """nesterov=True, cautious=True and maximize=True run in every precision: the
     8-bit and ultra steps' lookahead numerator lerp(g, m, beta1) without the SNR gain
     and the compact, full and auto steps' two addcdiv passes (lerp(g, m, beta1) for
     quad v); the numerator m times the sign-agreement mask over its mean; the negated
-    grads.  amsgrad=True runs in the compact, full and auto precisions (a running max
-    of v beside it, no quad v).  Factored second moments, nesterov together with
-    cautious, and amsgrad in the 8bit and ultra precisions do not."""
+    grads.  amsgrad=True and lion=True run in the compact, full and auto precisions
+    (a running max of v beside it, no quad v; the sign update on m alone, which takes
+    the place of the AdamW update and of its variants).  Factored second moments,
+    nesterov together with cautious, and amsgrad or lion in the 8bit and ultra
+    precisions do not."""
     for name, on in (("nesterov", nesterov), ("cautious", cautious), ("maximize", maximize),
                      ("amsgrad", amsgrad)):
         if not on:
@@ -58,6 +60,8 @@ def _check_variants(precision, factored, nesterov, cautious, maximize=False, ams
         raise NotImplementedError("apexw_amd: nesterov=True together with cautious=True")
     if amsgrad and precision in ("8bit", "ultra"):
         raise NotImplementedError(f"apexw_amd: amsgrad=True with precision={precision!r}")
+    if lion and precision in ("8bit", "ultra"):
+        raise NotImplementedError(f"apexw_amd: lion=True with precision={precision!r}")
 
 
 class ApexW(Optimizer):
@@ -154,8 +158,9 @@ class ApexW(Optimizer):
         if bad or beta3 is not None:
             what = ", ".join(bad + (["beta3"] if beta3 is not None else []))
             raise NotImplementedError(f"apexw_amd implements the standard AdamW step; not supported: {what}")
-        if nesterov or cautious or maximize or amsgrad:
-            _check_variants(S.normalize_precision(precision), factored_v, nesterov, cautious, maximize, amsgrad)
+        if nesterov or cautious or maximize or amsgrad or lion:
+            _check_variants(S.normalize_precision(precision), factored_v and not lion and not amsgrad,
+                            nesterov and not lion, cautious and not lion, maximize, amsgrad and not lion, lion)
         if precision == "compact" and betas[1] >= 0.99 and not stochastic_rounding and not adamw_compat:
             warnings.warn(
                 f"ApexW: beta2={betas[1]} with precision='compact' and stochastic_rounding=False "
@@ -267,9 +272,14 @@ class ApexW(Optimizer):
                     old = self._plans.pop(gid, None)
                     if old is not None:
                         old.amp_fold(sync=True)       # its counters are the states' until the new plan reads them
-                    plan = self._build_plan(group)
+                    keep = old is not None and getattr(old, "keep_replay", False)
+                    plan = self._build_plan(group, foreach=keep)
                     if plan is None:
                         continue
+                    if keep:
+                        # a lion switch over a replayed plan: the next step replays too
+                        plan.cold_done = True
+                        plan._sg_scale = dict(old._sg_scale)
                     self._plans[gid] = plan
                 # a plan's first launch (the cold rounding order) stays on the host read, so that
                 # a skipped step cannot use it up: the next real step is the cold one, as in the reference
@@ -323,7 +333,9 @@ class ApexW(Optimizer):
         for plan in self._plans.values():
             plan.amp_fold(sync=True)
 
-    def _build_plan(self, group):
+    def _build_plan(self, group, foreach=False):
+        """The group's StepPlan from its parameters with grads (states made as needed);
+        foreach: never the native fused order."""
         group["precision"] = S.normalize_precision(group.get("precision", "compact"))
         params = []
         for p in group["params"]:
@@ -345,11 +357,21 @@ class ApexW(Optimizer):
                 self.state[p].update(S.init_state(p, group, peft, has16))
             if p.dtype == torch.float16 and self.state[p].get("is_factored_v", False):
                 raise NotImplementedError("apexw_amd: factored_v with fp16 parameters")
-        ams = bool(group.get("amsgrad", False))
-        if group.get("nesterov", False) or group.get("cautious", False) or group.get("maximize", False) or ams:
+        lion = bool(group.get("lion", False))
+        # lion takes the place of the AdamW update and of its variants (optimizer.py:5375-5380,
+        # :5677-5683): nesterov, cautious and amsgrad do not apply under it
+        ams = bool(group.get("amsgrad", False)) and not lion
+        if (group.get("nesterov", False) or group.get("cautious", False) or group.get("maximize", False) or ams
+                or lion):
             _check_variants(group["precision"], any(self.state[p].get("is_factored_v", False) for p in params),
-                            bool(group.get("nesterov", False)), bool(group.get("cautious", False)),
-                            bool(group.get("maximize", False)), ams)
+                            bool(group.get("nesterov", False)) and not lion,
+                            bool(group.get("cautious", False)) and not lion,
+                            bool(group.get("maximize", False)), ams, lion)
+        if not lion:
+            for p in params:
+                if "exp_avg_sq" not in self.state[p] and not self.state[p].get("is_factored_v", False):
+                    raise NotImplementedError("apexw_amd: lion=False on a tensor whose state holds no second "
+                                              "moment (made under lion=True)")
         if ams:
             for p in params:
                 st = self.state[p]
@@ -369,7 +391,8 @@ class ApexW(Optimizer):
         # maximize, nesterov and cautious leave the native fused plan (FastExecutionPlan.
         # is_valid_for_step, optimizer.py:593-600): the foreach order instead
         native = (homogeneous and group.get("fused") is not False and not group.get("maximize", False)
-                  and not group.get("nesterov", False) and not group.get("cautious", False))
+                  and not group.get("nesterov", False) and not group.get("cautious", False) and not lion
+                  and not foreach)
         return StepPlan(self, group, params, "compact", native=native)
 
     # ------------------------------------------------------------------ checkpoints
@@ -443,7 +466,8 @@ class ApexW(Optimizer):
         models (optimizer.py:2059-2167)."""
         d = self.defaults
         if not force and (d.get("clip_grad_norm") is not None or d.get("grad_centralization", False)
-                          or d.get("nesterov", False) or d.get("maximize", False) or d.get("amsgrad", False)):
+                          or d.get("nesterov", False) or d.get("maximize", False) or d.get("amsgrad", False)
+                          or d.get("lion", False)):
             return
         trainable = []
         total = 0
@@ -667,6 +691,9 @@ class ApexW(Optimizer):
             if p.dtype not in (torch.float32, torch.bfloat16):
                 raise NotImplementedError(f"apexw_amd steps fp32/bf16 parameters, got {p.dtype}")
             kind = "q8" if (state.get("is_8bit", False) or prec == "8bit") else "compact"
+            if kind == "compact" and "exp_avg_sq" not in state:
+                raise RuntimeError("enable_fused_backward needs exp_avg_sq; this parameter has lion state "
+                                   "(no second moment) from an earlier step()")
             if kind == "compact" and state["exp_avg_sq"].numel() != p.numel():
                 # the reference's update broadcasts a full-size square against it and fails
                 raise RuntimeError("enable_fused_backward needs full-size exp_avg_sq; this parameter "

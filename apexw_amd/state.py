@@ -125,7 +125,8 @@ def _auto_subbyte(p, group, bs, factored=False):
     n = p.numel()
     raw_int4 = group.get("int4_m", group.get("four_bit", None))
     pow2 = bs >= 64 and (bs & (bs - 1)) == 0
-    return (raw_int4 is not False and not factored and not group.get("amsgrad", False) and n >= 16384 and n % 4 == 0 and pow2
+    return (raw_int4 is not False and not factored and not group.get("amsgrad", False)
+            and not group.get("lion", False) and n >= 16384 and n % 4 == 0 and pow2
             and (p.dim() < 2 or min(p.shape) >= 8))
 
 
@@ -217,7 +218,7 @@ def init_state(p, group, peft_ctx, has_16bit_params=False):
     "auto" precision keeps fp32 moments only when none is).  amsgrad adds
     ``max_exp_avg_sq`` (ensure_max_v)."""
     st = _init_state(p, group, peft_ctx, has_16bit_params)
-    if group.get("amsgrad", False):
+    if group.get("amsgrad", False) and not group.get("lion", False):
         ensure_max_v(st, p)
     return st
 
@@ -242,6 +243,7 @@ def _init_state(p, group, peft_ctx, has_16bit_params):
     st = {"stochastic_rounding": sr, "step": torch.tensor(0.0, dtype=torch.float32)}
     is_peft = is_peft_parameter(p) or peft_ctx
     ams = bool(group.get("amsgrad", False))
+    lion = bool(group.get("lion", False))
     large = p.dim() >= 2 or n >= group.get("threshold", 65536)
     if group.get("fused") is True or prec == "full":
         # optimizer.py:2625-2626, :2769-2772
@@ -267,14 +269,14 @@ def _init_state(p, group, peft_ctx, has_16bit_params):
                                                                                    is_peft)
         if fp32_training or not large:
             return _moments(st, p, torch.float32, group, is_peft, prec)
-        if bool(group.get("factored_v", False)) and _can_factor(p, is_peft, FACTORED_MIN_COMPACT, ams):
+        if bool(group.get("factored_v", False)) and _can_factor(p, is_peft, FACTORED_MIN_COMPACT, ams or lion):
             st["is_factored_v"] = True
             return _factored_compact(st, p)
         return _moments(st, p, compact_dtype(p), group, is_peft, prec)
     if prec == "8bit" and n >= 64:
         bs = block_size_8bit(p, group.get("block_size"))
         narrow = p.dim() >= 2 and min(p.shape) <= 32 and n < 2048
-        factored = bool(group.get("factored_v", False)) and _can_factor(p, is_peft, FACTORED_MIN_8BIT, ams)
+        factored = bool(group.get("factored_v", False)) and _can_factor(p, is_peft, FACTORED_MIN_8BIT, ams or lion)
         auto_sub = _auto_subbyte(p, group, bs, factored)
         raw_int4 = group.get("int4_m", group.get("four_bit", None))
         six = bool(group.get("six_bit", False)) and factored and n >= SIX_BIT_MIN and bs % 4 == 0
@@ -284,7 +286,7 @@ def _init_state(p, group, peft_ctx, has_16bit_params):
     if prec == "8bit":
         st.update(is_8bit=False, is_factored_v=False, is_6bit_m=False, is_4bit_m=False, is_quad_v=False)
     else:
-        factored = bool(group.get("factored_v", False)) and _can_factor(p, is_peft, FACTORED_MIN_COMPACT, ams)
+        factored = bool(group.get("factored_v", False)) and _can_factor(p, is_peft, FACTORED_MIN_COMPACT, ams or lion)
         st.update(is_6bit_m=False, is_4bit_m=False, is_factored_v=factored)
         if factored:
             return _factored_compact(st, p)
@@ -304,15 +306,15 @@ def _factored_compact(st, p):
 
 def _moments(st, p, mdt, group, is_peft, prec):
     """Dense m in ``mdt``, v in the beta2 rule's dtype, quad v for large 16-bit
-    compact / auto tensors, not under nesterov or amsgrad (optimizer.py:2788-2810,
-    :2838-2872)."""
+    compact / auto tensors, not under nesterov, amsgrad or lion; no v under lion
+    (optimizer.py:2788-2810, :2838-2872)."""
     n, dev = p.numel(), p.device
     vdt = v_dtype_for_beta2(mdt, group["betas"][1], group.get("force_compact_v", False),
                             bool(group.get("stochastic_rounding", True)))
     quad = (prec in ("compact", "auto") and mdt in (torch.bfloat16, torch.float16)
             and vdt in (torch.bfloat16, torch.float16)
             and group.get("int4_m", None) is not False and not group.get("nesterov", False)
-            and not group.get("amsgrad", False)
+            and not group.get("amsgrad", False) and not group.get("lion", False)
             and n >= 16384 and n % 4 == 0
             and (p.dim() < 2 or min(p.shape) >= 8)
             and (is_peft or len(group["params"]) >= 8))
@@ -321,13 +323,16 @@ def _moments(st, p, mdt, group, is_peft, prec):
     st["state_dtype"] = mdt
     st["state_dtype_v"] = vdt
     st["exp_avg"] = torch.zeros(p.shape, dtype=mdt, device=dev)
-    if quad:
+    lion = bool(group.get("lion", False))
+    if lion:
+        pass                       # lion keeps no second moment (optimizer.py:2857)
+    elif quad:
         st["exp_avg_sq"] = torch.zeros((n // 4,), dtype=vdt, device=dev)
     else:
         st["exp_avg_sq"] = torch.zeros(p.shape, dtype=vdt, device=dev)
     # an fp16 v holds the second moment times a dynamic scale, 1024 at first
     # (optimizer.py:2889-2898); every other v is unscaled
-    scaled = bool(group.get("dynamic_scaling", True)) and vdt == torch.float16
+    scaled = bool(group.get("dynamic_scaling", True)) and vdt == torch.float16 and not lion
     st["scale_v"] = 1024.0 if scaled else 1.0
     st["sqrt_scale_v"] = 32.0 if scaled else 1.0
     return st

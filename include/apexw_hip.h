@@ -173,6 +173,14 @@ typedef struct apexw_unit {
                                           16-byte aligned unless APEXW_FLAG_SCALAR).  Cold and replay:
                                           v' as stored; native: the fp32 v' (torch._fused_adamw_),
                                           vmax stored rounded.  A NaN on either side gives NaN. */
+#define APEXW_HP_LION (1u << 12)       /* lion=True.  Compact step (cold and replay modes; no
+                                          APEXW_HP_NESTEROV / _CAUTIOUS / _AMSGRAD, no quad rows): with
+                                          g' the prepared grad in m's dtype, p += a * sign(lerp(g', m,
+                                          beta1)) (look_coef / APEXW_HP_LOOK_HI; the lerp rounded to m's
+                                          dtype, sign(0) = sign(NaN) = 0), a = -gain_hi (gain_hi = lr),
+                                          rounded to p's dtype when p and m share a 16-bit dtype; then m
+                                          = lerp(m, g', 1 - beta2) (lerp_coef / APEXW_HP_LERP_HI).  v is
+                                          neither read nor written (descriptors may point v at m). */
 
 /* Step scalars of one launch, written on the device by apexw_amp_prepare (32 bytes). */
 typedef struct apexw_amp_dyn {

@@ -1,8 +1,8 @@
 """Compact-mode multi-tensor AdamW step (CPU oracle; test infrastructure only).
 
 Restates ``ApexW._multi_tensor_step`` (``apexw/optimizer.py:5297-5887``) for the
-AdamW update and its nesterov, cautious and amsgrad variants (no lion / AdEMAMix)
-with the same torch ops, so every bf16 rounding point of the reference is
+AdamW update, its nesterov, cautious and amsgrad variants and the lion update (no
+AdEMAMix) with the same torch ops, so every bf16 rounding point of the reference is
 reproduced:
 
 1. decoupled weight decay ``p *= 1 - lr*wd`` (dim>=2 tensors when
@@ -21,6 +21,10 @@ reproduced:
    the same in fp32 (:5728-5731);
    amsgrad: ``max_v = maximum(max_v, v)`` after the v EMA and ``d`` from max_v instead of v
    (:5788-5790; the quad branch :5700-5702 is never reached, quad v being off under amsgrad)
+
+lion (``lion_update``) replaces steps 2-5 after the weight decay: u = lerp(g', m, b1) with g'
+the grads cast to m's dtype, ``p += -lr * sign(u)``, ``m = lerp(m, g', 1-b2)`` -- :5677-5683
+(the replayed plan: :1214-1225, the same ops)
 
 That is the *cold* step, taken whenever the optimizer (re)builds its cached
 execution plan.  Every later step replays the plan through
@@ -79,6 +83,17 @@ def _denominators(vs, eps_scaled, scale_v, sqrt_scale_v):
     return dens
 
 
+def lion_update(params, grads, ms, *, lr, beta1, beta2):
+    """The lion update of a subgroup after its weight decay (optimizer.py:5677-5683,
+    :1214-1225): grads cast to m's dtype, sign of lerp(g', m, beta1) times -lr added to
+    p (one foreach add with alpha), then m = lerp(m, g', 1 - beta2)."""
+    target = ms[0].dtype
+    gc = [g.to(target) for g in grads] if grads[0].dtype != target else list(grads)
+    updates = [u.sign() for u in torch._foreach_lerp(gc, ms, beta1)]
+    torch._foreach_add_(params, updates, alpha=-lr)
+    torch._foreach_lerp_(ms, gc, 1.0 - beta2)
+
+
 def _amsgrad_max(max_vs, vs):
     """amsgrad: max_v = maximum(max_v, v) in place and the denominators' source
     (optimizer.py:5788-5790, :1253-1255); plain v otherwise."""
@@ -111,7 +126,7 @@ def _masked(nums, lhs, rhs, params):
 
 def compact_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weight_decay,
                           decay_norm_only, step, is_quad, stochastic, scale_v=1.0, sqrt_scale_v=1.0,
-                          nesterov=False, cautious=False, max_vs=None):
+                          nesterov=False, cautious=False, max_vs=None, lion=False):
     """One step over a subgroup sharing (p dtype, m dtype, step count, quad flag).
 
     ``step`` is the already-incremented step count.  Tensors are updated in place.
@@ -124,6 +139,9 @@ def compact_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weigh
         decay = [p for p in params if p.dim() >= 2] if decay_norm_only else list(params)
         if decay:
             torch._foreach_mul_(decay, 1.0 - lr * weight_decay)
+    if lion:
+        lion_update(params, grads, ms, lr=lr, beta1=beta1, beta2=beta2)
+        return
     gf = [g if g.dtype == torch.float32 else g.float() for g in grads]
     if ms[0].dtype in (torch.bfloat16, torch.float16):
         torch._foreach_mul_(ms, beta1)
@@ -185,17 +203,20 @@ def compact_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weigh
 
 def replay_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weight_decay,
                          apply_wd_mask, step, is_quad, stochastic, scale_v=1.0, sqrt_scale_v=1.0,
-                         nesterov=False, cautious=False, max_vs=None):
+                         nesterov=False, cautious=False, max_vs=None, lion=False):
     """One replayed step over an (p dtype, compact, quad) subgroup (optimizer.py:1200-1338).
 
     With an fp16 parameter, m or v the denominators are clamped below by eps
     (:1202, :1264-1265, :1310-1311)."""
-    has_fp16 = torch.float16 in (params[0].dtype, ms[0].dtype, vs[0].dtype)
     step_size, eps_scaled = bias_terms(lr, beta1, beta2, eps, step)
     if weight_decay != 0.0:
         decay = [p for p, w in zip(params, apply_wd_mask) if w]
         if decay:
             torch._foreach_mul_(decay, 1.0 - lr * weight_decay)
+    if lion:
+        lion_update(params, grads, ms, lr=lr, beta1=beta1, beta2=beta2)
+        return
+    has_fp16 = torch.float16 in (params[0].dtype, ms[0].dtype, vs[0].dtype)
     if grads[0].dtype == ms[0].dtype:
         torch._foreach_lerp_(ms, grads, 1.0 - beta1)
     else:

@@ -91,7 +91,7 @@ def init_state(p, group, n_params_in_group, peft_ctx, has_16bit_params=None, cud
     amsgrad adds ``max_exp_avg_sq``: numel zeros in p's shape, fp32 for quantized v,
     else v's dtype (optimizer.py:2878-2886)."""
     st = _init_state(p, group, n_params_in_group, peft_ctx, has_16bit_params, cuda)
-    if group.get("amsgrad", False):
+    if group.get("amsgrad", False) and not group.get("lion", False):
         ensure_max_v(st, p)
     return st
 
@@ -114,6 +114,7 @@ def _init_state(p, group, n_params_in_group, peft_ctx, has_16bit_params, cuda):
     n = p.numel()
     is_peft = is_peft_param(p) or peft_ctx
     ams = bool(group.get("amsgrad", False))
+    lion = bool(group.get("lion", False))
     threshold = group.get("threshold", 65536)
     massive = p.dim() >= 2 or n >= threshold
     if group.get("fused") is True or prec == "full":
@@ -145,7 +146,7 @@ def _init_state(p, group, n_params_in_group, peft_ctx, has_16bit_params, cuda):
         if not massive:
             return _dense(st, p, torch.float32, group, is_peft, n_params_in_group, prec)
         cdt = compact_dtype(p)
-        if bool(group.get("factored_v", False)) and can_factor(p, is_peft, 524288, ams):
+        if bool(group.get("factored_v", False)) and can_factor(p, is_peft, 524288, ams or lion):
             st["is_factored_v"] = True
             return _factored_compact(st, p, cdt)
         return _dense(st, p, cdt, group, is_peft, n_params_in_group, prec)
@@ -154,8 +155,8 @@ def _init_state(p, group, n_params_in_group, peft_ctx, has_16bit_params, cuda):
         narrow = p.dim() >= 2 and min(p.shape) <= 32 and n < 2048
         raw_int4 = group.get("int4_m")
         pow2 = bs >= 64 and (bs & (bs - 1)) == 0
-        fv = bool(group.get("factored_v", False)) and can_factor(p, is_peft, 65536, ams)
-        auto_sub = (raw_int4 is not False and not fv and not ams and n >= 16384 and n % 4 == 0 and pow2
+        fv = bool(group.get("factored_v", False)) and can_factor(p, is_peft, 65536, ams or lion)
+        auto_sub = (raw_int4 is not False and not fv and not ams and not lion and n >= 16384 and n % 4 == 0 and pow2
                     and (p.dim() < 2 or min(p.shape) >= 8))
         six = bool(group.get("six_bit", False)) and fv and n >= 524288 and bs % 4 == 0
         int4 = auto_sub or (bool(raw_int4) and not fv and n >= 512 and n >= bs and not narrow and not is_peft)
@@ -186,7 +187,7 @@ def _init_state(p, group, n_params_in_group, peft_ctx, has_16bit_params, cuda):
     if prec == "8bit":
         st.update(is_8bit=False, is_factored_v=False, is_6bit_m=False, is_4bit_m=False, is_quad_v=False)
     elif prec == "compact":
-        fv = bool(group.get("factored_v", False)) and can_factor(p, is_peft, 524288, ams)
+        fv = bool(group.get("factored_v", False)) and can_factor(p, is_peft, 524288, ams or lion)
         st.update(is_6bit_m=False, is_4bit_m=False, is_factored_v=fv)
         if fv:
             return _factored_compact(st, p, compact_dtype(p))
@@ -210,23 +211,25 @@ def _factored_compact(st, p, mdt):
 
 def _dense(st, p, mdt, group, is_peft, n_params_in_group, prec):
     """m in ``mdt``, v in the dtype the beta2 rule gives, quad-shared v for large
-    16-bit compact/auto tensors, not under nesterov or amsgrad (optimizer.py:2788-2810,
-    :2838-2872)."""
+    16-bit compact/auto tensors, not under nesterov, amsgrad or lion; no v under lion
+    (optimizer.py:2788-2810, :2838-2872)."""
     n = p.numel()
     vdt = v_dtype(mdt, group["betas"][1], group.get("force_compact_v", False), bool(group["stochastic_rounding"]))
     quad = (prec in ("compact", "auto") and mdt in (torch.bfloat16, torch.float16)
             and vdt in (torch.bfloat16, torch.float16)
             and group.get("int4_m") is not False and not group.get("nesterov", False)
-            and not group.get("amsgrad", False) and n >= 16384 and n % 4 == 0
+            and not group.get("amsgrad", False) and not group.get("lion", False) and n >= 16384 and n % 4 == 0
             and (p.dim() < 2 or min(p.shape) >= 8) and (is_peft or n_params_in_group >= 8))
     if quad:
         st["is_quad_v"] = True
     st["state_dtype"] = mdt
     st["state_dtype_v"] = vdt
     st["exp_avg"] = torch.zeros(p.shape, dtype=mdt)
-    st["exp_avg_sq"] = torch.zeros((n // 4,), dtype=vdt) if quad else torch.zeros(p.shape, dtype=vdt)
+    lion = bool(group.get("lion", False))
+    if not lion:                   # lion keeps no second moment (optimizer.py:2857)
+        st["exp_avg_sq"] = torch.zeros((n // 4,), dtype=vdt) if quad else torch.zeros(p.shape, dtype=vdt)
     # fp16 v starts with a dynamic scale of 1024 (optimizer.py:2889-2898)
-    fp16_scaled = bool(group.get("dynamic_scaling", True)) and vdt == torch.float16
+    fp16_scaled = bool(group.get("dynamic_scaling", True)) and vdt == torch.float16 and not lion
     st["scale_v"] = 1024.0 if fp16_scaled else 1.0
     st["sqrt_scale_v"] = 32.0 if fp16_scaled else 1.0
     return st

@@ -68,7 +68,7 @@ class OracleApexW:
                  adamw_compat=False, clip_grad_norm=None, precision="compact", stochastic_rounding=True,
                  block_size=None, force_compact_v=False, int4_m=None, grad_centralization=False,
                  factored_v=False, six_bit=False, threshold=65536, amp=None, dynamic_scaling=True, nesterov=False,
-                 cautious=False, maximize=False, amsgrad=False, fused=None):
+                 cautious=False, maximize=False, amsgrad=False, fused=None, lion=False):
         precision = normalize_precision(precision)
         if betas is None:
             betas = (0.9, 0.999) if precision in ("8bit", "full") else (0.9, 0.99)
@@ -84,7 +84,7 @@ class OracleApexW:
                           grad_centralization=grad_centralization, factored_v=factored_v, six_bit=six_bit,
                           threshold=threshold, amp=amp, dynamic_scaling=dynamic_scaling, nesterov=bool(nesterov),
                           cautious=bool(cautious), maximize=bool(maximize), amsgrad=bool(amsgrad),
-                          fused=fused, params=self.params)
+                          fused=fused, lion=bool(lion), params=self.params)
         self.state = {}
         self._plan = None
         self.grad_scale = None
@@ -97,8 +97,13 @@ class OracleApexW:
         active = set(plan["params"])
         if any(p.grad is None for p in plan["params"]):
             return False
-        # amsgrad switched on or off since the plan was made (optimizer.py:585-586)
+        # amsgrad switched on or off since the plan was made (optimizer.py:585-586): the
+        # plan holds max lists only when made with amsgrad and without lion
         if plan["amsgrad"] != self.group["amsgrad"]:
+            return False
+        # the native fused plan does not replay the variants (optimizer.py:593-600)
+        grp = self.group
+        if plan["kind"] == "native" and (grp["nesterov"] or grp["lion"] or grp["cautious"] or grp["maximize"]):
             return False
         return all(p.grad is None for p in self.params if p.requires_grad and p not in active)
 
@@ -168,12 +173,14 @@ class OracleApexW:
         for p in plist:
             if p not in self.state:
                 self.state[p] = L.init_state(p, grp, len(self.params), peft)
-            elif grp["amsgrad"] and not grp["precision"] in ("8bit", "ultra"):
+            elif grp["amsgrad"] and not grp["lion"] and not grp["precision"] in ("8bit", "ultra"):
                 L.ensure_max_v(self.state[p], p)      # amsgrad switched on later (optimizer.py:2917-2922)
         prec = grp["precision"]
         ams = grp["amsgrad"]
-        if ams and prec in ("8bit", "ultra"):
-            raise NotImplementedError("oracle: amsgrad in the 8bit / ultra precisions")
+        if (ams or grp["lion"]) and prec in ("8bit", "ultra"):
+            raise NotImplementedError("oracle: amsgrad / lion in the 8bit / ultra precisions")
+        lion = grp["lion"]
+        ams = ams and not lion                  # lion keeps no v, nor its max (optimizer.py:5375-5380)
         quantized = prec in ("8bit", "ultra")     # both run _step_ultra (optimizer.py:3583-3587)
         grads, scale = self._prepare(self._signed([p.grad for p in plist], quantized),
                                      sanitize=not quantized or grp["clip_grad_norm"] is not None)
@@ -189,7 +196,8 @@ class OracleApexW:
         sts = [self.state[p] for p in plist]
         homogeneous = all("exp_avg_sq" in st and st["exp_avg"].dtype == st["exp_avg_sq"].dtype == p.dtype
                           and st["exp_avg"].numel() == st["exp_avg_sq"].numel() for p, st in zip(plist, sts))
-        if homogeneous and grp["fused"] is not False and not (grp["maximize"] or grp["nesterov"] or grp["cautious"]):
+        if homogeneous and grp["fused"] is not False and not (grp["maximize"] or grp["nesterov"] or grp["cautious"]
+                                                              or lion):
             # maximize, nesterov and cautious leave the native fused step (optimizer.py:3733, :593-600),
             # and so does fused=False (:3723)
             self._native_fused(plist, grads, sts, grad_scale=scale, amsgrad=ams, **kw)
@@ -214,9 +222,9 @@ class OracleApexW:
             for _, _, st in items:
                 st["step"].add_(1)
             step = int(items[0][2]["step"].item())
-            vs = [i[2]["exp_avg_sq"] for i in items]
+            vs = [i[2].get("exp_avg_sq") for i in items]
             scale_v, sqrt_scale_v = 1.0, 1.0
-            if grp.get("dynamic_scaling", True) and mdt == torch.float16:
+            if grp.get("dynamic_scaling", True) and mdt == torch.float16 and not lion:
                 # the subgroup's v scale lives in its parameters' states; every 100 steps
                 # it is recalibrated from max(v) (optimizer.py:5600-5645; keyed on m's dtype)
                 st0 = items[0][2]
@@ -233,13 +241,15 @@ class OracleApexW:
                                   [i[2]["exp_avg"] for i in items], vs, step=step, is_quad=quad,
                                   stochastic=grp["stochastic_rounding"], scale_v=scale_v,
                                   sqrt_scale_v=sqrt_scale_v, nesterov=grp["nesterov"],
-                                  cautious=grp["cautious"],
+                                  cautious=grp["cautious"], lion=lion,
                                   max_vs=[i[2]["max_exp_avg_sq"] for i in items] if ams else None, **kw)
         # the replayed plan's per-subgroup scales start at 1.0 (optimizer.py:546-560)
         self._plan = {"kind": "foreach", "params": plan_params, "sg_scale": {}, "amsgrad": ams}
 
     def _is_quad(self, p):
-        v = self.state[p]["exp_avg_sq"]
+        v = self.state[p].get("exp_avg_sq")
+        if v is None:                           # lion: no second moment
+            return False
         return p.numel() >= 4 and p.numel() % 4 == 0 and v.numel() * 4 == p.numel()
 
     def _replay(self):
@@ -258,7 +268,8 @@ class OracleApexW:
             return
         grads, scale = self._prepare(self._signed(grads, False), sanitize=grp["clip_grad_norm"] is not None)
         sts = [self.state[p] for p in plist]
-        ams = plan["amsgrad"]
+        lion = grp["lion"]
+        ams = plan["amsgrad"] and not lion
         if plan["kind"] == "native":
             self._native_fused(plist, grads, sts, sanitize=False, grad_scale=scale, amsgrad=ams, **kw)
             return
@@ -283,8 +294,8 @@ class OracleApexW:
             # takes its scale from the first parameter's state, which the replay never
             # updates (optimizer.py:1165-1178, :1193-1199)
             for key, items in sub.items():
-                vs = [i[2]["exp_avg_sq"] for i in items]
-                if vs[0].dtype == torch.float16:
+                vs = [i[2].get("exp_avg_sq") for i in items]
+                if vs[0] is not None and vs[0].dtype == torch.float16:
                     rescale_v(vs, sg_scale.get(key, 1.0))
         for key, items in sub.items():
             quad = key[2]
@@ -293,11 +304,11 @@ class OracleApexW:
             sqrt_scale_v = st0.get("sqrt_scale_v", math.sqrt(scale_v))
             sg_scale[key] = scale_v
             replay_subgroup_step([i[0] for i in items], [i[1] for i in items],
-                                 [i[2]["exp_avg"] for i in items], [i[2]["exp_avg_sq"] for i in items],
+                                 [i[2]["exp_avg"] for i in items], [i[2].get("exp_avg_sq") for i in items],
                                  apply_wd_mask=[(i[0].dim() >= 2) if dno else True for i in items],
                                  step=step, is_quad=quad, stochastic=grp["stochastic_rounding"],
                                  scale_v=scale_v, sqrt_scale_v=sqrt_scale_v, nesterov=grp["nesterov"],
-                                 cautious=grp["cautious"],
+                                 cautious=grp["cautious"], lion=lion,
                                  max_vs=[i[2]["max_exp_avg_sq"] for i in items] if ams else None, **kw)
 
     def _factored(self, p, g, st, step, inv, sanitize):

@@ -530,6 +530,15 @@ PREC_CASES = {
                               dict(PREC_KW, precision="auto", adamw_compat=True, amsgrad=True)),
     "compact_bf16_amsgrad_cautious_rne": (PREC_SHAPES, torch.bfloat16, 4, 90,
                                           dict(PREC_KW, amsgrad=True, cautious=True)),
+    # lion=True in the compact-kernel precisions: m only (no v, no quad), the sign update with
+    # -lr rounded to a shared 16-bit dtype, m = lerp(m, g, 1 - beta2); cold then replayed.
+    # lr 1e-2 moves bf16 parameters of 0.02 by more than half an ulp.  (The reference's step
+    # raises IndexError for lion when the first tensor's m is fp32 -- its fused-path test
+    # indexes the empty v list, optimizer.py:3684-3687 -- so "full" has no trajectory.)
+    "compact_bf16_lion_rne": (PREC_SHAPES, torch.bfloat16, 5, 91, dict(PREC_KW, lion=True, lr=1e-2)),
+    "compact_fp32_lion_rne": (PREC_SHAPES, torch.float32, 4, 92, dict(PREC_KW, lion=True)),
+    "auto_bf16_lion_rne": (PREC_SHAPES, torch.bfloat16, 4, 95,
+                           dict(PREC_KW, precision="auto", adamw_compat=True, lion=True, lr=1e-2)),
 }
 
 
@@ -557,6 +566,8 @@ FP16_CASES = {
     # scale (fused=False)
     "fp16_amsgrad_native_rne": (FP16_SHAPES, 4, 58, dict(FP16_KW, amsgrad=True, betas=(0.9, 0.5)), ()),
     "fp16_amsgrad_foreach_rne": (FP16_SHAPES, 5, 59, dict(FP16_KW, amsgrad=True, fused=False), ()),
+    # lion: fp16 m, -lr rounded to fp16
+    "fp16_lion_rne": (FP16_SHAPES, 4, 60, dict(FP16_KW, lion=True, lr=1e-2), ()),
 }
 
 

@@ -162,12 +162,15 @@ def test_constructor_contract():
         ApexW(p, block_size=0)
     with pytest.raises(ValueError):
         ApexW(p, precision="nope")
-    # amsgrad: the compact, full and auto precisions, not 8bit / ultra nor factored_v
-    for prec in ("compact", "full", "auto"):
-        assert ApexW(p, precision=prec, amsgrad=True).defaults["amsgrad"]
-    for kw in (dict(precision="8bit"), dict(precision="ultra"), dict(precision="compact", factored_v=True)):
-        with pytest.raises(NotImplementedError):
-            ApexW(p, amsgrad=True, **kw)
+    # amsgrad and lion: the compact, full and auto precisions, not 8bit / ultra; factored_v=True
+    # is accepted and lays out no factored state under them, as in the reference
+    for opt in ("amsgrad", "lion"):
+        for prec in ("compact", "full", "auto"):
+            assert ApexW(p, precision=prec, **{opt: True}).defaults[opt]
+        assert ApexW(p, precision="compact", factored_v=True, **{opt: True}).defaults["factored_v"]
+        for prec in ("8bit", "ultra"):
+            with pytest.raises(NotImplementedError):
+                ApexW(p, precision=prec, **{opt: True})
     # nesterov: every precision, without factored second moments
     for prec in ("8bit", "ultra", "3byte", "compact", "full", "auto"):
         assert ApexW(p, precision=prec, nesterov=True).defaults["nesterov"]

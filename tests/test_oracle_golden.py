@@ -79,7 +79,7 @@ def test_oracle_matches_reference_trajectory(name, monkeypatch):
         assert int(s.get("block_size_8bit", 0) or 0) == fl[3]
 
 
-VARIANT_OPTIONS = ("amsgrad", "maximize", "nesterov", "cautious")
+VARIANT_OPTIONS = ("amsgrad", "lion", "maximize", "nesterov", "cautious")
 
 
 @pytest.mark.parametrize("name", sorted(n for n in CASES if any(o in n for o in VARIANT_OPTIONS)))
@@ -126,6 +126,25 @@ def test_amsgrad_goldens_pin_the_max_in_the_denominator(name, monkeypatch):
     assert (opt._plan["kind"] == "native") == (name in AMSGRAD_NATIVE)
     if name in AMSGRAD_NATIVE:
         return
+    assert any(not np.array_equal(_as_np(p.data).reshape(-1), gold[f"p_{i}"].reshape(-1))
+               for i, p in enumerate(params))
+
+
+@pytest.mark.parametrize("name", ["compact_bf16_lion_rne", "fp16_lion_rne"])
+def test_lion_goldens_pin_the_rounded_scalar(name, monkeypatch):
+    """The 16-bit lion trajectories tell torch's same-dtype add (the scalar -lr rounded to
+    the tensors' dtype) from an fp32 scalar: an oracle with the latter ends elsewhere."""
+    import oracle.compact as C
+
+    def fp32_alpha(params, grads, ms, *, lr, beta1, beta2):
+        target = ms[0].dtype
+        gc = [g.to(target) for g in grads] if grads[0].dtype != target else list(grads)
+        for p, g, m in zip(params, gc, ms):
+            u = torch.lerp(g, m, beta1).sign()
+            p.copy_((p.float() - lr * u.float()).to(p.dtype))
+        torch._foreach_lerp_(ms, gc, 1.0 - beta2)
+    monkeypatch.setattr(C, "lion_update", fp32_alpha)
+    params, _, gold = replay(name, OracleApexW)
     assert any(not np.array_equal(_as_np(p.data).reshape(-1), gold[f"p_{i}"].reshape(-1))
                for i, p in enumerate(params))
 

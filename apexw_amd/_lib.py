@@ -13,7 +13,7 @@ import numpy as np
 
 from ._build import LIB_PATH
 
-ABI_VERSION = 22
+ABI_VERSION = 23
 
 # dtype codes
 F32, BF16, F16, U8, I8 = 0, 1, 2, 3, 4
@@ -49,6 +49,8 @@ HP_NESTEROV = 1 << 9
 HP_CAUTIOUS = 1 << 10
 HP_AMSGRAD = 1 << 11
 HP_LION = 1 << 12
+HP_SLOW = 1 << 13
+HP_LERP3_HI = 1 << 14
 
 STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported dtype combination", 3: "launch failed",
           4: "misaligned pointer", 5: "exceeds the fixed workspace of the allocation-free entry point"}
@@ -92,10 +94,11 @@ class HParams(ctypes.Structure):
                 ("clip_coef", ctypes.c_void_p), ("seed", ctypes.c_uint64), ("step", ctypes.c_uint32),
                 ("mode", ctypes.c_uint32), ("flags", ctypes.c_uint32), ("grad_inv_scale", ctypes.c_float),
                 ("amp", ctypes.c_void_p), ("rows", ctypes.c_void_p), ("counts", ctypes.c_void_p),
-                ("max_v", ctypes.c_void_p)]
+                ("max_v", ctypes.c_void_p), ("beta3", ctypes.c_float), ("one_minus_beta3", ctypes.c_float),
+                ("lerp3_coef", ctypes.c_float), ("slow_ratio", ctypes.c_float), ("slow", ctypes.c_void_p)]
 
 
-assert ctypes.sizeof(HParams) == 120
+assert ctypes.sizeof(HParams) == 144
 # apexw_row_means: grad centralization's row means of one 8-bit / ultra descriptor
 ROW_MEANS_DTYPE = np.dtype([("means", np.uint64), ("row_len", np.int64)])
 

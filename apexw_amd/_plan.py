@@ -101,6 +101,11 @@ class StepPlan:
         self.lion = self._lion_of(group)
         # amsgrad=True: the compact step keeps a running max of v (hparams.max_v)
         self.amsgrad = self._amsgrad_of(group)
+        # beta3 (AdEMAMix): the compact step keeps a slow first moment (hparams.slow);
+        # slow_made: whether the group had beta3 when the plan was made (validity)
+        self.slow = self._slow_of(group)
+        self.slow_made = group.get("beta3") is not None
+        self.beta3, self.alpha = group.get("beta3"), float(group.get("alpha", 5.0))
         self.d_counts = None
         self.cold_done = False
         self._nesterov = False
@@ -124,6 +129,12 @@ class StepPlan:
         the in-backward batches nor the per-parameter update (which step without it,
         optimizer.py:2360, :2373-2471)."""
         return (bool(group.get("amsgrad", False)) and self.kind == "compact" and not self.hooked
+                and not self._lion_of(group))
+
+    def _slow_of(self, group):
+        """beta3 as this plan's kernels take it: the compact step without lion, not the
+        in-backward batches nor the per-parameter update (optimizer.py:2360, :2373-2471)."""
+        return (group.get("beta3") is not None and self.kind == "compact" and not self.hooked
                 and not self._lion_of(group))
 
     def _lion_of(self, group):
@@ -151,6 +162,9 @@ class StepPlan:
         # optimizer.py:585-586: the plan holds max_exp_avg_sq lists only when it was made
         # with amsgrad and without lion, so lion with amsgrad makes every step a cold one)
         if self.kind == "compact" and not self.hooked and bool(group.get("amsgrad", False)) != self.amsgrad:
+            return False
+        # beta3 set or cleared: a new plan (optimizer.py:587-588)
+        if (group.get("beta3") is not None) != self.slow_made:
             return False
         if self.kind == "q8":
             # cautious keeps every 8-bit tensor in the generic order: another table
@@ -282,6 +296,16 @@ class StepPlan:
                     raise NotImplementedError(f"apexw_amd: amsgrad state of tensor {i} ({tuple(p.shape)}): "
                                               "max_exp_avg_sq must be a contiguous full-size tensor in v's dtype")
                 self.max_v_ptrs[i] = mx.data_ptr()
+        self.slow_ptrs = self.d_slow = None
+        if self.slow:
+            self.slow_ptrs = np.zeros(n, dtype=np.uint64)
+            for i, (p, st) in enumerate(zip(self.params, self.states)):
+                ms, m = st.get("exp_avg_slow"), st["exp_avg"]
+                if (ms is None or tab[i]["flags"] & (L.FLAG_QUAD | L.FLAG_FACTORED) or ms.numel() != p.numel()
+                        or ms.dtype != m.dtype or not ms.is_contiguous() or ms.device != p.device):
+                    raise NotImplementedError(f"apexw_amd: beta3 state of tensor {i} ({tuple(p.shape)}): "
+                                              "exp_avg_slow must be a contiguous full-size tensor in m's dtype")
+                self.slow_ptrs[i] = ms.data_ptr()
         # per tensor {scale_v, sqrt(scale_v)} of this launch, for rows flagged APEXW_FLAG_VSCALE
         self.vscaled = (tab["flags"] & np.uint32(L.FLAG_VSCALE)) != 0
         self.d_vscale = self.h_vscale = None
@@ -410,6 +434,8 @@ class StepPlan:
         if self.max_v_ptrs is not None:
             # hparams.max_v: one pointer per descriptor, in device-table order
             self.d_max_v = _upload(np.ascontiguousarray(self.max_v_ptrs[perm]), self.device)
+        if self.slow_ptrs is not None:
+            self.d_slow = _upload(np.ascontiguousarray(self.slow_ptrs[perm]), self.device)
         self.d_unit_begin = _upload(self.unit_begin, self.device)
         # the step kernels' units: all but the factored rows' (apexw_factored_step steps
         # those; the clip's norm pass still covers every unit).  Factored tensors are
@@ -517,8 +543,9 @@ class StepPlan:
         recomputed for all rows at once."""
         tab = self.host_table
         scalar = ((tab["p"] | tab["g"] | tab["m"] | tab["v"]) & np.uint64(15)) != 0
-        if self.max_v_ptrs is not None:
-            scalar |= (self.max_v_ptrs & np.uint64(15)) != 0
+        for extra in (self.max_v_ptrs, self.slow_ptrs):
+            if extra is not None:
+                scalar |= (extra & np.uint64(15)) != 0
         if self.kind == "q8":
             scalar |= (tab["block"] % 8) != 0
         bit = np.uint32(L.FLAG_SCALAR)
@@ -570,7 +597,7 @@ class StepPlan:
         # could not skip an inf / NaN step: such plans read found_inf on the host
         return not (self.hooked or self.single or self.factored.any() or self.vscaled.any()
                     or (self.gc and not self.gc_fold) or self.maximize
-                    or (self.kind == "compact" and self.nesterov))
+                    or (self.kind == "compact" and self.nesterov) or self.slow)
 
     def amp_fold(self, sync=False):
         """Subtract from the step counters the steps GradScaler skipped that the host
@@ -734,6 +761,9 @@ class StepPlan:
             self.d_counts = torch.zeros(len(self.params), dtype=torch.int64, device=self.device)
         # the in-backward flush steps without nesterov whatever the group says (optimizer.py:2358)
         self._nesterov = bool(group.get("nesterov", False)) and not (self.single or self.hooked)
+        # beta3's value and alpha are read from the group each step, as the reference's step does
+        if self.slow:
+            self.beta3, self.alpha = group["beta3"], float(group.get("alpha", 5.0))
         keep = self._refresh_grads()      # contiguous copies of non-contiguous grads, alive until the launch
         if amp is not None:
             inv_scale = 1.0          # a stand-in: the kernels read the factor from the device scalars
@@ -996,7 +1026,7 @@ class StepPlan:
                 # the counts from apexw_compact_cautious_count
                 flags |= L.HP_CAUTIOUS
                 hp.counts = self.d_counts.data_ptr()
-            elif self._nesterov:
+            elif self._nesterov and not self.slow:
                 # nesterov (optimizer.py:5865-5877, :1329-1331): p += (-step_size*b1) m / d, then
                 # p += (-step_size*(1-b1)) g / d, the Python products taken to fp32 by torch;
                 # quad tensors take lerp(g, m, b1) as the numerator (look_coef below)
@@ -1028,6 +1058,17 @@ class StepPlan:
             # torch._fused_adamw_ for the native plan)
             flags |= L.HP_AMSGRAD
             hp.max_v = self.d_max_v.data_ptr()
+        if self.slow:
+            # beta3 (AdEMAMix): the slow moment's EMA and its weight alpha (1 - b1^t) / (1 - b3^t)
+            # in double, as the reference's (optimizer.py:5584, :1101); nesterov does not apply
+            b3 = float(self.beta3)
+            flags |= L.HP_SLOW
+            hp.slow = self.d_slow.data_ptr()
+            hp.beta3, hp.one_minus_beta3 = b3, 1.0 - b3
+            hp.lerp3_coef, hi = _lerp_coef(1.0 - b3)
+            if hi:
+                flags |= L.HP_LERP3_HI
+            hp.slow_ratio = self.alpha * ((1.0 - b1 ** step) / (1.0 - b3 ** step))
         hp.seed = seed
         hp.step = step & 0xFFFFFFFF
         hp.flags = flags

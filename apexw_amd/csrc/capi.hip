@@ -96,6 +96,8 @@ bool hp_ok(const apexw_hparams* hp) {
   if ((hp->flags & APEXW_HP_CAUTIOUS) && (!hp->counts || hp->mode == APEXW_MODE_SINGLE)) return false;
   if ((hp->flags & APEXW_HP_AMSGRAD) && (!hp->max_v || ((uintptr_t)hp->max_v & 7u) || hp->mode == APEXW_MODE_SINGLE))
     return false;
+  if ((hp->flags & APEXW_HP_SLOW) && (!hp->slow || ((uintptr_t)hp->slow & 7u) || hp->mode == APEXW_MODE_SINGLE))
+    return false;
   if (hp->flags & APEXW_HP_AMP) {
     // device-side AMP scalars: the compact and 8-bit step modes, with the unscale they carry
     if (!hp->amp || ((uintptr_t)hp->amp & 15u) || hp->mode == APEXW_MODE_SINGLE) return false;
@@ -182,15 +184,19 @@ static int launch_args_status(int32_t kind, int32_t n_tensors, int64_t n_units, 
       // lion: the cold and replayed orders, alone (it takes the place of the AdamW update)
       if ((hp->flags & APEXW_HP_LION) &&
           (hp->mode == APEXW_MODE_NATIVE || hp->mode == APEXW_MODE_SINGLE ||
-           (hp->flags & (APEXW_HP_NESTEROV | APEXW_HP_CAUTIOUS | APEXW_HP_AMSGRAD))))
+           (hp->flags & (APEXW_HP_NESTEROV | APEXW_HP_CAUTIOUS | APEXW_HP_AMSGRAD | APEXW_HP_SLOW))))
+        return APEXW_ERR_ARG;
+      // beta3: the cold and replayed orders with the host's slow_ratio (no device AMP), not with cautious
+      if ((hp->flags & APEXW_HP_SLOW) &&
+          (hp->mode == APEXW_MODE_NATIVE || (hp->flags & (APEXW_HP_CAUTIOUS | APEXW_HP_AMP))))
         return APEXW_ERR_ARG;
       return APEXW_OK;
     case APEXW_LAUNCH_ULTRA:
-      if (n_fast_units || n_fast_f32_units || (hp->flags & (APEXW_HP_AMSGRAD | APEXW_HP_LION))) return APEXW_ERR_ARG;
+      if (n_fast_units || n_fast_f32_units || (hp->flags & (APEXW_HP_AMSGRAD | APEXW_HP_LION | APEXW_HP_SLOW))) return APEXW_ERR_ARG;
       return (hp->mode == APEXW_MODE_NATIVE || hp->mode == APEXW_MODE_SINGLE) ? APEXW_ERR_ARG : APEXW_OK;
     case APEXW_LAUNCH_Q8:
       if (n_fast_units < 0 || n_fast_f32_units < 0 || n_fast_units + n_fast_f32_units > n_units) return APEXW_ERR_ARG;
-      if (hp->mode == APEXW_MODE_NATIVE || (hp->flags & (APEXW_HP_AMSGRAD | APEXW_HP_LION))) return APEXW_ERR_ARG;
+      if (hp->mode == APEXW_MODE_NATIVE || (hp->flags & (APEXW_HP_AMSGRAD | APEXW_HP_LION | APEXW_HP_SLOW))) return APEXW_ERR_ARG;
       if (hp->mode == APEXW_MODE_SINGLE && (n_fast_units || n_fast_f32_units)) return APEXW_ERR_ARG;
       return APEXW_OK;
     case APEXW_LAUNCH_CAUTIOUS:
@@ -199,7 +205,7 @@ static int launch_args_status(int32_t kind, int32_t n_tensors, int64_t n_units, 
       if (hp->mode == APEXW_MODE_NATIVE || hp->mode == APEXW_MODE_SINGLE) return APEXW_ERR_ARG;
       return ((uintptr_t)hp->counts & 7u) ? APEXW_ERR_ALIGN : APEXW_OK;
     case APEXW_LAUNCH_FACTORED:
-      if (n_fast_units || n_fast_f32_units || (hp->flags & (APEXW_HP_AMSGRAD | APEXW_HP_LION))) return APEXW_ERR_ARG;
+      if (n_fast_units || n_fast_f32_units || (hp->flags & (APEXW_HP_AMSGRAD | APEXW_HP_LION | APEXW_HP_SLOW))) return APEXW_ERR_ARG;
       if (hp->mode == APEXW_MODE_SINGLE || hp->mode == APEXW_MODE_NATIVE) return APEXW_ERR_ARG;
       return (hp->flags & APEXW_HP_AMP) ? APEXW_ERR_ARG : APEXW_OK;   // factored steps take host-read AMP scalars
     default:

@@ -117,6 +117,27 @@ template <int GD, int MD> APEXW_DEV void m_update8(float (&m)[8], const float (&
   }
 }
 
+// The slow first moment of beta3 (APEXW_HP_SLOW), beside m and in its dtype, in the same
+// order as m: lerp with weight 1 - beta3 where m_update8 lerps, else mul by beta3 rounded to
+// m's dtype then add (1 - beta3) g (apexw/optimizer.py:5763-5765, :5781, :1232-1238)
+template <int GD, int MD> APEXW_DEV void slow_update8(float (&s)[8], const float (&g)[8], const apexw_hparams& hp) {
+  constexpr bool kLerpCold = MD == APEXW_F32, kLerpReplay = GD == MD;
+  if (hp.mode == APEXW_MODE_REPLAY ? kLerpReplay : kLerpCold) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float d = g[j] - s[j];
+      s[j] = rnd<MD>((hp.flags & APEXW_HP_LERP3_HI) ? fmaf(hp.lerp3_coef, d, g[j]) : fmaf(hp.lerp3_coef, d, s[j]));
+    }
+  } else {
+    const float b3_m = rnd<MD>(hp.beta3);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float s1 = rnd<MD>(s[j] * b3_m);
+      s[j] = rnd<MD>(fmaf(hp.one_minus_beta3, g[j], s1));
+    }
+  }
+}
+
 // cautious (APEXW_HP_CAUTIOUS): the mask g m >= 0 of one element (g prepared, m
 // updated), its product formed where the reference forms it: in fp32 for quad v
 // (apexw/optimizer.py:5728, :1272) and the cold order (:5851-5853), in the grads'
@@ -149,12 +170,14 @@ template <int PD, int MD> constexpr int caut_cold_dtype() {
 // e0 is the element index of slot 0 within the tensor (RNG counter).
 // SR: the launch's APEXW_HP_SR flag (a template parameter so that each path
 // compiles to its own code); APEXW_HP_SR_V implies it.
-// VAR: the launch may carry nesterov, cautious or amsgrad (APEXW_HP_NESTEROV /
-// _CAUTIOUS / _AMSGRAD); the plain instantiation compiles without them and keeps its
-// registers for the rest.  x: amsgrad's running max of v (8 entries, non-quad only).
+// VAR: the launch may carry nesterov, cautious, amsgrad, lion or beta3 (APEXW_HP_NESTEROV /
+// _CAUTIOUS / _AMSGRAD / _LION / _SLOW); the plain instantiation compiles without them and
+// keeps its registers for the rest.  x: amsgrad's running max of v; ms: beta3's slow moment
+// (8 entries each, non-quad only).
 template <int PD, int GD, int MD, int VD, bool QUAD, bool SR, bool VAR>
-APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8], float (&x)[8], int cnt,
-                       uint32_t e0, const Ctx& c, bool gc, const float (&mean)[8], bool ams) {
+APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8], float (&x)[8], float (&ms)[8],
+                       int cnt, uint32_t e0, const Ctx& c, bool gc, const float (&mean)[8], bool ams, bool slow,
+                       int tj) {
   const apexw_hparams& hp = *c.hp;
   constexpr bool sr = SR;
   const bool srv = SR && (hp.flags & APEXW_HP_SR_V);
@@ -188,7 +211,8 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
       // lion (the cold and the replayed order alike, apexw/optimizer.py:5677-5683,
       // :1214-1225): the grads cast to m's dtype; u = lerp(g', m, beta1) rounded to it;
       // p += -lr * sign(u), the scalar rounded to p's dtype when p and u share a 16-bit
-      // dtype (torch's same-dtype add with alpha); m = lerp(m, g', 1 - beta2)
+      // dtype (torch's same-dtype add with alpha, see tj below: the product with a sign is
+      // exact either way); m = lerp(m, g', 1 - beta2)
       constexpr bool kAlpha16 = PD == MD && PD != APEXW_F32;
       const float alpha = kAlpha16 ? rnd<PD>(-hp.gain_hi) : -hp.gain_hi;
       const float wd_l = rnd<PD>(hp.wd_factor);
@@ -270,6 +294,7 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
     for (int j = 0; j < 8; ++j) p[j] = rnd<PD>(p[j] * wd_p);
   }
   m_update8<GD, MD>(m, g, hp);
+  if (slow) slow_update8<GD, MD>(ms, g, hp);
   const bool p16 = PD != APEXW_F32;
   // nesterov (the cold and the replayed foreach orders): quad tensors take
   // lerp(g, m, beta1) as the numerator (apexw/optimizer.py:5732-5733, :1276-1277,
@@ -340,7 +365,21 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
       den = rnd<VD>(den + eps_v);
       if (scaled) den = rnd<VD>(den / sqrt_scale_v);
       if (clamp_den) den = fmaxf(den, eps_floor);
-      if (caut) {
+      if (slow) {
+        // AdEMAMix: m + slow_ratio s, upcast to fp32 in the cold order for an fp32 p over
+        // 16-bit m (apexw/optimizer.py:5834-5845), else in m's dtype with the ratio rounded
+        // to a 16-bit m dtype (torch's same-dtype add with alpha; replay :1332-1334); then one
+        // round-to-nearest addcdiv, nesterov ignored
+        constexpr bool kUp = PD == APEXW_F32 && MD != APEXW_F32;
+        float num;
+        if ((kUp && hp.mode != APEXW_MODE_REPLAY) || MD == APEXW_F32) {
+          num = fmaf(hp.slow_ratio, ms[j], m[j]);
+        } else {
+          const float r16 = rnd<MD>(hp.slow_ratio);
+          num = rnd<MD>(j < tj ? fmaf(r16, ms[j], m[j]) : m[j] + rnd<MD>(r16 * ms[j]));
+        }
+        p[j] = rnd<PD>(p[j] + (-hp.step_size * num) / den);
+      } else if (caut) {
         const bool replay = hp.mode == APEXW_MODE_REPLAY;
         const float num = replay ? rnd<GD>(m[j]) : m[j];
         float nf = num * (caut_mask<GD, false>(g[j], m[j], hp.mode) ? c.cq : 0.0f);
@@ -365,7 +404,7 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
 // Group k (512 elements, 8 per lane) of the unit starting at element `start`.
 // vmax: amsgrad's running max of v for this tensor (hparams.max_v), else NULL.
 template <int PD, int MD, int VD, bool QUAD, bool SR, bool VAR>
-APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const Ctx& c, void* vmax) {
+APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const Ctx& c, void* vmax, void* mslow) {
   constexpr int GD = PD;
   const int64_t n = t.n;
   const int lane = lane_id();
@@ -374,15 +413,17 @@ APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const 
     const int64_t e0 = start + (int64_t)(k * 64 + lane) * 8;
     if (e0 >= n) return;
     const int cnt = (int)((n - e0) < 8 ? (n - e0) : 8);
-    float p[8], g[8], m[8], v[8], x[8];
+    float p[8], g[8], m[8], v[8], x[8], ms[8];
     const bool full = vec && cnt == 8;
     const bool ams = VAR && !QUAD && vmax != nullptr;
+    const bool slow = VAR && !QUAD && mslow != nullptr;
     // lion keeps no second moment: v is neither read nor written
     const bool lion = VAR && !QUAD && (c.hp->flags & APEXW_HP_LION);
     if (full) {
       load8<PD>(t.p, e0, p);
       load8<GD>(t.g, e0, g);
       load8<MD>(t.m, e0, m);
+      if (slow) load8<MD>(mslow, e0, ms);
       if constexpr (QUAD) {
         if constexpr (VD == APEXW_F32) {
           const u32x2 w = __builtin_nontemporal_load((const u32x2*)((const float*)t.v + (e0 >> 2)));
@@ -406,6 +447,7 @@ APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const 
         m[j] = ok ? load1<MD>(t.m, e0 + j) : 0.0f;
         if constexpr (!QUAD) v[j] = (ok && !lion) ? load1<VD>(t.v, e0 + j) : 0.0f;
         x[j] = (ams && ok) ? load1<VD>(vmax, e0 + j) : 0.0f;
+        ms[j] = (slow && ok) ? load1<MD>(mslow, e0 + j) : 0.0f;
       }
       if constexpr (QUAD) {
         v[0] = cnt >= 4 ? load1<VD>(t.v, e0 >> 2) : 0.0f;
@@ -420,10 +462,21 @@ APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const 
       cs.vscale = t.v_scale[0];
       cs.vscale_sqrt = t.v_scale[1];
     }
-    update8<PD, GD, MD, VD, QUAD, SR, VAR>(p, g, m, v, x, cnt, (uint32_t)e0, cs, gc, mean, ams);
+    // torch's CPU add with alpha over two tensors of one 16-bit dtype (beta3's numerator)
+    // rounds alpha to that dtype and computes a + alpha b with one fused multiply-add in its
+    // vector loop, 32 elements at a time, but rounds the product to the dtype first in the
+    // scalar loop that ends each tensor (its last n % 32 elements); tj: this group's first
+    // element in that remainder (8: none)
+    int tj = 8;
+    if constexpr (VAR && !QUAD) {
+      const int64_t rel = (t.n - (t.n & 31)) - e0;
+      tj = rel < 0 ? 0 : (rel > 8 ? 8 : (int)rel);
+    }
+    update8<PD, GD, MD, VD, QUAD, SR, VAR>(p, g, m, v, x, ms, cnt, (uint32_t)e0, cs, gc, mean, ams, slow, tj);
     if (full) {
       store8<PD>(t.p, e0, p);
       store8<MD>(t.m, e0, m);
+      if (slow) store8<MD>(mslow, e0, ms);
       if constexpr (QUAD) {
         if constexpr (VD == APEXW_F32) {
           u32x2 w = {__float_as_uint(v[0]), __float_as_uint(v[1])};
@@ -447,6 +500,7 @@ APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const 
             if (!lion) store1<VD>(t.v, e0 + j, v[j]);
           }
           if (ams) store1<VD>(vmax, e0 + j, x[j]);
+          if (slow) store1<MD>(mslow, e0 + j, ms[j]);
         }
       }
       if constexpr (QUAD) {
@@ -459,29 +513,29 @@ APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const 
 
 template <bool SR, bool VAR>
 APEXW_DEV void dispatch_group(const apexw_tensor& t, int64_t start, int k, const Ctx& c, uint32_t pd, uint32_t md,
-                              uint32_t vd, bool quad, void* vmax) {
+                              uint32_t vd, bool quad, void* vmax, void* mslow) {
   if (md == APEXW_F32) {
     // fp32 moments ("full" precision, small "auto" tensors): fp32 v, no quad (checked on the host)
-    if (pd == APEXW_F32) compact_group<APEXW_F32, APEXW_F32, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax);
-    else if (pd == APEXW_BF16) compact_group<APEXW_BF16, APEXW_F32, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax);
-    else compact_group<APEXW_F16, APEXW_F32, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax);
+    if (pd == APEXW_F32) compact_group<APEXW_F32, APEXW_F32, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax, mslow);
+    else if (pd == APEXW_BF16) compact_group<APEXW_BF16, APEXW_F32, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax, mslow);
+    else compact_group<APEXW_F16, APEXW_F32, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax, mslow);
     return;
   }
   if (pd == APEXW_F16) {
     // fp16 parameters keep fp16 m (and fp16 or fp32 v)
-    if (vd == APEXW_F32) compact_group<APEXW_F16, APEXW_F16, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax);
-    else if (quad) compact_group<APEXW_F16, APEXW_F16, APEXW_F16, true, SR, VAR>(t, start, k, c, vmax);
-    else compact_group<APEXW_F16, APEXW_F16, APEXW_F16, false, SR, VAR>(t, start, k, c, vmax);
+    if (vd == APEXW_F32) compact_group<APEXW_F16, APEXW_F16, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax, mslow);
+    else if (quad) compact_group<APEXW_F16, APEXW_F16, APEXW_F16, true, SR, VAR>(t, start, k, c, vmax, mslow);
+    else compact_group<APEXW_F16, APEXW_F16, APEXW_F16, false, SR, VAR>(t, start, k, c, vmax, mslow);
     return;
   }
   if (pd == APEXW_F32) {
-    if (vd == APEXW_F32) compact_group<APEXW_F32, APEXW_BF16, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax);
-    else if (quad) compact_group<APEXW_F32, APEXW_BF16, APEXW_BF16, true, SR, VAR>(t, start, k, c, vmax);
-    else compact_group<APEXW_F32, APEXW_BF16, APEXW_BF16, false, SR, VAR>(t, start, k, c, vmax);
+    if (vd == APEXW_F32) compact_group<APEXW_F32, APEXW_BF16, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax, mslow);
+    else if (quad) compact_group<APEXW_F32, APEXW_BF16, APEXW_BF16, true, SR, VAR>(t, start, k, c, vmax, mslow);
+    else compact_group<APEXW_F32, APEXW_BF16, APEXW_BF16, false, SR, VAR>(t, start, k, c, vmax, mslow);
   } else {
-    if (vd == APEXW_F32) compact_group<APEXW_BF16, APEXW_BF16, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax);
-    else if (quad) compact_group<APEXW_BF16, APEXW_BF16, APEXW_BF16, true, SR, VAR>(t, start, k, c, vmax);
-    else compact_group<APEXW_BF16, APEXW_BF16, APEXW_BF16, false, SR, VAR>(t, start, k, c, vmax);
+    if (vd == APEXW_F32) compact_group<APEXW_BF16, APEXW_BF16, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax, mslow);
+    else if (quad) compact_group<APEXW_BF16, APEXW_BF16, APEXW_BF16, true, SR, VAR>(t, start, k, c, vmax, mslow);
+    else compact_group<APEXW_BF16, APEXW_BF16, APEXW_BF16, false, SR, VAR>(t, start, k, c, vmax, mslow);
   }
 }
 
@@ -619,8 +673,9 @@ __global__ __launch_bounds__(256) void compact_step_kernel(const apexw_tensor* _
     if (t.flags & APEXW_FLAG_FACTORED) continue;        // stepped by apexw_factored_step
     if (VAR && (hp.flags & APEXW_HP_CAUTIOUS)) c.cq = caut_q(hp.counts[un.tensor], t.n, quad, pd);
     void* vmax = (VAR && (hp.flags & APEXW_HP_AMSGRAD) && !quad) ? hp.max_v[un.tensor] : nullptr;
-    if (sr) dispatch_group<true, VAR>(t, start, k, c, pd, md, vd, quad, vmax);
-    else dispatch_group<false, VAR>(t, start, k, c, pd, md, vd, quad, vmax);
+    void* mslow = (VAR && (hp.flags & APEXW_HP_SLOW) && !quad) ? hp.slow[un.tensor] : nullptr;
+    if (sr) dispatch_group<true, VAR>(t, start, k, c, pd, md, vd, quad, vmax, mslow);
+    else dispatch_group<false, VAR>(t, start, k, c, pd, md, vd, quad, vmax, mslow);
   }
 }
 
@@ -647,8 +702,9 @@ int apexw_launch_compact(const apexw_tensor* tensors, int64_t n_units, const ape
   // resident grid striding over the whole launch).  Launches that a resident grid
   // covers in a few passes keep it (C2, 124 M elements: 0.234-0.257 ms against
   // 0.252-0.288 with a workgroup per unit).
-  // nesterov / cautious / amsgrad / lion launches take the instantiation that holds them
-  const bool var = hp->flags & (APEXW_HP_NESTEROV | APEXW_HP_CAUTIOUS | APEXW_HP_AMSGRAD | APEXW_HP_LION);
+  // nesterov / cautious / amsgrad / lion / beta3 launches take the instantiation that holds them
+  const bool var =
+      hp->flags & (APEXW_HP_NESTEROV | APEXW_HP_CAUTIOUS | APEXW_HP_AMSGRAD | APEXW_HP_LION | APEXW_HP_SLOW);
   const void* kernel = var ? (const void*)compact_step_kernel<true> : (const void*)compact_step_kernel<false>;
   const int resident = apexw_resident_grid(kernel, n_units * kGroups);
   const int grid = n_units > (int64_t)resident * 8 ? (int)(n_units < INT32_MAX ? n_units : INT32_MAX) : resident;

@@ -40,16 +40,18 @@ HOOK_MIN_NUMEL = 16384             # optimizer.py:2131
 HOOK_BATCH = 14                    # optimizer.py:2142
 
 _UNSUPPORTED_FLAGS = ("capturable", "differentiable", "auto_pack")
-def _check_variants(precision, factored, nesterov, cautious, maximize=False, amsgrad=False, lion=False):
+def _check_variants(precision, factored, nesterov, cautious, maximize=False, amsgrad=False, lion=False,
+                    beta3=None):
     """nesterov=True, cautious=True and maximize=True run in every precision: the
     8-bit and ultra steps' lookahead numerator lerp(g, m, beta1) without the SNR gain
     and the compact, full and auto steps' two addcdiv passes (lerp(g, m, beta1) for
     quad v); the numerator m times the sign-agreement mask over its mean; the negated
-    grads.  amsgrad=True and lion=True run in the compact, full and auto precisions
-    (a running max of v beside it, no quad v; the sign update on m alone, which takes
-    the place of the AdamW update and of its variants).  Factored second moments,
-    nesterov together with cautious, and amsgrad or lion in the 8bit and ultra
-    precisions do not."""
+    grads.  amsgrad=True, lion=True and beta3 (AdEMAMix) run in the compact, full and
+    auto precisions (a running max of v beside it, no quad v; the sign update on m
+    alone, which takes the place of the AdamW update and of its variants; a slow first
+    moment beside m, no quad v).  Factored second moments, nesterov together with
+    cautious, beta3 together with cautious, and amsgrad, lion or beta3 in the 8bit and
+    ultra precisions do not."""
     for name, on in (("nesterov", nesterov), ("cautious", cautious), ("maximize", maximize),
                      ("amsgrad", amsgrad)):
         if not on:
@@ -62,6 +64,13 @@ def _check_variants(precision, factored, nesterov, cautious, maximize=False, ams
         raise NotImplementedError(f"apexw_amd: amsgrad=True with precision={precision!r}")
     if lion and precision in ("8bit", "ultra"):
         raise NotImplementedError(f"apexw_amd: lion=True with precision={precision!r}")
+    if beta3 is not None and not lion:
+        if precision in ("8bit", "ultra"):
+            raise NotImplementedError(f"apexw_amd: beta3 with precision={precision!r}")
+        if factored:
+            raise NotImplementedError("apexw_amd: beta3 with factored_v")
+        if cautious:
+            raise NotImplementedError("apexw_amd: beta3 together with cautious=True")
 
 
 class ApexW(Optimizer):
@@ -155,12 +164,14 @@ class ApexW(Optimizer):
                     lion=lion, maximize=maximize, capturable=capturable, differentiable=differentiable,
                     auto_pack=auto_pack, factored_v=factored_v, six_bit=six_bit)
         bad = [k for k in _UNSUPPORTED_FLAGS if opts[k]]
-        if bad or beta3 is not None:
-            what = ", ".join(bad + (["beta3"] if beta3 is not None else []))
-            raise NotImplementedError(f"apexw_amd implements the standard AdamW step; not supported: {what}")
-        if nesterov or cautious or maximize or amsgrad or lion:
-            _check_variants(S.normalize_precision(precision), factored_v and not lion and not amsgrad,
-                            nesterov and not lion, cautious and not lion, maximize, amsgrad and not lion, lion)
+        if bad:
+            raise NotImplementedError(f"apexw_amd implements the standard AdamW step; not supported: {', '.join(bad)}")
+        if nesterov or cautious or maximize or amsgrad or lion or beta3 is not None:
+            # factored_v=True lays out no factored state under amsgrad, lion or beta3
+            _check_variants(S.normalize_precision(precision),
+                            factored_v and not lion and not amsgrad and beta3 is None,
+                            nesterov and not lion, cautious and not lion, maximize, amsgrad and not lion, lion,
+                            beta3)
         if precision == "compact" and betas[1] >= 0.99 and not stochastic_rounding and not adamw_compat:
             warnings.warn(
                 f"ApexW: beta2={betas[1]} with precision='compact' and stochastic_rounding=False "
@@ -359,14 +370,21 @@ class ApexW(Optimizer):
                 raise NotImplementedError("apexw_amd: factored_v with fp16 parameters")
         lion = bool(group.get("lion", False))
         # lion takes the place of the AdamW update and of its variants (optimizer.py:5375-5380,
-        # :5677-5683): nesterov, cautious and amsgrad do not apply under it
+        # :5677-5683): nesterov, cautious, amsgrad and beta3 do not apply under it
         ams = bool(group.get("amsgrad", False)) and not lion
+        beta3 = group.get("beta3") if not lion else None
         if (group.get("nesterov", False) or group.get("cautious", False) or group.get("maximize", False) or ams
-                or lion):
+                or lion or beta3 is not None):
             _check_variants(group["precision"], any(self.state[p].get("is_factored_v", False) for p in params),
                             bool(group.get("nesterov", False)) and not lion,
                             bool(group.get("cautious", False)) and not lion,
-                            bool(group.get("maximize", False)), ams, lion)
+                            bool(group.get("maximize", False)), ams, lion, beta3)
+        if beta3 is not None:
+            for p in params:
+                st = self.state[p]
+                if st["exp_avg_sq"].numel() != p.numel():
+                    raise NotImplementedError("apexw_amd: beta3 on a tensor whose state holds quad v")
+                S.ensure_slow(st, p)          # beta3 set after the first step (optimizer.py:2903-2915)
         if not lion:
             for p in params:
                 if "exp_avg_sq" not in self.state[p] and not self.state[p].get("is_factored_v", False):
@@ -392,7 +410,7 @@ class ApexW(Optimizer):
         # is_valid_for_step, optimizer.py:593-600): the foreach order instead
         native = (homogeneous and group.get("fused") is not False and not group.get("maximize", False)
                   and not group.get("nesterov", False) and not group.get("cautious", False) and not lion
-                  and not foreach)
+                  and group.get("beta3") is None and not foreach)
         return StepPlan(self, group, params, "compact", native=native)
 
     # ------------------------------------------------------------------ checkpoints
@@ -467,7 +485,7 @@ class ApexW(Optimizer):
         d = self.defaults
         if not force and (d.get("clip_grad_norm") is not None or d.get("grad_centralization", False)
                           or d.get("nesterov", False) or d.get("maximize", False) or d.get("amsgrad", False)
-                          or d.get("lion", False)):
+                          or d.get("lion", False) or d.get("beta3") is not None):
             return
         trainable = []
         total = 0

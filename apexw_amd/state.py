@@ -126,7 +126,7 @@ def _auto_subbyte(p, group, bs, factored=False):
     raw_int4 = group.get("int4_m", group.get("four_bit", None))
     pow2 = bs >= 64 and (bs & (bs - 1)) == 0
     return (raw_int4 is not False and not factored and not group.get("amsgrad", False)
-            and not group.get("lion", False) and n >= 16384 and n % 4 == 0 and pow2
+            and not group.get("lion", False) and group.get("beta3") is None and n >= 16384 and n % 4 == 0 and pow2
             and (p.dim() < 2 or min(p.shape) >= 8))
 
 
@@ -220,7 +220,18 @@ def init_state(p, group, peft_ctx, has_16bit_params=False):
     st = _init_state(p, group, peft_ctx, has_16bit_params)
     if group.get("amsgrad", False) and not group.get("lion", False):
         ensure_max_v(st, p)
+    if group.get("beta3") is not None:
+        ensure_slow(st, p)
     return st
+
+
+def ensure_slow(st, p):
+    """AdEMAMix's slow first moment (beta3): zeros in p's shape and m's dtype, created
+    when missing (at init, or on the first step after beta3 is set: optimizer.py:2842-2845,
+    :2903-2915).  Quantized states are not given one here (beta3 is refused there)."""
+    if "exp_avg_slow" in st or st.get("is_8bit", False) or st.get("is_ultra", False):
+        return
+    st["exp_avg_slow"] = torch.zeros(p.shape, dtype=st["exp_avg"].dtype, device=p.device)
 
 
 def ensure_max_v(st, p):
@@ -244,6 +255,7 @@ def _init_state(p, group, peft_ctx, has_16bit_params):
     is_peft = is_peft_parameter(p) or peft_ctx
     ams = bool(group.get("amsgrad", False))
     lion = bool(group.get("lion", False))
+    slow = group.get("beta3") is not None
     large = p.dim() >= 2 or n >= group.get("threshold", 65536)
     if group.get("fused") is True or prec == "full":
         # optimizer.py:2625-2626, :2769-2772
@@ -269,14 +281,14 @@ def _init_state(p, group, peft_ctx, has_16bit_params):
                                                                                    is_peft)
         if fp32_training or not large:
             return _moments(st, p, torch.float32, group, is_peft, prec)
-        if bool(group.get("factored_v", False)) and _can_factor(p, is_peft, FACTORED_MIN_COMPACT, ams or lion):
+        if bool(group.get("factored_v", False)) and _can_factor(p, is_peft, FACTORED_MIN_COMPACT, ams or lion or slow):
             st["is_factored_v"] = True
             return _factored_compact(st, p)
         return _moments(st, p, compact_dtype(p), group, is_peft, prec)
     if prec == "8bit" and n >= 64:
         bs = block_size_8bit(p, group.get("block_size"))
         narrow = p.dim() >= 2 and min(p.shape) <= 32 and n < 2048
-        factored = bool(group.get("factored_v", False)) and _can_factor(p, is_peft, FACTORED_MIN_8BIT, ams or lion)
+        factored = bool(group.get("factored_v", False)) and _can_factor(p, is_peft, FACTORED_MIN_8BIT, ams or lion or slow)
         auto_sub = _auto_subbyte(p, group, bs, factored)
         raw_int4 = group.get("int4_m", group.get("four_bit", None))
         six = bool(group.get("six_bit", False)) and factored and n >= SIX_BIT_MIN and bs % 4 == 0
@@ -286,7 +298,7 @@ def _init_state(p, group, peft_ctx, has_16bit_params):
     if prec == "8bit":
         st.update(is_8bit=False, is_factored_v=False, is_6bit_m=False, is_4bit_m=False, is_quad_v=False)
     else:
-        factored = bool(group.get("factored_v", False)) and _can_factor(p, is_peft, FACTORED_MIN_COMPACT, ams or lion)
+        factored = bool(group.get("factored_v", False)) and _can_factor(p, is_peft, FACTORED_MIN_COMPACT, ams or lion or slow)
         st.update(is_6bit_m=False, is_4bit_m=False, is_factored_v=factored)
         if factored:
             return _factored_compact(st, p)
@@ -306,7 +318,7 @@ def _factored_compact(st, p):
 
 def _moments(st, p, mdt, group, is_peft, prec):
     """Dense m in ``mdt``, v in the beta2 rule's dtype, quad v for large 16-bit
-    compact / auto tensors, not under nesterov, amsgrad or lion; no v under lion
+    compact / auto tensors, not under nesterov, amsgrad, lion or beta3; no v under lion
     (optimizer.py:2788-2810, :2838-2872)."""
     n, dev = p.numel(), p.device
     vdt = v_dtype_for_beta2(mdt, group["betas"][1], group.get("force_compact_v", False),
@@ -315,7 +327,7 @@ def _moments(st, p, mdt, group, is_peft, prec):
             and vdt in (torch.bfloat16, torch.float16)
             and group.get("int4_m", None) is not False and not group.get("nesterov", False)
             and not group.get("amsgrad", False) and not group.get("lion", False)
-            and n >= 16384 and n % 4 == 0
+            and group.get("beta3") is None and n >= 16384 and n % 4 == 0
             and (p.dim() < 2 or min(p.shape) >= 8)
             and (is_peft or len(group["params"]) >= 8))
     if quad:

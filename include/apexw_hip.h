@@ -44,7 +44,7 @@
 extern "C" {
 #endif
 
-#define APEXW_ABI_VERSION 22
+#define APEXW_ABI_VERSION 23
 
 /* status codes */
 enum apexw_status {
@@ -178,9 +178,23 @@ typedef struct apexw_unit {
                                           g' the prepared grad in m's dtype, p += a * sign(lerp(g', m,
                                           beta1)) (look_coef / APEXW_HP_LOOK_HI; the lerp rounded to m's
                                           dtype, sign(0) = sign(NaN) = 0), a = -gain_hi (gain_hi = lr),
-                                          rounded to p's dtype when p and m share a 16-bit dtype; then m
-                                          = lerp(m, g', 1 - beta2) (lerp_coef / APEXW_HP_LERP_HI).  v is
-                                          neither read nor written (descriptors may point v at m). */
+                                          rounded to p's dtype when p and m share a 16-bit dtype; then
+                                          m = lerp(m, g', 1 - beta2) (lerp_coef / APEXW_HP_LERP_HI).  v
+                                          is neither read nor written (descriptors may point v at m). */
+#define APEXW_HP_SLOW (1u << 13)       /* beta3 (AdEMAMix).  Compact step (cold and replay modes; no
+                                          APEXW_HP_CAUTIOUS / _LION / _AMP, no quad rows): a slow first
+                                          moment s = slow[t] (m's dtype, n elements, 16-byte aligned
+                                          unless APEXW_FLAG_SCALAR) follows m's update with beta3 (the
+                                          replay's lerp when the grad and m dtypes match, else mul by
+                                          beta3 rounded to m's dtype then add (1 - beta3) g; fp32 m:
+                                          lerp), lerp3_coef / APEXW_HP_LERP3_HI the lerp's coefficient
+                                          as lerp_coef's; the numerator is m + slow_ratio s (fp32 in
+                                          the cold mode for an fp32 p over 16-bit m, else in m's dtype:
+                                          for a 16-bit m with r = slow_ratio rounded to it, fma(r, s, m)
+                                          rounded, but m + rnd(r s) rounded in each tensor's last n % 32
+                                          elements, as torch's CPU add with alpha), then one
+                                          round-to-nearest addcdiv into p (nesterov ignored). */
+#define APEXW_HP_LERP3_HI (1u << 14)   /* APEXW_HP_SLOW: the slow lerp weight (1 - beta3) >= 0.5 */
 
 /* Step scalars of one launch, written on the device by apexw_amp_prepare (32 bytes). */
 typedef struct apexw_amp_dyn {
@@ -222,7 +236,11 @@ typedef struct apexw_hparams {
   unsigned long long* counts;   /* APEXW_HP_CAUTIOUS: one counter per descriptor of the table */
   void* const* max_v;           /* APEXW_HP_AMSGRAD: one device pointer per descriptor of the table
                                    (the running max of v), in device memory, else NULL */
-} apexw_hparams;          /* 120 bytes */
+  float beta3, one_minus_beta3; /* APEXW_HP_SLOW: the slow moment's EMA factors */
+  float lerp3_coef;             /* APEXW_HP_SLOW: its lerp coefficient (lerp_coef's rule, w = fp32(1 - beta3)) */
+  float slow_ratio;             /* APEXW_HP_SLOW: alpha (1 - beta1^t) / (1 - beta3^t) */
+  void* const* slow;            /* APEXW_HP_SLOW: one device pointer per descriptor (exp_avg_slow), else NULL */
+} apexw_hparams;          /* 144 bytes */
 
 /*
  * GradScaler hands the optimizer its scale and found_inf as device tensors

@@ -1,8 +1,8 @@
 """Compact-mode multi-tensor AdamW step (CPU oracle; test infrastructure only).
 
 Restates ``ApexW._multi_tensor_step`` (``apexw/optimizer.py:5297-5887``) for the
-AdamW update, its nesterov, cautious and amsgrad variants and the lion update (no
-AdEMAMix) with the same torch ops, so every bf16 rounding point of the reference is
+AdamW update, its nesterov, cautious, amsgrad and AdEMAMix (beta3) variants and the lion
+update with the same torch ops, so every bf16 rounding point of the reference is
 reproduced:
 
 1. decoupled weight decay ``p *= 1 - lr*wd`` (dim>=2 tensors when
@@ -21,6 +21,11 @@ reproduced:
    the same in fp32 (:5728-5731);
    amsgrad: ``max_v = maximum(max_v, v)`` after the v EMA and ``d`` from max_v instead of v
    (:5788-5790; the quad branch :5700-5702 is never reached, quad v being off under amsgrad)
+
+beta3 (AdEMAMix): a slow first moment follows m's update with beta3 (:5763-5765, :5781), and
+the numerator is ``m + slow_ratio * m_slow`` (fp32 for an fp32 p over 16-bit m, :5834-5845),
+``slow_ratio = alpha (1 - b1^t) / (1 - b3^t)``, then one addcdiv (nesterov ignored); the replay
+adds in m's dtype (:1232-1238, :1332-1334)
 
 lion (``lion_update``) replaces steps 2-5 after the weight decay: u = lerp(g', m, b1) with g'
 the grads cast to m's dtype, ``p += -lr * sign(u)``, ``m = lerp(m, g', 1-b2)`` -- :5677-5683
@@ -69,6 +74,19 @@ def bias_terms(lr, beta1, beta2, eps, step):
     bc2 = 1.0 - beta2 ** step
     bc2_sqrt = math.sqrt(bc2)
     return lr * bc2_sqrt / bc1, eps * bc2_sqrt
+
+
+def slow_ratio(alpha, beta1, beta3, step):
+    """AdEMAMix's weight of the slow moment, in double (optimizer.py:5584, :1101)."""
+    return alpha * ((1.0 - beta1 ** step) / (1.0 - beta3 ** step))
+
+
+def _slow_numerators(ms, slows, ratio, upcast):
+    """m + ratio * m_slow by one foreach add with alpha, on fp32 copies (upcast) or in
+    m's dtype (optimizer.py:5834-5845, :1332-1334)."""
+    if upcast:
+        ms, slows = [m.float() for m in ms], [m.float() for m in slows]
+    return torch._foreach_add(ms, slows, alpha=ratio)
 
 
 def _denominators(vs, eps_scaled, scale_v, sqrt_scale_v):
@@ -126,7 +144,8 @@ def _masked(nums, lhs, rhs, params):
 
 def compact_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weight_decay,
                           decay_norm_only, step, is_quad, stochastic, scale_v=1.0, sqrt_scale_v=1.0,
-                          nesterov=False, cautious=False, max_vs=None, lion=False):
+                          nesterov=False, cautious=False, max_vs=None, lion=False, slows=None, beta3=None,
+                          alpha=5.0):
     """One step over a subgroup sharing (p dtype, m dtype, step count, quad flag).
 
     ``step`` is the already-incremented step count.  Tensors are updated in place.
@@ -146,16 +165,21 @@ def compact_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weigh
     if ms[0].dtype in (torch.bfloat16, torch.float16):
         torch._foreach_mul_(ms, beta1)
         torch._foreach_add_(ms, gf, alpha=1.0 - beta1)
+        if slows is not None:
+            torch._foreach_mul_(slows, beta3)
+            torch._foreach_add_(slows, gf, alpha=1.0 - beta3)
     elif ms[0].dtype == torch.float32:
         # fp32 moments ("full", small "auto" tensors): the grads cast to m's dtype
         # and one lerp (optimizer.py:5669-5674, :5778-5781)
         torch._foreach_lerp_(ms, gf, 1.0 - beta1)
+        if slows is not None:
+            torch._foreach_lerp_(slows, gf, 1.0 - beta3)
     else:
         raise NotImplementedError(f"oracle compact step: m dtype {ms[0].dtype}")
     v16 = vs[0].dtype in (torch.bfloat16, torch.float16)
     if is_quad:
-        if max_vs is not None:
-            raise NotImplementedError("oracle compact step: amsgrad with quad v")
+        if max_vs is not None or slows is not None:
+            raise NotImplementedError("oracle compact step: amsgrad or beta3 with quad v")
         gq = [g.reshape(-1, 4).square().mean(dim=1) for g in gf]
         if beta2 >= 0.995 and stochastic and v16:
             for v, q in zip(vs, gq):
@@ -182,7 +206,12 @@ def compact_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weigh
         torch._foreach_mul_(vs, beta2)
         torch._foreach_addcmul_(vs, gf, gf, value=(1.0 - beta2) * scale_v)
     dens = _denominators(_amsgrad_max(max_vs, vs), eps_scaled, scale_v, sqrt_scale_v)
-    if cautious:
+    if slows is not None:
+        # fp32 p with 16-bit m takes both moments upcast (optimizer.py:5834-5845)
+        up = params[0].dtype == torch.float32 and ms[0].dtype != torch.float32
+        nums = _slow_numerators(ms, slows, slow_ratio(alpha, beta1, beta3, step), up)
+        torch._foreach_addcdiv_(params, nums, dens, value=-step_size)
+    elif cautious:
         # fp32 p with 16-bit m takes m upcast (optimizer.py:5834-5838); the mask from
         # g.float() * num.float() (:5851-5853)
         mf = [m.float() for m in ms] if params[0].dtype == torch.float32 and ms[0].dtype != torch.float32 else ms
@@ -203,7 +232,8 @@ def compact_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weigh
 
 def replay_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weight_decay,
                          apply_wd_mask, step, is_quad, stochastic, scale_v=1.0, sqrt_scale_v=1.0,
-                         nesterov=False, cautious=False, max_vs=None, lion=False):
+                         nesterov=False, cautious=False, max_vs=None, lion=False, slows=None, beta3=None,
+                         alpha=5.0):
     """One replayed step over an (p dtype, compact, quad) subgroup (optimizer.py:1200-1338).
 
     With an fp16 parameter, m or v the denominators are clamped below by eps
@@ -219,14 +249,19 @@ def replay_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weight
     has_fp16 = torch.float16 in (params[0].dtype, ms[0].dtype, vs[0].dtype)
     if grads[0].dtype == ms[0].dtype:
         torch._foreach_lerp_(ms, grads, 1.0 - beta1)
+        if slows is not None:
+            torch._foreach_lerp_(slows, grads, 1.0 - beta3)
     else:
         torch._foreach_mul_(ms, beta1)
         torch._foreach_add_(ms, grads, alpha=1.0 - beta1)
+        if slows is not None:
+            torch._foreach_mul_(slows, beta3)
+            torch._foreach_add_(slows, grads, alpha=1.0 - beta3)
     v16 = vs[0].dtype in (torch.bfloat16, torch.float16)
     sr_v = beta2 >= 0.995 and stochastic and v16
     if is_quad:
-        if max_vs is not None:
-            raise NotImplementedError("oracle compact replay: amsgrad with quad v")
+        if max_vs is not None or slows is not None:
+            raise NotImplementedError("oracle compact replay: amsgrad or beta3 with quad v")
         gf = grads if grads[0].dtype == torch.float32 else [g.float() for g in grads]
         gq = [g.reshape(-1, 4).square().mean(dim=1) for g in gf]
         if sr_v:
@@ -263,10 +298,14 @@ def replay_subgroup_step(params, grads, ms, vs, *, lr, beta1, beta2, eps, weight
         # m cast to the grads' dtype, the mask from their product in it (optimizer.py:1321-1328)
         nums = [m.to(g.dtype) if m.dtype != g.dtype else m for g, m in zip(grads, ms)]
         torch._foreach_addcdiv_(params, _masked(nums, grads, nums, params), dens, value=-step_size)
-    elif nesterov:
+    elif nesterov and slows is None:
         # the grads in their own dtype (optimizer.py:1329-1331)
         torch._foreach_addcdiv_(params, ms, dens, value=-step_size * beta1)
         torch._foreach_addcdiv_(params, grads, dens, value=-step_size * (1.0 - beta1))
+    elif slows is not None:
+        # in m's dtype, no upcast (optimizer.py:1332-1334)
+        nums = _slow_numerators(ms, slows, slow_ratio(alpha, beta1, beta3, step), False)
+        torch._foreach_addcdiv_(params, nums, dens, value=-step_size)
     elif params[0].dtype in (torch.bfloat16, torch.float16):
         for p, m, d in zip(params, ms, dens):
             delta = (m.float() / d.float()) * step_size

@@ -93,7 +93,17 @@ def init_state(p, group, n_params_in_group, peft_ctx, has_16bit_params=None, cud
     st = _init_state(p, group, n_params_in_group, peft_ctx, has_16bit_params, cuda)
     if group.get("amsgrad", False) and not group.get("lion", False):
         ensure_max_v(st, p)
+    if group.get("beta3") is not None:
+        ensure_slow(st, p)
     return st
+
+
+def ensure_slow(st, p):
+    """beta3's slow first moment, zeros in p's shape and m's dtype, created when missing
+    (optimizer.py:2842-2845, :2903-2915; quantized states aside)."""
+    if "exp_avg_slow" in st or st.get("is_8bit", False) or st.get("is_ultra", False):
+        return
+    st["exp_avg_slow"] = torch.zeros(p.shape, dtype=st["exp_avg"].dtype, device=p.device)
 
 
 def ensure_max_v(st, p):
@@ -115,6 +125,7 @@ def _init_state(p, group, n_params_in_group, peft_ctx, has_16bit_params, cuda):
     is_peft = is_peft_param(p) or peft_ctx
     ams = bool(group.get("amsgrad", False))
     lion = bool(group.get("lion", False))
+    slow = group.get("beta3") is not None
     threshold = group.get("threshold", 65536)
     massive = p.dim() >= 2 or n >= threshold
     if group.get("fused") is True or prec == "full":
@@ -146,7 +157,7 @@ def _init_state(p, group, n_params_in_group, peft_ctx, has_16bit_params, cuda):
         if not massive:
             return _dense(st, p, torch.float32, group, is_peft, n_params_in_group, prec)
         cdt = compact_dtype(p)
-        if bool(group.get("factored_v", False)) and can_factor(p, is_peft, 524288, ams or lion):
+        if bool(group.get("factored_v", False)) and can_factor(p, is_peft, 524288, ams or lion or slow):
             st["is_factored_v"] = True
             return _factored_compact(st, p, cdt)
         return _dense(st, p, cdt, group, is_peft, n_params_in_group, prec)
@@ -155,8 +166,8 @@ def _init_state(p, group, n_params_in_group, peft_ctx, has_16bit_params, cuda):
         narrow = p.dim() >= 2 and min(p.shape) <= 32 and n < 2048
         raw_int4 = group.get("int4_m")
         pow2 = bs >= 64 and (bs & (bs - 1)) == 0
-        fv = bool(group.get("factored_v", False)) and can_factor(p, is_peft, 65536, ams or lion)
-        auto_sub = (raw_int4 is not False and not fv and not ams and not lion and n >= 16384 and n % 4 == 0 and pow2
+        fv = bool(group.get("factored_v", False)) and can_factor(p, is_peft, 65536, ams or lion or slow)
+        auto_sub = (raw_int4 is not False and not fv and not ams and not lion and not slow and n >= 16384 and n % 4 == 0 and pow2
                     and (p.dim() < 2 or min(p.shape) >= 8))
         six = bool(group.get("six_bit", False)) and fv and n >= 524288 and bs % 4 == 0
         int4 = auto_sub or (bool(raw_int4) and not fv and n >= 512 and n >= bs and not narrow and not is_peft)
@@ -187,7 +198,7 @@ def _init_state(p, group, n_params_in_group, peft_ctx, has_16bit_params, cuda):
     if prec == "8bit":
         st.update(is_8bit=False, is_factored_v=False, is_6bit_m=False, is_4bit_m=False, is_quad_v=False)
     elif prec == "compact":
-        fv = bool(group.get("factored_v", False)) and can_factor(p, is_peft, 524288, ams or lion)
+        fv = bool(group.get("factored_v", False)) and can_factor(p, is_peft, 524288, ams or lion or slow)
         st.update(is_6bit_m=False, is_4bit_m=False, is_factored_v=fv)
         if fv:
             return _factored_compact(st, p, compact_dtype(p))
@@ -211,14 +222,15 @@ def _factored_compact(st, p, mdt):
 
 def _dense(st, p, mdt, group, is_peft, n_params_in_group, prec):
     """m in ``mdt``, v in the dtype the beta2 rule gives, quad-shared v for large
-    16-bit compact/auto tensors, not under nesterov, amsgrad or lion; no v under lion
+    16-bit compact/auto tensors, not under nesterov, amsgrad, lion or beta3; no v under lion
     (optimizer.py:2788-2810, :2838-2872)."""
     n = p.numel()
     vdt = v_dtype(mdt, group["betas"][1], group.get("force_compact_v", False), bool(group["stochastic_rounding"]))
     quad = (prec in ("compact", "auto") and mdt in (torch.bfloat16, torch.float16)
             and vdt in (torch.bfloat16, torch.float16)
             and group.get("int4_m") is not False and not group.get("nesterov", False)
-            and not group.get("amsgrad", False) and not group.get("lion", False) and n >= 16384 and n % 4 == 0
+            and not group.get("amsgrad", False) and not group.get("lion", False)
+            and group.get("beta3") is None and n >= 16384 and n % 4 == 0
             and (p.dim() < 2 or min(p.shape) >= 8) and (is_peft or n_params_in_group >= 8))
     if quad:
         st["is_quad_v"] = True

@@ -68,8 +68,10 @@ class OracleApexW:
                  adamw_compat=False, clip_grad_norm=None, precision="compact", stochastic_rounding=True,
                  block_size=None, force_compact_v=False, int4_m=None, grad_centralization=False,
                  factored_v=False, six_bit=False, threshold=65536, amp=None, dynamic_scaling=True, nesterov=False,
-                 cautious=False, maximize=False, amsgrad=False, fused=None, lion=False):
+                 cautious=False, maximize=False, amsgrad=False, fused=None, lion=False, beta3=None, alpha=5.0):
         precision = normalize_precision(precision)
+        if betas is not None and len(betas) > 2 and beta3 is None:
+            beta3 = betas[2]
         if betas is None:
             betas = (0.9, 0.999) if precision in ("8bit", "full") else (0.9, 0.99)
         if adamw_compat:
@@ -77,14 +79,14 @@ class OracleApexW:
             if tuple(betas) in ((0.9, 0.95), (0.9, 0.99)):
                 betas = (0.9, 0.999)
         self.params = list(params)
-        self.group = dict(lr=lr, betas=tuple(betas), eps=eps, weight_decay=weight_decay,
+        self.group = dict(lr=lr, betas=tuple(betas[:2]), eps=eps, weight_decay=weight_decay,
                           decay_norm_only=decay_norm_only, clip_grad_norm=clip_grad_norm,
                           precision=precision, stochastic_rounding=stochastic_rounding,
                           block_size=block_size, force_compact_v=force_compact_v, int4_m=int4_m,
                           grad_centralization=grad_centralization, factored_v=factored_v, six_bit=six_bit,
                           threshold=threshold, amp=amp, dynamic_scaling=dynamic_scaling, nesterov=bool(nesterov),
                           cautious=bool(cautious), maximize=bool(maximize), amsgrad=bool(amsgrad),
-                          fused=fused, lion=bool(lion), params=self.params)
+                          fused=fused, lion=bool(lion), beta3=beta3, alpha=alpha, params=self.params)
         self.state = {}
         self._plan = None
         self.grad_scale = None
@@ -101,8 +103,11 @@ class OracleApexW:
         # plan holds max lists only when made with amsgrad and without lion
         if plan["amsgrad"] != self.group["amsgrad"]:
             return False
-        # the native fused plan does not replay the variants (optimizer.py:593-600)
+        # beta3 set or cleared since the plan was made (optimizer.py:587-588)
         grp = self.group
+        if plan.get("slow", False) != (grp["beta3"] is not None):
+            return False
+        # the native fused plan does not replay the variants (optimizer.py:593-600)
         if plan["kind"] == "native" and (grp["nesterov"] or grp["lion"] or grp["cautious"] or grp["maximize"]):
             return False
         return all(p.grad is None for p in self.params if p.requires_grad and p not in active)
@@ -175,12 +180,15 @@ class OracleApexW:
                 self.state[p] = L.init_state(p, grp, len(self.params), peft)
             elif grp["amsgrad"] and not grp["lion"] and not grp["precision"] in ("8bit", "ultra"):
                 L.ensure_max_v(self.state[p], p)      # amsgrad switched on later (optimizer.py:2917-2922)
+            if grp["beta3"] is not None and grp["precision"] not in ("8bit", "ultra"):
+                L.ensure_slow(self.state[p], p)       # beta3 set later (optimizer.py:2903-2915)
         prec = grp["precision"]
         ams = grp["amsgrad"]
-        if (ams or grp["lion"]) and prec in ("8bit", "ultra"):
-            raise NotImplementedError("oracle: amsgrad / lion in the 8bit / ultra precisions")
+        if (ams or grp["lion"] or grp["beta3"] is not None) and prec in ("8bit", "ultra"):
+            raise NotImplementedError("oracle: amsgrad / lion / beta3 in the 8bit / ultra precisions")
         lion = grp["lion"]
         ams = ams and not lion                  # lion keeps no v, nor its max (optimizer.py:5375-5380)
+        slow = grp["beta3"] is not None and not lion
         quantized = prec in ("8bit", "ultra")     # both run _step_ultra (optimizer.py:3583-3587)
         grads, scale = self._prepare(self._signed([p.grad for p in plist], quantized),
                                      sanitize=not quantized or grp["clip_grad_norm"] is not None)
@@ -197,11 +205,11 @@ class OracleApexW:
         homogeneous = all("exp_avg_sq" in st and st["exp_avg"].dtype == st["exp_avg_sq"].dtype == p.dtype
                           and st["exp_avg"].numel() == st["exp_avg_sq"].numel() for p, st in zip(plist, sts))
         if homogeneous and grp["fused"] is not False and not (grp["maximize"] or grp["nesterov"] or grp["cautious"]
-                                                              or lion):
+                                                              or lion or grp["beta3"] is not None):
             # maximize, nesterov and cautious leave the native fused step (optimizer.py:3733, :593-600),
             # and so does fused=False (:3723)
             self._native_fused(plist, grads, sts, grad_scale=scale, amsgrad=ams, **kw)
-            self._plan = {"kind": "native", "params": plist, "amsgrad": ams}
+            self._plan = {"kind": "native", "params": plist, "amsgrad": ams, "slow": False}
             return
         # factored-v tensors: their own update with their own step (optimizer.py:5382-5432)
         for p, g, st in zip(plist, grads, sts):
@@ -242,9 +250,12 @@ class OracleApexW:
                                   stochastic=grp["stochastic_rounding"], scale_v=scale_v,
                                   sqrt_scale_v=sqrt_scale_v, nesterov=grp["nesterov"],
                                   cautious=grp["cautious"], lion=lion,
-                                  max_vs=[i[2]["max_exp_avg_sq"] for i in items] if ams else None, **kw)
+                                  max_vs=[i[2]["max_exp_avg_sq"] for i in items] if ams else None,
+                                  slows=[i[2]["exp_avg_slow"] for i in items] if slow else None,
+                                  beta3=grp["beta3"], alpha=grp["alpha"], **kw)
         # the replayed plan's per-subgroup scales start at 1.0 (optimizer.py:546-560)
-        self._plan = {"kind": "foreach", "params": plan_params, "sg_scale": {}, "amsgrad": ams}
+        self._plan = {"kind": "foreach", "params": plan_params, "sg_scale": {}, "amsgrad": ams,
+                      "slow": grp["beta3"] is not None}
 
     def _is_quad(self, p):
         v = self.state[p].get("exp_avg_sq")
@@ -270,6 +281,7 @@ class OracleApexW:
         sts = [self.state[p] for p in plist]
         lion = grp["lion"]
         ams = plan["amsgrad"] and not lion
+        slow = plan.get("slow", False) and not lion
         if plan["kind"] == "native":
             self._native_fused(plist, grads, sts, sanitize=False, grad_scale=scale, amsgrad=ams, **kw)
             return
@@ -309,7 +321,9 @@ class OracleApexW:
                                  step=step, is_quad=quad, stochastic=grp["stochastic_rounding"],
                                  scale_v=scale_v, sqrt_scale_v=sqrt_scale_v, nesterov=grp["nesterov"],
                                  cautious=grp["cautious"], lion=lion,
-                                 max_vs=[i[2]["max_exp_avg_sq"] for i in items] if ams else None, **kw)
+                                 max_vs=[i[2]["max_exp_avg_sq"] for i in items] if ams else None,
+                                 slows=[i[2]["exp_avg_slow"] for i in items] if slow else None,
+                                 beta3=grp["beta3"], alpha=grp["alpha"], **kw)
 
     def _factored(self, p, g, st, step, inv, sanitize):
         grp = self.group

@@ -539,6 +539,17 @@ PREC_CASES = {
     "compact_fp32_lion_rne": (PREC_SHAPES, torch.float32, 4, 92, dict(PREC_KW, lion=True)),
     "auto_bf16_lion_rne": (PREC_SHAPES, torch.bfloat16, 4, 95,
                            dict(PREC_KW, precision="auto", adamw_compat=True, lion=True, lr=1e-2)),
+    # beta3 (AdEMAMix) in the compact-kernel precisions: a slow first moment beside m (no quad
+    # v), the numerator m + slow_ratio m_slow (fp32 for fp32 parameters over bf16 m in the cold
+    # order, m's dtype otherwise), one addcdiv; cold then replayed
+    "compact_bf16_beta3_rne": (PREC_SHAPES, torch.bfloat16, 5, 96, dict(PREC_KW, beta3=0.9999, alpha=5.0)),
+    "compact_fp32_beta3_rne": (PREC_SHAPES, torch.float32, 4, 97, dict(PREC_KW, beta3=0.999, alpha=2.0)),
+    "full_bf16_beta3_rne": (PREC_SHAPES, torch.bfloat16, 4, 98, dict(PREC_KW, precision="full", beta3=0.9999)),
+    "full_fp32_beta3_rne": (PREC_SHAPES, torch.float32, 4, 99, dict(PREC_KW, precision="full", beta3=0.9999)),
+    "auto_bf16_beta3_rne": (PREC_SHAPES, torch.bfloat16, 4, 100,
+                            dict(PREC_KW, precision="auto", adamw_compat=True, beta3=0.9999)),
+    "compact_bf16_beta3_amsgrad_rne": (PREC_SHAPES, torch.bfloat16, 4, 101,
+                                       dict(PREC_KW, beta3=0.999, amsgrad=True, nesterov=True)),
 }
 
 
@@ -568,6 +579,8 @@ FP16_CASES = {
     "fp16_amsgrad_foreach_rne": (FP16_SHAPES, 5, 59, dict(FP16_KW, amsgrad=True, fused=False), ()),
     # lion: fp16 m, -lr rounded to fp16
     "fp16_lion_rne": (FP16_SHAPES, 4, 60, dict(FP16_KW, lion=True, lr=1e-2), ()),
+    # beta3: fp16 m and slow moment, the dynamic v scale
+    "fp16_beta3_rne": (FP16_SHAPES, 5, 61, dict(FP16_KW, beta3=0.999), ()),
 }
 
 

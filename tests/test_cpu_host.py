@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 def test_struct_layouts_match_header():
     from apexw_amd import _lib
     assert ctypes.sizeof(_lib.Tensor) == 64 == _lib.TENSOR_DTYPE.itemsize
-    assert ctypes.sizeof(_lib.HParams) == 120
+    assert ctypes.sizeof(_lib.HParams) == 144
     assert _lib.GEMM_PROBLEM_DTYPE.itemsize == 120
     assert ctypes.sizeof(_lib.StateLayout) == 56
 
@@ -162,15 +162,18 @@ def test_constructor_contract():
         ApexW(p, block_size=0)
     with pytest.raises(ValueError):
         ApexW(p, precision="nope")
-    # amsgrad and lion: the compact, full and auto precisions, not 8bit / ultra; factored_v=True
-    # is accepted and lays out no factored state under them, as in the reference
-    for opt in ("amsgrad", "lion"):
+    # amsgrad, lion and beta3: the compact, full and auto precisions, not 8bit / ultra;
+    # factored_v=True is accepted and lays out no factored state under them, as in the reference
+    for opt, val in (("amsgrad", True), ("lion", True), ("beta3", 0.999)):
         for prec in ("compact", "full", "auto"):
-            assert ApexW(p, precision=prec, **{opt: True}).defaults[opt]
-        assert ApexW(p, precision="compact", factored_v=True, **{opt: True}).defaults["factored_v"]
+            assert ApexW(p, precision=prec, **{opt: val}).defaults[opt] == val
+        assert ApexW(p, precision="compact", factored_v=True, **{opt: val}).defaults["factored_v"]
         for prec in ("8bit", "ultra"):
             with pytest.raises(NotImplementedError):
-                ApexW(p, precision=prec, **{opt: True})
+                ApexW(p, precision=prec, **{opt: val})
+    assert ApexW(p, betas=(0.9, 0.999, 0.9999)).defaults["beta3"] == 0.9999
+    with pytest.raises(NotImplementedError):
+        ApexW(p, beta3=0.999, cautious=True)
     # nesterov: every precision, without factored second moments
     for prec in ("8bit", "ultra", "3byte", "compact", "full", "auto"):
         assert ApexW(p, precision=prec, nesterov=True).defaults["nesterov"]
@@ -316,6 +319,6 @@ def test_integration_binding_loads():
     from integration_binding import load_binding
     rx = load_binding()
     assert callable(rx.step_fused) and callable(rx.step_fused_8bit)
-    assert ctypes.sizeof(rx.HParams) == 120 and ctypes.sizeof(rx.Tensor) == 64 and ctypes.sizeof(rx.Unit) == 8
+    assert ctypes.sizeof(rx.HParams) == 144 and ctypes.sizeof(rx.Tensor) == 64 and ctypes.sizeof(rx.Unit) == 8
     p = torch.zeros(4)          # CPU tensors: not handled, nothing written
     assert rx.step_fused([p], [p], [p], [p], 1e-3, 0.9, 0.999, 1e-8, 0.0) is False

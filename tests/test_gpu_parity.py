@@ -89,7 +89,11 @@ def test_hip_step_matches_reference_trajectory(name):
     params, opt, gold = replay(name, ApexW, device=dev)
     torch.cuda.synchronize()
     if "flags_0" not in gold:
-        _cmp_factored(params, opt, gold, initial_params(name), CASES[name][2])
+        # beta3: torch's CPU fp32 sqrt is faithfully rounded where the kernel's is IEEE, and
+        # beta3's updates (slow_ratio up to ~5000) are ~6e-3 per step: fp32 p near 0 may
+        # differ by ~1 ulp of the update per step
+        _cmp_factored(params, opt, gold, initial_params(name), CASES[name][2],
+                      floor=4e-9 if "beta3" in name else 1e-9)
         return
     rel, floor = 1e-6, 1e-9
     if name in FP32_CLIP_CASES:
@@ -113,7 +117,7 @@ def _codes6(q):
     return torch.stack([(word >> (6 * i)) & 63 for i in range(4)], 1).reshape(-1)
 
 
-def _cmp_factored(params, opt, gold, init, steps):
+def _cmp_factored(params, opt, gold, init, steps, floor=1e-9):
     for i, p in enumerate(params):
         st = opt.state[p]
         keys = state_keys(gold, i)
@@ -123,7 +127,7 @@ def _cmp_factored(params, opt, gold, init, steps):
             assert [float(st["scale_v"]), float(st["sqrt_scale_v"])] == gold[f"scale_{i}"].tolist(), f"scale_{i}"
         fac = bool(st.get("is_factored_v", False))
         if not fac:
-            _cmp_tensor(p.data, gold[f"p_{i}"], f"p_{i}")
+            _cmp_tensor(p.data, gold[f"p_{i}"], f"p_{i}", floor=floor)
             for k in keys:
                 g = gold[f"st_{i}_{k}"]
                 if k.endswith("scales"):

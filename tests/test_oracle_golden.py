@@ -149,6 +149,29 @@ def test_lion_goldens_pin_the_rounded_scalar(name, monkeypatch):
                for i, p in enumerate(params))
 
 
+def _no_upcast(ms, slows, ratio, upcast):
+    return torch._foreach_add(ms, slows, alpha=ratio)
+
+
+def _fp32_ratio(ms, slows, ratio, upcast):
+    return [(m.float() + ratio * s.float()).to(torch.float32 if upcast else m.dtype) for m, s in zip(ms, slows)]
+
+
+@pytest.mark.parametrize("name,mistake", [("compact_fp32_beta3_rne", _no_upcast),
+                                          ("compact_bf16_beta3_rne", _fp32_ratio),
+                                          ("fp16_beta3_rne", _fp32_ratio)])
+def test_beta3_goldens_pin_the_numerator(name, mistake, monkeypatch):
+    """The beta3 trajectories tell the reference's numerator m + slow_ratio m_slow from
+    a plausible other: the cold order's fp32 upcast for fp32 parameters over bf16 m
+    skipped, or the ratio kept in fp32 where torch's same-dtype add rounds it to the
+    16-bit dtype; an oracle with either ends elsewhere."""
+    import oracle.compact as C
+    monkeypatch.setattr(C, "_slow_numerators", mistake)
+    params, _, gold = replay(name, OracleApexW)
+    assert any(not np.array_equal(_as_np(p.data).reshape(-1), gold[f"p_{i}"].reshape(-1))
+               for i, p in enumerate(params))
+
+
 def test_oracle_clip_matches_reference():
     z = load("clip_bf16")
     n = len([k for k in z if k.startswith("g_")])

@@ -51,6 +51,7 @@ HP_AMSGRAD = 1 << 11
 HP_LION = 1 << 12
 HP_SLOW = 1 << 13
 HP_LERP3_HI = 1 << 14
+HP_GRAD_DTYPES = 1 << 15
 
 STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported dtype combination", 3: "launch failed",
           4: "misaligned pointer", 5: "exceeds the fixed workspace of the allocation-free entry point"}

@@ -59,7 +59,7 @@ CHUNKED_MIN_NUMEL = 262144  # larger 8-bit tensors take the reference's chunked 
 _GRAD = operator.attrgetter("grad")
 
 # status of _host.scan (csrc/host.cpp)
-SCAN_SAME, SCAN_GRADS_MOVED, SCAN_MISSING, SCAN_REBUILT, SCAN_SLOW = range(5)
+SCAN_SAME, SCAN_GRADS_MOVED, SCAN_MISSING, SCAN_REBUILT, SCAN_SLOW, SCAN_GRAD_DTYPE = range(6)
 
 
 @functools.lru_cache(maxsize=64)
@@ -110,6 +110,10 @@ class StepPlan:
         self.cold_done = False
         self._nesterov = False
         self.amp_dirty = False      # skips counted on the device that the host has not folded
+        # each grad's dtype as the table is built for it: a parameter's grads may be of another
+        # dtype (torch's Tensor.grad_dtype), and a change of it makes a new plan
+        self.grad_dtypes = [p.grad.dtype if p.grad is not None else p.dtype for p in self.params]
+        self.mixed = any(gd != p.dtype for gd, p in zip(self.grad_dtypes, self.params))
         self._build_steps()
         self._build_tables(group)
 
@@ -182,6 +186,12 @@ class StepPlan:
         if self.native and self.nesterov:
             return False
         self._scan_status = self._scan()
+        if self._scan_status == SCAN_GRAD_DTYPE:
+            # a grad of another dtype than the table's: new descriptors; the reference's replayed
+            # foreach plan steps it in place (its validity test reads no dtype), so the new plan
+            # keeps this one's replay order
+            self.keep_replay = self.cold_done and not self.native
+            return False
         ok = self._scan_status in (SCAN_SAME, SCAN_GRADS_MOVED, SCAN_SLOW)
         if ok and self._lion_of(group) != self.lion:
             # lion switched on or off: the descriptors change (no v under lion), so a new
@@ -205,8 +215,8 @@ class StepPlan:
         for i, st in enumerate(self.states):
             st["step"] = self.steps[i]
 
-    def _tensor_flags(self, p, st, wd_on):
-        f = (_DT[p.dtype] << L.PDT_SHIFT) | (_DT[p.dtype] << L.GDT_SHIFT)
+    def _tensor_flags(self, p, st, wd_on, gdt):
+        f = (_DT[p.dtype] << L.PDT_SHIFT) | (_DT[gdt] << L.GDT_SHIFT)
         if wd_on and (not self.decay_norm_only or p.dim() >= 2):
             f |= L.FLAG_WD
         if st.get("is_factored_v", False):
@@ -256,10 +266,24 @@ class StepPlan:
         n = len(self.params)
         tab = np.zeros(n, dtype=L.TENSOR_DTYPE)
         counts = np.zeros(n, dtype=np.int64)
+        if self.mixed:
+            # grads of another dtype than their parameters (Tensor.grad_dtype): the compact,
+            # full and auto steps, with one grad dtype per parameter dtype, as the reference's
+            # foreach subgroups take them (one conversion rule per subgroup, optimizer.py:5662)
+            if self.kind != "compact" or self.single:
+                raise NotImplementedError("apexw_amd: grads of another dtype than their parameters in the "
+                                          f"{self.precision} precision or the per-parameter update")
+            per = {}
+            for p, gd in zip(self.params, self.grad_dtypes):
+                per.setdefault(p.dtype, set()).add(gd)
+            if any(len(v) > 1 for v in per.values()):
+                raise NotImplementedError("apexw_amd: the grads of parameters of one dtype must share a dtype")
         for i, (p, st) in enumerate(zip(self.params, self.states)):
             if not p.is_contiguous():
                 raise NotImplementedError("ApexW HIP step needs contiguous parameters")
-            f, block = self._tensor_flags(p, st, wd_on)
+            f, block = self._tensor_flags(p, st, wd_on, self.grad_dtypes[i])
+            if f & L.FLAG_FACTORED and self.grad_dtypes[i] != p.dtype:
+                raise NotImplementedError("apexw_amd: factored_v with grads of another dtype than the parameter")
             tab[i]["p"] = p.data_ptr()
             tab[i]["m"] = st["exp_avg"].data_ptr()
             if f & L.FLAG_FACTORED:
@@ -324,9 +348,14 @@ class StepPlan:
         self._H.snapshot(self.params, self.p_ptrs.ctypes.data, self.p_dtypes.ctypes.data)
         self.g_ptrs = np.zeros(n, dtype=np.uint64)     # grad pointers the table was built from
         self.g_scan = np.zeros(n, dtype=np.uint64)     # the scan's current grad pointers
+        # the grad dtypes the table was built for (torch's codes, as the scan reads them)
+        self.g_dtypes = np.zeros(n, dtype=np.int8)
+        grads = [p.grad if p.grad is not None else p for p in self.params]
+        g_seen = np.zeros(n, dtype=np.uint64)          # held by name: the snapshot writes into it
+        self._H.snapshot(grads, g_seen.ctypes.data, self.g_dtypes.ctypes.data)
         # the arrays never move: their addresses are taken once
         self._scan_addrs = (self.p_ptrs.ctypes.data, self.p_dtypes.ctypes.data, self.g_ptrs.ctypes.data,
-                            self.g_scan.ctypes.data)
+                            self.g_scan.ctypes.data, self.g_dtypes.ctypes.data)
         self._scan_status = None
         # centralization: folded into the step kernels and the clip (row means only: compact
         # descriptors hold them in m_scale / block, 8-bit and ultra ones in a side table)
@@ -354,7 +383,7 @@ class StepPlan:
         # the reference centralizes dim >= 2 grads over dims 1.. (optimizer.py:239-243)
         prep["row_len"] = [p.numel() // p.shape[0] if p.dim() >= 2 and p.numel() > 0 else 0 for p in self.params]
         prep["n"] = [p.numel() for p in self.params]
-        prep["dtype"] = [_DT[p.dtype] for p in self.params]
+        prep["dtype"] = [_DT[gd] for gd in self.grad_dtypes]
         if self.gc_fold:
             self.gc_means = [torch.empty(max(p.numel() // int(prep["row_len"][i]), 1) if prep["row_len"][i] else 1,
                                          dtype=torch.float32, device=self.device)
@@ -494,14 +523,14 @@ class StepPlan:
         self._scan_status = None
         if st == SCAN_SAME and self.d_table is not None:
             return None
-        if st in (SCAN_MISSING, SCAN_REBUILT):
+        if st in (SCAN_MISSING, SCAN_REBUILT, SCAN_GRAD_DTYPE):
             raise RuntimeError("the step plan no longer matches its parameters or grads")
         keep = None
         if st == SCAN_SLOW:
             keep = list(map(_GRAD, self.params))
             for i, (p, g) in enumerate(zip(self.params, keep)):
-                if g.dtype != p.dtype:
-                    raise NotImplementedError("grad dtype must match the parameter dtype")
+                if g.dtype != self.grad_dtypes[i]:
+                    raise RuntimeError("a grad's dtype changed under the step plan")
                 if g.numel() != p.numel():
                     raise RuntimeError(f"grad of parameter {i} has {g.numel()} elements, the parameter {p.numel()}")
                 if not g.is_contiguous():
@@ -1053,6 +1082,9 @@ class StepPlan:
             hp.grad_inv_scale = inv_scale
         if self.d_rows is not None:
             hp.rows = self.d_rows.data_ptr()
+        if self.mixed:
+            # grads of another dtype than their parameters: the variant instantiation reads them
+            flags |= L.HP_GRAD_DTYPES
         if self.amsgrad:
             # amsgrad: the denominators take max(max_v, v) (optimizer.py:5788-5790, :1253-1255;
             # torch._fused_adamw_ for the native plan)

@@ -133,6 +133,9 @@ int apexw_check_tensor(const apexw_tensor* t, int32_t kind) {
   if ((t->flags & APEXW_FLAG_GC) && (kind == 3 || kind == 4)) return APEXW_ERR_ARG;
   if (kind == 0 || kind == 3) {
     if (!apexw_compact_flags_ok(t->flags)) return APEXW_ERR_DTYPE;
+    // the per-parameter update takes grads in the parameter's dtype only
+    if (kind == 3 && ((t->flags >> APEXW_FLAG_GDT_SHIFT) & 3u) != ((t->flags >> APEXW_FLAG_PDT_SHIFT) & 3u))
+      return APEXW_ERR_DTYPE;
     if ((t->flags & APEXW_FLAG_QUAD) && (kind == 3 || (t->n % 4) != 0)) return APEXW_ERR_ARG;
     if ((t->flags & APEXW_FLAG_GC) && (!t->m_scale || t->block == 0 || (t->n % t->block) != 0)) return APEXW_ERR_ARG;
     if ((t->flags & APEXW_FLAG_VSCALE) && (!t->v_scale || ((uintptr_t)t->v_scale & 7u))) return APEXW_ERR_ARG;
@@ -190,13 +193,21 @@ static int launch_args_status(int32_t kind, int32_t n_tensors, int64_t n_units, 
       if ((hp->flags & APEXW_HP_SLOW) &&
           (hp->mode == APEXW_MODE_NATIVE || (hp->flags & (APEXW_HP_CAUTIOUS | APEXW_HP_AMP))))
         return APEXW_ERR_ARG;
+      // grads of another dtype than their parameters: the cold and replayed orders (torch._fused_adamw_
+      // refuses them, and so does the native mode)
+      if ((hp->flags & APEXW_HP_GRAD_DTYPES) && (hp->mode == APEXW_MODE_NATIVE || hp->mode == APEXW_MODE_SINGLE))
+        return APEXW_ERR_ARG;
       return APEXW_OK;
     case APEXW_LAUNCH_ULTRA:
-      if (n_fast_units || n_fast_f32_units || (hp->flags & (APEXW_HP_AMSGRAD | APEXW_HP_LION | APEXW_HP_SLOW))) return APEXW_ERR_ARG;
+      if (n_fast_units || n_fast_f32_units ||
+          (hp->flags & (APEXW_HP_AMSGRAD | APEXW_HP_LION | APEXW_HP_SLOW | APEXW_HP_GRAD_DTYPES)))
+        return APEXW_ERR_ARG;
       return (hp->mode == APEXW_MODE_NATIVE || hp->mode == APEXW_MODE_SINGLE) ? APEXW_ERR_ARG : APEXW_OK;
     case APEXW_LAUNCH_Q8:
       if (n_fast_units < 0 || n_fast_f32_units < 0 || n_fast_units + n_fast_f32_units > n_units) return APEXW_ERR_ARG;
-      if (hp->mode == APEXW_MODE_NATIVE || (hp->flags & (APEXW_HP_AMSGRAD | APEXW_HP_LION | APEXW_HP_SLOW))) return APEXW_ERR_ARG;
+      if (hp->mode == APEXW_MODE_NATIVE ||
+          (hp->flags & (APEXW_HP_AMSGRAD | APEXW_HP_LION | APEXW_HP_SLOW | APEXW_HP_GRAD_DTYPES)))
+        return APEXW_ERR_ARG;
       if (hp->mode == APEXW_MODE_SINGLE && (n_fast_units || n_fast_f32_units)) return APEXW_ERR_ARG;
       return APEXW_OK;
     case APEXW_LAUNCH_CAUTIOUS:
@@ -205,7 +216,9 @@ static int launch_args_status(int32_t kind, int32_t n_tensors, int64_t n_units, 
       if (hp->mode == APEXW_MODE_NATIVE || hp->mode == APEXW_MODE_SINGLE) return APEXW_ERR_ARG;
       return ((uintptr_t)hp->counts & 7u) ? APEXW_ERR_ALIGN : APEXW_OK;
     case APEXW_LAUNCH_FACTORED:
-      if (n_fast_units || n_fast_f32_units || (hp->flags & (APEXW_HP_AMSGRAD | APEXW_HP_LION | APEXW_HP_SLOW))) return APEXW_ERR_ARG;
+      if (n_fast_units || n_fast_f32_units ||
+          (hp->flags & (APEXW_HP_AMSGRAD | APEXW_HP_LION | APEXW_HP_SLOW | APEXW_HP_GRAD_DTYPES)))
+        return APEXW_ERR_ARG;
       if (hp->mode == APEXW_MODE_SINGLE || hp->mode == APEXW_MODE_NATIVE) return APEXW_ERR_ARG;
       return (hp->flags & APEXW_HP_AMP) ? APEXW_ERR_ARG : APEXW_OK;   // factored steps take host-read AMP scalars
     default:

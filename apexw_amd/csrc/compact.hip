@@ -383,7 +383,8 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
         const bool replay = hp.mode == APEXW_MODE_REPLAY;
         const float num = replay ? rnd<GD>(m[j]) : m[j];
         float nf = num * (caut_mask<GD, false>(g[j], m[j], hp.mode) ? c.cq : 0.0f);
-        nf = replay ? rnd<PD>(nf) : rnd<caut_cold_dtype<PD, MD>()>(nf);
+        // the replay's m (cast to the grad dtype) times the mask (parameter dtype): their promotion
+        nf = replay ? rnd<(GD == PD ? PD : APEXW_F32)>(nf) : rnd<caut_cold_dtype<PD, MD>()>(nf);
         p[j] = rnd<PD>(p[j] + (-hp.step_size * nf) / den);
       } else if (nest) {
         const float p1 = rnd<PD>(p[j] + (hp.gain_hi * m[j]) / den);
@@ -403,9 +404,8 @@ APEXW_DEV void update8(float (&p)[8], float (&g)[8], float (&m)[8], float (&v)[8
 
 // Group k (512 elements, 8 per lane) of the unit starting at element `start`.
 // vmax: amsgrad's running max of v for this tensor (hparams.max_v), else NULL.
-template <int PD, int MD, int VD, bool QUAD, bool SR, bool VAR>
+template <int PD, int GD, int MD, int VD, bool QUAD, bool SR, bool VAR>
 APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const Ctx& c, void* vmax, void* mslow) {
-  constexpr int GD = PD;
   const int64_t n = t.n;
   const int lane = lane_id();
   const bool vec = !(c.tflags & APEXW_FLAG_SCALAR);
@@ -511,40 +511,55 @@ APEXW_DEV void compact_group(const apexw_tensor& t, int64_t start, int k, const 
   }
 }
 
+// The grad dtype of a group: the parameter's in the plain instantiation; any of the
+// three in the variant one (APEXW_HP_GRAD_DTYPES launches)
+template <int PD, int MD, int VD, bool QUAD, bool SR, bool VAR>
+APEXW_DEV void group_gd(const apexw_tensor& t, int64_t start, int k, const Ctx& c, void* vmax, void* mslow,
+                        uint32_t gd) {
+  if constexpr (VAR) {
+    if (gd != (uint32_t)PD) {
+      if (gd == APEXW_F32) compact_group<PD, APEXW_F32, MD, VD, QUAD, SR, VAR>(t, start, k, c, vmax, mslow);
+      else if (gd == APEXW_BF16) compact_group<PD, APEXW_BF16, MD, VD, QUAD, SR, VAR>(t, start, k, c, vmax, mslow);
+      else compact_group<PD, APEXW_F16, MD, VD, QUAD, SR, VAR>(t, start, k, c, vmax, mslow);
+      return;
+    }
+  }
+  compact_group<PD, PD, MD, VD, QUAD, SR, VAR>(t, start, k, c, vmax, mslow);
+}
+
 template <bool SR, bool VAR>
 APEXW_DEV void dispatch_group(const apexw_tensor& t, int64_t start, int k, const Ctx& c, uint32_t pd, uint32_t md,
-                              uint32_t vd, bool quad, void* vmax, void* mslow) {
+                              uint32_t vd, bool quad, void* vmax, void* mslow, uint32_t gd) {
   if (md == APEXW_F32) {
     // fp32 moments ("full" precision, small "auto" tensors): fp32 v, no quad (checked on the host)
-    if (pd == APEXW_F32) compact_group<APEXW_F32, APEXW_F32, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax, mslow);
-    else if (pd == APEXW_BF16) compact_group<APEXW_BF16, APEXW_F32, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax, mslow);
-    else compact_group<APEXW_F16, APEXW_F32, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax, mslow);
+    if (pd == APEXW_F32) group_gd<APEXW_F32, APEXW_F32, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax, mslow, gd);
+    else if (pd == APEXW_BF16) group_gd<APEXW_BF16, APEXW_F32, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax, mslow, gd);
+    else group_gd<APEXW_F16, APEXW_F32, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax, mslow, gd);
     return;
   }
   if (pd == APEXW_F16) {
     // fp16 parameters keep fp16 m (and fp16 or fp32 v)
-    if (vd == APEXW_F32) compact_group<APEXW_F16, APEXW_F16, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax, mslow);
-    else if (quad) compact_group<APEXW_F16, APEXW_F16, APEXW_F16, true, SR, VAR>(t, start, k, c, vmax, mslow);
-    else compact_group<APEXW_F16, APEXW_F16, APEXW_F16, false, SR, VAR>(t, start, k, c, vmax, mslow);
+    if (vd == APEXW_F32) group_gd<APEXW_F16, APEXW_F16, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax, mslow, gd);
+    else if (quad) group_gd<APEXW_F16, APEXW_F16, APEXW_F16, true, SR, VAR>(t, start, k, c, vmax, mslow, gd);
+    else group_gd<APEXW_F16, APEXW_F16, APEXW_F16, false, SR, VAR>(t, start, k, c, vmax, mslow, gd);
     return;
   }
   if (pd == APEXW_F32) {
-    if (vd == APEXW_F32) compact_group<APEXW_F32, APEXW_BF16, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax, mslow);
-    else if (quad) compact_group<APEXW_F32, APEXW_BF16, APEXW_BF16, true, SR, VAR>(t, start, k, c, vmax, mslow);
-    else compact_group<APEXW_F32, APEXW_BF16, APEXW_BF16, false, SR, VAR>(t, start, k, c, vmax, mslow);
+    if (vd == APEXW_F32) group_gd<APEXW_F32, APEXW_BF16, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax, mslow, gd);
+    else if (quad) group_gd<APEXW_F32, APEXW_BF16, APEXW_BF16, true, SR, VAR>(t, start, k, c, vmax, mslow, gd);
+    else group_gd<APEXW_F32, APEXW_BF16, APEXW_BF16, false, SR, VAR>(t, start, k, c, vmax, mslow, gd);
   } else {
-    if (vd == APEXW_F32) compact_group<APEXW_BF16, APEXW_BF16, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax, mslow);
-    else if (quad) compact_group<APEXW_BF16, APEXW_BF16, APEXW_BF16, true, SR, VAR>(t, start, k, c, vmax, mslow);
-    else compact_group<APEXW_BF16, APEXW_BF16, APEXW_BF16, false, SR, VAR>(t, start, k, c, vmax, mslow);
+    if (vd == APEXW_F32) group_gd<APEXW_BF16, APEXW_BF16, APEXW_F32, false, SR, VAR>(t, start, k, c, vmax, mslow, gd);
+    else if (quad) group_gd<APEXW_BF16, APEXW_BF16, APEXW_BF16, true, SR, VAR>(t, start, k, c, vmax, mslow, gd);
+    else group_gd<APEXW_BF16, APEXW_BF16, APEXW_BF16, false, SR, VAR>(t, start, k, c, vmax, mslow, gd);
   }
 }
 
 // cautious count pass: of group k (8 elements per lane) of the unit at `start`, the
 // elements whose mask is set, from the grads as the step prepares them and the first
 // moment as it updates it (nothing is written)
-template <int PD, int MD, bool QUAD>
+template <int PD, int GD, int MD, bool QUAD>
 APEXW_DEV uint32_t count_group(const apexw_tensor& t, int64_t start, int k, const Ctx& c) {
-  constexpr int GD = PD;
   const int64_t e0 = start + (int64_t)(k * 64 + lane_id()) * 8;
   if (e0 >= t.n) return 0u;
   const int cnt = (int)((t.n - e0) < 8 ? (t.n - e0) : 8);
@@ -572,21 +587,28 @@ APEXW_DEV uint32_t count_group(const apexw_tensor& t, int64_t start, int k, cons
   return n_set;
 }
 
+template <int PD, int MD, bool QUAD>
+APEXW_DEV uint32_t count_gd(const apexw_tensor& t, int64_t start, int k, const Ctx& c, uint32_t gd) {
+  if (gd == APEXW_F32) return count_group<PD, APEXW_F32, MD, QUAD>(t, start, k, c);
+  if (gd == APEXW_BF16) return count_group<PD, APEXW_BF16, MD, QUAD>(t, start, k, c);
+  return count_group<PD, APEXW_F16, MD, QUAD>(t, start, k, c);
+}
+
 APEXW_DEV uint32_t dispatch_count(const apexw_tensor& t, int64_t start, int k, const Ctx& c, uint32_t pd, uint32_t md,
-                                  bool quad) {
+                                  bool quad, uint32_t gd) {
   if (md == APEXW_F32) {
-    if (pd == APEXW_F32) return count_group<APEXW_F32, APEXW_F32, false>(t, start, k, c);
-    if (pd == APEXW_BF16) return count_group<APEXW_BF16, APEXW_F32, false>(t, start, k, c);
-    return count_group<APEXW_F16, APEXW_F32, false>(t, start, k, c);
+    if (pd == APEXW_F32) return count_gd<APEXW_F32, APEXW_F32, false>(t, start, k, c, gd);
+    if (pd == APEXW_BF16) return count_gd<APEXW_BF16, APEXW_F32, false>(t, start, k, c, gd);
+    return count_gd<APEXW_F16, APEXW_F32, false>(t, start, k, c, gd);
   }
   if (pd == APEXW_F16)
-    return quad ? count_group<APEXW_F16, APEXW_F16, true>(t, start, k, c)
-                : count_group<APEXW_F16, APEXW_F16, false>(t, start, k, c);
+    return quad ? count_gd<APEXW_F16, APEXW_F16, true>(t, start, k, c, gd)
+                : count_gd<APEXW_F16, APEXW_F16, false>(t, start, k, c, gd);
   if (pd == APEXW_F32)
-    return quad ? count_group<APEXW_F32, APEXW_BF16, true>(t, start, k, c)
-                : count_group<APEXW_F32, APEXW_BF16, false>(t, start, k, c);
-  return quad ? count_group<APEXW_BF16, APEXW_BF16, true>(t, start, k, c)
-              : count_group<APEXW_BF16, APEXW_BF16, false>(t, start, k, c);
+    return quad ? count_gd<APEXW_F32, APEXW_BF16, true>(t, start, k, c, gd)
+                : count_gd<APEXW_F32, APEXW_BF16, false>(t, start, k, c, gd);
+  return quad ? count_gd<APEXW_BF16, APEXW_BF16, true>(t, start, k, c, gd)
+              : count_gd<APEXW_BF16, APEXW_BF16, false>(t, start, k, c, gd);
 }
 
 // Per tensor, the count of set mask bits into hp.counts (cleared before the pass);
@@ -614,7 +636,7 @@ __global__ __launch_bounds__(256) void compact_count_kernel(const apexw_tensor* 
     c.tflags = t.flags;
     const uint32_t pd = (t.flags >> APEXW_FLAG_PDT_SHIFT) & 3u, md = (t.flags >> APEXW_FLAG_MDT_SHIFT) & 3u;
     uint32_t n_set = dispatch_count(t, (int64_t)un.unit * APEXW_COMPACT_UNIT, (int)(w % kGroups), c, pd, md,
-                                    t.flags & APEXW_FLAG_QUAD);
+                                    t.flags & APEXW_FLAG_QUAD, (t.flags >> APEXW_FLAG_GDT_SHIFT) & 3u);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) n_set += __shfl_xor(n_set, off, 64);
     if (lane_id() == 0 && n_set) atomicAdd(&hp.counts[un.tensor], (unsigned long long)n_set);
@@ -669,13 +691,17 @@ __global__ __launch_bounds__(256) void compact_step_kernel(const apexw_tensor* _
     const uint32_t md = (t.flags >> APEXW_FLAG_MDT_SHIFT) & 3u;
     const uint32_t vd = (t.flags >> APEXW_FLAG_VDT_SHIFT) & 3u;
     const bool quad = t.flags & APEXW_FLAG_QUAD;
+    const uint32_t gd = (t.flags >> APEXW_FLAG_GDT_SHIFT) & 3u;
     if (quad && hp.mode == APEXW_MODE_SINGLE) continue;  // rejected on the host; never read v out of range
+    // a grad of another dtype than its parameter: only the variant instantiation reads it
+    // (APEXW_HP_GRAD_DTYPES); the plain one never reads a grad at the wrong width
+    if (!VAR && gd != pd) continue;
     if (t.flags & APEXW_FLAG_FACTORED) continue;        // stepped by apexw_factored_step
     if (VAR && (hp.flags & APEXW_HP_CAUTIOUS)) c.cq = caut_q(hp.counts[un.tensor], t.n, quad, pd);
     void* vmax = (VAR && (hp.flags & APEXW_HP_AMSGRAD) && !quad) ? hp.max_v[un.tensor] : nullptr;
     void* mslow = (VAR && (hp.flags & APEXW_HP_SLOW) && !quad) ? hp.slow[un.tensor] : nullptr;
-    if (sr) dispatch_group<true, VAR>(t, start, k, c, pd, md, vd, quad, vmax, mslow);
-    else dispatch_group<false, VAR>(t, start, k, c, pd, md, vd, quad, vmax, mslow);
+    if (sr) dispatch_group<true, VAR>(t, start, k, c, pd, md, vd, quad, vmax, mslow, gd);
+    else dispatch_group<false, VAR>(t, start, k, c, pd, md, vd, quad, vmax, mslow, gd);
   }
 }
 
@@ -685,7 +711,9 @@ __global__ __launch_bounds__(256) void compact_step_kernel(const apexw_tensor* _
 static bool compact_combo_ok(uint32_t flags) {
   const uint32_t pd = (flags >> APEXW_FLAG_PDT_SHIFT) & 3u, gd = (flags >> APEXW_FLAG_GDT_SHIFT) & 3u;
   const uint32_t md = (flags >> APEXW_FLAG_MDT_SHIFT) & 3u, vd = (flags >> APEXW_FLAG_VDT_SHIFT) & 3u;
-  if (!(pd == APEXW_F32 || pd == APEXW_BF16 || pd == APEXW_F16) || gd != pd) return false;
+  // the grads may be of another dtype than their parameter (read by the variant instantiation)
+  if (!(pd == APEXW_F32 || pd == APEXW_BF16 || pd == APEXW_F16) || !(gd == APEXW_F32 || gd == APEXW_BF16 || gd == APEXW_F16))
+    return false;
   if (md == APEXW_F32) return vd == APEXW_F32 && !(flags & APEXW_FLAG_QUAD);   // fp32 moments
   // 16-bit moments are in the parameter's compact dtype: fp16 for fp16, else bf16
   const uint32_t cd = pd == APEXW_F16 ? APEXW_F16 : APEXW_BF16;
@@ -702,9 +730,10 @@ int apexw_launch_compact(const apexw_tensor* tensors, int64_t n_units, const ape
   // resident grid striding over the whole launch).  Launches that a resident grid
   // covers in a few passes keep it (C2, 124 M elements: 0.234-0.257 ms against
   // 0.252-0.288 with a workgroup per unit).
-  // nesterov / cautious / amsgrad / lion / beta3 launches take the instantiation that holds them
-  const bool var =
-      hp->flags & (APEXW_HP_NESTEROV | APEXW_HP_CAUTIOUS | APEXW_HP_AMSGRAD | APEXW_HP_LION | APEXW_HP_SLOW);
+  // nesterov / cautious / amsgrad / lion / beta3 launches, and those with grads of another dtype
+  // than their parameters, take the instantiation that holds them
+  const bool var = hp->flags & (APEXW_HP_NESTEROV | APEXW_HP_CAUTIOUS | APEXW_HP_AMSGRAD | APEXW_HP_LION |
+                                APEXW_HP_SLOW | APEXW_HP_GRAD_DTYPES);
   const void* kernel = var ? (const void*)compact_step_kernel<true> : (const void*)compact_step_kernel<false>;
   const int resident = apexw_resident_grid(kernel, n_units * kGroups);
   const int grid = n_units > (int64_t)resident * 8 ? (int)(n_units < INT32_MAX ? n_units : INT32_MAX) : resident;

@@ -25,7 +25,8 @@ constexpr long kSame = 0;        // every pointer and dtype as recorded
 constexpr long kGradsMoved = 1;  // only grad pointers changed (written to the scratch buffer)
 constexpr long kMissing = 2;     // a plan parameter lost its grad, or another parameter gained one
 constexpr long kRebuilt = 3;     // a parameter's storage or dtype changed
-constexpr long kSlowPath = 4;    // a grad is non-contiguous or of another dtype than its parameter
+constexpr long kSlowPath = 4;    // a grad is non-contiguous or of another size than its parameter
+constexpr long kGradDtype = 5;   // a grad's dtype differs from the one the table was built for
 
 bool unpack_list(PyObject* obj, const char* what) {
   if (!PyList_Check(obj)) {
@@ -67,23 +68,26 @@ PyObject* snapshot(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
   Py_RETURN_NONE;
 }
 
-// scan(params, inactive, p_ptrs_addr, dtypes_addr, g_ptrs_addr, g_scratch_addr) -> status
+// scan(params, inactive, p_ptrs_addr, dtypes_addr, g_ptrs_addr, g_scratch_addr, g_dtypes_addr) -> status
 //   params: the plan's parameters, in table order; inactive: the group's other
 //   trainable parameters.  g_ptrs holds the grad pointers the table was built
-//   from; on kGradsMoved the current ones are in g_scratch.
+//   from; on kGradsMoved the current ones are in g_scratch.  g_dtypes: the grad
+//   dtypes the table was built for (a grad may differ from its parameter's dtype:
+//   torch's Tensor.grad_dtype).
 PyObject* scan(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
-  if (nargs != 6) {
-    PyErr_SetString(PyExc_TypeError, "scan(params, inactive, p_ptrs, dtypes, g_ptrs, g_scratch)");
+  if (nargs != 7) {
+    PyErr_SetString(PyExc_TypeError, "scan(params, inactive, p_ptrs, dtypes, g_ptrs, g_scratch, g_dtypes)");
     return nullptr;
   }
-  uintptr_t pa, da, ga, sa;
+  uintptr_t pa, da, ga, sa, gda;
   if (!unpack_list(args[0], "params") || !unpack_list(args[1], "inactive") || !as_addr(args[2], &pa) ||
-      !as_addr(args[3], &da) || !as_addr(args[4], &ga) || !as_addr(args[5], &sa))
+      !as_addr(args[3], &da) || !as_addr(args[4], &ga) || !as_addr(args[5], &sa) || !as_addr(args[6], &gda))
     return nullptr;
   const auto* p_ptrs = reinterpret_cast<const uint64_t*>(pa);
   const auto* dtypes = reinterpret_cast<const int8_t*>(da);
   const auto* g_ptrs = reinterpret_cast<const uint64_t*>(ga);
   auto* g_scratch = reinterpret_cast<uint64_t*>(sa);
+  const auto* g_dtypes = reinterpret_cast<const int8_t*>(gda);
 
   const Py_ssize_t n_in = PyList_GET_SIZE(args[1]);
   for (Py_ssize_t i = 0; i < n_in; ++i) {
@@ -91,14 +95,18 @@ PyObject* scan(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
     if (p.grad().defined()) return PyLong_FromLong(kMissing);
   }
   const Py_ssize_t n = PyList_GET_SIZE(args[0]);
-  bool moved = false, slow = false;
+  bool moved = false, slow = false, gdt = false;
   for (Py_ssize_t i = 0; i < n; ++i) {
     const at::Tensor& p = THPVariable_Unpack(PyList_GET_ITEM(args[0], i));
     if (reinterpret_cast<uint64_t>(p.data_ptr()) != p_ptrs[i] || static_cast<int8_t>(p.scalar_type()) != dtypes[i])
       return PyLong_FromLong(kRebuilt);
     const at::Tensor& g = p.grad();
     if (!g.defined()) return PyLong_FromLong(kMissing);
-    if (g.scalar_type() != p.scalar_type() || !g.is_contiguous() || g.numel() != p.numel()) {
+    if (static_cast<int8_t>(g.scalar_type()) != g_dtypes[i]) {
+      gdt = true;
+      continue;
+    }
+    if (!g.is_contiguous() || g.numel() != p.numel()) {
       slow = true;
       continue;
     }
@@ -106,6 +114,7 @@ PyObject* scan(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
     g_scratch[i] = gp;
     moved |= gp != g_ptrs[i];
   }
+  if (gdt) return PyLong_FromLong(kGradDtype);
   if (slow) return PyLong_FromLong(kSlowPath);
   return PyLong_FromLong(moved ? kGradsMoved : kSame);
 }

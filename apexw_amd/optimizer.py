@@ -288,7 +288,7 @@ class ApexW(Optimizer):
                     if plan is None:
                         continue
                     if keep:
-                        # a lion switch over a replayed plan: the next step replays too
+                        # a lion switch or a grad dtype change over a replayed plan: the next step replays too
                         plan.cold_done = True
                         plan._sg_scale = dict(old._sg_scale)
                     self._plans[gid] = plan
@@ -411,6 +411,12 @@ class ApexW(Optimizer):
         native = (homogeneous and group.get("fused") is not False and not group.get("maximize", False)
                   and not group.get("nesterov", False) and not group.get("cautious", False) and not lion
                   and group.get("beta3") is None and not foreach)
+        if native and any(p.grad.dtype != p.dtype for p in params):
+            # torch._fused_adamw_ takes grads in their parameters' dtype only (it raises "expected
+            # scalar type"), so the reference's native fused step fails on such grads; fused=False
+            # steps them in the foreach order
+            raise RuntimeError("apexw_amd: the native fused step needs grads in their parameters' dtype "
+                               "(as torch._fused_adamw_ does); pass fused=False to step grads of another dtype")
         return StepPlan(self, group, params, "compact", native=native)
 
     # ------------------------------------------------------------------ checkpoints

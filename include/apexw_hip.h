@@ -195,6 +195,12 @@ typedef struct apexw_unit {
                                           elements, as torch's CPU add with alpha), then one
                                           round-to-nearest addcdiv into p (nesterov ignored). */
 #define APEXW_HP_LERP3_HI (1u << 14)   /* APEXW_HP_SLOW: the slow lerp weight (1 - beta3) >= 0.5 */
+#define APEXW_HP_GRAD_DTYPES (1u << 15) /* compact step (cold and replay modes) and its cautious count: some
+                                          descriptor's grad dtype (GDT) differs from its parameter's
+                                          (torch's Tensor.grad_dtype); such descriptors are stepped only
+                                          when this flag is set and skipped otherwise.  The grads are
+                                          prepared in their own dtype and read as fp32 values, as the
+                                          reference's foreach order does. */
 
 /* Step scalars of one launch, written on the device by apexw_amp_prepare (32 bytes). */
 typedef struct apexw_amp_dyn {

@@ -87,13 +87,17 @@ def _record_state(out, opt, params):
 
 
 def run_trajectory(ApexW, shapes, dtype, steps, seed, opt_kwargs, grad_scales=None, zero_grad_idx=(),
-                   record_all=False, none_grad=()):
+                   record_all=False, none_grad=(), grad_dtype=None):
     """Step ApexW on CPU and record inputs per step plus the final state
     (record_all: every state tensor, keyed st_<i>_<key>, instead of m / v / scales).
     none_grad: (step, parameter) pairs whose grad is None at that step (its grad is
-    still drawn, so the inputs of later steps do not shift)."""
+    still drawn, so the inputs of later steps do not shift).  grad_dtype: the grads'
+    dtype when it differs from the parameters' (torch's Tensor.grad_dtype)."""
     gen = torch.Generator().manual_seed(seed)
     params = [torch.nn.Parameter(_param(s, dtype, gen)) for s in shapes]
+    if grad_dtype is not None:
+        for p in params:
+            p.grad_dtype = grad_dtype
     out = {}
     # Inputs are regenerated by the tests from the same seeded generator; only a
     # fingerprint is stored so that a generator change is detected.
@@ -102,7 +106,7 @@ def run_trajectory(ApexW, shapes, dtype, steps, seed, opt_kwargs, grad_scales=No
     for step in range(steps):
         for i, p in enumerate(params):
             sc = 1e-3 if grad_scales is None else grad_scales[i]
-            g = _grad(p.shape, dtype, gen, sc)
+            g = _grad(p.shape, dtype if grad_dtype is None else grad_dtype, gen, sc)
             if i in zero_grad_idx:
                 g.zero_()
             p.grad = None if (step, i) in none_grad else g
@@ -584,6 +588,34 @@ FP16_CASES = {
 }
 
 
+GD_KW = dict(lr=1e-3, weight_decay=0.1, stochastic_rounding=False, threshold=4096)
+# grads of another dtype than their parameters (Tensor.grad_dtype):
+# name -> (shapes, param dtype, grad dtype, steps, seed, kwargs); the foreach order
+# (the native fused step refuses such grads), cold then replayed
+GRAD_DTYPE_CASES = {
+    "gd_compact_bf16_g32_rne": (PREC_SHAPES, torch.bfloat16, torch.float32, 5, 110, GD_KW),
+    # the clip and centralization on bf16 grads (norms and means rounded to bf16; fp32 grads
+    # would take the fp32-norm drift of compact_fp32_clip_rne)
+    "gd_compact_fp32_g16_clip_gc_rne": (PREC_SHAPES, torch.float32, torch.bfloat16, 4, 111,
+                                        dict(GD_KW, clip_grad_norm=1e-3, grad_centralization=True)),
+    "gd_compact_fp32_g16_rne": (PREC_SHAPES, torch.float32, torch.bfloat16, 4, 112, GD_KW),
+    "gd_full_bf16_g32_rne": (PREC_SHAPES, torch.bfloat16, torch.float32, 4, 113, dict(GD_KW, precision="full")),
+    "gd_auto_bf16_g32_rne": (PREC_SHAPES, torch.bfloat16, torch.float32, 4, 114,
+                             dict(GD_KW, precision="auto", adamw_compat=True)),
+    "gd_compact_bf16_g32_cautious_rne": (PREC_SHAPES, torch.bfloat16, torch.float32, 4, 115,
+                                         dict(GD_KW, cautious=True)),
+    "gd_compact_fp32_g16_cautious_rne": (PREC_SHAPES, torch.float32, torch.bfloat16, 4, 116,
+                                         dict(GD_KW, cautious=True)),
+    "gd_compact_fp16_g32_rne": (FP16_SHAPES, torch.float16, torch.float32, 5, 117, dict(GD_KW, threshold=65536)),
+}
+
+
+def golden_grad_dtypes(ApexW):
+    """Parameters stepped with grads of another dtype."""
+    return {name: run_trajectory(ApexW, shapes, dt, steps, seed, kw, record_all=True, grad_dtype=gd)
+            for name, (shapes, dt, gd, steps, seed, kw) in GRAD_DTYPE_CASES.items()}
+
+
 def golden_fp16(ApexW):
     """fp16 parameters in every precision mode the product steps them in."""
     return {name: run_trajectory(ApexW, shapes, torch.float16, steps, seed, kw, record_all=True, none_grad=ng)
@@ -621,6 +653,7 @@ def main():
     allc.update(golden_state_dict(ApexW))
     allc.update(golden_precisions(ApexW))
     allc.update(golden_fp16(ApexW))
+    allc.update(golden_grad_dtypes(ApexW))
     for name, arrays in allc.items():
         if args.only and name not in args.only:
             continue

@@ -9,8 +9,8 @@ import os
 import numpy as np
 import torch
 
-from golden.make_golden import (FP16_CASES, FUSED_CASES, FUSED_SHAPES, FV_KW, FV_Q8_SHAPES, HOOK_KW, HOOK_SHAPES,
-                                 PREC_CASES, SD_CASES, _fingerprint, _grad, _param)
+from golden.make_golden import (FP16_CASES, FUSED_CASES, FUSED_SHAPES, FV_KW, FV_Q8_SHAPES, GRAD_DTYPE_CASES, HOOK_KW,
+                                 HOOK_SHAPES, PREC_CASES, SD_CASES, _fingerprint, _grad, _param)
 from golden.sd_codec import decode
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -60,6 +60,8 @@ CASES.update({k: (sh, dt, n, seed, kw, None, ()) for k, (sh, dt, n, seed, kw) in
 # (step, parameter) pairs without a grad
 FP16_NAMES = sorted(FP16_CASES)
 CASES.update({k: (sh, torch.float16, n, seed, kw, None, (), ng) for k, (sh, n, seed, kw, ng) in FP16_CASES.items()})
+# grads of another dtype than their parameters: the ninth entry is the grads' dtype
+CASES.update({k: (sh, dt, n, seed, kw, None, (), (), gd) for k, (sh, dt, gd, n, seed, kw) in GRAD_DTYPE_CASES.items()})
 # in-backward trajectories: name -> (steps, backward passes per step, seed)
 HOOK_CASES = {"hooks_k1_rne": (3, 1, 31), "hooks_k2_rne": (3, 2, 32)}
 
@@ -79,15 +81,20 @@ def replay(name, make_opt, device="cpu", get_state=None):
     """Run case ``name`` with ``make_opt(params, **kwargs)``; return (params, opt, golden dict)."""
     shapes, dtype, steps, seed, kwargs, scales, zidx = CASES[name][:7]
     none_grad = CASES[name][7] if len(CASES[name]) > 7 else ()
+    grad_dtype = CASES[name][8] if len(CASES[name]) > 8 else None
     gold = load(name)
     gen = torch.Generator().manual_seed(seed)
     host = [_param(s, dtype, gen) for s in shapes]
     fp = [_fingerprint(p) for p in host]
     params = [torch.nn.Parameter(h.to(device)) for h in host]
+    if grad_dtype is not None:
+        for p in params:
+            p.grad_dtype = grad_dtype
     opt = make_opt(params, **kwargs)
     for step in range(steps):
         for i, p in enumerate(params):
-            g = _grad(p.shape, dtype, gen, 1e-3 if scales is None else scales[i])
+            g = _grad(p.shape, dtype if grad_dtype is None else grad_dtype, gen,
+                      1e-3 if scales is None else scales[i])
             if i in zidx:
                 g.zero_()
             fp.append(_fingerprint(g))

@@ -76,8 +76,11 @@ def test_check_tensor_rejects_bad_descriptors():
     assert lib.apexw_check_tensor(ctypes.byref(t), 0) == 0
     t.flags = (_lib.F16 << 0) | (_lib.F16 << 2) | (_lib.BF16 << 4) | (_lib.BF16 << 6)   # fp16 p keeps fp16 m
     assert lib.apexw_check_tensor(ctypes.byref(t), 0) == 2
-    t.flags = (_lib.F16 << 0) | (_lib.BF16 << 2)                                      # p and g dtypes differ
-    assert lib.apexw_check_tensor(ctypes.byref(t), 0) == 2
+    # p and g dtypes differ (torch's Tensor.grad_dtype): the compact step takes it, the
+    # per-parameter update does not
+    t.flags = (_lib.F16 << 0) | (_lib.BF16 << 2) | _lib.FLAG_SCALAR
+    assert lib.apexw_check_tensor(ctypes.byref(t), 0) == 0
+    assert lib.apexw_check_tensor(ctypes.byref(t), 3) == 2
     q = _lib.Tensor(16, 32, 48, 64, 80, 96, 4096, (_lib.BF16 << 0) | (_lib.BF16 << 2) | _lib.FLAG_NF4 | _lib.FLAG_QUAD,
                     2048)
     assert lib.apexw_check_tensor(ctypes.byref(q), 1) == 0

@@ -193,8 +193,9 @@ def test_noncontiguous_grad_is_copied(cpu_plans):
     assert keep[0].is_contiguous() and int(_table(plan)["g"][0]) == keep[0].data_ptr()
     ps[0].grad_dtype = None                       # torch then accepts a grad of another dtype
     ps[0].grad = torch.ones(64, 32, dtype=torch.float32).t()
-    assert plan.valid_for(group)
-    with pytest.raises(NotImplementedError):
+    # a grad of another dtype than the table's: a new plan (the table's descriptors change)
+    assert not plan.valid_for(group)
+    with pytest.raises(RuntimeError):
         plan._refresh_grads()
 
 

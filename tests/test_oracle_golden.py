@@ -172,6 +172,30 @@ def test_beta3_goldens_pin_the_numerator(name, mistake, monkeypatch):
                for i, p in enumerate(params))
 
 
+GD_NAMES = sorted(n for n in CASES if n.startswith("gd_"))
+
+
+@pytest.mark.parametrize("name", GD_NAMES)
+def test_grad_dtype_goldens_pin_the_grad_dtype(name):
+    """The trajectories with grads of another dtype tell the reference's handling from
+    an optimizer handed the same grads in the parameter dtype (fp32 grads of 16-bit
+    parameters rounded, bf16 grads of fp32 parameters widened): such an oracle ends
+    elsewhere, so the goldens pin the grads' own precision and their dtype-dependent
+    rounding order."""
+    class InParamDtype(OracleApexW):
+        def step(self):
+            for p in self.params:
+                if p.grad is not None:
+                    g = p.grad
+                    p.grad = None
+                    p.grad_dtype = None
+                    p.grad = g.to(p.dtype)
+            super().step()
+    params, _, gold = replay(name, InParamDtype)
+    assert any(not np.array_equal(_as_np(p.data).reshape(-1), gold[f"p_{i}"].reshape(-1))
+               for i, p in enumerate(params))
+
+
 def test_oracle_clip_matches_reference():
     z = load("clip_bf16")
     n = len([k for k in z if k.startswith("g_")])

@@ -261,6 +261,29 @@ class StepPlan:
             block = L.COMPACT_UNIT
         return f, block
 
+    def _check_strided(self, i, p, st):
+        """A non-contiguous parameter (channels_last and the like): the compact, full and
+        auto steps take it when it is dense and non-overlapping and its state shares its
+        layout, since their update is element by element and can walk all four tensors in
+        memory order.  Quad v (groups of four logical elements; the reference's
+        `.view(-1, 4)` fails on such tensors too), centralization (rows in logical order)
+        and the quantized and per-parameter steps are refused."""
+        from torch._prims_common import is_non_overlapping_and_dense
+        what = f"parameter {i} ({tuple(p.shape)}, strides {p.stride()})"
+        if self.kind != "compact" or self.single or not is_non_overlapping_and_dense(p):
+            raise NotImplementedError(f"apexw_amd: {what}: the HIP step needs contiguous parameters, or dense "
+                                      "non-overlapping ones in the compact, full and auto precisions")
+        if self.gc:
+            raise NotImplementedError(f"apexw_amd: {what}: grad centralization needs contiguous parameters")
+        for k in ("exp_avg", "exp_avg_sq"):
+            t = st.get(k)
+            if t is None:
+                continue
+            if t.numel() != p.numel():
+                raise NotImplementedError(f"apexw_amd: {what}: quad v needs contiguous parameters")
+            if t.stride() != p.stride():
+                raise NotImplementedError(f"apexw_amd: {what}: state '{k}' is not in the parameter's layout")
+
     def _build_tables(self, group):
         wd_on = group["weight_decay"] != 0
         n = len(self.params)
@@ -280,7 +303,7 @@ class StepPlan:
                 raise NotImplementedError("apexw_amd: the grads of parameters of one dtype must share a dtype")
         for i, (p, st) in enumerate(zip(self.params, self.states)):
             if not p.is_contiguous():
-                raise NotImplementedError("ApexW HIP step needs contiguous parameters")
+                self._check_strided(i, p, st)
             f, block = self._tensor_flags(p, st, wd_on, self.grad_dtypes[i])
             if f & L.FLAG_FACTORED and self.grad_dtypes[i] != p.dtype:
                 raise NotImplementedError("apexw_amd: factored_v with grads of another dtype than the parameter")
@@ -315,7 +338,7 @@ class StepPlan:
             for i, (p, st) in enumerate(zip(self.params, self.states)):
                 mx, v = st.get("max_exp_avg_sq"), st.get("exp_avg_sq")
                 if (mx is None or v is None or tab[i]["flags"] & (L.FLAG_QUAD | L.FLAG_FACTORED)
-                        or mx.numel() != p.numel() or mx.dtype != v.dtype or not mx.is_contiguous()
+                        or mx.numel() != p.numel() or mx.dtype != v.dtype or mx.stride() != p.stride()
                         or mx.device != p.device):
                     raise NotImplementedError(f"apexw_amd: amsgrad state of tensor {i} ({tuple(p.shape)}): "
                                               "max_exp_avg_sq must be a contiguous full-size tensor in v's dtype")
@@ -326,7 +349,7 @@ class StepPlan:
             for i, (p, st) in enumerate(zip(self.params, self.states)):
                 ms, m = st.get("exp_avg_slow"), st["exp_avg"]
                 if (ms is None or tab[i]["flags"] & (L.FLAG_QUAD | L.FLAG_FACTORED) or ms.numel() != p.numel()
-                        or ms.dtype != m.dtype or not ms.is_contiguous() or ms.device != p.device):
+                        or ms.dtype != m.dtype or ms.stride() != p.stride() or ms.device != p.device):
                     raise NotImplementedError(f"apexw_amd: beta3 state of tensor {i} ({tuple(p.shape)}): "
                                               "exp_avg_slow must be a contiguous full-size tensor in m's dtype")
                 self.slow_ptrs[i] = ms.data_ptr()
@@ -533,8 +556,9 @@ class StepPlan:
                     raise RuntimeError("a grad's dtype changed under the step plan")
                 if g.numel() != p.numel():
                     raise RuntimeError(f"grad of parameter {i} has {g.numel()} elements, the parameter {p.numel()}")
-                if not g.is_contiguous():
-                    keep[i] = g.contiguous()
+                if g.stride() != p.stride():
+                    # the step walks memory in the parameter's layout: the grad is copied into it
+                    keep[i] = torch.empty_like(p, dtype=g.dtype).copy_(g)
             self.g_scan[:] = [g.data_ptr() for g in keep]
         ptrs = self.g_scan.copy()
         self.g_ptrs[:] = ptrs

@@ -25,7 +25,7 @@ constexpr long kSame = 0;        // every pointer and dtype as recorded
 constexpr long kGradsMoved = 1;  // only grad pointers changed (written to the scratch buffer)
 constexpr long kMissing = 2;     // a plan parameter lost its grad, or another parameter gained one
 constexpr long kRebuilt = 3;     // a parameter's storage or dtype changed
-constexpr long kSlowPath = 4;    // a grad is non-contiguous or of another size than its parameter
+constexpr long kSlowPath = 4;    // a grad is laid out unlike its parameter, or of another size
 constexpr long kGradDtype = 5;   // a grad's dtype differs from the one the table was built for
 
 bool unpack_list(PyObject* obj, const char* what) {
@@ -106,7 +106,8 @@ PyObject* scan(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
       gdt = true;
       continue;
     }
-    if (!g.is_contiguous() || g.numel() != p.numel()) {
+    // the step walks the grad in its parameter's memory layout
+    if (g.strides() != p.strides() || g.numel() != p.numel()) {
       slow = true;
       continue;
     }

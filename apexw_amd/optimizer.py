@@ -398,6 +398,16 @@ class ApexW(Optimizer):
                     # torch._foreach_maximum_ over max_v (numel) and v (numel / 4) fails too
                     raise NotImplementedError("apexw_amd: amsgrad=True on a tensor whose state holds quad v")
                 S.ensure_max_v(st, p)         # amsgrad switched on after the first step (optimizer.py:2917-2922)
+        for p in params:
+            if not p.is_contiguous():
+                # a dense non-contiguous parameter (channels_last and the like) is stepped in its
+                # memory layout: its full-size state tensors take that layout too (a checkpoint's,
+                # or amsgrad's max, may be contiguous)
+                st = self.state[p]
+                for k in ("exp_avg", "exp_avg_sq", "max_exp_avg_sq", "exp_avg_slow"):
+                    t = st.get(k)
+                    if torch.is_tensor(t) and t.shape == p.shape and t.stride() != p.stride():
+                        st[k] = torch.empty_like(p, dtype=t.dtype).copy_(t)
         if group["precision"] in ("8bit", "ultra"):
             # both run the reference's _step_ultra (optimizer.py:3583-3587)
             return StepPlan(self, group, params, "q8")

@@ -231,7 +231,7 @@ def ensure_slow(st, p):
     :2903-2915).  Quantized states are not given one here (beta3 is refused there)."""
     if "exp_avg_slow" in st or st.get("is_8bit", False) or st.get("is_ultra", False):
         return
-    st["exp_avg_slow"] = torch.zeros(p.shape, dtype=st["exp_avg"].dtype, device=p.device)
+    st["exp_avg_slow"] = torch.zeros_like(p, dtype=st["exp_avg"].dtype, memory_format=torch.preserve_format)
 
 
 def ensure_max_v(st, p):
@@ -334,14 +334,16 @@ def _moments(st, p, mdt, group, is_peft, prec):
         st["is_quad_v"] = True
     st["state_dtype"] = mdt
     st["state_dtype_v"] = vdt
-    st["exp_avg"] = torch.zeros(p.shape, dtype=mdt, device=dev)
+    # in the parameter's layout (channels_last and the like), as zeros_like(p,
+    # memory_format=torch.preserve_format) gives it (optimizer.py:2848-2850, :2873-2875)
+    st["exp_avg"] = torch.zeros_like(p, dtype=mdt, memory_format=torch.preserve_format)
     lion = bool(group.get("lion", False))
     if lion:
         pass                       # lion keeps no second moment (optimizer.py:2857)
     elif quad:
         st["exp_avg_sq"] = torch.zeros((n // 4,), dtype=vdt, device=dev)
     else:
-        st["exp_avg_sq"] = torch.zeros(p.shape, dtype=vdt, device=dev)
+        st["exp_avg_sq"] = torch.zeros_like(p, dtype=vdt, memory_format=torch.preserve_format)
     # an fp16 v holds the second moment times a dynamic scale, 1024 at first
     # (optimizer.py:2889-2898); every other v is unscaled
     scaled = bool(group.get("dynamic_scaling", True)) and vdt == torch.float16 and not lion

@@ -103,7 +103,7 @@ def ensure_slow(st, p):
     (optimizer.py:2842-2845, :2903-2915; quantized states aside)."""
     if "exp_avg_slow" in st or st.get("is_8bit", False) or st.get("is_ultra", False):
         return
-    st["exp_avg_slow"] = torch.zeros(p.shape, dtype=st["exp_avg"].dtype, device=p.device)
+    st["exp_avg_slow"] = torch.zeros_like(p, dtype=st["exp_avg"].dtype, memory_format=torch.preserve_format)
 
 
 def ensure_max_v(st, p):
@@ -236,10 +236,13 @@ def _dense(st, p, mdt, group, is_peft, n_params_in_group, prec):
         st["is_quad_v"] = True
     st["state_dtype"] = mdt
     st["state_dtype_v"] = vdt
-    st["exp_avg"] = torch.zeros(p.shape, dtype=mdt)
+    # in the parameter's memory layout (zeros_like(p, memory_format=torch.preserve_format),
+    # optimizer.py:2848-2850, :2873-2875): torch._fused_adamw_ walks its tensors in memory order
+    st["exp_avg"] = torch.zeros_like(p, dtype=mdt, memory_format=torch.preserve_format)
     lion = bool(group.get("lion", False))
     if not lion:                   # lion keeps no second moment (optimizer.py:2857)
-        st["exp_avg_sq"] = torch.zeros((n // 4,), dtype=vdt) if quad else torch.zeros(p.shape, dtype=vdt)
+        st["exp_avg_sq"] = (torch.zeros((n // 4,), dtype=vdt) if quad
+                            else torch.zeros_like(p, dtype=vdt, memory_format=torch.preserve_format))
     # fp16 v starts with a dynamic scale of 1024 (optimizer.py:2889-2898)
     fp16_scaled = bool(group.get("dynamic_scaling", True)) and vdt == torch.float16 and not lion
     st["scale_v"] = 1024.0 if fp16_scaled else 1.0

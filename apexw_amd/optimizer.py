@@ -640,8 +640,8 @@ class ApexW(Optimizer):
             for p in params:
                 if p.device.type != "cuda":
                     raise RuntimeError("apexw_amd runs the optimizer step on the GPU; parameters must be on cuda")
-                if p.dtype not in (torch.float32, torch.bfloat16):
-                    raise NotImplementedError(f"apexw_amd steps fp32/bf16 parameters, got {p.dtype}")
+                if p.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+                    raise NotImplementedError(f"apexw_amd steps fp32, bf16 and fp16 parameters, got {p.dtype}")
             plan = StepPlan(self, group, params, "q8", hooked=True)
             self._hook_plans[key] = plan
         return plan
@@ -722,8 +722,8 @@ class ApexW(Optimizer):
         if plan is None or not plan.valid_for(group):
             if p.device.type != "cuda":
                 raise RuntimeError("apexw_amd runs the optimizer step on the GPU; parameters must be on cuda")
-            if p.dtype not in (torch.float32, torch.bfloat16):
-                raise NotImplementedError(f"apexw_amd steps fp32/bf16 parameters, got {p.dtype}")
+            if p.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+                raise NotImplementedError(f"apexw_amd steps fp32, bf16 and fp16 parameters, got {p.dtype}")
             kind = "q8" if (state.get("is_8bit", False) or prec == "8bit") else "compact"
             if kind == "compact" and "exp_avg_sq" not in state:
                 raise RuntimeError("enable_fused_backward needs exp_avg_sq; this parameter has lion state "

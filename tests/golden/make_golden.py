@@ -212,12 +212,13 @@ HOOK_SHAPES = [(256, 1024), (512, 512), (128, 256), (256,), (64, 512), (300, 100
 HOOK_KW = dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, precision="8bit", stochastic_rounding=False)
 
 
-def run_hooked(ApexW, shapes, steps, passes, seed, kwargs):
+def run_hooked(ApexW, shapes, steps, passes, seed, kwargs, dtype=torch.float32):
     """In-backward 8-bit steps: fp32 parameters (the large ones become bf16 at
-    construction), `passes` backward passes per optimizer step, each handing every
-    parameter a fresh grad through p.view_as(p), then step() and zero_grad()."""
+    construction) or fp16 ones (kept), `passes` backward passes per optimizer step,
+    each handing every parameter a fresh grad through p.view_as(p), then step() and
+    zero_grad()."""
     gen = torch.Generator().manual_seed(seed)
-    params = [torch.nn.Parameter(_param(s, torch.float32, gen)) for s in shapes]
+    params = [torch.nn.Parameter(_param(s, dtype, gen)) for s in shapes]
     fp = [_fingerprint(p.data) for p in params]
     opt = ApexW(params, **kwargs)
     out = {"dtypes": np.array([_dtype_code(p.dtype) for p in params], dtype=np.int64)}
@@ -240,7 +241,8 @@ def golden_hooks(ApexW):
     """The reference's in-backward 8-bit path (_flush_auto_8bit_hook_queue) over
     several steps: one backward per step, and two (gradient accumulation, K = 2)."""
     return {"hooks_k1_rne": run_hooked(ApexW, HOOK_SHAPES, 3, 1, 31, HOOK_KW),
-            "hooks_k2_rne": run_hooked(ApexW, HOOK_SHAPES, 3, 2, 32, HOOK_KW)}
+            "hooks_k2_rne": run_hooked(ApexW, HOOK_SHAPES, 3, 2, 32, HOOK_KW),
+            "hooks_fp16_k2_rne": run_hooked(ApexW, HOOK_SHAPES, 3, 2, 33, HOOK_KW, dtype=torch.float16)}
 
 
 FUSED_SHAPES = [(256, 512), (128, 256), (300, 100), (512,), (40, 8), (33,)]
@@ -253,6 +255,10 @@ FUSED_CASES = {
                            dict(lr=1e-2, weight_decay=0.1, precision="8bit", stochastic_rounding=False)),
     "fused_compact_bf16_k1": (torch.bfloat16, 6, 1, 63, dict(lr=1e-2, weight_decay=0.1, stochastic_rounding=False)),
     "fused_compact_fp32_k2": (torch.float32, 6, 2, 64, dict(lr=1e-2, weight_decay=0.1, stochastic_rounding=False)),
+    # fp16 parameters: fp16 moments in the compact precision (state.py:124-129), no dynamic v scale
+    "fused_compact_fp16_k2": (torch.float16, 6, 2, 65, dict(lr=1e-2, weight_decay=0.1, stochastic_rounding=False)),
+    "fused_8bit_fp16_k1": (torch.float16, 6, 1, 66,
+                           dict(lr=1e-2, weight_decay=0.1, precision="8bit", stochastic_rounding=False)),
 }
 
 

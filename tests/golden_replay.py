@@ -62,8 +62,9 @@ FP16_NAMES = sorted(FP16_CASES)
 CASES.update({k: (sh, torch.float16, n, seed, kw, None, (), ng) for k, (sh, n, seed, kw, ng) in FP16_CASES.items()})
 # grads of another dtype than their parameters: the ninth entry is the grads' dtype
 CASES.update({k: (sh, dt, n, seed, kw, None, (), (), gd) for k, (sh, dt, gd, n, seed, kw) in GRAD_DTYPE_CASES.items()})
-# in-backward trajectories: name -> (steps, backward passes per step, seed)
-HOOK_CASES = {"hooks_k1_rne": (3, 1, 31), "hooks_k2_rne": (3, 2, 32)}
+# in-backward trajectories: name -> (steps, backward passes per step, seed, parameter dtype)
+HOOK_CASES = {"hooks_k1_rne": (3, 1, 31, torch.float32), "hooks_k2_rne": (3, 2, 32, torch.float32),
+              "hooks_fp16_k2_rne": (3, 2, 33, torch.float16)}
 
 
 def load(name):
@@ -114,13 +115,13 @@ def bf16_ulp_diff(a, b):
 
 
 def hook_inputs(name):
-    """Initial fp32 parameters and, per step, per pass, the grads of the in-backward
-    case ``name`` (grads in the dtype each parameter has after the downcast)."""
+    """Initial parameters (fp32 or fp16) and, per step, per pass, the grads of the
+    in-backward case ``name`` (grads in the dtype each parameter has after the downcast)."""
     from oracle import hooks as H
-    steps, passes, seed = HOOK_CASES[name]
+    steps, passes, seed, dtype = HOOK_CASES[name]
     gold = load(name)
     gen = torch.Generator().manual_seed(seed)
-    host = [_param(s, torch.float32, gen) for s in HOOK_SHAPES]
+    host = [_param(s, dtype, gen) for s in HOOK_SHAPES]
     fp = [_fingerprint(p) for p in host]
     dts = [H.downcast_dtype(p) for p in host]
     grads = []

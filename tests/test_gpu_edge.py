@@ -15,6 +15,7 @@ import pytest
 import torch
 
 from golden_replay import bf16_ulp_diff
+from test_gpu_parity import _cmp_f16
 
 pytestmark = pytest.mark.gpu
 
@@ -43,6 +44,8 @@ def _assert_close(gpu, cpu, what):
     elif got.dtype == torch.float32:
         err = (got.double() - ref.double()).abs() - (1e-6 * ref.double().abs() + 1e-9)
         assert float(err.max()) <= 0, f"{what}: excess {float(err.max()):.3e}"
+    elif got.dtype == torch.float16:
+        _cmp_f16(got.reshape(-1), ref.reshape(-1), what=what)
     else:
         a, b = got.reshape(-1).to(torch.int32), ref.reshape(-1).to(torch.int32)
         if got.dtype == torch.uint8:

@@ -290,8 +290,9 @@ def _compare_fused(params, opt, cpu, states, tag, prev):
             cpu[p].copy_(p.detach().cpu())
 
 
-@pytest.mark.parametrize("prec,dtype", [("8bit", torch.float32), ("8bit", torch.bfloat16),
-                                        ("compact", torch.float32), ("compact", torch.bfloat16)])
+@pytest.mark.parametrize("prec,dtype", [("8bit", torch.float32), ("8bit", torch.bfloat16), ("8bit", torch.float16),
+                                        ("compact", torch.float32), ("compact", torch.bfloat16),
+                                        ("compact", torch.float16)])
 def test_fused_backward_matches_oracle(prec, dtype):
     _need_gpu()
     from oracle import hooks as H

@@ -56,7 +56,7 @@ def test_in_backward_matches_reference_trajectory(name):
     host, grads, gold = hook_inputs(name)
     params = [nn.Parameter(h.cuda()) for h in host]
     opt = ApexW(params, **HOOK_KW)
-    assert [{torch.float32: 0, torch.bfloat16: 1}[p.dtype] for p in params] == gold["dtypes"].tolist()
+    assert [{torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}[p.dtype] for p in params] == gold["dtypes"].tolist()
     assert opt._auto_hook_handles, "the in-backward path is not on"
     for per_step in grads:
         for gs in per_step:

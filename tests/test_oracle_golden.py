@@ -292,7 +292,7 @@ def test_oracle_hooks_match_reference_trajectory(name):
         for p in rest:
             p.grad = None
         K = len(per_step)
-    np.testing.assert_array_equal(np.array([{torch.float32: 0, torch.bfloat16: 1}[p.dtype] for p in params]),
+    np.testing.assert_array_equal(np.array([{torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}[p.dtype] for p in params]),
                                   gold["dtypes"])
     for i, p in enumerate(params):
         np.testing.assert_array_equal(_as_np(p.data).reshape(-1), gold[f"p_{i}"].reshape(-1), err_msg=f"p_{i}")

@@ -10,6 +10,11 @@ re-encoded in the layout a fresh state of the new mode would have
 ``apexw_state_encode`` (csrc/convert.hip).  The step counts carry over, so
 the bias correction continues where the checkpoint left off.
 
+An fp16 v holds the second moment times its state's dynamic scale (scale_v,
+a power of two): decode divides it out and encode multiplies the new state's
+scale in, both exactly.  The scale a state records is the one its checkpoint
+carries (the reference's _dynamic_scaling_meta).
+
 Factored second moments (row / column EMAs) are not converted: a state with
 them, or a target layout that would have them, raises NotImplementedError.
 """
@@ -58,6 +63,14 @@ def _layout(st, n):
     return lay
 
 
+def v_scale(st):
+    """The dynamic scale an fp16 v of state ``st`` holds (1 for every other v)."""
+    v = st.get("exp_avg_sq")
+    if torch.is_tensor(v) and v.dtype == torch.float16 and not st.get("is_8bit", False):
+        return float(st.get("scale_v", 1.0))
+    return 1.0
+
+
 def convert(p, st, group, peft):
     """A new state for ``p`` in the layout ``group``'s precision gives it, holding the
     moments of ``st`` (another mode's state); the step count carries over."""
@@ -77,6 +90,9 @@ def convert(p, st, group, peft):
         stream = torch.cuda.current_stream(p.device).cuda_stream
         L.check(lib.apexw_state_decode(ctypes.byref(_layout(src, n)), m32.data_ptr(), v32.data_ptr(), stream),
                 "apexw_state_decode")
+        ratio = v_scale(target) / v_scale(st)
+        if ratio != 1.0:
+            v32.mul_(ratio)               # powers of two: exact
         L.check(lib.apexw_state_encode(ctypes.byref(_layout(target, n)), m32.data_ptr(), v32.data_ptr(), stream),
                 "apexw_state_encode")
     if "max_exp_avg_sq" in target and "max_exp_avg_sq" in st:

@@ -474,9 +474,6 @@ class ApexW(Optimizer):
         if prec not in ("compact", "8bit"):
             raise NotImplementedError(f"apexw_amd implements the compact and 8-bit AdamW step; not supported: "
                                       f"precision={prec!r}")
-        if any(p.dtype == torch.float16 for g in self.param_groups for p in g["params"]):
-            # an fp16 v holds the moment times its dynamic scale; no conversion of it here
-            raise NotImplementedError("apexw_amd: set_precision with fp16 parameters")
         if prec == "8bit" and any(g.get("amsgrad", False) for g in self.param_groups):
             raise NotImplementedError("apexw_amd: amsgrad=True with precision='8bit'")
         peft = S.detect_peft_context(self.param_groups)

@@ -14,10 +14,15 @@ apexw_state_encode) have a checker:
   (quant_nf4 / quant_int8 / quant_logu8, old_scales=None, round to nearest);
   a quad v is first reduced to the mean of each 4 consecutive values, summed
   pairwise ((a + b) + (c + d)) * 0.25, so 4 equal values give that value back;
-  dense buffers take the fp32 values rounded to nearest-even.
+  dense buffers take the fp32 values rounded to nearest-even;
+* an fp16 dense v holds the moment times its state's dynamic scale scale_v
+  (apexw/optimizer.py:2478-2482 saves it beside the state): decode divides it
+  out, encode multiplies the target state's scale in.
 
 Pinned by (tests/test_oracle_convert.py): decode is the dequantizers, which
-the reference's trajectories pin; encode(decode(s)) reproduces the codes of a
+the reference's trajectories pin; an fp16 v of scale 2^k decodes to the
+stored value times 2^-k exactly, and encodes back to the same bits;
+encode(decode(s)) reproduces the codes of a
 state s that encode built, with the same NF4 / log-uint8 scales (a block's
 largest element decodes to exactly +-scale) and INT8 scales within one fp32 ulp;
 decode(encode(x)) stays within half a quantization step of x (NF4: half the
@@ -36,6 +41,14 @@ def quad_mean(v):
     return ((q[:, 0] + q[:, 1]) + (q[:, 2] + q[:, 3])) * 0.25
 
 
+def v_scale(st):
+    """Dynamic scale of an fp16 dense v (1 for every other v)."""
+    v = st.get("exp_avg_sq")
+    if torch.is_tensor(v) and v.dtype == torch.float16 and not st.get("is_8bit", False):
+        return float(st.get("scale_v", 1.0))
+    return 1.0
+
+
 def decode(st, n):
     """fp32 (m, v) of n elements from a state dict (compact or 8-bit, not factored)."""
     m, v = st["exp_avg"], st["exp_avg_sq"]
@@ -48,7 +61,7 @@ def decode(st, n):
             mf = Q.dequant_int8(m.reshape(-1), st["exp_avg_scales"], bs)
         vf = Q.dequant_logu8(v.reshape(-1), st["exp_avg_sq_scales"], bs // 4 if quad else bs)
     else:
-        mf, vf = m.reshape(-1).float(), v.reshape(-1).float()
+        mf, vf = m.reshape(-1).float(), v.reshape(-1).float() / v_scale(st)
     if quad:
         vf = vf.repeat_interleave(4)
     return mf.reshape(-1).clone(), vf.reshape(-1).clone()
@@ -73,5 +86,5 @@ def encode(st, m, v):
         st["exp_avg_sq_scales"].view(-1).copy_(s.reshape(-1))
     else:
         dm.view(-1).copy_(m.reshape(-1).to(dm.dtype))
-        dv.view(-1).copy_(vv.to(dv.dtype))
+        dv.view(-1).copy_((vv * v_scale(st)).to(dv.dtype))
     return st

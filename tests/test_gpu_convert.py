@@ -84,11 +84,14 @@ def test_decode_encode_match_oracle(shape, prec):
     assert torch.equal(v32.cpu(), rv)
 
 
-SWITCH = [("8bit", "compact"), ("compact", "8bit")]
+# fp16 parameters with beta2 = 0.99: the compact v is fp16 and holds the moment times
+# its dynamic scale (1024), which the conversion divides out or multiplies in
+SWITCH = [("8bit", "compact", torch.bfloat16), ("compact", "8bit", torch.bfloat16),
+          ("8bit", "compact", torch.float16), ("compact", "8bit", torch.float16)]
 
 
-@pytest.mark.parametrize("src,dst", SWITCH)
-def test_checkpoint_resumes_in_other_precision(src, dst):
+@pytest.mark.parametrize("src,dst,dtype", SWITCH, ids=[f"{a}-{b}-{str(d)[6:]}" for a, b, d in SWITCH])
+def test_checkpoint_resumes_in_other_precision(src, dst, dtype):
     """Train 3 steps in one mode, save, load into an optimizer, switch it to the
     other mode with set_precision, and step: the converted state equals the
     oracle's conversion, and the step equals the oracle's step from it."""
@@ -97,16 +100,19 @@ def test_checkpoint_resumes_in_other_precision(src, dst):
     from oracle import convert as C
     from oracle import layout as Lay
     from oracle.optim import OracleApexW
-    print(f"resume {src} -> {dst}", flush=True)
+    print(f"resume {src} -> {dst} {dtype}", flush=True)
     shapes = [(512, 256), (16384,), (4096,), (300,), (64, 33), (40,), (128, 130), (96, 256)]
     gen = torch.Generator().manual_seed(99)
-    host = [(torch.randn(s, generator=gen) * 0.02).bfloat16() for s in shapes]
+    host = [(torch.randn(s, generator=gen) * 0.02).to(dtype) for s in shapes]
     kw = dict(lr=1e-3, weight_decay=0.1, adamw_compat=True, stochastic_rounding=False)
+    if dtype == torch.float16:
+        del kw["adamw_compat"]        # which sets beta2 = 0.999, and so an fp32 v
+        kw["betas"] = (0.9, 0.99)
     ps = [nn.Parameter(h.cuda()) for h in host]
     opt = ApexW(ps, precision=src, **kw)
     for _ in range(3):
         for p in ps:
-            p.grad = (torch.randn(p.shape, generator=gen) * 1e-3).bfloat16().cuda()
+            p.grad = (torch.randn(p.shape, generator=gen) * 1e-3).to(dtype).cuda()
         opt.step()
     sd = opt.state_dict()
     ps2 = [nn.Parameter(p.detach().clone()) for p in ps]
@@ -118,6 +124,7 @@ def test_checkpoint_resumes_in_other_precision(src, dst):
     cps = [nn.Parameter(p.detach().cpu().clone()) for p in ps2]
     copt = OracleApexW(cps, precision=dst, **kw)
     grp = copt.group
+    scaled = 0
     for p0, p, cp in zip(ps, ps2, cps):
         saved = {k: (v.detach().cpu().clone() if torch.is_tensor(v) else v) for k, v in opt.state[p0].items()}
         mf, vf = C.decode(saved, p.numel())
@@ -130,14 +137,20 @@ def test_checkpoint_resumes_in_other_precision(src, dst):
         for k in ("exp_avg", "exp_avg_sq", "exp_avg_scales", "exp_avg_sq_scales"):
             if k in tgt:
                 a, b = gs[k].cpu(), tgt[k]
+                if k == "exp_avg_sq" and tgt[k].dtype == torch.float16:
+                    assert gs["scale_v"] == tgt["scale_v"] == 1024.0
+                    scaled += 1
                 if a.dtype == torch.uint8 and k == "exp_avg_sq":
                     assert int((a.int() - b.int()).abs().max()) <= 1, k
                 else:
                     assert torch.equal(a, b), k
                 gs[k].copy_(b.to(gs[k].device))   # start the step from the oracle's codes
         assert float(gs["step"]) == 3.0
+    if dtype == torch.float16:
+        src_scaled = sum(opt.state[p0]["exp_avg_sq"].dtype == torch.float16 for p0 in ps)
+        assert (scaled if dst == "compact" else src_scaled) > 0, "no fp16 v with a dynamic scale on either side"
     for p, cp in zip(ps2, cps):
-        g = (torch.randn(p.shape, generator=gen) * 1e-3).bfloat16()
+        g = (torch.randn(p.shape, generator=gen) * 1e-3).to(dtype)
         p.grad, cp.grad = g.cuda(), g.clone()
     opt2.step()
     copt.step()

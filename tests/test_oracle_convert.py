@@ -111,3 +111,27 @@ def test_nf4_encode_known_answers():
     assert int(codes[15]) == 9
     assert bool((codes[16:2048] == 7).all())          # zeros -> code 7 (0.0)
     assert bool((st["exp_avg_sq"] == 0).all())
+
+
+def test_fp16_scaled_v_decodes_to_the_moment():
+    """An fp16 compact v holds the moment times scale_v (1024 for a fresh fp16 state
+    with stochastic rounding): decode gives stored / 1024 exactly, and encode writes
+    the same fp16 bits back; an 8-bit target gets the unscaled moment."""
+    p, st = _state((64, 32), "compact", dtype=torch.float16)
+    assert st["exp_avg_sq"].dtype == torch.float16 and st["scale_v"] == 1024.0
+    g = torch.Generator().manual_seed(7)
+    stored = ((torch.rand(p.numel(), generator=g) * 8.0).to(torch.float16))
+    st["exp_avg_sq"].view(-1).copy_(stored)
+    mf, vf = C.decode(st, p.numel())
+    assert torch.equal(vf, stored.float() / 1024.0)
+    assert float(vf.max()) < 8.0 / 1024.0 * 1.001
+    _, st2 = _state((64, 32), "compact", dtype=torch.float16)
+    C.encode(st2, mf, vf)
+    assert torch.equal(st2["exp_avg_sq"].view(torch.int16), st["exp_avg_sq"].view(torch.int16))
+    _, q8 = _state((64, 32), "8bit", dtype=torch.float16)
+    C.encode(q8, mf, vf)
+    _, v8 = C.decode(q8, p.numel())
+    # log-uint8 keeps the magnitude: within a factor 2^(12/254) of the unscaled moment
+    big = vf > vf.max() * 2.0 ** -20
+    ratio = v8[big] / vf[big]
+    assert float(ratio.max()) <= 2.0 ** (12 / 254) * 1.0001 and float(ratio.min()) >= 2.0 ** (-12 / 254) / 1.0001

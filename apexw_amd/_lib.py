@@ -13,7 +13,7 @@ import numpy as np
 
 from ._build import LIB_PATH
 
-ABI_VERSION = 23
+ABI_VERSION = 24
 
 # dtype codes
 F32, BF16, F16, U8, I8 = 0, 1, 2, 3, 4
@@ -144,7 +144,7 @@ FV_TENSOR_DTYPE = np.dtype([("tensor", np.uint32), ("rows", np.int32), ("cols", 
 assert FV_TENSOR_DTYPE.itemsize == 32
 FV_SUM_COLS = 1
 FV_BAND_ROWS = 32
-FV_UNIT_RANGES = 6   # (bf16, fp32 parameters) x (INT8, 6-bit, bf16 m)
+FV_UNIT_RANGES = 9   # (bf16, fp32, fp16 parameters) x (INT8, 6-bit, 16-bit m)
 
 GEMM_SYM, GEMM_B_KN, GEMM_ADD_B, GEMM_APPLY, GEMM_APPLY_T, GEMM_APPLY_WD, GEMM_PANEL = 1, 2, 4, 8, 16, 32, 64
 GEMM_OUT_C, GEMM_OUT_CT, GEMM_ADD, GEMM_KIND_NN, GEMM_KIND_PANEL = 1, 2, 4, 8, 16

@@ -521,11 +521,12 @@ class StepPlan:
             L.check(-ws, "apexw_factored_layout")
         sel = np.isin(self._host_units["tensor"], np.array(rows, dtype=np.uint32))
         units = self._host_units[sel]
-        # units grouped by (parameter dtype, m kind): each group runs on its own kernel
+        # units grouped by (parameter dtype: bf16, fp32, fp16; m kind): each group runs on its own kernel
         tab = self.host_table[self.perm]
-        p32 = ((tab["flags"] >> L.PDT_SHIFT) & 3) == L.F32
+        pdt = (tab["flags"] >> L.PDT_SHIFT) & 3
+        pk = np.where(pdt == L.F32, 1, np.where(pdt == L.F16, 2, 0)).astype(np.int64)
         mk = np.where(tab["block"] == 0, 2, np.where(tab["flags"] & L.FLAG_M6, 1, 0))
-        group = (p32.astype(np.int64) * 3 + mk)[units["tensor"]]
+        group = (pk * 3 + mk)[units["tensor"]]
         order = np.argsort(group, kind="stable")
         units = np.ascontiguousarray(units[order])
         ends = np.cumsum(np.bincount(group, minlength=L.FV_UNIT_RANGES)).astype(np.int64)

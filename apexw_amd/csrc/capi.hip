@@ -143,10 +143,13 @@ int apexw_check_tensor(const apexw_tensor* t, int32_t kind) {
     // factored row: v / v_scale are the fp32 row / column EMAs
     const uint32_t f = t->flags;
     const uint32_t pd = (f >> APEXW_FLAG_PDT_SHIFT) & 3u, gd = (f >> APEXW_FLAG_GDT_SHIFT) & 3u;
-    if (!(f & APEXW_FLAG_FACTORED) || !(pd == APEXW_F32 || pd == APEXW_BF16) || gd != pd) return APEXW_ERR_DTYPE;
+    if (!(f & APEXW_FLAG_FACTORED) || !(pd == APEXW_F32 || pd == APEXW_BF16 || pd == APEXW_F16) || gd != pd)
+      return APEXW_ERR_DTYPE;
     if (f & (APEXW_FLAG_QUAD | APEXW_FLAG_NF4 | APEXW_FLAG_DENSE)) return APEXW_ERR_ARG;
     if (t->block == 0) {
-      if ((f & APEXW_FLAG_M6) || ((f >> APEXW_FLAG_MDT_SHIFT) & 3u) != APEXW_BF16) return APEXW_ERR_DTYPE;
+      // 16-bit m in the parameter's compact dtype: fp16 for fp16 parameters, else bf16
+      const uint32_t md16 = pd == APEXW_F16 ? APEXW_F16 : APEXW_BF16;
+      if ((f & APEXW_FLAG_M6) || ((f >> APEXW_FLAG_MDT_SHIFT) & 3u) != md16) return APEXW_ERR_DTYPE;
     } else {
       if (t->block > 2048 || !t->m_scale) return APEXW_ERR_ARG;
       if ((f & APEXW_FLAG_M6) && (t->block % 4) != 0) return APEXW_ERR_ARG;

@@ -268,7 +268,9 @@ __global__ __launch_bounds__(256) void fv_stats_kernel(const apexw_tensor* __res
   // one copy of the LDS for both grad dtypes' instantiations
   __shared__ float s_row[4][kBand];
   __shared__ float s_t[4][kBand][65];
-  if (((t.flags >> APEXW_FLAG_GDT_SHIFT) & 3u) == APEXW_F32) fv_stats_band<APEXW_F32, PLAIN>(t, e, lb, ws, c, s_row, s_t);
+  const uint32_t gdt = (t.flags >> APEXW_FLAG_GDT_SHIFT) & 3u;
+  if (gdt == APEXW_F32) fv_stats_band<APEXW_F32, PLAIN>(t, e, lb, ws, c, s_row, s_t);
+  else if (gdt == APEXW_F16) fv_stats_band<APEXW_F16, PLAIN>(t, e, lb, ws, c, s_row, s_t);
   else fv_stats_band<APEXW_BF16, PLAIN>(t, e, lb, ws, c, s_row, s_t);
 }
 
@@ -344,12 +346,13 @@ __global__ __launch_bounds__(256) void fv_finalize_kernel(const apexw_tensor* __
 // m kinds
 constexpr int kM8 = 0;    // INT8 codes
 constexpr int kM6 = 1;    // packed 6-bit codes (code + 31, 4 codes per 3 bytes, little-endian 24-bit words)
-constexpr int kM16 = 2;   // bf16 tensor
+constexpr int kM16 = 2;   // 16-bit tensor: fp16 for fp16 parameters, else bf16
 
 template <int PD, int MK>
 APEXW_DEV void fv_unit(const apexw_tensor& t, const apexw_fv_tensor& e, uint32_t tix, uint32_t unit, float* ws,
                        const FvCtx& c) {
   constexpr int GD = PD;
+  constexpr int MD16 = PD == APEXW_F16 ? APEXW_F16 : APEXW_BF16;
   const apexw_hparams& hp = *c.hp;
   const bool sr = hp.flags & APEXW_HP_SR;
   const bool wd = t.flags & APEXW_FLAG_WD;
@@ -407,10 +410,10 @@ APEXW_DEV void fv_unit(const apexw_tensor& t, const apexw_fv_tensor& e, uint32_t
       }
     } else {
       if (full) {
-        load8<APEXW_BF16>(t.m, e0, m);
+        load8<MD16>(t.m, e0, m);
       } else {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) m[j] = j < cnt ? load1<APEXW_BF16>(t.m, e0 + j) : 0.0f;
+        for (int j = 0; j < 8; ++j) m[j] = j < cnt ? load1<MD16>(t.m, e0 + j) : 0.0f;
       }
     }
     // row / column of element e0; later elements step across the row boundary
@@ -425,13 +428,17 @@ APEXW_DEV void fv_unit(const apexw_tensor& t, const apexw_fv_tensor& e, uint32_t
         const float upd = (m[j] / den) * hp.step_size;
         if constexpr (PD == APEXW_F32) {
           p[j] = (wd ? p[j] * hp.wd_factor : p[j]) - upd;
+        } else if constexpr (PD == APEXW_F16) {
+          // p.float(), mul_(wd), sub_(update), clamp_(-65504, 65504) (NaN kept), one rounding
+          const float pf = (wd ? p[j] * hp.wd_factor : p[j]) - upd;
+          p[j] = rnd<PD>(pf > 65504.0f ? 65504.0f : (pf < -65504.0f ? -65504.0f : pf));
         } else {
           const float pd = wd ? rnd<PD>(p[j] * hp.wd_factor) : p[j];
           p[j] = rnd<PD>(pd - rnd<PD>(upd));
         }
         mnew[k][j] = m[j];
         amax = fmaxf(amax, fabsf(m[j]));
-        if constexpr (MK == kM16) m[j] = rnd<APEXW_BF16>(m[j]);  // m.copy_(mf.to(bf16)): nearest-even
+        if constexpr (MK == kM16) m[j] = rnd<MD16>(m[j]);  // m.copy_(mf.to(m.dtype)): nearest-even
         if (++col == cols) {
           col = 0;
           ++row;
@@ -447,11 +454,11 @@ APEXW_DEV void fv_unit(const apexw_tensor& t, const apexw_fv_tensor& e, uint32_t
     }
     if constexpr (MK == kM16) {
       if (full) {
-        store8<APEXW_BF16>(t.m, e0, m);
+        store8<MD16>(t.m, e0, m);
       } else {
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-          if (j < cnt) store1<APEXW_BF16>(t.m, e0 + j, m[j]);
+          if (j < cnt) store1<MD16>(t.m, e0 + j, m[j]);
       }
     }
   }
@@ -899,9 +906,14 @@ __global__ __launch_bounds__(256) void fv_update_kernel(const apexw_tensor* __re
     const apexw_fv_tensor& e = fv[un.tensor];
     const apexw_tensor& t = tensors[e.tensor];
     if (!(t.flags & APEXW_FLAG_FACTORED)) continue;
-    const bool p32 = ((t.flags >> APEXW_FLAG_PDT_SHIFT) & 3u) == APEXW_F32;
+    const uint32_t pdt = (t.flags >> APEXW_FLAG_PDT_SHIFT) & 3u;
     const int mk = t.block == 0 ? kM16 : (t.flags & APEXW_FLAG_M6) ? kM6 : kM8;
-    if (p32 != (PDK == APEXW_F32) || mk != MK) continue;
+    if (pdt != (uint32_t)PDK || mk != MK) continue;
+    if constexpr (PDK == APEXW_F16) {
+      // fp16 parameters take the general path (the full-unit and row paths unpack bf16 / fp32 words)
+      fv_unit<PDK, MK>(t, e, e.tensor, un.unit, ws, c);
+      continue;
+    }
     const bool full = !(t.flags & APEXW_FLAG_SCALAR) && (t.block == 0 || t.block == 2048) &&
                       (int64_t)(un.unit + 1) * 2048 <= t.n;
     if (full) {
@@ -945,5 +957,8 @@ int apexw_launch_factored(const apexw_tensor* tensors, const apexw_fv_tensor* fv
   launch_update<APEXW_F32, kM8>(tensors, fv, n_fv, units, ends[2], ends[3], ws, hp, stream);
   launch_update<APEXW_F32, kM6>(tensors, fv, n_fv, units, ends[3], ends[4], ws, hp, stream);
   launch_update<APEXW_F32, kM16>(tensors, fv, n_fv, units, ends[4], ends[5], ws, hp, stream);
+  launch_update<APEXW_F16, kM8>(tensors, fv, n_fv, units, ends[5], ends[6], ws, hp, stream);
+  launch_update<APEXW_F16, kM6>(tensors, fv, n_fv, units, ends[6], ends[7], ws, hp, stream);
+  launch_update<APEXW_F16, kM16>(tensors, fv, n_fv, units, ends[7], ends[8], ws, hp, stream);
   return hipGetLastError() == hipSuccess ? APEXW_OK : APEXW_ERR_LAUNCH;
 }

@@ -366,8 +366,6 @@ class ApexW(Optimizer):
         for p in params:
             if len(self.state[p]) == 0:
                 self.state[p].update(S.init_state(p, group, peft, has16))
-            if p.dtype == torch.float16 and self.state[p].get("is_factored_v", False):
-                raise NotImplementedError("apexw_amd: factored_v with fp16 parameters")
         lion = bool(group.get("lion", False))
         # lion takes the place of the AdamW update and of its variants (optimizer.py:5375-5380,
         # :5677-5683): nesterov, cautious, amsgrad and beta3 do not apply under it

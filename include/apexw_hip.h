@@ -44,7 +44,7 @@
 extern "C" {
 #endif
 
-#define APEXW_ABI_VERSION 23
+#define APEXW_ABI_VERSION 24
 
 /* status codes */
 enum apexw_status {
@@ -414,13 +414,15 @@ int64_t apexw_factored_layout(apexw_fv_tensor* fv, int32_t n_fv, int64_t* n_band
  * elements for 16-bit m; a unit's `tensor` field is the index of its entry in
  * fv, not a row of the tensor table, so no lookup precedes its loads).  The
  * units are grouped by (parameter dtype, m kind) in the order bf16 / INT8 m,
- * bf16 / 6-bit m, bf16 / bf16 m, fp32 / INT8 m, fp32 / 6-bit m, fp32 / bf16 m;
+ * bf16 / 6-bit m, bf16 / bf16 m, fp32 / INT8 m, fp32 / 6-bit m, fp32 / bf16 m,
+ * fp16 / INT8 m, fp16 / 6-bit m, fp16 / fp16 m (fp16 parameters: decay and update
+ * in fp32, clamped to +-65504, one rounding; 16-bit m in fp16);
  * range_ends (HOST array of APEXW_FV_UNIT_RANGES) holds the end offset of each
  * group (the last is n_units), and each non-empty group runs on its own kernel.
  * workspace: the floats apexw_factored_layout returned.  hp as for the step
  * kernels (mode ignored); APEXW_HP_SR rounds the m codes stochastically.
  */
-#define APEXW_FV_UNIT_RANGES 6
+#define APEXW_FV_UNIT_RANGES 9
 int apexw_factored_step(const apexw_tensor* tensors, int32_t n_tensors, const apexw_fv_tensor* fv, int32_t n_fv,
                         int64_t n_bands, int64_t n_col_blocks, const apexw_unit* units, int64_t n_units,
                         const int64_t* range_ends, float* workspace, const apexw_hparams* hp, void* stream);

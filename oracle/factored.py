@@ -123,6 +123,14 @@ def factored_update(p, g, st, *, beta1, beta2, step_size, eps_scaled, eps, stoch
         if wd_factor is not None:
             pf.mul_(wd_factor)
         pf.sub_(upd)
+    elif p.dtype == torch.float16:
+        # apexw/state.py:405-410: decay and update in fp32, clamped to fp16's range,
+        # one rounding
+        pw = pf.float()
+        if wd_factor is not None:
+            pw.mul_(wd_factor)
+        pw.sub_(upd).clamp_(-65504.0, 65504.0)
+        pf.copy_(pw.to(torch.float16))
     else:
         if wd_factor is not None:
             pf.mul_(wd_factor)

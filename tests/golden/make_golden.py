@@ -204,6 +204,12 @@ def golden_factored(ApexW):
         ApexW, [(512, 1024)], torch.bfloat16, 3, 23, dict(FV_KW, precision="8bit", six_bit=True), record_all=True)
     cases["fv_compact_bf16_rne"] = run_trajectory(
         ApexW, [(512, 1024), (768,)], torch.bfloat16, 3, 24, FV_KW, record_all=True)
+    # fp16 parameters: decay and update in fp32, clamped, one rounding (state.py:405-410); fp16 m
+    cases["fv_q8_fp16_rne"] = run_trajectory(
+        ApexW, [(256, 256), (640, 512), (700,)], torch.float16, 3, 25, dict(FV_KW, precision="8bit"),
+        record_all=True)
+    cases["fv_compact_fp16_rne"] = run_trajectory(
+        ApexW, [(512, 1024), (768,)], torch.float16, 3, 26, FV_KW, record_all=True)
     return cases
 
 

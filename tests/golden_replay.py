@@ -51,6 +51,9 @@ FV_CASES = {
     "fv_6bit_bf16_rne": ([(512, 1024)], torch.bfloat16, 3, 23, dict(FV_KW, precision="8bit", six_bit=True),
                          None, ()),
     "fv_compact_bf16_rne": ([(512, 1024), (768,)], torch.bfloat16, 3, 24, FV_KW, None, ()),
+    "fv_q8_fp16_rne": ([(256, 256), (640, 512), (700,)], torch.float16, 3, 25, dict(FV_KW, precision="8bit"),
+                       None, ()),
+    "fv_compact_fp16_rne": ([(512, 1024), (768,)], torch.float16, 3, 26, FV_KW, None, ()),
 }
 CASES.update(FV_CASES)
 # the full / auto / ultra precisions (every state tensor recorded)

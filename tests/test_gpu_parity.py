@@ -142,6 +142,14 @@ def _cmp_factored(params, opt, gold, init, steps, floor=1e-9):
             tol = 2.0 ** -7 * steps * (p0.abs() + 2.0 * r64.abs())
             bad = (d > 2) & ((g64 - r64).abs() > tol)
             assert not bool(bad.any()), f"p_{i}: {int(bad.sum())} elements beyond the bar (max {int(d.max())} ulps)"
+        elif p.dtype == torch.float16:
+            # fp32 decay and update, one rounding to fp16 per step: the bf16 bar with fp16's ulp
+            got, ref = p.data.cpu().reshape(-1), torch.from_numpy(gold[f"p_{i}"]).reshape(-1)
+            d = bf16_ulp_diff(got, ref)
+            g64, r64, p0 = got.double(), ref.double(), init[i].reshape(-1).double()
+            tol = 2.0 ** -10 * steps * (p0.abs() + 2.0 * r64.abs())
+            bad = (d > 2) & ((g64 - r64).abs() > tol)
+            assert not bool(bad.any()), f"p_{i}: {int(bad.sum())} elements beyond the bar (max {int(d.max())} ulps)"
         else:
             _cmp_f32(p.data.reshape(-1), torch.from_numpy(gold[f"p_{i}"]).reshape(-1), rel=1e-5, what=f"p_{i}")
         for k in ("exp_avg_sq_row", "exp_avg_sq_col"):
@@ -154,6 +162,8 @@ def _cmp_factored(params, opt, gold, init, steps, floor=1e-9):
         elif m.dtype == torch.int8:
             d = (m.reshape(-1).to(torch.int32) - torch.from_numpy(gm.reshape(-1).astype(np.int32))).abs()
             assert int(d.max()) <= 1, f"int8 m_{i}: codes differ by {int(d.max())}"
+        elif m.dtype == torch.float16:
+            _cmp_f16(m.reshape(-1), torch.from_numpy(gm).reshape(-1), ulps=2, what=f"fp16 m_{i}")
         else:
             _cmp_bf16(m.reshape(-1), to_torch(gm, torch.bfloat16).reshape(-1), ulps=2, what=f"bf16 m_{i}")
         if "exp_avg_scales" in keys:

@@ -49,11 +49,12 @@ def _check_variants(precision, factored, nesterov, cautious, maximize=False, ams
     grads.  amsgrad=True, lion=True and beta3 (AdEMAMix) run in the compact, full and
     auto precisions (a running max of v beside it, no quad v; the sign update on m
     alone, which takes the place of the AdamW update and of its variants; a slow first
-    moment beside m, no quad v).  Factored second moments, nesterov together with
+    moment beside m, no quad v).  maximize also runs with factored second moments
+    (the negated grads reach the factored kernels through the unscale factor).
+    nesterov, cautious and amsgrad with factored second moments, nesterov together with
     cautious, beta3 together with cautious, and amsgrad, lion or beta3 in the 8bit and
     ultra precisions do not."""
-    for name, on in (("nesterov", nesterov), ("cautious", cautious), ("maximize", maximize),
-                     ("amsgrad", amsgrad)):
+    for name, on in (("nesterov", nesterov), ("cautious", cautious), ("amsgrad", amsgrad)):
         if not on:
             continue
         if factored:

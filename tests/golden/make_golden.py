@@ -210,6 +210,12 @@ def golden_factored(ApexW):
         record_all=True)
     cases["fv_compact_fp16_rne"] = run_trajectory(
         ApexW, [(512, 1024), (768,)], torch.float16, 3, 26, FV_KW, record_all=True)
+    # maximize: the grads negated before sanitizing and unscaling (state.py:430-439)
+    cases["fv_q8_bf16_maximize_rne"] = run_trajectory(
+        ApexW, [(256, 256), (640, 512), (700,)], torch.bfloat16, 3, 27, dict(FV_KW, precision="8bit", maximize=True),
+        record_all=True)
+    cases["fv_compact_bf16_maximize_rne"] = run_trajectory(
+        ApexW, [(512, 1024), (768,)], torch.bfloat16, 3, 28, dict(FV_KW, maximize=True), record_all=True)
     return cases
 
 

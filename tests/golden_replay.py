@@ -54,6 +54,10 @@ FV_CASES = {
     "fv_q8_fp16_rne": ([(256, 256), (640, 512), (700,)], torch.float16, 3, 25, dict(FV_KW, precision="8bit"),
                        None, ()),
     "fv_compact_fp16_rne": ([(512, 1024), (768,)], torch.float16, 3, 26, FV_KW, None, ()),
+    "fv_q8_bf16_maximize_rne": ([(256, 256), (640, 512), (700,)], torch.bfloat16, 3, 27,
+                                dict(FV_KW, precision="8bit", maximize=True), None, ()),
+    "fv_compact_bf16_maximize_rne": ([(512, 1024), (768,)], torch.bfloat16, 3, 28, dict(FV_KW, maximize=True),
+                                     None, ()),
 }
 CASES.update(FV_CASES)
 # the full / auto / ultra precisions (every state tensor recorded)

@@ -190,12 +190,11 @@ def test_constructor_contract():
                dict(precision="8bit", nesterov=True), dict(precision="compact", nesterov=True)):
         with pytest.raises(NotImplementedError):
             ApexW(p, cautious=True, **kw)
-    # maximize: every precision, not with factored second moments
+    # maximize: every precision, factored second moments included
     for prec in ("8bit", "ultra", "compact", "full", "auto"):
         assert ApexW(p, precision=prec, maximize=True).defaults["maximize"]
     for kw in (dict(precision="8bit", factored_v=True), dict(precision="compact", factored_v=True)):
-        with pytest.raises(NotImplementedError):
-            ApexW(p, maximize=True, **kw)
+        assert ApexW(p, maximize=True, **kw).defaults["maximize"]
     for prec, betas in (("full", (0.9, 0.999)), ("fp32", (0.9, 0.999)), ("auto", (0.9, 0.99)),
                         ("smart", (0.9, 0.99)), ("ultra", (0.9, 0.99)), ("3byte", (0.9, 0.99))):
         o = ApexW(p, precision=prec)
